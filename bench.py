@@ -1,0 +1,314 @@
+#!/usr/bin/env python3
+"""Fused-MoE layer benchmark on one MI355X.
+
+A step is one MoE layer call over one batch of T synthetic tokens already
+resident in HBM: routing (softmax top-k or grouped sigmoid top-k) followed by
+XpuFusedMoe.apply (alignment, w13 grouped GEMM + fused activation, w2 grouped
+GEMM, weighted top-k reduction).  The headline line is configuration C2
+(Qwen3-30B-A3B shape, bf16, T=4096); the other BASELINE configurations are
+reported in the same JSON line under "sweep".
+
+Timed region: W eager warm-up steps, then K steps captured in one HIP graph
+and replayed once between two events (torch.cuda.synchronize on both sides).
+Stage durations for the roofline come from a second, eager pass in which the
+library records HIP events around each of its five launches on the same
+stream (mi355moe_fused_moe_timed).
+
+Only the cpu_baseline leg imports the CPU oracle (oracle/), and only to time
+it as the reported baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vllm-xpu-kernels_amd"))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemm_work(cfg, T, active, which):
+    """Algorithmic (bytes, flops) of one grouped-GEMM launch."""
+    H, I, k = cfg.hidden, cfg.inter, cfg.topk
+    slots = T * k
+    if cfg.recipe == "bf16":
+        bw, sc, bx, sx = 2.0, 0.0, 2.0, 0.0
+    elif cfg.recipe == "fp8block":
+        bw, sc, bx, sx = 1.0, 4.0 / (128 * 128), 1.0, 4.0 / 128
+    else:
+        bw, sc, bx, sx = 0.5, 1.0 / 32, 2.0, 0.0
+    if which == "gemm_w13":
+        n = 2 * I * H
+        b = active * (n * (bw + sc) + (2 * 2 * I if cfg.bias else 0))
+        b += T * H * (bx + sx) + slots * I * (bx + sx)
+        f = 2.0 * slots * n
+    else:
+        n = H * I
+        b = active * (n * (bw + sc) + (2 * H if cfg.bias else 0))
+        b += slots * I * (bx + sx) + slots * H * 2
+        f = 2.0 * slots * n
+    return b, f
+
+
+def _oracle_inputs(cfg, w, x, tw, ti):
+    """CPU copies of only the experts the given tokens route to, ids remapped
+    to that compact set (nk layouts)."""
+    ti_c = ti.cpu().long()
+    used = torch.unique(ti_c)
+    remap = torch.full((cfg.experts,), -1, dtype=torch.long)
+    remap[used] = torch.arange(used.numel())
+    ids = remap[ti_c]
+    u = used.to(w.w13.device)
+    if cfg.recipe == "bf16":
+        w13 = w.w13.index_select(0, u).transpose(1, 2).contiguous().cpu()
+        w2 = w.w2.index_select(0, u).transpose(1, 2).contiguous().cpu()
+    else:
+        w13 = w.w13.view(torch.uint8).index_select(0, u).cpu()
+        w2 = w.w2.view(torch.uint8).index_select(0, u).cpu()
+        if cfg.recipe == "fp8block":
+            w13, w2 = w13.view(torch.float8_e4m3fn), w2.view(torch.float8_e4m3fn)
+    pick = lambda t: t.index_select(0, u).cpu() if t is not None else None  # noqa: E731
+    return (x.cpu(), w13, pick(w.w13_scale), pick(w.w13_bias), w2,
+            pick(w.w2_scale), pick(w.w2_bias), tw.cpu(), ids)
+
+
+def cpu_baseline(cfg, w, x, tw, ti, n_tok, budget_s=20.0):
+    """Times the CPU oracle (torch on the host cores) on the first n_tok
+    tokens of the workload: 1 warm-up, then the median of up to 5 runs within
+    the budget."""
+    from oracle import moe_oracle as O
+    args = _oracle_inputs(cfg, w, x[:n_tok], tw[:n_tok], ti[:n_tok])
+    O.fused_moe(cfg.recipe, *args, activation=cfg.activation)
+    times = []
+    t_start = time.time()
+    while len(times) < 5 and (time.time() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        O.fused_moe(cfg.recipe, *args, activation=cfg.activation)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": n_tok / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{cfg.name} first {n_tok} of the timed batch's tokens "
+                      f"(their {int(args[-1].max()) + 1} experts), oracle/moe_oracle.py "
+                      f"fused_moe, median of {len(times)} runs, "
+                      f"{med * 1e3:.1f} ms per run, os.cpu_count()={os.cpu_count()}"}
+
+
+class Point:
+    def __init__(self, cfg, T, dev, weights=None):
+        from vllm_xpu_kernels import workloads as W
+        from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+        self.cfg, self.T, self.dev = cfg, T, dev
+        self.w = weights if weights is not None else W.make_weights(cfg, dev)
+        self.x = W.make_activations(cfg, T, dev)
+        self.logits = W.make_router_logits(cfg, T, dev)
+        self.bias = (W.make_correction_bias(cfg, dev)
+                     if cfg.routing == "grouped_sigmoid" else None)
+        w = self.w
+        self.moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale,
+                               w.w2_bias, cfg.topk, cfg.activation, cfg.experts)
+        self.out = torch.empty_like(self.x)
+        self.tw, self.ti = W.route(cfg, self.logits, self.bias)
+        self.active = int(torch.unique(self.ti).numel())
+
+    def step(self):
+        from vllm_xpu_kernels import workloads as W
+        tw, ti = W.route(self.cfg, self.logits, self.bias)
+        self.moe.apply(self.out, self.x, tw, ti)
+
+    def time_steps(self, steps, warmup, graph=True):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(steps):
+                    self.step()
+            g.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            del g
+        else:
+            e0.record()
+            for _ in range(steps):
+                self.step()
+            e1.record()
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    def stage_times(self, steps):
+        from vllm_xpu_kernels import capi
+        args = capi.fused_args(self.moe, self.out, self.x, self.tw, self.ti)
+        ws = capi.workspace_for(args, self.dev)
+        timer = capi.StageTimer(steps)
+        try:
+            torch.cuda.synchronize()
+            try:   # give the host a head start so no stage waits for a launch
+                torch.cuda._sleep(int(5e6))
+            except Exception:
+                pass
+            for i in range(steps):
+                timer.run(args, ws, i)
+            torch.cuda.synchronize()
+            per = [timer.stage_ms(i) for i in range(steps)]
+        finally:
+            timer.close()
+        return [statistics.mean(p[j] for p in per) for j in range(capi.FUSED_STAGES)]
+
+
+def summarize(pt, ms, stages):
+    from vllm_xpu_kernels import capi
+    from vllm_xpu_kernels import workloads as W
+    cfg, T = pt.cfg, pt.T
+    t_h, t_m = W.roofline_time_s(cfg, T, pt.active)
+    t = ms * 1e-3
+    d = {"config": cfg.name, "recipe": cfg.recipe, "tokens": T, "active_experts": pt.active,
+         "us_per_layer": round(ms * 1e3, 2), "tokens_per_s": round(T / t, 1),
+         "hbm_GBps": round(W.algorithmic_bytes(cfg, T, pt.active) / t / 1e9, 1),
+         "TFLOPs": round(W.algorithmic_flops(cfg, T) / t / 1e12, 2),
+         "roofline_frac": round(max(t_h, t_m) / t, 4),
+         "bound": "hbm" if t_h >= t_m else "mfma",
+         "stage_us": {n: round(v * 1e3, 2) for n, v in zip(capi.STAGE_NAMES, stages)}}
+    return d
+
+
+def kernel_roofline(pt, stages):
+    from vllm_xpu_kernels import capi
+    from vllm_xpu_kernels import workloads as W
+    names = capi.STAGE_NAMES
+    gi = max((2, 3), key=lambda i: stages[i])
+    name = names[gi]
+    ms = stages[gi]
+    b, f = gemm_work(pt.cfg, pt.T, pt.active, name)
+    peak_tf = W.PEAK_TFLOPS[pt.cfg.recipe]
+    t_h, t_m = b / 8e12, f / (peak_tf * 1e12)
+    if t_h >= t_m:
+        ach = b / (ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(ach / 8000.0, 4), "traffic": None, "kernel": name,
+                "bytes_per_launch": int(b), "flops_per_launch": int(f),
+                "ms_per_launch": round(ms, 5)}
+    ach = f / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 2), "peak": peak_tf, "unit": "TFLOP/s",
+            "frac": round(ach / peak_tf, 4), "traffic": None, "kernel": name,
+            "bytes_per_launch": int(b), "flops_per_launch": int(f),
+            "ms_per_launch": round(ms, 5)}
+
+
+SWEEP = [("C1", 64), ("C2", 1), ("C2", 16), ("C2", 64), ("C2", 256), ("C2", 4096),
+         ("C3", 1), ("C3", 64), ("C3", 8192), ("C4", 2048), ("C5", 1), ("C5", 128),
+         ("C5", 4096)]
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--sweep", default="default",
+                    help="'none', 'default' or a list like C3:1,C3:8192")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs the MoE layer on a "
+              "single MI355X (no collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from vllm_xpu_kernels import workloads as W
+    dev = torch.device("cuda:0")
+    graph = not args.no_graph
+    cfg = W.CONFIGS[args.config]
+    log(f"bench: {args.config} ({cfg.name}) T={args.tokens} steps={args.steps} "
+        f"warmup={args.warmup} graph={graph} on {torch.cuda.get_device_name(0)}")
+
+    pt = Point(cfg, args.tokens, dev)
+    ms = pt.time_steps(args.steps, args.warmup, graph)
+    stages = pt.stage_times(args.steps)
+    head = summarize(pt, ms, stages)
+    log("headline:", json.dumps(head))
+    roof = kernel_roofline(pt, stages)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=64)
+        log("cpu baseline:", json.dumps(cpu))
+
+    sweep = []
+    if args.sweep != "none":
+        pts = SWEEP if args.sweep == "default" else [
+            (s.split(":")[0], int(s.split(":")[1])) for s in args.sweep.split(",")]
+        cache = {args.config: pt.w}
+        for name, T in pts:
+            if name == args.config and T == args.tokens:
+                sweep.append(head)
+                continue
+            c = W.CONFIGS[name]
+            if name not in cache:
+                for k in list(cache):
+                    if k != name:
+                        del cache[k]
+                torch.cuda.empty_cache()
+                cache[name] = W.make_weights(c, dev)
+            p = Point(c, T, dev, weights=cache[name])
+            m = p.time_steps(args.steps, args.warmup, graph)
+            st = p.stage_times(args.steps)
+            d = summarize(p, m, st)
+            d["kernel_roofline"] = kernel_roofline(p, st)
+            log("sweep:", json.dumps(d))
+            sweep.append(d)
+            del p
+
+    line = {
+        "metric": "fused-MoE layer tokens/s",
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"bf16": "bf16", "fp8block": "fp8e4m3", "mxfp4": "mxfp4xbf16"}[cfg.recipe],
+        "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights; random init)",
+        "config": {"workload": f"{args.config} {cfg.name} fused MoE layer, T={args.tokens}",
+                   "tokens": args.tokens, "hidden": cfg.hidden, "inter": cfg.inter,
+                   "experts": cfg.experts, "topk": cfg.topk, "recipe": cfg.recipe,
+                   "routing": cfg.routing, "graph": graph, "parallelism": "none (1 GPU)"},
+        "layer_roofline_frac": head["roofline_frac"],
+        "hbm_GBps": head["hbm_GBps"],
+        "TFLOPs": head["TFLOPs"],
+        "stage_us": head["stage_us"],
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

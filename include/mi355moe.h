@@ -1,0 +1,278 @@
+/*
+ * mi355moe.h — C ABI of the MI355X (gfx950) fused Mixture-of-Experts library.
+ *
+ * Plain pointers, sizes and enums only; no torch types.  Every function is
+ * asynchronous on the given HIP stream (`stream` is a hipStream_t, NULL = the
+ * null stream), never synchronises the host, and returns MI355MOE_OK (0) or a
+ * negative mi355moe_status; mi355moe_last_error() then returns a
+ * thread-local message whose substrings mirror the reference's TORCH_CHECK
+ * messages.  Device pointers are caller-allocated.  Functions that need
+ * scratch memory take a caller-provided workspace sized by the matching
+ * *_workspace_size query.
+ *
+ * Each entry point cites the reference interface it replaces (paths relative
+ * to the vllm-xpu-kernels repository root).
+ */
+#ifndef MI355MOE_H_
+#define MI355MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MI355MOE_OK = 0,
+  MI355MOE_ERR_INVALID = -1,     /* bad argument (shape, dtype, size)       */
+  MI355MOE_ERR_UNSUPPORTED = -2, /* valid but not implemented combination   */
+  MI355MOE_ERR_HIP = -3,         /* HIP runtime / launch failure            */
+  MI355MOE_ERR_WORKSPACE = -4    /* workspace too small                     */
+} mi355moe_status;
+
+typedef enum {
+  MI355MOE_F32 = 0,
+  MI355MOE_BF16 = 1,
+  MI355MOE_F16 = 2,
+  MI355MOE_I32 = 3,
+  MI355MOE_I64 = 4,
+  MI355MOE_U32 = 5,
+  MI355MOE_FP8E4M3 = 6, /* OCP float8_e4m3fn                              */
+  MI355MOE_U8 = 7,      /* raw bytes: packed e2m1 pairs or e8m0 scales    */
+  MI355MOE_I16 = 8
+} mi355moe_dtype;
+
+/* Weight recipes of the grouped GEMM / fused layer
+ * (vllm_xpu_kernels/fused_moe_interface.py:33-45). */
+typedef enum {
+  MI355MOE_RECIPE_BF16 = 0,     /* bf16 weights, bf16 activations          */
+  MI355MOE_RECIPE_FP8BLOCK = 1, /* e4m3 weights, fp32 128x128 block scales;
+                                   activations quantised 1x128 e4m3       */
+  MI355MOE_RECIPE_MXFP4 = 2     /* e2m1 weights packed along K, e8m0 scale
+                                   per 32 along K; bf16 activations       */
+} mi355moe_recipe;
+
+typedef enum {
+  MI355MOE_ACT_SILU = 0,      /* silu(x[:, :I]) * x[:, I:]                 */
+  MI355MOE_ACT_SWIGLUOAI = 1  /* interleaved gate/up, alpha 1.702, lim 7   */
+} mi355moe_activation;
+
+const char* mi355moe_last_error(void);
+int mi355moe_version(void);
+
+/* ---------------------------------------------------------------- routing */
+
+/* Replaces torch.ops._moe_C.topk_softmax (csrc/moe/torch_bindings.cpp:59-63,
+ * csrc/moe/topk.cpp:848-898).  gating [T,E] (f32/bf16/f16) -> weights f32
+ * [T,k], ids [T,k] (i32/i64/u32), token_expert_indices i32 [T,k].
+ * bias: optional f32 [E] added for selection only. */
+int mi355moe_topk_softmax(float* topk_weights, void* topk_indices,
+                          int indices_dtype, int32_t* token_expert_indices,
+                          const void* gating_output, int gating_dtype,
+                          int64_t num_tokens, int64_t num_experts,
+                          int64_t topk, int renormalize, const float* bias,
+                          void* stream);
+
+/* Replaces torch.ops._moe_C.topk_sigmoid (csrc/moe/torch_bindings.cpp:65-69,
+ * csrc/moe/topk.cpp:900-952). */
+int mi355moe_topk_sigmoid(float* topk_weights, void* topk_indices,
+                          int indices_dtype, int32_t* token_expert_indices,
+                          const void* gating_output, int gating_dtype,
+                          int64_t num_tokens, int64_t num_experts,
+                          int64_t topk, int renormalize, const float* bias,
+                          float routed_scaling_factor, void* stream);
+
+/* Replaces torch.ops._moe_C.grouped_topk (csrc/moe/torch_bindings.cpp:53-57,
+ * csrc/moe/grouped_topk.cpp:782-876).  scores / scores_with_bias [T,E] in
+ * `dtype` (f32/bf16/f16) -> values [T,k] (same dtype), ids i32 [T,k]. */
+int mi355moe_grouped_topk(void* topk_values, int32_t* topk_indices,
+                          const void* scores, const void* scores_with_bias,
+                          int dtype, int64_t num_tokens, int64_t num_experts,
+                          int64_t n_group, int64_t topk_group, int64_t topk,
+                          int renormalize, float routed_scaling_factor,
+                          void* stream);
+
+/* ----------------------------------------------------- alignment / permute */
+
+/* Replaces torch.ops._moe_C.moe_align_block_size
+ * (csrc/moe/torch_bindings.cpp:14-20, csrc/moe/moe_align_sum_kernels.cpp:
+ * 1034-1181).  Deterministic: a stable counting sort (tokens of one expert
+ * keep their flat order).  expert_map: optional i32 [num_experts]. */
+size_t mi355moe_moe_align_block_size_workspace_size(int64_t numel,
+                                                    int64_t num_experts);
+int mi355moe_moe_align_block_size(const void* topk_ids, int ids_dtype,
+                                  int64_t numel, int64_t num_experts,
+                                  int64_t block_size,
+                                  int32_t* sorted_token_ids,
+                                  int64_t max_num_tokens_padded,
+                                  int32_t* expert_ids,
+                                  int64_t max_num_m_blocks,
+                                  int32_t* num_tokens_post_pad,
+                                  const int32_t* expert_map,
+                                  void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* Replaces torch.ops._moe_C.remap_hidden_states
+ * (csrc/moe/torch_bindings.cpp:99-108, csrc/moe/remap_hidden_states.cpp:
+ * 418-568).  Stable order within an expert.  hidden [T,H] (elem_bytes per
+ * element), optional scales [T,S] (scale_bytes per element). */
+size_t mi355moe_remap_hidden_states_workspace_size(int64_t num_tokens,
+                                                   int64_t topk,
+                                                   int64_t local_experts);
+int mi355moe_remap_hidden_states(const void* hidden_states, int64_t elem_bytes,
+                                 const void* hidden_scales, int64_t scale_cols,
+                                 int64_t scale_bytes, void* remapped,
+                                 void* remapped_scales,
+                                 const int32_t* expert_map,
+                                 int32_t* rows_per_expert,
+                                 int32_t* unpermuted_row_to_permuted_row,
+                                 const void* topk_ids, int ids_dtype,
+                                 int64_t num_tokens, int64_t hidden_cols,
+                                 int64_t topk, int64_t total_experts,
+                                 int64_t local_experts, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Replaces torch.ops._moe_C.init_expert_map (csrc/moe/torch_bindings.cpp:
+ * 93-98, csrc/moe/init_expert_map.cpp:9-95). */
+int mi355moe_init_expert_map(int32_t* expert_map, int64_t num_experts,
+                             int64_t ep_rank, int64_t ep_size, void* stream);
+
+/* -------------------------------------------------------------- reductions */
+
+/* Replaces torch.ops._moe_C.moe_sum (csrc/moe/torch_bindings.cpp:7-10,
+ * csrc/moe/moe_align_sum_kernels.cpp:1224-1372).  input [T,k,H] -> out
+ * [T,H]; optional topk_ids [T,k] / expert_map skip padded or non-local
+ * slots. */
+int mi355moe_moe_sum(const void* input, void* output, int dtype,
+                     int64_t num_tokens, int64_t topk, int64_t hidden,
+                     const void* topk_ids, int ids_dtype,
+                     const int32_t* expert_map, int64_t expert_map_len,
+                     void* stream);
+
+/* Replaces torch.ops._moe_C.moe_gather (csrc/moe/torch_bindings.cpp:78-82,
+ * csrc/moe/moe_gather.cpp:161-204).  out[t] = sum_j w[t,j]*in[perm[t,j]]. */
+int mi355moe_moe_gather(void* output, const void* moe_output, int dtype,
+                        const float* topk_weights, const int32_t* perm,
+                        int64_t num_tokens, int64_t topk, int64_t hidden,
+                        void* stream);
+
+/* ------------------------------------------------------------ activations */
+
+/* Replaces torch.ops._C.silu_and_mul (csrc/torch_bindings.cpp:80-81,
+ * csrc/activation.cpp:492-499).  in [rows, 2d] -> out [rows, d]. */
+int mi355moe_silu_and_mul(void* out, const void* input, int dtype,
+                          int64_t rows, int64_t d, void* stream);
+
+/* Replaces torch.ops._C.swigluoai_and_mul (csrc/torch_bindings.cpp:187-191,
+ * csrc/activation.cpp:626-689). */
+int mi355moe_swigluoai_and_mul(void* out, const void* input, int dtype,
+                               int64_t rows, int64_t d, float alpha,
+                               float limit, void* stream);
+
+/* ----------------------------------------------------------- quantisation */
+
+/* Replaces torch.ops._C.per_token_group_fp8_quant (csrc/torch_bindings.cpp:
+ * 170-177, csrc/quantization/fp8/fp8_quant.cpp:724-881).  Row-major scales
+ * [rows, cols/group]. */
+int mi355moe_per_token_group_fp8_quant(const void* input, int dtype,
+                                       void* output_q, float* output_s,
+                                       int64_t rows, int64_t cols,
+                                       int64_t group_size, float eps,
+                                       float fp8_min, float fp8_max,
+                                       int scale_ue8m0, void* stream);
+
+/* Replaces torch.ops._C.per_token_group_quant_mxfp4 (csrc/torch_bindings.cpp:
+ * 180-184, csrc/quantization/fp4/mxfp4_quant.cpp:24-126). */
+int mi355moe_per_token_group_quant_mxfp4(const void* input, int dtype,
+                                         uint8_t* output_q, float* output_s,
+                                         int64_t rows, int64_t cols,
+                                         int64_t group_size, float eps,
+                                         void* stream);
+
+/* ------------------------------------------------------------ grouped GEMM */
+
+/* Replaces torch.ops._xpu_C.cutlass_grouped_gemm_interface
+ * (csrc/xpu/torch_bindings.cpp:46-53, csrc/xpu/grouped_gemm/
+ * grouped_gemm_interface.cpp:12-60).  Rows of expert e are contiguous in A
+ * and D (prefix sums of rows_per_expert, read on device).
+ *   recipe BF16:     A bf16 [M,K]; B bf16 [E,N,K]
+ *   recipe FP8BLOCK: A e4m3 [M,K] + a_scale f32 [M,K/128] (1x128 groups);
+ *                    B e4m3 [E,N,K] + b_scale f32 [E,N/128,K/128]
+ *   recipe MXFP4:    A bf16 [M,K]; B u8 [E,N,K/2] + b_scale e8m0 [E,N,K/32]
+ * bias: optional [E,N] in out_dtype; D [M,N] bf16 (or f16 for recipe BF16
+ * when a_dtype is F16). */
+size_t mi355moe_grouped_gemm_workspace_size(int64_t total_rows,
+                                            int64_t num_experts);
+/* Workspace including the on-the-fly 1x128 quantisation a 16-bit A needs
+ * under the fp8 recipe. */
+size_t mi355moe_grouped_gemm_workspace_size_k(int recipe, int a_dtype,
+                                              int64_t total_rows, int64_t K,
+                                              int64_t num_experts);
+int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
+                          const float* a_scale, const void* B,
+                          const void* b_scale, const void* bias, void* D,
+                          int out_dtype, const int32_t* rows_per_expert,
+                          int64_t total_rows, int64_t N, int64_t K,
+                          int64_t num_experts, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------- fused MoE layer */
+
+/* The whole XpuFusedMoe.apply path (vllm_xpu_kernels/fused_moe_interface.py:
+ * 273-419) in one call: align -> [act quant] -> w13 grouped GEMM with the
+ * activation (and fp8 re-quantisation) fused in its epilogue -> w2 grouped
+ * GEMM -> weighted top-k reduction.  Weights use the canonical layout:
+ * w13 [E, 2I, H] (gate rows 0..I-1, up rows I..2I-1; swigluoai weights are
+ * de-interleaved by the caller), w2 [E, H, I], K contiguous. */
+typedef struct {
+  int recipe;            /* mi355moe_recipe                                  */
+  int activation;        /* mi355moe_activation                              */
+  int act_dtype;         /* MI355MOE_BF16 (hidden_states and output)         */
+  int ids_dtype;         /* dtype of topk_ids: I32 or I64                    */
+  int64_t num_tokens;    /* T                                                */
+  int64_t hidden;        /* H                                                */
+  int64_t inter;         /* I                                                */
+  int64_t num_experts;   /* E (local experts)                                */
+  int64_t topk;          /* k                                                */
+  const void* hidden_states;  /* [T, H]                                      */
+  const float* topk_weights;  /* [T, k] f32                                  */
+  const void* topk_ids;       /* [T, k]                                      */
+  const int32_t* expert_map;  /* optional [expert_map_len]: global -> local  */
+  int64_t expert_map_len;
+  const void* w13;            /* per recipe                                  */
+  const void* w13_scale;
+  const void* w13_bias;       /* optional [E, 2I] bf16 (same row order)      */
+  const void* w2;
+  const void* w2_scale;
+  const void* w2_bias;        /* optional [E, H] bf16                        */
+  float gemm1_clamp_limit;    /* <= 0: off                                   */
+  float swiglu_alpha;         /* swigluoai alpha (1.702)                     */
+  float swiglu_limit;         /* swigluoai limit (7.0)                       */
+  void* output;               /* [T, H]                                      */
+} mi355moe_fused_moe_args;
+
+size_t mi355moe_fused_moe_workspace_size(const mi355moe_fused_moe_args* args);
+int mi355moe_fused_moe(const mi355moe_fused_moe_args* args, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* Stage timing (no counterpart in the reference, whose benchmark brackets
+ * each op with torch.xpu.Event, benchmark/src/fused_moe_interface_.py:144-226).
+ * mi355moe_fused_moe_timed records HIP events on `stream` around its five
+ * stages (align, activation quant, w13 GEMM, w2 GEMM, top-k reduction) into
+ * slot `step` of the timer; mi355moe_timer_stage_ms waits for that step and
+ * returns the five stage durations in milliseconds. */
+#define MI355MOE_FUSED_STAGES 5
+typedef struct mi355moe_timer_s* mi355moe_timer;
+int mi355moe_timer_create(int max_steps, mi355moe_timer* out);
+int mi355moe_timer_destroy(mi355moe_timer timer);
+int mi355moe_fused_moe_timed(const mi355moe_fused_moe_args* args,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream, mi355moe_timer timer, int step);
+int mi355moe_timer_stage_ms(mi355moe_timer timer, int step, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355MOE_H_ */

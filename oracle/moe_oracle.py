@@ -1,0 +1,567 @@
+"""CPU restatement of the reference's fused-MoE path (TEST INFRASTRUCTURE ONLY).
+
+Every function restates the reference algorithm named in its docstring
+(paths relative to the reference repository root).  It is used as the checker
+by ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` and nothing else; the product library never calls it.
+
+Pinning (how each function is checked independently of a retyped formula):
+
+* ``topk_softmax`` / ``topk_sigmoid``   brute-force stable sort, softmax
+  monotonicity, invariants (ids unique, in range, ordered)  -> pinned
+* ``grouped_topk``                      brute force over every subset of groups
+  on small cases + invariants                               -> pinned
+* ``moe_align_block_size``              docstring KAT (tests/ops/
+  moe_align_block_size_ops.py:56-69), golden stable-sort restatement of
+  tests/test_moe_align_block_size.py:97-183                 -> pinned
+* ``silu_and_mul`` / ``swigluoai_and_mul`` closed forms at special points
+  (x=0, clamp limits) and torch.nn.functional.silu           -> pinned
+* ``per_token_group_fp8_quant``         exact e4m3 grid (all 254 finite codes),
+  round-trip and scale closed form                          -> pinned
+* ``per_token_group_quant_mxfp4``       known-value KAT
+  (tests/test_mxfp4_quant.py:113-142)                       -> pinned
+* ``to_mxfp4``                          RCEIL/RNE special cases, e2m1 grid
+  round trip                                                -> pinned
+* ``moe_sum`` / ``moe_gather``          fixed-order fp32 sums vs float64 sum  -> pinned
+* ``remap_hidden_states``               un-permute invariant (tests/fused_moe/
+  test_remap_hidden_states.py:204-217)                      -> pinned
+* ``grouped_gemm`` / ``fused_moe``      all-finite-e4m3 identity KAT
+  (tests/fused_moe/test_grouped_gemm.py:275-307), E=1 special case vs
+  torch.matmul, per-expert brute force                      -> pinned
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+import torch
+
+FP8_MAX = 448.0
+FP8_MIN_SCALE = 1.0 / (448.0 * 512.0)   # csrc/quantization/fp8/quant_utils.h:35-37
+FP4_MAX = 6.0
+E2M1_VALUES = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+
+# ----------------------------------------------------------------------------
+# Routing
+# ----------------------------------------------------------------------------
+def _stable_topk_desc(vals: torch.Tensor, k: int):
+    """Descending top-k with ties to the lower index (tests/ops/topk_op.py:11-13,
+    csrc/moe/topk.cpp:536-545)."""
+    v, i = torch.sort(vals, dim=-1, descending=True, stable=True)
+    return v[..., :k], i[..., :k]
+
+
+def topk_softmax(gating: torch.Tensor, topk: int, renormalize: bool,
+                 bias: Optional[torch.Tensor] = None):
+    """tests/ops/topk_op.py:16-35 with the kernel's renorm guard
+    (csrc/moe/topk.cpp:573-583) and token_expert_indices (topk.cpp:563).
+
+    Returns (weights f32 [T,k], ids i32 [T,k], token_expert_indices i32 [T,k]).
+    """
+    T, E = gating.shape
+    p = torch.softmax(gating.float(), dim=-1)
+    sel = p + bias.float().unsqueeze(0) if bias is not None else p
+    _, ids = _stable_topk_desc(sel, topk)
+    w = p.gather(1, ids)
+    if renormalize:
+        s = w.sum(dim=-1, keepdim=True)
+        w = w * (1.0 / torch.where(s > 0, s, torch.ones_like(s)))
+    tei = (torch.arange(topk, dtype=torch.int32).unsqueeze(0) * T +
+           torch.arange(T, dtype=torch.int32).unsqueeze(1))
+    return w.float(), ids.int(), tei
+
+
+def sigmoid_typed(x: torch.Tensor) -> torch.Tensor:
+    """sigmoid in fp32 rounded to the input dtype (csrc/moe/topk.cpp:17-23)."""
+    s = 1.0 / (1.0 + torch.exp(-x.float()))
+    return s.to(x.dtype).float()
+
+
+def topk_sigmoid(gating: torch.Tensor, topk: int, renormalize: bool,
+                 bias: Optional[torch.Tensor] = None,
+                 routed_scaling_factor: float = 1.0):
+    """tests/ops/topk_op.py:38-59 with csrc/moe/topk.cpp:573-583 scaling."""
+    T, E = gating.shape
+    p = sigmoid_typed(gating)
+    sel = p + bias.float().unsqueeze(0) if bias is not None else p
+    _, ids = _stable_topk_desc(sel, topk)
+    w = p.gather(1, ids)
+    scale = torch.full((T, 1), float(routed_scaling_factor))
+    if renormalize:
+        s = w.sum(dim=-1, keepdim=True)
+        scale = scale / torch.where(s > 0, s, torch.ones_like(s))
+    w = w * scale
+    tei = (torch.arange(topk, dtype=torch.int32).unsqueeze(0) * T +
+           torch.arange(T, dtype=torch.int32).unsqueeze(1))
+    return w.float(), ids.int(), tei
+
+
+def grouped_topk(scores: torch.Tensor, scores_with_bias: torch.Tensor,
+                 n_group: int, topk_group: int, topk: int, renormalize: bool,
+                 routed_scaling_factor: float):
+    """Kernel semantics of csrc/moe/grouped_topk.cpp:405-695 (golden
+    tests/ops/grouped_topk_op.py:11-64).
+
+    * group score = top1 + top2 of scores_with_bias inside the group, summed
+      in fp32 and stored in the input dtype (:433-446);
+    * keep ``topk_group`` groups by (score desc, group asc) (:556-623);
+    * ids = top-k of scores_with_bias over the kept groups, (value desc,
+      id asc) (:588-625, ``is_better_than`` :36-45);
+    * weights = scores[ids] / (1e-20 + sum) (if renormalize) * rsf, rounded
+      to the input dtype (:636-668); all-(-inf) group scores fall back to
+      ids 0..k-1 with 1/k (:669-674).
+
+    Returns (values [T,k] in scores.dtype, ids int32 [T,k]) ordered by
+    descending scores_with_bias.
+    """
+    dt = scores.dtype
+    T, E = scores.shape
+    epg = E // n_group
+    sb = scores_with_bias.float()
+    sbv = sb.view(T, n_group, epg)
+    top2 = torch.topk(sbv, 2 if epg >= 2 else 1, dim=-1).values
+    gs = top2.sum(-1) if epg >= 2 else top2[..., 0] * 2
+    gs = gs.to(dt).float()
+    vals = torch.empty(T, topk, dtype=torch.float32)
+    ids = torch.empty(T, topk, dtype=torch.int32)
+    for t in range(T):
+        g = gs[t].clone()
+        g[~torch.isfinite(g)] = -math.inf
+        order = sorted(range(n_group), key=lambda i: (-g[i].item(), i))
+        kept = order[:topk_group]
+        if g[kept[-1]].item() == -math.inf and g[order[0]].item() == -math.inf:
+            ids[t] = torch.arange(topk, dtype=torch.int32)
+            vals[t] = 1.0 / topk
+            continue
+        cand = []
+        for gi in sorted(kept):
+            for e in range(gi * epg, (gi + 1) * epg):
+                v = sb[t, e].item()
+                cand.append((-(v if math.isfinite(v) else -math.inf), e))
+        cand.sort()
+        sel = [e for _, e in cand[:topk]]
+        w = scores[t, sel].float()
+        if renormalize:
+            ssum = np.float32(1e-20)
+            for x in w.tolist():
+                ssum = np.float32(ssum + np.float32(x))
+            w = w / float(ssum) * routed_scaling_factor
+        else:
+            w = w * routed_scaling_factor
+        ids[t] = torch.tensor(sel, dtype=torch.int32)
+        vals[t] = w
+    return vals.to(dt), ids
+
+
+# ----------------------------------------------------------------------------
+# Alignment / permutation
+# ----------------------------------------------------------------------------
+def align_buffer_sizes(numel: int, num_experts: int, block_size: int,
+                       pad_sorted_ids: bool = False):
+    """Caller-side buffer sizes (tests/ops/moe_align_block_size_ops.py:71-86)."""
+    mx = numel + num_experts * (block_size - 1)
+    if pad_sorted_ids:
+        mx = (mx + block_size - 1) // block_size * block_size
+    if numel < num_experts:
+        mx = min(numel * block_size, mx)
+    return mx, (mx + block_size - 1) // block_size
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int,
+                         block_size: int, max_num_tokens_padded: int,
+                         max_num_m_blocks: int,
+                         expert_map: Optional[torch.Tensor] = None):
+    """Stable counting sort of the flattened ids (golden
+    tests/test_moe_align_block_size.py:97-183; kernel id filtering
+    csrc/moe/moe_align_sum_kernels.cpp:196-206, expert-map remap :330-336,
+    tail expert ids = 0 :266-272).
+
+    Ids outside [0, num_experts) and experts mapped to -1 are dropped.
+    Returns numpy int32 arrays (sorted_token_ids, expert_ids, ntp[1]).
+    """
+    flat = topk_ids.reshape(-1).to(torch.int64).numpy()
+    numel = flat.size
+    local = flat.copy()
+    valid = (flat >= 0) & (flat < num_experts)
+    if expert_map is not None:
+        em = expert_map.to(torch.int64).numpy()
+        local = np.where(valid, em[np.clip(flat, 0, len(em) - 1)], -1)
+        valid = valid & (local >= 0)
+    counts = np.bincount(local[valid], minlength=num_experts)[:num_experts]
+    padded = (counts + block_size - 1) // block_size * block_size
+    cumsum = np.concatenate([[0], np.cumsum(padded)]).astype(np.int64)
+    sorted_ids = np.full(max_num_tokens_padded, numel, dtype=np.int32)
+    expert_ids = np.zeros(max_num_m_blocks, dtype=np.int32)
+    order = np.argsort(np.where(valid, local, num_experts), kind="stable")
+    pos = cumsum[:-1].copy()
+    for i in order[:int(valid.sum())]:
+        e = local[i]
+        sorted_ids[pos[e]] = i
+        pos[e] += 1
+    for e in range(num_experts):
+        expert_ids[cumsum[e] // block_size:cumsum[e + 1] // block_size] = e
+    ntp = np.array([cumsum[-1]], dtype=np.int32)
+    return sorted_ids, expert_ids, ntp
+
+
+def remap_hidden_states(hidden: torch.Tensor, topk_ids: torch.Tensor,
+                        local_experts_num: int,
+                        expert_map: Optional[torch.Tensor] = None,
+                        scales: Optional[torch.Tensor] = None):
+    """tests/fused_moe/test_remap_hidden_states.py:38-83 (stable order: the
+    destination of slot (t, j) is prefix[e] + rank of (t, j) among earlier
+    slots of the same expert in row-major order).
+
+    Returns (remapped [T*k,H], remapped_scales or None, rows_per_expert [E]
+    int32, perm [T,k] int32 (-1 when not local)).
+    """
+    T, k = topk_ids.shape
+    ids = topk_ids.to(torch.int64)
+    if expert_map is not None:
+        ids = expert_map.to(torch.int64)[ids]
+    counts = torch.bincount(ids[ids >= 0].flatten(),
+                            minlength=local_experts_num)[:local_experts_num]
+    prefix = torch.cat([torch.zeros(1, dtype=torch.int64), counts.cumsum(0)])
+    off = torch.zeros(local_experts_num, dtype=torch.int64)
+    perm = torch.full((T, k), -1, dtype=torch.int32)
+    out = torch.zeros((T * k,) + tuple(hidden.shape[1:]), dtype=hidden.dtype)
+    out_s = None
+    if scales is not None:
+        out_s = torch.zeros((T * k,) + tuple(scales.shape[1:]),
+                            dtype=scales.dtype)
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            if e < 0:
+                continue
+            d = int(prefix[e] + off[e])
+            off[e] += 1
+            out[d] = hidden[t]
+            if scales is not None:
+                out_s[d] = scales[t]
+            perm[t, j] = d
+    return out, out_s, counts.to(torch.int32), perm
+
+
+def init_expert_map(num_experts: int, ep_rank: int, ep_size: int):
+    """csrc/moe/init_expert_map.cpp:40-60: map[g] = g - rank*E if local."""
+    g = torch.arange(num_experts * ep_size, dtype=torch.int32)
+    lo = ep_rank * num_experts
+    return torch.where((g >= lo) & (g < lo + num_experts), g - lo,
+                       torch.full_like(g, -1))
+
+
+# ----------------------------------------------------------------------------
+# Reductions
+# ----------------------------------------------------------------------------
+def moe_sum(inp: torch.Tensor, topk_ids: Optional[torch.Tensor] = None,
+            expert_map: Optional[torch.Tensor] = None):
+    """csrc/moe/moe_align_sum_kernels.cpp:585-664: out[t] = T(sum_j float(in[t,j]))
+    in fixed j order, skipping id<0 and expert_map[id]<0."""
+    T, k, H = inp.shape
+    acc = torch.zeros(T, H, dtype=torch.float32)
+    for j in range(k):
+        x = inp[:, j].float()
+        if topk_ids is not None:
+            ids = topk_ids[:, j].to(torch.int64)
+            ok = ids >= 0
+            if expert_map is not None:
+                em = expert_map.to(torch.int64)
+                ok = ok & (em[ids.clamp(min=0)] >= 0)
+            x = x * ok.unsqueeze(1).float()
+        acc = acc + x
+    return acc.to(inp.dtype)
+
+
+def moe_gather(moe_output: torch.Tensor, topk_weights: torch.Tensor,
+               perm: torch.Tensor):
+    """csrc/moe/moe_gather.cpp:9-98: y[t] = T(sum_j w[t,j] * float(G[perm[t,j]]))
+    in fixed j order, skipping perm == -1."""
+    T, k = perm.shape
+    H = moe_output.shape[1]
+    acc = torch.zeros(T, H, dtype=torch.float32)
+    for j in range(k):
+        p = perm[:, j].to(torch.int64)
+        ok = p >= 0
+        rows = moe_output[p.clamp(min=0)].float()
+        acc = acc + torch.where(ok.unsqueeze(1),
+                                topk_weights[:, j].float().unsqueeze(1) * rows,
+                                torch.zeros_like(rows))
+    return acc.to(moe_output.dtype)
+
+
+# ----------------------------------------------------------------------------
+# Activations
+# ----------------------------------------------------------------------------
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """csrc/activation.cpp:16-20,81-87: out = T(float(T(silu_f32(g))) * float(u)),
+    g = x[..., :d], u = x[..., d:]."""
+    d = x.shape[-1] // 2
+    g = x[..., :d].float()
+    u = x[..., d:].float()
+    s = (g / (1.0 + torch.exp(-g))).to(x.dtype).float()
+    return (s * u).to(x.dtype)
+
+
+def swigluoai_and_mul(x: torch.Tensor, alpha: float = 1.702,
+                      limit: float = 7.0) -> torch.Tensor:
+    """csrc/activation.cpp:277-295: interleaved gate/up, fp32, one rounding."""
+    g = x[..., 0::2].float().clamp(max=limit)
+    u = x[..., 1::2].float().clamp(min=-limit, max=limit)
+    glu = g * (1.0 / (1.0 + torch.exp(-g * alpha)))
+    return ((u + 1.0) * glu).to(x.dtype)
+
+
+# ----------------------------------------------------------------------------
+# Quantisation
+# ----------------------------------------------------------------------------
+def per_token_group_fp8_quant(x: torch.Tensor, group_size: int,
+                              eps: float = 1e-10, scale_ue8m0: bool = False):
+    """csrc/quantization/fp8/fp8_quant.cpp:209-255 + quant_utils.h:35-37,61-71:
+    amax = max(eps, max|x|); s = max(amax/448, 1/(448*512)); optional
+    s = 2^ceil(log2(max(|s|,1e-10))); q = e4m3(clamp(x * (1/s), +-448)).
+    Returns (q float8_e4m3fn [M,K], s float32 [M, K/group])."""
+    M, K = x.shape
+    xg = x.float().reshape(M, K // group_size, group_size)
+    amax = torch.clamp(xg.abs().amax(-1), min=eps)
+    s = torch.clamp(amax / FP8_MAX, min=FP8_MIN_SCALE)
+    if scale_ue8m0:
+        s = torch.exp2(torch.ceil(torch.log2(torch.clamp(s.abs(), min=1e-10))))
+    inv = 1.0 / s
+    q = torch.clamp(xg * inv.unsqueeze(-1), -FP8_MAX, FP8_MAX)
+    return q.reshape(M, K).to(torch.float8_e4m3fn), s
+
+
+def dequant_fp8_groups(q: torch.Tensor, s: torch.Tensor, group_size: int):
+    """vllm_xpu_kernels/moe_utils.py:143-148 (dequant_fp8_block_act)."""
+    M, K = q.shape
+    return (q.float().reshape(M, K // group_size, group_size) *
+            s.unsqueeze(-1)).reshape(M, K)
+
+
+def fp4_code(a: torch.Tensor) -> torch.Tensor:
+    """Strict-midpoint e2m1 code of csrc/quantization/fp4/mxfp4_quant.h:17-25
+    (round-half-toward-zero in magnitude); sign bit from x < 0."""
+    b = [0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0]
+    m = a.abs()
+    code = torch.zeros_like(a, dtype=torch.int32)
+    for t in b:
+        code += (m > t).int()
+    return code | ((a < 0).int() << 3)
+
+
+def per_token_group_quant_mxfp4(x: torch.Tensor, group_size: int = 32,
+                                eps: float = 1e-10):
+    """csrc/quantization/fp4/mxfp4_quant.h:37-134: s = 2^ceil(log2(max(amax/6,eps)))
+    with amax starting at eps; codes of clamp(x/s, +-6); byte = c[2i+1]<<4|c[2i].
+    Returns (q uint8 [M, K/2], s float32 [M, K/group])."""
+    M, K = x.shape
+    xg = x.float().reshape(M, K // group_size, group_size)
+    amax = torch.clamp(xg.abs().amax(-1), min=eps)
+    s = torch.exp2(torch.ceil(torch.log2(torch.clamp((amax / FP4_MAX).abs(),
+                                                     min=eps))))
+    v = torch.clamp(xg * (1.0 / s).unsqueeze(-1), -FP4_MAX, FP4_MAX)
+    c = fp4_code(v).reshape(M, K)
+    q = (c[:, 0::2] | (c[:, 1::2] << 4)).to(torch.uint8)
+    return q, s
+
+
+def _e2m1_rne(v: torch.Tensor) -> torch.Tensor:
+    """Round-to-nearest-even onto the e2m1 grid (OCP MX v1.0 sec. 5.3.3);
+    ties go to the code with an even mantissa bit."""
+    grid = torch.tensor(E2M1_VALUES, dtype=torch.float32)
+    m = v.abs().clamp(max=FP4_MAX)
+    d = (m.unsqueeze(-1) - grid).abs()
+    best = d.argmin(-1)
+    dmin = d.gather(-1, best.unsqueeze(-1)).squeeze(-1)
+    # tie: two grid points at the same distance -> pick the even code
+    nxt = (best + 1).clamp(max=7)
+    tie = (d.gather(-1, nxt.unsqueeze(-1)).squeeze(-1) == dmin) & (nxt != best)
+    best = torch.where(tie & (best % 2 == 1), nxt, best)
+    return best.int() | ((v < 0).int() << 3)
+
+
+def to_mxfp4(w: torch.Tensor):
+    """MXFP4 weight generator, semantics of to_mxfp(format="mxfp4")
+    (tests/ops/mx_utils.py:277-353): RCEIL e8m0 exponent per 32 along the last
+    dim, data cast to bf16 then RNE e2m1, low nibble = even element.
+    Returns (packed uint8 [..., K/2], e8m0 uint8 [..., K/32])."""
+    shp = w.shape
+    K = shp[-1]
+    x = w.float().reshape(-1, K // 32, 32)
+    amax = x.abs().amax(-1, keepdim=True)
+    desc = amax / FP4_MAX
+    e = (torch.clamp(torch.ceil(torch.log2(desc)), min=-127, max=127) + 127)
+    e = torch.where(torch.isnan(desc), torch.full_like(e, 255), e)
+    e_u8 = e.to(torch.uint8)
+    dsc = torch.where(e == 0, torch.ones_like(e), torch.exp2(127 - e))
+    v = torch.clamp(x * dsc, -FP4_MAX, FP4_MAX).to(torch.bfloat16).float()
+    c = _e2m1_rne(v).reshape(-1, K)
+    q = (c[:, 0::2] | (c[:, 1::2] << 4)).to(torch.uint8)
+    return q.reshape(shp[:-1] + (K // 2,)), e_u8.reshape(shp[:-1] + (K // 32,))
+
+
+def dequant_mxfp4(q: torch.Tensor, e8m0: torch.Tensor) -> torch.Tensor:
+    """LUT dequant of tests/fused_moe/test_fused_moe.py:79-116 (e8m0 via
+    (e<<7) as bf16, so e=0 -> 0) == 2^(e-127) for 0<e<255."""
+    lut = torch.tensor(E2M1_VALUES + [-v for v in E2M1_VALUES],
+                       dtype=torch.float32)
+    qi = q.to(torch.int64)
+    lo = lut[qi & 0xF]
+    hi = lut[qi >> 4]
+    vals = torch.stack([lo, hi], dim=-1).reshape(q.shape[:-1] +
+                                                 (q.shape[-1] * 2,))
+    sc = (e8m0.to(torch.int32) << 7).to(torch.int16).view(
+        torch.bfloat16).float()
+    sc = sc.repeat_interleave(32, dim=-1)
+    return vals * sc
+
+
+def fp8_block_quant_weight(w: torch.Tensor, eps: float = 1e-6):
+    """128x128 block quant of the last two dims (tests/ops/fp8_quant_op.py:16-78):
+    s = clamp(amax/448, min=eps), q = e4m3(w / s).
+    Returns (q float8_e4m3fn, s float32 [..., N/128, K/128])."""
+    *lead, N, K = w.shape
+    x = w.float().reshape(*lead, N // 128, 128, K // 128, 128)
+    amax = x.abs().amax(dim=(-3, -1))
+    s = torch.clamp(amax / FP8_MAX, min=eps)
+    q = (x / s.unsqueeze(-2).unsqueeze(-1)).reshape(*lead, N, K)
+    return q.to(torch.float8_e4m3fn), s
+
+
+def dequant_fp8_block_weight(q: torch.Tensor, s: torch.Tensor):
+    """[N,K] e4m3 weights with [N/128, K/128] scales -> fp32 (kernel convention
+    of csrc/xpu/grouped_gemm/xe_2/grouped_gemm_xe2_interface.hpp:362-376)."""
+    N, K = q.shape
+    x = q.float().reshape(N // 128, 128, K // 128, 128)
+    return (x * s.reshape(N // 128, 1, K // 128, 1)).reshape(N, K)
+
+
+# ----------------------------------------------------------------------------
+# Grouped GEMM and the fused layer
+# ----------------------------------------------------------------------------
+def dequant_weight(recipe: str, w_e: torch.Tensor, s_e) -> torch.Tensor:
+    """[N, K] fp32 weights of one expert, per recipe
+    (vllm_xpu_kernels/moe_utils.py:189-202)."""
+    if recipe == "bf16":
+        return w_e.float()
+    if recipe == "fp8block":
+        return dequant_fp8_block_weight(w_e, s_e)
+    if recipe == "mxfp4":
+        return dequant_mxfp4(w_e, s_e)
+    raise ValueError(recipe)
+
+
+def qdq_act(recipe: str, x: torch.Tensor) -> torch.Tensor:
+    """Activation quant-dequant round trip of the recipe
+    (vllm_xpu_kernels/moe_utils.py:176-187): fp8block -> 1x128 e4m3; bf16 and
+    mxfp4 (w4a16 kernel semantics) -> unchanged."""
+    if recipe == "fp8block":
+        q, s = per_token_group_fp8_quant(x, 128)
+        return dequant_fp8_groups(q, s, 128)
+    return x.float()
+
+
+def grouped_gemm(recipe: str, a: torch.Tensor, w: torch.Tensor, w_scale,
+                 bias, rows_per_expert, out_dtype=torch.bfloat16):
+    """cutlass_grouped_gemm_interface semantics (csrc/xpu/grouped_gemm/
+    grouped_gemm_interface.cpp:12-60; per-expert loop of
+    vllm_xpu_kernels/moe_utils.py:319-363): rows of expert e are contiguous;
+    D = T(A_qdq @ deq(W_e)^T + b_e) with fp32 accumulation.  ``w`` is [E,N,K]
+    (nk) for every recipe (mxfp4 packed along K)."""
+    M = a.shape[0]
+    E = w.shape[0]
+    N = w.shape[1]
+    out = torch.zeros(M, N, dtype=out_dtype)
+    off = 0
+    for e in range(E):
+        n = int(rows_per_expert[e])
+        if n == 0:
+            continue
+        x = qdq_act(recipe, a[off:off + n])
+        we = dequant_weight(recipe, w[e], None if w_scale is None else w_scale[e])
+        y = x @ we.t()
+        if bias is not None:
+            y = y + bias[e].float()
+        out[off:off + n] = y.to(out_dtype)
+        off += n
+    return out
+
+
+def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
+              w2, w2_scale, w2_bias, topk_weights: torch.Tensor,
+              topk_ids: torch.Tensor, activation: str = "silu",
+              expert_map: Optional[torch.Tensor] = None,
+              gemm1_clamp_limit: Optional[float] = None,
+              experts=None):
+    """XpuFusedMoe.apply semantics (vllm_xpu_kernels/fused_moe_interface.py:
+    319-419, reference path moe_utils.py:236-403, rounding points of
+    SURVEY Appendix A):
+
+      G1  = T(qdq(x) @ deq(W13_e)^T + b13_e)            per slot
+      act = silu_and_mul(G1) | swigluoai_and_mul(G1)
+      G2  = T(qdq(act) @ deq(W2_e)^T + b2_e)
+      y   = T(sum_j w[t,j] * float(G2[t,j]))            fixed j order
+
+    Weights are [E, N, K] (nk); for mxfp4 packed uint8 [E, N, K/2] with e8m0
+    [E, N, K/32].  The expert loop dequantises one expert at a time.
+    ``experts`` optionally restricts the computation to a subset of expert ids
+    (the CPU-baseline sample); slots of other experts contribute zero.
+    """
+    T, H = hidden.shape
+    k = topk_ids.shape[1]
+    dt = hidden.dtype
+    ids = topk_ids.to(torch.int64)
+    if expert_map is not None:
+        ids = expert_map.to(torch.int64)[ids]
+    E = w13.shape[0]
+    I2 = w13.shape[1]
+    g2 = torch.zeros(T * k, H, dtype=dt)
+    flat = ids.reshape(-1)
+    todo = range(E) if experts is None else experts
+    xq_all = qdq_act(recipe, hidden)
+    for e in todo:
+        slots = (flat == e).nonzero().flatten()
+        if slots.numel() == 0:
+            continue
+        toks = slots // k
+        x = xq_all[toks]
+        w1 = dequant_weight(recipe, w13[e],
+                            None if w13_scale is None else w13_scale[e])
+        g1 = x @ w1.t()
+        del w1
+        if w13_bias is not None:
+            g1 = g1 + w13_bias[e].float()
+        g1 = g1.to(dt)
+        if gemm1_clamp_limit is not None and gemm1_clamp_limit > 0:
+            I = I2 // 2
+            g1 = g1.clone()
+            g1[:, :I] = g1[:, :I].clamp(max=gemm1_clamp_limit)
+            g1[:, I:] = g1[:, I:].clamp(min=-gemm1_clamp_limit,
+                                        max=gemm1_clamp_limit)
+        if activation == "silu":
+            act = silu_and_mul(g1)
+        elif activation == "swigluoai":
+            act = swigluoai_and_mul(g1)
+        else:
+            raise ValueError(activation)
+        aq = qdq_act(recipe, act)
+        wd = dequant_weight(recipe, w2[e],
+                            None if w2_scale is None else w2_scale[e])
+        y = aq @ wd.t()
+        del wd
+        if w2_bias is not None:
+            y = y + w2_bias[e].float()
+        g2[slots] = y.to(dt)
+    perm = torch.arange(T * k, dtype=torch.int32).reshape(T, k)
+    perm = torch.where(ids >= 0, perm, torch.full_like(perm, -1))
+    return moe_gather(g2, topk_weights.float(), perm)
+
+
+def active_experts(topk_ids: torch.Tensor, num_experts: int) -> int:
+    """|A| of the roofline: experts with at least one routed slot."""
+    f = topk_ids.reshape(-1).to(torch.int64)
+    f = f[(f >= 0) & (f < num_experts)]
+    return int(torch.unique(f).numel())

@@ -1,0 +1,149 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+symbol include/mi355moe.h declares, rejects invalid arguments before any
+device work, and the torch op schemas match the reference verbatim."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mi355moe.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(mi355moe_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from vllm_xpu_kernels import _ops
+    return _ops.lib
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_version_and_error_plumbing(lib):
+    assert lib.mi355moe_version() == 1
+    rc = lib.mi355moe_moe_sum(None, None, 1, ctypes.c_int64(4), ctypes.c_int64(2),
+                              ctypes.c_int64(8), None, 3, ctypes.c_void_p(16),
+                              ctypes.c_int64(4), None)
+    assert rc == -1
+    assert b"expert_map requires topk_ids" in lib.mi355moe_last_error()
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda L: L.mi355moe_topk_softmax(None, None, 3, None, None, 0,
+                                       ctypes.c_int64(4), ctypes.c_int64(8),
+                                       ctypes.c_int64(9), 1, None, None),
+     b"topk must be in"),
+    (lambda L: L.mi355moe_topk_softmax(None, None, 3, None, None, 0,
+                                       ctypes.c_int64(4), ctypes.c_int64(2048),
+                                       ctypes.c_int64(2), 1, None, None),
+     b"num_experts > 1024"),
+    (lambda L: L.mi355moe_grouped_topk(None, None, None, None, 0, ctypes.c_int64(4),
+                                       ctypes.c_int64(256), ctypes.c_int64(33),
+                                       ctypes.c_int64(4), ctypes.c_int64(8), 1,
+                                       ctypes.c_float(1.0), None),
+     b"n_group"),
+    (lambda L: L.mi355moe_moe_align_block_size(None, 3, ctypes.c_int64(8),
+                                               ctypes.c_int64(1024), ctypes.c_int64(16),
+                                               None, ctypes.c_int64(0), None,
+                                               ctypes.c_int64(0), None, None, None,
+                                               ctypes.c_size_t(0), None),
+     b"padded_num_experts must be less than 1024"),
+    (lambda L: L.mi355moe_per_token_group_fp8_quant(None, 1, None, None,
+                                                    ctypes.c_int64(2), ctypes.c_int64(100),
+                                                    ctypes.c_int64(128), ctypes.c_float(1e-10),
+                                                    ctypes.c_float(-448), ctypes.c_float(448),
+                                                    0, None),
+     b"divisible by group_size"),
+    (lambda L: L.mi355moe_grouped_gemm(1, None, 1, None, None, None, None, None, 1, None,
+                                       ctypes.c_int64(4), ctypes.c_int64(204),
+                                       ctypes.c_int64(256), ctypes.c_int64(2), None,
+                                       ctypes.c_size_t(0), None),
+     b"N must be a multiple of 8"),
+    (lambda L: L.mi355moe_grouped_gemm(1, None, 1, None, None, None, None, None, 1, None,
+                                       ctypes.c_int64(4), ctypes.c_int64(192),
+                                       ctypes.c_int64(256), ctypes.c_int64(2), None,
+                                       ctypes.c_size_t(0), None),
+     b"% 128"),
+])
+def test_invalid_arguments_rejected_before_launch(lib, call, msg):
+    rc = call(lib)
+    assert rc < 0
+    assert msg in lib.mi355moe_last_error()
+
+
+def test_fused_moe_workspace_query_and_validation(lib):
+    from vllm_xpu_kernels import _ops  # noqa: F401
+
+    class Args(ctypes.Structure):
+        _fields_ = [("recipe", ctypes.c_int), ("activation", ctypes.c_int),
+                    ("act_dtype", ctypes.c_int), ("ids_dtype", ctypes.c_int),
+                    ("num_tokens", ctypes.c_int64), ("hidden", ctypes.c_int64),
+                    ("inter", ctypes.c_int64), ("num_experts", ctypes.c_int64),
+                    ("topk", ctypes.c_int64), ("hidden_states", ctypes.c_void_p),
+                    ("topk_weights", ctypes.c_void_p), ("topk_ids", ctypes.c_void_p),
+                    ("expert_map", ctypes.c_void_p), ("expert_map_len", ctypes.c_int64),
+                    ("w13", ctypes.c_void_p), ("w13_scale", ctypes.c_void_p),
+                    ("w13_bias", ctypes.c_void_p), ("w2", ctypes.c_void_p),
+                    ("w2_scale", ctypes.c_void_p), ("w2_bias", ctypes.c_void_p),
+                    ("gemm1_clamp_limit", ctypes.c_float), ("swiglu_alpha", ctypes.c_float),
+                    ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p)]
+
+    a = Args(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=64,
+             hidden=7168, inter=2048, num_experts=256, topk=8)
+    lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t
+    ws = lib.mi355moe_fused_moe_workspace_size(ctypes.byref(a))
+    assert ws > 64 * 7168
+    a.hidden = 7100
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"% 128" in lib.mi355moe_last_error()
+    a.hidden = 7168
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"need scales" in lib.mi355moe_last_error()
+
+
+# schema strings as written in the reference's registration files
+# (csrc/moe/torch_bindings.cpp, csrc/torch_bindings.cpp, csrc/xpu/torch_bindings.cpp)
+REFERENCE_SCHEMAS = {
+    "_moe_C::moe_sum": "moe_sum(Tensor input, Tensor! output, Tensor? topk_ids, Tensor? expert_map) -> ()",
+    "_moe_C::moe_align_block_size": "moe_align_block_size(Tensor topk_ids, int num_experts, int block_size, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, Tensor? maybe_expert_map) -> ()",
+    "_moe_C::topk_softmax": "topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias) -> ()",
+    "_moe_C::topk_sigmoid": "topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias, float routed_scaling_factor) -> ()",
+    "_moe_C::grouped_topk": "grouped_topk(Tensor scores, Tensor scores_with_bias, int n_group, int topk_group, int topk, bool renormalize, float routed_scaling_factor) -> (Tensor, Tensor)",
+    "_moe_C::moe_gather": "moe_gather(Tensor! output, Tensor moe_output, Tensor topk_weights, Tensor unpermuted_row_to_permuted_row, int num_experts) -> ()",
+    "_moe_C::init_expert_map": "init_expert_map(Tensor expert_map, int num_experts, int ep_rank, int ep_size) -> ()",
+    "_moe_C::remap_hidden_states": "remap_hidden_states(Tensor hidden_states, Tensor? hidden_states_scales, Tensor remapped_hidden_states, Tensor? remapped_hidden_states_scales, Tensor? expert_map, Tensor rows_per_expert, Tensor unpermuted_row_to_permuted_row, Tensor topk_ids, int total_experts_num, int local_experts_num) -> ()",
+    "_C::silu_and_mul": "silu_and_mul(Tensor! result, Tensor input) -> ()",
+    "_C::swigluoai_and_mul": "swigluoai_and_mul(Tensor! out, Tensor input, float alpha=1.702, float limit=7.0) -> ()",
+    "_C::per_token_group_fp8_quant": "per_token_group_fp8_quant(Tensor input, Tensor! output_q, Tensor! output_s, int group_size, float eps, float fp8_min, float fp8_max, bool scale_ue8m0, bool dummy_is_scale_transposed, bool dummy_is_tma_aligned ) -> ()",
+    "_C::per_token_group_quant_mxfp4": "per_token_group_quant_mxfp4(Tensor input, Tensor! output_q, Tensor! output_s, int group_size, float eps) -> ()",
+    "_xpu_C::cutlass_grouped_gemm_interface": "cutlass_grouped_gemm_interface(Tensor ptr_A, Tensor? ptr_A_scale, Tensor ptr_B, Tensor? ptr_B_scale, Tensor? ptr_bias, Tensor ptr_D, Tensor rows_per_expert, int N, int K, int num_experts) -> Tensor",
+}
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_SCHEMAS))
+def test_op_schemas_match_reference(name):
+    import vllm_xpu_kernels  # noqa: F401
+    ns, op = name.split("::")
+    packet = getattr(getattr(torch.ops, ns), op)
+    ref = torch._C.parse_schema(ns + "::" + REFERENCE_SCHEMAS[name])
+    assert str(packet.default._schema) == str(ref)
+
+
+def test_no_cpu_kernel_registered():
+    """The ops exist only for GPU tensors: no silent CPU path."""
+    import vllm_xpu_kernels  # noqa: F401
+    x = torch.zeros(2, 8)
+    out = torch.empty(2, 4)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops._C.silu_and_mul(out, x)

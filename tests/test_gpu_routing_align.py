@@ -1,0 +1,179 @@
+"""GPU parity: routing and token->expert alignment are bit-exact against the
+CPU oracle on the same inputs."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from vllm_xpu_kernels import ops
+    return ops
+
+
+@pytest.mark.parametrize("T", [1, 33, 64])
+@pytest.mark.parametrize("E", [16, 128, 192, 512, 1024])
+@pytest.mark.parametrize("k", [2, 8])
+@pytest.mark.parametrize("renorm", [True, False])
+@pytest.mark.parametrize("has_bias", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_topk_softmax(dev, T, E, k, renorm, has_bias, dtype):
+    g = torch.Generator().manual_seed(T * 7919 + E * 31 + k)
+    logits = torch.randn(T, E, generator=g).to(dtype)
+    bias = torch.randn(E, generator=g) if has_bias else None
+    w, ids, tei = _ops().topk_softmax(logits.to(dev), k, renorm,
+                                      bias.to(dev) if has_bias else None)
+    rw, rids, rtei = O.topk_softmax(logits, k, renorm, bias)
+    assert torch.equal(ids.cpu(), rids)
+    assert torch.equal(tei.cpu(), rtei)
+    torch.testing.assert_close(w.cpu(), rw, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("T", [1, 64])
+@pytest.mark.parametrize("E", [16, 256])
+@pytest.mark.parametrize("renorm", [True, False])
+@pytest.mark.parametrize("rsf", [1.0, 2.5])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_topk_sigmoid(dev, T, E, renorm, rsf, dtype):
+    g = torch.Generator().manual_seed(T + E)
+    logits = torch.randn(T, E, generator=g).to(dtype)
+    bias = torch.randn(E, generator=g)
+    w, ids, _ = _ops().topk_sigmoid(logits.to(dev), 8, renorm, bias.to(dev),
+                                    routed_scaling_factor=rsf)
+    rw, rids, _ = O.topk_sigmoid(logits, 8, renorm, bias, rsf)
+    assert torch.equal(ids.cpu(), rids)
+    torch.testing.assert_close(w.cpu(), rw, rtol=2e-6, atol=1e-7)
+
+
+def test_topk_softmax_int64_ids_and_ties(dev):
+    logits = torch.tensor([[1.0, 3.0, 3.0, 0.0, 3.0, -1.0, 3.0, 2.0]])
+    w, ids, _ = _ops().topk_softmax(logits.to(dev), 3, False,
+                                    indices_type=torch.int64)
+    assert ids.dtype == torch.int64
+    assert ids.cpu().tolist() == [[1, 2, 4]]
+
+
+@pytest.mark.parametrize("T", [1, 64, 512])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_grouped_topk_deepseek_shape(dev, T, dtype, renorm):
+    """C3 routing: sigmoid scores, +bias N(0,0.01), 8 groups keep 4, top-8,
+    rsf 2.5."""
+    g = torch.Generator().manual_seed(T)
+    logits = torch.randn(T, 256, generator=g)
+    bias = torch.randn(256, generator=g) * 0.01
+    s = logits.sigmoid().to(dtype)
+    sb = (s.float() + bias).to(dtype)
+    v, ids = _ops().grouped_topk(s.to(dev), sb.to(dev), 8, 4, 8, renorm, 2.5)
+    rv, rids = O.grouped_topk(s, sb, 8, 4, 8, renorm, 2.5)
+    assert torch.equal(ids.cpu(), rids)
+    assert v.dtype == dtype
+    torch.testing.assert_close(v.cpu().float(), rv.float(), rtol=4e-6 if dtype == torch.float32 else 8e-3, atol=1e-7)
+
+
+def test_grouped_topk_full_size_invariants(dev):
+    """T=8192 (C3 prefill): every id lies in one of the 4 kept groups and the
+    kept groups are the top-4 by top-2 sums; ids unique per token."""
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(8192, 256, generator=g)
+    bias = torch.randn(256, generator=g) * 0.01
+    s = logits.sigmoid()
+    sb = s + bias
+    v, ids = _ops().grouped_topk(s.to(dev), sb.to(dev), 8, 4, 8, True, 2.5)
+    ids = ids.cpu().long()
+    gs = sb.view(8192, 8, 32).topk(2, dim=-1).values.sum(-1)
+    kept = torch.sort(gs, dim=-1, descending=True, stable=True).indices[:, :4]
+    grp = ids // 32
+    assert all(set(grp[t].tolist()) <= set(kept[t].tolist()) for t in range(0, 8192, 97))
+    assert (torch.sort(ids, dim=-1).values[:, 1:] != torch.sort(ids, dim=-1).values[:, :-1]).all()
+    torch.testing.assert_close(v.cpu().sum(-1), torch.full((8192,), 2.5), rtol=1e-5, atol=1e-5)
+    # sampled exact parity at full size
+    rv, rids = O.grouped_topk(s[:256], sb[:256], 8, 4, 8, True, 2.5)
+    assert torch.equal(ids[:256].int(), rids)
+
+
+# ---------------------------------------------------------------- alignment
+ALIGN_CASES = [(1, 1, 32, 32), (3, 2, 160, 128), (256, 16, 256, 32),
+               (2256, 32, 257, 128), (4096, 2, 32, 128), (4096, 8, 256, 16),
+               (8192, 8, 256, 64)]
+
+
+@pytest.mark.parametrize("m,topk,E,bs", ALIGN_CASES)
+@pytest.mark.parametrize("id_dtype", [torch.int32, torch.int64])
+def test_moe_align_block_size_bit_exact(dev, m, topk, E, bs, id_dtype):
+    g = torch.Generator().manual_seed(m + 13 * E + bs)
+    ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(m)]).to(id_dtype)
+    srt, eids, ntp = _ops().moe_align_block_size(ids.to(dev), bs, E)
+    mx, nb = O.align_buffer_sizes(ids.numel(), E, bs)
+    rs, re, rn = O.moe_align_block_size(ids, E, bs, mx, nb)
+    assert ntp.cpu().tolist() == rn.tolist()
+    assert np.array_equal(eids.cpu().numpy(), re)
+    assert np.array_equal(srt.cpu().numpy(), rs)
+
+
+def test_moe_align_zipf_skew_c4(dev):
+    from vllm_xpu_kernels import workloads as W
+    cfg = W.CONFIGS["C4"]
+    logits = W.make_router_logits(cfg, 2048, dev)
+    _, ids = W.route(cfg, logits)
+    cnt = torch.bincount(ids.flatten().long(), minlength=128).sort(descending=True).values
+    assert 0.45 < float(cnt[:13].sum()) / ids.numel() < 0.55
+    srt, eids, ntp = _ops().moe_align_block_size(ids, 64, 128)
+    mx, nb = O.align_buffer_sizes(ids.numel(), 128, 64)
+    rs, re, rn = O.moe_align_block_size(ids.cpu(), 128, 64, mx, nb)
+    assert np.array_equal(srt.cpu().numpy(), rs) and np.array_equal(eids.cpu().numpy(), re)
+
+
+def test_moe_align_expert_map(dev):
+    E, m, k, bs = 8, 32, 4, 64
+    g = torch.Generator().manual_seed(5)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(m)]).int()
+    em = torch.full((E,), -1, dtype=torch.int32)
+    em[0::2] = torch.arange(4, dtype=torch.int32)
+    srt, eids, ntp = _ops().moe_align_block_size(ids.to(dev), bs, E, em.to(dev),
+                                                 ignore_invalid_experts=True)
+    mx, nb = O.align_buffer_sizes(ids.numel(), E, bs)
+    rs, re, rn = O.moe_align_block_size(ids, E, bs, mx, nb, expert_map=em)
+    assert ntp.cpu().tolist() == rn.tolist()
+    assert np.array_equal(eids.cpu().numpy(), re)
+    assert np.array_equal(srt.cpu().numpy(), rs)
+
+
+def test_moe_align_deterministic(dev):
+    g = torch.Generator().manual_seed(42)
+    ids = torch.randint(0, 32, (4096, 8), generator=g, dtype=torch.int32).to(dev)
+    outs = [_ops().moe_align_block_size(ids, 64, 32) for _ in range(5)]
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,k,E,with_map", [(32, 1, 16, False), (257, 8, 64, True),
+                                             (1024, 4, 128, False)])
+def test_remap_hidden_states(dev, T, k, E, with_map):
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, 128, generator=g).to(torch.bfloat16)
+    total = E * 2 if with_map else E
+    ids = torch.stack([torch.randperm(total, generator=g)[:k] for _ in range(T)]).int()
+    em = None
+    if with_map:
+        em = torch.full((total,), -1, dtype=torch.int32)
+        em[E:] = torch.arange(E, dtype=torch.int32)
+    scales = torch.randn(T, 1, generator=g)
+    out, osc, rows, perm = _ops().remap_hidden_states(
+        x.to(dev), ids.to(dev), total, E, em.to(dev) if em is not None else None,
+        scales.to(dev))
+    ro, rsc, rrows, rperm = O.remap_hidden_states(x, ids, E, em, scales)
+    assert torch.equal(rows.cpu(), rrows)
+    assert torch.equal(perm.cpu(), rperm)
+    valid = int(rrows.sum())
+    assert torch.equal(out.cpu()[:valid], ro[:valid])
+    assert torch.equal(osc.cpu()[:valid], rsc[:valid])
+
+
+def test_init_expert_map(dev):
+    m = _ops().init_expert_map(32, 2, 4, dev)
+    assert torch.equal(m.cpu(), O.init_expert_map(32, 2, 4))

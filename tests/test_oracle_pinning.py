@@ -1,0 +1,375 @@
+"""Pins the CPU oracle (oracle/moe_oracle.py) against the reference's
+known-answer vectors, closed forms and independent brute force.  CPU only."""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+
+# ------------------------------------------------------------------ routing
+def test_topk_softmax_ties_go_to_lower_index():
+    g = torch.tensor([[1.0, 3.0, 3.0, 0.0, 3.0]])
+    w, ids, tei = O.topk_softmax(g, 3, renormalize=False)
+    assert ids.tolist() == [[1, 2, 4]]
+    assert tei.tolist() == [[0, 1, 2]]
+
+
+def test_topk_softmax_matches_logit_order_and_closed_form():
+    torch.manual_seed(0)
+    T, E, k = 33, 192, 8
+    g = torch.randn(T, E)
+    w, ids, tei = O.topk_softmax(g, k, renormalize=True)
+    # softmax is monotone: ids are the stable top-k of the logits themselves
+    ref_ids = torch.sort(g, dim=-1, descending=True, stable=True).indices[:, :k]
+    assert torch.equal(ids.long(), ref_ids)
+    for t in range(T):
+        m = max(g[t].tolist())
+        ex = [math.exp(float(g[t, i]) - m) for i in ids[t].tolist()]
+        s = sum(ex)
+        assert np.allclose(w[t].numpy(), [x / s for x in ex], rtol=1e-6)
+    assert torch.equal(tei, (torch.arange(k) * T).unsqueeze(0) +
+                       torch.arange(T).unsqueeze(1))
+
+
+def test_topk_softmax_bias_selects_but_does_not_weight():
+    g = torch.tensor([[0.0, 0.0, 0.0, 0.0]])
+    bias = torch.tensor([0.0, 1.0, 0.0, 2.0])
+    w, ids, _ = O.topk_softmax(g, 2, renormalize=False, bias=bias)
+    assert ids.tolist() == [[3, 1]]
+    assert np.allclose(w.numpy(), [[0.25, 0.25]])
+
+
+def test_topk_sigmoid_rounds_to_input_dtype_and_scales():
+    g = torch.tensor([[0.3, -1.2, 2.0, 0.7]], dtype=torch.bfloat16)
+    w, ids, _ = O.topk_sigmoid(g, 2, renormalize=True, routed_scaling_factor=2.5)
+    assert ids.tolist() == [[2, 3]]
+    sig = [float(torch.tensor(1 / (1 + math.exp(-float(x))), dtype=torch.bfloat16))
+           for x in g[0].float().tolist()]
+    s = sig[2] + sig[3]
+    assert np.allclose(w.numpy(), [[sig[2] * 2.5 / s, sig[3] * 2.5 / s]], rtol=1e-6)
+
+
+def _grouped_brute(s, sb, n_group, topk_group, k):
+    E = s.shape[0]
+    epg = E // n_group
+    gs = []
+    for g in range(n_group):
+        v = sorted(sb[g * epg:(g + 1) * epg].tolist(), reverse=True)
+        gs.append(v[0] + v[1])
+    best = None
+    # brute force: the kept set is the lexicographically best subset by
+    # (sorted scores desc, then lowest group ids)
+    for combo in itertools.combinations(range(n_group), topk_group):
+        key = (sorted([gs[c] for c in combo], reverse=True),
+               [-c for c in combo])
+        if best is None or key > best[0]:
+            best = (key, combo)
+    kept = best[1]
+    cand = [(float(sb[e]), -e) for g in kept for e in range(g * epg, (g + 1) * epg)]
+    cand.sort(reverse=True)
+    return [-c[1] for c in cand[:k]]
+
+
+def test_grouped_topk_brute_force():
+    torch.manual_seed(1)
+    T, E, n_group, topk_group, k = 16, 64, 8, 4, 6
+    logits = torch.randn(T, E)
+    s = logits.sigmoid()
+    sb = s + 0.1 * torch.randn(E)
+    v, ids = O.grouped_topk(s, sb, n_group, topk_group, k, True, 2.5)
+    for t in range(T):
+        exp_ids = _grouped_brute(s[t], sb[t], n_group, topk_group, k)
+        assert ids[t].tolist() == exp_ids
+        ws = s[t, exp_ids].double()
+        assert np.allclose(v[t].double().numpy(),
+                           (ws / (1e-20 + ws.sum()) * 2.5).numpy(), rtol=1e-6)
+
+
+def test_grouped_topk_group_ties_lower_group_wins():
+    # 4 groups of 2; groups 1 and 2 tie for the second slot
+    sb = torch.tensor([[0.9, 0.8, 0.5, 0.5, 0.5, 0.5, 0.1, 0.1]])
+    v, ids = O.grouped_topk(sb.clone(), sb, 4, 2, 2, False, 1.0)
+    assert ids.tolist() == [[0, 1]]
+    v, ids = O.grouped_topk(sb.clone(), sb, 4, 2, 4, False, 1.0)
+    assert ids.tolist() == [[0, 1, 2, 3]]
+
+
+# ---------------------------------------------------------------- alignment
+def test_moe_align_docstring_kat():
+    """tests/ops/moe_align_block_size_ops.py:56-69 (self-consistent for
+    num_experts = 5: experts 1..4 used)."""
+    ids = torch.tensor([[2, 3, 4], [1, 2, 4], [1, 3, 4], [1, 2, 3]])
+    mx, nb = O.align_buffer_sizes(12, 5, 4)
+    srt, eids, ntp = O.moe_align_block_size(ids, 5, 4, mx, nb)
+    assert srt[:16].tolist() == [3, 6, 9, 12, 0, 4, 10, 12, 1, 7, 11, 12, 2, 5, 8, 12]
+    assert (srt[16:] == 12).all()
+    assert eids.tolist()[:4] == [1, 2, 3, 4] and (eids[4:] == 0).all()
+    assert ntp.tolist() == [16]
+
+
+def _golden_align(topk_ids, block_size, num_experts, mx, nb, expert_map=None):
+    """Restatement of the reference golden tests/test_moe_align_block_size.py:97-183."""
+    flat = topk_ids.flatten()
+    sorted_e, order = torch.sort(flat, stable=True)
+    tok = torch.arange(flat.numel(), dtype=torch.int32)[order]
+    out = torch.full((mx,), flat.numel(), dtype=torch.int32)
+    eids = torch.zeros(nb, dtype=torch.int32)
+    pos = blk = 0
+    for e in range(num_experts):
+        if expert_map is not None and expert_map[e] == -1:
+            continue
+        t = tok[sorted_e == e]
+        if t.numel() == 0:
+            continue
+        padded = (t.numel() + block_size - 1) // block_size * block_size
+        out[pos:pos + t.numel()] = t
+        eids[blk:blk + padded // block_size] = (e if expert_map is None
+                                                else int(expert_map[e]))
+        pos += padded
+        blk += padded // block_size
+    return out, eids, pos
+
+
+@pytest.mark.parametrize("m,topk,E,bs", [(1, 1, 32, 32), (3, 2, 160, 128),
+                                         (256, 16, 32, 32), (257, 8, 257, 128),
+                                         (64, 4, 8, 16)])
+def test_moe_align_vs_reference_golden(m, topk, E, bs):
+    g = torch.Generator().manual_seed(m * 1000 + E)
+    ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(m)])
+    mx, nb = O.align_buffer_sizes(ids.numel(), E, bs)
+    srt, eids, ntp = O.moe_align_block_size(ids, E, bs, mx, nb)
+    g_srt, g_eids, g_ntp = _golden_align(ids, bs, E, mx, nb)
+    assert ntp[0] == g_ntp
+    assert torch.equal(torch.from_numpy(eids), g_eids)
+    assert torch.equal(torch.from_numpy(srt), g_srt)
+
+
+def test_moe_align_expert_map_vs_golden():
+    g = torch.Generator().manual_seed(7)
+    E, m, k, bs = 8, 32, 4, 64
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(m)])
+    em = torch.full((E,), -1, dtype=torch.int32)
+    for i, e in enumerate(range(0, E, 2)):
+        em[e] = i
+    mx, nb = O.align_buffer_sizes(ids.numel(), E, bs)
+    srt, eids, ntp = O.moe_align_block_size(ids, E, bs, mx, nb, expert_map=em)
+    g_srt, g_eids, g_ntp = _golden_align(ids, bs, E, mx, nb, expert_map=em)
+    assert ntp[0] == g_ntp
+    assert torch.equal(torch.from_numpy(eids), g_eids)
+    assert torch.equal(torch.from_numpy(srt), g_srt)
+
+
+def test_remap_unpermute_invariant():
+    torch.manual_seed(3)
+    T, H, k, E = 40, 16, 4, 8
+    x = torch.randn(T, H)
+    ids = torch.stack([torch.randperm(E)[:k] for _ in range(T)])
+    out, _, rows, perm = O.remap_hidden_states(x, ids, E)
+    assert rows.tolist() == torch.bincount(ids.flatten(), minlength=E).tolist()
+    for t in range(T):
+        for j in range(k):
+            assert torch.equal(out[perm[t, j]], x[t])
+    # rows of expert e are contiguous and in [prefix[e], prefix[e+1])
+    pre = torch.cat([torch.zeros(1, dtype=torch.long), rows.long().cumsum(0)])
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            assert pre[e] <= perm[t, j] < pre[e + 1]
+
+
+def test_init_expert_map_closed_form():
+    m = O.init_expert_map(4, 1, 3)
+    assert m.tolist() == [-1, -1, -1, -1, 0, 1, 2, 3, -1, -1, -1, -1]
+
+
+# ---------------------------------------------------------------- reductions
+def test_moe_sum_and_gather_vs_float64():
+    torch.manual_seed(4)
+    T, k, H = 7, 3, 33
+    x = torch.randn(T, k, H)
+    ids = torch.randint(0, 6, (T, k))
+    ids[:, -1] = -1
+    em = torch.tensor([0, 1, 2, -1, -1, 3], dtype=torch.int32)
+    y = O.moe_sum(x, ids, em)
+    mask = (ids >= 0) & (em[ids.clamp(min=0)] >= 0)
+    ref = (x.double() * mask.unsqueeze(-1)).sum(1)
+    assert torch.allclose(y.double(), ref, atol=1e-5)
+    w = torch.rand(T, k)
+    perm = torch.randperm(T * k).reshape(T, k).int()
+    perm[0, 1] = -1
+    g = torch.randn(T * k, H)
+    y = O.moe_gather(g, w, perm)
+    ref = torch.zeros(T, H, dtype=torch.float64)
+    for t in range(T):
+        for j in range(k):
+            if perm[t, j] >= 0:
+                ref[t] += float(w[t, j]) * g[perm[t, j]].double()
+    assert torch.allclose(y.double(), ref, atol=1e-5)
+
+
+# --------------------------------------------------------------- activations
+def test_silu_and_mul_closed_form():
+    x = torch.tensor([[0.0, 1.0, -2.0, 3.0, 5.0, 7.0]])
+    y = O.silu_and_mul(x)
+    silu = torch.nn.functional.silu(torch.tensor([0.0, 1.0, -2.0]))
+    assert torch.allclose(y, silu * torch.tensor([3.0, 5.0, 7.0]), rtol=1e-6)
+    assert y[0, 0] == 0.0
+
+
+def test_swigluoai_special_points():
+    # gate clamped at +7 from above only, up clamped to [-7, 7]
+    x = torch.tensor([[10.0, 10.0, -3.0, -10.0, 0.0, 2.0]])
+    y = O.swigluoai_and_mul(x)
+    sig = lambda v: 1 / (1 + math.exp(-v))
+    exp = [(7 + 1) * 7 * sig(7 * 1.702), (-7 + 1) * -3 * sig(-3 * 1.702), 0.0]
+    assert np.allclose(y[0].numpy(), exp, rtol=1e-6)
+
+
+# -------------------------------------------------------------- quantisation
+def test_fp8_group_quant_all_finite_e4m3_round_trip():
+    codes = torch.tensor([c for c in range(256) if c not in (0x7F, 0xFF)],
+                         dtype=torch.uint8)
+    vals = codes.view(torch.float8_e4m3fn).float()
+    # groups of 127 codes + one 448 so every group has amax 448 -> scale 1
+    row = torch.cat([vals[:127], torch.tensor([448.0]), vals[127:],
+                     torch.tensor([448.0])]).unsqueeze(0)
+    q, s = O.per_token_group_fp8_quant(row, 128)
+    assert torch.equal(s, torch.ones(1, 2))
+    assert torch.equal(q.view(torch.uint8)[0, :127], codes[:127])
+    assert torch.equal(q.view(torch.uint8)[0, 128:255], codes[127:])
+
+
+def test_fp8_group_quant_scale_closed_form():
+    x = torch.zeros(2, 128)
+    x[0, 5] = 3.0
+    q, s = O.per_token_group_fp8_quant(x, 128)
+    assert s[0, 0].item() == pytest.approx(3.0 / 448.0, rel=1e-7)
+    assert s[1, 0].item() == pytest.approx(1.0 / (448.0 * 512.0), rel=1e-7)
+    assert float(q[0, 5].float()) == 448.0
+    q, s = O.per_token_group_fp8_quant(x, 128, scale_ue8m0=True)
+    assert s[0, 0].item() == 2.0 ** math.ceil(math.log2(3.0 / 448.0))
+
+
+MXFP4_KNOWN = {0.5: (0.125, 6), 1.0: (0.25, 6), 1.5: (0.25, 7), 2.0: (0.5, 6),
+               3.0: (0.5, 7), 4.0: (1.0, 6), 6.0: (1.0, 7)}
+
+
+@pytest.mark.parametrize("val", sorted(MXFP4_KNOWN))
+def test_mxfp4_quant_known_values(val):
+    """tests/test_mxfp4_quant.py:113-142, expected scale/code derived by hand."""
+    x = torch.zeros(1, 32)
+    x[0, 0] = val
+    q, s = O.per_token_group_quant_mxfp4(x)
+    es, ec = MXFP4_KNOWN[val]
+    assert s[0, 0].item() == es
+    assert int(q[0, 0]) & 0xF == ec
+    assert (q[0, 1:] == 0).all()
+
+
+def test_to_mxfp4_rne_ties_and_grid():
+    # block max 6 -> e8m0 127 (scale 1); midpoints tie to the even code
+    v = torch.tensor([6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.75, 0.5,
+                      1.0, 1.5, 2.0, 3.0, 4.0, -6.0] + [0.0] * 16)
+    q, e = O.to_mxfp4(v.unsqueeze(0))
+    assert e.tolist() == [[127]]
+    codes = torch.stack([q[0] & 0xF, q[0] >> 4], -1).flatten().tolist()
+    assert codes[:16] == [7, 0, 2, 2, 4, 4, 6, 6, 0xA, 1, 2, 3, 4, 5, 6, 0xF]
+    # decode round trip is exact on the grid
+    d = O.dequant_mxfp4(q, e)
+    assert torch.equal(d[0, 9:16], torch.tensor([0.5, 1, 1.5, 2, 3, 4, -6.0]))
+
+
+# ----------------------------------------------------------- GEMM and layer
+def test_grouped_gemm_fp8_block_all_finite_e4m3_kat():
+    """tests/fused_moe/test_grouped_gemm.py:275-307: identity A x every finite
+    e4m3 code x block scales {0.5, 2.0} is reproduced bit-exactly."""
+    n, k = 128, 256
+    a = torch.eye(k, dtype=torch.bfloat16)
+    codes = torch.tensor([c for c in range(256) if c not in (0x7F, 0xFF)],
+                         dtype=torch.uint8)
+    b = codes.repeat((n * k + 253) // 254)[:n * k].reshape(1, n, k)
+    b = b.view(torch.float8_e4m3fn)
+    scales = torch.tensor([[[0.5, 2.0]]])
+    out = O.grouped_gemm("fp8block", a, b, scales, None,
+                         torch.tensor([k], dtype=torch.int32))
+    ref = (b.float() * scales.repeat_interleave(128, 1).repeat_interleave(128, 2))
+    assert torch.equal(out.float(), ref[0].t().to(torch.bfloat16).float())
+
+
+def test_grouped_gemm_single_expert_is_matmul():
+    torch.manual_seed(5)
+    a = torch.randn(9, 64).to(torch.bfloat16)
+    w = (torch.randn(1, 32, 64) * 0.1).to(torch.bfloat16)
+    bias = torch.randn(1, 32).to(torch.bfloat16)
+    out = O.grouped_gemm("bf16", a, w, None, bias, [9])
+    ref = (a.float() @ w[0].float().t() + bias[0].float()).to(torch.bfloat16)
+    assert torch.equal(out, ref)
+
+
+def _reference_test_golden(x, w13, b13, w2, b2, weights, ids, k):
+    """Restatement of the reference test golden
+    tests/fused_moe/test_fused_moe.py:119-176 (argsort / bincount /
+    scatter_reduce structure), weights in nk layout."""
+    flat_i = ids.view(-1)
+    flat_w = weights.view(-1, 1)
+    cache = torch.zeros_like(x)
+    idxs = flat_i.argsort()
+    counts = flat_i.bincount().numpy()
+    ends = counts.cumsum()
+    tok = idxs // k
+    for e, end in enumerate(ends):
+        st = 0 if e == 0 else ends[e - 1]
+        if st == end:
+            continue
+        xt = x[tok[st:end]]
+        w1, w3 = torch.split(w13[e], w13.shape[1] // 2, dim=0)
+        g = xt.float() @ w1.t().float()
+        u = xt.float() @ w3.t().float()
+        if b13 is not None:
+            b1, b3 = b13[e].chunk(2)
+            g, u = g + b1.float(), u + b3.float()
+        o = (torch.nn.functional.silu(g) * u) @ w2[e].t().float()
+        if b2 is not None:
+            o = o + b2[e].float()
+        o = o.to(x.dtype)
+        o.mul_(flat_w[idxs[st:end]])
+        cache.scatter_reduce_(0, tok[st:end].view(-1, 1).repeat(1, x.shape[-1]),
+                              o, reduce="sum")
+    return cache
+
+
+def test_fused_moe_oracle_vs_reference_golden():
+    torch.manual_seed(6)
+    T, H, I, E, k = 24, 64, 32, 6, 2
+    x = torch.randn(T, H).to(torch.bfloat16) / 4
+    w13 = (torch.randn(E, 2 * I, H) / 8).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I) / 8).to(torch.bfloat16)
+    b13 = (torch.randn(E, 2 * I) / 16).to(torch.bfloat16)
+    b2 = (torch.randn(E, H) / 16).to(torch.bfloat16)
+    scores = torch.randn(T, E)
+    w, ids = torch.topk(scores, k, dim=-1)
+    y = O.fused_moe("bf16", x, w13, None, b13, w2, None, b2, w, ids)
+    ref = _reference_test_golden(x, w13, b13, w2, b2, w, ids, k)
+    torch.testing.assert_close(y.float(), ref.float(), rtol=2e-2, atol=2e-2)
+
+
+def test_fused_moe_oracle_fp8block_close_to_dequant_fp32():
+    """fp8block = dequantised fp32 layer up to activation quantisation noise."""
+    torch.manual_seed(8)
+    T, H, I, E, k = 12, 256, 128, 4, 2
+    x = torch.randn(T, H).to(torch.bfloat16)
+    w13m = torch.randn(E, 2 * I, H) * 0.02
+    w2m = torch.randn(E, H, I) * 0.02
+    q13, s13 = O.fp8_block_quant_weight(w13m)
+    q2, s2 = O.fp8_block_quant_weight(w2m)
+    scores = torch.randn(T, E)
+    w, ids, _ = O.topk_softmax(scores, k, True)
+    y = O.fused_moe("fp8block", x, q13, s13, None, q2, s2, None, w, ids)
+    d13 = torch.stack([O.dequant_fp8_block_weight(q13[e], s13[e]) for e in range(E)])
+    d2 = torch.stack([O.dequant_fp8_block_weight(q2[e], s2[e]) for e in range(E)])
+    ref = O.fused_moe("bf16", x, d13, None, None, d2, None, None, w, ids)
+    torch.testing.assert_close(y.float(), ref.float(), rtol=0.1, atol=0.05)

@@ -1,0 +1,383 @@
+// Token -> expert alignment: a deterministic, stable counting sort of the
+// flattened top-k expert ids in one 1024-thread workgroup.
+//
+// The 16 wavefronts each own a contiguous chunk of the flat ids, so
+// "chunk order, then rank inside the chunk" is flat order.  Per-chunk expert
+// counts live in LDS (16 x E ints); a block-wide scan turns them into each
+// chunk's first output slot per expert; the scatter pass ranks the lanes of
+// every 64-element step that carry the same expert with 11 ballots (one per
+// key bit), so no atomics decide the order.  Replaces the reference's
+// count + device-atomic scatter (csrc/moe/moe_align_sum_kernels.cpp:135-455),
+// whose within-expert order is not deterministic.
+#include "common.h"
+
+namespace mi355 {
+namespace {
+
+constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kMaxKeys = 1024;
+constexpr uint32_t kInvalidKey = 2047u;  // 11 bits, never a valid key
+
+template <typename Id>
+__device__ __forceinline__ uint32_t load_key(const Id* ids, int64_t i,
+                                             int64_t id_bound,
+                                             const int32_t* map,
+                                             int num_keys) {
+  int64_t v = static_cast<int64_t>(ids[i]);
+  if (v < 0 || v >= id_bound) return kInvalidKey;
+  if (map) v = map[v];
+  if (v < 0 || v >= num_keys) return kInvalidKey;
+  return static_cast<uint32_t>(v);
+}
+
+// Block-wide exclusive scan of one int per thread (1024 threads).
+__device__ int block_exclusive_scan(int v, int* s_wave_tot, int& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_wave_tot[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int t = lane < kSortWaves ? s_wave_tot[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      int y = __shfl_up(t, o, 64);
+      if (lane >= o) t += y;
+    }
+    if (lane < kSortWaves) s_wave_tot[lane] = t;  // inclusive wave totals
+  }
+  __syncthreads();
+  int before = wave > 0 ? s_wave_tot[wave - 1] : 0;
+  total = s_wave_tot[kSortWaves - 1];
+  __syncthreads();
+  return before + x - v;
+}
+
+template <typename Id>
+__global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
+    const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
+    const int32_t* __restrict__ map, int num_keys, int block_size,
+    int32_t* __restrict__ sorted_ids, int64_t max_padded,
+    int32_t* __restrict__ expert_ids, int64_t max_blocks,
+    int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
+    int32_t* __restrict__ counts_out, int32_t pad_value) {
+  __shared__ int s_cnt[kSortWaves][kMaxKeys];
+  __shared__ int s_cum[kMaxKeys + 1];
+  __shared__ int s_wave_tot[kSortWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int i = tid; i < kSortWaves * kMaxKeys; i += kSortThreads)
+    (&s_cnt[0][0])[i] = 0;
+  __syncthreads();
+
+  const int64_t chunk = ((numel + kSortWaves - 1) / kSortWaves + 63) / 64 * 64;
+  const int64_t lo = wave * chunk;
+  const int64_t hi = lo + chunk < numel ? lo + chunk : numel;
+  const int steps = static_cast<int>(chunk / 64);
+
+  // phase 1: per-chunk counts
+  for (int s = 0; s < steps; ++s) {
+    int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
+    if (i < hi) {
+      uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+      if (key != kInvalidKey) atomicAdd(&s_cnt[wave][key], 1);
+    }
+  }
+  __syncthreads();
+
+  // phase 2: per-expert totals, chunk-exclusive offsets, padded scan
+  int total_e = 0;
+  if (tid < num_keys) {
+    for (int w = 0; w < kSortWaves; ++w) {
+      int c = s_cnt[w][tid];
+      s_cnt[w][tid] = total_e;
+      total_e += c;
+    }
+  }
+  const int padded = (total_e + block_size - 1) / block_size * block_size;
+  int total_padded = 0;
+  const int start = block_exclusive_scan(tid < num_keys ? padded : 0,
+                                         s_wave_tot, total_padded);
+  if (tid < num_keys) {
+    s_cum[tid] = start;
+    for (int w = 0; w < kSortWaves; ++w) s_cnt[w][tid] += start;
+    if (counts_out) counts_out[tid] = total_e;
+  }
+  if (tid == 0) {
+    s_cum[num_keys] = total_padded;
+    if (ntp) ntp[0] = total_padded;
+  }
+  __syncthreads();
+
+  // padding slots inside each expert's range and the tail
+  if (sorted_ids) {
+    if (tid < num_keys) {
+      for (int p = start + total_e; p < start + padded && p < max_padded; ++p)
+        sorted_ids[p] = pad_value;
+    }
+    for (int64_t p = total_padded + tid; p < max_padded; p += kSortThreads)
+      sorted_ids[p] = pad_value;
+  }
+  // expert id of every block (binary search over the padded prefix)
+  if (expert_ids) {
+    const int nblk = total_padded / block_size;
+    for (int64_t b = tid; b < max_blocks; b += kSortThreads) {
+      int e = 0;
+      if (b < nblk) {
+        int lo_e = 0, hi_e = num_keys - 1;
+        const int p = static_cast<int>(b) * block_size;
+        while (lo_e < hi_e) {  // last e with s_cum[e] <= p
+          int mid = (lo_e + hi_e + 1) >> 1;
+          if (s_cum[mid] <= p) lo_e = mid; else hi_e = mid - 1;
+        }
+        e = lo_e;
+      }
+      expert_ids[b] = e;
+    }
+  }
+
+  // phase 3: stable scatter
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int s = 0; s < steps; ++s) {
+    int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
+    uint32_t key = kInvalidKey;
+    if (i < hi) key = load_key(ids, i, id_bound, map, num_keys);
+    unsigned long long same = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 11; ++b) {
+      unsigned long long bb = __ballot((key >> b) & 1u);
+      same &= ((key >> b) & 1u) ? bb : ~bb;
+    }
+    const int rank = __popcll(same & below);
+    const int cnt = __popcll(same);
+    int pos = -1;
+    if (key != kInvalidKey) {
+      pos = s_cnt[wave][key] + rank;
+      if (sorted_ids && pos < max_padded) sorted_ids[pos] = static_cast<int32_t>(i);
+    }
+    if (inv_pos && i < hi) inv_pos[i] = pos;
+    __syncthreads();
+    if (key != kInvalidKey && rank == 0) s_cnt[wave][key] += cnt;
+    __syncthreads();
+  }
+}
+
+// rows_per_expert (contiguous segments) -> block-padded row list:
+// row_ids[p] = first_row(e) + r for r < rows(e), else pad_value.
+__global__ __launch_bounds__(kSortThreads) void segments_to_blocks_kernel(
+    const int32_t* __restrict__ rows, int num_keys, int block_size,
+    int32_t* __restrict__ row_ids, int64_t max_padded,
+    int32_t* __restrict__ expert_ids, int64_t max_blocks,
+    int32_t* __restrict__ ntp, int32_t pad_value) {
+  __shared__ int s_cum[kMaxKeys + 1];
+  __shared__ int s_off[kMaxKeys + 1];
+  __shared__ int s_wave_tot[kSortWaves];
+  const int tid = threadIdx.x;
+  const int c = tid < num_keys ? rows[tid] : 0;
+  const int padded = (c + block_size - 1) / block_size * block_size;
+  int tp = 0, tr = 0;
+  int start = block_exclusive_scan(padded, s_wave_tot, tp);
+  int roff = block_exclusive_scan(c, s_wave_tot, tr);
+  if (tid < num_keys) {
+    s_cum[tid] = start;
+    s_off[tid] = roff;
+  }
+  if (tid == 0) {
+    s_cum[num_keys] = tp;
+    s_off[num_keys] = tr;
+    if (ntp) ntp[0] = tp;
+  }
+  __syncthreads();
+  for (int64_t p = tid; p < max_padded; p += kSortThreads) {
+    int v = pad_value;
+    if (p < tp) {
+      int lo_e = 0, hi_e = num_keys - 1;
+      while (lo_e < hi_e) {
+        int mid = (lo_e + hi_e + 1) >> 1;
+        if (s_cum[mid] <= p) lo_e = mid; else hi_e = mid - 1;
+      }
+      int r = static_cast<int>(p) - s_cum[lo_e];
+      if (r < s_off[lo_e + 1] - s_off[lo_e]) v = s_off[lo_e] + r;
+    }
+    row_ids[p] = v;
+  }
+  const int nblk = tp / block_size;
+  for (int64_t b = tid; b < max_blocks; b += kSortThreads) {
+    int e = 0;
+    if (b < nblk) {
+      const int p = static_cast<int>(b) * block_size;
+      int lo_e = 0, hi_e = num_keys - 1;
+      while (lo_e < hi_e) {
+        int mid = (lo_e + hi_e + 1) >> 1;
+        if (s_cum[mid] <= p) lo_e = mid; else hi_e = mid - 1;
+      }
+      e = lo_e;
+    }
+    expert_ids[b] = e;
+  }
+}
+
+// Row copies of remap_hidden_states: remapped[perm[i]] = hidden[i / topk].
+__global__ __launch_bounds__(256) void remap_copy_kernel(
+    const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+    int64_t row_bytes, const int32_t* __restrict__ perm, int topk,
+    int64_t slots) {
+  const int64_t i = blockIdx.x;
+  if (i >= slots) return;
+  const int p = perm[i];
+  if (p < 0) return;
+  const uint8_t* s = src + (i / topk) * row_bytes;
+  uint8_t* d = dst + static_cast<int64_t>(p) * row_bytes;
+  if ((row_bytes & 15) == 0 && ((reinterpret_cast<uintptr_t>(src) |
+                                 reinterpret_cast<uintptr_t>(dst)) & 15) == 0) {
+    const int64_t n = row_bytes >> 4;
+    for (int64_t j = threadIdx.x; j < n; j += 256)
+      reinterpret_cast<uint4*>(d)[j] = reinterpret_cast<const uint4*>(s)[j];
+  } else {
+    for (int64_t j = threadIdx.x; j < row_bytes; j += 256) d[j] = s[j];
+  }
+}
+
+__global__ void init_expert_map_kernel(int32_t* map, int num_experts,
+                                       int ep_rank, int ep_size) {
+  int g = blockIdx.x * blockDim.x + threadIdx.x;
+  int total = num_experts * ep_size;
+  if (g >= total) return;
+  int lo = ep_rank * num_experts;
+  map[g] = (g >= lo && g < lo + num_experts) ? g - lo : -1;
+}
+
+template <typename Id>
+void launch_sort(const void* ids, int64_t numel, int64_t id_bound,
+                 const int32_t* map, int num_keys, int bs, int32_t* sorted,
+                 int64_t max_padded, int32_t* eids, int64_t max_blocks,
+                 int32_t* ntp, int32_t* inv, int32_t* counts, int32_t pad,
+                 hipStream_t st) {
+  hipLaunchKernelGGL(counting_sort_kernel<Id>, dim3(1), dim3(kSortThreads), 0,
+                     st, static_cast<const Id*>(ids), numel, id_bound, map,
+                     num_keys, bs, sorted, max_padded, eids, max_blocks, ntp,
+                     inv, counts, pad);
+}
+
+}  // namespace
+
+// Shared by the fused layer and the grouped GEMM entry points.
+int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
+                      int64_t id_bound, const int32_t* map, int64_t num_keys,
+                      int64_t bs, int32_t* sorted, int64_t max_padded,
+                      int32_t* eids, int64_t max_blocks, int32_t* ntp,
+                      int32_t* inv, int32_t* counts, int32_t pad,
+                      hipStream_t st) {
+  MI_ARG(num_keys > 0 && num_keys <= kMaxKeys,
+         "padded_num_experts must be less than 1024");
+  MI_ARG(bs > 0, "block_size must be positive");
+  MI_ARG(numel >= 0 && numel < (int64_t(1) << 31), "too many topk_ids");
+  switch (ids_dtype) {
+    case MI355MOE_I32:
+      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, st);
+      break;
+    case MI355MOE_I64:
+      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, st);
+      break;
+    case MI355MOE_U32:
+      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, st);
+      break;
+    default:
+      return set_error(MI355MOE_ERR_INVALID, "topk_ids must be int32, int64 or uint32");
+  }
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
+                           int32_t* row_ids, int64_t max_padded,
+                           int32_t* eids, int64_t max_blocks, int32_t* ntp,
+                           int32_t pad, hipStream_t st) {
+  MI_ARG(num_keys > 0 && num_keys <= kMaxKeys, "num_experts must be in [1, 1024]");
+  hipLaunchKernelGGL(segments_to_blocks_kernel, dim3(1), dim3(kSortThreads), 0,
+                     st, rows, (int)num_keys, (int)bs, row_ids, max_padded,
+                     eids, max_blocks, ntp, pad);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+}  // namespace mi355
+
+using namespace mi355;
+
+extern "C" size_t mi355moe_moe_align_block_size_workspace_size(int64_t, int64_t) {
+  return 0;
+}
+
+extern "C" int mi355moe_moe_align_block_size(
+    const void* topk_ids, int ids_dtype, int64_t numel, int64_t num_experts,
+    int64_t block_size, int32_t* sorted_token_ids, int64_t max_num_tokens_padded,
+    int32_t* expert_ids, int64_t max_num_m_blocks, int32_t* ntp,
+    const int32_t* expert_map, void* /*workspace*/, size_t /*ws*/,
+    void* stream) {
+  MI_ARG(num_experts > 0, "num_experts must be positive");
+  MI_ARG((num_experts + 31) / 32 * 32 < 1024,
+         "padded_num_experts must be less than 1024");
+  return run_counting_sort(topk_ids, ids_dtype, numel, num_experts, expert_map,
+                           num_experts, block_size, sorted_token_ids,
+                           max_num_tokens_padded, expert_ids, max_num_m_blocks,
+                           ntp, nullptr, nullptr, static_cast<int32_t>(numel),
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t mi355moe_remap_hidden_states_workspace_size(int64_t, int64_t,
+                                                              int64_t) {
+  return 0;
+}
+
+extern "C" int mi355moe_remap_hidden_states(
+    const void* hidden, int64_t elem_bytes, const void* hscales,
+    int64_t scale_cols, int64_t scale_bytes, void* remapped,
+    void* remapped_scales, const int32_t* expert_map, int32_t* rows_per_expert,
+    int32_t* perm, const void* topk_ids, int ids_dtype, int64_t T, int64_t H,
+    int64_t k, int64_t total_experts, int64_t local_experts, void*, size_t,
+    void* stream) {
+  MI_ARG(local_experts > 0 && local_experts <= 1024,
+         "local experts number must be in [1, 1024]");
+  MI_ARG(k > 0, "Unsupported TopK value");
+  MI_ARG(elem_bytes > 0 && H > 0, "invalid hidden_states");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t slots = T * k;
+  if (slots == 0) return MI355MOE_OK;
+  int rc = run_counting_sort(topk_ids, ids_dtype, slots, total_experts,
+                             expert_map, local_experts, 1, nullptr, 0, nullptr,
+                             0, nullptr, perm, rows_per_expert, 0, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(remap_copy_kernel, dim3(static_cast<unsigned>(slots)),
+                     dim3(256), 0, st, static_cast<const uint8_t*>(hidden),
+                     static_cast<uint8_t*>(remapped), H * elem_bytes, perm,
+                     (int)k, slots);
+  MI_LAUNCH_CHECK();
+  if (hscales && remapped_scales) {
+    hipLaunchKernelGGL(remap_copy_kernel, dim3(static_cast<unsigned>(slots)),
+                       dim3(256), 0, st, static_cast<const uint8_t*>(hscales),
+                       static_cast<uint8_t*>(remapped_scales),
+                       scale_cols * scale_bytes, perm, (int)k, slots);
+    MI_LAUNCH_CHECK();
+  }
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_init_expert_map(int32_t* map, int64_t num_experts,
+                                        int64_t ep_rank, int64_t ep_size,
+                                        void* stream) {
+  MI_ARG(num_experts > 0 && ep_size > 0 && ep_rank >= 0 && ep_rank < ep_size,
+         "invalid expert-parallel configuration");
+  int64_t total = num_experts * ep_size;
+  hipLaunchKernelGGL(init_expert_map_kernel,
+                     dim3(static_cast<unsigned>(cdiv(total, 256))), dim3(256),
+                     0, static_cast<hipStream_t>(stream), map, (int)num_experts,
+                     (int)ep_rank, (int)ep_size);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}

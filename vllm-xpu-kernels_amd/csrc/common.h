@@ -1,0 +1,146 @@
+// Shared device/host helpers for the MI355X (gfx950) fused-MoE library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/mi355moe.h"
+
+namespace mi355 {
+
+// ---------------------------------------------------------------------------
+// Error plumbing: every C-ABI entry point returns 0 or a negative code and
+// leaves a message in a thread-local buffer (mi355moe_last_error()).
+// ---------------------------------------------------------------------------
+int set_error(int code, const std::string& msg);
+
+#define MI_CHECK(cond, code, msg)                                  \
+  do {                                                             \
+    if (!(cond)) return ::mi355::set_error((code), (msg));         \
+  } while (0)
+
+#define MI_ARG(cond, msg) MI_CHECK(cond, MI355MOE_ERR_INVALID, msg)
+
+#define MI_HIP(expr)                                                         \
+  do {                                                                       \
+    hipError_t _e = (expr);                                                  \
+    if (_e != hipSuccess)                                                    \
+      return ::mi355::set_error(MI355MOE_ERR_HIP,                            \
+                                std::string("HIP error: ") +                 \
+                                    hipGetErrorString(_e) + " at " #expr);   \
+  } while (0)
+
+#define MI_LAUNCH_CHECK()                                                    \
+  do {                                                                       \
+    hipError_t _e = hipGetLastError();                                       \
+    if (_e != hipSuccess)                                                    \
+      return ::mi355::set_error(MI355MOE_ERR_HIP,                            \
+                                std::string("kernel launch failed: ") +      \
+                                    hipGetErrorString(_e));                  \
+  } while (0)
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Scalar conversions.  bf16/fp16 are carried as raw 16-bit words; fp32->bf16
+// uses the hardware RNE convert (v_cvt_pk_bf16_f32 on gfx950).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  __bf16 b = static_cast<__bf16>(f);
+  return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return static_cast<float>(v);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  _Float16 v = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+// Element-type traits used by templated kernels: load as float, store from
+// float with one rounding.
+struct F32 {
+  using T = float;
+  static __device__ __forceinline__ float ld(float v) { return v; }
+  static __device__ __forceinline__ float st(float v) { return v; }
+};
+struct BF16 {
+  using T = uint16_t;
+  static __device__ __forceinline__ float ld(uint16_t v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t st(float v) { return f32_to_bf16(v); }
+};
+struct F16 {
+  using T = uint16_t;
+  static __device__ __forceinline__ float ld(uint16_t v) { return f16_to_f32(v); }
+  static __device__ __forceinline__ uint16_t st(float v) { return f32_to_f16(v); }
+};
+
+// OCP e4m3fn decode (bias 7, no infinities, 0x7f/0xff NaN).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  uint32_t s = (b & 0x80u) << 24;
+  uint32_t e = (b >> 3) & 0xFu;
+  uint32_t m = b & 0x7u;
+  float v;
+  if (e == 0) {
+    v = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  } else {
+    v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  }
+  if ((b & 0x7Fu) == 0x7Fu) v = __uint_as_float(0x7FC00000u);
+  return __uint_as_float(__float_as_uint(v) | s);
+}
+
+// fp32 -> OCP e4m3fn, round to nearest even, for |x| <= 448 (callers clamp
+// first, as the reference quantisers do).  Subnormals (|x| < 2^-6) are on the
+// 2^-9 grid.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;  // NaN
+  uint32_t r;
+  if (a < 0x3C800000u) {                      // |x| < 2^-6: subnormal range
+    float f = __uint_as_float(a) * 512.0f;    // exact scaling to units of 2^-9
+    // round half to even on the integer grid 0..8
+    float fl = __builtin_floorf(f);
+    float d = f - fl;
+    uint32_t q = static_cast<uint32_t>(fl);
+    if (d > 0.5f || (d == 0.5f && (q & 1u))) q += 1u;
+    r = q;                                     // q == 8 -> 0x08 = 2^-6 (normal)
+  } else {
+    // normal: keep 3 mantissa bits, RNE on the dropped 20 bits
+    uint32_t lsb = (a >> 20) & 1u;
+    uint32_t rounded = a + 0x7FFFFu + lsb;
+    uint32_t e = (rounded >> 23) - 120u;
+    uint32_t m = (rounded >> 20) & 0x7u;
+    r = (e << 3) | m;
+    if (r > 0x7Eu) r = 0x7Eu;                  // saturate at 448
+  }
+  return sign | r;
+}
+
+// ---------------------------------------------------------------------------
+// Wavefront (64-lane) reductions via cross-lane shuffles.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace mi355

@@ -1,0 +1,346 @@
+// Bandwidth-bound helpers of the MoE path: activations (silu_and_mul,
+// swigluoai_and_mul), per-token-group fp8 / mxfp4 activation quantisers and
+// the top-k reductions (moe_sum, moe_gather).  Every kernel moves 16 bytes
+// per lane per access where the row length allows it.
+#include "common.h"
+
+namespace mi355 {
+namespace {
+
+// ----------------------------------------------------------------- helpers
+template <typename E>
+struct Vec8 {  // 8 elements of a 16-bit type in one uint4
+  static __device__ __forceinline__ void load(const uint16_t* p, float* f) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = E::ld(static_cast<uint16_t>(w[i] & 0xFFFFu));
+      f[2 * i + 1] = E::ld(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(E::st(f[2 * i])) |
+             (static_cast<uint32_t>(E::st(f[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+template <typename E>
+__device__ __forceinline__ float ldx(const void* p, int64_t i) {
+  return E::ld(static_cast<const typename E::T*>(p)[i]);
+}
+template <typename E>
+__device__ __forceinline__ void stx(void* p, int64_t i, float v) {
+  static_cast<typename E::T*>(p)[i] = E::st(v);
+}
+
+// ceil(log2(x)) for a positive normal float, exact (bit arithmetic).
+__device__ __forceinline__ int ceil_log2(float x) {
+  uint32_t u = __float_as_uint(x);
+  int e = static_cast<int>((u >> 23) & 0xFF) - 127;
+  return (u & 0x7FFFFFu) ? e + 1 : e;
+}
+__device__ __forceinline__ float pow2i(int e) {
+  return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
+// ------------------------------------------------------------- activations
+template <typename E>
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // reference rounds silu(g) to the element type before the multiply
+  float s = E::ld(E::st(g / (1.f + expf(-g))));
+  return s * u;
+}
+__device__ __forceinline__ float swigluoai(float g, float u, float alpha,
+                                           float limit) {
+  g = g > limit ? limit : g;
+  u = u > limit ? limit : (u < -limit ? -limit : u);
+  float glu = g * (1.f / (1.f + expf(-g * alpha)));
+  return (u + 1.f) * glu;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void silu_and_mul_kernel(
+    void* __restrict__ out, const void* __restrict__ in, int64_t rows,
+    int64_t d) {
+  const int64_t r = blockIdx.y;
+  const typename E::T* x = static_cast<const typename E::T*>(in) + r * 2 * d;
+  typename E::T* y = static_cast<typename E::T*>(out) + r * d;
+  if constexpr (sizeof(typename E::T) == 2) {
+    if ((d & 7) == 0) {
+      for (int64_t c = (blockIdx.x * 256 + threadIdx.x) * 8; c < d;
+           c += static_cast<int64_t>(gridDim.x) * 256 * 8) {
+        float g[8], u[8], o[8];
+        Vec8<E>::load(x + c, g);
+        Vec8<E>::load(x + d + c, u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = silu_mul<E>(g[i], u[i]);
+        Vec8<E>::store(y + c, o);
+      }
+      return;
+    }
+  }
+  for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < d;
+       c += static_cast<int64_t>(gridDim.x) * 256)
+    y[c] = E::st(silu_mul<E>(E::ld(x[c]), E::ld(x[d + c])));
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void swigluoai_kernel(
+    void* __restrict__ out, const void* __restrict__ in, int64_t rows,
+    int64_t d, float alpha, float limit) {
+  const int64_t r = blockIdx.y;
+  const typename E::T* x = static_cast<const typename E::T*>(in) + r * 2 * d;
+  typename E::T* y = static_cast<typename E::T*>(out) + r * d;
+  for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < d;
+       c += static_cast<int64_t>(gridDim.x) * 256)
+    y[c] = E::st(swigluoai(E::ld(x[2 * c]), E::ld(x[2 * c + 1]), alpha, limit));
+}
+
+// ----------------------------------------------------------- quantisation
+// One group of G elements is owned by G/8 consecutive lanes (8 elements per
+// lane); requires G % 8 == 0 and G/8 a power of two <= 64.
+template <typename E>
+__global__ __launch_bounds__(256) void group_fp8_quant_kernel(
+    const void* __restrict__ in, uint8_t* __restrict__ q,
+    float* __restrict__ s, int64_t rows, int64_t cols, int group, float eps,
+    float fp8_max, int ue8m0) {
+  const int lpg = group >> 3;
+  const int64_t ngroups = rows * (cols / group);
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t g = gtid / lpg;
+  const int sub = static_cast<int>(gtid % lpg);
+  const bool active = g < ngroups;
+  const int64_t base = (active ? g : 0) * group + sub * 8;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = active ? ldx<E>(in, base + i) : 0.f;
+  float amax = eps;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int o = lpg >> 1; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  float ys = fmaxf(amax / fp8_max, 1.0f / (fp8_max * 512.0f));
+  if (ue8m0) ys = pow2i(ceil_log2(fmaxf(fabsf(ys), 1e-10f)));
+  if (!active) return;
+  if (sub == 0) s[g] = ys;
+  const float inv = 1.0f / ys;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float x = fminf(fmaxf(v[i] * inv, -fp8_max), fp8_max);
+    uint32_t b = f32_to_e4m3(x);
+    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+  }
+  *reinterpret_cast<uint2*>(q + base) = make_uint2(lo, hi);
+}
+
+__device__ __forceinline__ uint32_t fp4_code(float x) {
+  float a = fabsf(x);
+  uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) +
+               (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
+  return c | (x < 0.f ? 0x8u : 0u);
+}
+
+// mxfp4: groups of 32 owned by 4 lanes x 8 elements.
+template <typename E>
+__global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
+    const void* __restrict__ in, uint8_t* __restrict__ q,
+    float* __restrict__ s, int64_t rows, int64_t cols, float eps) {
+  const int64_t ngroups = rows * (cols / 32);
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t g = gtid >> 2;
+  const int sub = static_cast<int>(gtid & 3);
+  const bool active = g < ngroups;
+  const int64_t base = (active ? g : 0) * 32 + sub * 8;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = active ? ldx<E>(in, base + i) : 0.f;
+  float amax = eps;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float ys = pow2i(ceil_log2(fmaxf(fabsf(amax / 6.0f), eps)));
+  if (!active) return;
+  if (sub == 0) s[g] = ys;
+  const float inv = 1.0f / ys;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float x = fminf(fmaxf(v[i] * inv, -6.0f), 6.0f);
+    packed |= fp4_code(x) << (4 * i);
+  }
+  *reinterpret_cast<uint32_t*>(q + base / 2) = packed;
+}
+
+// -------------------------------------------------------------- reductions
+template <typename E, typename Id>
+__global__ __launch_bounds__(256) void moe_sum_kernel(
+    const void* __restrict__ in, void* __restrict__ out, int64_t T, int topk,
+    int64_t H, const Id* __restrict__ ids, const int32_t* __restrict__ map,
+    int64_t map_len) {
+  const int64_t t = blockIdx.y;
+  const int64_t h = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (h >= H) return;
+  float acc = 0.f;
+  for (int j = 0; j < topk; ++j) {
+    if (ids) {
+      int64_t e = static_cast<int64_t>(ids[t * topk + j]);
+      if (e < 0) continue;
+      if (map && (e >= map_len || map[e] < 0)) continue;
+    }
+    acc += ldx<E>(in, (t * topk + j) * H + h);
+  }
+  stx<E>(out, t * H + h, acc);
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void moe_gather_kernel(
+    void* __restrict__ out, const void* __restrict__ in,
+    const float* __restrict__ w, const int32_t* __restrict__ perm, int64_t T,
+    int topk, int64_t H) {
+  const int64_t t = blockIdx.y;
+  const int64_t h0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (h0 >= H) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const bool vec = sizeof(typename E::T) == 2 && (H & 7) == 0;
+  for (int j = 0; j < topk; ++j) {
+    const int p = perm[t * topk + j];
+    if (p < 0) continue;
+    const float wj = w[t * topk + j];
+    const int64_t row = static_cast<int64_t>(p) * H;
+    if constexpr (sizeof(typename E::T) == 2) {
+      if (vec) {
+        float f[8];
+        Vec8<E>::load(static_cast<const uint16_t*>(in) + row + h0, f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += wj * f[i];
+        continue;
+      }
+    }
+    for (int i = 0; i < 8 && h0 + i < H; ++i) acc[i] += wj * ldx<E>(in, row + h0 + i);
+  }
+  if constexpr (sizeof(typename E::T) == 2) {
+    if (vec) {
+      Vec8<E>::store(static_cast<uint16_t*>(out) + t * H + h0, acc);
+      return;
+    }
+  }
+  for (int i = 0; i < 8 && h0 + i < H; ++i) stx<E>(out, t * H + h0 + i, acc[i]);
+}
+
+}  // namespace
+}  // namespace mi355
+
+using namespace mi355;
+
+#define MI_DISPATCH_FLOAT(dt, KERNEL_CALL, what)                                \
+  switch (dt) {                                                                 \
+    case MI355MOE_F32: { using E = F32; KERNEL_CALL; break; }                   \
+    case MI355MOE_BF16: { using E = BF16; KERNEL_CALL; break; }                 \
+    case MI355MOE_F16: { using E = F16; KERNEL_CALL; break; }                   \
+    default: return set_error(MI355MOE_ERR_INVALID, what);                      \
+  }
+
+extern "C" int mi355moe_silu_and_mul(void* out, const void* in, int dt,
+                                     int64_t rows, int64_t d, void* stream) {
+  MI_ARG(rows >= 0 && d >= 0, "invalid shape");
+  if (rows == 0 || d == 0) return MI355MOE_OK;
+  MI_ARG(rows <= 0x7fffffff, "too many rows");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t per = (d & 7) == 0 ? d / 8 : d;
+  dim3 grid(static_cast<unsigned>(std::min<int64_t>(cdiv(per, 256), 64)),
+            static_cast<unsigned>(rows));
+  MI_DISPATCH_FLOAT(dt, (silu_and_mul_kernel<E><<<grid, dim3(256), 0, st>>>(out, in, rows, d)),
+                    "silu_and_mul: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_swigluoai_and_mul(void* out, const void* in, int dt,
+                                          int64_t rows, int64_t d, float alpha,
+                                          float limit, void* stream) {
+  MI_ARG(rows >= 0 && d >= 0, "invalid shape");
+  if (rows == 0 || d == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(std::min<int64_t>(cdiv(d, 256), 64)),
+            static_cast<unsigned>(rows));
+  MI_DISPATCH_FLOAT(dt, (swigluoai_kernel<E><<<grid, dim3(256), 0, st>>>(out, in, rows, d, alpha, limit)),
+                    "swigluoai_and_mul: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_per_token_group_fp8_quant(
+    const void* in, int dt, void* q, float* s, int64_t rows, int64_t cols,
+    int64_t group, float eps, float /*fp8_min*/, float fp8_max, int ue8m0,
+    void* stream) {
+  MI_ARG(group > 0 && cols % group == 0,
+         "the last dimension must be divisible by group_size");
+  MI_ARG(group % 8 == 0 && group <= 512 && ((group / 8) & (group / 8 - 1)) == 0,
+         "group_size must be 8 x a power of two, at most 512");
+  if (rows == 0 || cols == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t threads = rows * cols / 8;
+  dim3 grid(static_cast<unsigned>(cdiv(threads, 256)));
+  MI_DISPATCH_FLOAT(dt, (group_fp8_quant_kernel<E><<<grid, dim3(256), 0, st>>>(in, static_cast<uint8_t*>(q), s, rows, cols, (int)group, eps, fp8_max, ue8m0)),
+                    "per_token_group_fp8_quant: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_per_token_group_quant_mxfp4(
+    const void* in, int dt, uint8_t* q, float* s, int64_t rows, int64_t cols,
+    int64_t group, float eps, void* stream) {
+  MI_ARG(group == 32, "group_size must be 32 for MXFP4");
+  MI_ARG(cols % 32 == 0, "the last dimension must be divisible by 32");
+  if (rows == 0 || cols == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t threads = rows * cols / 8;
+  dim3 grid(static_cast<unsigned>(cdiv(threads, 256)));
+  MI_DISPATCH_FLOAT(dt, (group_mxfp4_quant_kernel<E><<<grid, dim3(256), 0, st>>>(in, q, s, rows, cols, eps)),
+                    "per_token_group_quant_mxfp4: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_moe_sum(const void* in, void* out, int dt, int64_t T,
+                                int64_t topk, int64_t H, const void* ids,
+                                int ids_dtype, const int32_t* map,
+                                int64_t map_len, void* stream) {
+  MI_ARG(!(map && !ids), "expert_map requires topk_ids");
+  MI_ARG(topk > 0, "topk must be positive");
+  if (T == 0 || H == 0) return MI355MOE_OK;
+  MI_ARG(T <= 0x7fffffff, "too many tokens");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(H, 256)), static_cast<unsigned>(T));
+  if (!ids || ids_dtype == MI355MOE_I32) {
+    MI_DISPATCH_FLOAT(dt, (moe_sum_kernel<E, int32_t><<<grid, dim3(256), 0, st>>>(in, out, T, (int)topk, H, static_cast<const int32_t*>(ids), map, map_len)),
+                      "moe_sum: unsupported dtype")
+  } else if (ids_dtype == MI355MOE_I64) {
+    MI_DISPATCH_FLOAT(dt, (moe_sum_kernel<E, int64_t><<<grid, dim3(256), 0, st>>>(in, out, T, (int)topk, H, static_cast<const int64_t*>(ids), map, map_len)),
+                      "moe_sum: unsupported dtype")
+  } else {
+    return set_error(MI355MOE_ERR_INVALID, "topk_ids must be int32 or int64");
+  }
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_moe_gather(void* out, const void* in, int dt,
+                                   const float* w, const int32_t* perm,
+                                   int64_t T, int64_t topk, int64_t H,
+                                   void* stream) {
+  MI_ARG(topk > 0, "topk must be positive");
+  if (T == 0 || H == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(cdiv(H, 8), 256)), static_cast<unsigned>(T));
+  MI_DISPATCH_FLOAT(dt, (moe_gather_kernel<E><<<grid, dim3(256), 0, st>>>(out, in, w, perm, T, (int)topk, H)),
+                    "moe_gather: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}

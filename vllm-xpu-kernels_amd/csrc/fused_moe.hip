@@ -1,0 +1,435 @@
+// C-ABI entry points of the grouped GEMM and of the whole fused-MoE layer.
+//
+// Fused layer (one call, no host synchronisation, 4-5 launches):
+//   1. stable counting sort of topk_ids into block-aligned sorted slots
+//   2. (fp8block) 1x128 e4m3 quantisation of hidden_states, once per token
+//   3. w13 grouped GEMM gathering activation rows through the sorted slots,
+//      GLU epilogue (SiLU-mul / swigluoai), activation written in slot order
+//      (fp8block: re-quantised to e4m3 + 1x128 scales in the same epilogue)
+//   4. w2 grouped GEMM reading the activation rows contiguously, writing each
+//      slot's row to its flat (token, j) position
+//   5. weighted top-k reduction y[t] = sum_j w[t,j] * G2[t*k + j] in fixed j
+//      order (no floating-point atomics).
+#include <vector>
+
+#include "moe_gemm.h"
+
+namespace mi355 {
+
+int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,
+                      int64_t max_blocks, void* qs, hipStream_t st);
+
+namespace {
+
+struct Carver {
+  uint8_t* base;
+  size_t off = 0;
+  template <typename T>
+  T* take(int64_t n) {
+    off = (off + 255) & ~size_t(255);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += static_cast<size_t>(n) * sizeof(T);
+    return p;
+  }
+};
+
+// Buffer sizes of the block-aligned slot layout (the reference's
+// max_num_tokens_padded rule, tests/ops/moe_align_block_size_ops.py:71-86).
+void padded_sizes(int64_t slots, int64_t experts, int64_t bm,
+                  int64_t& max_padded, int64_t& max_blocks) {
+  max_padded = slots + experts * (bm - 1);
+  if (slots < experts) max_padded = std::min(max_padded, slots * bm);
+  max_blocks = cdiv(max_padded, bm);
+}
+
+// Blocks that can hold at least one valid slot: every active expert adds at
+// most one partial block, so ceil(slots/bm) + min(E, slots) bounds them.
+int64_t launch_blocks(int64_t slots, int64_t experts, int64_t bm,
+                      int64_t max_blocks) {
+  int64_t b = cdiv(slots, bm) + std::min(experts, slots);
+  return std::min(b, max_blocks);
+}
+
+template <typename Id>
+__global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ g2,
+    const float* __restrict__ w, const Id* __restrict__ ids,
+    const int32_t* __restrict__ map, int64_t map_len, int64_t num_experts,
+    int64_t T, int topk, int64_t H) {
+  const int64_t t = blockIdx.y;
+  const int64_t h0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (h0 >= H) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int j = 0; j < topk; ++j) {
+    int64_t id = static_cast<int64_t>(ids[t * topk + j]);
+    if (map) {
+      if (id < 0 || id >= map_len) continue;
+      id = map[id];
+    }
+    if (id < 0 || id >= num_experts) continue;
+    const float wj = w[t * topk + j];
+    const uint16_t* row = g2 + (t * topk + j) * H + h0;
+    if ((H & 7) == 0) {
+      uint4 u = *reinterpret_cast<const uint4*>(row);
+      uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += wj * bf16_to_f32(static_cast<uint16_t>(wd[i] & 0xFFFF));
+        acc[2 * i + 1] += wj * bf16_to_f32(static_cast<uint16_t>(wd[i] >> 16));
+      }
+    } else {
+      for (int i = 0; i < 8 && h0 + i < H; ++i) acc[i] += wj * bf16_to_f32(row[i]);
+    }
+  }
+  uint16_t* o = out + t * H + h0;
+  if ((H & 7) == 0) {
+    uint32_t wd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      wd[i] = f32_to_bf16(acc[2 * i]) | (uint32_t(f32_to_bf16(acc[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(o) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  } else {
+    for (int i = 0; i < 8 && h0 + i < H; ++i) o[i] = f32_to_bf16(acc[i]);
+  }
+}
+
+int group_quant_fp8(const void* x, int dt, uint8_t* q, float* s, int64_t rows,
+                    int64_t cols, hipStream_t st) {
+  return mi355moe_per_token_group_fp8_quant(x, dt, q, s, rows, cols, 128, 1e-10f,
+                                            -448.f, 448.f, 0, st);
+}
+
+struct FusedLayout {
+  int bm;
+  int64_t slots, max_padded, max_blocks, grid_blocks;
+  int32_t *sorted, *eids, *ntp;
+  uint8_t* xq;    // fp8 hidden [T, H]
+  float* xs;      // [T, H/128]
+  void* act;      // bf16 [max_padded, I] or e4m3 [max_padded, I]
+  float* acts;    // [max_padded, I/128]
+  uint16_t* g2;   // bf16 [slots, H]
+  size_t bytes;
+};
+
+FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
+  FusedLayout L{};
+  const int64_t E = a->num_experts;
+  L.slots = a->num_tokens * a->topk;
+  L.bm = pick_block_m(L.slots, E);
+  padded_sizes(L.slots, E, L.bm, L.max_padded, L.max_blocks);
+  L.grid_blocks = launch_blocks(L.slots, E, L.bm, L.max_blocks);
+  Carver c{base};
+  L.sorted = c.take<int32_t>(std::max<int64_t>(L.max_padded, 1));
+  L.eids = c.take<int32_t>(std::max<int64_t>(L.max_blocks, 1));
+  L.ntp = c.take<int32_t>(1);
+  const bool fp8 = a->recipe == MI355MOE_RECIPE_FP8BLOCK;
+  if (fp8) {
+    L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
+    L.xs = c.take<float>(a->num_tokens * (a->hidden / 128));
+    L.act = c.take<uint8_t>(L.max_padded * a->inter);
+    L.acts = c.take<float>(L.max_padded * (a->inter / 128));
+  } else {
+    L.act = c.take<uint16_t>(L.max_padded * a->inter);
+  }
+  L.g2 = c.take<uint16_t>(L.slots * a->hidden);
+  L.bytes = c.off + 256;
+  return L;
+}
+
+}  // namespace
+}  // namespace mi355
+
+using namespace mi355;
+
+extern "C" size_t mi355moe_fused_moe_workspace_size(const mi355moe_fused_moe_args* a) {
+  if (!a) return 0;
+  return plan(a, nullptr).bytes;
+}
+
+namespace mi355 {
+namespace {
+int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
+                   void* stream, hipEvent_t* ev);
+}
+}  // namespace mi355
+
+struct mi355moe_timer_s {
+  int max_steps;
+  std::vector<hipEvent_t> ev;  // (kFusedStages + 1) per step
+};
+
+extern "C" int mi355moe_fused_moe(const mi355moe_fused_moe_args* a, void* ws,
+                                  size_t ws_bytes, void* stream) {
+  return fused_moe_impl(a, ws, ws_bytes, stream, nullptr);
+}
+
+extern "C" int mi355moe_timer_create(int max_steps, mi355moe_timer* out) {
+  MI_ARG(max_steps > 0 && out != nullptr, "invalid timer arguments");
+  auto* t = new mi355moe_timer_s{max_steps, {}};
+  t->ev.resize(static_cast<size_t>(max_steps) * (MI355MOE_FUSED_STAGES + 1));
+  for (auto& e : t->ev) {
+    hipError_t rc = hipEventCreate(&e);
+    if (rc != hipSuccess) {
+      for (auto& f : t->ev) if (f) (void)hipEventDestroy(f);
+      delete t;
+      return set_error(MI355MOE_ERR_HIP, std::string("hipEventCreate: ") + hipGetErrorString(rc));
+    }
+  }
+  *out = t;
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_timer_destroy(mi355moe_timer t) {
+  if (!t) return MI355MOE_OK;
+  for (auto& e : t->ev) if (e) (void)hipEventDestroy(e);
+  delete t;
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_fused_moe_timed(const mi355moe_fused_moe_args* a, void* ws,
+                                        size_t ws_bytes, void* stream,
+                                        mi355moe_timer t, int step) {
+  MI_ARG(t && step >= 0 && step < t->max_steps, "timer step out of range");
+  return fused_moe_impl(a, ws, ws_bytes, stream,
+                        &t->ev[static_cast<size_t>(step) * (MI355MOE_FUSED_STAGES + 1)]);
+}
+
+extern "C" int mi355moe_timer_stage_ms(mi355moe_timer t, int step, float* ms) {
+  MI_ARG(t && ms && step >= 0 && step < t->max_steps, "timer step out of range");
+  hipEvent_t* e = &t->ev[static_cast<size_t>(step) * (MI355MOE_FUSED_STAGES + 1)];
+  MI_HIP(hipEventSynchronize(e[MI355MOE_FUSED_STAGES]));
+  for (int i = 0; i < MI355MOE_FUSED_STAGES; ++i) MI_HIP(hipEventElapsedTime(&ms[i], e[i], e[i + 1]));
+  return MI355MOE_OK;
+}
+
+namespace mi355 {
+namespace {
+int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
+                   void* stream, hipEvent_t* ev) {
+  MI_ARG(a != nullptr, "null arguments");
+  const int64_t T = a->num_tokens, H = a->hidden, I = a->inter,
+                E = a->num_experts, k = a->topk;
+  MI_ARG(T >= 0 && H > 0 && I > 0 && E > 0 && k > 0, "invalid layer shape");
+  MI_ARG(E <= 1024, "num_experts must be at most 1024");
+  MI_ARG(a->act_dtype == MI355MOE_BF16, "hidden_states must be bfloat16");
+  MI_ARG(a->ids_dtype == MI355MOE_I32 || a->ids_dtype == MI355MOE_I64,
+         "topk_ids must be int32 or int64");
+  MI_ARG(a->activation == MI355MOE_ACT_SILU || a->activation == MI355MOE_ACT_SWIGLUOAI,
+         "unsupported activation");
+  const int recipe = a->recipe;
+  if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
+    MI_ARG(H % 128 == 0 && I % 128 == 0,
+           "fp8 block-scaled weights need hidden and intermediate sizes % 128 == 0");
+    MI_ARG(a->w13_scale && a->w2_scale, "fp8 block-scaled weights need scales");
+  } else if (recipe == MI355MOE_RECIPE_MXFP4) {
+    MI_ARG(H % 32 == 0 && I % 32 == 0, "mxfp4 weights need K % 32 == 0");
+    MI_ARG(a->w13_scale && a->w2_scale, "mxfp4 weights need e8m0 scales");
+  } else {
+    MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
+    MI_ARG(H % 8 == 0 && I % 8 == 0, "bf16 weights need K % 8 == 0");
+  }
+  if (T == 0) return MI355MOE_OK;
+  FusedLayout L = plan(a, static_cast<uint8_t*>(ws));
+  MI_CHECK(ws && ws_bytes >= L.bytes, MI355MOE_ERR_WORKSPACE,
+           "workspace too small for fused_moe");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t id_bound = a->expert_map ? a->expert_map_len : E;
+  auto mark = [&](int i) -> int {
+    if (ev) MI_HIP(hipEventRecord(ev[i], st));
+    return MI355MOE_OK;
+  };
+
+  if (int m = mark(0)) return m;
+  int rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
+                             a->expert_map, E, L.bm, L.sorted, L.max_padded,
+                             L.eids, L.max_blocks, L.ntp, nullptr, nullptr,
+                             static_cast<int32_t>(L.slots), st);
+  if (rc) return rc;
+
+  const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
+  if (int m = mark(1)) return m;
+  if (fp8) {
+    rc = group_quant_fp8(a->hidden_states, MI355MOE_BF16, L.xq, L.xs, T, H, st);
+    if (rc) return rc;
+  }
+  if (int m = mark(2)) return m;
+
+  GemmArgs g1{};
+  g1.A = fp8 ? static_cast<const void*>(L.xq) : a->hidden_states;
+  g1.a_scale = fp8 ? L.xs : nullptr;
+  g1.B = a->w13;
+  g1.b_scale = a->w13_scale;
+  g1.bias = static_cast<const uint16_t*>(a->w13_bias);
+  g1.D = L.act;
+  g1.row_ids = L.sorted;
+  g1.block_expert = L.eids;
+  g1.ntp = L.ntp;
+  g1.num_valid = static_cast<int32_t>(L.slots);
+  g1.a_div = static_cast<int32_t>(k);
+  g1.a_by_pos = 0;
+  g1.d_by_pos = 1;
+  g1.N = I;
+  g1.K = H;
+  g1.ldb_rows = 2 * I;
+  g1.up_off = I;
+  g1.clamp_limit = a->gemm1_clamp_limit;
+  g1.alpha = a->swiglu_alpha;
+  g1.limit = a->swiglu_limit;
+  g1.act = a->activation;
+  rc = launch_moe_gemm_q(recipe, EPI_GLU, fp8, L.bm, g1, L.grid_blocks, L.acts, st);
+  if (rc) return rc;
+  if (int m = mark(3)) return m;
+
+  GemmArgs g2{};
+  g2.A = L.act;
+  g2.a_scale = fp8 ? L.acts : nullptr;
+  g2.B = a->w2;
+  g2.b_scale = a->w2_scale;
+  g2.bias = static_cast<const uint16_t*>(a->w2_bias);
+  g2.D = L.g2;
+  g2.row_ids = L.sorted;
+  g2.block_expert = L.eids;
+  g2.ntp = L.ntp;
+  g2.num_valid = static_cast<int32_t>(L.slots);
+  g2.a_div = 1;
+  g2.a_by_pos = 1;
+  g2.d_by_pos = 0;
+  g2.N = H;
+  g2.K = I;
+  g2.ldb_rows = H;
+  g2.up_off = 0;
+  rc = launch_moe_gemm_q(recipe, EPI_STORE, false, L.bm, g2, L.grid_blocks, nullptr, st);
+  if (rc) return rc;
+  if (int m = mark(4)) return m;
+
+  // Slots dropped by the sort (invalid or non-local experts) were never
+  // written by the w2 GEMM; the reduction skips them by the same rule.
+  dim3 grid(static_cast<unsigned>(cdiv(cdiv(H, 8), 256)), static_cast<unsigned>(T));
+  if (a->ids_dtype == MI355MOE_I32)
+    weighted_topk_sum_kernel<int32_t><<<grid, dim3(256), 0, st>>>(
+        static_cast<uint16_t*>(a->output), L.g2, a->topk_weights,
+        static_cast<const int32_t*>(a->topk_ids), a->expert_map,
+        a->expert_map_len, E, T, (int)k, H);
+  else
+    weighted_topk_sum_kernel<int64_t><<<grid, dim3(256), 0, st>>>(
+        static_cast<uint16_t*>(a->output), L.g2, a->topk_weights,
+        static_cast<const int64_t*>(a->topk_ids), a->expert_map,
+        a->expert_map_len, E, T, (int)k, H);
+  MI_LAUNCH_CHECK();
+  return mark(5);
+}
+}  // namespace
+}  // namespace mi355
+
+// ------------------------------------------------------------ grouped GEMM
+namespace {
+struct GGLayout {
+  int bm;
+  int64_t max_padded, max_blocks, grid_blocks;
+  int32_t *rows, *eids, *ntp;
+  uint8_t* aq;
+  float* as;
+  size_t bytes;
+};
+GGLayout gg_plan(int recipe, bool need_quant, int64_t M, int64_t K, int64_t E,
+                 uint8_t* base) {
+  GGLayout L{};
+  L.bm = pick_block_m(M, E);
+  padded_sizes(M, E, L.bm, L.max_padded, L.max_blocks);
+  L.grid_blocks = launch_blocks(M, E, L.bm, L.max_blocks);
+  Carver c{base};
+  L.rows = c.take<int32_t>(std::max<int64_t>(L.max_padded, 1));
+  L.eids = c.take<int32_t>(std::max<int64_t>(L.max_blocks, 1));
+  L.ntp = c.take<int32_t>(1);
+  if (need_quant) {
+    L.aq = c.take<uint8_t>(M * K);
+    L.as = c.take<float>(M * (K / 128));
+  }
+  L.bytes = c.off + 256;
+  (void)recipe;
+  return L;
+}
+}  // namespace
+
+extern "C" size_t mi355moe_grouped_gemm_workspace_size(int64_t total_rows,
+                                                       int64_t num_experts) {
+  // worst case: the fp8 recipe quantising a 16-bit A; K is not known here, so
+  // callers that pass a 16-bit A to the fp8 recipe must use
+  // mi355moe_grouped_gemm_workspace_size_k.
+  return gg_plan(0, false, total_rows, 0, num_experts, nullptr).bytes;
+}
+
+extern "C" size_t mi355moe_grouped_gemm_workspace_size_k(int recipe, int a_dtype,
+                                                         int64_t total_rows,
+                                                         int64_t K,
+                                                         int64_t num_experts) {
+  const bool q = recipe == MI355MOE_RECIPE_FP8BLOCK && a_dtype != MI355MOE_FP8E4M3;
+  return gg_plan(recipe, q, total_rows, K, num_experts, nullptr).bytes;
+}
+
+extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
+                                     const float* a_scale, const void* B,
+                                     const void* b_scale, const void* bias,
+                                     void* D, int out_dtype,
+                                     const int32_t* rows_per_expert,
+                                     int64_t M, int64_t N, int64_t K, int64_t E,
+                                     void* ws, size_t ws_bytes, void* stream) {
+  MI_ARG(M >= 0 && N > 0 && K > 0 && E > 0 && E <= 1024, "invalid GEMM shape");
+  MI_ARG(N % 8 == 0, "N must be a multiple of 8");
+  bool need_quant = false;
+  if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
+    MI_ARG(N % 128 == 0 && K % 128 == 0, "fp8 block scaling needs N and K % 128 == 0");
+    MI_ARG(b_scale != nullptr, "fp8 block scaling needs ptr_B_scale");
+    if (a_dtype == MI355MOE_FP8E4M3) {
+      MI_ARG(a_scale != nullptr, "e4m3 activations need ptr_A_scale [M, K/128]");
+    } else {
+      MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
+             "activations must be bfloat16, float16 or e4m3");
+      need_quant = true;
+    }
+    MI_ARG(out_dtype == MI355MOE_BF16 || out_dtype == MI355MOE_F16, "output must be 16-bit");
+  } else if (recipe == MI355MOE_RECIPE_MXFP4) {
+    MI_ARG(K % 32 == 0, "mxfp4 needs K % 32 == 0");
+    MI_ARG(a_dtype == MI355MOE_BF16, "mxfp4 activations must be bfloat16");
+    MI_ARG(b_scale != nullptr, "mxfp4 needs e8m0 scales");
+  } else {
+    MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
+    MI_ARG(a_dtype == MI355MOE_BF16, "bf16 recipe needs bfloat16 activations");
+    MI_ARG(K % 8 == 0, "K must be a multiple of 8");
+  }
+  if (M == 0) return MI355MOE_OK;
+  GGLayout L = gg_plan(recipe, need_quant, M, K, E, static_cast<uint8_t*>(ws));
+  MI_CHECK(ws && ws_bytes >= L.bytes, MI355MOE_ERR_WORKSPACE,
+           "workspace too small for grouped_gemm");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = run_segments_to_blocks(rows_per_expert, E, L.bm, L.rows, L.max_padded,
+                                  L.eids, L.max_blocks, L.ntp,
+                                  static_cast<int32_t>(M), st);
+  if (rc) return rc;
+  const void* Aq = A;
+  const float* As = a_scale;
+  if (need_quant) {
+    rc = mi355moe_per_token_group_fp8_quant(A, a_dtype, L.aq, L.as, M, K, 128,
+                                            1e-10f, -448.f, 448.f, 0, st);
+    if (rc) return rc;
+    Aq = L.aq;
+    As = L.as;
+  }
+  GemmArgs g{};
+  g.A = Aq;
+  g.a_scale = As;
+  g.B = B;
+  g.b_scale = b_scale;
+  g.bias = static_cast<const uint16_t*>(bias);
+  g.D = D;
+  g.row_ids = L.rows;
+  g.block_expert = L.eids;
+  g.ntp = L.ntp;
+  g.num_valid = static_cast<int32_t>(M);
+  g.a_div = 1;
+  g.N = N;
+  g.K = K;
+  g.ldb_rows = N;
+  g.out_f16 = out_dtype == MI355MOE_F16;
+  return launch_moe_gemm_q(recipe, EPI_STORE, false, L.bm, g, L.grid_blocks, nullptr, st);
+}

@@ -1,0 +1,61 @@
+// Grouped-GEMM launcher shared by the grouped_gemm and fused_moe entry points.
+#pragma once
+
+#include "common.h"
+
+namespace mi355 {
+
+// One launch computes, for every block b of BM sorted slots (all of one
+// expert e = block_expert[b]):
+//   rows  r_i = row_ids[b*BM + i]   (r_i >= num_valid: padding slot)
+//   A row = a_by_pos ? b*BM+i : r_i / a_div
+//   D row = d_by_pos ? b*BM+i : r_i
+//   STORE: D[row, n] = T(sum_k A[row,k] W_e[n,k] + bias_e[n])
+//   GLU:   g = T(acc(n) + b(n)), u = T(acc(I+n) + b(I+n)),
+//          D[row, n] = act(g, u)          (n < N = I; W_e has 2I rows)
+struct GemmArgs {
+  const void* A;
+  const float* a_scale;  // fp8: [rowsA, K/128]
+  const void* B;         // [E, ldb_rows, K] (mxfp4: K/2 bytes per row)
+  const void* b_scale;   // fp8: f32 [E, ldb_rows/128, K/128]; mxfp4: u8 [E, ldb_rows, K/32]
+  const uint16_t* bias;  // [E, ldb_rows] bf16 or null
+  void* D;
+  const int32_t* row_ids;
+  const int32_t* block_expert;
+  const int32_t* ntp;    // [1] number of valid padded slots
+  int32_t num_valid;
+  int32_t a_div;
+  int32_t a_by_pos;
+  int32_t d_by_pos;
+  int64_t N;
+  int64_t K;
+  int64_t ldb_rows;
+  int64_t up_off;        // GLU: row offset of the up half (= I)
+  float clamp_limit;     // GLU: <= 0 off
+  float alpha;           // swigluoai alpha
+  float limit;           // swigluoai limit
+  int32_t act;           // mi355moe_activation
+  int32_t out_f16;       // store fp16 instead of bf16 (recipe BF16 only)
+};
+
+enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };
+
+// Launch over max_blocks M-blocks of bm rows.  bm in {16, 32, 64, 128}.
+int launch_moe_gemm(int recipe, int epi, int bm, const GemmArgs& a,
+                    int64_t max_blocks, hipStream_t st);
+
+// Choose the M tile for an expected number of rows per active expert.
+int pick_block_m(int64_t slots, int64_t num_experts);
+
+int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
+                      int64_t id_bound, const int32_t* map, int64_t num_keys,
+                      int64_t bs, int32_t* sorted, int64_t max_padded,
+                      int32_t* eids, int64_t max_blocks, int32_t* ntp,
+                      int32_t* inv, int32_t* counts, int32_t pad,
+                      hipStream_t st);
+int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
+                           int32_t* row_ids, int64_t max_padded,
+                           int32_t* eids, int64_t max_blocks, int32_t* ntp,
+                           int32_t pad, hipStream_t st);
+
+}  // namespace mi355

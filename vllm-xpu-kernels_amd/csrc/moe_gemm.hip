@@ -1,0 +1,374 @@
+// Grouped GEMM over block-aligned expert segments on gfx950 MFMA.
+//
+// Layout of one workgroup (256 threads = 4 wavefronts): BM sorted slots of a
+// single expert x BN output columns; wave w owns columns [w*BN/4, (w+1)*BN/4)
+// for all BM rows.  The MFMA's A operand is the expert weight fragment (16
+// output columns, loaded straight from HBM into VGPRs: weights are streamed
+// exactly once per workgroup) and its B operand is the activation fragment
+// (16 slots, staged in LDS and shared by the 4 waves), so every lane ends up
+// holding 4 consecutive output columns of one slot row.
+//
+//   bf16     v_mfma_f32_16x16x32_bf16, K stage 128 (4 MFMA steps)
+//   fp8block v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 x e4m3, unit scales), one
+//            MFMA per 128-wide K block; the fp32 block scales of the weight
+//            (128x128) and activation (1x128) multiply its partial sum.
+//   mxfp4    e2m1 weights converted in registers to bf16 with their e8m0
+//            scale (v_cvt_scalef32_pk_bf16_fp4), then the bf16 MFMA.
+//
+// Epilogues: STORE (bias, round) and GLU (gate/up halves of w13 -> SiLU-mul or
+// swigluoai), optionally re-quantising the activation to e4m3 with 1x128
+// scales for the w2 GEMM.
+#include "moe_gemm.h"
+
+namespace mi355 {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int KB = 128;  // K elements per LDS stage
+
+__device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// e4m3 x e4m3, 16x16x128, scale exponents 127 (= 1.0) on both operands.
+__device__ __forceinline__ f32x4 mfma_fp8(uint4 a0, uint4 a1, uint4 b0,
+                                          uint4 b1) {
+  i32x8 a = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+             (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+  i32x8 b = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+             (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127,
+                                                          0, 127);
+}
+
+// 8 e2m1 codes (one 32-bit word, element t in bits 4t..4t+3) -> 8 bf16 scaled
+// by 2^(e-127).
+__device__ __forceinline__ uint4 fp4x8_to_bf16(uint32_t w, float scale) {
+  uint4 r;
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  r.x = __builtin_bit_cast(uint32_t, p0);
+  r.y = __builtin_bit_cast(uint32_t, p1);
+  r.z = __builtin_bit_cast(uint32_t, p2);
+  r.w = __builtin_bit_cast(uint32_t, p3);
+  return r;
+}
+
+__device__ __forceinline__ float round_out(float v, bool f16) {
+  return f16 ? f16_to_f32(f32_to_f16(v)) : bf16_to_f32(f32_to_bf16(v));
+}
+
+__device__ __forceinline__ float glu(float g, float u, const GemmArgs& a) {
+  if (a.act == MI355MOE_ACT_SILU) {
+    float s = bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g))));
+    return s * u;
+  }
+  g = g > a.limit ? a.limit : g;
+  u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+  return (u + 1.f) * (g * (1.f / (1.f + expf(-g * a.alpha))));
+}
+
+template <int RECIPE, int BM, int BN, int EPI, bool QOUT>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
+                                                       void* __restrict__ qs) {
+  constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
+  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4;
+  constexpr int XB = kFp8 ? 1 : 2;      // bytes per activation element
+  constexpr int ROWB = KB * XB + 16;    // padded LDS row pitch (bytes)
+  constexpr int CPR = KB * XB / 16;     // 16-byte chunks per staged row
+  constexpr int MT = BM / 16;
+  constexpr int WN = BN / 4;
+  constexpr int NT = WN / 16;
+  constexpr int NB = EPI == EPI_GLU ? 2 * NT : NT;
+  constexpr int KS = kFp8 ? 1 : 4;      // MFMA k-steps per stage
+
+  __shared__ __attribute__((aligned(16))) uint8_t sX[BM * ROWB];
+  __shared__ int s_arow[BM];
+  __shared__ int s_drow[BM];
+  __shared__ float s_xs[BM];
+  __shared__ float s_amax[4][BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, q = lane >> 4;
+  const int blk = blockIdx.y;
+  if (blk * BM >= *a.ntp) return;  // uniform for the workgroup
+  const int e = a.block_expert[blk];
+  const int64_t K = a.K;
+  const int64_t wrow_bytes = kFp4 ? K / 2 : K * XB;
+
+  if (tid < BM) {
+    const int rid = a.row_ids[static_cast<int64_t>(blk) * BM + tid];
+    const bool ok = rid >= 0 && rid < a.num_valid;
+    s_arow[tid] = ok ? (a.a_by_pos ? blk * BM + tid : rid / a.a_div) : -1;
+    s_drow[tid] = ok ? (a.d_by_pos ? blk * BM + tid : rid) : -1;
+  }
+
+  const int64_t nbase = static_cast<int64_t>(blockIdx.x) * BN + wave * WN;
+  const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
+                         static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
+  const uint8_t* wptr[NB];
+  bool wok[NB];
+  int64_t wrow[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int64_t n = nbase + (j % NT) * 16 + l16;
+    wok[j] = n < a.N;
+    wrow[j] = (j >= NT ? a.up_off : 0) + (wok[j] ? n : 0);
+    wptr[j] = wbase + wrow[j] * wrow_bytes;
+  }
+
+  f32x4 acc[MT][NB];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+
+  for (int64_t k0 = 0; k0 < K; k0 += KB) {
+    const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
+    // ---- weight fragments: HBM -> VGPR
+    uint4 wf[KS][NB][kFp8 ? 2 : 1];
+    float wsc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if constexpr (kFp8) {
+        const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + k0 + 32 * q);
+        wf[0][j][0] = wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
+        wf[0][j][1] = wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
+        const float* bs = static_cast<const float*>(a.b_scale);
+        wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wrow[j] / 128) *
+                        (K / 128) + k0 / 128];
+      } else if constexpr (kFp4) {
+        const bool ok = wok[j] && 32 * q < kb;
+        uint4 v = ok ? *reinterpret_cast<const uint4*>(wptr[j] + (k0 + 32 * q) / 2)
+                     : make_uint4(0, 0, 0, 0);
+        const uint8_t* bs = static_cast<const uint8_t*>(a.b_scale);
+        uint32_t ex = ok ? bs[(static_cast<int64_t>(e) * a.ldb_rows + wrow[j]) *
+                                  (K / 32) + (k0 + 32 * q) / 32]
+                         : 0u;
+        if (ex == 0u) v = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> scale 0
+        const float sc = __uint_as_float(ex << 23);
+        wf[0][j][0] = fp4x8_to_bf16(v.x, sc);
+        wf[1][j][0] = fp4x8_to_bf16(v.y, sc);
+        wf[2][j][0] = fp4x8_to_bf16(v.z, sc);
+        wf[3][j][0] = fp4x8_to_bf16(v.w, sc);
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bool ok = wok[j] && 32 * s + 8 * q + 8 <= kb;
+          wf[s][j][0] = ok ? *reinterpret_cast<const uint4*>(
+                                 wptr[j] + (k0 + 32 * s + 8 * q) * 2)
+                           : make_uint4(0, 0, 0, 0);
+        }
+      }
+    }
+    // ---- activation tile -> LDS
+    __syncthreads();
+    for (int idx = tid; idx < BM * CPR; idx += 256) {
+      const int r = idx / CPR, c = idx % CPR;
+      const int ar = s_arow[r];
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (ar >= 0 && c * 16 < kb * XB)
+        v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
+                                            (static_cast<int64_t>(ar) * K + k0) * XB +
+                                            c * 16);
+      *reinterpret_cast<uint4*>(sX + r * ROWB + c * 16) = v;
+    }
+    if constexpr (kFp8) {
+      if (tid < BM) {
+        const int ar = s_arow[tid];
+        s_xs[tid] = ar >= 0 ? a.a_scale[static_cast<int64_t>(ar) * (K / 128) + k0 / 128] : 0.f;
+      }
+    }
+    __syncthreads();
+    // ---- MFMA
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint8_t* xr = sX + (mt * 16 + l16) * ROWB;
+      if constexpr (kFp8) {
+        const uint4 x0 = *reinterpret_cast<const uint4*>(xr + 32 * q);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(xr + 32 * q + 16);
+        const float xs = s_xs[mt * 16 + l16];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          f32x4 p = mfma_fp8(wf[0][j][0], wf[0][j][1], x0, x1);
+          const float sc = xs * wsc[j];
+          acc[mt][j] += p * sc;
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int koff = kFp4 ? (32 * q + 8 * s) : (32 * s + 8 * q);
+          const uint4 x = *reinterpret_cast<const uint4*>(xr + koff * 2);
+#pragma unroll
+          for (int j = 0; j < NB; ++j) acc[mt][j] = mfma_bf16(wf[s][j][0], x, acc[mt][j]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds D[row = mt*16 + l16][n = nbase + j*16 + 4q + r]
+  const bool f16 = a.out_f16 != 0;
+  const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  float outv[MT][NT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t n = nbase + j * 16 + 4 * q;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool nok = n + r < a.N;
+        float v = acc[mt][j][r];
+        if (a.bias && nok) v += bf16_to_f32(a.bias[bias_base + n + r]);
+        v = round_out(v, f16);
+        if constexpr (EPI == EPI_GLU) {
+          float u = acc[mt][j + NT][r];
+          if (a.bias && nok) u += bf16_to_f32(a.bias[bias_base + a.up_off + n + r]);
+          u = round_out(u, f16);
+          if (a.clamp_limit > 0.f) {
+            v = fminf(v, a.clamp_limit);
+            u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
+          }
+          v = round_out(glu(v, u, a), f16);
+        }
+        outv[mt][j][r] = nok ? v : 0.f;
+      }
+    }
+  }
+
+  if constexpr (QOUT) {
+    // e4m3 output with one fp32 scale per (row, 128 columns): BN == 128 and
+    // the 4 waves cover the 128 columns of the group.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float m = 1e-10f;
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(outv[mt][j][r]));
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      if (q == 0) s_amax[wave][mt * 16 + l16] = m;
+    }
+    __syncthreads();
+    uint8_t* dq = static_cast<uint8_t*>(a.D);
+    float* ds = static_cast<float*>(qs);
+    const int64_t ngroups = a.N / 128;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = mt * 16 + l16;
+      const int drow = s_drow[row];
+      if (drow < 0) continue;
+      const float am = fmaxf(fmaxf(s_amax[0][row], s_amax[1][row]),
+                             fmaxf(s_amax[2][row], s_amax[3][row]));
+      const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
+      const float inv = 1.0f / sc;
+      if (wave == 0 && q == 0) ds[static_cast<int64_t>(drow) * ngroups + blockIdx.x] = sc;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t n = nbase + j * 16 + 4 * q;
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float x = fminf(fmaxf(outv[mt][j][r] * inv, -448.f), 448.f);
+          w |= f32_to_e4m3(x) << (8 * r);
+        }
+        *reinterpret_cast<uint32_t*>(dq + static_cast<int64_t>(drow) * a.N + n) = w;
+      }
+    }
+  } else {
+    uint16_t* d = static_cast<uint16_t*>(a.D);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int drow = s_drow[mt * 16 + l16];
+      if (drow < 0) continue;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t n = nbase + j * 16 + 4 * q;
+        uint16_t h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          h[r] = f16 ? f32_to_f16(outv[mt][j][r]) : f32_to_bf16(outv[mt][j][r]);
+        uint16_t* dst = d + static_cast<int64_t>(drow) * a.N + n;
+        if (n + 3 < a.N && (a.N & 3) == 0) {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < a.N) dst[r] = h[r];
+        }
+      }
+    }
+  }
+}
+
+template <int RECIPE, int BM, int EPI, bool QOUT>
+void launch_tile(const GemmArgs& a, int64_t max_blocks, void* qs,
+                 hipStream_t st) {
+  constexpr int BN = (BM == 16 && !QOUT) ? 64 : 128;
+  dim3 grid(static_cast<unsigned>(cdiv(a.N, BN)),
+            static_cast<unsigned>(max_blocks));
+  moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT><<<grid, dim3(256), 0, st>>>(a, qs);
+}
+
+template <int RECIPE, int EPI, bool QOUT>
+int launch_bm(int bm, const GemmArgs& a, int64_t max_blocks, void* qs,
+              hipStream_t st) {
+  switch (bm) {
+    case 16: launch_tile<RECIPE, 16, EPI, QOUT>(a, max_blocks, qs, st); break;
+    case 32: launch_tile<RECIPE, 32, EPI, QOUT>(a, max_blocks, qs, st); break;
+    case 64: launch_tile<RECIPE, 64, EPI, QOUT>(a, max_blocks, qs, st); break;
+    case 128: launch_tile<RECIPE, 128, EPI, QOUT>(a, max_blocks, qs, st); break;
+    default: return set_error(MI355MOE_ERR_INVALID, "block_m must be 16, 32, 64 or 128");
+  }
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+}  // namespace
+
+int pick_block_m(int64_t slots, int64_t num_experts) {
+  const int64_t active = slots < num_experts ? slots : num_experts;
+  const int64_t avg = active > 0 ? slots / active : 0;
+  if (avg <= 24) return 16;
+  if (avg <= 48) return 32;
+  if (avg <= 96) return 64;
+  return 128;
+}
+
+int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,
+                      int64_t max_blocks, void* qs, hipStream_t st) {
+  if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
+  if (qout) {
+    MI_ARG(recipe == MI355MOE_RECIPE_FP8BLOCK && epi == EPI_GLU && a.N % 128 == 0,
+           "fp8 activation output needs the fp8block recipe and I % 128 == 0");
+    return launch_bm<MI355MOE_RECIPE_FP8BLOCK, EPI_GLU, true>(bm, a, max_blocks, qs, st);
+  }
+#define MI_EPI(R)                                                            \
+  return epi == EPI_GLU ? launch_bm<R, EPI_GLU, false>(bm, a, max_blocks, qs, st) \
+                        : launch_bm<R, EPI_STORE, false>(bm, a, max_blocks, qs, st);
+  switch (recipe) {
+    case MI355MOE_RECIPE_BF16: MI_EPI(MI355MOE_RECIPE_BF16)
+    case MI355MOE_RECIPE_FP8BLOCK: MI_EPI(MI355MOE_RECIPE_FP8BLOCK)
+    case MI355MOE_RECIPE_MXFP4: MI_EPI(MI355MOE_RECIPE_MXFP4)
+    default: return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
+  }
+#undef MI_EPI
+}
+
+int launch_moe_gemm(int recipe, int epi, int bm, const GemmArgs& a,
+                    int64_t max_blocks, hipStream_t st) {
+  return launch_moe_gemm_q(recipe, epi, false, bm, a, max_blocks, nullptr, st);
+}
+
+}  // namespace mi355

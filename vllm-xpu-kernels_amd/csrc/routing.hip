@@ -1,0 +1,343 @@
+// Routing: softmax / sigmoid top-k and grouped top-k, one 64-lane wavefront
+// per token.  Ties always go to the lower expert index (reference:
+// csrc/moe/topk.cpp:536-545, csrc/moe/grouped_topk.cpp:36-45).
+#include "common.h"
+
+namespace mi355 {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+
+template <typename In>
+__device__ __forceinline__ float load_in(const void* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_in<F32>(const void* p, int64_t i) {
+  return static_cast<const float*>(p)[i];
+}
+template <>
+__device__ __forceinline__ float load_in<BF16>(const void* p, int64_t i) {
+  return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <>
+__device__ __forceinline__ float load_in<F16>(const void* p, int64_t i) {
+  return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+__device__ __forceinline__ void store_idx(void* p, int dt, int64_t i, int v) {
+  if (dt == MI355MOE_I64)
+    static_cast<int64_t*>(p)[i] = v;
+  else
+    static_cast<int32_t*>(p)[i] = v;  // I32 and U32 share the bit pattern
+}
+
+// (value desc, index asc) "is a better than b"
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// Wave-wide argmax over (value, index) pairs; every lane gets the winner.
+__device__ __forceinline__ void wave_argmax(float& v, float& aux, int& idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    float oa = __shfl_xor(aux, o, 64);
+    int oi = __shfl_xor(idx, o, 64);
+    if (better(ov, oi, v, idx)) {
+      v = ov;
+      aux = oa;
+      idx = oi;
+    }
+  }
+}
+
+// Lane l holds experts e = i*64 + l, i < VPT (coalesced loads).
+template <typename In, int VPT, bool SIGMOID>
+__global__ __launch_bounds__(256) void topk_gating_kernel(
+    const void* __restrict__ gating, float* __restrict__ out_w,
+    void* __restrict__ out_idx, int idx_dtype, int32_t* __restrict__ out_src,
+    const float* __restrict__ bias, int num_tokens, int num_experts, int k,
+    int renormalize, float rsf) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (row >= num_tokens) return;
+  const int64_t base = static_cast<int64_t>(row) * num_experts;
+
+  float p[VPT], sel[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    int e = i * 64 + lane;
+    p[i] = e < num_experts ? load_in<In>(gating, base + e) : -INFINITY;
+  }
+  if constexpr (!SIGMOID) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) m = fmaxf(m, p[i]);
+    m = wave_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      int e = i * 64 + lane;
+      p[i] = e < num_experts ? expf(p[i] - m) : 0.f;
+      s += p[i];
+    }
+    s = wave_sum(s);
+    const float r = 1.f / s;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) p[i] *= r;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      float sg = 1.f / (1.f + expf(-p[i]));
+      // round to the input dtype (csrc/moe/topk.cpp:19-23)
+      if constexpr (std::is_same<In, BF16>::value) sg = bf16_to_f32(f32_to_bf16(sg));
+      if constexpr (std::is_same<In, F16>::value) sg = f16_to_f32(f32_to_f16(sg));
+      p[i] = sg;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    int e = i * 64 + lane;
+    if (e < num_experts)
+      sel[i] = bias ? p[i] + bias[e] : p[i];
+    else
+      sel[i] = -INFINITY;
+  }
+
+  float wsum = 0.f;
+  float myw = 0.f;  // lane j < k keeps the j-th weight
+  int myid = 0;
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY, bp = 0.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      int e = i * 64 + lane;
+      if (e < num_experts && better(sel[i], e, bv, bi)) {
+        bv = sel[i];
+        bp = p[i];
+        bi = e;
+      }
+    }
+    wave_argmax(bv, bp, bi);
+    wsum += bp;
+    if (lane == j) {
+      myw = bp;
+      myid = bi;
+    }
+    // retire the winner so the next round cannot pick it again
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (i * 64 + lane == bi) sel[i] = -INFINITY;
+  }
+  if (lane < k) {
+    float scale = rsf;
+    if (renormalize) scale /= (wsum > 0.f ? wsum : 1.f);
+    const int64_t o = static_cast<int64_t>(row) * k + lane;
+    out_w[o] = myw * scale;
+    store_idx(out_idx, idx_dtype, o, myid);
+    out_src[o] = lane * num_tokens + row;
+  }
+}
+
+template <typename In, bool SIGMOID>
+int launch_topk(float* w, void* idx, int idt, int32_t* src, const void* g,
+                int64_t T, int64_t E, int64_t k, int renorm, const float* bias,
+                float rsf, hipStream_t st) {
+  dim3 grid(static_cast<unsigned>(cdiv(T, kWavesPerBlock))), block(256);
+  if (T == 0) return MI355MOE_OK;
+#define MI_TOPK_CASE(V)                                                       \
+  if (E <= 64 * V) {                                                          \
+    hipLaunchKernelGGL((topk_gating_kernel<In, V, SIGMOID>), grid, block, 0,  \
+                       st, g, w, idx, idt, src, bias, (int)T, (int)E, (int)k, \
+                       renorm, rsf);                                          \
+    MI_LAUNCH_CHECK();                                                        \
+    return MI355MOE_OK;                                                       \
+  }
+  MI_TOPK_CASE(1)
+  MI_TOPK_CASE(2)
+  MI_TOPK_CASE(4)
+  MI_TOPK_CASE(8)
+  MI_TOPK_CASE(16)
+#undef MI_TOPK_CASE
+  return set_error(MI355MOE_ERR_UNSUPPORTED, "num_experts > 1024 is not supported");
+}
+
+template <bool SIGMOID>
+int topk_dispatch(float* w, void* idx, int idt, int32_t* src, const void* g,
+                  int gdt, int64_t T, int64_t E, int64_t k, int renorm,
+                  const float* bias, float rsf, void* stream) {
+  MI_ARG(T >= 0 && E > 0, "invalid num_tokens / num_experts");
+  MI_ARG(k > 0 && k <= E && k <= 64, "topk must be in [1, min(num_experts, 64)]");
+  MI_ARG(idt == MI355MOE_I32 || idt == MI355MOE_I64 || idt == MI355MOE_U32,
+         "topk_indices must be int32, int64 or uint32");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (gdt) {
+    case MI355MOE_F32: return launch_topk<F32, SIGMOID>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st);
+    case MI355MOE_BF16: return launch_topk<BF16, SIGMOID>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st);
+    case MI355MOE_F16: return launch_topk<F16, SIGMOID>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st);
+    default: return set_error(MI355MOE_ERR_INVALID, "gating_output must be float32, bfloat16 or float16");
+  }
+}
+
+// ----------------------------------------------------------------------------
+// grouped top-k (DeepSeek-V3 noaux_tc routing).  One wave per token; the
+// scores_with_bias row is staged in LDS.
+//   group score = top1 + top2 of scores_with_bias in the group (fp32 sum,
+//                 stored in the input dtype)
+//   keep topk_group groups by (score desc, group asc)
+//   ids = top-k of scores_with_bias over kept groups (value desc, id asc)
+//   w   = scores[id] / (1e-20 + sum) * rsf   (or scores[id] * rsf)
+// ----------------------------------------------------------------------------
+constexpr int kMaxGroupedExperts = 1024;
+
+template <typename In>
+__global__ __launch_bounds__(256) void grouped_topk_kernel(
+    const void* __restrict__ scores, const void* __restrict__ scores_b,
+    void* __restrict__ out_v, int32_t* __restrict__ out_i, int num_tokens,
+    int num_experts, int n_group, int topk_group, int k, int renormalize,
+    float rsf) {
+  __shared__ float s_sb[kWavesPerBlock][kMaxGroupedExperts];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kWavesPerBlock + wave;
+  if (row >= num_tokens) return;  // whole wave exits together
+  const int64_t base = static_cast<int64_t>(row) * num_experts;
+  float* sb = s_sb[wave];
+  for (int e = lane; e < num_experts; e += 64) {
+    float v = load_in<In>(scores_b, base + e);
+    sb[e] = v;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  const int epg = num_experts / n_group;
+
+  // --- group scores: lane g < n_group scans its group
+  float gscore = -INFINITY;
+  if (lane < n_group) {
+    float t1 = -INFINITY, t2 = -INFINITY;
+    for (int i = 0; i < epg; ++i) {
+      float v = sb[lane * epg + i];
+      if (v > t1) {
+        t2 = t1;
+        t1 = v;
+      } else if (v > t2) {
+        t2 = v;
+      }
+    }
+    float s = (epg >= 2) ? t1 + t2 : t1 + t1;
+    if constexpr (std::is_same<In, BF16>::value) s = bf16_to_f32(f32_to_bf16(s));
+    if constexpr (std::is_same<In, F16>::value) s = f16_to_f32(f32_to_f16(s));
+    gscore = __builtin_isfinite(s) ? s : -INFINITY;
+  }
+  // --- pick topk_group groups
+  unsigned long long kept = 0ull;
+  float thr = -INFINITY;
+  {
+    float gv = lane < n_group ? gscore : -INFINITY;
+    for (int j = 0; j < topk_group; ++j) {
+      float v = gv, aux = 0.f;
+      int gi = lane < n_group ? lane : 0x7fffffff;
+      wave_argmax(v, aux, gi);
+      thr = v;
+      if (gi >= 0 && gi < 64) kept |= (1ull << gi);
+      if (lane == gi) gv = -INFINITY;
+    }
+  }
+  const bool proceed = thr != -INFINITY;
+  float myv = 0.f;
+  int myid = 0;
+  if (proceed) {
+    float wsum = 1e-20f;
+    // candidates live in LDS: experts of dropped groups and non-finite
+    // values become -inf; each round retires its winner in place.
+    for (int e = lane; e < num_experts; e += 64) {
+      float v = sb[e];
+      if (!((kept >> (e / epg)) & 1ull) || !__builtin_isfinite(v)) v = -INFINITY;
+      sb[e] = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    for (int j = 0; j < k; ++j) {
+      float bv = -INFINITY, aux = 0.f;
+      int bi = 0x7fffffff;
+      for (int e = lane; e < num_experts; e += 64) {
+        float v = sb[e];
+        if (better(v, e, bv, bi)) {
+          bv = v;
+          bi = e;
+        }
+      }
+      wave_argmax(bv, aux, bi);
+      float sv = load_in<In>(scores, base + bi);
+      wsum += sv;
+      if (lane == j) {
+        myv = sv;
+        myid = bi;
+      }
+      if (lane == 0) sb[bi] = -INFINITY;
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+    if (lane < k) myv = renormalize ? myv / wsum * rsf : myv * rsf;
+  } else if (lane < k) {
+    myv = 1.f / k;
+    myid = lane;
+  }
+  if (lane < k) {
+    const int64_t o = static_cast<int64_t>(row) * k + lane;
+    out_i[o] = myid;
+    if constexpr (std::is_same<In, F32>::value)
+      static_cast<float*>(out_v)[o] = myv;
+    else if constexpr (std::is_same<In, BF16>::value)
+      static_cast<uint16_t*>(out_v)[o] = f32_to_bf16(myv);
+    else
+      static_cast<uint16_t*>(out_v)[o] = f32_to_f16(myv);
+  }
+}
+
+}  // namespace
+}  // namespace mi355
+
+using namespace mi355;
+
+extern "C" int mi355moe_topk_softmax(float* w, void* idx, int idt, int32_t* src,
+                                     const void* g, int gdt, int64_t T,
+                                     int64_t E, int64_t k, int renorm,
+                                     const float* bias, void* stream) {
+  return topk_dispatch<false>(w, idx, idt, src, g, gdt, T, E, k, renorm, bias, 1.f, stream);
+}
+
+extern "C" int mi355moe_topk_sigmoid(float* w, void* idx, int idt, int32_t* src,
+                                     const void* g, int gdt, int64_t T,
+                                     int64_t E, int64_t k, int renorm,
+                                     const float* bias, float rsf,
+                                     void* stream) {
+  return topk_dispatch<true>(w, idx, idt, src, g, gdt, T, E, k, renorm, bias, rsf, stream);
+}
+
+extern "C" int mi355moe_grouped_topk(void* vals, int32_t* ids, const void* scores,
+                                     const void* scores_b, int dt, int64_t T,
+                                     int64_t E, int64_t n_group,
+                                     int64_t topk_group, int64_t k, int renorm,
+                                     float rsf, void* stream) {
+  MI_ARG(E > 0 && E <= kMaxGroupedExperts, "num_experts must be in [1, 1024]");
+  MI_ARG(n_group > 0 && n_group <= 32, "n_group must be in [1, 32]");
+  MI_ARG(E % n_group == 0, "num_experts must be divisible by n_group");
+  MI_ARG(topk_group > 0 && topk_group <= n_group, "topk_group must be in [1, n_group]");
+  MI_ARG(k > 0 && k <= 32, "topk must be in [1, 32]");
+  MI_ARG(k <= topk_group * (E / n_group), "topk exceeds the experts of the kept groups");
+  if (T == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(T, kWavesPerBlock))), block(256);
+#define MI_GT(In)                                                               \
+  hipLaunchKernelGGL(grouped_topk_kernel<In>, grid, block, 0, st, scores,       \
+                     scores_b, vals, ids, (int)T, (int)E, (int)n_group,         \
+                     (int)topk_group, (int)k, renorm, rsf);
+  switch (dt) {
+    case MI355MOE_F32: MI_GT(F32) break;
+    case MI355MOE_BF16: MI_GT(BF16) break;
+    case MI355MOE_F16: MI_GT(F16) break;
+    default: return set_error(MI355MOE_ERR_INVALID, "scores must be float32, bfloat16 or float16");
+  }
+#undef MI_GT
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}

@@ -1,0 +1,560 @@
+// PyTorch-ROCm op registration over the mi355moe C ABI.
+//
+// Registers the reference's schemas verbatim in the same namespaces
+// (_moe_C, _C, _xpu_C; reference csrc/moe/torch_bindings.cpp,
+// csrc/torch_bindings.cpp, csrc/xpu/torch_bindings.cpp) for the CUDA dispatch
+// key, which is how HIP devices appear in PyTorch-ROCm.  There is no CPU
+// implementation: the ops exist only on the GPU.  Argument checks mirror the
+// reference's TORCH_CHECK messages; the C ABI's own checks surface through
+// mi355moe_last_error().
+#include <ATen/ATen.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "../../include/mi355moe.h"
+
+namespace {
+
+hipStream_t cur_stream(const at::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_rc(int rc, const char* op) {
+  TORCH_CHECK(rc == MI355MOE_OK, op, ": ", mi355moe_last_error());
+}
+
+int dtype_code(at::ScalarType s) {
+  switch (s) {
+    case at::kFloat: return MI355MOE_F32;
+    case at::kBFloat16: return MI355MOE_BF16;
+    case at::kHalf: return MI355MOE_F16;
+    case at::kInt: return MI355MOE_I32;
+    case at::kLong: return MI355MOE_I64;
+    case at::kUInt32: return MI355MOE_U32;
+    case at::kFloat8_e4m3fn: return MI355MOE_FP8E4M3;
+    case at::kByte: return MI355MOE_U8;
+    case at::kFloat4_e2m1fn_x2: return MI355MOE_U8;
+    case at::kFloat8_e8m0fnu: return MI355MOE_U8;
+    case at::kShort: return MI355MOE_I16;
+    default: return -1;
+  }
+}
+
+void check_gpu(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be on a GPU device");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+const void* opt_ptr(const std::optional<at::Tensor>& t) {
+  return t.has_value() ? t->data_ptr() : nullptr;
+}
+
+// ------------------------------------------------------------------ routing
+void topk_softmax(at::Tensor& topk_weights, at::Tensor& topk_indices,
+                  at::Tensor& token_expert_indices, at::Tensor& gating_output,
+                  bool renormalize, const std::optional<at::Tensor>& bias) {
+  check_gpu(gating_output, "gating_output");
+  check_gpu(topk_weights, "topk_weights");
+  check_gpu(topk_indices, "topk_indices");
+  check_gpu(token_expert_indices, "token_expert_indices");
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  TORCH_CHECK(token_expert_indices.scalar_type() == at::kInt,
+              "token_expert_indices must be int32");
+  const int64_t E = gating_output.size(-1);
+  const int64_t T = gating_output.numel() / E;
+  const int64_t k = topk_weights.size(-1);
+  if (bias) {
+    check_gpu(*bias, "bias");
+    TORCH_CHECK(bias->scalar_type() == at::kFloat, "bias must be float32");
+    TORCH_CHECK(bias->numel() == E, "bias must have num_experts elements");
+  }
+  c10::hip::HIPGuard g(gating_output.device());
+  check_rc(mi355moe_topk_softmax(
+               topk_weights.data_ptr<float>(), topk_indices.data_ptr(),
+               dtype_code(topk_indices.scalar_type()),
+               token_expert_indices.data_ptr<int32_t>(), gating_output.data_ptr(),
+               dtype_code(gating_output.scalar_type()), T, E, k, renormalize,
+               bias ? bias->data_ptr<float>() : nullptr, cur_stream(gating_output)),
+           "topk_softmax");
+}
+
+void topk_sigmoid(at::Tensor& topk_weights, at::Tensor& topk_indices,
+                  at::Tensor& token_expert_indices, at::Tensor& gating_output,
+                  bool renormalize, const std::optional<at::Tensor>& bias,
+                  double routed_scaling_factor) {
+  check_gpu(gating_output, "gating_output");
+  check_gpu(topk_weights, "topk_weights");
+  check_gpu(topk_indices, "topk_indices");
+  check_gpu(token_expert_indices, "token_expert_indices");
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  const int64_t E = gating_output.size(-1);
+  const int64_t T = gating_output.numel() / E;
+  const int64_t k = topk_weights.size(-1);
+  if (bias) {
+    check_gpu(*bias, "bias");
+    TORCH_CHECK(bias->scalar_type() == at::kFloat, "bias must be float32");
+  }
+  c10::hip::HIPGuard g(gating_output.device());
+  check_rc(mi355moe_topk_sigmoid(
+               topk_weights.data_ptr<float>(), topk_indices.data_ptr(),
+               dtype_code(topk_indices.scalar_type()),
+               token_expert_indices.data_ptr<int32_t>(), gating_output.data_ptr(),
+               dtype_code(gating_output.scalar_type()), T, E, k, renormalize,
+               bias ? bias->data_ptr<float>() : nullptr,
+               static_cast<float>(routed_scaling_factor), cur_stream(gating_output)),
+           "topk_sigmoid");
+}
+
+std::tuple<at::Tensor, at::Tensor> grouped_topk(at::Tensor& scores,
+                                                at::Tensor& scores_with_bias,
+                                                int64_t n_group,
+                                                int64_t topk_group, int64_t topk,
+                                                bool renormalize,
+                                                double routed_scaling_factor) {
+  check_gpu(scores, "scores");
+  check_gpu(scores_with_bias, "scores_with_bias");
+  TORCH_CHECK(scores.scalar_type() == scores_with_bias.scalar_type(),
+              "scores and scores_with_bias must have the same dtype");
+  TORCH_CHECK(n_group <= 32,
+              "n_group should be smaller than or equal to 32 for now");
+  TORCH_CHECK(topk <= 32, "topk should be smaller than or equal to 32 for now");
+  const int64_t T = scores.size(0), E = scores.size(1);
+  auto vals = at::empty({T, topk}, scores.options());
+  auto ids = at::empty({T, topk}, scores.options().dtype(at::kInt));
+  c10::hip::HIPGuard g(scores.device());
+  check_rc(mi355moe_grouped_topk(vals.data_ptr(), ids.data_ptr<int32_t>(),
+                                 scores.data_ptr(), scores_with_bias.data_ptr(),
+                                 dtype_code(scores.scalar_type()), T, E, n_group,
+                                 topk_group, topk, renormalize,
+                                 static_cast<float>(routed_scaling_factor),
+                                 cur_stream(scores)),
+           "grouped_topk");
+  return {vals, ids};
+}
+
+std::tuple<at::Tensor, at::Tensor> grouped_topk_meta(
+    at::Tensor& scores, at::Tensor&, int64_t, int64_t, int64_t topk, bool,
+    double) {
+  auto vals = at::empty({scores.size(0), topk}, scores.options());
+  auto ids = at::empty({scores.size(0), topk}, scores.options().dtype(at::kInt));
+  return {vals, ids};
+}
+
+// ---------------------------------------------------------------- alignment
+void moe_align_block_size(at::Tensor topk_ids, int64_t num_experts,
+                          int64_t block_size, at::Tensor sorted_token_ids,
+                          at::Tensor experts_ids, at::Tensor num_tokens_post_pad,
+                          const std::optional<at::Tensor>& maybe_expert_map) {
+  check_gpu(topk_ids, "topk_ids");
+  check_gpu(sorted_token_ids, "sorted_token_ids");
+  check_gpu(experts_ids, "experts_ids");
+  check_gpu(num_tokens_post_pad, "num_tokens_post_pad");
+  TORCH_CHECK(sorted_token_ids.scalar_type() == at::kInt &&
+                  experts_ids.scalar_type() == at::kInt &&
+                  num_tokens_post_pad.scalar_type() == at::kInt,
+              "sorted_token_ids, experts_ids and num_tokens_post_pad must be int32");
+  if (maybe_expert_map) {
+    check_gpu(*maybe_expert_map, "expert_map");
+    TORCH_CHECK(maybe_expert_map->scalar_type() == at::kInt, "expert_map must be int32");
+  }
+  c10::hip::HIPGuard g(topk_ids.device());
+  check_rc(mi355moe_moe_align_block_size(
+               topk_ids.data_ptr(), dtype_code(topk_ids.scalar_type()),
+               topk_ids.numel(), num_experts, block_size,
+               sorted_token_ids.data_ptr<int32_t>(), sorted_token_ids.numel(),
+               experts_ids.data_ptr<int32_t>(), experts_ids.numel(),
+               num_tokens_post_pad.data_ptr<int32_t>(),
+               maybe_expert_map ? maybe_expert_map->data_ptr<int32_t>() : nullptr,
+               nullptr, 0, cur_stream(topk_ids)),
+           "moe_align_block_size");
+}
+
+void remap_hidden_states(at::Tensor& hidden_states,
+                         const std::optional<at::Tensor>& hidden_states_scales,
+                         at::Tensor& remapped_hidden_states,
+                         const std::optional<at::Tensor>& remapped_hidden_states_scales,
+                         const std::optional<at::Tensor>& expert_map,
+                         at::Tensor& rows_per_expert,
+                         at::Tensor& unpermuted_row_to_permuted_row,
+                         at::Tensor& topk_ids, int64_t total_experts_num,
+                         int64_t local_experts_num) {
+  check_gpu(hidden_states, "hidden_states");
+  check_gpu(remapped_hidden_states, "remapped_hidden_states");
+  check_gpu(rows_per_expert, "rows_per_expert");
+  check_gpu(unpermuted_row_to_permuted_row, "unpermuted_row_to_permuted_row");
+  check_gpu(topk_ids, "topk_ids");
+  TORCH_CHECK(local_experts_num <= 1024,
+              "local experts number should be less than or equal to 1024");
+  const int64_t T = hidden_states.size(0);
+  const int64_t k = topk_ids.size(1);
+  int64_t scale_cols = 0, scale_bytes = 0;
+  if (hidden_states_scales && remapped_hidden_states_scales) {
+    scale_cols = hidden_states_scales->numel() / std::max<int64_t>(T, 1);
+    scale_bytes = hidden_states_scales->element_size();
+  }
+  c10::hip::HIPGuard g(hidden_states.device());
+  check_rc(mi355moe_remap_hidden_states(
+               hidden_states.data_ptr(), hidden_states.element_size(),
+               opt_ptr(hidden_states_scales), scale_cols, scale_bytes,
+               remapped_hidden_states.data_ptr(),
+               remapped_hidden_states_scales ? remapped_hidden_states_scales->data_ptr()
+                                             : nullptr,
+               expert_map ? expert_map->data_ptr<int32_t>() : nullptr,
+               rows_per_expert.data_ptr<int32_t>(),
+               unpermuted_row_to_permuted_row.data_ptr<int32_t>(),
+               topk_ids.data_ptr(), dtype_code(topk_ids.scalar_type()), T,
+               hidden_states.numel() / std::max<int64_t>(T, 1), k,
+               total_experts_num, local_experts_num, nullptr, 0,
+               cur_stream(hidden_states)),
+           "remap_hidden_states");
+}
+
+void init_expert_map(at::Tensor expert_map, int64_t num_experts,
+                     int64_t ep_rank, int64_t ep_size) {
+  check_gpu(expert_map, "expert_map");
+  TORCH_CHECK(expert_map.scalar_type() == at::kInt, "expert_map must be int32");
+  TORCH_CHECK(expert_map.numel() >= num_experts * ep_size,
+              "expert_map must hold num_experts * ep_size entries");
+  c10::hip::HIPGuard g(expert_map.device());
+  check_rc(mi355moe_init_expert_map(expert_map.data_ptr<int32_t>(), num_experts,
+                                    ep_rank, ep_size, cur_stream(expert_map)),
+           "init_expert_map");
+}
+
+// --------------------------------------------------------------- reductions
+void moe_sum(at::Tensor& input, at::Tensor& output,
+             const std::optional<at::Tensor>& topk_ids,
+             const std::optional<at::Tensor>& expert_map) {
+  const int64_t H = input.size(-1);
+  const int64_t T = output.numel() / H;
+  const int64_t topk = input.size(1);
+  TORCH_CHECK(input.scalar_type() == output.scalar_type(),
+              "moe_sum: input and output must have the same dtype");
+  TORCH_CHECK(input.device() == output.device(),
+              "moe_sum: input and output must be on the same device");
+  TORCH_CHECK(input.is_contiguous() && output.is_contiguous(),
+              "moe_sum expects contiguous input and output");
+  TORCH_CHECK(input.numel() == output.numel() * topk,
+              "moe_sum: input shape must be [num_tokens, topk, hidden] matching "
+              "output [num_tokens, hidden]");
+  TORCH_CHECK(!(expert_map.has_value() && !topk_ids.has_value()),
+              "moe_sum: expert_map requires topk_ids to be provided");
+  if (topk_ids) {
+    const auto& tk = *topk_ids;
+    TORCH_CHECK(tk.is_contiguous(), "moe_sum: topk_ids must be contiguous");
+    TORCH_CHECK(tk.device() == input.device(),
+                "moe_sum: topk_ids must be on the same device as input");
+    TORCH_CHECK(tk.dim() == 2 && tk.size(0) == T && tk.size(1) == topk,
+                "moe_sum: topk_ids must have shape [num_tokens, topk]");
+    if (expert_map) {
+      const auto& em = *expert_map;
+      TORCH_CHECK(em.scalar_type() == at::kInt, "moe_sum: expert_map must be int32");
+      TORCH_CHECK(em.is_contiguous(), "moe_sum: expert_map must be contiguous");
+      TORCH_CHECK(em.device() == input.device(),
+                  "moe_sum: expert_map must be on the same device as input");
+    }
+  }
+  TORCH_CHECK(input.is_cuda(), "moe_sum: input must be on a GPU device");
+  c10::hip::HIPGuard g(input.device());
+  check_rc(mi355moe_moe_sum(input.data_ptr(), output.data_ptr(),
+                            dtype_code(input.scalar_type()), T, topk, H,
+                            topk_ids ? topk_ids->data_ptr() : nullptr,
+                            topk_ids ? dtype_code(topk_ids->scalar_type()) : MI355MOE_I32,
+                            expert_map ? expert_map->data_ptr<int32_t>() : nullptr,
+                            expert_map ? expert_map->numel() : 0, cur_stream(input)),
+           "moe_sum");
+}
+
+void moe_gather(at::Tensor& output, at::Tensor& moe_output,
+                at::Tensor& topk_weights, at::Tensor& perm, int64_t num_experts) {
+  check_gpu(output, "output");
+  check_gpu(moe_output, "moe_output");
+  check_gpu(topk_weights, "topk_weights");
+  check_gpu(perm, "unpermuted_row_to_permuted_row");
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  TORCH_CHECK(perm.scalar_type() == at::kInt, "unpermuted_row_to_permuted_row must be int32");
+  TORCH_CHECK(output.scalar_type() == moe_output.scalar_type(),
+              "output and moe_output must have the same dtype");
+  const int64_t T = output.size(0), H = output.size(1), k = perm.size(1);
+  (void)num_experts;
+  c10::hip::HIPGuard g(output.device());
+  check_rc(mi355moe_moe_gather(output.data_ptr(), moe_output.data_ptr(),
+                               dtype_code(output.scalar_type()),
+                               topk_weights.data_ptr<float>(),
+                               perm.data_ptr<int32_t>(), T, k, H, cur_stream(output)),
+           "moe_gather");
+}
+
+// ------------------------------------------------------------- activations
+void silu_and_mul(at::Tensor& out, at::Tensor& input) {
+  check_gpu(out, "out");
+  check_gpu(input, "input");
+  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
+  const int64_t d = input.size(-1) / 2;
+  const int64_t rows = input.numel() / std::max<int64_t>(2 * d, 1);
+  c10::hip::HIPGuard g(input.device());
+  check_rc(mi355moe_silu_and_mul(out.data_ptr(), input.data_ptr(),
+                                 dtype_code(input.scalar_type()), rows, d,
+                                 cur_stream(input)),
+           "silu_and_mul");
+}
+
+void swigluoai_and_mul(at::Tensor& out, at::Tensor& input, double alpha, double limit) {
+  check_gpu(out, "out");
+  check_gpu(input, "input");
+  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
+  const int64_t d = input.size(-1) / 2;
+  const int64_t rows = input.numel() / std::max<int64_t>(2 * d, 1);
+  c10::hip::HIPGuard g(input.device());
+  check_rc(mi355moe_swigluoai_and_mul(out.data_ptr(), input.data_ptr(),
+                                      dtype_code(input.scalar_type()), rows, d,
+                                      static_cast<float>(alpha),
+                                      static_cast<float>(limit), cur_stream(input)),
+           "swigluoai_and_mul");
+}
+
+// ------------------------------------------------------------ quantisation
+void per_token_group_fp8_quant(const at::Tensor& input, at::Tensor& output_q,
+                               at::Tensor& output_s, int64_t group_size,
+                               double eps, double fp8_min, double fp8_max,
+                               bool scale_ue8m0, bool, bool) {
+  check_gpu(input, "input");
+  check_gpu(output_q, "output_q");
+  check_gpu(output_s, "output_s");
+  TORCH_CHECK(output_q.scalar_type() == at::kFloat8_e4m3fn, "output_q must be float8_e4m3fn");
+  TORCH_CHECK(output_s.scalar_type() == at::kFloat, "output_s must be float32");
+  TORCH_CHECK(input.numel() % group_size == 0,
+              "the last dimension of input must be divisible by group_size");
+  const int64_t cols = input.size(-1);
+  const int64_t rows = input.numel() / std::max<int64_t>(cols, 1);
+  c10::hip::HIPGuard g(input.device());
+  check_rc(mi355moe_per_token_group_fp8_quant(
+               input.data_ptr(), dtype_code(input.scalar_type()), output_q.data_ptr(),
+               output_s.data_ptr<float>(), rows, cols, group_size,
+               static_cast<float>(eps), static_cast<float>(fp8_min),
+               static_cast<float>(fp8_max), scale_ue8m0, cur_stream(input)),
+           "per_token_group_fp8_quant");
+}
+
+void per_token_group_quant_mxfp4(const at::Tensor& input, at::Tensor& output_q,
+                                 at::Tensor& output_s, int64_t group_size,
+                                 double eps) {
+  check_gpu(input, "input");
+  check_gpu(output_q, "output_q");
+  check_gpu(output_s, "output_s");
+  TORCH_CHECK(output_s.scalar_type() == at::kFloat, "output_s must be float32");
+  const int64_t cols = input.size(-1);
+  const int64_t rows = input.numel() / std::max<int64_t>(cols, 1);
+  c10::hip::HIPGuard g(input.device());
+  check_rc(mi355moe_per_token_group_quant_mxfp4(
+               input.data_ptr(), dtype_code(input.scalar_type()),
+               static_cast<uint8_t*>(output_q.data_ptr()), output_s.data_ptr<float>(),
+               rows, cols, group_size, static_cast<float>(eps), cur_stream(input)),
+           "per_token_group_quant_mxfp4");
+}
+
+// ------------------------------------------------------------- grouped GEMM
+at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
+                                          const std::optional<at::Tensor>& ptr_A_scale,
+                                          at::Tensor& ptr_B,
+                                          const std::optional<at::Tensor>& ptr_B_scale,
+                                          const std::optional<at::Tensor>& ptr_bias,
+                                          at::Tensor& ptr_D, at::Tensor& rows_per_expert,
+                                          int64_t N, int64_t K, int64_t num_experts) {
+  TORCH_CHECK(N % 8 == 0, "N must be divisible by 8");
+  TORCH_CHECK(ptr_A.dim() == 2, "ptr_A must be 2D [Total_M, K]");
+  TORCH_CHECK(ptr_B.dim() == 3, "ptr_B must be 3D");
+  TORCH_CHECK(ptr_D.dim() == 2, "ptr_D must be 2D [Total_M, N]");
+  TORCH_CHECK(ptr_A.is_contiguous(), "ptr_A must be contiguous");
+  TORCH_CHECK(ptr_B.is_contiguous(), "ptr_B must be contiguous");
+  TORCH_CHECK(ptr_D.is_contiguous(), "ptr_D must be contiguous");
+  check_gpu(rows_per_expert, "rows_per_expert");
+  TORCH_CHECK(ptr_B.size(0) == num_experts, "ptr_B.size(0) must match num_experts");
+  TORCH_CHECK(ptr_A.size(0) == ptr_D.size(0), "ptr_A.size(0) must match ptr_D.size(0)");
+  if (ptr_bias) {
+    TORCH_CHECK(ptr_bias->dim() == 2, "ptr_bias must be 2D [num_experts, N]");
+    TORCH_CHECK(ptr_bias->is_contiguous(), "ptr_bias must be contiguous");
+    TORCH_CHECK(ptr_bias->size(0) == num_experts, "ptr_bias.size(0) must match num_experts");
+    TORCH_CHECK(ptr_bias->size(1) == N, "ptr_bias.size(1) must match N");
+  }
+  const auto bdt = ptr_B.scalar_type();
+  const bool is_fp8 = bdt == at::kFloat8_e4m3fn;
+  const bool is_mxfp4 = bdt == at::kFloat4_e2m1fn_x2 ||
+                        (bdt == at::kByte && ptr_B_scale.has_value() &&
+                         ptr_B_scale->scalar_type() != at::kFloat);
+  int recipe = MI355MOE_RECIPE_BF16;
+  at::Tensor B = ptr_B;
+  if (is_mxfp4) {
+    recipe = MI355MOE_RECIPE_MXFP4;
+    TORCH_CHECK(ptr_B_scale.has_value(), "mxfp4 weights need ptr_B_scale");
+    TORCH_CHECK(ptr_B.size(1) == N && ptr_B.size(2) * 2 == K,
+                "ptr_B logical N dimension must match ptr_D N dimension and N");
+  } else if (is_fp8) {
+    TORCH_CHECK(ptr_B_scale.has_value() && ptr_B_scale->dim() == 3,
+                "block scales must be 3D [num_experts, N / 128, K / 128]");
+    TORCH_CHECK(N % 128 == 0 && K % 128 == 0,
+                "block-scaled grouped GEMM requires N and K divisible by 128");
+    TORCH_CHECK(ptr_B_scale->size(0) == num_experts &&
+                    ptr_B_scale->size(1) == N / 128 && ptr_B_scale->size(2) == K / 128,
+                "block scales must have shape [num_experts, N / 128, K / 128]");
+    const bool nk = ptr_B.size(1) == N && ptr_B.size(2) == K;
+    const bool kn = N != K && ptr_B.size(1) == K && ptr_B.size(2) == N;
+    TORCH_CHECK(nk || kn, "block FP8 ptr_B must be [num_experts, N, K] or "
+                          "[num_experts, K, N] (N=", N, ", K=", K, "), got ",
+                ptr_B.sizes());
+    if (!nk) B = ptr_B.transpose(1, 2).contiguous();
+    recipe = MI355MOE_RECIPE_FP8BLOCK;
+  } else {
+    TORCH_CHECK(bdt == ptr_A.scalar_type(),
+                "bf16/fp16 weights must have the activation dtype");
+    // reference layout is [E, K, N]
+    TORCH_CHECK(ptr_B.size(1) == K && ptr_B.size(2) == N,
+                "ptr_A K dimension must match ptr_B logical K dimension and K");
+    B = ptr_B.transpose(1, 2).contiguous();
+  }
+  TORCH_CHECK(ptr_A.size(1) == K,
+              "ptr_A K dimension must match ptr_B logical K dimension and K");
+  TORCH_CHECK(ptr_D.size(1) == N,
+              "ptr_B logical N dimension must match ptr_D N dimension and N");
+  const int64_t M = ptr_A.size(0);
+  const int adt = dtype_code(ptr_A.scalar_type());
+  const size_t ws_bytes =
+      mi355moe_grouped_gemm_workspace_size_k(recipe, adt, M, K, num_experts);
+  auto ws = at::empty({static_cast<int64_t>(ws_bytes)}, ptr_A.options().dtype(at::kByte));
+  c10::hip::HIPGuard g(ptr_A.device());
+  check_rc(mi355moe_grouped_gemm(
+               recipe, ptr_A.data_ptr(), adt,
+               ptr_A_scale ? ptr_A_scale->data_ptr<float>() : nullptr, B.data_ptr(),
+               ptr_B_scale ? ptr_B_scale->data_ptr() : nullptr, opt_ptr(ptr_bias),
+               ptr_D.data_ptr(), dtype_code(ptr_D.scalar_type()),
+               rows_per_expert.data_ptr<int32_t>(), M, N, K, num_experts,
+               ws.data_ptr(), ws_bytes, cur_stream(ptr_A)),
+           "cutlass_grouped_gemm_interface");
+  return ptr_D;
+}
+
+// -------------------------------------------------------- fused MoE layer
+// Not a reference op: the one-call layer used by XpuFusedMoe.apply.
+void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
+                     const at::Tensor& topk_weights, const at::Tensor& topk_ids,
+                     const at::Tensor& w13, const std::optional<at::Tensor>& w13_scale,
+                     const std::optional<at::Tensor>& w13_bias, const at::Tensor& w2,
+                     const std::optional<at::Tensor>& w2_scale,
+                     const std::optional<at::Tensor>& w2_bias, int64_t recipe,
+                     int64_t activation, int64_t inter_size, double clamp_limit,
+                     const std::optional<at::Tensor>& expert_map) {
+  check_gpu(output, "output");
+  check_gpu(hidden_states, "hidden_states");
+  check_gpu(topk_weights, "topk_weights");
+  check_gpu(topk_ids, "topk_ids");
+  check_gpu(w13, "w13");
+  check_gpu(w2, "w2");
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  TORCH_CHECK(output.sizes() == hidden_states.sizes(), "output must match hidden_states");
+  mi355moe_fused_moe_args a{};
+  a.recipe = static_cast<int>(recipe);
+  a.activation = static_cast<int>(activation);
+  a.act_dtype = dtype_code(hidden_states.scalar_type());
+  a.ids_dtype = dtype_code(topk_ids.scalar_type());
+  a.num_tokens = hidden_states.size(0);
+  a.hidden = hidden_states.size(1);
+  a.inter = inter_size;
+  a.num_experts = w13.size(0);
+  a.topk = topk_ids.size(1);
+  a.hidden_states = hidden_states.data_ptr();
+  a.topk_weights = topk_weights.data_ptr<float>();
+  a.topk_ids = topk_ids.data_ptr();
+  a.expert_map = expert_map ? expert_map->data_ptr<int32_t>() : nullptr;
+  a.expert_map_len = expert_map ? expert_map->numel() : 0;
+  a.w13 = w13.data_ptr();
+  a.w13_scale = opt_ptr(w13_scale);
+  a.w13_bias = opt_ptr(w13_bias);
+  a.w2 = w2.data_ptr();
+  a.w2_scale = opt_ptr(w2_scale);
+  a.w2_bias = opt_ptr(w2_bias);
+  a.gemm1_clamp_limit = static_cast<float>(clamp_limit);
+  a.swiglu_alpha = 1.702f;
+  a.swiglu_limit = 7.0f;
+  a.output = output.data_ptr();
+  const size_t ws_bytes = mi355moe_fused_moe_workspace_size(&a);
+  auto ws = at::empty({static_cast<int64_t>(ws_bytes)},
+                      hidden_states.options().dtype(at::kByte));
+  c10::hip::HIPGuard g(hidden_states.device());
+  check_rc(mi355moe_fused_moe(&a, ws.data_ptr(), ws_bytes, cur_stream(hidden_states)),
+           "fused_moe");
+}
+
+}  // namespace
+
+TORCH_LIBRARY(_moe_C, m) {
+  m.def("moe_sum(Tensor input, Tensor! output, Tensor? topk_ids, Tensor? expert_map) -> ()");
+  m.def("moe_align_block_size(Tensor topk_ids, int num_experts, int block_size, "
+        "Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, "
+        "Tensor? maybe_expert_map) -> ()");
+  m.def("grouped_topk(Tensor scores, Tensor scores_with_bias, int n_group, int "
+        "topk_group, int topk, bool renormalize, float routed_scaling_factor) -> "
+        "(Tensor, Tensor)");
+  m.def("topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! "
+        "token_expert_indices, Tensor gating_output, bool renormalize, Tensor? "
+        "bias) -> ()");
+  m.def("topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! "
+        "token_expert_indices, Tensor gating_output, bool renormalize, Tensor? "
+        "bias, float routed_scaling_factor) -> ()");
+  m.def("moe_gather(Tensor! output, Tensor moe_output, Tensor topk_weights, "
+        "Tensor unpermuted_row_to_permuted_row, int num_experts) -> ()");
+  m.def("init_expert_map(Tensor expert_map, int num_experts, int ep_rank, int "
+        "ep_size) -> ()");
+  m.def("remap_hidden_states(Tensor hidden_states, Tensor? hidden_states_scales, "
+        "Tensor remapped_hidden_states, Tensor? remapped_hidden_states_scales, "
+        "Tensor? expert_map, Tensor rows_per_expert, Tensor "
+        "unpermuted_row_to_permuted_row, Tensor topk_ids, int total_experts_num, "
+        "int local_experts_num) -> ()");
+  m.def("mi355_fused_moe(Tensor! output, Tensor hidden_states, Tensor topk_weights, "
+        "Tensor topk_ids, Tensor w13, Tensor? w13_scale, Tensor? w13_bias, Tensor w2, "
+        "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
+        "inter_size, float clamp_limit, Tensor? expert_map) -> ()");
+}
+
+TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
+  m.impl("moe_sum", &moe_sum);
+  m.impl("moe_align_block_size", &moe_align_block_size);
+  m.impl("grouped_topk", &grouped_topk);
+  m.impl("topk_softmax", &topk_softmax);
+  m.impl("topk_sigmoid", &topk_sigmoid);
+  m.impl("moe_gather", &moe_gather);
+  m.impl("init_expert_map", &init_expert_map);
+  m.impl("remap_hidden_states", &remap_hidden_states);
+  m.impl("mi355_fused_moe", &mi355_fused_moe);
+}
+
+TORCH_LIBRARY_IMPL(_moe_C, Meta, m) { m.impl("grouped_topk", &grouped_topk_meta); }
+
+TORCH_LIBRARY(_C, m) {
+  m.def("silu_and_mul(Tensor! result, Tensor input) -> ()");
+  m.def("swigluoai_and_mul(Tensor! out, Tensor input, float alpha=1.702, float "
+        "limit=7.0) -> ()");
+  m.def("per_token_group_fp8_quant(Tensor input, Tensor! output_q, Tensor! "
+        "output_s, int group_size, float eps, float fp8_min, float fp8_max, bool "
+        "scale_ue8m0, bool dummy_is_scale_transposed, bool dummy_is_tma_aligned ) "
+        "-> ()");
+  m.def("per_token_group_quant_mxfp4(Tensor input, Tensor! output_q, Tensor! "
+        "output_s, int group_size, float eps) -> ()");
+}
+
+TORCH_LIBRARY_IMPL(_C, CUDA, m) {
+  m.impl("silu_and_mul", &silu_and_mul);
+  m.impl("swigluoai_and_mul", &swigluoai_and_mul);
+  m.impl("per_token_group_fp8_quant", &per_token_group_fp8_quant);
+  m.impl("per_token_group_quant_mxfp4", &per_token_group_quant_mxfp4);
+}
+
+TORCH_LIBRARY(_xpu_C, m) {
+  m.def("cutlass_grouped_gemm_interface(Tensor ptr_A, Tensor? ptr_A_scale, "
+        "Tensor ptr_B, Tensor? ptr_B_scale, Tensor? ptr_bias, Tensor ptr_D, "
+        "Tensor rows_per_expert, int N, int K, int num_experts) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(_xpu_C, CUDA, m) {
+  m.impl("cutlass_grouped_gemm_interface", &cutlass_grouped_gemm_interface);
+}

@@ -1,0 +1,2 @@
+"""Op namespace torch.ops._C (registered by _mi355moe_torch.so)."""
+from . import _ops  # noqa: F401

@@ -1,0 +1,119 @@
+"""ctypes binding of the fused-layer C ABI (include/mi355moe.h).
+
+This is the binding a non-torch host (or a maintainer wiring the library
+into another runtime) would write; ``bench.py`` uses it for the stage-timed
+entry point.  Pointers come from ``tensor.data_ptr()`` and the stream from
+``torch.cuda.current_stream().cuda_stream``.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._ops import lib
+
+F32, BF16, F16, I32, I64 = 0, 1, 2, 3, 4
+FUSED_STAGES = 5
+STAGE_NAMES = ("align", "act_quant", "gemm_w13", "gemm_w2", "topk_reduce")
+
+
+class FusedMoeArgs(ctypes.Structure):
+    _fields_ = [("recipe", ctypes.c_int), ("activation", ctypes.c_int),
+                ("act_dtype", ctypes.c_int), ("ids_dtype", ctypes.c_int),
+                ("num_tokens", ctypes.c_int64), ("hidden", ctypes.c_int64),
+                ("inter", ctypes.c_int64), ("num_experts", ctypes.c_int64),
+                ("topk", ctypes.c_int64), ("hidden_states", ctypes.c_void_p),
+                ("topk_weights", ctypes.c_void_p), ("topk_ids", ctypes.c_void_p),
+                ("expert_map", ctypes.c_void_p), ("expert_map_len", ctypes.c_int64),
+                ("w13", ctypes.c_void_p), ("w13_scale", ctypes.c_void_p),
+                ("w13_bias", ctypes.c_void_p), ("w2", ctypes.c_void_p),
+                ("w2_scale", ctypes.c_void_p), ("w2_bias", ctypes.c_void_p),
+                ("gemm1_clamp_limit", ctypes.c_float),
+                ("swiglu_alpha", ctypes.c_float),
+                ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p)]
+
+
+lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t
+lib.mi355moe_fused_moe_workspace_size.argtypes = [ctypes.POINTER(FusedMoeArgs)]
+lib.mi355moe_fused_moe.argtypes = [ctypes.POINTER(FusedMoeArgs), ctypes.c_void_p,
+                                   ctypes.c_size_t, ctypes.c_void_p]
+lib.mi355moe_fused_moe_timed.argtypes = [ctypes.POINTER(FusedMoeArgs),
+                                         ctypes.c_void_p, ctypes.c_size_t,
+                                         ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_int]
+lib.mi355moe_timer_create.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]
+lib.mi355moe_timer_destroy.argtypes = [ctypes.c_void_p]
+lib.mi355moe_timer_stage_ms.argtypes = [ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_float)]
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what}: {lib.mi355moe_last_error().decode()}")
+
+
+def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
+               expert_map=None) -> FusedMoeArgs:
+    """Arguments for an XpuFusedMoe's prepared weights."""
+    a = FusedMoeArgs()
+    a.recipe = moe._recipe
+    a.activation = moe._act
+    a.act_dtype = BF16
+    a.ids_dtype = I64 if topk_ids.dtype == torch.int64 else I32
+    a.num_tokens, a.hidden = hidden_states.shape
+    a.inter = moe.inter_size
+    a.num_experts = moe.w13.shape[0]
+    a.topk = topk_ids.shape[1]
+    a.hidden_states = hidden_states.data_ptr()
+    a.topk_weights = topk_weights.data_ptr()
+    a.topk_ids = topk_ids.data_ptr()
+    a.expert_map = expert_map.data_ptr() if expert_map is not None else None
+    a.expert_map_len = expert_map.numel() if expert_map is not None else 0
+    a.w13 = moe.w13.data_ptr()
+    a.w13_scale = (moe.gemm1_wei_scales.data_ptr()
+                   if moe.gemm1_wei_scales is not None else None)
+    a.w13_bias = moe.w13_bias.data_ptr() if moe.w13_bias is not None else None
+    a.w2 = moe.w2.data_ptr()
+    a.w2_scale = (moe.gemm2_wei_scales.data_ptr()
+                  if moe.gemm2_wei_scales is not None else None)
+    a.w2_bias = moe.w2_bias.data_ptr() if moe.w2_bias is not None else None
+    a.gemm1_clamp_limit = float(moe.gemm1_clamp_limit or 0.0)
+    a.swiglu_alpha = 1.702
+    a.swiglu_limit = 7.0
+    a.output = output.data_ptr()
+    return a
+
+
+class StageTimer:
+    """HIP-event timer of the five fused stages over `steps` calls."""
+
+    def __init__(self, steps: int):
+        self.steps = steps
+        self.h = ctypes.c_void_p()
+        _check(lib.mi355moe_timer_create(steps, ctypes.byref(self.h)), "timer_create")
+
+    def run(self, args: FusedMoeArgs, ws: torch.Tensor, step: int) -> None:
+        stream = torch.cuda.current_stream().cuda_stream
+        _check(lib.mi355moe_fused_moe_timed(ctypes.byref(args), _p(ws), ws.numel(),
+                                            ctypes.c_void_p(stream), self.h, step),
+               "fused_moe_timed")
+
+    def stage_ms(self, step: int) -> list[float]:
+        buf = (ctypes.c_float * FUSED_STAGES)()
+        _check(lib.mi355moe_timer_stage_ms(self.h, step, buf), "timer_stage_ms")
+        return list(buf)
+
+    def close(self) -> None:
+        if self.h:
+            lib.mi355moe_timer_destroy(self.h)
+            self.h = ctypes.c_void_p()
+
+
+def workspace_for(args: FusedMoeArgs, device) -> torch.Tensor:
+    n = lib.mi355moe_fused_moe_workspace_size(ctypes.byref(args))
+    return torch.empty(int(n), dtype=torch.uint8, device=device)

@@ -1,0 +1,205 @@
+"""Fused MoE layer API (reference vllm_xpu_kernels/fused_moe_interface.py).
+
+``XpuFusedMoe(...)`` keeps the reference constructor and ``apply`` signature
+(:165-181, :273-281).  At construction the weights are converted once into
+the layout the gfx950 kernels stream (every expert matrix [N, K] with K
+contiguous; swigluoai's interleaved gate/up rows split into a gate half and an
+up half) and the converted tensors are tagged so that a second
+``XpuFusedMoe`` over the same tensors does not convert again.  ``apply``
+makes one call, ``torch.ops._moe_C.mi355_fused_moe``, which launches the whole
+layer on the current stream without synchronising the host.
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+
+from . import _ops  # noqa: F401  (loads the HIP library)
+
+REF_FUSED_MOE_ENV = "VLLM_XPU_FUSED_MOE_USE_REF"
+FP8_BLOCK_SIZE = 128
+
+RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4 = 0, 1, 2
+ACT_SILU, ACT_SWIGLUOAI = 0, 1
+
+
+def _is_env_enabled(env_name: str, default: str = "0") -> bool:
+    value = os.environ.get(env_name, default).strip().upper()
+    return value in ("1", "ON", "TRUE", "YES", "Y")
+
+
+def _get_weights_dtype(weight, scales):
+    """Recipe detection of the reference (fused_moe_interface.py:47-61)."""
+    weight_dtype = weight.dtype
+    is_fp8 = weight_dtype in (torch.float8_e4m3fn, torch.float8_e5m2)
+    is_int4 = weight_dtype == torch.uint8 and (scales is None or
+                                               scales.dtype != torch.uint8)
+    is_mxfp4 = weight_dtype == torch.float4_e2m1fn_x2 or (
+        weight_dtype == torch.uint8 and scales is not None and
+        scales.dtype in (torch.uint8, torch.float8_e8m0fnu))
+    is_mxfp8 = is_fp8 and scales is not None and scales.dtype == torch.uint8
+    is_block_fp8 = (is_fp8 and scales is not None and
+                    scales.dtype == torch.float32 and scales.ndim == 3)
+    is_fp8 = is_fp8 and not is_mxfp8 and not is_block_fp8
+    return is_fp8, is_int4, is_mxfp4, is_mxfp8, is_block_fp8
+
+
+def _get_inter_size(w13, w13_scales, is_int4, is_mxfp4, is_block_fp8):
+    """Reference fused_moe_interface.py:64-69."""
+    if is_block_fp8:
+        return w13_scales.shape[-2] * FP8_BLOCK_SIZE // 2
+    if is_int4 or is_mxfp4:
+        return w13.shape[-2] // 2
+    return w13.shape[-1] // 2
+
+
+def _deinterleave_rows(t: torch.Tensor, dim: int) -> torch.Tensor:
+    """[.., 2I, ..] with gate at even / up at odd rows -> [gate; up]."""
+    even = t.narrow(dim, 0, t.shape[dim]).index_select(
+        dim, torch.arange(0, t.shape[dim], 2, device=t.device))
+    odd = t.index_select(dim, torch.arange(1, t.shape[dim], 2, device=t.device))
+    return torch.cat([even, odd], dim=dim).contiguous()
+
+
+class XpuFusedMoe:
+    """Drop-in for the reference's XpuFusedMoe (fused_moe_interface.py:165-419).
+
+    Weight layouts accepted (as the reference):
+      bf16 / fp16     w13 [E, H, 2I], w2 [E, I, H]            ("kn")
+      fp8 block       w13 [E, 2I, H] or [E, H, 2I], w2 likewise, fp32 scales
+                      [E, N/128, K/128]
+      mxfp4           w13 [E, 2I, H/2] float4_e2m1fn_x2 (or uint8), e8m0
+                      scales [E, 2I, H/32] uint8; w2 [E, H, I/2]
+    """
+
+    def __init__(self, w13, w13_scales, w13_bias, w2, w2_scales, w2_bias,
+                 n_experts_per_token, activation, num_experts, ep_rank=0,
+                 ep_size=1, expert_map=None,
+                 gemm1_clamp_limit: Optional[float] = None):
+        assert w13.is_contiguous() and w2.is_contiguous()
+        (is_fp8, is_int4, is_mxfp4, is_mxfp8,
+         is_block_fp8) = _get_weights_dtype(w13, w13_scales)
+        if is_int4 or is_mxfp8 or is_fp8:
+            raise NotImplementedError(
+                "recipes int4, mxfp8 and per-tensor fp8 are not implemented "
+                "on MI355X yet; use bf16, fp8 block (128x128) or mxfp4")
+        self.inter_size = _get_inter_size(w13, w13_scales, is_int4, is_mxfp4,
+                                          is_block_fp8)
+        self.n_experts_per_token = n_experts_per_token
+        self.activation = activation
+        self.num_experts = num_experts
+        self.ep_rank = ep_rank
+        self.ep_size = ep_size
+        self.is_fp8 = is_fp8
+        self.is_int4 = is_int4
+        self.is_mxfp4 = is_mxfp4
+        self.is_mxfp8 = is_mxfp8
+        self.is_block_fp8 = is_block_fp8
+        self.gemm1_clamp_limit = gemm1_clamp_limit
+        if activation == "silu":
+            self._act = ACT_SILU
+        elif activation == "swigluoai" or "SWIGLUOAI" in str(activation):
+            self._act = ACT_SWIGLUOAI
+        else:
+            raise ValueError(f"Unsupported FusedMoe activation: {activation}.")
+        if is_block_fp8:
+            self.recipe = "fp8block"
+            self._recipe = RECIPE_FP8BLOCK
+        elif is_mxfp4:
+            self.recipe = "mxfp4"
+            self._recipe = RECIPE_MXFP4
+        else:
+            self.recipe = "bf16"
+            self._recipe = RECIPE_BF16
+        if _is_env_enabled(REF_FUSED_MOE_ENV):
+            raise NotImplementedError(
+                f"{REF_FUSED_MOE_ENV}=1 (torch reference path) is not provided "
+                "by the MI355X build; the HIP kernels are the only path")
+        self._prepare_weights(w13, w13_scales, w13_bias, w2, w2_scales, w2_bias)
+
+        self.expert_map = expert_map
+        if self.expert_map is None and self.ep_size > 1:
+            self.expert_map = torch.empty(self.num_experts * self.ep_size,
+                                          dtype=torch.int32, device=w13.device)
+            torch.ops._moe_C.init_expert_map(self.expert_map, self.num_experts,
+                                             self.ep_rank, self.ep_size)
+        if self.expert_map is not None:
+            self.total_experts_num = self.expert_map.shape[0]
+        else:
+            self.total_experts_num = self.num_experts * self.ep_size
+        self.local_experts_num = self.num_experts
+
+    # ------------------------------------------------------------------
+    def _prepare_weights(self, w13, s13, b13, w2, s2, b2):
+        I = self.inter_size
+        E = w13.shape[0]
+        swiglu = self._act == ACT_SWIGLUOAI
+        if self._recipe == RECIPE_BF16:
+            if w13.dtype != torch.bfloat16:
+                raise NotImplementedError("only bfloat16 weights are supported")
+            # reference layout [E, K, N] -> [E, N, K]
+            w13c = w13.transpose(1, 2).contiguous()
+            w2c = w2.transpose(1, 2).contiguous()
+            s13c = s2c = None
+        elif self._recipe == RECIPE_FP8BLOCK:
+            # [E, N, K] preferred when ambiguous, as the reference
+            # (grouped_gemm_xe2_interface.hpp:206-223)
+            w13c = w13 if w13.shape[1] == 2 * I else w13.transpose(1, 2).contiguous()
+            w2c = w2 if w2.shape[2] == I else w2.transpose(1, 2).contiguous()
+            s13c, s2c = s13.contiguous(), s2.contiguous()
+            if swiglu:
+                raise NotImplementedError(
+                    "swigluoai with 128x128 fp8 block scales is not supported")
+        else:
+            w13c = w13.view(torch.uint8)
+            w2c = w2.view(torch.uint8)
+            s13c = s13.view(torch.uint8) if s13.dtype != torch.uint8 else s13
+            s2c = s2.view(torch.uint8) if s2.dtype != torch.uint8 else s2
+        b13c = b13.to(torch.bfloat16).contiguous() if b13 is not None else None
+        b2c = b2.to(torch.bfloat16).contiguous() if b2 is not None else None
+        if swiglu:
+            w13c = _deinterleave_rows(w13c, 1)
+            if s13c is not None:
+                s13c = _deinterleave_rows(s13c, 1)
+            if b13c is not None:
+                b13c = _deinterleave_rows(b13c, 1)
+        assert w13c.shape[0] == E and w13c.shape[1] == 2 * I
+        self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
+        self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
+        self.w13_bias, self.w2_bias = b13c, b2c
+        self.w13._mi355_prepared = True
+
+    # ------------------------------------------------------------------
+    def apply(self, output, hidden_states, topk_weights, topk_ids,
+              expert_map=None, a1q_scale=None):
+        if a1q_scale is not None:
+            raise NotImplementedError(
+                "pre-quantised activations (a1q_scale) are not supported yet; "
+                "pass bf16 hidden_states (quantised on the fly per 1x128)")
+        if expert_map is None and self.ep_size > 1:
+            expert_map = self.expert_map
+        clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
+        torch.ops._moe_C.mi355_fused_moe(
+            output, hidden_states, topk_weights.to(torch.float32).contiguous(),
+            topk_ids.contiguous(), self.w13, self.gemm1_wei_scales,
+            self.w13_bias, self.w2, self.gemm2_wei_scales, self.w2_bias,
+            self._recipe, self._act, self.inter_size, clamp, expert_map)
+        return output
+
+
+def xpu_fused_moe(hidden_states, w13, w13_scales, w13_bias, w2, w2_scales,
+                  w2_bias, topk_weights, topk_ids, n_experts_per_token,
+                  activation, num_experts, ep_rank=0, ep_size=1,
+                  output=None, is_fp8=False, is_int4=False, is_mxfp4=False,
+                  expert_map=None, gemm1_clamp_limit=None):
+    """Functional entry (reference fused_moe_interface.py:421-442): builds an
+    XpuFusedMoe and applies it once."""
+    moe = XpuFusedMoe(w13, w13_scales, w13_bias, w2, w2_scales, w2_bias,
+                      n_experts_per_token, activation, num_experts, ep_rank,
+                      ep_size, expert_map, gemm1_clamp_limit)
+    if output is None:
+        output = torch.empty_like(hidden_states)
+    return moe.apply(output, hidden_states, topk_weights, topk_ids,
+                     expert_map=expert_map)

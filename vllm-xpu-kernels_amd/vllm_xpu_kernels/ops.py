@@ -1,0 +1,191 @@
+"""Allocating Python wrappers over the registered ops.
+
+They mirror the caller-side helpers vLLM and the reference tests use
+(reference tests/ops/topk_op.py:62-147, tests/ops/grouped_topk_op.py:67-92,
+tests/ops/moe_align_block_size_ops.py:14-100), so code written against the
+reference can swap the import.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _ops  # noqa: F401
+
+FP8_E4M3_MAX = 448.0
+
+
+def topk_softmax(gating_output: torch.Tensor, topk: int, renormalize: bool,
+                 bias: Optional[torch.Tensor] = None,
+                 indices_type: Optional[torch.dtype] = None):
+    T = gating_output.shape[0]
+    dev = gating_output.device
+    w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, topk, dtype=indices_type or torch.int32, device=dev)
+    tei = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    torch.ops._moe_C.topk_softmax(w, ids, tei, gating_output, renormalize, bias)
+    return w, ids, tei
+
+
+def topk_sigmoid(gating_output: torch.Tensor, topk: int, renormalize: bool,
+                 bias: Optional[torch.Tensor] = None,
+                 indices_type: Optional[torch.dtype] = None,
+                 routed_scaling_factor: float = 1.0):
+    T = gating_output.shape[0]
+    dev = gating_output.device
+    w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, topk, dtype=indices_type or torch.int32, device=dev)
+    tei = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    torch.ops._moe_C.topk_sigmoid(w, ids, tei, gating_output, renormalize, bias,
+                                  routed_scaling_factor)
+    return w, ids, tei
+
+
+def grouped_topk(scores: torch.Tensor, scores_with_bias: torch.Tensor,
+                 n_group: int, topk_group: int, topk: int, renormalize: bool,
+                 routed_scaling_factor: float = 1.0):
+    return torch.ops._moe_C.grouped_topk(scores, scores_with_bias, n_group,
+                                         topk_group, topk, renormalize,
+                                         routed_scaling_factor)
+
+
+def fused_grouped_topk(gating_output: torch.Tensor, topk: int,
+                       renormalize: bool,
+                       e_score_correction_bias: torch.Tensor,
+                       num_expert_group: int, topk_group: int,
+                       scoring_func: str = "sigmoid",
+                       routed_scaling_factor: float = 1.0):
+    """Caller-side score function + bias, then the grouped top-k kernel
+    (reference tests/ops/grouped_topk_op.py:67-92)."""
+    if scoring_func == "softmax":
+        scores = torch.softmax(gating_output, dim=-1)
+    elif scoring_func == "sigmoid":
+        scores = gating_output.sigmoid()
+    else:
+        raise ValueError(f"Unsupported scoring function: {scoring_func}")
+    swb = scores + e_score_correction_bias.unsqueeze(0)
+    v, i = grouped_topk(scores, swb.to(scores.dtype), num_expert_group,
+                        topk_group, topk, renormalize, routed_scaling_factor)
+    return v.to(torch.float32), i
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+def align_buffer_sizes(numel: int, num_experts: int, block_size: int,
+                       pad_sorted_ids: bool = False):
+    mx = numel + num_experts * (block_size - 1)
+    if pad_sorted_ids:
+        mx = _round_up(mx, block_size)
+    if numel < num_experts:
+        mx = min(numel * block_size, mx)
+    return mx, (mx + block_size - 1) // block_size
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
+                         num_experts: int,
+                         expert_map: Optional[torch.Tensor] = None,
+                         pad_sorted_ids: bool = False,
+                         ignore_invalid_experts: bool = False):
+    mx, nb = align_buffer_sizes(topk_ids.numel(), num_experts, block_size,
+                                pad_sorted_ids)
+    dev = topk_ids.device
+    sorted_ids = torch.empty(mx, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(nb, dtype=torch.int32, device=dev)
+    ntp = torch.empty(1, dtype=torch.int32, device=dev)
+    torch.ops._moe_C.moe_align_block_size(
+        topk_ids, num_experts, block_size, sorted_ids, expert_ids, ntp,
+        expert_map if ignore_invalid_experts else None)
+    if expert_map is not None and not ignore_invalid_experts:
+        expert_ids = expert_map[expert_ids]
+    return sorted_ids, expert_ids, ntp
+
+
+def moe_sum(inp: torch.Tensor, out: torch.Tensor,
+            topk_ids: Optional[torch.Tensor] = None,
+            expert_map: Optional[torch.Tensor] = None) -> None:
+    torch.ops._moe_C.moe_sum(inp, out, topk_ids, expert_map)
+
+
+def moe_gather(out: torch.Tensor, moe_output: torch.Tensor,
+               topk_weights: torch.Tensor, perm: torch.Tensor,
+               num_experts: int) -> None:
+    torch.ops._moe_C.moe_gather(out, moe_output, topk_weights, perm,
+                                num_experts)
+
+
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    d = x.shape[-1] // 2
+    out = torch.empty(x.shape[:-1] + (d,), dtype=x.dtype, device=x.device)
+    torch.ops._C.silu_and_mul(out, x)
+    return out
+
+
+def swigluoai_and_mul(x: torch.Tensor, alpha: float = 1.702,
+                      limit: float = 7.0) -> torch.Tensor:
+    d = x.shape[-1] // 2
+    out = torch.empty(x.shape[:-1] + (d,), dtype=x.dtype, device=x.device)
+    torch.ops._C.swigluoai_and_mul(out, x, alpha, limit)
+    return out
+
+
+def per_token_group_fp8_quant(x: torch.Tensor, group_size: int = 128,
+                              eps: float = 1e-10,
+                              scale_ue8m0: bool = False):
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty(x.shape[:-1] + (x.shape[-1] // group_size,),
+                    dtype=torch.float32, device=x.device)
+    torch.ops._C.per_token_group_fp8_quant(x, q, s, group_size, eps,
+                                           -FP8_E4M3_MAX, FP8_E4M3_MAX,
+                                           scale_ue8m0, False, False)
+    return q, s
+
+
+def per_token_group_quant_mxfp4(x: torch.Tensor, group_size: int = 32,
+                                eps: float = 1e-10):
+    M, N = x.shape
+    q = torch.empty(M, N // 2, dtype=torch.uint8, device=x.device)
+    s = torch.empty(M, N // group_size, dtype=torch.float32, device=x.device)
+    torch.ops._C.per_token_group_quant_mxfp4(x, q, s, group_size, eps)
+    return q.view(torch.float4_e2m1fn_x2), s
+
+
+def init_expert_map(num_experts: int, ep_rank: int, ep_size: int,
+                    device) -> torch.Tensor:
+    m = torch.empty(num_experts * ep_size, dtype=torch.int32, device=device)
+    torch.ops._moe_C.init_expert_map(m, num_experts, ep_rank, ep_size)
+    return m
+
+
+def remap_hidden_states(hidden_states: torch.Tensor, topk_ids: torch.Tensor,
+                        total_experts_num: int, local_experts_num: int,
+                        expert_map: Optional[torch.Tensor] = None,
+                        hidden_states_scales: Optional[torch.Tensor] = None):
+    T, k = topk_ids.shape
+    dev = hidden_states.device
+    remapped = torch.empty((T * k,) + tuple(hidden_states.shape[1:]),
+                           dtype=hidden_states.dtype, device=dev)
+    rscales = None
+    if hidden_states_scales is not None:
+        rscales = torch.empty((T * k,) + tuple(hidden_states_scales.shape[1:]),
+                              dtype=hidden_states_scales.dtype, device=dev)
+    rows = torch.zeros(local_experts_num, dtype=torch.int32, device=dev)
+    perm = torch.empty(T, k, dtype=torch.int32, device=dev)
+    torch.ops._moe_C.remap_hidden_states(hidden_states, hidden_states_scales,
+                                         remapped, rscales, expert_map, rows,
+                                         perm, topk_ids, total_experts_num,
+                                         local_experts_num)
+    return remapped, rscales, rows, perm
+
+
+def cutlass_grouped_gemm(ptr_A: torch.Tensor, ptr_B: torch.Tensor,
+                         ptr_B_scale: Optional[torch.Tensor],
+                         ptr_bias: Optional[torch.Tensor], ptr_D: torch.Tensor,
+                         rows_per_expert: torch.Tensor, N: int, K: int,
+                         num_experts: int,
+                         ptr_A_scale: Optional[torch.Tensor] = None):
+    return torch.ops._xpu_C.cutlass_grouped_gemm_interface(
+        ptr_A, ptr_A_scale, ptr_B, ptr_B_scale, ptr_bias, ptr_D,
+        rows_per_expert, N, K, num_experts)
