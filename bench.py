@@ -232,14 +232,29 @@ def main():
                     help="'none', 'default' or a list like C3:1,C3:8192")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB 5 times (the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the MoE layer on a "
               "single MI355X (no collectives); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
-    from vllm_xpu_kernels import workloads as W
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n,
+                          "launches": 5}), flush=True)
+        return
+
+    from vllm_xpu_kernels import workloads as W
     graph = not args.no_graph
     cfg = W.CONFIGS[args.config]
     log(f"bench: {args.config} ({cfg.name}) T={args.tokens} steps={args.steps} "

@@ -8,16 +8,19 @@
 // reference's TORCH_CHECK messages; the C ABI's own checks surface through
 // mi355moe_last_error().
 #include <ATen/ATen.h>
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
 #include "../../include/mi355moe.h"
 
 namespace {
 
+// PyTorch-ROCm exposes HIP devices as DeviceType::CUDA ("masquerading").
+using DevGuard = c10::hip::HIPGuardMasqueradingAsCUDA;
+
 hipStream_t cur_stream(const at::Tensor& t) {
-  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
 }
 
 void check_rc(int rc, const char* op) {
@@ -69,7 +72,7 @@ void topk_softmax(at::Tensor& topk_weights, at::Tensor& topk_indices,
     TORCH_CHECK(bias->scalar_type() == at::kFloat, "bias must be float32");
     TORCH_CHECK(bias->numel() == E, "bias must have num_experts elements");
   }
-  c10::hip::HIPGuard g(gating_output.device());
+  DevGuard g(gating_output.device());
   check_rc(mi355moe_topk_softmax(
                topk_weights.data_ptr<float>(), topk_indices.data_ptr(),
                dtype_code(topk_indices.scalar_type()),
@@ -95,7 +98,7 @@ void topk_sigmoid(at::Tensor& topk_weights, at::Tensor& topk_indices,
     check_gpu(*bias, "bias");
     TORCH_CHECK(bias->scalar_type() == at::kFloat, "bias must be float32");
   }
-  c10::hip::HIPGuard g(gating_output.device());
+  DevGuard g(gating_output.device());
   check_rc(mi355moe_topk_sigmoid(
                topk_weights.data_ptr<float>(), topk_indices.data_ptr(),
                dtype_code(topk_indices.scalar_type()),
@@ -122,7 +125,7 @@ std::tuple<at::Tensor, at::Tensor> grouped_topk(at::Tensor& scores,
   const int64_t T = scores.size(0), E = scores.size(1);
   auto vals = at::empty({T, topk}, scores.options());
   auto ids = at::empty({T, topk}, scores.options().dtype(at::kInt));
-  c10::hip::HIPGuard g(scores.device());
+  DevGuard g(scores.device());
   check_rc(mi355moe_grouped_topk(vals.data_ptr(), ids.data_ptr<int32_t>(),
                                  scores.data_ptr(), scores_with_bias.data_ptr(),
                                  dtype_code(scores.scalar_type()), T, E, n_group,
@@ -158,7 +161,7 @@ void moe_align_block_size(at::Tensor topk_ids, int64_t num_experts,
     check_gpu(*maybe_expert_map, "expert_map");
     TORCH_CHECK(maybe_expert_map->scalar_type() == at::kInt, "expert_map must be int32");
   }
-  c10::hip::HIPGuard g(topk_ids.device());
+  DevGuard g(topk_ids.device());
   check_rc(mi355moe_moe_align_block_size(
                topk_ids.data_ptr(), dtype_code(topk_ids.scalar_type()),
                topk_ids.numel(), num_experts, block_size,
@@ -193,7 +196,7 @@ void remap_hidden_states(at::Tensor& hidden_states,
     scale_cols = hidden_states_scales->numel() / std::max<int64_t>(T, 1);
     scale_bytes = hidden_states_scales->element_size();
   }
-  c10::hip::HIPGuard g(hidden_states.device());
+  DevGuard g(hidden_states.device());
   check_rc(mi355moe_remap_hidden_states(
                hidden_states.data_ptr(), hidden_states.element_size(),
                opt_ptr(hidden_states_scales), scale_cols, scale_bytes,
@@ -216,7 +219,7 @@ void init_expert_map(at::Tensor expert_map, int64_t num_experts,
   TORCH_CHECK(expert_map.scalar_type() == at::kInt, "expert_map must be int32");
   TORCH_CHECK(expert_map.numel() >= num_experts * ep_size,
               "expert_map must hold num_experts * ep_size entries");
-  c10::hip::HIPGuard g(expert_map.device());
+  DevGuard g(expert_map.device());
   check_rc(mi355moe_init_expert_map(expert_map.data_ptr<int32_t>(), num_experts,
                                     ep_rank, ep_size, cur_stream(expert_map)),
            "init_expert_map");
@@ -256,7 +259,7 @@ void moe_sum(at::Tensor& input, at::Tensor& output,
     }
   }
   TORCH_CHECK(input.is_cuda(), "moe_sum: input must be on a GPU device");
-  c10::hip::HIPGuard g(input.device());
+  DevGuard g(input.device());
   check_rc(mi355moe_moe_sum(input.data_ptr(), output.data_ptr(),
                             dtype_code(input.scalar_type()), T, topk, H,
                             topk_ids ? topk_ids->data_ptr() : nullptr,
@@ -278,7 +281,7 @@ void moe_gather(at::Tensor& output, at::Tensor& moe_output,
               "output and moe_output must have the same dtype");
   const int64_t T = output.size(0), H = output.size(1), k = perm.size(1);
   (void)num_experts;
-  c10::hip::HIPGuard g(output.device());
+  DevGuard g(output.device());
   check_rc(mi355moe_moe_gather(output.data_ptr(), moe_output.data_ptr(),
                                dtype_code(output.scalar_type()),
                                topk_weights.data_ptr<float>(),
@@ -293,7 +296,7 @@ void silu_and_mul(at::Tensor& out, at::Tensor& input) {
   TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
   const int64_t d = input.size(-1) / 2;
   const int64_t rows = input.numel() / std::max<int64_t>(2 * d, 1);
-  c10::hip::HIPGuard g(input.device());
+  DevGuard g(input.device());
   check_rc(mi355moe_silu_and_mul(out.data_ptr(), input.data_ptr(),
                                  dtype_code(input.scalar_type()), rows, d,
                                  cur_stream(input)),
@@ -306,7 +309,7 @@ void swigluoai_and_mul(at::Tensor& out, at::Tensor& input, double alpha, double 
   TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
   const int64_t d = input.size(-1) / 2;
   const int64_t rows = input.numel() / std::max<int64_t>(2 * d, 1);
-  c10::hip::HIPGuard g(input.device());
+  DevGuard g(input.device());
   check_rc(mi355moe_swigluoai_and_mul(out.data_ptr(), input.data_ptr(),
                                       dtype_code(input.scalar_type()), rows, d,
                                       static_cast<float>(alpha),
@@ -328,7 +331,7 @@ void per_token_group_fp8_quant(const at::Tensor& input, at::Tensor& output_q,
               "the last dimension of input must be divisible by group_size");
   const int64_t cols = input.size(-1);
   const int64_t rows = input.numel() / std::max<int64_t>(cols, 1);
-  c10::hip::HIPGuard g(input.device());
+  DevGuard g(input.device());
   check_rc(mi355moe_per_token_group_fp8_quant(
                input.data_ptr(), dtype_code(input.scalar_type()), output_q.data_ptr(),
                output_s.data_ptr<float>(), rows, cols, group_size,
@@ -346,7 +349,7 @@ void per_token_group_quant_mxfp4(const at::Tensor& input, at::Tensor& output_q,
   TORCH_CHECK(output_s.scalar_type() == at::kFloat, "output_s must be float32");
   const int64_t cols = input.size(-1);
   const int64_t rows = input.numel() / std::max<int64_t>(cols, 1);
-  c10::hip::HIPGuard g(input.device());
+  DevGuard g(input.device());
   check_rc(mi355moe_per_token_group_quant_mxfp4(
                input.data_ptr(), dtype_code(input.scalar_type()),
                static_cast<uint8_t*>(output_q.data_ptr()), output_s.data_ptr<float>(),
@@ -422,7 +425,7 @@ at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
   const size_t ws_bytes =
       mi355moe_grouped_gemm_workspace_size_k(recipe, adt, M, K, num_experts);
   auto ws = at::empty({static_cast<int64_t>(ws_bytes)}, ptr_A.options().dtype(at::kByte));
-  c10::hip::HIPGuard g(ptr_A.device());
+  DevGuard g(ptr_A.device());
   check_rc(mi355moe_grouped_gemm(
                recipe, ptr_A.data_ptr(), adt,
                ptr_A_scale ? ptr_A_scale->data_ptr<float>() : nullptr, B.data_ptr(),
@@ -480,7 +483,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   const size_t ws_bytes = mi355moe_fused_moe_workspace_size(&a);
   auto ws = at::empty({static_cast<int64_t>(ws_bytes)},
                       hidden_states.options().dtype(at::kByte));
-  c10::hip::HIPGuard g(hidden_states.device());
+  DevGuard g(hidden_states.device());
   check_rc(mi355moe_fused_moe(&a, ws.data_ptr(), ws_bytes, cur_stream(hidden_states)),
            "fused_moe");
 }
