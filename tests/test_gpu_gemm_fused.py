@@ -236,3 +236,72 @@ def test_fused_moe_expert_map(dev):
     tw_c = torch.where(ti >= 8, tw, torch.zeros_like(tw))
     ref = _oracle_layer(cfg, w, x, tw_c, ti)
     _close(out, ref)
+
+
+# ------------------------------------------------- prefill (128x256) tiles
+BIG_ROWS = [300, 260, 0, 129]
+
+
+@pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4"])
+def test_grouped_gemm_big_tiles(dev, recipe):
+    """>96 rows per expert selects the LDS-staged 128x256 kernel; N=2880 is
+    not a multiple of the tile (ragged last tile)."""
+    g = torch.Generator().manual_seed(4)
+    E, K = 4, 1024
+    N = 640 if recipe == "fp8block" else 2880
+    M = sum(BIG_ROWS)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    rows = torch.tensor(BIG_ROWS, dtype=torch.int32)
+    d = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    if recipe == "bf16":
+        b = (torch.randn(E, N, K, generator=g) * 0.03).to(torch.bfloat16)
+        bias = (torch.randn(E, N, generator=g) * 0.1).to(torch.bfloat16)
+        _ops().cutlass_grouped_gemm(a.to(dev), b.transpose(1, 2).contiguous().to(dev), None,
+                                    bias.to(dev), d, rows.to(dev), N, K, E)
+        ref = O.grouped_gemm("bf16", a, b, None, bias, BIG_ROWS)
+    elif recipe == "fp8block":
+        q, s = O.fp8_block_quant_weight(torch.randn(E, N, K, generator=g) * 0.02)
+        _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), s.to(dev), None, d, rows.to(dev),
+                                    N, K, E)
+        ref = O.grouped_gemm("fp8block", a, q, s, None, BIG_ROWS)
+    else:
+        q, sc = O.to_mxfp4(torch.randn(E, N, K, generator=g) * 0.05)
+        _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), sc.to(dev), None, d, rows.to(dev),
+                                    N, K, E)
+        ref = O.grouped_gemm("mxfp4", a, q, sc, None, BIG_ROWS)
+    torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("name,T,sample", [("C2", 4096, 24), ("C3", 8192, 6),
+                                           ("C4", 2048, 12), ("C5", 4096, 12)])
+def test_fused_moe_prefill_full_size_sampled(dev, name, T, sample):
+    """Full BASELINE prefill shapes through the big-tile kernels; the oracle
+    checks evenly spaced sampled tokens."""
+    cfg, w, x, tw, ti, out, _ = _layer(_W().CONFIGS[name], T, dev)
+    toks = torch.linspace(0, T - 1, sample).long().to(dev)
+    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks), fp8=cfg.recipe == "fp8block")
+
+
+def test_fused_moe_hip_graph_replays(dev):
+    """The layer captured in a HIP graph: every replay (with eager work and
+    synchronisation between replays) equals the eager result."""
+    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C2"], 64, dev)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    gout = torch.empty_like(out)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        moe.apply(gout, x, tw, ti)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        moe.apply(gout, x, tw, ti)
+    for i in range(4):
+        gout.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, eager), f"replay {i}"
+        junk = torch.randn(1 << 20, device=dev).sum()   # eager work between replays
+        torch.cuda.synchronize()
+        del junk

@@ -15,10 +15,6 @@
 #include "moe_gemm.h"
 
 namespace mi355 {
-
-int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,
-                      int64_t max_blocks, void* qs, hipStream_t st);
-
 namespace {
 
 struct Carver {
@@ -101,6 +97,7 @@ int group_quant_fp8(const void* x, int dt, uint8_t* q, float* s, int64_t rows,
 
 struct FusedLayout {
   int bm;
+  GemmTile tile;
   int64_t slots, max_padded, max_blocks, grid_blocks;
   int32_t *sorted, *eids, *ntp;
   uint8_t* xq;    // fp8 hidden [T, H]
@@ -115,7 +112,7 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
   const int64_t E = a->num_experts;
   L.slots = a->num_tokens * a->topk;
-  L.bm = pick_block_m(L.slots, E);
+  L.tile = pick_tile(L.slots, E, &L.bm);
   padded_sizes(L.slots, E, L.bm, L.max_padded, L.max_blocks);
   L.grid_blocks = launch_blocks(L.slots, E, L.bm, L.max_blocks);
   Carver c{base};
@@ -276,7 +273,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.alpha = a->swiglu_alpha;
   g1.limit = a->swiglu_limit;
   g1.act = a->activation;
-  rc = launch_moe_gemm_q(recipe, EPI_GLU, fp8, L.bm, g1, L.grid_blocks, L.acts, st);
+  rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
   if (rc) return rc;
   if (int m = mark(3)) return m;
 
@@ -298,7 +295,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.K = I;
   g2.ldb_rows = H;
   g2.up_off = 0;
-  rc = launch_moe_gemm_q(recipe, EPI_STORE, false, L.bm, g2, L.grid_blocks, nullptr, st);
+  rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g2, L.grid_blocks, nullptr, st);
   if (rc) return rc;
   if (int m = mark(4)) return m;
 
@@ -325,6 +322,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
 namespace {
 struct GGLayout {
   int bm;
+  GemmTile tile;
   int64_t max_padded, max_blocks, grid_blocks;
   int32_t *rows, *eids, *ntp;
   uint8_t* aq;
@@ -334,7 +332,7 @@ struct GGLayout {
 GGLayout gg_plan(int recipe, bool need_quant, int64_t M, int64_t K, int64_t E,
                  uint8_t* base) {
   GGLayout L{};
-  L.bm = pick_block_m(M, E);
+  L.tile = pick_tile(M, E, &L.bm);
   padded_sizes(M, E, L.bm, L.max_padded, L.max_blocks);
   L.grid_blocks = launch_blocks(M, E, L.bm, L.max_blocks);
   Carver c{base};
@@ -431,5 +429,5 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
   g.K = K;
   g.ldb_rows = N;
   g.out_f16 = out_dtype == MI355MOE_F16;
-  return launch_moe_gemm_q(recipe, EPI_STORE, false, L.bm, g, L.grid_blocks, nullptr, st);
+  return launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g, L.grid_blocks, nullptr, st);
 }

@@ -47,6 +47,34 @@ int launch_moe_gemm(int recipe, int epi, int bm, const GemmArgs& a,
 // Choose the M tile for an expected number of rows per active expert.
 int pick_block_m(int64_t slots, int64_t num_experts);
 
+// Kernel family by the expected rows per active expert:
+//   <= 24   STREAM: independent-wave weight streaming, 16-slot blocks
+//   <= 96   SMALL:  LDS-shared activation tile, 32/64-slot blocks
+//   >  96   BIG:    128x256 LDS-staged tiles, 128-slot blocks
+// MI355MOE_GEMM_TILE=stream|small|big overrides (A/B measurements).
+// (TILE_BIG runs the LDS-DMA pipelined kernel where pipe_supported(),
+// TILE_BIGREG forces the register-staged one.)
+enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3 };
+GemmTile pick_tile(int64_t slots, int64_t num_experts, int* bm);
+
+// Launch the chosen family over max_blocks blocks of bm slots.
+int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
+                     const GemmArgs& a, int64_t max_blocks, void* qs,
+                     hipStream_t st);
+
+int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,
+                      int64_t max_blocks, void* qs, hipStream_t st);
+// 128-slot blocks; GLU tiles cover 128 output columns, STORE tiles 256.
+int launch_moe_gemm_big(int recipe, int epi, bool qout, const GemmArgs& a,
+                        int64_t max_blocks, void* qs, hipStream_t st);
+// 128-slot blocks, 3-stage global->LDS DMA ring (moe_gemm_pipe.hip).
+bool pipe_supported(int recipe, const GemmArgs& a);
+int launch_moe_gemm_pipe(int recipe, int epi, bool qout, const GemmArgs& a,
+                         int64_t max_blocks, void* qs, hipStream_t st);
+// 16-slot blocks; GLU blocks cover 128 output columns, STORE blocks 256.
+int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
+                           int64_t max_blocks, void* qs, hipStream_t st);
+
 int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t id_bound, const int32_t* map, int64_t num_keys,
                       int64_t bs, int32_t* sorted, int64_t max_padded,

@@ -18,6 +18,9 @@
 // Epilogues: STORE (bias, round) and GLU (gate/up halves of w13 -> SiLU-mul or
 // swigluoai), optionally re-quantising the activation to e4m3 with 1x128
 // scales for the w2 GEMM.
+#include <cstdlib>
+#include <cstring>
+
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -344,6 +347,37 @@ int pick_block_m(int64_t slots, int64_t num_experts) {
   if (avg <= 48) return 32;
   if (avg <= 96) return 64;
   return 128;
+}
+
+GemmTile pick_tile(int64_t slots, int64_t num_experts, int* bm) {
+  static const int force = [] {
+    const char* v = getenv("MI355MOE_GEMM_TILE");
+    if (!v) return -1;
+    if (!strcmp(v, "stream")) return static_cast<int>(TILE_STREAM);
+    if (!strcmp(v, "small")) return static_cast<int>(TILE_SMALL);
+    if (!strcmp(v, "big")) return static_cast<int>(TILE_BIG);
+    if (!strcmp(v, "bigreg")) return static_cast<int>(TILE_BIGREG);
+    return -1;
+  }();
+  const int m = pick_block_m(slots, num_experts);
+  GemmTile t = m == 16 ? TILE_STREAM : (m == 128 ? TILE_BIG : TILE_SMALL);
+  if (force >= 0) t = static_cast<GemmTile>(force);
+  *bm = t == TILE_STREAM ? 16 : ((t == TILE_BIG || t == TILE_BIGREG) ? 128 : m);
+  return t;
+}
+
+int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
+                     const GemmArgs& a, int64_t max_blocks, void* qs,
+                     hipStream_t st) {
+  switch (tile) {
+    case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
+    case TILE_BIG:
+      if (pipe_supported(recipe, a))
+        return launch_moe_gemm_pipe(recipe, epi, qout, a, max_blocks, qs, st);
+      return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
+    case TILE_BIGREG: return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
+    default: return launch_moe_gemm_q(recipe, epi, qout, bm, a, max_blocks, qs, st);
+  }
 }
 
 int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,

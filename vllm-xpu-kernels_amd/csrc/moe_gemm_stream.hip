@@ -1,0 +1,333 @@
+// Decode grouped GEMM: weight streaming with independent wavefronts.
+//
+// At decode an expert sees a handful of slots, so the GEMM is a stream over
+// the active experts' weights.  A workgroup = 8 wavefronts = 16 sorted slots of
+// one expert; every wave owns two 16-row weight sub-tiles (GLU: the gate rows
+// and the matching up rows of 16 activation columns; STORE: 32 output columns)
+// and walks the whole K range on its own: no LDS and no barrier inside the K
+// loop.  Weight fragments are prefetched PD K-stages ahead in VGPRs; the few
+// activation rows are read through L1/L2 (every workgroup of the expert reads
+// the same rows).  The MFMA A operand is the weight (16 rows n), the B operand
+// the activation (16 slots m): lane l holds rows n = 4*(l/16) + r of slot
+// m = l%16.  The only barrier is in the fp8 epilogue, which finds the amax of
+// each slot's 128 activation columns across the 8 waves.
+#include "moe_gemm.h"
+
+namespace mi355 {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int KS = 128;   // K elements per stage
+constexpr int WAVES = 8;
+
+__device__ __forceinline__ f32x4 mma_bf16(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma_fp8(uint4 a0, uint4 a1, uint4 b0, uint4 b1) {
+  i32x8 a = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+             (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+  i32x8 b = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+             (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
+}
+__device__ __forceinline__ uint4 fp4x8(uint32_t w, float sc) {
+  uint4 r;
+  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
+  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
+  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
+  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+  return r;
+}
+__device__ __forceinline__ float rnd(float v, bool f16) {
+  return f16 ? f16_to_f32(f32_to_f16(v)) : bf16_to_f32(f32_to_bf16(v));
+}
+__device__ __forceinline__ float glu_fn(float g, float u, const GemmArgs& a) {
+  if (a.act == MI355MOE_ACT_SILU) {
+    float s = bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g))));
+    return s * u;
+  }
+  g = g > a.limit ? a.limit : g;
+  u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+  return (u + 1.f) * (g * (1.f / (1.f + expf(-g * a.alpha))));
+}
+
+// Per-stage register fragments of one lane.
+template <int RECIPE>
+struct Frag;
+template <>
+struct Frag<MI355MOE_RECIPE_FP8BLOCK> {  // 32 e4m3 of the weight row / act row
+  uint4 w[2][2];
+  uint4 x[2];
+  float xs;
+};
+template <>
+struct Frag<MI355MOE_RECIPE_BF16> {      // 4 MFMA steps x 8 bf16
+  uint4 w[2][4];
+  uint4 x[4];
+};
+template <>
+struct Frag<MI355MOE_RECIPE_MXFP4> {     // 32 e2m1 + e8m0 of the weight row
+  uint4 w[2];
+  uint32_t sc[2];
+  uint4 x[4];
+};
+
+template <int RECIPE, int EPI, bool QOUT, int PD>
+__global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
+                                                              void* __restrict__ qs) {
+  constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
+  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4;
+  constexpr bool kGlu = EPI == EPI_GLU;
+  constexpr int XB = kFp8 ? 1 : 2;
+
+  __shared__ int s_arow[16];
+  __shared__ int s_drow[16];
+  __shared__ float s_amax[WAVES][16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, q = lane >> 4;
+  const int blk = blockIdx.y;
+  if (blk * 16 >= *a.ntp) return;  // uniform
+  const int e = a.block_expert[blk];
+  const int64_t K = a.K, N = a.N;
+  if (tid < 16) {
+    const int rid = a.row_ids[static_cast<int64_t>(blk) * 16 + tid];
+    const bool ok = rid >= 0 && rid < a.num_valid;
+    s_arow[tid] = ok ? (a.a_by_pos ? blk * 16 + tid : rid / a.a_div) : -1;
+    s_drow[tid] = ok ? (a.d_by_pos ? blk * 16 + tid : rid) : -1;
+  }
+  __syncthreads();
+
+  // output columns of this wave: GLU 16 activation columns, STORE 32 columns
+  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) +
+                       wave * (kGlu ? 16 : 32);
+  const int64_t wrow_bytes = kFp4 ? K / 2 : K * XB;
+  const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
+                        static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
+  int64_t wrow[2];
+  bool wok[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t n = kGlu ? col0 + l16 : col0 + 16 * t + l16;
+    wok[t] = n < N;
+    wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
+  }
+  const uint8_t* wp0 = wexp + wrow[0] * wrow_bytes;
+  const uint8_t* wp1 = wexp + wrow[1] * wrow_bytes;
+  const int arow = s_arow[l16];
+  const bool xok = arow >= 0;
+  const uint8_t* xp = static_cast<const uint8_t*>(a.A) +
+                      static_cast<int64_t>(xok ? arow : 0) * K * XB;
+  // fp8 weight-block scale rows (16-row sub-tiles sit inside one 128-row block)
+  int64_t wsr[2];
+  wsr[0] = (wrow[0] / 128);
+  wsr[1] = (wrow[1] / 128);
+
+  auto load = [&](Frag<RECIPE>& f, int64_t k0) {
+    const int64_t kb = K - k0;
+    if constexpr (kFp8) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint8_t* p = (t ? wp1 : wp0) + k0 + 32 * q;
+        f.w[t][0] = wok[t] ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
+        f.w[t][1] = wok[t] ? *reinterpret_cast<const uint4*>(p + 16) : make_uint4(0, 0, 0, 0);
+      }
+      const uint8_t* px = xp + k0 + 32 * q;
+      f.x[0] = xok ? *reinterpret_cast<const uint4*>(px) : make_uint4(0, 0, 0, 0);
+      f.x[1] = xok ? *reinterpret_cast<const uint4*>(px + 16) : make_uint4(0, 0, 0, 0);
+      f.xs = xok ? a.a_scale[static_cast<int64_t>(arow) * (K / 128) + k0 / 128] : 0.f;
+    } else if constexpr (kFp4) {
+      const bool in = 32 * q < kb;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bool ok = wok[t] && in;
+        f.w[t] = ok ? *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + (k0 + 32 * q) / 2)
+                    : make_uint4(0, 0, 0, 0);
+        f.sc[t] = ok ? static_cast<const uint8_t*>(a.b_scale)
+                           [(static_cast<int64_t>(e) * a.ldb_rows + wrow[t]) * (K / 32) +
+                            (k0 + 32 * q) / 32]
+                     : 0u;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        f.x[s] = (xok && in) ? *reinterpret_cast<const uint4*>(xp + (k0 + 32 * q + 8 * s) * 2)
+                             : make_uint4(0, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bool in = 32 * s + 8 * q + 8 <= kb;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          f.w[t][s] = (wok[t] && in) ? *reinterpret_cast<const uint4*>(
+                                           (t ? wp1 : wp0) + (k0 + 32 * s + 8 * q) * 2)
+                                     : make_uint4(0, 0, 0, 0);
+        f.x[s] = (xok && in) ? *reinterpret_cast<const uint4*>(xp + (k0 + 32 * s + 8 * q) * 2)
+                             : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  f32x4 acc[2];
+  acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* bsc = static_cast<const float*>(a.b_scale);
+
+  auto compute = [&](const Frag<RECIPE>& f, int64_t k0) {
+    if constexpr (kFp8) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float ws = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) *
+                                 (K / 128) + k0 / 128];
+        const f32x4 p = mma_fp8(f.w[t][0], f.w[t][1], f.x[0], f.x[1]);
+        acc[t] += p * (f.xs * ws);
+      }
+    } else if constexpr (kFp4) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint4 w = f.w[t];
+        if (f.sc[t] == 0u) w = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> 0
+        const float sc = __uint_as_float(f.sc[t] << 23);
+        acc[t] = mma_bf16(fp4x8(w.x, sc), f.x[0], acc[t]);
+        acc[t] = mma_bf16(fp4x8(w.y, sc), f.x[1], acc[t]);
+        acc[t] = mma_bf16(fp4x8(w.z, sc), f.x[2], acc[t]);
+        acc[t] = mma_bf16(fp4x8(w.w, sc), f.x[3], acc[t]);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[t] = mma_bf16(f.w[t][s], f.x[s], acc[t]);
+    }
+  };
+
+  // ---- K loop, PD stages in flight
+  const int nk = static_cast<int>((K + KS - 1) / KS);
+  Frag<RECIPE> buf[PD];
+#pragma unroll
+  for (int d = 0; d < PD; ++d)
+    if (d < nk) load(buf[d], static_cast<int64_t>(d) * KS);
+  for (int kt = 0; kt < nk; kt += PD) {
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+      const int k = kt + d;
+      if (k < nk) {
+        compute(buf[d], static_cast<int64_t>(k) * KS);
+        if (k + PD < nk) load(buf[d], static_cast<int64_t>(k + PD) * KS);
+      }
+    }
+  }
+
+  // ---- epilogue: lane holds slot m = l16, columns col0 + 4q + r
+  const bool f16 = a.out_f16 != 0;
+  const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  const int drow = s_drow[l16];
+  constexpr int NO = kGlu ? 1 : 2;
+  float ov[NO][4];
+#pragma unroll
+  for (int t = 0; t < NO; ++t) {
+    const int64_t n = col0 + 16 * t + 4 * q;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool nok = n + r < N;
+      float v = acc[t][r];
+      if (a.bias && nok) v += bf16_to_f32(a.bias[bias_base + n + r]);
+      v = rnd(v, f16);
+      if constexpr (kGlu) {
+        float u = acc[1][r];
+        if (a.bias && nok) u += bf16_to_f32(a.bias[bias_base + a.up_off + n + r]);
+        u = rnd(u, f16);
+        if (a.clamp_limit > 0.f) {
+          v = fminf(v, a.clamp_limit);
+          u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
+        }
+        v = rnd(glu_fn(v, u, a), f16);
+      }
+      ov[t][r] = nok ? v : 0.f;
+    }
+  }
+  if constexpr (QOUT) {
+    float m = 1e-10f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[0][r]));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (q == 0) s_amax[wave][l16] = m;
+    __syncthreads();
+    if (drow < 0) return;
+    float am = s_amax[0][l16];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][l16]);
+    const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
+    const float inv = 1.0f / sc;
+    if (wave == 0 && q == 0)
+      static_cast<float*>(qs)[static_cast<int64_t>(drow) * (N / 128) + blockIdx.x] = sc;
+    uint32_t w = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      w |= f32_to_e4m3(fminf(fmaxf(ov[0][r] * inv, -448.f), 448.f)) << (8 * r);
+    *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * N +
+                                 col0 + 4 * q) = w;
+  } else {
+    if (drow < 0) return;
+    uint16_t* d = static_cast<uint16_t*>(a.D);
+#pragma unroll
+    for (int t = 0; t < NO; ++t) {
+      const int64_t n = col0 + 16 * t + 4 * q;
+      uint16_t h[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) h[r] = f16 ? f32_to_f16(ov[t][r]) : f32_to_bf16(ov[t][r]);
+      uint16_t* dst = d + static_cast<int64_t>(drow) * N + n;
+      if (n + 3 < N && (N & 3) == 0) {
+        *reinterpret_cast<uint2*>(dst) =
+            make_uint2(h[0] | (uint32_t(h[1]) << 16), h[2] | (uint32_t(h[3]) << 16));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n + r < N) dst[r] = h[r];
+      }
+    }
+  }
+}
+
+template <int RECIPE, int EPI, bool QOUT>
+int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+  constexpr int PD = RECIPE == MI355MOE_RECIPE_BF16 ? 2 : 4;
+  const int64_t cols = EPI == EPI_GLU ? 128 : 256;
+  dim3 grid(static_cast<unsigned>(cdiv(a.N, cols)), static_cast<unsigned>(max_blocks));
+  moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(a, qs);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+}  // namespace
+
+// 16-slot blocks (the caller aligns expert segments to 16).
+int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
+                           int64_t max_blocks, void* qs, hipStream_t st) {
+  if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
+  if (qout) {
+    MI_ARG(recipe == MI355MOE_RECIPE_FP8BLOCK && epi == EPI_GLU && a.N % 128 == 0,
+           "fp8 activation output needs the fp8block recipe and I % 128 == 0");
+    return launch_stream<MI355MOE_RECIPE_FP8BLOCK, EPI_GLU, true>(a, max_blocks, qs, st);
+  }
+  switch (recipe) {
+    case MI355MOE_RECIPE_BF16:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_BF16, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_BF16, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_FP8BLOCK:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_FP8BLOCK, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_FP8BLOCK, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_MXFP4:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_MXFP4, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_MXFP4, EPI_STORE, false>(a, max_blocks, qs, st);
+    default:
+      return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
+  }
+}
+
+}  // namespace mi355
