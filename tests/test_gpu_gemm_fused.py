@@ -272,6 +272,43 @@ def test_grouped_gemm_big_tiles(dev, recipe):
     torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
+# ------------------------------------------- bf16 prefill (256x256) tiles
+WIDE_ROWS = [1, 31, 64, 65, 256, 513]
+
+
+@pytest.mark.parametrize("K", [32, 64, 96, 352])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_grouped_gemm_wide_tiles(dev, K, out_dtype):
+    """bf16 weights with >96 rows per expert select the 256x256 kernel.
+    Valid rows per 256-slot block 1..256 (empty and half-empty waves, skipped
+    DMA groups); K from one 32-element stage (shorter than the 3-deep
+    prefetch) to 11; N=200 is one ragged tile; bias; bf16 or fp16 output."""
+    g = torch.Generator().manual_seed(K)
+    E, N = len(WIDE_ROWS), 200
+    M = sum(WIDE_ROWS)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = (torch.randn(E, N, generator=g) * 0.1).to(torch.bfloat16)
+    rows = torch.tensor(WIDE_ROWS, dtype=torch.int32)
+    d = torch.full((M, N), float("nan"), dtype=out_dtype, device=dev)
+    _ops().cutlass_grouped_gemm(a.to(dev), b.transpose(1, 2).contiguous().to(dev), None,
+                                bias.to(dev), d, rows.to(dev), N, K, E)
+    ref = O.grouped_gemm("bf16", a, b, None, bias, WIDE_ROWS, out_dtype=out_dtype)
+    torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("activation", ["silu", "swigluoai"])
+def test_fused_moe_wide_tiles_ragged(dev, activation):
+    """Whole bf16 layer through the 256x256 kernels (256 slots per expert on
+    average): I=224 leaves a ragged GLU tile and a 7-stage w2 K loop, H=352
+    an 11-stage w13 loop; swigluoai adds biases and the clamps."""
+    import dataclasses
+    base = _W().CONFIGS["C5" if activation == "swigluoai" else "C2"]
+    cfg = dataclasses.replace(base, recipe="bf16", hidden=352, inter=224, experts=8, topk=2)
+    cfg, w, x, tw, ti, out, _ = _layer(cfg, 1024, dev)
+    _close(out, _oracle_layer(cfg, w, x, tw, ti))
+
+
 @pytest.mark.parametrize("name,T,sample", [("C2", 4096, 24), ("C3", 8192, 6),
                                            ("C4", 2048, 12), ("C5", 4096, 12)])
 def test_fused_moe_prefill_full_size_sampled(dev, name, T, sample):

@@ -96,9 +96,11 @@ def test_grouped_topk_full_size_invariants(dev):
 
 
 # ---------------------------------------------------------------- alignment
+# above 4096 ids the sort runs in chunks of workgroups: 4097 leaves a
+# one-id last chunk, E=990 a large key space
 ALIGN_CASES = [(1, 1, 32, 32), (3, 2, 160, 128), (256, 16, 256, 32),
                (2256, 32, 257, 128), (4096, 2, 32, 128), (4096, 8, 256, 16),
-               (8192, 8, 256, 64)]
+               (8192, 8, 256, 64), (4097, 1, 64, 32), (1700, 3, 990, 8)]
 
 
 @pytest.mark.parametrize("m,topk,E,bs", ALIGN_CASES)
@@ -127,8 +129,9 @@ def test_moe_align_zipf_skew_c4(dev):
     assert np.array_equal(srt.cpu().numpy(), rs) and np.array_equal(eids.cpu().numpy(), re)
 
 
-def test_moe_align_expert_map(dev):
-    E, m, k, bs = 8, 32, 4, 64
+@pytest.mark.parametrize("m", [32, 2048])
+def test_moe_align_expert_map(dev, m):
+    E, k, bs = 8, 4, 64
     g = torch.Generator().manual_seed(5)
     ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(m)]).int()
     em = torch.full((E,), -1, dtype=torch.int32)
@@ -152,7 +155,7 @@ def test_moe_align_deterministic(dev):
 
 
 @pytest.mark.parametrize("T,k,E,with_map", [(32, 1, 16, False), (257, 8, 64, True),
-                                             (1024, 4, 128, False)])
+                                             (1024, 4, 128, False), (2048, 8, 128, True)])
 def test_remap_hidden_states(dev, T, k, E, with_map):
     g = torch.Generator().manual_seed(T)
     x = torch.randn(T, 128, generator=g).to(torch.bfloat16)

@@ -1,5 +1,9 @@
 // Token -> expert alignment: a deterministic, stable counting sort of the
-// flattened top-k expert ids in one 1024-thread workgroup.
+// flattened top-k expert ids.  Up to kOneBlockMax ids it runs in one
+// 1024-thread workgroup (one launch, the decode case); larger inputs use
+// three launches over 1024-id chunks (count, scan, scatter) with the same
+// ordering rule, so that the scattered stores of the sorted ids spread over
+// the whole GPU instead of one CU.
 //
 // The 16 wavefronts each own a contiguous chunk of the flat ids, so
 // "chunk order, then rank inside the chunk" is flat order.  Per-chunk expert
@@ -167,6 +171,179 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-workgroup sort.  Chunk c holds ids [c*chunk, (c+1)*chunk); chunk is a
+// multiple of 256 so each of a chunk's 4 waves owns a contiguous multiple of
+// 64 ids.  "chunk order, wave order, rank inside the 64-id step" is flat
+// order, as in the one-workgroup kernel.
+constexpr int kOneBlockMax = 4096;
+constexpr int kChunkIds = 1024;
+constexpr int kMaxChunks = 1024;
+
+inline int64_t sort_chunk(int64_t numel) {
+  int64_t c = cdiv(numel, kChunkIds);
+  if (c > kMaxChunks) c = kMaxChunks;
+  return cdiv(cdiv(numel, c), 256) * 256;
+}
+
+// per-chunk expert counts: cnt[c][e]
+template <typename Id>
+__global__ __launch_bounds__(256) void chunk_count_kernel(
+    const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
+    const int32_t* __restrict__ map, int num_keys, int64_t chunk,
+    int32_t* __restrict__ cnt) {
+  __shared__ int s[kMaxKeys];
+  for (int e = threadIdx.x; e < num_keys; e += 256) s[e] = 0;
+  __syncthreads();
+  const int64_t lo = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t hi = lo + chunk < numel ? lo + chunk : numel;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+    const uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+    if (key != kInvalidKey) atomicAdd(&s[key], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < num_keys; e += 256)
+    cnt[static_cast<int64_t>(blockIdx.x) * num_keys + e] = s[e];
+}
+
+// cnt[c][e] -> ids of expert e in chunks before c; cum[e] = padded start of
+// expert e (cum[num_keys] = total padded), tot[e] = its id count.  The
+// chunk counts are read 8 at a time so the loads overlap.
+__global__ __launch_bounds__(kSortThreads) void chunk_scan_kernel(
+    int32_t* __restrict__ cnt, int nchunks, int num_keys, int block_size,
+    int32_t* __restrict__ cum, int32_t* __restrict__ tot,
+    int32_t* __restrict__ ntp, int32_t* __restrict__ counts_out) {
+  __shared__ int s_wave_tot[kSortWaves];
+  const int tid = threadIdx.x;
+  int total_e = 0;
+  if (tid < num_keys) {
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = c0 + u < nchunks ? cnt[static_cast<int64_t>(c0 + u) * num_keys + tid] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (c0 + u < nchunks) cnt[static_cast<int64_t>(c0 + u) * num_keys + tid] = total_e;
+        total_e += v[u];
+      }
+    }
+  }
+  const int padded = (total_e + block_size - 1) / block_size * block_size;
+  int total_padded = 0;
+  const int start = block_exclusive_scan(tid < num_keys ? padded : 0, s_wave_tot,
+                                         total_padded);
+  if (tid < num_keys) {
+    cum[tid] = start;
+    tot[tid] = total_e;
+    if (counts_out) counts_out[tid] = total_e;
+  }
+  if (tid == 0) {
+    cum[num_keys] = total_padded;
+    if (ntp) ntp[0] = total_padded;
+  }
+}
+
+// Stable scatter of chunk blockIdx.x, then (grid-strided) the padding slots,
+// the tail past the padded total and the expert id of every block.
+template <typename Id>
+__global__ __launch_bounds__(256) void chunk_scatter_kernel(
+    const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
+    const int32_t* __restrict__ map, int num_keys, int64_t chunk,
+    const int32_t* __restrict__ off, const int32_t* __restrict__ cum,
+    const int32_t* __restrict__ tot, int block_size,
+    int32_t* __restrict__ sorted_ids, int64_t max_padded,
+    int32_t* __restrict__ expert_ids, int64_t max_blocks,
+    int32_t* __restrict__ inv_pos, int32_t pad_value) {
+  __shared__ int s_cnt[4][kMaxKeys];
+  __shared__ int s_cum[kMaxKeys + 1];
+  __shared__ int s_tot[kMaxKeys];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < 4 * kMaxKeys; i += 256) (&s_cnt[0][0])[i] = 0;
+  for (int e = tid; e <= num_keys; e += 256) {
+    s_cum[e] = cum[e];
+    if (e < num_keys) s_tot[e] = tot[e];
+  }
+  __syncthreads();
+
+  const int64_t sub = chunk / 4;
+  const int64_t clo = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t lo = clo + wave * sub;
+  const int64_t hi0 = lo + sub < numel ? lo + sub : numel;
+  const int64_t hi = hi0 > lo ? hi0 : lo;
+  const int steps = static_cast<int>(sub / 64);
+  for (int s = 0; s < steps; ++s) {
+    const int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
+    if (i < hi) {
+      const uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+      if (key != kInvalidKey) atomicAdd(&s_cnt[wave][key], 1);
+    }
+  }
+  __syncthreads();
+  // wave w's first slot for expert e: expert start + ids in earlier chunks
+  // + ids of waves < w
+  for (int e = tid; e < num_keys; e += 256) {
+    int run = s_cum[e] + off[static_cast<int64_t>(blockIdx.x) * num_keys + e];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int c = s_cnt[w][e];
+      s_cnt[w][e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  // each wave ranks its own 64-id steps; its counters are its own, and the
+  // LDS accesses of one wave execute in program order
+  const unsigned long long below = (1ull << lane) - 1ull;
+  for (int s = 0; s < steps; ++s) {
+    const int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
+    uint32_t key = kInvalidKey;
+    if (i < hi) key = load_key(ids, i, id_bound, map, num_keys);
+    unsigned long long same = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 11; ++b) {
+      const unsigned long long bb = __ballot((key >> b) & 1u);
+      same &= ((key >> b) & 1u) ? bb : ~bb;
+    }
+    const int rank = __popcll(same & below);
+    const int cnt = __popcll(same);
+    int pos = -1;
+    if (key != kInvalidKey) {
+      pos = s_cnt[wave][key] + rank;
+      if (sorted_ids && pos < max_padded) sorted_ids[pos] = static_cast<int32_t>(i);
+    }
+    if (inv_pos && i < hi) inv_pos[i] = pos;
+    if (key != kInvalidKey && rank == 0) s_cnt[wave][key] += cnt;
+  }
+
+  // padding slots of every expert and the tail, expert id of every block
+  const int total_padded = s_cum[num_keys];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  auto expert_at = [&](int p) -> int {  // last e with s_cum[e] <= p
+    int lo_e = 0, hi_e = num_keys - 1;
+    while (lo_e < hi_e) {
+      const int mid = (lo_e + hi_e + 1) >> 1;
+      if (s_cum[mid] <= p) lo_e = mid; else hi_e = mid - 1;
+    }
+    return lo_e;
+  };
+  if (sorted_ids) {
+    for (int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + tid; p < max_padded; p += stride) {
+      if (p >= total_padded) {
+        sorted_ids[p] = pad_value;
+      } else {
+        const int e = expert_at(static_cast<int>(p));
+        if (p - s_cum[e] >= s_tot[e]) sorted_ids[p] = pad_value;
+      }
+    }
+  }
+  if (expert_ids) {
+    const int nblk = total_padded / block_size;
+    for (int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + tid; b < max_blocks; b += stride)
+      expert_ids[b] = b < nblk ? expert_at(static_cast<int>(b) * block_size) : 0;
+  }
+}
+
 // rows_per_expert (contiguous segments) -> block-padded row list:
 // row_ids[p] = first_row(e) + r for r < rows(e), else pad_value.
 __global__ __launch_bounds__(kSortThreads) void segments_to_blocks_kernel(
@@ -257,35 +434,60 @@ void launch_sort(const void* ids, int64_t numel, int64_t id_bound,
                  const int32_t* map, int num_keys, int bs, int32_t* sorted,
                  int64_t max_padded, int32_t* eids, int64_t max_blocks,
                  int32_t* ntp, int32_t* inv, int32_t* counts, int32_t pad,
-                 hipStream_t st) {
-  hipLaunchKernelGGL(counting_sort_kernel<Id>, dim3(1), dim3(kSortThreads), 0,
-                     st, static_cast<const Id*>(ids), numel, id_bound, map,
-                     num_keys, bs, sorted, max_padded, eids, max_blocks, ntp,
-                     inv, counts, pad);
+                 int32_t* ws, hipStream_t st) {
+  const Id* id = static_cast<const Id*>(ids);
+  if (!ws) {
+    counting_sort_kernel<Id><<<1, kSortThreads, 0, st>>>(
+        id, numel, id_bound, map, num_keys, bs, sorted, max_padded, eids,
+        max_blocks, ntp, inv, counts, pad);
+    return;
+  }
+  const int64_t chunk = sort_chunk(numel);
+  const int nchunks = static_cast<int>(cdiv(numel, chunk));
+  int32_t* cnt = ws;
+  int32_t* cum = cnt + static_cast<int64_t>(nchunks) * num_keys;
+  int32_t* tot = cum + num_keys + 1;
+  chunk_count_kernel<Id><<<nchunks, 256, 0, st>>>(id, numel, id_bound, map,
+                                                   num_keys, chunk, cnt);
+  chunk_scan_kernel<<<1, kSortThreads, 0, st>>>(cnt, nchunks, num_keys, bs, cum,
+                                                tot, ntp, counts);
+  chunk_scatter_kernel<Id><<<nchunks, 256, 0, st>>>(
+      id, numel, id_bound, map, num_keys, chunk, cnt, cum, tot, bs, sorted,
+      max_padded, eids, max_blocks, inv, pad);
 }
 
 }  // namespace
 
-// Shared by the fused layer and the grouped GEMM entry points.
+// Workspace of the multi-workgroup sort (0: the one-workgroup kernel runs).
+size_t counting_sort_ws_bytes(int64_t numel, int64_t num_keys) {
+  if (numel <= kOneBlockMax || num_keys <= 0) return 0;
+  const int64_t nchunks = cdiv(numel, sort_chunk(numel));
+  return static_cast<size_t>(nchunks * num_keys + 2 * num_keys + 1) * sizeof(int32_t);
+}
+
+// Shared by the fused layer and the alignment entry points.  ws: at least
+// counting_sort_ws_bytes(numel, num_keys) bytes, or null (one workgroup).
 int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t id_bound, const int32_t* map, int64_t num_keys,
                       int64_t bs, int32_t* sorted, int64_t max_padded,
                       int32_t* eids, int64_t max_blocks, int32_t* ntp,
                       int32_t* inv, int32_t* counts, int32_t pad,
-                      hipStream_t st) {
+                      void* ws, size_t ws_bytes, hipStream_t st) {
   MI_ARG(num_keys > 0 && num_keys <= kMaxKeys,
          "padded_num_experts must be less than 1024");
   MI_ARG(bs > 0, "block_size must be positive");
   MI_ARG(numel >= 0 && numel < (int64_t(1) << 31), "too many topk_ids");
+  const size_t need = counting_sort_ws_bytes(numel, num_keys);
+  int32_t* w = (need > 0 && ws && ws_bytes >= need) ? static_cast<int32_t*>(ws) : nullptr;
   switch (ids_dtype) {
     case MI355MOE_I32:
-      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, st);
+      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, w, st);
       break;
     case MI355MOE_I64:
-      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, st);
+      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, w, st);
       break;
     case MI355MOE_U32:
-      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, st);
+      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, w, st);
       break;
     default:
       return set_error(MI355MOE_ERR_INVALID, "topk_ids must be int32, int64 or uint32");
@@ -310,15 +512,16 @@ int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
 
 using namespace mi355;
 
-extern "C" size_t mi355moe_moe_align_block_size_workspace_size(int64_t, int64_t) {
-  return 0;
+extern "C" size_t mi355moe_moe_align_block_size_workspace_size(int64_t numel,
+                                                               int64_t num_experts) {
+  return counting_sort_ws_bytes(numel, num_experts);
 }
 
 extern "C" int mi355moe_moe_align_block_size(
     const void* topk_ids, int ids_dtype, int64_t numel, int64_t num_experts,
     int64_t block_size, int32_t* sorted_token_ids, int64_t max_num_tokens_padded,
     int32_t* expert_ids, int64_t max_num_m_blocks, int32_t* ntp,
-    const int32_t* expert_map, void* /*workspace*/, size_t /*ws*/,
+    const int32_t* expert_map, void* workspace, size_t workspace_bytes,
     void* stream) {
   MI_ARG(num_experts > 0, "num_experts must be positive");
   MI_ARG((num_experts + 31) / 32 * 32 < 1024,
@@ -327,12 +530,13 @@ extern "C" int mi355moe_moe_align_block_size(
                            num_experts, block_size, sorted_token_ids,
                            max_num_tokens_padded, expert_ids, max_num_m_blocks,
                            ntp, nullptr, nullptr, static_cast<int32_t>(numel),
-                           static_cast<hipStream_t>(stream));
+                           workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
-extern "C" size_t mi355moe_remap_hidden_states_workspace_size(int64_t, int64_t,
-                                                              int64_t) {
-  return 0;
+extern "C" size_t mi355moe_remap_hidden_states_workspace_size(int64_t num_tokens,
+                                                              int64_t topk,
+                                                              int64_t local_experts) {
+  return counting_sort_ws_bytes(num_tokens * topk, local_experts);
 }
 
 extern "C" int mi355moe_remap_hidden_states(
@@ -340,8 +544,8 @@ extern "C" int mi355moe_remap_hidden_states(
     int64_t scale_cols, int64_t scale_bytes, void* remapped,
     void* remapped_scales, const int32_t* expert_map, int32_t* rows_per_expert,
     int32_t* perm, const void* topk_ids, int ids_dtype, int64_t T, int64_t H,
-    int64_t k, int64_t total_experts, int64_t local_experts, void*, size_t,
-    void* stream) {
+    int64_t k, int64_t total_experts, int64_t local_experts, void* workspace,
+    size_t workspace_bytes, void* stream) {
   MI_ARG(local_experts > 0 && local_experts <= 1024,
          "local experts number must be in [1, 1024]");
   MI_ARG(k > 0, "Unsupported TopK value");
@@ -351,7 +555,8 @@ extern "C" int mi355moe_remap_hidden_states(
   if (slots == 0) return MI355MOE_OK;
   int rc = run_counting_sort(topk_ids, ids_dtype, slots, total_experts,
                              expert_map, local_experts, 1, nullptr, 0, nullptr,
-                             0, nullptr, perm, rows_per_expert, 0, st);
+                             0, nullptr, perm, rows_per_expert, 0, workspace,
+                             workspace_bytes, st);
   if (rc) return rc;
   hipLaunchKernelGGL(remap_copy_kernel, dim3(static_cast<unsigned>(slots)),
                      dim3(256), 0, st, static_cast<const uint8_t*>(hidden),

@@ -100,6 +100,8 @@ struct FusedLayout {
   GemmTile tile;
   int64_t slots, max_padded, max_blocks, grid_blocks;
   int32_t *sorted, *eids, *ntp;
+  int32_t* sortws;  // multi-workgroup sort scratch (sortws_bytes, may be 0)
+  size_t sortws_bytes;
   uint8_t* xq;    // fp8 hidden [T, H]
   float* xs;      // [T, H/128]
   void* act;      // bf16 [max_padded, I] or e4m3 [max_padded, I]
@@ -112,13 +114,15 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
   const int64_t E = a->num_experts;
   L.slots = a->num_tokens * a->topk;
-  L.tile = pick_tile(L.slots, E, &L.bm);
+  L.tile = pick_tile(a->recipe, a->hidden % 32 == 0 && a->inter % 32 == 0, L.slots, E, &L.bm);
   padded_sizes(L.slots, E, L.bm, L.max_padded, L.max_blocks);
   L.grid_blocks = launch_blocks(L.slots, E, L.bm, L.max_blocks);
   Carver c{base};
   L.sorted = c.take<int32_t>(std::max<int64_t>(L.max_padded, 1));
   L.eids = c.take<int32_t>(std::max<int64_t>(L.max_blocks, 1));
   L.ntp = c.take<int32_t>(1);
+  L.sortws_bytes = counting_sort_ws_bytes(L.slots, E);
+  L.sortws = c.take<int32_t>(static_cast<int64_t>(L.sortws_bytes / sizeof(int32_t)));
   const bool fp8 = a->recipe == MI355MOE_RECIPE_FP8BLOCK;
   if (fp8) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
@@ -240,7 +244,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   int rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
                              a->expert_map, E, L.bm, L.sorted, L.max_padded,
                              L.eids, L.max_blocks, L.ntp, nullptr, nullptr,
-                             static_cast<int32_t>(L.slots), st);
+                             static_cast<int32_t>(L.slots), L.sortws, L.sortws_bytes, st);
   if (rc) return rc;
 
   const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
@@ -332,7 +336,7 @@ struct GGLayout {
 GGLayout gg_plan(int recipe, bool need_quant, int64_t M, int64_t K, int64_t E,
                  uint8_t* base) {
   GGLayout L{};
-  L.tile = pick_tile(M, E, &L.bm);
+  L.tile = pick_tile(recipe, K % 32 == 0, M, E, &L.bm);
   padded_sizes(M, E, L.bm, L.max_padded, L.max_blocks);
   L.grid_blocks = launch_blocks(M, E, L.bm, L.max_blocks);
   Carver c{base};
@@ -374,6 +378,7 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
                                      void* ws, size_t ws_bytes, void* stream) {
   MI_ARG(M >= 0 && N > 0 && K > 0 && E > 0 && E <= 1024, "invalid GEMM shape");
   MI_ARG(N % 8 == 0, "N must be a multiple of 8");
+  MI_ARG(out_dtype == MI355MOE_BF16 || out_dtype == MI355MOE_F16, "output must be 16-bit");
   bool need_quant = false;
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
     MI_ARG(N % 128 == 0 && K % 128 == 0, "fp8 block scaling needs N and K % 128 == 0");
@@ -385,7 +390,6 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
              "activations must be bfloat16, float16 or e4m3");
       need_quant = true;
     }
-    MI_ARG(out_dtype == MI355MOE_BF16 || out_dtype == MI355MOE_F16, "output must be 16-bit");
   } else if (recipe == MI355MOE_RECIPE_MXFP4) {
     MI_ARG(K % 32 == 0, "mxfp4 needs K % 32 == 0");
     MI_ARG(a_dtype == MI355MOE_BF16, "mxfp4 activations must be bfloat16");

@@ -50,12 +50,15 @@ int pick_block_m(int64_t slots, int64_t num_experts);
 // Kernel family by the expected rows per active expert:
 //   <= 24   STREAM: independent-wave weight streaming, 16-slot blocks
 //   <= 96   SMALL:  LDS-shared activation tile, 32/64-slot blocks
-//   >  96   BIG:    128x256 LDS-staged tiles, 128-slot blocks
-// MI355MOE_GEMM_TILE=stream|small|big overrides (A/B measurements).
+//   >  96   WIDE:   bf16 weights with every K % 32 == 0 (wide_ok): 256x256
+//                   tiles, 256-slot blocks
+//           BIG:    otherwise, 128x256 LDS-staged tiles, 128-slot blocks
+// MI355MOE_GEMM_TILE=stream|small|big|bigreg|wide overrides (A/B
+// measurements; wide falls back to big where it does not apply).
 // (TILE_BIG runs the LDS-DMA pipelined kernel where pipe_supported(),
 // TILE_BIGREG forces the register-staged one.)
-enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3 };
-GemmTile pick_tile(int64_t slots, int64_t num_experts, int* bm);
+enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3, TILE_WIDE = 4 };
+GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm);
 
 // Launch the chosen family over max_blocks blocks of bm slots.
 int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
@@ -71,16 +74,21 @@ int launch_moe_gemm_big(int recipe, int epi, bool qout, const GemmArgs& a,
 bool pipe_supported(int recipe, const GemmArgs& a);
 int launch_moe_gemm_pipe(int recipe, int epi, bool qout, const GemmArgs& a,
                          int64_t max_blocks, void* qs, hipStream_t st);
+// 256-slot blocks, bf16 weights, K % 32 == 0 (moe_gemm_wide.hip).
+bool wide_supported(int recipe, const GemmArgs& a);
+int launch_moe_gemm_wide(int recipe, int epi, const GemmArgs& a,
+                         int64_t max_blocks, hipStream_t st);
 // 16-slot blocks; GLU blocks cover 128 output columns, STORE blocks 256.
 int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
                            int64_t max_blocks, void* qs, hipStream_t st);
 
+size_t counting_sort_ws_bytes(int64_t numel, int64_t num_keys);
 int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t id_bound, const int32_t* map, int64_t num_keys,
                       int64_t bs, int32_t* sorted, int64_t max_padded,
                       int32_t* eids, int64_t max_blocks, int32_t* ntp,
                       int32_t* inv, int32_t* counts, int32_t pad,
-                      hipStream_t st);
+                      void* ws, size_t ws_bytes, hipStream_t st);
 int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
                            int32_t* row_ids, int64_t max_padded,
                            int32_t* eids, int64_t max_blocks, int32_t* ntp,

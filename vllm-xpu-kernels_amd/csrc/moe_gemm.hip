@@ -349,7 +349,7 @@ int pick_block_m(int64_t slots, int64_t num_experts) {
   return 128;
 }
 
-GemmTile pick_tile(int64_t slots, int64_t num_experts, int* bm) {
+GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm) {
   static const int force = [] {
     const char* v = getenv("MI355MOE_GEMM_TILE");
     if (!v) return -1;
@@ -357,12 +357,15 @@ GemmTile pick_tile(int64_t slots, int64_t num_experts, int* bm) {
     if (!strcmp(v, "small")) return static_cast<int>(TILE_SMALL);
     if (!strcmp(v, "big")) return static_cast<int>(TILE_BIG);
     if (!strcmp(v, "bigreg")) return static_cast<int>(TILE_BIGREG);
+    if (!strcmp(v, "wide")) return static_cast<int>(TILE_WIDE);
     return -1;
   }();
+  const bool wide = wide_ok && recipe == MI355MOE_RECIPE_BF16;
   const int m = pick_block_m(slots, num_experts);
-  GemmTile t = m == 16 ? TILE_STREAM : (m == 128 ? TILE_BIG : TILE_SMALL);
+  GemmTile t = m == 16 ? TILE_STREAM : (m == 128 ? (wide ? TILE_WIDE : TILE_BIG) : TILE_SMALL);
   if (force >= 0) t = static_cast<GemmTile>(force);
-  *bm = t == TILE_STREAM ? 16 : ((t == TILE_BIG || t == TILE_BIGREG) ? 128 : m);
+  if (t == TILE_WIDE && !wide) t = TILE_BIG;
+  *bm = t == TILE_STREAM ? 16 : (t == TILE_WIDE ? 256 : ((t == TILE_BIG || t == TILE_BIGREG) ? 128 : m));
   return t;
 }
 
@@ -376,6 +379,9 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
         return launch_moe_gemm_pipe(recipe, epi, qout, a, max_blocks, qs, st);
       return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIGREG: return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
+    case TILE_WIDE:
+      MI_ARG(!qout, "wide GEMM: no fp8 activation output");
+      return launch_moe_gemm_wide(recipe, epi, a, max_blocks, st);
     default: return launch_moe_gemm_q(recipe, epi, qout, bm, a, max_blocks, qs, st);
   }
 }

@@ -264,8 +264,9 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
     __syncthreads();
   }
 
-  epilogue_32x32<kGlu, QOUT>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax,
-                            static_cast<int>(blockIdx.x));
+  static_assert(sizeof(sW) >= 128 * (2 * 256 + 16), "epilogue staging");
+  epilogue_32x32_any<kGlu, QOUT>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax,
+                                static_cast<int>(blockIdx.x), &sW[0][0]);
 }
 
 template <int RECIPE, int EPI, bool QOUT>

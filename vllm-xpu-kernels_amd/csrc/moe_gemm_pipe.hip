@@ -279,7 +279,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   }
 
-  epilogue_32x32<kGlu, QOUT>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax, ntile);
+  static_assert(sizeof(ring) >= 128 * (2 * 256 + 16), "epilogue staging");
+  epilogue_32x32_any<kGlu, QOUT>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax, ntile, ring);
 }
 
 template <int RECIPE, int EPI, bool QOUT>

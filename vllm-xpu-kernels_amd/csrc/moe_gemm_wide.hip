@@ -1,0 +1,387 @@
+// Prefill grouped GEMM for bf16 weights: 256-slot x 256-weight-row tiles,
+// 8 waves, 4-slot LDS ring fed by direct global->LDS DMA.
+//
+// Why this shape.  Every K element of a tile moves (256 + 256) x 2 bytes from
+// L2 into LDS for 2 x 256 x 256 flops, half the bytes per flop of a 128 x 256
+// tile; the per-CU vector-memory path (about 64 B/clk) then needs ~32 B/clk
+// at full MFMA rate instead of ~48.  Two waves per SIMD (waves w and w + 4
+// share SIMD w % 4) let one wave's MFMAs cover the other's LDS latency, so no
+// register double buffering is needed and each wave keeps its 128 x 64
+// accumulator block (8 32x32 tiles, 128 registers) resident.
+//
+// Layout.  A K stage holds 32 bf16 (64 bytes) of each of the 256 activation
+// rows and 256 weight rows: 32 KB, written by 32 global_load_lds_dwordx4 (16
+// rows x 64 B each; lane l writes LDS bytes [16l, 16l + 16) of its 1 KB
+// block).  16-byte chunk c of row r sits at slot c ^ ((r >> 2) & 3): sixteen
+// consecutive rows read at one logical chunk then hit sixteen distinct 16-byte
+// bank groups.  A and W use the same K permutation, so the MFMA sums are
+// unchanged.
+//
+// Pipeline.  Stages kt+1..kt+3 are in flight while stage kt is computed; the
+// DMA instructions of stage kt+3 are spread between the MFMAs of stage kt so
+// the vector-memory queue drains while the matrix cores run.
+//
+// Padding.  The slots of a block are its expert's rows followed by padding;
+// with v valid slots, DMA of 16-row groups at or past v is skipped, and a wave
+// whose 128 rows hold fewer than 65 (or no) valid slots runs the MFMAs of its
+// first 64 rows only (or none).
+#include <type_traits>
+
+#include "moe_gemm.h"
+
+namespace mi355 {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int BM = 256, BN = 256, ROWB = 64, KE = 32;
+constexpr int A_BYTES = BM * ROWB;             // 16 KB
+constexpr int STAGE = (BM + BN) * ROWB;        // 32 KB
+constexpr int NSTAGE = 4;
+constexpr int DMA_PER_WAVE = STAGE / 1024 / 8;  // 4
+constexpr int RING_BYTES = NSTAGE * STAGE;
+constexpr int EPI_PITCH_MAX = 2 * 256 + 16;     // bytes per staged output row
+constexpr int LDS_BYTES = RING_BYTES > BM * EPI_PITCH_MAX ? RING_BYTES : BM * EPI_PITCH_MAX;
+
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
+}
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(lds_base) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+// wave-uniform count of DMA instructions allowed to stay outstanding
+__device__ __forceinline__ void wait_vm_dyn(int n) {
+  switch (n) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<1>(); break;
+    case 2: wait_vm<2>(); break;
+    case 3: wait_vm<3>(); break;
+    case 4: wait_vm<4>(); break;
+    case 5: wait_vm<5>(); break;
+    case 6: wait_vm<6>(); break;
+    case 7: wait_vm<7>(); break;
+    default: wait_vm<8>(); break;
+  }
+}
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+
+__device__ __forceinline__ f32x16 mfma(uint4 a, uint4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+      __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <bool F16>
+__device__ __forceinline__ float round16(float v) {
+  if constexpr (F16) return f16_to_f32(f32_to_f16(v));
+  else return bf16_to_f32(f32_to_bf16(v));
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t to16(float v) {
+  if constexpr (F16) return f32_to_f16(v);
+  else return f32_to_bf16(v);
+}
+// x * sigmoid(k x) with the hardware exp2 and reciprocal (about 1 ulp each,
+// far below the 16-bit rounding that follows)
+__device__ __forceinline__ float x_sigmoid(float x, float k) {
+  const float e = __builtin_amdgcn_exp2f(-k * x * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.f + e);
+}
+
+struct Frags {
+  uint4 x[2][4];  // [ks][j]: activation rows 128wm + 32j + l32
+  uint4 w[2][2];  // [ks][i]: weight rows wrow_t[i] + l32
+};
+
+// One K stage of one wave: read its fragments, then NJ/32 x 2 x 2 MFMAs with
+// the next-next-next stage's DMA instructions spread between them.
+template <int NJ>
+__device__ __forceinline__ void stage_compute(f32x16 (&acc)[2][4], const uint8_t* As,
+                                              const uint8_t* Ws, const int (&xoff)[2][4],
+                                              const int (&woff)[2][2], bool dma,
+                                              const uint8_t* const (&src)[DMA_PER_WAVE],
+                                              int64_t koff, uint32_t dst_base, int nd) {
+  Frags f;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) f.x[ks][j] = *reinterpret_cast<const uint4*>(As + xoff[ks][j]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f.w[ks][i] = *reinterpret_cast<const uint4*>(Ws + woff[ks][i]);
+  }
+  // 4 groups of MFMAs, one DMA instruction after each
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int ks = g >> 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if ((g & 1) == i || NJ == 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(f.w[ks][i], f.x[ks][j], acc[i][j]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (dma && g < nd)
+      dma16(src[g] + koff, __builtin_amdgcn_readfirstlane(dst_base + g * 1024));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int EPI, bool F16>
+__global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
+  constexpr bool kGlu = EPI == EPI_GLU;
+  constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
+
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  __shared__ int s_arow[BM];
+  __shared__ int s_drow[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int l32 = lane & 31, h = lane >> 5;
+
+  // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
+  // XCD x takes the contiguous range [x*per, (x+1)*per) of the valid tiles,
+  // ordered (M-block, N-tile), so the N-tiles sharing a block's activation
+  // rows and the blocks of one expert sharing its weight rows meet in one L2.
+  // The grid is a multiple of 8 and at least the tile upper bound.
+  const int n_tiles = static_cast<int>((a.N + NOUT - 1) / NOUT);
+  const int valid = (*a.ntp / BM) * n_tiles;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int per = (valid + 7) / 8;
+  const int tile = (bid & 7) * per + (bid >> 3);
+  if ((bid >> 3) >= per || tile >= valid) return;  // uniform
+  const int blk = tile / n_tiles;
+  const int ntile = tile % n_tiles;
+  const int e = a.block_expert[blk];
+  const int64_t K = a.K, N = a.N;
+  const int64_t n0 = static_cast<int64_t>(ntile) * NOUT;
+  const int64_t wrow_bytes = K * 2;
+
+  int ok = 0;
+  if (tid < BM) {
+    const int rid = a.row_ids[static_cast<int64_t>(blk) * BM + tid];
+    ok = rid >= 0 && rid < a.num_valid;
+    s_arow[tid] = ok ? (a.a_by_pos ? blk * BM + tid : rid / a.a_div) : -1;
+    s_drow[tid] = ok ? (a.d_by_pos ? blk * BM + tid : rid) : -1;
+  }
+  // valid slots form a prefix of the block
+  const int v = __syncthreads_count(ok);
+
+  // weight row staged at tile row r; rows past N read row 0 (finite data
+  // whose outputs are never stored).  GLU: rows [0,128) gate, [128,256) up.
+  auto wrow_of = [&](int r) -> int64_t {
+    if constexpr (kGlu) {
+      const int64_t c = n0 + (r & 127);
+      return (r >= 128 ? a.up_off : 0) + (c < N ? c : 0);
+    } else {
+      const int64_t c = n0 + r;
+      return c < N ? c : 0;
+    }
+  };
+
+  // DMA instructions of this wave: blocks b = 4 wave + q of a stage, A rows
+  // for b < 16, weight rows after.  Padding-only activation groups are skipped.
+  const uint8_t* src[DMA_PER_WAVE];
+  int nd = 0;  // the used instructions are a prefix (A groups past v are a suffix)
+  {
+    const uint8_t* abase = static_cast<const uint8_t*>(a.A);
+    const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
+                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
+#pragma unroll
+    for (int q = 0; q < DMA_PER_WAVE; ++q) {
+      const int b = DMA_PER_WAVE * wave + q;
+      const int r = (b & 15) * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ swz(r);
+      const uint8_t* p;
+      bool use = true;
+      if (b < 16) {
+        const int ar = s_arow[r];
+        p = abase + static_cast<int64_t>(ar >= 0 ? ar : 0) * wrow_bytes + c * 16;
+        use = (b & 15) * 16 < v;
+      } else {
+        p = wexp + wrow_of(r) * wrow_bytes + c * 16;
+      }
+      src[q] = p;
+      nd += use ? 1 : 0;
+    }
+  }
+  const uint32_t dst0 = DMA_PER_WAVE * wave * 1024;  // LDS block of src[0]
+
+  // per-wave MFMA rows: 128 wm + [0, 32 NJ)
+  const int vw = v - 128 * wm;
+  const int nj = vw > 64 ? 4 : (vw > 0 ? 2 : 0);
+
+  // fragment offsets within a stage: chunk c = 2 ks + h
+  int xoff[2][4], woff[2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int c = 2 * ks + h;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = 128 * wm + 32 * j + l32;
+      xoff[ks][j] = m * ROWB + ((c ^ swz(m)) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (kGlu ? 128 * i + 32 * wn : 64 * wn + 32 * i) + l32;
+      woff[ks][i] = A_BYTES + r * ROWB + ((c ^ swz(r)) << 4);
+    }
+  }
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const uint32_t ring0 = lds_off(lds);
+  const int nk = static_cast<int>(K / KE);
+  auto issue_all = [&](int kt) {
+    const uint32_t base = ring0 + (kt % NSTAGE) * STAGE + dst0;
+    const int64_t koff = static_cast<int64_t>(kt) * ROWB;
+#pragma unroll
+    for (int q = 0; q < DMA_PER_WAVE; ++q)
+      if (q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(base + q * 1024));
+  };
+  for (int s = 0; s < 3 && s < nk; ++s) issue_all(s);
+
+  // one K loop per MFMA row count (a loop body with a run-time choice of
+  // variant needs more than the 256 registers two waves per SIMD leave)
+  auto kloop = [&](auto nj_c) {
+    constexpr int NJ = decltype(nj_c)::value;
+    for (int kt = 0; kt < nk; ++kt) {
+      // stage kt landed for this wave; later stages issued so far may pend
+      const int later = (nk - 1 - kt) < 2 ? (nk - 1 - kt) : 2;
+      wait_vm_dyn(nd * later);
+      __builtin_amdgcn_s_barrier();
+      const uint8_t* As = lds + (kt % NSTAGE) * STAGE;
+      const bool dma = kt + 3 < nk;
+      const int64_t koff = static_cast<int64_t>(kt + 3) * ROWB;
+      const uint32_t dbase = ring0 + ((kt + 3) % NSTAGE) * STAGE + dst0;
+      stage_compute<NJ>(acc, As, As, xoff, woff, dma, src, koff, dbase, nd);
+    }
+  };
+  if (nj == 4)
+    kloop(std::integral_constant<int, 4>{});
+  else if (nj == 2)
+    kloop(std::integral_constant<int, 2>{});
+  else
+    kloop(std::integral_constant<int, 0>{});
+
+  // ---- epilogue: bias, rounding, activation; output tile staged in LDS and
+  //      written with 16-byte row-contiguous stores
+  constexpr int PITCH = 2 * NOUT + 16;
+  const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  __syncthreads();  // every wave is done with the ring
+  auto tcol = [&](int i, int r) -> int {  // tile output column of (i, r)
+    return (kGlu ? 32 * wn : 64 * wn + 32 * i) + 8 * (r >> 2) + 4 * h + (r & 3);
+  };
+  constexpr int NI = kGlu ? 1 : 2;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    float bg[16], bu[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      bg[r] = 0.f;
+      bu[r] = 0.f;
+      if (a.bias) {
+        const int64_t n = n0 + tcol(i, r);
+        if (n < N) {
+          bg[r] = bf16_to_f32(a.bias[bias_base + n]);
+          if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 128 * wm + 32 * j + l32;
+      float ov[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float g = round16<F16>(acc[i][j][r] + bg[r]);
+        if constexpr (kGlu) {
+          float u = round16<F16>(acc[1][j][r] + bu[r]);
+          if (a.clamp_limit > 0.f) {
+            g = fminf(g, a.clamp_limit);
+            u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
+          }
+          float y;
+          if (a.act == MI355MOE_ACT_SILU) {
+            y = round16<F16>(x_sigmoid(g, 1.f)) * u;
+          } else {
+            g = g > a.limit ? a.limit : g;
+            u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+            y = (u + 1.f) * x_sigmoid(g, a.alpha);
+          }
+          g = round16<F16>(y);
+        }
+        ov[r] = g;
+      }
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const uint32_t lo = to16<F16>(ov[4 * g4]) | (to16<F16>(ov[4 * g4 + 1]) << 16);
+        const uint32_t hi = to16<F16>(ov[4 * g4 + 2]) | (to16<F16>(ov[4 * g4 + 3]) << 16);
+        *reinterpret_cast<uint2*>(lds + row * PITCH + 2 * tcol(i, 4 * g4)) = make_uint2(lo, hi);
+      }
+    }
+  }
+  __syncthreads();
+  uint16_t* d = static_cast<uint16_t*>(a.D);
+  const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
+  constexpr int CPR = 2 * NOUT / 16;  // 16-byte chunks per row
+  for (int idx = tid; idx < BM * CPR; idx += 512) {
+    const int row = idx / CPR, ch = idx % CPR;
+    const int drow = s_drow[row];
+    const int64_t col = n0 + ch * 8;
+    if (drow < 0 || col >= N) continue;
+    const uint4 val = *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
+    uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
+    if (vec) {
+      *reinterpret_cast<uint4*>(dst) = val;
+    } else {
+      const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+    }
+  }
+}
+
+template <int EPI, bool F16>
+int launch_wide(const GemmArgs& a, int64_t max_blocks, hipStream_t st) {
+  const int64_t cols = EPI == EPI_GLU ? 128 : 256;
+  const int64_t total = cdiv(a.N, cols) * max_blocks;
+  dim3 grid(static_cast<unsigned>(cdiv(total, 8) * 8));
+  moe_gemm_wide_kernel<EPI, F16><<<grid, dim3(512), 0, st>>>(a);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+}  // namespace
+
+bool wide_supported(int recipe, const GemmArgs& a) {
+  return recipe == MI355MOE_RECIPE_BF16 && a.K % KE == 0 && a.K > 0;
+}
+
+// 256-slot blocks; bf16 weights, K % 32 == 0.
+int launch_moe_gemm_wide(int recipe, int epi, const GemmArgs& a,
+                         int64_t max_blocks, hipStream_t st) {
+  if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
+  MI_ARG(wide_supported(recipe, a), "wide GEMM: needs bf16 weights and K % 32 == 0");
+  if (epi == EPI_GLU)
+    return a.out_f16 ? launch_wide<EPI_GLU, true>(a, max_blocks, st)
+                     : launch_wide<EPI_GLU, false>(a, max_blocks, st);
+  return a.out_f16 ? launch_wide<EPI_STORE, true>(a, max_blocks, st)
+                   : launch_wide<EPI_STORE, false>(a, max_blocks, st);
+}
+
+}  // namespace mi355

@@ -162,6 +162,10 @@ void moe_align_block_size(at::Tensor topk_ids, int64_t num_experts,
     TORCH_CHECK(maybe_expert_map->scalar_type() == at::kInt, "expert_map must be int32");
   }
   DevGuard g(topk_ids.device());
+  const size_t ws_bytes =
+      mi355moe_moe_align_block_size_workspace_size(topk_ids.numel(), num_experts);
+  at::Tensor ws;
+  if (ws_bytes) ws = at::empty({static_cast<int64_t>(ws_bytes)}, topk_ids.options().dtype(at::kByte));
   check_rc(mi355moe_moe_align_block_size(
                topk_ids.data_ptr(), dtype_code(topk_ids.scalar_type()),
                topk_ids.numel(), num_experts, block_size,
@@ -169,7 +173,7 @@ void moe_align_block_size(at::Tensor topk_ids, int64_t num_experts,
                experts_ids.data_ptr<int32_t>(), experts_ids.numel(),
                num_tokens_post_pad.data_ptr<int32_t>(),
                maybe_expert_map ? maybe_expert_map->data_ptr<int32_t>() : nullptr,
-               nullptr, 0, cur_stream(topk_ids)),
+               ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, cur_stream(topk_ids)),
            "moe_align_block_size");
 }
 
@@ -197,6 +201,10 @@ void remap_hidden_states(at::Tensor& hidden_states,
     scale_bytes = hidden_states_scales->element_size();
   }
   DevGuard g(hidden_states.device());
+  const size_t ws_bytes =
+      mi355moe_remap_hidden_states_workspace_size(T, k, local_experts_num);
+  at::Tensor ws;
+  if (ws_bytes) ws = at::empty({static_cast<int64_t>(ws_bytes)}, topk_ids.options().dtype(at::kByte));
   check_rc(mi355moe_remap_hidden_states(
                hidden_states.data_ptr(), hidden_states.element_size(),
                opt_ptr(hidden_states_scales), scale_cols, scale_bytes,
@@ -208,8 +216,8 @@ void remap_hidden_states(at::Tensor& hidden_states,
                unpermuted_row_to_permuted_row.data_ptr<int32_t>(),
                topk_ids.data_ptr(), dtype_code(topk_ids.scalar_type()), T,
                hidden_states.numel() / std::max<int64_t>(T, 1), k,
-               total_experts_num, local_experts_num, nullptr, 0,
-               cur_stream(hidden_states)),
+               total_experts_num, local_experts_num, ws_bytes ? ws.data_ptr() : nullptr,
+               ws_bytes, cur_stream(hidden_states)),
            "remap_hidden_states");
 }
 
