@@ -17,9 +17,13 @@
 // bank groups.  A and W use the same K permutation, so the MFMA sums are
 // unchanged.
 //
-// Pipeline.  Stages kt+1..kt+3 are in flight while stage kt is computed; the
-// DMA instructions of stage kt+3 are spread between the MFMAs of stage kt so
-// the vector-memory queue drains while the matrix cores run.
+// Pipeline.  Up to three stages are in flight ahead of the one computed; the
+// barrier that publishes stage kt+1 sits between the two K steps of stage kt,
+// so stage kt+1's fragment reads overlap stage kt's second MFMA group (all
+// waves meet the barrier together, and without this every stage would start
+// with the matrix cores idle behind the LDS reads).  The DMA instructions of
+// stage kt+3 are issued between MFMAs so the vector-memory queue drains while
+// the matrix cores run.
 //
 // Padding.  The slots of a block are its expert's rows followed by padding;
 // with v valid slots, DMA of 16-row groups at or past v is skipped, and a wave
@@ -94,41 +98,35 @@ __device__ __forceinline__ float x_sigmoid(float x, float k) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
-struct Frags {
-  uint4 x[2][4];  // [ks][j]: activation rows 128wm + 32j + l32
-  uint4 w[2][2];  // [ks][i]: weight rows wrow_t[i] + l32
+// Fragments of one 16-element K step: 4 activation tiles (rows 128 wm + 32 j
+// + l32) and 2 weight tiles.
+struct Frag {
+  uint4 x[4];
+  uint4 w[2];
 };
 
-// One K stage of one wave: read its fragments, then NJ/32 x 2 x 2 MFMAs with
-// the next-next-next stage's DMA instructions spread between them.
 template <int NJ>
-__device__ __forceinline__ void stage_compute(f32x16 (&acc)[2][4], const uint8_t* As,
-                                              const uint8_t* Ws, const int (&xoff)[2][4],
-                                              const int (&woff)[2][2], bool dma,
-                                              const uint8_t* const (&src)[DMA_PER_WAVE],
-                                              int64_t koff, uint32_t dst_base, int nd) {
-  Frags f;
+__device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, const int (&xoff)[4],
+                                          const int (&woff)[2]) {
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int j = 0; j < NJ; ++j) f.x[j] = *reinterpret_cast<const uint4*>(S + xoff[j]);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) f.x[ks][j] = *reinterpret_cast<const uint4*>(As + xoff[ks][j]);
+  for (int i = 0; i < 2; ++i) f.w[i] = *reinterpret_cast<const uint4*>(S + woff[i]);
+}
+
+// 2 x NJ MFMAs of one K step; with `dma`, the step's DMA instructions q0 and
+// q0 + 1 go out between its two MFMA groups and after them.
+template <int NJ>
+__device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][4], const Frag& f, bool dma,
+                                          const uint8_t* const (&src)[DMA_PER_WAVE],
+                                          int64_t koff, uint32_t dst_base, int nd, int q0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) f.w[ks][i] = *reinterpret_cast<const uint4*>(Ws + woff[ks][i]);
-  }
-  // 4 groups of MFMAs, one DMA instruction after each
+  for (int i = 0; i < 2; ++i) {
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int ks = g >> 1;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      if ((g & 1) == i || NJ == 0) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(f.w[ks][i], f.x[ks][j], acc[i][j]);
-      }
-    }
+    for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(f.w[i], f.x[j], acc[i][j]);
     __builtin_amdgcn_sched_barrier(0);
-    if (dma && g < nd)
-      dma16(src[g] + koff, __builtin_amdgcn_readfirstlane(dst_base + g * 1024));
+    const int q = q0 + i;
+    if (dma && q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(dst_base + q * 1024));
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -254,20 +252,41 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   };
   for (int s = 0; s < 3 && s < nk; ++s) issue_all(s);
 
-  // one K loop per MFMA row count (a loop body with a run-time choice of
-  // variant needs more than the 256 registers two waves per SIMD leave)
+  // K loop.  Stage kt's fragments are in registers when iteration kt starts;
+  // its first K step runs, then the barrier publishes stage kt+1 and its
+  // fragment reads go out while the second K step's MFMAs run.  Stage kt-1
+  // was consumed by every wave before that barrier, so the DMA of stage kt+3
+  // into its slot is issued after it.
   auto kloop = [&](auto nj_c) {
     constexpr int NJ = decltype(nj_c)::value;
-    for (int kt = 0; kt < nk; ++kt) {
-      // stage kt landed for this wave; later stages issued so far may pend
-      const int later = (nk - 1 - kt) < 2 ? (nk - 1 - kt) : 2;
-      wait_vm_dyn(nd * later);
+    Frag f0, f1;
+    {
+      wait_vm_dyn(nd * ((nk - 1) < 2 ? (nk - 1) : 2));
       __builtin_amdgcn_s_barrier();
-      const uint8_t* As = lds + (kt % NSTAGE) * STAGE;
+      read_frag<NJ>(f0, lds, xoff[0], woff[0]);
+      read_frag<NJ>(f1, lds, xoff[1], woff[1]);
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+      mfma_step<NJ>(acc, f0, false, src, 0, 0, 0, 0);
+      const bool more = kt + 1 < nk;
+      if (more) {
+        // stage kt+1 landed; stage kt+2 (if issued) may pend
+        wait_vm_dyn(kt + 2 < nk ? nd : 0);
+        __builtin_amdgcn_s_barrier();
+        read_frag<NJ>(f0, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[0], woff[0]);
+      }
       const bool dma = kt + 3 < nk;
       const int64_t koff = static_cast<int64_t>(kt + 3) * ROWB;
       const uint32_t dbase = ring0 + ((kt + 3) % NSTAGE) * STAGE + dst0;
-      stage_compute<NJ>(acc, As, As, xoff, woff, dma, src, koff, dbase, nd);
+      mfma_step<NJ>(acc, f1, dma, src, koff, dbase, nd, 0);
+      if (dma && nd > 2) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 2; q < DMA_PER_WAVE; ++q)
+          if (q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(dbase + q * 1024));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (more) read_frag<NJ>(f1, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[1], woff[1]);
     }
   };
   if (nj == 4)
