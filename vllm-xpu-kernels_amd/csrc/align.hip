@@ -69,7 +69,8 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
     int32_t* __restrict__ sorted_ids, int64_t max_padded,
     int32_t* __restrict__ expert_ids, int64_t max_blocks,
     int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
-    int32_t* __restrict__ counts_out, int32_t pad_value) {
+    int32_t* __restrict__ counts_out, int32_t* __restrict__ cum_out,
+    int32_t pad_value) {
   __shared__ int s_cnt[kSortWaves][kMaxKeys];
   __shared__ int s_cum[kMaxKeys + 1];
   __shared__ int s_wave_tot[kSortWaves];
@@ -111,10 +112,12 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
     s_cum[tid] = start;
     for (int w = 0; w < kSortWaves; ++w) s_cnt[w][tid] += start;
     if (counts_out) counts_out[tid] = total_e;
+    if (cum_out) cum_out[tid] = start;
   }
   if (tid == 0) {
     s_cum[num_keys] = total_padded;
     if (ntp) ntp[0] = total_padded;
+    if (cum_out) cum_out[num_keys] = total_padded;
   }
   __syncthreads();
 
@@ -212,7 +215,8 @@ __global__ __launch_bounds__(256) void chunk_count_kernel(
 __global__ __launch_bounds__(kSortThreads) void chunk_scan_kernel(
     int32_t* __restrict__ cnt, int nchunks, int num_keys, int block_size,
     int32_t* __restrict__ cum, int32_t* __restrict__ tot,
-    int32_t* __restrict__ ntp, int32_t* __restrict__ counts_out) {
+    int32_t* __restrict__ ntp, int32_t* __restrict__ counts_out,
+    int32_t* __restrict__ cum_out) {
   __shared__ int s_wave_tot[kSortWaves];
   const int tid = threadIdx.x;
   int total_e = 0;
@@ -237,10 +241,12 @@ __global__ __launch_bounds__(kSortThreads) void chunk_scan_kernel(
     cum[tid] = start;
     tot[tid] = total_e;
     if (counts_out) counts_out[tid] = total_e;
+    if (cum_out) cum_out[tid] = start;
   }
   if (tid == 0) {
     cum[num_keys] = total_padded;
     if (ntp) ntp[0] = total_padded;
+    if (cum_out) cum_out[num_keys] = total_padded;
   }
 }
 
@@ -350,7 +356,7 @@ __global__ __launch_bounds__(kSortThreads) void segments_to_blocks_kernel(
     const int32_t* __restrict__ rows, int num_keys, int block_size,
     int32_t* __restrict__ row_ids, int64_t max_padded,
     int32_t* __restrict__ expert_ids, int64_t max_blocks,
-    int32_t* __restrict__ ntp, int32_t pad_value) {
+    int32_t* __restrict__ ntp, int32_t* __restrict__ cum_out, int32_t pad_value) {
   __shared__ int s_cum[kMaxKeys + 1];
   __shared__ int s_off[kMaxKeys + 1];
   __shared__ int s_wave_tot[kSortWaves];
@@ -363,11 +369,13 @@ __global__ __launch_bounds__(kSortThreads) void segments_to_blocks_kernel(
   if (tid < num_keys) {
     s_cum[tid] = start;
     s_off[tid] = roff;
+    if (cum_out) cum_out[tid] = start;
   }
   if (tid == 0) {
     s_cum[num_keys] = tp;
     s_off[num_keys] = tr;
     if (ntp) ntp[0] = tp;
+    if (cum_out) cum_out[num_keys] = tp;
   }
   __syncthreads();
   for (int64_t p = tid; p < max_padded; p += kSortThreads) {
@@ -433,13 +441,13 @@ template <typename Id>
 void launch_sort(const void* ids, int64_t numel, int64_t id_bound,
                  const int32_t* map, int num_keys, int bs, int32_t* sorted,
                  int64_t max_padded, int32_t* eids, int64_t max_blocks,
-                 int32_t* ntp, int32_t* inv, int32_t* counts, int32_t pad,
-                 int32_t* ws, hipStream_t st) {
+                 int32_t* ntp, int32_t* inv, int32_t* counts, int32_t* cum_out,
+                 int32_t pad, int32_t* ws, hipStream_t st) {
   const Id* id = static_cast<const Id*>(ids);
   if (!ws) {
     counting_sort_kernel<Id><<<1, kSortThreads, 0, st>>>(
         id, numel, id_bound, map, num_keys, bs, sorted, max_padded, eids,
-        max_blocks, ntp, inv, counts, pad);
+        max_blocks, ntp, inv, counts, cum_out, pad);
     return;
   }
   const int64_t chunk = sort_chunk(numel);
@@ -450,7 +458,7 @@ void launch_sort(const void* ids, int64_t numel, int64_t id_bound,
   chunk_count_kernel<Id><<<nchunks, 256, 0, st>>>(id, numel, id_bound, map,
                                                    num_keys, chunk, cnt);
   chunk_scan_kernel<<<1, kSortThreads, 0, st>>>(cnt, nchunks, num_keys, bs, cum,
-                                                tot, ntp, counts);
+                                                tot, ntp, counts, cum_out);
   chunk_scatter_kernel<Id><<<nchunks, 256, 0, st>>>(
       id, numel, id_bound, map, num_keys, chunk, cnt, cum, tot, bs, sorted,
       max_padded, eids, max_blocks, inv, pad);
@@ -472,7 +480,7 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t bs, int32_t* sorted, int64_t max_padded,
                       int32_t* eids, int64_t max_blocks, int32_t* ntp,
                       int32_t* inv, int32_t* counts, int32_t pad,
-                      void* ws, size_t ws_bytes, hipStream_t st) {
+                      void* ws, size_t ws_bytes, hipStream_t st, int32_t* cum_out) {
   MI_ARG(num_keys > 0 && num_keys <= kMaxKeys,
          "padded_num_experts must be less than 1024");
   MI_ARG(bs > 0, "block_size must be positive");
@@ -481,13 +489,13 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
   int32_t* w = (need > 0 && ws && ws_bytes >= need) ? static_cast<int32_t*>(ws) : nullptr;
   switch (ids_dtype) {
     case MI355MOE_I32:
-      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, w, st);
+      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st);
       break;
     case MI355MOE_I64:
-      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, w, st);
+      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st);
       break;
     case MI355MOE_U32:
-      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, pad, w, st);
+      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st);
       break;
     default:
       return set_error(MI355MOE_ERR_INVALID, "topk_ids must be int32, int64 or uint32");
@@ -499,11 +507,11 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
 int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
                            int32_t* row_ids, int64_t max_padded,
                            int32_t* eids, int64_t max_blocks, int32_t* ntp,
-                           int32_t pad, hipStream_t st) {
+                           int32_t pad, hipStream_t st, int32_t* cum_out) {
   MI_ARG(num_keys > 0 && num_keys <= kMaxKeys, "num_experts must be in [1, 1024]");
   hipLaunchKernelGGL(segments_to_blocks_kernel, dim3(1), dim3(kSortThreads), 0,
                      st, rows, (int)num_keys, (int)bs, row_ids, max_padded,
-                     eids, max_blocks, ntp, pad);
+                     eids, max_blocks, ntp, cum_out, pad);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }
@@ -530,7 +538,8 @@ extern "C" int mi355moe_moe_align_block_size(
                            num_experts, block_size, sorted_token_ids,
                            max_num_tokens_padded, expert_ids, max_num_m_blocks,
                            ntp, nullptr, nullptr, static_cast<int32_t>(numel),
-                           workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                           workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                           nullptr);
 }
 
 extern "C" size_t mi355moe_remap_hidden_states_workspace_size(int64_t num_tokens,
@@ -556,7 +565,7 @@ extern "C" int mi355moe_remap_hidden_states(
   int rc = run_counting_sort(topk_ids, ids_dtype, slots, total_experts,
                              expert_map, local_experts, 1, nullptr, 0, nullptr,
                              0, nullptr, perm, rows_per_expert, 0, workspace,
-                             workspace_bytes, st);
+                             workspace_bytes, st, nullptr);
   if (rc) return rc;
   hipLaunchKernelGGL(remap_copy_kernel, dim3(static_cast<unsigned>(slots)),
                      dim3(256), 0, st, static_cast<const uint8_t*>(hidden),

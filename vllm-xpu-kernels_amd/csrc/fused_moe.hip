@@ -100,6 +100,7 @@ struct FusedLayout {
   GemmTile tile;
   int64_t slots, max_padded, max_blocks, grid_blocks;
   int32_t *sorted, *eids, *ntp;
+  int32_t* cum;     // [E+1] padded slot start of every expert
   int32_t* sortws;  // multi-workgroup sort scratch (sortws_bytes, may be 0)
   size_t sortws_bytes;
   uint8_t* xq;    // fp8 hidden [T, H]
@@ -121,6 +122,7 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   L.sorted = c.take<int32_t>(std::max<int64_t>(L.max_padded, 1));
   L.eids = c.take<int32_t>(std::max<int64_t>(L.max_blocks, 1));
   L.ntp = c.take<int32_t>(1);
+  L.cum = c.take<int32_t>(E + 1);
   L.sortws_bytes = counting_sort_ws_bytes(L.slots, E);
   L.sortws = c.take<int32_t>(static_cast<int64_t>(L.sortws_bytes / sizeof(int32_t)));
   const bool fp8 = a->recipe == MI355MOE_RECIPE_FP8BLOCK;
@@ -244,7 +246,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   int rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
                              a->expert_map, E, L.bm, L.sorted, L.max_padded,
                              L.eids, L.max_blocks, L.ntp, nullptr, nullptr,
-                             static_cast<int32_t>(L.slots), L.sortws, L.sortws_bytes, st);
+                             static_cast<int32_t>(L.slots), L.sortws, L.sortws_bytes, st,
+                             L.cum);
   if (rc) return rc;
 
   const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
@@ -265,6 +268,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.row_ids = L.sorted;
   g1.block_expert = L.eids;
   g1.ntp = L.ntp;
+  g1.expert_cum = L.cum;
   g1.num_valid = static_cast<int32_t>(L.slots);
   g1.a_div = static_cast<int32_t>(k);
   g1.a_by_pos = 0;
@@ -291,6 +295,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.row_ids = L.sorted;
   g2.block_expert = L.eids;
   g2.ntp = L.ntp;
+  g2.expert_cum = L.cum;
   g2.num_valid = static_cast<int32_t>(L.slots);
   g2.a_div = 1;
   g2.a_by_pos = 1;
@@ -329,6 +334,7 @@ struct GGLayout {
   GemmTile tile;
   int64_t max_padded, max_blocks, grid_blocks;
   int32_t *rows, *eids, *ntp;
+  int32_t* cum;     // [E+1] padded row start of every expert
   uint8_t* aq;
   float* as;
   size_t bytes;
@@ -343,6 +349,7 @@ GGLayout gg_plan(int recipe, bool need_quant, int64_t M, int64_t K, int64_t E,
   L.rows = c.take<int32_t>(std::max<int64_t>(L.max_padded, 1));
   L.eids = c.take<int32_t>(std::max<int64_t>(L.max_blocks, 1));
   L.ntp = c.take<int32_t>(1);
+  L.cum = c.take<int32_t>(E + 1);
   if (need_quant) {
     L.aq = c.take<uint8_t>(M * K);
     L.as = c.take<float>(M * (K / 128));
@@ -406,7 +413,7 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
   hipStream_t st = static_cast<hipStream_t>(stream);
   int rc = run_segments_to_blocks(rows_per_expert, E, L.bm, L.rows, L.max_padded,
                                   L.eids, L.max_blocks, L.ntp,
-                                  static_cast<int32_t>(M), st);
+                                  static_cast<int32_t>(M), st, L.cum);
   if (rc) return rc;
   const void* Aq = A;
   const float* As = a_scale;
@@ -427,6 +434,7 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
   g.row_ids = L.rows;
   g.block_expert = L.eids;
   g.ntp = L.ntp;
+  g.expert_cum = L.cum;
   g.num_valid = static_cast<int32_t>(M);
   g.a_div = 1;
   g.N = N;

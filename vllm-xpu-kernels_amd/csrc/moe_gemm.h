@@ -23,6 +23,7 @@ struct GemmArgs {
   const int32_t* row_ids;
   const int32_t* block_expert;
   const int32_t* ntp;    // [1] number of valid padded slots
+  const int32_t* expert_cum;  // [E+1] padded slot start per expert, or null
   int32_t num_valid;
   int32_t a_div;
   int32_t a_by_pos;
@@ -39,6 +40,26 @@ struct GemmArgs {
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };
+
+// Tile t of the (block, N-tile) grid.  With expert_cum the order is (expert,
+// N-tile, block): the blocks of one expert take the same weight rows back
+// to back, so they share them in L2 instead of each streaming them from
+// HBM; without it, row-major (block, N-tile).
+__device__ __forceinline__ void tile_coords(const GemmArgs& a, int t, int n_tiles, int bm,
+                                            int& blk, int& nt) {
+  if (a.expert_cum) {
+    const int b0 = t / n_tiles;
+    const int e = a.block_expert[b0];
+    const int fb = a.expert_cum[e] / bm;
+    const int nb = a.expert_cum[e + 1] / bm - fb;
+    const int local = t - fb * n_tiles;
+    nt = local / nb;
+    blk = fb + local % nb;
+  } else {
+    blk = t / n_tiles;
+    nt = t % n_tiles;
+  }
+}
 
 // Launch over max_blocks M-blocks of bm rows.  bm in {16, 32, 64, 128}.
 int launch_moe_gemm(int recipe, int epi, int bm, const GemmArgs& a,
@@ -88,10 +109,11 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t bs, int32_t* sorted, int64_t max_padded,
                       int32_t* eids, int64_t max_blocks, int32_t* ntp,
                       int32_t* inv, int32_t* counts, int32_t pad,
-                      void* ws, size_t ws_bytes, hipStream_t st);
+                      void* ws, size_t ws_bytes, hipStream_t st,
+                      int32_t* cum_out = nullptr);
 int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
                            int32_t* row_ids, int64_t max_padded,
                            int32_t* eids, int64_t max_blocks, int32_t* ntp,
-                           int32_t pad, hipStream_t st);
+                           int32_t pad, hipStream_t st, int32_t* cum_out = nullptr);
 
 }  // namespace mi355

@@ -71,9 +71,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int l32 = lane & 31, h = lane >> 5;
   // XCD-aware tile order.  Workgroups are dealt round-robin to the 8 XCDs;
   // give XCD x the contiguous range [x*per, (x+1)*per) of the valid tiles
-  // (row-major over (M-block, N-tile)), so the N-tiles that share an M-block's
-  // activation rows and the M-blocks of one expert that share its weight
-  // tiles meet in the same L2.
+  // (ordered by tile_coords), so the tiles that share an expert's weight rows
+  // or a block's activation rows meet in the same L2.
   // The 1-D grid is a multiple of 8 and >= the tile upper bound, so every
   // XCD receives at least `per` workgroups.
   const int n_tiles = static_cast<int>((a.N + (kGlu ? 127 : BN - 1)) / (kGlu ? 128 : BN));
@@ -82,17 +81,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int per = (valid + 7) / 8;
   const int tile = (bid & 7) * per + (bid >> 3);
   if ((bid >> 3) >= per || tile >= valid) return;  // uniform
-  // Grouped order inside the range: for each N-tile, GM consecutive M-blocks
-  // (mostly one expert) run back to back, so a 1 MB weight slice is reused
-  // while it is still in L2, and the group's activation rows (GM x 0.5 MB)
-  // stay resident across the N-tiles.
-  constexpr int GM = 4;
-  const int mblocks = *a.ntp / BM;
-  const int g = tile / (GM * n_tiles);
-  const int rem = tile % (GM * n_tiles);
-  const int gm = (mblocks - g * GM) < GM ? (mblocks - g * GM) : GM;
-  const int blk = g * GM + rem % gm;
-  const int ntile = rem / gm;
+  int blk, ntile;
+  tile_coords(a, tile, n_tiles, BM, blk, ntile);
   const int e = a.block_expert[blk];
   const int64_t K = a.K;
   const int64_t N = a.N;

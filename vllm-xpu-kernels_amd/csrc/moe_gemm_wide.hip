@@ -145,9 +145,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   const int l32 = lane & 31, h = lane >> 5;
 
   // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
-  // XCD x takes the contiguous range [x*per, (x+1)*per) of the valid tiles,
-  // ordered (M-block, N-tile), so the N-tiles sharing a block's activation
-  // rows and the blocks of one expert sharing its weight rows meet in one L2.
+  // XCD x takes the contiguous range [x*per, (x+1)*per) of the valid tiles
+  // (ordered by tile_coords), so the tiles sharing an expert's weight rows or
+  // a block's activation rows meet in one L2.
   // The grid is a multiple of 8 and at least the tile upper bound.
   const int n_tiles = static_cast<int>((a.N + NOUT - 1) / NOUT);
   const int valid = (*a.ntp / BM) * n_tiles;
@@ -155,8 +155,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   const int per = (valid + 7) / 8;
   const int tile = (bid & 7) * per + (bid >> 3);
   if ((bid >> 3) >= per || tile >= valid) return;  // uniform
-  const int blk = tile / n_tiles;
-  const int ntile = tile % n_tiles;
+  int blk, ntile;
+  tile_coords(a, tile, n_tiles, BM, blk, ntile);
   const int e = a.block_expert[blk];
   const int64_t K = a.K, N = a.N;
   const int64_t n0 = static_cast<int64_t>(ntile) * NOUT;
