@@ -76,8 +76,9 @@ int pick_block_m(int64_t slots, int64_t num_experts);
 //           BIG:    otherwise, 128x256 LDS-staged tiles, 128-slot blocks
 // MI355MOE_GEMM_TILE=stream|small|big|bigreg|wide overrides (A/B
 // measurements; wide falls back to big where it does not apply).
-// (TILE_BIG runs the LDS-DMA pipelined kernel where pipe_supported(),
-// TILE_BIGREG forces the register-staged one.)
+// (TILE_BIG runs the 8-wave fp8 kernel where wide8_supported(), else the
+// LDS-DMA pipelined kernel where pipe_supported(); TILE_BIGREG forces the
+// register-staged one.)
 enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3, TILE_WIDE = 4 };
 GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm);
 
@@ -95,6 +96,11 @@ int launch_moe_gemm_big(int recipe, int epi, bool qout, const GemmArgs& a,
 bool pipe_supported(int recipe, const GemmArgs& a);
 int launch_moe_gemm_pipe(int recipe, int epi, bool qout, const GemmArgs& a,
                          int64_t max_blocks, void* qs, hipStream_t st);
+// 128-slot blocks, fp8 block-scaled weights, K % 128 == 0, K <= 8192
+// (moe_gemm_wide8.hip).
+bool wide8_supported(int recipe, const GemmArgs& a);
+int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
+                          int64_t max_blocks, void* qs, hipStream_t st);
 // 256-slot blocks, bf16 weights, K % 32 == 0 (moe_gemm_wide.hip).
 bool wide_supported(int recipe, const GemmArgs& a);
 int launch_moe_gemm_wide(int recipe, int epi, const GemmArgs& a,

@@ -375,6 +375,8 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:
+      if (wide8_supported(recipe, a) && getenv("MI355MOE_FP8_PIPE") == nullptr)
+        return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
       if (pipe_supported(recipe, a))
         return launch_moe_gemm_pipe(recipe, epi, qout, a, max_blocks, qs, st);
       return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
