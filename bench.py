@@ -193,25 +193,44 @@ def summarize(pt, ms, stages):
     return d
 
 
-def kernel_roofline(pt, stages):
+def measured_traffic(key, stage):
+    """HBM bytes per launch of a GEMM stage from the committed rocprofv3
+    summaries (profiles/*.txt lines "traffic[<config> T=<tokens> <stage>] = N":
+    FETCH_SIZE and WRITE_SIZE of separate --pmc runs, each scaled by what the
+    counter reads for a plain copy of known size); None when no summary covers
+    this workload."""
+    import glob
+    import re
+    pat = re.compile(r"^traffic\[" + re.escape(f"{key} {stage}") + r"\] = (\d+)")
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.txt"))):
+        with open(path) as fh:
+            for line in fh:
+                m = pat.match(line)
+                if m:
+                    return int(m.group(1))
+    return None
+
+
+def kernel_roofline(pt, stages, key):
     from vllm_xpu_kernels import capi
     from vllm_xpu_kernels import workloads as W
     names = capi.STAGE_NAMES
     gi = max((2, 3), key=lambda i: stages[i])
     name = names[gi]
     ms = stages[gi]
+    traffic = measured_traffic(key, name)
     b, f = gemm_work(pt.cfg, pt.T, pt.active, name)
     peak_tf = W.PEAK_TFLOPS[pt.cfg.recipe]
     t_h, t_m = b / 8e12, f / (peak_tf * 1e12)
     if t_h >= t_m:
         ach = b / (ms * 1e-3) / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(ach / 8000.0, 4), "traffic": None, "kernel": name,
+                "frac": round(ach / 8000.0, 4), "traffic": traffic, "kernel": name,
                 "bytes_per_launch": int(b), "flops_per_launch": int(f),
                 "ms_per_launch": round(ms, 5)}
     ach = f / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "achieved": round(ach, 2), "peak": peak_tf, "unit": "TFLOP/s",
-            "frac": round(ach / peak_tf, 4), "traffic": None, "kernel": name,
+            "frac": round(ach / peak_tf, 4), "traffic": traffic, "kernel": name,
             "bytes_per_launch": int(b), "flops_per_launch": int(f),
             "ms_per_launch": round(ms, 5)}
 
@@ -265,7 +284,7 @@ def main():
     stages = pt.stage_times(args.steps)
     head = summarize(pt, ms, stages)
     log("headline:", json.dumps(head))
-    roof = kernel_roofline(pt, stages)
+    roof = kernel_roofline(pt, stages, f"{args.config} T={args.tokens}")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
@@ -292,7 +311,7 @@ def main():
             m = p.time_steps(args.steps, args.warmup, graph)
             st = p.stage_times(args.steps)
             d = summarize(p, m, st)
-            d["kernel_roofline"] = kernel_roofline(p, st)
+            d["kernel_roofline"] = kernel_roofline(p, st, f"{name} T={T}")
             log("sweep:", json.dumps(d))
             sweep.append(d)
             del p
