@@ -209,11 +209,15 @@ def test_fused_moe_c5_gpt_oss_mxfp4_swigluoai(dev, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
 
 
-def test_fused_moe_deterministic(dev):
-    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C2"], 256, dev)
-    again = torch.empty_like(out)
-    moe.apply(again, x, tw, ti)
-    assert torch.equal(out, again)
+@pytest.mark.parametrize("name,T", [("C2", 256), ("C2", 1), ("C3", 1)])
+def test_fused_moe_deterministic(dev, name, T):
+    """Bit-identical repeats; at T=1 the decode GEMMs split K over workgroups
+    and a second launch sums the partial tiles in a fixed order."""
+    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS[name], T, dev)
+    for _ in range(3):
+        again = torch.empty_like(out)
+        moe.apply(again, x, tw, ti)
+        assert torch.equal(out, again)
 
 
 def test_fused_moe_expert_map(dev):
@@ -319,10 +323,12 @@ def test_fused_moe_prefill_full_size_sampled(dev, name, T, sample):
     _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks), fp8=cfg.recipe == "fp8block")
 
 
-def test_fused_moe_hip_graph_replays(dev):
+@pytest.mark.parametrize("T", [64, 1])
+def test_fused_moe_hip_graph_replays(dev, T):
     """The layer captured in a HIP graph: every replay (with eager work and
-    synchronisation between replays) equals the eager result."""
-    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C2"], 64, dev)
+    synchronisation between replays) equals the eager result.  T=1 runs the
+    split-K decode GEMMs (split launch + partial-sum launch)."""
+    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C2"], T, dev)
     torch.cuda.synchronize()
     eager = out.clone()
     gout = torch.empty_like(out)

@@ -101,6 +101,8 @@ struct FusedLayout {
   int64_t slots, max_padded, max_blocks, grid_blocks;
   int32_t *sorted, *eids, *ntp;
   int32_t* cum;     // [E+1] padded slot start of every expert
+  int ks1, ks2;     // STREAM split-K of w13 / w2 (1: none)
+  float *part1, *part2;    // split-K partial tiles
   int32_t* sortws;  // multi-workgroup sort scratch (sortws_bytes, may be 0)
   size_t sortws_bytes;
   uint8_t* xq;    // fp8 hidden [T, H]
@@ -123,6 +125,17 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   L.eids = c.take<int32_t>(std::max<int64_t>(L.max_blocks, 1));
   L.ntp = c.take<int32_t>(1);
   L.cum = c.take<int32_t>(E + 1);
+  L.ks1 = L.ks2 = 1;
+  L.part1 = L.part2 = nullptr;
+  if (L.tile == TILE_STREAM) {
+    const int64_t act_blocks = std::min<int64_t>(L.slots, E);
+    const int64_t nt1 = cdiv(a->inter, 128), nt2 = cdiv(a->hidden, 256);
+    L.ks1 = stream_ksplit(nt1, act_blocks, a->hidden);
+    L.ks2 = stream_ksplit(nt2, act_blocks, a->inter);
+    const int64_t tile_f = 512 * 8;
+    if (L.ks1 > 1) L.part1 = c.take<float>(L.max_blocks * nt1 * L.ks1 * tile_f);
+    if (L.ks2 > 1) L.part2 = c.take<float>(L.max_blocks * nt2 * L.ks2 * tile_f);
+  }
   L.sortws_bytes = counting_sort_ws_bytes(L.slots, E);
   L.sortws = c.take<int32_t>(static_cast<int64_t>(L.sortws_bytes / sizeof(int32_t)));
   const bool fp8 = a->recipe == MI355MOE_RECIPE_FP8BLOCK;
@@ -281,6 +294,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.alpha = a->swiglu_alpha;
   g1.limit = a->swiglu_limit;
   g1.act = a->activation;
+  g1.ksplit = L.ks1;
+  g1.part = L.part1;
   rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
   if (rc) return rc;
   if (int m = mark(3)) return m;
@@ -304,6 +319,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.K = I;
   g2.ldb_rows = H;
   g2.up_off = 0;
+  g2.ksplit = L.ks2;
+  g2.part = L.part2;
   rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g2, L.grid_blocks, nullptr, st);
   if (rc) return rc;
   if (int m = mark(4)) return m;

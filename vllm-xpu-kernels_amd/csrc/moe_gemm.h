@@ -37,6 +37,14 @@ struct GemmArgs {
   float limit;           // swigluoai limit
   int32_t act;           // mi355moe_activation
   int32_t out_f16;       // store fp16 instead of bf16 (recipe BF16 only)
+  // STREAM family split-K: ksplit workgroups share one output tile, each
+  // summing 1/ksplit of the K stages into an fp32 partial tile in `part`; a
+  // second launch adds the partials in split order and runs the epilogue.
+  // (No workgroup waits for another: the per-XCD L2s are not coherent, so a
+  // device-scope fence would write back and invalidate a whole L2.)
+  int32_t ksplit;        // 0 or 1: no split
+  float* part;           // [blocks, n_tiles, ksplit, 512 x 8]
+  int32_t finalize;      // set by the launcher for the second launch
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };
@@ -117,6 +125,9 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int32_t* inv, int32_t* counts, int32_t pad,
                       void* ws, size_t ws_bytes, hipStream_t st,
                       int32_t* cum_out = nullptr);
+// K stages per split of the STREAM family for a GEMM of n_tiles output tiles
+// over about `blocks` expert blocks (1: no split)
+int stream_ksplit(int64_t n_tiles, int64_t blocks, int64_t K);
 int run_segments_to_blocks(const int32_t* rows, int64_t num_keys, int64_t bs,
                            int32_t* row_ids, int64_t max_padded,
                            int32_t* eids, int64_t max_blocks, int32_t* ntp,

@@ -63,7 +63,9 @@ template <>
 struct Frag<MI355MOE_RECIPE_FP8BLOCK> {  // 32 e4m3 of the weight row / act row
   uint4 w[2][2];
   uint4 x[2];
-  float xs;
+  float xs;     // activation scale of the 128-K block
+  float ws[2];  // weight-block scales, loaded with the stage (a load issued in
+                // the compute step would wait for every prefetched stage)
 };
 template <>
 struct Frag<MI355MOE_RECIPE_BF16> {      // 4 MFMA steps x 8 bf16
@@ -128,6 +130,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   wsr[0] = (wrow[0] / 128);
   wsr[1] = (wrow[1] / 128);
 
+  const float* bsc = static_cast<const float*>(a.b_scale);
   auto load = [&](Frag<RECIPE>& f, int64_t k0) {
     const int64_t kb = K - k0;
     if constexpr (kFp8) {
@@ -141,6 +144,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       f.x[0] = xok ? *reinterpret_cast<const uint4*>(px) : make_uint4(0, 0, 0, 0);
       f.x[1] = xok ? *reinterpret_cast<const uint4*>(px + 16) : make_uint4(0, 0, 0, 0);
       f.xs = xok ? a.a_scale[static_cast<int64_t>(arow) * (K / 128) + k0 / 128] : 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        f.ws[t] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) * (K / 128) + k0 / 128];
     } else if constexpr (kFp4) {
       const bool in = 32 * q < kb;
 #pragma unroll
@@ -175,16 +181,13 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   f32x4 acc[2];
   acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
   acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float* bsc = static_cast<const float*>(a.b_scale);
 
   auto compute = [&](const Frag<RECIPE>& f, int64_t k0) {
     if constexpr (kFp8) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const float ws = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) *
-                                 (K / 128) + k0 / 128];
         const f32x4 p = mma_fp8(f.w[t][0], f.w[t][1], f.x[0], f.x[1]);
-        acc[t] += p * (f.xs * ws);
+        acc[t] += p * (f.xs * f.ws[t]);
       }
     } else if constexpr (kFp4) {
 #pragma unroll
@@ -205,20 +208,42 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     }
   };
 
-  // ---- K loop, PD stages in flight
-  const int nk = static_cast<int>((K + KS - 1) / KS);
+  // ---- K loop over this split's stages [s0, s0 + nk), PD stages in flight
+  const int ks = a.ksplit > 1 ? a.ksplit : 1;
+  const int nk_all = static_cast<int>((K + KS - 1) / KS);
+  const int per = (nk_all + ks - 1) / ks;
+  const int s0 = static_cast<int>(blockIdx.z) * per;
+  const int nk = a.finalize ? 0 : ((nk_all - s0) < per ? (nk_all - s0) : per);
   Frag<RECIPE> buf[PD];
 #pragma unroll
   for (int d = 0; d < PD; ++d)
-    if (d < nk) load(buf[d], static_cast<int64_t>(d) * KS);
+    if (d < nk) load(buf[d], static_cast<int64_t>(s0 + d) * KS);
   for (int kt = 0; kt < nk; kt += PD) {
 #pragma unroll
     for (int d = 0; d < PD; ++d) {
       const int k = kt + d;
       if (k < nk) {
-        compute(buf[d], static_cast<int64_t>(k) * KS);
-        if (k + PD < nk) load(buf[d], static_cast<int64_t>(k + PD) * KS);
+        compute(buf[d], static_cast<int64_t>(s0 + k) * KS);
+        if (k + PD < nk) load(buf[d], static_cast<int64_t>(s0 + k + PD) * KS);
       }
+    }
+  }
+
+  // ---- split-K: the split launch leaves its partial tile; the finalize
+  //      launch sums the partials in split order (bit-reproducible)
+  if (ks > 1) {
+    const int64_t tile_id = static_cast<int64_t>(blk) * gridDim.x + blockIdx.x;
+    if (!a.finalize) {
+      float4* mine = reinterpret_cast<float4*>(a.part + (tile_id * ks + blockIdx.z) * (512 * 8)) + 2 * tid;
+      mine[0] = make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+      mine[1] = make_float4(acc[1][0], acc[1][1], acc[1][2], acc[1][3]);
+      return;
+    }
+    for (int z = 0; z < ks; ++z) {
+      const float4* p = reinterpret_cast<const float4*>(a.part + (tile_id * ks + z) * (512 * 8)) + 2 * tid;
+      const float4 v0 = p[0], v1 = p[1];
+      acc[0] += f32x4{v0.x, v0.y, v0.z, v0.w};
+      acc[1] += f32x4{v1.x, v1.y, v1.z, v1.w};
     }
   }
 
@@ -298,13 +323,37 @@ template <int RECIPE, int EPI, bool QOUT>
 int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
   constexpr int PD = RECIPE == MI355MOE_RECIPE_BF16 ? 2 : 4;
   const int64_t cols = EPI == EPI_GLU ? 128 : 256;
-  dim3 grid(static_cast<unsigned>(cdiv(a.N, cols)), static_cast<unsigned>(max_blocks));
-  moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(a, qs);
+  dim3 grid(static_cast<unsigned>(cdiv(a.N, cols)), static_cast<unsigned>(max_blocks),
+            static_cast<unsigned>(a.ksplit > 1 ? a.ksplit : 1));
+  GemmArgs g = a;
+  g.finalize = 0;
+  moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(g, qs);
   MI_LAUNCH_CHECK();
+  if (a.ksplit > 1) {  // sum the partial tiles and run the epilogue
+    grid.z = 1;
+    g.finalize = 1;
+    moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(g, qs);
+    MI_LAUNCH_CHECK();
+  }
   return MI355MOE_OK;
 }
 
 }  // namespace
+
+int stream_ksplit(int64_t n_tiles, int64_t blocks, int64_t K) {
+  // split only grids that leave most CUs idle (the partial-sum launch costs a
+  // few microseconds); then aim for about 512 workgroups (two per CU), at
+  // most 8 splits and at least two K stages per split
+  const int64_t wgs = n_tiles * (blocks > 0 ? blocks : 1);
+  if (wgs >= 192) return 1;
+  int64_t s = 512 / (wgs > 0 ? wgs : 1);
+  const int64_t nk = cdiv(K, KS);
+  if (s > 8) s = 8;
+  if (s > nk / 2) s = nk / 2;
+  if (s < 2) return 1;
+  const int64_t per = cdiv(nk, s);
+  return static_cast<int>(cdiv(nk, per));  // no empty split
+}
 
 // 16-slot blocks (the caller aligns expert segments to 16).
 int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
