@@ -131,49 +131,44 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   wsr[1] = (wrow[1] / 128);
 
   const float* bsc = static_cast<const float*>(a.b_scale);
+  const int64_t xsrow = static_cast<int64_t>(xok ? arow : 0) * (K / 128);
+  // Loads are unconditional and in bounds: rows past N and padding slots read
+  // row 0 (their outputs are never stored), the K tail re-reads the last
+  // chunk and compute() zeroes it.  A load under a condition would make the
+  // compiler wait for every prefetched stage where the branches join.
   auto load = [&](Frag<RECIPE>& f, int64_t k0) {
-    const int64_t kb = K - k0;
-    if constexpr (kFp8) {
+    if constexpr (kFp8) {  // K % 128 == 0: no tail
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint8_t* p = (t ? wp1 : wp0) + k0 + 32 * q;
-        f.w[t][0] = wok[t] ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
-        f.w[t][1] = wok[t] ? *reinterpret_cast<const uint4*>(p + 16) : make_uint4(0, 0, 0, 0);
+        f.w[t][0] = *reinterpret_cast<const uint4*>(p);
+        f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
+        f.ws[t] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) * (K / 128) + k0 / 128];
       }
       const uint8_t* px = xp + k0 + 32 * q;
-      f.x[0] = xok ? *reinterpret_cast<const uint4*>(px) : make_uint4(0, 0, 0, 0);
-      f.x[1] = xok ? *reinterpret_cast<const uint4*>(px + 16) : make_uint4(0, 0, 0, 0);
-      f.xs = xok ? a.a_scale[static_cast<int64_t>(arow) * (K / 128) + k0 / 128] : 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        f.ws[t] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) * (K / 128) + k0 / 128];
-    } else if constexpr (kFp4) {
-      const bool in = 32 * q < kb;
+      f.x[0] = *reinterpret_cast<const uint4*>(px);
+      f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
+      f.xs = a.a_scale[xsrow + k0 / 128];
+    } else if constexpr (kFp4) {  // K % 32 == 0
+      const int64_t k = k0 + 32 * q;
+      const int64_t kc = k < K ? k : K - 32;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const bool ok = wok[t] && in;
-        f.w[t] = ok ? *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + (k0 + 32 * q) / 2)
-                    : make_uint4(0, 0, 0, 0);
-        f.sc[t] = ok ? static_cast<const uint8_t*>(a.b_scale)
-                           [(static_cast<int64_t>(e) * a.ldb_rows + wrow[t]) * (K / 32) +
-                            (k0 + 32 * q) / 32]
-                     : 0u;
+        f.w[t] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + kc / 2);
+        f.sc[t] = static_cast<const uint8_t*>(a.b_scale)
+            [(static_cast<int64_t>(e) * a.ldb_rows + wrow[t]) * (K / 32) + kc / 32];
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        f.x[s] = (xok && in) ? *reinterpret_cast<const uint4*>(xp + (k0 + 32 * q + 8 * s) * 2)
-                             : make_uint4(0, 0, 0, 0);
-    } else {
+      for (int s = 0; s < 4; ++s) f.x[s] = *reinterpret_cast<const uint4*>(xp + (kc + 8 * s) * 2);
+    } else {  // K % 8 == 0
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bool in = 32 * s + 8 * q + 8 <= kb;
+        const int64_t k = k0 + 32 * s + 8 * q;
+        const int64_t kc = k + 8 <= K ? k : K - 8;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          f.w[t][s] = (wok[t] && in) ? *reinterpret_cast<const uint4*>(
-                                           (t ? wp1 : wp0) + (k0 + 32 * s + 8 * q) * 2)
-                                     : make_uint4(0, 0, 0, 0);
-        f.x[s] = (xok && in) ? *reinterpret_cast<const uint4*>(xp + (k0 + 32 * s + 8 * q) * 2)
-                             : make_uint4(0, 0, 0, 0);
+          f.w[t][s] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + kc * 2);
+        f.x[s] = *reinterpret_cast<const uint4*>(xp + kc * 2);
       }
     }
   };
@@ -182,7 +177,21 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
   acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const Frag<RECIPE>& f, int64_t k0) {
+  auto compute = [&](const Frag<RECIPE>& fin, int64_t k0) {
+    Frag<RECIPE> f = fin;
+    if (k0 + KS > K) {  // the last stage of a K that is not a multiple of 128
+      const uint4 z4 = make_uint4(0, 0, 0, 0);
+      if constexpr (kFp4) {
+        if (k0 + 32 * q >= K) {
+          f.w[0] = f.w[1] = z4;
+          f.sc[0] = f.sc[1] = 0u;
+        }
+      } else if constexpr (!kFp8) {
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+          if (k0 + 32 * s2 + 8 * q + 8 > K) f.w[0][s2] = f.w[1][s2] = z4;
+      }
+    }
     if constexpr (kFp8) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -215,10 +224,22 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const int s0 = static_cast<int>(blockIdx.z) * per;
   const int nk = a.finalize ? 0 : ((nk_all - s0) < per ? (nk_all - s0) : per);
   Frag<RECIPE> buf[PD];
+  if (nk > 0) {
 #pragma unroll
-  for (int d = 0; d < PD; ++d)
-    if (d < nk) load(buf[d], static_cast<int64_t>(s0 + d) * KS);
-  for (int kt = 0; kt < nk; kt += PD) {
+    for (int d = 0; d < PD; ++d)
+      load(buf[d], static_cast<int64_t>(s0 + (d < nk ? d : nk - 1)) * KS);
+  }
+  int kt = 0;
+  // main part: every prefetch is in range, so no load sits in a branch
+  for (; kt + 2 * PD <= nk; kt += PD) {
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+      compute(buf[d], static_cast<int64_t>(s0 + kt + d) * KS);
+      load(buf[d], static_cast<int64_t>(s0 + kt + d + PD) * KS);
+    }
+  }
+  // remainder: fewer than 2 PD stages
+  for (; kt < nk; kt += PD) {
 #pragma unroll
     for (int d = 0; d < PD; ++d) {
       const int k = kt + d;
