@@ -75,6 +75,12 @@ def test_version_and_error_plumbing(lib):
                                        ctypes.c_int64(256), ctypes.c_int64(2), None,
                                        ctypes.c_size_t(0), None),
      b"% 128"),
+    (lambda L: L.mi355moe_pack_weights_kb32(None, None, 1, ctypes.c_int64(2),
+                                            ctypes.c_int64(64), ctypes.c_int64(48), None),
+     b"K % 32 == 0"),
+    (lambda L: L.mi355moe_pack_weights_kb32(None, None, 6, ctypes.c_int64(2),
+                                            ctypes.c_int64(64), ctypes.c_int64(64), None),
+     b"16-bit"),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, call, msg):
     rc = call(lib)
@@ -97,7 +103,8 @@ def test_fused_moe_workspace_query_and_validation(lib):
                     ("w13_bias", ctypes.c_void_p), ("w2", ctypes.c_void_p),
                     ("w2_scale", ctypes.c_void_p), ("w2_bias", ctypes.c_void_p),
                     ("gemm1_clamp_limit", ctypes.c_float), ("swiglu_alpha", ctypes.c_float),
-                    ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p)]
+                    ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
+                    ("w_layout", ctypes.c_int)]
 
     a = Args(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=64,
              hidden=7168, inter=2048, num_experts=256, topk=8)
@@ -110,6 +117,17 @@ def test_fused_moe_workspace_query_and_validation(lib):
     a.hidden = 7168
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"need scales" in lib.mi355moe_last_error()
+    # the K-blocked layout is a bf16-only layout with K % 32 == 0
+    a.w_layout = 1
+    a.w13_scale = a.w2_scale = 1
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"K-blocked weights need the bf16 recipe" in lib.mi355moe_last_error()
+    a.recipe, a.hidden = 0, 7176
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"K-blocked weights need the bf16 recipe" in lib.mi355moe_last_error()
+    a.w_layout = 7
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"unknown weight layout" in lib.mi355moe_last_error()
 
 
 # schema strings as written in the reference's registration files

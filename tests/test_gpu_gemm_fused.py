@@ -313,6 +313,59 @@ def test_fused_moe_wide_tiles_ragged(dev, activation):
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
 
 
+# ------------------------------------------------- K-blocked bf16 weights
+@pytest.mark.parametrize("shape", [(3, 72, 96), (2, 768, 2048), (1, 8, 32)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pack_weights_kb32_layout(dev, shape, dtype):
+    """[E, N, K] -> [E, K/32, N, 32]: element (e, n, k) lands at
+    (e, k // 32, n, k % 32)."""
+    from vllm_xpu_kernels.fused_moe_interface import pack_weights_kb32
+    E, N, K = shape
+    g = torch.Generator().manual_seed(7)
+    w = torch.randn(E, N, K, generator=g).to(dtype)
+    out = pack_weights_kb32(w.to(dev)).cpu()
+    assert out.shape == (E, K // 32, N, 32)
+    e, n, k = (torch.randint(0, d, (4096,), generator=g) for d in (E, N, K))
+    assert torch.equal(out[e, k // 32, n, k % 32].view(torch.int16),
+                       w[e, n, k].view(torch.int16))
+    assert torch.equal(out.view(torch.int16),
+                       w.view(E, N, K // 32, 32).permute(0, 2, 1, 3).contiguous().view(torch.int16))
+
+
+def _layer_both_layouts(cfg, T, dev, monkeypatch):
+    monkeypatch.setenv("MI355MOE_WEIGHT_LAYOUT", "nk")
+    _, _, _, _, _, out_nk, moe_nk = _layer(cfg, T, dev)
+    monkeypatch.delenv("MI355MOE_WEIGHT_LAYOUT")
+    res = _layer(cfg, T, dev)
+    assert moe_nk._w_layout == 0 and res[6]._w_layout == 1
+    return res, out_nk
+
+
+@pytest.mark.parametrize("T", [1, 16, 256, 512, 1024, 2048])
+def test_fused_moe_kb32_equals_nk_c2(dev, monkeypatch, T):
+    """The K-blocked layout changes addresses only: every kernel family (T=1
+    split-K stream, 16/256 stream, 512/1024 small, 2048 wide) gives the
+    row-major layer's output bit for bit, and that output meets the oracle."""
+    (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(_W().CONFIGS["C2"], T, dev,
+                                                             monkeypatch)
+    assert torch.equal(out, out_nk)
+    toks = torch.linspace(0, T - 1, min(T, 8)).long().to(dev)
+    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks))
+
+
+@pytest.mark.parametrize("T", [8, 96, 160, 1024])
+@pytest.mark.parametrize("activation", ["silu", "swigluoai"])
+def test_fused_moe_kb32_ragged(dev, monkeypatch, activation, T):
+    """H=352 / I=224: K loops that end inside a 128-wide stage (stream,
+    small) and GLU tiles with rows past I, over the K-blocked weights."""
+    import dataclasses
+    base = _W().CONFIGS["C5" if activation == "swigluoai" else "C2"]
+    cfg = dataclasses.replace(base, recipe="bf16", hidden=352, inter=224, experts=8, topk=2)
+    (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
+    assert torch.equal(out, out_nk)
+    _close(out, _oracle_layer(cfg, w, x, tw, ti))
+
+
 @pytest.mark.parametrize("name,T,sample", [("C2", 4096, 24), ("C3", 8192, 6),
                                            ("C4", 2048, 12), ("C5", 4096, 12)])
 def test_fused_moe_prefill_full_size_sampled(dev, name, T, sample):

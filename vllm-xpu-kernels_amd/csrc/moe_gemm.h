@@ -37,6 +37,11 @@ struct GemmArgs {
   float limit;           // swigluoai limit
   int32_t act;           // mi355moe_activation
   int32_t out_f16;       // store fp16 instead of bf16 (recipe BF16 only)
+  // Weight layout (recipe BF16): 0 row-major [E, ldb_rows, K]; 1 K-blocked
+  // [E, K/32, ldb_rows, 32] (K % 32 == 0), in which the 64-byte K-slices
+  // of consecutive weight rows are contiguous, so a 16-row fragment of one
+  // K-block is a single 1 KiB run of HBM instead of 16 runs of 64 bytes.
+  int32_t w_kblock;
   // STREAM family split-K: ksplit workgroups share one output tile, each
   // summing 1/ksplit of the K stages into an fp32 partial tile in `part`; a
   // second launch adds the partials in split order and runs the epilogue.
@@ -48,6 +53,20 @@ struct GemmArgs {
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };
+
+// Byte strides of 16-bit weights: element (row r, k) of one expert sits at
+// r * row + (k / 32) * kblk + (k % 32) * 2 (row-major: row = 2K, kblk = 64;
+// K-blocked: row = 64, kblk = 64 ldb_rows).  An expert spans 2 K ldb_rows
+// bytes in both layouts.
+struct WStride {
+  int64_t row, kblk;
+};
+__device__ __forceinline__ WStride w_stride16(const GemmArgs& a) {
+  return a.w_kblock ? WStride{64, a.ldb_rows * 64} : WStride{a.K * 2, 64};
+}
+__device__ __forceinline__ int64_t w_koff16(const WStride& s, int64_t k) {
+  return (k >> 5) * s.kblk + (k & 31) * 2;
+}
 
 // Tile t of the (block, N-tile) grid.  With expert_cum the order is (expert,
 // N-tile, block): the blocks of one expert take the same weight rows back

@@ -117,6 +117,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
   const int64_t nbase = static_cast<int64_t>(blockIdx.x) * BN + wave * WN;
   const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
+  // 16-bit weights may be K-blocked; fp8 and mxfp4 weights are row-major
+  const WStride wst = kFp8 || kFp4 ? WStride{wrow_bytes, 0} : w_stride16(a);
   const uint8_t* wptr[NB];
   bool wok[NB];
   int64_t wrow[NB];
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
     const int64_t n = nbase + (j % NT) * 16 + l16;
     wok[j] = n < a.N;
     wrow[j] = (j >= NT ? a.up_off : 0) + (wok[j] ? n : 0);
-    wptr[j] = wbase + wrow[j] * wrow_bytes;
+    wptr[j] = wbase + wrow[j] * wst.row;
   }
 
   f32x4 acc[MT][NB];
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
         for (int s = 0; s < KS; ++s) {
           const bool ok = wok[j] && 32 * s + 8 * q + 8 <= kb;
           wf[s][j][0] = ok ? *reinterpret_cast<const uint4*>(
-                                 wptr[j] + (k0 + 32 * s + 8 * q) * 2)
+                                 wptr[j] + w_koff16(wst, k0 + 32 * s + 8 * q))
                            : make_uint4(0, 0, 0, 0);
         }
       }
@@ -372,6 +374,10 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
 int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
                      const GemmArgs& a, int64_t max_blocks, void* qs,
                      hipStream_t st) {
+  MI_ARG(!a.w_kblock || (recipe == MI355MOE_RECIPE_BF16 && a.K % 32 == 0 &&
+                         (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE)),
+         "K-blocked weights need the bf16 recipe, K % 32 == 0 and the stream, "
+         "small or wide tile");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:

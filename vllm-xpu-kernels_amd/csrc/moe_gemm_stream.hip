@@ -119,8 +119,10 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     wok[t] = n < N;
     wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
   }
-  const uint8_t* wp0 = wexp + wrow[0] * wrow_bytes;
-  const uint8_t* wp1 = wexp + wrow[1] * wrow_bytes;
+  // 16-bit weights may be K-blocked; fp8 and mxfp4 weights are row-major
+  const WStride wst = kFp8 || kFp4 ? WStride{wrow_bytes, 0} : w_stride16(a);
+  const uint8_t* wp0 = wexp + wrow[0] * wst.row;
+  const uint8_t* wp1 = wexp + wrow[1] * wst.row;
   const int arow = s_arow[l16];
   const bool xok = arow >= 0;
   const uint8_t* xp = static_cast<const uint8_t*>(a.A) +
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         const int64_t kc = k + 8 <= K ? k : K - 8;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          f.w[t][s] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + kc * 2);
+          f.w[t][s] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + w_koff16(wst, kc));
         f.x[s] = *reinterpret_cast<const uint4*>(xp + kc * 2);
       }
     }

@@ -188,6 +188,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   // for b < 16, weight rows after.  Padding-only activation groups are skipped.
   const uint8_t* src[DMA_PER_WAVE];
   int nd = 0;  // the used instructions are a prefix (A groups past v are a suffix)
+  // Waves 0-3 stage A rows, waves 4-7 weight rows (b = 4 wave + q): the
+  // bytes between two K stages of a wave's sources are uniform per wave.
+  const WStride wst = w_stride16(a);
+  const int64_t kstep = wave < 16 / DMA_PER_WAVE ? ROWB : wst.kblk;
   {
     const uint8_t* abase = static_cast<const uint8_t*>(a.A);
     const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
@@ -204,7 +208,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
         p = abase + static_cast<int64_t>(ar >= 0 ? ar : 0) * wrow_bytes + c * 16;
         use = (b & 15) * 16 < v;
       } else {
-        p = wexp + wrow_of(r) * wrow_bytes + c * 16;
+        p = wexp + wrow_of(r) * wst.row + c * 16;
       }
       src[q] = p;
       nd += use ? 1 : 0;
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   const int nk = static_cast<int>(K / KE);
   auto issue_all = [&](int kt) {
     const uint32_t base = ring0 + (kt % NSTAGE) * STAGE + dst0;
-    const int64_t koff = static_cast<int64_t>(kt) * ROWB;
+    const int64_t koff = static_cast<int64_t>(kt) * kstep;
 #pragma unroll
     for (int q = 0; q < DMA_PER_WAVE; ++q)
       if (q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(base + q * 1024));
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
         read_frag<NJ>(f0, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[0], woff[0]);
       }
       const bool dma = kt + 3 < nk;
-      const int64_t koff = static_cast<int64_t>(kt + 3) * ROWB;
+      const int64_t koff = static_cast<int64_t>(kt + 3) * kstep;
       const uint32_t dbase = ring0 + ((kt + 3) % NSTAGE) * STAGE + dst0;
       mfma_step<NJ>(acc, f1, dma, src, koff, dbase, nd, 0);
       if (dma && nd > 2) {

@@ -454,7 +454,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
                      const std::optional<at::Tensor>& w2_scale,
                      const std::optional<at::Tensor>& w2_bias, int64_t recipe,
                      int64_t activation, int64_t inter_size, double clamp_limit,
-                     const std::optional<at::Tensor>& expert_map) {
+                     const std::optional<at::Tensor>& expert_map, int64_t w_layout) {
   check_gpu(output, "output");
   check_gpu(hidden_states, "hidden_states");
   check_gpu(topk_weights, "topk_weights");
@@ -488,12 +488,29 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.swiglu_alpha = 1.702f;
   a.swiglu_limit = 7.0f;
   a.output = output.data_ptr();
+  a.w_layout = static_cast<int>(w_layout);
   const size_t ws_bytes = mi355moe_fused_moe_workspace_size(&a);
   auto ws = at::empty({static_cast<int64_t>(ws_bytes)},
                       hidden_states.options().dtype(at::kByte));
   DevGuard g(hidden_states.device());
   check_rc(mi355moe_fused_moe(&a, ws.data_ptr(), ws_bytes, cur_stream(hidden_states)),
            "fused_moe");
+}
+
+// Not a reference op: one-time K-blocked repacking of 16-bit [E, N, K]
+// weights into dst [E, K/32, N, 32] (XpuFusedMoe.__init__).
+void mi355_pack_weights_kb32(const at::Tensor& src, at::Tensor& dst) {
+  check_gpu(src, "src");
+  check_gpu(dst, "dst");
+  TORCH_CHECK(src.dim() == 3 && src.is_contiguous() && dst.is_contiguous(),
+              "src must be a contiguous [E, N, K] tensor");
+  TORCH_CHECK(dst.scalar_type() == src.scalar_type() && dst.numel() == src.numel(),
+              "dst must match src in dtype and size");
+  DevGuard g(src.device());
+  check_rc(mi355moe_pack_weights_kb32(src.data_ptr(), dst.data_ptr(),
+                                      dtype_code(src.scalar_type()), src.size(0),
+                                      src.size(1), src.size(2), cur_stream(src)),
+           "pack_weights_kb32");
 }
 
 }  // namespace
@@ -524,7 +541,8 @@ TORCH_LIBRARY(_moe_C, m) {
   m.def("mi355_fused_moe(Tensor! output, Tensor hidden_states, Tensor topk_weights, "
         "Tensor topk_ids, Tensor w13, Tensor? w13_scale, Tensor? w13_bias, Tensor w2, "
         "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
-        "inter_size, float clamp_limit, Tensor? expert_map) -> ()");
+        "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0) -> ()");
+  m.def("mi355_pack_weights_kb32(Tensor src, Tensor! dst) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
@@ -537,6 +555,7 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("init_expert_map", &init_expert_map);
   m.impl("remap_hidden_states", &remap_hidden_states);
   m.impl("mi355_fused_moe", &mi355_fused_moe);
+  m.impl("mi355_pack_weights_kb32", &mi355_pack_weights_kb32);
 }
 
 TORCH_LIBRARY_IMPL(_moe_C, Meta, m) { m.impl("grouped_topk", &grouped_topk_meta); }

@@ -31,7 +31,8 @@ class FusedMoeArgs(ctypes.Structure):
                 ("w2_scale", ctypes.c_void_p), ("w2_bias", ctypes.c_void_p),
                 ("gemm1_clamp_limit", ctypes.c_float),
                 ("swiglu_alpha", ctypes.c_float),
-                ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p)]
+                ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
+                ("w_layout", ctypes.c_int)]
 
 
 lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t
@@ -86,6 +87,7 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.swiglu_alpha = 1.702
     a.swiglu_limit = 7.0
     a.output = output.data_ptr()
+    a.w_layout = moe._w_layout
     return a
 
 

@@ -2,12 +2,15 @@
 
 ``XpuFusedMoe(...)`` keeps the reference constructor and ``apply`` signature
 (:165-181, :273-281).  At construction the weights are converted once into
-the layout the gfx950 kernels stream (every expert matrix [N, K] with K
-contiguous; swigluoai's interleaved gate/up rows split into a gate half and an
-up half) and the converted tensors are tagged so that a second
-``XpuFusedMoe`` over the same tensors does not convert again.  ``apply``
-makes one call, ``torch.ops._moe_C.mi355_fused_moe``, which launches the whole
-layer on the current stream without synchronising the host.
+the layout the gfx950 kernels stream: every expert matrix [N, K] with K
+contiguous, swigluoai's interleaved gate/up rows split into a gate half and an
+up half, and bf16 weights with K % 32 == 0 (hidden and intermediate sizes)
+further K-blocked to [E, K/32, N, 32] (``mi355_pack_weights_kb32``), so that
+the decode kernels read each 16-row weight fragment as one contiguous 1 KiB
+run.  ``MI355MOE_WEIGHT_LAYOUT=nk`` keeps the row-major [E, N, K] layout.
+``apply`` makes one call, ``torch.ops._moe_C.mi355_fused_moe``, which
+launches the whole layer on the current stream without synchronising the
+host.
 """
 from __future__ import annotations
 
@@ -23,6 +26,8 @@ FP8_BLOCK_SIZE = 128
 
 RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4 = 0, 1, 2
 ACT_SILU, ACT_SWIGLUOAI = 0, 1
+WLAYOUT_NK, WLAYOUT_KB32 = 0, 1
+WEIGHT_LAYOUT_ENV = "MI355MOE_WEIGHT_LAYOUT"
 
 
 def _is_env_enabled(env_name: str, default: str = "0") -> bool:
@@ -61,6 +66,14 @@ def _deinterleave_rows(t: torch.Tensor, dim: int) -> torch.Tensor:
         dim, torch.arange(0, t.shape[dim], 2, device=t.device))
     odd = t.index_select(dim, torch.arange(1, t.shape[dim], 2, device=t.device))
     return torch.cat([even, odd], dim=dim).contiguous()
+
+
+def pack_weights_kb32(w: torch.Tensor) -> torch.Tensor:
+    """16-bit [E, N, K] -> K-blocked [E, K/32, N, 32] on the device."""
+    E, N, K = w.shape
+    out = torch.empty((E, K // 32, N, 32), dtype=w.dtype, device=w.device)
+    torch.ops._moe_C.mi355_pack_weights_kb32(w.contiguous(), out)
+    return out
 
 
 class XpuFusedMoe:
@@ -166,10 +179,15 @@ class XpuFusedMoe:
             if b13c is not None:
                 b13c = _deinterleave_rows(b13c, 1)
         assert w13c.shape[0] == E and w13c.shape[1] == 2 * I
+        H = w13c.shape[2]
+        self._w_layout = WLAYOUT_NK
+        if (self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0 and
+                os.environ.get(WEIGHT_LAYOUT_ENV, "kb32").lower() != "nk"):
+            w13c, w2c = pack_weights_kb32(w13c), pack_weights_kb32(w2c)
+            self._w_layout = WLAYOUT_KB32
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
         self.w13_bias, self.w2_bias = b13c, b2c
-        self.w13._mi355_prepared = True
 
     # ------------------------------------------------------------------
     def apply(self, output, hidden_states, topk_weights, topk_ids,
@@ -185,7 +203,8 @@ class XpuFusedMoe:
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
             topk_ids.contiguous(), self.w13, self.gemm1_wei_scales,
             self.w13_bias, self.w2, self.gemm2_wei_scales, self.w2_bias,
-            self._recipe, self._act, self.inter_size, clamp, expert_map)
+            self._recipe, self._act, self.inter_size, clamp, expert_map,
+            self._w_layout)
         return output
 
 
