@@ -276,16 +276,17 @@ def test_grouped_gemm_big_tiles(dev, recipe):
     torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
-# ------------------------------------------- bf16 prefill (256x256) tiles
-WIDE_ROWS = [1, 31, 64, 65, 256, 513]
+# ------------------------------------------- bf16 prefill (320x256) tiles
+WIDE_ROWS = [1, 31, 33, 64, 97, 159, 160, 161, 255, 319, 320, 321, 700]
 
 
 @pytest.mark.parametrize("K", [32, 64, 96, 352])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_grouped_gemm_wide_tiles(dev, K, out_dtype):
-    """bf16 weights with >96 rows per expert select the 256x256 kernel.
-    Valid rows per 256-slot block 1..256 (empty and half-empty waves, skipped
-    DMA groups); K from one 32-element stage (shorter than the 3-deep
+    """bf16 weights with >96 rows per expert select the 320x256 kernel.
+    Valid rows per 320-slot block 1..320 (every count of 32-row MFMA groups
+    per wave half, 0..5, and of skipped 16-row DMA groups; experts of 1, 2
+    and 3 blocks); K from one 32-element stage (shorter than the 3-deep
     prefetch) to 11; N=200 is one ragged tile; bias; bf16 or fp16 output."""
     g = torch.Generator().manual_seed(K)
     E, N = len(WIDE_ROWS), 200
@@ -303,7 +304,7 @@ def test_grouped_gemm_wide_tiles(dev, K, out_dtype):
 
 @pytest.mark.parametrize("activation", ["silu", "swigluoai"])
 def test_fused_moe_wide_tiles_ragged(dev, activation):
-    """Whole bf16 layer through the 256x256 kernels (256 slots per expert on
+    """Whole bf16 layer through the 320x256 kernels (256 slots per expert on
     average): I=224 leaves a ragged GLU tile and a 7-stage w2 K loop, H=352
     an 11-stage w13 loop; swigluoai adds biases and the clamps."""
     import dataclasses

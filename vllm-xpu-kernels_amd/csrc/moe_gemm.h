@@ -98,8 +98,8 @@ int pick_block_m(int64_t slots, int64_t num_experts);
 // Kernel family by the expected rows per active expert:
 //   <= 24   STREAM: independent-wave weight streaming, 16-slot blocks
 //   <= 96   SMALL:  LDS-shared activation tile, 32/64-slot blocks
-//   >  96   WIDE:   bf16 weights with every K % 32 == 0 (wide_ok): 256x256
-//                   tiles, 256-slot blocks
+//   >  96   WIDE:   bf16 weights with every K % 32 == 0 (wide_ok): 320x256
+//                   tiles, 320-slot blocks (kWideBM)
 //           BIG:    otherwise, 128x256 LDS-staged tiles, 128-slot blocks
 // MI355MOE_GEMM_TILE=stream|small|big|bigreg|wide overrides (A/B
 // measurements; wide falls back to big where it does not apply).
@@ -107,6 +107,7 @@ int pick_block_m(int64_t slots, int64_t num_experts);
 // LDS-DMA pipelined kernel where pipe_supported(); TILE_BIGREG forces the
 // register-staged one.)
 enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3, TILE_WIDE = 4 };
+constexpr int kWideBM = 320;  // slots per block of the WIDE family
 GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm);
 
 // Launch the chosen family over max_blocks blocks of bm slots.
@@ -128,8 +129,11 @@ int launch_moe_gemm_pipe(int recipe, int epi, bool qout, const GemmArgs& a,
 bool wide8_supported(int recipe, const GemmArgs& a);
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
                           int64_t max_blocks, void* qs, hipStream_t st);
-// 256-slot blocks, bf16 weights, K % 32 == 0 (moe_gemm_wide.hip).
+// kWideBM-slot blocks, bf16 weights, K % 32 == 0 (moe_gemm_wide.hip).
 bool wide_supported(int recipe, const GemmArgs& a);
+// The WIDE family addresses activations and one expert's weights with 32-bit
+// byte offsets: a_rows x K and ldb_rows x K 16-bit elements must fit.
+bool wide_offsets_fit(int64_t a_rows, int64_t ldb_rows, int64_t K);
 int launch_moe_gemm_wide(int recipe, int epi, const GemmArgs& a,
                          int64_t max_blocks, hipStream_t st);
 // 16-slot blocks; GLU blocks cover 128 output columns, STORE blocks 256.

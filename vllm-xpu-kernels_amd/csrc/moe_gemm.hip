@@ -367,7 +367,7 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
   GemmTile t = m == 16 ? TILE_STREAM : (m == 128 ? (wide ? TILE_WIDE : TILE_BIG) : TILE_SMALL);
   if (force >= 0) t = static_cast<GemmTile>(force);
   if (t == TILE_WIDE && !wide) t = TILE_BIG;
-  *bm = t == TILE_STREAM ? 16 : (t == TILE_WIDE ? 256 : ((t == TILE_BIG || t == TILE_BIGREG) ? 128 : m));
+  *bm = t == TILE_STREAM ? 16 : (t == TILE_WIDE ? kWideBM : ((t == TILE_BIG || t == TILE_BIGREG) ? 128 : m));
   return t;
 }
 

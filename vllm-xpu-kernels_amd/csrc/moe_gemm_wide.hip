@@ -1,18 +1,23 @@
-// Prefill grouped GEMM for bf16 weights: 256-slot x 256-weight-row tiles,
+// Prefill grouped GEMM for bf16 weights: 320-slot x 256-weight-row tiles,
 // 8 waves, 4-slot LDS ring fed by direct global->LDS DMA.
 //
-// Why this shape.  Every K element of a tile moves (256 + 256) x 2 bytes from
-// L2 into LDS for 2 x 256 x 256 flops, half the bytes per flop of a 128 x 256
-// tile; the per-CU vector-memory path (about 64 B/clk) then needs ~32 B/clk
-// at full MFMA rate instead of ~48.  Two waves per SIMD (waves w and w + 4
-// share SIMD w % 4) let one wave's MFMAs cover the other's LDS latency, so no
-// register double buffering is needed and each wave keeps its 128 x 64
-// accumulator block (8 32x32 tiles, 128 registers) resident.
+// Why this shape.  A tile streams its expert's 256 weight rows over the whole
+// K once, so the weight bytes a layer moves into LDS are (tiles per expert) x
+// (weight bytes).  Routing spreads about n +- sqrt(n) slots over an expert, and
+// a 256-slot block at n = 256 leaves half the experts with a second, nearly
+// empty block that streams the weights a second time; 320 slots hold n + 4
+// sigma.  Compute and activation DMA scale with the valid rows only (empty
+// 32-row groups skip their MFMAs, empty 16-row groups their DMA).  Each K
+// element moves (320 + 256) x 2 bytes into LDS for 2 x 320 x 256 flops.  Two
+// waves per SIMD (waves w and w + 4 share SIMD w % 4) let one wave's MFMAs
+// cover the other's LDS latency; each wave keeps its 160 x 64 accumulator
+// block (10 32x32 tiles, 160 registers) resident.
 //
-// Layout.  A K stage holds 32 bf16 (64 bytes) of each of the 256 activation
-// rows and 256 weight rows: 32 KB, written by 32 global_load_lds_dwordx4 (16
+// Layout.  A K stage holds 32 bf16 (64 bytes) of each of the 320 activation
+// rows and 256 weight rows: 36 KB, written by 36 global_load_lds_dwordx4 (16
 // rows x 64 B each; lane l writes LDS bytes [16l, 16l + 16) of its 1 KB
-// block).  16-byte chunk c of row r sits at slot c ^ ((r >> 2) & 3): sixteen
+// block): waves 0-3 stage 5 activation blocks each, waves 4-7 4 weight blocks
+// each.  16-byte chunk c of row r sits at slot c ^ ((r >> 2) & 3): sixteen
 // consecutive rows read at one logical chunk then hit sixteen distinct 16-byte
 // bank groups.  A and W use the same K permutation, so the MFMA sums are
 // unchanged.
@@ -27,8 +32,7 @@
 //
 // Padding.  The slots of a block are its expert's rows followed by padding;
 // with v valid slots, DMA of 16-row groups at or past v is skipped, and a wave
-// whose 128 rows hold fewer than 65 (or no) valid slots runs the MFMAs of its
-// first 64 rows only (or none).
+// runs the MFMAs of its 32-row groups that hold valid slots only.
 #include <type_traits>
 
 #include "moe_gemm.h"
@@ -40,21 +44,37 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int BM = 256, BN = 256, ROWB = 64, KE = 32;
-constexpr int A_BYTES = BM * ROWB;             // 16 KB
-constexpr int STAGE = (BM + BN) * ROWB;        // 32 KB
+constexpr int MG = 5;                          // 32-row groups per wave
+constexpr int BM = 2 * 32 * MG, BN = 256, ROWB = 64, KE = 32;
+static_assert(BM == kWideBM, "block size of the WIDE family");
+constexpr int A_BYTES = BM * ROWB;             // 20 KB
+constexpr int STAGE = (BM + BN) * ROWB;        // 36 KB
 constexpr int NSTAGE = 4;
-constexpr int DMA_PER_WAVE = STAGE / 1024 / 8;  // 4
+constexpr int A_DMA = BM / 16 / 4;             // activation blocks per wave (waves 0-3)
+constexpr int W_DMA = BN / 16 / 4;             // weight blocks per wave (waves 4-7)
+constexpr int DMA_PER_WAVE = A_DMA > W_DMA ? A_DMA : W_DMA;
 constexpr int RING_BYTES = NSTAGE * STAGE;
-constexpr int EPI_PITCH_MAX = 2 * 256 + 16;     // bytes per staged output row
-constexpr int LDS_BYTES = RING_BYTES > BM * EPI_PITCH_MAX ? RING_BYTES : BM * EPI_PITCH_MAX;
+constexpr int LDS_BYTES = RING_BYTES;
+static_assert(BM * (2 * 128 + 16) <= RING_BYTES, "GLU output tile staged in one pass");
+static_assert(BM / 2 * (2 * 256 + 16) <= RING_BYTES, "STORE output tile staged in two passes");
 
 __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
 }
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(lds_base) : "memory");
+// 16 bytes per lane from sbase + voff (scalar base, 32-bit lane offset) into
+// LDS at lds_base + 16 lane.
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory");
+}
+// readfirstlane returns int: each half goes through uint32_t so that the low
+// half is zero-extended (a sign-extended low half with bit 31 set would fill
+// the high half with ones).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
+  return reinterpret_cast<const uint8_t*>((hi << 32) | lo);
 }
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -71,7 +91,9 @@ __device__ __forceinline__ void wait_vm_dyn(int n) {
     case 5: wait_vm<5>(); break;
     case 6: wait_vm<6>(); break;
     case 7: wait_vm<7>(); break;
-    default: wait_vm<8>(); break;
+    case 8: wait_vm<8>(); break;
+    case 9: wait_vm<9>(); break;
+    default: wait_vm<10>(); break;
   }
 }
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
@@ -98,35 +120,39 @@ __device__ __forceinline__ float x_sigmoid(float x, float k) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
-// Fragments of one 16-element K step: 4 activation tiles (rows 128 wm + 32 j
+// Fragments of one 16-element K step: MG activation tiles (rows 160 wm + 32 j
 // + l32) and 2 weight tiles.
 struct Frag {
-  uint4 x[4];
+  uint4 x[MG];
   uint4 w[2];
 };
 
+// The swizzle of rows r + 32 j equals that of r, so fragment j sits a
+// constant 32 x 64 bytes past fragment 0 (immediate offsets of one address).
+// Weight tile 1 sits `wstep` bytes past weight tile 0.
 template <int NJ>
-__device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, const int (&xoff)[4],
-                                          const int (&woff)[2]) {
+__device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, int xoff, int woff,
+                                          int wstep) {
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) f.x[j] = *reinterpret_cast<const uint4*>(S + xoff[j]);
+  for (int j = 0; j < NJ; ++j) f.x[j] = *reinterpret_cast<const uint4*>(S + xoff + j * 32 * ROWB);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) f.w[i] = *reinterpret_cast<const uint4*>(S + woff[i]);
+  for (int i = 0; i < 2; ++i) f.w[i] = *reinterpret_cast<const uint4*>(S + woff + i * wstep);
 }
 
 // 2 x NJ MFMAs of one K step; with `dma`, the step's DMA instructions q0 and
 // q0 + 1 go out between its two MFMA groups and after them.
 template <int NJ>
-__device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][4], const Frag& f, bool dma,
-                                          const uint8_t* const (&src)[DMA_PER_WAVE],
-                                          int64_t koff, uint32_t dst_base, int nd, int q0) {
+__device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][MG], const Frag& f, bool dma,
+                                          const uint32_t (&voff)[DMA_PER_WAVE],
+                                          const uint8_t* sbase, uint32_t dst_base, int nd,
+                                          int q0) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(f.w[i], f.x[j], acc[i][j]);
     __builtin_amdgcn_sched_barrier(0);
     const int q = q0 + i;
-    if (dma && q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(dst_base + q * 1024));
+    if (dma && q < nd) dma16(voff[q], sbase, __builtin_amdgcn_readfirstlane(dst_base + q * 1024));
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -140,7 +166,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
   const int wm = wave >> 2, wn = wave & 3;
   const int l32 = lane & 31, h = lane >> 5;
 
@@ -184,64 +211,63 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
     }
   };
 
-  // DMA instructions of this wave: blocks b = 4 wave + q of a stage, A rows
-  // for b < 16, weight rows after.  Padding-only activation groups are skipped.
-  const uint8_t* src[DMA_PER_WAVE];
-  int nd = 0;  // the used instructions are a prefix (A groups past v are a suffix)
-  // Waves 0-3 stage A rows, waves 4-7 weight rows (b = 4 wave + q): the
-  // bytes between two K stages of a wave's sources are uniform per wave.
+  // DMA instructions of this wave: waves 0-3 stage activation blocks
+  // A_DMA wave + q, waves 4-7 weight blocks W_DMA (wave - 4) + q (a block is
+  // 16 rows of a stage).  Activation blocks of padding only are skipped; the
+  // used instructions are a prefix of q.  The bytes between two K stages of a
+  // wave's sources are uniform per wave.
+  // Sources are a scalar base (the activation matrix or the expert's weights)
+  // plus 32-bit lane offsets (launch_moe_gemm_wide checks that both fit).
+  const bool a_wave = wave < 4;
   const WStride wst = w_stride16(a);
-  const int64_t kstep = wave < 16 / DMA_PER_WAVE ? ROWB : wst.kblk;
-  {
-    const uint8_t* abase = static_cast<const uint8_t*>(a.A);
-    const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
-                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
+  const int64_t kstep = a_wave ? ROWB : wst.kblk;
+  const uint8_t* sbase0 = uniform_ptr(
+      a_wave ? static_cast<const uint8_t*>(a.A)
+             : static_cast<const uint8_t*>(a.B) + static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes);
+  uint32_t voff[DMA_PER_WAVE];
+  int nd = 0;
 #pragma unroll
-    for (int q = 0; q < DMA_PER_WAVE; ++q) {
-      const int b = DMA_PER_WAVE * wave + q;
-      const int r = (b & 15) * 16 + (lane >> 2);
-      const int c = (lane & 3) ^ swz(r);
-      const uint8_t* p;
-      bool use = true;
-      if (b < 16) {
-        const int ar = s_arow[r];
-        p = abase + static_cast<int64_t>(ar >= 0 ? ar : 0) * wrow_bytes + c * 16;
-        use = (b & 15) * 16 < v;
-      } else {
-        p = wexp + wrow_of(r) * wst.row + c * 16;
-      }
-      src[q] = p;
-      nd += use ? 1 : 0;
+  for (int q = 0; q < DMA_PER_WAVE; ++q) {
+    int64_t o;
+    bool use;
+    if (a_wave) {
+      const int b = A_DMA * wave + (q < A_DMA ? q : 0);
+      const int r = b * 16 + (lane >> 2);
+      const int ar = s_arow[r];
+      o = static_cast<int64_t>(ar >= 0 ? ar : 0) * wrow_bytes + (((lane & 3) ^ swz(r)) << 4);
+      use = q < A_DMA && b * 16 < v;
+    } else {
+      const int b = W_DMA * (wave - 4) + (q < W_DMA ? q : 0);
+      const int r = b * 16 + (lane >> 2);
+      o = wrow_of(r) * wst.row + (((lane & 3) ^ swz(r)) << 4);
+      use = q < W_DMA;
     }
+    voff[q] = static_cast<uint32_t>(o);
+    nd += use ? 1 : 0;
   }
-  const uint32_t dst0 = DMA_PER_WAVE * wave * 1024;  // LDS block of src[0]
+  // LDS block of src[0]
+  const uint32_t dst0 = a_wave ? A_DMA * wave * 1024 : A_BYTES + W_DMA * (wave - 4) * 1024;
 
-  // per-wave MFMA rows: 128 wm + [0, 32 NJ)
-  const int vw = v - 128 * wm;
-  const int nj = vw > 64 ? 4 : (vw > 0 ? 2 : 0);
+  // per-wave MFMA rows: 160 wm + [0, 32 nj)
+  const int vw = v - 32 * MG * wm;
+  const int nj = vw <= 0 ? 0 : (vw >= 32 * MG ? MG : (vw + 31) / 32);
 
-  // fragment offsets within a stage: chunk c = 2 ks + h
-  int xoff[2][4], woff[2][2];
+  // fragment offsets within a stage: chunk c = 2 ks + h; every row this lane
+  // reads (l32 plus a multiple of 32) has the swizzle of l32
+  int xoff[2], woff[2];
+  constexpr int WSTEP = (kGlu ? 128 : 32) * ROWB;  // weight tile 1 - tile 0
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const int c = 2 * ks + h;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = 128 * wm + 32 * j + l32;
-      xoff[ks][j] = m * ROWB + ((c ^ swz(m)) << 4);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = (kGlu ? 128 * i + 32 * wn : 64 * wn + 32 * i) + l32;
-      woff[ks][i] = A_BYTES + r * ROWB + ((c ^ swz(r)) << 4);
-    }
+    const int c = (2 * ks + h) ^ swz(l32);
+    xoff[ks] = (32 * MG * wm + l32) * ROWB + (c << 4);
+    woff[ks] = A_BYTES + ((kGlu ? 32 * wn : 64 * wn) + l32) * ROWB + (c << 4);
   }
 
-  f32x16 acc[2][4];
+  f32x16 acc[2][MG];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < MG; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -249,10 +275,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   const int nk = static_cast<int>(K / KE);
   auto issue_all = [&](int kt) {
     const uint32_t base = ring0 + (kt % NSTAGE) * STAGE + dst0;
-    const int64_t koff = static_cast<int64_t>(kt) * kstep;
+    const uint8_t* sb = sbase0 + static_cast<int64_t>(kt) * kstep;
 #pragma unroll
     for (int q = 0; q < DMA_PER_WAVE; ++q)
-      if (q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(base + q * 1024));
+      if (q < nd) dma16(voff[q], sb, __builtin_amdgcn_readfirstlane(base + q * 1024));
   };
   for (int s = 0; s < 3 && s < nk; ++s) issue_all(s);
 
@@ -267,115 +293,127 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
     {
       wait_vm_dyn(nd * ((nk - 1) < 2 ? (nk - 1) : 2));
       __builtin_amdgcn_s_barrier();
-      read_frag<NJ>(f0, lds, xoff[0], woff[0]);
-      read_frag<NJ>(f1, lds, xoff[1], woff[1]);
+      read_frag<NJ>(f0, lds, xoff[0], woff[0], WSTEP);
+      read_frag<NJ>(f1, lds, xoff[1], woff[1], WSTEP);
     }
     for (int kt = 0; kt < nk; ++kt) {
-      mfma_step<NJ>(acc, f0, false, src, 0, 0, 0, 0);
+      mfma_step<NJ>(acc, f0, false, voff, sbase0, 0, 0, 0);
       const bool more = kt + 1 < nk;
       if (more) {
         // stage kt+1 landed; stage kt+2 (if issued) may pend
         wait_vm_dyn(kt + 2 < nk ? nd : 0);
         __builtin_amdgcn_s_barrier();
-        read_frag<NJ>(f0, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[0], woff[0]);
+        read_frag<NJ>(f0, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[0], woff[0], WSTEP);
       }
       const bool dma = kt + 3 < nk;
-      const int64_t koff = static_cast<int64_t>(kt + 3) * kstep;
+      const uint8_t* sb = sbase0 + static_cast<int64_t>(kt + 3) * kstep;
       const uint32_t dbase = ring0 + ((kt + 3) % NSTAGE) * STAGE + dst0;
-      mfma_step<NJ>(acc, f1, dma, src, koff, dbase, nd, 0);
+      mfma_step<NJ>(acc, f1, dma, voff, sb, dbase, nd, 0);
       if (dma && nd > 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 2; q < DMA_PER_WAVE; ++q)
-          if (q < nd) dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(dbase + q * 1024));
+          if (q < nd) dma16(voff[q], sb, __builtin_amdgcn_readfirstlane(dbase + q * 1024));
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (more) read_frag<NJ>(f1, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[1], woff[1]);
+      if (more) read_frag<NJ>(f1, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[1], woff[1], WSTEP);
     }
   };
-  if (nj == 4)
-    kloop(std::integral_constant<int, 4>{});
-  else if (nj == 2)
-    kloop(std::integral_constant<int, 2>{});
-  else
-    kloop(std::integral_constant<int, 0>{});
+  switch (nj) {
+    case 5: kloop(std::integral_constant<int, 5>{}); break;
+    case 4: kloop(std::integral_constant<int, 4>{}); break;
+    case 3: kloop(std::integral_constant<int, 3>{}); break;
+    case 2: kloop(std::integral_constant<int, 2>{}); break;
+    case 1: kloop(std::integral_constant<int, 1>{}); break;
+    default: kloop(std::integral_constant<int, 0>{}); break;
+  }
+  static_assert(MG == 5, "kloop variants cover 0..MG row groups");
 
   // ---- epilogue: bias, rounding, activation; output tile staged in LDS and
-  //      written with 16-byte row-contiguous stores
+  //      written with 16-byte row-contiguous stores (STORE tiles in two
+  //      passes of 160 rows, one per wave half)
   constexpr int PITCH = 2 * NOUT + 16;
+  constexpr int PASSES = BM * PITCH <= RING_BYTES ? 1 : 2;
+  constexpr int PROWS = BM / PASSES;
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
-  __syncthreads();  // every wave is done with the ring
   auto tcol = [&](int i, int r) -> int {  // tile output column of (i, r)
     return (kGlu ? 32 * wn : 64 * wn + 32 * i) + 8 * (r >> 2) + 4 * h + (r & 3);
   };
   constexpr int NI = kGlu ? 1 : 2;
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    float bg[16], bu[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      bg[r] = 0.f;
-      bu[r] = 0.f;
-      if (a.bias) {
-        const int64_t n = n0 + tcol(i, r);
-        if (n < N) {
-          bg[r] = bf16_to_f32(a.bias[bias_base + n]);
-          if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 128 * wm + 32 * j + l32;
-      float ov[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float g = round16<F16>(acc[i][j][r] + bg[r]);
-        if constexpr (kGlu) {
-          float u = round16<F16>(acc[1][j][r] + bu[r]);
-          if (a.clamp_limit > 0.f) {
-            g = fminf(g, a.clamp_limit);
-            u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-          }
-          float y;
-          if (a.act == MI355MOE_ACT_SILU) {
-            y = round16<F16>(x_sigmoid(g, 1.f)) * u;
-          } else {
-            g = g > a.limit ? a.limit : g;
-            u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-            y = (u + 1.f) * x_sigmoid(g, a.alpha);
-          }
-          g = round16<F16>(y);
-        }
-        ov[r] = g;
-      }
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const uint32_t lo = to16<F16>(ov[4 * g4]) | (to16<F16>(ov[4 * g4 + 1]) << 16);
-        const uint32_t hi = to16<F16>(ov[4 * g4 + 2]) | (to16<F16>(ov[4 * g4 + 3]) << 16);
-        *reinterpret_cast<uint2*>(lds + row * PITCH + 2 * tcol(i, 4 * g4)) = make_uint2(lo, hi);
-      }
-    }
-  }
-  __syncthreads();
   uint16_t* d = static_cast<uint16_t*>(a.D);
   const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
   constexpr int CPR = 2 * NOUT / 16;  // 16-byte chunks per row
-  for (int idx = tid; idx < BM * CPR; idx += 512) {
-    const int row = idx / CPR, ch = idx % CPR;
-    const int drow = s_drow[row];
-    const int64_t col = n0 + ch * 8;
-    if (drow < 0 || col >= N) continue;
-    const uint4 val = *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
-    uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
-    if (vec) {
-      *reinterpret_cast<uint4*>(dst) = val;
-    } else {
-      const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+  __syncthreads();  // every wave is done with the ring
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+  for (int pass = 0; pass < PASSES; ++pass) {
+    if (PASSES == 1 || wm == pass) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float bg[16], bu[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          bg[r] = 0.f;
+          bu[r] = 0.f;
+          if (a.bias) {
+            const int64_t n = n0 + tcol(i, r);
+            if (n < N) {
+              bg[r] = bf16_to_f32(a.bias[bias_base + n]);
+              if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < MG; ++j) {
+          const int srow = 32 * MG * wm + 32 * j + l32 - pass * PROWS;
+          float ov[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float g = round16<F16>(acc[i][j][r] + bg[r]);
+            if constexpr (kGlu) {
+              float u = round16<F16>(acc[1][j][r] + bu[r]);
+              if (a.clamp_limit > 0.f) {
+                g = fminf(g, a.clamp_limit);
+                u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
+              }
+              float y;
+              if (a.act == MI355MOE_ACT_SILU) {
+                y = round16<F16>(x_sigmoid(g, 1.f)) * u;
+              } else {
+                g = g > a.limit ? a.limit : g;
+                u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+                y = (u + 1.f) * x_sigmoid(g, a.alpha);
+              }
+              g = round16<F16>(y);
+            }
+            ov[r] = g;
+          }
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const uint32_t lo = to16<F16>(ov[4 * g4]) | (to16<F16>(ov[4 * g4 + 1]) << 16);
+            const uint32_t hi = to16<F16>(ov[4 * g4 + 2]) | (to16<F16>(ov[4 * g4 + 3]) << 16);
+            *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(i, 4 * g4)) = make_uint2(lo, hi);
+          }
+        }
+      }
     }
+    __syncthreads();
+    for (int idx = tid; idx < PROWS * CPR; idx += 512) {
+      const int srow = idx / CPR, ch = idx % CPR;
+      const int drow = s_drow[pass * PROWS + srow];
+      const int64_t col = n0 + ch * 8;
+      if (drow < 0 || col >= N) continue;
+      const uint4 val = *reinterpret_cast<const uint4*>(lds + srow * PITCH + ch * 16);
+      uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
+      if (vec) {
+        *reinterpret_cast<uint4*>(dst) = val;
+      } else {
+        const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+      }
+    }
+    if (pass + 1 < PASSES) __syncthreads();  // the staging area is rewritten
   }
 }
 
@@ -395,11 +433,20 @@ bool wide_supported(int recipe, const GemmArgs& a) {
   return recipe == MI355MOE_RECIPE_BF16 && a.K % KE == 0 && a.K > 0;
 }
 
-// 256-slot blocks; bf16 weights, K % 32 == 0.
+bool wide_offsets_fit(int64_t a_rows, int64_t ldb_rows, int64_t K) {
+  const int64_t lim = int64_t(1) << 32;
+  return a_rows * K * 2 < lim && ldb_rows * K * 2 < lim;
+}
+
+// 320-slot blocks; bf16 weights, K % 32 == 0.
 int launch_moe_gemm_wide(int recipe, int epi, const GemmArgs& a,
                          int64_t max_blocks, hipStream_t st) {
   if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
   MI_ARG(wide_supported(recipe, a), "wide GEMM: needs bf16 weights and K % 32 == 0");
+  // activation rows: tokens (gathered) or padded slots (by position)
+  const int64_t a_rows = a.a_by_pos ? max_blocks * BM : a.num_valid;
+  MI_ARG(wide_offsets_fit(a_rows, a.ldb_rows, a.K),
+         "wide GEMM: activation and per-expert weight bytes must stay below 4 GiB");
   if (epi == EPI_GLU)
     return a.out_f16 ? launch_wide<EPI_GLU, true>(a, max_blocks, st)
                      : launch_wide<EPI_GLU, false>(a, max_blocks, st);
