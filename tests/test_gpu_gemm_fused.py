@@ -248,8 +248,9 @@ BIG_ROWS = [300, 260, 0, 129]
 
 @pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4"])
 def test_grouped_gemm_big_tiles(dev, recipe):
-    """>96 rows per expert selects the LDS-staged 128x256 kernel; N=2880 is
-    not a multiple of the tile (ragged last tile)."""
+    """>96 rows per expert: bf16 and fp8 select the 320x256 kernels, mxfp4
+    the LDS-staged 128x256 one; N=2880 is not a multiple of the tile (ragged
+    last tile)."""
     g = torch.Generator().manual_seed(4)
     E, K = 4, 1024
     N = 640 if recipe == "fp8block" else 2880
@@ -312,6 +313,75 @@ def test_fused_moe_wide_tiles_ragged(dev, activation):
     cfg = dataclasses.replace(base, recipe="bf16", hidden=352, inter=224, experts=8, topk=2)
     cfg, w, x, tw, ti, out, _ = _layer(cfg, 1024, dev)
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
+
+
+# ------------------------------------------- fp8 prefill (320x256) tiles
+W8_ROWS = [1, 15, 17, 64, 100, 159, 160, 161, 200, 319, 320, 321, 700, 1000, 1200]
+
+
+@pytest.mark.parametrize("K", [128, 384, 1024])
+def test_grouped_gemm_wide8_tiles(dev, K):
+    """fp8 block-scaled weights with >160 rows per expert select the 320x256
+    kernel.  Valid rows per 320-slot block 1..320 (every count of 16-slot
+    MFMA tiles per wave half, 0..10, skipped 8-row DMA groups and 64-slot
+    scale groups); experts of 1, 2 and 3 blocks; K from one 128-element
+    stage (no DMA ahead) to 8; N=640 is two and a half 256-row tiles."""
+    g = torch.Generator().manual_seed(K + 1)
+    E, N = len(W8_ROWS), 640
+    M = sum(W8_ROWS)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    q, s = O.fp8_block_quant_weight(torch.randn(E, N, K, generator=g) * 0.02)
+    rows = torch.tensor(W8_ROWS, dtype=torch.int32)
+    d = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), s.to(dev), None, d, rows.to(dev),
+                                N, K, E)
+    ref = O.grouped_gemm("fp8block", a, q, s, None, W8_ROWS)
+    torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_grouped_gemm_big8_tiles(dev):
+    """fp8 block-scaled weights with 97..160 rows per expert select the
+    128x256 8-wave kernel (128-slot blocks; experts of 1 and 2 blocks, a
+    partial last block)."""
+    g = torch.Generator().manual_seed(13)
+    rows_l = [129, 100, 150, 0, 201]
+    E, N, K = len(rows_l), 384, 512
+    M = sum(rows_l)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    q, s = O.fp8_block_quant_weight(torch.randn(E, N, K, generator=g) * 0.02)
+    d = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), s.to(dev), None, d,
+                                torch.tensor(rows_l, dtype=torch.int32, device=dev), N, K, E)
+    ref = O.grouped_gemm("fp8block", a, q, s, None, rows_l)
+    torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_grouped_gemm_fp8_k_beyond_wide8(dev):
+    """K = 8320 exceeds the 320-slot kernel's scale table (64 blocks of 128):
+    the 128x256 LDS pipeline kernel runs instead."""
+    g = torch.Generator().manual_seed(11)
+    rows_l = [150, 300]
+    E, N, K = 2, 256, 8320
+    M = sum(rows_l)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    q, s = O.fp8_block_quant_weight(torch.randn(E, N, K, generator=g) * 0.01)
+    d = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), s.to(dev), None, d,
+                                torch.tensor(rows_l, dtype=torch.int32, device=dev), N, K, E)
+    ref = O.grouped_gemm("fp8block", a, q, s, None, rows_l)
+    torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("T", [1024, 700])
+def test_fused_moe_wide8_ragged(dev, T):
+    """Whole fp8 block-scaled layer through the 320x256 kernels: the w13
+    epilogue re-quantises the activation to e4m3 (1x128 groups) in LDS;
+    T=700 leaves about 175 slots per expert (second wave half nearly idle)."""
+    import dataclasses
+    cfg = dataclasses.replace(_W().CONFIGS["C2"], recipe="fp8block", hidden=384, inter=256,
+                              experts=8, topk=2)
+    cfg, w, x, tw, ti, out, _ = _layer(cfg, T, dev)
+    _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
 # ------------------------------------------------- K-blocked bf16 weights

@@ -118,9 +118,8 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   const int64_t E = a->num_experts;
   L.slots = a->num_tokens * a->topk;
   const int64_t H = a->hidden, I = a->inter;
-  const bool wide_ok = H % 32 == 0 && I % 32 == 0 &&
-                       wide_offsets_fit(a->num_tokens, 2 * I, H) &&
-                       wide_offsets_fit(L.slots + E * kWideBM, H, I);
+  const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H) &&
+                       wide_ok_for(a->recipe, L.slots + E * kWideBM, H, I);
   L.tile = pick_tile(a->recipe, wide_ok, L.slots, E, &L.bm);
   // K-blocked weights: the families that read them (STREAM, SMALL, WIDE)
   if (a->w_layout == MI355MOE_WLAYOUT_KB32 && L.tile != TILE_STREAM &&
@@ -377,7 +376,7 @@ struct GGLayout {
 GGLayout gg_plan(int recipe, bool need_quant, int64_t M, int64_t K, int64_t E,
                  uint8_t* base) {
   GGLayout L{};
-  L.tile = pick_tile(recipe, K % 32 == 0 && wide_offsets_fit(M, 0, K), M, E, &L.bm);
+  L.tile = pick_tile(recipe, wide_ok_for(recipe, M, 0, K), M, E, &L.bm);
   padded_sizes(M, E, L.bm, L.max_padded, L.max_blocks);
   L.grid_blocks = launch_blocks(M, E, L.bm, L.max_blocks);
   Carver c{base};

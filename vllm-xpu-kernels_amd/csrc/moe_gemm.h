@@ -98,17 +98,21 @@ int pick_block_m(int64_t slots, int64_t num_experts);
 // Kernel family by the expected rows per active expert:
 //   <= 24   STREAM: independent-wave weight streaming, 16-slot blocks
 //   <= 96   SMALL:  LDS-shared activation tile, 32/64-slot blocks
-//   >  96   WIDE:   bf16 weights with every K % 32 == 0 (wide_ok): 320x256
-//                   tiles, 320-slot blocks (kWideBM)
+//   >  96   WIDE:   bf16 weights (fp8 block-scaled: > 160 rows) whose
+//                   shapes the WIDE kernels take (wide_ok, see wide_ok_for):
+//                   320x256 tiles, 320-slot blocks (kWideBM)
 //           BIG:    otherwise, 128x256 LDS-staged tiles, 128-slot blocks
 // MI355MOE_GEMM_TILE=stream|small|big|bigreg|wide overrides (A/B
 // measurements; wide falls back to big where it does not apply).
-// (TILE_BIG runs the 8-wave fp8 kernel where wide8_supported(), else the
-// LDS-DMA pipelined kernel where pipe_supported(); TILE_BIGREG forces the
-// register-staged one.)
+// (TILE_BIG runs the 8-wave fp8 kernel where big8_supported(), else the
+// LDS-DMA pipelined kernel where pipe_supported(), else the register-staged
+// one, which TILE_BIGREG forces.)
 enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3, TILE_WIDE = 4 };
 constexpr int kWideBM = 320;  // slots per block of the WIDE family
 GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm);
+// Whether a GEMM with a_rows activation rows, ldb_rows weight rows per
+// expert (0: not known yet) and reduction length K fits the WIDE kernels.
+bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K);
 
 // Launch the chosen family over max_blocks blocks of bm slots.
 int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
@@ -125,8 +129,14 @@ bool pipe_supported(int recipe, const GemmArgs& a);
 int launch_moe_gemm_pipe(int recipe, int epi, bool qout, const GemmArgs& a,
                          int64_t max_blocks, void* qs, hipStream_t st);
 // 128-slot blocks, fp8 block-scaled weights, K % 128 == 0, K <= 8192
+// (moe_gemm_big8.hip).
+bool big8_supported(int recipe, const GemmArgs& a);
+int launch_moe_gemm_big8(int recipe, int epi, bool qout, const GemmArgs& a,
+                         int64_t max_blocks, void* qs, hipStream_t st);
+// kWideBM-slot blocks, fp8 block-scaled weights, K % 128 == 0, K <= 8192
 // (moe_gemm_wide8.hip).
 bool wide8_supported(int recipe, const GemmArgs& a);
+bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K);
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
                           int64_t max_blocks, void* qs, hipStream_t st);
 // kWideBM-slot blocks, bf16 weights, K % 32 == 0 (moe_gemm_wide.hip).

@@ -351,6 +351,12 @@ int pick_block_m(int64_t slots, int64_t num_experts) {
   return 128;
 }
 
+bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K) {
+  if (recipe == MI355MOE_RECIPE_BF16) return K % 32 == 0 && wide_offsets_fit(a_rows, ldb_rows, K);
+  if (recipe == MI355MOE_RECIPE_FP8BLOCK) return wide8_shape_ok(a_rows, ldb_rows, K);
+  return false;
+}
+
 GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm) {
   static const int force = [] {
     const char* v = getenv("MI355MOE_GEMM_TILE");
@@ -362,7 +368,13 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     if (!strcmp(v, "wide")) return static_cast<int>(TILE_WIDE);
     return -1;
   }();
-  const bool wide = wide_ok && recipe == MI355MOE_RECIPE_BF16;
+  // fp8: a 320-slot stage is 73 KB, so its kernel keeps one stage of DMA in
+  // flight against the 128-slot kernel's two; it wins where experts average
+  // well above 128 slots (fewer weight passes), not at about 128.
+  const int64_t active = slots < num_experts ? slots : num_experts;
+  const int64_t avg = active > 0 ? slots / active : 0;
+  const bool wide = wide_ok && (recipe == MI355MOE_RECIPE_BF16 ||
+                                (recipe == MI355MOE_RECIPE_FP8BLOCK && avg > 160));
   const int m = pick_block_m(slots, num_experts);
   GemmTile t = m == 16 ? TILE_STREAM : (m == 128 ? (wide ? TILE_WIDE : TILE_BIG) : TILE_SMALL);
   if (force >= 0) t = static_cast<GemmTile>(force);
@@ -381,13 +393,15 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:
-      if (wide8_supported(recipe, a) && getenv("MI355MOE_FP8_PIPE") == nullptr)
-        return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
+      if (big8_supported(recipe, a))
+        return launch_moe_gemm_big8(recipe, epi, qout, a, max_blocks, qs, st);
       if (pipe_supported(recipe, a))
         return launch_moe_gemm_pipe(recipe, epi, qout, a, max_blocks, qs, st);
       return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIGREG: return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_WIDE:
+      if (recipe == MI355MOE_RECIPE_FP8BLOCK)
+        return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
       MI_ARG(!qout, "wide GEMM: no fp8 activation output");
       return launch_moe_gemm_wide(recipe, epi, a, max_blocks, st);
     default: return launch_moe_gemm_q(recipe, epi, qout, bm, a, max_blocks, qs, st);

@@ -1,32 +1,39 @@
 // Prefill grouped GEMM for fp8 e4m3 weights with 128x128 block scales and
-// e4m3 activations with 1x128 scales: 128-slot x 256-weight-row tiles, 8
-// waves, 3-slot LDS ring fed by direct global->LDS DMA.
+// e4m3 activations with 1x128 scales: 320-slot x 256-weight-row tiles, 8
+// waves, 2-slot LDS ring fed by direct global->LDS DMA.
+//
+// Why 320 slots.  A tile streams its 256 weight rows over the whole K, so the
+// weight bytes a layer moves are (tiles per expert) x (expert weights);
+// routing spreads n +- sqrt(n) slots over an expert and 320 slots hold the
+// usual prefill n = 256 with four standard deviations to spare, where
+// 128-slot blocks stream every expert's weights three times.  Compute and
+// activation DMA scale with the valid slots only.
 //
 // Waves.  Eight waves, two per SIMD (waves w and w + 4 share SIMD w % 4), each
-// owning 64 slots x 64 weight rows: 4 x 4 tiles of the 16x16x128 e4m3 MFMA
-// with the weight as the A operand.  One MFMA covers one whole 128-K scale
-// block, so its result is scaled and added at once (acc += p * xs * ws, one
-// FMA per output element per block) and the partial products never outlive
-// the instruction that made them; the FMAs of one tile run while the MFMAs
-// of the next do.
+// owning 160 slots x 64 weight rows: 4 x 10 tiles of the 16x16x128 e4m3 MFMA
+// with the weight as the A operand (160 accumulator registers).  One MFMA
+// covers one whole 128-K scale block, so its result is scaled and added at
+// once (acc += p * xs * ws).  The four weight fragments of a stage stay in
+// registers; the ten activation fragments stream from LDS one tile ahead.
 //
-// Stages.  A stage holds 128 K elements (128 bytes) of the 128 activation
-// rows and 256 weight rows plus the block's 128 activation scales: 48.5 KB,
-// written by 48 global_load_lds_dwordx4 (8 rows x 128 B each) and two
-// global_load_lds_dword.  16-byte chunk c of row r sits at slot
-// c ^ ((r >> 1) & 7), so sixteen rows read at one logical chunk hit sixteen
-// distinct bank groups.
+// Stages.  A stage holds 128 K elements (128 bytes) of the 320 activation
+// rows and 256 weight rows plus the 320 activation scales of the 128-K block:
+// 73.25 KB, so two fit.  Waves 0-3 move 10 activation blocks of 8 rows each,
+// waves 4-7 8 weight blocks and the scales (global_load_lds_dwordx4 /
+// _dword).  16-byte chunk c of row r sits at slot c ^ ((r >> 1) & 7), so
+// sixteen rows read at one logical chunk hit sixteen distinct bank groups.
+// DMA addresses are a scalar base plus 32-bit lane offsets recomputed each
+// stage from small LDS tables (no registers held across the K loop).
 //
-// Pipeline.  A wave computes stage kt from registers and reads stage kt+1's
-// fragments into the same registers as the MFMAs release them; the barrier
-// before stage kt's MFMAs certifies that every wave's reads of stage kt are
-// complete, so the DMA of stage kt+3 goes into that slot while stage kt
-// computes (two stages of lookahead in three slots).
+// Pipeline.  Iteration kt waits for its own DMA of stage kt, meets the others
+// at a barrier (stage kt is complete and visible, and every wave has finished
+// reading stage kt-1), then issues stage kt+1 into stage kt-1's slot and
+// computes stage kt while that DMA is in flight.
 //
-// Tiles, GLU pairing and the fp8 activation output are those of the 128x256
-// kernels: a GLU tile's 256 weight rows are 128 gate rows and the matching
-// 128 up rows, so its 128 output columns are one whole 1x128 quantisation
-// group of the next GEMM's input.
+// Tiles, GLU pairing and the fp8 activation output are those of the other
+// prefill kernels: a GLU tile's 256 weight rows are 128 gate rows and the
+// matching 128 up rows, so its 128 output columns are one whole 1x128
+// quantisation group of the next GEMM's input.
 #include <type_traits>
 
 #include "moe_gemm.h"
@@ -38,40 +45,42 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int BM = 128, BN = 256, ROWB = 128, KE = 128;
-constexpr int A_BYTES = BM * ROWB;                 // 16 KB
+constexpr int BM = 320, BN = 256, ROWB = 128, KE = 128;
+static_assert(BM == kWideBM, "block size of the WIDE family");
+constexpr int A_BYTES = BM * ROWB;                 // 40 KB
 constexpr int W_BYTES = BN * ROWB;                 // 32 KB
 constexpr int S_OFF = A_BYTES + W_BYTES;           // activation scales
-constexpr int STAGE = S_OFF + BM * 4;              // 48.5 KB
-constexpr int NSTAGE = 3;
-constexpr int DMA_PER_WAVE = (A_BYTES + W_BYTES) / 1024 / 8;  // 6
+constexpr int STAGE = S_OFF + BM * 4;              // 73.25 KB
+constexpr int NSTAGE = 2;
+constexpr int RING = NSTAGE * STAGE;
+constexpr int A_BLK = BM / 8 / 4;                  // activation blocks per wave (waves 0-3)
+constexpr int W_BLK = BN / 8 / 4;                  // weight blocks per wave (waves 4-7)
 constexpr int MAX_KBLK = 64;                       // K <= 8192
-constexpr int EPI_BYTES = BM * (2 * 256 + 16);     // largest staged output tile
+constexpr int TJ = BM / 2 / 16;                    // activation tiles per wave
+static_assert(BM * (2 * 128 + 16) <= RING, "GLU output tile staged in one pass");
+static_assert(BM / 2 * (2 * 256 + 16) <= RING, "STORE output tile staged in two passes");
+static_assert(BM * (128 + 16) + 4 * BM * 4 <= RING, "fp8 output tile and row maxima");
 
 __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
 }
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(lds_base) : "memory");
+// 16 (dma16) or 4 (dma4) bytes per lane from sbase + voff (scalar base,
+// 32-bit lane offset) into LDS at lds_base + 16 lane (4 lane).
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory");
 }
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
-               :: "v"(g), "s"(lds_base) : "memory");
+__device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory");
 }
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-// wave-uniform number of DMA instructions allowed to stay outstanding
-__device__ __forceinline__ void wait_vm_dyn(int n) {
-  switch (n) {
-    case 6: wait_vm<6>(); break;
-    case 8: wait_vm<8>(); break;
-    case 12: wait_vm<12>(); break;
-    case 16: wait_vm<16>(); break;
-    default: wait_vm<0>(); break;  // 0, and never less strict than needed
-  }
+// readfirstlane returns int: each half goes through uint32_t so that the low
+// half is zero-extended.
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
+  return reinterpret_cast<const uint8_t*>((hi << 32) | lo);
 }
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
@@ -104,25 +113,15 @@ __device__ __forceinline__ float x_sigmoid(float x, float k) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
-// Fragments of one wave: [j] activation tiles (slots 64 wm + 16 j + l%16),
-// [i] weight tiles; two 16-byte chunks each (K [32g, 32g + 32) of the stage,
-// g = l / 16).
-typedef i32x8_t XFrag[4];
-typedef i32x8_t WFrag[4];
-
-// Tile rows start at multiples of 16, where the slot swizzle (r >> 1) & 7
-// depends on r % 16 only: one base offset per chunk, tiles at constant
-// distances (16 rows = 2 KB).
-__device__ __forceinline__ void read_x(XFrag& x, const uint8_t* S, const int (&xo)[2]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = ld32(S + j * 16 * ROWB, xo[0], xo[1]);
-}
+// Weight fragments of one wave (4 tiles of 16 rows).  Tile rows start at
+// multiples of 16, where the row swizzle (r >> 1) & 7 depends on r % 16 only:
+// one base offset per chunk, tiles at constant distances.
 template <bool kGlu>
-__device__ __forceinline__ void read_w(WFrag& w, int i0, const uint8_t* S, const int (&wo)[2]) {
+__device__ __forceinline__ void read_w(i32x8_t (&w)[4], const uint8_t* S, int wo0, int wo1) {
 #pragma unroll
-  for (int i = i0; i < i0 + 2; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int t = kGlu ? (i < 2 ? 0 : 128) + 16 * (i & 1) : 16 * i;  // tile row - wave row
-    w[i] = ld32(S + t * ROWB, wo[0], wo[1]);
+    w[i] = ld32(S + t * ROWB, wo0, wo1);
   }
 }
 
@@ -131,13 +130,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[RING];
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
+  __shared__ uint32_t s_woff[BN];       // byte offset of tile weight row r in the expert
   __shared__ float s_wsc[2][MAX_KBLK];  // weight-block scales of the tile's two row blocks
-  __shared__ float s_amax[4][BM];       // QOUT: per-wave-column row maxima
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, g = lane >> 4;
 
@@ -156,9 +156,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
   const int64_t n0 = static_cast<int64_t>(ntile) * NOUT;
   const int nkb = static_cast<int>(K / 128);
 
+  int ok = 0;
   if (tid < BM) {
     const int rid = a.row_ids[static_cast<int64_t>(blk) * BM + tid];
-    const bool ok = rid >= 0 && rid < a.num_valid;
+    ok = rid >= 0 && rid < a.num_valid;
     s_arow[tid] = ok ? (a.a_by_pos ? blk * BM + tid : rid / a.a_div) : -1;
     s_drow[tid] = ok ? (a.d_by_pos ? blk * BM + tid : rid) : -1;
   }
@@ -173,6 +174,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       return c < N ? c : 0;
     }
   };
+  if (tid < BN) s_woff[tid] = static_cast<uint32_t>(wrow_of(tid) * K);
   {
     const float* bsc = static_cast<const float*>(a.b_scale);
     for (int i = tid; i < 2 * nkb; i += 512) {
@@ -181,143 +183,148 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wr) * nkb + kb];
     }
   }
-  __syncthreads();
+  // valid slots form a prefix of the block
+  const int v = __syncthreads_count(ok);
 
-  // DMA sources: blocks b = 6 wave + q of a stage, activation rows for b < 16
-  // (8 rows each), weight rows after; wave 0 also moves the activation
-  // scales of the stage's 128-K block (128 floats, two 256-byte DMAs).
-  const uint8_t* src[DMA_PER_WAVE];
-  {
-    const uint8_t* abase = static_cast<const uint8_t*>(a.A);
-    const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
-                          static_cast<int64_t>(e) * a.ldb_rows * K;
-#pragma unroll
-    for (int q = 0; q < DMA_PER_WAVE; ++q) {
-      const int b = DMA_PER_WAVE * wave + q;
-      const int r = (b < 16 ? b : b - 16) * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ swz(r);
-      if (b < 16) {
-        const int ar = s_arow[r];
-        src[q] = abase + static_cast<int64_t>(ar >= 0 ? ar : 0) * K + c * 16;
-      } else {
-        src[q] = wexp + wrow_of(r) * K + c * 16;
-      }
-    }
-  }
-  const int nd = DMA_PER_WAVE + (wave == 0 ? 2 : 0);
-  const float* ssrc0 = a.a_scale;
-  const float* ssrc1 = a.a_scale;
-  if (wave == 0) {
-    const int r0 = s_arow[lane], r1 = s_arow[64 + lane];
-    ssrc0 += static_cast<int64_t>(r0 >= 0 ? r0 : 0) * nkb;
-    ssrc1 += static_cast<int64_t>(r1 >= 0 ? r1 : 0) * nkb;
-  }
+  // DMA of stage kt into slot kt % 2.  Waves 0-3: activation blocks
+  // A_BLK wave + q (8 rows each; blocks of padding only are skipped); waves
+  // 4-7: weight blocks W_BLK (wave - 4) + q and the activation scales of the
+  // 128-K block, 64 slots per dword DMA (wave 4: groups 0, 1; waves 5-7:
+  // groups 2-4).  Offsets come from s_arow / s_woff at every issue.
+  const bool a_wave = wave < 4;
+  const uint8_t* abase = uniform_ptr(a.A);
+  const uint8_t* wbase = uniform_ptr(static_cast<const uint8_t*>(a.B) +
+                                     static_cast<int64_t>(e) * a.ldb_rows * K);
+  const uint8_t* sbase = uniform_ptr(a.a_scale);
+  // Lane l of a block b moves row 8 b + l / 8, 16-byte slot l % 8; that row's
+  // swizzle is (4 b + l / 16) & 7 = (l / 16) ^ 4 (b & 1), so the lane's
+  // source chunk is c0 ^ 64 (b & 1) bytes.  Table entries are read at
+  // immediate offsets from one lane address.
+  // Per-wave lane addresses into the tables, so that block q's entry sits at
+  // an immediate offset; A_BLK and W_BLK are even, so a block's parity is q's.
+  static_assert(A_BLK % 2 == 0 && W_BLK % 2 == 0, "block parity is q's");
   const uint32_t ring0 = lds_off(lds);
-  const uint32_t dst0 = DMA_PER_WAVE * wave * 1024;
+  const int w4 = wave - 4;
+  const int b0 = a_wave ? A_BLK * wave : W_BLK * w4;  // first block of the wave
+  const int* arow_w = s_arow + b0 * 8 + (lane >> 3);
+  const uint32_t* woff_w = s_woff + b0 * 8 + (lane >> 3);
+  const int d0 = w4 <= 0 ? 0 : w4 + 1;               // scale groups of waves 4-7
+  const int dn = w4 == 0 ? 2 : 1;
+  const int* arow_s = s_arow + d0 * 64 + lane;
+  const uint32_t c0 = static_cast<uint32_t>((lane & 7) ^ (lane >> 4)) << 4;
+  const uint32_t Ku = static_cast<uint32_t>(K), nkbu = static_cast<uint32_t>(nkb);
   auto issue = [&](int kt) {
-    const uint32_t base = ring0 + (kt % NSTAGE) * STAGE;
-    const int64_t koff = static_cast<int64_t>(kt) * ROWB;
+    const uint32_t base = ring0 + (kt & 1) * STAGE;
+    const uint32_t kofs = static_cast<uint32_t>(kt) * ROWB;
+    if (a_wave) {
+      const uint32_t dst = base + b0 * 1024;
 #pragma unroll
-    for (int q = 0; q < DMA_PER_WAVE; ++q)
-      dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(base + dst0 + q * 1024));
-    if (wave == 0) {
-      dma4(ssrc0 + kt, __builtin_amdgcn_readfirstlane(base + S_OFF));
-      dma4(ssrc1 + kt, __builtin_amdgcn_readfirstlane(base + S_OFF + 256));
+      for (int q = 0; q < A_BLK; ++q) {
+        if ((b0 + q) * 8 < v) {
+          const int ar = arow_w[q * 8];
+          const uint32_t off = static_cast<uint32_t>(ar >= 0 ? ar : 0) * Ku + kofs +
+                               (c0 ^ ((q & 1) << 6));
+          dma16(off, abase, __builtin_amdgcn_readfirstlane(dst + q * 1024));
+        }
+      }
+    } else {
+      const uint32_t dst = base + A_BYTES + b0 * 1024;
+#pragma unroll
+      for (int q = 0; q < W_BLK; ++q) {
+        const uint32_t off = woff_w[q * 8] + kofs + (c0 ^ ((q & 1) << 6));
+        dma16(off, wbase, __builtin_amdgcn_readfirstlane(dst + q * 1024));
+      }
+      const uint32_t sdst = base + S_OFF + d0 * 256;
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd) {
+        if (dd < dn && (d0 + dd) * 64 < v) {
+          const int ar = arow_s[dd * 64];
+          const uint32_t off = (static_cast<uint32_t>(ar >= 0 ? ar : 0) * nkbu +
+                                static_cast<uint32_t>(kt)) * 4u;
+          dma4(off, sbase, __builtin_amdgcn_readfirstlane(sdst + dd * 256));
+        }
+      }
     }
   };
 
   // fragment offsets: chunks 2g and 2g + 1 of the wave's first activation /
   // weight row + l%16
-  int xo[2], wo[2];
-  {
-    const int mx = 64 * wm + l16;
-    const int rw = (kGlu ? 32 * wn : 64 * wn) + l16;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int ch = 2 * g + c;
-      xo[c] = mx * ROWB + ((ch ^ swz(mx)) << 4);
-      wo[c] = A_BYTES + rw * ROWB + ((ch ^ swz(rw)) << 4);
-    }
-  }
+  const int mx = (BM / 2) * wm + l16;
+  const int rw = (kGlu ? 32 * wn : 64 * wn) + l16;
+  const int xo0 = mx * ROWB + (((2 * g) ^ swz(mx)) << 4);
+  const int xo1 = mx * ROWB + (((2 * g + 1) ^ swz(mx)) << 4);
+  const int wo0 = A_BYTES + rw * ROWB + (((2 * g) ^ swz(rw)) << 4);
+  const int wo1 = A_BYTES + rw * ROWB + (((2 * g + 1) ^ swz(rw)) << 4);
   // weight-block row of tile i (s_wsc index)
   int wblk[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) wblk[i] = kGlu ? (i >> 1) : (wn >> 1);
+  // activation tiles of this wave holding valid slots
+  const int vw = v - (BM / 2) * wm;
+  const int nj = vw <= 0 ? 0 : (vw >= BM / 2 ? TJ : (vw + 15) / 16);
 
-  f32x4_t acc[4][4];
+  f32x4_t acc[4][TJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nk = static_cast<int>(K / KE);
-  for (int s = 0; s < NSTAGE && s < nk; ++s) issue(s);
-  XFrag xf;
-  WFrag wf;
-  wait_vm_dyn(nd * ((nk - 1) < NSTAGE - 1 ? (nk - 1) : NSTAGE - 1));
-  __builtin_amdgcn_s_barrier();
-  read_x(xf, lds, xo);
-  read_w<kGlu>(wf, 0, lds, wo);
-  read_w<kGlu>(wf, 2, lds, wo);
-
-  // Stage kt.  Its fragments are in registers; the barrier publishes stage
-  // kt+1 and certifies that every wave's reads of stage kt are complete
-  // (lgkmcnt(0) before it), so the DMA of stage kt+3 goes into that slot
-  // between the MFMAs.  Stage kt+1's fragments replace those of stage kt,
-  // each group right after the MFMAs that last read it.
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    const uint8_t* cur = lds + (kt % NSTAGE) * STAGE;
-    const uint8_t* nxt = lds + ((kt + 1) % NSTAGE) * STAGE;
-    float xs[4];
+  issue(0);
+  auto kloop = [&](auto nj_c) {
+    constexpr int NJ = decltype(nj_c)::value;
+    for (int kt = 0; kt < nk; ++kt) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's DMA of stage kt
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); // its reads of stage kt-1
+      __builtin_amdgcn_s_barrier();
+      if (kt + 1 < nk) issue(kt + 1);
+      const uint8_t* S = lds + (kt & 1) * STAGE;
+      i32x8_t w[4];
+      read_w<kGlu>(w, S, wo0, wo1);
+      float ws[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      xs[j] = reinterpret_cast<const float*>(cur + S_OFF)[64 * wm + 16 * j + l16];
-    float ws[4];
+      for (int i = 0; i < 4; ++i) ws[i] = s_wsc[wblk[i]][kt];
+      if constexpr (NJ > 0) {
+        const float* xsp = reinterpret_cast<const float*>(S + S_OFF) + (BM / 2) * wm + l16;
+        i32x8_t x = ld32(S, xo0, xo1);
+        float xs = xsp[0];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ws[i] = s_wsc[wblk[i]][kt];
-    if (more) {
-      // stage kt+1 landed (stage kt+2 may pend)
-      const int issued = (kt + NSTAGE - 1 < nk ? kt + NSTAGE - 1 : nk - 1);
-      wait_vm_dyn(nd * (issued - (kt + 1)));
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    const bool dma = kt + NSTAGE < nk;
-    const uint32_t dbase = ring0 + (kt % NSTAGE) * STAGE;
-    const int64_t koff = static_cast<int64_t>(kt + NSTAGE) * ROWB;
+        for (int j = 0; j < NJ; ++j) {
+          i32x8_t xn = x;
+          float xsn = xs;
+          if (j + 1 < NJ) {  // next tile's fragment, one tile ahead
+            xn = ld32(S + (j + 1) * 16 * ROWB, xo0, xo1);
+            xsn = xsp[16 * (j + 1)];
+          }
+          f32x4_t pr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // four MFMAs in flight, then their scale FMAs
-      f32x4_t pr[4];
+          for (int i = 0; i < 4; ++i) pr[i] = mfma16(w[i], x);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) pr[j] = mfma16(wf[i], xf[j]);
+          for (int i = 0; i < 4; ++i) {
+            const float sc = xs * ws[i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float sc = xs[j] * ws[i];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] += pr[j][r] * sc;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (dma) {
-        // DMA instructions 2i, 2i + 1 of stage kt+3 (and wave 0's scales)
-#pragma unroll
-        for (int q = 2 * i; q < 2 * i + 2; ++q)
-          if (q < DMA_PER_WAVE)
-            dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(dbase + dst0 + q * 1024));
-        if (i == 3 && wave == 0) {
-          dma4(ssrc0 + (kt + NSTAGE), __builtin_amdgcn_readfirstlane(dbase + S_OFF));
-          dma4(ssrc1 + (kt + NSTAGE), __builtin_amdgcn_readfirstlane(dbase + S_OFF + 256));
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += pr[i][r] * sc;
+          }
+          x = xn;
+          xs = xsn;
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    // stage kt+1's fragments (after the last stage: a stale slot, unused;
-    // unconditional so the loads land in the loop-carried registers)
-    read_w<kGlu>(wf, 0, nxt, wo);
-    read_w<kGlu>(wf, 2, nxt, wo);
-    read_x(xf, nxt, xo);
+  };
+  switch (nj) {
+    case 10: kloop(std::integral_constant<int, 10>{}); break;
+    case 9: kloop(std::integral_constant<int, 9>{}); break;
+    case 8: kloop(std::integral_constant<int, 8>{}); break;
+    case 7: kloop(std::integral_constant<int, 7>{}); break;
+    case 6: kloop(std::integral_constant<int, 6>{}); break;
+    case 5: kloop(std::integral_constant<int, 5>{}); break;
+    case 4: kloop(std::integral_constant<int, 4>{}); break;
+    case 3: kloop(std::integral_constant<int, 3>{}); break;
+    case 2: kloop(std::integral_constant<int, 2>{}); break;
+    case 1: kloop(std::integral_constant<int, 1>{}); break;
+    default: kloop(std::integral_constant<int, 0>{}); break;
   }
+  static_assert(TJ == 10, "kloop variants cover 0..TJ activation tiles");
 
   // ---- epilogue
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
@@ -328,71 +335,66 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
     return (kGlu ? 32 * wn + 16 * i : 64 * wn + 16 * i) + 4 * g + r;
   };
   constexpr int NI = kGlu ? 2 : 4;
-  float ov[NI][4][4];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    float bg[4], bu[4];
+  // bias, rounding and activation of (tile i, activation tile j)
+  auto outv = [&](int i, int j, float (&o)[4]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      bg[r] = 0.f;
-      bu[r] = 0.f;
+      float bg = 0.f, bu = 0.f;
       if (a.bias) {
         const int64_t n = n0 + tcol(i, r);
         if (n < N) {
-          bg[r] = bf16_to_f32(a.bias[bias_base + n]);
-          if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+          bg = bf16_to_f32(a.bias[bias_base + n]);
+          if constexpr (kGlu) bu = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
         }
       }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float gv = round16<F16>(acc[i][j][r] + bg[r]);
-        if constexpr (kGlu) {
-          float u = round16<F16>(acc[i + 2][j][r] + bu[r]);
-          if (a.clamp_limit > 0.f) {
-            gv = fminf(gv, a.clamp_limit);
-            u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-          }
-          float y;
-          if (a.act == MI355MOE_ACT_SILU) {
-            y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
-          } else {
-            gv = gv > a.limit ? a.limit : gv;
-            u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-            y = (u + 1.f) * x_sigmoid(gv, a.alpha);
-          }
-          gv = round16<F16>(y);
+      float gv = round16<F16>(acc[i][j][r] + bg);
+      if constexpr (kGlu) {
+        float u = round16<F16>(acc[i + 2][j][r] + bu);
+        if (a.clamp_limit > 0.f) {
+          gv = fminf(gv, a.clamp_limit);
+          u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
         }
-        ov[i][j][r] = gv;
+        float y;
+        if (a.act == MI355MOE_ACT_SILU) {
+          y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
+        } else {
+          gv = gv > a.limit ? a.limit : gv;
+          u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+          y = (u + 1.f) * x_sigmoid(gv, a.alpha);
+        }
+        gv = round16<F16>(y);
       }
+      o[r] = gv;
     }
-  }
+  };
 
   if constexpr (QOUT) {
     // e4m3 activation with one fp32 scale per (slot, 128 columns): the four
     // waves with the same wm cover the tile's 128 columns (N % 128 == 0).
-    // Lane l holds slots 64 wm + 16 j + l%16; lanes l, l+16, l+32, l+48 hold
-    // the same slot.
+    // Lane l holds slots 160 wm + 16 j + l%16; lanes l, l+16, l+32, l+48 hold
+    // the same slot.  Row maxima go to LDS after the staged tile.
+    constexpr int PITCH = NOUT + 16;
+    float (*s_amax)[BM] = reinterpret_cast<float (*)[BM]>(lds + BM * PITCH);
+    float ov[NI][TJ][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < TJ; ++j) {
       float m = 1e-10f;
 #pragma unroll
-      for (int i = 0; i < NI; ++i)
+      for (int i = 0; i < NI; ++i) {
+        outv(i, j, ov[i][j]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[i][j][r]));
+      }
       m = fmaxf(m, __shfl_xor(m, 16, 64));
       m = fmaxf(m, __shfl_xor(m, 32, 64));
-      if (g == 0) s_amax[wn][64 * wm + 16 * j + l16] = m;
+      if (g == 0) s_amax[wn][(BM / 2) * wm + 16 * j + l16] = m;
     }
     __syncthreads();
-    constexpr int PITCH = NOUT + 16;
     float* ds = static_cast<float*>(qs);
     const int64_t ngroups = N / 128;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 64 * wm + 16 * j + l16;
+    for (int j = 0; j < TJ; ++j) {
+      const int row = (BM / 2) * wm + 16 * j + l16;
       const float am = fmaxf(fmaxf(s_amax[0][row], s_amax[1][row]),
                              fmaxf(s_amax[2][row], s_amax[3][row]));
       const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
@@ -421,35 +423,47 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
           *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
     }
   } else {
+    // 16-bit output staged in LDS (STORE tiles in two passes of 160 rows,
+    // one per wave half) and written with 16-byte row-contiguous stores
     constexpr int PITCH = 2 * NOUT + 16;
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = 64 * wm + 16 * j + l16;
-        const uint32_t lo = to16<F16>(ov[i][j][0]) | (to16<F16>(ov[i][j][1]) << 16);
-        const uint32_t hi = to16<F16>(ov[i][j][2]) | (to16<F16>(ov[i][j][3]) << 16);
-        *reinterpret_cast<uint2*>(lds + row * PITCH + 2 * tcol(i, 0)) = make_uint2(lo, hi);
-      }
-    __syncthreads();
+    constexpr int PASSES = BM * PITCH <= RING ? 1 : 2;
+    constexpr int PROWS = BM / PASSES;
     uint16_t* d = static_cast<uint16_t*>(a.D);
     const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
     constexpr int CPR = 2 * NOUT / 16;
-    for (int idx = tid; idx < BM * CPR; idx += 512) {
-      const int row = idx / CPR, ch = idx % CPR;
-      const int drow = s_drow[row];
-      const int64_t col = n0 + ch * 8;
-      if (drow < 0 || col >= N) continue;
-      const uint4 val = *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
-      uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
-      if (vec) {
-        *reinterpret_cast<uint4*>(dst) = val;
-      } else {
-        const uint32_t w[4] = {val.x, val.y, val.z, val.w};
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+    for (int pass = 0; pass < PASSES; ++pass) {
+      if (PASSES == 1 || wm == pass) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            float o[4];
+            outv(i, j, o);
+            const int srow = (BM / 2) * wm + 16 * j + l16 - pass * PROWS;
+            const uint32_t lo = to16<F16>(o[0]) | (to16<F16>(o[1]) << 16);
+            const uint32_t hi = to16<F16>(o[2]) | (to16<F16>(o[3]) << 16);
+            *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(i, 0)) = make_uint2(lo, hi);
+          }
       }
+      __syncthreads();
+      for (int idx = tid; idx < PROWS * CPR; idx += 512) {
+        const int srow = idx / CPR, ch = idx % CPR;
+        const int drow = s_drow[pass * PROWS + srow];
+        const int64_t col = n0 + ch * 8;
+        if (drow < 0 || col >= N) continue;
+        const uint4 val = *reinterpret_cast<const uint4*>(lds + srow * PITCH + ch * 16);
+        uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
+        if (vec) {
+          *reinterpret_cast<uint4*>(dst) = val;
+        } else {
+          const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+        }
+      }
+      if (pass + 1 < PASSES) __syncthreads();  // the staging area is rewritten
     }
   }
 }
@@ -471,11 +485,20 @@ bool wide8_supported(int recipe, const GemmArgs& a) {
          a.K / 128 <= MAX_KBLK;
 }
 
-// 128-slot blocks; fp8 block-scaled weights, K % 128 == 0, K <= 8192.
+bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K) {
+  const int64_t lim = int64_t(1) << 32;
+  return K % 128 == 0 && K > 0 && K / 128 <= MAX_KBLK && a_rows * K < lim && ldb_rows * K < lim;
+}
+
+// kWideBM-slot blocks; fp8 block-scaled weights, K % 128 == 0, K <= 8192.
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
                           int64_t max_blocks, void* qs, hipStream_t st) {
   if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
   MI_ARG(wide8_supported(recipe, a), "fp8 prefill GEMM: needs K % 128 == 0 and K <= 8192");
+  // activation rows: tokens (gathered) or padded slots (by position)
+  const int64_t a_rows = a.a_by_pos ? max_blocks * BM : a.num_valid;
+  MI_ARG(wide8_shape_ok(a_rows, a.ldb_rows, a.K),
+         "fp8 prefill GEMM: activation and per-expert weight bytes must stay below 4 GiB");
   if (qout) {
     MI_ARG(epi == EPI_GLU && a.N % 128 == 0,
            "fp8 activation output needs the GLU epilogue and I % 128 == 0");
