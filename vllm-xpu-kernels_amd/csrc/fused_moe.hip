@@ -89,6 +89,66 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
   }
 }
 
+// Decode: the split-K w2 partials summed and reduced over each token's top-k
+// slots in one launch.  Workgroup (tile, t) makes columns [256 tile, +256)
+// of token t:
+//   y[t, h] = bf16(sum_j w[t,j] * bf16(sum_z part(slot, h, z) + bias[e, h]))
+// with the slot's partial tile found through its sorted position
+// (inv_pos[t k + j], -1 for slots the sort dropped): four groups of 64
+// threads finish the slots j = g, g + 4, ... (4 columns per thread) into
+// LDS, then one group sums them in j order -- the same operations in the
+// same order as the STREAM finalize launch followed by
+// weighted_topk_sum_kernel.  Partial layout of a 256-column STREAM tile:
+// column c of slot m is float (2 (64 (c / 32) + 16 ((c % 16) / 4) + m) +
+// (c % 32) / 16) 4 + c % 4.
+constexpr int kFuseMaxTopk = 32;
+__global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
+    uint16_t* __restrict__ out, const float* __restrict__ part, int ks, int n_tiles,
+    const int32_t* __restrict__ inv_pos, const int32_t* __restrict__ block_expert,
+    const uint16_t* __restrict__ bias, const float* __restrict__ w, int topk, int64_t H) {
+  __shared__ float4 s_g[kFuseMaxTopk][64];
+  const int64_t t = blockIdx.y;
+  const int nt = blockIdx.x;
+  const int cg = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int c = 4 * cg;
+  const int64_t h = static_cast<int64_t>(nt) * 256 + c;  // H % 4 == 0: h < H covers h..h+3
+  const int wv = c / 32, tt = (c % 32) / 16, q = (c % 16) / 4;
+  for (int j = grp; j < topk; j += 4) {
+    const int pos = inv_pos[t * topk + j];
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (pos >= 0 && h < H) {
+      const int blk = pos / 16, m = pos % 16;
+      const float* tp = part + (static_cast<int64_t>(blk) * n_tiles + nt) * ks * 4096 +
+                        (2 * (64 * wv + 16 * q + m) + tt) * 4;
+      float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+      for (int z = 0; z < ks; ++z) {
+        const float4 a = *reinterpret_cast<const float4*>(tp + z * 4096);
+        v0 += a.x; v1 += a.y; v2 += a.z; v3 += a.w;
+      }
+      if (bias) {
+        const uint16_t* b = bias + static_cast<int64_t>(block_expert[blk]) * H + h;
+        v0 += bf16_to_f32(b[0]); v1 += bf16_to_f32(b[1]);
+        v2 += bf16_to_f32(b[2]); v3 += bf16_to_f32(b[3]);
+      }
+      g = make_float4(bf16_to_f32(f32_to_bf16(v0)), bf16_to_f32(f32_to_bf16(v1)),
+                      bf16_to_f32(f32_to_bf16(v2)), bf16_to_f32(f32_to_bf16(v3)));
+    }
+    s_g[j][cg] = g;
+  }
+  __syncthreads();
+  if (grp != 0 || h >= H) return;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int j = 0; j < topk; ++j) {
+    if (inv_pos[t * topk + j] < 0) continue;
+    const float wj = w[t * topk + j];
+    const float4 g = s_g[j][cg];
+    a0 += wj * g.x; a1 += wj * g.y; a2 += wj * g.z; a3 += wj * g.w;
+  }
+  *reinterpret_cast<uint2*>(out + t * H + h) =
+      make_uint2(f32_to_bf16(a0) | (uint32_t(f32_to_bf16(a1)) << 16),
+                 f32_to_bf16(a2) | (uint32_t(f32_to_bf16(a3)) << 16));
+}
+
 int group_quant_fp8(const void* x, int dt, uint8_t* q, float* s, int64_t rows,
                     int64_t cols, hipStream_t st) {
   return mi355moe_per_token_group_fp8_quant(x, dt, q, s, rows, cols, 128, 1e-10f,
@@ -103,6 +163,7 @@ struct FusedLayout {
   int32_t* cum;     // [E+1] padded slot start of every expert
   int ks1, ks2;     // STREAM split-K of w13 / w2 (1: none)
   float *part1, *part2;    // split-K partial tiles
+  int32_t* inv;     // [slots] sorted position of every flat slot (-1: dropped)
   int32_t* sortws;  // multi-workgroup sort scratch (sortws_bytes, may be 0)
   size_t sortws_bytes;
   uint8_t* xq;    // fp8 hidden [T, H]
@@ -145,6 +206,7 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     if (L.ks1 > 1) L.part1 = c.take<float>(L.max_blocks * nt1 * L.ks1 * tile_f);
     if (L.ks2 > 1) L.part2 = c.take<float>(L.max_blocks * nt2 * L.ks2 * tile_f);
   }
+  L.inv = c.take<int32_t>(std::max<int64_t>(L.slots, 1));
   L.sortws_bytes = counting_sort_ws_bytes(L.slots, E);
   L.sortws = c.take<int32_t>(static_cast<int64_t>(L.sortws_bytes / sizeof(int32_t)));
   const bool fp8 = a->recipe == MI355MOE_RECIPE_FP8BLOCK;
@@ -273,7 +335,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   if (int m = mark(0)) return m;
   int rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
                              a->expert_map, E, L.bm, L.sorted, L.max_padded,
-                             L.eids, L.max_blocks, L.ntp, nullptr, nullptr,
+                             L.eids, L.max_blocks, L.ntp, L.inv, nullptr,
                              static_cast<int32_t>(L.slots), L.sortws, L.sortws_bytes, st,
                              L.cum);
   if (rc) return rc;
@@ -338,9 +400,21 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.ksplit = L.ks2;
   g2.part = L.part2;
   g2.w_kblock = kb32;
+  // split-K decode: the partial sums are finished by the top-k reduction
+  const bool fuse_reduce = L.tile == TILE_STREAM && L.ks2 > 1 && k <= kFuseMaxTopk;
+  g2.partials_only = fuse_reduce;
   rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g2, L.grid_blocks, nullptr, st);
   if (rc) return rc;
   if (int m = mark(4)) return m;
+  if (fuse_reduce) {
+    dim3 grid(static_cast<unsigned>(cdiv(H, 256)), static_cast<unsigned>(T));
+    finalize_topk_sum_kernel<<<grid, dim3(256), 0, st>>>(
+        static_cast<uint16_t*>(a->output), L.part2, L.ks2, static_cast<int>(cdiv(H, 256)),
+        L.inv, L.eids, static_cast<const uint16_t*>(a->w2_bias), a->topk_weights,
+        static_cast<int>(k), H);
+    MI_LAUNCH_CHECK();
+    return mark(5);
+  }
 
   // Slots dropped by the sort (invalid or non-local experts) were never
   // written by the w2 GEMM; the reduction skips them by the same rule.

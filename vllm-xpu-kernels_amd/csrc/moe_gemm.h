@@ -50,6 +50,7 @@ struct GemmArgs {
   int32_t ksplit;        // 0 or 1: no split
   float* part;           // [blocks, n_tiles, ksplit, 512 x 8]
   int32_t finalize;      // set by the launcher for the second launch
+  int32_t partials_only; // split launch only: the caller consumes `part`
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };

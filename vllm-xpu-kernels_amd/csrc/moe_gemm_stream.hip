@@ -352,7 +352,7 @@ int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t s
   g.finalize = 0;
   moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(g, qs);
   MI_LAUNCH_CHECK();
-  if (a.ksplit > 1) {  // sum the partial tiles and run the epilogue
+  if (a.ksplit > 1 && !a.partials_only) {  // sum the partial tiles and run the epilogue
     grid.z = 1;
     g.finalize = 1;
     moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(g, qs);
