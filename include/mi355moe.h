@@ -58,15 +58,17 @@ typedef enum {
   MI355MOE_ACT_SWIGLUOAI = 1  /* interleaved gate/up, alpha 1.702, lim 7   */
 } mi355moe_activation;
 
-/* Layout of the fused layer's 16-bit weights.  NK is the canonical [E, N, K]
- * (K contiguous).  KB32 is the same data K-blocked, [E, K/32, N, 32]: the
- * 64-byte K-slices of consecutive weight rows are contiguous, so a kernel
- * that streams a 16-row weight fragment reads one 1 KiB run of HBM instead of
- * 16 runs of 64 bytes.  KB32 needs the bf16 recipe and K % 32 == 0 (hidden
- * and intermediate sizes); mi355moe_pack_weights_kb32 makes it. */
+/* Layout of the fused layer's bf16 and e4m3 weights.  NK is the canonical
+ * [E, N, K] (K contiguous).  KBLOCK is the same data K-blocked, [E, K/B, N, B]
+ * with B = 32 elements (64 bytes) for 16-bit and B = 128 (128 bytes) for e4m3
+ * weights: the K-slices of consecutive weight rows are contiguous, so a
+ * kernel that streams a 16-row weight fragment of one K stage reads one run of
+ * 1-2 KiB instead of 16 runs of 64-128 bytes.  KBLOCK needs the bf16 or
+ * fp8block recipe with hidden and intermediate sizes % B == 0, and fp8block
+ * sizes of at most 8192; mi355moe_pack_weights_kblock makes it. */
 typedef enum {
   MI355MOE_WLAYOUT_NK = 0,
-  MI355MOE_WLAYOUT_KB32 = 1
+  MI355MOE_WLAYOUT_KBLOCK = 1
 } mi355moe_weight_layout;
 
 const char* mi355moe_last_error(void);
@@ -266,12 +268,12 @@ typedef struct {
 
 /* One-time weight preparation, the counterpart of the repacking the
  * reference's XpuFusedMoe.__init__ does on its weights
- * (vllm_xpu_kernels/fused_moe_interface.py:194-206): src 16-bit [E, N, K]
- * -> dst [E, K/32, N, 32] (MI355MOE_WLAYOUT_KB32).  dtype BF16 or F16;
- * K % 32 == 0; src and dst must not overlap. */
-int mi355moe_pack_weights_kb32(const void* src, void* dst, int dtype,
-                               int64_t num_experts, int64_t N, int64_t K,
-                               void* stream);
+ * (vllm_xpu_kernels/fused_moe_interface.py:194-206): src [E, N, K] -> dst
+ * [E, K/B, N, B] (MI355MOE_WLAYOUT_KBLOCK): dtype BF16 or F16 (B = 32) or
+ * FP8E4M3 (B = 128); K % B == 0; src and dst must not overlap. */
+int mi355moe_pack_weights_kblock(const void* src, void* dst, int dtype,
+                                 int64_t num_experts, int64_t N, int64_t K,
+                                 void* stream);
 
 size_t mi355moe_fused_moe_workspace_size(const mi355moe_fused_moe_args* args);
 int mi355moe_fused_moe(const mi355moe_fused_moe_args* args, void* workspace,

@@ -75,12 +75,15 @@ def test_version_and_error_plumbing(lib):
                                        ctypes.c_int64(256), ctypes.c_int64(2), None,
                                        ctypes.c_size_t(0), None),
      b"% 128"),
-    (lambda L: L.mi355moe_pack_weights_kb32(None, None, 1, ctypes.c_int64(2),
-                                            ctypes.c_int64(64), ctypes.c_int64(48), None),
+    (lambda L: L.mi355moe_pack_weights_kblock(None, None, 1, ctypes.c_int64(2),
+                                              ctypes.c_int64(64), ctypes.c_int64(48), None),
      b"K % 32 == 0"),
-    (lambda L: L.mi355moe_pack_weights_kb32(None, None, 6, ctypes.c_int64(2),
-                                            ctypes.c_int64(64), ctypes.c_int64(64), None),
-     b"16-bit"),
+    (lambda L: L.mi355moe_pack_weights_kblock(None, None, 6, ctypes.c_int64(2),
+                                              ctypes.c_int64(64), ctypes.c_int64(96), None),
+     b"K % 128 == 0 (e4m3)"),
+    (lambda L: L.mi355moe_pack_weights_kblock(None, None, 0, ctypes.c_int64(2),
+                                              ctypes.c_int64(64), ctypes.c_int64(64), None),
+     b"16-bit or e4m3"),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, call, msg):
     rc = call(lib)
@@ -117,9 +120,14 @@ def test_fused_moe_workspace_query_and_validation(lib):
     a.hidden = 7168
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"need scales" in lib.mi355moe_last_error()
-    # the K-blocked layout is a bf16-only layout with K % 32 == 0
+    # the K-blocked layout: bf16 with K % 32 == 0 or fp8block with K <= 8192
     a.w_layout = 1
     a.w13_scale = a.w2_scale = 1
+    a.hidden = 8320
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"K-blocked weights need the bf16 recipe" in lib.mi355moe_last_error()
+    a.recipe = 2
+    a.hidden = 7168
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"K-blocked weights need the bf16 recipe" in lib.mi355moe_last_error()
     a.recipe, a.hidden = 0, 7176

@@ -384,23 +384,24 @@ def test_fused_moe_wide8_ragged(dev, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
-# ------------------------------------------------- K-blocked bf16 weights
-@pytest.mark.parametrize("shape", [(3, 72, 96), (2, 768, 2048), (1, 8, 32)])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_pack_weights_kb32_layout(dev, shape, dtype):
-    """[E, N, K] -> [E, K/32, N, 32]: element (e, n, k) lands at
-    (e, k // 32, n, k % 32)."""
-    from vllm_xpu_kernels.fused_moe_interface import pack_weights_kb32
+# ---------------------------------------------- K-blocked bf16 / fp8 weights
+@pytest.mark.parametrize("shape", [(3, 72, 256), (2, 768, 2048), (1, 8, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float8_e4m3fn])
+def test_pack_weights_kblock_layout(dev, shape, dtype):
+    """[E, N, K] -> [E, K/B, N, B] (B = 32 for 16-bit, 128 for e4m3): element
+    (e, n, k) lands at (e, k // B, n, k % B)."""
+    from vllm_xpu_kernels.fused_moe_interface import pack_weights_kblock
     E, N, K = shape
+    B = 128 if dtype == torch.float8_e4m3fn else 32
     g = torch.Generator().manual_seed(7)
     w = torch.randn(E, N, K, generator=g).to(dtype)
-    out = pack_weights_kb32(w.to(dev)).cpu()
-    assert out.shape == (E, K // 32, N, 32)
+    ib = torch.uint8 if B == 128 else torch.int16
+    out = pack_weights_kblock(w.to(dev)).cpu()
+    assert out.shape == (E, K // B, N, B)
     e, n, k = (torch.randint(0, d, (4096,), generator=g) for d in (E, N, K))
-    assert torch.equal(out[e, k // 32, n, k % 32].view(torch.int16),
-                       w[e, n, k].view(torch.int16))
-    assert torch.equal(out.view(torch.int16),
-                       w.view(E, N, K // 32, 32).permute(0, 2, 1, 3).contiguous().view(torch.int16))
+    assert torch.equal(out.view(ib)[e, k // B, n, k % B], w.view(ib)[e, n, k])
+    assert torch.equal(out.view(ib),
+                       w.view(ib).view(E, N, K // B, B).permute(0, 2, 1, 3).contiguous())
 
 
 def _layer_both_layouts(cfg, T, dev, monkeypatch):
@@ -413,7 +414,7 @@ def _layer_both_layouts(cfg, T, dev, monkeypatch):
 
 
 @pytest.mark.parametrize("T", [1, 16, 256, 512, 1024, 2048])
-def test_fused_moe_kb32_equals_nk_c2(dev, monkeypatch, T):
+def test_fused_moe_kblock_equals_nk_c2(dev, monkeypatch, T):
     """The K-blocked layout changes addresses only: every kernel family (T=1
     split-K stream, 16/256 stream, 512/1024 small, 2048 wide) gives the
     row-major layer's output bit for bit, and that output meets the oracle."""
@@ -426,7 +427,7 @@ def test_fused_moe_kb32_equals_nk_c2(dev, monkeypatch, T):
 
 @pytest.mark.parametrize("T", [8, 96, 160, 1024])
 @pytest.mark.parametrize("activation", ["silu", "swigluoai"])
-def test_fused_moe_kb32_ragged(dev, monkeypatch, activation, T):
+def test_fused_moe_kblock_ragged(dev, monkeypatch, activation, T):
     """H=352 / I=224: K loops that end inside a 128-wide stage (stream,
     small) and GLU tiles with rows past I, over the K-blocked weights."""
     import dataclasses
@@ -435,6 +436,31 @@ def test_fused_moe_kb32_ragged(dev, monkeypatch, activation, T):
     (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
     assert torch.equal(out, out_nk)
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
+
+
+@pytest.mark.parametrize("T", [8, 96, 160, 300, 500, 1024])
+def test_fused_moe_kblock_fp8_families(dev, monkeypatch, T):
+    """fp8 block-scaled weights K-blocked in 128-byte blocks (H=384, I=256,
+    8 experts, top-2: about T/4 slots per expert): stream (T=8, 96), small
+    (160, 300), 128-slot 8-wave (500) and 320-slot (1024) kernels each give
+    the row-major layer's output bit for bit, within the fp8 bar of the
+    oracle."""
+    import dataclasses
+    cfg = dataclasses.replace(_W().CONFIGS["C2"], recipe="fp8block", hidden=384, inter=256,
+                              experts=8, topk=2)
+    (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
+    assert torch.equal(out, out_nk)
+    _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_fused_moe_kblock_fp8_c3_decode(dev, monkeypatch, T):
+    """DeepSeek-V3 shapes at decode (split-K stream kernels): K-blocked and
+    row-major fp8 weights give the same layer output bit for bit."""
+    (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(_W().CONFIGS["C3"], T, dev,
+                                                             monkeypatch)
+    assert torch.equal(out, out_nk)
+    _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
 @pytest.mark.parametrize("name,T,sample", [("C2", 4096, 24), ("C3", 8192, 6),

@@ -182,9 +182,11 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H) &&
                        wide_ok_for(a->recipe, L.slots + E * kWideBM, H, I);
   L.tile = pick_tile(a->recipe, wide_ok, L.slots, E, &L.bm);
-  // K-blocked weights: the families that read them (STREAM, SMALL, WIDE)
-  if (a->w_layout == MI355MOE_WLAYOUT_KB32 && L.tile != TILE_STREAM &&
-      L.tile != TILE_SMALL && L.tile != TILE_WIDE) {
+  // K-blocked weights: the families that read them (STREAM, SMALL, WIDE, and
+  // BIG for fp8, whose 8-wave kernel takes K <= 8192)
+  if (a->w_layout == MI355MOE_WLAYOUT_KBLOCK && L.tile != TILE_STREAM &&
+      L.tile != TILE_SMALL && L.tile != TILE_WIDE &&
+      !(L.tile == TILE_BIG && a->recipe == MI355MOE_RECIPE_FP8BLOCK)) {
     L.tile = TILE_SMALL;
     L.bm = 64;
   }
@@ -315,12 +317,13 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
     MI_ARG(H % 8 == 0 && I % 8 == 0, "bf16 weights need K % 8 == 0");
   }
-  MI_ARG(a->w_layout == MI355MOE_WLAYOUT_NK || a->w_layout == MI355MOE_WLAYOUT_KB32,
+  MI_ARG(a->w_layout == MI355MOE_WLAYOUT_NK || a->w_layout == MI355MOE_WLAYOUT_KBLOCK,
          "unknown weight layout");
-  const bool kb32 = a->w_layout == MI355MOE_WLAYOUT_KB32;
-  MI_ARG(!kb32 || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0),
-         "K-blocked weights need the bf16 recipe and hidden and intermediate "
-         "sizes % 32 == 0");
+  const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
+  MI_ARG(!kblock || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0) ||
+             (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && I <= 8192),
+         "K-blocked weights need the bf16 recipe (hidden and intermediate sizes "
+         "% 32 == 0) or the fp8block recipe (sizes at most 8192)");
   if (T == 0) return MI355MOE_OK;
   FusedLayout L = plan(a, static_cast<uint8_t*>(ws));
   MI_CHECK(ws && ws_bytes >= L.bytes, MI355MOE_ERR_WORKSPACE,
@@ -373,7 +376,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.act = a->activation;
   g1.ksplit = L.ks1;
   g1.part = L.part1;
-  g1.w_kblock = kb32;
+  g1.w_kblock = kblock;
   rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
   if (rc) return rc;
   if (int m = mark(3)) return m;
@@ -399,7 +402,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.up_off = 0;
   g2.ksplit = L.ks2;
   g2.part = L.part2;
-  g2.w_kblock = kb32;
+  g2.w_kblock = kblock;
   // split-K decode: the partial sums are finished by the top-k reduction
   const bool fuse_reduce = L.tile == TILE_STREAM && L.ks2 > 1 && k <= kFuseMaxTopk;
   g2.partials_only = fuse_reduce;
@@ -554,43 +557,49 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
 
 // ------------------------------------------------- K-blocked weight packing
 namespace {
-// dst[e][kb][n][32] = src[e][n][32 kb .. 32 kb + 31]; one thread moves one
-// 16-byte chunk, destination-ordered so the writes are contiguous.
-__global__ __launch_bounds__(256) void pack_kb32_kernel(const uint4* __restrict__ src,
-                                                        uint4* __restrict__ dst,
-                                                        int64_t N, int64_t K,
-                                                        int64_t chunks) {
+// dst[e][kb][n][B bytes] = src[e][n][B kb .. B kb + B); one thread moves one
+// 16-byte chunk (cpb chunks per block row), destination-ordered so the
+// writes are contiguous.
+__global__ __launch_bounds__(256) void pack_kblock_kernel(const uint4* __restrict__ src,
+                                                          uint4* __restrict__ dst,
+                                                          int64_t N, int64_t row_chunks,
+                                                          int cpb, int64_t chunks) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= chunks) return;
-  const int c = static_cast<int>(i & 3);
-  const int64_t row = i >> 2;  // (e, kb, n)
+  const int c = static_cast<int>(i % cpb);
+  const int64_t row = i / cpb;  // (e, kb, n)
   const int64_t n = row % N;
   const int64_t ekb = row / N;
-  const int64_t nkb = K / 32;
+  const int64_t nkb = row_chunks / cpb;
   const int64_t e = ekb / nkb, kb = ekb % nkb;
-  dst[i] = src[((e * N + n) * K + kb * 32) / 8 + c];
+  dst[i] = src[(e * N + n) * row_chunks + kb * cpb + c];
 }
 }  // namespace
 
-extern "C" int mi355moe_pack_weights_kb32(const void* src, void* dst, int dtype,
-                                          int64_t num_experts, int64_t N, int64_t K,
-                                          void* stream) {
+extern "C" int mi355moe_pack_weights_kblock(const void* src, void* dst, int dtype,
+                                            int64_t num_experts, int64_t N, int64_t K,
+                                            void* stream) {
   using namespace mi355;
-  MI_ARG(dtype == MI355MOE_BF16 || dtype == MI355MOE_F16, "weights must be 16-bit");
-  MI_ARG(num_experts > 0 && N > 0 && K > 0 && K % 32 == 0,
-         "K-blocked packing needs positive sizes and K % 32 == 0");
+  MI_ARG(dtype == MI355MOE_BF16 || dtype == MI355MOE_F16 || dtype == MI355MOE_FP8E4M3,
+         "weights must be 16-bit or e4m3");
+  const int eb = dtype == MI355MOE_FP8E4M3 ? 1 : 2;       // bytes per element
+  const int kblk = dtype == MI355MOE_FP8E4M3 ? 128 : 32;  // elements per K block
+  MI_ARG(num_experts > 0 && N > 0 && K > 0 && K % kblk == 0,
+         "K-blocked packing needs positive sizes and K % 32 == 0 (16-bit) or "
+         "K % 128 == 0 (e4m3)");
   MI_ARG(src && dst && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
              (reinterpret_cast<uintptr_t>(dst) & 15) == 0,
          "weights must be 16-byte aligned");
-  const int64_t bytes = num_experts * N * K * 2;
+  const int64_t bytes = num_experts * N * K * eb;
   const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
   MI_ARG(s0 + bytes <= d0 || d0 + bytes <= s0, "src and dst overlap");
   const int64_t chunks = bytes / 16;
   const int64_t blocks = cdiv(chunks, 256);
   MI_ARG(blocks < (int64_t(1) << 31), "weights too large");
-  pack_kb32_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint4*>(src), static_cast<uint4*>(dst), N, K, chunks);
+  pack_kblock_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint4*>(src), static_cast<uint4*>(dst), N, K * eb / 16,
+      kblk * eb / 16, chunks);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }

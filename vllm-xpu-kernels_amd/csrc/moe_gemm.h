@@ -37,10 +37,11 @@ struct GemmArgs {
   float limit;           // swigluoai limit
   int32_t act;           // mi355moe_activation
   int32_t out_f16;       // store fp16 instead of bf16 (recipe BF16 only)
-  // Weight layout (recipe BF16): 0 row-major [E, ldb_rows, K]; 1 K-blocked
-  // [E, K/32, ldb_rows, 32] (K % 32 == 0), in which the 64-byte K-slices
-  // of consecutive weight rows are contiguous, so a 16-row fragment of one
-  // K-block is a single 1 KiB run of HBM instead of 16 runs of 64 bytes.
+  // Weight layout: 0 row-major [E, ldb_rows, K]; 1 K-blocked [E, K/B,
+  // ldb_rows, B] (recipe BF16: B = 32, recipe FP8BLOCK: B = 128 elements),
+  // in which the K-slices of consecutive weight rows are contiguous, so a
+  // 16-row fragment of one K block is a single 1-2 KiB run of HBM instead of
+  // 16 runs of 64-128 bytes.
   int32_t w_kblock;
   // STREAM family split-K: ksplit workgroups share one output tile, each
   // summing 1/ksplit of the K stages into an fp32 partial tile in `part`; a
@@ -67,6 +68,11 @@ __device__ __forceinline__ WStride w_stride16(const GemmArgs& a) {
 }
 __device__ __forceinline__ int64_t w_koff16(const WStride& s, int64_t k) {
   return (k >> 5) * s.kblk + (k & 31) * 2;
+}
+// e4m3 weights (K blocks of 128 bytes): element (row r, k) at r * row +
+// (k / 128) * kblk + k % 128.
+__device__ __forceinline__ WStride w_stride8(const GemmArgs& a) {
+  return a.w_kblock ? WStride{128, a.ldb_rows * 128} : WStride{a.K, 128};
 }
 
 // Tile t of the (block, N-tile) grid.  With expert_cum the order is (expert,

@@ -117,8 +117,8 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
   const int64_t nbase = static_cast<int64_t>(blockIdx.x) * BN + wave * WN;
   const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
-  // 16-bit weights may be K-blocked; fp8 and mxfp4 weights are row-major
-  const WStride wst = kFp8 || kFp4 ? WStride{wrow_bytes, 0} : w_stride16(a);
+  // bf16 and fp8 weights may be K-blocked; mxfp4 weights are row-major
+  const WStride wst = kFp4 ? WStride{wrow_bytes, 0} : (kFp8 ? w_stride8(a) : w_stride16(a));
   const uint8_t* wptr[NB];
   bool wok[NB];
   int64_t wrow[NB];
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if constexpr (kFp8) {
-        const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + k0 + 32 * q);
+        const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (k0 >> 7) * wst.kblk + 32 * q);
         wf[0][j][0] = wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
         wf[0][j][1] = wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
         const float* bs = static_cast<const float*>(a.b_scale);
@@ -386,10 +386,14 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
 int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
                      const GemmArgs& a, int64_t max_blocks, void* qs,
                      hipStream_t st) {
-  MI_ARG(!a.w_kblock || (recipe == MI355MOE_RECIPE_BF16 && a.K % 32 == 0 &&
-                         (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE)),
-         "K-blocked weights need the bf16 recipe, K % 32 == 0 and the stream, "
-         "small or wide tile");
+  MI_ARG(!a.w_kblock ||
+             (recipe == MI355MOE_RECIPE_BF16 && a.K % 32 == 0 &&
+              (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE)) ||
+             (recipe == MI355MOE_RECIPE_FP8BLOCK &&
+              (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
+               (tile == TILE_BIG && big8_supported(recipe, a)))),
+         "K-blocked weights need the bf16 (K % 32 == 0) or fp8block recipe and a "
+         "kernel family that reads them");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:

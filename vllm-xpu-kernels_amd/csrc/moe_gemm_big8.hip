@@ -139,7 +139,8 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
   __shared__ float s_wsc[2][MAX_KBLK];  // weight-block scales of the tile's two row blocks
   __shared__ float s_amax[4][BM];       // QOUT: per-wave-column row maxima
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, g = lane >> 4;
 
@@ -188,6 +189,11 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
   // DMA sources: blocks b = 6 wave + q of a stage, activation rows for b < 16
   // (8 rows each), weight rows after; wave 0 also moves the activation
   // scales of the stage's 128-K block (128 floats, two 256-byte DMAs).
+  // weights may be K-blocked: bytes between two K stages of a weight row
+  const WStride wst = w_stride8(a);
+  auto kstep = [&](int q) -> int64_t {  // uniform: activation or weight source
+    return DMA_PER_WAVE * wave + q < 16 ? static_cast<int64_t>(ROWB) : wst.kblk;
+  };
   const uint8_t* src[DMA_PER_WAVE];
   {
     const uint8_t* abase = static_cast<const uint8_t*>(a.A);
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
         const int ar = s_arow[r];
         src[q] = abase + static_cast<int64_t>(ar >= 0 ? ar : 0) * K + c * 16;
       } else {
-        src[q] = wexp + wrow_of(r) * K + c * 16;
+        src[q] = wexp + wrow_of(r) * wst.row + c * 16;
       }
     }
   }
@@ -218,10 +224,9 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
   const uint32_t dst0 = DMA_PER_WAVE * wave * 1024;
   auto issue = [&](int kt) {
     const uint32_t base = ring0 + (kt % NSTAGE) * STAGE;
-    const int64_t koff = static_cast<int64_t>(kt) * ROWB;
 #pragma unroll
     for (int q = 0; q < DMA_PER_WAVE; ++q)
-      dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(base + dst0 + q * 1024));
+      dma16(src[q] + kt * kstep(q), __builtin_amdgcn_readfirstlane(base + dst0 + q * 1024));
     if (wave == 0) {
       dma4(ssrc0 + kt, __builtin_amdgcn_readfirstlane(base + S_OFF));
       dma4(ssrc1 + kt, __builtin_amdgcn_readfirstlane(base + S_OFF + 256));
@@ -287,7 +292,7 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
     __builtin_amdgcn_s_barrier();
     const bool dma = kt + NSTAGE < nk;
     const uint32_t dbase = ring0 + (kt % NSTAGE) * STAGE;
-    const int64_t koff = static_cast<int64_t>(kt + NSTAGE) * ROWB;
+    const int kn = kt + NSTAGE;  // stage whose DMA goes out in this iteration
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // four MFMAs in flight, then their scale FMAs
@@ -306,7 +311,7 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
 #pragma unroll
         for (int q = 2 * i; q < 2 * i + 2; ++q)
           if (q < DMA_PER_WAVE)
-            dma16(src[q] + koff, __builtin_amdgcn_readfirstlane(dbase + dst0 + q * 1024));
+            dma16(src[q] + kn * kstep(q), __builtin_amdgcn_readfirstlane(dbase + dst0 + q * 1024));
         if (i == 3 && wave == 0) {
           dma4(ssrc0 + (kt + NSTAGE), __builtin_amdgcn_readfirstlane(dbase + S_OFF));
           dma4(ssrc1 + (kt + NSTAGE), __builtin_amdgcn_readfirstlane(dbase + S_OFF + 256));

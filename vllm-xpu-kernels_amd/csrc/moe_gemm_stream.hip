@@ -119,8 +119,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     wok[t] = n < N;
     wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
   }
-  // 16-bit weights may be K-blocked; fp8 and mxfp4 weights are row-major
-  const WStride wst = kFp8 || kFp4 ? WStride{wrow_bytes, 0} : w_stride16(a);
+  // bf16 and fp8 weights may be K-blocked; mxfp4 weights are row-major
+  const WStride wst = kFp4 ? WStride{wrow_bytes, 0} : (kFp8 ? w_stride8(a) : w_stride16(a));
   const uint8_t* wp0 = wexp + wrow[0] * wst.row;
   const uint8_t* wp1 = wexp + wrow[1] * wst.row;
   const int arow = s_arow[l16];
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     if constexpr (kFp8) {  // K % 128 == 0: no tail
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint8_t* p = (t ? wp1 : wp0) + k0 + 32 * q;
+        const uint8_t* p = (t ? wp1 : wp0) + (k0 >> 7) * wst.kblk + 32 * q;
         f.w[t][0] = *reinterpret_cast<const uint4*>(p);
         f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
         f.ws[t] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) * (K / 128) + k0 / 128];

@@ -174,7 +174,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       return c < N ? c : 0;
     }
   };
-  if (tid < BN) s_woff[tid] = static_cast<uint32_t>(wrow_of(tid) * K);
+  // weights may be K-blocked: row stride and bytes between two K stages
+  const WStride wst = w_stride8(a);
+  if (tid < BN) s_woff[tid] = static_cast<uint32_t>(wrow_of(tid) * wst.row);
   {
     const float* bsc = static_cast<const float*>(a.b_scale);
     for (int i = tid; i < 2 * nkb; i += 512) {
@@ -213,9 +215,11 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
   const int* arow_s = s_arow + d0 * 64 + lane;
   const uint32_t c0 = static_cast<uint32_t>((lane & 7) ^ (lane >> 4)) << 4;
   const uint32_t Ku = static_cast<uint32_t>(K), nkbu = static_cast<uint32_t>(nkb);
+  const uint32_t wkstep = static_cast<uint32_t>(wst.kblk);
   auto issue = [&](int kt) {
     const uint32_t base = ring0 + (kt & 1) * STAGE;
     const uint32_t kofs = static_cast<uint32_t>(kt) * ROWB;
+    const uint32_t wkofs = static_cast<uint32_t>(kt) * wkstep;
     if (a_wave) {
       const uint32_t dst = base + b0 * 1024;
 #pragma unroll
@@ -231,7 +235,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       const uint32_t dst = base + A_BYTES + b0 * 1024;
 #pragma unroll
       for (int q = 0; q < W_BLK; ++q) {
-        const uint32_t off = woff_w[q * 8] + kofs + (c0 ^ ((q & 1) << 6));
+        const uint32_t off = woff_w[q * 8] + wkofs + (c0 ^ ((q & 1) << 6));
         dma16(off, wbase, __builtin_amdgcn_readfirstlane(dst + q * 1024));
       }
       const uint32_t sdst = base + S_OFF + d0 * 256;

@@ -497,9 +497,9 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
            "fused_moe");
 }
 
-// Not a reference op: one-time K-blocked repacking of 16-bit [E, N, K]
-// weights into dst [E, K/32, N, 32] (XpuFusedMoe.__init__).
-void mi355_pack_weights_kb32(const at::Tensor& src, at::Tensor& dst) {
+// Not a reference op: one-time K-blocked repacking of [E, N, K] weights into
+// dst [E, K/B, N, B] (B = 32 for 16-bit, 128 for e4m3; XpuFusedMoe.__init__).
+void mi355_pack_weights_kblock(const at::Tensor& src, at::Tensor& dst) {
   check_gpu(src, "src");
   check_gpu(dst, "dst");
   TORCH_CHECK(src.dim() == 3 && src.is_contiguous() && dst.is_contiguous(),
@@ -507,10 +507,10 @@ void mi355_pack_weights_kb32(const at::Tensor& src, at::Tensor& dst) {
   TORCH_CHECK(dst.scalar_type() == src.scalar_type() && dst.numel() == src.numel(),
               "dst must match src in dtype and size");
   DevGuard g(src.device());
-  check_rc(mi355moe_pack_weights_kb32(src.data_ptr(), dst.data_ptr(),
-                                      dtype_code(src.scalar_type()), src.size(0),
-                                      src.size(1), src.size(2), cur_stream(src)),
-           "pack_weights_kb32");
+  check_rc(mi355moe_pack_weights_kblock(src.data_ptr(), dst.data_ptr(),
+                                        dtype_code(src.scalar_type()), src.size(0),
+                                        src.size(1), src.size(2), cur_stream(src)),
+           "pack_weights_kblock");
 }
 
 }  // namespace
@@ -542,7 +542,7 @@ TORCH_LIBRARY(_moe_C, m) {
         "Tensor topk_ids, Tensor w13, Tensor? w13_scale, Tensor? w13_bias, Tensor w2, "
         "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
         "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0) -> ()");
-  m.def("mi355_pack_weights_kb32(Tensor src, Tensor! dst) -> ()");
+  m.def("mi355_pack_weights_kblock(Tensor src, Tensor! dst) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
@@ -555,7 +555,7 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("init_expert_map", &init_expert_map);
   m.impl("remap_hidden_states", &remap_hidden_states);
   m.impl("mi355_fused_moe", &mi355_fused_moe);
-  m.impl("mi355_pack_weights_kb32", &mi355_pack_weights_kb32);
+  m.impl("mi355_pack_weights_kblock", &mi355_pack_weights_kblock);
 }
 
 TORCH_LIBRARY_IMPL(_moe_C, Meta, m) { m.impl("grouped_topk", &grouped_topk_meta); }

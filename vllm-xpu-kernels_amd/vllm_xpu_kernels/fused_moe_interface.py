@@ -5,9 +5,11 @@
 the layout the gfx950 kernels stream: every expert matrix [N, K] with K
 contiguous, swigluoai's interleaved gate/up rows split into a gate half and an
 up half, and bf16 weights with K % 32 == 0 (hidden and intermediate sizes)
-further K-blocked to [E, K/32, N, 32] (``mi355_pack_weights_kb32``), so that
-the decode kernels read each 16-row weight fragment as one contiguous 1 KiB
-run.  ``MI355MOE_WEIGHT_LAYOUT=nk`` keeps the row-major [E, N, K] layout.
+or fp8 block-scaled weights with K <= 8192 further K-blocked to [E, K/B, N, B]
+(B = 32 bf16 / 128 e4m3 elements, ``mi355_pack_weights_kblock``), so that
+the kernels read each 16-row weight fragment of a K stage as one contiguous
+1-2 KiB run.  ``MI355MOE_WEIGHT_LAYOUT=nk`` keeps the row-major [E, N, K]
+layout.
 ``apply`` makes one call, ``torch.ops._moe_C.mi355_fused_moe``, which
 launches the whole layer on the current stream without synchronising the
 host.
@@ -26,7 +28,7 @@ FP8_BLOCK_SIZE = 128
 
 RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4 = 0, 1, 2
 ACT_SILU, ACT_SWIGLUOAI = 0, 1
-WLAYOUT_NK, WLAYOUT_KB32 = 0, 1
+WLAYOUT_NK, WLAYOUT_KBLOCK = 0, 1
 WEIGHT_LAYOUT_ENV = "MI355MOE_WEIGHT_LAYOUT"
 
 
@@ -68,11 +70,13 @@ def _deinterleave_rows(t: torch.Tensor, dim: int) -> torch.Tensor:
     return torch.cat([even, odd], dim=dim).contiguous()
 
 
-def pack_weights_kb32(w: torch.Tensor) -> torch.Tensor:
-    """16-bit [E, N, K] -> K-blocked [E, K/32, N, 32] on the device."""
+def pack_weights_kblock(w: torch.Tensor) -> torch.Tensor:
+    """[E, N, K] -> K-blocked [E, K/B, N, B] on the device (B = 32 for 16-bit,
+    128 for e4m3 weights)."""
     E, N, K = w.shape
-    out = torch.empty((E, K // 32, N, 32), dtype=w.dtype, device=w.device)
-    torch.ops._moe_C.mi355_pack_weights_kb32(w.contiguous(), out)
+    B = 128 if w.element_size() == 1 else 32
+    out = torch.empty((E, K // B, N, B), dtype=w.dtype, device=w.device)
+    torch.ops._moe_C.mi355_pack_weights_kblock(w.contiguous(), out)
     return out
 
 
@@ -181,10 +185,11 @@ class XpuFusedMoe:
         assert w13c.shape[0] == E and w13c.shape[1] == 2 * I
         H = w13c.shape[2]
         self._w_layout = WLAYOUT_NK
-        if (self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0 and
-                os.environ.get(WEIGHT_LAYOUT_ENV, "kb32").lower() != "nk"):
-            w13c, w2c = pack_weights_kb32(w13c), pack_weights_kb32(w2c)
-            self._w_layout = WLAYOUT_KB32
+        kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
+                  (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and I <= 8192))
+        if kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk":
+            w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)
+            self._w_layout = WLAYOUT_KBLOCK
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
         self.w13_bias, self.w2_bias = b13c, b2c
