@@ -344,7 +344,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 
 template <int RECIPE, int EPI, bool QOUT>
 int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
-  constexpr int PD = RECIPE == MI355MOE_RECIPE_BF16 ? 2 : 4;
+  constexpr int PD = 2;  // stages in flight per wave (deeper costs occupancy, measured no faster)
   const int64_t cols = EPI == EPI_GLU ? 128 : 256;
   dim3 grid(static_cast<unsigned>(cdiv(a.N, cols)), static_cast<unsigned>(max_blocks),
             static_cast<unsigned>(a.ksplit > 1 ? a.ksplit : 1));
