@@ -296,15 +296,16 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
       read_frag<NJ>(f0, lds, xoff[0], woff[0], WSTEP);
       read_frag<NJ>(f1, lds, xoff[1], woff[1], WSTEP);
     }
+    // The next stage's fragment reads are unconditional (after the last
+    // stage they read a stale slot, unused): reads under a condition make
+    // the compiler copy every loop-carried fragment register where the
+    // branches join.
     for (int kt = 0; kt < nk; ++kt) {
       mfma_step<NJ>(acc, f0, false, voff, sbase0, 0, 0, 0);
-      const bool more = kt + 1 < nk;
-      if (more) {
-        // stage kt+1 landed; stage kt+2 (if issued) may pend
-        wait_vm_dyn(kt + 2 < nk ? nd : 0);
-        __builtin_amdgcn_s_barrier();
-        read_frag<NJ>(f0, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[0], woff[0], WSTEP);
-      }
+      // stage kt+1 landed; stage kt+2 (if issued) may pend
+      wait_vm_dyn(kt + 2 < nk ? nd : 0);
+      __builtin_amdgcn_s_barrier();
+      read_frag<NJ>(f0, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[0], woff[0], WSTEP);
       const bool dma = kt + 3 < nk;
       const uint8_t* sb = sbase0 + static_cast<int64_t>(kt + 3) * kstep;
       const uint32_t dbase = ring0 + ((kt + 3) % NSTAGE) * STAGE + dst0;
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
           if (q < nd) dma16(voff[q], sb, __builtin_amdgcn_readfirstlane(dbase + q * 1024));
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (more) read_frag<NJ>(f1, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[1], woff[1], WSTEP);
+      read_frag<NJ>(f1, lds + ((kt + 1) % NSTAGE) * STAGE, xoff[1], woff[1], WSTEP);
     }
   };
   switch (nj) {
