@@ -58,14 +58,15 @@ typedef enum {
   MI355MOE_ACT_SWIGLUOAI = 1  /* interleaved gate/up, alpha 1.702, lim 7   */
 } mi355moe_activation;
 
-/* Layout of the fused layer's bf16 and e4m3 weights.  NK is the canonical
- * [E, N, K] (K contiguous).  KBLOCK is the same data K-blocked, [E, K/B, N, B]
- * with B = 32 elements (64 bytes) for 16-bit and B = 128 (128 bytes) for e4m3
- * weights: the K-slices of consecutive weight rows are contiguous, so a
- * kernel that streams a 16-row weight fragment of one K stage reads one run of
- * 1-2 KiB instead of 16 runs of 64-128 bytes.  KBLOCK needs the bf16 or
- * fp8block recipe with hidden and intermediate sizes % B == 0, and fp8block
- * sizes of at most 8192; mi355moe_pack_weights_kblock makes it. */
+/* Layout of the fused layer's weights.  NK is the canonical [E, N, K] (K
+ * contiguous).  KBLOCK is the same data K-blocked, [E, K/B, N, B] with
+ * B = 32 values (64 bytes) for 16-bit, B = 128 (128 bytes) for e4m3 and
+ * B = 32 (16 bytes) for e2m1 weights, whose e8m0 scales are then [E, K/32, N]:
+ * the K-slices of consecutive weight rows are contiguous, so a kernel that
+ * streams a 16-row weight fragment of one K stage reads one run of 0.25-2 KiB
+ * instead of 16 short runs.  KBLOCK needs hidden and intermediate sizes
+ * % B == 0 and, for fp8block, of at most 8192; mi355moe_pack_weights_kblock
+ * and mi355moe_pack_scales_kblock make it. */
 typedef enum {
   MI355MOE_WLAYOUT_NK = 0,
   MI355MOE_WLAYOUT_KBLOCK = 1
@@ -269,11 +270,16 @@ typedef struct {
 /* One-time weight preparation, the counterpart of the repacking the
  * reference's XpuFusedMoe.__init__ does on its weights
  * (vllm_xpu_kernels/fused_moe_interface.py:194-206): src [E, N, K] -> dst
- * [E, K/B, N, B] (MI355MOE_WLAYOUT_KBLOCK): dtype BF16 or F16 (B = 32) or
- * FP8E4M3 (B = 128); K % B == 0; src and dst must not overlap. */
+ * [E, K/B, N, B] (MI355MOE_WLAYOUT_KBLOCK): dtype BF16 or F16 (B = 32),
+ * FP8E4M3 (B = 128) or U8 = packed e2m1 pairs (B = 32 values = 16 bytes; K
+ * counts values); K % B == 0; src and dst must not overlap. */
 int mi355moe_pack_weights_kblock(const void* src, void* dst, int dtype,
                                  int64_t num_experts, int64_t N, int64_t K,
                                  void* stream);
+/* mxfp4 e8m0 scales for MI355MOE_WLAYOUT_KBLOCK: u8 [E, N, kblocks] ->
+ * [E, kblocks, N] (kblocks = K/32); src and dst must not overlap. */
+int mi355moe_pack_scales_kblock(const void* src, void* dst, int64_t num_experts,
+                                int64_t N, int64_t kblocks, void* stream);
 
 size_t mi355moe_fused_moe_workspace_size(const mi355moe_fused_moe_args* args);
 int mi355moe_fused_moe(const mi355moe_fused_moe_args* args, void* workspace,

@@ -83,7 +83,13 @@ def test_version_and_error_plumbing(lib):
      b"K % 128 == 0 (e4m3)"),
     (lambda L: L.mi355moe_pack_weights_kblock(None, None, 0, ctypes.c_int64(2),
                                               ctypes.c_int64(64), ctypes.c_int64(64), None),
-     b"16-bit or e4m3"),
+     b"16-bit, e4m3 or packed e2m1"),
+    (lambda L: L.mi355moe_pack_weights_kblock(None, None, 7, ctypes.c_int64(2),
+                                              ctypes.c_int64(64), ctypes.c_int64(48), None),
+     b"K % 32 == 0 (16-bit, e2m1)"),
+    (lambda L: L.mi355moe_pack_scales_kblock(None, None, ctypes.c_int64(2),
+                                             ctypes.c_int64(64), ctypes.c_int64(0), None),
+     b"positive sizes"),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, call, msg):
     rc = call(lib)
@@ -124,10 +130,6 @@ def test_fused_moe_workspace_query_and_validation(lib):
     a.w_layout = 1
     a.w13_scale = a.w2_scale = 1
     a.hidden = 8320
-    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
-    assert rc == -1 and b"K-blocked weights need the bf16 recipe" in lib.mi355moe_last_error()
-    a.recipe = 2
-    a.hidden = 7168
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"K-blocked weights need the bf16 recipe" in lib.mi355moe_last_error()
     a.recipe, a.hidden = 0, 7176

@@ -453,6 +453,35 @@ def test_fused_moe_kblock_fp8_families(dev, monkeypatch, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
+@pytest.mark.parametrize("shape", [(3, 72, 256), (2, 64, 2880)])
+def test_pack_mxfp4_kblock_layout(dev, shape):
+    """e2m1 pairs u8 [E, N, K/2] -> [E, K/32, N, 16] and e8m0 scales
+    [E, N, K/32] -> [E, K/32, N]."""
+    from vllm_xpu_kernels.fused_moe_interface import pack_scales_kblock, pack_weights_kblock
+    E, N, K = shape
+    g = torch.Generator().manual_seed(9)
+    w = torch.randint(0, 256, (E, N, K // 2), generator=g, dtype=torch.uint8)
+    sc = torch.randint(0, 256, (E, N, K // 32), generator=g, dtype=torch.uint8)
+    pw = pack_weights_kblock(w.to(dev)).cpu()
+    ps = pack_scales_kblock(sc.to(dev)).cpu()
+    assert pw.shape == (E, K // 32, N, 16) and ps.shape == (E, K // 32, N)
+    assert torch.equal(pw, w.view(E, N, K // 32, 16).permute(0, 2, 1, 3))
+    assert torch.equal(ps, sc.permute(0, 2, 1))
+
+
+@pytest.mark.parametrize("T", [8, 96, 160, 1024])
+def test_fused_moe_kblock_mxfp4_families(dev, monkeypatch, T):
+    """mxfp4 weights and e8m0 scales K-blocked (32-value blocks; H=320,
+    I=256, swigluoai with biases, 8 experts, top-2): stream (T=8, 96), small
+    (160) and 128-slot register-staged (1024) kernels give the row-major
+    layer's output bit for bit, within the bar of the oracle."""
+    import dataclasses
+    cfg = dataclasses.replace(_W().CONFIGS["C5"], hidden=320, inter=256, experts=8, topk=2)
+    (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
+    assert torch.equal(out, out_nk)
+    _close(out, _oracle_layer(cfg, w, x, tw, ti))
+
+
 @pytest.mark.parametrize("T", [1, 16])
 def test_fused_moe_kblock_fp8_c3_decode(dev, monkeypatch, T):
     """DeepSeek-V3 shapes at decode (split-K stream kernels): K-blocked and

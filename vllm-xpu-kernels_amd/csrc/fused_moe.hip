@@ -183,9 +183,9 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
                        wide_ok_for(a->recipe, L.slots + E * kWideBM, H, I);
   L.tile = pick_tile(a->recipe, wide_ok, L.slots, E, &L.bm);
   // K-blocked weights: the families that read them (STREAM, SMALL, WIDE, and
-  // BIG for fp8, whose 8-wave kernel takes K <= 8192)
-  if (a->w_layout == MI355MOE_WLAYOUT_KBLOCK && L.tile != TILE_STREAM &&
-      L.tile != TILE_SMALL && L.tile != TILE_WIDE &&
+  // BIG for fp8, whose 8-wave kernel takes K <= 8192, and for mxfp4)
+  if (a->w_layout == MI355MOE_WLAYOUT_KBLOCK && a->recipe != MI355MOE_RECIPE_MXFP4 &&
+      L.tile != TILE_STREAM && L.tile != TILE_SMALL && L.tile != TILE_WIDE &&
       !(L.tile == TILE_BIG && a->recipe == MI355MOE_RECIPE_FP8BLOCK)) {
     L.tile = TILE_SMALL;
     L.bm = 64;
@@ -321,9 +321,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
          "unknown weight layout");
   const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
   MI_ARG(!kblock || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0) ||
-             (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && I <= 8192),
+             (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && I <= 8192) ||
+             recipe == MI355MOE_RECIPE_MXFP4,
          "K-blocked weights need the bf16 recipe (hidden and intermediate sizes "
-         "% 32 == 0) or the fp8block recipe (sizes at most 8192)");
+         "% 32 == 0), the fp8block recipe (sizes at most 8192) or mxfp4");
   if (T == 0) return MI355MOE_OK;
   FusedLayout L = plan(a, static_cast<uint8_t*>(ws));
   MI_CHECK(ws && ws_bytes >= L.bytes, MI355MOE_ERR_WORKSPACE,
@@ -580,17 +581,21 @@ extern "C" int mi355moe_pack_weights_kblock(const void* src, void* dst, int dtyp
                                             int64_t num_experts, int64_t N, int64_t K,
                                             void* stream) {
   using namespace mi355;
-  MI_ARG(dtype == MI355MOE_BF16 || dtype == MI355MOE_F16 || dtype == MI355MOE_FP8E4M3,
-         "weights must be 16-bit or e4m3");
-  const int eb = dtype == MI355MOE_FP8E4M3 ? 1 : 2;       // bytes per element
-  const int kblk = dtype == MI355MOE_FP8E4M3 ? 128 : 32;  // elements per K block
+  MI_ARG(dtype == MI355MOE_BF16 || dtype == MI355MOE_F16 || dtype == MI355MOE_FP8E4M3 ||
+             dtype == MI355MOE_U8,
+         "weights must be 16-bit, e4m3 or packed e2m1 pairs (u8)");
+  // bytes per K block: 32 16-bit values, 128 e4m3 values, 32 e2m1 values;
+  // K counts values
+  const int64_t blk_bytes = dtype == MI355MOE_FP8E4M3 ? 128 : (dtype == MI355MOE_U8 ? 16 : 64);
+  const int64_t kblk = dtype == MI355MOE_FP8E4M3 ? 128 : 32;
   MI_ARG(num_experts > 0 && N > 0 && K > 0 && K % kblk == 0,
-         "K-blocked packing needs positive sizes and K % 32 == 0 (16-bit) or "
+         "K-blocked packing needs positive sizes and K % 32 == 0 (16-bit, e2m1) or "
          "K % 128 == 0 (e4m3)");
+  const int64_t row_bytes = K / kblk * blk_bytes;
   MI_ARG(src && dst && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
              (reinterpret_cast<uintptr_t>(dst) & 15) == 0,
          "weights must be 16-byte aligned");
-  const int64_t bytes = num_experts * N * K * eb;
+  const int64_t bytes = num_experts * N * row_bytes;
   const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
   MI_ARG(s0 + bytes <= d0 || d0 + bytes <= s0, "src and dst overlap");
   const int64_t chunks = bytes / 16;
@@ -598,8 +603,40 @@ extern "C" int mi355moe_pack_weights_kblock(const void* src, void* dst, int dtyp
   MI_ARG(blocks < (int64_t(1) << 31), "weights too large");
   pack_kblock_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                        static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint4*>(src), static_cast<uint4*>(dst), N, K * eb / 16,
-      kblk * eb / 16, chunks);
+      static_cast<const uint4*>(src), static_cast<uint4*>(dst), N, row_bytes / 16,
+      static_cast<int>(blk_bytes / 16), chunks);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+namespace {
+// dst[e][kb][n] = src[e][n][kb] (bytes), one thread per destination byte.
+__global__ __launch_bounds__(256) void pack_scales_kernel(const uint8_t* __restrict__ src,
+                                                          uint8_t* __restrict__ dst,
+                                                          int64_t N, int64_t KB,
+                                                          int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t n = i % N;
+  const int64_t ekb = i / N;
+  const int64_t e = ekb / KB, kb = ekb % KB;
+  dst[i] = src[(e * N + n) * KB + kb];
+}
+}  // namespace
+
+extern "C" int mi355moe_pack_scales_kblock(const void* src, void* dst, int64_t num_experts,
+                                           int64_t N, int64_t kblocks, void* stream) {
+  using namespace mi355;
+  MI_ARG(num_experts > 0 && N > 0 && kblocks > 0, "scale packing needs positive sizes");
+  MI_ARG(src && dst, "null scales");
+  const int64_t total = num_experts * N * kblocks;
+  const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), d0 = reinterpret_cast<uintptr_t>(dst);
+  MI_ARG(s0 + total <= d0 || d0 + total <= s0, "src and dst overlap");
+  const int64_t blocks = cdiv(total, 256);
+  MI_ARG(blocks < (int64_t(1) << 31), "scales too large");
+  pack_scales_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), N, kblocks, total);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }

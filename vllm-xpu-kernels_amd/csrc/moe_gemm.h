@@ -38,7 +38,8 @@ struct GemmArgs {
   int32_t act;           // mi355moe_activation
   int32_t out_f16;       // store fp16 instead of bf16 (recipe BF16 only)
   // Weight layout: 0 row-major [E, ldb_rows, K]; 1 K-blocked [E, K/B,
-  // ldb_rows, B] (recipe BF16: B = 32, recipe FP8BLOCK: B = 128 elements),
+  // ldb_rows, B] (recipe BF16: B = 32, FP8BLOCK: B = 128, MXFP4: B = 32
+  // elements, with the e8m0 scales K-blocked too, [E, K/32, ldb_rows]),
   // in which the K-slices of consecutive weight rows are contiguous, so a
   // 16-row fragment of one K block is a single 1-2 KiB run of HBM instead of
   // 16 runs of 64-128 bytes.
@@ -73,6 +74,15 @@ __device__ __forceinline__ int64_t w_koff16(const WStride& s, int64_t k) {
 // (k / 128) * kblk + k % 128.
 __device__ __forceinline__ WStride w_stride8(const GemmArgs& a) {
   return a.w_kblock ? WStride{128, a.ldb_rows * 128} : WStride{a.K, 128};
+}
+// mxfp4 e2m1 pairs (K blocks of 32 values = 16 bytes): block kb of row r at
+// r * row + kb * kblk; its e8m0 scale byte at r * row + kb * kblk of
+// s_stride4 (row-major scales [E, N, K/32], K-blocked [E, K/32, N]).
+__device__ __forceinline__ WStride w_stride4(const GemmArgs& a) {
+  return a.w_kblock ? WStride{16, a.ldb_rows * 16} : WStride{a.K / 2, 16};
+}
+__device__ __forceinline__ WStride s_stride4(const GemmArgs& a) {
+  return a.w_kblock ? WStride{1, a.ldb_rows} : WStride{a.K / 32, 1};
 }
 
 // Tile t of the (block, N-tile) grid.  With expert_cum the order is (expert,

@@ -117,8 +117,9 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
   const int64_t nbase = static_cast<int64_t>(blockIdx.x) * BN + wave * WN;
   const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
-  // bf16 and fp8 weights may be K-blocked; mxfp4 weights are row-major
-  const WStride wst = kFp4 ? WStride{wrow_bytes, 0} : (kFp8 ? w_stride8(a) : w_stride16(a));
+  // weights (and mxfp4 scales) may be K-blocked
+  const WStride wst = kFp4 ? w_stride4(a) : (kFp8 ? w_stride8(a) : w_stride16(a));
+  const WStride sst = s_stride4(a);
   const uint8_t* wptr[NB];
   bool wok[NB];
   int64_t wrow[NB];
@@ -153,11 +154,12 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
                         (K / 128) + k0 / 128];
       } else if constexpr (kFp4) {
         const bool ok = wok[j] && 32 * q < kb;
-        uint4 v = ok ? *reinterpret_cast<const uint4*>(wptr[j] + (k0 + 32 * q) / 2)
+        const int64_t blk32 = (k0 + 32 * q) / 32;  // the lane's 32-value K block
+        uint4 v = ok ? *reinterpret_cast<const uint4*>(wptr[j] + blk32 * wst.kblk)
                      : make_uint4(0, 0, 0, 0);
         const uint8_t* bs = static_cast<const uint8_t*>(a.b_scale);
-        uint32_t ex = ok ? bs[(static_cast<int64_t>(e) * a.ldb_rows + wrow[j]) *
-                                  (K / 32) + (k0 + 32 * q) / 32]
+        uint32_t ex = ok ? bs[static_cast<int64_t>(e) * a.ldb_rows * (K / 32) +
+                              wrow[j] * sst.row + blk32 * sst.kblk]
                          : 0u;
         if (ex == 0u) v = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> scale 0
         const float sc = __uint_as_float(ex << 23);
@@ -391,9 +393,10 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE)) ||
              (recipe == MI355MOE_RECIPE_FP8BLOCK &&
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
-               (tile == TILE_BIG && big8_supported(recipe, a)))),
-         "K-blocked weights need the bf16 (K % 32 == 0) or fp8block recipe and a "
-         "kernel family that reads them");
+               (tile == TILE_BIG && big8_supported(recipe, a)))) ||
+             (recipe == MI355MOE_RECIPE_MXFP4 && tile != TILE_WIDE),
+         "K-blocked weights need the bf16 (K % 32 == 0), fp8block or mxfp4 "
+         "recipe and a kernel family that reads them");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:

@@ -96,6 +96,12 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
   }
   const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
                         static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
+  // mxfp4 weights and scales may be K-blocked (16-bit and fp8 weights here
+  // are row-major)
+  const WStride wst = kFp4 ? w_stride4(a) : WStride{wrow_bytes, 0};
+  const WStride sst = s_stride4(a);
+  const uint8_t* const sexp = static_cast<const uint8_t*>(a.b_scale) +
+                              (kFp4 ? static_cast<int64_t>(e) * a.ldb_rows * (K / 32) : 0);
   const uint8_t* wsrc[NW];
   bool wokv[NW];
   int64_t wrowv[NW];
@@ -108,7 +114,7 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
     const int64_t n = tile_wrow(r, n0, kGlu, a.up_off, N, ok);
     wokv[i] = ok;
     wrowv[i] = n;
-    wsrc[i] = wexp + n * wrow_bytes + c * 16;
+    wsrc[i] = kFp4 ? wexp + n * wst.row + c * wst.kblk : wexp + n * wrow_bytes + c * 16;
   }
 
   uint4 ra[NA], rw[NW];
@@ -129,12 +135,9 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
       if constexpr (kFp4) {
         const int c = idx % 2;  // 16 bytes = 32 e2m1 values = one scale group
         const bool ok = wokv[i] && 32 * c < kb;
-        rw[i] = ok ? *reinterpret_cast<const uint4*>(wsrc[i] + k0 / 2)
+        rw[i] = ok ? *reinterpret_cast<const uint4*>(wsrc[i] + (k0 / 32) * wst.kblk)
                    : make_uint4(0, 0, 0, 0);
-        rsc[i] = ok ? static_cast<const uint8_t*>(a.b_scale)
-                          [(static_cast<int64_t>(e) * a.ldb_rows + wrowv[i]) * (K / 32) +
-                           k0 / 32 + c]
-                    : 0u;
+        rsc[i] = ok ? sexp[wrowv[i] * sst.row + (k0 / 32 + c) * sst.kblk] : 0u;
       } else {
         const int c = idx % (ROWB / 16);
         const bool ok = wokv[i] && (c * 16) < kb * (kFp8 ? 1 : 2);

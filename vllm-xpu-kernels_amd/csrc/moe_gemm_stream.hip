@@ -119,8 +119,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     wok[t] = n < N;
     wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
   }
-  // bf16 and fp8 weights may be K-blocked; mxfp4 weights are row-major
-  const WStride wst = kFp4 ? WStride{wrow_bytes, 0} : (kFp8 ? w_stride8(a) : w_stride16(a));
+  // weights (and mxfp4 scales) may be K-blocked
+  const WStride wst = kFp4 ? w_stride4(a) : (kFp8 ? w_stride8(a) : w_stride16(a));
+  const WStride sst = s_stride4(a);
   const uint8_t* wp0 = wexp + wrow[0] * wst.row;
   const uint8_t* wp1 = wexp + wrow[1] * wst.row;
   const int arow = s_arow[l16];
@@ -156,9 +157,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       const int64_t kc = k < K ? k : K - 32;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        f.w[t] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + kc / 2);
+        f.w[t] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + (kc / 32) * wst.kblk);
         f.sc[t] = static_cast<const uint8_t*>(a.b_scale)
-            [(static_cast<int64_t>(e) * a.ldb_rows + wrow[t]) * (K / 32) + kc / 32];
+            [static_cast<int64_t>(e) * a.ldb_rows * (K / 32) + wrow[t] * sst.row + (kc / 32) * sst.kblk];
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) f.x[s] = *reinterpret_cast<const uint4*>(xp + (kc + 8 * s) * 2);

@@ -507,10 +507,26 @@ void mi355_pack_weights_kblock(const at::Tensor& src, at::Tensor& dst) {
   TORCH_CHECK(dst.scalar_type() == src.scalar_type() && dst.numel() == src.numel(),
               "dst must match src in dtype and size");
   DevGuard g(src.device());
-  check_rc(mi355moe_pack_weights_kblock(src.data_ptr(), dst.data_ptr(),
-                                        dtype_code(src.scalar_type()), src.size(0),
-                                        src.size(1), src.size(2), cur_stream(src)),
+  const int dt = dtype_code(src.scalar_type());
+  // packed e2m1 pairs: K counts values, two per byte
+  const int64_t K = dt == MI355MOE_U8 ? 2 * src.size(2) : src.size(2);
+  check_rc(mi355moe_pack_weights_kblock(src.data_ptr(), dst.data_ptr(), dt, src.size(0),
+                                        src.size(1), K, cur_stream(src)),
            "pack_weights_kblock");
+}
+
+// Not a reference op: mxfp4 e8m0 scales u8 [E, N, K/32] -> [E, K/32, N].
+void mi355_pack_scales_kblock(const at::Tensor& src, at::Tensor& dst) {
+  check_gpu(src, "src");
+  check_gpu(dst, "dst");
+  TORCH_CHECK(src.dim() == 3 && src.is_contiguous() && dst.is_contiguous() &&
+                  src.element_size() == 1 && dst.element_size() == 1 &&
+                  dst.numel() == src.numel(),
+              "src must be a contiguous byte [E, N, K/32] tensor and dst match it");
+  DevGuard g(src.device());
+  check_rc(mi355moe_pack_scales_kblock(src.data_ptr(), dst.data_ptr(), src.size(0),
+                                       src.size(1), src.size(2), cur_stream(src)),
+           "pack_scales_kblock");
 }
 
 }  // namespace
@@ -543,6 +559,7 @@ TORCH_LIBRARY(_moe_C, m) {
         "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
         "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0) -> ()");
   m.def("mi355_pack_weights_kblock(Tensor src, Tensor! dst) -> ()");
+  m.def("mi355_pack_scales_kblock(Tensor src, Tensor! dst) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
@@ -556,6 +573,7 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("remap_hidden_states", &remap_hidden_states);
   m.impl("mi355_fused_moe", &mi355_fused_moe);
   m.impl("mi355_pack_weights_kblock", &mi355_pack_weights_kblock);
+  m.impl("mi355_pack_scales_kblock", &mi355_pack_scales_kblock);
 }
 
 TORCH_LIBRARY_IMPL(_moe_C, Meta, m) { m.impl("grouped_topk", &grouped_topk_meta); }

@@ -71,12 +71,24 @@ def _deinterleave_rows(t: torch.Tensor, dim: int) -> torch.Tensor:
 
 
 def pack_weights_kblock(w: torch.Tensor) -> torch.Tensor:
-    """[E, N, K] -> K-blocked [E, K/B, N, B] on the device (B = 32 for 16-bit,
-    128 for e4m3 weights)."""
-    E, N, K = w.shape
-    B = 128 if w.element_size() == 1 else 32
-    out = torch.empty((E, K // B, N, B), dtype=w.dtype, device=w.device)
+    """[E, N, K] -> K-blocked [E, K/B, N, B] on the device: B = 32 values for
+    16-bit, 128 for e4m3 weights; packed e2m1 pairs (uint8 [E, N, K/2]) go to
+    [E, K/32, N, 16]."""
+    E, N, Kb = w.shape
+    if w.dtype == torch.uint8:        # e2m1 pairs: 16 bytes per 32 values
+        B = 16
+    else:
+        B = 128 if w.element_size() == 1 else 32
+    out = torch.empty((E, Kb // B, N, B), dtype=w.dtype, device=w.device)
     torch.ops._moe_C.mi355_pack_weights_kblock(w.contiguous(), out)
+    return out
+
+
+def pack_scales_kblock(s: torch.Tensor) -> torch.Tensor:
+    """mxfp4 e8m0 scales uint8 [E, N, K/32] -> [E, K/32, N] on the device."""
+    E, N, KB = s.shape
+    out = torch.empty((E, KB, N), dtype=s.dtype, device=s.device)
+    torch.ops._moe_C.mi355_pack_scales_kblock(s.contiguous(), out)
     return out
 
 
@@ -185,10 +197,15 @@ class XpuFusedMoe:
         assert w13c.shape[0] == E and w13c.shape[1] == 2 * I
         H = w13c.shape[2]
         self._w_layout = WLAYOUT_NK
+        if self._recipe == RECIPE_MXFP4:
+            H = w13c.shape[2] * 2
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
-                  (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and I <= 8192))
+                  (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and I <= 8192) or
+                  self._recipe == RECIPE_MXFP4)
         if kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk":
             w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)
+            if self._recipe == RECIPE_MXFP4:
+                s13c, s2c = pack_scales_kblock(s13c), pack_scales_kblock(s2c)
             self._w_layout = WLAYOUT_KBLOCK
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
