@@ -416,7 +416,7 @@ def _layer_both_layouts(cfg, T, dev, monkeypatch):
 @pytest.mark.parametrize("T", [1, 16, 256, 512, 1024, 2048])
 def test_fused_moe_kblock_equals_nk_c2(dev, monkeypatch, T):
     """The K-blocked layout changes addresses only: every kernel family (T=1
-    split-K stream, 16/256 stream, 512/1024 small, 2048 wide) gives the
+    split-K stream, 16 stream, 256/512 small, 1024/2048 wide) gives the
     row-major layer's output bit for bit, and that output meets the oracle."""
     (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(_W().CONFIGS["C2"], T, dev,
                                                              monkeypatch)
@@ -438,11 +438,11 @@ def test_fused_moe_kblock_ragged(dev, monkeypatch, activation, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
 
 
-@pytest.mark.parametrize("T", [8, 96, 160, 300, 500, 1024])
+@pytest.mark.parametrize("T", [8, 32, 48, 96, 500, 1024])
 def test_fused_moe_kblock_fp8_families(dev, monkeypatch, T):
     """fp8 block-scaled weights K-blocked in 128-byte blocks (H=384, I=256,
-    8 experts, top-2: about T/4 slots per expert): stream (T=8, 96), small
-    (160, 300), 128-slot 8-wave (500) and 320-slot (1024) kernels each give
+    8 experts, top-2: about T/4 slots per expert): stream (T=8), small
+    (32, 48), 128-slot 8-wave (96, 500) and 320-slot (1024) kernels each give
     the row-major layer's output bit for bit, within the fp8 bar of the
     oracle."""
     import dataclasses
@@ -469,17 +469,71 @@ def test_pack_mxfp4_kblock_layout(dev, shape):
     assert torch.equal(ps, sc.permute(0, 2, 1))
 
 
-@pytest.mark.parametrize("T", [8, 96, 160, 1024])
+@pytest.mark.parametrize("T", [8, 96, 160])
 def test_fused_moe_kblock_mxfp4_families(dev, monkeypatch, T):
     """mxfp4 weights and e8m0 scales K-blocked (32-value blocks; H=320,
-    I=256, swigluoai with biases, 8 experts, top-2): stream (T=8, 96), small
-    (160) and 128-slot register-staged (1024) kernels give the row-major
+    I=256, swigluoai with biases, 8 experts, top-2): stream (T=8) and small
+    (96: 16-slot blocks, 160: 32-slot blocks) kernels give the row-major
     layer's output bit for bit, within the bar of the oracle."""
     import dataclasses
     cfg = dataclasses.replace(_W().CONFIGS["C5"], hidden=320, inter=256, experts=8, topk=2)
     (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
     assert torch.equal(out, out_nk)
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
+
+
+def _assert_near_layouts(out, out_nk):
+    """Two kernel families over the same operands: fp32 sums in different
+    orders, so the bf16 outputs may differ in the last place only."""
+    a, b = out.float(), out_nk.float()
+    assert torch.isfinite(a).all()
+    assert ((a - b).abs() <= 1e-2 * b.abs() + 1e-3).all()
+
+
+@pytest.mark.parametrize("shape", [(320, 256, 1024), (320, 256, 2000), (352, 160, 700),
+                                   (96, 64, 1200)])
+def test_fused_moe_mxfp4_wide(dev, monkeypatch, shape):
+    """K-blocked mxfp4 layers whose experts average > 96 slots run the
+    320-slot mxfp4 kernel (row-major weights: the 128-slot register-staged
+    one): H=320 / I=256 (10 and 8 K stages), H=352 / I=160 (11 and 5 K
+    stages: GLU and STORE tiles with columns past N), H=96 / I=64 (K loops
+    shorter than the DMA lookahead).  Within the oracle's bar and near the
+    row-major layer's output."""
+    import dataclasses
+    H, I, T = shape
+    cfg = dataclasses.replace(_W().CONFIGS["C5"], hidden=H, inter=I, experts=8, topk=2)
+    (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
+    _assert_near_layouts(out, out_nk)
+    toks = torch.linspace(0, T - 1, min(T, 64)).long().to(dev)
+    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks))
+
+
+@pytest.mark.parametrize("hot", [0.0, 0.6, 1.0])
+def test_fused_moe_mxfp4_wide_skewed(dev, hot):
+    """Skewed routing over the 320-slot mxfp4 kernel: a share `hot` of the
+    tokens put expert 3 first, so the experts hold from a few slots (blocks
+    with one or two 32-row groups) to several full 320-slot blocks."""
+    import dataclasses
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    W = _W()
+    T = 1500
+    cfg = dataclasses.replace(W.CONFIGS["C5"], hidden=320, inter=256, experts=8, topk=2)
+    w = W.make_weights(cfg, dev)
+    x = W.make_activations(cfg, T, dev, seed=5)
+    g = torch.Generator().manual_seed(17)
+    first = torch.where(torch.rand(T, generator=g) < hot, torch.full((T,), 3),
+                        torch.randint(0, 8, (T,), generator=g))
+    second = (first + 1 + torch.randint(0, 7, (T,), generator=g)) % 8
+    ti = torch.stack([first, second], 1).to(torch.int32).to(dev)
+    tw = torch.rand(T, 2, generator=g) + 0.1
+    tw = (tw / tw.sum(1, keepdim=True)).to(dev)
+    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                      cfg.topk, cfg.activation, cfg.experts)
+    assert moe._w_layout == 1
+    out = torch.empty_like(x)
+    moe.apply(out, x, tw, ti)
+    toks = torch.linspace(0, T - 1, 96).long().to(dev)
+    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks))
 
 
 @pytest.mark.parametrize("T", [1, 16])

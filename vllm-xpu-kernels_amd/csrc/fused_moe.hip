@@ -179,12 +179,13 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   const int64_t E = a->num_experts;
   L.slots = a->num_tokens * a->topk;
   const int64_t H = a->hidden, I = a->inter;
-  const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H) &&
-                       wide_ok_for(a->recipe, L.slots + E * kWideBM, H, I);
+  const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
+  const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H, kblock) &&
+                       wide_ok_for(a->recipe, L.slots + E * kWideBM, H, I, kblock);
   L.tile = pick_tile(a->recipe, wide_ok, L.slots, E, &L.bm);
   // K-blocked weights: the families that read them (STREAM, SMALL, WIDE, and
   // BIG for fp8, whose 8-wave kernel takes K <= 8192, and for mxfp4)
-  if (a->w_layout == MI355MOE_WLAYOUT_KBLOCK && a->recipe != MI355MOE_RECIPE_MXFP4 &&
+  if (kblock && a->recipe != MI355MOE_RECIPE_MXFP4 &&
       L.tile != TILE_STREAM && L.tile != TILE_SMALL && L.tile != TILE_WIDE &&
       !(L.tile == TILE_BIG && a->recipe == MI355MOE_RECIPE_FP8BLOCK)) {
     L.tile = TILE_SMALL;

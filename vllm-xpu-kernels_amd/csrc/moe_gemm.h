@@ -109,18 +109,25 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int t, int n_tile
 int launch_moe_gemm(int recipe, int epi, int bm, const GemmArgs& a,
                     int64_t max_blocks, hipStream_t st);
 
-// Choose the M tile for an expected number of rows per active expert.
+// Block size by the expected rows per active expert (16 up to 24, 32 up to
+// 48, 64 up to 96, else 128): the SMALL family's block when forced.
 int pick_block_m(int64_t slots, int64_t num_experts);
 
-// Kernel family by the expected rows per active expert:
-//   <= 24   STREAM: independent-wave weight streaming, 16-slot blocks
-//   <= 96   SMALL:  LDS-shared activation tile, 32/64-slot blocks
-//   >  96   WIDE:   bf16 weights (fp8 block-scaled: > 160 rows) whose
-//                   shapes the WIDE kernels take (wide_ok, see wide_ok_for):
-//                   320x256 tiles, 320-slot blocks (kWideBM)
-//           BIG:    otherwise, 128x256 LDS-staged tiles, 128-slot blocks
+// Kernel family and block size by recipe and the expected slots per active
+// expert (avg), break points measured over the benchmark configurations
+// (bf16 Qwen3-30B-A3B, fp8 DeepSeek-V3 and Qwen3-235B, mxfp4 gpt-oss-20b,
+// 1..8192 tokens, every family forced in turn):
+//   bf16   avg <= 10 STREAM;  <= 48 SMALL bm 64;                     else WIDE
+//   fp8    avg <= 4  STREAM;  <= 12 SMALL bm 16;   <= 160 BIG;        else WIDE
+//   mxfp4  avg <= 2  STREAM;  <= 24 SMALL bm 16;   <= 40 SMALL bm 32; else WIDE
+// STREAM: independent-wave weight streaming, 16-slot blocks; SMALL: LDS-shared
+// activation tile; BIG: 128x256 LDS-staged tiles, 128-slot blocks; WIDE:
+// 320x256 tiles, 320-slot blocks (kWideBM), where the shape fits (wide_ok,
+// see wide_ok_for; otherwise bf16 SMALL bm 64 up to avg 96, mxfp4 SMALL bm 32
+// up to 48, then BIG).
 // MI355MOE_GEMM_TILE=stream|small|big|bigreg|wide overrides (A/B
-// measurements; wide falls back to big where it does not apply).
+// measurements; wide falls back to big where it does not apply, small takes
+// pick_block_m's block size).
 // (TILE_BIG runs the 8-wave fp8 kernel where big8_supported(), else the
 // LDS-DMA pipelined kernel where pipe_supported(), else the register-staged
 // one, which TILE_BIGREG forces.)
@@ -128,8 +135,9 @@ enum GemmTile { TILE_STREAM = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_BIGREG = 3, 
 constexpr int kWideBM = 320;  // slots per block of the WIDE family
 GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm);
 // Whether a GEMM with a_rows activation rows, ldb_rows weight rows per
-// expert (0: not known yet) and reduction length K fits the WIDE kernels.
-bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K);
+// expert (0: not known yet), reduction length K and the given weight layout
+// fits the WIDE kernels (mxfp4: K-blocked weights only).
+bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w_kblock = false);
 
 // Launch the chosen family over max_blocks blocks of bm slots.
 int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
@@ -163,6 +171,11 @@ bool wide_supported(int recipe, const GemmArgs& a);
 bool wide_offsets_fit(int64_t a_rows, int64_t ldb_rows, int64_t K);
 int launch_moe_gemm_wide(int recipe, int epi, const GemmArgs& a,
                          int64_t max_blocks, hipStream_t st);
+// kWideBM-slot blocks, K-blocked mxfp4 weights and scales, K % 32 == 0, N and
+// ldb_rows % 4 == 0 (moe_gemm_wide4.hip).
+bool wide4_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t N, int64_t K);
+int launch_moe_gemm_wide4(int recipe, int epi, const GemmArgs& a,
+                          int64_t max_blocks, hipStream_t st);
 // 16-slot blocks; GLU blocks cover 128 output columns, STORE blocks 256.
 int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
                            int64_t max_blocks, void* qs, hipStream_t st);

@@ -353,9 +353,11 @@ int pick_block_m(int64_t slots, int64_t num_experts) {
   return 128;
 }
 
-bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K) {
+bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w_kblock) {
   if (recipe == MI355MOE_RECIPE_BF16) return K % 32 == 0 && wide_offsets_fit(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) return wide8_shape_ok(a_rows, ldb_rows, K);
+  if (recipe == MI355MOE_RECIPE_MXFP4)
+    return w_kblock && wide4_shape_ok(a_rows, ldb_rows, ldb_rows, K);
   return false;
 }
 
@@ -370,18 +372,39 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     if (!strcmp(v, "wide")) return static_cast<int>(TILE_WIDE);
     return -1;
   }();
-  // fp8: a 320-slot stage is 73 KB, so its kernel keeps one stage of DMA in
-  // flight against the 128-slot kernel's two; it wins where experts average
-  // well above 128 slots (fewer weight passes), not at about 128.
   const int64_t active = slots < num_experts ? slots : num_experts;
   const int64_t avg = active > 0 ? slots / active : 0;
-  const bool wide = wide_ok && (recipe == MI355MOE_RECIPE_BF16 ||
-                                (recipe == MI355MOE_RECIPE_FP8BLOCK && avg > 160));
-  const int m = pick_block_m(slots, num_experts);
-  GemmTile t = m == 16 ? TILE_STREAM : (m == 128 ? (wide ? TILE_WIDE : TILE_BIG) : TILE_SMALL);
-  if (force >= 0) t = static_cast<GemmTile>(force);
-  if (t == TILE_WIDE && !wide) t = TILE_BIG;
-  *bm = t == TILE_STREAM ? 16 : (t == TILE_WIDE ? kWideBM : ((t == TILE_BIG || t == TILE_BIGREG) ? 128 : m));
+  GemmTile t;
+  int b;
+  if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
+    // a 320-slot fp8 stage is 73 KB, so the WIDE kernel keeps one stage of
+    // DMA in flight against the 128-slot kernel's two: it wins where experts
+    // average well above 128 slots (fewer weight passes), not at about 128
+    if (avg <= 4) t = TILE_STREAM, b = 16;
+    else if (avg <= 12) t = TILE_SMALL, b = 16;
+    else if (avg > 160 && wide_ok) t = TILE_WIDE, b = kWideBM;
+    else t = TILE_BIG, b = 128;
+  } else if (recipe == MI355MOE_RECIPE_MXFP4) {
+    if (avg <= 2) t = TILE_STREAM, b = 16;
+    else if (avg <= 24) t = TILE_SMALL, b = 16;
+    else if (avg <= 40 || (!wide_ok && avg <= 48)) t = TILE_SMALL, b = 32;
+    else if (wide_ok) t = TILE_WIDE, b = kWideBM;
+    else t = TILE_BIG, b = 128;
+  } else {
+    if (avg <= 10) t = TILE_STREAM, b = 16;
+    else if (avg <= 48 || (!wide_ok && avg <= 96)) t = TILE_SMALL, b = 64;
+    else if (wide_ok) t = TILE_WIDE, b = kWideBM;
+    else t = TILE_BIG, b = 128;
+  }
+  if (force >= 0) {
+    t = static_cast<GemmTile>(force);
+    if (t == TILE_WIDE && !wide_ok) t = TILE_BIG;
+    b = t == TILE_STREAM ? 16
+        : t == TILE_WIDE ? kWideBM
+        : (t == TILE_BIG || t == TILE_BIGREG) ? 128
+                                              : pick_block_m(slots, num_experts);
+  }
+  *bm = b;
   return t;
 }
 
@@ -394,7 +417,7 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
              (recipe == MI355MOE_RECIPE_FP8BLOCK &&
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
                (tile == TILE_BIG && big8_supported(recipe, a)))) ||
-             (recipe == MI355MOE_RECIPE_MXFP4 && tile != TILE_WIDE),
+             recipe == MI355MOE_RECIPE_MXFP4,
          "K-blocked weights need the bf16 (K % 32 == 0), fp8block or mxfp4 "
          "recipe and a kernel family that reads them");
   switch (tile) {
@@ -410,6 +433,8 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
       if (recipe == MI355MOE_RECIPE_FP8BLOCK)
         return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
       MI_ARG(!qout, "wide GEMM: no fp8 activation output");
+      if (recipe == MI355MOE_RECIPE_MXFP4)
+        return launch_moe_gemm_wide4(recipe, epi, a, max_blocks, st);
       return launch_moe_gemm_wide(recipe, epi, a, max_blocks, st);
     default: return launch_moe_gemm_q(recipe, epi, qout, bm, a, max_blocks, qs, st);
   }
