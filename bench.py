@@ -240,6 +240,53 @@ SWEEP = [("C1", 64), ("C2", 1), ("C2", 16), ("C2", 64), ("C2", 256), ("C2", 4096
          ("C5", 4096)]
 
 
+def op_bandwidth(dev, steps):
+    """Standalone ops of the path at the shapes they see inside the layers
+    (C3 DeepSeek-V3 T=8192: 65536 slots, I=2048, H=7168; C5 gpt-oss-20b
+    T=4096: 16384 slots, I=2880; C2 Qwen3-30B-A3B T=4096: 32768 slots,
+    I=768): algorithmic bytes (inputs read once, outputs written once) over
+    the mean time of `steps` launches between HIP events on torch's current
+    stream, which the ops launch on."""
+    from vllm_xpu_kernels import ops
+    g = torch.Generator(device=dev).manual_seed(3)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=g, device=dev).bfloat16()
+
+    cases = [
+        ("silu_and_mul_per_block_quant e4m3 g128", (65536, 2048),
+         lambda x: ops.silu_and_mul_per_block_quant(x, 128, torch.float8_e4m3fn),
+         lambda T, H: T * 2 * H * 2 + T * H + T * (H // 128) * 4),
+        ("silu_and_mul_mxfp4_quant", (16384, 2880),
+         lambda x: ops.silu_and_mul_mxfp4_quant(x),
+         lambda T, H: T * 2 * H * 2 + T * H // 2 + T * (H // 32) * 4),
+        ("silu_and_mul", (32768, 768), lambda x: ops.silu_and_mul(x),
+         lambda T, H: T * 2 * H * 2 + T * H * 2),
+        ("per_token_group_fp8_quant g128", (8192, 7168 // 2),
+         lambda x: ops.per_token_group_fp8_quant(x, 128),
+         lambda T, H: T * 2 * H * 2 + T * 2 * H + T * (2 * H // 128) * 4),
+    ]
+    out = []
+    for name, (T, H), fn, nbytes in cases:
+        x = rnd(T, 2 * H)
+        for _ in range(3):
+            fn(x)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            fn(x)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / steps
+        gbps = nbytes(T, H) / us / 1e3
+        out.append({"op": name, "input": [T, 2 * H], "bytes": nbytes(T, H),
+                    "us": round(us, 2), "GBps": round(gbps, 1),
+                    "hbm_frac": round(gbps / 8000.0, 3)})
+        del x
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,6 +298,8 @@ def main():
                     help="'none', 'default' or a list like C3:1,C3:8192")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ops", action="store_true",
+                    help="skip the standalone-op bandwidth table")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / "
@@ -290,6 +339,12 @@ def main():
         log("cpu baseline ...")
         cpu = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=64)
         log("cpu baseline:", json.dumps(cpu))
+
+    op_table = None
+    if not args.no_ops:
+        op_table = op_bandwidth(dev, max(args.steps, 10))
+        for d in op_table:
+            log("op:", json.dumps(d))
 
     sweep = []
     if args.sweep != "none":
@@ -339,6 +394,7 @@ def main():
         "stage_us": head["stage_us"],
         "roofline": roof,
         "cpu_baseline": cpu,
+        "ops": op_table,
         "sweep": sweep,
     }
     print(json.dumps(line), flush=True)

@@ -40,7 +40,9 @@ typedef enum {
   MI355MOE_U32 = 5,
   MI355MOE_FP8E4M3 = 6, /* OCP float8_e4m3fn                              */
   MI355MOE_U8 = 7,      /* raw bytes: packed e2m1 pairs or e8m0 scales    */
-  MI355MOE_I16 = 8
+  MI355MOE_I16 = 8,
+  MI355MOE_FP8E5M2 = 9, /* OCP float8_e5m2                                */
+  MI355MOE_I8 = 10
 } mi355moe_dtype;
 
 /* Weight recipes of the grouped GEMM / fused layer
@@ -203,6 +205,35 @@ int mi355moe_per_token_group_quant_mxfp4(const void* input, int dtype,
                                          int64_t rows, int64_t cols,
                                          int64_t group_size, float eps,
                                          void* stream);
+
+/* Replaces torch.ops._C.silu_and_mul_per_block_quant (csrc/torch_bindings.cpp:
+ * 88-101, csrc/quantization/fused_kernels/fused_silu_mul_block_quant.cpp:
+ * 14-137 kernel, 141-239 checks).  input [rows, 2*hidden] bf16/f16 (gate ||
+ * up); r = silu(gate) * up in fp32; per group of group_size (32, 64, 128)
+ * columns: s = max(amax / qmax, 1 / (qmax * 512)) for fp8 (then clamped to
+ * *scale_ub if given, and rounded up to a power of two if scale_ue8m0),
+ * s = max(amax / 127, FLT_EPSILON) for int8; out [rows, hidden] of out_dtype
+ * (FP8E4M3, FP8E5M2, I8) = saturate(r / s).  Scale (t, g) is stored at
+ * scales[t * scale_stride_token + g * scale_stride_group]. */
+int mi355moe_silu_and_mul_per_block_quant(void* out, int out_dtype, const void* input,
+                                          int in_dtype, float* scales,
+                                          int64_t scale_stride_token,
+                                          int64_t scale_stride_group, int64_t rows,
+                                          int64_t hidden, int64_t group_size,
+                                          const float* scale_ub, int scale_ue8m0,
+                                          void* stream);
+
+/* Replaces torch.ops._C.silu_and_mul_mxfp4_quant (csrc/torch_bindings.cpp:
+ * 103-107, csrc/quantization/fused_kernels/fused_silu_mul_mxfp4_quant.cpp:
+ * 18-130 kernel, 134-209 checks).  r as above; per 32 columns s =
+ * 2^ceil(log2(max(amax / 6, eps))) (fp32, stored like the block quantiser's
+ * scales); out [rows, hidden/2] e2m1 codes of clamp(r / s, +-6), two per
+ * byte, the even column in the low nibble.  eps must be a normal float. */
+int mi355moe_silu_and_mul_mxfp4_quant(uint8_t* out, const void* input, int in_dtype,
+                                      float* scales, int64_t scale_stride_token,
+                                      int64_t scale_stride_group, int64_t rows,
+                                      int64_t hidden, int64_t group_size, float eps,
+                                      void* stream);
 
 /* ------------------------------------------------------------ grouped GEMM */
 

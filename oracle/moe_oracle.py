@@ -368,6 +368,65 @@ def per_token_group_quant_mxfp4(x: torch.Tensor, group_size: int = 32,
     return q, s
 
 
+def silu_mul_f32(x: torch.Tensor) -> torch.Tensor:
+    """csrc/quantization/fused_kernels/fused_silu_mul_block_quant.cpp:73 and
+    fused_silu_mul_mxfp4_quant.cpp:77: r = (g / (1 + exp(-g))) * u in fp32
+    with no intermediate rounding; g = x[:, :H], u = x[:, H:]."""
+    H = x.shape[-1] // 2
+    g = x[:, :H].float()
+    u = x[:, H:].float()
+    return (g / (1.0 + torch.exp(-g))) * u
+
+
+_QMAX = {torch.float8_e4m3fn: 448.0, torch.float8_e5m2: 57344.0}
+
+
+def silu_and_mul_per_block_quant(x: torch.Tensor, group_size: int,
+                                 quant_dtype: torch.dtype,
+                                 scale_ub: Optional[float] = None,
+                                 scale_ue8m0: bool = False):
+    """csrc/quantization/fused_kernels/fused_silu_mul_block_quant.cpp:80-121 +
+    quant_conversions.h:19-71.  Per group of r = silu_mul_f32(x): amax =
+    max|r| (from 0); fp8: s = max(amax/qmax, 1/(qmax*512)), with scale_ub
+    s = max(min(s, ub), 1/(qmax*512)), with ue8m0 s = 2^ceil(log2(max(|s|,
+    1e-10))); q = cast_rne(clamp(r / s, +-qmax)).  int8: s = max(amax/127,
+    FLT_EPSILON) (no ub / ue8m0), q = clamp(rint(r / s), -128, 127).
+    Returns (q [T, H] quant_dtype, s float32 [T, H/group_size])."""
+    r = silu_mul_f32(x)
+    T, H = r.shape
+    rg = r.reshape(T, H // group_size, group_size)
+    amax = rg.abs().amax(-1)
+    if quant_dtype == torch.int8:
+        s = torch.clamp(amax / 127.0, min=torch.finfo(torch.float32).eps)
+        q = torch.clamp(torch.round(rg / s.unsqueeze(-1)), -128, 127)
+        return q.reshape(T, H).to(torch.int8), s
+    qmax = _QMAX[quant_dtype]
+    min_sf = torch.tensor(1.0, dtype=torch.float32) / (qmax * 512.0)
+    s = torch.maximum(amax / qmax, min_sf)
+    if scale_ub is not None:
+        s = torch.maximum(torch.clamp(s, max=scale_ub), min_sf)
+    if scale_ue8m0:
+        s = torch.exp2(torch.ceil(torch.log2(torch.clamp(s.abs(), min=1e-10))))
+    q = torch.clamp(rg / s.unsqueeze(-1), -qmax, qmax)
+    return q.reshape(T, H).to(quant_dtype), s
+
+
+def silu_and_mul_mxfp4_quant(x: torch.Tensor, eps: float = 1e-10):
+    """csrc/quantization/fused_kernels/fused_silu_mul_mxfp4_quant.cpp:83-115:
+    per 32 columns of r = silu_mul_f32(x), amax = max|r| (from 0), s =
+    2^ceil(log2(max(|amax/6|, eps))), codes of clamp(r * (1/s), +-6) with the
+    strict-midpoint e2m1 rounding of mxfp4_quant.h:17-25, the even column in
+    the low nibble.  Returns (q uint8 [T, H/2], s float32 [T, H/32])."""
+    r = silu_mul_f32(x)
+    T, H = r.shape
+    rg = r.reshape(T, H // 32, 32)
+    amax = rg.abs().amax(-1)
+    s = torch.exp2(torch.ceil(torch.log2(torch.clamp((amax / FP4_MAX).abs(), min=eps))))
+    v = torch.clamp(rg * (1.0 / s).unsqueeze(-1), -FP4_MAX, FP4_MAX)
+    c = fp4_code(v).reshape(T, H)
+    return (c[:, 0::2] | (c[:, 1::2] << 4)).to(torch.uint8), s
+
+
 def _e2m1_rne(v: torch.Tensor) -> torch.Tensor:
     """Round-to-nearest-even onto the e2m1 grid (OCP MX v1.0 sec. 5.3.3);
     ties go to the code with an even mantissa bit."""

@@ -90,6 +90,34 @@ def test_version_and_error_plumbing(lib):
     (lambda L: L.mi355moe_pack_scales_kblock(None, None, ctypes.c_int64(2),
                                              ctypes.c_int64(64), ctypes.c_int64(0), None),
      b"positive sizes"),
+    (lambda L: L.mi355moe_silu_and_mul_per_block_quant(
+        None, 6, None, 1, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(96), ctypes.c_int64(48), None, 0, None),
+     b"group_size must be 32, 64, or 128"),
+    (lambda L: L.mi355moe_silu_and_mul_per_block_quant(
+        None, 1, None, 1, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(128), ctypes.c_int64(64), None, 0, None),
+     b"out must be float8_e4m3fn, float8_e5m2, or int8"),
+    (lambda L: L.mi355moe_silu_and_mul_per_block_quant(
+        None, 10, None, 1, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(128), ctypes.c_int64(64), ctypes.c_void_p(256), 0, None),
+     b"scale_ub is only supported for FP8 output"),
+    (lambda L: L.mi355moe_silu_and_mul_per_block_quant(
+        None, 9, None, 2, None, ctypes.c_int64(3), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(96), ctypes.c_int64(64), None, 0, None),
+     b"hidden_size must be divisible by group_size"),
+    (lambda L: L.mi355moe_silu_and_mul_per_block_quant(
+        None, 6, None, 0, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(128), ctypes.c_int64(64), None, 0, None),
+     b"input must be float16 or bfloat16"),
+    (lambda L: L.mi355moe_silu_and_mul_mxfp4_quant(
+        None, None, 1, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(128), ctypes.c_int64(64), ctypes.c_float(1e-10), None),
+     b"MXFP4 requires group_size == 32"),
+    (lambda L: L.mi355moe_silu_and_mul_mxfp4_quant(
+        None, None, 1, None, ctypes.c_int64(4), ctypes.c_int64(1), ctypes.c_int64(4),
+        ctypes.c_int64(128), ctypes.c_int64(32), ctypes.c_float(0.0), None),
+     b"eps must be a normal float"),
 ])
 def test_invalid_arguments_rejected_before_launch(lib, call, msg):
     rc = call(lib)
@@ -155,6 +183,8 @@ REFERENCE_SCHEMAS = {
     "_C::swigluoai_and_mul": "swigluoai_and_mul(Tensor! out, Tensor input, float alpha=1.702, float limit=7.0) -> ()",
     "_C::per_token_group_fp8_quant": "per_token_group_fp8_quant(Tensor input, Tensor! output_q, Tensor! output_s, int group_size, float eps, float fp8_min, float fp8_max, bool scale_ue8m0, bool dummy_is_scale_transposed, bool dummy_is_tma_aligned ) -> ()",
     "_C::per_token_group_quant_mxfp4": "per_token_group_quant_mxfp4(Tensor input, Tensor! output_q, Tensor! output_s, int group_size, float eps) -> ()",
+    "_C::silu_and_mul_per_block_quant": "silu_and_mul_per_block_quant(Tensor! out, Tensor input, Tensor! scales, int group_size, Tensor? scale_ub=None, bool is_scale_transposed=False, bool scale_ue8m0=False) -> ()",
+    "_C::silu_and_mul_mxfp4_quant": "silu_and_mul_mxfp4_quant(Tensor! out, Tensor input, Tensor! scales, int group_size, float eps=1e-10) -> ()",
     "_xpu_C::cutlass_grouped_gemm_interface": "cutlass_grouped_gemm_interface(Tensor ptr_A, Tensor? ptr_A_scale, Tensor ptr_B, Tensor? ptr_B_scale, Tensor? ptr_bias, Tensor ptr_D, Tensor rows_per_expert, int N, int K, int num_experts) -> Tensor",
 }
 

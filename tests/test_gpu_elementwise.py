@@ -138,3 +138,146 @@ def test_moe_gather(dev, T, k, H, dt):
     _ops().moe_gather(out, src.to(dev), w.to(dev), perm.to(dev), 8)
     torch.testing.assert_close(out.cpu(), O.moe_gather(src, w, perm),
                                rtol=1e-5 if dt == torch.float32 else 8e-3, atol=1e-5)
+
+
+# ------------------------------------------- fused SiLU-and-mul + quantisers
+# Shapes of the reference's tests (tests/test_fused_silu_mul_block_quant.py:
+# 16-26, tests/test_fused_silu_mul_mxfp4_quant.py:11-19), hidden % group == 0.
+BQ_SHAPES = [(1, 64), (1, 1024), (1, 2048), (1, 5120), (16, 64), (16, 1024), (16, 5120),
+             (128, 64), (128, 1024), (512, 64), (512, 5120)]
+QDT = [torch.float8_e4m3fn, torch.float8_e5m2, torch.int8]
+_STEP = {torch.float8_e4m3fn: (0.125, 2.0 ** -9), torch.float8_e5m2: (0.25, 2.0 ** -16),
+         torch.int8: (0.0, 1.0)}
+
+
+def _gate_up(T, H, seed, dt, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(T, 2 * H, generator=g) * scale).to(dt)
+
+
+def _assert_block_quant_close(q, s, qr, sr, qdt):
+    """The GPU's exp and the CPU oracle's may differ by an ulp, so a group's
+    amax, and with it its scale, by a few ulp and a code sitting on a
+    rounding boundary by one step: scales within rtol 1e-6, at least 99.9 %
+    of the codes identical and every code within one step of the oracle's
+    (relative 1/8 for e4m3, 1/4 for e5m2 above their subnormal steps; one
+    unit for int8)."""
+    s = s.cpu().contiguous()
+    torch.testing.assert_close(s, sr, rtol=1e-6, atol=0)
+    qb, qrb = q.cpu().view(torch.uint8), qr.view(torch.uint8)
+    assert (qb == qrb).float().mean().item() >= 0.999
+    qf, qrf = q.cpu().float(), qr.float()
+    rel, sub = _STEP[qdt]
+    assert torch.all((qf - qrf).abs() <= torch.maximum(qrf.abs() * rel, torch.tensor(sub)) * 1.001)
+
+
+@pytest.mark.parametrize("T,H", BQ_SHAPES)
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("qdt", QDT)
+def test_silu_and_mul_per_block_quant(dev, T, H, group, transposed, qdt):
+    if H % group:
+        pytest.skip("hidden_size not divisible by group_size (the op rejects it)")
+    x = _gate_up(T, H, 31 * T + H, torch.bfloat16)
+    q, s = _ops().silu_and_mul_per_block_quant(x.to(dev), group, qdt, None, transposed)
+    assert q.dtype == qdt and q.shape == (T, H) and s.shape == (T, H // group)
+    if transposed:
+        assert s.stride() == (1, T)
+    qr, sr = O.silu_and_mul_per_block_quant(x, group, qdt)
+    _assert_block_quant_close(q, s, qr, sr, qdt)
+
+
+@pytest.mark.parametrize("T,H", [(1, 1024), (16, 5120), (128, 64)])
+@pytest.mark.parametrize("qdt", QDT)
+def test_silu_and_mul_per_block_quant_fp16_and_reference_scale(dev, T, H, qdt):
+    """fp16 input, and the reference test's data scale (x / hidden), which
+    puts the fp8 scales on their 1/(qmax*512) floor."""
+    for scale in (1.0, 1.0 / H):
+        x = _gate_up(T, H, 7 * T + H, torch.float16, scale)
+        q, s = _ops().silu_and_mul_per_block_quant(x.to(dev), 64, qdt)
+        qr, sr = O.silu_and_mul_per_block_quant(x, 64, qdt)
+        _assert_block_quant_close(q, s, qr, sr, qdt)
+
+
+@pytest.mark.parametrize("qdt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_silu_and_mul_per_block_quant_scale_ub_ue8m0(dev, qdt):
+    x = _gate_up(64, 1024, 5, torch.bfloat16)
+    _, sr = O.silu_and_mul_per_block_quant(x, 128, qdt)
+    ub = float(sr.median())
+    q, s = _ops().silu_and_mul_per_block_quant(
+        x.to(dev), 128, qdt, torch.tensor([ub], device=dev))
+    qr, sr2 = O.silu_and_mul_per_block_quant(x, 128, qdt, scale_ub=ub)
+    _assert_block_quant_close(q, s, qr, sr2, qdt)
+    assert (s.cpu() == ub).float().mean().item() >= 0.4
+    q, s = _ops().silu_and_mul_per_block_quant(x.to(dev), 128, qdt, None, False, True)
+    qr, sr3 = O.silu_and_mul_per_block_quant(x, 128, qdt, scale_ue8m0=True)
+    assert (s.cpu() == sr3).float().mean().item() >= 0.999
+    m, _ = torch.frexp(s.cpu())
+    assert torch.all(m == 0.5)
+
+
+@pytest.mark.parametrize("B", [1, 16, 256])
+@pytest.mark.parametrize("H", [1024, 5120, 14336])
+def test_silu_and_mul_per_block_quant_edge_cases(dev, B, H):
+    """Reference edge-case shapes (tests/test_fused_silu_mul_block_quant.py:
+    165-190): unit-variance fp16, group 128, finite outputs, oracle parity."""
+    x = _gate_up(B, H, B + H, torch.float16)
+    q, s = _ops().silu_and_mul_per_block_quant(x.to(dev), 128, torch.float8_e4m3fn)
+    assert not torch.isnan(q.float()).any() and torch.isfinite(s).all()
+    qr, sr = O.silu_and_mul_per_block_quant(x, 128, torch.float8_e4m3fn)
+    _assert_block_quant_close(q, s, qr, sr, torch.float8_e4m3fn)
+
+
+def _nibbles(q):
+    q = q.cpu()
+    return torch.stack([q & 0xF, q >> 4], -1).reshape(q.shape[0], -1).long()
+
+
+@pytest.mark.parametrize("T", [1, 7, 83, 2048])
+@pytest.mark.parametrize("H", [128, 1024, 5120])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_silu_and_mul_mxfp4_quant(dev, T, H, dt, transposed):
+    """Scales are powers of two equal to the oracle's except where an ulp of
+    exp moves amax/6 across a power of two (then a factor of 2, and that
+    group's codes are not compared); at least 99.9 % of the codes identical,
+    the rest one e2m1 step away with the same sign."""
+    x = _gate_up(T, H, 13 * T + H, dt)
+    G = H // 32
+    q = torch.empty(T, H // 2, dtype=torch.uint8, device=dev)
+    s = (torch.empty(G, T, dtype=torch.float32, device=dev).t() if transposed
+         else torch.empty(T, G, dtype=torch.float32, device=dev))
+    torch.ops._C.silu_and_mul_mxfp4_quant(q, x.to(dev), s, 32, 1e-10)
+    qr, sr = O.silu_and_mul_mxfp4_quant(x)
+    s = s.cpu().contiguous()
+    same = s == sr
+    assert same.float().mean().item() >= 0.999
+    assert torch.all(torch.where(same, torch.ones_like(s), s / sr).log2().abs() <= 1)
+    c, cr = _nibbles(q), _nibbles(qr)
+    keep = same.repeat_interleave(32, dim=1)
+    assert (c[keep] == cr[keep]).float().mean().item() >= 0.999
+    d = c[keep] - cr[keep]
+    assert torch.all((d.abs() <= 1) & ((c[keep] >> 3) == (cr[keep] >> 3)) | (d == 0))
+
+
+def test_fused_quant_validation_messages(dev):
+    x = torch.randn(4, 256, device=dev).bfloat16()
+    q = torch.empty(4, 128, device=dev, dtype=torch.float8_e4m3fn)
+    with pytest.raises(RuntimeError, match="group_size must be 32, 64, or 128"):
+        torch.ops._C.silu_and_mul_per_block_quant(q, x, torch.empty(4, 3, device=dev), 48)
+    with pytest.raises(RuntimeError, match="out must be float8_e4m3fn, float8_e5m2, or int8"):
+        torch.ops._C.silu_and_mul_per_block_quant(
+            torch.empty(4, 128, device=dev, dtype=torch.bfloat16), x,
+            torch.empty(4, 2, device=dev), 64)
+    with pytest.raises(RuntimeError, match="scale_ub is only supported for FP8 output"):
+        torch.ops._C.silu_and_mul_per_block_quant(
+            q.view(torch.int8), x, torch.empty(4, 2, device=dev), 64,
+            torch.ones(1, device=dev))
+    with pytest.raises(RuntimeError, match="scales must have logical shape"):
+        torch.ops._C.silu_and_mul_per_block_quant(q, x, torch.empty(4, 3, device=dev), 64)
+    with pytest.raises(RuntimeError, match="scales must be row-major"):
+        torch.ops._C.silu_and_mul_per_block_quant(
+            q, x, torch.empty(4, 2, device=dev), 64, None, True)
+    with pytest.raises(RuntimeError, match="MXFP4 requires group_size == 32"):
+        torch.ops._C.silu_and_mul_mxfp4_quant(
+            torch.empty(4, 64, device=dev, dtype=torch.uint8), x, torch.empty(4, 2, device=dev), 64)

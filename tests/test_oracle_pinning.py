@@ -254,6 +254,102 @@ def test_fp8_group_quant_scale_closed_form():
     assert s[0, 0].item() == 2.0 ** math.ceil(math.log2(3.0 / 448.0))
 
 
+# ------------------------------------------- fused SiLU-and-mul + quantisers
+def _gate_up(T, H, seed, dtype=torch.bfloat16, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(T, 2 * H, generator=g) * scale).to(dtype)
+
+
+def test_silu_mul_f32_gate_first_unrounded():
+    """r = silu(first half) * second half in fp32: within 3 ulp of torch's
+    own silu, unlike the swapped halves or a 16-bit-rounded silu."""
+    x = _gate_up(8, 256, 1)
+    r = O.silu_mul_f32(x)
+    g, u = x[:, :256].float(), x[:, 256:].float()
+    assert torch.allclose(r, torch.nn.functional.silu(g) * u, rtol=4e-7, atol=0)
+    assert not torch.allclose(r, torch.nn.functional.silu(u) * g, rtol=1e-2)
+    rounded = torch.nn.functional.silu(g).bfloat16().float() * u
+    assert (r != rounded).float().mean().item() > 0.5
+
+
+def _reference_test_group_quant(r, group_size, quant_dtype):
+    """The quantiser of the reference's own test
+    (tests/test_fused_silu_mul_block_quant.py:49-66) applied to fp32 r."""
+    T, H = r.shape
+    rg = r.reshape(T, H // group_size, group_size)
+    gmax = rg.abs().amax(-1)
+    if quant_dtype == torch.int8:
+        s = gmax.clamp(min=1e-10) / 127.0
+        q = (rg / s.unsqueeze(-1)).round().clamp(-128, 127)
+    else:
+        qmax = torch.finfo(quant_dtype).max
+        s = gmax.clamp(min=torch.finfo(torch.float32).tiny) / qmax
+        q = (rg / s.unsqueeze(-1)).clamp(-qmax, qmax)
+    return q.reshape(T, H).to(quant_dtype), s
+
+
+@pytest.mark.parametrize("quant_dtype", [torch.float8_e4m3fn, torch.float8_e5m2, torch.int8])
+@pytest.mark.parametrize("group_size", [32, 64, 128])
+def test_block_quant_matches_reference_test_quantiser(quant_dtype, group_size):
+    """On unit-scale data (every group's scale above the floors) the oracle
+    quantises silu(gate)*up exactly as the reference test's quantiser does."""
+    x = _gate_up(16, 512, 2)
+    q, s = O.silu_and_mul_per_block_quant(x, group_size, quant_dtype)
+    qr, sr = _reference_test_group_quant(O.silu_mul_f32(x), group_size, quant_dtype)
+    assert torch.equal(s, sr)
+    assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8))
+
+
+def test_block_quant_floors_and_qmax():
+    """qmax is the format's largest finite value; an all-zero group takes
+    the floor scale 1/(qmax*512) (fp8) or FLT_EPSILON (int8), codes 0."""
+    assert O._QMAX[torch.float8_e4m3fn] == torch.finfo(torch.float8_e4m3fn).max
+    assert O._QMAX[torch.float8_e5m2] == torch.finfo(torch.float8_e5m2).max
+    x = _gate_up(2, 128, 3)
+    x[0, :64] = 0.0                       # gate of group 0 of row 0: silu(0) = 0
+    for dt, floor in [(torch.float8_e4m3fn, 1.0 / (448.0 * 512.0)),
+                      (torch.float8_e5m2, 1.0 / (57344.0 * 512.0)),
+                      (torch.int8, torch.finfo(torch.float32).eps)]:
+        q, s = O.silu_and_mul_per_block_quant(x, 64, dt)
+        assert s[0, 0].item() == pytest.approx(floor, rel=1e-7)
+        assert not q.float()[0, :64].any()   # +-0 (0 * negative up is -0)
+        assert s[0, 1].item() > floor and s[1, 0].item() > floor
+
+
+def test_block_quant_scale_ub_and_ue8m0():
+    """scale_ub caps the scale (the largest values then saturate at qmax) and
+    never lowers it below the floor; ue8m0 rounds the scale up to a power of
+    two."""
+    x = _gate_up(4, 256, 4)
+    q, s = O.silu_and_mul_per_block_quant(x, 128, torch.float8_e4m3fn)
+    ub = float(s.min()) / 4
+    qu, su = O.silu_and_mul_per_block_quant(x, 128, torch.float8_e4m3fn, scale_ub=ub)
+    assert torch.all(su == torch.tensor(ub, dtype=torch.float32))
+    assert torch.all(qu.float().abs().reshape(4, 2, 128).amax(-1) == 448.0)
+    _, sf = O.silu_and_mul_per_block_quant(x, 128, torch.float8_e4m3fn, scale_ub=1e-12)
+    assert torch.all(sf == torch.tensor(1.0, dtype=torch.float32) / (448.0 * 512.0))
+    _, se = O.silu_and_mul_per_block_quant(x, 128, torch.float8_e4m3fn, scale_ue8m0=True)
+    m, _ = torch.frexp(se)
+    assert torch.all(m == 0.5) and torch.all(se >= s) and torch.all(se < 2 * s)
+
+
+def test_mxfp4_fused_is_silu_then_pinned_quantiser():
+    """The fused mxfp4 quantiser equals the pinned per-token-group mxfp4
+    quantiser applied to silu(gate)*up, all-zero groups included, and its
+    scales equal the reference test's RCEIL e8m0 scales
+    (tests/ops/mx_utils.py:307-330)."""
+    x = _gate_up(6, 256, 5)
+    x[1, :32] = 0.0
+    q, s = O.silu_and_mul_mxfp4_quant(x)
+    q2, s2 = O.per_token_group_quant_mxfp4(O.silu_mul_f32(x), 32)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    amax = O.silu_mul_f32(x).reshape(6, 8, 32).abs().amax(-1)
+    e = torch.clamp(torch.ceil(torch.log2(amax / 6.0)), -127, 127) + 127
+    rceil = torch.where(e == 0, torch.ones_like(amax), torch.exp2(e - 127))
+    nz = amax > 0
+    assert torch.equal(s[nz], rceil[nz])
+
+
 MXFP4_KNOWN = {0.5: (0.125, 6), 1.0: (0.25, 6), 1.5: (0.25, 7), 2.0: (0.5, 6),
                3.0: (0.5, 7), 4.0: (1.0, 6), 6.0: (1.0, 7)}
 

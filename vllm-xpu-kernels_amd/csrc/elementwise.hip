@@ -177,6 +177,123 @@ __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
   *reinterpret_cast<uint32_t*>(q + base / 2) = packed;
 }
 
+// --------------------------------------------- fused SiLU-and-mul + quant
+// f32 -> OCP e5m2 (float8_e5m2: bias 15, 2 mantissa bits), round to nearest
+// even; callers clamp to +-57344 first.
+__device__ __forceinline__ uint32_t f32_to_e5m2(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;   // NaN
+  uint32_t r;
+  if (a < 0x38800000u) {                       // |x| < 2^-14: subnormal range
+    const float f = __uint_as_float(a) * 65536.0f;  // exact: units of 2^-16
+    r = static_cast<uint32_t>(__builtin_rintf(f));  // 0..4 (4 = 2^-14, normal)
+  } else {
+    const uint32_t lsb = (a >> 21) & 1u;
+    const uint32_t rounded = a + 0xFFFFFu + lsb;
+    r = (((rounded >> 23) - 112u) << 2) | ((rounded >> 21) & 3u);
+    if (r > 0x7Bu) r = 0x7Bu;                  // saturate at 57344
+  }
+  return sign | r;
+}
+
+enum QOut { Q_E4M3 = 0, Q_E5M2 = 1, Q_I8 = 2 };
+
+// silu(g) * u in fp32 with no intermediate rounding, as both fused
+// quantisers compute it.
+__device__ __forceinline__ float silu_mul_f32(float g, float u) {
+  return (g / (1.f + expf(-g))) * u;
+}
+
+// One lane: 8 consecutive output columns c0..c0+7 of row r (16 bytes of gate
+// and of up); a group of G columns is owned by G/8 consecutive lanes, which
+// exchange their maxima with xor shuffles (hidden % G == 0, so groups never
+// straddle rows and the lanes of a group are aligned).
+template <typename E, int QO>
+__global__ __launch_bounds__(256) void silu_mul_block_quant_kernel(
+    const void* __restrict__ in, uint8_t* __restrict__ q, float* __restrict__ s,
+    int64_t rows, int64_t hidden, int group, int64_t sst, int64_t ssg,
+    const float* __restrict__ scale_ub, int ue8m0) {
+  const int lpg = group >> 3;
+  const int64_t cpr = hidden >> 3;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const bool active = gtid < rows * cpr;
+  const int64_t r = active ? gtid / cpr : 0;
+  const int64_t c0 = (active ? gtid % cpr : 0) * 8;
+  const uint16_t* x = static_cast<const uint16_t*>(in) + r * 2 * hidden;
+  float g[8], u[8], v[8];
+  Vec8<E>::load(x + c0, g);
+  Vec8<E>::load(x + hidden + c0, u);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = silu_mul_f32(g[i], u[i]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  for (int o = 1; o < lpg; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  float ys;
+  if constexpr (QO == Q_I8) {
+    ys = fmaxf(amax / 127.0f, 1.1920928955078125e-7f);  // FLT_EPSILON
+  } else {
+    constexpr float qmax = QO == Q_E4M3 ? 448.0f : 57344.0f;
+    constexpr float min_sf = 1.0f / (qmax * 512.0f);
+    ys = fmaxf(amax / qmax, min_sf);
+    if (scale_ub) ys = fmaxf(fminf(ys, *scale_ub), min_sf);
+    if (ue8m0) ys = pow2i(ceil_log2(fmaxf(fabsf(ys), 1e-10f)));
+  }
+  if (!active) return;
+  if ((gtid & (lpg - 1)) == 0) s[r * sst + (c0 / group) * ssg] = ys;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t b;
+    if constexpr (QO == Q_I8) {
+      const float t = fminf(fmaxf(__builtin_rintf(v[i] / ys), -128.0f), 127.0f);
+      b = static_cast<uint32_t>(static_cast<int32_t>(t)) & 0xFFu;
+    } else if constexpr (QO == Q_E4M3) {
+      b = f32_to_e4m3(fminf(fmaxf(v[i] / ys, -448.0f), 448.0f));
+    } else {
+      b = f32_to_e5m2(fminf(fmaxf(v[i] / ys, -57344.0f), 57344.0f));
+    }
+    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+  }
+  *reinterpret_cast<uint2*>(q + r * hidden + c0) = make_uint2(lo, hi);
+}
+
+// mxfp4: groups of 32 columns, 4 lanes each.
+template <typename E>
+__global__ __launch_bounds__(256) void silu_mul_mxfp4_quant_kernel(
+    const void* __restrict__ in, uint8_t* __restrict__ q, float* __restrict__ s,
+    int64_t rows, int64_t hidden, int64_t sst, int64_t ssg, float eps) {
+  const int64_t cpr = hidden >> 3;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const bool active = gtid < rows * cpr;
+  const int64_t r = active ? gtid / cpr : 0;
+  const int64_t c0 = (active ? gtid % cpr : 0) * 8;
+  const uint16_t* x = static_cast<const uint16_t*>(in) + r * 2 * hidden;
+  float g[8], u[8], v[8];
+  Vec8<E>::load(x + c0, g);
+  Vec8<E>::load(x + hidden + c0, u);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = silu_mul_f32(g[i], u[i]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float ys = pow2i(ceil_log2(fmaxf(fabsf(amax / 6.0f), eps)));
+  if (!active) return;
+  if ((gtid & 3) == 0) s[r * sst + (c0 >> 5) * ssg] = ys;
+  const float inv = 1.0f / ys;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    packed |= fp4_code(fminf(fmaxf(v[i] * inv, -6.0f), 6.0f)) << (4 * i);
+  *reinterpret_cast<uint32_t*>(q + (r * hidden + c0) / 2) = packed;
+}
+
 // -------------------------------------------------------------- reductions
 template <typename E, typename Id>
 __global__ __launch_bounds__(256) void moe_sum_kernel(
@@ -304,6 +421,69 @@ extern "C" int mi355moe_per_token_group_quant_mxfp4(
   dim3 grid(static_cast<unsigned>(cdiv(threads, 256)));
   MI_DISPATCH_FLOAT(dt, (group_mxfp4_quant_kernel<E><<<grid, dim3(256), 0, st>>>(in, q, s, rows, cols, eps)),
                     "per_token_group_quant_mxfp4: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+#define MI_DISPATCH_HALF(dt, KERNEL_CALL, what)                                 \
+  switch (dt) {                                                                 \
+    case MI355MOE_BF16: { using E = BF16; KERNEL_CALL; break; }                 \
+    case MI355MOE_F16: { using E = F16; KERNEL_CALL; break; }                   \
+    default: return set_error(MI355MOE_ERR_INVALID, what);                      \
+  }
+
+extern "C" int mi355moe_silu_and_mul_per_block_quant(
+    void* out, int out_dtype, const void* in, int in_dtype, float* scales,
+    int64_t sst, int64_t ssg, int64_t rows, int64_t hidden, int64_t group,
+    const float* scale_ub, int ue8m0, void* stream) {
+  MI_ARG(out_dtype == MI355MOE_FP8E4M3 || out_dtype == MI355MOE_FP8E5M2 ||
+             out_dtype == MI355MOE_I8,
+         "out must be float8_e4m3fn, float8_e5m2, or int8");
+  MI_ARG(in_dtype == MI355MOE_F16 || in_dtype == MI355MOE_BF16,
+         "input must be float16 or bfloat16");
+  MI_ARG(group == 32 || group == 64 || group == 128, "group_size must be 32, 64, or 128");
+  MI_ARG(!scale_ub || out_dtype != MI355MOE_I8, "scale_ub is only supported for FP8 output");
+  MI_ARG(rows >= 0 && hidden >= 0, "invalid shape");
+  MI_ARG(hidden % group == 0, "hidden_size must be divisible by group_size");
+  if (rows == 0 || hidden == 0) return MI355MOE_OK;
+  MI_ARG(out && in && scales, "null pointer");
+  MI_ARG((reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
+         "input must be 16-byte and out 8-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(rows * (hidden / 8), 256)));
+  uint8_t* q = static_cast<uint8_t*>(out);
+#define MI_BQ(QO) \
+  MI_DISPATCH_HALF(in_dtype, (silu_mul_block_quant_kernel<E, QO><<<grid, dim3(256), 0, st>>>( \
+      in, q, scales, rows, hidden, static_cast<int>(group), sst, ssg, scale_ub, ue8m0)), \
+      "input must be float16 or bfloat16")
+  if (out_dtype == MI355MOE_FP8E4M3) { MI_BQ(Q_E4M3) }
+  else if (out_dtype == MI355MOE_FP8E5M2) { MI_BQ(Q_E5M2) }
+  else { MI_BQ(Q_I8) }
+#undef MI_BQ
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+extern "C" int mi355moe_silu_and_mul_mxfp4_quant(uint8_t* out, const void* in, int in_dtype,
+                                                 float* scales, int64_t sst, int64_t ssg,
+                                                 int64_t rows, int64_t hidden, int64_t group,
+                                                 float eps, void* stream) {
+  MI_ARG(in_dtype == MI355MOE_F16 || in_dtype == MI355MOE_BF16,
+         "input must be float16 or bfloat16");
+  MI_ARG(group == 32, "MXFP4 requires group_size == 32");
+  MI_ARG(rows >= 0 && hidden >= 0, "invalid shape");
+  MI_ARG(hidden % group == 0, "hidden_size must be divisible by group_size");
+  MI_ARG(eps >= 1.17549435e-38f && eps <= 3.40282347e+38f,
+         "eps must be a normal float (at least 2^-126)");
+  if (rows == 0 || hidden == 0) return MI355MOE_OK;
+  MI_ARG(out && in && scales, "null pointer");
+  MI_ARG((reinterpret_cast<uintptr_t>(in) & 15) == 0 && (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+         "input must be 16-byte and out 4-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(rows * (hidden / 8), 256)));
+  MI_DISPATCH_HALF(in_dtype, (silu_mul_mxfp4_quant_kernel<E><<<grid, dim3(256), 0, st>>>(
+                                  in, out, scales, rows, hidden, sst, ssg, eps)),
+                   "input must be float16 or bfloat16")
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }

@@ -40,6 +40,8 @@ int dtype_code(at::ScalarType s) {
     case at::kFloat4_e2m1fn_x2: return MI355MOE_U8;
     case at::kFloat8_e8m0fnu: return MI355MOE_U8;
     case at::kShort: return MI355MOE_I16;
+    case at::kFloat8_e5m2: return MI355MOE_FP8E5M2;
+    case at::kChar: return MI355MOE_I8;
     default: return -1;
   }
 }
@@ -365,6 +367,100 @@ void per_token_group_quant_mxfp4(const at::Tensor& input, at::Tensor& output_q,
            "per_token_group_quant_mxfp4");
 }
 
+// Scales of the fused quantisers are written at t * sst + g * ssg: the tensor
+// must have exactly that layout (row-major [T, G] or a transposed [G, T]).
+void check_scale_strides(const at::Tensor& s, int64_t sst, int64_t ssg) {
+  TORCH_CHECK((s.size(0) <= 1 || s.stride(0) == sst) && (s.size(1) <= 1 || s.stride(1) == ssg),
+              "scales must be row-major [num_tokens, num_groups] or the transpose of a "
+              "row-major [num_groups, num_tokens] tensor");
+}
+
+// reference csrc/quantization/fused_kernels/fused_silu_mul_block_quant.cpp:141-239
+void silu_and_mul_per_block_quant(at::Tensor& out, const at::Tensor& input, at::Tensor& scales,
+                                  int64_t group_size, const std::optional<at::Tensor>& scale_ub,
+                                  bool is_scale_transposed, bool scale_ue8m0) {
+  TORCH_CHECK(out.scalar_type() == at::kFloat8_e4m3fn || out.scalar_type() == at::kFloat8_e5m2 ||
+                  out.scalar_type() == at::kChar,
+              "out must be float8_e4m3fn, float8_e5m2, or int8");
+  TORCH_CHECK(input.scalar_type() == at::kHalf || input.scalar_type() == at::kBFloat16,
+              "input must be float16 or bfloat16");
+  TORCH_CHECK(out.is_contiguous(), "out must be contiguous");
+  TORCH_CHECK(input.is_contiguous(), "input must be contiguous");
+  TORCH_CHECK(scales.scalar_type() == at::kFloat, "scales must be float32");
+  TORCH_CHECK(group_size == 32 || group_size == 64 || group_size == 128,
+              "group_size must be 32, 64, or 128, got ", group_size);
+  if (scale_ub.has_value())
+    TORCH_CHECK(out.scalar_type() != at::kChar, "scale_ub is only supported for FP8 output");
+  TORCH_CHECK(input.dim() == 2, "input must be 2-dimensional");
+  TORCH_CHECK(out.dim() == 2, "out must be 2-dimensional");
+  const int64_t T = input.size(0);
+  const int64_t hidden = out.size(-1);
+  const int64_t groups = hidden / group_size;
+  TORCH_CHECK(input.size(-1) == hidden * 2, "input last dim must be 2 * hidden_size");
+  TORCH_CHECK(hidden % group_size == 0, "hidden_size must be divisible by group_size");
+  TORCH_CHECK(out.size(0) == T, "out.size(0) must equal num_tokens (input.size(0))");
+  TORCH_CHECK(scales.size(0) == T && scales.size(1) == groups,
+              "scales must have logical shape [num_tokens, num_groups]");
+  if (T == 0) return;
+  check_gpu(input, "input");
+  check_gpu(out, "out");
+  TORCH_CHECK(scales.is_cuda(), "scales must be on a GPU device");
+  const float* ub = nullptr;
+  if (scale_ub.has_value()) {
+    check_gpu(*scale_ub, "scale_ub");
+    TORCH_CHECK(scale_ub->scalar_type() == at::kFloat && scale_ub->numel() >= 1,
+                "scale_ub must be a float32 tensor");
+    ub = scale_ub->data_ptr<float>();
+  }
+  const int64_t sst = is_scale_transposed ? 1 : groups;
+  const int64_t ssg = is_scale_transposed ? T : 1;
+  check_scale_strides(scales, sst, ssg);
+  DevGuard g(input.device());
+  check_rc(mi355moe_silu_and_mul_per_block_quant(
+               out.data_ptr(), dtype_code(out.scalar_type()), input.data_ptr(),
+               dtype_code(input.scalar_type()), scales.data_ptr<float>(), sst, ssg, T, hidden,
+               group_size, ub, scale_ue8m0, cur_stream(input)),
+           "silu_and_mul_per_block_quant");
+}
+
+// reference csrc/quantization/fused_kernels/fused_silu_mul_mxfp4_quant.cpp:134-209
+void silu_and_mul_mxfp4_quant(at::Tensor& out, const at::Tensor& input, at::Tensor& scales,
+                              int64_t group_size, double eps) {
+  TORCH_CHECK(input.scalar_type() == at::kHalf || input.scalar_type() == at::kBFloat16,
+              "input must be float16 or bfloat16");
+  TORCH_CHECK(out.scalar_type() == at::kByte, "out must be uint8 (packed FP4)");
+  TORCH_CHECK(out.is_contiguous(), "out must be contiguous");
+  TORCH_CHECK(input.is_contiguous(), "input must be contiguous");
+  TORCH_CHECK(scales.scalar_type() == at::kFloat, "scales must be float32");
+  TORCH_CHECK(group_size == 32, "MXFP4 requires group_size == 32, got ", group_size);
+  TORCH_CHECK(input.dim() == 2, "input must be 2-dimensional");
+  TORCH_CHECK(out.dim() == 2, "out must be 2-dimensional");
+  TORCH_CHECK(scales.dim() == 2, "scales must be 2-dimensional");
+  const int64_t T = input.size(0);
+  const int64_t hidden = input.size(-1) / 2;
+  const int64_t groups = hidden / group_size;
+  TORCH_CHECK(input.size(-1) == hidden * 2, "input last dim must be 2 * hidden_size");
+  TORCH_CHECK(hidden % group_size == 0, "hidden_size must be divisible by group_size");
+  TORCH_CHECK(out.size(0) == T && out.size(1) == hidden / 2,
+              "out must have shape [num_tokens, hidden_size / 2]");
+  TORCH_CHECK(scales.size(0) == T && scales.size(1) == groups,
+              "scales must have logical shape [num_tokens, num_groups]");
+  if (T == 0) return;
+  check_gpu(input, "input");
+  check_gpu(out, "out");
+  TORCH_CHECK(scales.is_cuda(), "scales must be on a GPU device");
+  const bool transposed = scales.stride(0) < scales.stride(1);
+  const int64_t sst = transposed ? 1 : groups;
+  const int64_t ssg = transposed ? T : 1;
+  check_scale_strides(scales, sst, ssg);
+  DevGuard g(input.device());
+  check_rc(mi355moe_silu_and_mul_mxfp4_quant(
+               static_cast<uint8_t*>(out.data_ptr()), input.data_ptr(),
+               dtype_code(input.scalar_type()), scales.data_ptr<float>(), sst, ssg, T, hidden,
+               group_size, static_cast<float>(eps), cur_stream(input)),
+           "silu_and_mul_mxfp4_quant");
+}
+
 // ------------------------------------------------------------- grouped GEMM
 at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
                                           const std::optional<at::Tensor>& ptr_A_scale,
@@ -588,12 +684,19 @@ TORCH_LIBRARY(_C, m) {
         "-> ()");
   m.def("per_token_group_quant_mxfp4(Tensor input, Tensor! output_q, Tensor! "
         "output_s, int group_size, float eps) -> ()");
+  m.def("silu_and_mul_per_block_quant(Tensor! out, Tensor input, Tensor! scales, "
+        "int group_size, Tensor? scale_ub=None, bool is_scale_transposed=False, "
+        "bool scale_ue8m0=False) -> ()");
+  m.def("silu_and_mul_mxfp4_quant(Tensor! out, Tensor input, Tensor! scales, "
+        "int group_size, float eps=1e-10) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(_C, CUDA, m) {
   m.impl("silu_and_mul", &silu_and_mul);
   m.impl("swigluoai_and_mul", &swigluoai_and_mul);
   m.impl("per_token_group_fp8_quant", &per_token_group_fp8_quant);
+  m.impl("silu_and_mul_per_block_quant", &silu_and_mul_per_block_quant);
+  m.impl("silu_and_mul_mxfp4_quant", &silu_and_mul_mxfp4_quant);
   m.impl("per_token_group_quant_mxfp4", &per_token_group_quant_mxfp4);
 }
 

@@ -152,6 +152,40 @@ def per_token_group_quant_mxfp4(x: torch.Tensor, group_size: int = 32,
     return q.view(torch.float4_e2m1fn_x2), s
 
 
+def silu_and_mul_per_block_quant(input: torch.Tensor, group_size: int,
+                                 quant_dtype: torch.dtype,
+                                 scale_ub: Optional[torch.Tensor] = None,
+                                 is_scale_transposed: bool = False,
+                                 scale_ue8m0: bool = False):
+    """silu(gate) * up fused with per-group dynamic quantisation to
+    float8_e4m3fn / float8_e5m2 / int8 (reference tests/register_ops.py:34-74
+    allocation, csrc/torch_bindings.cpp:88-101 op).  Returns (out [T, H],
+    scales [T, H/group_size]; a transposed view when is_scale_transposed)."""
+    T, H = input.shape[0], input.shape[-1] // 2
+    G = H // group_size
+    out = torch.empty((T, H), dtype=quant_dtype, device=input.device)
+    if is_scale_transposed:
+        scales = torch.empty((G, T), dtype=torch.float32, device=input.device).t()
+    else:
+        scales = torch.empty((T, G), dtype=torch.float32, device=input.device)
+    torch.ops._C.silu_and_mul_per_block_quant(out, input, scales, group_size,
+                                              scale_ub, is_scale_transposed,
+                                              scale_ue8m0)
+    return out, scales
+
+
+def silu_and_mul_mxfp4_quant(input: torch.Tensor, group_size: int = 32,
+                             eps: float = 1e-10):
+    """silu(gate) * up fused with mxfp4 quantisation (csrc/torch_bindings.cpp:
+    103-107).  Returns (packed e2m1 uint8 [T, H/2], float32 power-of-two
+    scales [T, H/32])."""
+    T, H = input.shape[0], input.shape[-1] // 2
+    out = torch.empty((T, H // 2), dtype=torch.uint8, device=input.device)
+    scales = torch.empty((T, H // group_size), dtype=torch.float32, device=input.device)
+    torch.ops._C.silu_and_mul_mxfp4_quant(out, input, scales, group_size, eps)
+    return out, scales
+
+
 def init_expert_map(num_experts: int, ep_rank: int, ep_size: int,
                     device) -> torch.Tensor:
     m = torch.empty(num_experts * ep_size, dtype=torch.int32, device=device)
