@@ -296,6 +296,13 @@ typedef struct {
   float swiglu_limit;         /* swigluoai limit (7.0)                       */
   void* output;               /* [T, H]                                      */
   int w_layout;               /* mi355moe_weight_layout of w13 and w2 (bf16) */
+  /* fp8block only, optional (the reference's a1q_scale,
+   * vllm_xpu_kernels/fused_moe_interface.py:326-360): when non-null,
+   * hidden_states are already quantised, e4m3 [T, H], with these f32 scales
+   * [T, H/128] (1x128 groups, as per_token_group_fp8_quant makes them), and
+   * the layer uses them as they are instead of quantising hidden_states
+   * itself; act_dtype still names the output's type. */
+  const float* hidden_scale;
 } mi355moe_fused_moe_args;
 
 /* One-time weight preparation, the counterpart of the repacking the

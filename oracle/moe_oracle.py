@@ -554,7 +554,7 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
               topk_ids: torch.Tensor, activation: str = "silu",
               expert_map: Optional[torch.Tensor] = None,
               gemm1_clamp_limit: Optional[float] = None,
-              experts=None):
+              experts=None, a1q_scale: Optional[torch.Tensor] = None):
     """XpuFusedMoe.apply semantics (vllm_xpu_kernels/fused_moe_interface.py:
     319-419, reference path moe_utils.py:236-403, rounding points of
     SURVEY Appendix A):
@@ -568,10 +568,13 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
     [E, N, K/32].  The expert loop dequantises one expert at a time.
     ``experts`` optionally restricts the computation to a subset of expert ids
     (the CPU-baseline sample); slots of other experts contribute zero.
+    ``a1q_scale`` (fp8block): ``hidden`` is already e4m3 with these [T, H/128]
+    scales, dequantised as given and computed in bf16
+    (fused_moe_interface.py:326-360, moe_utils.py:285, 338-347).
     """
     T, H = hidden.shape
     k = topk_ids.shape[1]
-    dt = hidden.dtype
+    dt = hidden.dtype if a1q_scale is None else torch.bfloat16
     ids = topk_ids.to(torch.int64)
     if expert_map is not None:
         ids = expert_map.to(torch.int64)[ids]
@@ -580,7 +583,11 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
     g2 = torch.zeros(T * k, H, dtype=dt)
     flat = ids.reshape(-1)
     todo = range(E) if experts is None else experts
-    xq_all = qdq_act(recipe, hidden)
+    if a1q_scale is not None:
+        assert recipe == "fp8block", "a1q_scale: fp8block recipe only"
+        xq_all = dequant_fp8_groups(hidden, a1q_scale.float(), 128)
+    else:
+        xq_all = qdq_act(recipe, hidden)
     for e in todo:
         slots = (flat == e).nonzero().flatten()
         if slots.numel() == 0:

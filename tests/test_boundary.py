@@ -141,7 +141,8 @@ def test_fused_moe_workspace_query_and_validation(lib):
                     ("w2_scale", ctypes.c_void_p), ("w2_bias", ctypes.c_void_p),
                     ("gemm1_clamp_limit", ctypes.c_float), ("swiglu_alpha", ctypes.c_float),
                     ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
-                    ("w_layout", ctypes.c_int)]
+                    ("w_layout", ctypes.c_int),
+                    ("hidden_scale", ctypes.c_void_p)]
 
     a = Args(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=64,
              hidden=7168, inter=2048, num_experts=256, topk=8)
@@ -166,6 +167,10 @@ def test_fused_moe_workspace_query_and_validation(lib):
     a.w_layout = 7
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"unknown weight layout" in lib.mi355moe_last_error()
+    # caller-quantised hidden states: fp8block only
+    a.w_layout, a.hidden_scale = 0, 64
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"need the fp8block recipe" in lib.mi355moe_last_error()
 
 
 # schema strings as written in the reference's registration files

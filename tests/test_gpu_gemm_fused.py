@@ -147,11 +147,13 @@ def _layer(cfg, T, dev, E=None, seed_shift=0):
     return cfg, w, x, tw, ti, out, moe
 
 
-def _oracle_layer(cfg, w, x, tw, ti, tokens=None):
+def _oracle_layer(cfg, w, x, tw, ti, tokens=None, a1q_scale=None):
     """Run the oracle on CPU copies of only the experts the (sampled) tokens
-    route to."""
+    route to (a1q_scale: x is pre-quantised e4m3 with these scales)."""
     if tokens is not None:
         x, tw, ti = x[tokens], tw[tokens], ti[tokens]
+        if a1q_scale is not None:
+            a1q_scale = a1q_scale[tokens]
     ti_c = ti.cpu().long()
     used = torch.unique(ti_c)
     remap = torch.full((cfg.experts,), -1, dtype=torch.long)
@@ -171,7 +173,8 @@ def _oracle_layer(cfg, w, x, tw, ti, tokens=None):
     b13 = w.w13_bias.index_select(0, usedd).cpu() if w.w13_bias is not None else None
     b2 = w.w2_bias.index_select(0, usedd).cpu() if w.w2_bias is not None else None
     return O.fused_moe(cfg.recipe, x.cpu(), w13, s13, b13, w2, s2, b2, tw.cpu(), ids,
-                       activation=cfg.activation)
+                       activation=cfg.activation,
+                       a1q_scale=None if a1q_scale is None else a1q_scale.cpu())
 
 
 def test_fused_moe_c1_tiny(dev):
@@ -534,6 +537,35 @@ def test_fused_moe_mxfp4_wide_skewed(dev, hot):
     moe.apply(out, x, tw, ti)
     toks = torch.linspace(0, T - 1, 96).long().to(dev)
     _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks))
+
+
+@pytest.mark.parametrize("T", [1, 16, 48, 300, 1024])
+def test_fused_moe_a1q_scale_pre_quantised(dev, T):
+    """Pre-quantised hidden states (a1q_scale, fp8block; H=384, I=256, 8
+    experts, top-2): the (q, s) of the layer's own 1x128 quantiser give its
+    bf16-input output bit for bit in every family (T=1 split-K stream, 16
+    stream, 48 small, 300 128-slot, 1024 320-slot); other scales (ue8m0)
+    meet the oracle run on the same pre-quantised input."""
+    import dataclasses
+    from vllm_xpu_kernels import ops
+    cfg = dataclasses.replace(_W().CONFIGS["C2"], recipe="fp8block", hidden=384, inter=256,
+                              experts=8, topk=2)
+    cfg, w, x, tw, ti, out, moe = _layer(cfg, T, dev)
+    xq, xs = ops.per_token_group_fp8_quant(x, 128)
+    out2 = torch.empty_like(out)
+    moe.apply(out2, xq, tw, ti, a1q_scale=xs)
+    assert torch.equal(out2, out)
+    xq3, xs3 = ops.per_token_group_fp8_quant(x, 128, scale_ue8m0=True)
+    out3 = torch.empty_like(out)
+    moe.apply(out3, xq3, tw, ti, a1q_scale=xs3)
+    toks = torch.linspace(0, T - 1, min(T, 64)).long().to(dev)
+    _close(out3[toks], _oracle_layer(cfg, w, xq3, tw, ti, toks, a1q_scale=xs3), fp8=True)
+
+
+def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):
+    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C1"], 8, dev)
+    with pytest.raises(NotImplementedError, match="fp8 block-scaled recipe"):
+        moe.apply(out, x, tw, ti, a1q_scale=torch.ones(8, 1, device=dev))
 
 
 @pytest.mark.parametrize("T", [1, 16])

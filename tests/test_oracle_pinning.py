@@ -469,3 +469,13 @@ def test_fused_moe_oracle_fp8block_close_to_dequant_fp32():
     d2 = torch.stack([O.dequant_fp8_block_weight(q2[e], s2[e]) for e in range(E)])
     ref = O.fused_moe("bf16", x, d13, None, None, d2, None, None, w, ids)
     torch.testing.assert_close(y.float(), ref.float(), rtol=0.1, atol=0.05)
+    # pre-quantised input (a1q_scale): the pinned 1x128 quantiser's own
+    # (q, s) give exactly the layer that quantises x itself; other scales
+    # (a power of two above) give a different but close layer
+    xq, xs = O.per_token_group_fp8_quant(x, 128)
+    yq = O.fused_moe("fp8block", xq, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xs)
+    assert yq.dtype == torch.bfloat16 and torch.equal(yq, y)
+    xq2, xs2 = O.per_token_group_fp8_quant(x, 128, scale_ue8m0=True)
+    y2 = O.fused_moe("fp8block", xq2, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xs2)
+    assert not torch.equal(y2, y)
+    torch.testing.assert_close(y2.float(), y.float(), rtol=0.1, atol=0.05)

@@ -3,6 +3,7 @@
 // Fused layer (one call, no host synchronisation, 4-5 launches):
 //   1. stable counting sort of topk_ids into block-aligned sorted slots
 //   2. (fp8block) 1x128 e4m3 quantisation of hidden_states, once per token
+//      (skipped when the caller hands them over quantised: hidden_scale)
 //   3. w13 grouped GEMM gathering activation rows through the sorted slots,
 //      GLU epilogue (SiLU-mul / swigluoai), activation written in slot order
 //      (fp8block: re-quantised to e4m3 + 1x128 scales in the same epilogue)
@@ -302,6 +303,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   MI_ARG(T >= 0 && H > 0 && I > 0 && E > 0 && k > 0, "invalid layer shape");
   MI_ARG(E <= 1024, "num_experts must be at most 1024");
   MI_ARG(a->act_dtype == MI355MOE_BF16, "hidden_states must be bfloat16");
+  MI_ARG(!a->hidden_scale || a->recipe == MI355MOE_RECIPE_FP8BLOCK,
+         "pre-quantised hidden_states (hidden_scale) need the fp8block recipe");
   MI_ARG(a->ids_dtype == MI355MOE_I32 || a->ids_dtype == MI355MOE_I64,
          "topk_ids must be int32 or int64");
   MI_ARG(a->activation == MI355MOE_ACT_SILU || a->activation == MI355MOE_ACT_SWIGLUOAI,
@@ -346,16 +349,18 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   if (rc) return rc;
 
   const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
+  // caller-quantised hidden states (e4m3 + 1x128 scales) go to w13 as given
+  const bool preq = fp8 && a->hidden_scale;
   if (int m = mark(1)) return m;
-  if (fp8) {
+  if (fp8 && !preq) {
     rc = group_quant_fp8(a->hidden_states, MI355MOE_BF16, L.xq, L.xs, T, H, st);
     if (rc) return rc;
   }
   if (int m = mark(2)) return m;
 
   GemmArgs g1{};
-  g1.A = fp8 ? static_cast<const void*>(L.xq) : a->hidden_states;
-  g1.a_scale = fp8 ? L.xs : nullptr;
+  g1.A = fp8 && !preq ? static_cast<const void*>(L.xq) : a->hidden_states;
+  g1.a_scale = preq ? a->hidden_scale : (fp8 ? L.xs : nullptr);
   g1.B = a->w13;
   g1.b_scale = a->w13_scale;
   g1.bias = static_cast<const uint16_t*>(a->w13_bias);

@@ -550,9 +550,19 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
                      const std::optional<at::Tensor>& w2_scale,
                      const std::optional<at::Tensor>& w2_bias, int64_t recipe,
                      int64_t activation, int64_t inter_size, double clamp_limit,
-                     const std::optional<at::Tensor>& expert_map, int64_t w_layout) {
+                     const std::optional<at::Tensor>& expert_map, int64_t w_layout,
+                     const std::optional<at::Tensor>& hidden_scale) {
   check_gpu(output, "output");
   check_gpu(hidden_states, "hidden_states");
+  if (hidden_scale) {
+    check_gpu(*hidden_scale, "hidden_scale");
+    TORCH_CHECK(hidden_states.scalar_type() == at::kFloat8_e4m3fn,
+                "pre-quantised hidden_states must be float8_e4m3fn");
+    TORCH_CHECK(hidden_scale->scalar_type() == at::kFloat && hidden_scale->dim() == 2 &&
+                    hidden_scale->size(0) == hidden_states.size(0) &&
+                    hidden_scale->size(1) * 128 == hidden_states.size(1),
+                "a1q_scale must be float32 [num_tokens, hidden_size / 128]");
+  }
   check_gpu(topk_weights, "topk_weights");
   check_gpu(topk_ids, "topk_ids");
   check_gpu(w13, "w13");
@@ -562,7 +572,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   mi355moe_fused_moe_args a{};
   a.recipe = static_cast<int>(recipe);
   a.activation = static_cast<int>(activation);
-  a.act_dtype = dtype_code(hidden_states.scalar_type());
+  a.act_dtype = dtype_code((hidden_scale ? output : hidden_states).scalar_type());
   a.ids_dtype = dtype_code(topk_ids.scalar_type());
   a.num_tokens = hidden_states.size(0);
   a.hidden = hidden_states.size(1);
@@ -585,6 +595,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.swiglu_limit = 7.0f;
   a.output = output.data_ptr();
   a.w_layout = static_cast<int>(w_layout);
+  a.hidden_scale = hidden_scale ? hidden_scale->data_ptr<float>() : nullptr;
   const size_t ws_bytes = mi355moe_fused_moe_workspace_size(&a);
   auto ws = at::empty({static_cast<int64_t>(ws_bytes)},
                       hidden_states.options().dtype(at::kByte));
@@ -653,7 +664,8 @@ TORCH_LIBRARY(_moe_C, m) {
   m.def("mi355_fused_moe(Tensor! output, Tensor hidden_states, Tensor topk_weights, "
         "Tensor topk_ids, Tensor w13, Tensor? w13_scale, Tensor? w13_bias, Tensor w2, "
         "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
-        "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0) -> ()");
+        "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0, "
+        "Tensor? hidden_scale=None) -> ()");
   m.def("mi355_pack_weights_kblock(Tensor src, Tensor! dst) -> ()");
   m.def("mi355_pack_scales_kblock(Tensor src, Tensor! dst) -> ()");
 }

@@ -32,7 +32,8 @@ class FusedMoeArgs(ctypes.Structure):
                 ("gemm1_clamp_limit", ctypes.c_float),
                 ("swiglu_alpha", ctypes.c_float),
                 ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
-                ("w_layout", ctypes.c_int)]
+                ("w_layout", ctypes.c_int),
+                ("hidden_scale", ctypes.c_void_p)]
 
 
 lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t

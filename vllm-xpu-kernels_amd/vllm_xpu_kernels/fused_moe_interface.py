@@ -215,9 +215,13 @@ class XpuFusedMoe:
     def apply(self, output, hidden_states, topk_weights, topk_ids,
               expert_map=None, a1q_scale=None):
         if a1q_scale is not None:
-            raise NotImplementedError(
-                "pre-quantised activations (a1q_scale) are not supported yet; "
-                "pass bf16 hidden_states (quantised on the fly per 1x128)")
+            # reference fused_moe_interface.py:326-360: hidden_states already
+            # quantised, the layer consumes them with their scales
+            if self._recipe != RECIPE_FP8BLOCK:
+                raise NotImplementedError(
+                    "pre-quantised activations (a1q_scale) are supported for "
+                    "the fp8 block-scaled recipe (e4m3 + [T, H/128] scales)")
+            a1q_scale = a1q_scale.to(torch.float32).contiguous()
         if expert_map is None and self.ep_size > 1:
             expert_map = self.expert_map
         clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
@@ -226,7 +230,7 @@ class XpuFusedMoe:
             topk_ids.contiguous(), self.w13, self.gemm1_wei_scales,
             self.w13_bias, self.w2, self.gemm2_wei_scales, self.w2_bias,
             self._recipe, self._act, self.inter_size, clamp, expert_map,
-            self._w_layout)
+            self._w_layout, a1q_scale)
         return output
 
 
