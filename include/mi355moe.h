@@ -56,8 +56,13 @@ typedef enum {
 } mi355moe_recipe;
 
 typedef enum {
-  MI355MOE_ACT_SILU = 0,      /* silu(x[:, :I]) * x[:, I:]                 */
-  MI355MOE_ACT_SWIGLUOAI = 1  /* interleaved gate/up, alpha 1.702, lim 7   */
+  MI355MOE_ACT_SILU = 0,       /* silu(x[:, :I]) * x[:, I:]                */
+  MI355MOE_ACT_SWIGLUOAI = 1,  /* interleaved gate/up, alpha 1.702, lim 7  */
+  MI355MOE_ACT_GELU = 2,       /* gelu(x[:, :I]) * x[:, I:] (erf form)     */
+  MI355MOE_ACT_GELU_TANH = 3,  /* gelu_tanh(x[:, :I]) * x[:, I:]           */
+  MI355MOE_ACT_SWIGLUSTEP = 4, /* min(silu(g), lim) * clamp(u, +-lim)      */
+  MI355MOE_ACT_RELU2 = 5       /* relu(x)^2 over all 2I columns, no gate:
+                                  w2 then has K = 2I (relu2_no_mul)        */
 } mi355moe_activation;
 
 /* Layout of the fused layer's weights.  NK is the canonical [E, N, K] (K
@@ -185,6 +190,27 @@ int mi355moe_silu_and_mul(void* out, const void* input, int dtype,
 int mi355moe_swigluoai_and_mul(void* out, const void* input, int dtype,
                                int64_t rows, int64_t d, float alpha,
                                float limit, void* stream);
+
+/* Replace torch.ops._C.gelu_and_mul / gelu_tanh_and_mul (csrc/
+ * torch_bindings.cpp:112-116, csrc/activation.cpp:52-73, 577-593):
+ * in [rows, 2d] -> out[r, c] = T(T(act(x[r, c])) * x[r, d + c]), act the
+ * exact (erf) or tanh-approximated GELU in fp32; dtype F32, F16 or BF16. */
+int mi355moe_gelu_and_mul(void* out, const void* input, int dtype, int64_t rows,
+                          int64_t d, void* stream);
+int mi355moe_gelu_tanh_and_mul(void* out, const void* input, int dtype, int64_t rows,
+                               int64_t d, void* stream);
+
+/* Replaces torch.ops._C.swiglustep_and_mul (csrc/torch_bindings.cpp:197-201,
+ * csrc/activation.cpp:297-311, 711-716): out = T(min(silu(g), limit) *
+ * clamp(u, -limit, limit)) in fp32, g = x[:, :d], u = x[:, d:]. */
+int mi355moe_swiglustep_and_mul(void* out, const void* input, int dtype, int64_t rows,
+                                int64_t d, float limit, void* stream);
+
+/* Replaces torch.ops._C.relu2_no_mul (csrc/torch_bindings.cpp:193-195,
+ * csrc/activation.cpp:44-50, 674-681): out[r, c] = T(max(x, 0)^2),
+ * in and out [rows, d]. */
+int mi355moe_relu2_no_mul(void* out, const void* input, int dtype, int64_t rows,
+                          int64_t d, void* stream);
 
 /* ----------------------------------------------------------- quantisation */
 

@@ -314,6 +314,44 @@ def swigluoai_and_mul(x: torch.Tensor, alpha: float = 1.702,
     return ((u + 1.0) * glu).to(x.dtype)
 
 
+def gelu_erf_f32(f: torch.Tensor) -> torch.Tensor:
+    """csrc/activation.cpp:52-60: f * 0.5 * (1 + erf(f / sqrt(2))) in fp32."""
+    return f * 0.5 * (1.0 + torch.erf(f * 0.7071067811865476))
+
+
+def gelu_tanh_f32(f: torch.Tensor) -> torch.Tensor:
+    """csrc/activation.cpp:62-73: 0.5 f (1 + tanh(sqrt(2/pi) (f + 0.044715
+    f^3))) in fp32."""
+    inner = 0.7978845608028654 * (f + 0.044715 * (f * f * f))
+    return 0.5 * f * (1.0 + torch.tanh(inner))
+
+
+def gelu_and_mul(x: torch.Tensor, approximate: str = "none") -> torch.Tensor:
+    """csrc/activation.cpp:81-86 (act_first): out = T(float(T(gelu(g))) * u),
+    g = x[..., :d], u = x[..., d:]."""
+    d = x.shape[-1] // 2
+    g = x[..., :d].float()
+    u = x[..., d:].float()
+    a = gelu_erf_f32(g) if approximate == "none" else gelu_tanh_f32(g)
+    return (a.to(x.dtype).float() * u).to(x.dtype)
+
+
+def swiglustep_and_mul(x: torch.Tensor, limit: float = 7.0) -> torch.Tensor:
+    """csrc/activation.cpp:297-311: T(min(silu(g), limit) * clamp(u, +-limit))
+    in fp32, one rounding."""
+    d = x.shape[-1] // 2
+    g = x[..., :d].float()
+    u = x[..., d:].float()
+    sg = torch.clamp(g / (1.0 + torch.exp(-g)), max=limit)
+    return (sg * u.clamp(min=-limit, max=limit)).to(x.dtype)
+
+
+def relu2_no_mul(x: torch.Tensor) -> torch.Tensor:
+    """csrc/activation.cpp:44-50: T(max(x, 0)^2) elementwise."""
+    r = torch.clamp(x.float(), min=0.0)
+    return (r * r).to(x.dtype)
+
+
 # ----------------------------------------------------------------------------
 # Quantisation
 # ----------------------------------------------------------------------------
@@ -611,6 +649,14 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
             act = silu_and_mul(g1)
         elif activation == "swigluoai":
             act = swigluoai_and_mul(g1)
+        elif activation == "gelu":
+            act = gelu_and_mul(g1)
+        elif activation == "gelu_tanh":
+            act = gelu_and_mul(g1, "tanh")
+        elif activation == "swiglustep":
+            act = swiglustep_and_mul(g1)
+        elif activation == "relu2_no_mul":
+            act = relu2_no_mul(g1)       # all 2I columns; w2 has K = 2I
         else:
             raise ValueError(activation)
         aq = qdq_act(recipe, act)

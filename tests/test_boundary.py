@@ -114,6 +114,13 @@ def test_version_and_error_plumbing(lib):
         None, None, 1, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
         ctypes.c_int64(128), ctypes.c_int64(64), ctypes.c_float(1e-10), None),
      b"MXFP4 requires group_size == 32"),
+    (lambda L: L.mi355moe_gelu_and_mul(None, None, 3, ctypes.c_int64(2), ctypes.c_int64(8), None),
+     b"gelu_and_mul: unsupported dtype"),
+    (lambda L: L.mi355moe_swiglustep_and_mul(None, None, 4, ctypes.c_int64(2), ctypes.c_int64(8),
+                                             ctypes.c_float(7.0), None),
+     b"swiglustep_and_mul: unsupported dtype"),
+    (lambda L: L.mi355moe_relu2_no_mul(None, None, 7, ctypes.c_int64(2), ctypes.c_int64(8), None),
+     b"relu2_no_mul: unsupported dtype"),
     (lambda L: L.mi355moe_silu_and_mul_mxfp4_quant(
         None, None, 1, None, ctypes.c_int64(4), ctypes.c_int64(1), ctypes.c_int64(4),
         ctypes.c_int64(128), ctypes.c_int64(32), ctypes.c_float(0.0), None),
@@ -167,6 +174,10 @@ def test_fused_moe_workspace_query_and_validation(lib):
     a.w_layout = 7
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"unknown weight layout" in lib.mi355moe_last_error()
+    a.w_layout, a.activation = 0, 6
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"unsupported activation" in lib.mi355moe_last_error()
+    a.activation = 0
     # caller-quantised hidden states: fp8block only
     a.w_layout, a.hidden_scale = 0, 64
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
@@ -188,6 +199,10 @@ REFERENCE_SCHEMAS = {
     "_C::swigluoai_and_mul": "swigluoai_and_mul(Tensor! out, Tensor input, float alpha=1.702, float limit=7.0) -> ()",
     "_C::per_token_group_fp8_quant": "per_token_group_fp8_quant(Tensor input, Tensor! output_q, Tensor! output_s, int group_size, float eps, float fp8_min, float fp8_max, bool scale_ue8m0, bool dummy_is_scale_transposed, bool dummy_is_tma_aligned ) -> ()",
     "_C::per_token_group_quant_mxfp4": "per_token_group_quant_mxfp4(Tensor input, Tensor! output_q, Tensor! output_s, int group_size, float eps) -> ()",
+    "_C::gelu_and_mul": "gelu_and_mul(Tensor! out, Tensor input) -> ()",
+    "_C::gelu_tanh_and_mul": "gelu_tanh_and_mul(Tensor! out, Tensor input) -> ()",
+    "_C::relu2_no_mul": "relu2_no_mul(Tensor! out, Tensor! input) -> ()",
+    "_C::swiglustep_and_mul": "swiglustep_and_mul(Tensor! out, Tensor input, float limit=7.0) -> ()",
     "_C::silu_and_mul_per_block_quant": "silu_and_mul_per_block_quant(Tensor! out, Tensor input, Tensor! scales, int group_size, Tensor? scale_ub=None, bool is_scale_transposed=False, bool scale_ue8m0=False) -> ()",
     "_C::silu_and_mul_mxfp4_quant": "silu_and_mul_mxfp4_quant(Tensor! out, Tensor input, Tensor! scales, int group_size, float eps=1e-10) -> ()",
     "_xpu_C::cutlass_grouped_gemm_interface": "cutlass_grouped_gemm_interface(Tensor ptr_A, Tensor? ptr_A_scale, Tensor ptr_B, Tensor? ptr_B_scale, Tensor? ptr_bias, Tensor ptr_D, Tensor rows_per_expert, int N, int K, int num_experts) -> Tensor",

@@ -31,6 +31,29 @@ def test_silu_and_mul(dev, rows, d, dt):
     torch.testing.assert_close(y, O.silu_and_mul(x), rtol=rtol, atol=atol)
 
 
+# reference tests/test_activation.py:13-15 shapes, plus an odd d (scalar path)
+@pytest.mark.parametrize("rows,d", [(7, 512), (83, 13824), (2048, 512), (3, 1000)])
+@pytest.mark.parametrize("dt", DT)
+@pytest.mark.parametrize("act", ["gelu", "gelu_tanh", "swiglustep", "relu2"])
+def test_gelu_swiglustep_relu2(dev, rows, d, dt, act):
+    scale = 4.0 if act == "swiglustep" else 1.0
+    x = (torch.randn(rows, 2 * d, generator=torch.Generator().manual_seed(d + rows)) * scale).to(dt)
+    ops = _ops()
+    if act == "gelu":
+        y, ref = ops.gelu_and_mul(x.to(dev)), O.gelu_and_mul(x)
+    elif act == "gelu_tanh":
+        y, ref = ops.gelu_tanh_and_mul(x.to(dev)), O.gelu_and_mul(x, "tanh")
+    elif act == "swiglustep":
+        y, ref = ops.swiglustep_and_mul(x.to(dev), 3.0), O.swiglustep_and_mul(x, 3.0)
+    else:
+        y, ref = ops.relu2_no_mul(x.to(dev)), O.relu2_no_mul(x)
+    rtol, atol = _tol(dt)
+    if act == "relu2":
+        assert torch.equal(y.cpu(), ref)     # one product, one rounding
+    else:
+        torch.testing.assert_close(y.cpu(), ref, rtol=rtol, atol=atol)
+
+
 @pytest.mark.parametrize("rows,d", [(7, 1024), (33, 2880)])
 @pytest.mark.parametrize("dt", DT)
 def test_swigluoai_and_mul(dev, rows, d, dt):

@@ -562,6 +562,51 @@ def test_fused_moe_a1q_scale_pre_quantised(dev, T):
     _close(out3[toks], _oracle_layer(cfg, w, xq3, tw, ti, toks, a1q_scale=xs3), fp8=True)
 
 
+@pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4"])
+@pytest.mark.parametrize("act", ["gelu", "gelu_tanh", "swiglustep", "relu2_no_mul"])
+@pytest.mark.parametrize("T", [2, 48, 1024])
+def test_fused_moe_generic_activations(dev, recipe, act, T):
+    """Activations with no GEMM-epilogue form (w13 stores G1, one kernel
+    applies the activation and, for fp8, the 1x128 re-quantisation; relu2_no_mul
+    keeps 2I columns, so w2 has K = 2I): H=384, I=256, 8 experts, top-2,
+    T = 2 (split-K stream), 48 (small), 1024 (320-slot) against the oracle."""
+    import dataclasses
+    cfg = dataclasses.replace(_W().CONFIGS["C2"], recipe=recipe, hidden=384, inter=256,
+                              experts=8, topk=2, activation=act)
+    cfg, w, x, tw, ti, out, moe = _layer(cfg, T, dev)
+    toks = torch.linspace(0, T - 1, min(T, 48)).long().to(dev)
+    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks), fp8=recipe == "fp8block")
+
+
+def test_fused_moe_generic_activation_clamp(dev):
+    """gemm1_clamp_limit on the bf16 halves before the activation."""
+    import dataclasses
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    W = _W()
+    for act in ("gelu", "relu2_no_mul"):
+        cfg = dataclasses.replace(W.CONFIGS["C2"], hidden=256, inter=128, experts=4, topk=2,
+                                  activation=act)
+        w = W.make_weights(cfg, dev)
+        x = W.make_activations(cfg, 40, dev) * 30
+        tw, ti = W.route(cfg, W.make_router_logits(cfg, 40, dev))
+        moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                          cfg.topk, act, cfg.experts, gemm1_clamp_limit=0.5)
+        out = torch.empty_like(x)
+        moe.apply(out, x, tw, ti)
+        ref = _oracle_layer(cfg, w, x, tw, ti)
+        ti_c = ti.cpu().long()
+        used = torch.unique(ti_c)
+        remap = torch.full((cfg.experts,), -1, dtype=torch.long)
+        remap[used] = torch.arange(used.numel())
+        ref = O.fused_moe("bf16", x.cpu(),
+                          w.w13.index_select(0, used.to(dev)).transpose(1, 2).contiguous().cpu(),
+                          None, None,
+                          w.w2.index_select(0, used.to(dev)).transpose(1, 2).contiguous().cpu(),
+                          None, None, tw.cpu(), remap[ti_c], activation=act,
+                          gemm1_clamp_limit=0.5)
+        _close(out, ref)
+
+
 def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):
     cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C1"], 8, dev)
     with pytest.raises(NotImplementedError, match="fp8 block-scaled recipe"):

@@ -254,6 +254,51 @@ def test_fp8_group_quant_scale_closed_form():
     assert s[0, 0].item() == 2.0 ** math.ceil(math.log2(3.0 / 448.0))
 
 
+# ----------------------------------------------- gelu / swiglustep / relu2
+def test_gelu_forms_match_torch_and_identities():
+    """The erf and tanh GELU forms agree with torch's own GELU (within 2e-6:
+    1 + erf(x/sqrt 2) cancels for negative x, in the reference kernel's form
+    as in this one);
+    the erf form satisfies gelu(x) - gelu(-x) = x (its odd part) and
+    gelu(0) = 0; gelu_and_mul rounds gelu(g) to the element type before the
+    multiply."""
+    F = torch.nn.functional
+    x = torch.linspace(-8, 8, 4001)
+    torch.testing.assert_close(O.gelu_erf_f32(x), F.gelu(x), rtol=1e-6, atol=2e-6)
+    torch.testing.assert_close(O.gelu_tanh_f32(x), F.gelu(x, approximate="tanh"),
+                               rtol=1e-6, atol=2e-6)
+    torch.testing.assert_close(O.gelu_erf_f32(x) - O.gelu_erf_f32(-x), x, rtol=1e-6, atol=1e-6)
+    assert O.gelu_erf_f32(torch.zeros(1)).item() == 0.0
+    g = torch.Generator().manual_seed(3)
+    xx = torch.randn(16, 512, generator=g).bfloat16()
+    y = O.gelu_and_mul(xx)
+    unrounded = (F.gelu(xx[:, :256].float()) * xx[:, 256:].float()).bfloat16()
+    assert not torch.equal(y, unrounded)
+    torch.testing.assert_close(y.float(), unrounded.float(), rtol=1.6e-2, atol=1e-3)
+    yt = O.gelu_and_mul(xx, "tanh")
+    ref = (F.gelu(xx[:, :256].float(), approximate="tanh").bfloat16().float() *
+           xx[:, 256:].float()).bfloat16()
+    torch.testing.assert_close(yt.float(), ref.float(), rtol=1.6e-2, atol=1e-3)
+
+
+def test_swiglustep_matches_reference_test_formula():
+    """fp32 input: the reference test's forward_native
+    (tests/ops/swiglustep_and_mul_op.py:23-29) up to the exp ulp; the gate
+    clamps only from above, the up input both ways."""
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(32, 256, generator=g) * 6
+    ref = F.silu(x[:, :128]).clamp(max=7.0) * x[:, 128:].clamp(min=-7.0, max=7.0)
+    torch.testing.assert_close(O.swiglustep_and_mul(x), ref, rtol=2e-6, atol=1e-6)
+    t = torch.tensor([[20.0, -20.0, 100.0, -100.0]])
+    assert O.swiglustep_and_mul(t).tolist() == [[7.0 * 7.0, pytest.approx(-20.0 / (1 + math.exp(20.0)) * -7.0)]]
+
+
+def test_relu2_exact_values():
+    x = torch.tensor([-1.0, 0.0, 1.5, 3.0, -0.0]).bfloat16()
+    assert O.relu2_no_mul(x).float().tolist() == [0.0, 0.0, 2.25, 9.0, 0.0]
+
+
 # ------------------------------------------- fused SiLU-and-mul + quantisers
 def _gate_up(T, H, seed, dtype=torch.bfloat16, scale=1.0):
     g = torch.Generator().manual_seed(seed)

@@ -80,6 +80,16 @@ struct F16 {
   static __device__ __forceinline__ uint16_t st(float v) { return f32_to_f16(v); }
 };
 
+// GELU in fp32, textbook forms: exact (erf) and the tanh approximation
+// sqrt(2/pi) (x + 0.044715 x^3).
+__device__ __forceinline__ float gelu_erf(float f) {
+  return f * 0.5f * (1.0f + erff(f * 0.70710678118654752f));
+}
+__device__ __forceinline__ float gelu_tanh(float f) {
+  const float inner = 0.7978845608028654f * (f + 0.044715f * (f * f * f));
+  return 0.5f * f * (1.0f + tanhf(inner));
+}
+
 // OCP e4m3fn decode (bias 7, no infinities, 0x7f/0xff NaN).
 __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
   uint32_t s = (b & 0x80u) << 24;

@@ -101,6 +101,62 @@ __global__ __launch_bounds__(256) void swigluoai_kernel(
     y[c] = E::st(swigluoai(E::ld(x[2 * c]), E::ld(x[2 * c + 1]), alpha, limit));
 }
 
+// Gated activations other than SiLU (gelu_erf, gelu_tanh: common.h).
+enum GluAct { GLU_GELU = 0, GLU_GELU_TANH = 1, GLU_SWIGLUSTEP = 2 };
+// gate g, up u -> output before the final rounding to E: gelu forms round
+// act(g) to E first (the activation returns the element type), swiglustep
+// stays in fp32.
+template <typename E, int ACT>
+__device__ __forceinline__ float glu_op(float g, float u, float limit) {
+  if constexpr (ACT == GLU_GELU) {
+    return E::ld(E::st(gelu_erf(g))) * u;
+  } else if constexpr (ACT == GLU_GELU_TANH) {
+    return E::ld(E::st(gelu_tanh(g))) * u;
+  } else {
+    const float sg = fminf(g / (1.f + expf(-g)), limit);
+    return sg * fminf(fmaxf(u, -limit), limit);
+  }
+}
+
+template <typename E, int ACT>
+__global__ __launch_bounds__(256) void glu_act_kernel(
+    void* __restrict__ out, const void* __restrict__ in, int64_t rows, int64_t d,
+    float limit) {
+  const int64_t r = blockIdx.y;
+  const typename E::T* x = static_cast<const typename E::T*>(in) + r * 2 * d;
+  typename E::T* y = static_cast<typename E::T*>(out) + r * d;
+  if constexpr (sizeof(typename E::T) == 2) {
+    if ((d & 7) == 0) {
+      for (int64_t c = (blockIdx.x * 256 + threadIdx.x) * 8; c < d;
+           c += static_cast<int64_t>(gridDim.x) * 256 * 8) {
+        float g[8], u[8], o[8];
+        Vec8<E>::load(x + c, g);
+        Vec8<E>::load(x + d + c, u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = glu_op<E, ACT>(g[i], u[i], limit);
+        Vec8<E>::store(y + c, o);
+      }
+      return;
+    }
+  }
+  for (int64_t c = blockIdx.x * 256 + threadIdx.x; c < d;
+       c += static_cast<int64_t>(gridDim.x) * 256)
+    y[c] = E::st(glu_op<E, ACT>(E::ld(x[c]), E::ld(x[d + c]), limit));
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void relu2_kernel(void* __restrict__ out,
+                                                    const void* __restrict__ in,
+                                                    int64_t n) {
+  const typename E::T* x = static_cast<const typename E::T*>(in);
+  typename E::T* y = static_cast<typename E::T*>(out);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const float r = fmaxf(E::ld(x[i]), 0.f);
+    y[i] = E::st(r * r);
+  }
+}
+
 // ----------------------------------------------------------- quantisation
 // One group of G elements is owned by G/8 consecutive lanes (8 elements per
 // lane); requires G % 8 == 0 and G/8 a power of two <= 64.
@@ -388,6 +444,63 @@ extern "C" int mi355moe_swigluoai_and_mul(void* out, const void* in, int dt,
             static_cast<unsigned>(rows));
   MI_DISPATCH_FLOAT(dt, (swigluoai_kernel<E><<<grid, dim3(256), 0, st>>>(out, in, rows, d, alpha, limit)),
                     "swigluoai_and_mul: unsupported dtype")
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+namespace {
+int launch_glu(int act, void* out, const void* in, int dt, int64_t rows, int64_t d,
+               float limit, void* stream, const char* what) {
+  MI_ARG(rows >= 0 && d >= 0, "invalid shape");
+  if (rows == 0 || d == 0) return MI355MOE_OK;
+  MI_ARG(rows <= 0x7fffffff, "too many rows");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t per = (d & 7) == 0 ? d / 8 : d;
+  dim3 grid(static_cast<unsigned>(std::min<int64_t>(cdiv(per, 256), 64)),
+            static_cast<unsigned>(rows));
+  switch (act) {
+    case GLU_GELU:
+      MI_DISPATCH_FLOAT(dt, (glu_act_kernel<E, GLU_GELU><<<grid, dim3(256), 0, st>>>(out, in, rows, d, limit)), what)
+      break;
+    case GLU_GELU_TANH:
+      MI_DISPATCH_FLOAT(dt, (glu_act_kernel<E, GLU_GELU_TANH><<<grid, dim3(256), 0, st>>>(out, in, rows, d, limit)), what)
+      break;
+    default:
+      MI_DISPATCH_FLOAT(dt, (glu_act_kernel<E, GLU_SWIGLUSTEP><<<grid, dim3(256), 0, st>>>(out, in, rows, d, limit)), what)
+      break;
+  }
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+}  // namespace
+
+extern "C" int mi355moe_gelu_and_mul(void* out, const void* in, int dt, int64_t rows,
+                                     int64_t d, void* stream) {
+  return launch_glu(GLU_GELU, out, in, dt, rows, d, 0.f, stream,
+                    "gelu_and_mul: unsupported dtype");
+}
+
+extern "C" int mi355moe_gelu_tanh_and_mul(void* out, const void* in, int dt, int64_t rows,
+                                          int64_t d, void* stream) {
+  return launch_glu(GLU_GELU_TANH, out, in, dt, rows, d, 0.f, stream,
+                    "gelu_tanh_and_mul: unsupported dtype");
+}
+
+extern "C" int mi355moe_swiglustep_and_mul(void* out, const void* in, int dt, int64_t rows,
+                                           int64_t d, float limit, void* stream) {
+  return launch_glu(GLU_SWIGLUSTEP, out, in, dt, rows, d, limit, stream,
+                    "swiglustep_and_mul: unsupported dtype");
+}
+
+extern "C" int mi355moe_relu2_no_mul(void* out, const void* in, int dt, int64_t rows,
+                                     int64_t d, void* stream) {
+  MI_ARG(rows >= 0 && d >= 0, "invalid shape");
+  const int64_t n = rows * d;
+  if (n == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(std::min<int64_t>(cdiv(n, 256), 8192)));
+  MI_DISPATCH_FLOAT(dt, (relu2_kernel<E><<<grid, dim3(256), 0, st>>>(out, in, n)),
+                    "relu2_no_mul: unsupported dtype")
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }

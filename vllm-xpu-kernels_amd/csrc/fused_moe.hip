@@ -150,6 +150,122 @@ __global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
                  f32_to_bf16(a2) | (uint32_t(f32_to_bf16(a3)) << 16));
 }
 
+struct FusedActArgs {
+  const uint16_t* g1;
+  void* act;
+  float* acts;
+  const int32_t* ntp;
+  int64_t rows, inter;
+  float clamp, limit;
+};
+
+// Activations without a GEMM-epilogue form (gelu, gelu_tanh, swiglustep,
+// relu2_no_mul): the w13 output G1 (bf16 [rows, 2I] by sorted position,
+// gate | up) -> activation [rows, K2], K2 = I (gated) or 2I (relu2_no_mul),
+// with the reference's rounding points (G1 and, for gelu, act(gate) rounded
+// to bf16; swiglustep in fp32; gemm1_clamp_limit on the bf16 halves first;
+// fused_moe_interface.py:383-396).  Each lane makes 8 output columns; Q8:
+// e4m3 with 1x128 scales of the bf16 activation (16 lanes per group), as the
+// fp8 GLU epilogues quantise it.  Rows from *ntp on (padding past the last
+// block) are not touched; K2 % 128 == 0 when Q8, so a group's lanes share a
+// row and leave together.
+__device__ __forceinline__ float rbf(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <int ACT, bool Q8>
+__global__ __launch_bounds__(256) void fused_act_kernel(
+    const uint16_t* __restrict__ g1, void* __restrict__ act, float* __restrict__ acts,
+    const int32_t* __restrict__ ntp, int64_t inter, float clamp, float limit) {
+  const int64_t k2 = ACT == MI355MOE_ACT_RELU2 ? 2 * inter : inter;
+  const int64_t cpr = k2 >> 3;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t r = gtid / cpr;
+  const int64_t c0 = (gtid % cpr) * 8;
+  if (r >= *ntp) return;
+  const uint16_t* x = g1 + r * 2 * inter;
+  const uint4 xa = *reinterpret_cast<const uint4*>(x + c0);
+  const uint32_t wa[4] = {xa.x, xa.y, xa.z, xa.w};
+  float y[8];
+  if constexpr (ACT == MI355MOE_ACT_RELU2) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = bf16_to_f32(static_cast<uint16_t>(wa[i >> 1] >> (16 * (i & 1))));
+      if (clamp > 0.f)
+        v = rbf(c0 + i < inter ? fminf(v, clamp) : fminf(fmaxf(v, -clamp), clamp));
+      const float p = fmaxf(v, 0.f);
+      y[i] = rbf(p * p);
+    }
+  } else {
+    const uint4 xb = *reinterpret_cast<const uint4*>(x + inter + c0);
+    const uint32_t wb[4] = {xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float g = bf16_to_f32(static_cast<uint16_t>(wa[i >> 1] >> (16 * (i & 1))));
+      float u = bf16_to_f32(static_cast<uint16_t>(wb[i >> 1] >> (16 * (i & 1))));
+      if (clamp > 0.f) {
+        g = rbf(fminf(g, clamp));
+        u = rbf(fminf(fmaxf(u, -clamp), clamp));
+      }
+      float v;
+      if constexpr (ACT == MI355MOE_ACT_GELU) {
+        v = rbf(gelu_erf(g)) * u;
+      } else if constexpr (ACT == MI355MOE_ACT_GELU_TANH) {
+        v = rbf(gelu_tanh(g)) * u;
+      } else {
+        v = fminf(g / (1.f + expf(-g)), limit) * fminf(fmaxf(u, -limit), limit);
+      }
+      y[i] = rbf(v);
+    }
+  }
+  if constexpr (Q8) {
+    float amax = 1e-10f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(y[i]));
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float sc = fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
+    if ((gtid & 15) == 0) acts[r * (k2 / 128) + c0 / 128] = sc;
+    const float inv = 1.0f / sc;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t b = f32_to_e4m3(fminf(fmaxf(y[i] * inv, -448.0f), 448.0f));
+      if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+    }
+    *reinterpret_cast<uint2*>(static_cast<uint8_t*>(act) + r * k2 + c0) = make_uint2(lo, hi);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = f32_to_bf16(y[2 * i]) | (static_cast<uint32_t>(f32_to_bf16(y[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(act) + r * k2 + c0) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <bool Q8>
+void launch_fused_act(int act, const FusedActArgs& f, hipStream_t st) {
+  const int64_t k2 = act == MI355MOE_ACT_RELU2 ? 2 * f.inter : f.inter;
+  dim3 grid(static_cast<unsigned>(cdiv(f.rows * (k2 / 8), 256)));
+  switch (act) {
+    case MI355MOE_ACT_GELU:
+      fused_act_kernel<MI355MOE_ACT_GELU, Q8><<<grid, dim3(256), 0, st>>>(
+          f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
+      break;
+    case MI355MOE_ACT_GELU_TANH:
+      fused_act_kernel<MI355MOE_ACT_GELU_TANH, Q8><<<grid, dim3(256), 0, st>>>(
+          f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
+      break;
+    case MI355MOE_ACT_SWIGLUSTEP:
+      fused_act_kernel<MI355MOE_ACT_SWIGLUSTEP, Q8><<<grid, dim3(256), 0, st>>>(
+          f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
+      break;
+    default:
+      fused_act_kernel<MI355MOE_ACT_RELU2, Q8><<<grid, dim3(256), 0, st>>>(
+          f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
+      break;
+  }
+}
+
 int group_quant_fp8(const void* x, int dt, uint8_t* q, float* s, int64_t rows,
                     int64_t cols, hipStream_t st) {
   return mi355moe_per_token_group_fp8_quant(x, dt, q, s, rows, cols, 128, 1e-10f,
@@ -169,20 +285,32 @@ struct FusedLayout {
   size_t sortws_bytes;
   uint8_t* xq;    // fp8 hidden [T, H]
   float* xs;      // [T, H/128]
-  void* act;      // bf16 [max_padded, I] or e4m3 [max_padded, I]
-  float* acts;    // [max_padded, I/128]
+  void* act;      // bf16 [max_padded, K2] or e4m3 [max_padded, K2]
+  float* acts;    // [max_padded, K2/128]
+  uint16_t* g1;   // generic activations: w13 output bf16 [max_padded, 2I]
   uint16_t* g2;   // bf16 [slots, H]
   size_t bytes;
 };
+
+// Activations the w13 GEMM epilogue applies itself; the others run as a
+// separate kernel over the stored w13 output.
+bool epilogue_act(int act) {
+  return act == MI355MOE_ACT_SILU || act == MI355MOE_ACT_SWIGLUOAI;
+}
+// Width of the activation (and K of the w2 GEMM): relu2_no_mul keeps all 2I.
+int64_t act_width(const mi355moe_fused_moe_args* a) {
+  return a->activation == MI355MOE_ACT_RELU2 ? 2 * a->inter : a->inter;
+}
 
 FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
   const int64_t E = a->num_experts;
   L.slots = a->num_tokens * a->topk;
-  const int64_t H = a->hidden, I = a->inter;
+  const int64_t H = a->hidden, I = a->inter, K2 = act_width(a);
+  const bool glu = epilogue_act(a->activation);
   const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
   const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H, kblock) &&
-                       wide_ok_for(a->recipe, L.slots + E * kWideBM, H, I, kblock);
+                       wide_ok_for(a->recipe, L.slots + E * kWideBM, H, K2, kblock);
   L.tile = pick_tile(a->recipe, wide_ok, L.slots, E, &L.bm);
   // K-blocked weights: the families that read them (STREAM, SMALL, WIDE, and
   // BIG for fp8, whose 8-wave kernel takes K <= 8192, and for mxfp4)
@@ -203,9 +331,10 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   L.part1 = L.part2 = nullptr;
   if (L.tile == TILE_STREAM) {
     const int64_t act_blocks = std::min<int64_t>(L.slots, E);
-    const int64_t nt1 = cdiv(a->inter, 128), nt2 = cdiv(a->hidden, 256);
-    L.ks1 = stream_ksplit(nt1, act_blocks, a->hidden);
-    L.ks2 = stream_ksplit(nt2, act_blocks, a->inter);
+    // GLU tiles cover 128 activation columns, STORE tiles 256 of G1
+    const int64_t nt1 = glu ? cdiv(I, 128) : cdiv(2 * I, 256), nt2 = cdiv(H, 256);
+    L.ks1 = stream_ksplit(nt1, act_blocks, H);
+    L.ks2 = stream_ksplit(nt2, act_blocks, K2);
     const int64_t tile_f = 512 * 8;
     if (L.ks1 > 1) L.part1 = c.take<float>(L.max_blocks * nt1 * L.ks1 * tile_f);
     if (L.ks2 > 1) L.part2 = c.take<float>(L.max_blocks * nt2 * L.ks2 * tile_f);
@@ -217,11 +346,12 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   if (fp8) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
     L.xs = c.take<float>(a->num_tokens * (a->hidden / 128));
-    L.act = c.take<uint8_t>(L.max_padded * a->inter);
-    L.acts = c.take<float>(L.max_padded * (a->inter / 128));
+    L.act = c.take<uint8_t>(L.max_padded * K2);
+    L.acts = c.take<float>(L.max_padded * (K2 / 128));
   } else {
-    L.act = c.take<uint16_t>(L.max_padded * a->inter);
+    L.act = c.take<uint16_t>(L.max_padded * K2);
   }
+  L.g1 = glu ? nullptr : c.take<uint16_t>(L.max_padded * 2 * I);
   L.g2 = c.take<uint16_t>(L.slots * a->hidden);
   L.bytes = c.off + 256;
   return L;
@@ -307,7 +437,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
          "pre-quantised hidden_states (hidden_scale) need the fp8block recipe");
   MI_ARG(a->ids_dtype == MI355MOE_I32 || a->ids_dtype == MI355MOE_I64,
          "topk_ids must be int32 or int64");
-  MI_ARG(a->activation == MI355MOE_ACT_SILU || a->activation == MI355MOE_ACT_SWIGLUOAI,
+  MI_ARG(a->activation >= MI355MOE_ACT_SILU && a->activation <= MI355MOE_ACT_RELU2,
          "unsupported activation");
   const int recipe = a->recipe;
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
@@ -325,7 +455,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
          "unknown weight layout");
   const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
   MI_ARG(!kblock || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0) ||
-             (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && I <= 8192) ||
+             (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && act_width(a) <= 8192) ||
              recipe == MI355MOE_RECIPE_MXFP4,
          "K-blocked weights need the bf16 recipe (hidden and intermediate sizes "
          "% 32 == 0), the fp8block recipe (sizes at most 8192) or mxfp4");
@@ -358,13 +488,17 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   }
   if (int m = mark(2)) return m;
 
+  // gelu / gelu_tanh / swiglustep / relu2_no_mul: w13 stores G1, a separate
+  // kernel applies the activation (and the fp8 re-quantisation)
+  const bool glu = epilogue_act(a->activation);
+  const int64_t K2 = act_width(a);
   GemmArgs g1{};
   g1.A = fp8 && !preq ? static_cast<const void*>(L.xq) : a->hidden_states;
   g1.a_scale = preq ? a->hidden_scale : (fp8 ? L.xs : nullptr);
   g1.B = a->w13;
   g1.b_scale = a->w13_scale;
   g1.bias = static_cast<const uint16_t*>(a->w13_bias);
-  g1.D = L.act;
+  g1.D = glu ? L.act : static_cast<void*>(L.g1);
   g1.row_ids = L.sorted;
   g1.block_expert = L.eids;
   g1.ntp = L.ntp;
@@ -373,10 +507,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.a_div = static_cast<int32_t>(k);
   g1.a_by_pos = 0;
   g1.d_by_pos = 1;
-  g1.N = I;
+  g1.N = glu ? I : 2 * I;
   g1.K = H;
   g1.ldb_rows = 2 * I;
-  g1.up_off = I;
+  g1.up_off = glu ? I : 0;
   g1.clamp_limit = a->gemm1_clamp_limit;
   g1.alpha = a->swiglu_alpha;
   g1.limit = a->swiglu_limit;
@@ -384,8 +518,19 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.ksplit = L.ks1;
   g1.part = L.part1;
   g1.w_kblock = kblock;
-  rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
-  if (rc) return rc;
+  if (glu) {
+    rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
+    if (rc) return rc;
+  } else {
+    rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g1, L.grid_blocks, nullptr,
+                          st);
+    if (rc) return rc;
+    const FusedActArgs f{L.g1, L.act, L.acts, L.ntp, L.max_padded, I,
+                         a->gemm1_clamp_limit, a->swiglu_limit};
+    if (fp8) launch_fused_act<true>(a->activation, f, st);
+    else launch_fused_act<false>(a->activation, f, st);
+    MI_LAUNCH_CHECK();
+  }
   if (int m = mark(3)) return m;
 
   GemmArgs g2{};
@@ -404,7 +549,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.a_by_pos = 1;
   g2.d_by_pos = 0;
   g2.N = H;
-  g2.K = I;
+  g2.K = K2;
   g2.ldb_rows = H;
   g2.up_off = 0;
   g2.ksplit = L.ks2;

@@ -300,12 +300,20 @@ void moe_gather(at::Tensor& output, at::Tensor& moe_output,
 }
 
 // ------------------------------------------------------------- activations
-void silu_and_mul(at::Tensor& out, at::Tensor& input) {
+// in [..., 2d] -> out [..., d] of the same dtype; returns (rows, d)
+std::pair<int64_t, int64_t> gated_shape(const at::Tensor& out, const at::Tensor& input) {
   check_gpu(out, "out");
   check_gpu(input, "input");
   TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
   const int64_t d = input.size(-1) / 2;
   const int64_t rows = input.numel() / std::max<int64_t>(2 * d, 1);
+  TORCH_CHECK(input.size(-1) == 2 * d && out.size(-1) == d && out.numel() == rows * d,
+              "out must be [..., d] for input [..., 2 * d]");
+  return {rows, d};
+}
+
+void silu_and_mul(at::Tensor& out, at::Tensor& input) {
+  const auto [rows, d] = gated_shape(out, input);
   DevGuard g(input.device());
   check_rc(mi355moe_silu_and_mul(out.data_ptr(), input.data_ptr(),
                                  dtype_code(input.scalar_type()), rows, d,
@@ -314,17 +322,55 @@ void silu_and_mul(at::Tensor& out, at::Tensor& input) {
 }
 
 void swigluoai_and_mul(at::Tensor& out, at::Tensor& input, double alpha, double limit) {
-  check_gpu(out, "out");
-  check_gpu(input, "input");
-  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
-  const int64_t d = input.size(-1) / 2;
-  const int64_t rows = input.numel() / std::max<int64_t>(2 * d, 1);
+  const auto [rows, d] = gated_shape(out, input);
   DevGuard g(input.device());
   check_rc(mi355moe_swigluoai_and_mul(out.data_ptr(), input.data_ptr(),
                                       dtype_code(input.scalar_type()), rows, d,
                                       static_cast<float>(alpha),
                                       static_cast<float>(limit), cur_stream(input)),
            "swigluoai_and_mul");
+}
+
+// reference csrc/activation.cpp:577-593
+void gelu_and_mul(at::Tensor& out, const at::Tensor& input) {
+  const auto [rows, d] = gated_shape(out, input);
+  DevGuard g(input.device());
+  check_rc(mi355moe_gelu_and_mul(out.data_ptr(), input.data_ptr(),
+                                 dtype_code(input.scalar_type()), rows, d, cur_stream(input)),
+           "gelu_and_mul");
+}
+
+void gelu_tanh_and_mul(at::Tensor& out, const at::Tensor& input) {
+  const auto [rows, d] = gated_shape(out, input);
+  DevGuard g(input.device());
+  check_rc(mi355moe_gelu_tanh_and_mul(out.data_ptr(), input.data_ptr(),
+                                      dtype_code(input.scalar_type()), rows, d,
+                                      cur_stream(input)),
+           "gelu_tanh_and_mul");
+}
+
+// reference csrc/activation.cpp:711-716
+void swiglustep_and_mul(at::Tensor& out, const at::Tensor& input, double limit) {
+  const auto [rows, d] = gated_shape(out, input);
+  DevGuard g(input.device());
+  check_rc(mi355moe_swiglustep_and_mul(out.data_ptr(), input.data_ptr(),
+                                       dtype_code(input.scalar_type()), rows, d,
+                                       static_cast<float>(limit), cur_stream(input)),
+           "swiglustep_and_mul");
+}
+
+// reference csrc/activation.cpp:674-681 (input and out [..., d])
+void relu2_no_mul(at::Tensor& out, at::Tensor& input) {
+  check_gpu(out, "out");
+  check_gpu(input, "input");
+  TORCH_CHECK(out.scalar_type() == input.scalar_type(), "out and input must have the same dtype");
+  TORCH_CHECK(out.numel() == input.numel(), "out must have the shape of input");
+  const int64_t d = input.dim() > 0 ? input.size(-1) : 1;
+  const int64_t rows = d > 0 ? input.numel() / d : 0;
+  DevGuard g(input.device());
+  check_rc(mi355moe_relu2_no_mul(out.data_ptr(), input.data_ptr(),
+                                 dtype_code(input.scalar_type()), rows, d, cur_stream(input)),
+           "relu2_no_mul");
 }
 
 // ------------------------------------------------------------ quantisation
@@ -696,6 +742,10 @@ TORCH_LIBRARY(_C, m) {
         "-> ()");
   m.def("per_token_group_quant_mxfp4(Tensor input, Tensor! output_q, Tensor! "
         "output_s, int group_size, float eps) -> ()");
+  m.def("gelu_and_mul(Tensor! out, Tensor input) -> ()");
+  m.def("gelu_tanh_and_mul(Tensor! out, Tensor input) -> ()");
+  m.def("relu2_no_mul(Tensor! out, Tensor! input) -> ()");
+  m.def("swiglustep_and_mul(Tensor! out, Tensor input, float limit=7.0) -> ()");
   m.def("silu_and_mul_per_block_quant(Tensor! out, Tensor input, Tensor! scales, "
         "int group_size, Tensor? scale_ub=None, bool is_scale_transposed=False, "
         "bool scale_ue8m0=False) -> ()");
@@ -708,6 +758,10 @@ TORCH_LIBRARY_IMPL(_C, CUDA, m) {
   m.impl("swigluoai_and_mul", &swigluoai_and_mul);
   m.impl("per_token_group_fp8_quant", &per_token_group_fp8_quant);
   m.impl("silu_and_mul_per_block_quant", &silu_and_mul_per_block_quant);
+  m.impl("gelu_and_mul", &gelu_and_mul);
+  m.impl("gelu_tanh_and_mul", &gelu_tanh_and_mul);
+  m.impl("relu2_no_mul", &relu2_no_mul);
+  m.impl("swiglustep_and_mul", &swiglustep_and_mul);
   m.impl("silu_and_mul_mxfp4_quant", &silu_and_mul_mxfp4_quant);
   m.impl("per_token_group_quant_mxfp4", &per_token_group_quant_mxfp4);
 }

@@ -27,7 +27,11 @@ REF_FUSED_MOE_ENV = "VLLM_XPU_FUSED_MOE_USE_REF"
 FP8_BLOCK_SIZE = 128
 
 RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4 = 0, 1, 2
-ACT_SILU, ACT_SWIGLUOAI = 0, 1
+ACT_SILU, ACT_SWIGLUOAI, ACT_GELU, ACT_GELU_TANH, ACT_SWIGLUSTEP, ACT_RELU2 = range(6)
+# reference fused_moe_interface.py:119-133, 239-254
+_ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
+              "gelu_tanh": ACT_GELU_TANH, "swiglustep": ACT_SWIGLUSTEP,
+              "relu2_no_mul": ACT_RELU2}
 WLAYOUT_NK, WLAYOUT_KBLOCK = 0, 1
 WEIGHT_LAYOUT_ENV = "MI355MOE_WEIGHT_LAYOUT"
 
@@ -127,12 +131,15 @@ class XpuFusedMoe:
         self.is_mxfp8 = is_mxfp8
         self.is_block_fp8 = is_block_fp8
         self.gemm1_clamp_limit = gemm1_clamp_limit
-        if activation == "silu":
-            self._act = ACT_SILU
-        elif activation == "swigluoai" or "SWIGLUOAI" in str(activation):
+        if "SWIGLUOAI" in str(activation):
             self._act = ACT_SWIGLUOAI
+        elif activation in _ACT_CODES:
+            self._act = _ACT_CODES[activation]
         else:
             raise ValueError(f"Unsupported FusedMoe activation: {activation}.")
+        # relu2_no_mul keeps all 2I columns: the activation, and w2's K, are
+        # 2I wide (reference :226)
+        self.inter_size_scale = 2 if self._act == ACT_RELU2 else 1
         if is_block_fp8:
             self.recipe = "fp8block"
             self._recipe = RECIPE_FP8BLOCK
@@ -163,6 +170,7 @@ class XpuFusedMoe:
     # ------------------------------------------------------------------
     def _prepare_weights(self, w13, s13, b13, w2, s2, b2):
         I = self.inter_size
+        K2 = I * self.inter_size_scale
         E = w13.shape[0]
         swiglu = self._act == ACT_SWIGLUOAI
         if self._recipe == RECIPE_BF16:
@@ -176,7 +184,7 @@ class XpuFusedMoe:
             # [E, N, K] preferred when ambiguous, as the reference
             # (grouped_gemm_xe2_interface.hpp:206-223)
             w13c = w13 if w13.shape[1] == 2 * I else w13.transpose(1, 2).contiguous()
-            w2c = w2 if w2.shape[2] == I else w2.transpose(1, 2).contiguous()
+            w2c = w2 if w2.shape[2] == K2 else w2.transpose(1, 2).contiguous()
             s13c, s2c = s13.contiguous(), s2.contiguous()
             if swiglu:
                 raise NotImplementedError(
@@ -200,7 +208,7 @@ class XpuFusedMoe:
         if self._recipe == RECIPE_MXFP4:
             H = w13c.shape[2] * 2
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
-                  (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and I <= 8192) or
+                  (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and K2 <= 8192) or
                   self._recipe == RECIPE_MXFP4)
         if kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk":
             w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)

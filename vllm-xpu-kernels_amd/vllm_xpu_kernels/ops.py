@@ -131,6 +131,30 @@ def swigluoai_and_mul(x: torch.Tensor, alpha: float = 1.702,
     return out
 
 
+def gelu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    out = torch.empty(x.shape[:-1] + (x.shape[-1] // 2,), dtype=x.dtype, device=x.device)
+    torch.ops._C.gelu_and_mul(out, x)
+    return out
+
+
+def gelu_tanh_and_mul(x: torch.Tensor) -> torch.Tensor:
+    out = torch.empty(x.shape[:-1] + (x.shape[-1] // 2,), dtype=x.dtype, device=x.device)
+    torch.ops._C.gelu_tanh_and_mul(out, x)
+    return out
+
+
+def swiglustep_and_mul(x: torch.Tensor, limit: float = 7.0) -> torch.Tensor:
+    out = torch.empty(x.shape[:-1] + (x.shape[-1] // 2,), dtype=x.dtype, device=x.device)
+    torch.ops._C.swiglustep_and_mul(out, x, limit)
+    return out
+
+
+def relu2_no_mul(x: torch.Tensor) -> torch.Tensor:
+    out = torch.empty_like(x)
+    torch.ops._C.relu2_no_mul(out, x)
+    return out
+
+
 def per_token_group_fp8_quant(x: torch.Tensor, group_size: int = 128,
                               eps: float = 1e-10,
                               scale_ue8m0: bool = False):

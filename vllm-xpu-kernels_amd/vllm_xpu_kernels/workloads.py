@@ -110,12 +110,18 @@ class MoeWeights:
     w2_bias: Optional[torch.Tensor]
 
 
+def act_width(cfg: MoeConfig) -> int:
+    """Width of the activation, and K of w2: 2I for relu2_no_mul (no gate),
+    else I."""
+    return 2 * cfg.inter if cfg.activation == "relu2_no_mul" else cfg.inter
+
+
 def expert_weights_nk(cfg: MoeConfig, e: int, device, seed: int = 0):
-    """One expert in [N, K] layout: (w13 [2I,H], s13, w2 [H,I], s2), recipe
-    encoded; biases separately via make_biases."""
+    """One expert in [N, K] layout: (w13 [2I,H], s13, w2 [H,K2], s2), recipe
+    encoded (K2 = act_width); biases separately via make_biases."""
     H, I = cfg.hidden, cfg.inter
     w13 = _randn((2 * I, H), 0.02, seed * 1000003 + 2 * e, device)
-    w2 = _randn((H, I), 0.02, seed * 1000003 + 2 * e + 1, device)
+    w2 = _randn((H, act_width(cfg)), 0.02, seed * 1000003 + 2 * e + 1, device)
     if cfg.recipe == "bf16":
         return w13.to(torch.bfloat16), None, w2.to(torch.bfloat16), None
     if cfg.recipe == "fp8block":
@@ -137,21 +143,21 @@ def make_biases(cfg: MoeConfig, device, seed: int = 0):
 
 
 def make_weights(cfg: MoeConfig, device, seed: int = 0) -> MoeWeights:
-    E, H, I = cfg.experts, cfg.hidden, cfg.inter
+    E, H, I, K2 = cfg.experts, cfg.hidden, cfg.inter, act_width(cfg)
     if cfg.recipe == "bf16":
         w13 = torch.empty(E, H, 2 * I, dtype=torch.bfloat16, device=device)
-        w2 = torch.empty(E, I, H, dtype=torch.bfloat16, device=device)
+        w2 = torch.empty(E, K2, H, dtype=torch.bfloat16, device=device)
         s13 = s2 = None
     elif cfg.recipe == "fp8block":
         w13 = torch.empty(E, 2 * I, H, dtype=torch.float8_e4m3fn, device=device)
-        w2 = torch.empty(E, H, I, dtype=torch.float8_e4m3fn, device=device)
+        w2 = torch.empty(E, H, K2, dtype=torch.float8_e4m3fn, device=device)
         s13 = torch.empty(E, 2 * I // 128, H // 128, device=device)
-        s2 = torch.empty(E, H // 128, I // 128, device=device)
+        s2 = torch.empty(E, H // 128, K2 // 128, device=device)
     else:
         w13 = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=device)
-        w2 = torch.empty(E, H, I // 2, dtype=torch.uint8, device=device)
+        w2 = torch.empty(E, H, K2 // 2, dtype=torch.uint8, device=device)
         s13 = torch.empty(E, 2 * I, H // 32, dtype=torch.uint8, device=device)
-        s2 = torch.empty(E, H, I // 32, dtype=torch.uint8, device=device)
+        s2 = torch.empty(E, H, K2 // 32, dtype=torch.uint8, device=device)
     for e in range(E):
         a, sa, b, sb = expert_weights_nk(cfg, e, device, seed)
         if cfg.recipe == "bf16":
