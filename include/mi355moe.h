@@ -48,11 +48,14 @@ typedef enum {
 /* Weight recipes of the grouped GEMM / fused layer
  * (vllm_xpu_kernels/fused_moe_interface.py:33-45). */
 typedef enum {
-  MI355MOE_RECIPE_BF16 = 0,     /* bf16 weights, bf16 activations          */
+  MI355MOE_RECIPE_BF16 = 0,     /* 16-bit weights and activations of one
+                                   type, bf16 or fp16                     */
   MI355MOE_RECIPE_FP8BLOCK = 1, /* e4m3 weights, fp32 128x128 block scales;
                                    activations quantised 1x128 e4m3       */
   MI355MOE_RECIPE_MXFP4 = 2     /* e2m1 weights packed along K, e8m0 scale
-                                   per 32 along K; bf16 activations       */
+                                   per 32 along K; bf16 or fp16
+                                   activations (weights dequantised to
+                                   their type)                            */
 } mi355moe_recipe;
 
 typedef enum {
@@ -267,12 +270,14 @@ int mi355moe_silu_and_mul_mxfp4_quant(uint8_t* out, const void* input, int in_dt
  * (csrc/xpu/torch_bindings.cpp:46-53, csrc/xpu/grouped_gemm/
  * grouped_gemm_interface.cpp:12-60).  Rows of expert e are contiguous in A
  * and D (prefix sums of rows_per_expert, read on device).
- *   recipe BF16:     A bf16 [M,K]; B bf16 [E,N,K]
- *   recipe FP8BLOCK: A e4m3 [M,K] + a_scale f32 [M,K/128] (1x128 groups);
+ *   recipe BF16:     A bf16 or f16 [M,K]; B of the same type [E,N,K]
+ *   recipe FP8BLOCK: A e4m3 [M,K] + a_scale f32 [M,K/128] (1x128 groups),
+ *                    or A bf16/f16 (quantised 1x128 in the workspace);
  *                    B e4m3 [E,N,K] + b_scale f32 [E,N/128,K/128]
- *   recipe MXFP4:    A bf16 [M,K]; B u8 [E,N,K/2] + b_scale e8m0 [E,N,K/32]
- * bias: optional [E,N] in out_dtype; D [M,N] bf16 (or f16 for recipe BF16
- * when a_dtype is F16). */
+ *   recipe MXFP4:    A bf16 or f16 [M,K]; B u8 [E,N,K/2] + b_scale e8m0
+ *                    [E,N,K/32]
+ * bias: optional [E,N] in out_dtype; D [M,N] bf16 or f16 (out_dtype; equal
+ * to a_dtype for recipes BF16 and MXFP4). */
 size_t mi355moe_grouped_gemm_workspace_size(int64_t total_rows,
                                             int64_t num_experts);
 /* Workspace including the on-the-fly 1x128 quantisation a 16-bit A needs
@@ -299,7 +304,8 @@ int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
 typedef struct {
   int recipe;            /* mi355moe_recipe                                  */
   int activation;        /* mi355moe_activation                              */
-  int act_dtype;         /* MI355MOE_BF16 (hidden_states and output)         */
+  int act_dtype;         /* MI355MOE_BF16 or MI355MOE_F16: hidden_states,
+                            output, biases, 16-bit weights and intermediates */
   int ids_dtype;         /* dtype of topk_ids: I32 or I64                    */
   int64_t num_tokens;    /* T                                                */
   int64_t hidden;        /* H                                                */

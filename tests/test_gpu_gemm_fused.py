@@ -54,18 +54,22 @@ def _close(out, ref, rtol=LAYER_RTOL, atol=LAYER_ATOL, fp8=False):
 ROWS = [130, 0, 67, 9]
 
 
-def test_grouped_gemm_bf16_reference_layout(dev):
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_grouped_gemm_bf16_reference_layout(dev, dt):
+    """16-bit weights [E, K, N] of the activations' type, bf16 or fp16 (the
+    reference's tests/fused_moe/test_grouped_gemm.py:46 dtypes)."""
     g = torch.Generator().manual_seed(1)
     E, N, K = 4, 384, 256
     M = sum(ROWS)
-    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
-    b_kn = (torch.randn(E, K, N, generator=g) * 0.05).to(torch.bfloat16)
-    bias = (torch.randn(E, N, generator=g) * 0.1).to(torch.bfloat16)
-    d = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    a = torch.randn(M, K, generator=g).to(dt)
+    b_kn = (torch.randn(E, K, N, generator=g) * 0.05).to(dt)
+    bias = (torch.randn(E, N, generator=g) * 0.1).to(dt)
+    d = torch.empty(M, N, dtype=dt, device=dev)
     rows = torch.tensor(ROWS, dtype=torch.int32)
     out = _ops().cutlass_grouped_gemm(a.to(dev), b_kn.to(dev), None, bias.to(dev), d,
                                       rows.to(dev), N, K, E)
-    ref = O.grouped_gemm("bf16", a, b_kn.transpose(1, 2).contiguous(), None, bias, ROWS)
+    ref = O.grouped_gemm("bf16", a, b_kn.transpose(1, 2).contiguous(), None, bias, ROWS,
+                         out_dtype=dt)
     torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
@@ -98,18 +102,19 @@ def test_grouped_gemm_fp8_block_all_finite_e4m3_kat(dev):
     torch.testing.assert_close(out.cpu(), ref.half(), rtol=0, atol=0)
 
 
-def test_grouped_gemm_mxfp4(dev):
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_grouped_gemm_mxfp4(dev, dt):
     g = torch.Generator().manual_seed(3)
     E, N, K = 4, 256, 512
     M = sum(ROWS)
-    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    a = torch.randn(M, K, generator=g).to(dt)
     w = torch.randint(0, 256, (E, N, K // 2), generator=g, dtype=torch.uint8)
     sc = torch.randint(118, 128, (E, N, K // 32), generator=g, dtype=torch.uint8)
-    d = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    d = torch.empty(M, N, dtype=dt, device=dev)
     _ops().cutlass_grouped_gemm(a.to(dev), w.to(dev).view(torch.float4_e2m1fn_x2), sc.to(dev),
                                 None, d, torch.tensor(ROWS, dtype=torch.int32, device=dev),
                                 N, K, E)
-    ref = O.grouped_gemm("mxfp4", a, w, sc, None, ROWS)
+    ref = O.grouped_gemm("mxfp4", a, w, sc, None, ROWS, out_dtype=dt)
     torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
@@ -249,8 +254,9 @@ def test_fused_moe_expert_map(dev):
 BIG_ROWS = [300, 260, 0, 129]
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4"])
-def test_grouped_gemm_big_tiles(dev, recipe):
+def test_grouped_gemm_big_tiles(dev, recipe, dt):
     """>96 rows per expert: bf16 and fp8 select the 320x256 kernels, mxfp4
     the LDS-staged 128x256 one; N=2880 is not a multiple of the tile (ragged
     last tile)."""
@@ -258,25 +264,25 @@ def test_grouped_gemm_big_tiles(dev, recipe):
     E, K = 4, 1024
     N = 640 if recipe == "fp8block" else 2880
     M = sum(BIG_ROWS)
-    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    a = torch.randn(M, K, generator=g).to(dt)
     rows = torch.tensor(BIG_ROWS, dtype=torch.int32)
-    d = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    d = torch.empty(M, N, dtype=dt, device=dev)
     if recipe == "bf16":
-        b = (torch.randn(E, N, K, generator=g) * 0.03).to(torch.bfloat16)
-        bias = (torch.randn(E, N, generator=g) * 0.1).to(torch.bfloat16)
+        b = (torch.randn(E, N, K, generator=g) * 0.03).to(dt)
+        bias = (torch.randn(E, N, generator=g) * 0.1).to(dt)
         _ops().cutlass_grouped_gemm(a.to(dev), b.transpose(1, 2).contiguous().to(dev), None,
                                     bias.to(dev), d, rows.to(dev), N, K, E)
-        ref = O.grouped_gemm("bf16", a, b, None, bias, BIG_ROWS)
+        ref = O.grouped_gemm("bf16", a, b, None, bias, BIG_ROWS, out_dtype=dt)
     elif recipe == "fp8block":
         q, s = O.fp8_block_quant_weight(torch.randn(E, N, K, generator=g) * 0.02)
         _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), s.to(dev), None, d, rows.to(dev),
                                     N, K, E)
-        ref = O.grouped_gemm("fp8block", a, q, s, None, BIG_ROWS)
+        ref = O.grouped_gemm("fp8block", a, q, s, None, BIG_ROWS, out_dtype=dt)
     else:
         q, sc = O.to_mxfp4(torch.randn(E, N, K, generator=g) * 0.05)
         _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), sc.to(dev), None, d, rows.to(dev),
                                     N, K, E)
-        ref = O.grouped_gemm("mxfp4", a, q, sc, None, BIG_ROWS)
+        ref = O.grouped_gemm("mxfp4", a, q, sc, None, BIG_ROWS, out_dtype=dt)
     torch.testing.assert_close(d.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
@@ -291,13 +297,14 @@ def test_grouped_gemm_wide_tiles(dev, K, out_dtype):
     Valid rows per 320-slot block 1..320 (every count of 32-row MFMA groups
     per wave half, 0..5, and of skipped 16-row DMA groups; experts of 1, 2
     and 3 blocks); K from one 32-element stage (shorter than the 3-deep
-    prefetch) to 11; N=200 is one ragged tile; bias; bf16 or fp16 output."""
+    prefetch) to 11; N=200 is one ragged tile; bias; bf16 or fp16 operands
+    and output (one 16-bit type per call)."""
     g = torch.Generator().manual_seed(K)
     E, N = len(WIDE_ROWS), 200
     M = sum(WIDE_ROWS)
-    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
-    b = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
-    bias = (torch.randn(E, N, generator=g) * 0.1).to(torch.bfloat16)
+    a = torch.randn(M, K, generator=g).to(out_dtype)
+    b = (torch.randn(E, N, K, generator=g) * 0.05).to(out_dtype)
+    bias = (torch.randn(E, N, generator=g) * 0.1).to(out_dtype)
     rows = torch.tensor(WIDE_ROWS, dtype=torch.int32)
     d = torch.full((M, N), float("nan"), dtype=out_dtype, device=dev)
     _ops().cutlass_grouped_gemm(a.to(dev), b.transpose(1, 2).contiguous().to(dev), None,
@@ -605,6 +612,53 @@ def test_fused_moe_generic_activation_clamp(dev):
                           None, None, tw.cpu(), remap[ti_c], activation=act,
                           gemm1_clamp_limit=0.5)
         _close(out, ref)
+
+
+@pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4"])
+@pytest.mark.parametrize("T", [1, 16, 48, 300, 1024])
+def test_fused_moe_fp16(dev, recipe, T):
+    """fp16 hidden states, output and biases (16-bit recipe: fp16 weights;
+    mxfp4 dequantised to fp16) through every kernel family (H=384, I=256, 8
+    experts, top-2; T=1 split-K stream ... 1024 320-slot), at the reference's
+    fp16 bar rtol = atol = 1e-2 (tests/fused_moe/test_fused_moe.py:288-294;
+    fp8 at its own bar).  mxfp4 runs swigluoai with biases, the others SiLU."""
+    import dataclasses
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    W = _W()
+    cfg = dataclasses.replace(W.CONFIGS["C5" if recipe == "mxfp4" else "C2"], recipe=recipe,
+                              hidden=384, inter=256, experts=8, topk=2, bias=True)
+    w = W.make_weights(cfg, dev)
+    h = torch.float16
+    w = dataclasses.replace(w, w13=w.w13.to(h) if recipe == "bf16" else w.w13,
+                            w2=w.w2.to(h) if recipe == "bf16" else w.w2,
+                            w13_bias=w.w13_bias.to(h), w2_bias=w.w2_bias.to(h))
+    x = W.make_activations(cfg, T, dev).to(h)
+    tw, ti = W.route(cfg, W.make_router_logits(cfg, T, dev))
+    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                      cfg.topk, cfg.activation, cfg.experts)
+    out = torch.empty_like(x)
+    moe.apply(out, x, tw, ti)
+    toks = torch.linspace(0, T - 1, min(T, 48)).long().to(dev)
+    ref = _oracle_layer(cfg, w, x, tw, ti, toks)
+    assert ref.dtype == h
+    if recipe == "fp8block":
+        _close(out[toks], ref, fp8=True)
+    else:
+        _close(out[toks], ref, rtol=1e-2, atol=1e-2)
+
+
+def test_fused_moe_fp16_bias_follows_call_dtype(dev):
+    """bf16 biases with fp16 activations (fp8 weights): converted once to the
+    call's type; a bf16 call with the same layer reuses the originals."""
+    import dataclasses
+    W = _W()
+    cfg = dataclasses.replace(W.CONFIGS["C2"], recipe="fp8block", hidden=256, inter=128,
+                              experts=4, topk=2, bias=True)
+    cfg, w, x, tw, ti, out, moe = _layer(cfg, 24, dev)
+    out16 = torch.empty_like(x, dtype=torch.float16)
+    moe.apply(out16, x.half(), tw, ti)
+    _close(out16.float(), out.float(), fp8=True)
+    assert torch.float16 in moe._bias_cache
 
 
 def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):

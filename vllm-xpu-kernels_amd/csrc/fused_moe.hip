@@ -13,6 +13,7 @@
 //      order (no floating-point atomics).
 #include <vector>
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -47,7 +48,7 @@ int64_t launch_blocks(int64_t slots, int64_t experts, int64_t bm,
   return std::min(b, max_blocks);
 }
 
-template <typename Id>
+template <typename Id, bool F16>
 __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ g2,
     const float* __restrict__ w, const Id* __restrict__ ids,
@@ -71,11 +72,11 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
       uint32_t wd[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += wj * bf16_to_f32(static_cast<uint16_t>(wd[i] & 0xFFFF));
-        acc[2 * i + 1] += wj * bf16_to_f32(static_cast<uint16_t>(wd[i] >> 16));
+        acc[2 * i] += wj * ld16<F16>(static_cast<uint16_t>(wd[i] & 0xFFFF));
+        acc[2 * i + 1] += wj * ld16<F16>(static_cast<uint16_t>(wd[i] >> 16));
       }
     } else {
-      for (int i = 0; i < 8 && h0 + i < H; ++i) acc[i] += wj * bf16_to_f32(row[i]);
+      for (int i = 0; i < 8 && h0 + i < H; ++i) acc[i] += wj * ld16<F16>(row[i]);
     }
   }
   uint16_t* o = out + t * H + h0;
@@ -83,17 +84,18 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
     uint32_t wd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      wd[i] = f32_to_bf16(acc[2 * i]) | (uint32_t(f32_to_bf16(acc[2 * i + 1])) << 16);
+      wd[i] = st16<F16>(acc[2 * i]) | (uint32_t(st16<F16>(acc[2 * i + 1])) << 16);
     *reinterpret_cast<uint4*>(o) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
   } else {
-    for (int i = 0; i < 8 && h0 + i < H; ++i) o[i] = f32_to_bf16(acc[i]);
+    for (int i = 0; i < 8 && h0 + i < H; ++i) o[i] = st16<F16>(acc[i]);
   }
 }
 
 // Decode: the split-K w2 partials summed and reduced over each token's top-k
 // slots in one launch.  Workgroup (tile, t) makes columns [256 tile, +256)
 // of token t:
-//   y[t, h] = bf16(sum_j w[t,j] * bf16(sum_z part(slot, h, z) + bias[e, h]))
+//   y[t, h] = T(sum_j w[t,j] * T(sum_z part(slot, h, z) + bias[e, h]))
+// (T the call's 16-bit type)
 // with the slot's partial tile found through its sorted position
 // (inv_pos[t k + j], -1 for slots the sort dropped): four groups of 64
 // threads finish the slots j = g, g + 4, ... (4 columns per thread) into
@@ -103,6 +105,7 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
 // column c of slot m is float (2 (64 (c / 32) + 16 ((c % 16) / 4) + m) +
 // (c % 32) / 16) 4 + c % 4.
 constexpr int kFuseMaxTopk = 32;
+template <bool F16>
 __global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ part, int ks, int n_tiles,
     const int32_t* __restrict__ inv_pos, const int32_t* __restrict__ block_expert,
@@ -128,11 +131,11 @@ __global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
       }
       if (bias) {
         const uint16_t* b = bias + static_cast<int64_t>(block_expert[blk]) * H + h;
-        v0 += bf16_to_f32(b[0]); v1 += bf16_to_f32(b[1]);
-        v2 += bf16_to_f32(b[2]); v3 += bf16_to_f32(b[3]);
+        v0 += ld16<F16>(b[0]); v1 += ld16<F16>(b[1]);
+        v2 += ld16<F16>(b[2]); v3 += ld16<F16>(b[3]);
       }
-      g = make_float4(bf16_to_f32(f32_to_bf16(v0)), bf16_to_f32(f32_to_bf16(v1)),
-                      bf16_to_f32(f32_to_bf16(v2)), bf16_to_f32(f32_to_bf16(v3)));
+      g = make_float4(rnd16<F16>((v0)), rnd16<F16>((v1)),
+                      rnd16<F16>((v2)), rnd16<F16>((v3)));
     }
     s_g[j][cg] = g;
   }
@@ -146,8 +149,8 @@ __global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
     a0 += wj * g.x; a1 += wj * g.y; a2 += wj * g.z; a3 += wj * g.w;
   }
   *reinterpret_cast<uint2*>(out + t * H + h) =
-      make_uint2(f32_to_bf16(a0) | (uint32_t(f32_to_bf16(a1)) << 16),
-                 f32_to_bf16(a2) | (uint32_t(f32_to_bf16(a3)) << 16));
+      make_uint2(st16<F16>(a0) | (uint32_t(st16<F16>(a1)) << 16),
+                 st16<F16>(a2) | (uint32_t(st16<F16>(a3)) << 16));
 }
 
 struct FusedActArgs {
@@ -160,18 +163,17 @@ struct FusedActArgs {
 };
 
 // Activations without a GEMM-epilogue form (gelu, gelu_tanh, swiglustep,
-// relu2_no_mul): the w13 output G1 (bf16 [rows, 2I] by sorted position,
+// relu2_no_mul): the w13 output G1 (16-bit [rows, 2I] by sorted position,
 // gate | up) -> activation [rows, K2], K2 = I (gated) or 2I (relu2_no_mul),
 // with the reference's rounding points (G1 and, for gelu, act(gate) rounded
-// to bf16; swiglustep in fp32; gemm1_clamp_limit on the bf16 halves first;
+// to the 16-bit type; swiglustep in fp32; gemm1_clamp_limit on the 16-bit
+// halves first;
 // fused_moe_interface.py:383-396).  Each lane makes 8 output columns; Q8:
-// e4m3 with 1x128 scales of the bf16 activation (16 lanes per group), as the
+// e4m3 with 1x128 scales of the 16-bit activation (16 lanes per group), as the
 // fp8 GLU epilogues quantise it.  Rows from *ntp on (padding past the last
 // block) are not touched; K2 % 128 == 0 when Q8, so a group's lanes share a
 // row and leave together.
-__device__ __forceinline__ float rbf(float v) { return bf16_to_f32(f32_to_bf16(v)); }
-
-template <int ACT, bool Q8>
+template <int ACT, bool Q8, bool F16>
 __global__ __launch_bounds__(256) void fused_act_kernel(
     const uint16_t* __restrict__ g1, void* __restrict__ act, float* __restrict__ acts,
     const int32_t* __restrict__ ntp, int64_t inter, float clamp, float limit) {
@@ -188,32 +190,32 @@ __global__ __launch_bounds__(256) void fused_act_kernel(
   if constexpr (ACT == MI355MOE_ACT_RELU2) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float v = bf16_to_f32(static_cast<uint16_t>(wa[i >> 1] >> (16 * (i & 1))));
+      float v = ld16<F16>(static_cast<uint16_t>(wa[i >> 1] >> (16 * (i & 1))));
       if (clamp > 0.f)
-        v = rbf(c0 + i < inter ? fminf(v, clamp) : fminf(fmaxf(v, -clamp), clamp));
+        v = rnd16<F16>(c0 + i < inter ? fminf(v, clamp) : fminf(fmaxf(v, -clamp), clamp));
       const float p = fmaxf(v, 0.f);
-      y[i] = rbf(p * p);
+      y[i] = rnd16<F16>(p * p);
     }
   } else {
     const uint4 xb = *reinterpret_cast<const uint4*>(x + inter + c0);
     const uint32_t wb[4] = {xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float g = bf16_to_f32(static_cast<uint16_t>(wa[i >> 1] >> (16 * (i & 1))));
-      float u = bf16_to_f32(static_cast<uint16_t>(wb[i >> 1] >> (16 * (i & 1))));
+      float g = ld16<F16>(static_cast<uint16_t>(wa[i >> 1] >> (16 * (i & 1))));
+      float u = ld16<F16>(static_cast<uint16_t>(wb[i >> 1] >> (16 * (i & 1))));
       if (clamp > 0.f) {
-        g = rbf(fminf(g, clamp));
-        u = rbf(fminf(fmaxf(u, -clamp), clamp));
+        g = rnd16<F16>(fminf(g, clamp));
+        u = rnd16<F16>(fminf(fmaxf(u, -clamp), clamp));
       }
       float v;
       if constexpr (ACT == MI355MOE_ACT_GELU) {
-        v = rbf(gelu_erf(g)) * u;
+        v = rnd16<F16>(gelu_erf(g)) * u;
       } else if constexpr (ACT == MI355MOE_ACT_GELU_TANH) {
-        v = rbf(gelu_tanh(g)) * u;
+        v = rnd16<F16>(gelu_tanh(g)) * u;
       } else {
         v = fminf(g / (1.f + expf(-g)), limit) * fminf(fmaxf(u, -limit), limit);
       }
-      y[i] = rbf(v);
+      y[i] = rnd16<F16>(v);
     }
   }
   if constexpr (Q8) {
@@ -236,31 +238,31 @@ __global__ __launch_bounds__(256) void fused_act_kernel(
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = f32_to_bf16(y[2 * i]) | (static_cast<uint32_t>(f32_to_bf16(y[2 * i + 1])) << 16);
+      w[i] = st16<F16>(y[2 * i]) | (static_cast<uint32_t>(st16<F16>(y[2 * i + 1])) << 16);
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(act) + r * k2 + c0) =
         make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
-template <bool Q8>
+template <bool Q8, bool F16>
 void launch_fused_act(int act, const FusedActArgs& f, hipStream_t st) {
   const int64_t k2 = act == MI355MOE_ACT_RELU2 ? 2 * f.inter : f.inter;
   dim3 grid(static_cast<unsigned>(cdiv(f.rows * (k2 / 8), 256)));
   switch (act) {
     case MI355MOE_ACT_GELU:
-      fused_act_kernel<MI355MOE_ACT_GELU, Q8><<<grid, dim3(256), 0, st>>>(
+      fused_act_kernel<MI355MOE_ACT_GELU, Q8, F16><<<grid, dim3(256), 0, st>>>(
           f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
       break;
     case MI355MOE_ACT_GELU_TANH:
-      fused_act_kernel<MI355MOE_ACT_GELU_TANH, Q8><<<grid, dim3(256), 0, st>>>(
+      fused_act_kernel<MI355MOE_ACT_GELU_TANH, Q8, F16><<<grid, dim3(256), 0, st>>>(
           f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
       break;
     case MI355MOE_ACT_SWIGLUSTEP:
-      fused_act_kernel<MI355MOE_ACT_SWIGLUSTEP, Q8><<<grid, dim3(256), 0, st>>>(
+      fused_act_kernel<MI355MOE_ACT_SWIGLUSTEP, Q8, F16><<<grid, dim3(256), 0, st>>>(
           f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
       break;
     default:
-      fused_act_kernel<MI355MOE_ACT_RELU2, Q8><<<grid, dim3(256), 0, st>>>(
+      fused_act_kernel<MI355MOE_ACT_RELU2, Q8, F16><<<grid, dim3(256), 0, st>>>(
           f.g1, f.act, f.acts, f.ntp, f.inter, f.clamp, f.limit);
       break;
   }
@@ -432,7 +434,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
                 E = a->num_experts, k = a->topk;
   MI_ARG(T >= 0 && H > 0 && I > 0 && E > 0 && k > 0, "invalid layer shape");
   MI_ARG(E <= 1024, "num_experts must be at most 1024");
-  MI_ARG(a->act_dtype == MI355MOE_BF16, "hidden_states must be bfloat16");
+  MI_ARG(a->act_dtype == MI355MOE_BF16 || a->act_dtype == MI355MOE_F16,
+         "hidden_states must be bfloat16 or float16");
   MI_ARG(!a->hidden_scale || a->recipe == MI355MOE_RECIPE_FP8BLOCK,
          "pre-quantised hidden_states (hidden_scale) need the fp8block recipe");
   MI_ARG(a->ids_dtype == MI355MOE_I32 || a->ids_dtype == MI355MOE_I64,
@@ -479,11 +482,12 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   if (rc) return rc;
 
   const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
+  const bool f16 = a->act_dtype == MI355MOE_F16;  // the call's 16-bit type
   // caller-quantised hidden states (e4m3 + 1x128 scales) go to w13 as given
   const bool preq = fp8 && a->hidden_scale;
   if (int m = mark(1)) return m;
   if (fp8 && !preq) {
-    rc = group_quant_fp8(a->hidden_states, MI355MOE_BF16, L.xq, L.xs, T, H, st);
+    rc = group_quant_fp8(a->hidden_states, a->act_dtype, L.xq, L.xs, T, H, st);
     if (rc) return rc;
   }
   if (int m = mark(2)) return m;
@@ -518,6 +522,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.ksplit = L.ks1;
   g1.part = L.part1;
   g1.w_kblock = kblock;
+  g1.out_f16 = f16;
   if (glu) {
     rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
     if (rc) return rc;
@@ -527,8 +532,13 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     if (rc) return rc;
     const FusedActArgs f{L.g1, L.act, L.acts, L.ntp, L.max_padded, I,
                          a->gemm1_clamp_limit, a->swiglu_limit};
-    if (fp8) launch_fused_act<true>(a->activation, f, st);
-    else launch_fused_act<false>(a->activation, f, st);
+    if (fp8) {
+      if (f16) launch_fused_act<true, true>(a->activation, f, st);
+      else launch_fused_act<true, false>(a->activation, f, st);
+    } else {
+      if (f16) launch_fused_act<false, true>(a->activation, f, st);
+      else launch_fused_act<false, false>(a->activation, f, st);
+    }
     MI_LAUNCH_CHECK();
   }
   if (int m = mark(3)) return m;
@@ -555,6 +565,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.ksplit = L.ks2;
   g2.part = L.part2;
   g2.w_kblock = kblock;
+  g2.out_f16 = f16;
   // split-K decode: the partial sums are finished by the top-k reduction
   const bool fuse_reduce = L.tile == TILE_STREAM && L.ks2 > 1 && k <= kFuseMaxTopk;
   g2.partials_only = fuse_reduce;
@@ -563,7 +574,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   if (int m = mark(4)) return m;
   if (fuse_reduce) {
     dim3 grid(static_cast<unsigned>(cdiv(H, 256)), static_cast<unsigned>(T));
-    finalize_topk_sum_kernel<<<grid, dim3(256), 0, st>>>(
+    auto fin = f16 ? finalize_topk_sum_kernel<true> : finalize_topk_sum_kernel<false>;
+    fin<<<grid, dim3(256), 0, st>>>(
         static_cast<uint16_t*>(a->output), L.part2, L.ks2, static_cast<int>(cdiv(H, 256)),
         L.inv, L.eids, static_cast<const uint16_t*>(a->w2_bias), a->topk_weights,
         static_cast<int>(k), H);
@@ -574,16 +586,19 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   // Slots dropped by the sort (invalid or non-local experts) were never
   // written by the w2 GEMM; the reduction skips them by the same rule.
   dim3 grid(static_cast<unsigned>(cdiv(cdiv(H, 8), 256)), static_cast<unsigned>(T));
-  if (a->ids_dtype == MI355MOE_I32)
-    weighted_topk_sum_kernel<int32_t><<<grid, dim3(256), 0, st>>>(
-        static_cast<uint16_t*>(a->output), L.g2, a->topk_weights,
-        static_cast<const int32_t*>(a->topk_ids), a->expert_map,
-        a->expert_map_len, E, T, (int)k, H);
-  else
-    weighted_topk_sum_kernel<int64_t><<<grid, dim3(256), 0, st>>>(
-        static_cast<uint16_t*>(a->output), L.g2, a->topk_weights,
-        static_cast<const int64_t*>(a->topk_ids), a->expert_map,
-        a->expert_map_len, E, T, (int)k, H);
+  if (a->ids_dtype == MI355MOE_I32) {
+    auto red = f16 ? weighted_topk_sum_kernel<int32_t, true>
+                   : weighted_topk_sum_kernel<int32_t, false>;
+    red<<<grid, dim3(256), 0, st>>>(static_cast<uint16_t*>(a->output), L.g2, a->topk_weights,
+                                    static_cast<const int32_t*>(a->topk_ids), a->expert_map,
+                                    a->expert_map_len, E, T, (int)k, H);
+  } else {
+    auto red = f16 ? weighted_topk_sum_kernel<int64_t, true>
+                   : weighted_topk_sum_kernel<int64_t, false>;
+    red<<<grid, dim3(256), 0, st>>>(static_cast<uint16_t*>(a->output), L.g2, a->topk_weights,
+                                    static_cast<const int64_t*>(a->topk_ids), a->expert_map,
+                                    a->expert_map_len, E, T, (int)k, H);
+  }
   MI_LAUNCH_CHECK();
   return mark(5);
 }
@@ -662,11 +677,15 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
     }
   } else if (recipe == MI355MOE_RECIPE_MXFP4) {
     MI_ARG(K % 32 == 0, "mxfp4 needs K % 32 == 0");
-    MI_ARG(a_dtype == MI355MOE_BF16, "mxfp4 activations must be bfloat16");
+    MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
+           "mxfp4 activations must be bfloat16 or float16");
+    MI_ARG(out_dtype == a_dtype, "mxfp4: the output must have the activation dtype");
     MI_ARG(b_scale != nullptr, "mxfp4 needs e8m0 scales");
   } else {
     MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
-    MI_ARG(a_dtype == MI355MOE_BF16, "bf16 recipe needs bfloat16 activations");
+    MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
+           "16-bit recipe needs bfloat16 or float16 activations (and weights)");
+    MI_ARG(out_dtype == a_dtype, "16-bit recipe: the output must have the activation dtype");
     MI_ARG(K % 8 == 0, "K must be a multiple of 8");
   }
   if (M == 0) return MI355MOE_OK;

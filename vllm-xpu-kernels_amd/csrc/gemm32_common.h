@@ -2,6 +2,7 @@
 // 256-weight-row tiles, 4 waves as 2 (slots) x 2 (weight rows)).
 #pragma once
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -11,10 +12,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ f32x16 mfma32_bf16(uint4 a, uint4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-      __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
 
 // e4m3 x e4m3, 32x32x64, unit e8m0 scales.
 __device__ __forceinline__ f32x16 mfma32_fp8(uint4 a0, uint4 a1, uint4 b0,
@@ -27,14 +24,6 @@ __device__ __forceinline__ f32x16 mfma32_fp8(uint4 a0, uint4 a1, uint4 b0,
                                                          0, 127);
 }
 
-__device__ __forceinline__ uint4 fp4x8_bf16(uint32_t w, float sc) {
-  uint4 r;
-  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
-  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
-  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
-  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
-  return r;
-}
 
 // Round to the 16-bit output type and back.
 template <bool F16>
@@ -104,8 +93,8 @@ __device__ __forceinline__ void epilogue_32x32(const GemmArgs& a, void* qs,
       for (int r = 0; r < 16; ++r) {
         const int64_t n = n0 + tile_col(i, r);
         if (n < N) {
-          bg[r] = bf16_to_f32(a.bias[bias_base + n]);
-          if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+          bg[r] = ld16<F16>(a.bias[bias_base + n]);
+          if constexpr (kGlu) bu[r] = ld16<F16>(a.bias[bias_base + a.up_off + n]);
         }
       }
     }
@@ -214,24 +203,6 @@ __device__ __forceinline__ void epilogue_32x32(const GemmArgs& a, void* qs,
       }
     }
   }
-}
-
-// Dispatch on the 16-bit output type (fp16 only without the fp8 output).
-template <bool kGlu, bool QOUT>
-__device__ __forceinline__ void epilogue_32x32_any(const GemmArgs& a, void* qs,
-                                                   f32x16 (&acc)[4][2], int e,
-                                                   int64_t n0, int wm, int wn,
-                                                   int l32, int h,
-                                                   const int* s_drow,
-                                                   float (*s_amax)[128],
-                                                   int ngroup, uint8_t* stage) {
-  if constexpr (!QOUT) {
-    if (a.out_f16) {
-      epilogue_32x32<kGlu, false, true>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax, ngroup, stage);
-      return;
-    }
-  }
-  epilogue_32x32<kGlu, QOUT, false>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax, ngroup, stage);
 }
 
 }  // namespace mi355

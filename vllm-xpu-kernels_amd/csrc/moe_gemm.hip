@@ -8,12 +8,14 @@
 // (16 slots, staged in LDS and shared by the 4 waves), so every lane ends up
 // holding 4 consecutive output columns of one slot row.
 //
-//   bf16     v_mfma_f32_16x16x32_bf16, K stage 128 (4 MFMA steps)
+//   bf16     v_mfma_f32_16x16x32_bf16 (fp16 calls: _f16), K stage 128 (4
+//            MFMA steps)
 //   fp8block v_mfma_scale_f32_16x16x128_f8f6f4 (e4m3 x e4m3, unit scales), one
 //            MFMA per 128-wide K block; the fp32 block scales of the weight
 //            (128x128) and activation (1x128) multiply its partial sum.
-//   mxfp4    e2m1 weights converted in registers to bf16 with their e8m0
-//            scale (v_cvt_scalef32_pk_bf16_fp4), then the bf16 MFMA.
+//   mxfp4    e2m1 weights converted in registers to the call's 16-bit type
+//            with their e8m0 scale (v_cvt_scalef32_pk_{bf16,f16}_fp4), then
+//            the 16-bit MFMA.
 //
 // Epilogues: STORE (bias, round) and GLU (gate/up halves of w13 -> SiLU-mul or
 // swigluoai), optionally re-quantising the activation to e4m3 with 1x128
@@ -21,22 +23,17 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int KB = 128;  // K elements per LDS stage
 
-__device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
 
 // e4m3 x e4m3, 16x16x128, scale exponents 127 (= 1.0) on both operands.
 __device__ __forceinline__ f32x4 mfma_fp8(uint4 a0, uint4 a1, uint4 b0,
@@ -50,36 +47,7 @@ __device__ __forceinline__ f32x4 mfma_fp8(uint4 a0, uint4 a1, uint4 b0,
                                                           0, 127);
 }
 
-// 8 e2m1 codes (one 32-bit word, element t in bits 4t..4t+3) -> 8 bf16 scaled
-// by 2^(e-127).
-__device__ __forceinline__ uint4 fp4x8_to_bf16(uint32_t w, float scale) {
-  uint4 r;
-  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
-  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
-  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
-  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
-  r.x = __builtin_bit_cast(uint32_t, p0);
-  r.y = __builtin_bit_cast(uint32_t, p1);
-  r.z = __builtin_bit_cast(uint32_t, p2);
-  r.w = __builtin_bit_cast(uint32_t, p3);
-  return r;
-}
-
-__device__ __forceinline__ float round_out(float v, bool f16) {
-  return f16 ? f16_to_f32(f32_to_f16(v)) : bf16_to_f32(f32_to_bf16(v));
-}
-
-__device__ __forceinline__ float glu(float g, float u, const GemmArgs& a) {
-  if (a.act == MI355MOE_ACT_SILU) {
-    float s = bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g))));
-    return s * u;
-  }
-  g = g > a.limit ? a.limit : g;
-  u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-  return (u + 1.f) * (g * (1.f / (1.f + expf(-g * a.alpha))));
-}
-
-template <int RECIPE, int BM, int BN, int EPI, bool QOUT>
+template <int RECIPE, int BM, int BN, int EPI, bool QOUT, bool F16>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
                                                        void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -163,10 +131,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
                          : 0u;
         if (ex == 0u) v = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> scale 0
         const float sc = __uint_as_float(ex << 23);
-        wf[0][j][0] = fp4x8_to_bf16(v.x, sc);
-        wf[1][j][0] = fp4x8_to_bf16(v.y, sc);
-        wf[2][j][0] = fp4x8_to_bf16(v.z, sc);
-        wf[3][j][0] = fp4x8_to_bf16(v.w, sc);
+        wf[0][j][0] = fp4x8_to16<F16>(v.x, sc);
+        wf[1][j][0] = fp4x8_to16<F16>(v.y, sc);
+        wf[2][j][0] = fp4x8_to16<F16>(v.z, sc);
+        wf[3][j][0] = fp4x8_to16<F16>(v.w, sc);
       } else {
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
@@ -216,14 +184,14 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
           const int koff = kFp4 ? (32 * q + 8 * s) : (32 * s + 8 * q);
           const uint4 x = *reinterpret_cast<const uint4*>(xr + koff * 2);
 #pragma unroll
-          for (int j = 0; j < NB; ++j) acc[mt][j] = mfma_bf16(wf[s][j][0], x, acc[mt][j]);
+          for (int j = 0; j < NB; ++j)
+            acc[mt][j] = mfma16_16x16x32<F16>(wf[s][j][0], x, acc[mt][j]);
         }
       }
     }
   }
 
   // ---- epilogue: lane holds D[row = mt*16 + l16][n = nbase + j*16 + 4q + r]
-  const bool f16 = a.out_f16 != 0;
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
   float outv[MT][NT][4];
 #pragma unroll
@@ -235,17 +203,17 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
       for (int r = 0; r < 4; ++r) {
         const bool nok = n + r < a.N;
         float v = acc[mt][j][r];
-        if (a.bias && nok) v += bf16_to_f32(a.bias[bias_base + n + r]);
-        v = round_out(v, f16);
+        if (a.bias && nok) v += ld16<F16>(a.bias[bias_base + n + r]);
+        v = rnd16<F16>(v);
         if constexpr (EPI == EPI_GLU) {
           float u = acc[mt][j + NT][r];
-          if (a.bias && nok) u += bf16_to_f32(a.bias[bias_base + a.up_off + n + r]);
-          u = round_out(u, f16);
+          if (a.bias && nok) u += ld16<F16>(a.bias[bias_base + a.up_off + n + r]);
+          u = rnd16<F16>(u);
           if (a.clamp_limit > 0.f) {
             v = fminf(v, a.clamp_limit);
             u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
           }
-          v = round_out(glu(v, u, a), f16);
+          v = rnd16<F16>(glu16<F16>(v, u, a.act, a.alpha, a.limit));
         }
         outv[mt][j][r] = nok ? v : 0.f;
       }
@@ -304,7 +272,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
         uint16_t h[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          h[r] = f16 ? f32_to_f16(outv[mt][j][r]) : f32_to_bf16(outv[mt][j][r]);
+          h[r] = st16<F16>(outv[mt][j][r]);
         uint16_t* dst = d + static_cast<int64_t>(drow) * a.N + n;
         if (n + 3 < a.N && (a.N & 3) == 0) {
           *reinterpret_cast<uint2*>(dst) =
@@ -325,7 +293,10 @@ void launch_tile(const GemmArgs& a, int64_t max_blocks, void* qs,
   constexpr int BN = (BM == 16 && !QOUT) ? 64 : 128;
   dim3 grid(static_cast<unsigned>(cdiv(a.N, BN)),
             static_cast<unsigned>(max_blocks));
-  moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT><<<grid, dim3(256), 0, st>>>(a, qs);
+  if (a.out_f16)
+    moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT, true><<<grid, dim3(256), 0, st>>>(a, qs);
+  else
+    moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT, false><<<grid, dim3(256), 0, st>>>(a, qs);
 }
 
 template <int RECIPE, int EPI, bool QOUT>

@@ -43,7 +43,7 @@ __device__ __forceinline__ int64_t tile_wrow(int r, int64_t n0, bool glu,
   return n;
 }
 
-template <int RECIPE, int EPI, bool QOUT>
+template <int RECIPE, int EPI, bool QOUT, bool F16>
 __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -162,10 +162,10 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
         if (rsc[i] == 0u) v = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> 0
         const float sc = __uint_as_float(rsc[i] << 23);
         uint8_t* d = &sW[buf][r * PITCH + c * 64];
-        *reinterpret_cast<uint4*>(d) = fp4x8_bf16(v.x, sc);
-        *reinterpret_cast<uint4*>(d + 16) = fp4x8_bf16(v.y, sc);
-        *reinterpret_cast<uint4*>(d + 32) = fp4x8_bf16(v.z, sc);
-        *reinterpret_cast<uint4*>(d + 48) = fp4x8_bf16(v.w, sc);
+        *reinterpret_cast<uint4*>(d) = fp4x8_to16<F16>(v.x, sc);
+        *reinterpret_cast<uint4*>(d + 16) = fp4x8_to16<F16>(v.y, sc);
+        *reinterpret_cast<uint4*>(d + 32) = fp4x8_to16<F16>(v.z, sc);
+        *reinterpret_cast<uint4*>(d + 48) = fp4x8_to16<F16>(v.w, sc);
       } else {
         const int r = idx / (ROWB / 16), c = idx % (ROWB / 16);
         *reinterpret_cast<uint4*>(&sW[buf][r * PITCH + c * 16]) = rw[i];
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
           const uint4 wf =
               *reinterpret_cast<const uint4*>(Ws + (wtile_row[i] + l32) * PITCH + koff);
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32_bf16(wf, xf[j], acc[i][j]);
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma16_32x32x16<F16>(wf, xf[j], acc[i][j]);
         }
       }
     }
@@ -268,17 +268,22 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
   }
 
   static_assert(sizeof(sW) >= 128 * (2 * 256 + 16), "epilogue staging");
-  epilogue_32x32_any<kGlu, QOUT>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax,
+  epilogue_32x32<kGlu, QOUT, F16>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax,
                                 static_cast<int>(blockIdx.x), &sW[0][0]);
 }
 
-template <int RECIPE, int EPI, bool QOUT>
-int launch_big(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+template <int RECIPE, int EPI, bool QOUT, bool F16>
+int launch_big_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
   const int64_t cols = EPI == EPI_GLU ? 128 : BN;
   dim3 grid(static_cast<unsigned>(cdiv(a.N, cols)), static_cast<unsigned>(max_blocks));
-  moe_gemm_big_kernel<RECIPE, EPI, QOUT><<<grid, dim3(256), 0, st>>>(a, qs);
+  moe_gemm_big_kernel<RECIPE, EPI, QOUT, F16><<<grid, dim3(256), 0, st>>>(a, qs);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
+}
+template <int RECIPE, int EPI, bool QOUT>
+int launch_big(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+  return a.out_f16 ? launch_big_t<RECIPE, EPI, QOUT, true>(a, max_blocks, qs, st)
+                   : launch_big_t<RECIPE, EPI, QOUT, false>(a, max_blocks, qs, st);
 }
 
 }  // namespace

@@ -31,6 +31,7 @@
 // group of the next GEMM's input.
 #include <type_traits>
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -346,8 +347,8 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
       if (a.bias) {
         const int64_t n = n0 + tcol(i, r);
         if (n < N) {
-          bg[r] = bf16_to_f32(a.bias[bias_base + n]);
-          if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+          bg[r] = ld16<F16>(a.bias[bias_base + n]);
+          if constexpr (kGlu) bu[r] = ld16<F16>(a.bias[bias_base + a.up_off + n]);
         }
       }
     }
@@ -486,7 +487,8 @@ int launch_moe_gemm_big8(int recipe, int epi, bool qout, const GemmArgs& a,
   if (qout) {
     MI_ARG(epi == EPI_GLU && a.N % 128 == 0,
            "fp8 activation output needs the GLU epilogue and I % 128 == 0");
-    return launch_b8<EPI_GLU, true, false>(a, max_blocks, qs, st);
+    return a.out_f16 ? launch_b8<EPI_GLU, true, true>(a, max_blocks, qs, st)
+                     : launch_b8<EPI_GLU, true, false>(a, max_blocks, qs, st);
   }
   if (epi == EPI_GLU)
     return a.out_f16 ? launch_b8<EPI_GLU, false, true>(a, max_blocks, qs, st)

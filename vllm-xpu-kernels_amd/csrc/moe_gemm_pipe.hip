@@ -52,7 +52,7 @@ __device__ __forceinline__ void wait_vm() {
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
-template <int RECIPE, int EPI, bool QOUT>
+template <int RECIPE, int EPI, bool QOUT, bool F16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void moe_gemm_pipe_kernel(const GemmArgs a,
                                                                void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma32_bf16(wf[ks][i], xf[ks][j], acc[i][j]);
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma16_32x32x16<F16>(wf[ks][i], xf[ks][j], acc[i][j]);
       // keep the 24 LDS reads ahead of the 32 MFMAs (the default schedule
       // re-interleaves them one pair at a time and exposes LDS latency)
       __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);
@@ -270,17 +270,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
 
   static_assert(sizeof(ring) >= 128 * (2 * 256 + 16), "epilogue staging");
-  epilogue_32x32_any<kGlu, QOUT>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax, ntile, ring);
+  epilogue_32x32<kGlu, QOUT, F16>(a, qs, acc, e, n0, wm, wn, l32, h, s_drow, s_amax, ntile, ring);
 }
 
-template <int RECIPE, int EPI, bool QOUT>
-int launch_pipe(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+template <int RECIPE, int EPI, bool QOUT, bool F16>
+int launch_pipe_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
   const int64_t cols = EPI == EPI_GLU ? 128 : BN;
   const int64_t total = cdiv(a.N, cols) * max_blocks;
   dim3 grid(static_cast<unsigned>(cdiv(total, 8) * 8));
-  moe_gemm_pipe_kernel<RECIPE, EPI, QOUT><<<grid, dim3(256), 0, st>>>(a, qs);
+  moe_gemm_pipe_kernel<RECIPE, EPI, QOUT, F16><<<grid, dim3(256), 0, st>>>(a, qs);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
+}
+template <int RECIPE, int EPI, bool QOUT>
+int launch_pipe(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+  return a.out_f16 ? launch_pipe_t<RECIPE, EPI, QOUT, true>(a, max_blocks, qs, st)
+                   : launch_pipe_t<RECIPE, EPI, QOUT, false>(a, max_blocks, qs, st);
 }
 
 }  // namespace

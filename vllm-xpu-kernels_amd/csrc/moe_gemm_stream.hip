@@ -11,22 +11,18 @@
 // the activation (16 slots m): lane l holds rows n = 4*(l/16) + r of slot
 // m = l%16.  The only barrier is in the fp8 epilogue, which finds the amax of
 // each slot's 128 activation columns across the 8 waves.
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int KS = 128;   // K elements per stage
 constexpr int WAVES = 8;
 
-__device__ __forceinline__ f32x4 mma_bf16(uint4 a, uint4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x4 mma_fp8(uint4 a0, uint4 a1, uint4 b0, uint4 b1) {
   i32x8 a = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
              (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
@@ -35,27 +31,6 @@ __device__ __forceinline__ f32x4 mma_fp8(uint4 a0, uint4 a1, uint4 b0, uint4 b1)
   f32x4 z = {0.f, 0.f, 0.f, 0.f};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
 }
-__device__ __forceinline__ uint4 fp4x8(uint32_t w, float sc) {
-  uint4 r;
-  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
-  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
-  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
-  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
-  return r;
-}
-__device__ __forceinline__ float rnd(float v, bool f16) {
-  return f16 ? f16_to_f32(f32_to_f16(v)) : bf16_to_f32(f32_to_bf16(v));
-}
-__device__ __forceinline__ float glu_fn(float g, float u, const GemmArgs& a) {
-  if (a.act == MI355MOE_ACT_SILU) {
-    float s = bf16_to_f32(f32_to_bf16(g / (1.f + expf(-g))));
-    return s * u;
-  }
-  g = g > a.limit ? a.limit : g;
-  u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-  return (u + 1.f) * (g * (1.f / (1.f + expf(-g * a.alpha))));
-}
-
 // Per-stage register fragments of one lane.
 template <int RECIPE>
 struct Frag;
@@ -79,7 +54,7 @@ struct Frag<MI355MOE_RECIPE_MXFP4> {     // 32 e2m1 + e8m0 of the weight row
   uint4 x[4];
 };
 
-template <int RECIPE, int EPI, bool QOUT, int PD>
+template <int RECIPE, int EPI, bool QOUT, int PD, bool F16>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -207,16 +182,16 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         uint4 w = f.w[t];
         if (f.sc[t] == 0u) w = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> 0
         const float sc = __uint_as_float(f.sc[t] << 23);
-        acc[t] = mma_bf16(fp4x8(w.x, sc), f.x[0], acc[t]);
-        acc[t] = mma_bf16(fp4x8(w.y, sc), f.x[1], acc[t]);
-        acc[t] = mma_bf16(fp4x8(w.z, sc), f.x[2], acc[t]);
-        acc[t] = mma_bf16(fp4x8(w.w, sc), f.x[3], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.x, sc), f.x[0], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.y, sc), f.x[1], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.z, sc), f.x[2], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.w, sc), f.x[3], acc[t]);
       }
     } else {
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) acc[t] = mma_bf16(f.w[t][s], f.x[s], acc[t]);
+        for (int t = 0; t < 2; ++t) acc[t] = mfma16_16x16x32<F16>(f.w[t][s], f.x[s], acc[t]);
     }
   };
 
@@ -272,7 +247,6 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   }
 
   // ---- epilogue: lane holds slot m = l16, columns col0 + 4q + r
-  const bool f16 = a.out_f16 != 0;
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
   const int drow = s_drow[l16];
   constexpr int NO = kGlu ? 1 : 2;
@@ -284,17 +258,17 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     for (int r = 0; r < 4; ++r) {
       const bool nok = n + r < N;
       float v = acc[t][r];
-      if (a.bias && nok) v += bf16_to_f32(a.bias[bias_base + n + r]);
-      v = rnd(v, f16);
+      if (a.bias && nok) v += ld16<F16>(a.bias[bias_base + n + r]);
+      v = rnd16<F16>(v);
       if constexpr (kGlu) {
         float u = acc[1][r];
-        if (a.bias && nok) u += bf16_to_f32(a.bias[bias_base + a.up_off + n + r]);
-        u = rnd(u, f16);
+        if (a.bias && nok) u += ld16<F16>(a.bias[bias_base + a.up_off + n + r]);
+        u = rnd16<F16>(u);
         if (a.clamp_limit > 0.f) {
           v = fminf(v, a.clamp_limit);
           u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
         }
-        v = rnd(glu_fn(v, u, a), f16);
+        v = rnd16<F16>(glu16<F16>(v, u, a.act, a.alpha, a.limit));
       }
       ov[t][r] = nok ? v : 0.f;
     }
@@ -329,7 +303,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       const int64_t n = col0 + 16 * t + 4 * q;
       uint16_t h[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) h[r] = f16 ? f32_to_f16(ov[t][r]) : f32_to_bf16(ov[t][r]);
+      for (int r = 0; r < 4; ++r) h[r] = st16<F16>(ov[t][r]);
       uint16_t* dst = d + static_cast<int64_t>(drow) * N + n;
       if (n + 3 < N && (N & 3) == 0) {
         *reinterpret_cast<uint2*>(dst) =
@@ -343,23 +317,28 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   }
 }
 
-template <int RECIPE, int EPI, bool QOUT>
-int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+template <int RECIPE, int EPI, bool QOUT, bool F16>
+int launch_stream_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
   constexpr int PD = 2;  // stages in flight per wave (deeper costs occupancy, measured no faster)
   const int64_t cols = EPI == EPI_GLU ? 128 : 256;
   dim3 grid(static_cast<unsigned>(cdiv(a.N, cols)), static_cast<unsigned>(max_blocks),
             static_cast<unsigned>(a.ksplit > 1 ? a.ksplit : 1));
   GemmArgs g = a;
   g.finalize = 0;
-  moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(g, qs);
+  moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
   MI_LAUNCH_CHECK();
   if (a.ksplit > 1 && !a.partials_only) {  // sum the partial tiles and run the epilogue
     grid.z = 1;
     g.finalize = 1;
-    moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD><<<grid, dim3(512), 0, st>>>(g, qs);
+    moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
     MI_LAUNCH_CHECK();
   }
   return MI355MOE_OK;
+}
+template <int RECIPE, int EPI, bool QOUT>
+int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+  return a.out_f16 ? launch_stream_t<RECIPE, EPI, QOUT, true>(a, max_blocks, qs, st)
+                   : launch_stream_t<RECIPE, EPI, QOUT, false>(a, max_blocks, qs, st);
 }
 
 }  // namespace

@@ -35,6 +35,7 @@
 // runs the MFMAs of its 32-row groups that hold valid slots only.
 #include <type_traits>
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -98,10 +99,6 @@ __device__ __forceinline__ void wait_vm_dyn(int n) {
 }
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
-__device__ __forceinline__ f32x16 mfma(uint4 a, uint4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-      __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
 
 template <bool F16>
 __device__ __forceinline__ float round16(float v) {
@@ -141,7 +138,7 @@ __device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, int xoff, i
 
 // 2 x NJ MFMAs of one K step; with `dma`, the step's DMA instructions q0 and
 // q0 + 1 go out between its two MFMA groups and after them.
-template <int NJ>
+template <int NJ, bool F16>
 __device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][MG], const Frag& f, bool dma,
                                           const uint32_t (&voff)[DMA_PER_WAVE],
                                           const uint8_t* sbase, uint32_t dst_base, int nd,
@@ -149,7 +146,7 @@ __device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][MG], const Frag& f, b
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(f.w[i], f.x[j], acc[i][j]);
+    for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16_32x32x16<F16>(f.w[i], f.x[j], acc[i][j]);
     __builtin_amdgcn_sched_barrier(0);
     const int q = q0 + i;
     if (dma && q < nd) dma16(voff[q], sbase, __builtin_amdgcn_readfirstlane(dst_base + q * 1024));
@@ -301,7 +298,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
     // the compiler copy every loop-carried fragment register where the
     // branches join.
     for (int kt = 0; kt < nk; ++kt) {
-      mfma_step<NJ>(acc, f0, false, voff, sbase0, 0, 0, 0);
+      mfma_step<NJ, F16>(acc, f0, false, voff, sbase0, 0, 0, 0);
       // stage kt+1 landed; stage kt+2 (if issued) may pend
       wait_vm_dyn(kt + 2 < nk ? nd : 0);
       __builtin_amdgcn_s_barrier();
@@ -309,7 +306,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
       const bool dma = kt + 3 < nk;
       const uint8_t* sb = sbase0 + static_cast<int64_t>(kt + 3) * kstep;
       const uint32_t dbase = ring0 + ((kt + 3) % NSTAGE) * STAGE + dst0;
-      mfma_step<NJ>(acc, f1, dma, voff, sb, dbase, nd, 0);
+      mfma_step<NJ, F16>(acc, f1, dma, voff, sb, dbase, nd, 0);
       if (dma && nd > 2) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -358,8 +355,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
           if (a.bias) {
             const int64_t n = n0 + tcol(i, r);
             if (n < N) {
-              bg[r] = bf16_to_f32(a.bias[bias_base + n]);
-              if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+              bg[r] = ld16<F16>(a.bias[bias_base + n]);
+              if constexpr (kGlu) bu[r] = ld16<F16>(a.bias[bias_base + a.up_off + n]);
             }
           }
         }

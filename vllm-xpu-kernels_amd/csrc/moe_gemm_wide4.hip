@@ -21,10 +21,11 @@
 //
 // Dequantisation.  A lane's MFMA fragment of weight row r for K step ks is
 // the 8 values [16 ks + 8 h, +8): 4 bytes of e2m1, converted with
-// v_cvt_scalef32_pk_bf16_fp4 under the row's scale (2^(code - 127); code 0
+// v_cvt_scalef32_pk_{bf16,f16}_fp4 (the call's 16-bit type) under the row's scale (2^(code - 127); code 0
 // gives 0, as the other mxfp4 kernels).
 #include <type_traits>
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -104,19 +105,6 @@ __device__ __forceinline__ void wait_vm_dyn(int n) {
 }
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
-__device__ __forceinline__ f32x16 mfma(uint4 a, uint4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-      __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-// 8 e2m1 values (4 bytes) -> 8 bf16 under an fp32 scale
-__device__ __forceinline__ uint4 e2m1x8_bf16(uint32_t w, float sc) {
-  uint4 r;
-  r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
-  r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
-  r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
-  r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
-  return r;
-}
 
 template <bool F16>
 __device__ __forceinline__ float round16(float v) {
@@ -145,7 +133,7 @@ struct Frag {
 // Activation tile j sits 32 x 64 bytes past tile 0 (rows 32 apart share the
 // swizzle).  Weight tile i: row woff_r + i * wstep_r; its 4 e2m1 bytes at
 // W_OFF + 16 row + wb, its scale at S_OFF + row.
-template <int NJ>
+template <int NJ, bool F16>
 __device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, int xoff, int wrow0,
                                           int wstep_r, int wb) {
 #pragma unroll
@@ -155,16 +143,16 @@ __device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, int xoff, i
     const int r = wrow0 + i * wstep_r;
     const uint32_t w = *reinterpret_cast<const uint32_t*>(S + W_OFF + 16 * r + wb);
     const uint32_t code = S[S_OFF + r];
-    f.w[i] = e2m1x8_bf16(w, __uint_as_float(code << 23));
+    f.w[i] = fp4x8_to16<F16>(w, __uint_as_float(code << 23));
   }
 }
 
-template <int NJ>
+template <int NJ, bool F16>
 __device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][MG], const Frag& f) {
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[i][j] = mfma(f.w[i], f.x[j], acc[i][j]);
+    for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16_32x32x16<F16>(f.w[i], f.x[j], acc[i][j]);
 }
 
 template <int EPI, bool F16>
@@ -311,18 +299,18 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
     Frag f0, f1;
     wait_vm_dyn(pending_after(0, NSTAGE - 2));
     __builtin_amdgcn_s_barrier();
-    read_frag<NJ>(f0, lds, xoff[0], wrow0, WSTEP_R, 4 * h);
-    read_frag<NJ>(f1, lds, xoff[1], wrow0, WSTEP_R, 8 + 4 * h);
+    read_frag<NJ, F16>(f0, lds, xoff[0], wrow0, WSTEP_R, 4 * h);
+    read_frag<NJ, F16>(f1, lds, xoff[1], wrow0, WSTEP_R, 8 + 4 * h);
     for (int kt = 0; kt < nk; ++kt) {
-      mfma_step<NJ>(acc, f0);
+      mfma_step<NJ, F16>(acc, f0);
       // stage kt+1 landed; later stages this wave issued may pend
       wait_vm_dyn(pending_after(kt + 1, kt + NSTAGE - 2));
       __builtin_amdgcn_s_barrier();
       const uint8_t* S1 = lds + ((kt + 1) % NSTAGE) * STAGE;
-      read_frag<NJ>(f0, S1, xoff[0], wrow0, WSTEP_R, 4 * h);
+      read_frag<NJ, F16>(f0, S1, xoff[0], wrow0, WSTEP_R, 4 * h);
       if (kt + NSTAGE - 1 < nk) issue(kt + NSTAGE - 1);
-      mfma_step<NJ>(acc, f1);
-      read_frag<NJ>(f1, S1, xoff[1], wrow0, WSTEP_R, 8 + 4 * h);
+      mfma_step<NJ, F16>(acc, f1);
+      read_frag<NJ, F16>(f1, S1, xoff[1], wrow0, WSTEP_R, 8 + 4 * h);
     }
   };
   switch (nj) {
@@ -363,8 +351,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
           if (a.bias) {
             const int64_t n = n0 + tcol(i, r);
             if (n < N) {
-              bg[r] = bf16_to_f32(a.bias[bias_base + n]);
-              if constexpr (kGlu) bu[r] = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+              bg[r] = ld16<F16>(a.bias[bias_base + n]);
+              if constexpr (kGlu) bu[r] = ld16<F16>(a.bias[bias_base + a.up_off + n]);
             }
           }
         }

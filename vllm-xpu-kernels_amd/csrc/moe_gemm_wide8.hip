@@ -36,6 +36,7 @@
 // quantisation group of the next GEMM's input.
 #include <type_traits>
 
+#include "mfma16.h"
 #include "moe_gemm.h"
 
 namespace mi355 {
@@ -347,8 +348,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       if (a.bias) {
         const int64_t n = n0 + tcol(i, r);
         if (n < N) {
-          bg = bf16_to_f32(a.bias[bias_base + n]);
-          if constexpr (kGlu) bu = bf16_to_f32(a.bias[bias_base + a.up_off + n]);
+          bg = ld16<F16>(a.bias[bias_base + n]);
+          if constexpr (kGlu) bu = ld16<F16>(a.bias[bias_base + a.up_off + n]);
         }
       }
       float gv = round16<F16>(acc[i][j][r] + bg);
@@ -506,7 +507,8 @@ int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
   if (qout) {
     MI_ARG(epi == EPI_GLU && a.N % 128 == 0,
            "fp8 activation output needs the GLU epilogue and I % 128 == 0");
-    return launch_w8<EPI_GLU, true, false>(a, max_blocks, qs, st);
+    return a.out_f16 ? launch_w8<EPI_GLU, true, true>(a, max_blocks, qs, st)
+                     : launch_w8<EPI_GLU, true, false>(a, max_blocks, qs, st);
   }
   if (epi == EPI_GLU)
     return a.out_f16 ? launch_w8<EPI_GLU, false, true>(a, max_blocks, qs, st)

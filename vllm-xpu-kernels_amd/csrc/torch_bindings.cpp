@@ -570,6 +570,9 @@ at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
               "ptr_A K dimension must match ptr_B logical K dimension and K");
   TORCH_CHECK(ptr_D.size(1) == N,
               "ptr_B logical N dimension must match ptr_D N dimension and N");
+  if (ptr_bias)
+    TORCH_CHECK(ptr_bias->scalar_type() == ptr_D.scalar_type(),
+                "ptr_bias must have the output dtype");
   const int64_t M = ptr_A.size(0);
   const int adt = dtype_code(ptr_A.scalar_type());
   const size_t ws_bytes =
@@ -642,6 +645,10 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.output = output.data_ptr();
   a.w_layout = static_cast<int>(w_layout);
   a.hidden_scale = hidden_scale ? hidden_scale->data_ptr<float>() : nullptr;
+  for (const auto* b : {&w13_bias, &w2_bias})
+    if (b->has_value())
+      TORCH_CHECK((*b)->scalar_type() == output.scalar_type(),
+                  "biases must have the output dtype");
   const size_t ws_bytes = mi355moe_fused_moe_workspace_size(&a);
   auto ws = at::empty({static_cast<int64_t>(ws_bytes)},
                       hidden_states.options().dtype(at::kByte));

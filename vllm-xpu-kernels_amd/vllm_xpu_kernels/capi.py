@@ -65,7 +65,8 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a = FusedMoeArgs()
     a.recipe = moe._recipe
     a.activation = moe._act
-    a.act_dtype = BF16
+    a.act_dtype = F16 if output.dtype == torch.float16 else BF16
+    b13, b2 = moe._biases(output.dtype)
     a.ids_dtype = I64 if topk_ids.dtype == torch.int64 else I32
     a.num_tokens, a.hidden = hidden_states.shape
     a.inter = moe.inter_size
@@ -79,11 +80,11 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.w13 = moe.w13.data_ptr()
     a.w13_scale = (moe.gemm1_wei_scales.data_ptr()
                    if moe.gemm1_wei_scales is not None else None)
-    a.w13_bias = moe.w13_bias.data_ptr() if moe.w13_bias is not None else None
+    a.w13_bias = b13.data_ptr() if b13 is not None else None
     a.w2 = moe.w2.data_ptr()
     a.w2_scale = (moe.gemm2_wei_scales.data_ptr()
                   if moe.gemm2_wei_scales is not None else None)
-    a.w2_bias = moe.w2_bias.data_ptr() if moe.w2_bias is not None else None
+    a.w2_bias = b2.data_ptr() if b2 is not None else None
     a.gemm1_clamp_limit = float(moe.gemm1_clamp_limit or 0.0)
     a.swiglu_alpha = 1.702
     a.swiglu_limit = 7.0

@@ -66,6 +66,14 @@ def _get_inter_size(w13, w13_scales, is_int4, is_mxfp4, is_block_fp8):
     return w13.shape[-1] // 2
 
 
+def _bias16(b):
+    if b is None:
+        return None
+    if b.dtype not in (torch.bfloat16, torch.float16):
+        b = b.to(torch.bfloat16)
+    return b.contiguous()
+
+
 def _deinterleave_rows(t: torch.Tensor, dim: int) -> torch.Tensor:
     """[.., 2I, ..] with gate at even / up at odd rows -> [gate; up]."""
     even = t.narrow(dim, 0, t.shape[dim]).index_select(
@@ -174,8 +182,8 @@ class XpuFusedMoe:
         E = w13.shape[0]
         swiglu = self._act == ACT_SWIGLUOAI
         if self._recipe == RECIPE_BF16:
-            if w13.dtype != torch.bfloat16:
-                raise NotImplementedError("only bfloat16 weights are supported")
+            if w13.dtype not in (torch.bfloat16, torch.float16):
+                raise NotImplementedError("16-bit weights must be bfloat16 or float16")
             # reference layout [E, K, N] -> [E, N, K]
             w13c = w13.transpose(1, 2).contiguous()
             w2c = w2.transpose(1, 2).contiguous()
@@ -194,8 +202,9 @@ class XpuFusedMoe:
             w2c = w2.view(torch.uint8)
             s13c = s13.view(torch.uint8) if s13.dtype != torch.uint8 else s13
             s2c = s2.view(torch.uint8) if s2.dtype != torch.uint8 else s2
-        b13c = b13.to(torch.bfloat16).contiguous() if b13 is not None else None
-        b2c = b2.to(torch.bfloat16).contiguous() if b2 is not None else None
+        # biases keep their 16-bit type; apply() converts them to the call's
+        b13c = _bias16(b13)
+        b2c = _bias16(b2)
         if swiglu:
             w13c = _deinterleave_rows(w13c, 1)
             if s13c is not None:
@@ -218,6 +227,19 @@ class XpuFusedMoe:
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
         self.w13_bias, self.w2_bias = b13c, b2c
+        self._bias_cache = {}
+
+    def _biases(self, dtype):
+        """Biases in the call's 16-bit type (the kernels read them as such)."""
+        if self.w13_bias is None and self.w2_bias is None:
+            return None, None
+        if all(b is None or b.dtype == dtype for b in (self.w13_bias, self.w2_bias)):
+            return self.w13_bias, self.w2_bias
+        if dtype not in self._bias_cache:
+            self._bias_cache[dtype] = tuple(
+                None if b is None else b.to(dtype).contiguous()
+                for b in (self.w13_bias, self.w2_bias))
+        return self._bias_cache[dtype]
 
     # ------------------------------------------------------------------
     def apply(self, output, hidden_states, topk_weights, topk_ids,
@@ -230,13 +252,17 @@ class XpuFusedMoe:
                     "pre-quantised activations (a1q_scale) are supported for "
                     "the fp8 block-scaled recipe (e4m3 + [T, H/128] scales)")
             a1q_scale = a1q_scale.to(torch.float32).contiguous()
+        if self._recipe == RECIPE_BF16 and hidden_states.dtype != self.w13.dtype:
+            raise ValueError(f"hidden_states ({hidden_states.dtype}) must have the "
+                             f"16-bit weights' dtype ({self.w13.dtype})")
         if expert_map is None and self.ep_size > 1:
             expert_map = self.expert_map
         clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
+        b13, b2 = self._biases(output.dtype)
         torch.ops._moe_C.mi355_fused_moe(
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
             topk_ids.contiguous(), self.w13, self.gemm1_wei_scales,
-            self.w13_bias, self.w2, self.gemm2_wei_scales, self.w2_bias,
+            b13, self.w2, self.gemm2_wei_scales, b2,
             self._recipe, self._act, self.inter_size, clamp, expert_map,
             self._w_layout, a1q_scale)
         return output
