@@ -270,7 +270,11 @@ int mi355moe_silu_and_mul_mxfp4_quant(uint8_t* out, const void* input, int in_dt
  * (csrc/xpu/torch_bindings.cpp:46-53, csrc/xpu/grouped_gemm/
  * grouped_gemm_interface.cpp:12-60).  Rows of expert e are contiguous in A
  * and D (prefix sums of rows_per_expert, read on device).
- *   recipe BF16:     A bf16 or f16 [M,K]; B of the same type [E,N,K]
+ *   recipe BF16:     A bf16 or f16 [M,K]; B of the same type [E,N,K];
+ *                    b_scale optional f32 [E]: each expert's accumulators
+ *                    times b_scale[e] before the bias (per-expert-scaled
+ *                    fp8 weights converted exactly to the 16-bit type; the
+ *                    reference's acc * s_e, gemm_xe2.hpp:192-198)
  *   recipe FP8BLOCK: A e4m3 [M,K] + a_scale f32 [M,K/128] (1x128 groups),
  *                    or A bf16/f16 (quantised 1x128 in the workspace);
  *                    B e4m3 [E,N,K] + b_scale f32 [E,N/128,K/128]
@@ -318,10 +322,11 @@ typedef struct {
   const int32_t* expert_map;  /* optional [expert_map_len]: global -> local  */
   int64_t expert_map_len;
   const void* w13;            /* per recipe                                  */
-  const void* w13_scale;
+  const void* w13_scale;      /* per recipe; BF16: optional f32 [E] factor
+                                 on the accumulators (per-expert fp8)     */
   const void* w13_bias;       /* optional [E, 2I] bf16 (same row order)      */
   const void* w2;
-  const void* w2_scale;
+  const void* w2_scale;       /* as w13_scale                               */
   const void* w2_bias;        /* optional [E, H] bf16                        */
   float gemm1_clamp_limit;    /* <= 0: off                                   */
   float swiglu_alpha;         /* swigluoai alpha (1.702)                     */

@@ -544,6 +544,10 @@ def dequant_weight(recipe: str, w_e: torch.Tensor, s_e) -> torch.Tensor:
     (vllm_xpu_kernels/moe_utils.py:189-202)."""
     if recipe == "bf16":
         return w_e.float()
+    if recipe == "fp8":
+        # per-expert scale (moe_utils.py:212-213; gemm_xe2.hpp:192-198 applies
+        # it to the accumulators, the same product up to fp32 rounding)
+        return w_e.float() * float(s_e)
     if recipe == "fp8block":
         return dequant_fp8_block_weight(w_e, s_e)
     if recipe == "mxfp4":

@@ -661,6 +661,68 @@ def test_fused_moe_fp16_bias_follows_call_dtype(dev):
     assert torch.float16 in moe._bias_cache
 
 
+def _fp8_expert_weights(E, N, K, fp8, g):
+    """[E, N, K] weights randn/16 quantised per expert with power-of-two
+    scales 2^-3..2^3 (the reference's tests/fused_moe/test_fused_moe.py:
+    226-246 recipe); returns (q nk, scales [E])."""
+    w = torch.randn(E, N, K, generator=g) / 16
+    s = torch.pow(2.0, torch.randint(-3, 4, (E,), generator=g).float())
+    fmax = torch.finfo(fp8).max
+    return (w / s.view(E, 1, 1)).clamp(-fmax, fmax).to(fp8), s
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fp8", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("has_bias", [False, True])
+def test_grouped_gemm_fp8_per_expert(dev, dt, fp8, has_bias):
+    """Per-expert fp8 weights [E, K, N] (e5m2 or e4m3) with fp32 scales [E]
+    (reference tests/fused_moe/test_grouped_gemm.py:153-221): D = T(s_e A W_e +
+    bias), within rtol = atol = 1e-2 of the oracle."""
+    g = torch.Generator().manual_seed(21)
+    E, N, K = 4, 384, 512
+    M = sum(ROWS)
+    a = torch.randn(M, K, generator=g).to(dt)
+    q, sc = _fp8_expert_weights(E, N, K, fp8, g)
+    bias = (torch.randn(E, N, generator=g) * 100).to(dt) if has_bias else None
+    d = torch.empty(M, N, dtype=dt, device=dev)
+    _ops().cutlass_grouped_gemm(a.to(dev), q.transpose(1, 2).contiguous().to(dev), sc.to(dev),
+                                None if bias is None else bias.to(dev), d,
+                                torch.tensor(ROWS, dtype=torch.int32, device=dev), N, K, E)
+    ref = O.grouped_gemm("fp8", a, q, sc, bias, ROWS, out_dtype=dt)
+    torch.testing.assert_close(d.cpu(), ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fp8", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("T,topk", [(1, 1), (4, 1), (16, 1), (512, 1), (2048, 2)])
+def test_fused_moe_fp8_per_expert(dev, dt, fp8, T, topk):
+    """The reference's per-expert fp8 layer (tests/fused_moe/test_fused_moe.py:
+    179-295, Llama-4-scout structure at H=1024, I=512, 16 experts): weights
+    [E, K, N] e5m2 / e4m3 with scales [E], biases, raw top-k scores as
+    weights, bf16 or fp16; every element within the reference's bar (bf16
+    2e-2, fp16 1e-2).  T covers the split-K stream, stream, small and 320-slot
+    kernels; the oracle checks 64 sampled tokens at T=2048."""
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    g = torch.Generator().manual_seed(7 + T)
+    E, H, I = 16, 1024, 512
+    q13, s13 = _fp8_expert_weights(E, 2 * I, H, fp8, g)
+    q2, s2 = _fp8_expert_weights(E, H, I, fp8, g)
+    b13 = (torch.randn(E, 2 * I, generator=g) / 16).to(dt)
+    b2 = (torch.randn(E, H, generator=g) / 16).to(dt)
+    x = (torch.randn(T, H, generator=g) / 16).to(dt)
+    tw, ti = torch.topk(torch.randn(T, E, generator=g), k=topk, dim=-1, sorted=False)
+    moe = XpuFusedMoe(q13.transpose(1, 2).contiguous().to(dev), s13.to(dev), b13.to(dev),
+                      q2.transpose(1, 2).contiguous().to(dev), s2.to(dev), b2.to(dev),
+                      topk, "silu", E)
+    assert moe.recipe == "fp8"
+    out = torch.empty(T, H, dtype=dt, device=dev)
+    moe.apply(out, x.to(dev), tw.to(dev), ti.to(dev))
+    toks = torch.linspace(0, T - 1, min(T, 64)).long()
+    ref = O.fused_moe("fp8", x[toks], q13, s13, b13, q2, s2, b2, tw[toks], ti[toks])
+    tol = 2e-2 if dt == torch.bfloat16 else 1e-2
+    torch.testing.assert_close(out.cpu()[toks], ref, rtol=tol, atol=tol)
+
+
 def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):
     cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C1"], 8, dev)
     with pytest.raises(NotImplementedError, match="fp8 block-scaled recipe"):

@@ -498,6 +498,31 @@ def test_fused_moe_oracle_vs_reference_golden():
     torch.testing.assert_close(y.float(), ref.float(), rtol=2e-2, atol=2e-2)
 
 
+def test_fp8_per_expert_is_the_16bit_layer_on_dequantised_weights():
+    """Recipe "fp8" (per-expert scales, w8a16): e4m3 and e5m2 codes times a
+    power-of-two scale are exact in fp32, so the grouped GEMM and the layer
+    equal the 16-bit recipe run on the dequantised weights."""
+    g = torch.Generator().manual_seed(12)
+    E, N, K = 3, 64, 96
+    rows = [5, 0, 7]
+    a = torch.randn(sum(rows), K, generator=g).bfloat16()
+    s = torch.tensor([0.25, 2.0, 8.0])
+    for dt in (torch.float8_e4m3fn, torch.float8_e5m2):
+        q = (torch.randn(E, N, K, generator=g) * 4).to(dt)
+        deq = q.float() * s.view(E, 1, 1)
+        y = O.grouped_gemm("fp8", a, q, s, None, rows)
+        assert torch.equal(y, O.grouped_gemm("bf16", a, deq, None, None, rows))
+    T, H, I, k = 10, 64, 32, 2
+    x = torch.randn(T, H, generator=g).bfloat16()
+    q13 = (torch.randn(E, 2 * I, H, generator=g) * 4).to(torch.float8_e5m2)
+    q2 = (torch.randn(E, H, I, generator=g) * 4).to(torch.float8_e5m2)
+    w, ids, _ = O.topk_softmax(torch.randn(T, E, generator=g), k, True)
+    y = O.fused_moe("fp8", x, q13, s, None, q2, s * 0.5, None, w, ids)
+    ref = O.fused_moe("bf16", x, q13.float() * s.view(E, 1, 1), None, None,
+                      q2.float() * (s * 0.5).view(E, 1, 1), None, None, w, ids)
+    assert torch.equal(y, ref)
+
+
 def test_fused_moe_oracle_fp8block_close_to_dequant_fp32():
     """fp8block = dequantised fp32 layer up to activation quantisation noise."""
     torch.manual_seed(8)

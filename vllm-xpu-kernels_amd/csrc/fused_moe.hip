@@ -109,7 +109,8 @@ template <bool F16>
 __global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
     uint16_t* __restrict__ out, const float* __restrict__ part, int ks, int n_tiles,
     const int32_t* __restrict__ inv_pos, const int32_t* __restrict__ block_expert,
-    const uint16_t* __restrict__ bias, const float* __restrict__ w, int topk, int64_t H) {
+    const uint16_t* __restrict__ bias, const float* __restrict__ escale,
+    const float* __restrict__ w, int topk, int64_t H) {
   __shared__ float4 s_g[kFuseMaxTopk][64];
   const int64_t t = blockIdx.y;
   const int nt = blockIdx.x;
@@ -128,6 +129,10 @@ __global__ __launch_bounds__(256) void finalize_topk_sum_kernel(
       for (int z = 0; z < ks; ++z) {
         const float4 a = *reinterpret_cast<const float4*>(tp + z * 4096);
         v0 += a.x; v1 += a.y; v2 += a.z; v3 += a.w;
+      }
+      if (escale) {  // per-expert factor before the bias (recipe BF16)
+        const float es = escale[block_expert[blk]];
+        v0 *= es; v1 *= es; v2 *= es; v3 *= es;
       }
       if (bias) {
         const uint16_t* b = bias + static_cast<int64_t>(block_expert[blk]) * H + h;
@@ -523,6 +528,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.part = L.part1;
   g1.w_kblock = kblock;
   g1.out_f16 = f16;
+  g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w13_scale)
+                                                    : nullptr;
   if (glu) {
     rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
     if (rc) return rc;
@@ -566,6 +573,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.part = L.part2;
   g2.w_kblock = kblock;
   g2.out_f16 = f16;
+  g2.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w2_scale)
+                                                    : nullptr;
   // split-K decode: the partial sums are finished by the top-k reduction
   const bool fuse_reduce = L.tile == TILE_STREAM && L.ks2 > 1 && k <= kFuseMaxTopk;
   g2.partials_only = fuse_reduce;
@@ -577,8 +586,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     auto fin = f16 ? finalize_topk_sum_kernel<true> : finalize_topk_sum_kernel<false>;
     fin<<<grid, dim3(256), 0, st>>>(
         static_cast<uint16_t*>(a->output), L.part2, L.ks2, static_cast<int>(cdiv(H, 256)),
-        L.inv, L.eids, static_cast<const uint16_t*>(a->w2_bias), a->topk_weights,
-        static_cast<int>(k), H);
+        L.inv, L.eids, static_cast<const uint16_t*>(a->w2_bias), g2.expert_scale,
+        a->topk_weights, static_cast<int>(k), H);
     MI_LAUNCH_CHECK();
     return mark(5);
   }
@@ -723,6 +732,7 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
   g.K = K;
   g.ldb_rows = N;
   g.out_f16 = out_dtype == MI355MOE_F16;
+  g.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(b_scale) : nullptr;
   return launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g, L.grid_blocks, nullptr, st);
 }
 

@@ -73,6 +73,7 @@ __device__ __forceinline__ void epilogue_32x32(const GemmArgs& a, void* qs,
                                                int ngroup, uint8_t* stage) {
   const int64_t N = a.N;
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  const float es = a.expert_scale ? a.expert_scale[e] : 1.f;  // recipe BF16 only
   constexpr int NO = kGlu ? 2 : 4;       // output n-tiles per wave
   constexpr int NOUT = kGlu ? 128 : 256;  // output columns of the tile
   // tile column of (tile i, reg r)
@@ -102,9 +103,9 @@ __device__ __forceinline__ void epilogue_32x32(const GemmArgs& a, void* qs,
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float v = round16<F16>(acc[i][j][r] + bg[r]);
+        float v = round16<F16>(acc[i][j][r] * es + bg[r]);
         if constexpr (kGlu) {
-          float u = round16<F16>(acc[i + 2][j][r] + bu[r]);
+          float u = round16<F16>(acc[i + 2][j][r] * es + bu[r]);
           if (a.clamp_limit > 0.f) {
             v = fminf(v, a.clamp_limit);
             u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);

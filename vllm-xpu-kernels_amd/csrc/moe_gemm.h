@@ -53,6 +53,10 @@ struct GemmArgs {
   float* part;           // [blocks, n_tiles, ksplit, 512 x 8]
   int32_t finalize;      // set by the launcher for the second launch
   int32_t partials_only; // split launch only: the caller consumes `part`
+  // Recipe BF16 only, optional: fp32 [E] factor on each expert's accumulators
+  // before the bias (per-expert-scaled fp8 weights, converted exactly to the
+  // 16-bit type: D = T(s_e * sum_k A W_e + bias_e)).
+  const float* expert_scale;
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };

@@ -193,6 +193,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
 
   // ---- epilogue: lane holds D[row = mt*16 + l16][n = nbase + j*16 + 4q + r]
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  const float es = a.expert_scale ? a.expert_scale[e] : 1.f;
   float outv[MT][NT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -202,11 +203,11 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool nok = n + r < a.N;
-        float v = acc[mt][j][r];
+        float v = acc[mt][j][r] * es;
         if (a.bias && nok) v += ld16<F16>(a.bias[bias_base + n + r]);
         v = rnd16<F16>(v);
         if constexpr (EPI == EPI_GLU) {
-          float u = acc[mt][j + NT][r];
+          float u = acc[mt][j + NT][r] * es;
           if (a.bias && nok) u += ld16<F16>(a.bias[bias_base + a.up_off + n + r]);
           u = rnd16<F16>(u);
           if (a.clamp_limit > 0.f) {

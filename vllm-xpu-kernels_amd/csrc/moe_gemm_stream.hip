@@ -248,6 +248,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 
   // ---- epilogue: lane holds slot m = l16, columns col0 + 4q + r
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  const float es = a.expert_scale ? a.expert_scale[e] : 1.f;
   const int drow = s_drow[l16];
   constexpr int NO = kGlu ? 1 : 2;
   float ov[NO][4];
@@ -257,11 +258,11 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool nok = n + r < N;
-      float v = acc[t][r];
+      float v = acc[t][r] * es;
       if (a.bias && nok) v += ld16<F16>(a.bias[bias_base + n + r]);
       v = rnd16<F16>(v);
       if constexpr (kGlu) {
-        float u = acc[1][r];
+        float u = acc[1][r] * es;
         if (a.bias && nok) u += ld16<F16>(a.bias[bias_base + a.up_off + n + r]);
         u = rnd16<F16>(u);
         if (a.clamp_limit > 0.f) {

@@ -334,6 +334,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
   constexpr int PASSES = BM * PITCH <= RING_BYTES ? 1 : 2;
   constexpr int PROWS = BM / PASSES;
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  const float es = a.expert_scale ? a.expert_scale[e] : 1.f;  // recipe BF16 only
   auto tcol = [&](int i, int r) -> int {  // tile output column of (i, r)
     return (kGlu ? 32 * wn : 64 * wn + 32 * i) + 8 * (r >> 2) + 4 * h + (r & 3);
   };
@@ -366,9 +367,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
           float ov[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            float g = round16<F16>(acc[i][j][r] + bg[r]);
+            float g = round16<F16>(acc[i][j][r] * es + bg[r]);
             if constexpr (kGlu) {
-              float u = round16<F16>(acc[1][j][r] + bu[r]);
+              float u = round16<F16>(acc[1][j][r] * es + bu[r]);
               if (a.clamp_limit > 0.f) {
                 g = fminf(g, a.clamp_limit);
                 u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);

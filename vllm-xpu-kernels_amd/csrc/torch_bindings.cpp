@@ -532,13 +532,28 @@ at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
     TORCH_CHECK(ptr_bias->size(1) == N, "ptr_bias.size(1) must match N");
   }
   const auto bdt = ptr_B.scalar_type();
-  const bool is_fp8 = bdt == at::kFloat8_e4m3fn;
+  // fp8 weights with one scale per expert (not the 3-D block scales): the
+  // reference's w8a16 per-expert path, acc * s_e (gemm_xe2.hpp:192-198)
+  const bool is_fp8_expert = (bdt == at::kFloat8_e4m3fn || bdt == at::kFloat8_e5m2) &&
+                             ptr_B_scale.has_value() && ptr_B_scale->dim() != 3;
+  const bool is_fp8 = bdt == at::kFloat8_e4m3fn && !is_fp8_expert;
   const bool is_mxfp4 = bdt == at::kFloat4_e2m1fn_x2 ||
                         (bdt == at::kByte && ptr_B_scale.has_value() &&
                          ptr_B_scale->scalar_type() != at::kFloat);
   int recipe = MI355MOE_RECIPE_BF16;
   at::Tensor B = ptr_B;
-  if (is_mxfp4) {
+  at::Tensor expert_scale;
+  if (is_fp8_expert) {
+    TORCH_CHECK(ptr_A.scalar_type() == at::kBFloat16 || ptr_A.scalar_type() == at::kHalf,
+                "per-expert fp8 weights need bfloat16 or float16 activations");
+    TORCH_CHECK(ptr_B_scale->numel() == num_experts,
+                "per-expert fp8 scales must have num_experts elements");
+    TORCH_CHECK(ptr_B.size(1) == K && ptr_B.size(2) == N,
+                "ptr_A K dimension must match ptr_B logical K dimension and K");
+    // every e4m3 / e5m2 value is exact in bf16 and fp16
+    B = ptr_B.to(ptr_A.scalar_type()).transpose(1, 2).contiguous();
+    expert_scale = ptr_B_scale->to(at::kFloat).reshape({num_experts}).contiguous();
+  } else if (is_mxfp4) {
     recipe = MI355MOE_RECIPE_MXFP4;
     TORCH_CHECK(ptr_B_scale.has_value(), "mxfp4 weights need ptr_B_scale");
     TORCH_CHECK(ptr_B.size(1) == N && ptr_B.size(2) * 2 == K,
@@ -558,7 +573,7 @@ at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
                 ptr_B.sizes());
     if (!nk) B = ptr_B.transpose(1, 2).contiguous();
     recipe = MI355MOE_RECIPE_FP8BLOCK;
-  } else {
+  } else if (!is_fp8_expert) {
     TORCH_CHECK(bdt == ptr_A.scalar_type(),
                 "bf16/fp16 weights must have the activation dtype");
     // reference layout is [E, K, N]
@@ -582,7 +597,10 @@ at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
   check_rc(mi355moe_grouped_gemm(
                recipe, ptr_A.data_ptr(), adt,
                ptr_A_scale ? ptr_A_scale->data_ptr<float>() : nullptr, B.data_ptr(),
-               ptr_B_scale ? ptr_B_scale->data_ptr() : nullptr, opt_ptr(ptr_bias),
+               is_fp8_expert ? expert_scale.data_ptr()
+                             : (ptr_B_scale && recipe != MI355MOE_RECIPE_BF16
+                                    ? ptr_B_scale->data_ptr() : nullptr),
+               opt_ptr(ptr_bias),
                ptr_D.data_ptr(), dtype_code(ptr_D.scalar_type()),
                rows_per_expert.data_ptr<int32_t>(), M, N, K, num_experts,
                ws.data_ptr(), ws_bytes, cur_stream(ptr_A)),

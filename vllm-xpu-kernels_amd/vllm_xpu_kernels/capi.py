@@ -67,6 +67,7 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.activation = moe._act
     a.act_dtype = F16 if output.dtype == torch.float16 else BF16
     b13, b2 = moe._biases(output.dtype)
+    w13, w2 = moe._call_weights(hidden_states.dtype)
     a.ids_dtype = I64 if topk_ids.dtype == torch.int64 else I32
     a.num_tokens, a.hidden = hidden_states.shape
     a.inter = moe.inter_size
@@ -77,11 +78,11 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.topk_ids = topk_ids.data_ptr()
     a.expert_map = expert_map.data_ptr() if expert_map is not None else None
     a.expert_map_len = expert_map.numel() if expert_map is not None else 0
-    a.w13 = moe.w13.data_ptr()
+    a.w13 = w13.data_ptr()
     a.w13_scale = (moe.gemm1_wei_scales.data_ptr()
                    if moe.gemm1_wei_scales is not None else None)
     a.w13_bias = b13.data_ptr() if b13 is not None else None
-    a.w2 = moe.w2.data_ptr()
+    a.w2 = w2.data_ptr()
     a.w2_scale = (moe.gemm2_wei_scales.data_ptr()
                   if moe.gemm2_wei_scales is not None else None)
     a.w2_bias = b2.data_ptr() if b2 is not None else None

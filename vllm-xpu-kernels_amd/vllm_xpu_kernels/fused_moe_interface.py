@@ -122,10 +122,10 @@ class XpuFusedMoe:
         assert w13.is_contiguous() and w2.is_contiguous()
         (is_fp8, is_int4, is_mxfp4, is_mxfp8,
          is_block_fp8) = _get_weights_dtype(w13, w13_scales)
-        if is_int4 or is_mxfp8 or is_fp8:
+        if is_int4 or is_mxfp8:
             raise NotImplementedError(
-                "recipes int4, mxfp8 and per-tensor fp8 are not implemented "
-                "on MI355X yet; use bf16, fp8 block (128x128) or mxfp4")
+                "recipes int4 and mxfp8 are not implemented on MI355X yet; use "
+                "bf16/fp16, fp8 (per-expert or 128x128 block scales) or mxfp4")
         self.inter_size = _get_inter_size(w13, w13_scales, is_int4, is_mxfp4,
                                           is_block_fp8)
         self.n_experts_per_token = n_experts_per_token
@@ -148,9 +148,16 @@ class XpuFusedMoe:
         # relu2_no_mul keeps all 2I columns: the activation, and w2's K, are
         # 2I wide (reference :226)
         self.inter_size_scale = 2 if self._act == ACT_RELU2 else 1
+        # per-expert fp8 (reference recipe "fp8", w8a16): the weights are
+        # converted exactly to the call's 16-bit type and run the 16-bit
+        # kernels with each expert's scale on the accumulators
+        self._fp8_expert = is_fp8
         if is_block_fp8:
             self.recipe = "fp8block"
             self._recipe = RECIPE_FP8BLOCK
+        elif is_fp8:
+            self.recipe = "fp8"
+            self._recipe = RECIPE_BF16
         elif is_mxfp4:
             self.recipe = "mxfp4"
             self._recipe = RECIPE_MXFP4
@@ -181,7 +188,13 @@ class XpuFusedMoe:
         K2 = I * self.inter_size_scale
         E = w13.shape[0]
         swiglu = self._act == ACT_SWIGLUOAI
-        if self._recipe == RECIPE_BF16:
+        if self._fp8_expert:
+            # reference layout [E, K, N] (as 16-bit) -> [E, N, K], kept in fp8
+            w13c = w13.transpose(1, 2).contiguous()
+            w2c = w2.transpose(1, 2).contiguous()
+            s13c = s13.to(torch.float32).reshape(E).contiguous()
+            s2c = s2.to(torch.float32).reshape(E).contiguous()
+        elif self._recipe == RECIPE_BF16:
             if w13.dtype not in (torch.bfloat16, torch.float16):
                 raise NotImplementedError("16-bit weights must be bfloat16 or float16")
             # reference layout [E, K, N] -> [E, N, K]
@@ -207,7 +220,7 @@ class XpuFusedMoe:
         b2c = _bias16(b2)
         if swiglu:
             w13c = _deinterleave_rows(w13c, 1)
-            if s13c is not None:
+            if s13c is not None and not self._fp8_expert:
                 s13c = _deinterleave_rows(s13c, 1)
             if b13c is not None:
                 b13c = _deinterleave_rows(b13c, 1)
@@ -219,15 +232,32 @@ class XpuFusedMoe:
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
                   (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and K2 <= 8192) or
                   self._recipe == RECIPE_MXFP4)
-        if kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk":
+        self._kblock = kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk"
+        if self._kblock and not self._fp8_expert:
             w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)
             if self._recipe == RECIPE_MXFP4:
                 s13c, s2c = pack_scales_kblock(s13c), pack_scales_kblock(s2c)
             self._w_layout = WLAYOUT_KBLOCK
+        if self._fp8_expert and self._kblock:
+            self._w_layout = WLAYOUT_KBLOCK   # applies to the 16-bit copies
+        self._w16_cache = {}
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
         self.w13_bias, self.w2_bias = b13c, b2c
         self._bias_cache = {}
+
+    def _call_weights(self, dtype):
+        """(w13, w2) the kernels read for a call in `dtype`: the prepared
+        weights, or for per-expert fp8 their exact 16-bit copies (made
+        once per dtype, K-blocked like 16-bit weights)."""
+        if not self._fp8_expert:
+            return self.w13, self.w2
+        if dtype not in self._w16_cache:
+            w13, w2 = self.w13.to(dtype), self.w2.to(dtype)
+            if self._kblock:
+                w13, w2 = pack_weights_kblock(w13), pack_weights_kblock(w2)
+            self._w16_cache[dtype] = (w13.contiguous(), w2.contiguous())
+        return self._w16_cache[dtype]
 
     def _biases(self, dtype):
         """Biases in the call's 16-bit type (the kernels read them as such)."""
@@ -252,17 +282,19 @@ class XpuFusedMoe:
                     "pre-quantised activations (a1q_scale) are supported for "
                     "the fp8 block-scaled recipe (e4m3 + [T, H/128] scales)")
             a1q_scale = a1q_scale.to(torch.float32).contiguous()
-        if self._recipe == RECIPE_BF16 and hidden_states.dtype != self.w13.dtype:
+        if (self._recipe == RECIPE_BF16 and not self._fp8_expert and
+                hidden_states.dtype != self.w13.dtype):
             raise ValueError(f"hidden_states ({hidden_states.dtype}) must have the "
                              f"16-bit weights' dtype ({self.w13.dtype})")
         if expert_map is None and self.ep_size > 1:
             expert_map = self.expert_map
         clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
         b13, b2 = self._biases(output.dtype)
+        w13, w2 = self._call_weights(hidden_states.dtype)
         torch.ops._moe_C.mi355_fused_moe(
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
-            topk_ids.contiguous(), self.w13, self.gemm1_wei_scales,
-            b13, self.w2, self.gemm2_wei_scales, b2,
+            topk_ids.contiguous(), w13, self.gemm1_wei_scales,
+            b13, w2, self.gemm2_wei_scales, b2,
             self._recipe, self._act, self.inter_size, clamp, expert_map,
             self._w_layout, a1q_scale)
         return output
