@@ -52,10 +52,16 @@ typedef enum {
                                    type, bf16 or fp16                     */
   MI355MOE_RECIPE_FP8BLOCK = 1, /* e4m3 weights, fp32 128x128 block scales;
                                    activations quantised 1x128 e4m3       */
-  MI355MOE_RECIPE_MXFP4 = 2     /* e2m1 weights packed along K, e8m0 scale
+  MI355MOE_RECIPE_MXFP4 = 2,    /* e2m1 weights packed along K, e8m0 scale
                                    per 32 along K; bf16 or fp16
                                    activations (weights dequantised to
                                    their type)                            */
+  MI355MOE_RECIPE_INT4 = 3      /* signed int4 weights (two's complement,
+                                   the even K value in the low nibble)
+                                   packed along K [E, N, K/2], scales
+                                   [E, N, K/group] in the activations'
+                                   16-bit type, group 32/64/128/256:
+                                   w = T(v * scale) (w4a16)               */
 } mi355moe_recipe;
 
 typedef enum {
@@ -297,6 +303,17 @@ int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
                           int64_t num_experts, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* The int4 (w4a16) path of torch.ops._xpu_C.cutlass_grouped_gemm_interface
+ * (csrc/xpu/grouped_gemm/xe_2/grouped_gemm_xe2_interface.hpp:178, 267-290,
+ * gemm_xe2.hpp:391-471): B [E, N, K/2] two's-complement int4 (the even K value
+ * in the low nibble), b_scale [E, N, K/group_size] in a_dtype (bf16 or
+ * f16), group_size 32/64/128/256; D [M, N] in a_dtype. */
+int mi355moe_grouped_gemm_int4(const void* A, int a_dtype, const void* B,
+                               const void* b_scale, int64_t group_size, const void* bias,
+                               void* D, const int32_t* rows_per_expert, int64_t total_rows,
+                               int64_t N, int64_t K, int64_t num_experts, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------- fused MoE layer */
 
 /* The whole XpuFusedMoe.apply path (vllm_xpu_kernels/fused_moe_interface.py:
@@ -340,6 +357,8 @@ typedef struct {
    * the layer uses them as they are instead of quantising hidden_states
    * itself; act_dtype still names the output's type. */
   const float* hidden_scale;
+  /* recipe INT4: K values per group scale (32, 64, 128 or 256) */
+  int64_t w_group;
 } mi355moe_fused_moe_args;
 
 /* One-time weight preparation, the counterpart of the repacking the

@@ -539,6 +539,21 @@ def dequant_fp8_block_weight(q: torch.Tensor, s: torch.Tensor):
 # ----------------------------------------------------------------------------
 # Grouped GEMM and the fused layer
 # ----------------------------------------------------------------------------
+def dequant_int4(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """[N, K/2] two's-complement int4 (even K value in the low nibble) with
+    16-bit group scales [N, K/group] -> [N, K] fp32 of T(v * scale), T the
+    scales' type (the reference kernel's 16-bit dequantisation,
+    csrc/xpu/grouped_gemm/xe_2/gemm_xe2.hpp:455-470; its test's
+    dequantize_uint4, tests/fused_moe/test_grouped_gemm.py:310-323, is the same
+    value through (u4 - 8) * scale)."""
+    b = q.view(torch.uint8).to(torch.int32)
+    lo = ((b & 0xF) ^ 8) - 8
+    hi = ((b >> 4) ^ 8) - 8
+    v = torch.stack([lo, hi], -1).reshape(q.shape[0], -1).float()
+    g = v.shape[1] // s.shape[1]
+    return (v * s.float().repeat_interleave(g, dim=1)).to(s.dtype).float()
+
+
 def dequant_weight(recipe: str, w_e: torch.Tensor, s_e) -> torch.Tensor:
     """[N, K] fp32 weights of one expert, per recipe
     (vllm_xpu_kernels/moe_utils.py:189-202)."""
@@ -548,6 +563,8 @@ def dequant_weight(recipe: str, w_e: torch.Tensor, s_e) -> torch.Tensor:
         # per-expert scale (moe_utils.py:212-213; gemm_xe2.hpp:192-198 applies
         # it to the accumulators, the same product up to fp32 rounding)
         return w_e.float() * float(s_e)
+    if recipe == "int4":
+        return dequant_int4(w_e, s_e)
     if recipe == "fp8block":
         return dequant_fp8_block_weight(w_e, s_e)
     if recipe == "mxfp4":

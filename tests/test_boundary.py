@@ -149,7 +149,8 @@ def test_fused_moe_workspace_query_and_validation(lib):
                     ("gemm1_clamp_limit", ctypes.c_float), ("swiglu_alpha", ctypes.c_float),
                     ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
                     ("w_layout", ctypes.c_int),
-                    ("hidden_scale", ctypes.c_void_p)]
+                    ("hidden_scale", ctypes.c_void_p),
+                    ("w_group", ctypes.c_int64)]
 
     a = Args(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=64,
              hidden=7168, inter=2048, num_experts=256, topk=8)

@@ -723,6 +723,60 @@ def test_fused_moe_fp8_per_expert(dev, dt, fp8, T, topk):
     torch.testing.assert_close(out.cpu()[toks], ref, rtol=tol, atol=tol)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("grp", [128, 32])
+@pytest.mark.parametrize("has_bias", [False, True])
+def test_grouped_gemm_int4(dev, dt, grp, has_bias):
+    """int4 weights (reference tests/fused_moe/test_grouped_gemm.py:358-420):
+    u4 [E, N, K/2] with zero point 8 converted to two's complement, 16-bit
+    scales [E, N, K/group]; within rtol = atol = 1e-2 of the oracle."""
+    g = torch.Generator().manual_seed(31)
+    E, N, K = 4, 256, 512
+    M = sum(ROWS)
+    a = torch.randn(M, K, generator=g).to(dt)
+    u = torch.randint(0, 0xff, (E, N, K // 2), generator=g).to(torch.uint8)
+    sc = torch.pow(2.0, torch.randint(-3, 4, (E, N, K // grp), generator=g).float()).to(dt)
+    q = (u ^ 0x88).view(torch.int8)
+    bias = (torch.randn(E, N, generator=g) * 100).to(dt) if has_bias else None
+    d = torch.empty(M, N, dtype=dt, device=dev)
+    _ops().cutlass_grouped_gemm(a.to(dev), q.to(dev), sc.to(dev),
+                                None if bias is None else bias.to(dev), d,
+                                torch.tensor(ROWS, dtype=torch.int32, device=dev), N, K, E)
+    ref = O.grouped_gemm("int4", a, q, sc, bias, ROWS, out_dtype=dt)
+    torch.testing.assert_close(d.cpu(), ref, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,topk", [(1, 1), (4, 1), (16, 2), (512, 1), (2048, 2)])
+def test_fused_moe_int4(dev, dt, T, topk):
+    """The reference's int4 layer (tests/fused_moe/test_fused_moe.py:303-420 at
+    H=1024, I=512, 16 experts, group 128): u4 weights with zero point 8, scales
+    2^-5 in the activation type, biases; every element within the reference's
+    bar.  T covers the split-K stream ... 128-slot kernels (int4 is
+    row-major only)."""
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    g = torch.Generator().manual_seed(11 + T)
+    E, H, I, grp = 16, 1024, 512, 128
+    u13 = torch.randint(0, 0xff, (E, 2 * I, H // 2), generator=g).to(torch.uint8)
+    u2 = torch.randint(0, 0xff, (E, H, I // 2), generator=g).to(torch.uint8)
+    s13 = torch.full((E, 2 * I, H // grp), 2.0 ** -5).to(dt)
+    s2 = torch.full((E, H, I // grp), 2.0 ** -5).to(dt)
+    b13 = (torch.randn(E, 2 * I, generator=g) / 16).to(dt)
+    b2 = (torch.randn(E, H, generator=g) / 16).to(dt)
+    x = (torch.randn(T, H, generator=g) / 16).to(dt)
+    tw, ti = torch.topk(torch.randn(T, E, generator=g), k=topk, dim=-1, sorted=False)
+    moe = XpuFusedMoe(u13.to(dev), s13.to(dev), b13.to(dev), u2.to(dev), s2.to(dev), b2.to(dev),
+                      topk, "silu", E)
+    assert moe.recipe == "int4"
+    out = torch.empty(T, H, dtype=dt, device=dev)
+    moe.apply(out, x.to(dev), tw.to(dev), ti.to(dev))
+    toks = torch.linspace(0, T - 1, min(T, 64)).long()
+    ref = O.fused_moe("int4", x[toks], u13 ^ 0x88, s13, b13, u2 ^ 0x88, s2, b2, tw[toks],
+                      ti[toks])
+    tol = 2e-2 if dt == torch.bfloat16 else 1e-2
+    torch.testing.assert_close(out.cpu()[toks], ref, rtol=tol, atol=tol)
+
+
 def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):
     cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C1"], 8, dev)
     with pytest.raises(NotImplementedError, match="fp8 block-scaled recipe"):

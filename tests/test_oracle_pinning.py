@@ -523,6 +523,28 @@ def test_fp8_per_expert_is_the_16bit_layer_on_dequantised_weights():
     assert torch.equal(y, ref)
 
 
+def test_int4_zero_point_conversion_and_dequant():
+    """u4 with zero point 8 -> two's-complement int4 is `byte ^ 0x88` ((u4 -
+    8) mod 16 per nibble, all 256 bytes); the oracle's int4 dequantisation of
+    the converted bytes equals the reference test's (u4 - 8) * scale in the
+    scale's type (tests/fused_moe/test_grouped_gemm.py:310-323)."""
+    b = torch.arange(256, dtype=torch.int32)
+    zp = ((((b & 0xF) - 8) & 0xF) | ((((b >> 4) - 8) & 0xF) << 4))
+    assert torch.equal(zp, b ^ 0x88)
+    g = torch.Generator().manual_seed(13)
+    N, K, grp = 48, 256, 64
+    u = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+    for dt in (torch.bfloat16, torch.float16):
+        s = torch.pow(2.0, torch.randint(-3, 4, (N, K // grp), generator=g).float()).to(dt)
+        nib = torch.stack([u.to(torch.int32) & 0xF, u.to(torch.int32) >> 4], -1).reshape(N, K)
+        ref = ((nib - 8) * s.repeat_interleave(grp, 1)).to(dt).float()
+        assert torch.equal(O.dequant_int4(u ^ 0x88, s), ref)
+    # non-power-of-two scales round the product to the scale's type
+    s = torch.full((N, K // grp), 0.3).bfloat16()
+    v = O.dequant_int4(torch.full((N, K // 2), 0x77, dtype=torch.uint8), s)
+    assert torch.all(v == (7 * s.float()).bfloat16().float()[0, 0])
+
+
 def test_fused_moe_oracle_fp8block_close_to_dequant_fp32():
     """fp8block = dequantised fp32 layer up to activation quantisation noise."""
     torch.manual_seed(8)

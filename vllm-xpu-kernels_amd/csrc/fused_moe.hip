@@ -452,6 +452,14 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     MI_ARG(H % 128 == 0 && I % 128 == 0,
            "fp8 block-scaled weights need hidden and intermediate sizes % 128 == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "fp8 block-scaled weights need scales");
+  } else if (recipe == MI355MOE_RECIPE_INT4) {
+    const int64_t g = a->w_group;
+    MI_ARG(g == 32 || g == 64 || g == 128 || g == 256,
+           "int4 group size must be 32, 64, 128 or 256");
+    MI_ARG(H % g == 0 && act_width(a) % g == 0,
+           "int4 weights need hidden and intermediate sizes % group_size == 0");
+    MI_ARG(a->w13_scale && a->w2_scale, "int4 weights need group scales");
+    MI_ARG(a->w_layout == MI355MOE_WLAYOUT_NK, "int4 weights are row-major only");
   } else if (recipe == MI355MOE_RECIPE_MXFP4) {
     MI_ARG(H % 32 == 0 && I % 32 == 0, "mxfp4 weights need K % 32 == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "mxfp4 weights need e8m0 scales");
@@ -528,6 +536,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.part = L.part1;
   g1.w_kblock = kblock;
   g1.out_f16 = f16;
+  g1.w_group = static_cast<int32_t>(a->w_group);
   g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w13_scale)
                                                     : nullptr;
   if (glu) {
@@ -573,6 +582,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.part = L.part2;
   g2.w_kblock = kblock;
   g2.out_f16 = f16;
+  g2.w_group = static_cast<int32_t>(a->w_group);
   g2.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w2_scale)
                                                     : nullptr;
   // split-K decode: the partial sums are finished by the top-k reduction
@@ -663,13 +673,12 @@ extern "C" size_t mi355moe_grouped_gemm_workspace_size_k(int recipe, int a_dtype
   return gg_plan(recipe, q, total_rows, K, num_experts, nullptr).bytes;
 }
 
-extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
-                                     const float* a_scale, const void* B,
-                                     const void* b_scale, const void* bias,
-                                     void* D, int out_dtype,
-                                     const int32_t* rows_per_expert,
-                                     int64_t M, int64_t N, int64_t K, int64_t E,
-                                     void* ws, size_t ws_bytes, void* stream) {
+namespace {
+int grouped_gemm_impl(int recipe, const void* A, int a_dtype, const float* a_scale,
+                      const void* B, const void* b_scale, int64_t w_group, const void* bias,
+                      void* D, int out_dtype, const int32_t* rows_per_expert, int64_t M,
+                      int64_t N, int64_t K, int64_t E, void* ws, size_t ws_bytes,
+                      void* stream) {
   MI_ARG(M >= 0 && N > 0 && K > 0 && E > 0 && E <= 1024, "invalid GEMM shape");
   MI_ARG(N % 8 == 0, "N must be a multiple of 8");
   MI_ARG(out_dtype == MI355MOE_BF16 || out_dtype == MI355MOE_F16, "output must be 16-bit");
@@ -684,6 +693,14 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
              "activations must be bfloat16, float16 or e4m3");
       need_quant = true;
     }
+  } else if (recipe == MI355MOE_RECIPE_INT4) {
+    MI_ARG(w_group == 32 || w_group == 64 || w_group == 128 || w_group == 256,
+           "int4 group size must be 32, 64, 128 or 256");
+    MI_ARG(K % w_group == 0, "int4 needs K % group_size == 0");
+    MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
+           "int4 activations must be bfloat16 or float16");
+    MI_ARG(out_dtype == a_dtype, "int4: the output must have the activation dtype");
+    MI_ARG(b_scale != nullptr, "int4 needs group scales");
   } else if (recipe == MI355MOE_RECIPE_MXFP4) {
     MI_ARG(K % 32 == 0, "mxfp4 needs K % 32 == 0");
     MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
@@ -733,7 +750,32 @@ extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
   g.ldb_rows = N;
   g.out_f16 = out_dtype == MI355MOE_F16;
   g.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(b_scale) : nullptr;
+  g.w_group = static_cast<int32_t>(w_group);
   return launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g, L.grid_blocks, nullptr, st);
+}
+}  // namespace
+
+extern "C" int mi355moe_grouped_gemm(int recipe, const void* A, int a_dtype,
+                                     const float* a_scale, const void* B,
+                                     const void* b_scale, const void* bias,
+                                     void* D, int out_dtype,
+                                     const int32_t* rows_per_expert,
+                                     int64_t M, int64_t N, int64_t K, int64_t E,
+                                     void* ws, size_t ws_bytes, void* stream) {
+  MI_ARG(recipe != MI355MOE_RECIPE_INT4, "int4 weights: use mi355moe_grouped_gemm_int4");
+  return grouped_gemm_impl(recipe, A, a_dtype, a_scale, B, b_scale, 0, bias, D, out_dtype,
+                           rows_per_expert, M, N, K, E, ws, ws_bytes, stream);
+}
+
+extern "C" int mi355moe_grouped_gemm_int4(const void* A, int a_dtype, const void* B,
+                                          const void* b_scale, int64_t group_size,
+                                          const void* bias, void* D,
+                                          const int32_t* rows_per_expert, int64_t M,
+                                          int64_t N, int64_t K, int64_t E, void* ws,
+                                          size_t ws_bytes, void* stream) {
+  return grouped_gemm_impl(MI355MOE_RECIPE_INT4, A, a_dtype, nullptr, B, b_scale, group_size,
+                           bias, D, a_dtype, rows_per_expert, M, N, K, E, ws, ws_bytes,
+                           stream);
 }
 
 // ------------------------------------------------- K-blocked weight packing

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "common.h"
+#include "moe_gemm.h"
 
 namespace mi355 {
 
@@ -66,6 +67,48 @@ __device__ __forceinline__ uint4 fp4x8_to16(uint32_t w, float sc) {
     r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
   }
   return r;
+}
+
+// 8 signed int4 values (two's-complement nibbles, value t in bits 4t..4t+3)
+// -> 8 16-bit values T(v * scale), the reference's dequantisation
+// (gemm_xe2.hpp:455-470: the 16-bit weight times its 16-bit group scale).
+template <bool F16>
+__device__ __forceinline__ uint4 int4x8_to16(uint32_t w, float sc) {
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = static_cast<float>(static_cast<int32_t>(w << (28 - 8 * i)) >> 28) * sc;
+    const float hi = static_cast<float>(static_cast<int32_t>(w << (24 - 8 * i)) >> 28) * sc;
+    o[i] = st16<F16>(lo) | (static_cast<uint32_t>(st16<F16>(hi)) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// 4-bit weights (recipes MXFP4 and INT4), one 32-value K block (16 bytes) of
+// weight row `wrow` of expert e at a time.  Its scale code: the e8m0 byte
+// (mxfp4, [E, ldb_rows, K/32] or K-blocked) or the bits of the 16-bit group
+// scale (int4, [E, ldb_rows, K/w_group] in the call's 16-bit type).
+template <int RECIPE>
+__device__ __forceinline__ uint32_t w4_scale_code(const GemmArgs& a, int e, int64_t wrow,
+                                                  int64_t blk32, const WStride& sst) {
+  if constexpr (RECIPE == MI355MOE_RECIPE_INT4) {
+    const int64_t groups = a.K / a.w_group;
+    return static_cast<const uint16_t*>(a.b_scale)
+        [(static_cast<int64_t>(e) * a.ldb_rows + wrow) * groups + (blk32 * 32) / a.w_group];
+  } else {
+    return static_cast<const uint8_t*>(a.b_scale)
+        [static_cast<int64_t>(e) * a.ldb_rows * (a.K / 32) + wrow * sst.row + blk32 * sst.kblk];
+  }
+}
+// 8 values of a block word under its scale code (mxfp4: code 0 -> 0, as the
+// reference's kernel maps e8m0 0, gemm_xe2.hpp:411-418).
+template <int RECIPE, bool F16>
+__device__ __forceinline__ uint4 w4_decode8(uint32_t w, uint32_t code) {
+  if constexpr (RECIPE == MI355MOE_RECIPE_INT4) {
+    return int4x8_to16<F16>(w, ld16<F16>(static_cast<uint16_t>(code)));
+  } else {
+    return fp4x8_to16<F16>(code ? w : 0u, __uint_as_float(code << 23));
+  }
 }
 
 // GLU activations of the w13 epilogue: SiLU-and-mul rounds silu(g) to the

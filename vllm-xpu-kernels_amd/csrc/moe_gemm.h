@@ -57,6 +57,7 @@ struct GemmArgs {
   // before the bias (per-expert-scaled fp8 weights, converted exactly to the
   // 16-bit type: D = T(s_e * sum_k A W_e + bias_e)).
   const float* expert_scale;
+  int32_t w_group;       // recipe INT4: K values per 16-bit scale (32..256)
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };

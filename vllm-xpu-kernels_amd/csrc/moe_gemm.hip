@@ -51,7 +51,7 @@ template <int RECIPE, int BM, int BN, int EPI, bool QOUT, bool F16>
 __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
                                                        void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
-  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4;
+  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
   constexpr int XB = kFp8 ? 1 : 2;      // bytes per activation element
   constexpr int ROWB = KB * XB + 16;    // padded LDS row pitch (bytes)
   constexpr int CPR = KB * XB / 16;     // 16-byte chunks per staged row
@@ -125,16 +125,11 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
         const int64_t blk32 = (k0 + 32 * q) / 32;  // the lane's 32-value K block
         uint4 v = ok ? *reinterpret_cast<const uint4*>(wptr[j] + blk32 * wst.kblk)
                      : make_uint4(0, 0, 0, 0);
-        const uint8_t* bs = static_cast<const uint8_t*>(a.b_scale);
-        uint32_t ex = ok ? bs[static_cast<int64_t>(e) * a.ldb_rows * (K / 32) +
-                              wrow[j] * sst.row + blk32 * sst.kblk]
-                         : 0u;
-        if (ex == 0u) v = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> scale 0
-        const float sc = __uint_as_float(ex << 23);
-        wf[0][j][0] = fp4x8_to16<F16>(v.x, sc);
-        wf[1][j][0] = fp4x8_to16<F16>(v.y, sc);
-        wf[2][j][0] = fp4x8_to16<F16>(v.z, sc);
-        wf[3][j][0] = fp4x8_to16<F16>(v.w, sc);
+        const uint32_t code = ok ? w4_scale_code<RECIPE>(a, e, wrow[j], blk32, sst) : 0u;
+        wf[0][j][0] = w4_decode8<RECIPE, F16>(v.x, code);
+        wf[1][j][0] = w4_decode8<RECIPE, F16>(v.y, code);
+        wf[2][j][0] = w4_decode8<RECIPE, F16>(v.z, code);
+        wf[3][j][0] = w4_decode8<RECIPE, F16>(v.w, code);
       } else {
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
@@ -356,7 +351,7 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     else if (avg <= 12) t = TILE_SMALL, b = 16;
     else if (avg > 160 && wide_ok) t = TILE_WIDE, b = kWideBM;
     else t = TILE_BIG, b = 128;
-  } else if (recipe == MI355MOE_RECIPE_MXFP4) {
+  } else if (recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4) {
     if (avg <= 2) t = TILE_STREAM, b = 16;
     else if (avg <= 24) t = TILE_SMALL, b = 16;
     else if (avg <= 40 || (!wide_ok && avg <= 48)) t = TILE_SMALL, b = 32;
@@ -427,6 +422,7 @@ int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,
     case MI355MOE_RECIPE_BF16: MI_EPI(MI355MOE_RECIPE_BF16)
     case MI355MOE_RECIPE_FP8BLOCK: MI_EPI(MI355MOE_RECIPE_FP8BLOCK)
     case MI355MOE_RECIPE_MXFP4: MI_EPI(MI355MOE_RECIPE_MXFP4)
+    case MI355MOE_RECIPE_INT4: MI_EPI(MI355MOE_RECIPE_INT4)
     default: return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
   }
 #undef MI_EPI

@@ -47,7 +47,7 @@ template <int RECIPE, int EPI, bool QOUT, bool F16>
 __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
-  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4;
+  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int KE = kFp8 ? 128 : 64;        // K elements per stage
   // per-thread staging: activations, then weights
@@ -100,8 +100,6 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
   // are row-major)
   const WStride wst = kFp4 ? w_stride4(a) : WStride{wrow_bytes, 0};
   const WStride sst = s_stride4(a);
-  const uint8_t* const sexp = static_cast<const uint8_t*>(a.b_scale) +
-                              (kFp4 ? static_cast<int64_t>(e) * a.ldb_rows * (K / 32) : 0);
   const uint8_t* wsrc[NW];
   bool wokv[NW];
   int64_t wrowv[NW];
@@ -137,7 +135,7 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
         const bool ok = wokv[i] && 32 * c < kb;
         rw[i] = ok ? *reinterpret_cast<const uint4*>(wsrc[i] + (k0 / 32) * wst.kblk)
                    : make_uint4(0, 0, 0, 0);
-        rsc[i] = ok ? sexp[wrowv[i] * sst.row + (k0 / 32 + c) * sst.kblk] : 0u;
+        rsc[i] = ok ? w4_scale_code<RECIPE>(a, e, wrowv[i], k0 / 32 + c, sst) : 0u;
       } else {
         const int c = idx % (ROWB / 16);
         const bool ok = wokv[i] && (c * 16) < kb * (kFp8 ? 1 : 2);
@@ -158,14 +156,12 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
       const int idx = i * 256 + tid;
       if constexpr (kFp4) {
         const int r = idx / 2, c = idx % 2;
-        uint4 v = rw[i];
-        if (rsc[i] == 0u) v = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> 0
-        const float sc = __uint_as_float(rsc[i] << 23);
+        const uint4 v = rw[i];
         uint8_t* d = &sW[buf][r * PITCH + c * 64];
-        *reinterpret_cast<uint4*>(d) = fp4x8_to16<F16>(v.x, sc);
-        *reinterpret_cast<uint4*>(d + 16) = fp4x8_to16<F16>(v.y, sc);
-        *reinterpret_cast<uint4*>(d + 32) = fp4x8_to16<F16>(v.z, sc);
-        *reinterpret_cast<uint4*>(d + 48) = fp4x8_to16<F16>(v.w, sc);
+        *reinterpret_cast<uint4*>(d) = w4_decode8<RECIPE, F16>(v.x, rsc[i]);
+        *reinterpret_cast<uint4*>(d + 16) = w4_decode8<RECIPE, F16>(v.y, rsc[i]);
+        *reinterpret_cast<uint4*>(d + 32) = w4_decode8<RECIPE, F16>(v.z, rsc[i]);
+        *reinterpret_cast<uint4*>(d + 48) = w4_decode8<RECIPE, F16>(v.w, rsc[i]);
       } else {
         const int r = idx / (ROWB / 16), c = idx % (ROWB / 16);
         *reinterpret_cast<uint4*>(&sW[buf][r * PITCH + c * 16]) = rw[i];
@@ -307,6 +303,9 @@ int launch_moe_gemm_big(int recipe, int epi, bool qout, const GemmArgs& a,
     case MI355MOE_RECIPE_MXFP4:
       return epi == EPI_GLU ? launch_big<MI355MOE_RECIPE_MXFP4, EPI_GLU, false>(a, max_blocks, qs, st)
                             : launch_big<MI355MOE_RECIPE_MXFP4, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_INT4:
+      return epi == EPI_GLU ? launch_big<MI355MOE_RECIPE_INT4, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_big<MI355MOE_RECIPE_INT4, EPI_STORE, false>(a, max_blocks, qs, st);
     default:
       return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
   }

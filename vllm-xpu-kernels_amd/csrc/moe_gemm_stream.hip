@@ -50,15 +50,17 @@ struct Frag<MI355MOE_RECIPE_BF16> {      // 4 MFMA steps x 8 bf16
 template <>
 struct Frag<MI355MOE_RECIPE_MXFP4> {     // 32 e2m1 + e8m0 of the weight row
   uint4 w[2];
-  uint32_t sc[2];
+  uint32_t sc[2];                        // scale codes (w4_scale_code)
   uint4 x[4];
 };
+template <>
+struct Frag<MI355MOE_RECIPE_INT4> : Frag<MI355MOE_RECIPE_MXFP4> {};  // 32 int4 + scale
 
 template <int RECIPE, int EPI, bool QOUT, int PD, bool F16>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
-  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4;
+  constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int XB = kFp8 ? 1 : 2;
 
@@ -133,8 +135,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         f.w[t] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + (kc / 32) * wst.kblk);
-        f.sc[t] = static_cast<const uint8_t*>(a.b_scale)
-            [static_cast<int64_t>(e) * a.ldb_rows * (K / 32) + wrow[t] * sst.row + (kc / 32) * sst.kblk];
+        f.sc[t] = w4_scale_code<RECIPE>(a, e, wrow[t], kc / 32, sst);
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) f.x[s] = *reinterpret_cast<const uint4*>(xp + (kc + 8 * s) * 2);
@@ -179,13 +180,12 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     } else if constexpr (kFp4) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        uint4 w = f.w[t];
-        if (f.sc[t] == 0u) w = make_uint4(0, 0, 0, 0);  // e8m0 code 0 -> 0
-        const float sc = __uint_as_float(f.sc[t] << 23);
-        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.x, sc), f.x[0], acc[t]);
-        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.y, sc), f.x[1], acc[t]);
-        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.z, sc), f.x[2], acc[t]);
-        acc[t] = mfma16_16x16x32<F16>(fp4x8_to16<F16>(w.w, sc), f.x[3], acc[t]);
+        const uint4 w = f.w[t];
+        const uint32_t c = f.sc[t];
+        acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.x, c), f.x[0], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.y, c), f.x[1], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.z, c), f.x[2], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.w, c), f.x[3], acc[t]);
       }
     } else {
 #pragma unroll
@@ -378,6 +378,9 @@ int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
     case MI355MOE_RECIPE_MXFP4:
       return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_MXFP4, EPI_GLU, false>(a, max_blocks, qs, st)
                             : launch_stream<MI355MOE_RECIPE_MXFP4, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_INT4:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_INT4, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_INT4, EPI_STORE, false>(a, max_blocks, qs, st);
     default:
       return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
   }

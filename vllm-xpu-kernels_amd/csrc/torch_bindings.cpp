@@ -543,6 +543,34 @@ at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
   int recipe = MI355MOE_RECIPE_BF16;
   at::Tensor B = ptr_B;
   at::Tensor expert_scale;
+  // int4 (reference grouped_gemm_xe2_interface.hpp:178, 267-290): int8 B
+  // [E, N, K/2] of two's-complement nibbles, 16-bit scales [E, N, K/group]
+  if (bdt == at::kChar && ptr_B_scale.has_value()) {
+    TORCH_CHECK(ptr_B_scale->dim() == 3, "ptr_scales of int4 must be 3D [num_experts, N, group_num]");
+    TORCH_CHECK(ptr_B_scale->size(0) == num_experts, "ptr_scales.size(0) of int4 must match num_experts");
+    TORCH_CHECK(ptr_B_scale->size(1) == N, "ptr_scales.size(1) of int4 must match N");
+    TORCH_CHECK(K % ptr_B_scale->size(2) == 0, "ptr_scales.size(2) of int4 must divide K");
+    TORCH_CHECK(ptr_B_scale->scalar_type() == ptr_A.scalar_type(),
+                "int4 scales must have the activation dtype");
+    TORCH_CHECK(ptr_B.size(1) == N && ptr_B.size(2) * 2 == K,
+                "ptr_B logical N dimension must match ptr_D N dimension and N");
+    TORCH_CHECK(ptr_A.size(1) == K, "ptr_A K dimension must match ptr_B logical K dimension and K");
+    TORCH_CHECK(ptr_D.scalar_type() == ptr_A.scalar_type(), "ptr_D must have the activation dtype");
+    const int64_t M = ptr_A.size(0);
+    const int adt = dtype_code(ptr_A.scalar_type());
+    const size_t ws_bytes = mi355moe_grouped_gemm_workspace_size_k(MI355MOE_RECIPE_INT4, adt, M, K,
+                                                                   num_experts);
+    auto ws = at::empty({static_cast<int64_t>(ws_bytes)}, ptr_A.options().dtype(at::kByte));
+    const auto scales = ptr_B_scale->contiguous();
+    DevGuard g(ptr_A.device());
+    check_rc(mi355moe_grouped_gemm_int4(ptr_A.data_ptr(), adt, ptr_B.data_ptr(), scales.data_ptr(),
+                                        K / ptr_B_scale->size(2), opt_ptr(ptr_bias),
+                                        ptr_D.data_ptr(), rows_per_expert.data_ptr<int32_t>(), M,
+                                        N, K, num_experts, ws.data_ptr(), ws_bytes,
+                                        cur_stream(ptr_A)),
+             "cutlass_grouped_gemm_interface");
+    return ptr_D;
+  }
   if (is_fp8_expert) {
     TORCH_CHECK(ptr_A.scalar_type() == at::kBFloat16 || ptr_A.scalar_type() == at::kHalf,
                 "per-expert fp8 weights need bfloat16 or float16 activations");
@@ -618,7 +646,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
                      const std::optional<at::Tensor>& w2_bias, int64_t recipe,
                      int64_t activation, int64_t inter_size, double clamp_limit,
                      const std::optional<at::Tensor>& expert_map, int64_t w_layout,
-                     const std::optional<at::Tensor>& hidden_scale) {
+                     const std::optional<at::Tensor>& hidden_scale, int64_t w_group) {
   check_gpu(output, "output");
   check_gpu(hidden_states, "hidden_states");
   if (hidden_scale) {
@@ -663,6 +691,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.output = output.data_ptr();
   a.w_layout = static_cast<int>(w_layout);
   a.hidden_scale = hidden_scale ? hidden_scale->data_ptr<float>() : nullptr;
+  a.w_group = w_group;
   for (const auto* b : {&w13_bias, &w2_bias})
     if (b->has_value())
       TORCH_CHECK((*b)->scalar_type() == output.scalar_type(),
@@ -736,7 +765,7 @@ TORCH_LIBRARY(_moe_C, m) {
         "Tensor topk_ids, Tensor w13, Tensor? w13_scale, Tensor? w13_bias, Tensor w2, "
         "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
         "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0, "
-        "Tensor? hidden_scale=None) -> ()");
+        "Tensor? hidden_scale=None, int w_group=0) -> ()");
   m.def("mi355_pack_weights_kblock(Tensor src, Tensor! dst) -> ()");
   m.def("mi355_pack_scales_kblock(Tensor src, Tensor! dst) -> ()");
 }

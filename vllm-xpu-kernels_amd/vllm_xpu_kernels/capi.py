@@ -33,7 +33,8 @@ class FusedMoeArgs(ctypes.Structure):
                 ("swiglu_alpha", ctypes.c_float),
                 ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
                 ("w_layout", ctypes.c_int),
-                ("hidden_scale", ctypes.c_void_p)]
+                ("hidden_scale", ctypes.c_void_p),
+                ("w_group", ctypes.c_int64)]
 
 
 lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t
@@ -68,6 +69,7 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.act_dtype = F16 if output.dtype == torch.float16 else BF16
     b13, b2 = moe._biases(output.dtype)
     w13, w2 = moe._call_weights(hidden_states.dtype)
+    s13, s2 = moe._scales(hidden_states.dtype)
     a.ids_dtype = I64 if topk_ids.dtype == torch.int64 else I32
     a.num_tokens, a.hidden = hidden_states.shape
     a.inter = moe.inter_size
@@ -79,18 +81,17 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.expert_map = expert_map.data_ptr() if expert_map is not None else None
     a.expert_map_len = expert_map.numel() if expert_map is not None else 0
     a.w13 = w13.data_ptr()
-    a.w13_scale = (moe.gemm1_wei_scales.data_ptr()
-                   if moe.gemm1_wei_scales is not None else None)
+    a.w13_scale = s13.data_ptr() if s13 is not None else None
     a.w13_bias = b13.data_ptr() if b13 is not None else None
     a.w2 = w2.data_ptr()
-    a.w2_scale = (moe.gemm2_wei_scales.data_ptr()
-                  if moe.gemm2_wei_scales is not None else None)
+    a.w2_scale = s2.data_ptr() if s2 is not None else None
     a.w2_bias = b2.data_ptr() if b2 is not None else None
     a.gemm1_clamp_limit = float(moe.gemm1_clamp_limit or 0.0)
     a.swiglu_alpha = 1.702
     a.swiglu_limit = 7.0
     a.output = output.data_ptr()
     a.w_layout = moe._w_layout
+    a.w_group = moe._w_group
     return a
 
 

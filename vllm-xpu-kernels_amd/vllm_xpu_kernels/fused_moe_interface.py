@@ -26,7 +26,7 @@ from . import _ops  # noqa: F401  (loads the HIP library)
 REF_FUSED_MOE_ENV = "VLLM_XPU_FUSED_MOE_USE_REF"
 FP8_BLOCK_SIZE = 128
 
-RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4 = 0, 1, 2
+RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4, RECIPE_INT4 = 0, 1, 2, 3
 ACT_SILU, ACT_SWIGLUOAI, ACT_GELU, ACT_GELU_TANH, ACT_SWIGLUSTEP, ACT_RELU2 = range(6)
 # reference fused_moe_interface.py:119-133, 239-254
 _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
@@ -122,10 +122,10 @@ class XpuFusedMoe:
         assert w13.is_contiguous() and w2.is_contiguous()
         (is_fp8, is_int4, is_mxfp4, is_mxfp8,
          is_block_fp8) = _get_weights_dtype(w13, w13_scales)
-        if is_int4 or is_mxfp8:
+        if is_mxfp8:
             raise NotImplementedError(
-                "recipes int4 and mxfp8 are not implemented on MI355X yet; use "
-                "bf16/fp16, fp8 (per-expert or 128x128 block scales) or mxfp4")
+                "recipe mxfp8 is not implemented on MI355X (the reference has no "
+                "kernel for it either); use bf16/fp16, fp8, int4 or mxfp4")
         self.inter_size = _get_inter_size(w13, w13_scales, is_int4, is_mxfp4,
                                           is_block_fp8)
         self.n_experts_per_token = n_experts_per_token
@@ -158,6 +158,9 @@ class XpuFusedMoe:
         elif is_fp8:
             self.recipe = "fp8"
             self._recipe = RECIPE_BF16
+        elif is_int4:
+            self.recipe = "int4"
+            self._recipe = RECIPE_INT4
         elif is_mxfp4:
             self.recipe = "mxfp4"
             self._recipe = RECIPE_MXFP4
@@ -188,7 +191,19 @@ class XpuFusedMoe:
         K2 = I * self.inter_size_scale
         E = w13.shape[0]
         swiglu = self._act == ACT_SWIGLUOAI
-        if self._fp8_expert:
+        self._w_group = 0
+        if self._recipe == RECIPE_INT4:
+            # u4 with zero point 8 -> two's-complement int4 (the reference's
+            # implement_zp, :135-163, is (u4 - 8) & 0xF = u4 ^ 8 per nibble);
+            # weights the reference already converted carry `xpu_fused_moe`
+            w13c, w2c = w13.view(torch.uint8), w2.view(torch.uint8)
+            if not getattr(w13, "xpu_fused_moe", False):
+                w13c, w2c = w13c ^ 0x88, w2c ^ 0x88
+            s13c, s2c = s13.contiguous(), s2.contiguous()
+            self._w_group = (w13c.shape[2] * 2) // s13c.shape[-1]
+            if (K2 // s2c.shape[-1]) != self._w_group:
+                raise ValueError("w13 and w2 int4 scales must use one group size")
+        elif self._fp8_expert:
             # reference layout [E, K, N] (as 16-bit) -> [E, N, K], kept in fp8
             w13c = w13.transpose(1, 2).contiguous()
             w2c = w2.transpose(1, 2).contiguous()
@@ -227,7 +242,7 @@ class XpuFusedMoe:
         assert w13c.shape[0] == E and w13c.shape[1] == 2 * I
         H = w13c.shape[2]
         self._w_layout = WLAYOUT_NK
-        if self._recipe == RECIPE_MXFP4:
+        if self._recipe in (RECIPE_MXFP4, RECIPE_INT4):
             H = w13c.shape[2] * 2
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
                   (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and K2 <= 8192) or
@@ -258,6 +273,16 @@ class XpuFusedMoe:
                 w13, w2 = pack_weights_kblock(w13), pack_weights_kblock(w2)
             self._w16_cache[dtype] = (w13.contiguous(), w2.contiguous())
         return self._w16_cache[dtype]
+
+    def _scales(self, dtype):
+        """int4 group scales in the call's 16-bit type."""
+        s13, s2 = self.gemm1_wei_scales, self.gemm2_wei_scales
+        if self._recipe != RECIPE_INT4 or s13.dtype == dtype:
+            return s13, s2
+        key = ("scales", dtype)
+        if key not in self._bias_cache:
+            self._bias_cache[key] = (s13.to(dtype).contiguous(), s2.to(dtype).contiguous())
+        return self._bias_cache[key]
 
     def _biases(self, dtype):
         """Biases in the call's 16-bit type (the kernels read them as such)."""
@@ -291,12 +316,12 @@ class XpuFusedMoe:
         clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
         b13, b2 = self._biases(output.dtype)
         w13, w2 = self._call_weights(hidden_states.dtype)
+        s13, s2 = self._scales(hidden_states.dtype)
         torch.ops._moe_C.mi355_fused_moe(
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
-            topk_ids.contiguous(), w13, self.gemm1_wei_scales,
-            b13, w2, self.gemm2_wei_scales, b2,
+            topk_ids.contiguous(), w13, s13, b13, w2, s2, b2,
             self._recipe, self._act, self.inter_size, clamp, expert_map,
-            self._w_layout, a1q_scale)
+            self._w_layout, a1q_scale, self._w_group)
         return output
 
 
