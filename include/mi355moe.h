@@ -113,6 +113,22 @@ int mi355moe_topk_sigmoid(float* topk_weights, void* topk_indices,
                           int64_t topk, int renormalize, const float* bias,
                           float routed_scaling_factor, void* stream);
 
+/* Replaces torch.ops._moe_C.topk_softplus_sqrt (csrc/moe/torch_bindings.cpp:
+ * 70-76, csrc/moe/topk_softplus_sqrt_kernels.cpp:225-416, 596-772).  Scores
+ * sqrt(softplus(x)) in fp32 (softplus(x) = x above 20, else log(1 + e^x));
+ * top-k of score + correction_bias (ties to the lower id), each weight the
+ * chosen (score + bias) - bias; weights times routed_scaling_factor, divided
+ * by their sum when renormalize.  With tid2eid (and input_ids, both of the
+ * indices' dtype) the experts are tid2eid[input_ids[t] * topk + j] and the
+ * weights their scores (non-finite -> 0).  num_experts one of 1..512 (powers
+ * of two), 192, 320, 384, 448, 576. */
+int mi355moe_topk_softplus_sqrt(float* topk_weights, void* topk_indices, int indices_dtype,
+                                int32_t* token_expert_indices, const void* gating_output,
+                                int gating_dtype, int64_t num_tokens, int64_t num_experts,
+                                int64_t topk, int renormalize, float routed_scaling_factor,
+                                const float* correction_bias, const void* input_ids,
+                                const void* tid2eid, void* stream);
+
 /* Replaces torch.ops._moe_C.grouped_topk (csrc/moe/torch_bindings.cpp:53-57,
  * csrc/moe/grouped_topk.cpp:782-876).  scores / scores_with_bias [T,E] in
  * `dtype` (f32/bf16/f16) -> values [T,k] (same dtype), ids i32 [T,k]. */

@@ -98,6 +98,36 @@ def topk_sigmoid(gating: torch.Tensor, topk: int, renormalize: bool,
     return w.float(), ids.int(), tei
 
 
+def topk_softplus_sqrt(gating: torch.Tensor, topk: int, renormalize: bool,
+                       routed_scaling_factor: float = 1.0,
+                       correction_bias: Optional[torch.Tensor] = None,
+                       input_ids: Optional[torch.Tensor] = None,
+                       tid2eid: Optional[torch.Tensor] = None):
+    """csrc/moe/topk_softplus_sqrt_kernels.cpp:233-416: s = sqrt(x if x > 20
+    else log(1 + exp(x))) in fp32; top-k of s + bias (value desc, id asc),
+    weight (s + b) - b; hash: ids tid2eid[input_ids[t]], weights s (non-finite
+    -> 0); scale = rsf / (sum if renormalize and sum > 0, else 1 when
+    renormalize), weights * scale.  Returns (weights f32, ids i64)."""
+    x = gating.float()
+    s = torch.sqrt(torch.where(x > 20, x, torch.log(1.0 + torch.exp(x))))
+    T, E = s.shape
+    if tid2eid is not None:
+        ids = tid2eid.long()[input_ids.long()][:, :topk]
+        w = s.gather(1, ids.clamp(0, E - 1))
+        w = torch.where(torch.isfinite(w) & (ids >= 0) & (ids < E), w, torch.zeros_like(w))
+    else:
+        sel = s + correction_bias.float().unsqueeze(0) if correction_bias is not None else s
+        _, ids = _stable_topk_desc(sel, topk)
+        w = sel.gather(1, ids)
+        if correction_bias is not None:
+            w = w - correction_bias.float()[ids]
+    scale = torch.full((T, 1), float(routed_scaling_factor))
+    if renormalize:
+        tot = w.sum(-1, keepdim=True)
+        scale = scale / torch.where(tot > 0, tot, torch.ones_like(tot))
+    return w * scale, ids
+
+
 def grouped_topk(scores: torch.Tensor, scores_with_bias: torch.Tensor,
                  n_group: int, topk_group: int, topk: int, renormalize: bool,
                  routed_scaling_factor: float):

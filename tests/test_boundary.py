@@ -114,6 +114,15 @@ def test_version_and_error_plumbing(lib):
         None, None, 1, None, ctypes.c_int64(2), ctypes.c_int64(1), ctypes.c_int64(4),
         ctypes.c_int64(128), ctypes.c_int64(64), ctypes.c_float(1e-10), None),
      b"MXFP4 requires group_size == 32"),
+    (lambda L: L.mi355moe_topk_softplus_sqrt(None, None, 3, None, None, 0, ctypes.c_int64(4),
+                                             ctypes.c_int64(100), ctypes.c_int64(8), 1,
+                                             ctypes.c_float(1.0), None, None, None, None),
+     b"Unsupported expert number"),
+    (lambda L: L.mi355moe_topk_softplus_sqrt(None, None, 3, None, None, 0, ctypes.c_int64(4),
+                                             ctypes.c_int64(256), ctypes.c_int64(8), 1,
+                                             ctypes.c_float(1.0), None, None,
+                                             ctypes.c_void_p(64), None),
+     b"input_ids is required for hash MoE"),
     (lambda L: L.mi355moe_gelu_and_mul(None, None, 3, ctypes.c_int64(2), ctypes.c_int64(8), None),
      b"gelu_and_mul: unsupported dtype"),
     (lambda L: L.mi355moe_swiglustep_and_mul(None, None, 4, ctypes.c_int64(2), ctypes.c_int64(8),
@@ -192,6 +201,7 @@ REFERENCE_SCHEMAS = {
     "_moe_C::moe_align_block_size": "moe_align_block_size(Tensor topk_ids, int num_experts, int block_size, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, Tensor? maybe_expert_map) -> ()",
     "_moe_C::topk_softmax": "topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias) -> ()",
     "_moe_C::topk_sigmoid": "topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias, float routed_scaling_factor) -> ()",
+    "_moe_C::topk_softplus_sqrt": "topk_softplus_sqrt(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, float routed_scaling_factor, Tensor? correction_bias=None, Tensor? input_ids=None, Tensor? tid2eid=None) -> ()",
     "_moe_C::grouped_topk": "grouped_topk(Tensor scores, Tensor scores_with_bias, int n_group, int topk_group, int topk, bool renormalize, float routed_scaling_factor) -> (Tensor, Tensor)",
     "_moe_C::moe_gather": "moe_gather(Tensor! output, Tensor moe_output, Tensor topk_weights, Tensor unpermuted_row_to_permuted_row, int num_experts) -> ()",
     "_moe_C::init_expert_map": "init_expert_map(Tensor expert_map, int num_experts, int ep_rank, int ep_size) -> ()",

@@ -48,6 +48,59 @@ def test_topk_sigmoid(dev, T, E, renorm, rsf, dtype):
     torch.testing.assert_close(w.cpu(), rw, rtol=2e-6, atol=1e-7)
 
 
+# reference tests/test_topk_softplus_sqrt.py:250-349 parameter grid
+@pytest.mark.parametrize("T", [1, 33, 128])
+@pytest.mark.parametrize("E", [128, 256, 384, 512])
+@pytest.mark.parametrize("k", [6, 8, 16])
+@pytest.mark.parametrize("renorm,rsf", [(True, 1.0), (False, 1.5), (True, 1.5)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_topk_softplus_sqrt(dev, T, E, k, renorm, rsf, dtype):
+    """With a correction bias (biased selection, (s + b) - b weights): the
+    same experts per row as the oracle (the reference test's criterion,
+    sorted ids), weights matched by expert within fp32 ulps of exp / log /
+    sqrt, and the same order in at least 95 % of rows (scores an ulp apart
+    may swap places, as they may between the reference kernel and torch)."""
+    g = torch.Generator().manual_seed(T * 7 + E + k)
+    logits = torch.randn(T, E, generator=g).to(dtype)
+    bias = torch.randn(E, generator=g) * 0.1
+    w, ids = _ops().topk_softplus_sqrt(logits.to(dev), k, renorm, rsf, bias.to(dev))
+    rw, rids = O.topk_softplus_sqrt(logits, k, renorm, rsf, bias)
+    gi, gw = ids.cpu().long(), w.cpu()
+    assert torch.equal(gi.sort(-1).values, rids.sort(-1).values)
+    assert (gi == rids).all(-1).float().mean().item() >= 0.95
+    torch.testing.assert_close(gw.gather(1, gi.argsort(1)), rw.gather(1, rids.argsort(1)),
+                               rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("T", [1, 33, 1024])
+@pytest.mark.parametrize("E", [256, 576])
+@pytest.mark.parametrize("k", [6, 16])
+@pytest.mark.parametrize("idt", [torch.int32, torch.int64])
+def test_topk_softplus_sqrt_hash(dev, T, E, k, idt):
+    """Hash routing: experts tid2eid[input_ids[t]] (of the indices' dtype),
+    weights their sqrt(softplus) scores, renormalised and scaled by 2.5."""
+    g = torch.Generator().manual_seed(T + E + k)
+    logits = torch.randn(T, E, generator=g)
+    tab = torch.randint(0, E, (4096, k), generator=g).to(idt)
+    tok = torch.randint(0, 4096, (T,), generator=g).to(idt)
+    w = torch.empty(T, k, device=dev)
+    ids = torch.empty(T, k, dtype=idt, device=dev)
+    src = torch.empty(T, k, dtype=torch.int32, device=dev)
+    torch.ops._moe_C.topk_softplus_sqrt(w, ids, src, logits.to(dev), True, 2.5, None,
+                                        tok.to(dev), tab.to(dev))
+    rw, rids = O.topk_softplus_sqrt(logits, k, True, 2.5, None, tok, tab)
+    assert torch.equal(ids.cpu().long(), rids)
+    torch.testing.assert_close(w.cpu(), rw, rtol=2e-6, atol=1e-7)
+    assert torch.equal(src.cpu(), (torch.arange(k).view(1, k) * T + torch.arange(T).view(T, 1))
+                       .int())
+
+
+def test_topk_softplus_sqrt_rejects_unsupported_expert_count(dev):
+    x = torch.randn(4, 100, device=dev)
+    with pytest.raises(RuntimeError, match="Unsupported expert number"):
+        _ops().topk_softplus_sqrt(x, 4, True)
+
+
 def test_topk_softmax_int64_ids_and_ties(dev):
     logits = torch.tensor([[1.0, 3.0, 3.0, 0.0, 3.0, -1.0, 3.0, 2.0]])
     w, ids, _ = _ops().topk_softmax(logits.to(dev), 3, False,

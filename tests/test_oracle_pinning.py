@@ -74,6 +74,37 @@ def _grouped_brute(s, sb, n_group, topk_group, k):
     return [-c[1] for c in cand[:k]]
 
 
+def test_topk_softplus_sqrt_vs_reference_test_oracle():
+    """Against the reference test's torch oracle
+    (tests/test_topk_softplus_sqrt.py:19-47: F.softplus(x).sqrt(), topk of the
+    biased scores, weights the unbiased scores): same ids, weights within an
+    ulp-level tolerance (the kernel reports (s + b) - b, the test oracle s);
+    closed forms of the softplus branches; hash routing."""
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(14)
+    T, E, k = 33, 256, 8
+    x = torch.randn(T, E, generator=g)
+    b = torch.randn(E, generator=g) * 0.1
+    w, ids = O.topk_softplus_sqrt(x, k, True, 1.5, b)
+    s = F.softplus(x).sqrt()
+    rid = torch.topk(s + b, k, dim=-1, sorted=True)[1]
+    rw = s.gather(1, rid)
+    rw = rw / rw.sum(-1, keepdim=True) * 1.5
+    assert torch.equal(ids, rid)
+    torch.testing.assert_close(w, rw, rtol=1e-5, atol=1e-6)
+    one = torch.tensor([[25.0, 0.0, -30.0]])
+    w1, i1 = O.topk_softplus_sqrt(one, 3, False, 1.0)
+    assert i1.tolist() == [[0, 1, 2]]
+    assert w1[0, 0].item() == 5.0 and w1[0, 2].item() == 0.0     # log(1 + e^-30) = 0 in fp32
+    assert w1[0, 1].item() == pytest.approx(math.sqrt(math.log(2.0)), rel=1e-6)
+    ids_tab = torch.randint(0, E, (50, k), generator=g)
+    tok = torch.randint(0, 50, (T,), generator=g)
+    wh, ih = O.topk_softplus_sqrt(x, k, True, 2.5, None, tok, ids_tab)
+    assert torch.equal(ih, ids_tab[tok])
+    rh = s.gather(1, ids_tab[tok])
+    torch.testing.assert_close(wh, rh / rh.sum(-1, keepdim=True) * 2.5, rtol=1e-5, atol=1e-6)
+
+
 def test_grouped_topk_brute_force():
     torch.manual_seed(1)
     T, E, n_group, topk_group, k = 16, 64, 8, 4, 6

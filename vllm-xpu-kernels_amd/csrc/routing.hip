@@ -50,17 +50,61 @@ __device__ __forceinline__ void wave_argmax(float& v, float& aux, int& idx) {
   }
 }
 
+enum GateMode { GATE_SOFTMAX = 0, GATE_SIGMOID = 1, GATE_SOFTPLUS_SQRT = 2 };
+
+// sqrt(softplus(x)) in fp32, softplus(x) = x above 20, else log(1 + e^x)
+// (reference csrc/moe/topk_softplus_sqrt_kernels.cpp:233-262, 300-310)
+__device__ __forceinline__ float softplus_sqrt(float x) {
+  return sqrtf(x > 20.f ? x : logf(1.f + expf(x)));
+}
+
+__device__ __forceinline__ int64_t load_id(const void* p, int dt, int64_t i) {
+  if (dt == MI355MOE_I64) return static_cast<const int64_t*>(p)[i];
+  if (dt == MI355MOE_U32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const int32_t*>(p)[i];
+}
+
 // Lane l holds experts e = i*64 + l, i < VPT (coalesced loads).
-template <typename In, int VPT, bool SIGMOID>
+template <typename In, int VPT, int MODE>
 __global__ __launch_bounds__(256) void topk_gating_kernel(
     const void* __restrict__ gating, float* __restrict__ out_w,
     void* __restrict__ out_idx, int idx_dtype, int32_t* __restrict__ out_src,
     const float* __restrict__ bias, int num_tokens, int num_experts, int k,
-    int renormalize, float rsf) {
+    int renormalize, float rsf, const void* __restrict__ input_ids,
+    const void* __restrict__ tid2eid) {
+  constexpr bool SIGMOID = MODE == GATE_SIGMOID;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= num_tokens) return;
   const int64_t base = static_cast<int64_t>(row) * num_experts;
+  if constexpr (MODE == GATE_SOFTPLUS_SQRT) {
+    if (tid2eid) {
+      // hash routing: the experts of the token id are fixed by the table;
+      // weights sqrt(softplus) of those logits, non-finite ones 0
+      // (topk_softplus_sqrt_kernels.cpp:238-296)
+      float wv = 0.f;
+      int64_t ex = 0;
+      if (lane < k) {
+        const int64_t tok = load_id(input_ids, idx_dtype, row);
+        ex = load_id(tid2eid, idx_dtype, tok * k + lane);
+        if (ex >= 0 && ex < num_experts) {
+          wv = softplus_sqrt(load_in<In>(gating, base + ex));
+          if (!isfinite(wv)) wv = 0.f;
+        }
+      }
+      const float wsum = wave_sum(lane < k ? wv : 0.f);
+      if (lane < k) {
+        float scale = rsf;
+        if (renormalize) scale /= (wsum > 0.f ? wsum : 1.f);
+        const int64_t o = static_cast<int64_t>(row) * k + lane;
+        out_w[o] = wv * scale;
+        store_idx(out_idx, idx_dtype, o,
+                  ex >= 0 && ex < num_experts ? static_cast<int>(ex) : num_experts);
+        out_src[o] = lane * num_tokens + row;
+      }
+      return;
+    }
+  }
 
   float p[VPT], sel[VPT];
 #pragma unroll
@@ -68,7 +112,7 @@ __global__ __launch_bounds__(256) void topk_gating_kernel(
     int e = i * 64 + lane;
     p[i] = e < num_experts ? load_in<In>(gating, base + e) : -INFINITY;
   }
-  if constexpr (!SIGMOID) {
+  if constexpr (MODE == GATE_SOFTMAX) {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) m = fmaxf(m, p[i]);
@@ -84,6 +128,9 @@ __global__ __launch_bounds__(256) void topk_gating_kernel(
     const float r = 1.f / s;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) p[i] *= r;
+  } else if constexpr (MODE == GATE_SOFTPLUS_SQRT) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) p[i] = softplus_sqrt(p[i]);
   } else {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -119,15 +166,18 @@ __global__ __launch_bounds__(256) void topk_gating_kernel(
       }
     }
     wave_argmax(bv, bp, bi);
+    // softplus_sqrt reports the biased value minus the bias, (s + b) - b
+    if constexpr (MODE == GATE_SOFTPLUS_SQRT) bp = bias ? bv - bias[bi] : bv;
     wsum += bp;
     if (lane == j) {
       myw = bp;
       myid = bi;
     }
-    // retire the winner so the next round cannot pick it again
+    // retire the winner so the next round cannot pick it again (softplus_sqrt:
+    // -10000, as its reference kernel, :393-401)
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      if (i * 64 + lane == bi) sel[i] = -INFINITY;
+      if (i * 64 + lane == bi) sel[i] = MODE == GATE_SOFTPLUS_SQRT ? -10000.f : -INFINITY;
   }
   if (lane < k) {
     float scale = rsf;
@@ -139,17 +189,18 @@ __global__ __launch_bounds__(256) void topk_gating_kernel(
   }
 }
 
-template <typename In, bool SIGMOID>
+template <typename In, int MODE>
 int launch_topk(float* w, void* idx, int idt, int32_t* src, const void* g,
                 int64_t T, int64_t E, int64_t k, int renorm, const float* bias,
-                float rsf, hipStream_t st) {
+                float rsf, hipStream_t st, const void* input_ids = nullptr,
+                const void* tid2eid = nullptr) {
   dim3 grid(static_cast<unsigned>(cdiv(T, kWavesPerBlock))), block(256);
   if (T == 0) return MI355MOE_OK;
 #define MI_TOPK_CASE(V)                                                       \
   if (E <= 64 * V) {                                                          \
-    hipLaunchKernelGGL((topk_gating_kernel<In, V, SIGMOID>), grid, block, 0,  \
+    hipLaunchKernelGGL((topk_gating_kernel<In, V, MODE>), grid, block, 0,     \
                        st, g, w, idx, idt, src, bias, (int)T, (int)E, (int)k, \
-                       renorm, rsf);                                          \
+                       renorm, rsf, input_ids, tid2eid);                      \
     MI_LAUNCH_CHECK();                                                        \
     return MI355MOE_OK;                                                       \
   }
@@ -162,19 +213,20 @@ int launch_topk(float* w, void* idx, int idt, int32_t* src, const void* g,
   return set_error(MI355MOE_ERR_UNSUPPORTED, "num_experts > 1024 is not supported");
 }
 
-template <bool SIGMOID>
+template <int MODE>
 int topk_dispatch(float* w, void* idx, int idt, int32_t* src, const void* g,
                   int gdt, int64_t T, int64_t E, int64_t k, int renorm,
-                  const float* bias, float rsf, void* stream) {
+                  const float* bias, float rsf, void* stream,
+                  const void* input_ids = nullptr, const void* tid2eid = nullptr) {
   MI_ARG(T >= 0 && E > 0, "invalid num_tokens / num_experts");
   MI_ARG(k > 0 && k <= E && k <= 64, "topk must be in [1, min(num_experts, 64)]");
   MI_ARG(idt == MI355MOE_I32 || idt == MI355MOE_I64 || idt == MI355MOE_U32,
          "topk_indices must be int32, int64 or uint32");
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (gdt) {
-    case MI355MOE_F32: return launch_topk<F32, SIGMOID>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st);
-    case MI355MOE_BF16: return launch_topk<BF16, SIGMOID>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st);
-    case MI355MOE_F16: return launch_topk<F16, SIGMOID>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st);
+    case MI355MOE_F32: return launch_topk<F32, MODE>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st, input_ids, tid2eid);
+    case MI355MOE_BF16: return launch_topk<BF16, MODE>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st, input_ids, tid2eid);
+    case MI355MOE_F16: return launch_topk<F16, MODE>(w, idx, idt, src, g, T, E, k, renorm, bias, rsf, st, input_ids, tid2eid);
     default: return set_error(MI355MOE_ERR_INVALID, "gating_output must be float32, bfloat16 or float16");
   }
 }
@@ -302,7 +354,7 @@ extern "C" int mi355moe_topk_softmax(float* w, void* idx, int idt, int32_t* src,
                                      const void* g, int gdt, int64_t T,
                                      int64_t E, int64_t k, int renorm,
                                      const float* bias, void* stream) {
-  return topk_dispatch<false>(w, idx, idt, src, g, gdt, T, E, k, renorm, bias, 1.f, stream);
+  return topk_dispatch<GATE_SOFTMAX>(w, idx, idt, src, g, gdt, T, E, k, renorm, bias, 1.f, stream);
 }
 
 extern "C" int mi355moe_topk_sigmoid(float* w, void* idx, int idt, int32_t* src,
@@ -310,7 +362,22 @@ extern "C" int mi355moe_topk_sigmoid(float* w, void* idx, int idt, int32_t* src,
                                      int64_t E, int64_t k, int renorm,
                                      const float* bias, float rsf,
                                      void* stream) {
-  return topk_dispatch<true>(w, idx, idt, src, g, gdt, T, E, k, renorm, bias, rsf, stream);
+  return topk_dispatch<GATE_SIGMOID>(w, idx, idt, src, g, gdt, T, E, k, renorm, bias, rsf, stream);
+}
+
+extern "C" int mi355moe_topk_softplus_sqrt(float* w, void* idx, int idt, int32_t* src,
+                                          const void* g, int gdt, int64_t T, int64_t E,
+                                          int64_t k, int renorm, float rsf,
+                                          const float* correction_bias,
+                                          const void* input_ids, const void* tid2eid,
+                                          void* stream) {
+  // the reference kernel's expert counts (topk_softplus_sqrt_kernels.cpp:538-591)
+  MI_ARG(E == 1 || E == 2 || E == 4 || E == 8 || E == 16 || E == 32 || E == 64 || E == 128 ||
+             E == 256 || E == 512 || E == 192 || E == 320 || E == 384 || E == 448 || E == 576,
+         "Unsupported expert number");
+  MI_ARG(!tid2eid || input_ids, "input_ids is required for hash MoE");
+  return topk_dispatch<GATE_SOFTPLUS_SQRT>(w, idx, idt, src, g, gdt, T, E, k, renorm,
+                                           correction_bias, rsf, stream, input_ids, tid2eid);
 }
 
 extern "C" int mi355moe_grouped_topk(void* vals, int32_t* ids, const void* scores,

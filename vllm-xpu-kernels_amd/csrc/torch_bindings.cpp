@@ -111,6 +111,48 @@ void topk_sigmoid(at::Tensor& topk_weights, at::Tensor& topk_indices,
            "topk_sigmoid");
 }
 
+// reference csrc/moe/topk_softplus_sqrt_kernels.cpp:596-772
+void topk_softplus_sqrt(at::Tensor& topk_weights, at::Tensor& topk_indices,
+                        at::Tensor& token_expert_indices, at::Tensor& gating_output,
+                        bool renormalize, double routed_scaling_factor,
+                        const std::optional<at::Tensor>& correction_bias,
+                        const std::optional<at::Tensor>& input_ids,
+                        const std::optional<at::Tensor>& tid2eid) {
+  check_gpu(gating_output, "gating_output");
+  check_gpu(topk_weights, "topk_weights");
+  check_gpu(topk_indices, "topk_indices");
+  check_gpu(token_expert_indices, "token_expert_indices");
+  TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  const int64_t E = gating_output.size(-1);
+  const int64_t T = gating_output.numel() / E;
+  const int64_t k = topk_weights.size(-1);
+  if (correction_bias) {
+    check_gpu(*correction_bias, "correction_bias");
+    TORCH_CHECK(correction_bias->scalar_type() == at::kFloat, "correction_bias must be float32");
+  }
+  if (tid2eid) {
+    TORCH_CHECK(input_ids.has_value(), "input_ids is required for hash MoE");
+    check_gpu(*input_ids, "input_ids");
+    check_gpu(*tid2eid, "tid2eid");
+    TORCH_CHECK(input_ids->scalar_type() == topk_indices.scalar_type(),
+                "input_ids dtype must match topk_indices dtype");
+    TORCH_CHECK(tid2eid->scalar_type() == topk_indices.scalar_type(),
+                "tid2eid dtype must match topk_indices dtype");
+    TORCH_CHECK(input_ids->numel() >= T, "input_ids needs one id per token");
+  }
+  DevGuard g(gating_output.device());
+  check_rc(mi355moe_topk_softplus_sqrt(
+               topk_weights.data_ptr<float>(), topk_indices.data_ptr(),
+               dtype_code(topk_indices.scalar_type()),
+               token_expert_indices.data_ptr<int32_t>(), gating_output.data_ptr(),
+               dtype_code(gating_output.scalar_type()), T, E, k, renormalize,
+               static_cast<float>(routed_scaling_factor),
+               correction_bias ? correction_bias->data_ptr<float>() : nullptr,
+               tid2eid ? input_ids->data_ptr() : nullptr,
+               tid2eid ? tid2eid->data_ptr() : nullptr, cur_stream(gating_output)),
+           "topk_softplus_sqrt");
+}
+
 std::tuple<at::Tensor, at::Tensor> grouped_topk(at::Tensor& scores,
                                                 at::Tensor& scores_with_bias,
                                                 int64_t n_group,
@@ -752,6 +794,10 @@ TORCH_LIBRARY(_moe_C, m) {
   m.def("topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! "
         "token_expert_indices, Tensor gating_output, bool renormalize, Tensor? "
         "bias, float routed_scaling_factor) -> ()");
+  m.def("topk_softplus_sqrt(Tensor! topk_weights, Tensor! topk_indices, "
+        "Tensor! token_expert_indices, Tensor gating_output, bool renormalize, "
+        "float routed_scaling_factor, Tensor? correction_bias=None, Tensor? "
+        "input_ids=None, Tensor? tid2eid=None) -> ()");
   m.def("moe_gather(Tensor! output, Tensor moe_output, Tensor topk_weights, "
         "Tensor unpermuted_row_to_permuted_row, int num_experts) -> ()");
   m.def("init_expert_map(Tensor expert_map, int num_experts, int ep_rank, int "
@@ -776,6 +822,7 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("grouped_topk", &grouped_topk);
   m.impl("topk_softmax", &topk_softmax);
   m.impl("topk_sigmoid", &topk_sigmoid);
+  m.impl("topk_softplus_sqrt", &topk_softplus_sqrt);
   m.impl("moe_gather", &moe_gather);
   m.impl("init_expert_map", &init_expert_map);
   m.impl("remap_hidden_states", &remap_hidden_states);

@@ -42,6 +42,23 @@ def topk_sigmoid(gating_output: torch.Tensor, topk: int, renormalize: bool,
     return w, ids, tei
 
 
+def topk_softplus_sqrt(gating_output: torch.Tensor, topk: int, renormalize: bool,
+                       routed_scaling_factor: float = 1.0,
+                       correction_bias: Optional[torch.Tensor] = None,
+                       input_ids: Optional[torch.Tensor] = None,
+                       tid2eid: Optional[torch.Tensor] = None):
+    """sqrt(softplus) routing (reference csrc/moe/torch_bindings.cpp:70-76);
+    returns (weights f32 [T, k], ids i32 [T, k])."""
+    T = gating_output.shape[0]
+    w = torch.empty(T, topk, dtype=torch.float32, device=gating_output.device)
+    ids = torch.empty(T, topk, dtype=torch.int32, device=gating_output.device)
+    src = torch.empty(T, topk, dtype=torch.int32, device=gating_output.device)
+    torch.ops._moe_C.topk_softplus_sqrt(w, ids, src, gating_output, renormalize,
+                                        routed_scaling_factor, correction_bias, input_ids,
+                                        tid2eid)
+    return w, ids
+
+
 def grouped_topk(scores: torch.Tensor, scores_with_bias: torch.Tensor,
                  n_group: int, topk_group: int, topk: int, renormalize: bool,
                  routed_scaling_factor: float = 1.0):
