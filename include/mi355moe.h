@@ -141,6 +141,24 @@ int mi355moe_grouped_topk(void* topk_values, int32_t* topk_indices,
 
 /* ----------------------------------------------------- alignment / permute */
 
+/* Replaces torch.ops._moe_C.moe_lora_align_block_size
+ * (csrc/moe/torch_bindings.cpp:37-50, csrc/moe/moe_align_sum_kernels.cpp:
+ * 725-1031, 1374-1520).  One stable counting sort per entry of lora_ids
+ * (num_lora_slots of them, max_loras + 1 at most): adapter id = lora_ids[w];
+ * -1, ids >= max_loras and adapters with adapter_enabled[id] == 0 write
+ * nothing.  Otherwise only the slots of tokens with token_lora_mapping[t] ==
+ * id are sorted, into sorted_token_ids[id * max_num_tokens_padded ...] (pad
+ * value num_tokens * topk), expert_ids[id * max_num_m_blocks ...] (unused
+ * blocks -1) and num_tokens_post_pad[id].  topk_ids [num_tokens, topk] i32 or
+ * i64; the other index arrays i32; expert_map optional i32 [num_experts]. */
+int mi355moe_moe_lora_align_block_size(
+    const void* topk_ids, int ids_dtype, int64_t num_tokens, int64_t topk,
+    const int32_t* token_lora_mapping, int64_t num_experts, int64_t block_size,
+    int64_t max_loras, int64_t max_num_tokens_padded, int64_t max_num_m_blocks,
+    int32_t* sorted_token_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
+    const int32_t* adapter_enabled, const int32_t* lora_ids, int64_t num_lora_slots,
+    const int32_t* expert_map, void* stream);
+
 /* Replaces torch.ops._moe_C.moe_align_block_size
  * (csrc/moe/torch_bindings.cpp:14-20, csrc/moe/moe_align_sum_kernels.cpp:
  * 1034-1181).  Deterministic: a stable counting sort (tokens of one expert

@@ -236,6 +236,49 @@ def moe_align_block_size(topk_ids: torch.Tensor, num_experts: int,
     return sorted_ids, expert_ids, ntp
 
 
+def moe_lora_align_block_size(topk_ids: torch.Tensor,
+                              token_lora_mapping: torch.Tensor,
+                              num_experts: int, block_size: int, max_loras: int,
+                              max_num_tokens_padded: int, max_num_m_blocks: int,
+                              sorted_token_ids: np.ndarray,
+                              expert_ids: np.ndarray,
+                              num_tokens_post_pad: np.ndarray,
+                              adapter_enabled: torch.Tensor,
+                              lora_ids: torch.Tensor,
+                              expert_map: Optional[torch.Tensor] = None) -> None:
+    """Multi-LoRA alignment, in place on the numpy outputs
+    (csrc/moe/moe_align_sum_kernels.cpp:800-845 and :984-1025: adapter
+    id = lora_ids[w] for w < max_loras + 1, skipped when -1, >= max_loras or
+    disabled; token mask token_lora_mapping[i // topk] == id :196-216; row
+    slices at id * max_num_tokens_padded / id * max_num_m_blocks :165-170;
+    unused blocks get -1 :839,267-272; padding value numel :172-178).
+
+    Inside one adapter's slice the slots are in flat order per expert (the
+    reference scatters them in any order within an expert's blocks).
+    """
+    topk = topk_ids.shape[1]
+    tok = token_lora_mapping.to(torch.int64).numpy()
+    lids = lora_ids.to(torch.int64).numpy()
+    enabled = adapter_enabled.to(torch.int64).numpy()
+    flat = topk_ids.reshape(-1).to(torch.int64)
+    for w in range(min(len(lids), max_loras + 1)):
+        lid = int(lids[w])
+        if lid == -1 or lid >= max_loras or enabled[lid] == 0:
+            continue
+        mask = torch.from_numpy(np.repeat(tok[:len(flat) // topk] == lid, topk))
+        # masked-out slots become an out-of-range id, which the sort drops
+        ids = torch.where(mask, flat, torch.full_like(flat, num_experts))
+        srt, eid, ntp = moe_align_block_size(ids, num_experts, block_size,
+                                             max_num_tokens_padded,
+                                             max_num_m_blocks, expert_map)
+        nblk = int(ntp[0]) // block_size
+        eid[nblk:] = -1
+        sorted_token_ids[lid * max_num_tokens_padded:
+                         (lid + 1) * max_num_tokens_padded] = srt
+        expert_ids[lid * max_num_m_blocks:(lid + 1) * max_num_m_blocks] = eid
+        num_tokens_post_pad[lid] = ntp[0]
+
+
 def remap_hidden_states(hidden: torch.Tensor, topk_ids: torch.Tensor,
                         local_experts_num: int,
                         expert_map: Optional[torch.Tensor] = None,

@@ -59,6 +59,11 @@ def test_version_and_error_plumbing(lib):
                                                ctypes.c_int64(0), None, None, None,
                                                ctypes.c_size_t(0), None),
      b"padded_num_experts must be less than 1024"),
+    (lambda L: L.mi355moe_moe_lora_align_block_size(
+        None, 3, ctypes.c_int64(8), ctypes.c_int64(2), None, ctypes.c_int64(64),
+        ctypes.c_int64(0), ctypes.c_int64(2), ctypes.c_int64(0), ctypes.c_int64(0), None, None,
+        None, None, None, ctypes.c_int64(3), None, None),
+     b"block_size should be greater than 0"),
     (lambda L: L.mi355moe_per_token_group_fp8_quant(None, 1, None, None,
                                                     ctypes.c_int64(2), ctypes.c_int64(100),
                                                     ctypes.c_int64(128), ctypes.c_float(1e-10),
@@ -199,6 +204,7 @@ def test_fused_moe_workspace_query_and_validation(lib):
 REFERENCE_SCHEMAS = {
     "_moe_C::moe_sum": "moe_sum(Tensor input, Tensor! output, Tensor? topk_ids, Tensor? expert_map) -> ()",
     "_moe_C::moe_align_block_size": "moe_align_block_size(Tensor topk_ids, int num_experts, int block_size, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, Tensor? maybe_expert_map) -> ()",
+    "_moe_C::moe_lora_align_block_size": "moe_lora_align_block_size(Tensor topk_ids, Tensor token_lora_mapping, int num_experts, int block_size, int max_loras, int max_num_tokens_padded, int max_num_m_blocks, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, Tensor! adapter_enabled, Tensor! lora_ids, Tensor? maybe_expert_map) -> ()",
     "_moe_C::topk_softmax": "topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias) -> ()",
     "_moe_C::topk_sigmoid": "topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias, float routed_scaling_factor) -> ()",
     "_moe_C::topk_softplus_sqrt": "topk_softplus_sqrt(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, float routed_scaling_factor, Tensor? correction_bias=None, Tensor? input_ids=None, Tensor? tid2eid=None) -> ()",

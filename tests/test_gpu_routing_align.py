@@ -207,6 +207,125 @@ def test_moe_align_deterministic(dev):
             assert torch.equal(a, b)
 
 
+# ----------------------------------------------------------- LoRA alignment
+def _lora_case(T, k, E, max_loras, bs, seed, id_dtype=torch.int32, base_tokens=0):
+    """Inputs and buffers as tests/test_moe_lora_align_sum.py:29-40, :55-80
+    builds them (k distinct experts per token, adapters in [0, max_loras))."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(id_dtype)
+    tok = torch.randint(0, max_loras, (T,), generator=g, dtype=torch.int32)
+    if base_tokens:
+        tok[T - base_tokens:] = -1
+    mx = (ids.numel() + E * (bs - 1) + bs - 1) // bs * bs
+    if ids.numel() < E:
+        mx = ids.numel() * bs
+    nb = (mx + bs - 1) // bs
+    return ids, tok, mx, nb
+
+
+def _lora_both(dev, ids, tok, E, bs, max_loras, mx, nb, lora_ids, enabled, em=None,
+               fill=(-7, -2, -13)):
+    """Run the op and the oracle on outputs pre-filled with sentinels."""
+    srt = torch.full((max_loras * mx,), fill[0], dtype=torch.int32)
+    eid = torch.full((max_loras * nb,), fill[1], dtype=torch.int32)
+    ntp = torch.full((max_loras,), fill[2], dtype=torch.int32)
+    d = [t.to(dev) for t in (srt, eid, ntp)]
+    _ops().moe_lora_align_block_size(ids.to(dev), tok.to(dev), E, bs, max_loras, mx, nb,
+                                     d[0], d[1], d[2], enabled.to(dev), lora_ids.to(dev),
+                                     em.to(dev) if em is not None else None)
+    r = [srt.numpy().copy(), eid.numpy().copy(), ntp.numpy().copy()]
+    O.moe_lora_align_block_size(ids, tok, E, bs, max_loras, mx, nb, r[0], r[1], r[2],
+                                enabled, lora_ids, em)
+    return [t.cpu().numpy() for t in d], r
+
+
+@pytest.mark.parametrize("T", [100, 200, 1024, 4096])
+@pytest.mark.parametrize("E", [64, 128, 256, 512])
+@pytest.mark.parametrize("max_loras", [2, 32])
+def test_moe_lora_align_block_size(dev, T, E, max_loras):
+    """The reference grid (tests/test_moe_lora_align_sum.py:43-108), bit-exact
+    against the oracle, which also checks its block-membership property."""
+    bs, k = 16, 6
+    ids, tok, mx, nb = _lora_case(T, k, E, max_loras, bs, seed=T + E + max_loras)
+    lora_ids = torch.arange(max_loras + 2, dtype=torch.int32)
+    enabled = torch.ones(max_loras + 1, dtype=torch.int32)
+    got, ref = _lora_both(dev, ids, tok, E, bs, max_loras, mx, nb, lora_ids, enabled)
+    for a, b in zip(got, ref):
+        assert np.array_equal(a, b)
+    flat = ids.flatten().numpy()
+    blocks = got[0].reshape(max_loras, -1, bs)
+    eid = got[1].reshape(max_loras, -1)
+    for lid in range(max_loras):
+        for b in range(blocks.shape[1]):
+            idx = blocks[lid, b][blocks[lid, b] != ids.numel()]
+            if idx.size:
+                assert (flat[idx] == eid[lid, b]).all()
+
+
+@pytest.mark.parametrize("T,k,E,bs,max_loras", [(33, 8, 256, 64, 4), (700, 8, 128, 128, 3)])
+def test_moe_lora_align_int64_ids_and_expert_map(dev, T, k, E, bs, max_loras):
+    ids, tok, mx, nb = _lora_case(T, k, E, max_loras, bs, seed=T, id_dtype=torch.int64,
+                                  base_tokens=5)
+    em = torch.full((E,), -1, dtype=torch.int32)
+    em[1::2] = torch.arange(E // 2, dtype=torch.int32)
+    # -1 in the middle, one disabled adapter, an out-of-range id at the end
+    lora_ids = torch.tensor([0, -1] + list(range(1, max_loras - 1)) + [max_loras + 3],
+                            dtype=torch.int32)[:max_loras + 1]
+    enabled = torch.ones(max_loras + 1, dtype=torch.int32)
+    enabled[1] = 0
+    for m in (None, em):
+        got, ref = _lora_both(dev, ids, tok, E, bs, max_loras, mx, nb, lora_ids, enabled, m)
+        for a, b in zip(got, ref):
+            assert np.array_equal(a, b)
+    assert got[2][1] == -13  # the disabled adapter's row stays as it was
+
+
+@pytest.mark.parametrize("max_loras", [1, 2])
+def test_moe_lora_align_mixed_base_and_lora(dev, max_loras):
+    """tests/test_moe_lora_align_sum.py:225-261: -1 first in lora_ids."""
+    E, bs, k = 64, 16, 6
+    ids, tok, mx, nb = _lora_case(16, k, E, 1, bs, seed=1, base_tokens=8)
+    lora_ids = torch.full((max_loras + 1,), -1, dtype=torch.int32)
+    lora_ids[1] = 0
+    enabled = torch.ones(max_loras + 1, dtype=torch.int32)
+    got, ref = _lora_both(dev, ids, tok, E, bs, max_loras, mx, nb, lora_ids, enabled)
+    for a, b in zip(got, ref):
+        assert np.array_equal(a, b)
+    assert 0 < got[2][0] <= mx and got[2][0] % bs == 0
+    assert (got[1].reshape(max_loras, -1)[0] != -2).all()
+    assert (got[0].reshape(max_loras, -1)[0] != -7).all()
+
+
+def test_moe_lora_align_disabled_and_out_of_range(dev):
+    """tests/test_moe_lora_align_sum.py:264-331."""
+    E, bs, k = 64, 16, 6
+    ids, _, mx, nb = _lora_case(16, k, E, 1, bs, seed=1)
+    tok = torch.zeros(16, dtype=torch.int32)
+    got, _ = _lora_both(dev, ids, tok, E, bs, 1, mx, nb, torch.tensor([0, -1], dtype=torch.int32),
+                        torch.zeros(2, dtype=torch.int32))
+    assert got[2][0] == -13 and (got[1] == -2).all() and (got[0] == -7).all()
+    got, ref = _lora_both(dev, ids, tok, E, bs, 1, mx, nb, torch.tensor([0, 5], dtype=torch.int32),
+                          torch.ones(2, dtype=torch.int32))
+    for a, b in zip(got, ref):
+        assert np.array_equal(a, b)
+    assert got[2][0] != -13
+
+
+def test_moe_lora_align_rejects_bad_buffers(dev):
+    ids, tok, mx, nb = _lora_case(8, 2, 64, 2, 16, seed=0)
+    small = torch.empty(mx, dtype=torch.int32, device=dev)  # one slice, two adapters
+    with pytest.raises(RuntimeError, match="smaller than max_loras"):
+        _ops().moe_lora_align_block_size(
+            ids.to(dev), tok.to(dev), 64, 16, 2, mx, nb, small,
+            torch.empty(2 * nb, dtype=torch.int32, device=dev),
+            torch.empty(2, dtype=torch.int32, device=dev),
+            torch.ones(3, dtype=torch.int32, device=dev),
+            torch.arange(3, dtype=torch.int32, device=dev))
+    with pytest.raises(RuntimeError, match="padded_num_experts"):
+        _ops().moe_lora_align_block_size(
+            ids.to(dev), tok.to(dev), 1000, 16, 2, mx, nb, small, small, small, small, small)
+
+
 @pytest.mark.parametrize("T,k,E,with_map", [(32, 1, 16, False), (257, 8, 64, True),
                                              (1024, 4, 128, False), (2048, 8, 128, True)])
 def test_remap_hidden_states(dev, T, k, E, with_map):

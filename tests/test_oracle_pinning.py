@@ -194,6 +194,82 @@ def test_moe_align_expert_map_vs_golden():
     assert torch.equal(torch.from_numpy(srt), g_srt)
 
 
+def _lora_inputs(T, k, E, max_loras, seed, base_tokens=0):
+    """Reference tests/test_moe_lora_align_sum.py:29-40 and :136-157: k
+    distinct experts per token, adapters drawn from [0, max_loras) (the last
+    `base_tokens` tokens are base-model tokens, adapter -1); buffer sizes as
+    in its :55-60."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    tok = torch.randint(0, max_loras, (T,), generator=g, dtype=torch.int32)
+    if base_tokens:
+        tok[T - base_tokens:] = -1
+    return ids, tok
+
+
+def _lora_run(ids, tok, E, bs, max_loras, lora_ids, enabled, fill=(-7, -2, -13)):
+    mx = (ids.numel() + E * (bs - 1) + bs - 1) // bs * bs
+    if ids.numel() < E:
+        mx = ids.numel() * bs
+    nb = (mx + bs - 1) // bs
+    srt = np.full(max_loras * mx, fill[0], np.int32)
+    eid = np.full(max_loras * nb, fill[1], np.int32)
+    ntp = np.full(max_loras, fill[2], np.int32)
+    O.moe_lora_align_block_size(ids, tok, E, bs, max_loras, mx, nb, srt, eid, ntp,
+                                enabled, lora_ids)
+    return srt, eid, ntp, mx, nb
+
+
+@pytest.mark.parametrize("T,E,max_loras", [(100, 64, 2), (200, 128, 32), (37, 64, 3)])
+def test_moe_lora_align_vs_golden(T, E, max_loras):
+    """Every adapter's slice equals the sort-based golden of the plain
+    alignment over that adapter's tokens, and passes the reference's own
+    membership check (tests/test_moe_lora_align_sum.py:98-108)."""
+    bs, k = 16, 6
+    ids, tok = _lora_inputs(T, k, E, max_loras, seed=T + max_loras)
+    lora_ids = torch.arange(max_loras + 2, dtype=torch.int32)
+    enabled = torch.ones(max_loras + 1, dtype=torch.int32)
+    srt, eid, ntp, mx, nb = _lora_run(ids, tok, E, bs, max_loras, lora_ids, enabled)
+    flat = ids.flatten()
+    for lid in range(max_loras):
+        masked = torch.where(tok.repeat_interleave(k) == lid, flat.long(), E).reshape(ids.shape)
+        g_srt, g_eids, g_ntp = _golden_align(masked, bs, E, mx, nb)
+        g_eids[g_ntp // bs:] = -1
+        assert ntp[lid] == g_ntp
+        assert np.array_equal(srt[lid * mx:(lid + 1) * mx], g_srt.numpy())
+        assert np.array_equal(eid[lid * nb:(lid + 1) * nb], g_eids.numpy())
+        blocks = srt[lid * mx:(lid + 1) * mx].reshape(-1, bs)
+        for b in range(blocks.shape[0]):
+            idx = blocks[b][blocks[b] != ids.numel()]
+            if idx.size:
+                assert (flat.numpy()[idx] == eid[lid * nb + b]).all()
+
+
+def test_moe_lora_align_sentinels():
+    """tests/test_moe_lora_align_sum.py:225-331: a mixed batch with -1 first in
+    lora_ids still sorts adapter 0; a disabled adapter and an out-of-range id
+    leave their rows untouched."""
+    E, bs, k = 64, 16, 6
+    ids, tok = _lora_inputs(16, k, E, 1, seed=1, base_tokens=8)
+    tok[:8] = 0
+    lora_ids = torch.tensor([-1, 0], dtype=torch.int32)
+    on = torch.ones(2, dtype=torch.int32)
+    srt, eid, ntp, mx, nb = _lora_run(ids, tok, E, bs, 1, lora_ids, on)
+    assert 0 < ntp[0] <= mx and ntp[0] % bs == 0
+    assert (srt != -7).all() and (eid != -2).all()
+    # 8 adapter tokens x 6 slots, all in distinct-or-shared experts; only
+    # slots of tokens 0..7 appear
+    got = srt[srt != ids.numel()]
+    assert sorted(got.tolist()) == list(range(48))
+    off = torch.tensor([0, 1], dtype=torch.int32)
+    srt, eid, ntp, mx, nb = _lora_run(ids, torch.zeros(16, dtype=torch.int32), E, bs, 1,
+                                      torch.tensor([0, -1], dtype=torch.int32), off * 0)
+    assert ntp[0] == -13 and (eid == -2).all() and (srt == -7).all()
+    srt, eid, ntp, mx, nb = _lora_run(ids, torch.zeros(16, dtype=torch.int32), E, bs, 1,
+                                      torch.tensor([0, 5], dtype=torch.int32), on)
+    assert ntp[0] != -13 and sorted(srt[srt != ids.numel()].tolist()) == list(range(96))
+
+
 def test_remap_unpermute_invariant():
     torch.manual_seed(3)
     T, H, k, E = 40, 16, 4, 8

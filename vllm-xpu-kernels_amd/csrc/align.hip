@@ -62,7 +62,19 @@ __device__ int block_exclusive_scan(int v, int* s_wave_tot, int& total) {
   return before + x - v;
 }
 
-template <typename Id>
+// Multi-LoRA alignment (moe_lora_align_block_size): workgroup w sorts, for
+// the adapter lora_ids[w], only the slots of tokens mapped to it, into its own
+// slices of the outputs; invalid (-1, >= max_loras) or disabled adapters
+// write nothing; unused blocks get expert id -1.
+struct LoraSel {
+  const int32_t* tok_lora;  // [tokens] adapter of every token
+  int topk;
+  const int32_t* lora_ids;
+  const int32_t* enabled;   // [> max_loras] adapter_enabled
+  int max_loras;
+};
+
+template <typename Id, bool LORA = false>
 __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
     const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
     const int32_t* __restrict__ map, int num_keys, int block_size,
@@ -70,11 +82,27 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
     int32_t* __restrict__ expert_ids, int64_t max_blocks,
     int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
     int32_t* __restrict__ counts_out, int32_t* __restrict__ cum_out,
-    int32_t pad_value) {
+    int32_t pad_value, LoraSel lora = {}) {
   __shared__ int s_cnt[kSortWaves][kMaxKeys];
   __shared__ int s_cum[kMaxKeys + 1];
   __shared__ int s_wave_tot[kSortWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int lora_id = 0;
+  if constexpr (LORA) {
+    lora_id = lora.lora_ids[blockIdx.x];  // uniform
+    if (lora_id < 0 || lora_id >= lora.max_loras || lora.enabled[lora_id] == 0) return;
+    sorted_ids += static_cast<int64_t>(lora_id) * max_padded;
+    expert_ids += static_cast<int64_t>(lora_id) * max_blocks;
+    ntp += lora_id;
+  }
+  // the slot's key, or kInvalidKey (bad or unmapped id, another adapter)
+  auto key_of = [&](int64_t i) -> uint32_t {
+    const uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+    if constexpr (LORA) {
+      if (lora.tok_lora[i / lora.topk] != lora_id) return kInvalidKey;
+    }
+    return key;
+  };
 
   for (int i = tid; i < kSortWaves * kMaxKeys; i += kSortThreads)
     (&s_cnt[0][0])[i] = 0;
@@ -89,7 +117,7 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
   for (int s = 0; s < steps; ++s) {
     int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
     if (i < hi) {
-      uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+      uint32_t key = key_of(i);
       if (key != kInvalidKey) atomicAdd(&s_cnt[wave][key], 1);
     }
   }
@@ -144,7 +172,7 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
         }
         e = lo_e;
       }
-      expert_ids[b] = e;
+      expert_ids[b] = b < nblk ? e : (LORA ? -1 : 0);
     }
   }
 
@@ -153,7 +181,7 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
   for (int s = 0; s < steps; ++s) {
     int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
     uint32_t key = kInvalidKey;
-    if (i < hi) key = load_key(ids, i, id_bound, map, num_keys);
+    if (i < hi) key = key_of(i);
     unsigned long long same = ~0ull;
 #pragma unroll
     for (int b = 0; b < 11; ++b) {
@@ -540,6 +568,41 @@ extern "C" int mi355moe_moe_align_block_size(
                            ntp, nullptr, nullptr, static_cast<int32_t>(numel),
                            workspace, workspace_bytes, static_cast<hipStream_t>(stream),
                            nullptr);
+}
+
+extern "C" int mi355moe_moe_lora_align_block_size(
+    const void* topk_ids, int ids_dtype, int64_t num_tokens, int64_t topk,
+    const int32_t* token_lora_mapping, int64_t num_experts, int64_t block_size,
+    int64_t max_loras, int64_t max_num_tokens_padded, int64_t max_num_m_blocks,
+    int32_t* sorted_token_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
+    const int32_t* adapter_enabled, const int32_t* lora_ids, int64_t num_lora_slots,
+    const int32_t* expert_map, void* stream) {
+  MI_ARG(block_size > 0, "block_size should be greater than 0. ");
+  MI_ARG((num_experts + 31) / 32 * 32 < 1024, "padded_num_experts must be less than 1024");
+  MI_ARG(num_tokens >= 0 && topk > 0 && max_loras >= 0 && num_lora_slots >= 0,
+         "invalid LoRA alignment sizes");
+  MI_ARG(ids_dtype == MI355MOE_I32 || ids_dtype == MI355MOE_I64,
+         "topk_ids must be int32 or int64");
+  if (num_lora_slots == 0 || max_loras == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const LoraSel sel{token_lora_mapping, static_cast<int>(topk), lora_ids, adapter_enabled,
+                    static_cast<int>(max_loras)};
+  const int64_t numel = num_tokens * topk;
+  dim3 grid(static_cast<unsigned>(num_lora_slots));
+  if (ids_dtype == MI355MOE_I32)
+    counting_sort_kernel<int32_t, true><<<grid, dim3(kSortThreads), 0, st>>>(
+        static_cast<const int32_t*>(topk_ids), numel, num_experts, expert_map,
+        static_cast<int>(num_experts), static_cast<int>(block_size), sorted_token_ids,
+        max_num_tokens_padded, expert_ids, max_num_m_blocks, num_tokens_post_pad, nullptr,
+        nullptr, nullptr, static_cast<int32_t>(numel), sel);
+  else
+    counting_sort_kernel<int64_t, true><<<grid, dim3(kSortThreads), 0, st>>>(
+        static_cast<const int64_t*>(topk_ids), numel, num_experts, expert_map,
+        static_cast<int>(num_experts), static_cast<int>(block_size), sorted_token_ids,
+        max_num_tokens_padded, expert_ids, max_num_m_blocks, num_tokens_post_pad, nullptr,
+        nullptr, nullptr, static_cast<int32_t>(numel), sel);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
 }
 
 extern "C" size_t mi355moe_remap_hidden_states_workspace_size(int64_t num_tokens,

@@ -221,6 +221,55 @@ void moe_align_block_size(at::Tensor topk_ids, int64_t num_experts,
            "moe_align_block_size");
 }
 
+void moe_lora_align_block_size(at::Tensor topk_ids, at::Tensor token_lora_mapping,
+                               int64_t num_experts, int64_t block_size, int64_t max_loras,
+                               int64_t max_num_tokens_padded, int64_t max_num_m_blocks,
+                               at::Tensor sorted_token_ids, at::Tensor experts_ids,
+                               at::Tensor num_tokens_post_pad, at::Tensor adapter_enabled,
+                               at::Tensor lora_ids,
+                               const std::optional<at::Tensor>& maybe_expert_map) {
+  TORCH_CHECK(block_size > 0, "block_size should be greater than 0. ");
+  TORCH_CHECK((num_experts + 31) / 32 * 32 < 1024, "padded_num_experts must be less than 1024");
+  check_gpu(topk_ids, "topk_ids");
+  TORCH_CHECK(topk_ids.dim() == 2, "topk_ids must be [num_tokens, topk]");
+  for (auto* t : {&token_lora_mapping, &sorted_token_ids, &experts_ids, &num_tokens_post_pad,
+                  &adapter_enabled, &lora_ids}) {
+    check_gpu(*t, "LoRA alignment tensor");
+    TORCH_CHECK(t->scalar_type() == at::kInt,
+                "token_lora_mapping, sorted_token_ids, experts_ids, num_tokens_post_pad, "
+                "adapter_enabled and lora_ids must be int32");
+  }
+  TORCH_CHECK(max_loras >= 0 && max_num_tokens_padded >= 0 && max_num_m_blocks >= 0,
+              "max_loras, max_num_tokens_padded and max_num_m_blocks must be >= 0");
+  TORCH_CHECK(token_lora_mapping.numel() >= topk_ids.size(0),
+              "token_lora_mapping needs one entry per token");
+  TORCH_CHECK(sorted_token_ids.numel() >= max_loras * max_num_tokens_padded &&
+                  experts_ids.numel() >= max_loras * max_num_m_blocks &&
+                  num_tokens_post_pad.numel() >= max_loras &&
+                  adapter_enabled.numel() >= max_loras,
+              "LoRA alignment outputs are smaller than max_loras slices");
+  if (maybe_expert_map) {
+    check_gpu(*maybe_expert_map, "expert_map");
+    TORCH_CHECK(maybe_expert_map->scalar_type() == at::kInt &&
+                    maybe_expert_map->numel() >= num_experts,
+                "expert_map must be int32 [num_experts]");
+  }
+  DevGuard g(topk_ids.device());
+  // one workgroup per entry of lora_ids, at most max_loras + 1 of them (the
+  // real adapters and a possible -1)
+  const int64_t slots = std::min<int64_t>(lora_ids.numel(), max_loras + 1);
+  check_rc(mi355moe_moe_lora_align_block_size(
+               topk_ids.data_ptr(), dtype_code(topk_ids.scalar_type()), topk_ids.size(0),
+               topk_ids.size(1), token_lora_mapping.data_ptr<int32_t>(), num_experts,
+               block_size, max_loras, max_num_tokens_padded, max_num_m_blocks,
+               sorted_token_ids.data_ptr<int32_t>(), experts_ids.data_ptr<int32_t>(),
+               num_tokens_post_pad.data_ptr<int32_t>(), adapter_enabled.data_ptr<int32_t>(),
+               lora_ids.data_ptr<int32_t>(), slots,
+               maybe_expert_map ? maybe_expert_map->data_ptr<int32_t>() : nullptr,
+               cur_stream(topk_ids)),
+           "moe_lora_align_block_size");
+}
+
 void remap_hidden_states(at::Tensor& hidden_states,
                          const std::optional<at::Tensor>& hidden_states_scales,
                          at::Tensor& remapped_hidden_states,
@@ -785,6 +834,11 @@ TORCH_LIBRARY(_moe_C, m) {
   m.def("moe_align_block_size(Tensor topk_ids, int num_experts, int block_size, "
         "Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, "
         "Tensor? maybe_expert_map) -> ()");
+  m.def("moe_lora_align_block_size(Tensor topk_ids, Tensor token_lora_mapping, int "
+        "num_experts, int block_size, int max_loras, int max_num_tokens_padded, int "
+        "max_num_m_blocks, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! "
+        "num_tokens_post_pad, Tensor! adapter_enabled, Tensor! lora_ids, Tensor? "
+        "maybe_expert_map) -> ()");
   m.def("grouped_topk(Tensor scores, Tensor scores_with_bias, int n_group, int "
         "topk_group, int topk, bool renormalize, float routed_scaling_factor) -> "
         "(Tensor, Tensor)");
@@ -819,6 +873,7 @@ TORCH_LIBRARY(_moe_C, m) {
 TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("moe_sum", &moe_sum);
   m.impl("moe_align_block_size", &moe_align_block_size);
+  m.impl("moe_lora_align_block_size", &moe_lora_align_block_size);
   m.impl("grouped_topk", &grouped_topk);
   m.impl("topk_softmax", &topk_softmax);
   m.impl("topk_sigmoid", &topk_sigmoid);

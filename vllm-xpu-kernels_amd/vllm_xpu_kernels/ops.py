@@ -120,6 +120,22 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
     return sorted_ids, expert_ids, ntp
 
 
+def moe_lora_align_block_size(topk_ids: torch.Tensor,
+                              token_lora_mapping: torch.Tensor,
+                              num_experts: int, block_size: int, max_loras: int,
+                              max_num_tokens_padded: int, max_num_m_blocks: int,
+                              sorted_token_ids: torch.Tensor,
+                              experts_ids: torch.Tensor,
+                              num_tokens_post_pad: torch.Tensor,
+                              adapter_enabled: torch.Tensor,
+                              lora_ids: torch.Tensor,
+                              expert_map: Optional[torch.Tensor] = None) -> None:
+    torch.ops._moe_C.moe_lora_align_block_size(
+        topk_ids, token_lora_mapping, num_experts, block_size, max_loras,
+        max_num_tokens_padded, max_num_m_blocks, sorted_token_ids, experts_ids,
+        num_tokens_post_pad, adapter_enabled, lora_ids, expert_map)
+
+
 def moe_sum(inp: torch.Tensor, out: torch.Tensor,
             topk_ids: Optional[torch.Tensor] = None,
             expert_map: Optional[torch.Tensor] = None) -> None:
