@@ -284,6 +284,49 @@ def op_bandwidth(dev, steps):
                     "us": round(us, 2), "GBps": round(gbps, 1),
                     "hbm_frac": round(gbps / 8000.0, 3)})
         del x
+    out += prologue_bandwidth(dev, steps, g)
+    return out
+
+
+def prologue_bandwidth(dev, steps, g):
+    """fused_moe_prologue at C3's T=8192 (fp8 block-scaled activations,
+    H=7168, k=8 of 256 experts) and at the reference test's largest case
+    (bf16, T=8192, H=8192, k=2 of 16).  Algorithmic bytes: every input row
+    and scale row read once, every routed row written once, the ids and
+    token scales read, the four per-row index/scale entries written."""
+    from vllm_xpu_kernels import capi, ops
+    out = []
+    for name, T, H, k, E, fp8 in (("fused_moe_prologue fp8block C3", 8192, 7168, 8, 256, True),
+                                  ("fused_moe_prologue bf16 ref-test", 8192, 8192, 2, 16, False)):
+        x = torch.randn(T, H, generator=g, device=dev)
+        x = x.to(torch.float8_e4m3fn) if fp8 else x.bfloat16()
+        sc = torch.rand(T, H // 128, generator=g, device=dev) if fp8 else None
+        ids = torch.stack([torch.randperm(E, device=dev, generator=g)[:k] for _ in range(T)])
+        fs = torch.rand(T, k, generator=g, device=dev)
+        eb, sb, bk = (1, 4, 128) if fp8 else (2, 0, 1)
+        total, _ = capi.prologue_layout(T, k, H, eb, bk, sb, E)
+        ws = torch.empty(total, dtype=torch.uint8, device=dev)
+
+        def fn():
+            ops.fused_moe_prologue(x, sc, ids, fs, ws, H, 2048, bk, 0, 1, E)
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / steps
+        N = T * k
+        row = H * eb + (H // bk) * sb
+        nbytes = T * row + N * row + N * (8 + 4) + N * 16 + (E + 1) * 8
+        gbps = nbytes / us / 1e3
+        out.append({"op": name, "input": [T, H, k, E], "bytes": nbytes,
+                    "us": round(us, 2), "GBps": round(gbps, 1),
+                    "hbm_frac": round(gbps / 8000.0, 3)})
+        del x, ws
     return out
 
 

@@ -177,6 +177,52 @@ int mi355moe_moe_align_block_size(const void* topk_ids, int ids_dtype,
                                   void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* fused_moe_prologue workspace: ten sections, each padded to 256 bytes, in
+ * this order (the reference's, csrc/moe/fused_moe_prologue.cpp:40-102):
+ *   0 permuted_row_to_unpermuted_row  i32 [N]      expanded row j*T + t
+ *   1 permuted_token_selected_experts i32 [N]      expert - rank's first
+ *   2 unpermuted_row_to_permuted_row  i32 [N]      -1: not routed here
+ *   3 blocked_expert_counts           i32 [E*nblk] scratch
+ *   4 blocked_expert_counts_cumsum    i32 [E*nblk] scratch
+ *   5 blocked_row_to_unpermuted_row   i32 [E*T]    scratch
+ *   6 expert_first_token_offset       i64 [E+1]
+ *   7 permuted_token_final_scales     f32 [N]
+ *   8 overlapped_gemm1_gemm2_inputs   [N, hidden] input elements
+ *   9 permuted_act_scales             [N*hidden/block_k] scale elements
+ * with N = T * k, E = num_experts_on_rank and nblk = ceil(T / b), b the
+ * smallest of 32, 64, ..., 1024 with ceil(T / b) * E <= b (else 1024).
+ * Rows past expert_first_token_offset[E] are not written.  Section 2 holds
+ * -1 for expanded rows not routed to this rank, where the reference leaves
+ * the bytes as they were. */
+#define MI355MOE_PROLOGUE_SECTIONS 10
+
+/* Byte layout of the fused_moe_prologue workspace: returns the total size
+ * and, when non-null, the offset and padded size of each section
+ * (offsets[10], sizes[10]); 0 for invalid sizes.  scale_bytes 0: no
+ * activation scales (section 9 empty). */
+size_t mi355moe_fused_moe_prologue_workspace_layout(
+    int64_t num_rows, int64_t experts_per_token, int64_t hidden_size, int64_t elem_bytes,
+    int64_t block_k, int64_t scale_bytes, int64_t num_experts_on_rank, size_t* offsets,
+    size_t* sizes);
+
+/* Replaces torch.ops._moe_C.fused_moe_prologue (csrc/moe/torch_bindings.cpp:
+ * 83-92, csrc/moe/fused_moe_prologue.cpp:5-151, fused_moe_prologue.hpp:
+ * 154-709).  input [num_rows, hidden_size] of elem_bytes (2: bf16 / fp16,
+ * 1: e4m3 or packed e2m1 pairs); input_scales [num_rows, hidden_size /
+ * block_k] of scale_bytes (4: f32, 1: e8m0; 0: none); token_selected_experts
+ * [num_rows, experts_per_token] i64 (or i32); token_final_scales f32 of the
+ * same shape (null: 1.0).  This rank owns experts [ep_rank * E, (ep_rank +
+ * 1) * E) with E = num_experts_on_rank <= 1024.  Permuted rows are in expert
+ * order and token order inside an expert; a token listing an expert twice
+ * is routed to it once.  inter_size is accepted and unused, as in the
+ * reference.  The workspace must hold the layout above. */
+int mi355moe_fused_moe_prologue(
+    const void* input, int64_t elem_bytes, const void* input_scales, int64_t scale_bytes,
+    const void* token_selected_experts, int ids_dtype, const float* token_final_scales,
+    void* workspace, size_t workspace_bytes, int64_t num_rows, int64_t hidden_size,
+    int64_t inter_size, int64_t block_k, int64_t experts_per_token, int64_t ep_rank,
+    int64_t ep_size, int64_t num_experts_on_rank, void* stream);
+
 /* Replaces torch.ops._moe_C.remap_hidden_states
  * (csrc/moe/torch_bindings.cpp:99-108, csrc/moe/remap_hidden_states.cpp:
  * 418-568).  Stable order within an expert.  hidden [T,H] (elem_bytes per

@@ -279,6 +279,87 @@ def moe_lora_align_block_size(topk_ids: torch.Tensor,
         num_tokens_post_pad[lid] = ntp[0]
 
 
+PROLOGUE_SECTIONS = ("permuted_row_to_unpermuted_row", "permuted_token_selected_experts",
+                     "unpermuted_row_to_permuted_row", "blocked_expert_counts",
+                     "blocked_expert_counts_cumsum", "blocked_row_to_unpermuted_row",
+                     "expert_first_token_offset", "permuted_token_final_scales",
+                     "overlapped_gemm1_gemm2_inputs", "permuted_act_scales")
+
+
+def prologue_tokens_per_block(T: int, E: int) -> int:
+    """csrc/moe/fused_moe_prologue.hpp:35-46."""
+    tpb = 32
+    while tpb <= 1024:
+        if -(-T // tpb) * E <= tpb:
+            return tpb
+        tpb *= 2
+    return 1024
+
+
+def prologue_layout(T: int, k: int, hidden: int, elem_bytes: int, block_k: int,
+                    scale_bytes: int, E: int):
+    """Workspace sections in order, each padded to 256 bytes
+    (csrc/moe/fused_moe_prologue.cpp:40-102).  Returns (total, {name: (size,
+    offset)})."""
+    N = T * k
+    nblk = -(-T // prologue_tokens_per_block(T, E)) if T else 0
+    raw = [N * 4, N * 4, N * 4, E * nblk * 4, E * nblk * 4, E * T * 4, (E + 1) * 8, N * 4,
+           N * hidden * elem_bytes, (N * hidden // block_k) * scale_bytes if scale_bytes else 0]
+    out, at = {}, 0
+    for name, r in zip(PROLOGUE_SECTIONS, raw):
+        sz = (r + 255) // 256 * 256
+        out[name] = (sz, at)
+        at += sz
+    return at, out
+
+
+def fused_moe_prologue(rows: np.ndarray, scale_rows: Optional[np.ndarray],
+                       token_selected_experts: np.ndarray,
+                       token_final_scales: np.ndarray, num_experts_on_rank: int,
+                       ep_rank: int = 0):
+    """The reference's three-step permutation and row expansion
+    (csrc/moe/fused_moe_prologue.hpp:154-229 block scan: token t matches
+    expert e at its FIRST top-k position j with id - start == e, expanded row
+    j * T + t; :260-372 prefix sums -> expert_first_token_offset; :423-472
+    merge -> the three index maps; :555-640 expand: row copy, scale-row copy,
+    token scale of flat slot t * k + j).
+
+    rows: u8 [T, row_bytes] (the input's bytes); scale_rows: u8 [T,
+    srow_bytes] or None.  Returns a dict of the written section values
+    (index maps over routed rows only; unpermuted_row_to_permuted_row as
+    {expanded row: permuted row}).
+    """
+    ids = np.asarray(token_selected_experts, dtype=np.int64)
+    T, k = ids.shape
+    E = num_experts_on_rank
+    start = E * ep_rank
+    p2u, experts = [], []
+    offsets = np.zeros(E + 1, dtype=np.int64)
+    tok = np.arange(T, dtype=np.int64)
+    for e in range(E):
+        offsets[e] = sum(len(r) for r in p2u)
+        match = ids - start == e                 # [T, k]
+        has = match.any(axis=1)
+        first = match.argmax(axis=1)             # first matching position j
+        p2u.append(first[has] * T + tok[has])    # tokens ascending
+        experts.append(np.full(int(has.sum()), e))
+    p2u = np.concatenate(p2u).astype(np.int32) if E else np.zeros(0, np.int32)
+    offsets[E] = p2u.size
+    u2p = {int(r): p for p, r in enumerate(p2u)}
+    src_t = p2u % T if T else p2u
+    src_j = p2u // T if T else p2u
+    fs = np.asarray(token_final_scales, dtype=np.float32).reshape(T, k)
+    return {
+        "permuted_row_to_unpermuted_row": p2u,
+        "permuted_token_selected_experts": np.concatenate(experts).astype(np.int32),
+        "unpermuted_row_to_permuted_row": u2p,
+        "expert_first_token_offset": offsets,
+        "permuted_token_final_scales": fs[src_t, src_j],
+        "overlapped_gemm1_gemm2_inputs": rows[src_t],
+        "permuted_act_scales": None if scale_rows is None else scale_rows[src_t],
+    }
+
+
 def remap_hidden_states(hidden: torch.Tensor, topk_ids: torch.Tensor,
                         local_experts_num: int,
                         expert_map: Optional[torch.Tensor] = None,

@@ -146,6 +146,34 @@ def test_invalid_arguments_rejected_before_launch(lib, call, msg):
     assert msg in lib.mi355moe_last_error()
 
 
+@pytest.mark.parametrize("T,k,hidden,eb,bk,sb,E", [
+    (1, 1, 128, 2, 1, 0, 2), (16, 2, 8192, 1, 128, 4, 16), (8192, 2, 8192, 1, 32, 1, 16),
+    (3000, 8, 7168, 1, 128, 4, 256), (5, 3, 100, 2, 1, 0, 1000)])
+def test_prologue_layout_matches_oracle(T, k, hidden, eb, bk, sb, E):
+    """The C ABI's workspace layout (host-only) is the reference's byte layout."""
+    from oracle import moe_oracle as O
+    from vllm_xpu_kernels import capi
+    total, ws = capi.prologue_layout(T, k, hidden, eb, bk, sb, E)
+    assert (total, ws) == O.prologue_layout(T, k, hidden, eb, bk, sb, E)
+
+
+def test_prologue_argument_validation(lib):
+    lib.mi355moe_fused_moe_prologue.argtypes = (
+        [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t] +
+        [ctypes.c_int64] * 8 + [ctypes.c_void_p])
+
+    def call(ws_bytes=1 << 20, E=16, rank=0, size=1, eb=2, sb=0, bk=1, hidden=256):
+        return lib.mi355moe_fused_moe_prologue(16, eb, 16 if sb else None, sb, 16, 4, 16, 16,
+                                               ws_bytes, 4, hidden, 512, bk, 2, rank, size, E,
+                                               None)
+    assert call(rank=2, size=2) == -1 and b"ep_rank" in lib.mi355moe_last_error()
+    assert call(E=1025) == -1 and b"num_experts_on_rank" in lib.mi355moe_last_error()
+    assert call(eb=4) == -1 and b"1- or 2-byte" in lib.mi355moe_last_error()
+    assert call(eb=1, sb=4, bk=100) == -1 and b"block_k" in lib.mi355moe_last_error()
+    assert call(ws_bytes=1024) == -1 and b"smaller than the prologue" in lib.mi355moe_last_error()
+
+
 def test_fused_moe_workspace_query_and_validation(lib):
     from vllm_xpu_kernels import _ops  # noqa: F401
 
@@ -168,6 +196,18 @@ def test_fused_moe_workspace_query_and_validation(lib):
 
     a = Args(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=64,
              hidden=7168, inter=2048, num_experts=256, topk=8)
+    # this struct, not the ctypes binding's (which may have set argtypes;
+    # restored at the end)
+    saved = (lib.mi355moe_fused_moe_workspace_size.argtypes, lib.mi355moe_fused_moe.argtypes)
+    lib.mi355moe_fused_moe_workspace_size.argtypes = None
+    lib.mi355moe_fused_moe.argtypes = None
+    try:
+        _workspace_query_checks(lib, a)
+    finally:
+        lib.mi355moe_fused_moe_workspace_size.argtypes, lib.mi355moe_fused_moe.argtypes = saved
+
+
+def _workspace_query_checks(lib, a):
     lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t
     ws = lib.mi355moe_fused_moe_workspace_size(ctypes.byref(a))
     assert ws > 64 * 7168
@@ -205,6 +245,7 @@ REFERENCE_SCHEMAS = {
     "_moe_C::moe_sum": "moe_sum(Tensor input, Tensor! output, Tensor? topk_ids, Tensor? expert_map) -> ()",
     "_moe_C::moe_align_block_size": "moe_align_block_size(Tensor topk_ids, int num_experts, int block_size, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, Tensor? maybe_expert_map) -> ()",
     "_moe_C::moe_lora_align_block_size": "moe_lora_align_block_size(Tensor topk_ids, Tensor token_lora_mapping, int num_experts, int block_size, int max_loras, int max_num_tokens_padded, int max_num_m_blocks, Tensor! sorted_token_ids, Tensor! experts_ids, Tensor! num_tokens_post_pad, Tensor! adapter_enabled, Tensor! lora_ids, Tensor? maybe_expert_map) -> ()",
+    "_moe_C::fused_moe_prologue": "fused_moe_prologue(Tensor input, Tensor? input_scales, Tensor token_selected_experts, Tensor token_final_scales, Tensor workspace, int hidden_size, int inter_size, int block_k, int ep_rank, int ep_size,int num_experts_on_rank) -> ()",
     "_moe_C::topk_softmax": "topk_softmax(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias) -> ()",
     "_moe_C::topk_sigmoid": "topk_sigmoid(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, Tensor? bias, float routed_scaling_factor) -> ()",
     "_moe_C::topk_softplus_sqrt": "topk_softplus_sqrt(Tensor! topk_weights, Tensor! topk_indices, Tensor! token_expert_indices, Tensor gating_output, bool renormalize, float routed_scaling_factor, Tensor? correction_bias=None, Tensor? input_ids=None, Tensor? tid2eid=None) -> ()",

@@ -270,6 +270,83 @@ def test_moe_lora_align_sentinels():
     assert ntp[0] != -13 and sorted(srt[srt != ids.numel()].tolist()) == list(range(96))
 
 
+# ------------------------------------------------------- fused_moe_prologue
+def _ref_prologue_golden(x, scales, ids, k):
+    """Restatement of the reference golden tests/fused_moe/test_moe_prologue.py:
+    52-97 (argsort of the flat expert ids; rows of token idx // k)."""
+    flat = ids.reshape(-1)
+    idxs = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat)
+    tok = idxs // k
+    offsets = counts.cumsum()
+    return offsets, x[tok], None if scales is None else scales[tok]
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 1, 16), (4, 2, 16), (16, 2, 16), (300, 2, 16), (64, 8, 64)])
+@pytest.mark.parametrize("row_bytes,srow_bytes", [(512, 0), (256, 8), (128, 16)])
+def test_prologue_vs_reference_golden(T, k, E, row_bytes, srow_bytes):
+    g = np.random.default_rng(T * 7 + k)
+    x = g.integers(0, 256, (T, row_bytes), dtype=np.uint8)
+    sc = g.integers(0, 256, (T, srow_bytes), dtype=np.uint8) if srow_bytes else None
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    fs = g.standard_normal((T, k)).astype(np.float32)
+    out = O.fused_moe_prologue(x, sc, ids, fs, E)
+    offs, gx, gs = _ref_prologue_golden(x, sc, ids, k)
+    # the reference test compares expert_first_token_offset[1:1 + n]
+    assert np.array_equal(out["expert_first_token_offset"][1:1 + offs.size], offs)
+    assert np.array_equal(out["overlapped_gemm1_gemm2_inputs"], gx)
+    if sc is not None:
+        assert np.array_equal(out["permuted_act_scales"], gs)
+    p2u = out["permuted_row_to_unpermuted_row"]
+    # maps are mutually inverse; experts and token scales follow the source slot
+    assert all(out["unpermuted_row_to_permuted_row"][int(r)] == p for p, r in enumerate(p2u))
+    assert np.array_equal(out["permuted_token_selected_experts"], ids[p2u % T, p2u // T])
+    assert np.array_equal(out["permuted_token_final_scales"], fs[p2u % T, p2u // T])
+
+
+def test_prologue_known_answer_ep_and_duplicates():
+    """Hand-worked: E = 2 on rank 1 (experts 2, 3); token 1 lists expert 3
+    twice and is routed once (first position); id 0 is another rank's."""
+    ids = np.array([[2, 3], [3, 3], [0, 2]], dtype=np.int64)
+    fs = np.arange(6, dtype=np.float32).reshape(3, 2)
+    x = np.arange(3, dtype=np.uint8).reshape(3, 1)
+    out = O.fused_moe_prologue(x, None, ids, fs, 2, ep_rank=1)
+    assert out["permuted_row_to_unpermuted_row"].tolist() == [0, 5, 3, 1]
+    assert out["permuted_token_selected_experts"].tolist() == [0, 0, 1, 1]
+    assert out["expert_first_token_offset"].tolist() == [0, 2, 4]
+    assert out["permuted_token_final_scales"].tolist() == [0.0, 5.0, 1.0, 2.0]
+    assert out["overlapped_gemm1_gemm2_inputs"].ravel().tolist() == [0, 2, 0, 1]
+    assert out["unpermuted_row_to_permuted_row"] == {0: 0, 5: 1, 3: 2, 1: 3}
+
+
+def _ref_test_ws_map(T, k, hidden, elem_bytes, block_k, scale_bytes, E):
+    """The layout as the reference test builds it
+    (tests/fused_moe/test_moe_prologue.py:151-204)."""
+    N = T * k
+    tpb = O.prologue_tokens_per_block(T, E)
+    nblk = -(-T // tpb)
+    sizes = [N * 4, N * 4, k * T * 4, E * nblk * 4, E * nblk * 4, E * T * 4, (E + 1) * 8, N * 4,
+             N * hidden * elem_bytes, (N * hidden) // block_k * scale_bytes if scale_bytes else 0]
+    ws, at = {}, 0
+    for name, sz in zip(O.PROLOGUE_SECTIONS, sizes):
+        if sz % 256:
+            sz += 256 - sz % 256
+        ws[name] = (sz, at)
+        at += sz
+    return at, ws
+
+
+@pytest.mark.parametrize("T,k,hidden,eb,bk,sb,E", [
+    (1, 1, 128, 2, 1, 0, 2), (4, 2, 8192, 2, 1, 0, 16), (16, 2, 8192, 1, 128, 4, 16),
+    (8192, 2, 8192, 1, 32, 1, 16), (8192, 1, 4096, 1, 16, 1, 16), (3000, 8, 7168, 1, 128, 4, 256)])
+def test_prologue_layout_matches_reference_test(T, k, hidden, eb, bk, sb, E):
+    assert O.prologue_layout(T, k, hidden, eb, bk, sb, E) == _ref_test_ws_map(T, k, hidden, eb, bk, sb, E)
+    # tokens per block: the smallest power of two in [32, 1024] whose block
+    # count times E fits in one block
+    tpb = O.prologue_tokens_per_block(T, E)
+    assert tpb == 1024 or (-(-T // tpb) * E <= tpb and (tpb == 32 or -(-T // (tpb // 2)) * E > tpb // 2))
+
+
 def test_remap_unpermute_invariant():
     torch.manual_seed(3)
     T, H, k, E = 40, 16, 4, 8

@@ -14,6 +14,7 @@
 // count + device-atomic scatter (csrc/moe/moe_align_sum_kernels.cpp:135-455),
 // whose within-expert order is not deterministic.
 #include "common.h"
+#include "moe_gemm.h"
 
 namespace mi355 {
 namespace {
@@ -23,13 +24,35 @@ constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kMaxKeys = 1024;
 constexpr uint32_t kInvalidKey = 2047u;  // 11 bits, never a valid key
 
+// Options of the fused_moe_prologue sort: ids are shifted by `start` (the
+// rank's first expert); with dedupe_k > 1 a slot whose token chose the same
+// expert at an earlier top-k position is dropped (only the first occurrence
+// of an expert per token is routed); keep_tail leaves sorted_ids past the
+// last sorted slot as it was; inv_rows > 0 stores the position of flat slot
+// i = t * k + j (k = dedupe_k) at inv_pos[j * inv_rows + t].
+struct KeyXform {
+  int64_t start;
+  int dedupe_k;
+  bool keep_tail;
+  int64_t inv_rows;
+};
+
+__device__ __forceinline__ int64_t inv_index(int64_t i, const KeyXform& xf) {
+  return xf.inv_rows > 0 ? (i % xf.dedupe_k) * xf.inv_rows + i / xf.dedupe_k : i;
+}
+
 template <typename Id>
 __device__ __forceinline__ uint32_t load_key(const Id* ids, int64_t i,
                                              int64_t id_bound,
                                              const int32_t* map,
-                                             int num_keys) {
-  int64_t v = static_cast<int64_t>(ids[i]);
+                                             int num_keys, KeyXform xf = {}) {
+  const Id raw = ids[i];
+  int64_t v = static_cast<int64_t>(raw) - xf.start;
   if (v < 0 || v >= id_bound) return kInvalidKey;
+  if (xf.dedupe_k > 1) {
+    for (int64_t q = i - i % xf.dedupe_k; q < i; ++q)
+      if (ids[q] == raw) return kInvalidKey;
+  }
   if (map) v = map[v];
   if (v < 0 || v >= num_keys) return kInvalidKey;
   return static_cast<uint32_t>(v);
@@ -82,7 +105,7 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
     int32_t* __restrict__ expert_ids, int64_t max_blocks,
     int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
     int32_t* __restrict__ counts_out, int32_t* __restrict__ cum_out,
-    int32_t pad_value, LoraSel lora = {}) {
+    int32_t pad_value, LoraSel lora = {}, KeyXform xf = {}) {
   __shared__ int s_cnt[kSortWaves][kMaxKeys];
   __shared__ int s_cum[kMaxKeys + 1];
   __shared__ int s_wave_tot[kSortWaves];
@@ -97,7 +120,7 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
   }
   // the slot's key, or kInvalidKey (bad or unmapped id, another adapter)
   auto key_of = [&](int64_t i) -> uint32_t {
-    const uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+    const uint32_t key = load_key(ids, i, id_bound, map, num_keys, xf);
     if constexpr (LORA) {
       if (lora.tok_lora[i / lora.topk] != lora_id) return kInvalidKey;
     }
@@ -155,8 +178,9 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
       for (int p = start + total_e; p < start + padded && p < max_padded; ++p)
         sorted_ids[p] = pad_value;
     }
-    for (int64_t p = total_padded + tid; p < max_padded; p += kSortThreads)
-      sorted_ids[p] = pad_value;
+    if (!xf.keep_tail)
+      for (int64_t p = total_padded + tid; p < max_padded; p += kSortThreads)
+        sorted_ids[p] = pad_value;
   }
   // expert id of every block (binary search over the padded prefix)
   if (expert_ids) {
@@ -195,7 +219,7 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
       pos = s_cnt[wave][key] + rank;
       if (sorted_ids && pos < max_padded) sorted_ids[pos] = static_cast<int32_t>(i);
     }
-    if (inv_pos && i < hi) inv_pos[i] = pos;
+    if (inv_pos && i < hi) inv_pos[inv_index(i, xf)] = pos;
     __syncthreads();
     if (key != kInvalidKey && rank == 0) s_cnt[wave][key] += cnt;
     __syncthreads();
@@ -222,14 +246,14 @@ template <typename Id>
 __global__ __launch_bounds__(256) void chunk_count_kernel(
     const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
     const int32_t* __restrict__ map, int num_keys, int64_t chunk,
-    int32_t* __restrict__ cnt) {
+    int32_t* __restrict__ cnt, KeyXform xf) {
   __shared__ int s[kMaxKeys];
   for (int e = threadIdx.x; e < num_keys; e += 256) s[e] = 0;
   __syncthreads();
   const int64_t lo = static_cast<int64_t>(blockIdx.x) * chunk;
   const int64_t hi = lo + chunk < numel ? lo + chunk : numel;
   for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
-    const uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+    const uint32_t key = load_key(ids, i, id_bound, map, num_keys, xf);
     if (key != kInvalidKey) atomicAdd(&s[key], 1);
   }
   __syncthreads();
@@ -288,7 +312,7 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
     const int32_t* __restrict__ tot, int block_size,
     int32_t* __restrict__ sorted_ids, int64_t max_padded,
     int32_t* __restrict__ expert_ids, int64_t max_blocks,
-    int32_t* __restrict__ inv_pos, int32_t pad_value) {
+    int32_t* __restrict__ inv_pos, int32_t pad_value, KeyXform xf) {
   __shared__ int s_cnt[4][kMaxKeys];
   __shared__ int s_cum[kMaxKeys + 1];
   __shared__ int s_tot[kMaxKeys];
@@ -309,7 +333,7 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
   for (int s = 0; s < steps; ++s) {
     const int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
     if (i < hi) {
-      const uint32_t key = load_key(ids, i, id_bound, map, num_keys);
+      const uint32_t key = load_key(ids, i, id_bound, map, num_keys, xf);
       if (key != kInvalidKey) atomicAdd(&s_cnt[wave][key], 1);
     }
   }
@@ -332,7 +356,7 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
   for (int s = 0; s < steps; ++s) {
     const int64_t i = lo + static_cast<int64_t>(s) * 64 + lane;
     uint32_t key = kInvalidKey;
-    if (i < hi) key = load_key(ids, i, id_bound, map, num_keys);
+    if (i < hi) key = load_key(ids, i, id_bound, map, num_keys, xf);
     unsigned long long same = ~0ull;
 #pragma unroll
     for (int b = 0; b < 11; ++b) {
@@ -346,7 +370,7 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
       pos = s_cnt[wave][key] + rank;
       if (sorted_ids && pos < max_padded) sorted_ids[pos] = static_cast<int32_t>(i);
     }
-    if (inv_pos && i < hi) inv_pos[i] = pos;
+    if (inv_pos && i < hi) inv_pos[inv_index(i, xf)] = pos;
     if (key != kInvalidKey && rank == 0) s_cnt[wave][key] += cnt;
   }
 
@@ -364,7 +388,7 @@ __global__ __launch_bounds__(256) void chunk_scatter_kernel(
   if (sorted_ids) {
     for (int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + tid; p < max_padded; p += stride) {
       if (p >= total_padded) {
-        sorted_ids[p] = pad_value;
+        if (!xf.keep_tail) sorted_ids[p] = pad_value;
       } else {
         const int e = expert_at(static_cast<int>(p));
         if (p - s_cum[e] >= s_tot[e]) sorted_ids[p] = pad_value;
@@ -470,12 +494,12 @@ void launch_sort(const void* ids, int64_t numel, int64_t id_bound,
                  const int32_t* map, int num_keys, int bs, int32_t* sorted,
                  int64_t max_padded, int32_t* eids, int64_t max_blocks,
                  int32_t* ntp, int32_t* inv, int32_t* counts, int32_t* cum_out,
-                 int32_t pad, int32_t* ws, hipStream_t st) {
+                 int32_t pad, int32_t* ws, hipStream_t st, KeyXform xf) {
   const Id* id = static_cast<const Id*>(ids);
   if (!ws) {
     counting_sort_kernel<Id><<<1, kSortThreads, 0, st>>>(
         id, numel, id_bound, map, num_keys, bs, sorted, max_padded, eids,
-        max_blocks, ntp, inv, counts, cum_out, pad);
+        max_blocks, ntp, inv, counts, cum_out, pad, LoraSel{}, xf);
     return;
   }
   const int64_t chunk = sort_chunk(numel);
@@ -484,12 +508,12 @@ void launch_sort(const void* ids, int64_t numel, int64_t id_bound,
   int32_t* cum = cnt + static_cast<int64_t>(nchunks) * num_keys;
   int32_t* tot = cum + num_keys + 1;
   chunk_count_kernel<Id><<<nchunks, 256, 0, st>>>(id, numel, id_bound, map,
-                                                   num_keys, chunk, cnt);
+                                                   num_keys, chunk, cnt, xf);
   chunk_scan_kernel<<<1, kSortThreads, 0, st>>>(cnt, nchunks, num_keys, bs, cum,
                                                 tot, ntp, counts, cum_out);
   chunk_scatter_kernel<Id><<<nchunks, 256, 0, st>>>(
       id, numel, id_bound, map, num_keys, chunk, cnt, cum, tot, bs, sorted,
-      max_padded, eids, max_blocks, inv, pad);
+      max_padded, eids, max_blocks, inv, pad, xf);
 }
 
 }  // namespace
@@ -508,7 +532,10 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t bs, int32_t* sorted, int64_t max_padded,
                       int32_t* eids, int64_t max_blocks, int32_t* ntp,
                       int32_t* inv, int32_t* counts, int32_t pad,
-                      void* ws, size_t ws_bytes, hipStream_t st, int32_t* cum_out) {
+                      void* ws, size_t ws_bytes, hipStream_t st, int32_t* cum_out,
+                      int64_t id_start, int dedupe_k, int64_t inv_rows) {
+  // the prologue's sort (dedupe_k > 0) writes only the sorted slots
+  const KeyXform xf{id_start, dedupe_k, dedupe_k > 0, dedupe_k > 0 ? inv_rows : 0};
   MI_ARG(num_keys > 0 && num_keys <= kMaxKeys,
          "padded_num_experts must be less than 1024");
   MI_ARG(bs > 0, "block_size must be positive");
@@ -517,13 +544,13 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
   int32_t* w = (need > 0 && ws && ws_bytes >= need) ? static_cast<int32_t*>(ws) : nullptr;
   switch (ids_dtype) {
     case MI355MOE_I32:
-      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st);
+      launch_sort<int32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st, xf);
       break;
     case MI355MOE_I64:
-      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st);
+      launch_sort<int64_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st, xf);
       break;
     case MI355MOE_U32:
-      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st);
+      launch_sort<uint32_t>(ids, numel, id_bound, map, (int)num_keys, (int)bs, sorted, max_padded, eids, max_blocks, ntp, inv, counts, cum_out, pad, w, st, xf);
       break;
     default:
       return set_error(MI355MOE_ERR_INVALID, "topk_ids must be int32, int64 or uint32");

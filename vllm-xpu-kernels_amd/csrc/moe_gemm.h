@@ -186,13 +186,20 @@ int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
                            int64_t max_blocks, void* qs, hipStream_t st);
 
 size_t counting_sort_ws_bytes(int64_t numel, int64_t num_keys);
+// Stable counting sort of ids into expert order (align.hip).  id_start and
+// dedupe_k > 0 select the fused_moe_prologue form: keys are id - id_start,
+// only the first occurrence of an expert among a token's dedupe_k ids is
+// kept, sorted entries past the last sorted slot are left as they were, and
+// with inv_rows > 0 the position of slot t * dedupe_k + j goes to
+// inv[j * inv_rows + t].
 int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       int64_t id_bound, const int32_t* map, int64_t num_keys,
                       int64_t bs, int32_t* sorted, int64_t max_padded,
                       int32_t* eids, int64_t max_blocks, int32_t* ntp,
                       int32_t* inv, int32_t* counts, int32_t pad,
                       void* ws, size_t ws_bytes, hipStream_t st,
-                      int32_t* cum_out = nullptr);
+                      int32_t* cum_out = nullptr, int64_t id_start = 0,
+                      int dedupe_k = 0, int64_t inv_rows = 0);
 // K stages per split of the STREAM family for a GEMM of n_tiles output tiles
 // over about `blocks` expert blocks (1: no split)
 int stream_ksplit(int64_t n_tiles, int64_t blocks, int64_t K);

@@ -270,6 +270,62 @@ void moe_lora_align_block_size(at::Tensor topk_ids, at::Tensor token_lora_mappin
            "moe_lora_align_block_size");
 }
 
+// Input / scale pairs as the reference dispatches them
+// (fused_moe_prologue.cpp:186-215): bf16 and fp16 without scales (given
+// scales are ignored), e4m3 with f32 or e8m0 scales, packed e2m1 with e8m0.
+void fused_moe_prologue(at::Tensor input, const std::optional<at::Tensor>& input_scales,
+                        at::Tensor token_selected_experts, at::Tensor token_final_scales,
+                        at::Tensor workspace, int64_t hidden_size, int64_t inter_size,
+                        int64_t block_k, int64_t ep_rank, int64_t ep_size,
+                        int64_t num_experts_on_rank) {
+  check_gpu(input, "input");
+  check_gpu(token_selected_experts, "token_selected_experts");
+  check_gpu(token_final_scales, "token_final_scales");
+  check_gpu(workspace, "workspace");
+  TORCH_CHECK(input.dim() == 2 && input.size(1) == hidden_size,
+              "input must be [num_rows, hidden_size]");
+  TORCH_CHECK(token_selected_experts.dim() == 2 &&
+                  token_selected_experts.size(0) == input.size(0),
+              "token_selected_experts must be [num_rows, experts_per_token]");
+  TORCH_CHECK(token_selected_experts.scalar_type() == at::kLong ||
+                  token_selected_experts.scalar_type() == at::kInt,
+              "token_selected_experts must be int64");
+  TORCH_CHECK(token_final_scales.scalar_type() == at::kFloat &&
+                  token_final_scales.sizes() == token_selected_experts.sizes(),
+              "token_final_scales must be float32 [num_rows, experts_per_token]");
+  TORCH_CHECK(workspace.scalar_type() == at::kByte && workspace.is_contiguous(),
+              "workspace must be a contiguous uint8 tensor");
+  const auto dt = input.scalar_type();
+  int64_t elem_bytes = 0, scale_bytes = 0;
+  const void* scales = nullptr;
+  if (dt == at::kBFloat16 || dt == at::kHalf) {
+    elem_bytes = 2;
+  } else if (dt == at::kFloat8_e4m3fn || dt == at::kFloat4_e2m1fn_x2) {
+    elem_bytes = 1;
+    TORCH_CHECK(input_scales.has_value(), "fp8 and fp4 inputs need input_scales");
+    const auto sdt = input_scales->scalar_type();
+    TORCH_CHECK(sdt == at::kFloat8_e8m0fnu || (dt == at::kFloat8_e4m3fn && sdt == at::kFloat),
+                "input_scales must be e8m0 (or float32 with e4m3 input)");
+    check_gpu(*input_scales, "input_scales");
+    TORCH_CHECK(block_k > 0 && hidden_size % block_k == 0 &&
+                    input_scales->numel() == input.size(0) * (hidden_size / block_k),
+                "input_scales must be [num_rows, hidden_size / block_k]");
+    scale_bytes = sdt == at::kFloat ? 4 : 1;
+    scales = input_scales->data_ptr();
+  } else {
+    TORCH_CHECK(false, "fused_moe_prologue: unsupported input dtype ", dt);
+  }
+  DevGuard g(input.device());
+  check_rc(mi355moe_fused_moe_prologue(
+               input.data_ptr(), elem_bytes, scales, scale_bytes,
+               token_selected_experts.data_ptr(), dtype_code(token_selected_experts.scalar_type()),
+               token_final_scales.data_ptr<float>(), workspace.data_ptr(),
+               static_cast<size_t>(workspace.numel()), input.size(0), hidden_size, inter_size,
+               block_k, token_selected_experts.size(1), ep_rank, ep_size, num_experts_on_rank,
+               cur_stream(input)),
+           "fused_moe_prologue");
+}
+
 void remap_hidden_states(at::Tensor& hidden_states,
                          const std::optional<at::Tensor>& hidden_states_scales,
                          at::Tensor& remapped_hidden_states,
@@ -854,6 +910,10 @@ TORCH_LIBRARY(_moe_C, m) {
         "input_ids=None, Tensor? tid2eid=None) -> ()");
   m.def("moe_gather(Tensor! output, Tensor moe_output, Tensor topk_weights, "
         "Tensor unpermuted_row_to_permuted_row, int num_experts) -> ()");
+  m.def("fused_moe_prologue(Tensor input, Tensor? input_scales, Tensor "
+        "token_selected_experts, Tensor token_final_scales, Tensor workspace, int "
+        "hidden_size, int inter_size, int block_k, int ep_rank, int ep_size,int "
+        "num_experts_on_rank) -> ()");
   m.def("init_expert_map(Tensor expert_map, int num_experts, int ep_rank, int "
         "ep_size) -> ()");
   m.def("remap_hidden_states(Tensor hidden_states, Tensor? hidden_states_scales, "
@@ -879,6 +939,7 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("topk_sigmoid", &topk_sigmoid);
   m.impl("topk_softplus_sqrt", &topk_softplus_sqrt);
   m.impl("moe_gather", &moe_gather);
+  m.impl("fused_moe_prologue", &fused_moe_prologue);
   m.impl("init_expert_map", &init_expert_map);
   m.impl("remap_hidden_states", &remap_hidden_states);
   m.impl("mi355_fused_moe", &mi355_fused_moe);

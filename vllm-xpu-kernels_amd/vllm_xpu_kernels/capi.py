@@ -51,6 +51,33 @@ lib.mi355moe_timer_stage_ms.argtypes = [ctypes.c_void_p, ctypes.c_int,
                                         ctypes.POINTER(ctypes.c_float)]
 
 
+lib.mi355moe_fused_moe_prologue_workspace_layout.restype = ctypes.c_size_t
+lib.mi355moe_fused_moe_prologue_workspace_layout.argtypes = (
+    [ctypes.c_int64] * 7 + [ctypes.POINTER(ctypes.c_size_t)] * 2)
+
+PROLOGUE_SECTIONS = ("permuted_row_to_unpermuted_row", "permuted_token_selected_experts",
+                     "unpermuted_row_to_permuted_row", "blocked_expert_counts",
+                     "blocked_expert_counts_cumsum", "blocked_row_to_unpermuted_row",
+                     "expert_first_token_offset", "permuted_token_final_scales",
+                     "overlapped_gemm1_gemm2_inputs", "permuted_act_scales")
+
+
+def prologue_layout(num_rows: int, experts_per_token: int, hidden_size: int,
+                    elem_bytes: int, block_k: int, scale_bytes: int,
+                    num_experts_on_rank: int) -> tuple[int, dict]:
+    """Total bytes and {section: (padded size, offset)} of the
+    fused_moe_prologue workspace (the reference's ``ws_map``)."""
+    off = (ctypes.c_size_t * len(PROLOGUE_SECTIONS))()
+    size = (ctypes.c_size_t * len(PROLOGUE_SECTIONS))()
+    total = lib.mi355moe_fused_moe_prologue_workspace_layout(
+        num_rows, experts_per_token, hidden_size, elem_bytes, block_k, scale_bytes,
+        num_experts_on_rank, off, size)
+    if total == 0:
+        raise ValueError("invalid fused_moe_prologue sizes")
+    return int(total), {n: (int(size[i]), int(off[i]))
+                        for i, n in enumerate(PROLOGUE_SECTIONS)}
+
+
 def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 

@@ -136,6 +136,16 @@ def moe_lora_align_block_size(topk_ids: torch.Tensor,
         num_tokens_post_pad, adapter_enabled, lora_ids, expert_map)
 
 
+def fused_moe_prologue(input: torch.Tensor, input_scales: Optional[torch.Tensor],
+                       token_selected_experts: torch.Tensor,
+                       token_final_scales: torch.Tensor, workspace: torch.Tensor,
+                       hidden_size: int, inter_size: int, block_k: int,
+                       ep_rank: int, ep_size: int, num_experts_on_rank: int) -> None:
+    torch.ops._moe_C.fused_moe_prologue(
+        input, input_scales, token_selected_experts, token_final_scales, workspace,
+        hidden_size, inter_size, block_k, ep_rank, ep_size, num_experts_on_rank)
+
+
 def moe_sum(inp: torch.Tensor, out: torch.Tensor,
             topk_ids: Optional[torch.Tensor] = None,
             expert_map: Optional[torch.Tensor] = None) -> None:
