@@ -29,6 +29,35 @@ struct Vec8 {  // 8 elements of a 16-bit type in one uint4
   }
 };
 
+// 8 consecutive elements from index i (a multiple of 8): 16-byte loads when
+// VEC (the base pointer is 16-byte aligned), element loads otherwise.
+template <typename E, bool VEC>
+__device__ __forceinline__ void load8(const void* p, int64_t i, float* f) {
+  if constexpr (VEC && sizeof(typename E::T) == 2) {
+    Vec8<E>::load(static_cast<const uint16_t*>(p) + i, f);
+  } else if constexpr (VEC) {
+    const uint4* q = reinterpret_cast<const uint4*>(static_cast<const float*>(p) + i);
+    const uint4 a = q[0], b = q[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = __uint_as_float(w[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = E::ld(static_cast<const typename E::T*>(p)[i + k]);
+  }
+}
+
+// Quantised outputs are written once and read by a later kernel:
+// non-temporal stores.
+typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void store_nt(uint8_t* p, uint32_t lo, uint32_t hi) {
+  nt_u32x2 v = {lo, hi};
+  __builtin_nontemporal_store(v, reinterpret_cast<nt_u32x2*>(p));
+}
+__device__ __forceinline__ void store_nt(uint8_t* p, uint32_t w) {
+  __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
+}
+
 template <typename E>
 __device__ __forceinline__ float ldx(const void* p, int64_t i) {
   return E::ld(static_cast<const typename E::T*>(p)[i]);
@@ -160,7 +189,7 @@ __global__ __launch_bounds__(256) void relu2_kernel(void* __restrict__ out,
 // ----------------------------------------------------------- quantisation
 // One group of G elements is owned by G/8 consecutive lanes (8 elements per
 // lane); requires G % 8 == 0 and G/8 a power of two <= 64.
-template <typename E>
+template <typename E, bool VEC>
 __global__ __launch_bounds__(256) void group_fp8_quant_kernel(
     const void* __restrict__ in, uint8_t* __restrict__ q,
     float* __restrict__ s, int64_t rows, int64_t cols, int group, float eps,
@@ -173,8 +202,7 @@ __global__ __launch_bounds__(256) void group_fp8_quant_kernel(
   const bool active = g < ngroups;
   const int64_t base = (active ? g : 0) * group + sub * 8;
   float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = active ? ldx<E>(in, base + i) : 0.f;
+  load8<E, VEC>(in, base, v);
   float amax = eps;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -191,7 +219,7 @@ __global__ __launch_bounds__(256) void group_fp8_quant_kernel(
     uint32_t b = f32_to_e4m3(x);
     if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
   }
-  *reinterpret_cast<uint2*>(q + base) = make_uint2(lo, hi);
+  store_nt(q + base, lo, hi);
 }
 
 __device__ __forceinline__ uint32_t fp4_code(float x) {
@@ -202,7 +230,7 @@ __device__ __forceinline__ uint32_t fp4_code(float x) {
 }
 
 // mxfp4: groups of 32 owned by 4 lanes x 8 elements.
-template <typename E>
+template <typename E, bool VEC>
 __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
     const void* __restrict__ in, uint8_t* __restrict__ q,
     float* __restrict__ s, int64_t rows, int64_t cols, float eps) {
@@ -213,8 +241,7 @@ __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
   const bool active = g < ngroups;
   const int64_t base = (active ? g : 0) * 32 + sub * 8;
   float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = active ? ldx<E>(in, base + i) : 0.f;
+  load8<E, VEC>(in, base, v);
   float amax = eps;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -230,7 +257,7 @@ __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
     float x = fminf(fmaxf(v[i] * inv, -6.0f), 6.0f);
     packed |= fp4_code(x) << (4 * i);
   }
-  *reinterpret_cast<uint32_t*>(q + base / 2) = packed;
+  store_nt(q + base / 2, packed);
 }
 
 // --------------------------------------------- fused SiLU-and-mul + quant
@@ -258,8 +285,12 @@ enum QOut { Q_E4M3 = 0, Q_E5M2 = 1, Q_I8 = 2 };
 
 // silu(g) * u in fp32 with no intermediate rounding, as both fused
 // quantisers compute it.
+// silu(g) * u in fp32 with the hardware exp2 and reciprocal (about 1 ulp
+// each; the division of the quantisers below stays exact).  Saturates
+// cleanly: g -> -inf gives g * rcp(inf) = -0.
 __device__ __forceinline__ float silu_mul_f32(float g, float u) {
-  return (g / (1.f + expf(-g))) * u;
+  const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  return g * __builtin_amdgcn_rcpf(1.f + e) * u;
 }
 
 // One lane: 8 consecutive output columns c0..c0+7 of row r (16 bytes of gate
@@ -314,7 +345,7 @@ __global__ __launch_bounds__(256) void silu_mul_block_quant_kernel(
     }
     if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
   }
-  *reinterpret_cast<uint2*>(q + r * hidden + c0) = make_uint2(lo, hi);
+  store_nt(q + r * hidden + c0, lo, hi);
 }
 
 // mxfp4: groups of 32 columns, 4 lanes each.
@@ -347,7 +378,7 @@ __global__ __launch_bounds__(256) void silu_mul_mxfp4_quant_kernel(
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     packed |= fp4_code(fminf(fmaxf(v[i] * inv, -6.0f), 6.0f)) << (4 * i);
-  *reinterpret_cast<uint32_t*>(q + (r * hidden + c0) / 2) = packed;
+  store_nt(q + (r * hidden + c0) / 2, packed);
 }
 
 // -------------------------------------------------------------- reductions
@@ -517,8 +548,13 @@ extern "C" int mi355moe_per_token_group_fp8_quant(
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t threads = rows * cols / 8;
   dim3 grid(static_cast<unsigned>(cdiv(threads, 256)));
-  MI_DISPATCH_FLOAT(dt, (group_fp8_quant_kernel<E><<<grid, dim3(256), 0, st>>>(in, static_cast<uint8_t*>(q), s, rows, cols, (int)group, eps, fp8_max, ue8m0)),
-                    "per_token_group_fp8_quant: unsupported dtype")
+  if ((reinterpret_cast<uintptr_t>(in) & 15) == 0) {
+    MI_DISPATCH_FLOAT(dt, (group_fp8_quant_kernel<E, true><<<grid, dim3(256), 0, st>>>(in, static_cast<uint8_t*>(q), s, rows, cols, (int)group, eps, fp8_max, ue8m0)),
+                      "per_token_group_fp8_quant: unsupported dtype")
+  } else {
+    MI_DISPATCH_FLOAT(dt, (group_fp8_quant_kernel<E, false><<<grid, dim3(256), 0, st>>>(in, static_cast<uint8_t*>(q), s, rows, cols, (int)group, eps, fp8_max, ue8m0)),
+                      "per_token_group_fp8_quant: unsupported dtype")
+  }
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }
@@ -532,8 +568,13 @@ extern "C" int mi355moe_per_token_group_quant_mxfp4(
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t threads = rows * cols / 8;
   dim3 grid(static_cast<unsigned>(cdiv(threads, 256)));
-  MI_DISPATCH_FLOAT(dt, (group_mxfp4_quant_kernel<E><<<grid, dim3(256), 0, st>>>(in, q, s, rows, cols, eps)),
-                    "per_token_group_quant_mxfp4: unsupported dtype")
+  if ((reinterpret_cast<uintptr_t>(in) & 15) == 0) {
+    MI_DISPATCH_FLOAT(dt, (group_mxfp4_quant_kernel<E, true><<<grid, dim3(256), 0, st>>>(in, q, s, rows, cols, eps)),
+                      "per_token_group_quant_mxfp4: unsupported dtype")
+  } else {
+    MI_DISPATCH_FLOAT(dt, (group_mxfp4_quant_kernel<E, false><<<grid, dim3(256), 0, st>>>(in, q, s, rows, cols, eps)),
+                      "per_token_group_quant_mxfp4: unsupported dtype")
+  }
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }
