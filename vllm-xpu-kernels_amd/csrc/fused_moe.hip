@@ -58,24 +58,43 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
   const int64_t h0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
   if (h0 >= H) return;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int j = 0; j < topk; ++j) {
+  auto routed = [&](int j) {  // the slot's expert is on this rank
     int64_t id = static_cast<int64_t>(ids[t * topk + j]);
     if (map) {
-      if (id < 0 || id >= map_len) continue;
+      if (id < 0 || id >= map_len) return false;
       id = map[id];
     }
-    if (id < 0 || id >= num_experts) continue;
-    const float wj = w[t * topk + j];
-    const uint16_t* row = g2 + (t * topk + j) * H + h0;
-    if ((H & 7) == 0) {
-      uint4 u = *reinterpret_cast<const uint4*>(row);
-      uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+    return id >= 0 && id < num_experts;
+  };
+  if ((H & 7) == 0) {
+    // four slots' rows in flight at a time, summed in slot order
+    for (int j0 = 0; j0 < topk; j0 += 4) {
+      bool ok[4];
+      uint4 u[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += wj * ld16<F16>(static_cast<uint16_t>(wd[i] & 0xFFFF));
-        acc[2 * i + 1] += wj * ld16<F16>(static_cast<uint16_t>(wd[i] >> 16));
+      for (int q = 0; q < 4; ++q) {
+        const int j = j0 + q;
+        ok[q] = j < topk && routed(j);
+        const int64_t slot = t * topk + (ok[q] ? j : 0);
+        u[q] = *reinterpret_cast<const uint4*>(g2 + slot * H + h0);
       }
-    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (!ok[q]) continue;
+        const float wj = w[t * topk + j0 + q];
+        const uint32_t wd[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += wj * ld16<F16>(static_cast<uint16_t>(wd[i] & 0xFFFF));
+          acc[2 * i + 1] += wj * ld16<F16>(static_cast<uint16_t>(wd[i] >> 16));
+        }
+      }
+    }
+  } else {
+    for (int j = 0; j < topk; ++j) {
+      if (!routed(j)) continue;
+      const float wj = w[t * topk + j];
+      const uint16_t* row = g2 + (t * topk + j) * H + h0;
       for (int i = 0; i < 8 && h0 + i < H; ++i) acc[i] += wj * ld16<F16>(row[i]);
     }
   }
