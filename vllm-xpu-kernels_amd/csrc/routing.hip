@@ -35,19 +35,51 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);
 }
 
+// One in-row step of wave_argmax: every lane compares with the lane that
+// the DPP control CTRL names inside its row of 16.
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float& v, float& aux, int& idx) {
+  const float ov = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+  const float oa = __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(aux), CTRL, 0xF, 0xF, false));
+  const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xF, 0xF, false);
+  if (better(ov, oi, v, idx)) {
+    v = ov;
+    aux = oa;
+    idx = oi;
+  }
+}
+
 // Wave-wide argmax over (value, index) pairs; every lane gets the winner.
+// (value, index) pairs are distinct (or identical), so the winner does not
+// depend on the reduction order.  Within each row of 16 lanes: DPP quad
+// permutations (lane ^ 1, lane ^ 2), then the half-row and row mirrors,
+// which pair each lane with one of the other quad / half-row once those
+// agree; the four row winners (lanes 0, 16, 32, 48) are then read as
+// wave-uniform values.  All 64 lanes must be active.
 __device__ __forceinline__ void wave_argmax(float& v, float& aux, int& idx) {
+  argmax_dpp_step<0xB1>(v, aux, idx);   // quad_perm [1,0,3,2]
+  argmax_dpp_step<0x4E>(v, aux, idx);   // quad_perm [2,3,0,1]
+  argmax_dpp_step<0x141>(v, aux, idx);  // row_half_mirror
+  argmax_dpp_step<0x140>(v, aux, idx);  // row_mirror
+  float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float ba = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aux), 0));
+  int bi = __builtin_amdgcn_readlane(idx, 0);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o, 64);
-    float oa = __shfl_xor(aux, o, 64);
-    int oi = __shfl_xor(idx, o, 64);
-    if (better(ov, oi, v, idx)) {
-      v = ov;
-      aux = oa;
-      idx = oi;
+  for (int r = 16; r < 64; r += 16) {
+    const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
+    const float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aux), r));
+    const int ri = __builtin_amdgcn_readlane(idx, r);
+    if (better(rv, ri, bv, bi)) {
+      bv = rv;
+      ba = ra;
+      bi = ri;
     }
   }
+  v = bv;
+  aux = ba;
+  idx = bi;
 }
 
 enum GateMode { GATE_SOFTMAX = 0, GATE_SIGMOID = 1, GATE_SOFTPLUS_SQRT = 2 };
