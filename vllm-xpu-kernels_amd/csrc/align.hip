@@ -13,6 +13,8 @@
 // key bit), so no atomics decide the order.  Replaces the reference's
 // count + device-atomic scatter (csrc/moe/moe_align_sum_kernels.cpp:135-455),
 // whose within-expert order is not deterministic.
+#include <type_traits>
+
 #include "common.h"
 #include "moe_gemm.h"
 
@@ -98,14 +100,14 @@ struct LoraSel {
 };
 
 template <typename Id, bool LORA = false>
-__global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
+__device__ __forceinline__ void counting_sort_body(
     const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
     const int32_t* __restrict__ map, int num_keys, int block_size,
     int32_t* __restrict__ sorted_ids, int64_t max_padded,
     int32_t* __restrict__ expert_ids, int64_t max_blocks,
     int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
     int32_t* __restrict__ counts_out, int32_t* __restrict__ cum_out,
-    int32_t pad_value, LoraSel lora = {}, KeyXform xf = {}) {
+    int32_t pad_value, LoraSel lora, KeyXform xf) {
   __shared__ int s_cnt[kSortWaves][kMaxKeys];
   __shared__ int s_cum[kMaxKeys + 1];
   __shared__ int s_wave_tot[kSortWaves];
@@ -224,6 +226,43 @@ __global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
     if (key != kInvalidKey && rank == 0) s_cnt[wave][key] += cnt;
     __syncthreads();
   }
+}
+
+template <typename Id, bool LORA = false>
+__global__ __launch_bounds__(kSortThreads) void counting_sort_kernel(
+    const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
+    const int32_t* __restrict__ map, int num_keys, int block_size,
+    int32_t* __restrict__ sorted_ids, int64_t max_padded,
+    int32_t* __restrict__ expert_ids, int64_t max_blocks,
+    int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
+    int32_t* __restrict__ counts_out, int32_t* __restrict__ cum_out,
+    int32_t pad_value, LoraSel lora = {}, KeyXform xf = {}) {
+  counting_sort_body<Id, LORA>(ids, numel, id_bound, map, num_keys, block_size, sorted_ids,
+                               max_padded, expert_ids, max_blocks, ntp, inv_pos, counts_out,
+                               cum_out, pad_value, lora, xf);
+}
+
+// The fused layer's first launch at small token counts: workgroup 0 runs the
+// one-workgroup sort, workgroups 1.. quantise the activations to e4m3 with one
+// fp32 scale per 1 x 128 block (fp8_quant_block8 in common.h, the arithmetic
+// of per_token_group_fp8_quant), the two jobs being independent.
+template <typename Id, bool F16>
+__global__ __launch_bounds__(kSortThreads) void sort_quant_kernel(
+    const Id* __restrict__ ids, int64_t numel, int64_t id_bound,
+    const int32_t* __restrict__ map, int num_keys, int block_size,
+    int32_t* __restrict__ sorted_ids, int64_t max_padded,
+    int32_t* __restrict__ expert_ids, int64_t max_blocks,
+    int32_t* __restrict__ ntp, int32_t* __restrict__ inv_pos,
+    int32_t* __restrict__ cum_out, int32_t pad_value, const uint16_t* __restrict__ x,
+    uint8_t* __restrict__ xq, float* __restrict__ xs, int64_t chunks) {
+  if (blockIdx.x == 0) {
+    counting_sort_body<Id, false>(ids, numel, id_bound, map, num_keys, block_size, sorted_ids,
+                                  max_padded, expert_ids, max_blocks, ntp, inv_pos, nullptr,
+                                  cum_out, pad_value, LoraSel{}, KeyXform{});
+    return;
+  }
+  fp8_quant_block8<F16>(x, xq, xs, (static_cast<int64_t>(blockIdx.x) - 1) * kSortThreads +
+                                       threadIdx.x, chunks);
 }
 
 // ---------------------------------------------------------------------------
@@ -555,6 +594,36 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
     default:
       return set_error(MI355MOE_ERR_INVALID, "topk_ids must be int32, int64 or uint32");
   }
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+// run_counting_sort's one-workgroup form plus the e4m3 1 x 128 quantisation
+// of x [rows, cols] (16-bit, 16-byte aligned, cols % 128 == 0) in the same
+// launch.  Returns 1 (nothing launched) when the sort needs more than one
+// workgroup; the caller then runs the two steps separately.
+int run_sort_quant_fp8(const void* ids, int ids_dtype, int64_t numel, int64_t id_bound,
+                       const int32_t* map, int64_t num_keys, int64_t bs, int32_t* sorted,
+                       int64_t max_padded, int32_t* eids, int64_t max_blocks, int32_t* ntp,
+                       int32_t* inv, int32_t pad, int32_t* cum_out, const void* x, bool f16,
+                       uint8_t* xq, float* xs, int64_t rows, int64_t cols, hipStream_t st) {
+  if (numel > kOneBlockMax || num_keys <= 0 || num_keys > kMaxKeys || bs <= 0 ||
+      cols % 128 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 ||
+      (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64))
+    return 1;
+  const int64_t chunks = rows * cols / 8;
+  const dim3 grid(static_cast<unsigned>(1 + cdiv(chunks, kSortThreads)));
+  auto go = [&](auto id_tag, auto f16_tag) {
+    using Id = decltype(id_tag);
+    sort_quant_kernel<Id, decltype(f16_tag)::value><<<grid, kSortThreads, 0, st>>>(
+        static_cast<const Id*>(ids), numel, id_bound, map, static_cast<int>(num_keys),
+        static_cast<int>(bs), sorted, max_padded, eids, max_blocks, ntp, inv, cum_out, pad,
+        static_cast<const uint16_t*>(x), xq, xs, chunks);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if (ids_dtype == MI355MOE_I32) { if (f16) go(int32_t{}, T_{}); else go(int32_t{}, F_{}); }
+  else { if (f16) go(int64_t{}, T_{}); else go(int64_t{}, F_{}); }
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }

@@ -143,6 +143,45 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false)) & 0xFFu;
 }
 
+// e4m3 quantisation with one fp32 scale per 1 x 128 block, chunk c of 8
+// values (16 lanes per block, consecutive and aligned): amax from 1e-10,
+// scale = max(amax / 448, 1 / (448 * 512)), code = e4m3(clamp(v / scale))
+// with the division done as v * (1 / scale) -- the arithmetic of
+// per_token_group_fp8_quant (group 128, eps 1e-10, fp8_max 448, no ue8m0).
+// Chunks >= `chunks` are inactive but take part in the block's shuffles;
+// all 64 lanes must be active.
+template <bool F16>
+__device__ __forceinline__ void fp8_quant_block8(const uint16_t* __restrict__ x,
+                                                 uint8_t* __restrict__ q,
+                                                 float* __restrict__ s, int64_t c,
+                                                 int64_t chunks) {
+  const bool active = c < chunks;
+  const uint4 u = *reinterpret_cast<const uint4*>(x + (active ? c : 0) * 8);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
+    v[2 * i] = F16 ? f16_to_f32(lo) : bf16_to_f32(lo);
+    v[2 * i + 1] = F16 ? f16_to_f32(hi) : bf16_to_f32(hi);
+  }
+  float amax = 1e-10f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  const float ys = fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
+  if (!active) return;
+  if ((c & 15) == 0) s[c >> 4] = ys;
+  const float inv = 1.0f / ys;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t b = f32_to_e4m3(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f));
+    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+  }
+  *reinterpret_cast<uint2*>(q + c * 8) = make_uint2(lo, hi);
+}
+
 // ---------------------------------------------------------------------------
 // Wavefront (64-lane) reductions via cross-lane shuffles.
 // ---------------------------------------------------------------------------

@@ -505,20 +505,34 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     return MI355MOE_OK;
   };
 
-  if (int m = mark(0)) return m;
-  int rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
-                             a->expert_map, E, L.bm, L.sorted, L.max_padded,
-                             L.eids, L.max_blocks, L.ntp, L.inv, nullptr,
-                             static_cast<int32_t>(L.slots), L.sortws, L.sortws_bytes, st,
-                             L.cum);
-  if (rc) return rc;
-
   const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
   const bool f16 = a->act_dtype == MI355MOE_F16;  // the call's 16-bit type
   // caller-quantised hidden states (e4m3 + 1x128 scales) go to w13 as given
   const bool preq = fp8 && a->hidden_scale;
-  if (int m = mark(1)) return m;
+
+  if (int m = mark(0)) return m;
+  // up to 4096 slots: the sort and the e4m3 activation quantisation share
+  // one launch (the quantisation stage is then empty)
+  int rc = 1;
   if (fp8 && !preq) {
+    rc = run_sort_quant_fp8(a->topk_ids, a->ids_dtype, L.slots, id_bound, a->expert_map, E,
+                            L.bm, L.sorted, L.max_padded, L.eids, L.max_blocks, L.ntp, L.inv,
+                            static_cast<int32_t>(L.slots), L.cum, a->hidden_states, f16, L.xq,
+                            L.xs, T, H, st);
+    if (rc < 0) return rc;
+  }
+  const bool quantised = rc == 0;
+  if (!quantised) {
+    rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
+                           a->expert_map, E, L.bm, L.sorted, L.max_padded,
+                           L.eids, L.max_blocks, L.ntp, L.inv, nullptr,
+                           static_cast<int32_t>(L.slots), L.sortws, L.sortws_bytes, st,
+                           L.cum);
+    if (rc) return rc;
+  }
+
+  if (int m = mark(1)) return m;
+  if (fp8 && !preq && !quantised) {
     rc = group_quant_fp8(a->hidden_states, a->act_dtype, L.xq, L.xs, T, H, st);
     if (rc) return rc;
   }

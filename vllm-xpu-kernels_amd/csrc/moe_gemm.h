@@ -200,6 +200,15 @@ int run_counting_sort(const void* ids, int ids_dtype, int64_t numel,
                       void* ws, size_t ws_bytes, hipStream_t st,
                       int32_t* cum_out = nullptr, int64_t id_start = 0,
                       int dedupe_k = 0, int64_t inv_rows = 0);
+// The one-workgroup sort and the e4m3 1 x 128 quantisation of x [rows, cols]
+// (16-bit, f16 or bf16) in one launch (align.hip).  Returns 1 without
+// launching when the sort needs more than one workgroup or x does not fit
+// (16-byte alignment, cols % 128 == 0, i32 / i64 ids).
+int run_sort_quant_fp8(const void* ids, int ids_dtype, int64_t numel, int64_t id_bound,
+                       const int32_t* map, int64_t num_keys, int64_t bs, int32_t* sorted,
+                       int64_t max_padded, int32_t* eids, int64_t max_blocks, int32_t* ntp,
+                       int32_t* inv, int32_t pad, int32_t* cum_out, const void* x, bool f16,
+                       uint8_t* xq, float* xs, int64_t rows, int64_t cols, hipStream_t st);
 // K stages per split of the STREAM family for a GEMM of n_tiles output tiles
 // over about `blocks` expert blocks (1: no split)
 int stream_ksplit(int64_t n_tiles, int64_t blocks, int64_t K);
