@@ -285,6 +285,49 @@ def op_bandwidth(dev, steps):
                     "hbm_frac": round(gbps / 8000.0, 3)})
         del x
     out += prologue_bandwidth(dev, steps, g)
+    out += index_op_latency(dev, steps, g)
+    return out
+
+
+def index_op_latency(dev, steps, g):
+    """Latency of the index-only ops (bytes are small; "bytes" counts the
+    index arrays read and written once): moe_lora_align_block_size at the
+    reference test's largest case (T=4096, k=6, E=512, 32 adapters) and
+    topk_softplus_sqrt at C3's routing shape (T=8192, E=256, k=8)."""
+    from vllm_xpu_kernels import ops
+    out = []
+    T, k, E, L, bs = 4096, 6, 512, 32, 16
+    ids = torch.stack([torch.randperm(E, device=dev, generator=g)[:k] for _ in range(T)]).int()
+    tok = torch.randint(0, L, (T,), generator=g, device=dev, dtype=torch.int32)
+    mx = (ids.numel() + E * (bs - 1) + bs - 1) // bs * bs
+    nb = mx // bs
+    srt = torch.empty(L * mx, dtype=torch.int32, device=dev)
+    eid = torch.empty(L * nb, dtype=torch.int32, device=dev)
+    ntp = torch.empty(L, dtype=torch.int32, device=dev)
+    en = torch.ones(L + 1, dtype=torch.int32, device=dev)
+    lids = torch.arange(L + 1, dtype=torch.int32, device=dev)
+    logits = torch.randn(8192, 256, generator=g, device=dev)
+    cases = [("moe_lora_align_block_size T=4096 k=6 E=512 32 adapters", [T, k, E, L],
+              lambda: ops.moe_lora_align_block_size(ids, tok, E, bs, L, mx, nb, srt, eid, ntp,
+                                                    en, lids),
+              ids.numel() * 4 + T * 4 + (srt.numel() + eid.numel()) * 4),
+             ("topk_softplus_sqrt T=8192 E=256 k=8", [8192, 256, 8],
+              lambda: ops.topk_softplus_sqrt(logits, 8, True, 2.5),
+              logits.numel() * 4 + 8192 * 8 * 8)]
+    for name, shape, fn, nbytes in cases:
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / steps
+        out.append({"op": name, "input": shape, "bytes": nbytes, "us": round(us, 2),
+                    "GBps": round(nbytes / us / 1e3, 1),
+                    "hbm_frac": round(nbytes / us / 1e3 / 8000.0, 3)})
     return out
 
 
