@@ -4,15 +4,20 @@
 A step is one MoE layer call over one batch of T synthetic tokens already
 resident in HBM: routing (softmax top-k or grouped sigmoid top-k) followed by
 XpuFusedMoe.apply (alignment, w13 grouped GEMM + fused activation, w2 grouped
-GEMM, weighted top-k reduction).  The headline line is configuration C2
-(Qwen3-30B-A3B shape, bf16, T=4096); the other BASELINE configurations are
+GEMM, weighted top-k reduction).  The headline line is configuration C3
+(DeepSeek-V3 shape, fp8 e4m3 weights with 128x128 block scales, T=8192), the
+largest single-GPU configuration; the other BASELINE configurations are
 reported in the same JSON line under "sweep".
 
 Timed region: W eager warm-up steps, then K steps captured in one HIP graph
 and replayed once between two events (torch.cuda.synchronize on both sides).
-Stage durations for the roofline come from a second, eager pass in which the
-library records HIP events around each of its five launches on the same
-stream (mi355moe_fused_moe_timed).
+When one step's weights and activations are smaller than 512 MB (decode
+points), consecutive steps rotate over several copies of the expert weights
+(each an XpuFusedMoe of its own), so that the weights come from HBM rather
+than from the 256 MB last-level cache.  Stage durations for the roofline come
+from a second, eager pass (rotating the same way) in which the library records
+HIP events around each of its launches on the same stream
+(mi355moe_fused_moe_timed).
 
 Only the cpu_baseline leg imports the CPU oracle (oracle/), and only to time
 it as the reported baseline.
@@ -83,6 +88,34 @@ def _oracle_inputs(cfg, w, x, tw, ti):
             pick(w.w2_scale), pick(w.w2_bias), tw.cpu(), ids)
 
 
+def host_cpu():
+    """(model name, physical cores, logical CPUs) of this host from
+    /proc/cpuinfo, and the CPUs this process may run on."""
+    model, cores, logical = "unknown", set(), 0
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    logical += 1
+                elif k == "model name":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                    cores.add((phys, core))
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return model, len(cores) or None, logical or os.cpu_count(), usable
+
+
 def cpu_baseline(cfg, w, x, tw, ti, n_tok, budget_s=20.0):
     """Times the CPU oracle (torch on the host cores) on the first n_tok
     tokens of the workload: 1 warm-up, then the median of up to 5 runs within
@@ -97,16 +130,23 @@ def cpu_baseline(cfg, w, x, tw, ti, n_tok, budget_s=20.0):
         O.fused_moe(cfg.recipe, *args, activation=cfg.activation)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
+    model, phys, logical, usable = host_cpu()
     return {"value": n_tok / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{cfg.name} first {n_tok} of the timed batch's tokens "
-                      f"(their {int(args[-1].max()) + 1} experts), oracle/moe_oracle.py "
-                      f"fused_moe, median of {len(times)} runs, "
-                      f"{med * 1e3:.1f} ms per run, os.cpu_count()={os.cpu_count()}"}
+            "sample": f"{cfg.name} ({cfg.recipe}) first {n_tok} of the timed batch's tokens "
+                      f"(their {int(args[-1].max()) + 1} experts, weights dequantised per "
+                      f"expert inside the loop), oracle/moe_oracle.py fused_moe, median of "
+                      f"{len(times)} runs, {med * 1e3:.1f} ms per run; host {model}, "
+                      f"{phys} physical cores / {logical} logical CPUs, {usable} usable by "
+                      f"this process, torch threads {torch.get_num_threads()}"}
+
+
+ROTATE_BYTES = 512e6   # 2x the MI355X last-level cache (256 MB MALL)
+MAX_COPIES = 8
 
 
 class Point:
-    def __init__(self, cfg, T, dev, weights=None):
+    def __init__(self, cfg, T, dev, weights=None, rotate_bytes=ROTATE_BYTES):
         from vllm_xpu_kernels import workloads as W
         from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
         self.cfg, self.T, self.dev = cfg, T, dev
@@ -116,16 +156,25 @@ class Point:
         self.bias = (W.make_correction_bias(cfg, dev)
                      if cfg.routing == "grouped_sigmoid" else None)
         w = self.w
-        self.moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale,
-                               w.w2_bias, cfg.topk, cfg.activation, cfg.experts)
         self.out = torch.empty_like(self.x)
         self.tw, self.ti = W.route(cfg, self.logits, self.bias)
         self.active = int(torch.unique(self.ti).numel())
+        # every XpuFusedMoe converts (and so copies) the expert weights: steps
+        # rotate over enough copies that one pass over them exceeds
+        # rotate_bytes
+        per_step = W.algorithmic_bytes(cfg, T, self.active)
+        self.copies = int(min(MAX_COPIES, max(1, math.ceil(rotate_bytes / per_step))))
+        self.moes = [XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale,
+                                 w.w2_bias, cfg.topk, cfg.activation, cfg.experts)
+                     for _ in range(self.copies)]
+        self.moe = self.moes[0]
+        self.i = 0
 
     def step(self):
         from vllm_xpu_kernels import workloads as W
         tw, ti = W.route(self.cfg, self.logits, self.bias)
-        self.moe.apply(self.out, self.x, tw, ti)
+        self.moes[self.i % self.copies].apply(self.out, self.x, tw, ti)
+        self.i += 1
 
     def time_steps(self, steps, warmup, graph=True):
         s = torch.cuda.Stream()
@@ -159,8 +208,8 @@ class Point:
 
     def stage_times(self, steps):
         from vllm_xpu_kernels import capi
-        args = capi.fused_args(self.moe, self.out, self.x, self.tw, self.ti)
-        ws = capi.workspace_for(args, self.dev)
+        args = [capi.fused_args(m, self.out, self.x, self.tw, self.ti) for m in self.moes]
+        ws = capi.workspace_for(args[0], self.dev)
         timer = capi.StageTimer(steps)
         try:
             torch.cuda.synchronize()
@@ -169,7 +218,7 @@ class Point:
             except Exception:
                 pass
             for i in range(steps):
-                timer.run(args, ws, i)
+                timer.run(args[i % len(args)], ws, i)
             torch.cuda.synchronize()
             per = [timer.stage_ms(i) for i in range(steps)]
         finally:
@@ -189,6 +238,7 @@ def summarize(pt, ms, stages):
          "TFLOPs": round(W.algorithmic_flops(cfg, T) / t / 1e12, 2),
          "roofline_frac": round(max(t_h, t_m) / t, 4),
          "bound": "hbm" if t_h >= t_m else "mfma",
+         "weight_copies": pt.copies,
          "stage_us": {n: round(v * 1e3, 2) for n, v in zip(capi.STAGE_NAMES, stages)}}
     return d
 
@@ -378,8 +428,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="C2")
-    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--config", default="C3")
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--cpu-tokens", type=int, default=0,
+                    help="tokens of the CPU-baseline sample (0: 16 for C3, else 64)")
     ap.add_argument("--sweep", default="default",
                     help="'none', 'default' or a list like C3:1,C3:8192")
     ap.add_argument("--no-graph", action="store_true")
@@ -423,7 +475,8 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
-        cpu = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=64)
+        n_cpu = args.cpu_tokens or (16 if args.config == "C3" else 64)
+        cpu = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=min(n_cpu, args.tokens))
         log("cpu baseline:", json.dumps(cpu))
 
     op_table = None

@@ -283,3 +283,84 @@ def test_no_cpu_kernel_registered():
     out = torch.empty(2, 4)
     with pytest.raises((NotImplementedError, RuntimeError)):
         torch.ops._C.silu_and_mul(out, x)
+
+
+# Python entry points of the reference, parameter names, order and defaults as
+# written in vllm_xpu_kernels/fused_moe_interface.py (XpuFusedMoe.__init__
+# :166-180, XpuFusedMoe.apply :273-281, xpu_fused_moe :421-442).
+_EMPTY = object()
+REFERENCE_PY_SIGNATURES = {
+    "XpuFusedMoe.__init__": [
+        ("self", _EMPTY), ("w13", _EMPTY), ("w13_scales", _EMPTY), ("w13_bias", _EMPTY),
+        ("w2", _EMPTY), ("w2_scales", _EMPTY), ("w2_bias", _EMPTY),
+        ("n_experts_per_token", _EMPTY), ("activation", _EMPTY), ("num_experts", _EMPTY),
+        ("ep_rank", 0), ("ep_size", 1), ("expert_map", None), ("gemm1_clamp_limit", None)],
+    "XpuFusedMoe.apply": [
+        ("self", _EMPTY), ("output", _EMPTY), ("hidden_states", _EMPTY),
+        ("topk_weights", _EMPTY), ("topk_ids", _EMPTY), ("expert_map", None),
+        ("a1q_scale", None)],
+    "xpu_fused_moe": [
+        ("hidden_states", _EMPTY), ("w13", _EMPTY), ("w13_scales", _EMPTY),
+        ("w13_bias", _EMPTY), ("w2", _EMPTY), ("w2_scales", _EMPTY), ("w2_bias", _EMPTY),
+        ("topk_weights", _EMPTY), ("topk_ids", _EMPTY), ("n_experts_per_token", _EMPTY),
+        ("activation", _EMPTY), ("num_experts", _EMPTY), ("ep_rank", 0), ("ep_size", 1),
+        ("expert_map", None), ("output", None), ("is_fp8", False), ("is_int4", False),
+        ("is_mxfp4", False), ("is_mxfp8", False), ("is_block_fp8", False),
+        ("gemm1_clamp_limit", None)],
+}
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_PY_SIGNATURES))
+def test_python_signatures_match_reference(name):
+    import inspect
+
+    from vllm_xpu_kernels import fused_moe_interface as F
+    obj = F
+    for part in name.split("."):
+        obj = getattr(obj, part)
+    params = list(inspect.signature(obj).parameters.values())
+    got = [(p.name, _EMPTY if p.default is inspect.Parameter.empty else p.default)
+           for p in params]
+    assert got == REFERENCE_PY_SIGNATURES[name]
+    assert all(p.kind == inspect.Parameter.POSITIONAL_OR_KEYWORD for p in params)
+
+
+def _cpu_layer(monkeypatch, E=4, H=64, I=32, k=2):
+    """A bf16 XpuFusedMoe on CPU tensors (row-major layout: the constructor
+    then launches nothing)."""
+    from vllm_xpu_kernels import fused_moe_interface as F
+    monkeypatch.setenv(F.WEIGHT_LAYOUT_ENV, "nk")
+    w13 = torch.zeros(E, H, 2 * I, dtype=torch.bfloat16)
+    w2 = torch.zeros(E, I, H, dtype=torch.bfloat16)
+    return F.XpuFusedMoe(w13, None, None, w2, None, None, k, "silu", E)
+
+
+def test_apply_rejects_output_dtype_and_weight_shape(monkeypatch):
+    moe = _cpu_layer(monkeypatch)
+    x = torch.zeros(3, 64, dtype=torch.bfloat16)
+    ids = torch.zeros(3, 2, dtype=torch.int32)
+    w = torch.zeros(3, 2)
+    with pytest.raises(ValueError, match="hidden_states' dtype"):
+        moe.apply(torch.empty(3, 64, dtype=torch.float16), x, w, ids)
+    with pytest.raises(ValueError, match="bfloat16 or float16"):
+        moe.apply(torch.empty(3, 64), x.float(), w, ids)
+    with pytest.raises(ValueError, match="same shape"):
+        moe.apply(torch.empty_like(x), x, torch.zeros(3, 3), ids)
+
+
+def test_xpu_fused_moe_flags_checked_against_dtypes():
+    from vllm_xpu_kernels import fused_moe_interface as F
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    w13 = torch.zeros(4, 64, 64, dtype=torch.bfloat16)
+    w2 = torch.zeros(4, 32, 64, dtype=torch.bfloat16)
+    ids = torch.zeros(2, 2, dtype=torch.int32)
+    tw = torch.zeros(2, 2)
+    with pytest.raises(ValueError, match="is_block_fp8=True"):
+        F.xpu_fused_moe(x, w13, None, None, w2, None, None, tw, ids, 2, "silu", 4,
+                        is_block_fp8=True)
+    with pytest.raises(ValueError, match="more than one recipe flag"):
+        F.xpu_fused_moe(x, w13, None, None, w2, None, None, tw, ids, 2, "silu", 4,
+                        is_fp8=True, is_int4=True)
+    with pytest.raises(AssertionError, match="output shape"):
+        F.xpu_fused_moe(x, w13, None, None, w2, None, None, tw, ids, 2, "silu", 4,
+                        output=torch.empty(3, 64, dtype=torch.bfloat16))

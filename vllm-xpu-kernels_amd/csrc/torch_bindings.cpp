@@ -810,7 +810,18 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   check_gpu(w13, "w13");
   check_gpu(w2, "w2");
   TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
+  TORCH_CHECK(topk_weights.sizes() == topk_ids.sizes(),
+              "topk_weights must have the shape of topk_ids");
   TORCH_CHECK(output.sizes() == hidden_states.sizes(), "output must match hidden_states");
+  // The kernels write the output, and read the biases, in the call's 16-bit
+  // type: hidden_states' type, or the output's when they come quantised.
+  if (hidden_scale) {
+    TORCH_CHECK(output.scalar_type() == at::kBFloat16 || output.scalar_type() == at::kHalf,
+                "output must be bfloat16 or float16");
+  } else {
+    TORCH_CHECK(output.scalar_type() == hidden_states.scalar_type(),
+                "output must have hidden_states' dtype");
+  }
   mi355moe_fused_moe_args a{};
   a.recipe = static_cast<int>(recipe);
   a.activation = static_cast<int>(activation);

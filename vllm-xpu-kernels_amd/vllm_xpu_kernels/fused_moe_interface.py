@@ -307,16 +307,27 @@ class XpuFusedMoe:
                     "pre-quantised activations (a1q_scale) are supported for "
                     "the fp8 block-scaled recipe (e4m3 + [T, H/128] scales)")
             a1q_scale = a1q_scale.to(torch.float32).contiguous()
+        # the call's 16-bit type: that of the activations, or of the output
+        # when they come quantised; the kernels write the output, and read
+        # the biases, in it
+        dt16 = output.dtype if a1q_scale is not None else hidden_states.dtype
+        if dt16 not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"output must be bfloat16 or float16, got {dt16}")
+        if output.dtype != dt16:
+            raise ValueError(f"output ({output.dtype}) must have hidden_states' "
+                             f"dtype ({hidden_states.dtype})")
         if (self._recipe == RECIPE_BF16 and not self._fp8_expert and
                 hidden_states.dtype != self.w13.dtype):
             raise ValueError(f"hidden_states ({hidden_states.dtype}) must have the "
                              f"16-bit weights' dtype ({self.w13.dtype})")
+        if tuple(topk_weights.shape) != tuple(topk_ids.shape):
+            raise ValueError("topk_weights and topk_ids must have the same shape")
         if expert_map is None and self.ep_size > 1:
             expert_map = self.expert_map
         clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
-        b13, b2 = self._biases(output.dtype)
-        w13, w2 = self._call_weights(hidden_states.dtype)
-        s13, s2 = self._scales(hidden_states.dtype)
+        b13, b2 = self._biases(dt16)
+        w13, w2 = self._call_weights(dt16)
+        s13, s2 = self._scales(dt16)
         torch.ops._moe_C.mi355_fused_moe(
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
             topk_ids.contiguous(), w13, s13, b13, w2, s2, b2,
@@ -325,17 +336,57 @@ class XpuFusedMoe:
         return output
 
 
-def xpu_fused_moe(hidden_states, w13, w13_scales, w13_bias, w2, w2_scales,
-                  w2_bias, topk_weights, topk_ids, n_experts_per_token,
-                  activation, num_experts, ep_rank=0, ep_size=1,
-                  output=None, is_fp8=False, is_int4=False, is_mxfp4=False,
-                  expert_map=None, gemm1_clamp_limit=None):
-    """Functional entry (reference fused_moe_interface.py:421-442): builds an
-    XpuFusedMoe and applies it once."""
+def xpu_fused_moe(hidden_states,
+                  w13,
+                  w13_scales,
+                  w13_bias,
+                  w2,
+                  w2_scales,
+                  w2_bias,
+                  topk_weights,
+                  topk_ids,
+                  n_experts_per_token,
+                  activation,
+                  num_experts,
+                  ep_rank=0,
+                  ep_size=1,
+                  expert_map=None,
+                  output=None,
+                  is_fp8=False,
+                  is_int4=False,
+                  is_mxfp4=False,
+                  is_mxfp8=False,
+                  is_block_fp8=False,
+                  gemm1_clamp_limit: Optional[float] = None):
+    """Functional entry (reference fused_moe_interface.py:421-442, same
+    parameters in the same order): builds an XpuFusedMoe and applies it once.
+
+    The is_* flags name the recipe as the reference's do; the weight and
+    scale dtypes must agree with the flag that is set (the reference reads the
+    flags only, this build checks them against the tensors and raises
+    ValueError on a mismatch).  No flag set: the recipe follows the dtypes.
+    """
+    if output is None:
+        output = torch.empty_like(hidden_states)
+    else:
+        assert output.shape == hidden_states.shape, \
+            "output shape must be the same as hidden_states shape"
+    flags = {"fp8": is_fp8, "int4": is_int4, "mxfp4": is_mxfp4,
+             "mxfp8": is_mxfp8, "block_fp8": is_block_fp8}
+    asked = [k for k, v in flags.items() if v]
+    if len(asked) > 1:
+        raise ValueError(f"xpu_fused_moe: more than one recipe flag set: {asked}")
+    det = dict(zip(("fp8", "int4", "mxfp4", "mxfp8", "block_fp8"),
+                   _get_weights_dtype(w13, w13_scales)))
+    if asked and not det[asked[0]]:
+        found = [k for k, v in det.items() if v] or ["bf16"]
+        raise ValueError(f"xpu_fused_moe: is_{asked[0]}=True but w13 "
+                         f"({w13.dtype}) with scales "
+                         f"({None if w13_scales is None else w13_scales.dtype}) "
+                         f"is recipe {found[0]}")
     moe = XpuFusedMoe(w13, w13_scales, w13_bias, w2, w2_scales, w2_bias,
                       n_experts_per_token, activation, num_experts, ep_rank,
                       ep_size, expert_map, gemm1_clamp_limit)
-    if output is None:
-        output = torch.empty_like(hidden_states)
-    return moe.apply(output, hidden_states, topk_weights, topk_ids,
-                     expert_map=expert_map)
+    moe.apply(output, hidden_states, topk_weights, topk_ids,
+              expert_map=expert_map)
+    return output
