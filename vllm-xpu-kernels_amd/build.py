@@ -24,7 +24,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIP_SOURCES = ["routing.hip", "align.hip", "elementwise.hip", "moe_gemm.hip",
                "moe_gemm_big.hip", "moe_gemm_pipe.hip", "moe_gemm_stream.hip",
-               "moe_gemm_wide.hip", "moe_gemm_wide8.hip", "moe_gemm_wide4.hip", "moe_gemm_big8.hip", "fused_moe.hip", "prologue.hip", "errors.cpp"]
+               "moe_gemm_wide.hip", "moe_gemm_wide8.hip", "moe_gemm_wide8p.hip", "moe_gemm_wide4.hip", "moe_gemm_big8.hip", "fused_moe.hip", "prologue.hip", "errors.cpp"]
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # no packed fp32 (v_pk_*_f32) code generation

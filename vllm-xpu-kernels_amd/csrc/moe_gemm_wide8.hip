@@ -34,6 +34,8 @@
 // prefill kernels: a GLU tile's 256 weight rows are 128 gate rows and the
 // matching 128 up rows, so its 128 output columns are one whole 1x128
 // quantisation group of the next GEMM's input.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "mfma16.h"
@@ -504,9 +506,15 @@ int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
   const int64_t a_rows = a.a_by_pos ? max_blocks * BM : a.num_valid;
   MI_ARG(wide8_shape_ok(a_rows, a.ldb_rows, a.K),
          "fp8 prefill GEMM: activation and per-expert weight bytes must stay below 4 GiB");
-  if (qout) {
+  static const bool v1 = [] {
+    const char* e = getenv("MI355MOE_WIDE8");
+    return e && !strcmp(e, "v1");
+  }();
+  if (qout)
     MI_ARG(epi == EPI_GLU && a.N % 128 == 0,
            "fp8 activation output needs the GLU epilogue and I % 128 == 0");
+  if (!v1) return launch_moe_gemm_wide8p(epi, qout, a, max_blocks, qs, st);
+  if (qout) {
     return a.out_f16 ? launch_w8<EPI_GLU, true, true>(a, max_blocks, qs, st)
                      : launch_w8<EPI_GLU, true, false>(a, max_blocks, qs, st);
   }

@@ -1,0 +1,509 @@
+// Prefill grouped GEMM for fp8 e4m3 weights with 128x128 block scales and
+// e4m3 activations with 1x128 scales: 320-slot x 256-weight-row tiles, 8
+// waves, each wave owning 32 weight rows x all 320 slots.
+//
+// Data movement.  The direct global->LDS path moves about 16-22 bytes per
+// clock per CU, half of what plain vector loads reach, so only the operand
+// that every wave shares goes through it:
+//   * weights: every wave loads its own two 16-row fragments of the 128-K
+//     stage (4 KB, the HBM stream of the kernel) straight into VGPRs, one
+//     stage ahead (copied into the operand registers at the end of a stage);
+//   * activations: the 320 rows x 128 bytes of the stage plus their 320
+//     scales go global->LDS (global_load_lds) into a 2-slot ring, 40 rows and
+//     40 scales per wave; one barrier per stage makes a slot visible and frees
+//     the other.  They are mostly L2 hits (every N-tile of an expert reads the
+//     same rows).
+// The transfers of stage kt + 1 are issued during stage kt (weights first,
+// the activation DMA spread over the slot tiles); the copy of the weights at
+// the end of stage kt waits for them, the top of stage kt + 1 for the rest.
+//
+// Compute: per stage and wave 2 x 20 v_mfma_scale_f32_16x16x128_f8f6f4 (one
+// MFMA covers a whole 128-K scale block, unit e8m0 scales), each result
+// scaled and added with one FMA per element: acc += p * (xs * ws), the same
+// operations in the same order as the other fp8 kernels.  The 20 activation
+// fragments stream from LDS one tile ahead; slot tiles made only of padding
+// are skipped in pairs (the K loop is specialised on their number).
+//
+// LDS layout of an activation slot: rows of 128 bytes whose 16-byte chunk c
+// holds source chunk c ^ ((r >> 1) & 7) (sixteen rows read at one logical
+// chunk hit sixteen distinct bank groups), then the 320 scales ordered so
+// that lane l16 finds the scales of its slots 16 j + l16 (j = 0..19) at 20
+// consecutive floats.
+#include <type_traits>
+
+#include "mfma16.h"
+#include "moe_gemm.h"
+
+namespace mi355 {
+namespace {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+// global-address-space view of a byte pointer: loads through it are
+// global_load (scalar base + 32-bit lane offset), not FLAT loads, which
+// would also count in lgkmcnt and so be waited for with every LDS read
+typedef __attribute__((address_space(1))) const uint8_t gbyte_t;
+typedef __attribute__((address_space(1))) const i32x4_t gi32x4_t;
+
+constexpr int BM = 320, BN = 256, KE = 128;
+static_assert(BM == kWideBM, "block size of the WIDE family");
+constexpr int WAVES = 8;
+constexpr int TJ = BM / 16;                 // slot tiles per wave
+constexpr int AROWS = BM / WAVES;           // activation rows moved per wave
+constexpr int A_BYTES = BM * KE;            // 40 KB of activations per stage
+constexpr int A_SLOT = A_BYTES + BM * 4;    // + scales
+constexpr int DUMMY = 2 * A_SLOT;           // scale DMA target of waves 5-7
+constexpr int RING = DUMMY + 256;
+constexpr int MAX_KBLK = 64;                // K <= 8192
+static_assert(RING <= 150 * 1024, "LDS budget");
+static_assert(BM * (128 + 16) + 2 * BM * 4 <= RING, "fp8 output tile, scales");
+
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
+}
+// 16 (dma16) or 4 (dma4) bytes per lane from sbase + voff (scalar base,
+// 32-bit lane offset) into LDS at lds_base + 16 lane (4 lane).
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory");
+}
+__device__ __forceinline__ void dma4(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory");
+}
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
+  return reinterpret_cast<const uint8_t*>((hi << 32) | lo);
+}
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+__device__ __forceinline__ f32x4_t mfma8(const i32x8_t& a, const i32x8_t& b) {
+  const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
+}
+__device__ __forceinline__ i32x8_t ld32(const uint8_t* S, int o0, int o1) {
+  const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(S + o0);
+  const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(S + o1);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+template <bool F16>
+__device__ __forceinline__ float round16(float v) {
+  if constexpr (F16) return f16_to_f32(f32_to_f16(v));
+  else return bf16_to_f32(f32_to_bf16(v));
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t to16(float v) {
+  if constexpr (F16) return f32_to_f16(v);
+  else return f32_to_bf16(v);
+}
+__device__ __forceinline__ float x_sigmoid(float x, float k) {
+  const float e = __builtin_amdgcn_exp2f(-k * x * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.f + e);
+}
+
+template <int EPI, bool QOUT, bool F16>
+__global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
+                                                              void* __restrict__ qs) {
+  constexpr bool kGlu = EPI == EPI_GLU;
+  constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
+
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[RING];
+  __shared__ int s_arow[BM];
+  __shared__ int s_drow[BM];
+  __shared__ float s_wsc[2][MAX_KBLK];    // block scales of the tile's two row blocks
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+
+  // XCD-aware order: XCD x takes the contiguous range [x*per, (x+1)*per) of
+  // the tiles ordered by tile_coords (all N-tiles of an expert's block run
+  // side by side in one L2).
+  const int n_tiles = static_cast<int>((a.N + NOUT - 1) / NOUT);
+  const int valid = (*a.ntp / BM) * n_tiles;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int per = (valid + 7) / 8;
+  const int tile = (bid & 7) * per + (bid >> 3);
+  if ((bid >> 3) >= per || tile >= valid) return;  // uniform
+  int blk, ntile;
+  tile_coords(a, tile, n_tiles, BM, blk, ntile);
+  const int e = a.block_expert[blk];
+  const int64_t K = a.K, N = a.N;
+  const int64_t n0 = static_cast<int64_t>(ntile) * NOUT;
+  const int nkb = static_cast<int>(K / KE);
+
+  int ok = 0;
+  if (tid < BM) {
+    const int rid = a.row_ids[static_cast<int64_t>(blk) * BM + tid];
+    ok = rid >= 0 && rid < a.num_valid;
+    s_arow[tid] = ok ? (a.a_by_pos ? blk * BM + tid : rid / a.a_div) : -1;
+    s_drow[tid] = ok ? (a.d_by_pos ? blk * BM + tid : rid) : -1;
+  }
+  // weight row of tile row r (rows past N read row 0: finite data whose
+  // outputs are never stored); GLU: [0,128) gate, [128,256) up
+  auto wrow_of = [&](int r) -> int64_t {
+    if constexpr (kGlu) {
+      const int64_t c = n0 + (r & 127);
+      return (r >= 128 ? a.up_off : 0) + (c < N ? c : 0);
+    } else {
+      const int64_t c = n0 + r;
+      return c < N ? c : 0;
+    }
+  };
+  {
+    const float* bsc = static_cast<const float*>(a.b_scale);
+    for (int i = tid; i < 2 * nkb; i += 512) {
+      const int t = i / nkb, kb = i % nkb;
+      const int64_t wr = wrow_of(128 * t) / 128;
+      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wr) * nkb + kb];
+    }
+  }
+  const int v = __syncthreads_count(ok);  // valid slots form a prefix of the block
+
+  // ---- DMA addressing (per-lane 32-bit offsets, held across the K loop)
+  const uint32_t ring0 = lds_off(lds);
+  const WStride wst = w_stride8(a);
+  const uint8_t* abase = uniform_ptr(a.A);
+  const uint8_t* sbase = uniform_ptr(a.a_scale);
+  const uint8_t* wbase = uniform_ptr(static_cast<const uint8_t*>(a.B) +
+                                     static_cast<int64_t>(e) * a.ldb_rows * K);
+  const uint32_t Ku = static_cast<uint32_t>(K);
+  // activation rows 40 wave + 8 q + lane / 8, 16-byte chunk lane % 8 of the
+  // LDS row, read from source chunk (lane % 8) ^ swz(row)
+  uint32_t aoff[AROWS / 8];
+#pragma unroll
+  for (int q = 0; q < AROWS / 8; ++q) {
+    const int r = AROWS * wave + 8 * q + (lane >> 3);
+    const int ar = s_arow[r];
+    aoff[q] = static_cast<uint32_t>(ar >= 0 ? ar : 0) * Ku +
+              (static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4);
+  }
+  // scales: waves 0-4 move them, LDS position p = 64 wave + lane holding the
+  // scale of slot 16 (p % 20) + p / 20; waves 5-7 issue the same DMA (so that
+  // no branch splits the K loop) into a dummy area
+  const bool s_wave = wave < BM / 64;
+  uint32_t soff = 0;
+  {
+    const int p = s_wave ? 64 * wave + lane : lane;
+    const int ar = s_arow[16 * (p % TJ) + p / TJ];
+    soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) * static_cast<uint32_t>(nkb) * 4u;
+  }
+  // the wave's weight fragments f = 0, 1: GLU gate rows 16 wave + l16 and the
+  // matching up rows; STORE rows 32 wave + 16 f + l16.  Lane (l16, g) loads
+  // the 32 bytes at K byte 32 g of its row of the stage.
+  uint32_t woff[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int r = kGlu ? (f ? 128 : 0) + 16 * wave + l16 : 32 * wave + 16 * f + l16;
+    woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row) + 32u * static_cast<uint32_t>(g);
+  }
+  const uint32_t wkstep = static_cast<uint32_t>(wst.kblk);
+
+  // part q of the activation DMA of stage kt into ring slot `parity` & 1:
+  // q < 5 eight of the wave's 40 rows, q = 5 the scales
+  constexpr int ACT_PARTS = AROWS / 8 + 1;
+  auto issue_act_part = [&](int q, int kt, int parity) {
+    const uint32_t slot = ring0 + (parity & 1) * A_SLOT;
+    if (q < AROWS / 8) {
+      dma16(aoff[q] + static_cast<uint32_t>(kt) * KE, abase,
+            slot + (AROWS * wave + 8 * q) * KE);
+    } else {
+      dma4(soff + 4u * kt, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
+    }
+  };
+  // weight fragments of stage kt (4 x 16-byte loads)
+  const gbyte_t* wglob = reinterpret_cast<const gbyte_t*>(reinterpret_cast<uintptr_t>(wbase));
+  auto load_w = [&](int kt, i32x8_t (&w)[2]) {
+    const uint32_t kofs = static_cast<uint32_t>(kt) * wkstep;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const gbyte_t* p = wglob + (woff[f] + kofs);
+      const i32x4_t lo = *reinterpret_cast<const gi32x4_t*>(p);
+      const i32x4_t hi = *reinterpret_cast<const gi32x4_t*>(p + 16);
+      w[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+
+  // fragment offsets within an activation slot: chunks 2g and 2g + 1 of row
+  // l16 (+ 16 j rows for tile j; the swizzle depends on r % 16 only)
+  const int xo0 = l16 * KE + (((2 * g) ^ swz(l16)) << 4);
+  const int xo1 = l16 * KE + (((2 * g + 1) ^ swz(l16)) << 4);
+  // s_wsc row of fragment f: GLU gate / up block; STORE the block of rows
+  // 32 wave .. 32 wave + 31
+  const int wsel0 = kGlu ? 0 : (wave >> 2), wsel1 = kGlu ? 1 : (wave >> 2);
+  // slot tiles holding valid slots, rounded up to pairs
+  const int njv = (v + 15) / 16;
+  const int nj = njv <= 0 ? 0 : (njv >= TJ ? TJ : ((njv + 1) & ~1));
+
+  f32x4_t acc[2][TJ];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = nkb;
+  // Stage kt: the weight loads of stage kt + 1 go out right after the
+  // barrier, the six parts of its activation DMA one every second slot tile
+  // (a wave that issues them back to back stalls until the slower DMA path
+  // takes them, and computes nothing meanwhile); the weights land in `wn`,
+  // which the end of the stage copies into `wc` (the compiler waits for the
+  // loads there; the activation DMA, inline assembly it does not count, is
+  // waited for at the top of the next stage).  The last stage moves its own
+  // (in-bounds, unused) data into the free slot instead of branching around
+  // the transfers.
+  auto kloop = [&](auto nj_c) {
+    constexpr int NJ = decltype(nj_c)::value;
+    // slot tile after which part q of the activation DMA is issued (parts
+    // past the last tile follow the loop)
+    auto part_at = [](int q) { return 2 * q; };
+    i32x8_t wc[2], wn[2];
+#pragma unroll
+    for (int q = 0; q < ACT_PARTS; ++q) issue_act_part(q, 0, 0);
+    load_w(0, wc);
+    // the first stage's weights are complete before the loop: otherwise the
+    // compiler's wait for them, merged into every iteration, would also
+    // drain the next stage's activation DMA
+    asm volatile("" :: "v"(wc[0]), "v"(wc[1]));
+    for (int kt = 0; kt < nk; ++kt) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of act(kt)
+      __builtin_amdgcn_s_barrier();   // act(kt) visible; act slot (kt+1)&1 free
+      asm volatile("" ::: "memory");  // no LDS read moves above the barrier
+      const int kn = kt + 1 < nk ? kt + 1 : kt;
+      load_w(kn, wn);
+      if constexpr (NJ > 0) {
+        const float ws0 = s_wsc[wsel0][kt], ws1 = s_wsc[wsel1][kt];
+        const uint8_t* S = lds + (kt & 1) * A_SLOT;
+        const float* xsp = reinterpret_cast<const float*>(S + A_BYTES) + TJ * l16;
+        // software pipeline: the scaling FMAs of slot tile j-1 follow the
+        // MFMAs of tile j, so no wave waits for its own MFMA results
+        i32x8_t x = ld32(S, xo0, xo1);
+        f32x4_t q0 = {0.f, 0.f, 0.f, 0.f}, q1 = q0;
+        float qs = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          i32x8_t xn = x;
+          if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
+          const float xs = xsp[j];
+          const f32x4_t p0 = mfma8(wc[0], x);
+          const f32x4_t p1 = mfma8(wc[1], x);
+#pragma unroll
+          for (int q = 0; q < ACT_PARTS; ++q)
+            if (part_at(q) == j) issue_act_part(q, kn, kt + 1);
+          if (j > 0) {
+            const float s0 = qs * ws0, s1 = qs * ws1;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc[0][j - 1][r] += q0[r] * s0;
+              acc[1][j - 1][r] += q1[r] * s1;
+            }
+          }
+          q0 = p0;
+          q1 = p1;
+          qs = xs;
+          x = xn;
+        }
+        {
+          const float s0 = qs * ws0, s1 = qs * ws1;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[0][NJ - 1][r] += q0[r] * s0;
+            acc[1][NJ - 1][r] += q1[r] * s1;
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < ACT_PARTS; ++q)
+        if (part_at(q) >= NJ) issue_act_part(q, kn, kt + 1);
+      wc[0] = wn[0];
+      wc[1] = wn[1];
+    }
+  };
+  switch (nj) {
+    case 20: kloop(std::integral_constant<int, 20>{}); break;
+    case 18: kloop(std::integral_constant<int, 18>{}); break;
+    case 16: kloop(std::integral_constant<int, 16>{}); break;
+    case 14: kloop(std::integral_constant<int, 14>{}); break;
+    case 12: kloop(std::integral_constant<int, 12>{}); break;
+    case 10: kloop(std::integral_constant<int, 10>{}); break;
+    case 8: kloop(std::integral_constant<int, 8>{}); break;
+    case 6: kloop(std::integral_constant<int, 6>{}); break;
+    case 4: kloop(std::integral_constant<int, 4>{}); break;
+    case 2: kloop(std::integral_constant<int, 2>{}); break;
+    default: kloop(std::integral_constant<int, 0>{}); break;
+  }
+  static_assert(TJ == 20, "kloop variants cover the even tile counts up to TJ");
+
+  // ---- epilogue: lane holds slot 16 j + l16, rows 4 g + r of fragment f
+  const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // the ring is free
+  // output column (within the tile) of (fragment f, reg r)
+  auto tcol = [&](int f, int r) -> int {
+    return (kGlu ? 16 * wave : 32 * wave + 16 * f) + 4 * g + r;
+  };
+  constexpr int NF = kGlu ? 1 : 2;
+  auto outv = [&](int f, int j, float (&o)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float bg = 0.f, bu = 0.f;
+      if (a.bias) {
+        const int64_t n = n0 + tcol(f, r);
+        if (n < N) {
+          bg = ld16<F16>(a.bias[bias_base + n]);
+          if constexpr (kGlu) bu = ld16<F16>(a.bias[bias_base + a.up_off + n]);
+        }
+      }
+      float gv = round16<F16>(acc[f][j][r] + bg);
+      if constexpr (kGlu) {
+        float u = round16<F16>(acc[1][j][r] + bu);
+        if (a.clamp_limit > 0.f) {
+          gv = round16<F16>(fminf(gv, a.clamp_limit));
+          u = round16<F16>(fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit));
+        }
+        float y;
+        if (a.act == MI355MOE_ACT_SILU) {
+          y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
+        } else {
+          gv = gv > a.limit ? a.limit : gv;
+          u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+          y = (u + 1.f) * x_sigmoid(gv, a.alpha);
+        }
+        gv = round16<F16>(y);
+      }
+      o[r] = gv;
+    }
+  };
+
+  if constexpr (QOUT) {
+    // e4m3 activation with one fp32 scale per (slot, 128 columns): the 8
+    // waves cover the tile's 128 columns (N % 128 == 0); lanes l, l+16, l+32,
+    // l+48 hold the same slot
+    constexpr int PITCH = NOUT + 16;
+    float (*s_amax)[BM] = reinterpret_cast<float (*)[BM]>(lds + BM * PITCH);
+    float* s_sc = reinterpret_cast<float*>(lds + BM * PITCH + WAVES * BM * 4);
+    float ov[TJ][4];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      outv(0, j, ov[j]);
+      float m = 1e-10f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[j][r]));
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      if (g == 0) s_amax[wave][16 * j + l16] = m;
+    }
+    __syncthreads();
+    float* ds = static_cast<float*>(qs);
+    const int64_t ngroups = N / 128;
+    if (tid < BM) {
+      float am = s_amax[0][tid];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
+      const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
+      s_sc[tid] = sc;
+      const int drow = s_drow[tid];
+      if (drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int row = 16 * j + l16;
+      const float inv = 1.0f / s_sc[row];
+      uint32_t w = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = fminf(fmaxf(ov[j][r] * inv, -448.f), 448.f);
+        w |= f32_to_e4m3(x) << (8 * r);
+      }
+      *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
+    }
+    __syncthreads();
+    uint8_t* dq = static_cast<uint8_t*>(a.D);
+    constexpr int CPR = NOUT / 16;
+    for (int idx = tid; idx < BM * CPR; idx += 512) {
+      const int row = idx / CPR, ch = idx % CPR;
+      const int drow = s_drow[row];
+      if (drow < 0) continue;
+      *reinterpret_cast<uint4*>(dq + static_cast<int64_t>(drow) * N + n0 + ch * 16) =
+          *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
+    }
+  } else {
+    // 16-bit output staged in LDS (STORE tiles in two passes of 160 slots)
+    // and written with 16-byte row-contiguous stores
+    constexpr int PITCH = 2 * NOUT + 16;
+    // passes of a whole number of slot tiles each, as few as the ring holds
+    constexpr int PASSES = BM * PITCH <= RING ? 1 : BM / 2 * PITCH <= RING ? 2
+                         : BM / 4 * PITCH <= RING ? 4 : 5;
+    static_assert(BM / PASSES * PITCH <= RING && TJ % PASSES == 0, "staging passes");
+    constexpr int PROWS = BM / PASSES;
+    constexpr int PJ = TJ / PASSES;
+    uint16_t* d = static_cast<uint16_t*>(a.D);
+    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
+    constexpr int CPR = 2 * NOUT / 16;
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int jj = 0; jj < PJ; ++jj) {
+          const int j = pass * PJ + jj;
+          float o[4];
+          outv(f, j, o);
+          const int srow = 16 * jj + l16;
+          const uint32_t lo = to16<F16>(o[0]) | (to16<F16>(o[1]) << 16);
+          const uint32_t hi = to16<F16>(o[2]) | (to16<F16>(o[3]) << 16);
+          *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(f, 0)) = make_uint2(lo, hi);
+        }
+      __syncthreads();
+      for (int idx = tid; idx < PROWS * CPR; idx += 512) {
+        const int srow = idx / CPR, ch = idx % CPR;
+        const int drow = s_drow[pass * PROWS + srow];
+        const int64_t col = n0 + ch * 8;
+        if (drow < 0 || col >= N) continue;
+        const uint4 val = *reinterpret_cast<const uint4*>(lds + srow * PITCH + ch * 16);
+        uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
+        if (vec) {
+          *reinterpret_cast<uint4*>(dst) = val;
+        } else {
+          const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+        }
+      }
+      if (pass + 1 < PASSES) __syncthreads();  // the staging area is rewritten
+    }
+  }
+}
+
+template <int EPI, bool QOUT, bool F16>
+int launch_w8p(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
+  const int64_t cols = EPI == EPI_GLU ? 128 : 256;
+  const int64_t total = cdiv(a.N, cols) * max_blocks;
+  dim3 grid(static_cast<unsigned>(cdiv(total, 8) * 8));
+  moe_gemm_wide8p_kernel<EPI, QOUT, F16><<<grid, dim3(512), 0, st>>>(a, qs);
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
+}  // namespace
+
+// kWideBM-slot blocks; fp8 block-scaled weights, K % 128 == 0, K <= 8192
+// (the caller checks wide8_supported / wide8_shape_ok).
+int launch_moe_gemm_wide8p(int epi, bool qout, const GemmArgs& a, int64_t max_blocks,
+                           void* qs, hipStream_t st) {
+  if (qout)
+    return a.out_f16 ? launch_w8p<EPI_GLU, true, true>(a, max_blocks, qs, st)
+                     : launch_w8p<EPI_GLU, true, false>(a, max_blocks, qs, st);
+  if (epi == EPI_GLU)
+    return a.out_f16 ? launch_w8p<EPI_GLU, false, true>(a, max_blocks, qs, st)
+                     : launch_w8p<EPI_GLU, false, false>(a, max_blocks, qs, st);
+  return a.out_f16 ? launch_w8p<EPI_STORE, false, true>(a, max_blocks, qs, st)
+                   : launch_w8p<EPI_STORE, false, false>(a, max_blocks, qs, st);
+}
+
+}  // namespace mi355
