@@ -459,6 +459,18 @@ size_t mi355moe_fused_moe_workspace_size(const mi355moe_fused_moe_args* args);
 int mi355moe_fused_moe(const mi355moe_fused_moe_args* args, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of mi355moe_fused_moe.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace is a static device array of MI355MOE_NOALLOC_SCRATCH_BYTES per GPU
+ * (held until the process ends); the call allocates nothing and returns
+ * MI355MOE_ERR_WORKSPACE when mi355moe_fused_moe_workspace_size(args) exceeds
+ * it (64 MiB covers decode batches: DeepSeek-V3 shape up to 256 tokens,
+ * Qwen3-30B-A3B up to 512).  Calls that overlap on one GPU share that array
+ * and race. */
+#define MI355MOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int mi355moe_fused_moe_noalloc(const mi355moe_fused_moe_args* args, void* stream);
+
 /* Stage timing (no counterpart in the reference, whose benchmark brackets
  * each op with torch.xpu.Event, benchmark/src/fused_moe_interface_.py:144-226).
  * mi355moe_fused_moe_timed records HIP events on `stream` around its five

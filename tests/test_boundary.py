@@ -364,3 +364,18 @@ def test_xpu_fused_moe_flags_checked_against_dtypes():
     with pytest.raises(AssertionError, match="output shape"):
         F.xpu_fused_moe(x, w13, None, None, w2, None, None, tw, ids, 2, "silu", 4,
                         output=torch.empty(3, 64, dtype=torch.bfloat16))
+
+
+def test_fused_moe_noalloc_rejects_calls_beyond_its_scratch(lib):
+    """The allocation-free entry refuses, before any device work, a call
+    whose workspace exceeds its static per-GPU scratch (C3 at 8192 tokens
+    needs about 1.25 GB)."""
+    from vllm_xpu_kernels import capi
+    a = capi.FusedMoeArgs(recipe=1, activation=0, act_dtype=1, ids_dtype=3,
+                          num_tokens=8192, hidden=7168, inter=2048, num_experts=256,
+                          topk=8, w_layout=1)
+    lib.mi355moe_fused_moe_noalloc.argtypes = [ctypes.POINTER(capi.FusedMoeArgs),
+                                               ctypes.c_void_p]
+    rc = lib.mi355moe_fused_moe_noalloc(ctypes.byref(a), None)
+    assert rc == -4
+    assert b"more than the static" in lib.mi355moe_last_error()

@@ -1,0 +1,49 @@
+"""GPU: the allocation-free entry point mi355moe_fused_moe_noalloc (static
+per-GPU scratch) against mi355moe_fused_moe (caller workspace), through the C
+ABI, on two calls in a row, the second with a smaller input: the two must be
+bit-identical (same kernels, same order of operations)."""
+import ctypes
+import dataclasses
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_pair(cfg, T, dev, moe, w, seed):
+    from vllm_xpu_kernels import capi
+    from vllm_xpu_kernels import workloads as W
+    x = W.make_activations(cfg, T, dev, seed=seed)
+    logits = W.make_router_logits(cfg, T, dev, seed=seed + 1)
+    bias = W.make_correction_bias(cfg, dev) if cfg.routing == "grouped_sigmoid" else None
+    tw, ti = W.route(cfg, logits, bias)
+    ref = torch.empty_like(x)
+    out = torch.full_like(x, float("nan"))
+    a_ref = capi.fused_args(moe, ref, x, tw, ti)
+    a_out = capi.fused_args(moe, out, x, tw, ti)
+    ws = capi.workspace_for(a_ref, dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lib = capi.lib
+    assert lib.mi355moe_fused_moe(ctypes.byref(a_ref), ctypes.c_void_p(ws.data_ptr()),
+                                  ctypes.c_size_t(ws.numel()), stream) == 0
+    lib.mi355moe_fused_moe_noalloc.argtypes = [ctypes.POINTER(capi.FusedMoeArgs),
+                                               ctypes.c_void_p]
+    rc = lib.mi355moe_fused_moe_noalloc(ctypes.byref(a_out), stream)
+    assert rc == 0, lib.mi355moe_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"T={T}: {(out.float() - ref.float()).abs().max()}"
+
+
+@pytest.mark.parametrize("name,E,sizes", [("C2", None, (64, 16)), ("C3", 32, (33, 4))])
+def test_fused_moe_noalloc_matches_workspace_entry(dev, name, E, sizes):
+    from vllm_xpu_kernels import workloads as W
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    cfg = W.CONFIGS[name]
+    if E is not None:
+        cfg = dataclasses.replace(cfg, experts=E)
+    w = W.make_weights(cfg, dev)
+    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                      cfg.topk, cfg.activation, cfg.experts)
+    for i, T in enumerate(sizes):   # second call smaller than the first
+        _run_pair(cfg, T, dev, moe, w, seed=10 + 3 * i)

@@ -11,6 +11,8 @@
 //      slot's row to its flat (token, j) position
 //   5. weighted top-k reduction y[t] = sum_j w[t,j] * G2[t*k + j] in fixed j
 //      order (no floating-point atomics).
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "mfma16.h"
@@ -408,6 +410,57 @@ struct mi355moe_timer_s {
 extern "C" int mi355moe_fused_moe(const mi355moe_fused_moe_args* a, void* ws,
                                   size_t ws_bytes, void* stream) {
   return fused_moe_impl(a, ws, ws_bytes, stream, nullptr);
+}
+
+// ----------------------------------------------- allocation-free variant
+// Scratch of mi355moe_fused_moe_noalloc: a file-scope device array, one copy
+// per GPU the library runs on, held until the process ends.  Host code never
+// uses its name as an address: the address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and kept per device.  Every
+// call on a GPU reuses that GPU's array (the kernels initialise what they
+// read), so calls that overlap on one GPU race.
+static __device__ __align__(256) uint8_t scratch[MI355MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // by device ordinal
+
+// Device address of `scratch` on the device of `stream` (the current device
+// for the null stream).
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = 0;
+  MI_HIP(hipGetDevice(&dev));
+  int sdev = dev;
+  if (stream) MI_HIP(hipStreamGetDevice(stream, &sdev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (static_cast<size_t>(sdev) >= g_scratch_ptr.size())
+    g_scratch_ptr.resize(static_cast<size_t>(sdev) + 1, nullptr);
+  if (!g_scratch_ptr[sdev]) {
+    if (sdev != dev) MI_HIP(hipSetDevice(sdev));
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (sdev != dev) MI_HIP(hipSetDevice(dev));
+    if (rc != hipSuccess || p == nullptr)
+      return set_error(MI355MOE_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") +
+                                             hipGetErrorString(rc));
+    g_scratch_ptr[sdev] = p;
+  }
+  *out = g_scratch_ptr[sdev];
+  return MI355MOE_OK;
+}
+}  // namespace
+
+extern "C" int mi355moe_fused_moe_noalloc(const mi355moe_fused_moe_args* a, void* stream) {
+  MI_ARG(a != nullptr, "null arguments");
+  const size_t need = mi355moe_fused_moe_workspace_size(a);
+  MI_CHECK(need <= MI355MOE_NOALLOC_SCRATCH_BYTES, MI355MOE_ERR_WORKSPACE,
+           "fused_moe_noalloc: this call needs " + std::to_string(need) +
+               " bytes of scratch, more than the static " +
+               std::to_string(MI355MOE_NOALLOC_SCRATCH_BYTES) +
+               " (use mi355moe_fused_moe with a caller workspace)");
+  void* ptr = nullptr;
+  if (int rc = scratch_address(static_cast<hipStream_t>(stream), &ptr)) return rc;
+  return fused_moe_impl(a, ptr, MI355MOE_NOALLOC_SCRATCH_BYTES, stream, nullptr);
 }
 
 extern "C" int mi355moe_timer_create(int max_steps, mi355moe_timer* out) {
