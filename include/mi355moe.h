@@ -56,12 +56,19 @@ typedef enum {
                                    per 32 along K; bf16 or fp16
                                    activations (weights dequantised to
                                    their type)                            */
-  MI355MOE_RECIPE_INT4 = 3      /* signed int4 weights (two's complement,
+  MI355MOE_RECIPE_INT4 = 3,     /* signed int4 weights (two's complement,
                                    the even K value in the low nibble)
                                    packed along K [E, N, K/2], scales
                                    [E, N, K/group] in the activations'
                                    16-bit type, group 32/64/128/256:
                                    w = T(v * scale) (w4a16)               */
+  MI355MOE_RECIPE_MXFP8 = 4     /* e4m3 weights [E, N, K] with an e8m0 scale
+                                   (u8) per 32 along K, [E, N, K/32];
+                                   activations quantised per 32 to e4m3
+                                   with ue8m0 scales (the reference's
+                                   _quant_mxfp8_act_xpu), both scales in
+                                   the scaled MFMA (vllm_xpu_kernels/
+                                   moe_utils.py:76-104)                   */
 } mi355moe_recipe;
 
 typedef enum {
@@ -430,13 +437,16 @@ typedef struct {
   float swiglu_limit;         /* swigluoai limit (7.0)                       */
   void* output;               /* [T, H]                                      */
   int w_layout;               /* mi355moe_weight_layout of w13 and w2 (bf16) */
-  /* fp8block only, optional (the reference's a1q_scale,
-   * vllm_xpu_kernels/fused_moe_interface.py:326-360): when non-null,
-   * hidden_states are already quantised, e4m3 [T, H], with these f32 scales
-   * [T, H/128] (1x128 groups, as per_token_group_fp8_quant makes them), and
-   * the layer uses them as they are instead of quantising hidden_states
-   * itself; act_dtype still names the output's type. */
-  const float* hidden_scale;
+  /* Optional (the reference's a1q_scale, vllm_xpu_kernels/
+   * fused_moe_interface.py:326-360, moe_utils.py:189-199): when non-null,
+   * hidden_states are already quantised and the layer uses them with these
+   * scales as they are; act_dtype still names the output's type.
+   *   FP8BLOCK  e4m3 [T, H] + f32 [T, H/128] (1x128 groups)
+   *   MXFP8     e4m3 [T, H] + e8m0 u8 [T, H/32]
+   *   MXFP4     packed e2m1 [T, H/2] + e8m0 u8 [T, H/32]: both GEMMs then
+   *             run e2m1 x e2m1 (the w13 epilogue re-quantises the
+   *             activation to mxfp4 for w2, as the reference's qdq_act). */
+  const void* hidden_scale;
   /* recipe INT4: K values per group scale (32, 64, 128 or 256) */
   int64_t w_group;
 } mi355moe_fused_moe_args;

@@ -670,6 +670,39 @@ def dequant_mxfp4(q: torch.Tensor, e8m0: torch.Tensor) -> torch.Tensor:
     return vals * sc
 
 
+def e8m0_value(e8m0: torch.Tensor) -> torch.Tensor:
+    """2^(e-127) of e8m0 bytes as the reference's _as_e8m0(s).to(float32)
+    (vllm_xpu_kernels/moe_utils.py:168-174): 0 -> 2^-127, 255 -> NaN."""
+    e = e8m0.view(torch.uint8).to(torch.int32)
+    v = torch.exp2((e - 127).double()).float()
+    return torch.where(e == 255, torch.full_like(v, float("nan")), v)
+
+
+def dequant_mxfp8(q: torch.Tensor, e8m0: torch.Tensor) -> torch.Tensor:
+    """e4m3 values [..., K] times their e8m0 scale per 32 along K
+    (vllm_xpu_kernels/moe_utils.py:76-82, dequant_mxfp8 / dequant_mxfp8_wei
+    with the weight transposed to [N, K])."""
+    return q.float() * e8m0_value(e8m0).repeat_interleave(32, dim=-1)
+
+
+def quant_mxfp8_act(x: torch.Tensor):
+    """_quant_mxfp8_act_xpu (vllm_xpu_kernels/moe_utils.py:90-104):
+    per_token_group_fp8_quant with group 32, eps 1e-10 and ue8m0 scales;
+    returns (e4m3 codes [M, K], e8m0 bytes [M, K/32])."""
+    q, sc = per_token_group_fp8_quant(x, 32, scale_ue8m0=True)
+    e = torch.log2(sc).round().to(torch.int32) + 127
+    return q, e.to(torch.uint8)
+
+
+def quant_mxfp4_act(x: torch.Tensor):
+    """_quant_mxfp4_act_xpu (vllm_xpu_kernels/moe_utils.py:106-120):
+    per_token_group_quant_mxfp4 with group 32, eps 1e-10; returns (packed
+    e2m1 [M, K/2], e8m0 bytes [M, K/32])."""
+    q, sc = per_token_group_quant_mxfp4(x, 32)
+    e = torch.log2(sc).round().to(torch.int32) + 127
+    return q, e.to(torch.uint8)
+
+
 def fp8_block_quant_weight(w: torch.Tensor, eps: float = 1e-6):
     """128x128 block quant of the last two dims (tests/ops/fp8_quant_op.py:16-78):
     s = clamp(amax/448, min=eps), q = e4m3(w / s).
@@ -723,16 +756,25 @@ def dequant_weight(recipe: str, w_e: torch.Tensor, s_e) -> torch.Tensor:
         return dequant_fp8_block_weight(w_e, s_e)
     if recipe == "mxfp4":
         return dequant_mxfp4(w_e, s_e)
+    if recipe == "mxfp8":
+        return dequant_mxfp8(w_e, s_e)
     raise ValueError(recipe)
 
 
 def qdq_act(recipe: str, x: torch.Tensor) -> torch.Tensor:
     """Activation quant-dequant round trip of the recipe
-    (vllm_xpu_kernels/moe_utils.py:176-187): fp8block -> 1x128 e4m3; bf16 and
-    mxfp4 (w4a16 kernel semantics) -> unchanged."""
+    (vllm_xpu_kernels/moe_utils.py:176-187): fp8block -> 1x128 e4m3; mxfp8
+    -> e4m3 with ue8m0 scales per 32; "mxfp4a4" (mxfp4 weights with
+    pre-quantised inputs, whose intermediate activation the reference
+    quantises with quant_act_xpu) -> e2m1 per 32; bf16 and mxfp4 (w4a16
+    kernel semantics) -> unchanged."""
     if recipe == "fp8block":
         q, s = per_token_group_fp8_quant(x, 128)
         return dequant_fp8_groups(q, s, 128)
+    if recipe == "mxfp8":
+        return dequant_mxfp8(*quant_mxfp8_act(x))
+    if recipe == "mxfp4a4":
+        return dequant_mxfp4(*quant_mxfp4_act(x))
     return x.float()
 
 
@@ -781,11 +823,13 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
     [E, N, K/32].  The expert loop dequantises one expert at a time.
     ``experts`` optionally restricts the computation to a subset of expert ids
     (the CPU-baseline sample); slots of other experts contribute zero.
-    ``a1q_scale`` (fp8block): ``hidden`` is already e4m3 with these [T, H/128]
-    scales, dequantised as given and computed in bf16
-    (fused_moe_interface.py:326-360, moe_utils.py:285, 338-347).
+    ``a1q_scale``: ``hidden`` is already quantised and dequantised as given,
+    computed in bf16 (fused_moe_interface.py:326-360, moe_utils.py:189-199,
+    285, 338-347): fp8block e4m3 with [T, H/128] f32 scales; mxfp8 e4m3
+    with e8m0 [T, H/32]; mxfp4 packed e2m1 [T, H/2] with e8m0 [T, H/32],
+    whose intermediate activation is then quantised to mxfp4 too.
     """
-    T, H = hidden.shape
+    T = hidden.shape[0]
     k = topk_ids.shape[1]
     dt = hidden.dtype if a1q_scale is None else torch.bfloat16
     ids = topk_ids.to(torch.int64)
@@ -793,14 +837,23 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
         ids = expert_map.to(torch.int64)[ids]
     E = w13.shape[0]
     I2 = w13.shape[1]
-    g2 = torch.zeros(T * k, H, dtype=dt)
     flat = ids.reshape(-1)
     todo = range(E) if experts is None else experts
+    act_recipe = recipe
     if a1q_scale is not None:
-        assert recipe == "fp8block", "a1q_scale: fp8block recipe only"
-        xq_all = dequant_fp8_groups(hidden, a1q_scale.float(), 128)
+        if recipe == "fp8block":
+            xq_all = dequant_fp8_groups(hidden, a1q_scale.float(), 128)
+        elif recipe == "mxfp8":
+            xq_all = dequant_mxfp8(hidden, a1q_scale)
+        elif recipe == "mxfp4":
+            xq_all = dequant_mxfp4(hidden.view(torch.uint8), a1q_scale.view(torch.uint8))
+            act_recipe = "mxfp4a4"
+        else:
+            raise ValueError(f"a1q_scale with recipe {recipe}")
     else:
         xq_all = qdq_act(recipe, hidden)
+    H = xq_all.shape[1]
+    g2 = torch.zeros(T * k, H, dtype=dt)
     for e in todo:
         slots = (flat == e).nonzero().flatten()
         if slots.numel() == 0:
@@ -834,7 +887,7 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
             act = relu2_no_mul(g1)       # all 2I columns; w2 has K = 2I
         else:
             raise ValueError(activation)
-        aq = qdq_act(recipe, act)
+        aq = qdq_act(act_recipe, act)
         wd = dequant_weight(recipe, w2[e],
                             None if w2_scale is None else w2_scale[e])
         y = aq @ wd.t()

@@ -233,10 +233,10 @@ def _workspace_query_checks(lib, a):
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"unsupported activation" in lib.mi355moe_last_error()
     a.activation = 0
-    # caller-quantised hidden states: fp8block only
+    # caller-quantised hidden states: fp8block and the MX recipes only
     a.w_layout, a.hidden_scale = 0, 64
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
-    assert rc == -1 and b"need the fp8block recipe" in lib.mi355moe_last_error()
+    assert rc == -1 and b"need the fp8block, mxfp8 or mxfp4" in lib.mi355moe_last_error()
 
 
 # schema strings as written in the reference's registration files

@@ -168,6 +168,11 @@ def _oracle_layer(cfg, w, x, tw, ti, tokens=None, a1q_scale=None):
     if cfg.recipe == "bf16":
         w13 = w.w13.index_select(0, usedd).transpose(1, 2).contiguous().cpu()
         w2 = w.w2.index_select(0, usedd).transpose(1, 2).contiguous().cpu()
+    elif cfg.recipe == "mxfp8":   # [E, K, N] + [E, K/32, N] -> [E, N, K] + [E, N, K/32]
+        tr = lambda t: t.index_select(0, usedd).transpose(1, 2).contiguous().cpu()  # noqa: E731
+        return O.fused_moe("mxfp8", x.cpu(), tr(w.w13), tr(w.w13_scale), None, tr(w.w2),
+                           tr(w.w2_scale), None, tw.cpu(), ids, activation=cfg.activation,
+                           a1q_scale=None if a1q_scale is None else a1q_scale.cpu())
     else:
         w13 = w.w13.view(torch.uint8).index_select(0, usedd).cpu()
         w2 = w.w2.view(torch.uint8).index_select(0, usedd).cpu()
@@ -779,8 +784,66 @@ def test_fused_moe_int4(dev, dt, T, topk):
 
 def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):
     cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C1"], 8, dev)
-    with pytest.raises(NotImplementedError, match="fp8 block-scaled recipe"):
+    with pytest.raises(NotImplementedError, match="fp8block, mxfp8 and mxfp4"):
         moe.apply(out, x, tw, ti, a1q_scale=torch.ones(8, 1, device=dev))
+
+
+def _e8m0(scale):
+    """float32 powers of two -> e8m0 bytes."""
+    return (torch.log2(scale).round().to(torch.int32) + 127).to(torch.uint8)
+
+
+@pytest.mark.parametrize("T", [1, 33, 200])
+def test_fused_moe_mxfp8_c3_32_experts(dev, T):
+    """mxfp8 (e4m3 weights [E, K, N] with e8m0 scales per 32 along K; the
+    input and the intermediate activation quantised to mxfp8 per 32) on
+    DeepSeek-V3 shapes with 32 experts; the layer's own quantisation of x
+    equals pre-quantised input from the 32-group ue8m0 quantiser bit for bit."""
+    import dataclasses
+    from vllm_xpu_kernels import ops
+    cfg = dataclasses.replace(_W().CONFIGS["C3"], recipe="mxfp8")
+    cfg, w, x, tw, ti, out, moe = _layer(cfg, T, dev, E=32)
+    assert moe.recipe == "mxfp8"
+    toks = torch.linspace(0, T - 1, min(T, 24)).long().to(dev)
+    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks), fp8=True)
+    xq, xs = ops.per_token_group_fp8_quant(x, 32, scale_ue8m0=True)
+    out2 = torch.empty_like(out)
+    moe.apply(out2, xq, tw, ti, a1q_scale=_e8m0(xs).view(torch.float8_e8m0fnu))
+    assert torch.equal(out2, out)
+
+
+def test_fused_moe_mxfp8_ignores_clamp_limit_like_reference(dev):
+    """The reference runs mxfp8 through its torch path, which takes no
+    gemm1_clamp_limit: a limit changes nothing."""
+    import dataclasses
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    cfg = dataclasses.replace(_W().CONFIGS["C2"], recipe="mxfp8", experts=8, topk=2)
+    cfg, w, x, tw, ti, out, moe = _layer(cfg, 16, dev)
+    moe2 = XpuFusedMoe(w.w13, w.w13_scale, None, w.w2, w.w2_scale, None, cfg.topk,
+                       cfg.activation, cfg.experts, gemm1_clamp_limit=1e-3)
+    out2 = torch.empty_like(out)
+    moe2.apply(out2, x, tw, ti)
+    assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("T", [1, 32, 160])
+def test_fused_moe_mxfp4_pre_quantised_w4a4(dev, T):
+    """gpt-oss shapes (H = I = 2880: K % 128 = 64 in both GEMMs) with
+    pre-quantised mxfp4 input (packed e2m1 [T, H/2] + e8m0 [T, H/32]): both
+    GEMMs are e2m1 x e2m1 with the intermediate activation quantised to mxfp4
+    per 32 (the reference's quant_act_xpu)."""
+    from vllm_xpu_kernels import ops
+    cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C5"], T, dev)
+    xq, xs = ops.per_token_group_quant_mxfp4(x, 32)
+    xq = xq.view(torch.uint8)
+    out4 = torch.empty_like(out)
+    moe.apply(out4, xq.view(torch.float4_e2m1fn_x2), tw, ti,
+              a1q_scale=_e8m0(xs).view(torch.float8_e8m0fnu))
+    toks = torch.linspace(0, T - 1, min(T, 24)).long().to(dev)
+    ref = _oracle_layer(cfg, w, xq, tw, ti, toks, a1q_scale=_e8m0(xs))
+    _close(out4[toks], ref, fp8=True)
+    # and close to the w4a16 layer on the same input
+    assert (out4.float() - out.float()).abs().mean() < 0.25 * out.float().abs().mean()
 
 
 @pytest.mark.parametrize("T", [1, 16])

@@ -755,3 +755,172 @@ def test_fused_moe_oracle_fp8block_close_to_dequant_fp32():
     y2 = O.fused_moe("fp8block", xq2, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xs2)
     assert not torch.equal(y2, y)
     torch.testing.assert_close(y2.float(), y.float(), rtol=0.1, atol=0.05)
+
+
+# ------------------------------------------------------------ MX recipes
+def _e4m3_grid():
+    """Every finite e4m3 value, decoded from its bit fields by hand
+    (sign, 4-bit exponent with bias 7, 3-bit mantissa; exponent 0 is
+    subnormal; 0x7f/0xff are NaN)."""
+    vals = []
+    for b in range(256):
+        if b & 0x7F == 0x7F:
+            continue
+        e, m = (b >> 3) & 0xF, b & 7
+        v = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        vals.append(-v if b & 0x80 else v)
+    return torch.tensor(sorted(set(vals)), dtype=torch.float64)
+
+
+def test_e8m0_value_special_codes():
+    e = torch.tensor([0, 1, 126, 127, 128, 254, 255], dtype=torch.uint8)
+    v = O.e8m0_value(e)
+    assert v[:6].tolist() == [2.0 ** -127, 2.0 ** -126, 0.5, 1.0, 2.0, 2.0 ** 127]
+    assert math.isnan(v[6].item())
+
+
+def test_dequant_mxfp8_kat_per_32_along_k():
+    """Group g of row r is scaled by 2^(s[r, g] - 127); nothing else."""
+    q = torch.ones(2, 64).to(torch.float8_e4m3fn)
+    q[1, 33] = torch.tensor(-448.0).to(torch.float8_e4m3fn)
+    s = torch.tensor([[127, 130], [120, 127]], dtype=torch.uint8)
+    d = O.dequant_mxfp8(q, s)
+    assert torch.all(d[0, :32] == 1.0) and torch.all(d[0, 32:] == 8.0)
+    assert torch.all(d[1, :32] == 2.0 ** -7)
+    assert d[1, 33].item() == -448.0 and d[1, 32].item() == 1.0
+
+
+def test_mxfp8_act_quant_scale_is_least_power_of_two_and_codes_nearest():
+    """Brute force on the e4m3 grid: the e8m0 scale s is the least power of
+    two with amax / s <= 448 for groups whose amax / 448 is above the
+    1 / (448 * 512) scale floor, 2^ceil(log2(floor)) = 2^-17 for the others,
+    and every code is a nearest grid value of x / s."""
+    torch.manual_seed(21)
+    x = (torch.randn(6, 256) * torch.logspace(-6, 4, 6).unsqueeze(1)).to(torch.bfloat16)
+    x[2, 64:96] = 0.0
+    q, e = O.quant_mxfp8_act(x)
+    assert q.dtype == torch.float8_e4m3fn and e.dtype == torch.uint8
+    assert e.shape == (6, 8)
+    xf = x.double().reshape(6, 8, 32)
+    s = torch.exp2(e.double() - 127)
+    amax = xf.abs().amax(-1)
+    live = amax > 1.0 / 512.0
+    assert live.any() and (~live).any()
+    assert torch.all(amax[live] / s[live] <= 448.0)
+    assert torch.all(amax[live] / (s[live] / 2) > 448.0)
+    assert torch.all(s[~live] == 2.0 ** -17)
+    grid = _e4m3_grid()
+    y = (xf / s.unsqueeze(-1)).flatten()
+    qd = q.double().flatten()
+    dist = (y.unsqueeze(1) - grid.unsqueeze(0)).abs()
+    best = dist.min(1).values
+    assert torch.all((qd - y).abs() <= best + 1e-300)
+    # the all-zero group dequantises to zero; the round trip moves the
+    # group amax by at most half a 3-bit-mantissa ulp
+    d = O.dequant_mxfp8(q, e)
+    assert torch.all(d[2, 64:96] == 0)
+    da = d.double().reshape(6, 8, 32).abs().amax(-1)
+    assert torch.all((da[live] - amax[live]).abs() <= amax[live] * 2.0 ** -4)
+
+
+def test_mxfp4_act_quant_matches_rceil_and_grid_brute_force():
+    """e8m0 scale = 2^ceil(log2(amax / 6)); every e2m1 code is the nearest
+    grid point of x / s, a midpoint going to the smaller magnitude
+    (csrc/quantization/fp4/mxfp4_quant.h:17-25 compares with strict >)."""
+    torch.manual_seed(22)
+    x = torch.randn(5, 128).to(torch.bfloat16) * 3
+    q, e = O.quant_mxfp4_act(x)
+    assert q.shape == (5, 64) and e.shape == (5, 4)
+    xf = x.double().reshape(5, 4, 32)
+    amax = xf.abs().amax(-1)
+    assert torch.equal(e.long(), (torch.ceil(torch.log2(amax / 6.0)) + 127).long())
+    grid = torch.tensor([0, 0.5, 1, 1.5, 2, 3, 4, 6], dtype=torch.float64)
+    y = (xf / torch.exp2(e.double() - 127).unsqueeze(-1)).flatten()
+    codes = torch.stack([q & 0xF, q >> 4], -1).reshape(-1).long()
+    mag = (y.abs().unsqueeze(1) - grid).abs()
+    best = mag.min(1).values
+    got = grid[codes & 7]
+    assert torch.all((got - y.abs()).abs() <= best + 1e-12)
+    tie = (mag == best.unsqueeze(1)).sum(1) > 1
+    assert tie.any()
+    lower = grid[(mag == best.unsqueeze(1)).int().argmax(1)]
+    assert torch.all(got[tie] == lower[tie])
+    nz = got != 0
+    assert torch.all(((codes[nz] >> 3) == 1) == (y[nz] < 0))
+
+
+def _mx_weights(E, N, K, seed, fmt):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(E, N, K, generator=g) * 0.05
+    if fmt == "mxfp8":
+        q, e = O.quant_mxfp8_act(w.reshape(E * N, K))
+        return q.reshape(E, N, K), e.reshape(E, N, K // 32)
+    q, e = O.quant_mxfp4_act(w.reshape(E * N, K))
+    return q.reshape(E, N, K // 2), e.reshape(E, N, K // 32)
+
+
+def test_fused_moe_oracle_mxfp8_is_bf16_layer_on_qdq_input_and_act():
+    """mxfp8 = the 16-bit layer on exactly dequantised weights whose input
+    and intermediate activation went through the pinned mxfp8 round trip;
+    a1q_scale with the quantiser's own (q, e) gives the same layer."""
+    torch.manual_seed(23)
+    T, H, I, E, k = 9, 128, 64, 4, 2
+    x = torch.randn(T, H).to(torch.bfloat16)
+    q13, s13 = _mx_weights(E, 2 * I, H, 1, "mxfp8")
+    q2, s2 = _mx_weights(E, H, I, 2, "mxfp8")
+    w, ids, _ = O.topk_softmax(torch.randn(T, E), k, True)
+    y = O.fused_moe("mxfp8", x, q13, s13, None, q2, s2, None, w, ids)
+    d13 = torch.stack([O.dequant_mxfp8(q13[e], s13[e]) for e in range(E)])
+    d2 = torch.stack([O.dequant_mxfp8(q2[e], s2[e]) for e in range(E)])
+    xq = O.dequant_mxfp8(*O.quant_mxfp8_act(x)).to(torch.bfloat16)
+    # 16-bit layer with the intermediate round trip spelled out per slot
+    flat = ids.reshape(-1).long()
+    g2 = torch.zeros(T * k, H, dtype=torch.bfloat16)
+    for e in range(E):
+        sl = (flat == e).nonzero().flatten()
+        if sl.numel() == 0:
+            continue
+        g1 = (xq[sl // k].float() @ d13[e].t()).to(torch.bfloat16)
+        a = O.silu_and_mul(g1)
+        aq = O.dequant_mxfp8(*O.quant_mxfp8_act(a))
+        g2[sl] = (aq @ d2[e].t()).to(torch.bfloat16)
+    ref = (g2.float().reshape(T, k, H) * w.float().unsqueeze(-1))
+    acc = torch.zeros(T, H)
+    for j in range(k):
+        acc = acc + ref[:, j]
+    assert torch.equal(y, acc.to(torch.bfloat16))
+    xq8, xe8 = O.quant_mxfp8_act(x)
+    ya = O.fused_moe("mxfp8", xq8, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xe8)
+    assert ya.dtype == torch.bfloat16 and torch.equal(ya, y)
+
+
+def test_fused_moe_oracle_mxfp4_a1q_quantises_both_gemm_inputs():
+    """mxfp4 with pre-quantised input: GEMM1 reads the dequantised packed
+    input, GEMM2 the mxfp4 round trip of the activation; without a1q_scale
+    the recipe is w4a16 (activation unrounded)."""
+    torch.manual_seed(24)
+    T, H, I, E, k = 7, 128, 64, 3, 2
+    x = torch.randn(T, H).to(torch.bfloat16)
+    q13, s13 = _mx_weights(E, 2 * I, H, 3, "mxfp4")
+    q2, s2 = _mx_weights(E, H, I, 4, "mxfp4")
+    w, ids, _ = O.topk_softmax(torch.randn(T, E), k, True)
+    xq, xe = O.quant_mxfp4_act(x)
+    ya = O.fused_moe("mxfp4", xq, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xe)
+    xd = O.dequant_mxfp4(xq, xe).to(torch.bfloat16)
+    y16 = O.fused_moe("mxfp4", xd, q13, s13, None, q2, s2, None, w, ids)
+    assert ya.shape == (T, H) and not torch.equal(ya, y16)
+    torch.testing.assert_close(ya.float(), y16.float(), rtol=0.25, atol=0.05)
+    flat = ids.reshape(-1).long()
+    g2 = torch.zeros(T * k, H, dtype=torch.bfloat16)
+    for e in range(E):
+        sl = (flat == e).nonzero().flatten()
+        if sl.numel() == 0:
+            continue
+        g1 = (xd[sl // k].float() @ O.dequant_mxfp4(q13[e], s13[e]).t()).to(torch.bfloat16)
+        a = O.silu_and_mul(g1)
+        aq = O.dequant_mxfp4(*O.quant_mxfp4_act(a))
+        g2[sl] = (aq @ O.dequant_mxfp4(q2[e], s2[e]).t()).to(torch.bfloat16)
+    acc = torch.zeros(T, H)
+    for j in range(k):
+        acc = acc + g2.float().reshape(T, k, H)[:, j] * w.float()[:, j:j + 1]
+    assert torch.equal(ya, acc.to(torch.bfloat16))

@@ -143,6 +143,26 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false)) & 0xFFu;
 }
 
+// ceil(log2(x)) of a positive finite float, exactly from its bits (a
+// mantissa above the power of two rounds the exponent up), and 2^e.
+__device__ __forceinline__ int ceil_log2(float x) {
+  uint32_t u = __float_as_uint(x);
+  int e = static_cast<int>((u >> 23) & 0xFF) - 127;
+  return (u & 0x7FFFFFu) ? e + 1 : e;
+}
+__device__ __forceinline__ float pow2i(int e) {
+  return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+// e2m1 code (sign in bit 3) of x in [-6, 6], magnitude by strict midpoints
+// (ties round down in magnitude), the rounding of the reference's mxfp4
+// quantiser (csrc/quantization/fp4/mxfp4_quant.h:17-25).
+__device__ __forceinline__ uint32_t fp4_code(float x) {
+  float a = fabsf(x);
+  uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) +
+               (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
+  return c | (x < 0.f ? 0x8u : 0u);
+}
+
 // e4m3 quantisation with one fp32 scale per 1 x 128 block, chunk c of 8
 // values (16 lanes per block, consecutive and aligned): amax from 1e-10,
 // scale = max(amax / 448, 1 / (448 * 512)), code = e4m3(clamp(v / scale))

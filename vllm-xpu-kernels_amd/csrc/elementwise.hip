@@ -67,16 +67,6 @@ __device__ __forceinline__ void stx(void* p, int64_t i, float v) {
   static_cast<typename E::T*>(p)[i] = E::st(v);
 }
 
-// ceil(log2(x)) for a positive normal float, exact (bit arithmetic).
-__device__ __forceinline__ int ceil_log2(float x) {
-  uint32_t u = __float_as_uint(x);
-  int e = static_cast<int>((u >> 23) & 0xFF) - 127;
-  return (u & 0x7FFFFFu) ? e + 1 : e;
-}
-__device__ __forceinline__ float pow2i(int e) {
-  return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
-}
-
 // ------------------------------------------------------------- activations
 template <typename E>
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -222,13 +212,6 @@ __global__ __launch_bounds__(256) void group_fp8_quant_kernel(
   store_nt(q + base, lo, hi);
 }
 
-__device__ __forceinline__ uint32_t fp4_code(float x) {
-  float a = fabsf(x);
-  uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) +
-               (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
-  return c | (x < 0.f ? 0x8u : 0u);
-}
-
 // mxfp4: groups of 32 owned by 4 lanes x 8 elements.
 template <typename E, bool VEC>
 __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
@@ -258,6 +241,44 @@ __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
     packed |= fp4_code(x) << (4 * i);
   }
   store_nt(q + base / 2, packed);
+}
+
+// mxfp8 activations (the reference's _quant_mxfp8_act_xpu,
+// vllm_xpu_kernels/moe_utils.py:90-104: per_token_group_fp8_quant with group
+// 32, eps 1e-10, +-448 and ue8m0 scales): groups of 32 owned by 4 lanes x 8
+// elements; codes e4m3 [rows, cols], each scale stored as its e8m0 byte
+// (exponent + 127) at s[row * s_ld + group].
+template <typename E, bool VEC>
+__global__ __launch_bounds__(256) void group_mx8_quant_kernel(
+    const void* __restrict__ in, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
+    int64_t s_ld, int64_t rows, int64_t cols) {
+  const int64_t gpr = cols / 32;
+  const int64_t ngroups = rows * gpr;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t g = gtid >> 2;
+  const int sub = static_cast<int>(gtid & 3);
+  const bool active = g < ngroups;
+  const int64_t base = (active ? g : 0) * 32 + sub * 8;
+  float v[8];
+  load8<E, VEC>(in, base, v);
+  float amax = 1e-10f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float ys0 = fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
+  const int ex = ceil_log2(fmaxf(fabsf(ys0), 1e-10f));
+  const float ys = pow2i(ex);
+  if (!active) return;
+  if (sub == 0) s[(g / gpr) * s_ld + g % gpr] = static_cast<uint8_t>(ex + 127);
+  const float inv = 1.0f / ys;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t b = f32_to_e4m3(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f));
+    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+  }
+  store_nt(q + base, lo, hi);
 }
 
 // --------------------------------------------- fused SiLU-and-mul + quant
@@ -438,6 +459,27 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(
 }
 
 }  // namespace
+
+// mxfp8 quantisation of 16-bit x [rows, cols] (cols % 32 == 0): codes q
+// [rows, cols] e4m3, scale bytes s [rows, s_ld] (group_mx8_quant_kernel).
+int mx8_quant_rows(const void* x, bool f16, uint8_t* q, uint8_t* s, int64_t s_ld,
+                   int64_t rows, int64_t cols, hipStream_t st) {
+  MI_ARG(cols % 32 == 0 && s_ld >= cols / 32, "mxfp8 quantisation needs cols % 32 == 0");
+  if (rows == 0) return MI355MOE_OK;
+  const int64_t threads = rows * (cols / 32) * 4;
+  dim3 grid(static_cast<unsigned>(cdiv(threads, 256)));
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (f16) {
+    if (vec) group_mx8_quant_kernel<F16, true><<<grid, dim3(256), 0, st>>>(x, q, s, s_ld, rows, cols);
+    else group_mx8_quant_kernel<F16, false><<<grid, dim3(256), 0, st>>>(x, q, s, s_ld, rows, cols);
+  } else {
+    if (vec) group_mx8_quant_kernel<BF16, true><<<grid, dim3(256), 0, st>>>(x, q, s, s_ld, rows, cols);
+    else group_mx8_quant_kernel<BF16, false><<<grid, dim3(256), 0, st>>>(x, q, s, s_ld, rows, cols);
+  }
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
+}
+
 }  // namespace mi355
 
 using namespace mi355;

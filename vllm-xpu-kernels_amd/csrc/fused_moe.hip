@@ -313,8 +313,12 @@ struct FusedLayout {
   size_t sortws_bytes;
   uint8_t* xq;    // fp8 hidden [T, H]
   float* xs;      // [T, H/128]
-  void* act;      // bf16 [max_padded, K2] or e4m3 [max_padded, K2]
+  void* act;      // bf16 [max_padded, K2] or e4m3 [max_padded, K2] (mxfp4 w4a4:
+                  // packed e2m1 [max_padded, K2/2])
   float* acts;    // [max_padded, K2/128]
+  uint8_t* xs8;   // MX: e8m0 scales of the quantised hidden [T, ld1]
+  uint8_t* acts8; // MX: e8m0 scales of the activation [max_padded, ld2]
+  int64_t ld1, ld2;
   uint16_t* g1;   // generic activations: w13 output bf16 [max_padded, 2I]
   uint16_t* g2;   // bf16 [slots, H]
   size_t bytes;
@@ -330,6 +334,17 @@ int64_t act_width(const mi355moe_fused_moe_args* a) {
   return a->activation == MI355MOE_ACT_RELU2 ? 2 * a->inter : a->inter;
 }
 
+// MX recipes (scales of both operands in the MFMA): mxfp8, and mxfp4 with
+// pre-quantised (e2m1) hidden states; the GEMMs then run recipe
+// gemm_recipe().
+bool mx_layer(const mi355moe_fused_moe_args* a) {
+  return a->recipe == MI355MOE_RECIPE_MXFP8 ||
+         (a->recipe == MI355MOE_RECIPE_MXFP4 && a->hidden_scale != nullptr);
+}
+int gemm_recipe(const mi355moe_fused_moe_args* a) {
+  return a->recipe == MI355MOE_RECIPE_MXFP4 && a->hidden_scale ? RECIPE_MX4A4 : a->recipe;
+}
+
 FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
   const int64_t E = a->num_experts;
@@ -339,7 +354,7 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
   const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H, kblock) &&
                        wide_ok_for(a->recipe, L.slots + E * kWideBM, H, K2, kblock);
-  L.tile = pick_tile(a->recipe, wide_ok, L.slots, E, &L.bm);
+  L.tile = pick_tile(gemm_recipe(a), wide_ok, L.slots, E, &L.bm);
   // K-blocked weights: the families that read them (STREAM, SMALL, WIDE, and
   // BIG for fp8, whose 8-wave kernel takes K <= 8192, and for mxfp4)
   if (kblock && a->recipe != MI355MOE_RECIPE_MXFP4 &&
@@ -371,7 +386,17 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   L.sortws_bytes = counting_sort_ws_bytes(L.slots, E);
   L.sortws = c.take<int32_t>(static_cast<int64_t>(L.sortws_bytes / sizeof(int32_t)));
   const bool fp8 = a->recipe == MI355MOE_RECIPE_FP8BLOCK;
-  if (fp8) {
+  if (mx_layer(a)) {
+    // e8m0 scale rows padded to a multiple of 4 bytes
+    L.ld1 = (a->hidden / 32 + 3) / 4 * 4;
+    L.ld2 = (K2 / 32 + 3) / 4 * 4;
+    if (!a->hidden_scale) {
+      L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
+      L.xs8 = c.take<uint8_t>(a->num_tokens * L.ld1);
+    }
+    L.act = c.take<uint8_t>(L.max_padded * (gemm_recipe(a) == RECIPE_MX4A4 ? K2 / 2 : K2));
+    L.acts8 = c.take<uint8_t>(L.max_padded * L.ld2);
+  } else if (fp8) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
     L.xs = c.take<float>(a->num_tokens * (a->hidden / 128));
     L.act = c.take<uint8_t>(L.max_padded * K2);
@@ -513,8 +538,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   MI_ARG(E <= 1024, "num_experts must be at most 1024");
   MI_ARG(a->act_dtype == MI355MOE_BF16 || a->act_dtype == MI355MOE_F16,
          "hidden_states must be bfloat16 or float16");
-  MI_ARG(!a->hidden_scale || a->recipe == MI355MOE_RECIPE_FP8BLOCK,
-         "pre-quantised hidden_states (hidden_scale) need the fp8block recipe");
+  MI_ARG(!a->hidden_scale || a->recipe == MI355MOE_RECIPE_FP8BLOCK ||
+             a->recipe == MI355MOE_RECIPE_MXFP8 || a->recipe == MI355MOE_RECIPE_MXFP4,
+         "pre-quantised hidden_states (hidden_scale) need the fp8block, mxfp8 or "
+         "mxfp4 recipe");
   MI_ARG(a->ids_dtype == MI355MOE_I32 || a->ids_dtype == MI355MOE_I64,
          "topk_ids must be int32 or int64");
   MI_ARG(a->activation >= MI355MOE_ACT_SILU && a->activation <= MI355MOE_ACT_RELU2,
@@ -535,6 +562,9 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   } else if (recipe == MI355MOE_RECIPE_MXFP4) {
     MI_ARG(H % 32 == 0 && I % 32 == 0, "mxfp4 weights need K % 32 == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "mxfp4 weights need e8m0 scales");
+  } else if (recipe == MI355MOE_RECIPE_MXFP8) {
+    MI_ARG(H % 32 == 0 && I % 32 == 0, "mxfp8 weights need hidden and intermediate sizes % 32 == 0");
+    MI_ARG(a->w13_scale && a->w2_scale, "mxfp8 weights need e8m0 scales");
   } else {
     MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
     MI_ARG(H % 8 == 0 && I % 8 == 0, "bf16 weights need K % 8 == 0");
@@ -544,9 +574,13 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
   MI_ARG(!kblock || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0) ||
              (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && act_width(a) <= 8192) ||
+             (recipe == MI355MOE_RECIPE_MXFP8 && H % 128 == 0 && act_width(a) % 128 == 0) ||
              recipe == MI355MOE_RECIPE_MXFP4,
          "K-blocked weights need the bf16 recipe (hidden and intermediate sizes "
-         "% 32 == 0), the fp8block recipe (sizes at most 8192) or mxfp4");
+         "% 32 == 0), the fp8block recipe (sizes at most 8192), mxfp8 (sizes % 128 "
+         "== 0) or mxfp4");
+  MI_ARG(!mx_layer(a) || epilogue_act(a->activation),
+         "mxfp8 and pre-quantised mxfp4 layers support the silu and swigluoai activations");
   if (T == 0) return MI355MOE_OK;
   FusedLayout L = plan(a, static_cast<uint8_t*>(ws));
   MI_CHECK(ws && ws_bytes >= L.bytes, MI355MOE_ERR_WORKSPACE,
@@ -559,6 +593,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   };
 
   const bool fp8 = recipe == MI355MOE_RECIPE_FP8BLOCK;
+  const bool mx = mx_layer(a);
+  const int grecipe = gemm_recipe(a);
   const bool f16 = a->act_dtype == MI355MOE_F16;  // the call's 16-bit type
   // caller-quantised hidden states (e4m3 + 1x128 scales) go to w13 as given
   const bool preq = fp8 && a->hidden_scale;
@@ -589,6 +625,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     rc = group_quant_fp8(a->hidden_states, a->act_dtype, L.xq, L.xs, T, H, st);
     if (rc) return rc;
   }
+  if (mx && !a->hidden_scale) {
+    rc = mx8_quant_rows(a->hidden_states, f16, L.xq, L.xs8, L.ld1, T, H, st);
+    if (rc) return rc;
+  }
   if (int m = mark(2)) return m;
 
   // gelu / gelu_tanh / swiglustep / relu2_no_mul: w13 stores G1, a separate
@@ -596,8 +636,14 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   const bool glu = epilogue_act(a->activation);
   const int64_t K2 = act_width(a);
   GemmArgs g1{};
-  g1.A = fp8 && !preq ? static_cast<const void*>(L.xq) : a->hidden_states;
-  g1.a_scale = preq ? a->hidden_scale : (fp8 ? L.xs : nullptr);
+  g1.A = (fp8 && !preq) || (mx && !a->hidden_scale) ? static_cast<const void*>(L.xq)
+                                                     : a->hidden_states;
+  g1.a_scale = preq ? static_cast<const float*>(a->hidden_scale) : (fp8 ? L.xs : nullptr);
+  if (mx) {
+    g1.a_mxs = a->hidden_scale ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
+    g1.a_mxs_ld = a->hidden_scale ? H / 32 : L.ld1;
+    g1.q_mxs_ld = L.ld2;
+  }
   g1.B = a->w13;
   g1.b_scale = a->w13_scale;
   g1.bias = static_cast<const uint16_t*>(a->w13_bias);
@@ -626,10 +672,11 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w13_scale)
                                                     : nullptr;
   if (glu) {
-    rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_GLU, fp8, g1, L.grid_blocks, L.acts, st);
+    rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_GLU, fp8 || mx, g1, L.grid_blocks,
+                          mx ? static_cast<void*>(L.acts8) : static_cast<void*>(L.acts), st);
     if (rc) return rc;
   } else {
-    rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g1, L.grid_blocks, nullptr,
+    rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_STORE, false, g1, L.grid_blocks, nullptr,
                           st);
     if (rc) return rc;
     const FusedActArgs f{L.g1, L.act, L.acts, L.ntp, L.max_padded, I,
@@ -648,6 +695,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   GemmArgs g2{};
   g2.A = L.act;
   g2.a_scale = fp8 ? L.acts : nullptr;
+  if (mx) {
+    g2.a_mxs = L.acts8;
+    g2.a_mxs_ld = L.ld2;
+  }
   g2.B = a->w2;
   g2.b_scale = a->w2_scale;
   g2.bias = static_cast<const uint16_t*>(a->w2_bias);
@@ -674,7 +725,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   // split-K decode: the partial sums are finished by the top-k reduction
   const bool fuse_reduce = L.tile == TILE_STREAM && L.ks2 > 1 && k <= kFuseMaxTopk;
   g2.partials_only = fuse_reduce;
-  rc = launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g2, L.grid_blocks, nullptr, st);
+  rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_STORE, false, g2, L.grid_blocks, nullptr, st);
   if (rc) return rc;
   if (int m = mark(4)) return m;
   if (fuse_reduce) {

@@ -13,6 +13,14 @@ namespace mi355 {
 //   STORE: D[row, n] = T(sum_k A[row,k] W_e[n,k] + bias_e[n])
 //   GLU:   g = T(acc(n) + b(n)), u = T(acc(I+n) + b(I+n)),
 //          D[row, n] = act(g, u)          (n < N = I; W_e has 2I rows)
+// Recipe codes of the grouped-GEMM kernels beyond the C ABI's: e2m1
+// activations with e8m0 scales against mxfp4 weights (both scales in the
+// MFMA), which the fused layer runs for mxfp4 with pre-quantised inputs.
+constexpr int RECIPE_MX4A4 = 5;
+__host__ __device__ constexpr bool is_mx_recipe(int r) {
+  return r == MI355MOE_RECIPE_MXFP8 || r == RECIPE_MX4A4;
+}
+
 struct GemmArgs {
   const void* A;
   const float* a_scale;  // fp8: [rowsA, K/128]
@@ -58,6 +66,13 @@ struct GemmArgs {
   // 16-bit type: D = T(s_e * sum_k A W_e + bias_e)).
   const float* expert_scale;
   int32_t w_group;       // recipe INT4: K values per 16-bit scale (32..256)
+  // MX recipes: e8m0 activation scales u8, row r's 32-K group g at
+  // a_mxs[r * a_mxs_ld + g] (a_mxs_ld >= K/32; a multiple of 4 where a kernel
+  // moves them four at a time); the w13 epilogue of the fused layer writes
+  // its quantised output's scales to qs with row stride q_mxs_ld.
+  const uint8_t* a_mxs;
+  int64_t a_mxs_ld;
+  int64_t q_mxs_ld;
 };
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };
@@ -213,6 +228,10 @@ int run_sort_quant_fp8(const void* ids, int ids_dtype, int64_t numel, int64_t id
                        int64_t max_padded, int32_t* eids, int64_t max_blocks, int32_t* ntp,
                        int32_t* inv, int32_t pad, int32_t* cum_out, const void* x, bool f16,
                        uint8_t* xq, float* xs, int64_t rows, int64_t cols, hipStream_t st);
+// mxfp8 quantisation (per 32, ue8m0 scales stored as e8m0 bytes) of a
+// 16-bit x [rows, cols] (elementwise.hip).
+int mx8_quant_rows(const void* x, bool f16, uint8_t* q, uint8_t* s, int64_t s_ld,
+                   int64_t rows, int64_t cols, hipStream_t st);
 // K stages per split of the STREAM family for a GEMM of n_tiles output tiles
 // over about `blocks` expert blocks (1: no split)
 int stream_ksplit(int64_t n_tiles, int64_t blocks, int64_t K);

@@ -343,7 +343,9 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
   const int64_t avg = active > 0 ? slots / active : 0;
   GemmTile t;
   int b;
-  if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
+  if (is_mx_recipe(recipe)) {
+    t = TILE_STREAM, b = 16;
+  } else if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
     // a 320-slot fp8 stage is 73 KB, so the WIDE kernel keeps one stage of
     // DMA in flight against the 128-slot kernel's two: it wins where experts
     // average well above 128 slots (fewer weight passes), not at about 128
@@ -363,7 +365,7 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     else if (wide_ok) t = TILE_WIDE, b = kWideBM;
     else t = TILE_BIG, b = 128;
   }
-  if (force >= 0) {
+  if (force >= 0 && !is_mx_recipe(recipe)) {
     t = static_cast<GemmTile>(force);
     if (t == TILE_WIDE && !wide_ok) t = TILE_BIG;
     b = t == TILE_STREAM ? 16
@@ -384,9 +386,10 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
              (recipe == MI355MOE_RECIPE_FP8BLOCK &&
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
                (tile == TILE_BIG && big8_supported(recipe, a)))) ||
-             recipe == MI355MOE_RECIPE_MXFP4,
-         "K-blocked weights need the bf16 (K % 32 == 0), fp8block or mxfp4 "
+             recipe == MI355MOE_RECIPE_MXFP4 || is_mx_recipe(recipe),
+         "K-blocked weights need the bf16 (K % 32 == 0), fp8block, mxfp4 or mxfp8 "
          "recipe and a kernel family that reads them");
+  MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM, "MX recipes run the STREAM kernels");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:

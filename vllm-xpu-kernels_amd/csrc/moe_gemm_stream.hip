@@ -55,14 +55,48 @@ struct Frag<MI355MOE_RECIPE_MXFP4> {     // 32 e2m1 + e8m0 of the weight row
 };
 template <>
 struct Frag<MI355MOE_RECIPE_INT4> : Frag<MI355MOE_RECIPE_MXFP4> {};  // 32 int4 + scale
+template <>
+struct Frag<MI355MOE_RECIPE_MXFP8> {     // 32 e4m3 of the weight / act row + e8m0 codes
+  uint4 w[2][2];
+  uint32_t ws[2];
+  uint4 x[2];
+  uint32_t xs;
+};
+template <>
+struct Frag<RECIPE_MX4A4> {              // 32 e2m1 (16 bytes) of each + e8m0 codes
+  uint4 w[2];
+  uint32_t ws[2];
+  uint4 x;
+  uint32_t xs;
+};
+
+// MX recipes: one 16x16x128 MFMA per stage with the e8m0 codes of both
+// operands in the instruction (format 0 e4m3, 4 e2m1), accumulating in c.
+// Lane l holds row l % 16, and its code scales K block l / 16 of that row.
+// e2m1 operand: K 32q..32q+31 (q = l / 16) in the low four dwords; e4m3
+// operand: K 16q..16q+15 in dwords 0-3 and 64+16q..64+16q+15 in dwords 4-7
+// (measured with a one-wave probe; the unit-scale fp8 kernels do not care,
+// both operands sharing any K order).
+template <int FMT>
+__device__ __forceinline__ f32x4 mma_mx(uint4 a0, uint4 a1, uint32_t as, uint4 b0, uint4 b1,
+                                        uint32_t bs, f32x4 c) {
+  i32x8 a = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+             (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+  i32x8 b = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w,
+             (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT, FMT, 0, as, 0, bs);
+}
 
 template <int RECIPE, int EPI, bool QOUT, int PD, bool F16>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
   constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
+  constexpr bool kMx8 = RECIPE == MI355MOE_RECIPE_MXFP8;
+  constexpr bool kMx4 = RECIPE == RECIPE_MX4A4;
+  constexpr bool kMx = kMx8 || kMx4;
   constexpr bool kGlu = EPI == EPI_GLU;
-  constexpr int XB = kFp8 ? 1 : 2;
+  constexpr int XB = (kFp8 || kMx8) ? 1 : 2;  // bytes per activation element (mx4: packed)
 
   __shared__ int s_arow[16];
   __shared__ int s_drow[16];
@@ -85,7 +119,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   // output columns of this wave: GLU 16 activation columns, STORE 32 columns
   const int64_t col0 = static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) +
                        wave * (kGlu ? 16 : 32);
-  const int64_t wrow_bytes = kFp4 ? K / 2 : K * XB;
+  const int64_t wrow_bytes = (kFp4 || kMx4) ? K / 2 : K * XB;
   const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
                         static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
   int64_t wrow[2];
@@ -97,14 +131,16 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
   }
   // weights (and mxfp4 scales) may be K-blocked
-  const WStride wst = kFp4 ? w_stride4(a) : (kFp8 ? w_stride8(a) : w_stride16(a));
+  const WStride wst = (kFp4 || kMx4) ? w_stride4(a) : ((kFp8 || kMx8) ? w_stride8(a) : w_stride16(a));
   const WStride sst = s_stride4(a);
   const uint8_t* wp0 = wexp + wrow[0] * wst.row;
   const uint8_t* wp1 = wexp + wrow[1] * wst.row;
   const int arow = s_arow[l16];
   const bool xok = arow >= 0;
   const uint8_t* xp = static_cast<const uint8_t*>(a.A) +
-                      static_cast<int64_t>(xok ? arow : 0) * K * XB;
+                      static_cast<int64_t>(xok ? arow : 0) * (kMx4 ? K / 2 : K * XB);
+  const uint8_t* xsp8 = kMx ? a.a_mxs + static_cast<int64_t>(xok ? arow : 0) * a.a_mxs_ld
+                            : nullptr;
   // fp8 weight-block scale rows (16-row sub-tiles sit inside one 128-row block)
   int64_t wsr[2];
   wsr[0] = (wrow[0] / 128);
@@ -117,7 +153,36 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   // chunk and compute() zeroes it.  A load under a condition would make the
   // compiler wait for every prefetched stage where the branches join.
   auto load = [&](Frag<RECIPE>& f, int64_t k0) {
-    if constexpr (kFp8) {  // K % 128 == 0: no tail
+    if constexpr (kMx) {  // K % 32 == 0; addresses clamped into range
+      // the lane's e8m0 codes: block q of the stage (row l16)
+      const int64_t k = k0 + 32 * q;
+      const int64_t kb = (k < K ? k : K - 32) / 32;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        f.ws[t] = w4_scale_code<MI355MOE_RECIPE_MXFP4>(a, e, wrow[t], kb, sst);
+      f.xs = xsp8[kb];
+      if constexpr (kMx8) {
+        // e4m3 operand bytes 0-15 hold K 16q..16q+15 of the stage, bytes
+        // 16-31 K 64+16q..64+16q+15 (lane groups 0-1 fill scale block 0
+        // and 2, groups 2-3 blocks 1 and 3)
+        const int64_t h0 = k0 + 16 * q, h1 = k0 + 64 + 16 * q;
+        const int64_t c0 = h0 < K ? h0 : K - 16, c1 = h1 < K ? h1 : K - 16;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint8_t* wp = t ? wp1 : wp0;
+          f.w[t][0] = *reinterpret_cast<const uint4*>(wp + (c0 >> 7) * wst.kblk + (c0 & 127));
+          f.w[t][1] = *reinterpret_cast<const uint4*>(wp + (c1 >> 7) * wst.kblk + (c1 & 127));
+        }
+        f.x[0] = *reinterpret_cast<const uint4*>(xp + c0);
+        f.x[1] = *reinterpret_cast<const uint4*>(xp + c1);
+      } else {
+        // e2m1: the lane's 32 values are K 32q..32q+31 of the stage
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          f.w[t] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + kb * wst.kblk);
+        f.x = *reinterpret_cast<const uint4*>(xp + kb * 16);
+      }
+    } else if constexpr (kFp8) {  // K % 128 == 0: no tail
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const uint8_t* p = (t ? wp1 : wp0) + (k0 >> 7) * wst.kblk + 32 * q;
@@ -158,20 +223,36 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 
   auto compute = [&](const Frag<RECIPE>& fin, int64_t k0) {
     Frag<RECIPE> f = fin;
-    if (k0 + KS > K) {  // the last stage of a K that is not a multiple of 128
+    if (!kMx && k0 + KS > K) {  // the last stage of a K that is not a multiple of 128
       const uint4 z4 = make_uint4(0, 0, 0, 0);
       if constexpr (kFp4) {
         if (k0 + 32 * q >= K) {
           f.w[0] = f.w[1] = z4;
           f.sc[0] = f.sc[1] = 0u;
         }
-      } else if constexpr (!kFp8) {
+      } else if constexpr (!kFp8 && !kMx) {
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
           if (k0 + 32 * s2 + 8 * q + 8 > K) f.w[0][s2] = f.w[1][s2] = z4;
       }
     }
-    if constexpr (kFp8) {
+    if constexpr (kMx) {
+      // past K (last stage of a K % 128 != 0): zero weights, unit scales
+      const uint4 z4 = make_uint4(0, 0, 0, 0);
+      const bool slive = k0 + 32 * q < K;  // this lane's scale block
+      const uint32_t xs = slive ? f.xs : 127u;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t ws = slive ? f.ws[t] : 127u;
+        if constexpr (kMx8) {
+          const bool live0 = k0 + 32 * (q >> 1) < K, live1 = k0 + 64 + 32 * (q >> 1) < K;
+          acc[t] = mma_mx<0>(live0 ? f.w[t][0] : z4, live1 ? f.w[t][1] : z4, ws, f.x[0], f.x[1],
+                             xs, acc[t]);
+        } else {
+          acc[t] = mma_mx<4>(slive ? f.w[t] : z4, z4, ws, f.x, z4, xs, acc[t]);
+        }
+      }
+    } else if constexpr (kFp8) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const f32x4 p = mma_fp8(f.w[t][0], f.w[t][1], f.x[0], f.x[1]);
@@ -274,7 +355,45 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       ov[t][r] = nok ? v : 0.f;
     }
   }
-  if constexpr (QOUT) {
+  if constexpr (QOUT && kMx) {
+    // MX activation for the w2 GEMM, one e8m0 scale per 32 columns (the
+    // output columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
+    // with ue8m0 scales, mxfp4 as per_token_group_quant_mxfp4 (eps 1e-10)
+    float m = 1e-10f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[0][r]));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (q == 0) s_amax[wave][l16] = m;
+    __syncthreads();
+    if (drow < 0) return;
+    const float am = fmaxf(s_amax[wave & ~1][l16], s_amax[wave | 1][l16]);
+    int ex;
+    if constexpr (kMx8) ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
+    else ex = ceil_log2(fmaxf(fabsf(am / 6.0f), 1e-10f));
+    const float inv = 1.0f / pow2i(ex);
+    // N % 32 == 0: a lane's 4 columns, and a wave pair's 32, lie wholly
+    // inside or wholly past N (the last column tile of an N % 128 != 0)
+    if (col0 + 4 * q >= N) return;
+    if ((wave & 1) == 0 && q == 0)
+      static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + col0 / 32] =
+          static_cast<uint8_t>(ex + 127);
+    if constexpr (kMx8) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        w |= f32_to_e4m3(fminf(fmaxf(ov[0][r] * inv, -448.f), 448.f)) << (8 * r);
+      *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * N +
+                                   col0 + 4 * q) = w;
+    } else {
+      uint32_t w = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        w |= fp4_code(fminf(fmaxf(ov[0][r] * inv, -6.f), 6.f)) << (4 * r);
+      *reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * (N / 2) +
+                                   (col0 + 4 * q) / 2) = static_cast<uint16_t>(w);
+    }
+  } else if constexpr (QOUT) {
     float m = 1e-10f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[0][r]));
@@ -364,7 +483,16 @@ int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
                            int64_t max_blocks, void* qs, hipStream_t st) {
   if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
   if (qout) {
-    MI_ARG(recipe == MI355MOE_RECIPE_FP8BLOCK && epi == EPI_GLU && a.N % 128 == 0,
+    MI_ARG(epi == EPI_GLU, "quantised activation output needs the GLU epilogue");
+    if (recipe == MI355MOE_RECIPE_MXFP8) {
+      MI_ARG(a.N % 32 == 0, "mxfp8 activation output needs I % 32 == 0");
+      return launch_stream<MI355MOE_RECIPE_MXFP8, EPI_GLU, true>(a, max_blocks, qs, st);
+    }
+    if (recipe == RECIPE_MX4A4) {
+      MI_ARG(a.N % 32 == 0, "mxfp4 activation output needs I % 32 == 0");
+      return launch_stream<RECIPE_MX4A4, EPI_GLU, true>(a, max_blocks, qs, st);
+    }
+    MI_ARG(recipe == MI355MOE_RECIPE_FP8BLOCK && a.N % 128 == 0,
            "fp8 activation output needs the fp8block recipe and I % 128 == 0");
     return launch_stream<MI355MOE_RECIPE_FP8BLOCK, EPI_GLU, true>(a, max_blocks, qs, st);
   }
@@ -381,6 +509,12 @@ int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
     case MI355MOE_RECIPE_INT4:
       return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_INT4, EPI_GLU, false>(a, max_blocks, qs, st)
                             : launch_stream<MI355MOE_RECIPE_INT4, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_MXFP8:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_MXFP8, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_MXFP8, EPI_STORE, false>(a, max_blocks, qs, st);
+    case RECIPE_MX4A4:
+      return epi == EPI_GLU ? launch_stream<RECIPE_MX4A4, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<RECIPE_MX4A4, EPI_STORE, false>(a, max_blocks, qs, st);
     default:
       return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
   }

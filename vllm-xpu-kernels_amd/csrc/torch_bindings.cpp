@@ -796,14 +796,33 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
                      const std::optional<at::Tensor>& hidden_scale, int64_t w_group) {
   check_gpu(output, "output");
   check_gpu(hidden_states, "hidden_states");
+  // packed e2m1 hidden states (mxfp4 with a1q_scale) hold two values a byte
+  const bool packed4 = hidden_scale && recipe == MI355MOE_RECIPE_MXFP4;
+  const int64_t hidden = packed4 ? 2 * hidden_states.size(1) : hidden_states.size(1);
   if (hidden_scale) {
     check_gpu(*hidden_scale, "hidden_scale");
-    TORCH_CHECK(hidden_states.scalar_type() == at::kFloat8_e4m3fn,
-                "pre-quantised hidden_states must be float8_e4m3fn");
-    TORCH_CHECK(hidden_scale->scalar_type() == at::kFloat && hidden_scale->dim() == 2 &&
-                    hidden_scale->size(0) == hidden_states.size(0) &&
-                    hidden_scale->size(1) * 128 == hidden_states.size(1),
-                "a1q_scale must be float32 [num_tokens, hidden_size / 128]");
+    TORCH_CHECK(hidden_scale->is_contiguous() && hidden_states.is_contiguous(),
+                "a1q_scale and hidden_states must be contiguous");
+    if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
+      TORCH_CHECK(hidden_states.scalar_type() == at::kFloat8_e4m3fn,
+                  "pre-quantised hidden_states must be float8_e4m3fn");
+      TORCH_CHECK(hidden_scale->scalar_type() == at::kFloat && hidden_scale->dim() == 2 &&
+                      hidden_scale->size(0) == hidden_states.size(0) &&
+                      hidden_scale->size(1) * 128 == hidden,
+                  "a1q_scale must be float32 [num_tokens, hidden_size / 128]");
+    } else {
+      TORCH_CHECK(recipe == MI355MOE_RECIPE_MXFP8 || recipe == MI355MOE_RECIPE_MXFP4,
+                  "pre-quantised hidden_states need the fp8block, mxfp8 or mxfp4 recipe");
+      TORCH_CHECK(packed4 ? hidden_states.element_size() == 1 &&
+                                hidden_states.scalar_type() != at::kFloat8_e4m3fn
+                          : hidden_states.scalar_type() == at::kFloat8_e4m3fn,
+                  "pre-quantised hidden_states must be float8_e4m3fn (mxfp8) or packed "
+                  "e2m1 (mxfp4, uint8 / float4_e2m1fn_x2 [num_tokens, hidden_size / 2])");
+      TORCH_CHECK(hidden_scale->element_size() == 1 && hidden_scale->dim() == 2 &&
+                      hidden_scale->size(0) == hidden_states.size(0) &&
+                      hidden_scale->size(1) * 32 == hidden,
+                  "a1q_scale must be e8m0 (uint8 / float8_e8m0fnu) [num_tokens, hidden_size / 32]");
+    }
   }
   check_gpu(topk_weights, "topk_weights");
   check_gpu(topk_ids, "topk_ids");
@@ -812,7 +831,9 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
   TORCH_CHECK(topk_weights.sizes() == topk_ids.sizes(),
               "topk_weights must have the shape of topk_ids");
-  TORCH_CHECK(output.sizes() == hidden_states.sizes(), "output must match hidden_states");
+  TORCH_CHECK(output.dim() == 2 && output.size(0) == hidden_states.size(0) &&
+                  output.size(1) == hidden,
+              "output must match hidden_states");
   // The kernels write the output, and read the biases, in the call's 16-bit
   // type: hidden_states' type, or the output's when they come quantised.
   if (hidden_scale) {
@@ -828,7 +849,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.act_dtype = dtype_code((hidden_scale ? output : hidden_states).scalar_type());
   a.ids_dtype = dtype_code(topk_ids.scalar_type());
   a.num_tokens = hidden_states.size(0);
-  a.hidden = hidden_states.size(1);
+  a.hidden = hidden;
   a.inter = inter_size;
   a.num_experts = w13.size(0);
   a.topk = topk_ids.size(1);
@@ -848,7 +869,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.swiglu_limit = 7.0f;
   a.output = output.data_ptr();
   a.w_layout = static_cast<int>(w_layout);
-  a.hidden_scale = hidden_scale ? hidden_scale->data_ptr<float>() : nullptr;
+  a.hidden_scale = hidden_scale ? hidden_scale->data_ptr() : nullptr;
   a.w_group = w_group;
   for (const auto* b : {&w13_bias, &w2_bias})
     if (b->has_value())

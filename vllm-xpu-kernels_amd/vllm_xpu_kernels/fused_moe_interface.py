@@ -24,9 +24,10 @@ import torch
 from . import _ops  # noqa: F401  (loads the HIP library)
 
 REF_FUSED_MOE_ENV = "VLLM_XPU_FUSED_MOE_USE_REF"
+USE_MXFP4_FP8_ENV = "VLLM_XPU_FUSED_MOE_USE_MXFP4_FP8"
 FP8_BLOCK_SIZE = 128
 
-RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4, RECIPE_INT4 = 0, 1, 2, 3
+RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4, RECIPE_INT4, RECIPE_MXFP8 = 0, 1, 2, 3, 4
 ACT_SILU, ACT_SWIGLUOAI, ACT_GELU, ACT_GELU_TANH, ACT_SWIGLUSTEP, ACT_RELU2 = range(6)
 # reference fused_moe_interface.py:119-133, 239-254
 _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
@@ -122,10 +123,6 @@ class XpuFusedMoe:
         assert w13.is_contiguous() and w2.is_contiguous()
         (is_fp8, is_int4, is_mxfp4, is_mxfp8,
          is_block_fp8) = _get_weights_dtype(w13, w13_scales)
-        if is_mxfp8:
-            raise NotImplementedError(
-                "recipe mxfp8 is not implemented on MI355X (the reference has no "
-                "kernel for it either); use bf16/fp16, fp8, int4 or mxfp4")
         self.inter_size = _get_inter_size(w13, w13_scales, is_int4, is_mxfp4,
                                           is_block_fp8)
         self.n_experts_per_token = n_experts_per_token
@@ -162,8 +159,13 @@ class XpuFusedMoe:
             self.recipe = "int4"
             self._recipe = RECIPE_INT4
         elif is_mxfp4:
-            self.recipe = "mxfp4"
+            # the reference's recipe selector (fused_moe_interface.py:33-44);
+            # its kernel path runs mxfp4_fp8 as mxfp4
+            self.recipe = "mxfp4_fp8" if _is_env_enabled(USE_MXFP4_FP8_ENV) else "mxfp4"
             self._recipe = RECIPE_MXFP4
+        elif is_mxfp8:
+            self.recipe = "mxfp8"
+            self._recipe = RECIPE_MXFP8
         else:
             self.recipe = "bf16"
             self._recipe = RECIPE_BF16
@@ -216,6 +218,13 @@ class XpuFusedMoe:
             w13c = w13.transpose(1, 2).contiguous()
             w2c = w2.transpose(1, 2).contiguous()
             s13c = s2c = None
+        elif self._recipe == RECIPE_MXFP8:
+            # reference layout (moe_utils.py:80-82): w [E, K, N] e4m3 with e8m0
+            # scales [E, K/32, N] -> [E, N, K] and [E, N, K/32]
+            w13c = w13.transpose(1, 2).contiguous()
+            w2c = w2.transpose(1, 2).contiguous()
+            s13c = s13.view(torch.uint8).transpose(1, 2).contiguous()
+            s2c = s2.view(torch.uint8).transpose(1, 2).contiguous()
         elif self._recipe == RECIPE_FP8BLOCK:
             # [E, N, K] preferred when ambiguous, as the reference
             # (grouped_gemm_xe2_interface.hpp:206-223)
@@ -246,11 +255,12 @@ class XpuFusedMoe:
             H = w13c.shape[2] * 2
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
                   (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and K2 <= 8192) or
+                  (self._recipe == RECIPE_MXFP8 and H % 128 == 0 and K2 % 128 == 0) or
                   self._recipe == RECIPE_MXFP4)
         self._kblock = kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk"
         if self._kblock and not self._fp8_expert:
             w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)
-            if self._recipe == RECIPE_MXFP4:
+            if self._recipe in (RECIPE_MXFP4, RECIPE_MXFP8):
                 s13c, s2c = pack_scales_kblock(s13c), pack_scales_kblock(s2c)
             self._w_layout = WLAYOUT_KBLOCK
         if self._fp8_expert and self._kblock:
@@ -300,13 +310,25 @@ class XpuFusedMoe:
     def apply(self, output, hidden_states, topk_weights, topk_ids,
               expert_map=None, a1q_scale=None):
         if a1q_scale is not None:
-            # reference fused_moe_interface.py:326-360: hidden_states already
-            # quantised, the layer consumes them with their scales
-            if self._recipe != RECIPE_FP8BLOCK:
+            # hidden_states already quantised, consumed with their scales as
+            # the reference's torch path dequantises them (moe_utils.py:189-199,
+            # 285-300): fp8block e4m3 + f32 [T, H/128]; mxfp8 e4m3 + e8m0
+            # [T, H/32]; mxfp4 packed e2m1 [T, H/2] + e8m0 [T, H/32], both GEMMs
+            # then e2m1 x e2m1
+            if self._recipe == RECIPE_FP8BLOCK:
+                a1q_scale = a1q_scale.to(torch.float32).contiguous()
+            elif self._recipe in (RECIPE_MXFP8, RECIPE_MXFP4):
+                if self.recipe == "mxfp4_fp8":
+                    # the reference's quant_act_xpu has no mxfp4_fp8 path
+                    raise NotImplementedError(
+                        "Unsupported recipe for quant_act_xpu: mxfp4_fp8")
+                a1q_scale = a1q_scale.view(torch.uint8).contiguous()
+                if self._recipe == RECIPE_MXFP4:
+                    hidden_states = hidden_states.view(torch.uint8)
+            else:
                 raise NotImplementedError(
-                    "pre-quantised activations (a1q_scale) are supported for "
-                    "the fp8 block-scaled recipe (e4m3 + [T, H/128] scales)")
-            a1q_scale = a1q_scale.to(torch.float32).contiguous()
+                    "pre-quantised activations (a1q_scale) are supported for the "
+                    "fp8block, mxfp8 and mxfp4 recipes")
         # the call's 16-bit type: that of the activations, or of the output
         # when they come quantised; the kernels write the output, and read
         # the biases, in it
@@ -325,6 +347,10 @@ class XpuFusedMoe:
         if expert_map is None and self.ep_size > 1:
             expert_map = self.expert_map
         clamp = float(self.gemm1_clamp_limit) if self.gemm1_clamp_limit else 0.0
+        if self._recipe == RECIPE_MXFP8:
+            # the reference runs mxfp8 through ref_fused_moe, which takes no
+            # clamp limit (fused_moe_interface.py:27-30, 296-317)
+            clamp = 0.0
         b13, b2 = self._biases(dt16)
         w13, w2 = self._call_weights(dt16)
         s13, s2 = self._scales(dt16)

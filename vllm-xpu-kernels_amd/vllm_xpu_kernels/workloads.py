@@ -25,7 +25,7 @@ class MoeConfig:
     inter: int
     experts: int
     topk: int
-    recipe: str                 # "bf16" | "fp8block" | "mxfp4"
+    recipe: str                 # "bf16" | "fp8block" | "mxfp4" | "mxfp8"
     routing: str                # "softmax" | "grouped_sigmoid"
     activation: str = "silu"
     renormalize: bool = True
@@ -99,6 +99,20 @@ def mxfp4_quant(w: torch.Tensor):
             e.to(torch.uint8).reshape(shp[:-1] + (K // 32,)))
 
 
+def mxfp8_quant(w: torch.Tensor):
+    """[..., K] fp32 -> e4m3 [..., K] + e8m0 [..., K/32]: exponent
+    ceil(log2(amax / 448)) per 32 values (the least power of two that keeps
+    the block within e4m3's range), values rounded to nearest even."""
+    shp = w.shape
+    K = shp[-1]
+    x = w.float().reshape(-1, K // 32, 32)
+    amax = x.abs().amax(-1, keepdim=True)
+    e = torch.clamp(torch.ceil(torch.log2(amax / 448.0)), -127, 127) + 127
+    e = torch.nan_to_num(e, nan=255.0)
+    q = torch.clamp(x * torch.exp2(127 - e), -448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.reshape(shp), e.to(torch.uint8).reshape(shp[:-1] + (K // 32,))
+
+
 @dataclass
 class MoeWeights:
     """Weights in the reference's constructor layouts (see XpuFusedMoe)."""
@@ -128,6 +142,10 @@ def expert_weights_nk(cfg: MoeConfig, e: int, device, seed: int = 0):
         q13, s13 = fp8_block_quant(w13)
         q2, s2 = fp8_block_quant(w2)
         return q13, s13, q2, s2
+    if cfg.recipe == "mxfp8":
+        q13, s13 = mxfp8_quant(w13)
+        q2, s2 = mxfp8_quant(w2)
+        return q13, s13, q2, s2
     q13, s13 = mxfp4_quant(w13)
     q2, s2 = mxfp4_quant(w2)
     return q13, s13, q2, s2
@@ -153,6 +171,12 @@ def make_weights(cfg: MoeConfig, device, seed: int = 0) -> MoeWeights:
         w2 = torch.empty(E, H, K2, dtype=torch.float8_e4m3fn, device=device)
         s13 = torch.empty(E, 2 * I // 128, H // 128, device=device)
         s2 = torch.empty(E, H // 128, K2 // 128, device=device)
+    elif cfg.recipe == "mxfp8":
+        # reference layout (moe_utils.py:80-82): [E, K, N] + e8m0 [E, K/32, N]
+        w13 = torch.empty(E, H, 2 * I, dtype=torch.float8_e4m3fn, device=device)
+        w2 = torch.empty(E, K2, H, dtype=torch.float8_e4m3fn, device=device)
+        s13 = torch.empty(E, H // 32, 2 * I, dtype=torch.uint8, device=device)
+        s2 = torch.empty(E, K2 // 32, H, dtype=torch.uint8, device=device)
     else:
         w13 = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=device)
         w2 = torch.empty(E, H, K2 // 2, dtype=torch.uint8, device=device)
@@ -163,6 +187,11 @@ def make_weights(cfg: MoeConfig, device, seed: int = 0) -> MoeWeights:
         if cfg.recipe == "bf16":
             w13[e].copy_(a.t())   # reference bf16 layout [E, K, N]
             w2[e].copy_(b.t())
+        elif cfg.recipe == "mxfp8":
+            w13[e].copy_(a.t())
+            w2[e].copy_(b.t())
+            s13[e].copy_(sa.t())
+            s2[e].copy_(sb.t())
         else:
             w13[e].copy_(a)
             w2[e].copy_(b)
@@ -217,6 +246,8 @@ def algorithmic_bytes(cfg: MoeConfig, T: int, active: int) -> float:
         wb = 2 * n
     elif cfg.recipe == "fp8block":
         wb = n + 4 * n / (128 * 128)
+    elif cfg.recipe == "mxfp8":
+        wb = n + n / 32
     else:
         wb = n / 2 + n / 32
     if cfg.bias:
@@ -228,7 +259,7 @@ def algorithmic_flops(cfg: MoeConfig, T: int) -> float:
     return 6.0 * T * cfg.topk * cfg.hidden * cfg.inter
 
 
-PEAK_TFLOPS = {"bf16": 2500.0, "fp8block": 5000.0, "mxfp4": 2500.0}
+PEAK_TFLOPS = {"bf16": 2500.0, "fp8block": 5000.0, "mxfp4": 2500.0, "mxfp8": 5000.0}
 PEAK_HBM_GBS = 8000.0
 
 
@@ -245,6 +276,6 @@ def expected_active(E: int, slots: int) -> float:
 
 __all__ = ["MoeConfig", "CONFIGS", "make_weights", "make_activations",
            "make_router_logits", "make_correction_bias", "route",
-           "fp8_block_quant", "mxfp4_quant", "expert_weights_nk",
+           "fp8_block_quant", "mxfp4_quant", "mxfp8_quant", "expert_weights_nk",
            "algorithmic_bytes", "algorithmic_flops", "roofline_time_s",
            "math"]
