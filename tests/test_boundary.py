@@ -379,3 +379,48 @@ def test_fused_moe_noalloc_rejects_calls_beyond_its_scratch(lib):
     rc = lib.mi355moe_fused_moe_noalloc(ctypes.byref(a), None)
     assert rc == -4
     assert b"more than the static" in lib.mi355moe_last_error()
+
+
+@pytest.mark.parametrize("weight_layout", ["nk", "kn"])
+def test_block_fp8_inter_size_uses_scales(monkeypatch, weight_layout):
+    """tests/fused_moe/test_fused_moe.py:37-60: fp8 weights [2, 512, 256] (or
+    their transpose) with 128x128 block scales [2, 4, 2]: the intermediate
+    size comes from the scales, 4 * 128 / 2 = 256, whatever the layout."""
+    from vllm_xpu_kernels import fused_moe_interface as F
+    monkeypatch.setenv(F.WEIGHT_LAYOUT_ENV, "nk")
+    weight_nk = torch.zeros(2, 512, 256, dtype=torch.float8_e4m3fn)
+    weight = weight_nk.transpose(-1, -2).contiguous() if weight_layout == "kn" else weight_nk
+    w2 = torch.zeros(2, 256, 256, dtype=torch.float8_e4m3fn)
+    moe = F.XpuFusedMoe(weight, torch.ones(2, 4, 2), None, w2, torch.ones(2, 2, 2), None,
+                        1, "silu", 2)
+    assert moe.inter_size == 256 and moe.recipe == "fp8block"
+
+
+def test_mx_recipe_selection(monkeypatch):
+    """Recipe detection of the reference (fused_moe_interface.py:33-61): e4m3
+    weights with uint8 scales are mxfp8; e2m1 weights are mxfp4, or
+    mxfp4_fp8 under VLLM_XPU_FUSED_MOE_USE_MXFP4_FP8, which then refuses
+    pre-quantised input as the reference's quant_act_xpu does."""
+    from vllm_xpu_kernels import fused_moe_interface as F
+    monkeypatch.setenv(F.WEIGHT_LAYOUT_ENV, "nk")
+    E, H, I = 2, 64, 32
+    moe8 = F.XpuFusedMoe(torch.zeros(E, H, 2 * I, dtype=torch.float8_e4m3fn),
+                         torch.zeros(E, H // 32, 2 * I, dtype=torch.uint8), None,
+                         torch.zeros(E, I, H, dtype=torch.float8_e4m3fn),
+                         torch.zeros(E, I // 32, H, dtype=torch.uint8), None, 1, "silu", E)
+    assert moe8.recipe == "mxfp8" and moe8.inter_size == I
+    assert tuple(moe8.w13.shape) == (E, 2 * I, H)
+    assert tuple(moe8.gemm1_wei_scales.shape) == (E, 2 * I, H // 32)
+    w13 = torch.zeros(E, 2 * I, H // 2, dtype=torch.uint8).view(torch.float4_e2m1fn_x2)
+    w2 = torch.zeros(E, H, I // 2, dtype=torch.uint8).view(torch.float4_e2m1fn_x2)
+    s13 = torch.zeros(E, 2 * I, H // 32, dtype=torch.uint8)
+    s2 = torch.zeros(E, H, I // 32, dtype=torch.uint8)
+    assert F.XpuFusedMoe(w13, s13, None, w2, s2, None, 1, "silu", E).recipe == "mxfp4"
+    monkeypatch.setenv(F.USE_MXFP4_FP8_ENV, "1")
+    moe = F.XpuFusedMoe(w13, s13, None, w2, s2, None, 1, "silu", E)
+    assert moe.recipe == "mxfp4_fp8"
+    with pytest.raises(NotImplementedError, match="mxfp4_fp8"):
+        moe.apply(torch.empty(3, H, dtype=torch.bfloat16),
+                  torch.zeros(3, H // 2, dtype=torch.uint8), torch.zeros(3, 1),
+                  torch.zeros(3, 1, dtype=torch.int32),
+                  a1q_scale=torch.zeros(3, H // 32, dtype=torch.uint8))

@@ -216,7 +216,7 @@ def test_fused_moe_c4_zipf_fp8(dev):
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
-@pytest.mark.parametrize("T", [1, 32])
+@pytest.mark.parametrize("T", [1, 32, 128])
 def test_fused_moe_c5_gpt_oss_mxfp4_swigluoai(dev, T):
     cfg, w, x, tw, ti, out, _ = _layer(_W().CONFIGS["C5"], T, dev)
     _close(out, _oracle_layer(cfg, w, x, tw, ti))

@@ -175,7 +175,7 @@ def test_moe_align_zipf_skew_c4(dev):
     logits = W.make_router_logits(cfg, 2048, dev)
     _, ids = W.route(cfg, logits)
     cnt = torch.bincount(ids.flatten().long(), minlength=128).sort(descending=True).values
-    assert 0.45 < float(cnt[:13].sum()) / ids.numel() < 0.55
+    assert 0.48 <= float(cnt[:13].sum()) / ids.numel() <= 0.52
     srt, eids, ntp = _ops().moe_align_block_size(ids, 64, 128)
     mx, nb = O.align_buffer_sizes(ids.numel(), 128, 64)
     rs, re, rn = O.moe_align_block_size(ids.cpu(), 128, 64, mx, nb)

@@ -11,6 +11,7 @@
 //      slot's row to its flat (token, j) position
 //   5. weighted top-k reduction y[t] = sum_j w[t,j] * G2[t*k + j] in fixed j
 //      order (no floating-point atomics).
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -330,6 +331,17 @@ bool epilogue_act(int act) {
   return act == MI355MOE_ACT_SILU || act == MI355MOE_ACT_SWIGLUOAI;
 }
 // Width of the activation (and K of the w2 GEMM): relu2_no_mul keeps all 2I.
+// x rounded to nearest even in the call's 16-bit type (host side).
+float round_to_16(float x, bool f16) {
+  if (f16) return static_cast<float>(static_cast<_Float16>(x));
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  if ((u & 0x7F800000u) != 0x7F800000u) u += 0x7FFFu + ((u >> 16) & 1u);
+  u &= 0xFFFF0000u;
+  std::memcpy(&x, &u, 4);
+  return x;
+}
+
 int64_t act_width(const mi355moe_fused_moe_args* a) {
   return a->activation == MI355MOE_ACT_RELU2 ? 2 * a->inter : a->inter;
 }
@@ -660,7 +672,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.K = H;
   g1.ldb_rows = 2 * I;
   g1.up_off = glu ? I : 0;
-  g1.clamp_limit = a->gemm1_clamp_limit;
+  // the reference clamps the 16-bit G1 in place: with the limit itself in
+  // that type, clamping 16-bit values needs no rounding afterwards
+  const float clamp16 = a->gemm1_clamp_limit > 0.f ? round_to_16(a->gemm1_clamp_limit, f16) : 0.f;
+  g1.clamp_limit = clamp16;
   g1.alpha = a->swiglu_alpha;
   g1.limit = a->swiglu_limit;
   g1.act = a->activation;
@@ -680,7 +695,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
                           st);
     if (rc) return rc;
     const FusedActArgs f{L.g1, L.act, L.acts, L.ntp, L.max_padded, I,
-                         a->gemm1_clamp_limit, a->swiglu_limit};
+                         clamp16, a->swiglu_limit};
     if (fp8) {
       if (f16) launch_fused_act<true, true>(a->activation, f, st);
       else launch_fused_act<true, false>(a->activation, f, st);

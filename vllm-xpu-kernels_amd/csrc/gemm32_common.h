@@ -106,10 +106,7 @@ __device__ __forceinline__ void epilogue_32x32(const GemmArgs& a, void* qs,
         float v = round16<F16>(acc[i][j][r] * es + bg[r]);
         if constexpr (kGlu) {
           float u = round16<F16>(acc[i + 2][j][r] * es + bu[r]);
-          if (a.clamp_limit > 0.f) {
-            v = fminf(v, a.clamp_limit);
-            u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-          }
+          glu_clamp(a, n0 + tile_col(i, r), v, u);
           v = round16<F16>(glu_act<F16>(v, u, a));
         }
         ov[i][j][r] = v;

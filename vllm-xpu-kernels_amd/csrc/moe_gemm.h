@@ -75,6 +75,24 @@ struct GemmArgs {
   int64_t q_mxs_ld;
 };
 
+// gemm1_clamp_limit on the (gate, up) pair of GLU output column n, both
+// already in the 16-bit type (the host rounds the limit to that type, so the
+// result needs no further rounding).  The reference clamps G1's columns
+// [0, I) from above and [I, 2I) on both sides (fused_moe_interface.py:
+// 384-389).  swigluoai's G1 interleaves gate and up (column n's pair at 2n,
+// 2n + 1): both are clamped from above, and from below where 2n >= I; for
+// the other activations gate = [0, I) and up = [I, 2I).
+__device__ __forceinline__ void glu_clamp(const GemmArgs& a, int64_t n, float& g, float& u) {
+  const float L = a.clamp_limit;
+  if (!(L > 0.f)) return;
+  const bool swig = a.act == MI355MOE_ACT_SWIGLUOAI;
+  const bool upper_half = 2 * n >= a.N;
+  g = fminf(g, L);
+  if (swig && upper_half) g = fmaxf(g, -L);
+  u = fminf(u, L);
+  if (!swig || upper_half) u = fmaxf(u, -L);
+}
+
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };
 
 // Byte strides of 16-bit weights: element (row r, k) of one expert sits at

@@ -205,10 +205,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
           float u = acc[mt][j + NT][r] * es;
           if (a.bias && nok) u += ld16<F16>(a.bias[bias_base + a.up_off + n + r]);
           u = rnd16<F16>(u);
-          if (a.clamp_limit > 0.f) {
-            v = fminf(v, a.clamp_limit);
-            u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-          }
+          glu_clamp(a, n + r, v, u);
           v = rnd16<F16>(glu16<F16>(v, u, a.act, a.alpha, a.limit));
         }
         outv[mt][j][r] = nok ? v : 0.f;

@@ -346,10 +346,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         float u = acc[1][r] * es;
         if (a.bias && nok) u += ld16<F16>(a.bias[bias_base + a.up_off + n + r]);
         u = rnd16<F16>(u);
-        if (a.clamp_limit > 0.f) {
-          v = fminf(v, a.clamp_limit);
-          u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-        }
+        glu_clamp(a, n + r, v, u);
         v = rnd16<F16>(glu16<F16>(v, u, a.act, a.alpha, a.limit));
       }
       ov[t][r] = nok ? v : 0.f;

@@ -370,10 +370,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide_kernel(const GemmArgs a) {
             float g = round16<F16>(acc[i][j][r] * es + bg[r]);
             if constexpr (kGlu) {
               float u = round16<F16>(acc[1][j][r] * es + bu[r]);
-              if (a.clamp_limit > 0.f) {
-                g = fminf(g, a.clamp_limit);
-                u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-              }
+              glu_clamp(a, n0 + tcol(i, r), g, u);
               float y;
               if (a.act == MI355MOE_ACT_SILU) {
                 y = round16<F16>(x_sigmoid(g, 1.f)) * u;

@@ -357,10 +357,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       float gv = round16<F16>(acc[i][j][r] + bg);
       if constexpr (kGlu) {
         float u = round16<F16>(acc[i + 2][j][r] + bu);
-        if (a.clamp_limit > 0.f) {
-          gv = fminf(gv, a.clamp_limit);
-          u = fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit);
-        }
+        glu_clamp(a, n0 + tcol(i, r), gv, u);
         float y;
         if (a.act == MI355MOE_ACT_SILU) {
           y = round16<F16>(x_sigmoid(gv, 1.f)) * u;

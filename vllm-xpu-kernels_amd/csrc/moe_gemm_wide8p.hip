@@ -360,10 +360,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       float gv = round16<F16>(acc[f][j][r] + bg);
       if constexpr (kGlu) {
         float u = round16<F16>(acc[1][j][r] + bu);
-        if (a.clamp_limit > 0.f) {
-          gv = round16<F16>(fminf(gv, a.clamp_limit));
-          u = round16<F16>(fminf(fmaxf(u, -a.clamp_limit), a.clamp_limit));
-        }
+        glu_clamp(a, n0 + tcol(f, r), gv, u);
         float y;
         if (a.act == MI355MOE_ACT_SILU) {
           y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
