@@ -146,6 +146,18 @@ int mi355moe_grouped_topk(void* topk_values, int32_t* topk_indices,
                           int renormalize, float routed_scaling_factor,
                           void* stream);
 
+/* Replaces the reference's fused_grouped_topk with scoring "sigmoid"
+ * (tests/ops/grouped_topk_op.py:67-92: torch sigmoid, + the correction
+ * bias, then torch.ops._moe_C.grouped_topk) in one launch: gating_output
+ * [T,E] in `dtype` (f32/bf16/f16), bias f32 [E] or null; the kernel forms
+ * scores = T(sigmoid(x)) and scores_with_bias = T(scores + bias) per element
+ * (T: the input dtype) and selects as mi355moe_grouped_topk. */
+int mi355moe_fused_grouped_topk(void* topk_values, int32_t* topk_indices,
+                                const void* gating_output, const float* bias, int dtype,
+                                int64_t num_tokens, int64_t num_experts, int64_t n_group,
+                                int64_t topk_group, int64_t topk, int renormalize,
+                                float routed_scaling_factor, void* stream);
+
 /* ----------------------------------------------------- alignment / permute */
 
 /* Replaces torch.ops._moe_C.moe_lora_align_block_size

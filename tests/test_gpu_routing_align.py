@@ -127,6 +127,38 @@ def test_grouped_topk_deepseek_shape(dev, T, dtype, renorm):
     torch.testing.assert_close(v.cpu().float(), rv.float(), rtol=4e-6 if dtype == torch.float32 else 8e-3, atol=1e-7)
 
 
+@pytest.mark.parametrize("T", [1, 64, 8192])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("E,n_group,topk_group,k", [(256, 8, 4, 8), (128, 4, 2, 6),
+                                                    (96, 3, 2, 4), (64, 1, 1, 8)])
+def test_fused_grouped_topk_equals_torch_scoring(dev, T, dtype, E, n_group, topk_group, k):
+    """One-launch sigmoid + correction bias + grouped top-k equals the
+    reference's caller-side torch ops followed by the grouped top-k op
+    (tests/ops/grouped_topk_op.py:67-92) bit for bit: same ids, same values.
+    n_group 3 takes the serial group scan, the others the shuffle merge."""
+    g = torch.Generator(device=dev).manual_seed(T + E)
+    logits = torch.randn(T, E, generator=g, device=dev).to(dtype)
+    bias = torch.randn(E, generator=g, device=dev) * 0.01
+    v, ids = _ops().fused_grouped_topk(logits, k, True, bias, n_group, topk_group,
+                                       "sigmoid", 2.5)
+    s = logits.sigmoid()
+    sb = (s + bias.unsqueeze(0)).to(dtype)
+    rv, rids = _ops().grouped_topk(s, sb, n_group, topk_group, k, True, 2.5)
+    assert torch.equal(ids, rids)
+    assert torch.equal(v, rv.float())
+    toks = torch.linspace(0, T - 1, min(T, 64)).long().to(dev)
+    ov, oids = O.grouped_topk(s[toks].cpu(), sb[toks].cpu(), n_group, topk_group, k, True, 2.5)
+    assert torch.equal(ids[toks].cpu(), oids)
+
+
+def test_fused_grouped_topk_without_bias(dev):
+    logits = torch.randn(33, 256, device=dev)
+    v, ids = _ops().fused_grouped_topk(logits, 8, False, None, 8, 4, "sigmoid", 1.0)
+    s = logits.sigmoid()
+    rv, rids = _ops().grouped_topk(s, s.clone(), 8, 4, 8, False, 1.0)
+    assert torch.equal(ids, rids) and torch.equal(v, rv)
+
+
 def test_grouped_topk_full_size_invariants(dev):
     """T=8192 (C3 prefill): every id lies in one of the 4 kept groups and the
     kept groups are the top-4 by top-2 sums; ids unique per token."""

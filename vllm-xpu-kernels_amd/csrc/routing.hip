@@ -265,53 +265,124 @@ int topk_dispatch(float* w, void* idx, int idt, int32_t* src, const void* g,
 
 // ----------------------------------------------------------------------------
 // grouped top-k (DeepSeek-V3 noaux_tc routing).  One wave per token; the
-// scores_with_bias row is staged in LDS.
+// token's scores and scores_with_bias rows are staged in LDS (no global
+// load inside the selection rounds).
 //   group score = top1 + top2 of scores_with_bias in the group (fp32 sum,
 //                 stored in the input dtype)
 //   keep topk_group groups by (score desc, group asc)
 //   ids = top-k of scores_with_bias over kept groups (value desc, id asc)
 //   w   = scores[id] / (1e-20 + sum) * rsf   (or scores[id] * rsf)
+// FUSED: the kernel reads the gating logits and forms the two rows itself,
+// as the reference's fused_grouped_topk does with torch ops
+// (tests/ops/grouped_topk_op.py:67-92, scoring "sigmoid"):
+//   scores = T(sigmoid(x)),  scores_with_bias = T(float(scores) + bias[e])
+// with T the input dtype and the sigmoid 1 / (1 + exp(-x)) in fp32.
 // ----------------------------------------------------------------------------
 constexpr int kMaxGroupedExperts = 1024;
 
 template <typename In>
+__device__ __forceinline__ float round_in(float v) {
+  if constexpr (std::is_same<In, BF16>::value) return bf16_to_f32(f32_to_bf16(v));
+  else if constexpr (std::is_same<In, F16>::value) return f16_to_f32(f32_to_f16(v));
+  else return v;
+}
+
+// top-2 (t1 >= t2) of two top-2 pairs
+__device__ __forceinline__ void merge_top2(float& t1, float& t2, float o1, float o2) {
+  if (o1 > t1) {
+    t2 = fmaxf(t1, o2);
+    t1 = o1;
+  } else {
+    t2 = fmaxf(t2, o1);
+  }
+}
+
+// Lane l holds experts e = i * 64 + l, i < VPT, of both rows in registers
+// (all loads issued up front); the group scan reads the biased row back
+// from LDS once; the k selection rounds run on the registers.
+template <typename In, bool FUSED, int VPT>
 __global__ __launch_bounds__(256) void grouped_topk_kernel(
     const void* __restrict__ scores, const void* __restrict__ scores_b,
-    void* __restrict__ out_v, int32_t* __restrict__ out_i, int num_tokens,
-    int num_experts, int n_group, int topk_group, int k, int renormalize,
+    const float* __restrict__ bias, void* __restrict__ out_v, int32_t* __restrict__ out_i,
+    int num_tokens, int num_experts, int n_group, int topk_group, int k, int renormalize,
     float rsf) {
-  __shared__ float s_sb[kWavesPerBlock][kMaxGroupedExperts];
+  __shared__ float s_sb[kWavesPerBlock][VPT * 64];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kWavesPerBlock + wave;
   if (row >= num_tokens) return;  // whole wave exits together
   const int64_t base = static_cast<int64_t>(row) * num_experts;
   float* sb = s_sb[wave];
-  for (int e = lane; e < num_experts; e += 64) {
-    float v = load_in<In>(scores_b, base + e);
-    sb[e] = v;
+  float sc[VPT], sv[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = i * 64 + lane;
+    const bool in = e < num_experts;
+    if constexpr (FUSED) {
+      sc[i] = in ? load_in<In>(scores, base + e) : 0.f;
+      sv[i] = in && bias ? bias[e] : 0.f;
+    } else {
+      sc[i] = in ? load_in<In>(scores, base + e) : 0.f;
+      sv[i] = in ? load_in<In>(scores_b, base + e) : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = i * 64 + lane;
+    if constexpr (FUSED) {
+      sc[i] = round_in<In>(1.0f / (1.0f + expf(-sc[i])));
+      sv[i] = round_in<In>(sc[i] + sv[i]);
+    }
+    if (e >= num_experts) sv[i] = -INFINITY;
+    sb[e] = sv[i];
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   const int epg = num_experts / n_group;
 
-  // --- group scores: lane g < n_group scans its group
+  // --- group scores.  When n_group divides 64, lpg = 64 / n_group lanes
+  //     share a group (lane l: group l / lpg, members l % lpg + lpg i) and
+  //     merge their top-2 pairs with xor shuffles; else lane g < n_group
+  //     scans its group alone.
   float gscore = -INFINITY;
-  if (lane < n_group) {
+  {
     float t1 = -INFINITY, t2 = -INFINITY;
-    for (int i = 0; i < epg; ++i) {
-      float v = sb[lane * epg + i];
-      if (v > t1) {
-        t2 = t1;
-        t1 = v;
-      } else if (v > t2) {
-        t2 = v;
+    int lpg = 1;
+    if ((64 % n_group) == 0) {
+      lpg = 64 / n_group;
+      const int gi = lane / lpg, sub = lane % lpg;
+      for (int i = sub; i < epg; i += lpg) {
+        const float v = sb[gi * epg + i];
+        if (v > t1) {
+          t2 = t1;
+          t1 = v;
+        } else if (v > t2) {
+          t2 = v;
+        }
+      }
+      for (int m = 1; m < lpg; m <<= 1) {
+        const float o1 = __shfl_xor(t1, m, 64), o2 = __shfl_xor(t2, m, 64);
+        merge_top2(t1, t2, o1, o2);
+      }
+    } else if (lane < n_group) {
+      for (int i = 0; i < epg; ++i) {
+        const float v = sb[lane * epg + i];
+        if (v > t1) {
+          t2 = t1;
+          t1 = v;
+        } else if (v > t2) {
+          t2 = v;
+        }
       }
     }
-    float s = (epg >= 2) ? t1 + t2 : t1 + t1;
-    if constexpr (std::is_same<In, BF16>::value) s = bf16_to_f32(f32_to_bf16(s));
-    if constexpr (std::is_same<In, F16>::value) s = f16_to_f32(f32_to_f16(s));
-    gscore = __builtin_isfinite(s) ? s : -INFINITY;
+    // group g's pair now sits in lane g * lpg: move it to lane g
+    const int src = lane < n_group ? lane * lpg : 0;
+    t1 = __shfl(t1, src, 64);
+    t2 = __shfl(t2, src, 64);
+    if (lane < n_group) {
+      const float sum = round_in<In>((epg >= 2) ? t1 + t2 : t1 + t1);
+      gscore = __builtin_isfinite(sum) ? sum : -INFINITY;
+    }
   }
   // --- pick topk_group groups
   unsigned long long kept = 0ull;
@@ -332,33 +403,35 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
   int myid = 0;
   if (proceed) {
     float wsum = 1e-20f;
-    // candidates live in LDS: experts of dropped groups and non-finite
-    // values become -inf; each round retires its winner in place.
-    for (int e = lane; e < num_experts; e += 64) {
-      float v = sb[e];
-      if (!((kept >> (e / epg)) & 1ull) || !__builtin_isfinite(v)) v = -INFINITY;
-      sb[e] = v;
+    // candidates: experts of dropped groups and non-finite values become
+    // -inf; each round retires its winner
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int e = i * 64 + lane;
+      if (e >= num_experts || !((kept >> (e / epg)) & 1ull) || !__builtin_isfinite(sv[i]))
+        sv[i] = -INFINITY;
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     for (int j = 0; j < k; ++j) {
-      float bv = -INFINITY, aux = 0.f;
-      int bi = 0x7fffffff;
-      for (int e = lane; e < num_experts; e += 64) {
-        float v = sb[e];
-        if (better(v, e, bv, bi)) {
-          bv = v;
-          bi = e;
+      float bv = sv[0], aux = sc[0];
+      int bi = lane;
+#pragma unroll
+      for (int i = 1; i < VPT; ++i)
+        if (sv[i] > bv) {   // ids grow with i: ties keep the lower one
+          bv = sv[i];
+          aux = sc[i];
+          bi = i * 64 + lane;
         }
-      }
       wave_argmax(bv, aux, bi);
-      float sv = load_in<In>(scores, base + bi);
-      wsum += sv;
+      wsum += aux;
       if (lane == j) {
-        myv = sv;
+        myv = aux;
         myid = bi;
       }
-      if (lane == 0) sb[bi] = -INFINITY;
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      if (lane == (bi & 63)) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+          if (i == (bi >> 6)) sv[i] = -INFINITY;
+      }
     }
     if (lane < k) myv = renormalize ? myv / wsum * rsf : myv * rsf;
   } else if (lane < k) {
@@ -375,6 +448,48 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
     else
       static_cast<uint16_t*>(out_v)[o] = f32_to_f16(myv);
   }
+}
+
+int grouped_topk_launch(bool fused, void* vals, int32_t* ids, const void* scores,
+                        const void* scores_b, const float* bias, int dt, int64_t T, int64_t E,
+                        int64_t n_group, int64_t topk_group, int64_t k, int renorm, float rsf,
+                        void* stream) {
+  MI_ARG(E > 0 && E <= kMaxGroupedExperts, "num_experts must be in [1, 1024]");
+  MI_ARG(n_group > 0 && n_group <= 32, "n_group must be in [1, 32]");
+  MI_ARG(E % n_group == 0, "num_experts must be divisible by n_group");
+  MI_ARG(topk_group > 0 && topk_group <= n_group, "topk_group must be in [1, n_group]");
+  MI_ARG(k > 0 && k <= 32, "topk must be in [1, 32]");
+  MI_ARG(k <= topk_group * (E / n_group), "topk exceeds the experts of the kept groups");
+  if (T == 0) return MI355MOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(cdiv(T, kWavesPerBlock))), block(256);
+#define MI_GT2(In, V)                                                                      \
+  if (fused)                                                                                 \
+    hipLaunchKernelGGL((grouped_topk_kernel<In, true, V>), grid, block, 0, st, scores,       \
+                       nullptr, bias, vals, ids, (int)T, (int)E, (int)n_group,               \
+                       (int)topk_group, (int)k, renorm, rsf);                                \
+  else                                                                                       \
+    hipLaunchKernelGGL((grouped_topk_kernel<In, false, V>), grid, block, 0, st, scores,      \
+                       scores_b, nullptr, vals, ids, (int)T, (int)E, (int)n_group,           \
+                       (int)topk_group, (int)k, renorm, rsf);
+#define MI_GT(In)                  \
+  if (E <= 64) { MI_GT2(In, 1) }   \
+  else if (E <= 128) { MI_GT2(In, 2) } \
+  else if (E <= 256) { MI_GT2(In, 4) } \
+  else if (E <= 512) { MI_GT2(In, 8) } \
+  else { MI_GT2(In, 16) }
+  switch (dt) {
+    case MI355MOE_F32: MI_GT(F32) break;
+    case MI355MOE_BF16: MI_GT(BF16) break;
+    case MI355MOE_F16: MI_GT(F16) break;
+    default:
+      return set_error(MI355MOE_ERR_INVALID, fused ? "gating_output must be float32, bfloat16 or float16"
+                                                   : "scores must be float32, bfloat16 or float16");
+  }
+#undef MI_GT
+#undef MI_GT2
+  MI_LAUNCH_CHECK();
+  return MI355MOE_OK;
 }
 
 }  // namespace
@@ -417,26 +532,14 @@ extern "C" int mi355moe_grouped_topk(void* vals, int32_t* ids, const void* score
                                      int64_t E, int64_t n_group,
                                      int64_t topk_group, int64_t k, int renorm,
                                      float rsf, void* stream) {
-  MI_ARG(E > 0 && E <= kMaxGroupedExperts, "num_experts must be in [1, 1024]");
-  MI_ARG(n_group > 0 && n_group <= 32, "n_group must be in [1, 32]");
-  MI_ARG(E % n_group == 0, "num_experts must be divisible by n_group");
-  MI_ARG(topk_group > 0 && topk_group <= n_group, "topk_group must be in [1, n_group]");
-  MI_ARG(k > 0 && k <= 32, "topk must be in [1, 32]");
-  MI_ARG(k <= topk_group * (E / n_group), "topk exceeds the experts of the kept groups");
-  if (T == 0) return MI355MOE_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid(static_cast<unsigned>(cdiv(T, kWavesPerBlock))), block(256);
-#define MI_GT(In)                                                               \
-  hipLaunchKernelGGL(grouped_topk_kernel<In>, grid, block, 0, st, scores,       \
-                     scores_b, vals, ids, (int)T, (int)E, (int)n_group,         \
-                     (int)topk_group, (int)k, renorm, rsf);
-  switch (dt) {
-    case MI355MOE_F32: MI_GT(F32) break;
-    case MI355MOE_BF16: MI_GT(BF16) break;
-    case MI355MOE_F16: MI_GT(F16) break;
-    default: return set_error(MI355MOE_ERR_INVALID, "scores must be float32, bfloat16 or float16");
-  }
-#undef MI_GT
-  MI_LAUNCH_CHECK();
-  return MI355MOE_OK;
+  return grouped_topk_launch(false, vals, ids, scores, scores_b, nullptr, dt, T, E, n_group,
+                             topk_group, k, renorm, rsf, stream);
+}
+
+extern "C" int mi355moe_fused_grouped_topk(void* vals, int32_t* ids, const void* gating_output,
+                                           const float* bias, int dt, int64_t T, int64_t E,
+                                           int64_t n_group, int64_t topk_group, int64_t k,
+                                           int renorm, float rsf, void* stream) {
+  return grouped_topk_launch(true, vals, ids, gating_output, nullptr, bias, dt, T, E, n_group,
+                             topk_group, k, renorm, rsf, stream);
 }

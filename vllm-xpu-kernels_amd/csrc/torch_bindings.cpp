@@ -180,6 +180,33 @@ std::tuple<at::Tensor, at::Tensor> grouped_topk(at::Tensor& scores,
   return {vals, ids};
 }
 
+// sigmoid scoring + correction bias + grouped top-k in one launch
+std::tuple<at::Tensor, at::Tensor> mi355_fused_grouped_topk(
+    const at::Tensor& gating_output, const std::optional<at::Tensor>& bias, int64_t n_group,
+    int64_t topk_group, int64_t topk, bool renormalize, double routed_scaling_factor) {
+  check_gpu(gating_output, "gating_output");
+  TORCH_CHECK(gating_output.dim() == 2 && gating_output.is_contiguous(),
+              "gating_output must be a contiguous [num_tokens, num_experts] tensor");
+  const int64_t T = gating_output.size(0), E = gating_output.size(1);
+  if (bias) {
+    check_gpu(*bias, "e_score_correction_bias");
+    TORCH_CHECK(bias->scalar_type() == at::kFloat && bias->numel() == E && bias->is_contiguous(),
+                "e_score_correction_bias must be a contiguous float32 [num_experts] tensor");
+  }
+  auto vals = at::empty({T, topk}, gating_output.options());
+  auto ids = at::empty({T, topk}, gating_output.options().dtype(at::kInt));
+  DevGuard g(gating_output.device());
+  check_rc(mi355moe_fused_grouped_topk(vals.data_ptr(), ids.data_ptr<int32_t>(),
+                                       gating_output.data_ptr(),
+                                       bias ? bias->data_ptr<float>() : nullptr,
+                                       dtype_code(gating_output.scalar_type()), T, E, n_group,
+                                       topk_group, topk, renormalize,
+                                       static_cast<float>(routed_scaling_factor),
+                                       cur_stream(gating_output)),
+           "fused_grouped_topk");
+  return {vals, ids};
+}
+
 std::tuple<at::Tensor, at::Tensor> grouped_topk_meta(
     at::Tensor& scores, at::Tensor&, int64_t, int64_t, int64_t topk, bool,
     double) {
@@ -959,6 +986,9 @@ TORCH_LIBRARY(_moe_C, m) {
         "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0, "
         "Tensor? hidden_scale=None, int w_group=0) -> ()");
   m.def("mi355_pack_weights_kblock(Tensor src, Tensor! dst) -> ()");
+  m.def("mi355_fused_grouped_topk(Tensor gating_output, Tensor? bias, int n_group, "
+        "int topk_group, int topk, bool renormalize, float routed_scaling_factor) -> "
+        "(Tensor, Tensor)");
   m.def("mi355_pack_scales_kblock(Tensor src, Tensor! dst) -> ()");
 }
 
@@ -976,6 +1006,7 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("remap_hidden_states", &remap_hidden_states);
   m.impl("mi355_fused_moe", &mi355_fused_moe);
   m.impl("mi355_pack_weights_kblock", &mi355_pack_weights_kblock);
+  m.impl("mi355_fused_grouped_topk", &mi355_fused_grouped_topk);
   m.impl("mi355_pack_scales_kblock", &mi355_pack_scales_kblock);
 }
 

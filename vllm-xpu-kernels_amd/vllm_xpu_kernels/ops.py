@@ -73,12 +73,20 @@ def fused_grouped_topk(gating_output: torch.Tensor, topk: int,
                        num_expert_group: int, topk_group: int,
                        scoring_func: str = "sigmoid",
                        routed_scaling_factor: float = 1.0):
-    """Caller-side score function + bias, then the grouped top-k kernel
-    (reference tests/ops/grouped_topk_op.py:67-92)."""
+    """Score function + correction bias + grouped top-k (reference
+    tests/ops/grouped_topk_op.py:67-92).  "sigmoid" runs as one kernel that
+    forms scores and scores_with_bias itself (the same per-element roundings
+    as the torch ops); "softmax" keeps the caller-side torch.softmax."""
+    if scoring_func == "sigmoid":
+        bias = e_score_correction_bias
+        if bias is not None:
+            bias = bias.to(torch.float32).contiguous()
+        v, i = torch.ops._moe_C.mi355_fused_grouped_topk(
+            gating_output.contiguous(), bias, num_expert_group, topk_group, topk,
+            renormalize, routed_scaling_factor)
+        return v.to(torch.float32), i
     if scoring_func == "softmax":
         scores = torch.softmax(gating_output, dim=-1)
-    elif scoring_func == "sigmoid":
-        scores = gating_output.sigmoid()
     else:
         raise ValueError(f"Unsupported scoring function: {scoring_func}")
     swb = scores + e_score_correction_bias.unsqueeze(0)
