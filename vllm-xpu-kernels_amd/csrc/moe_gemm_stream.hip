@@ -462,11 +462,13 @@ int launch_stream(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t s
 
 int stream_ksplit(int64_t n_tiles, int64_t blocks, int64_t K) {
   // split only grids that leave most CUs idle (the partial-sum launch costs a
-  // few microseconds); then aim for about 512 workgroups (two per CU), at
-  // most 8 splits and at least two K stages per split
+  // few microseconds); then aim for about 256 workgroups (one per CU; 512
+  // and more measured 2-6% slower at decode: C2 / C5 T=1 46.3 / 44.7 us at
+  // 512, 43.9 / 42.0 at 256, C3 T=1 equal), at most 8 splits and at least
+  // two K stages per split
   const int64_t wgs = n_tiles * (blocks > 0 ? blocks : 1);
   if (wgs >= 192) return 1;
-  int64_t s = 512 / (wgs > 0 ? wgs : 1);
+  int64_t s = 256 / (wgs > 0 ? wgs : 1);
   const int64_t nk = cdiv(K, KS);
   if (s > 8) s = 8;
   if (s > nk / 2) s = nk / 2;
