@@ -73,6 +73,46 @@ def test_fused_moe_clamp_limit(dev, T, activation, limit):
         assert (free.float() - ref.float()).abs().max() > 0.1 * scale
 
 
+@pytest.mark.parametrize("tile", ["stream", "small", "big", "bigreg", "wide"])
+@pytest.mark.parametrize("activation", ["silu", "swigluoai"])
+def test_fused_moe_clamp_limit_fp8_every_family(dev, monkeypatch, tile, activation):
+    """gemm1_clamp_limit through each GEMM family's GLU epilogue, forced with
+    MI355MOE_GEMM_TILE, on fp8 block-scaled weights (swigluoai: the same
+    layer with bf16 weights, fp8 has no swigluoai layout)."""
+    W = _W()
+    monkeypatch.setenv("MI355MOE_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(17)
+    E, H, I, topk, T = 8, 1024, 1024, 2, 600
+    x = (torch.randn(T, H, generator=g) / 2).to(torch.bfloat16)
+    w13 = torch.randn(E, 2 * I, H, generator=g) / 2
+    w2 = torch.randn(E, H, I, generator=g) / 16
+    tw, ti = torch.topk(torch.randn(T, E, generator=g).softmax(-1), k=topk, dim=-1)
+    if activation == "silu":
+        q13, s13 = W.fp8_block_quant(w13)
+        q2, s2 = W.fp8_block_quant(w2)
+        moe = _layer_cls()(q13.to(dev), s13.to(dev), None, q2.to(dev), s2.to(dev), None, topk,
+                           activation, E, gemm1_clamp_limit=5.0)
+        recipe, args = "fp8block", (q13, s13, None, q2, s2, None)
+    else:
+        b13, b2 = w13.to(torch.bfloat16), w2.to(torch.bfloat16)
+        moe = _layer_cls()(b13.transpose(1, 2).contiguous().to(dev), None, None,
+                           b2.transpose(1, 2).contiguous().to(dev), None, None, topk,
+                           activation, E, gemm1_clamp_limit=5.0)
+        recipe, args = "bf16", (b13, None, None, b2, None, None)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    moe.apply(out, x.to(dev), tw.to(dev), ti.to(dev))
+    toks = torch.linspace(0, T - 1, 32).long()
+    ref = O.fused_moe(recipe, x[toks], *args, tw[toks], ti[toks], activation=activation,
+                      gemm1_clamp_limit=5.0)
+    scale = ref.float().abs().max().item()
+    got = out.cpu()[toks].float()
+    err = (got - ref.float()).abs()
+    # fp8: the re-quantised activation may flip a code on a one-ulp accumulation
+    # difference; 99.9% within the reference's relative bar, all within 4x it
+    assert (err > 0.02 * scale + 0.02 * ref.float().abs()).float().mean() <= 1e-3
+    assert err.max() <= 0.08 * scale
+
+
 @pytest.mark.parametrize("T", [1, 48, 1024])
 def test_fused_moe_clamp_limit_mxfp4_swigluoai(dev, T):
     """gpt-oss's combination (mxfp4 weights, swigluoai, biases) with a clamp

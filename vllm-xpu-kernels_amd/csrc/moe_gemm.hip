@@ -326,7 +326,8 @@ bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w
 }
 
 GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts, int* bm) {
-  static const int force = [] {
+  // MI355MOE_GEMM_TILE forces a family (tests, measurements); read per call
+  const int force = [] {
     const char* v = getenv("MI355MOE_GEMM_TILE");
     if (!v) return -1;
     if (!strcmp(v, "stream")) return static_cast<int>(TILE_STREAM);
