@@ -450,6 +450,128 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
   }
 }
 
+// Four tokens per wave, one per row of 16 lanes (E = 16 VPT experts, lane
+// `sub` of a row holding experts sub * VPT .. sub * VPT + VPT - 1, groups of
+// E / n_group experts spanning whole lane chunks, n_group dividing 16, k up
+// to 16): every argmax is the row-local half of wave_argmax (four DPP steps,
+// no cross-row reads), and the four rows run side by side.  Same selection,
+// ties and roundings as grouped_topk_kernel.
+__device__ __forceinline__ void row_argmax(float& v, float& aux, int& idx) {
+  argmax_dpp_step<0xB1>(v, aux, idx);   // quad_perm [1,0,3,2]
+  argmax_dpp_step<0x4E>(v, aux, idx);   // quad_perm [2,3,0,1]
+  argmax_dpp_step<0x141>(v, aux, idx);  // row_half_mirror
+  argmax_dpp_step<0x140>(v, aux, idx);  // row_mirror
+}
+
+template <typename In, bool FUSED, int VPT>
+__global__ __launch_bounds__(256) void grouped_topk_row16_kernel(
+    const void* __restrict__ scores, const void* __restrict__ scores_b,
+    const float* __restrict__ bias, void* __restrict__ out_v, int32_t* __restrict__ out_i,
+    int num_tokens, int n_group, int topk_group, int k, int renormalize, float rsf) {
+  constexpr int E = 16 * VPT;
+  const int lane = threadIdx.x & 63, sub = lane & 15;
+  const int row = (blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  if ((row & ~3) >= num_tokens) return;  // whole wave exits together
+  const bool valid = row < num_tokens;
+  const int64_t base = static_cast<int64_t>(valid ? row : 0) * E + sub * VPT;
+  float sc[VPT], sv[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    sc[i] = load_in<In>(scores, base + i);
+    sv[i] = FUSED ? (bias ? bias[sub * VPT + i] : 0.f) : load_in<In>(scores_b, base + i);
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    if constexpr (FUSED) {
+      sc[i] = round_in<In>(1.0f / (1.0f + expf(-sc[i])));
+      sv[i] = round_in<In>(sc[i] + sv[i]);
+    }
+  }
+  // --- group scores: lpg = 16 / n_group lanes per group
+  const int lpg = 16 / n_group;
+  const int grp = sub / lpg;
+  float gscore;
+  {
+    float t1 = -INFINITY, t2 = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const float v = sv[i];
+      if (v > t1) {
+        t2 = t1;
+        t1 = v;
+      } else if (v > t2) {
+        t2 = v;
+      }
+    }
+    for (int m = 1; m < lpg; m <<= 1) {
+      const float o1 = __shfl_xor(t1, m, 64), o2 = __shfl_xor(t2, m, 64);
+      merge_top2(t1, t2, o1, o2);
+    }
+    const float sum = round_in<In>((E / n_group >= 2) ? t1 + t2 : t1 + t1);
+    gscore = __builtin_isfinite(sum) ? sum : -INFINITY;
+  }
+  // --- pick topk_group groups (lanes of one group carry the same pair)
+  unsigned kept = 0u;
+  float thr = -INFINITY;
+  {
+    float gv = gscore;
+    for (int j = 0; j < topk_group; ++j) {
+      float v = gv, aux = 0.f;
+      int gi = grp;
+      row_argmax(v, aux, gi);
+      thr = v;
+      kept |= 1u << gi;
+      if (grp == gi) gv = -INFINITY;
+    }
+  }
+  const bool proceed = thr != -INFINITY;
+  float myv = 0.f;
+  int myid = 0;
+  if (proceed) {
+    float wsum = 1e-20f;
+    const bool mine_kept = (kept >> grp) & 1u;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (!mine_kept || !__builtin_isfinite(sv[i])) sv[i] = -INFINITY;
+    for (int j = 0; j < k; ++j) {
+      float bv = sv[0], aux = sc[0];
+      int bi = sub * VPT;
+#pragma unroll
+      for (int i = 1; i < VPT; ++i)
+        if (sv[i] > bv) {   // ids grow with i: ties keep the lower one
+          bv = sv[i];
+          aux = sc[i];
+          bi = sub * VPT + i;
+        }
+      row_argmax(bv, aux, bi);
+      wsum += aux;
+      if (sub == j) {
+        myv = aux;
+        myid = bi;
+      }
+      if (sub == bi / VPT) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+          if (i == bi % VPT) sv[i] = -INFINITY;
+      }
+    }
+    if (sub < k) myv = renormalize ? myv / wsum * rsf : myv * rsf;
+  } else if (sub < k) {
+    myv = 1.f / k;
+    myid = sub;
+  }
+  if (valid && sub < k) {
+    const int64_t o = static_cast<int64_t>(row) * k + sub;
+    out_i[o] = myid;
+    if constexpr (std::is_same<In, F32>::value)
+      static_cast<float*>(out_v)[o] = myv;
+    else if constexpr (std::is_same<In, BF16>::value)
+      static_cast<uint16_t*>(out_v)[o] = f32_to_bf16(myv);
+    else
+      static_cast<uint16_t*>(out_v)[o] = f32_to_f16(myv);
+  }
+}
+
 int grouped_topk_launch(bool fused, void* vals, int32_t* ids, const void* scores,
                         const void* scores_b, const float* bias, int dt, int64_t T, int64_t E,
                         int64_t n_group, int64_t topk_group, int64_t k, int renorm, float rsf,
@@ -462,6 +584,35 @@ int grouped_topk_launch(bool fused, void* vals, int32_t* ids, const void* scores
   MI_ARG(k <= topk_group * (E / n_group), "topk exceeds the experts of the kept groups");
   if (T == 0) return MI355MOE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // four tokens per wave where the groups tile the 16 lane chunks
+  if (E % 16 == 0 && (E == 128 || E == 256 || E == 512) && 16 % n_group == 0 && k <= 16) {
+    dim3 grid(static_cast<unsigned>(cdiv(T, 4 * kWavesPerBlock))), block(256);
+#define MI_GR2(In, V)                                                                         \
+  if (fused)                                                                                  \
+    hipLaunchKernelGGL((grouped_topk_row16_kernel<In, true, V>), grid, block, 0, st, scores,  \
+                       nullptr, bias, vals, ids, (int)T, (int)n_group, (int)topk_group,       \
+                       (int)k, renorm, rsf);                                                  \
+  else                                                                                        \
+    hipLaunchKernelGGL((grouped_topk_row16_kernel<In, false, V>), grid, block, 0, st, scores, \
+                       scores_b, nullptr, vals, ids, (int)T, (int)n_group, (int)topk_group,   \
+                       (int)k, renorm, rsf);
+#define MI_GR(In)                        \
+  if (E == 128) { MI_GR2(In, 8) }        \
+  else if (E == 256) { MI_GR2(In, 16) }  \
+  else { MI_GR2(In, 32) }
+    switch (dt) {
+      case MI355MOE_F32: MI_GR(F32) break;
+      case MI355MOE_BF16: MI_GR(BF16) break;
+      case MI355MOE_F16: MI_GR(F16) break;
+      default:
+        return set_error(MI355MOE_ERR_INVALID, fused ? "gating_output must be float32, bfloat16 or float16"
+                                                     : "scores must be float32, bfloat16 or float16");
+    }
+#undef MI_GR
+#undef MI_GR2
+    MI_LAUNCH_CHECK();
+    return MI355MOE_OK;
+  }
   dim3 grid(static_cast<unsigned>(cdiv(T, kWavesPerBlock))), block(256);
 #define MI_GT2(In, V)                                                                      \
   if (fused)                                                                                 \
