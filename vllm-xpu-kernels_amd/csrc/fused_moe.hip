@@ -70,19 +70,22 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
     return id >= 0 && id < num_experts;
   };
   if ((H & 7) == 0) {
-    // four slots' rows in flight at a time, summed in slot order
-    for (int j0 = 0; j0 < topk; j0 += 4) {
-      bool ok[4];
-      uint4 u[4];
+    // eight slots' rows in flight at a time (read once: non-temporal),
+    // summed in slot order
+    for (int j0 = 0; j0 < topk; j0 += 8) {
+      bool ok[8];
+      uint4 u[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 8; ++q) {
         const int j = j0 + q;
         ok[q] = j < topk && routed(j);
         const int64_t slot = t * topk + (ok[q] ? j : 0);
-        u[q] = *reinterpret_cast<const uint4*>(g2 + slot * H + h0);
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(g2 + slot * H + h0));
+        u[q] = make_uint4(v[0], v[1], v[2], v[3]);
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 8; ++q) {
         if (!ok[q]) continue;
         const float wj = w[t * topk + j0 + q];
         const uint32_t wd[4] = {u[q].x, u[q].y, u[q].z, u[q].w};
@@ -107,7 +110,8 @@ __global__ __launch_bounds__(256) void weighted_topk_sum_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       wd[i] = st16<F16>(acc[2 * i]) | (uint32_t(st16<F16>(acc[2 * i + 1])) << 16);
-    *reinterpret_cast<uint4*>(o) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(u32x4{wd[0], wd[1], wd[2], wd[3]}, reinterpret_cast<u32x4*>(o));
   } else {
     for (int i = 0; i < 8 && h0 + i < H; ++i) o[i] = st16<F16>(acc[i]);
   }
