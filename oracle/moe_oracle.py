@@ -28,6 +28,11 @@ Pinning (how each function is checked independently of a retyped formula):
 * ``grouped_gemm`` / ``fused_moe``      all-finite-e4m3 identity KAT
   (tests/fused_moe/test_grouped_gemm.py:275-307), E=1 special case vs
   torch.matmul, per-expert brute force                      -> pinned
+
+The layer functions (quantisers, dequantisers, ``grouped_gemm``,
+``fused_moe``) use torch operations only and run on the tensors' device; the
+GPU tests run them on the device to check every token of the full-size
+prefill layers (fp32 matmuls with the same rounding points).
 """
 from __future__ import annotations
 
@@ -41,6 +46,14 @@ FP8_MAX = 448.0
 FP8_MIN_SCALE = 1.0 / (448.0 * 512.0)   # csrc/quantization/fp8/quant_utils.h:35-37
 FP4_MAX = 6.0
 E2M1_VALUES = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+
+def _div_const(a: torch.Tensor, c: float) -> torch.Tensor:
+    """a / c correctly rounded on every device.  torch's GPU division by a
+    Python scalar multiplies by the rounded reciprocal (one ulp off for about
+    half of the inputs when c = 448); a tensor divisor divides exactly, as
+    the CPU path and the kernels do."""
+    return a / torch.full_like(a, c)
 
 
 # ----------------------------------------------------------------------------
@@ -435,7 +448,7 @@ def moe_gather(moe_output: torch.Tensor, topk_weights: torch.Tensor,
     in fixed j order, skipping perm == -1."""
     T, k = perm.shape
     H = moe_output.shape[1]
-    acc = torch.zeros(T, H, dtype=torch.float32)
+    acc = torch.zeros(T, H, dtype=torch.float32, device=moe_output.device)
     for j in range(k):
         p = perm[:, j].to(torch.int64)
         ok = p >= 0
@@ -518,7 +531,7 @@ def per_token_group_fp8_quant(x: torch.Tensor, group_size: int,
     M, K = x.shape
     xg = x.float().reshape(M, K // group_size, group_size)
     amax = torch.clamp(xg.abs().amax(-1), min=eps)
-    s = torch.clamp(amax / FP8_MAX, min=FP8_MIN_SCALE)
+    s = torch.clamp(_div_const(amax, FP8_MAX), min=FP8_MIN_SCALE)
     if scale_ue8m0:
         s = torch.exp2(torch.ceil(torch.log2(torch.clamp(s.abs(), min=1e-10))))
     inv = 1.0 / s
@@ -552,7 +565,7 @@ def per_token_group_quant_mxfp4(x: torch.Tensor, group_size: int = 32,
     M, K = x.shape
     xg = x.float().reshape(M, K // group_size, group_size)
     amax = torch.clamp(xg.abs().amax(-1), min=eps)
-    s = torch.exp2(torch.ceil(torch.log2(torch.clamp((amax / FP4_MAX).abs(),
+    s = torch.exp2(torch.ceil(torch.log2(torch.clamp(_div_const(amax, FP4_MAX).abs(),
                                                      min=eps))))
     v = torch.clamp(xg * (1.0 / s).unsqueeze(-1), -FP4_MAX, FP4_MAX)
     c = fp4_code(v).reshape(M, K)
@@ -589,12 +602,12 @@ def silu_and_mul_per_block_quant(x: torch.Tensor, group_size: int,
     rg = r.reshape(T, H // group_size, group_size)
     amax = rg.abs().amax(-1)
     if quant_dtype == torch.int8:
-        s = torch.clamp(amax / 127.0, min=torch.finfo(torch.float32).eps)
+        s = torch.clamp(_div_const(amax, 127.0), min=torch.finfo(torch.float32).eps)
         q = torch.clamp(torch.round(rg / s.unsqueeze(-1)), -128, 127)
         return q.reshape(T, H).to(torch.int8), s
     qmax = _QMAX[quant_dtype]
     min_sf = torch.tensor(1.0, dtype=torch.float32) / (qmax * 512.0)
-    s = torch.maximum(amax / qmax, min_sf)
+    s = torch.maximum(_div_const(amax, qmax), min_sf)
     if scale_ub is not None:
         s = torch.maximum(torch.clamp(s, max=scale_ub), min_sf)
     if scale_ue8m0:
@@ -613,7 +626,7 @@ def silu_and_mul_mxfp4_quant(x: torch.Tensor, eps: float = 1e-10):
     T, H = r.shape
     rg = r.reshape(T, H // 32, 32)
     amax = rg.abs().amax(-1)
-    s = torch.exp2(torch.ceil(torch.log2(torch.clamp((amax / FP4_MAX).abs(), min=eps))))
+    s = torch.exp2(torch.ceil(torch.log2(torch.clamp(_div_const(amax, FP4_MAX).abs(), min=eps))))
     v = torch.clamp(rg * (1.0 / s).unsqueeze(-1), -FP4_MAX, FP4_MAX)
     c = fp4_code(v).reshape(T, H)
     return (c[:, 0::2] | (c[:, 1::2] << 4)).to(torch.uint8), s
@@ -643,7 +656,7 @@ def to_mxfp4(w: torch.Tensor):
     K = shp[-1]
     x = w.float().reshape(-1, K // 32, 32)
     amax = x.abs().amax(-1, keepdim=True)
-    desc = amax / FP4_MAX
+    desc = _div_const(amax, FP4_MAX)
     e = (torch.clamp(torch.ceil(torch.log2(desc)), min=-127, max=127) + 127)
     e = torch.where(torch.isnan(desc), torch.full_like(e, 255), e)
     e_u8 = e.to(torch.uint8)
@@ -658,7 +671,7 @@ def dequant_mxfp4(q: torch.Tensor, e8m0: torch.Tensor) -> torch.Tensor:
     """LUT dequant of tests/fused_moe/test_fused_moe.py:79-116 (e8m0 via
     (e<<7) as bf16, so e=0 -> 0) == 2^(e-127) for 0<e<255."""
     lut = torch.tensor(E2M1_VALUES + [-v for v in E2M1_VALUES],
-                       dtype=torch.float32)
+                       dtype=torch.float32, device=q.device)
     qi = q.to(torch.int64)
     lo = lut[qi & 0xF]
     hi = lut[qi >> 4]
@@ -710,7 +723,7 @@ def fp8_block_quant_weight(w: torch.Tensor, eps: float = 1e-6):
     *lead, N, K = w.shape
     x = w.float().reshape(*lead, N // 128, 128, K // 128, 128)
     amax = x.abs().amax(dim=(-3, -1))
-    s = torch.clamp(amax / FP8_MAX, min=eps)
+    s = torch.clamp(_div_const(amax, FP8_MAX), min=eps)
     q = (x / s.unsqueeze(-2).unsqueeze(-1)).reshape(*lead, N, K)
     return q.to(torch.float8_e4m3fn), s
 
@@ -788,7 +801,7 @@ def grouped_gemm(recipe: str, a: torch.Tensor, w: torch.Tensor, w_scale,
     M = a.shape[0]
     E = w.shape[0]
     N = w.shape[1]
-    out = torch.zeros(M, N, dtype=out_dtype)
+    out = torch.zeros(M, N, dtype=out_dtype, device=a.device)
     off = 0
     for e in range(E):
         n = int(rows_per_expert[e])
@@ -853,7 +866,7 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
     else:
         xq_all = qdq_act(recipe, hidden)
     H = xq_all.shape[1]
-    g2 = torch.zeros(T * k, H, dtype=dt)
+    g2 = torch.zeros(T * k, H, dtype=dt, device=xq_all.device)
     for e in todo:
         slots = (flat == e).nonzero().flatten()
         if slots.numel() == 0:
@@ -895,7 +908,7 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
         if w2_bias is not None:
             y = y + w2_bias[e].float()
         g2[slots] = y.to(dt)
-    perm = torch.arange(T * k, dtype=torch.int32).reshape(T, k)
+    perm = torch.arange(T * k, dtype=torch.int32, device=ids.device).reshape(T, k)
     perm = torch.where(ids >= 0, perm, torch.full_like(perm, -1))
     return moe_gather(g2, topk_weights.float(), perm)
 

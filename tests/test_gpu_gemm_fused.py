@@ -856,6 +856,29 @@ def test_fused_moe_kblock_fp8_c3_decode(dev, monkeypatch, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
+def _oracle_layer_on_device(cfg, w, x, tw, ti):
+    """The oracle run on the GPU tensors themselves (every token)."""
+    if cfg.recipe == "bf16":
+        w13 = w.w13.transpose(1, 2)
+        w2 = w.w2.transpose(1, 2)
+    elif cfg.recipe == "fp8block":
+        w13, w2 = w.w13, w.w2
+    else:
+        w13, w2 = w.w13.view(torch.uint8), w.w2.view(torch.uint8)
+    return O.fused_moe(cfg.recipe, x, w13, w.w13_scale, w.w13_bias, w2, w.w2_scale,
+                       w.w2_bias, tw, ti.long(), activation=cfg.activation)
+
+
+@pytest.mark.parametrize("name,T", [("C2", 4096), ("C3", 8192), ("C4", 2048), ("C5", 4096)])
+def test_fused_moe_prefill_full_size_every_token(dev, name, T):
+    """Full BASELINE prefill shapes: every token against the oracle run on the
+    device (fp32 matmuls, the oracle's rounding points); bf16 / mxfp4 every
+    element within rtol = atol = 2e-2, fp8 the fp8 bar."""
+    cfg, w, x, tw, ti, out, _ = _layer(_W().CONFIGS[name], T, dev)
+    ref = _oracle_layer_on_device(cfg, w, x, tw, ti)
+    _close(out, ref, fp8=cfg.recipe == "fp8block")
+
+
 @pytest.mark.parametrize("name,T,sample", [("C2", 4096, 24), ("C3", 8192, 6),
                                            ("C4", 2048, 12), ("C5", 4096, 12)])
 def test_fused_moe_prefill_full_size_sampled(dev, name, T, sample):
