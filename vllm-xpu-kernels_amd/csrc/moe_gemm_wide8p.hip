@@ -2,20 +2,25 @@
 // e4m3 activations with 1x128 scales: 320-slot x 256-weight-row tiles, 8
 // waves, each wave owning 32 weight rows x all 320 slots.
 //
-// Data movement.  The direct global->LDS path moves about 16-22 bytes per
-// clock per CU, half of what plain vector loads reach, so only the operand
-// that every wave shares goes through it:
-//   * weights: every wave loads its own two 16-row fragments of the 128-K
-//     stage (4 KB, the HBM stream of the kernel) straight into VGPRs, one
-//     stage ahead (copied into the operand registers at the end of a stage);
+// Data movement: both operands go global->LDS (global_load_lds), so no VGPR
+// holds data in flight.
 //   * activations: the 320 rows x 128 bytes of the stage plus their 320
-//     scales go global->LDS (global_load_lds) into a 2-slot ring, 40 rows and
-//     40 scales per wave; one barrier per stage makes a slot visible and frees
-//     the other.  They are mostly L2 hits (every N-tile of an expert reads the
-//     same rows).
-// The transfers of stage kt + 1 are issued during stage kt (weights first,
-// the activation DMA spread over the slot tiles); the copy of the weights at
-// the end of stage kt waits for them, the top of stage kt + 1 for the rest.
+//     scales go into a 2-slot ring, 40 rows and 40 scales per wave; one
+//     barrier per stage makes a slot visible and frees the other.  They are
+//     mostly L2 hits (every N-tile of an expert reads the same rows).  The
+//     transfer of stage kt + 1 is issued during stage kt, spread over the
+//     slot tiles.
+//   * weights (the HBM stream of the kernel): every wave moves its own two
+//     16-row fragments of a stage (4 KB) into its own region of a 2-slot
+//     weight ring, in lane order, two stages ahead: the transfer of stage
+//     kt + 2 goes out during stage kt after the activation parts, and the
+//     top of stage kt + 1 waits for all but those four newest transfers.  At
+//     the top of a stage each wave reads its fragments (four conflict-free
+//     16-byte LDS reads) into the operand registers, which frees the slot
+//     for the transfer two stages ahead.  Only the wave that wrote a weight
+//     region reads it, so the weights need no barrier.
+// Measured against loading the weights one stage ahead into VGPRs (C3,
+// T=8192): w2 1626 -> 1558 us, w13 2906 -> 2886 us per launch.
 //
 // Compute: per stage and wave 2 x 20 v_mfma_scale_f32_16x16x128_f8f6f4 (one
 // MFMA covers a whole 128-K scale block, unit e8m0 scales), each result
@@ -25,10 +30,15 @@
 // are skipped in pairs (the K loop is specialised on their number).
 //
 // LDS layout of an activation slot: rows of 128 bytes whose 16-byte chunk c
-// holds source chunk c ^ ((r >> 1) & 7) (sixteen rows read at one logical
-// chunk hit sixteen distinct bank groups), then the 320 scales ordered so
+// holds source chunk c ^ ((r >> 1) & 7), then the 320 scales ordered so
 // that lane l16 finds the scales of its slots 16 j + l16 (j = 0..19) at 20
-// consecutive floats.
+// consecutive floats.  Within each group of 16 rows, row t holds slot
+// (t >> 1) + 8 (t & 1): lane l16 reads row 2 (l16 & 7) + (l16 >> 3), so
+// lanes 0-7 read even rows and lanes 8-15 odd rows, and with the chunk
+// swizzle each 8-lane group covers one half of the banks.  A 16-byte read of
+// rows 0..15 at one logical chunk in plain order (every lane group spread
+// over both halves) moves 74 TB/s over the chip, this order 120 TB/s, the
+// same as lane-linear reads.
 #include <type_traits>
 
 #include "mfma16.h"
@@ -55,7 +65,9 @@ constexpr int AROWS = BM / WAVES;           // activation rows moved per wave
 constexpr int A_BYTES = BM * KE;            // 40 KB of activations per stage
 constexpr int A_SLOT = A_BYTES + BM * 4;    // + scales
 constexpr int DUMMY = 2 * A_SLOT;           // scale DMA target of waves 5-7
-constexpr int RING = DUMMY + 256;
+constexpr int W_OFF = DUMMY + 256;          // weight ring: 2 slots x 8 waves x 4 KB
+constexpr int WSLOT = WAVES * 4096;
+constexpr int RING = W_OFF + 2 * WSLOT;
 constexpr int MAX_KBLK = 64;                // K <= 8192
 static_assert(RING <= 150 * 1024, "LDS budget");
 static_assert(BM * (128 + 16) + 2 * BM * 4 <= RING, "fp8 output tile, scales");
@@ -80,6 +92,10 @@ __device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
   return reinterpret_cast<const uint8_t*>((hi << 32) | lo);
 }
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+// LDS row (within its group of 16) that lane l16 reads, and the slot that
+// LDS row t holds: inverse permutations of 0..15
+__device__ __forceinline__ int lds_row_of_lane(int l16) { return 2 * (l16 & 7) + (l16 >> 3); }
+__device__ __forceinline__ int slot_of_lds_row(int t) { return (t >> 1) + 8 * (t & 1); }
 
 __device__ __forceinline__ f32x4_t mfma8(const i32x8_t& a, const i32x8_t& b) {
   const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
@@ -178,7 +194,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
 #pragma unroll
   for (int q = 0; q < AROWS / 8; ++q) {
     const int r = AROWS * wave + 8 * q + (lane >> 3);
-    const int ar = s_arow[r];
+    const int ar = s_arow[(r & ~15) | slot_of_lds_row(r & 15)];
     aoff[q] = static_cast<uint32_t>(ar >= 0 ? ar : 0) * Ku +
               (static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4);
   }
@@ -215,23 +231,29 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       dma4(soff + 4u * kt, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
     }
   };
-  // weight fragments of stage kt (4 x 16-byte loads)
-  const gbyte_t* wglob = reinterpret_cast<const gbyte_t*>(reinterpret_cast<uintptr_t>(wbase));
-  auto load_w = [&](int kt, i32x8_t (&w)[2]) {
+  // weight fragments of stage kt: the wave's 4 KB region of weight slot
+  // `slot`, 1 KB per (fragment f, half h) in lane order
+  const uint32_t wring = ring0 + W_OFF + static_cast<uint32_t>(wave) * 4096u;
+  auto issue_w = [&](int kt, int slot) {
     const uint32_t kofs = static_cast<uint32_t>(kt) * wkstep;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      const gbyte_t* p = wglob + (woff[f] + kofs);
-      const i32x4_t lo = *reinterpret_cast<const gi32x4_t*>(p);
-      const i32x4_t hi = *reinterpret_cast<const gi32x4_t*>(p + 16);
-      w[f] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        dma16(woff[f] + kofs + 16u * h, wbase, wring + slot * WSLOT + (2 * f + h) * 1024);
+  };
+  auto read_w = [&](int slot, i32x8_t (&w)[2]) {
+    const uint8_t* W = lds + W_OFF + slot * WSLOT + wave * 4096 + 16 * lane;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) w[f] = ld32(W, 2 * f * 1024, (2 * f + 1) * 1024);
   };
 
-  // fragment offsets within an activation slot: chunks 2g and 2g + 1 of row
-  // l16 (+ 16 j rows for tile j; the swizzle depends on r % 16 only)
-  const int xo0 = l16 * KE + (((2 * g) ^ swz(l16)) << 4);
-  const int xo1 = l16 * KE + (((2 * g + 1) ^ swz(l16)) << 4);
+  // fragment offsets within an activation slot: chunks 2g and 2g + 1 of the
+  // LDS row holding slot l16 (+ 16 j rows for tile j; the swizzle depends on
+  // the row % 16 only)
+  const int xr = lds_row_of_lane(l16);
+  const int xo0 = xr * KE + (((2 * g) ^ swz(xr)) << 4);
+  const int xo1 = xr * KE + (((2 * g + 1) ^ swz(xr)) << 4);
   // s_wsc row of fragment f: GLU gate / up block; STORE the block of rows
   // 32 wave .. 32 wave + 31
   const int wsel0 = kGlu ? 0 : (wave >> 2), wsel1 = kGlu ? 1 : (wave >> 2);
@@ -246,34 +268,33 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nk = nkb;
-  // Stage kt: the weight loads of stage kt + 1 go out right after the
-  // barrier, the six parts of its activation DMA one every second slot tile
-  // (a wave that issues them back to back stalls until the slower DMA path
-  // takes them, and computes nothing meanwhile); the weights land in `wn`,
-  // which the end of the stage copies into `wc` (the compiler waits for the
-  // loads there; the activation DMA, inline assembly it does not count, is
-  // waited for at the top of the next stage).  The last stage moves its own
-  // (in-bounds, unused) data into the free slot instead of branching around
-  // the transfers.
+  // Stage kt: the six parts of the activation DMA of stage kt + 1 go out one
+  // every second slot tile (a wave that issues them back to back stalls
+  // until the DMA path takes them, and computes nothing meanwhile), then the
+  // weight DMA of stage kt + 2.  Transfers complete in issue order, so the
+  // wait at the top of stage kt + 1 for all but the four newest covers the
+  // activations of kt + 1 and the weights of kt + 1 (issued during kt - 1).
+  // Stages past the end move the last stage's (in-bounds, unused) data
+  // instead of branching around the transfers.
   auto kloop = [&](auto nj_c) {
     constexpr int NJ = decltype(nj_c)::value;
     // slot tile after which part q of the activation DMA is issued (parts
     // past the last tile follow the loop)
     auto part_at = [](int q) { return 2 * q; };
-    i32x8_t wc[2], wn[2];
+    constexpr int W_AT = 11;   // tile after which the weight DMA of stage kt + 2 goes out
+    i32x8_t wc[2];
 #pragma unroll
     for (int q = 0; q < ACT_PARTS; ++q) issue_act_part(q, 0, 0);
-    load_w(0, wc);
-    // the first stage's weights are complete before the loop: otherwise the
-    // compiler's wait for them, merged into every iteration, would also
-    // drain the next stage's activation DMA
-    asm volatile("" :: "v"(wc[0]), "v"(wc[1]));
+    issue_w(0, 0);
+    issue_w(nk > 1 ? 1 : 0, 1);
     for (int kt = 0; kt < nk; ++kt) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of act(kt)
+      // everything but the newest four transfers (the weights of stage kt+1)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
       __builtin_amdgcn_s_barrier();   // act(kt) visible; act slot (kt+1)&1 free
       asm volatile("" ::: "memory");  // no LDS read moves above the barrier
       const int kn = kt + 1 < nk ? kt + 1 : kt;
-      load_w(kn, wn);
+      const int kq = kt + 2 < nk ? kt + 2 : nk - 1;
+      read_w(kt & 1, wc);
       if constexpr (NJ > 0) {
         const float ws0 = s_wsc[wsel0][kt], ws1 = s_wsc[wsel1][kt];
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
@@ -293,6 +314,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
 #pragma unroll
           for (int q = 0; q < ACT_PARTS; ++q)
             if (part_at(q) == j) issue_act_part(q, kn, kt + 1);
+          if (j == W_AT) issue_w(kq, kt & 1);
           if (j > 0) {
             const float s0 = qs * ws0, s1 = qs * ws1;
 #pragma unroll
@@ -318,8 +340,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
 #pragma unroll
       for (int q = 0; q < ACT_PARTS; ++q)
         if (part_at(q) >= NJ) issue_act_part(q, kn, kt + 1);
-      wc[0] = wn[0];
-      wc[1] = wn[1];
+      if (NJ <= W_AT) issue_w(kq, kt & 1);
     }
   };
   switch (nj) {
