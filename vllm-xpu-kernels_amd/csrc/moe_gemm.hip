@@ -106,81 +106,144 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
     for (int j = 0; j < NB; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();
 
-  for (int64_t k0 = 0; k0 < K; k0 += KB) {
-    const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
-    // ---- weight fragments: HBM -> VGPR
-    uint4 wf[KS][NB][kFp8 ? 2 : 1];
-    float wsc[NB];
+  if constexpr (kFp4) {
+    // 4-bit weights: the raw words and scale codes of stage k0 + KB are
+    // loaded while stage k0 computes.  Each stage first issues its
+    // activation loads, then the next stage's weight loads, so the wait for
+    // the activations (loads complete in issue order) leaves the weight
+    // prefetch in flight.  (Two stages of weight lead need twice the raw
+    // registers, and the lost occupancy costs more than it gains.)
+    constexpr int ACH = (BM * CPR + 255) / 256;  // activation chunks per thread
+    uint4 rw[NB];
+    uint32_t rc[NB];
+    auto load_w4 = [&](int64_t k, uint4 (&v)[NB], uint32_t (&c)[NB]) {
+      const int kb = static_cast<int>(K - k < KB ? K - k : KB);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      if constexpr (kFp8) {
-        const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (k0 >> 7) * wst.kblk + 32 * q);
-        wf[0][j][0] = wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
-        wf[0][j][1] = wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
-        const float* bs = static_cast<const float*>(a.b_scale);
-        wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wrow[j] / 128) *
-                        (K / 128) + k0 / 128];
-      } else if constexpr (kFp4) {
-        const bool ok = wok[j] && 32 * q < kb;
-        const int64_t blk32 = (k0 + 32 * q) / 32;  // the lane's 32-value K block
-        uint4 v = ok ? *reinterpret_cast<const uint4*>(wptr[j] + blk32 * wst.kblk)
-                     : make_uint4(0, 0, 0, 0);
-        const uint32_t code = ok ? w4_scale_code<RECIPE>(a, e, wrow[j], blk32, sst) : 0u;
-        wf[0][j][0] = w4_decode8<RECIPE, F16>(v.x, code);
-        wf[1][j][0] = w4_decode8<RECIPE, F16>(v.y, code);
-        wf[2][j][0] = w4_decode8<RECIPE, F16>(v.z, code);
-        wf[3][j][0] = w4_decode8<RECIPE, F16>(v.w, code);
-      } else {
+      for (int j = 0; j < NB; ++j) {
+        const bool ok = k < K && wok[j] && 32 * q < kb;
+        const int64_t blk32 = (k + 32 * q) / 32;  // the lane's 32-value K block
+        v[j] = ok ? *reinterpret_cast<const uint4*>(wptr[j] + blk32 * wst.kblk)
+                  : make_uint4(0, 0, 0, 0);
+        c[j] = ok ? w4_scale_code<RECIPE>(a, e, wrow[j], blk32, sst) : 0u;
+      }
+    };
+    load_w4(0, rw, rc);
+    for (int64_t k0 = 0; k0 < K; k0 += KB) {
+      const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
+      uint4 av[ACH];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const bool ok = wok[j] && 32 * s + 8 * q + 8 <= kb;
-          wf[s][j][0] = ok ? *reinterpret_cast<const uint4*>(
-                                 wptr[j] + w_koff16(wst, k0 + 32 * s + 8 * q))
-                           : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < ACH; ++i) {
+        const int idx = tid + 256 * i;
+        av[i] = make_uint4(0, 0, 0, 0);
+        if (idx < BM * CPR) {
+          const int r = idx / CPR, c = idx % CPR;
+          const int ar = s_arow[r];
+          if (ar >= 0 && c * 16 < kb * XB)
+            av[i] = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
+                                                    (static_cast<int64_t>(ar) * K + k0) * XB +
+                                                    c * 16);
         }
       }
-    }
-    // ---- activation tile -> LDS
-    __syncthreads();
-    for (int idx = tid; idx < BM * CPR; idx += 256) {
-      const int r = idx / CPR, c = idx % CPR;
-      const int ar = s_arow[r];
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (ar >= 0 && c * 16 < kb * XB)
-        v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
-                                            (static_cast<int64_t>(ar) * K + k0) * XB +
-                                            c * 16);
-      *reinterpret_cast<uint4*>(sX + r * ROWB + c * 16) = v;
-    }
-    if constexpr (kFp8) {
-      if (tid < BM) {
-        const int ar = s_arow[tid];
-        s_xs[tid] = ar >= 0 ? a.a_scale[static_cast<int64_t>(ar) * (K / 128) + k0 / 128] : 0.f;
+      uint4 nw[NB];
+      uint32_t nc[NB];
+      load_w4(k0 + KB, nw, nc);
+      uint4 wf[KS][NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        wf[0][j] = w4_decode8<RECIPE, F16>(rw[j].x, rc[j]);
+        wf[1][j] = w4_decode8<RECIPE, F16>(rw[j].y, rc[j]);
+        wf[2][j] = w4_decode8<RECIPE, F16>(rw[j].z, rc[j]);
+        wf[3][j] = w4_decode8<RECIPE, F16>(rw[j].w, rc[j]);
       }
-    }
-    __syncthreads();
-    // ---- MFMA
+      __syncthreads();  // the previous stage's fragment reads are done
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const uint8_t* xr = sX + (mt * 16 + l16) * ROWB;
-      if constexpr (kFp8) {
-        const uint4 x0 = *reinterpret_cast<const uint4*>(xr + 32 * q);
-        const uint4 x1 = *reinterpret_cast<const uint4*>(xr + 32 * q + 16);
-        const float xs = s_xs[mt * 16 + l16];
+      for (int i = 0; i < ACH; ++i) {
+        const int idx = tid + 256 * i;
+        if (idx < BM * CPR)
+          *reinterpret_cast<uint4*>(sX + (idx / CPR) * ROWB + (idx % CPR) * 16) = av[i];
+      }
+      __syncthreads();
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          f32x4 p = mfma_fp8(wf[0][j][0], wf[0][j][1], x0, x1);
-          const float sc = xs * wsc[j];
-          acc[mt][j] += p * sc;
-        }
-      } else {
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t* xr = sX + (mt * 16 + l16) * ROWB;
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-          const int koff = kFp4 ? (32 * q + 8 * s) : (32 * s + 8 * q);
-          const uint4 x = *reinterpret_cast<const uint4*>(xr + koff * 2);
+          const uint4 x = *reinterpret_cast<const uint4*>(xr + (32 * q + 8 * s) * 2);
 #pragma unroll
           for (int j = 0; j < NB; ++j)
-            acc[mt][j] = mfma16_16x16x32<F16>(wf[s][j][0], x, acc[mt][j]);
+            acc[mt][j] = mfma16_16x16x32<F16>(wf[s][j], x, acc[mt][j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) rw[j] = nw[j], rc[j] = nc[j];
+    }
+  } else {
+    for (int64_t k0 = 0; k0 < K; k0 += KB) {
+      const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
+      // ---- weight fragments: HBM -> VGPR
+      uint4 wf[KS][NB][kFp8 ? 2 : 1];
+      float wsc[NB];
+  #pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        if constexpr (kFp8) {
+          const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (k0 >> 7) * wst.kblk + 32 * q);
+          wf[0][j][0] = wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
+          wf[0][j][1] = wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
+          const float* bs = static_cast<const float*>(a.b_scale);
+          wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wrow[j] / 128) *
+                          (K / 128) + k0 / 128];
+        } else {
+  #pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            const bool ok = wok[j] && 32 * s + 8 * q + 8 <= kb;
+            wf[s][j][0] = ok ? *reinterpret_cast<const uint4*>(
+                                   wptr[j] + w_koff16(wst, k0 + 32 * s + 8 * q))
+                             : make_uint4(0, 0, 0, 0);
+          }
+        }
+      }
+      // ---- activation tile -> LDS
+      __syncthreads();
+      for (int idx = tid; idx < BM * CPR; idx += 256) {
+        const int r = idx / CPR, c = idx % CPR;
+        const int ar = s_arow[r];
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (ar >= 0 && c * 16 < kb * XB)
+          v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
+                                              (static_cast<int64_t>(ar) * K + k0) * XB +
+                                              c * 16);
+        *reinterpret_cast<uint4*>(sX + r * ROWB + c * 16) = v;
+      }
+      if constexpr (kFp8) {
+        if (tid < BM) {
+          const int ar = s_arow[tid];
+          s_xs[tid] = ar >= 0 ? a.a_scale[static_cast<int64_t>(ar) * (K / 128) + k0 / 128] : 0.f;
+        }
+      }
+      __syncthreads();
+      // ---- MFMA
+  #pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint8_t* xr = sX + (mt * 16 + l16) * ROWB;
+        if constexpr (kFp8) {
+          const uint4 x0 = *reinterpret_cast<const uint4*>(xr + 32 * q);
+          const uint4 x1 = *reinterpret_cast<const uint4*>(xr + 32 * q + 16);
+          const float xs = s_xs[mt * 16 + l16];
+  #pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            f32x4 p = mfma_fp8(wf[0][j][0], wf[0][j][1], x0, x1);
+            const float sc = xs * wsc[j];
+            acc[mt][j] += p * sc;
+          }
+        } else {
+  #pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            const int koff = 32 * s + 8 * q;
+            const uint4 x = *reinterpret_cast<const uint4*>(xr + koff * 2);
+  #pragma unroll
+            for (int j = 0; j < NB; ++j)
+              acc[mt][j] = mfma16_16x16x32<F16>(wf[s][j][0], x, acc[mt][j]);
+          }
         }
       }
     }
@@ -353,7 +416,10 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     else t = TILE_BIG, b = 128;
   } else if (recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4) {
     if (avg <= 2) t = TILE_STREAM, b = 16;
-    else if (avg <= 24) t = TILE_SMALL, b = 16;
+    // 32-slot blocks from 12 slots per expert on: one block holds most
+    // experts, so each expert's weights stream once (C5 T=128, 16 slots per
+    // expert: 157 -> 127 us per layer against 16-slot blocks)
+    else if (avg <= 12) t = TILE_SMALL, b = 16;
     else if (avg <= 40 || (!wide_ok && avg <= 48)) t = TILE_SMALL, b = 32;
     else if (wide_ok) t = TILE_WIDE, b = kWideBM;
     else t = TILE_BIG, b = 128;
