@@ -793,12 +793,14 @@ def _e8m0(scale):
     return (torch.log2(scale).round().to(torch.int32) + 127).to(torch.uint8)
 
 
-@pytest.mark.parametrize("T", [1, 33, 200])
+@pytest.mark.parametrize("T", [1, 33, 200, 640])
 def test_fused_moe_mxfp8_c3_32_experts(dev, T):
     """mxfp8 (e4m3 weights [E, K, N] with e8m0 scales per 32 along K; the
     input and the intermediate activation quantised to mxfp8 per 32) on
-    DeepSeek-V3 shapes with 32 experts; the layer's own quantisation of x
-    equals pre-quantised input from the 32-group ue8m0 quantiser bit for bit."""
+    DeepSeek-V3 shapes with 32 experts (T = 1, 33: 16-slot STREAM blocks;
+    200, 640: 50 and 160 slots per expert, the 320-slot kernel with the codes
+    in the MFMA); the layer's own quantisation of x equals pre-quantised
+    input from the 32-group ue8m0 quantiser bit for bit."""
     import dataclasses
     from vllm_xpu_kernels import ops
     cfg = dataclasses.replace(_W().CONFIGS["C3"], recipe="mxfp8")
@@ -858,14 +860,18 @@ def test_fused_moe_kblock_fp8_c3_decode(dev, monkeypatch, T):
 
 def _oracle_layer_on_device(cfg, w, x, tw, ti):
     """The oracle run on the GPU tensors themselves (every token)."""
+    s13, s2 = w.w13_scale, w.w2_scale
     if cfg.recipe == "bf16":
         w13 = w.w13.transpose(1, 2)
         w2 = w.w2.transpose(1, 2)
     elif cfg.recipe == "fp8block":
         w13, w2 = w.w13, w.w2
+    elif cfg.recipe == "mxfp8":   # [E, K, N] + [E, K/32, N] -> [E, N, K] + [E, N, K/32]
+        w13, w2 = w.w13.transpose(1, 2), w.w2.transpose(1, 2)
+        s13, s2 = s13.transpose(1, 2), s2.transpose(1, 2)
     else:
         w13, w2 = w.w13.view(torch.uint8), w.w2.view(torch.uint8)
-    return O.fused_moe(cfg.recipe, x, w13, w.w13_scale, w.w13_bias, w2, w.w2_scale,
+    return O.fused_moe(cfg.recipe, x, w13, s13, w.w13_bias, w2, s2,
                        w.w2_bias, tw, ti.long(), activation=cfg.activation)
 
 
@@ -877,6 +883,17 @@ def test_fused_moe_prefill_full_size_every_token(dev, name, T):
     cfg, w, x, tw, ti, out, _ = _layer(_W().CONFIGS[name], T, dev)
     ref = _oracle_layer_on_device(cfg, w, x, tw, ti)
     _close(out, ref, fp8=cfg.recipe == "fp8block")
+
+
+@pytest.mark.parametrize("E,T", [(64, 1024), (256, 4096)])
+def test_fused_moe_mxfp8_prefill_every_token(dev, E, T):
+    """mxfp8 on DeepSeek-V3 shapes at prefill sizes (128 slots per expert:
+    the 320-slot kernel with the e8m0 codes of both operands in the MFMA):
+    every token against the oracle run on the device, to the fp8 bar."""
+    import dataclasses
+    cfg = dataclasses.replace(_W().CONFIGS["C3"], recipe="mxfp8")
+    cfg, w, x, tw, ti, out, _ = _layer(cfg, T, dev, E=E)
+    _close(out, _oracle_layer_on_device(cfg, w, x, tw, ti), fp8=True)
 
 
 @pytest.mark.parametrize("name,T,sample", [("C2", 4096, 24), ("C3", 8192, 6),

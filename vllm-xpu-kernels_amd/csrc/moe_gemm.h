@@ -197,15 +197,16 @@ bool big8_supported(int recipe, const GemmArgs& a);
 int launch_moe_gemm_big8(int recipe, int epi, bool qout, const GemmArgs& a,
                          int64_t max_blocks, void* qs, hipStream_t st);
 // kWideBM-slot blocks, fp8 block-scaled weights, K % 128 == 0, K <= 8192
-// (moe_gemm_wide8.hip).
+// (moe_gemm_wide8.hip); mxfp8 (K-blocked weights and e8m0 scales) runs the
+// 8-wave kernel only.
 bool wide8_supported(int recipe, const GemmArgs& a);
 bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K);
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
                           int64_t max_blocks, void* qs, hipStream_t st);
 // The same tiles with each wave's weight fragments in a private LDS ring
 // (moe_gemm_wide8p.hip); launch_moe_gemm_wide8 dispatches to it.
-int launch_moe_gemm_wide8p(int epi, bool qout, const GemmArgs& a, int64_t max_blocks,
-                           void* qs, hipStream_t st);
+int launch_moe_gemm_wide8p(int recipe, int epi, bool qout, const GemmArgs& a,
+                           int64_t max_blocks, void* qs, hipStream_t st);
 // kWideBM-slot blocks, bf16 weights, K % 32 == 0 (moe_gemm_wide.hip).
 bool wide_supported(int recipe, const GemmArgs& a);
 // The WIDE family addresses activations and one expert's weights with 32-bit

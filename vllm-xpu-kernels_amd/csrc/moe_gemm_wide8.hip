@@ -485,8 +485,9 @@ int launch_w8(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
 }  // namespace
 
 bool wide8_supported(int recipe, const GemmArgs& a) {
-  return recipe == MI355MOE_RECIPE_FP8BLOCK && a.K % 128 == 0 && a.K > 0 &&
-         a.K / 128 <= MAX_KBLK;
+  return (recipe == MI355MOE_RECIPE_FP8BLOCK ||
+          (recipe == MI355MOE_RECIPE_MXFP8 && a.w_kblock && a.a_mxs_ld % 4 == 0)) &&
+         a.K % 128 == 0 && a.K > 0 && a.K / 128 <= MAX_KBLK;
 }
 
 bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K) {
@@ -494,7 +495,8 @@ bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K) {
   return K % 128 == 0 && K > 0 && K / 128 <= MAX_KBLK && a_rows * K < lim && ldb_rows * K < lim;
 }
 
-// kWideBM-slot blocks; fp8 block-scaled weights, K % 128 == 0, K <= 8192.
+// kWideBM-slot blocks; fp8 block-scaled (or mxfp8, K-blocked) weights,
+// K % 128 == 0, K <= 8192.
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
                           int64_t max_blocks, void* qs, hipStream_t st) {
   if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
@@ -510,7 +512,8 @@ int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
   if (qout)
     MI_ARG(epi == EPI_GLU && a.N % 128 == 0,
            "fp8 activation output needs the GLU epilogue and I % 128 == 0");
-  if (!v1) return launch_moe_gemm_wide8p(epi, qout, a, max_blocks, qs, st);
+  if (!v1 || recipe == MI355MOE_RECIPE_MXFP8)
+    return launch_moe_gemm_wide8p(recipe, epi, qout, a, max_blocks, qs, st);
   if (qout) {
     return a.out_f16 ? launch_w8<EPI_GLU, true, true>(a, max_blocks, qs, st)
                      : launch_w8<EPI_GLU, true, false>(a, max_blocks, qs, st);

@@ -68,9 +68,13 @@ constexpr int DUMMY = 2 * A_SLOT;           // scale DMA target of waves 5-7
 constexpr int W_OFF = DUMMY + 256;          // weight ring: 2 slots x 8 waves x 4 KB
 constexpr int WSLOT = WAVES * 4096;
 constexpr int RING = W_OFF + 2 * WSLOT;
+// mxfp8: e8m0 codes of the weight fragments, 2 slots x 8 waves x 256 bytes
+constexpr int C_OFF = RING;
+constexpr int CSLOT = WAVES * 256;
+constexpr int RING_MX = C_OFF + 2 * CSLOT;
 constexpr int MAX_KBLK = 64;                // K <= 8192
 static_assert(RING <= 150 * 1024, "LDS budget");
-static_assert(BM * (128 + 16) + 2 * BM * 4 <= RING, "fp8 output tile, scales");
+static_assert(BM * (128 + 16) + WAVES * BM * 4 + 4 * BM * 4 <= RING, "e4m3 output tile, amax, scales");
 
 __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
@@ -121,13 +125,13 @@ __device__ __forceinline__ float x_sigmoid(float x, float k) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
-template <int EPI, bool QOUT, bool F16>
+template <int EPI, bool QOUT, bool F16, bool MX>
 __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[RING];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[MX ? RING_MX : RING];
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
   __shared__ float s_wsc[2][MAX_KBLK];    // block scales of the tile's two row blocks
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       return c < N ? c : 0;
     }
   };
-  {
+  if constexpr (!MX) {
     const float* bsc = static_cast<const float*>(a.b_scale);
     for (int i = tid; i < 2 * nkb; i += 512) {
       const int t = i / nkb, kb = i % nkb;
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   const uint32_t ring0 = lds_off(lds);
   const WStride wst = w_stride8(a);
   const uint8_t* abase = uniform_ptr(a.A);
-  const uint8_t* sbase = uniform_ptr(a.a_scale);
+  const uint8_t* sbase = MX ? uniform_ptr(a.a_mxs) : uniform_ptr(a.a_scale);
   const uint8_t* wbase = uniform_ptr(static_cast<const uint8_t*>(a.B) +
                                      static_cast<int64_t>(e) * a.ldb_rows * K);
   const uint32_t Ku = static_cast<uint32_t>(K);
@@ -199,23 +203,44 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
               (static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4);
   }
   // scales: waves 0-4 move them, LDS position p = 64 wave + lane holding the
-  // scale of slot 16 (p % 20) + p / 20; waves 5-7 issue the same DMA (so that
-  // no branch splits the K loop) into a dummy area
+  // scale of slot 16 (p % 20) + p / 20 (mxfp8: the four e8m0 codes of the
+  // stage's 32-K blocks); waves 5-7 issue the same DMA (so that no branch
+  // splits the K loop) into a dummy area
   const bool s_wave = wave < BM / 64;
   uint32_t soff = 0;
   {
     const int p = s_wave ? 64 * wave + lane : lane;
     const int ar = s_arow[16 * (p % TJ) + p / TJ];
-    soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) * static_cast<uint32_t>(nkb) * 4u;
+    soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) *
+           (MX ? static_cast<uint32_t>(a.a_mxs_ld) : static_cast<uint32_t>(nkb) * 4u);
   }
   // the wave's weight fragments f = 0, 1: GLU gate rows 16 wave + l16 and the
   // matching up rows; STORE rows 32 wave + 16 f + l16.  Lane (l16, g) loads
-  // the 32 bytes at K byte 32 g of its row of the stage.
+  // the 32 bytes at K byte 32 g of its row of the stage (mxfp8: the 16 bytes
+  // at 16 g and at 64 + 16 g, the scaled MFMA's e4m3 operand order).
   uint32_t woff[2];
 #pragma unroll
   for (int f = 0; f < 2; ++f) {
     const int r = kGlu ? (f ? 128 : 0) + 16 * wave + l16 : 32 * wave + 16 * f + l16;
-    woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row) + 32u * static_cast<uint32_t>(g);
+    woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row) +
+              (MX ? 16u : 32u) * static_cast<uint32_t>(g);
+  }
+  // mxfp8 weight codes (K-blocked [E, K/32, ldb_rows]): lane c = lane % 32
+  // moves 4 bytes, rows 4 (c % 4) .. + 3 of fragment c / 16 for the stage's
+  // 32-K block (c / 4) % 4, into LDS byte 4 lane of the wave's code region
+  // (lanes 32-63 repeat lanes 0-31 into the region's upper half)
+  uint32_t coff = 0;
+  const uint8_t* cbase = nullptr;
+  uint32_t ckstep = 0;
+  if constexpr (MX) {
+    const int c = lane & 31, f = c >> 4, b = (c >> 2) & 3;
+    const int r = kGlu ? (f ? 128 : 0) + 16 * wave : 32 * wave + 16 * f;
+    const uint32_t ldb = static_cast<uint32_t>(a.ldb_rows);
+    coff = static_cast<uint32_t>(b) * ldb + static_cast<uint32_t>(wrow_of(r)) +
+           4u * static_cast<uint32_t>(c & 3);
+    cbase = uniform_ptr(static_cast<const uint8_t*>(a.b_scale) +
+                        static_cast<int64_t>(e) * (K / 32) * a.ldb_rows);
+    ckstep = 4u * ldb;
   }
   const uint32_t wkstep = static_cast<uint32_t>(wst.kblk);
 
@@ -240,20 +265,32 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     for (int f = 0; f < 2; ++f)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        dma16(woff[f] + kofs + 16u * h, wbase, wring + slot * WSLOT + (2 * f + h) * 1024);
+        dma16(woff[f] + kofs + (MX ? 64u : 16u) * h, wbase,
+              wring + slot * WSLOT + (2 * f + h) * 1024);
+    if constexpr (MX)
+      dma4(coff + static_cast<uint32_t>(kt) * ckstep, cbase,
+           ring0 + C_OFF + slot * CSLOT + wave * 256);
   };
   auto read_w = [&](int slot, i32x8_t (&w)[2]) {
     const uint8_t* W = lds + W_OFF + slot * WSLOT + wave * 4096 + 16 * lane;
 #pragma unroll
     for (int f = 0; f < 2; ++f) w[f] = ld32(W, 2 * f * 1024, (2 * f + 1) * 1024);
   };
+  // mxfp8: e8m0 code of the lane's weight row l16 of fragment f for its 32-K
+  // block g of the stage
+  auto read_wc = [&](int slot, uint32_t (&c)[2]) {
+    const uint8_t* C = lds + C_OFF + slot * CSLOT + wave * 256 + 16 * g + l16;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) c[f] = C[64 * f];
+  };
 
   // fragment offsets within an activation slot: chunks 2g and 2g + 1 of the
   // LDS row holding slot l16 (+ 16 j rows for tile j; the swizzle depends on
   // the row % 16 only)
   const int xr = lds_row_of_lane(l16);
-  const int xo0 = xr * KE + (((2 * g) ^ swz(xr)) << 4);
-  const int xo1 = xr * KE + (((2 * g + 1) ^ swz(xr)) << 4);
+  const int xc0 = MX ? g : 2 * g, xc1 = MX ? g + 4 : 2 * g + 1;  // logical chunks
+  const int xo0 = xr * KE + ((xc0 ^ swz(xr)) << 4);
+  const int xo1 = xr * KE + ((xc1 ^ swz(xr)) << 4);
   // s_wsc row of fragment f: GLU gate / up block; STORE the block of rows
   // 32 wave .. 32 wave + 31
   const int wsel0 = kGlu ? 0 : (wave >> 2), wsel1 = kGlu ? 1 : (wave >> 2);
@@ -288,14 +325,37 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     issue_w(0, 0);
     issue_w(nk > 1 ? 1 : 0, 1);
     for (int kt = 0; kt < nk; ++kt) {
-      // everything but the newest four transfers (the weights of stage kt+1)
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      // everything but the newest transfers (the weights of stage kt + 2:
+      // four, mxfp8 five with the codes)
+      if constexpr (MX) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
       __builtin_amdgcn_s_barrier();   // act(kt) visible; act slot (kt+1)&1 free
       asm volatile("" ::: "memory");  // no LDS read moves above the barrier
       const int kn = kt + 1 < nk ? kt + 1 : kt;
       const int kq = kt + 2 < nk ? kt + 2 : nk - 1;
       read_w(kt & 1, wc);
-      if constexpr (NJ > 0) {
+      if constexpr (MX && NJ > 0) {
+        uint32_t wcode[2];
+        read_wc(kt & 1, wcode);
+        const uint8_t* S = lds + (kt & 1) * A_SLOT;
+        const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + TJ * l16;
+        i32x8_t x = ld32(S, xo0, xo1);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          i32x8_t xn = x;
+          if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
+          const uint32_t xcode = (xsp[j] >> (8 * g)) & 0xffu;  // slot's 32-K block g
+          acc[0][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wc[0], x, acc[0][j], 0, 0, 0, wcode[0], 0, xcode);
+          acc[1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wc[1], x, acc[1][j], 0, 0, 0, wcode[1], 0, xcode);
+#pragma unroll
+          for (int q = 0; q < ACT_PARTS; ++q)
+            if (part_at(q) == j) issue_act_part(q, kn, kt + 1);
+          if (j == W_AT) issue_w(kq, kt & 1);
+          x = xn;
+        }
+      } else if constexpr (NJ > 0) {
         const float ws0 = s_wsc[wsel0][kt], ws1 = s_wsc[wsel1][kt];
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
         const float* xsp = reinterpret_cast<const float*>(S + A_BYTES) + TJ * l16;
@@ -415,22 +475,39 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       if (g == 0) s_amax[wave][16 * j + l16] = m;
     }
     __syncthreads();
-    float* ds = static_cast<float*>(qs);
-    const int64_t ngroups = N / 128;
-    if (tid < BM) {
-      float am = s_amax[0][tid];
+    if constexpr (MX) {
+      // mxfp8 activation for the w2 GEMM: one e8m0 code per 32 columns (the
+      // 16 columns of waves 2p and 2p + 1), as per_token_group_fp8_quant with
+      // ue8m0 scales; s_sc[slot][p] holds 1 / 2^code
+      float (*s_inv)[4] = reinterpret_cast<float (*)[4]>(s_sc);
+      for (int i = tid; i < 4 * BM; i += 512) {
+        const int row = i >> 2, p = i & 3;
+        const float am = fmaxf(s_amax[2 * p][row], s_amax[2 * p + 1][row]);
+        const int ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
+        s_inv[row][p] = 1.0f / pow2i(ex);
+        const int drow = s_drow[row];
+        if (drow >= 0)
+          static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] =
+              static_cast<uint8_t>(ex + 127);
+      }
+    } else {
+      float* ds = static_cast<float*>(qs);
+      const int64_t ngroups = N / 128;
+      if (tid < BM) {
+        float am = s_amax[0][tid];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
-      const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
-      s_sc[tid] = sc;
-      const int drow = s_drow[tid];
-      if (drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+        for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
+        const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
+        s_sc[tid] = sc;
+        const int drow = s_drow[tid];
+        if (drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+      }
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
       const int row = 16 * j + l16;
-      const float inv = 1.0f / s_sc[row];
+      const float inv = MX ? s_sc[4 * row + (wave >> 1)] : 1.0f / s_sc[row];
       uint32_t w = 0;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -498,30 +575,40 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   }
 }
 
-template <int EPI, bool QOUT, bool F16>
+template <int EPI, bool QOUT, bool F16, bool MX>
 int launch_w8p(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
   const int64_t cols = EPI == EPI_GLU ? 128 : 256;
   const int64_t total = cdiv(a.N, cols) * max_blocks;
   dim3 grid(static_cast<unsigned>(cdiv(total, 8) * 8));
-  moe_gemm_wide8p_kernel<EPI, QOUT, F16><<<grid, dim3(512), 0, st>>>(a, qs);
+  moe_gemm_wide8p_kernel<EPI, QOUT, F16, MX><<<grid, dim3(512), 0, st>>>(a, qs);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }
 
+template <bool MX>
+int launch_w8p_recipe(int epi, bool qout, const GemmArgs& a, int64_t max_blocks, void* qs,
+                      hipStream_t st) {
+  if (qout)
+    return a.out_f16 ? launch_w8p<EPI_GLU, true, true, MX>(a, max_blocks, qs, st)
+                     : launch_w8p<EPI_GLU, true, false, MX>(a, max_blocks, qs, st);
+  if (epi == EPI_GLU)
+    return a.out_f16 ? launch_w8p<EPI_GLU, false, true, MX>(a, max_blocks, qs, st)
+                     : launch_w8p<EPI_GLU, false, false, MX>(a, max_blocks, qs, st);
+  return a.out_f16 ? launch_w8p<EPI_STORE, false, true, MX>(a, max_blocks, qs, st)
+                   : launch_w8p<EPI_STORE, false, false, MX>(a, max_blocks, qs, st);
+}
+
 }  // namespace
 
-// kWideBM-slot blocks; fp8 block-scaled weights, K % 128 == 0, K <= 8192
-// (the caller checks wide8_supported / wide8_shape_ok).
-int launch_moe_gemm_wide8p(int epi, bool qout, const GemmArgs& a, int64_t max_blocks,
-                           void* qs, hipStream_t st) {
-  if (qout)
-    return a.out_f16 ? launch_w8p<EPI_GLU, true, true>(a, max_blocks, qs, st)
-                     : launch_w8p<EPI_GLU, true, false>(a, max_blocks, qs, st);
-  if (epi == EPI_GLU)
-    return a.out_f16 ? launch_w8p<EPI_GLU, false, true>(a, max_blocks, qs, st)
-                     : launch_w8p<EPI_GLU, false, false>(a, max_blocks, qs, st);
-  return a.out_f16 ? launch_w8p<EPI_STORE, false, true>(a, max_blocks, qs, st)
-                   : launch_w8p<EPI_STORE, false, false>(a, max_blocks, qs, st);
+// kWideBM-slot blocks; fp8 block-scaled weights, or mxfp8 weights with
+// K-blocked e8m0 scales ([E, K/32, ldb_rows]) and e8m0 activation codes
+// (a_mxs); K % 128 == 0, K <= 8192 (the caller checks wide8_supported /
+// wide8_shape_ok).
+int launch_moe_gemm_wide8p(int recipe, int epi, bool qout, const GemmArgs& a,
+                           int64_t max_blocks, void* qs, hipStream_t st) {
+  if (recipe == MI355MOE_RECIPE_MXFP8)
+    return launch_w8p_recipe<true>(epi, qout, a, max_blocks, qs, st);
+  return launch_w8p_recipe<false>(epi, qout, a, max_blocks, qs, st);
 }
 
 }  // namespace mi355
