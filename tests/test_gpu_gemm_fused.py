@@ -828,12 +828,13 @@ def test_fused_moe_mxfp8_ignores_clamp_limit_like_reference(dev):
     assert torch.equal(out2, out)
 
 
-@pytest.mark.parametrize("T", [1, 32, 160])
+@pytest.mark.parametrize("T", [1, 32, 160, 1024])
 def test_fused_moe_mxfp4_pre_quantised_w4a4(dev, T):
-    """gpt-oss shapes (H = I = 2880: K % 128 = 64 in both GEMMs) with
-    pre-quantised mxfp4 input (packed e2m1 [T, H/2] + e8m0 [T, H/32]): both
-    GEMMs are e2m1 x e2m1 with the intermediate activation quantised to mxfp4
-    per 32 (the reference's quant_act_xpu)."""
+    """gpt-oss shapes (H = I = 2880: K % 256 = 64 in both GEMMs, N % 128 = 64)
+    with pre-quantised mxfp4 input (packed e2m1 [T, H/2] + e8m0 [T, H/32]):
+    both GEMMs are e2m1 x e2m1 with the intermediate activation quantised to
+    mxfp4 per 32 (the reference's quant_act_xpu).  T = 1, 32: 16-slot STREAM
+    blocks; 160, 1024: the 320-slot kernel (20 and 128 slots per expert)."""
     from vllm_xpu_kernels import ops
     cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C5"], T, dev)
     xq, xs = ops.per_token_group_quant_mxfp4(x, 32)
@@ -858,7 +859,7 @@ def test_fused_moe_kblock_fp8_c3_decode(dev, monkeypatch, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
-def _oracle_layer_on_device(cfg, w, x, tw, ti):
+def _oracle_layer_on_device(cfg, w, x, tw, ti, a1q_scale=None):
     """The oracle run on the GPU tensors themselves (every token)."""
     s13, s2 = w.w13_scale, w.w2_scale
     if cfg.recipe == "bf16":
@@ -872,7 +873,8 @@ def _oracle_layer_on_device(cfg, w, x, tw, ti):
     else:
         w13, w2 = w.w13.view(torch.uint8), w.w2.view(torch.uint8)
     return O.fused_moe(cfg.recipe, x, w13, s13, w.w13_bias, w2, s2,
-                       w.w2_bias, tw, ti.long(), activation=cfg.activation)
+                       w.w2_bias, tw, ti.long(), activation=cfg.activation,
+                       a1q_scale=a1q_scale)
 
 
 @pytest.mark.parametrize("name,T", [("C2", 4096), ("C3", 8192), ("C4", 2048), ("C5", 4096)])
@@ -883,6 +885,22 @@ def test_fused_moe_prefill_full_size_every_token(dev, name, T):
     cfg, w, x, tw, ti, out, _ = _layer(_W().CONFIGS[name], T, dev)
     ref = _oracle_layer_on_device(cfg, w, x, tw, ti)
     _close(out, ref, fp8=cfg.recipe == "fp8block")
+
+
+def test_fused_moe_w4a4_prefill_every_token(dev):
+    """mxfp4 weights with pre-quantised mxfp4 input at the C5 prefill size
+    (T=4096, 512 slots per expert: the 320-slot e2m1 x e2m1 kernel, K and N
+    with a 64-value tail): every token against the oracle run on the device,
+    to the fp8 bar."""
+    from vllm_xpu_kernels import ops
+    cfg, w, x, tw, ti, _, moe = _layer(_W().CONFIGS["C5"], 4096, dev)
+    xq, xs = ops.per_token_group_quant_mxfp4(x, 32)
+    xq = xq.view(torch.uint8)
+    out = torch.empty_like(x)
+    moe.apply(out, xq.view(torch.float4_e2m1fn_x2), tw, ti,
+              a1q_scale=_e8m0(xs).view(torch.float8_e8m0fnu))
+    ref = _oracle_layer_on_device(cfg, w, xq, tw, ti, a1q_scale=_e8m0(xs))
+    _close(out, ref, fp8=True)
 
 
 @pytest.mark.parametrize("E,T", [(64, 1024), (256, 4096)])

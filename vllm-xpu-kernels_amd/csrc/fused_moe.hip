@@ -193,6 +193,18 @@ struct FusedActArgs {
   float clamp, limit;
 };
 
+// e8m0 code rows [rows, w] -> [rows, ld] (ld > w), the padding set to 127
+// (scale 1.0): a kernel that moves codes four at a time past the last 32-K
+// block of a row then reads finite scales (with zero data there).
+__global__ __launch_bounds__(256) void repack_codes_kernel(const uint8_t* __restrict__ src,
+                                                           uint8_t* __restrict__ dst, int64_t w,
+                                                           int64_t ld, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t r = i / ld, c = i % ld;
+  dst[i] = c < w ? src[r * w + c] : static_cast<uint8_t>(127);
+}
+
 // Activations without a GEMM-epilogue form (gelu, gelu_tanh, swiglustep,
 // relu2_no_mul): the w13 output G1 (16-bit [rows, 2I] by sorted position,
 // gate | up) -> activation [rows, K2], K2 = I (gated) or 2I (relu2_no_mul),
@@ -368,8 +380,8 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   const int64_t H = a->hidden, I = a->inter, K2 = act_width(a);
   const bool glu = epilogue_act(a->activation);
   const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
-  const bool wide_ok = wide_ok_for(a->recipe, a->num_tokens, 2 * I, H, kblock) &&
-                       wide_ok_for(a->recipe, L.slots + E * kWideBM, H, K2, kblock);
+  const bool wide_ok = wide_ok_for(gemm_recipe(a), a->num_tokens, 2 * I, H, kblock) &&
+                       wide_ok_for(gemm_recipe(a), L.slots + E * kWideBM, H, K2, kblock);
   L.tile = pick_tile(gemm_recipe(a), wide_ok, L.slots, E, &L.bm);
   // K-blocked weights: the families that read them (STREAM, SMALL, WIDE, and
   // BIG for fp8, whose 8-wave kernel takes K <= 8192, and for mxfp4)
@@ -406,10 +418,10 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     // e8m0 scale rows padded to a multiple of 4 bytes
     L.ld1 = (a->hidden / 32 + 3) / 4 * 4;
     L.ld2 = (K2 / 32 + 3) / 4 * 4;
-    if (!a->hidden_scale) {
-      L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
+    if (!a->hidden_scale) L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
+    // the layer's own codes, or the caller's repacked to 4-byte rows
+    if (!a->hidden_scale || L.ld1 != a->hidden / 32)
       L.xs8 = c.take<uint8_t>(a->num_tokens * L.ld1);
-    }
     L.act = c.take<uint8_t>(L.max_padded * (gemm_recipe(a) == RECIPE_MX4A4 ? K2 / 2 : K2));
     L.acts8 = c.take<uint8_t>(L.max_padded * L.ld2);
   } else if (fp8) {
@@ -645,6 +657,15 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     rc = mx8_quant_rows(a->hidden_states, f16, L.xq, L.xs8, L.ld1, T, H, st);
     if (rc) return rc;
   }
+  // caller's codes [T, H/32] with rows not a multiple of 4 bytes: copied into
+  // 4-byte rows, which the 320-slot kernels move four codes at a time
+  const bool repack = mx && a->hidden_scale && L.ld1 != H / 32;
+  if (repack) {
+    const int64_t n = T * L.ld1;
+    repack_codes_kernel<<<static_cast<unsigned>(cdiv(n, 256)), dim3(256), 0, st>>>(
+        static_cast<const uint8_t*>(a->hidden_scale), L.xs8, H / 32, L.ld1, n);
+    MI_LAUNCH_CHECK();
+  }
   if (int m = mark(2)) return m;
 
   // gelu / gelu_tanh / swiglustep / relu2_no_mul: w13 stores G1, a separate
@@ -656,8 +677,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
                                                      : a->hidden_states;
   g1.a_scale = preq ? static_cast<const float*>(a->hidden_scale) : (fp8 ? L.xs : nullptr);
   if (mx) {
-    g1.a_mxs = a->hidden_scale ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
-    g1.a_mxs_ld = a->hidden_scale ? H / 32 : L.ld1;
+    g1.a_mxs = a->hidden_scale && !repack ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
+    g1.a_mxs_ld = a->hidden_scale && !repack ? H / 32 : L.ld1;
     g1.q_mxs_ld = L.ld2;
   }
   g1.B = a->w13;

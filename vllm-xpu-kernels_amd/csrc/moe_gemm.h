@@ -201,6 +201,8 @@ int launch_moe_gemm_big8(int recipe, int epi, bool qout, const GemmArgs& a,
 // 8-wave kernel only.
 bool wide8_supported(int recipe, const GemmArgs& a);
 bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K);
+// e2m1 x e2m1 (RECIPE_MX4A4) on the same tiles: K % 32 == 0, 32-bit byte offsets
+bool wide8_shape_ok_mx4(int64_t a_rows, int64_t ldb_rows, int64_t K);
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
                           int64_t max_blocks, void* qs, hipStream_t st);
 // The same tiles with each wave's weight fragments in a private LDS ring

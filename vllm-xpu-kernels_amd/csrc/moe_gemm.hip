@@ -384,6 +384,7 @@ bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w
   if (recipe == MI355MOE_RECIPE_BF16) return K % 32 == 0 && wide_offsets_fit(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) return wide8_shape_ok(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_MXFP8) return w_kblock && wide8_shape_ok(a_rows, ldb_rows, K);
+  if (recipe == RECIPE_MX4A4) return w_kblock && wide8_shape_ok_mx4(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_MXFP4)
     return w_kblock && wide4_shape_ok(a_rows, ldb_rows, ldb_rows, K);
   return false;
@@ -405,7 +406,7 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
   const int64_t avg = active > 0 ? slots / active : 0;
   GemmTile t;
   int b;
-  if (recipe == MI355MOE_RECIPE_MXFP8 && wide_ok && avg > 16) {
+  if ((recipe == MI355MOE_RECIPE_MXFP8 || recipe == RECIPE_MX4A4) && wide_ok && avg > 16) {
     // the 320-slot kernel with the e8m0 codes in the MFMA from 17 slots per
     // expert on (16-slot STREAM blocks would stream an expert's weights once
     // per block)
@@ -459,9 +460,8 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
              recipe == MI355MOE_RECIPE_MXFP4 || is_mx_recipe(recipe),
          "K-blocked weights need the bf16 (K % 32 == 0), fp8block, mxfp4 or mxfp8 "
          "recipe and a kernel family that reads them");
-  MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM ||
-             (recipe == MI355MOE_RECIPE_MXFP8 && tile == TILE_WIDE),
-         "MX recipes run the STREAM kernels (mxfp8 also the WIDE kernel)");
+  MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM || tile == TILE_WIDE,
+         "MX recipes run the STREAM and WIDE kernels");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:
@@ -472,7 +472,7 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
       return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIGREG: return launch_moe_gemm_big(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_WIDE:
-      if (recipe == MI355MOE_RECIPE_FP8BLOCK || recipe == MI355MOE_RECIPE_MXFP8)
+      if (recipe == MI355MOE_RECIPE_FP8BLOCK || is_mx_recipe(recipe))
         return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
       MI_ARG(!qout, "wide GEMM: no fp8 activation output");
       if (recipe == MI355MOE_RECIPE_MXFP4)

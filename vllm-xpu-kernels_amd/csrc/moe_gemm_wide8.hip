@@ -485,6 +485,8 @@ int launch_w8(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
 }  // namespace
 
 bool wide8_supported(int recipe, const GemmArgs& a) {
+  if (recipe == RECIPE_MX4A4)
+    return a.w_kblock && a.a_mxs_ld % 4 == 0 && a.K % 32 == 0 && a.K > 0;
   return (recipe == MI355MOE_RECIPE_FP8BLOCK ||
           (recipe == MI355MOE_RECIPE_MXFP8 && a.w_kblock && a.a_mxs_ld % 4 == 0)) &&
          a.K % 128 == 0 && a.K > 0 && a.K / 128 <= MAX_KBLK;
@@ -495,6 +497,11 @@ bool wide8_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t K) {
   return K % 128 == 0 && K > 0 && K / 128 <= MAX_KBLK && a_rows * K < lim && ldb_rows * K < lim;
 }
 
+bool wide8_shape_ok_mx4(int64_t a_rows, int64_t ldb_rows, int64_t K) {
+  const int64_t lim = int64_t(1) << 32;
+  return K % 32 == 0 && K > 0 && a_rows * (K / 2) < lim && ldb_rows * (K / 2) < lim;
+}
+
 // kWideBM-slot blocks; fp8 block-scaled (or mxfp8, K-blocked) weights,
 // K % 128 == 0, K <= 8192.
 int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
@@ -503,16 +510,17 @@ int launch_moe_gemm_wide8(int recipe, int epi, bool qout, const GemmArgs& a,
   MI_ARG(wide8_supported(recipe, a), "fp8 prefill GEMM: needs K % 128 == 0 and K <= 8192");
   // activation rows: tokens (gathered) or padded slots (by position)
   const int64_t a_rows = a.a_by_pos ? max_blocks * BM : a.num_valid;
-  MI_ARG(wide8_shape_ok(a_rows, a.ldb_rows, a.K),
+  MI_ARG(recipe == RECIPE_MX4A4 ? wide8_shape_ok_mx4(a_rows, a.ldb_rows, a.K)
+                                 : wide8_shape_ok(a_rows, a.ldb_rows, a.K),
          "fp8 prefill GEMM: activation and per-expert weight bytes must stay below 4 GiB");
   static const bool v1 = [] {
     const char* e = getenv("MI355MOE_WIDE8");
     return e && !strcmp(e, "v1");
   }();
   if (qout)
-    MI_ARG(epi == EPI_GLU && a.N % 128 == 0,
-           "fp8 activation output needs the GLU epilogue and I % 128 == 0");
-  if (!v1 || recipe == MI355MOE_RECIPE_MXFP8)
+    MI_ARG(epi == EPI_GLU && a.N % (recipe == RECIPE_MX4A4 ? 32 : 128) == 0,
+           "fp8 activation output needs the GLU epilogue and I % 128 == 0 (mxfp4: % 32)");
+  if (!v1 || recipe == MI355MOE_RECIPE_MXFP8 || recipe == RECIPE_MX4A4)
     return launch_moe_gemm_wide8p(recipe, epi, qout, a, max_blocks, qs, st);
   if (qout) {
     return a.out_f16 ? launch_w8<EPI_GLU, true, true>(a, max_blocks, qs, st)

@@ -63,7 +63,7 @@ constexpr int WAVES = 8;
 constexpr int TJ = BM / 16;                 // slot tiles per wave
 constexpr int AROWS = BM / WAVES;           // activation rows moved per wave
 constexpr int A_BYTES = BM * KE;            // 40 KB of activations per stage
-constexpr int A_SLOT = A_BYTES + BM * 4;    // + scales
+constexpr int A_SLOT = A_BYTES + 2 * BM * 4;  // + scales (e2m1: two words of codes)
 constexpr int DUMMY = 2 * A_SLOT;           // scale DMA target of waves 5-7
 constexpr int W_OFF = DUMMY + 256;          // weight ring: 2 slots x 8 waves x 4 KB
 constexpr int WSLOT = WAVES * 4096;
@@ -125,9 +125,13 @@ __device__ __forceinline__ float x_sigmoid(float x, float k) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
-template <int EPI, bool QOUT, bool F16, bool MX>
+// MXK: 0 fp8 block-scaled, 1 mxfp8, 2 mxfp4 x mxfp4 (e2m1 weights and
+// activations, a stage of 256 K values = 128 bytes per row, two MFMA K-steps).
+template <int EPI, bool QOUT, bool F16, int MXK>
 __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
+  constexpr bool MX = MXK != 0;   // e8m0 codes of both operands in the MFMA
+  constexpr bool MX4 = MXK == 2;
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
 
@@ -154,7 +158,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   const int e = a.block_expert[blk];
   const int64_t K = a.K, N = a.N;
   const int64_t n0 = static_cast<int64_t>(ntile) * NOUT;
-  const int nkb = static_cast<int>(K / KE);
+  const int nkb = static_cast<int>(MX4 ? (K + 255) / 256 : K / KE);  // K stages
+  const int nblk = static_cast<int>(K / 32);                           // 32-K blocks
 
   int ok = 0;
   if (tid < BM) {
@@ -186,12 +191,12 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
 
   // ---- DMA addressing (per-lane 32-bit offsets, held across the K loop)
   const uint32_t ring0 = lds_off(lds);
-  const WStride wst = w_stride8(a);
+  const WStride wst = MX4 ? w_stride4(a) : w_stride8(a);
   const uint8_t* abase = uniform_ptr(a.A);
   const uint8_t* sbase = MX ? uniform_ptr(a.a_mxs) : uniform_ptr(a.a_scale);
   const uint8_t* wbase = uniform_ptr(static_cast<const uint8_t*>(a.B) +
-                                     static_cast<int64_t>(e) * a.ldb_rows * K);
-  const uint32_t Ku = static_cast<uint32_t>(K);
+                                     static_cast<int64_t>(e) * a.ldb_rows * (MX4 ? K / 2 : K));
+  const uint32_t Ku = static_cast<uint32_t>(MX4 ? K / 2 : K);  // activation row bytes
   // activation rows 40 wave + 8 q + lane / 8, 16-byte chunk lane % 8 of the
   // LDS row, read from source chunk (lane % 8) ^ swz(row)
   uint32_t aoff[AROWS / 8];
@@ -200,8 +205,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     const int r = AROWS * wave + 8 * q + (lane >> 3);
     const int ar = s_arow[(r & ~15) | slot_of_lds_row(r & 15)];
     aoff[q] = static_cast<uint32_t>(ar >= 0 ? ar : 0) * Ku +
-              (static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4);
+              (MX4 ? 0u : static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4);
   }
+  // e2m1: the lane's source chunk of part q, added per stage (chunks past
+  // the row end in the last stage of a K % 256 != 0 re-read chunk 0)
+  auto achunk = [&](int q) -> uint32_t {
+    const int r = AROWS * wave + 8 * q + (lane >> 3);
+    return static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4;
+  };
   // scales: waves 0-4 move them, LDS position p = 64 wave + lane holding the
   // scale of slot 16 (p % 20) + p / 20 (mxfp8: the four e8m0 codes of the
   // stage's 32-K blocks); waves 5-7 issue the same DMA (so that no branch
@@ -225,19 +236,33 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row) +
               (MX ? 16u : 32u) * static_cast<uint32_t>(g);
   }
-  // mxfp8 weight codes (K-blocked [E, K/32, ldb_rows]): lane c = lane % 32
-  // moves 4 bytes, rows 4 (c % 4) .. + 3 of fragment c / 16 for the stage's
-  // 32-K block (c / 4) % 4, into LDS byte 4 lane of the wave's code region
-  // (lanes 32-63 repeat lanes 0-31 into the region's upper half)
+  // e2m1 (K-blocked [E, K/32, ldb_rows, 16 bytes]): lane (l16, g) of half h
+  // moves the 16 bytes of 32-K block 8 kt + 4 h + g of its row
+  if constexpr (MX4) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int r = kGlu ? (f ? 128 : 0) + 16 * wave + l16 : 32 * wave + 16 * f + l16;
+      woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row);
+    }
+  }
+  // MX weight codes (K-blocked [E, K/32, ldb_rows]), 4 bytes per lane into
+  // LDS byte 4 lane of the wave's code region.  mxfp8: lane c = lane % 32
+  // moves rows 4 (c % 4) .. + 3 of fragment c / 16 for the stage's 32-K block
+  // (c / 4) % 4 (lanes 32-63 repeat lanes 0-31 into the upper half); e2m1:
+  // lane c moves rows 4 (c % 4) .. + 3 of fragment c / 32 for block
+  // 8 kt + (c / 4) % 8.
   uint32_t coff = 0;
   const uint8_t* cbase = nullptr;
   uint32_t ckstep = 0;
+  const uint32_t ldb = static_cast<uint32_t>(a.ldb_rows);
+  int cblk = 0;  // e2m1: the lane's block within the stage
   if constexpr (MX) {
-    const int c = lane & 31, f = c >> 4, b = (c >> 2) & 3;
+    const int c = MX4 ? lane : (lane & 31);
+    const int f = MX4 ? c >> 5 : c >> 4, b = MX4 ? (c >> 2) & 7 : (c >> 2) & 3;
     const int r = kGlu ? (f ? 128 : 0) + 16 * wave : 32 * wave + 16 * f;
-    const uint32_t ldb = static_cast<uint32_t>(a.ldb_rows);
-    coff = static_cast<uint32_t>(b) * ldb + static_cast<uint32_t>(wrow_of(r)) +
+    coff = (MX4 ? 0u : static_cast<uint32_t>(b) * ldb) + static_cast<uint32_t>(wrow_of(r)) +
            4u * static_cast<uint32_t>(c & 3);
+    cblk = b;
     cbase = uniform_ptr(static_cast<const uint8_t*>(a.b_scale) +
                         static_cast<int64_t>(e) * (K / 32) * a.ldb_rows);
     ckstep = 4u * ldb;
@@ -249,9 +274,21 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   constexpr int ACT_PARTS = AROWS / 8 + 1;
   auto issue_act_part = [&](int q, int kt, int parity) {
     const uint32_t slot = ring0 + (parity & 1) * A_SLOT;
+    const uint32_t k0 = static_cast<uint32_t>(kt) * KE;  // stage start in row bytes
     if (q < AROWS / 8) {
-      dma16(aoff[q] + static_cast<uint32_t>(kt) * KE, abase,
-            slot + (AROWS * wave + 8 * q) * KE);
+      uint32_t off = aoff[q] + k0;
+      if constexpr (MX4) {
+        const uint32_t ch = achunk(q);
+        off += k0 + ch < Ku ? ch : 0u;
+      }
+      dma16(off, abase, slot + (AROWS * wave + 8 * q) * KE);
+    } else if constexpr (MX4) {
+      // eight e8m0 codes per slot: blocks 8 kt .. 8 kt + 3 and + 4 .. + 7
+      // (the second word re-reads the first past the code row)
+      const uint32_t c0 = 8u * static_cast<uint32_t>(kt);
+      const uint32_t c1 = c0 + 4u < static_cast<uint32_t>(a.a_mxs_ld) ? c0 + 4u : c0;
+      dma4(soff + c0, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
+      dma4(soff + c1, sbase, s_wave ? slot + A_BYTES + BM * 4 + 256 * wave : ring0 + DUMMY);
     } else {
       dma4(soff + 4u * kt, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
     }
@@ -264,12 +301,24 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
 #pragma unroll
     for (int f = 0; f < 2; ++f)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        dma16(woff[f] + kofs + (MX ? 64u : 16u) * h, wbase,
-              wring + slot * WSLOT + (2 * f + h) * 1024);
-    if constexpr (MX)
+      for (int h = 0; h < 2; ++h) {
+        uint32_t off;
+        if constexpr (MX4) {  // blocks past K re-read the last block
+          const int b = 8 * kt + 4 * h + g;
+          off = woff[f] + static_cast<uint32_t>(b < nblk ? b : nblk - 1) * wkstep;
+        } else {
+          off = woff[f] + kofs + (MX ? 64u : 16u) * h;
+        }
+        dma16(off, wbase, wring + slot * WSLOT + (2 * f + h) * 1024);
+      }
+    if constexpr (MX4) {
+      const int b = 8 * kt + cblk;
+      dma4(coff + static_cast<uint32_t>(b < nblk ? b : nblk - 1) * ldb, cbase,
+           ring0 + C_OFF + slot * CSLOT + wave * 256);
+    } else if constexpr (MX) {
       dma4(coff + static_cast<uint32_t>(kt) * ckstep, cbase,
            ring0 + C_OFF + slot * CSLOT + wave * 256);
+    }
   };
   auto read_w = [&](int slot, i32x8_t (&w)[2]) {
     const uint8_t* W = lds + W_OFF + slot * WSLOT + wave * 4096 + 16 * lane;
@@ -282,6 +331,15 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     const uint8_t* C = lds + C_OFF + slot * CSLOT + wave * 256 + 16 * g + l16;
 #pragma unroll
     for (int f = 0; f < 2; ++f) c[f] = C[64 * f];
+  };
+  // e2m1: codes of the lane's row for its blocks g (step 0) and 4 + g (step 1)
+  auto read_wc4 = [&](int slot, uint32_t (&c)[2][2]) {
+    const uint8_t* C = lds + C_OFF + slot * CSLOT + wave * 256 + 16 * g + l16;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      c[f][0] = C[128 * f];
+      c[f][1] = C[128 * f + 64];
+    }
   };
 
   // fragment offsets within an activation slot: chunks 2g and 2g + 1 of the
@@ -333,8 +391,53 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       asm volatile("" ::: "memory");  // no LDS read moves above the barrier
       const int kn = kt + 1 < nk ? kt + 1 : kt;
       const int kq = kt + 2 < nk ? kt + 2 : nk - 1;
+      if constexpr (MX4) {
+        // last stage of a K % 256 != 0: zero this lane's weight chunks of
+        // blocks past K (the DMA re-read the last block there; with a zero
+        // weight operand the product is zero, e2m1 holding no Inf or NaN,
+        // whatever the activation data and the finite codes)
+        if (8 * kt + 8 > nblk) {
+          uint8_t* W = lds + W_OFF + (kt & 1) * WSLOT + wave * 4096 + 16 * lane;
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              if (8 * kt + 4 * h + g >= nblk)
+                *reinterpret_cast<uint4*>(W + (2 * f + h) * 1024) = make_uint4(0, 0, 0, 0);
+        }
+      }
       read_w(kt & 1, wc);
-      if constexpr (MX && NJ > 0) {
+      if constexpr (MX4 && NJ > 0) {
+        uint32_t wcode[2][2];
+        read_wc4(kt & 1, wcode);
+        const uint8_t* S = lds + (kt & 1) * A_SLOT;
+        const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + TJ * l16;
+        i32x8_t x = ld32(S, xo0, xo1);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          i32x8_t xn = x;
+          if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
+          const uint32_t xc0 = (xsp[j] >> (8 * g)) & 0xffu;       // block g
+          const uint32_t xc1 = (xsp[BM + j] >> (8 * g)) & 0xffu;  // block 4 + g
+          // an e2m1 operand is four VGPRs: the low half of a fragment feeds
+          // K-step 0, the high half K-step 1
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+            acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                wc[f], x, acc[f][j], 4, 4, 0, wcode[f][0], 0, xc0);
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+            acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                __builtin_shufflevector(wc[f], wc[f], 4, 5, 6, 7, 0, 1, 2, 3),
+                __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3), acc[f][j], 4, 4, 0,
+                wcode[f][1], 0, xc1);
+#pragma unroll
+          for (int q = 0; q < ACT_PARTS; ++q)
+            if (part_at(q) == j) issue_act_part(q, kn, kt + 1);
+          if (j == W_AT) issue_w(kq, kt & 1);
+          x = xn;
+        }
+      } else if constexpr (MX && NJ > 0) {
         uint32_t wcode[2];
         read_wc(kt & 1, wcode);
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
@@ -476,19 +579,25 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     }
     __syncthreads();
     if constexpr (MX) {
-      // mxfp8 activation for the w2 GEMM: one e8m0 code per 32 columns (the
-      // 16 columns of waves 2p and 2p + 1), as per_token_group_fp8_quant with
-      // ue8m0 scales; s_sc[slot][p] holds 1 / 2^code
+      // MX activation for the w2 GEMM: one e8m0 code per 32 columns (the 16
+      // columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
+      // with ue8m0 scales, e2m1 as per_token_group_quant_mxfp4 (eps 1e-10);
+      // s_sc[slot][p] holds 1 / 2^code.  N % 32 == 0: groups past N (the
+      // last tile of an N % 128 != 0) are not written.
       float (*s_inv)[4] = reinterpret_cast<float (*)[4]>(s_sc);
       for (int i = tid; i < 4 * BM; i += 512) {
         const int row = i >> 2, p = i & 3;
         const float am = fmaxf(s_amax[2 * p][row], s_amax[2 * p + 1][row]);
-        const int ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
+        int ex;
+        if constexpr (MX4) ex = ceil_log2(fmaxf(fabsf(am / 6.0f), 1e-10f));
+        else ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
         s_inv[row][p] = 1.0f / pow2i(ex);
+        // groups past N inside the padded code row get 127 (scale 1.0): the
+        // w2 GEMM reads them, four codes at a time, against zero data
         const int drow = s_drow[row];
-        if (drow >= 0)
+        if (drow >= 0 && n0 / 32 + p < a.q_mxs_ld)
           static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] =
-              static_cast<uint8_t>(ex + 127);
+              static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
       }
     } else {
       float* ds = static_cast<float*>(qs);
@@ -508,22 +617,36 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     for (int j = 0; j < TJ; ++j) {
       const int row = 16 * j + l16;
       const float inv = MX ? s_sc[4 * row + (wave >> 1)] : 1.0f / s_sc[row];
-      uint32_t w = 0;
+      if constexpr (MX4) {
+        // e2m1 pairs, the even column in the low nibble
+        uint32_t w = 0;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = fminf(fmaxf(ov[j][r] * inv, -448.f), 448.f);
-        w |= f32_to_e4m3(x) << (8 * r);
+        for (int r = 0; r < 4; ++r)
+          w |= fp4_code(fminf(fmaxf(ov[j][r] * inv, -6.f), 6.f)) << (4 * r);
+        *reinterpret_cast<uint16_t*>(lds + row * PITCH + tcol(0, 0) / 2) =
+            static_cast<uint16_t>(w);
+      } else {
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = fminf(fmaxf(ov[j][r] * inv, -448.f), 448.f);
+          w |= f32_to_e4m3(x) << (8 * r);
+        }
+        *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
       }
-      *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
     }
     __syncthreads();
     uint8_t* dq = static_cast<uint8_t*>(a.D);
-    constexpr int CPR = NOUT / 16;
+    // 16-byte chunks of an output row: 16 e4m3 or 32 e2m1 columns; N % 32 ==
+    // 0, so an e2m1 chunk lies wholly inside or wholly past N
+    constexpr int CPR = MX4 ? NOUT / 32 : NOUT / 16;
+    const int64_t orow = MX4 ? N / 2 : N;  // output row bytes
     for (int idx = tid; idx < BM * CPR; idx += 512) {
       const int row = idx / CPR, ch = idx % CPR;
       const int drow = s_drow[row];
-      if (drow < 0) continue;
-      *reinterpret_cast<uint4*>(dq + static_cast<int64_t>(drow) * N + n0 + ch * 16) =
+      if (drow < 0 || n0 + ch * (MX4 ? 32 : 16) >= N) continue;
+      *reinterpret_cast<uint4*>(dq + static_cast<int64_t>(drow) * orow + (MX4 ? n0 / 2 : n0) +
+                                ch * 16) =
           *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
     }
   } else {
@@ -575,40 +698,43 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   }
 }
 
-template <int EPI, bool QOUT, bool F16, bool MX>
+template <int EPI, bool QOUT, bool F16, int MXK>
 int launch_w8p(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
   const int64_t cols = EPI == EPI_GLU ? 128 : 256;
   const int64_t total = cdiv(a.N, cols) * max_blocks;
   dim3 grid(static_cast<unsigned>(cdiv(total, 8) * 8));
-  moe_gemm_wide8p_kernel<EPI, QOUT, F16, MX><<<grid, dim3(512), 0, st>>>(a, qs);
+  moe_gemm_wide8p_kernel<EPI, QOUT, F16, MXK><<<grid, dim3(512), 0, st>>>(a, qs);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }
 
-template <bool MX>
+template <int MXK>
 int launch_w8p_recipe(int epi, bool qout, const GemmArgs& a, int64_t max_blocks, void* qs,
                       hipStream_t st) {
   if (qout)
-    return a.out_f16 ? launch_w8p<EPI_GLU, true, true, MX>(a, max_blocks, qs, st)
-                     : launch_w8p<EPI_GLU, true, false, MX>(a, max_blocks, qs, st);
+    return a.out_f16 ? launch_w8p<EPI_GLU, true, true, MXK>(a, max_blocks, qs, st)
+                     : launch_w8p<EPI_GLU, true, false, MXK>(a, max_blocks, qs, st);
   if (epi == EPI_GLU)
-    return a.out_f16 ? launch_w8p<EPI_GLU, false, true, MX>(a, max_blocks, qs, st)
-                     : launch_w8p<EPI_GLU, false, false, MX>(a, max_blocks, qs, st);
-  return a.out_f16 ? launch_w8p<EPI_STORE, false, true, MX>(a, max_blocks, qs, st)
-                   : launch_w8p<EPI_STORE, false, false, MX>(a, max_blocks, qs, st);
+    return a.out_f16 ? launch_w8p<EPI_GLU, false, true, MXK>(a, max_blocks, qs, st)
+                     : launch_w8p<EPI_GLU, false, false, MXK>(a, max_blocks, qs, st);
+  return a.out_f16 ? launch_w8p<EPI_STORE, false, true, MXK>(a, max_blocks, qs, st)
+                   : launch_w8p<EPI_STORE, false, false, MXK>(a, max_blocks, qs, st);
 }
 
 }  // namespace
 
-// kWideBM-slot blocks; fp8 block-scaled weights, or mxfp8 weights with
-// K-blocked e8m0 scales ([E, K/32, ldb_rows]) and e8m0 activation codes
-// (a_mxs); K % 128 == 0, K <= 8192 (the caller checks wide8_supported /
-// wide8_shape_ok).
+// kWideBM-slot blocks; fp8 block-scaled weights (K % 128 == 0, K <= 8192),
+// or mxfp8 weights with K-blocked e8m0 scales ([E, K/32, ldb_rows]) and e8m0
+// activation codes (a_mxs; K % 128 == 0), or e2m1 x e2m1 (RECIPE_MX4A4,
+// K-blocked mxfp4 weights and scales; K % 32 == 0); the caller checks
+// wide8_supported / wide8_shape_ok.
 int launch_moe_gemm_wide8p(int recipe, int epi, bool qout, const GemmArgs& a,
                            int64_t max_blocks, void* qs, hipStream_t st) {
   if (recipe == MI355MOE_RECIPE_MXFP8)
-    return launch_w8p_recipe<true>(epi, qout, a, max_blocks, qs, st);
-  return launch_w8p_recipe<false>(epi, qout, a, max_blocks, qs, st);
+    return launch_w8p_recipe<1>(epi, qout, a, max_blocks, qs, st);
+  if (recipe == RECIPE_MX4A4)
+    return launch_w8p_recipe<2>(epi, qout, a, max_blocks, qs, st);
+  return launch_w8p_recipe<0>(epi, qout, a, max_blocks, qs, st);
 }
 
 }  // namespace mi355
