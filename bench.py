@@ -51,6 +51,10 @@ def gemm_work(cfg, T, active, which):
         bw, sc, bx, sx = 2.0, 0.0, 2.0, 0.0
     elif cfg.recipe == "fp8block":
         bw, sc, bx, sx = 1.0, 4.0 / (128 * 128), 1.0, 4.0 / 128
+    elif cfg.recipe == "mxfp8":
+        bw, sc, bx, sx = 1.0, 1.0 / 32, 1.0, 1.0 / 32
+    elif cfg.prequant:   # e2m1 x e2m1
+        bw, sc, bx, sx = 0.5, 1.0 / 32, 0.5, 1.0 / 32
     else:
         bw, sc, bx, sx = 0.5, 1.0 / 32, 2.0, 0.0
     if which == "gemm_w13":
@@ -169,11 +173,23 @@ class Point:
                      for _ in range(self.copies)]
         self.moe = self.moes[0]
         self.i = 0
+        # pre-quantised mxfp4 input (w4a4): e2m1 bytes [T, H/2] + e8m0 [T, H/32]
+        self.xq = self.xs8 = None
+        if cfg.prequant:
+            from vllm_xpu_kernels import ops
+            q, sc = ops.per_token_group_quant_mxfp4(self.x, 32)
+            self.xq = q.view(torch.uint8)
+            self.xs8 = (torch.log2(sc).round().to(torch.int32) + 127).to(torch.uint8)
 
     def step(self):
         from vllm_xpu_kernels import workloads as W
         tw, ti = W.route(self.cfg, self.logits, self.bias)
-        self.moes[self.i % self.copies].apply(self.out, self.x, tw, ti)
+        moe = self.moes[self.i % self.copies]
+        if self.xq is not None:
+            moe.apply(self.out, self.xq.view(torch.float4_e2m1fn_x2), tw, ti,
+                      a1q_scale=self.xs8.view(torch.float8_e8m0fnu))
+        else:
+            moe.apply(self.out, self.x, tw, ti)
         self.i += 1
 
     def time_steps(self, steps, warmup, graph=True):
@@ -208,7 +224,9 @@ class Point:
 
     def stage_times(self, steps):
         from vllm_xpu_kernels import capi
-        args = [capi.fused_args(m, self.out, self.x, self.tw, self.ti) for m in self.moes]
+        x = self.xq if self.xq is not None else self.x
+        args = [capi.fused_args(m, self.out, x, self.tw, self.ti, hidden_scale=self.xs8)
+                for m in self.moes]
         ws = capi.workspace_for(args[0], self.dev)
         timer = capi.StageTimer(steps)
         try:
@@ -232,7 +250,9 @@ def summarize(pt, ms, stages):
     cfg, T = pt.cfg, pt.T
     t_h, t_m = W.roofline_time_s(cfg, T, pt.active)
     t = ms * 1e-3
-    d = {"config": cfg.name, "recipe": cfg.recipe, "tokens": T, "active_experts": pt.active,
+    d = {"config": cfg.name, "recipe": cfg.recipe + (" (pre-quantised mxfp4 input)"
+                                                     if cfg.prequant else ""),
+         "tokens": T, "active_experts": pt.active,
          "us_per_layer": round(ms * 1e3, 2), "tokens_per_s": round(T / t, 1),
          "hbm_GBps": round(W.algorithmic_bytes(cfg, T, pt.active) / t / 1e9, 1),
          "TFLOPs": round(W.algorithmic_flops(cfg, T) / t / 1e12, 2),
@@ -270,7 +290,7 @@ def kernel_roofline(pt, stages, key):
     ms = stages[gi]
     traffic = measured_traffic(key, name)
     b, f = gemm_work(pt.cfg, pt.T, pt.active, name)
-    peak_tf = W.PEAK_TFLOPS[pt.cfg.recipe]
+    peak_tf = W.PEAK_TFLOPS_FP4 if pt.cfg.prequant else W.PEAK_TFLOPS[pt.cfg.recipe]
     t_h, t_m = b / 8e12, f / (peak_tf * 1e12)
     if t_h >= t_m:
         ach = b / (ms * 1e-3) / 1e9
@@ -287,7 +307,9 @@ def kernel_roofline(pt, stages, key):
 
 SWEEP = [("C1", 64), ("C2", 1), ("C2", 16), ("C2", 64), ("C2", 256), ("C2", 4096),
          ("C3", 1), ("C3", 64), ("C3", 8192), ("C4", 2048), ("C5", 1), ("C5", 128),
-         ("C5", 4096)]
+         ("C5", 4096),
+         # recipe variants on the same shapes: mxfp8 weights, w4a4 (e2m1 x e2m1)
+         ("C3-mxfp8", 8192), ("C5-w4a4", 4096)]
 
 
 def op_bandwidth(dev, steps):
@@ -462,7 +484,7 @@ def main():
 
     from vllm_xpu_kernels import workloads as W
     graph = not args.no_graph
-    cfg = W.CONFIGS[args.config]
+    cfg = W.config(args.config)
     log(f"bench: {args.config} ({cfg.name}) T={args.tokens} steps={args.steps} "
         f"warmup={args.warmup} graph={graph} on {torch.cuda.get_device_name(0)}")
 
@@ -494,7 +516,7 @@ def main():
             if name == args.config and T == args.tokens:
                 sweep.append(head)
                 continue
-            c = W.CONFIGS[name]
+            c = W.config(name)
             if name not in cache:
                 for k in list(cache):
                     if k != name:
@@ -521,7 +543,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"bf16": "bf16", "fp8block": "fp8e4m3", "mxfp4": "mxfp4xbf16"}[cfg.recipe],
+        "dtype": ("mxfp4xmxfp4" if cfg.prequant else
+                  {"bf16": "bf16", "fp8block": "fp8e4m3", "mxfp4": "mxfp4xbf16",
+                   "mxfp8": "mxfp8e4m3"}[cfg.recipe]),
         "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights; random init)",
         "config": {"workload": f"{args.config} {cfg.name} fused MoE layer, T={args.tokens}",
                    "tokens": args.tokens, "hidden": cfg.hidden, "inter": cfg.inter,

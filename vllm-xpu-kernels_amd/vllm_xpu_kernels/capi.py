@@ -88,8 +88,11 @@ def _check(rc: int, what: str) -> None:
 
 
 def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
-               expert_map=None) -> FusedMoeArgs:
-    """Arguments for an XpuFusedMoe's prepared weights."""
+               expert_map=None, hidden_scale=None) -> FusedMoeArgs:
+    """Arguments for an XpuFusedMoe's prepared weights (hidden_scale:
+    hidden_states pre-quantised, its scales as XpuFusedMoe.apply takes them
+    after conversion: f32 for fp8block, e8m0 bytes for mxfp8 / mxfp4, whose
+    hidden_states are then packed e2m1 bytes [T, H/2])."""
     a = FusedMoeArgs()
     a.recipe = moe._recipe
     a.activation = moe._act
@@ -99,6 +102,10 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     s13, s2 = moe._scales(hidden_states.dtype)
     a.ids_dtype = I64 if topk_ids.dtype == torch.int64 else I32
     a.num_tokens, a.hidden = hidden_states.shape
+    if hidden_scale is not None:
+        a.hidden_scale = hidden_scale.data_ptr()
+        if moe.recipe.startswith("mxfp4"):
+            a.hidden *= 2
     a.inter = moe.inter_size
     a.num_experts = moe.w13.shape[0]
     a.topk = topk_ids.shape[1]

@@ -10,7 +10,7 @@ network, a checkpoint or the CPU oracle.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from typing import Optional
 
 import torch
@@ -35,6 +35,7 @@ class MoeConfig:
     bias: bool = False          # w13/w2 biases (gpt-oss)
     zipf_tau: float = 0.0       # >0: skewed router logits
     tokens: tuple = field(default_factory=tuple)
+    prequant: bool = False      # mxfp4: input handed over as e2m1 + e8m0 (w4a4)
 
 
 # Calibrated once (tests/golden/calibrate_zipf.py, on the device generator
@@ -55,6 +56,20 @@ CONFIGS = {
     "C5": MoeConfig("gpt-oss-20b", 2880, 2880, 32, 4, "mxfp4", "softmax",
                     activation="swigluoai", bias=True, tokens=(1, 128, 4096)),
 }
+
+
+# Recipe variants on the same shapes (not BASELINE configurations): DeepSeek-V3
+# with mxfp8 weights, gpt-oss-20b with pre-quantised mxfp4 input (both GEMMs
+# e2m1 x e2m1).
+VARIANTS = {
+    "C3-mxfp8": replace(CONFIGS["C3"], recipe="mxfp8"),
+    "C5-w4a4": replace(CONFIGS["C5"], prequant=True),
+}
+
+
+def config(name: str) -> MoeConfig:
+    """A configuration (C1-C5) or a recipe variant by name."""
+    return CONFIGS[name] if name in CONFIGS else VARIANTS[name]
 
 
 def _gen(device, seed: int) -> torch.Generator:
@@ -254,7 +269,8 @@ def algorithmic_bytes(cfg: MoeConfig, T: int, active: int) -> float:
         wb = n / 2 + n / 32
     if cfg.bias:
         wb += 2 * (2 * I + H)
-    return active * wb + T * H * 2 + T * H * 2 + T * E * 4 + T * k * 8
+    x_in = T * (H / 2 + H / 32) if cfg.prequant else T * H * 2
+    return active * wb + x_in + T * H * 2 + T * E * 4 + T * k * 8
 
 
 def algorithmic_flops(cfg: MoeConfig, T: int) -> float:
@@ -262,21 +278,24 @@ def algorithmic_flops(cfg: MoeConfig, T: int) -> float:
 
 
 PEAK_TFLOPS = {"bf16": 2500.0, "fp8block": 5000.0, "mxfp4": 2500.0, "mxfp8": 5000.0}
+PEAK_TFLOPS_FP4 = 10100.0   # e2m1 x e2m1 (pre-quantised mxfp4 input)
 PEAK_HBM_GBS = 8000.0
 
 
 def roofline_time_s(cfg: MoeConfig, T: int, active: int) -> tuple[float, float]:
-    """(t_hbm, t_mfma) lower bounds in seconds.  mxfp4 runs its MFMA in bf16
-    (weights dequantised in registers), so it is priced at the bf16 peak."""
+    """(t_hbm, t_mfma) lower bounds in seconds.  mxfp4 with 16-bit input runs
+    its MFMA in bf16 (weights dequantised in registers), so it is priced at
+    the bf16 peak; with pre-quantised input at the fp4 peak."""
+    peak = PEAK_TFLOPS_FP4 if cfg.prequant else PEAK_TFLOPS[cfg.recipe]
     return (algorithmic_bytes(cfg, T, active) / (PEAK_HBM_GBS * 1e9),
-            algorithmic_flops(cfg, T) / (PEAK_TFLOPS[cfg.recipe] * 1e12))
+            algorithmic_flops(cfg, T) / (peak * 1e12))
 
 
 def expected_active(E: int, slots: int) -> float:
     return E * (1.0 - (1.0 - 1.0 / E) ** slots)
 
 
-__all__ = ["MoeConfig", "CONFIGS", "make_weights", "make_activations",
+__all__ = ["MoeConfig", "CONFIGS", "VARIANTS", "config", "make_weights", "make_activations",
            "make_router_logits", "make_correction_bias", "route",
            "fp8_block_quant", "mxfp4_quant", "mxfp8_quant", "expert_weights_nk",
            "algorithmic_bytes", "algorithmic_flops", "roofline_time_s",
