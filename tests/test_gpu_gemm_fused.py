@@ -949,3 +949,29 @@ def test_fused_moe_hip_graph_replays(dev, T):
         junk = torch.randn(1 << 20, device=dev).sum()   # eager work between replays
         torch.cuda.synchronize()
         del junk
+
+
+@pytest.mark.parametrize("name,E", [("C1", None), ("C3", 16), ("C5", 8)])
+def test_fused_moe_prepare_in_place(dev, monkeypatch, name, E):
+    """MI355MOE_PREPARE_IN_PLACE=1: the prepared w13 / w2 replace the storage
+    of the caller's tensors (the weights are held once, as the reference
+    does for its int4 weights); the layer's output equals the default
+    preparation's bit for bit, and a second layer on the same tensors is
+    refused."""
+    import dataclasses
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    cfg = _W().CONFIGS[name]
+    if E is not None:
+        cfg = dataclasses.replace(cfg, experts=E)
+    cfg, w, x, tw, ti, out, _ = _layer(cfg, 64, dev)
+    w13, w2 = w.w13.clone(), w.w2.clone()
+    monkeypatch.setenv("MI355MOE_PREPARE_IN_PLACE", "1")
+    moe = XpuFusedMoe(w13, w.w13_scale, w.w13_bias, w2, w.w2_scale, w.w2_bias,
+                      cfg.topk, cfg.activation, cfg.experts)
+    assert w13.data_ptr() == moe.w13.data_ptr() and w2.data_ptr() == moe.w2.data_ptr()
+    out2 = torch.empty_like(out)
+    moe.apply(out2, x, tw, ti)
+    assert torch.equal(out2, out)
+    with pytest.raises(ValueError, match="prepared in place"):
+        XpuFusedMoe(w13, w.w13_scale, w.w13_bias, w2, w.w2_scale, w.w2_bias,
+                    cfg.topk, cfg.activation, cfg.experts)

@@ -35,6 +35,10 @@ _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
               "relu2_no_mul": ACT_RELU2}
 WLAYOUT_NK, WLAYOUT_KBLOCK = 0, 1
 WEIGHT_LAYOUT_ENV = "MI355MOE_WEIGHT_LAYOUT"
+# 1: the prepared w13 / w2 replace the storage of the caller's tensors (as the
+# reference does for its int4 weights, fused_moe_interface.py:195-205), so the
+# weights are not held twice; those tensors then hold the prepared layout
+PREPARE_IN_PLACE_ENV = "MI355MOE_PREPARE_IN_PLACE"
 
 
 def _is_env_enabled(env_name: str, default: str = "0") -> bool:
@@ -173,7 +177,17 @@ class XpuFusedMoe:
             raise NotImplementedError(
                 f"{REF_FUSED_MOE_ENV}=1 (torch reference path) is not provided "
                 "by the MI355X build; the HIP kernels are the only path")
+        if getattr(w13, "mi355moe_prepared", False) or getattr(w2, "mi355moe_prepared", False):
+            raise ValueError(
+                f"w13 / w2 already hold weights prepared in place ({PREPARE_IN_PLACE_ENV}=1) "
+                "by another XpuFusedMoe; construct a layer once per weight tensor")
         self._prepare_weights(w13, w13_scales, w13_bias, w2, w2_scales, w2_bias)
+        if _is_env_enabled(PREPARE_IN_PLACE_ENV):
+            for src, prepared in ((w13, self.w13), (w2, self.w2)):
+                if src.data_ptr() != prepared.data_ptr():
+                    src.data = prepared
+                src.mi355moe_prepared = True
+            self.w13, self.w2 = w13, w2
 
         self.expert_map = expert_map
         if self.expert_map is None and self.ep_size > 1:
