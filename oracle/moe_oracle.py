@@ -822,7 +822,8 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
               topk_ids: torch.Tensor, activation: str = "silu",
               expert_map: Optional[torch.Tensor] = None,
               gemm1_clamp_limit: Optional[float] = None,
-              experts=None, a1q_scale: Optional[torch.Tensor] = None):
+              experts=None, a1q_scale: Optional[torch.Tensor] = None,
+              compute_dtype: Optional[torch.dtype] = None):
     """XpuFusedMoe.apply semantics (vllm_xpu_kernels/fused_moe_interface.py:
     319-419, reference path moe_utils.py:236-403, rounding points of
     SURVEY Appendix A):
@@ -841,10 +842,17 @@ def fused_moe(recipe: str, hidden: torch.Tensor, w13, w13_scale, w13_bias,
     285, 338-347): fp8block e4m3 with [T, H/128] f32 scales; mxfp8 e4m3
     with e8m0 [T, H/32]; mxfp4 packed e2m1 [T, H/2] with e8m0 [T, H/32],
     whose intermediate activation is then quantised to mxfp4 too.
+    ``compute_dtype`` overrides that bf16 for pre-quantised input: the
+    reference's kernel path rounds both GEMM outputs to the caller's output
+    type (fused_moe_interface.py:368-371, 398-401), its torch path to bf16
+    (moe_utils.py:285); the two differ only for an fp16 output.
     """
     T = hidden.shape[0]
     k = topk_ids.shape[1]
-    dt = hidden.dtype if a1q_scale is None else torch.bfloat16
+    if a1q_scale is None:
+        dt = hidden.dtype
+    else:
+        dt = torch.bfloat16 if compute_dtype is None else compute_dtype
     ids = topk_ids.to(torch.int64)
     if expert_map is not None:
         ids = expert_map.to(torch.int64)[ids]

@@ -152,9 +152,10 @@ def _layer(cfg, T, dev, E=None, seed_shift=0):
     return cfg, w, x, tw, ti, out, moe
 
 
-def _oracle_layer(cfg, w, x, tw, ti, tokens=None, a1q_scale=None):
+def _oracle_layer(cfg, w, x, tw, ti, tokens=None, a1q_scale=None, compute_dtype=None):
     """Run the oracle on CPU copies of only the experts the (sampled) tokens
-    route to (a1q_scale: x is pre-quantised e4m3 with these scales)."""
+    route to (a1q_scale: x is pre-quantised with these scales; compute_dtype:
+    the 16-bit type its GEMM outputs round to, bf16 if None)."""
     if tokens is not None:
         x, tw, ti = x[tokens], tw[tokens], ti[tokens]
         if a1q_scale is not None:
@@ -170,8 +171,10 @@ def _oracle_layer(cfg, w, x, tw, ti, tokens=None, a1q_scale=None):
         w2 = w.w2.index_select(0, usedd).transpose(1, 2).contiguous().cpu()
     elif cfg.recipe == "mxfp8":   # [E, K, N] + [E, K/32, N] -> [E, N, K] + [E, N, K/32]
         tr = lambda t: t.index_select(0, usedd).transpose(1, 2).contiguous().cpu()  # noqa: E731
-        return O.fused_moe("mxfp8", x.cpu(), tr(w.w13), tr(w.w13_scale), None, tr(w.w2),
-                           tr(w.w2_scale), None, tw.cpu(), ids, activation=cfg.activation,
+        bias = lambda b: None if b is None else b.index_select(0, usedd).cpu()  # noqa: E731
+        return O.fused_moe("mxfp8", x.cpu(), tr(w.w13), tr(w.w13_scale), bias(w.w13_bias),
+                           tr(w.w2), tr(w.w2_scale), bias(w.w2_bias), tw.cpu(), ids,
+                           activation=cfg.activation,
                            a1q_scale=None if a1q_scale is None else a1q_scale.cpu())
     else:
         w13 = w.w13.view(torch.uint8).index_select(0, usedd).cpu()
@@ -184,7 +187,8 @@ def _oracle_layer(cfg, w, x, tw, ti, tokens=None, a1q_scale=None):
     b2 = w.w2_bias.index_select(0, usedd).cpu() if w.w2_bias is not None else None
     return O.fused_moe(cfg.recipe, x.cpu(), w13, s13, b13, w2, s2, b2, tw.cpu(), ids,
                        activation=cfg.activation,
-                       a1q_scale=None if a1q_scale is None else a1q_scale.cpu())
+                       a1q_scale=None if a1q_scale is None else a1q_scale.cpu(),
+                       compute_dtype=compute_dtype)
 
 
 def test_fused_moe_c1_tiny(dev):
@@ -619,7 +623,7 @@ def test_fused_moe_generic_activation_clamp(dev):
         _close(out, ref)
 
 
-@pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4"])
+@pytest.mark.parametrize("recipe", ["bf16", "fp8block", "mxfp4", "mxfp8"])
 @pytest.mark.parametrize("T", [1, 16, 48, 300, 1024])
 def test_fused_moe_fp16(dev, recipe, T):
     """fp16 hidden states, output and biases (16-bit recipe: fp16 weights;
@@ -646,7 +650,7 @@ def test_fused_moe_fp16(dev, recipe, T):
     toks = torch.linspace(0, T - 1, min(T, 48)).long().to(dev)
     ref = _oracle_layer(cfg, w, x, tw, ti, toks)
     assert ref.dtype == h
-    if recipe == "fp8block":
+    if recipe in ("fp8block", "mxfp8"):
         _close(out[toks], ref, fp8=True)
     else:
         _close(out[toks], ref, rtol=1e-2, atol=1e-2)
@@ -828,22 +832,27 @@ def test_fused_moe_mxfp8_ignores_clamp_limit_like_reference(dev):
     assert torch.equal(out2, out)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T", [1, 32, 160, 1024])
-def test_fused_moe_mxfp4_pre_quantised_w4a4(dev, T):
+def test_fused_moe_mxfp4_pre_quantised_w4a4(dev, T, dt):
     """gpt-oss shapes (H = I = 2880: K % 256 = 64 in both GEMMs, N % 128 = 64)
     with pre-quantised mxfp4 input (packed e2m1 [T, H/2] + e8m0 [T, H/32]):
     both GEMMs are e2m1 x e2m1 with the intermediate activation quantised to
     mxfp4 per 32 (the reference's quant_act_xpu).  T = 1, 32: 16-slot STREAM
-    blocks; 160, 1024: the 320-slot kernel (20 and 128 slots per expert)."""
+    blocks; 160, 1024: the 320-slot kernel (20 and 128 slots per expert).
+    The output buffer's type (bf16 or fp16) sets the call's type, as in the
+    reference's kernel path (fused_moe_interface.py:368-371, 398-401): both
+    GEMM outputs round to it before the activation re-quantisation, and the
+    oracle is run in that type."""
     from vllm_xpu_kernels import ops
     cfg, w, x, tw, ti, out, moe = _layer(_W().CONFIGS["C5"], T, dev)
     xq, xs = ops.per_token_group_quant_mxfp4(x, 32)
     xq = xq.view(torch.uint8)
-    out4 = torch.empty_like(out)
+    out4 = torch.empty_like(out, dtype=dt)
     moe.apply(out4, xq.view(torch.float4_e2m1fn_x2), tw, ti,
               a1q_scale=_e8m0(xs).view(torch.float8_e8m0fnu))
     toks = torch.linspace(0, T - 1, min(T, 24)).long().to(dev)
-    ref = _oracle_layer(cfg, w, xq, tw, ti, toks, a1q_scale=_e8m0(xs))
+    ref = _oracle_layer(cfg, w, xq, tw, ti, toks, a1q_scale=_e8m0(xs), compute_dtype=dt)
     _close(out4[toks], ref, fp8=True)
     # and close to the w4a16 layer on the same input
     assert (out4.float() - out.float()).abs().mean() < 0.25 * out.float().abs().mean()

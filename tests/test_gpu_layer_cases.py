@@ -170,6 +170,11 @@ def _ep_weights(recipe, dt, g, H, I):
         s2 = torch.full((E, H, I // 128), 2.0 ** -5).to(dt)
         return (u13, s13, b13, u2, s2, b2), (u13 ^ 0x88, s13, b13, u2 ^ 0x88, s2, b2)
     W = _W()
+    if recipe == "mxfp8":   # reference layout: e4m3 [E, K, N] + e8m0 [E, K/32, N]
+        q13, s13 = W.mxfp8_quant(w13)
+        q2, s2 = W.mxfp8_quant(w2)
+        tr = lambda t: t.transpose(1, 2).contiguous()  # noqa: E731
+        return (tr(q13), tr(s13), b13, tr(q2), tr(s2), b2), (q13, s13, b13, q2, s2, b2)
     if recipe == "mxfp4":
         q13, s13 = W.mxfp4_quant(w13)
         q2, s2 = W.mxfp4_quant(w2)
@@ -184,7 +189,8 @@ def _ep_weights(recipe, dt, g, H, I):
 
 @pytest.mark.parametrize("recipe,dt", [("bf16", torch.float16), ("fp8", torch.float16),
                                        ("int4", torch.float16), ("mxfp4", torch.bfloat16),
-                                       ("fp8block", torch.bfloat16)])
+                                       ("fp8block", torch.bfloat16), ("mxfp8", torch.bfloat16),
+                                       ("mxfp8", torch.float16)])
 @pytest.mark.parametrize("ep_rank", [0, 3])
 @pytest.mark.parametrize("T", [1, 16, 512])
 def test_fused_moe_ep(dev, recipe, dt, ep_rank, T):
@@ -206,7 +212,7 @@ def test_fused_moe_ep(dev, recipe, dt, ep_rank, T):
     # tokens with no local expert give exact zeros
     local = ((ti[toks] >= lo) & (ti[toks] < hi)).any(-1)
     assert torch.all(got[~local] == 0)
-    if recipe == "fp8block":
+    if recipe in ("fp8block", "mxfp8"):
         _close_fp8(got, ref)
     else:
         tol = 2e-2 if dt == torch.bfloat16 else 1e-2

@@ -755,6 +755,17 @@ def test_fused_moe_oracle_fp8block_close_to_dequant_fp32():
     y2 = O.fused_moe("fp8block", xq2, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xs2)
     assert not torch.equal(y2, y)
     torch.testing.assert_close(y2.float(), y.float(), rtol=0.1, atol=0.05)
+    # compute_dtype=fp16 on pre-quantised input is exactly the fp16 layer
+    # that quantises its own fp16 input (the quantiser's codes and scales
+    # are the same for x in bf16 and in fp16: bf16 -> fp16 is exact here)
+    xh = x.half()
+    yh = O.fused_moe("fp8block", xh, q13, s13, None, q2, s2, None, w, ids)
+    xqh, xsh = O.per_token_group_fp8_quant(xh, 128)
+    assert torch.equal(xqh.view(torch.uint8), xq.view(torch.uint8)) and torch.equal(xsh, xs)
+    yqh = O.fused_moe("fp8block", xq, q13, s13, None, q2, s2, None, w, ids, a1q_scale=xs,
+                      compute_dtype=torch.float16)
+    assert yqh.dtype == torch.float16 and torch.equal(yqh, yh)
+    assert not torch.equal(yqh.float(), yq.float())
 
 
 # ------------------------------------------------------------ MX recipes
