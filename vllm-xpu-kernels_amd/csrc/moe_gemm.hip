@@ -47,9 +47,17 @@ __device__ __forceinline__ f32x4 mfma_fp8(uint4 a0, uint4 a1, uint4 b0,
                                                           0, 127);
 }
 
+// Waves per SIMD the register allocation must allow: the 16-slot 4-bit
+// kernels are latency-bound and keep six (80 registers); the others take
+// what they need.
+template <int RECIPE, int BM>
+constexpr int small_min_waves() {
+  return (RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4) && BM == 16 ? 6 : 1;
+}
+
 template <int RECIPE, int BM, int BN, int EPI, bool QOUT, bool F16>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
-                                                       void* __restrict__ qs) {
+__global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm_kernel(
+    const GemmArgs a, void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
   constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
   constexpr int XB = kFp8 ? 1 : 2;      // bytes per activation element
@@ -107,61 +115,75 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
   __syncthreads();
 
   if constexpr (kFp4) {
-    // 4-bit weights: the raw words and scale codes of stage k0 + KB are
-    // loaded while stage k0 computes.  Each stage first issues its
-    // activation loads, then the next stage's weight loads, so the wait for
-    // the activations (loads complete in issue order) leaves the weight
-    // prefetch in flight.  (Two stages of weight lead need twice the raw
-    // registers, and the lost occupancy costs more than it gains.)
-    constexpr int ACH = (BM * CPR + 255) / 256;  // activation chunks per thread
+    // 4-bit weights, software-pipelined one stage ahead: the raw words and
+    // scale codes of stage k0 + KB and its activation chunks are in flight
+    // while stage k0 computes.  Every load is unconditional, from an address
+    // clamped into range (rows past N read row 0, chunks past K the last
+    // chunk; K % 32 == 0), and out-of-range data is zeroed where it is used:
+    // a load under a branch makes the compiler wait for every load in flight
+    // where the branches join.  The raw weight registers are decoded before
+    // they are reloaded, so no copy waits for the next stage's loads.
+    static_assert(BM * CPR % 256 == 0, "whole activation chunks per thread");
+    constexpr int ACH = BM * CPR / 256;  // activation chunks per thread
     uint4 rw[NB];
     uint32_t rc[NB];
-    auto load_w4 = [&](int64_t k, uint4 (&v)[NB], uint32_t (&c)[NB]) {
-      const int kb = static_cast<int>(K - k < KB ? K - k : KB);
+    auto load_w4 = [&](int64_t k) {
+      const int64_t kk = k + 32 * q;
+      const int64_t blk32 = (kk < K ? kk : K - 32) / 32;  // the lane's 32-value block
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        const bool ok = k < K && wok[j] && 32 * q < kb;
-        const int64_t blk32 = (k + 32 * q) / 32;  // the lane's 32-value K block
-        v[j] = ok ? *reinterpret_cast<const uint4*>(wptr[j] + blk32 * wst.kblk)
-                  : make_uint4(0, 0, 0, 0);
-        c[j] = ok ? w4_scale_code<RECIPE>(a, e, wrow[j], blk32, sst) : 0u;
+        rw[j] = *reinterpret_cast<const uint4*>(wptr[j] + blk32 * wst.kblk);
+        rc[j] = w4_scale_code<RECIPE>(a, e, wrow[j], blk32, sst);
       }
     };
-    load_w4(0, rw, rc);
-    for (int64_t k0 = 0; k0 < K; k0 += KB) {
-      const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
-      uint4 av[ACH];
+    // chunk i of this thread: activation row xar[i] (-1: padding slot), K
+    // offset xc inside the stage (the same for every i: 256 % CPR == 0);
+    // addresses are recomputed per stage to keep registers for occupancy
+    static_assert(256 % CPR == 0, "one chunk column per thread");
+    const int xc = (tid % CPR) * 8;
+    int xar[ACH];
 #pragma unroll
-      for (int i = 0; i < ACH; ++i) {
-        const int idx = tid + 256 * i;
-        av[i] = make_uint4(0, 0, 0, 0);
-        if (idx < BM * CPR) {
-          const int r = idx / CPR, c = idx % CPR;
-          const int ar = s_arow[r];
-          if (ar >= 0 && c * 16 < kb * XB)
-            av[i] = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
-                                                    (static_cast<int64_t>(ar) * K + k0) * XB +
-                                                    c * 16);
-        }
-      }
-      uint4 nw[NB];
-      uint32_t nc[NB];
-      load_w4(k0 + KB, nw, nc);
+    for (int i = 0; i < ACH; ++i) xar[i] = s_arow[(tid + 256 * i) / CPR];
+    uint4 av[ACH];
+    auto load_x = [&](int64_t k0) {
+      const int64_t kk = k0 + xc;
+      const int64_t off = (kk < K ? kk : K - 8) * XB;
+#pragma unroll
+      for (int i = 0; i < ACH; ++i)
+        av[i] = *reinterpret_cast<const uint4*>(
+            static_cast<const uint8_t*>(a.A) +
+            static_cast<int64_t>(xar[i] >= 0 ? xar[i] : 0) * K * XB + off);
+    };
+    // the same issue order as in the loop (weights, then activation), so
+    // that the waits at the loop top count the activation loads as newer
+    load_w4(0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(0);
+    for (int64_t k0 = 0; k0 < K; k0 += KB) {
       uint4 wf[KS][NB];
+      const bool klive = k0 + 32 * q < K;  // this lane's 32-value block of the stage
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        wf[0][j] = w4_decode8<RECIPE, F16>(rw[j].x, rc[j]);
-        wf[1][j] = w4_decode8<RECIPE, F16>(rw[j].y, rc[j]);
-        wf[2][j] = w4_decode8<RECIPE, F16>(rw[j].z, rc[j]);
-        wf[3][j] = w4_decode8<RECIPE, F16>(rw[j].w, rc[j]);
+        // masks rather than selects: a select becomes a branch around copies
+        const uint32_t m = klive && wok[j] ? ~0u : 0u;
+        const uint32_t c = rc[j] & m;
+        wf[0][j] = w4_decode8<RECIPE, F16>(rw[j].x & m, c);
+        wf[1][j] = w4_decode8<RECIPE, F16>(rw[j].y & m, c);
+        wf[2][j] = w4_decode8<RECIPE, F16>(rw[j].z & m, c);
+        wf[3][j] = w4_decode8<RECIPE, F16>(rw[j].w & m, c);
       }
-      __syncthreads();  // the previous stage's fragment reads are done
+      load_w4(k0 + KB);  // past K on the last stage: clamped, unused
+      // issued before anything below waits for this stage's activation
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();   // the previous stage's fragment reads are done
 #pragma unroll
       for (int i = 0; i < ACH; ++i) {
         const int idx = tid + 256 * i;
-        if (idx < BM * CPR)
-          *reinterpret_cast<uint4*>(sX + (idx / CPR) * ROWB + (idx % CPR) * 16) = av[i];
+        const uint32_t m = xar[i] >= 0 && k0 + xc < K ? ~0u : 0u;
+        *reinterpret_cast<uint4*>(sX + (idx / CPR) * ROWB + (idx % CPR) * 16) =
+            make_uint4(av[i].x & m, av[i].y & m, av[i].z & m, av[i].w & m);
       }
+      load_x(k0 + KB);
       __syncthreads();
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -174,8 +196,6 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(const GemmArgs a,
             acc[mt][j] = mfma16_16x16x32<F16>(wf[s][j], x, acc[mt][j]);
         }
       }
-#pragma unroll
-      for (int j = 0; j < NB; ++j) rw[j] = nw[j], rc[j] = nc[j];
     }
   } else {
     for (int64_t k0 = 0; k0 < K; k0 += KB) {
