@@ -52,7 +52,8 @@ __device__ __forceinline__ f32x4 mfma_fp8(uint4 a0, uint4 a1, uint4 b0,
 // what they need.
 template <int RECIPE, int BM>
 constexpr int small_min_waves() {
-  return (RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4) && BM == 16 ? 6 : 1;
+  constexpr bool k4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
+  return k4 && BM == 16 ? 6 : 1;
 }
 
 template <int RECIPE, int BM, int BN, int EPI, bool QOUT, bool F16>
@@ -198,6 +199,29 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
       }
     }
   } else {
+    // 16-bit and fp8 weights.  Per stage: the weight fragments HBM -> VGPR,
+    // then the activation chunks of the stage -> LDS.  STORE kernels load
+    // unconditionally from addresses clamped into range (rows past N read
+    // row 0, K past the end the last chunk), zero the out-of-range data
+    // where it is used, and keep all of a thread's activation chunks in
+    // flight together (one wait per stage; a load under a branch makes the
+    // compiler wait for every load in flight).  GLU kernels, which hold
+    // twice the weight fragments, move the activation one chunk at a time
+    // under conditions: in flight together the chunks cost them a wave per
+    // SIMD and measured slower (C2 T=256 w13 +2 %; STORE -3 to -20 %).
+    constexpr bool kBatchX = EPI != EPI_GLU;
+    constexpr int NCH = BM * CPR;           // activation chunks per stage
+    constexpr int ACH = (NCH + 255) / 256;  // per thread
+    static_assert(256 % CPR == 0, "one chunk column per thread");
+    constexpr int KE = 16 / XB;             // K elements per chunk
+    const int xc = (tid % CPR) * KE;
+    int xar[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int idx = tid + 256 * i;
+      xar[i] = idx < NCH ? s_arow[idx / CPR] : -1;
+    }
+    const int xsr = kFp8 && tid < BM ? s_arow[tid] : -1;  // fp8: this thread's scale row
     for (int64_t k0 = 0; k0 < K; k0 += KB) {
       const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
       // ---- weight fragments: HBM -> VGPR
@@ -205,39 +229,71 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
       float wsc[NB];
   #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        if constexpr (kFp8) {
+        if constexpr (kFp8) {  // K % 128 == 0: no tail
           const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (k0 >> 7) * wst.kblk + 32 * q);
-          wf[0][j][0] = wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
-          wf[0][j][1] = wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
+          wf[0][j][0] = kBatchX || wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
+          wf[0][j][1] = kBatchX || wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
           const float* bs = static_cast<const float*>(a.b_scale);
           wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wrow[j] / 128) *
                           (K / 128) + k0 / 128];
         } else {
   #pragma unroll
           for (int s = 0; s < KS; ++s) {
-            const bool ok = wok[j] && 32 * s + 8 * q + 8 <= kb;
-            wf[s][j][0] = ok ? *reinterpret_cast<const uint4*>(
-                                   wptr[j] + w_koff16(wst, k0 + 32 * s + 8 * q))
-                             : make_uint4(0, 0, 0, 0);
+            const int64_t kk = k0 + 32 * s + 8 * q;
+            if constexpr (kBatchX)
+              wf[s][j][0] = *reinterpret_cast<const uint4*>(
+                  wptr[j] + w_koff16(wst, kk + 8 <= K ? kk : K - 8));
+            else
+              wf[s][j][0] = wok[j] && 32 * s + 8 * q + 8 <= kb
+                                ? *reinterpret_cast<const uint4*>(wptr[j] + w_koff16(wst, kk))
+                                : make_uint4(0, 0, 0, 0);
           }
         }
       }
       // ---- activation tile -> LDS
-      __syncthreads();
-      for (int idx = tid; idx < BM * CPR; idx += 256) {
-        const int r = idx / CPR, c = idx % CPR;
-        const int ar = s_arow[r];
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (ar >= 0 && c * 16 < kb * XB)
-          v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
-                                              (static_cast<int64_t>(ar) * K + k0) * XB +
-                                              c * 16);
-        *reinterpret_cast<uint4*>(sX + r * ROWB + c * 16) = v;
-      }
-      if constexpr (kFp8) {
-        if (tid < BM) {
-          const int ar = s_arow[tid];
-          s_xs[tid] = ar >= 0 ? a.a_scale[static_cast<int64_t>(ar) * (K / 128) + k0 / 128] : 0.f;
+      const int64_t xoff = (k0 + xc < K ? k0 + xc : K - KE) * XB;
+      auto xload = [&](int i) {
+        return *reinterpret_cast<const uint4*>(
+            static_cast<const uint8_t*>(a.A) +
+            static_cast<int64_t>(xar[i] >= 0 ? xar[i] : 0) * K * XB + xoff);
+      };
+      auto xstore = [&](int i, const uint4& v) {
+        const int idx = tid + 256 * i;
+        const uint32_t m = xar[i] >= 0 && xc < kb ? ~0u : 0u;
+        if (idx < NCH)
+          *reinterpret_cast<uint4*>(sX + (idx / CPR) * ROWB + (idx % CPR) * 16) =
+              make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+      };
+      if constexpr (kBatchX) {
+        uint4 av[ACH];
+  #pragma unroll
+        for (int i = 0; i < ACH; ++i) av[i] = xload(i);
+        float xsv = 0.f;
+        if constexpr (kFp8)
+          xsv = a.a_scale[static_cast<int64_t>(xsr >= 0 ? xsr : 0) * (K / 128) + k0 / 128];
+        __syncthreads();  // the previous stage's fragment reads are done
+  #pragma unroll
+        for (int i = 0; i < ACH; ++i) xstore(i, av[i]);
+        if constexpr (kFp8) {
+          if (tid < BM) s_xs[tid] = xsr >= 0 ? xsv : 0.f;
+        }
+      } else {
+        __syncthreads();  // the previous stage's fragment reads are done
+        for (int idx = tid; idx < NCH; idx += 256) {
+          const int r = idx / CPR, c = idx % CPR;
+          const int ar = s_arow[r];
+          uint4 v = make_uint4(0, 0, 0, 0);
+          if (ar >= 0 && c * 16 < kb * XB)
+            v = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(a.A) +
+                                                (static_cast<int64_t>(ar) * K + k0) * XB +
+                                                c * 16);
+          *reinterpret_cast<uint4*>(sX + r * ROWB + c * 16) = v;
+        }
+        if constexpr (kFp8) {
+          if (tid < BM) {
+            const int ar = s_arow[tid];
+            s_xs[tid] = ar >= 0 ? a.a_scale[static_cast<int64_t>(ar) * (K / 128) + k0 / 128] : 0.f;
+          }
         }
       }
       __syncthreads();
@@ -260,9 +316,14 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
           for (int s = 0; s < KS; ++s) {
             const int koff = 32 * s + 8 * q;
             const uint4 x = *reinterpret_cast<const uint4*>(xr + koff * 2);
+            // weights past K (the last stage of a K % 128 != 0) read back in-range data
+            const uint32_t m = koff + 8 <= kb ? ~0u : 0u;
   #pragma unroll
-            for (int j = 0; j < NB; ++j)
-              acc[mt][j] = mfma16_16x16x32<F16>(wf[s][j][0], x, acc[mt][j]);
+            for (int j = 0; j < NB; ++j) {
+              const uint4 w = wf[s][j][0];
+              acc[mt][j] = mfma16_16x16x32<F16>(make_uint4(w.x & m, w.y & m, w.z & m, w.w & m),
+                                                x, acc[mt][j]);
+            }
           }
         }
       }
