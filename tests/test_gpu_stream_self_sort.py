@@ -1,0 +1,126 @@
+"""Decode layers with at most 16 slots: the STREAM w13 launch sorts the top-k
+ids itself (and quantises fp8 activations per 1 x 128 block into LDS)
+instead of a sort(+quantisation) launch before it.  The layer output must be
+the sort launch's bit for bit (MI355MOE_STREAM_SELF_SORT=0 selects it): the
+w2 and reduction launches read the sort outputs this launch writes, so any
+difference from the counting sort's outputs would show in the output."""
+import dataclasses
+
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _W():
+    from vllm_xpu_kernels import workloads
+    return workloads
+
+
+def _both(call, monkeypatch):
+    monkeypatch.setenv("MI355MOE_STREAM_SELF_SORT", "0")
+    ref = call()
+    monkeypatch.delenv("MI355MOE_STREAM_SELF_SORT")
+    got = call()
+    again = call()
+    torch.cuda.synchronize()
+    return ref, got, again
+
+
+def _layer_call(cfg, T, dev, dt=torch.bfloat16, ids_dtype=torch.int32, ti=None, tw=None,
+                expert_map=None, prequant=False):
+    from vllm_xpu_kernels import ops
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    W = _W()
+    w = W.make_weights(cfg, dev)
+    if dt == torch.float16:
+        w = dataclasses.replace(
+            w, w13=w.w13.half() if cfg.recipe == "bf16" else w.w13,
+            w2=w.w2.half() if cfg.recipe == "bf16" else w.w2,
+            w13_bias=None if w.w13_bias is None else w.w13_bias.half(),
+            w2_bias=None if w.w2_bias is None else w.w2_bias.half())
+    x = W.make_activations(cfg, T, dev).to(dt)
+    if ti is None:
+        bias = W.make_correction_bias(cfg, dev) if cfg.routing == "grouped_sigmoid" else None
+        tw, ti = W.route(cfg, W.make_router_logits(cfg, T, dev), bias)
+    ti = ti.to(ids_dtype)
+    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                      cfg.topk, cfg.activation, cfg.experts)
+    kw = {} if expert_map is None else {"expert_map": expert_map}
+    if prequant:
+        xq, xs = ops.per_token_group_fp8_quant(x, 128)
+        x, kw["a1q_scale"] = xq, xs
+
+    def call():
+        out = torch.full((T, cfg.hidden), float("nan"), dtype=dt, device=dev)
+        moe.apply(out, x, tw, ti, **kw)
+        return out
+    return call, (cfg, w, x, tw, ti)
+
+
+@pytest.mark.parametrize("T", [1, 2])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C5"])
+def test_self_sort_bit_identical(dev, monkeypatch, name, T):
+    call, _ = _layer_call(_W().CONFIGS[name], T, dev)
+    ref, got, again = _both(call, monkeypatch)
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, ref) and torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("variant", ["fp16", "int64_ids", "prequant", "fp16_bf16w"])
+def test_self_sort_bit_identical_variants(dev, monkeypatch, variant):
+    """(int4 runs the same routing through test_fused_moe_ep at T=1 and 16.)"""
+    W = _W()
+    if variant == "fp16":
+        call, _ = _layer_call(W.CONFIGS["C3"], 1, dev, dt=torch.float16)
+    elif variant == "int64_ids":
+        call, _ = _layer_call(W.CONFIGS["C3"], 2, dev, ids_dtype=torch.int64)
+    elif variant == "prequant":
+        call, _ = _layer_call(W.CONFIGS["C3"], 2, dev, prequant=True)
+    else:
+        call, _ = _layer_call(W.CONFIGS["C2"], 2, dev, dt=torch.float16)
+    ref, got, again = _both(call, monkeypatch)
+    assert torch.equal(got, ref) and torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("T", [1, 2, 8])
+def test_self_sort_expert_map_and_duplicates(dev, monkeypatch, T):
+    """A rank holding experts 16..23 of 64 (dropped slots, tokens with no
+    local slot) and ids repeated within a token."""
+    W = _W()
+    cfg = dataclasses.replace(W.CONFIGS["C2"], experts=8, hidden=512, inter=256, topk=2)
+    g = torch.Generator(device=dev).manual_seed(11 + T)
+    ti = torch.randint(12, 28, (T, 2), generator=g, device=dev)
+    ti[0] = torch.tensor([17, 17], device=dev)     # the same expert twice
+    if T > 1:
+        ti[1] = torch.tensor([40, 3], device=dev)  # no local expert
+    tw = torch.rand(T, 2, generator=g, device=dev)
+    emap = torch.full((64,), -1, dtype=torch.int32, device=dev)
+    emap[16:24] = torch.arange(8, dtype=torch.int32, device=dev)
+    call, _ = _layer_call(cfg, T, dev, ti=ti, tw=tw, expert_map=emap)
+    ref, got, again = _both(call, monkeypatch)
+    assert torch.equal(got, ref) and torch.equal(again, ref)
+    assert not torch.isnan(got.float()).any()
+    if T > 1:
+        assert torch.all(got[1] == 0)
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_self_sort_matches_oracle(dev, T):
+    """C3 (fp8, activations quantised in the kernel) against the oracle, and
+    the in-kernel quantisation against the group quantiser: the same layer
+    fed the oracle quantiser's codes and scales (a1q_scale, no quantisation
+    in the kernel) gives the same output bit for bit."""
+    from test_gpu_gemm_fused import _close, _oracle_layer
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    call, (cfg, w, x, tw, ti) = _layer_call(_W().CONFIGS["C3"], T, dev)
+    out = call()
+    _close(out, _oracle_layer(cfg, w, x, tw, ti.long()), fp8=True)
+    xq, xs = O.per_token_group_fp8_quant(x.cpu(), 128)
+    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                      cfg.topk, cfg.activation, cfg.experts)
+    out_q = torch.empty_like(out)
+    moe.apply(out_q, xq.to(dev), tw, ti, a1q_scale=xs.to(dev))
+    assert torch.equal(out_q, out)

@@ -373,6 +373,15 @@ int gemm_recipe(const mi355moe_fused_moe_args* a) {
   return a->recipe == MI355MOE_RECIPE_MXFP4 && a->hidden_scale ? RECIPE_MX4A4 : a->recipe;
 }
 
+// At most 16 slots on the STREAM kernels: the w13 launch sorts the slots
+// itself (and quantises fp8 activations into LDS) instead of a sort
+// launch before it.  MI355MOE_STREAM_SELF_SORT=0 keeps the sort launch (the
+// same outputs).  Read per call.
+bool stream_self_sort_enabled() {
+  const char* v = getenv("MI355MOE_STREAM_SELF_SORT");
+  return !(v && v[0] == '0');
+}
+
 FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
   const int64_t E = a->num_experts;
@@ -628,10 +637,22 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   const bool preq = fp8 && a->hidden_scale;
 
   if (int m = mark(0)) return m;
+  const bool glu = epilogue_act(a->activation);
+  // at most 16 slots on the STREAM kernels: the w13 launch routes them
+  // itself (and quantises fp8 activations into LDS)
+  // (fp8: every token row's K range of a split fits the kernel's LDS tile)
+  const int64_t self_per = cdiv(cdiv(H, 128), L.ks1);
+  const bool self_quant_ok =
+      H % 128 == 0 && T * self_per * 128 <= kStreamSelfXBytes &&
+      (reinterpret_cast<uintptr_t>(a->hidden_states) & 15) == 0;
+  const bool self_sort = L.tile == TILE_STREAM && L.slots <= 16 && !mx && glu &&
+                         (!fp8 || preq || self_quant_ok) && stream_self_sort_enabled();
   // up to 4096 slots: the sort and the e4m3 activation quantisation share
   // one launch (the quantisation stage is then empty)
   int rc = 1;
-  if (fp8 && !preq) {
+  if (self_sort) {
+    rc = 0;
+  } else if (fp8 && !preq) {
     rc = run_sort_quant_fp8(a->topk_ids, a->ids_dtype, L.slots, id_bound, a->expert_map, E,
                             L.bm, L.sorted, L.max_padded, L.eids, L.max_blocks, L.ntp, L.inv,
                             static_cast<int32_t>(L.slots), L.cum, a->hidden_states, f16, L.xq,
@@ -639,7 +660,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     if (rc < 0) return rc;
   }
   const bool quantised = rc == 0;
-  if (!quantised) {
+  if (!quantised && !self_sort) {
     rc = run_counting_sort(a->topk_ids, a->ids_dtype, L.slots, id_bound,
                            a->expert_map, E, L.bm, L.sorted, L.max_padded,
                            L.eids, L.max_blocks, L.ntp, L.inv, nullptr,
@@ -649,7 +670,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   }
 
   if (int m = mark(1)) return m;
-  if (fp8 && !preq && !quantised) {
+  if (fp8 && !preq && !quantised && !self_sort) {
     rc = group_quant_fp8(a->hidden_states, a->act_dtype, L.xq, L.xs, T, H, st);
     if (rc) return rc;
   }
@@ -670,7 +691,6 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
 
   // gelu / gelu_tanh / swiglustep / relu2_no_mul: w13 stores G1, a separate
   // kernel applies the activation (and the fp8 re-quantisation)
-  const bool glu = epilogue_act(a->activation);
   const int64_t K2 = act_width(a);
   GemmArgs g1{};
   g1.A = (fp8 && !preq) || (mx && !a->hidden_scale) ? static_cast<const void*>(L.xq)
@@ -711,6 +731,21 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.w_group = static_cast<int32_t>(a->w_group);
   g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w13_scale)
                                                     : nullptr;
+  if (self_sort) {
+    g1.sr_ids = a->topk_ids;
+    g1.sr_ids_dtype = a->ids_dtype;
+    g1.sr_map = a->expert_map;
+    g1.sr_id_bound = id_bound;
+    g1.sr_keys = static_cast<int32_t>(E);
+    g1.sr_max_padded = L.max_padded;
+    g1.sr_max_blocks = L.max_blocks;
+    g1.sr_sorted = L.sorted;
+    g1.sr_eids = L.eids;
+    g1.sr_ntp = L.ntp;
+    g1.sr_cum = L.cum;
+    g1.sr_inv = L.inv;
+    if (fp8 && !preq) g1.sr_x = static_cast<const uint16_t*>(a->hidden_states);
+  }
   if (glu) {
     rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_GLU, fp8 || mx, g1, L.grid_blocks,
                           mx ? static_cast<void*>(L.acts8) : static_cast<void*>(L.acts), st);

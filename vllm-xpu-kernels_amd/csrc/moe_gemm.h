@@ -73,7 +73,27 @@ struct GemmArgs {
   const uint8_t* a_mxs;
   int64_t a_mxs_ld;
   int64_t q_mxs_ld;
+  // STREAM w13 of the fused layer with at most 16 slots (num_valid): every
+  // workgroup of the split launch sorts the top-k ids itself, with the
+  // counting sort's key rule and ordering (block b = the b-th smallest
+  // routed expert, its rows the expert's slots in flat order), and
+  // workgroup (0, 0, 0) writes the sort's outputs (sr_sorted padded with
+  // num_valid, sr_eids, sr_ntp, sr_cum, sr_inv) for the launches that
+  // follow, so no sort launch runs.  With sr_x (fp8block recipe) the
+  // activation is the 16-bit hidden states [T, K], quantised per 1 x 128
+  // block by the group quantiser into LDS before the K loop.
+  const void* sr_ids;    // null: the sort launch ran
+  int32_t sr_ids_dtype;
+  const int32_t* sr_map;
+  int64_t sr_id_bound;
+  int32_t sr_keys;       // experts (sort keys)
+  int64_t sr_max_padded, sr_max_blocks;
+  int32_t *sr_sorted, *sr_eids, *sr_ntp, *sr_cum, *sr_inv;
+  const uint16_t* sr_x;
 };
+// LDS bytes a STREAM workgroup gives the in-kernel-quantised activation
+// (GemmArgs::sr_x): tokens x the split's K range, e4m3 (and 1 x 128 scales).
+constexpr int64_t kStreamSelfXBytes = 32768;
 
 // gemm1_clamp_limit on the (gate, up) pair of GLU output column n, both
 // already in the 16-bit type (the host rounds the limit to that type, so the

@@ -11,6 +11,8 @@
 // the activation (16 slots m): lane l holds rows n = 4*(l/16) + r of slot
 // m = l%16.  The only barrier is in the fp8 epilogue, which finds the amax of
 // each slot's 128 activation columns across the 8 waves.
+#include <type_traits>
+
 #include "mfma16.h"
 #include "moe_gemm.h"
 
@@ -87,7 +89,79 @@ __device__ __forceinline__ f32x4 mma_mx(uint4 a0, uint4 a1, uint32_t as, uint4 b
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT, FMT, 0, as, 0, bs);
 }
 
-template <int RECIPE, int EPI, bool QOUT, int PD, bool F16>
+// Routing of at most 16 slots (GemmArgs::sr_ids), run by wave 0 of every
+// workgroup: slot i's key is the counting sort's (ids outside [0,
+// sr_id_bound) and unmapped ids dropped); rank = number of distinct routed
+// experts below its expert, within = earlier slots of the same expert, so
+// its sorted position is 16 rank + within (one 16-slot block per expert).
+// Fills this block's rows, every slot's position, the experts by rank and
+// their count.
+__device__ __forceinline__ void route_slots(const GemmArgs& a, int blk, int lane, int* s_arow,
+                                            int* s_drow, int* s_pos, int* s_dkey, int* s_nd) {
+  constexpr int kNone = 0x7fffffff;
+  int key = kNone;
+  if (lane < a.num_valid) {
+    int64_t v;
+    if (a.sr_ids_dtype == MI355MOE_I64) v = static_cast<const int64_t*>(a.sr_ids)[lane];
+    else if (a.sr_ids_dtype == MI355MOE_U32) v = static_cast<const uint32_t*>(a.sr_ids)[lane];
+    else v = static_cast<const int32_t*>(a.sr_ids)[lane];
+    if (v >= 0 && v < a.sr_id_bound) {
+      if (a.sr_map) v = a.sr_map[v];
+      if (v >= 0 && v < a.sr_keys) key = static_cast<int>(v);
+    }
+  }
+  const bool routed = key != kNone;
+  int within = 0;
+  bool first = routed;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int kj = __shfl(key, j, 64);
+    if (j < lane && kj == key) {
+      ++within;
+      first = false;
+    }
+  }
+  const uint64_t fm = __ballot(first);
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int kj = __shfl(key, j, 64);
+    if (((fm >> j) & 1ull) && kj < key) ++rank;
+  }
+  if (lane < 16) {
+    s_arow[lane] = -1;
+    s_drow[lane] = -1;
+    s_pos[lane] = routed ? 16 * rank + within : -1;
+  }
+  if (routed && rank == blk) {
+    s_arow[within] = a.a_by_pos ? blk * 16 + within : lane / a.a_div;
+    s_drow[within] = a.d_by_pos ? blk * 16 + within : lane;
+  }
+  if (first) s_dkey[rank] = key;
+  if (lane == 0) *s_nd = __popcll(fm);
+}
+
+// The counting sort's outputs for the routing above (workgroup (0, 0, 0)):
+// sorted ids padded with num_valid, block experts (0 past the routed ones),
+// padded expert starts, the padded slot count and every slot's position.
+__device__ __forceinline__ void write_routing(const GemmArgs& a, int tid, int nthreads,
+                                              const int* s_pos, const int* s_dkey, int nd) {
+  for (int64_t p = tid; p < a.sr_max_padded; p += nthreads) a.sr_sorted[p] = a.num_valid;
+  for (int64_t b = tid; b < a.sr_max_blocks; b += nthreads)
+    a.sr_eids[b] = b < nd ? s_dkey[b] : 0;
+  for (int x = tid; x <= a.sr_keys; x += nthreads) {
+    int below = 0;
+    for (int d = 0; d < nd; ++d) below += s_dkey[d] < x ? 1 : 0;
+    a.sr_cum[x] = 16 * below;
+  }
+  if (tid == 0) *a.sr_ntp = 16 * nd;
+  if (tid < a.num_valid) a.sr_inv[tid] = s_pos[tid];
+  __syncthreads();  // the padding above is written before the slots below
+  if (tid < a.num_valid && s_pos[tid] >= 0 && s_pos[tid] < a.sr_max_padded)
+    a.sr_sorted[s_pos[tid]] = tid;
+}
+
+template <int RECIPE, int EPI, bool QOUT, int PD, bool F16, bool SELF8 = false>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -98,23 +172,38 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int XB = (kFp8 || kMx8) ? 1 : 2;  // bytes per activation element (mx4: packed)
 
+  static_assert(!SELF8 || (kFp8 && kGlu), "in-kernel quantisation: fp8block w13");
+  using FragT = Frag<RECIPE>;
+
   __shared__ int s_arow[16];
   __shared__ int s_drow[16];
   __shared__ float s_amax[WAVES][16];
+  __shared__ int s_pos[16], s_dkey[16], s_nd;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, q = lane >> 4;
   const int blk = blockIdx.y;
-  if (blk * 16 >= *a.ntp) return;  // uniform
-  const int e = a.block_expert[blk];
   const int64_t K = a.K, N = a.N;
-  if (tid < 16) {
-    const int rid = a.row_ids[static_cast<int64_t>(blk) * 16 + tid];
-    const bool ok = rid >= 0 && rid < a.num_valid;
-    s_arow[tid] = ok ? (a.a_by_pos ? blk * 16 + tid : rid / a.a_div) : -1;
-    s_drow[tid] = ok ? (a.d_by_pos ? blk * 16 + tid : rid) : -1;
+  int e;
+  if (a.sr_ids && !a.finalize) {  // uniform: this launch sorts the slots itself
+    if (wave == 0) route_slots(a, blk, lane, s_arow, s_drow, s_pos, s_dkey, &s_nd);
+    __syncthreads();
+    const int nd = s_nd;
+    if (blockIdx.x == 0 && blk == 0 && blockIdx.z == 0)
+      write_routing(a, tid, WAVES * 64, s_pos, s_dkey, nd);
+    if (blk >= nd) return;  // uniform
+    e = s_dkey[blk];
+  } else {
+    if (blk * 16 >= *a.ntp) return;  // uniform
+    e = a.block_expert[blk];
+    if (tid < 16) {
+      const int rid = a.row_ids[static_cast<int64_t>(blk) * 16 + tid];
+      const bool ok = rid >= 0 && rid < a.num_valid;
+      s_arow[tid] = ok ? (a.a_by_pos ? blk * 16 + tid : rid / a.a_div) : -1;
+      s_drow[tid] = ok ? (a.d_by_pos ? blk * 16 + tid : rid) : -1;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   // output columns of this wave: GLU 16 activation columns, STORE 32 columns
   const int64_t col0 = static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) +
@@ -141,6 +230,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                       static_cast<int64_t>(xok ? arow : 0) * (kMx4 ? K / 2 : K * XB);
   const uint8_t* xsp8 = kMx ? a.a_mxs + static_cast<int64_t>(xok ? arow : 0) * a.a_mxs_ld
                             : nullptr;
+
   // fp8 weight-block scale rows (16-row sub-tiles sit inside one 128-row block)
   int64_t wsr[2];
   wsr[0] = (wrow[0] / 128);
@@ -152,7 +242,19 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   // row 0 (their outputs are never stored), the K tail re-reads the last
   // chunk and compute() zeroes it.  A load under a condition would make the
   // compiler wait for every prefetched stage where the branches join.
-  auto load = [&](Frag<RECIPE>& f, int64_t k0) {
+  // ---- this split's K stages [s0, s0 + nk)
+  const int ks = a.ksplit > 1 ? a.ksplit : 1;
+  const int nk_all = static_cast<int>((K + KS - 1) / KS);
+  const int per = (nk_all + ks - 1) / ks;
+  const int s0 = static_cast<int>(blockIdx.z) * per;
+  const int nk = a.finalize ? 0 : ((nk_all - s0) < per ? (nk_all - s0) : per);
+  // SELF8: every token row's K range of the split, e4m3, and its 1 x 128
+  // scales in LDS (row pitch xrs bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t s_xq[SELF8 ? kStreamSelfXBytes : 16];
+  __shared__ float s_xsc[SELF8 ? kStreamSelfXBytes / 128 : 1];
+  const int64_t kx0 = static_cast<int64_t>(s0) * KS;
+  const int xrs = per * KS;
+  auto load = [&](FragT& f, int64_t k0) {
     if constexpr (kMx) {  // K % 32 == 0; addresses clamped into range
       // the lane's e8m0 codes: block q of the stage (row l16)
       const int64_t k = k0 + 32 * q;
@@ -190,10 +292,18 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
         f.ws[t] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) * (K / 128) + k0 / 128];
       }
-      const uint8_t* px = xp + k0 + 32 * q;
-      f.x[0] = *reinterpret_cast<const uint4*>(px);
-      f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
-      f.xs = a.a_scale[xsrow + k0 / 128];
+      if constexpr (SELF8) {  // the split's activation tile in LDS
+        const int64_t kk = k0 - kx0;
+        const uint8_t* px = s_xq + (xok ? arow : 0) * xrs + kk + 32 * q;
+        f.x[0] = *reinterpret_cast<const uint4*>(px);
+        f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
+        f.xs = s_xsc[(xok ? arow : 0) * (xrs / 128) + kk / 128];
+      } else {
+        const uint8_t* px = xp + k0 + 32 * q;
+        f.x[0] = *reinterpret_cast<const uint4*>(px);
+        f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
+        f.xs = a.a_scale[xsrow + k0 / 128];
+      }
     } else if constexpr (kFp4) {  // K % 32 == 0
       const int64_t k = k0 + 32 * q;
       const int64_t kc = k < K ? k : K - 32;
@@ -221,8 +331,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
   acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const Frag<RECIPE>& fin, int64_t k0) {
-    Frag<RECIPE> f = fin;
+  auto compute = [&](const FragT& fin, int64_t k0) {
+    FragT f = fin;
     if (!kMx && k0 + KS > K) {  // the last stage of a K that is not a multiple of 128
       const uint4 z4 = make_uint4(0, 0, 0, 0);
       if constexpr (kFp4) {
@@ -276,13 +386,24 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     }
   };
 
-  // ---- K loop over this split's stages [s0, s0 + nk), PD stages in flight
-  const int ks = a.ksplit > 1 ? a.ksplit : 1;
-  const int nk_all = static_cast<int>((K + KS - 1) / KS);
-  const int per = (nk_all + ks - 1) / ks;
-  const int s0 = static_cast<int>(blockIdx.z) * per;
-  const int nk = a.finalize ? 0 : ((nk_all - s0) < per ? (nk_all - s0) : per);
-  Frag<RECIPE> buf[PD];
+  // ---- K loop, PD stages in flight
+  if constexpr (SELF8) {
+    // quantise the tile with the group quantiser itself: 16 lanes (8 values
+    // each) per 128-value block; the trip count is uniform, lanes past the
+    // end take part in the shuffles and store nothing
+    const int T = a.num_valid / a.a_div;
+    const int cpr = nk * 16;  // 8-value chunks of a row in this split
+    const int nch = T * cpr;
+    for (int base = 0; base < nch; base += WAVES * 64) {
+      const int i = base + tid;
+      const bool act = i < nch;
+      const int r = act ? i / cpr : 0;
+      fp8_quant_block8<F16>(a.sr_x + static_cast<int64_t>(r) * K + kx0, s_xq + r * xrs,
+                            s_xsc + r * (xrs / KS), act ? i % cpr : cpr, cpr);
+    }
+    __syncthreads();
+  }
+  FragT buf[PD];
   if (nk > 0) {
 #pragma unroll
     for (int d = 0; d < PD; ++d)
@@ -442,9 +563,17 @@ int launch_stream_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t
             static_cast<unsigned>(a.ksplit > 1 ? a.ksplit : 1));
   GemmArgs g = a;
   g.finalize = 0;
-  moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
+  if constexpr (RECIPE == MI355MOE_RECIPE_FP8BLOCK && EPI == EPI_GLU) {
+    if (a.sr_x)
+      moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, true><<<grid, dim3(512), 0, st>>>(g, qs);
+    else
+      moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
+  } else {
+    moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
+  }
   MI_LAUNCH_CHECK();
   if (a.ksplit > 1 && !a.partials_only) {  // sum the partial tiles and run the epilogue
+    // (the routing is read back from what the split launch wrote)
     grid.z = 1;
     g.finalize = 1;
     moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
