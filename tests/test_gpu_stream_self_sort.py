@@ -1,9 +1,12 @@
-"""Decode layers with at most 16 slots: the STREAM w13 launch sorts the top-k
-ids itself (and quantises fp8 activations per 1 x 128 block into LDS)
-instead of a sort(+quantisation) launch before it.  The layer output must be
-the sort launch's bit for bit (MI355MOE_STREAM_SELF_SORT=0 selects it): the
-w2 and reduction launches read the sort outputs this launch writes, so any
-difference from the counting sort's outputs would show in the output."""
+"""Decode layers with at most 16 slots in fewer launches.  (1) The STREAM
+w13 launch sorts the top-k ids itself (and quantises fp8 activations per
+1 x 128 block into LDS) instead of a sort(+quantisation) launch before it:
+the layer output must be the sort launch's bit for bit
+(MI355MOE_STREAM_SELF_SORT=0 selects it); the w2 and reduction launches read
+the sort outputs this launch writes, so any difference from the counting
+sort's outputs would show in the output.  (2) Where the output columns fill
+the GPU (C3 shapes), w2 runs token-major and writes the layer output itself:
+bit for bit the top-k reduction launch's (MI355MOE_STREAM_TOKEN_W2=0)."""
 import dataclasses
 
 import pytest
@@ -19,10 +22,10 @@ def _W():
     return workloads
 
 
-def _both(call, monkeypatch):
-    monkeypatch.setenv("MI355MOE_STREAM_SELF_SORT", "0")
+def _both(call, monkeypatch, var="MI355MOE_STREAM_SELF_SORT"):
+    monkeypatch.setenv(var, "0")
     ref = call()
-    monkeypatch.delenv("MI355MOE_STREAM_SELF_SORT")
+    monkeypatch.delenv(var)
     got = call()
     again = call()
     torch.cuda.synchronize()
@@ -124,3 +127,53 @@ def test_self_sort_matches_oracle(dev, T):
     out_q = torch.empty_like(out)
     moe.apply(out_q, xq.to(dev), tw, ti, a1q_scale=xs.to(dev))
     assert torch.equal(out_q, out)
+
+
+TOKEN_W2 = "MI355MOE_STREAM_TOKEN_W2"
+
+
+@pytest.mark.parametrize("variant", ["T1", "T2", "fp16", "int64_ids"])
+def test_token_major_w2_bit_identical(dev, monkeypatch, variant):
+    C3 = _W().CONFIGS["C3"]
+    if variant == "T1":
+        call, _ = _layer_call(C3, 1, dev)
+    elif variant == "T2":
+        call, _ = _layer_call(C3, 2, dev)
+    elif variant == "fp16":
+        call, _ = _layer_call(C3, 1, dev, dt=torch.float16)
+    else:
+        call, _ = _layer_call(C3, 2, dev, ids_dtype=torch.int64)
+    ref, got, again = _both(call, monkeypatch, TOKEN_W2)
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, ref) and torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_token_major_w2_expert_parallel(dev, monkeypatch, T):
+    """DeepSeek-V3 shapes on a rank holding experts 64..95 of 256: dropped
+    slots (their waves stream nothing), a token with no local expert (exact
+    zeros), and a token listing one expert twice."""
+    W = _W()
+    cfg = dataclasses.replace(W.CONFIGS["C3"], experts=32)
+    g = torch.Generator(device=dev).manual_seed(21 + T)
+    ti = torch.randint(40, 120, (T, 8), generator=g, device=dev)
+    ti[0, :3] = torch.tensor([70, 70, 5], device=dev)
+    if T > 1:
+        ti[1] = torch.arange(200, 208, device=dev)
+    tw = torch.rand(T, 8, generator=g, device=dev)
+    emap = torch.full((256,), -1, dtype=torch.int32, device=dev)
+    emap[64:96] = torch.arange(32, dtype=torch.int32, device=dev)
+    call, _ = _layer_call(cfg, T, dev, ti=ti, tw=tw, expert_map=emap)
+    ref, got, again = _both(call, monkeypatch, TOKEN_W2)
+    assert torch.equal(got, ref) and torch.equal(again, ref)
+    assert not torch.isnan(got.float()).any()
+    if T > 1:
+        assert torch.all(got[1] == 0)
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_token_major_w2_matches_oracle(dev, T):
+    from test_gpu_gemm_fused import _close, _oracle_layer
+    cfg = dataclasses.replace(_W().CONFIGS["C3"], bias=True)
+    call, (cfg, w, x, tw, ti) = _layer_call(cfg, T, dev)
+    _close(call(), _oracle_layer(cfg, w, x, tw, ti.long()), fp8=True)

@@ -381,6 +381,14 @@ bool stream_self_sort_enabled() {
   const char* v = getenv("MI355MOE_STREAM_SELF_SORT");
   return !(v && v[0] == '0');
 }
+// At most 16 slots, top-k dividing 8 and enough output columns to fill the
+// GPU: the w2 launch runs token-major and writes the layer output (no top-k
+// reduction launch).  MI355MOE_STREAM_TOKEN_W2=0 keeps the reduction launch
+// (the same arithmetic).  Read per call.
+bool stream_token_w2_enabled() {
+  const char* v = getenv("MI355MOE_STREAM_TOKEN_W2");
+  return !(v && v[0] == '0');
+}
 
 FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
@@ -797,6 +805,20 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.w_group = static_cast<int32_t>(a->w_group);
   g2.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w2_scale)
                                                     : nullptr;
+  const bool token_w2 = L.tile == TILE_STREAM && L.ks2 <= 1 && L.slots <= 16 && k <= 8 &&
+                        8 % k == 0 && cdiv(H, 32 * (8 / k)) * T >= 192 &&
+                        stream_token_w2_enabled();
+  if (token_w2) {
+    g2.tok_inv = L.inv;
+    g2.tok_w = a->topk_weights;
+    g2.topk = static_cast<int32_t>(k);
+    g2.tok_out = a->output;
+    rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_STORE, false, g2, L.grid_blocks, nullptr,
+                          st);
+    if (rc) return rc;
+    if (int m = mark(4)) return m;
+    return mark(5);
+  }
   // split-K decode: the partial sums are finished by the top-k reduction
   const bool fuse_reduce = L.tile == TILE_STREAM && L.ks2 > 1 && k <= kFuseMaxTopk;
   g2.partials_only = fuse_reduce;

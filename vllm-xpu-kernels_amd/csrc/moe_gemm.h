@@ -90,6 +90,19 @@ struct GemmArgs {
   int64_t sr_max_padded, sr_max_blocks;
   int32_t *sr_sorted, *sr_eids, *sr_ntp, *sr_cum, *sr_inv;
   const uint16_t* sr_x;
+  // STREAM w2 of the fused layer in token-major form (tok_out set; STORE,
+  // no split, 8 % topk == 0): workgroup (x, t) covers token t and 8 / topk
+  // groups of 32 output columns; wave w takes slot j = w % topk of the token
+  // (its sorted position tok_inv[t topk + j], its expert block_expert[pos /
+  // 16], activation row pos) over the group's 32 weight rows, and the
+  // group's slots are summed through LDS into
+  //   tok_out[t, n] = T(sum_j tok_w[t topk + j] * T(acc_j(n) + bias_j(n)))
+  // over the slots the sort kept, in j order -- the arithmetic of the
+  // separate top-k reduction launch, which is then not needed.
+  const int32_t* tok_inv;
+  const float* tok_w;
+  int32_t topk;
+  void* tok_out;
 };
 // LDS bytes a STREAM workgroup gives the in-kernel-quantised activation
 // (GemmArgs::sr_x): tokens x the split's K range, e4m3 (and 1 x 128 scales).

@@ -161,7 +161,8 @@ __device__ __forceinline__ void write_routing(const GemmArgs& a, int tid, int nt
     a.sr_sorted[s_pos[tid]] = tid;
 }
 
-template <int RECIPE, int EPI, bool QOUT, int PD, bool F16, bool SELF8 = false>
+template <int RECIPE, int EPI, bool QOUT, int PD, bool F16, bool SELF8 = false,
+          bool TOKM = false>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -173,6 +174,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   constexpr int XB = (kFp8 || kMx8) ? 1 : 2;  // bytes per activation element (mx4: packed)
 
   static_assert(!SELF8 || (kFp8 && kGlu), "in-kernel quantisation: fp8block w13");
+  static_assert(!TOKM || (!kGlu && !QOUT), "token-major form: STORE w2");
   using FragT = Frag<RECIPE>;
 
   __shared__ int s_arow[16];
@@ -185,7 +187,11 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const int blk = blockIdx.y;
   const int64_t K = a.K, N = a.N;
   int e;
-  if (a.sr_ids && !a.finalize) {  // uniform: this launch sorts the slots itself
+  int tpos = -1;  // token-major: this wave's slot's sorted position (-1: dropped)
+  if constexpr (TOKM) {
+    tpos = a.tok_inv[static_cast<int64_t>(blockIdx.y) * a.topk + wave % a.topk];
+    e = a.block_expert[tpos >= 0 ? tpos / 16 : 0];
+  } else if (a.sr_ids && !a.finalize) {  // uniform: this launch sorts the slots itself
     if (wave == 0) route_slots(a, blk, lane, s_arow, s_drow, s_pos, s_dkey, &s_nd);
     __syncthreads();
     const int nd = s_nd;
@@ -206,8 +212,10 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   }
 
   // output columns of this wave: GLU 16 activation columns, STORE 32 columns
-  const int64_t col0 = static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) +
-                       wave * (kGlu ? 16 : 32);
+  // (token-major: the 32 columns of its group, shared by the group's slots)
+  const int64_t col0 =
+      TOKM ? (static_cast<int64_t>(blockIdx.x) * (WAVES / a.topk) + wave / a.topk) * 32
+           : static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) + wave * (kGlu ? 16 : 32);
   const int64_t wrow_bytes = (kFp4 || kMx4) ? K / 2 : K * XB;
   const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
                         static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const WStride sst = s_stride4(a);
   const uint8_t* wp0 = wexp + wrow[0] * wst.row;
   const uint8_t* wp1 = wexp + wrow[1] * wst.row;
-  const int arow = s_arow[l16];
+  const int arow = TOKM ? (l16 == 0 ? tpos : -1) : s_arow[l16];
   const bool xok = arow >= 0;
   const uint8_t* xp = static_cast<const uint8_t*>(a.A) +
                       static_cast<int64_t>(xok ? arow : 0) * (kMx4 ? K / 2 : K * XB);
@@ -247,7 +255,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const int nk_all = static_cast<int>((K + KS - 1) / KS);
   const int per = (nk_all + ks - 1) / ks;
   const int s0 = static_cast<int>(blockIdx.z) * per;
-  const int nk = a.finalize ? 0 : ((nk_all - s0) < per ? (nk_all - s0) : per);
+  const int nk = a.finalize || (TOKM && tpos < 0) ? 0  // a dropped slot streams nothing
+                                                    : ((nk_all - s0) < per ? (nk_all - s0) : per);
   // SELF8: every token row's K range of the split, e4m3, and its 1 x 128
   // scales in LDS (row pitch xrs bytes)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[SELF8 ? kStreamSelfXBytes : 16];
@@ -473,7 +482,28 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       ov[t][r] = nok ? v : 0.f;
     }
   }
-  if constexpr (QOUT && kMx) {
+  if constexpr (TOKM) {
+    // the group's slots summed in j order: the top-k reduction's arithmetic
+    // on the rounded slot values (lane l16 = 0 holds this wave's slot)
+    __shared__ float s_tok[WAVES][32];
+    if (l16 == 0) {
+#pragma unroll
+      for (int t = 0; t < NO; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_tok[wave][16 * t + 4 * q + r] = ov[t][r];
+    }
+    __syncthreads();
+    if (wave % a.topk != 0 || lane >= 32 || col0 + lane >= N) return;
+    const int64_t t = blockIdx.y;
+    float acc1 = 0.f;
+    for (int j = 0; j < a.topk; ++j) {
+      const int64_t slot = t * a.topk + j;
+      if (a.tok_inv[slot] < 0) continue;
+      const float wj = a.tok_w[slot];
+      acc1 += wj * s_tok[wave + j][lane];
+    }
+    static_cast<uint16_t*>(a.tok_out)[t * N + col0 + lane] = st16<F16>(acc1);
+  } else if constexpr (QOUT && kMx) {
     // MX activation for the w2 GEMM, one e8m0 scale per 32 columns (the
     // output columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
     // with ue8m0 scales, mxfp4 as per_token_group_quant_mxfp4 (eps 1e-10)
@@ -563,6 +593,16 @@ int launch_stream_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t
             static_cast<unsigned>(a.ksplit > 1 ? a.ksplit : 1));
   GemmArgs g = a;
   g.finalize = 0;
+  if constexpr (EPI == EPI_STORE && !QOUT) {
+    if (a.tok_out) {  // token-major w2: the output itself, no split
+      const int groups = WAVES / a.topk;
+      const dim3 tg(static_cast<unsigned>(cdiv(a.N, 32 * groups)),
+                    static_cast<unsigned>(a.num_valid / a.topk), 1);
+      moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, false, true><<<tg, dim3(512), 0, st>>>(g, qs);
+      MI_LAUNCH_CHECK();
+      return MI355MOE_OK;
+    }
+  }
   if constexpr (RECIPE == MI355MOE_RECIPE_FP8BLOCK && EPI == EPI_GLU) {
     if (a.sr_x)
       moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, true><<<grid, dim3(512), 0, st>>>(g, qs);
