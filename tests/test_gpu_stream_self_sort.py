@@ -6,7 +6,10 @@ the layer output must be the sort launch's bit for bit
 the sort outputs this launch writes, so any difference from the counting
 sort's outputs would show in the output.  (2) Where the output columns fill
 the GPU (C3 shapes), w2 runs token-major and writes the layer output itself:
-bit for bit the top-k reduction launch's (MI355MOE_STREAM_TOKEN_W2=0)."""
+bit for bit the top-k reduction launch's (MI355MOE_STREAM_TOKEN_W2=0).  (3)
+With a split-K w13 and a 16-bit activation (C2, C5), the w2 launch rebuilds
+its activation rows from the w13 partial tiles: bit for bit the w13
+finalize launch's (MI355MOE_STREAM_W2_FINISHES_W13=0)."""
 import dataclasses
 
 import pytest
@@ -177,3 +180,33 @@ def test_token_major_w2_matches_oracle(dev, T):
     cfg = dataclasses.replace(_W().CONFIGS["C3"], bias=True)
     call, (cfg, w, x, tw, ti) = _layer_call(cfg, T, dev)
     _close(call(), _oracle_layer(cfg, w, x, tw, ti.long()), fp8=True)
+
+
+W2_FIN = "MI355MOE_STREAM_W2_FINISHES_W13"
+
+
+@pytest.mark.parametrize("variant", ["C2-T1", "C2-T2", "C5-T1", "C5-T2", "C1-T2", "C2-fp16",
+                                     "C5-clamp"])
+def test_w2_finishes_w13_bit_identical(dev, monkeypatch, variant):
+    W = _W()
+    name, rest = variant.split("-")
+    cfg = W.CONFIGS[name]
+    if rest == "fp16":
+        call, _ = _layer_call(cfg, 1, dev, dt=torch.float16)
+    elif rest == "clamp":
+        from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+        w = W.make_weights(cfg, dev)
+        x = W.make_activations(cfg, 2, dev)
+        tw, ti = W.route(cfg, W.make_router_logits(cfg, 2, dev))
+        moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
+                          cfg.topk, cfg.activation, cfg.experts, gemm1_clamp_limit=0.05)
+
+        def call():
+            out = torch.empty_like(x)
+            moe.apply(out, x, tw, ti)
+            return out
+    else:
+        call, _ = _layer_call(cfg, int(rest[1:]), dev)
+    ref, got, again = _both(call, monkeypatch, W2_FIN)
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, ref) and torch.equal(again, ref)

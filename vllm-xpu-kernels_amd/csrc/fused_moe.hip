@@ -389,6 +389,14 @@ bool stream_token_w2_enabled() {
   const char* v = getenv("MI355MOE_STREAM_TOKEN_W2");
   return !(v && v[0] == '0');
 }
+// Split-K w13 with a 16-bit activation: the w2 launch rebuilds its
+// activation rows from the w13 partial tiles (no w13 finalize launch).
+// MI355MOE_STREAM_W2_FINISHES_W13=0 keeps the finalize launch (the same
+// arithmetic).  Read per call.
+bool stream_w2_finishes_w13_enabled() {
+  const char* v = getenv("MI355MOE_STREAM_W2_FINISHES_W13");
+  return !(v && v[0] == '0');
+}
 
 FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
@@ -754,6 +762,16 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     g1.sr_inv = L.inv;
     if (fp8 && !preq) g1.sr_x = static_cast<const uint16_t*>(a->hidden_states);
   }
+  // decode: w2 writes the output token-major (C3 shapes), or rebuilds its
+  // activation rows from the split-K w13 partials (16-bit activations)
+  const bool token_w2 = L.tile == TILE_STREAM && L.ks2 <= 1 && L.slots <= 16 && k <= 8 &&
+                        8 % k == 0 && cdiv(H, 32 * (8 / k)) * T >= 192 &&
+                        stream_token_w2_enabled();
+  const int64_t per2 = cdiv(cdiv(K2, 128), L.ks2 > 1 ? L.ks2 : 1);
+  const bool w2_finishes_w13 = L.tile == TILE_STREAM && L.ks1 > 1 && glu && !fp8 && !mx &&
+                               !token_w2 && 16 * per2 * 128 * 2 <= kStreamG1FinBytes &&
+                               stream_w2_finishes_w13_enabled();
+  g1.partials_only = w2_finishes_w13;
   if (glu) {
     rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_GLU, fp8 || mx, g1, L.grid_blocks,
                           mx ? static_cast<void*>(L.acts8) : static_cast<void*>(L.acts), st);
@@ -805,9 +823,20 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.w_group = static_cast<int32_t>(a->w_group);
   g2.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w2_scale)
                                                     : nullptr;
-  const bool token_w2 = L.tile == TILE_STREAM && L.ks2 <= 1 && L.slots <= 16 && k <= 8 &&
-                        8 % k == 0 && cdiv(H, 32 * (8 / k)) * T >= 192 &&
-                        stream_token_w2_enabled();
+  if (w2_finishes_w13) {
+    g2.g1f.part = L.part1;
+    g2.g1f.ks = L.ks1;
+    g2.g1f.n_tiles = static_cast<int32_t>(cdiv(I, 128));
+    g2.g1f.N = g1.N;
+    g2.g1f.up_off = g1.up_off;
+    g2.g1f.ldb_rows = g1.ldb_rows;
+    g2.g1f.bias = g1.bias;
+    g2.g1f.expert_scale = g1.expert_scale;
+    g2.g1f.clamp_limit = g1.clamp_limit;
+    g2.g1f.alpha = g1.alpha;
+    g2.g1f.limit = g1.limit;
+    g2.g1f.act = g1.act;
+  }
   if (token_w2) {
     g2.tok_inv = L.inv;
     g2.tok_w = a->topk_weights;

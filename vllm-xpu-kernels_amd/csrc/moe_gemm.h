@@ -21,6 +21,23 @@ __host__ __device__ constexpr bool is_mx_recipe(int r) {
   return r == MI355MOE_RECIPE_MXFP8 || r == RECIPE_MX4A4;
 }
 
+// The split-K w13 GEMM of the fused layer left its partial tiles (no
+// finalize launch); the STREAM w2 launch rebuilds each workgroup's 16-bit
+// activation rows from them (part != null): the w13 tile's partials summed
+// in split order, then its GLU epilogue (expert scale, bias, rounding,
+// clamp, activation).  The w13 GEMM's own parameters.
+struct G1Fin {
+  const float* part;     // [blocks, n_tiles, ks, 512 x 8]
+  int32_t ks, n_tiles;
+  int64_t N, up_off, ldb_rows;
+  const uint16_t* bias;
+  const float* expert_scale;
+  float clamp_limit, alpha, limit;
+  int32_t act;
+};
+// LDS bytes for those rows: 16 slots x the split's K range, 16-bit.
+constexpr int64_t kStreamG1FinBytes = 32768;
+
 struct GemmArgs {
   const void* A;
   const float* a_scale;  // fp8: [rowsA, K/128]
@@ -103,6 +120,9 @@ struct GemmArgs {
   const float* tok_w;
   int32_t topk;
   void* tok_out;
+  // STREAM w2 of the fused layer (16-bit activation): its activation rows
+  // rebuilt from the w13 partials (G1Fin) instead of read from A.
+  G1Fin g1f;
 };
 // LDS bytes a STREAM workgroup gives the in-kernel-quantised activation
 // (GemmArgs::sr_x): tokens x the split's K range, e4m3 (and 1 x 128 scales).
@@ -115,15 +135,19 @@ constexpr int64_t kStreamSelfXBytes = 32768;
 // 384-389).  swigluoai's G1 interleaves gate and up (column n's pair at 2n,
 // 2n + 1): both are clamped from above, and from below where 2n >= I; for
 // the other activations gate = [0, I) and up = [I, 2I).
-__device__ __forceinline__ void glu_clamp(const GemmArgs& a, int64_t n, float& g, float& u) {
-  const float L = a.clamp_limit;
+// (limit L, activation act, N = I of the GEMM)
+__device__ __forceinline__ void glu_clamp_with(float L, int act, int64_t N, int64_t n, float& g,
+                                               float& u) {
   if (!(L > 0.f)) return;
-  const bool swig = a.act == MI355MOE_ACT_SWIGLUOAI;
-  const bool upper_half = 2 * n >= a.N;
+  const bool swig = act == MI355MOE_ACT_SWIGLUOAI;
+  const bool upper_half = 2 * n >= N;
   g = fminf(g, L);
   if (swig && upper_half) g = fmaxf(g, -L);
   u = fminf(u, L);
   if (!swig || upper_half) u = fmaxf(u, -L);
+}
+__device__ __forceinline__ void glu_clamp(const GemmArgs& a, int64_t n, float& g, float& u) {
+  glu_clamp_with(a.clamp_limit, a.act, a.N, n, g, u);
 }
 
 enum GemmEpi { EPI_STORE = 0, EPI_GLU = 1 };

@@ -162,7 +162,7 @@ __device__ __forceinline__ void write_routing(const GemmArgs& a, int tid, int nt
 }
 
 template <int RECIPE, int EPI, bool QOUT, int PD, bool F16, bool SELF8 = false,
-          bool TOKM = false>
+          bool TOKM = false, bool XL = false>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -175,6 +175,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 
   static_assert(!SELF8 || (kFp8 && kGlu), "in-kernel quantisation: fp8block w13");
   static_assert(!TOKM || (!kGlu && !QOUT), "token-major form: STORE w2");
+  static_assert(!XL || (!kGlu && !QOUT && !kFp8 && !kMx && !TOKM),
+                "activation rows from the w13 partials: 16-bit activation, STORE w2");
   using FragT = Frag<RECIPE>;
 
   __shared__ int s_arow[16];
@@ -263,6 +265,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   __shared__ float s_xsc[SELF8 ? kStreamSelfXBytes / 128 : 1];
   const int64_t kx0 = static_cast<int64_t>(s0) * KS;
   const int xrs = per * KS;
+  // XL: this workgroup's 16 activation rows over the split's K range (16-bit,
+  // row pitch xrs elements), rebuilt from the w13 partials below
+  __shared__ __attribute__((aligned(16))) uint16_t s_xa[XL ? kStreamG1FinBytes / 2 : 8];
   auto load = [&](FragT& f, int64_t k0) {
     if constexpr (kMx) {  // K % 32 == 0; addresses clamped into range
       // the lane's e8m0 codes: block q of the stage (row l16)
@@ -322,7 +327,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         f.sc[t] = w4_scale_code<RECIPE>(a, e, wrow[t], kc / 32, sst);
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) f.x[s] = *reinterpret_cast<const uint4*>(xp + (kc + 8 * s) * 2);
+      for (int s = 0; s < 4; ++s)
+        f.x[s] = XL ? *reinterpret_cast<const uint4*>(s_xa + l16 * xrs + (kc - kx0) + 8 * s)
+                    : *reinterpret_cast<const uint4*>(xp + (kc + 8 * s) * 2);
     } else {  // K % 8 == 0
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -331,7 +338,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 #pragma unroll
         for (int t = 0; t < 2; ++t)
           f.w[t][s] = *reinterpret_cast<const uint4*>((t ? wp1 : wp0) + w_koff16(wst, kc));
-        f.x[s] = *reinterpret_cast<const uint4*>(xp + kc * 2);
+        f.x[s] = XL ? *reinterpret_cast<const uint4*>(s_xa + l16 * xrs + (kc - kx0))
+                    : *reinterpret_cast<const uint4*>(xp + kc * 2);
       }
     }
   };
@@ -409,6 +417,47 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       const int r = act ? i / cpr : 0;
       fp8_quant_block8<F16>(a.sr_x + static_cast<int64_t>(r) * K + kx0, s_xq + r * xrs,
                             s_xsc + r * (xrs / KS), act ? i % cpr : cpr, cpr);
+    }
+    __syncthreads();
+  }
+  if constexpr (XL) {
+    // the w13 finalize of this block's valid slots on the split's columns:
+    // its partial tiles summed in split order, then its GLU epilogue (the
+    // finalize launch's operations; 4 columns per item)
+    const G1Fin& g = a.g1f;
+    const int n4 = nk * KS / 4;
+    const float es1 = g.expert_scale ? g.expert_scale[e] : 1.f;
+    const int64_t bb = static_cast<int64_t>(e) * g.ldb_rows;
+    for (int it = tid; it < 16 * n4; it += WAVES * 64) {
+      const int m = it / n4, c4 = it - m * n4;
+      if (s_arow[m] < 0) continue;  // padding slot: its outputs are never stored
+      const int64_t c = kx0 + 4 * c4;
+      const int tid13 = static_cast<int>((c % 128) / 16) * 64 + static_cast<int>((c % 16) / 4) * 16 + m;
+      const float* tp = g.part + (static_cast<int64_t>(blk) * g.n_tiles + c / 128) * g.ks * 4096 +
+                        8 * tid13;
+      float gv[4] = {0.f, 0.f, 0.f, 0.f}, uv[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int z = 0; z < g.ks; ++z) {
+        const float4 g4 = *reinterpret_cast<const float4*>(tp + z * 4096);
+        const float4 u4 = *reinterpret_cast<const float4*>(tp + z * 4096 + 4);
+        gv[0] += g4.x; gv[1] += g4.y; gv[2] += g4.z; gv[3] += g4.w;
+        uv[0] += u4.x; uv[1] += u4.y; uv[2] += u4.z; uv[3] += u4.w;
+      }
+      uint32_t o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = c + r;
+        const bool nok = n < g.N;
+        float v = gv[r] * es1;
+        if (g.bias && nok) v += ld16<F16>(g.bias[bb + n]);
+        v = rnd16<F16>(v);
+        float u = uv[r] * es1;
+        if (g.bias && nok) u += ld16<F16>(g.bias[bb + g.up_off + n]);
+        u = rnd16<F16>(u);
+        glu_clamp_with(g.clamp_limit, g.act, g.N, n, v, u);
+        v = rnd16<F16>(glu16<F16>(v, u, g.act, g.alpha, g.limit));
+        o[r] = st16<F16>(nok ? v : 0.f);
+      }
+      *reinterpret_cast<uint2*>(s_xa + m * xrs + 4 * c4) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
     }
     __syncthreads();
   }
@@ -593,6 +642,22 @@ int launch_stream_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t
             static_cast<unsigned>(a.ksplit > 1 ? a.ksplit : 1));
   GemmArgs g = a;
   g.finalize = 0;
+  if constexpr (EPI == EPI_STORE && !QOUT && RECIPE != MI355MOE_RECIPE_FP8BLOCK &&
+                !is_mx_recipe(RECIPE)) {
+    if (a.g1f.part) {  // activation rows rebuilt from the w13 partials
+      moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, false, false, true>
+          <<<grid, dim3(512), 0, st>>>(g, qs);
+      MI_LAUNCH_CHECK();
+      if (a.ksplit > 1 && !a.partials_only) {
+        grid.z = 1;
+        g.finalize = 1;
+        g.g1f.part = nullptr;
+        moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16><<<grid, dim3(512), 0, st>>>(g, qs);
+        MI_LAUNCH_CHECK();
+      }
+      return MI355MOE_OK;
+    }
+  }
   if constexpr (EPI == EPI_STORE && !QOUT) {
     if (a.tok_out) {  // token-major w2: the output itself, no split
       const int groups = WAVES / a.topk;
