@@ -210,3 +210,32 @@ def test_w2_finishes_w13_bit_identical(dev, monkeypatch, variant):
     ref, got, again = _both(call, monkeypatch, W2_FIN)
     assert torch.isfinite(got.float()).all()
     assert torch.equal(got, ref) and torch.equal(again, ref)
+
+
+ALL_OFF = ("MI355MOE_STREAM_SELF_SORT", TOKEN_W2, W2_FIN)
+
+
+@pytest.mark.parametrize("shape", ["tokw2_tail", "w2fin_tail"])
+@pytest.mark.parametrize("T", [1, 2])
+def test_decode_paths_ragged_shapes(dev, monkeypatch, shape, T):
+    """Ragged decode shapes (row-major bf16 weights): H = 7192 (token-major
+    w2 with a last column group of 24) and I = 736 (w2 rebuilding its
+    activation from w13 tiles whose last one holds 96 columns), against the
+    separate launches bit for bit and against the oracle."""
+    from test_gpu_gemm_fused import _close, _oracle_layer
+    W = _W()
+    if shape == "tokw2_tail":
+        cfg = dataclasses.replace(W.CONFIGS["C2"], hidden=7192, inter=512, experts=64, topk=8)
+    else:
+        cfg = dataclasses.replace(W.CONFIGS["C2"], hidden=2048, inter=736, experts=64, topk=8,
+                                  bias=True)
+    call, (cfg, w, x, tw, ti) = _layer_call(cfg, T, dev)
+    for var in ALL_OFF:
+        monkeypatch.setenv(var, "0")
+    ref = call()
+    for var in ALL_OFF:
+        monkeypatch.delenv(var)
+    got = call()
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    _close(got, _oracle_layer(cfg, w, x, tw, ti.long()))
