@@ -53,6 +53,8 @@ def gemm_work(cfg, T, active, which):
         bw, sc, bx, sx = 1.0, 4.0 / (128 * 128), 1.0, 4.0 / 128
     elif cfg.recipe == "mxfp8":
         bw, sc, bx, sx = 1.0, 1.0 / 32, 1.0, 1.0 / 32
+    elif cfg.recipe == "fp8":    # per-expert e4m3 weights, 16-bit activations
+        bw, sc, bx, sx = 1.0, 0.0, 2.0, 0.0
     elif cfg.prequant:   # e2m1 x e2m1
         bw, sc, bx, sx = 0.5, 1.0 / 32, 0.5, 1.0 / 32
     else:
@@ -79,7 +81,7 @@ def _oracle_inputs(cfg, w, x, tw, ti):
     remap[used] = torch.arange(used.numel())
     ids = remap[ti_c]
     u = used.to(w.w13.device)
-    if cfg.recipe == "bf16":
+    if cfg.recipe in ("bf16", "fp8"):   # reference layout [E, K, N]
         w13 = w.w13.index_select(0, u).transpose(1, 2).contiguous().cpu()
         w2 = w.w2.index_select(0, u).transpose(1, 2).contiguous().cpu()
     else:
@@ -308,8 +310,9 @@ def kernel_roofline(pt, stages, key):
 SWEEP = [("C1", 64), ("C2", 1), ("C2", 16), ("C2", 64), ("C2", 256), ("C2", 4096),
          ("C3", 1), ("C3", 64), ("C3", 8192), ("C4", 2048), ("C5", 1), ("C5", 128),
          ("C5", 4096),
-         # recipe variants on the same shapes: mxfp8 weights, w4a4 (e2m1 x e2m1)
-         ("C3-mxfp8", 8192), ("C5-w4a4", 4096)]
+         # recipe variants on the same shapes: mxfp8 weights, w4a4 (e2m1 x e2m1),
+         # per-expert fp8 (decode reads the e4m3 weights themselves)
+         ("C3-mxfp8", 8192), ("C5-w4a4", 4096), ("C3-fp8", 1)]
 
 
 def op_bandwidth(dev, steps):
@@ -545,7 +548,7 @@ def main():
         "vs_baseline": None,
         "dtype": ("mxfp4xmxfp4" if cfg.prequant else
                   {"bf16": "bf16", "fp8block": "fp8e4m3", "mxfp4": "mxfp4xbf16",
-                   "mxfp8": "mxfp8e4m3"}[cfg.recipe]),
+                   "mxfp8": "mxfp8e4m3", "fp8": "e4m3xbf16"}[cfg.recipe]),
         "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights; random init)",
         "config": {"workload": f"{args.config} {cfg.name} fused MoE layer, T={args.tokens}",
                    "tokens": args.tokens, "hidden": cfg.hidden, "inter": cfg.inter,

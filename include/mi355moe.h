@@ -62,13 +62,30 @@ typedef enum {
                                    [E, N, K/group] in the activations'
                                    16-bit type, group 32/64/128/256:
                                    w = T(v * scale) (w4a16)               */
-  MI355MOE_RECIPE_MXFP8 = 4     /* e4m3 weights [E, N, K] with an e8m0 scale
+  MI355MOE_RECIPE_MXFP8 = 4,    /* e4m3 weights [E, N, K] with an e8m0 scale
                                    (u8) per 32 along K, [E, N, K/32];
                                    activations quantised per 32 to e4m3
                                    with ue8m0 scales (the reference's
                                    _quant_mxfp8_act_xpu), both scales in
                                    the scaled MFMA (vllm_xpu_kernels/
                                    moe_utils.py:76-104)                   */
+  MI355MOE_RECIPE_FP8 = 5,      /* per-expert fp8 (the reference's recipe
+                                   "fp8", vllm_xpu_kernels/
+                                   fused_moe_interface.py:42-59, w8a16):
+                                   e4m3 weights [E, N, K] (K-blocked
+                                   [E, K/128, N, 128]) with an f32 scale per
+                                   expert ([E] in w13_scale / w2_scale) and
+                                   16-bit activations; each weight is
+                                   converted exactly to the activations'
+                                   type as it is loaded and the expert's
+                                   scale multiplies the accumulators.
+                                   Decode kernels only: layers averaging
+                                   more than 10 slots per active expert,
+                                   or with hidden or intermediate sizes not
+                                   % 32, return MI355MOE_ERR_UNSUPPORTED
+                                   (run them as RECIPE_BF16 on exact 16-bit
+                                   copies)                                */
+  MI355MOE_RECIPE_FP8E5M2 = 6   /* as RECIPE_FP8 with e5m2 weights        */
 } mi355moe_recipe;
 
 typedef enum {
@@ -385,8 +402,12 @@ int mi355moe_silu_and_mul_mxfp4_quant(uint8_t* out, const void* input, int in_dt
  *                    B e4m3 [E,N,K] + b_scale f32 [E,N/128,K/128]
  *   recipe MXFP4:    A bf16 or f16 [M,K]; B u8 [E,N,K/2] + b_scale e8m0
  *                    [E,N,K/32]
+ *   recipe FP8 / FP8E5M2: A bf16 or f16 [M,K]; B e4m3 / e5m2 [E,N,K]
+ *                    (K % 32 == 0) + b_scale f32 [E]: the weights read as
+ *                    fp8 and converted exactly to a_dtype, the STREAM
+ *                    kernels at any M
  * bias: optional [E,N] in out_dtype; D [M,N] bf16 or f16 (out_dtype; equal
- * to a_dtype for recipes BF16 and MXFP4). */
+ * to a_dtype for recipes BF16, MXFP4, FP8 and FP8E5M2). */
 size_t mi355moe_grouped_gemm_workspace_size(int64_t total_rows,
                                             int64_t num_experts);
 /* Workspace including the on-the-fly 1x128 quantisation a 16-bit A needs
@@ -439,7 +460,8 @@ typedef struct {
   int64_t expert_map_len;
   const void* w13;            /* per recipe                                  */
   const void* w13_scale;      /* per recipe; BF16: optional f32 [E] factor
-                                 on the accumulators (per-expert fp8)     */
+                                 on the accumulators (per-expert fp8 on
+                                 16-bit copies); FP8 / FP8E5M2: f32 [E]   */
   const void* w13_bias;       /* optional [E, 2I] bf16 (same row order)      */
   const void* w2;
   const void* w2_scale;       /* as w13_scale                               */

@@ -732,6 +732,112 @@ def test_fused_moe_fp8_per_expert(dev, dt, fp8, T, topk):
     torch.testing.assert_close(out.cpu()[toks], ref, rtol=tol, atol=tol)
 
 
+def _finite_fp8_codes(fp8):
+    """Every byte whose fp8 value is finite (e4m3fn: all but 0x7f / 0xff;
+    e5m2: all but the Inf / NaN codes 0x7c-0x7f, 0xfc-0xff)."""
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    return codes[torch.isfinite(codes.view(fp8).float())]
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fp8", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("scale", [1.0, 0.125])
+def test_per_expert_fp8_weight_conversion_kat(dev, dt, fp8, scale):
+    """Per-expert fp8 weights read as they are (C ABI recipe FP8 / FP8E5M2,
+    grouped GEMM): against one-hot activation rows every output is one
+    weight times the expert scale, so each finite code's conversion to the
+    16-bit type shows exactly: D[m, n] = T(s * W[n, m]).  Row n holds every
+    finite code, rotated by n."""
+    import ctypes
+    from vllm_xpu_kernels import capi
+    lib = capi.lib
+    codes = _finite_fp8_codes(fp8)
+    K = N = 256
+    idx = (torch.arange(N).view(N, 1) + torch.arange(K).view(1, K)) % K
+    wb = torch.zeros(K, dtype=torch.uint8)
+    wb[:codes.numel()] = codes
+    w = wb[idx].view(fp8)                                  # [N, K]
+    a = torch.eye(K, dtype=dt)                             # M = K one-hot rows
+    recipe = 5 if fp8 == torch.float8_e4m3fn else 6
+    adt = capi.F16 if dt == torch.float16 else capi.BF16
+    lib.mi355moe_grouped_gemm_workspace_size_k.restype = ctypes.c_size_t
+    lib.mi355moe_grouped_gemm_workspace_size_k.argtypes = [ctypes.c_int, ctypes.c_int] + \
+        [ctypes.c_int64] * 3
+    lib.mi355moe_grouped_gemm.argtypes = (
+        [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p] +
+        [ctypes.c_int64] * 4 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p])
+    wsb = lib.mi355moe_grouped_gemm_workspace_size_k(recipe, adt, K, K, 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    A, W = a.to(dev), w.to(dev).contiguous()
+    sc = torch.tensor([scale], dtype=torch.float32, device=dev)
+    rows = torch.tensor([K], dtype=torch.int32, device=dev)
+    D = torch.full((K, N), float("nan"), dtype=dt, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.mi355moe_grouped_gemm(recipe, A.data_ptr(), adt, None, W.data_ptr(),
+                                   sc.data_ptr(), None, D.data_ptr(), adt, rows.data_ptr(),
+                                   K, N, K, 1, ws.data_ptr(), ws.numel(), stream)
+    assert rc == 0, lib.mi355moe_last_error()
+    torch.cuda.synchronize()
+    want = (w.float() * scale).to(dt).t()                  # exact: a power-of-two scale
+    assert torch.equal(D.cpu(), want)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fp8", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("shape", ["T1", "T2-k8", "T8", "C3-T1", "C2-T1", "rowmajor-T2",
+                                   "k-tail-T2"])
+def test_fused_moe_fp8_per_expert_decode_reads_fp8(dev, monkeypatch, dt, fp8, shape):
+    """Decode-sized per-expert fp8 layers read the fp8 weights themselves
+    (converted exactly in registers; no 16-bit copies are made): every
+    element within the reference's bar of the oracle (bf16 2e-2, fp16
+    1e-2) and of the 16-bit-copy path (MI355MOE_FP8_W8A16=0).  Shapes:
+    split-K and self-sorting w13 (T1), 16 slots (T2-k8), C3's token-major
+    w2 (C3-T1, H = 7168), C2's w2 rebuilding its rows from the w13 partials
+    (C2-T1), row-major weights (H = 1056, I = 544: the last K stage one
+    32-value chunk); with H = 1000 (not % 32) the layer runs on the copies."""
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    g = torch.Generator().manual_seed(11)
+    E, H, I, T, topk = 16, 1024, 512, 1, 2
+    if shape == "T2-k8":
+        T, topk = 2, 8
+    elif shape == "T8":
+        T = 8
+    elif shape == "C3-T1":
+        E, H, I, topk = 8, 7168, 2048, 8
+    elif shape == "C2-T1":
+        E, H, I, topk = 16, 2048, 768, 8
+    elif shape == "rowmajor-T2":
+        H, I, T = 1056, 544, 2
+    elif shape == "k-tail-T2":
+        H, I, T = 1000, 520, 2
+    q13, s13 = _fp8_expert_weights(E, 2 * I, H, fp8, g)
+    q2, s2 = _fp8_expert_weights(E, H, I, fp8, g)
+    b13 = (torch.randn(E, 2 * I, generator=g) / 16).to(dt)
+    b2 = (torch.randn(E, H, generator=g) / 16).to(dt)
+    x = (torch.randn(T, H, generator=g) / 16).to(dt)
+    tw, ti = torch.topk(torch.randn(T, E, generator=g), k=topk, dim=-1, sorted=False)
+    moe = XpuFusedMoe(q13.transpose(1, 2).contiguous().to(dev), s13.to(dev), b13.to(dev),
+                      q2.transpose(1, 2).contiguous().to(dev), s2.to(dev), b2.to(dev),
+                      topk, "silu", E)
+    native = shape != "k-tail-T2"
+    assert (moe._w8_recipe is not None) == native
+    if native:
+        assert moe._w8_layout == (0 if shape == "rowmajor-T2" else 1)
+    xd, twd, tid = x.to(dev), tw.to(dev), ti.to(dev)
+    out = torch.full((T, H), float("nan"), dtype=dt, device=dev)
+    moe.apply(out, xd, twd, tid)
+    torch.cuda.synchronize()
+    assert bool(moe._w16_cache) != native         # copies only where the layer needs them
+    monkeypatch.setenv("MI355MOE_FP8_W8A16", "0")
+    ref16 = torch.full_like(out, float("nan"))
+    moe.apply(ref16, xd, twd, tid)
+    ref = O.fused_moe("fp8", x, q13, s13, b13, q2, s2, b2, tw, ti)
+    tol = 2e-2 if dt == torch.bfloat16 else 1e-2
+    torch.testing.assert_close(out.cpu(), ref, rtol=tol, atol=tol)
+    torch.testing.assert_close(out, ref16, rtol=tol, atol=tol)
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("grp", [128, 32])
 @pytest.mark.parametrize("has_bias", [False, True])

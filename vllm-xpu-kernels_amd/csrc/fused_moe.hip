@@ -618,6 +618,16 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   } else if (recipe == MI355MOE_RECIPE_MXFP8) {
     MI_ARG(H % 32 == 0 && I % 32 == 0, "mxfp8 weights need hidden and intermediate sizes % 32 == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "mxfp8 weights need e8m0 scales");
+  } else if (is_w8a16_recipe(recipe)) {
+    MI_CHECK(H % 32 == 0 && act_width(a) % 32 == 0, MI355MOE_ERR_UNSUPPORTED,
+             "per-expert fp8 weights need hidden and intermediate sizes % 32 == 0 (others "
+             "run on 16-bit copies, recipe BF16)");
+    MI_ARG(a->w13_scale && a->w2_scale, "per-expert fp8 weights need f32 scales [E]");
+    // the decode kernels read them (the layout plan picks STREAM for these)
+    const int64_t slots = T * k, active = std::min<int64_t>(slots, E);
+    MI_CHECK(active == 0 || slots / active <= kStreamMaxAvg16, MI355MOE_ERR_UNSUPPORTED,
+             "per-expert fp8 weights: at most 10 slots per active expert on average "
+             "(larger layers run on 16-bit copies, recipe BF16)");
   } else {
     MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
     MI_ARG(H % 8 == 0 && I % 8 == 0, "bf16 weights need K % 8 == 0");
@@ -628,10 +638,11 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   MI_ARG(!kblock || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0) ||
              (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && act_width(a) <= 8192) ||
              (recipe == MI355MOE_RECIPE_MXFP8 && H % 128 == 0 && act_width(a) % 128 == 0) ||
+             (is_w8a16_recipe(recipe) && H % 128 == 0 && act_width(a) % 128 == 0) ||
              recipe == MI355MOE_RECIPE_MXFP4,
          "K-blocked weights need the bf16 recipe (hidden and intermediate sizes "
-         "% 32 == 0), the fp8block recipe (sizes at most 8192), mxfp8 (sizes % 128 "
-         "== 0) or mxfp4");
+         "% 32 == 0), the fp8block recipe (sizes at most 8192), mxfp8 or per-expert "
+         "fp8 (sizes % 128 == 0) or mxfp4");
   MI_ARG(!mx_layer(a) || epilogue_act(a->activation),
          "mxfp8 and pre-quantised mxfp4 layers support the silu and swigluoai activations");
   if (T == 0) return MI355MOE_OK;
@@ -745,8 +756,9 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.w_kblock = kblock;
   g1.out_f16 = f16;
   g1.w_group = static_cast<int32_t>(a->w_group);
-  g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w13_scale)
-                                                    : nullptr;
+  g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 || is_w8a16_recipe(recipe)
+                        ? static_cast<const float*>(a->w13_scale)
+                        : nullptr;
   if (self_sort) {
     g1.sr_ids = a->topk_ids;
     g1.sr_ids_dtype = a->ids_dtype;
@@ -821,8 +833,9 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.w_kblock = kblock;
   g2.out_f16 = f16;
   g2.w_group = static_cast<int32_t>(a->w_group);
-  g2.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(a->w2_scale)
-                                                    : nullptr;
+  g2.expert_scale = recipe == MI355MOE_RECIPE_BF16 || is_w8a16_recipe(recipe)
+                        ? static_cast<const float*>(a->w2_scale)
+                        : nullptr;
   if (w2_finishes_w13) {
     g2.g1f.part = L.part1;
     g2.g1f.ks = L.ks1;
@@ -970,6 +983,14 @@ int grouped_gemm_impl(int recipe, const void* A, int a_dtype, const float* a_sca
            "mxfp4 activations must be bfloat16 or float16");
     MI_ARG(out_dtype == a_dtype, "mxfp4: the output must have the activation dtype");
     MI_ARG(b_scale != nullptr, "mxfp4 needs e8m0 scales");
+  } else if (is_w8a16_recipe(recipe)) {
+    // row-major [E, N, K] e4m3 / e5m2 weights, f32 scales [E]; the STREAM
+    // kernels at any M
+    MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
+           "per-expert fp8 weights need bfloat16 or float16 activations");
+    MI_ARG(out_dtype == a_dtype, "per-expert fp8: the output must have the activation dtype");
+    MI_CHECK(K % 32 == 0, MI355MOE_ERR_UNSUPPORTED, "per-expert fp8 weights need K % 32 == 0");
+    MI_ARG(b_scale != nullptr, "per-expert fp8 weights need f32 scales [E]");
   } else {
     MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");
     MI_ARG(a_dtype == MI355MOE_BF16 || a_dtype == MI355MOE_F16,
@@ -1012,7 +1033,9 @@ int grouped_gemm_impl(int recipe, const void* A, int a_dtype, const float* a_sca
   g.K = K;
   g.ldb_rows = N;
   g.out_f16 = out_dtype == MI355MOE_F16;
-  g.expert_scale = recipe == MI355MOE_RECIPE_BF16 ? static_cast<const float*>(b_scale) : nullptr;
+  g.expert_scale = recipe == MI355MOE_RECIPE_BF16 || is_w8a16_recipe(recipe)
+                       ? static_cast<const float*>(b_scale)
+                       : nullptr;
   g.w_group = static_cast<int32_t>(w_group);
   return launch_tile_gemm(L.tile, L.bm, recipe, EPI_STORE, false, g, L.grid_blocks, nullptr, st);
 }

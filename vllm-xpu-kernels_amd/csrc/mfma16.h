@@ -69,6 +69,27 @@ __device__ __forceinline__ uint4 fp4x8_to16(uint32_t w, float sc) {
   return r;
 }
 
+// 8 fp8 codes (byte t = value t; e4m3, or e5m2 with E5M2) -> 8 16-bit
+// values, exactly: every e4m3 and e5m2 value is a bf16 and an fp16 value,
+// and the scale is 1 (v_cvt_scalef32_pk_{bf16,f16}_{fp8,bf8}, one 16-bit
+// half of the source word per instruction).
+template <bool E5M2, bool F16, bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to16(uint32_t v) {
+  if constexpr (E5M2 && F16)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(v, 1.0f, HI));
+  else if constexpr (E5M2)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v, 1.0f, HI));
+  else if constexpr (F16)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 1.0f, HI));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, HI));
+}
+template <bool E5M2, bool F16>
+__device__ __forceinline__ uint4 fp8x8_to16(uint2 w) {
+  return make_uint4(fp8x2_to16<E5M2, F16, false>(w.x), fp8x2_to16<E5M2, F16, true>(w.x),
+                    fp8x2_to16<E5M2, F16, false>(w.y), fp8x2_to16<E5M2, F16, true>(w.y));
+}
+
 // 8 signed int4 values (two's-complement nibbles, value t in bits 4t..4t+3)
 // -> 8 16-bit values T(v * scale), the reference's dequantisation
 // (gemm_xe2.hpp:455-470: the 16-bit weight times its 16-bit group scale).

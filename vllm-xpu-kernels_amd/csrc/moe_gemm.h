@@ -16,10 +16,18 @@ namespace mi355 {
 // Recipe codes of the grouped-GEMM kernels beyond the C ABI's: e2m1
 // activations with e8m0 scales against mxfp4 weights (both scales in the
 // MFMA), which the fused layer runs for mxfp4 with pre-quantised inputs.
-constexpr int RECIPE_MX4A4 = 5;
+constexpr int RECIPE_MX4A4 = 16;
 __host__ __device__ constexpr bool is_mx_recipe(int r) {
   return r == MI355MOE_RECIPE_MXFP8 || r == RECIPE_MX4A4;
 }
+// Per-expert fp8 weights (e4m3 or e5m2) against 16-bit activations: the
+// STREAM kernels convert them to the activations' type as they load them.
+__host__ __device__ constexpr bool is_w8a16_recipe(int r) {
+  return r == MI355MOE_RECIPE_FP8 || r == MI355MOE_RECIPE_FP8E5M2;
+}
+// 16-bit (and w8a16) weights: layers averaging at most this many slots per
+// active expert run the STREAM kernels
+constexpr int64_t kStreamMaxAvg16 = 10;
 
 // The split-K w13 GEMM of the fused layer left its partial tiles (no
 // finalize launch); the STREAM w2 launch rebuilds each workgroup's 16-bit

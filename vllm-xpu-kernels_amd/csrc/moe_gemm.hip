@@ -492,7 +492,7 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     // expert on (16-slot STREAM blocks would stream an expert's weights once
     // per block)
     t = TILE_WIDE, b = kWideBM;
-  } else if (is_mx_recipe(recipe)) {
+  } else if (is_mx_recipe(recipe) || is_w8a16_recipe(recipe)) {
     t = TILE_STREAM, b = 16;
   } else if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
     // a 320-slot fp8 stage is 73 KB, so the WIDE kernel keeps one stage of
@@ -512,12 +512,12 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     else if (wide_ok) t = TILE_WIDE, b = kWideBM;
     else t = TILE_BIG, b = 128;
   } else {
-    if (avg <= 10) t = TILE_STREAM, b = 16;
+    if (avg <= kStreamMaxAvg16) t = TILE_STREAM, b = 16;
     else if (avg <= 48 || (!wide_ok && avg <= 96)) t = TILE_SMALL, b = 64;
     else if (wide_ok) t = TILE_WIDE, b = kWideBM;
     else t = TILE_BIG, b = 128;
   }
-  if (force >= 0 && !is_mx_recipe(recipe)) {
+  if (force >= 0 && !is_mx_recipe(recipe) && !is_w8a16_recipe(recipe)) {
     t = static_cast<GemmTile>(force);
     if (t == TILE_WIDE && !wide_ok) t = TILE_BIG;
     b = t == TILE_STREAM ? 16
@@ -538,11 +538,14 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
              (recipe == MI355MOE_RECIPE_FP8BLOCK &&
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
                (tile == TILE_BIG && big8_supported(recipe, a)))) ||
-             recipe == MI355MOE_RECIPE_MXFP4 || is_mx_recipe(recipe),
-         "K-blocked weights need the bf16 (K % 32 == 0), fp8block, mxfp4 or mxfp8 "
-         "recipe and a kernel family that reads them");
+             recipe == MI355MOE_RECIPE_MXFP4 || is_mx_recipe(recipe) ||
+             (is_w8a16_recipe(recipe) && a.K % 128 == 0),
+         "K-blocked weights need the bf16 (K % 32 == 0), fp8block, mxfp4, mxfp8 or "
+         "per-expert fp8 (K % 128 == 0) recipe and a kernel family that reads them");
   MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM || tile == TILE_WIDE,
          "MX recipes run the STREAM and WIDE kernels");
+  MI_CHECK(!is_w8a16_recipe(recipe) || tile == TILE_STREAM, MI355MOE_ERR_UNSUPPORTED,
+           "per-expert fp8 weights run the decode (STREAM) kernels only");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:

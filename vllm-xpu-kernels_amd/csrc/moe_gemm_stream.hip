@@ -50,6 +50,13 @@ struct Frag<MI355MOE_RECIPE_BF16> {      // 4 MFMA steps x 8 bf16
   uint4 x[4];
 };
 template <>
+struct Frag<MI355MOE_RECIPE_FP8> {       // 32 fp8 of the weight row (K 32q..32q+31
+  uint4 w[2][2];                         // of the stage), 4 MFMA steps x 8 16-bit
+  uint4 x[4];                            // activations of the same K
+};
+template <>
+struct Frag<MI355MOE_RECIPE_FP8E5M2> : Frag<MI355MOE_RECIPE_FP8> {};
+template <>
 struct Frag<MI355MOE_RECIPE_MXFP4> {     // 32 e2m1 + e8m0 of the weight row
   uint4 w[2];
   uint32_t sc[2];                        // scale codes (w4_scale_code)
@@ -170,6 +177,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   constexpr bool kMx8 = RECIPE == MI355MOE_RECIPE_MXFP8;
   constexpr bool kMx4 = RECIPE == RECIPE_MX4A4;
   constexpr bool kMx = kMx8 || kMx4;
+  constexpr bool kW8 = is_w8a16_recipe(RECIPE);  // fp8 weights, 16-bit activations
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int XB = (kFp8 || kMx8) ? 1 : 2;  // bytes per activation element (mx4: packed)
 
@@ -218,7 +226,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const int64_t col0 =
       TOKM ? (static_cast<int64_t>(blockIdx.x) * (WAVES / a.topk) + wave / a.topk) * 32
            : static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) + wave * (kGlu ? 16 : 32);
-  const int64_t wrow_bytes = (kFp4 || kMx4) ? K / 2 : K * XB;
+  const int64_t wrow_bytes = (kFp4 || kMx4) ? K / 2 : (kW8 ? K : K * XB);
   const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
                         static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
   int64_t wrow[2];
@@ -230,7 +238,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
   }
   // weights (and mxfp4 scales) may be K-blocked
-  const WStride wst = (kFp4 || kMx4) ? w_stride4(a) : ((kFp8 || kMx8) ? w_stride8(a) : w_stride16(a));
+  const WStride wst = (kFp4 || kMx4) ? w_stride4(a)
+                                     : ((kFp8 || kMx8 || kW8) ? w_stride8(a) : w_stride16(a));
   const WStride sst = s_stride4(a);
   const uint8_t* wp0 = wexp + wrow[0] * wst.row;
   const uint8_t* wp1 = wexp + wrow[1] * wst.row;
@@ -318,6 +327,19 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
         f.xs = a.a_scale[xsrow + k0 / 128];
       }
+    } else if constexpr (kW8) {  // K % 32 == 0: a lane's 32 K values lie in or past K
+      const int64_t k = k0 + 32 * q;
+      const int64_t kc = k < K ? k : K - 32;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint8_t* p = (t ? wp1 : wp0) + (kc >> 7) * wst.kblk + (kc & 127);
+        f.w[t][0] = *reinterpret_cast<const uint4*>(p);
+        f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        f.x[s] = XL ? *reinterpret_cast<const uint4*>(s_xa + l16 * xrs + (kc - kx0) + 8 * s)
+                    : *reinterpret_cast<const uint4*>(xp + (kc + 8 * s) * 2);
     } else if constexpr (kFp4) {  // K % 32 == 0
       const int64_t k = k0 + 32 * q;
       const int64_t kc = k < K ? k : K - 32;
@@ -357,6 +379,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
           f.w[0] = f.w[1] = z4;
           f.sc[0] = f.sc[1] = 0u;
         }
+      } else if constexpr (kW8) {
+        if (k0 + 32 * q >= K) f.w[0][0] = f.w[0][1] = f.w[1][0] = f.w[1][1] = z4;
       } else if constexpr (!kFp8 && !kMx) {
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
@@ -394,6 +418,16 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.y, c), f.x[1], acc[t]);
         acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.z, c), f.x[2], acc[t]);
         acc[t] = mfma16_16x16x32<F16>(w4_decode8<RECIPE, F16>(w.w, c), f.x[3], acc[t]);
+      }
+    } else if constexpr (kW8) {
+      constexpr bool k52 = RECIPE == MI355MOE_RECIPE_FP8E5M2;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 a0 = f.w[t][0], a1 = f.w[t][1];
+        acc[t] = mfma16_16x16x32<F16>(fp8x8_to16<k52, F16>(make_uint2(a0.x, a0.y)), f.x[0], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp8x8_to16<k52, F16>(make_uint2(a0.z, a0.w)), f.x[1], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp8x8_to16<k52, F16>(make_uint2(a1.x, a1.y)), f.x[2], acc[t]);
+        acc[t] = mfma16_16x16x32<F16>(fp8x8_to16<k52, F16>(make_uint2(a1.z, a1.w)), f.x[3], acc[t]);
       }
     } else {
 #pragma unroll
@@ -745,6 +779,12 @@ int launch_moe_gemm_stream(int recipe, int epi, bool qout, const GemmArgs& a,
     case MI355MOE_RECIPE_MXFP8:
       return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_MXFP8, EPI_GLU, false>(a, max_blocks, qs, st)
                             : launch_stream<MI355MOE_RECIPE_MXFP8, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_FP8:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_FP8, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_FP8, EPI_STORE, false>(a, max_blocks, qs, st);
+    case MI355MOE_RECIPE_FP8E5M2:
+      return epi == EPI_GLU ? launch_stream<MI355MOE_RECIPE_FP8E5M2, EPI_GLU, false>(a, max_blocks, qs, st)
+                            : launch_stream<MI355MOE_RECIPE_FP8E5M2, EPI_STORE, false>(a, max_blocks, qs, st);
     case RECIPE_MX4A4:
       return epi == EPI_GLU ? launch_stream<RECIPE_MX4A4, EPI_GLU, false>(a, max_blocks, qs, st)
                             : launch_stream<RECIPE_MX4A4, EPI_STORE, false>(a, max_blocks, qs, st);

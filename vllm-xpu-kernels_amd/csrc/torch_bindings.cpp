@@ -855,6 +855,16 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   check_gpu(topk_ids, "topk_ids");
   check_gpu(w13, "w13");
   check_gpu(w2, "w2");
+  if (recipe == MI355MOE_RECIPE_FP8 || recipe == MI355MOE_RECIPE_FP8E5M2) {
+    const auto wt = recipe == MI355MOE_RECIPE_FP8 ? at::kFloat8_e4m3fn : at::kFloat8_e5m2;
+    TORCH_CHECK(w13.scalar_type() == wt && w2.scalar_type() == wt,
+                "per-expert fp8 weights must be float8_e4m3fn (recipe 5) or float8_e5m2 "
+                "(recipe 6)");
+    TORCH_CHECK(w13_scale && w2_scale && w13_scale->scalar_type() == at::kFloat &&
+                    w2_scale->scalar_type() == at::kFloat &&
+                    w13_scale->numel() == w13.size(0) && w2_scale->numel() == w2.size(0),
+                "per-expert fp8 weights need float32 scales [num_experts]");
+  }
   TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
   TORCH_CHECK(topk_weights.sizes() == topk_ids.sizes(),
               "topk_weights must have the shape of topk_ids");

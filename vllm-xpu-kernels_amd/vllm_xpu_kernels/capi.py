@@ -94,11 +94,12 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     after conversion: f32 for fp8block, e8m0 bytes for mxfp8 / mxfp4, whose
     hidden_states are then packed e2m1 bytes [T, H/2])."""
     a = FusedMoeArgs()
-    a.recipe = moe._recipe
+    recipe, w13, w2, layout = moe._call_plan(hidden_states.dtype, hidden_states.shape[0],
+                                             topk_ids.shape[1])
+    a.recipe = recipe
     a.activation = moe._act
     a.act_dtype = F16 if output.dtype == torch.float16 else BF16
     b13, b2 = moe._biases(output.dtype)
-    w13, w2 = moe._call_weights(hidden_states.dtype)
     s13, s2 = moe._scales(hidden_states.dtype)
     a.ids_dtype = I64 if topk_ids.dtype == torch.int64 else I32
     a.num_tokens, a.hidden = hidden_states.shape
@@ -124,7 +125,7 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.swiglu_alpha = 1.702
     a.swiglu_limit = 7.0
     a.output = output.data_ptr()
-    a.w_layout = moe._w_layout
+    a.w_layout = layout
     a.w_group = moe._w_group
     return a
 

@@ -28,6 +28,14 @@ USE_MXFP4_FP8_ENV = "VLLM_XPU_FUSED_MOE_USE_MXFP4_FP8"
 FP8_BLOCK_SIZE = 128
 
 RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4, RECIPE_INT4, RECIPE_MXFP8 = 0, 1, 2, 3, 4
+# per-expert fp8 weights read as they are (e4m3 / e5m2, converted in registers)
+RECIPE_FP8, RECIPE_FP8E5M2 = 5, 6
+# Layers averaging at most this many slots per active expert run the decode
+# (STREAM) kernels (moe_gemm.hip pick_tile, kStreamMaxAvg16): per-expert fp8
+# calls in that range read the fp8 weights; larger ones run on exact 16-bit
+# copies, made on the first such call.  "0" always uses the copies.
+FP8_W8A16_ENV = "MI355MOE_FP8_W8A16"
+STREAM_MAX_AVG_SLOTS = 10
 ACT_SILU, ACT_SWIGLUOAI, ACT_GELU, ACT_GELU_TANH, ACT_SWIGLUSTEP, ACT_RELU2 = range(6)
 # reference fused_moe_interface.py:119-133, 239-254
 _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
@@ -220,7 +228,9 @@ class XpuFusedMoe:
             if (K2 // s2c.shape[-1]) != self._w_group:
                 raise ValueError("w13 and w2 int4 scales must use one group size")
         elif self._fp8_expert:
-            # reference layout [E, K, N] (as 16-bit) -> [E, N, K], kept in fp8
+            # reference layout [E, K, N] -> [E, N, K], kept in fp8 (read as
+            # such by the decode kernels, K-blocked by 128 where the sizes
+            # allow; exact 16-bit copies are made for larger calls)
             w13c = w13.transpose(1, 2).contiguous()
             w2c = w2.transpose(1, 2).contiguous()
             s13c = s13.to(torch.float32).reshape(E).contiguous()
@@ -279,20 +289,55 @@ class XpuFusedMoe:
             self._w_layout = WLAYOUT_KBLOCK
         if self._fp8_expert and self._kblock:
             self._w_layout = WLAYOUT_KBLOCK   # applies to the 16-bit copies
+        self._w8_recipe = None
+        self._w8_layout = WLAYOUT_NK
+        if self._fp8_expert and H % 32 == 0 and K2 % 32 == 0:
+            self._w8_recipe = (RECIPE_FP8E5M2 if w13c.dtype == torch.float8_e5m2
+                               else RECIPE_FP8)
+            if (H % FP8_BLOCK_SIZE == 0 and K2 % FP8_BLOCK_SIZE == 0 and
+                    os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk"):
+                # K blocks of 128 bytes (the packing moves bytes; e5m2 goes
+                # through an e4m3 view)
+                e4 = torch.float8_e4m3fn
+                w13c = pack_weights_kblock(w13c.view(e4)).view(w13c.dtype)
+                w2c = pack_weights_kblock(w2c.view(e4)).view(w2c.dtype)
+                self._w8_layout = WLAYOUT_KBLOCK
         self._w16_cache = {}
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
         self.w13_bias, self.w2_bias = b13c, b2c
         self._bias_cache = {}
 
+    def _fp8_rows(self, w):
+        """[E, N, K] view of kept per-expert fp8 weights."""
+        if self._w8_layout != WLAYOUT_KBLOCK:
+            return w
+        E, KB, N, B = w.shape
+        return w.permute(0, 2, 1, 3).reshape(E, N, KB * B)
+
+    def _call_plan(self, dtype, num_tokens, topk):
+        """(recipe, w13, w2, weight layout) of a call in `dtype` with
+        num_tokens x topk slots: per-expert fp8 weights are read as they
+        are by decode-sized calls (the C ABI's rule, at most
+        STREAM_MAX_AVG_SLOTS slots per active expert) and through exact
+        16-bit copies otherwise."""
+        if self._w8_recipe is not None and _is_env_enabled(FP8_W8A16_ENV, "1"):
+            slots = num_tokens * topk
+            active = min(slots, self.w13.shape[0])
+            if active == 0 or slots // active <= STREAM_MAX_AVG_SLOTS:
+                return self._w8_recipe, self.w13, self.w2, self._w8_layout
+        w13, w2 = self._call_weights(dtype)
+        return self._recipe, w13, w2, self._w_layout
+
     def _call_weights(self, dtype):
-        """(w13, w2) the kernels read for a call in `dtype`: the prepared
-        weights, or for per-expert fp8 their exact 16-bit copies (made
-        once per dtype, K-blocked like 16-bit weights)."""
+        """(w13, w2) the 16-bit-recipe kernels read for a call in `dtype`:
+        the prepared weights, or for per-expert fp8 their exact 16-bit copies
+        (made once per dtype, K-blocked like 16-bit weights)."""
         if not self._fp8_expert:
             return self.w13, self.w2
         if dtype not in self._w16_cache:
-            w13, w2 = self.w13.to(dtype), self.w2.to(dtype)
+            w13 = self._fp8_rows(self.w13).to(dtype)
+            w2 = self._fp8_rows(self.w2).to(dtype)
             if self._kblock:
                 w13, w2 = pack_weights_kblock(w13), pack_weights_kblock(w2)
             self._w16_cache[dtype] = (w13.contiguous(), w2.contiguous())
@@ -366,13 +411,14 @@ class XpuFusedMoe:
             # clamp limit (fused_moe_interface.py:27-30, 296-317)
             clamp = 0.0
         b13, b2 = self._biases(dt16)
-        w13, w2 = self._call_weights(dt16)
+        recipe, w13, w2, layout = self._call_plan(dt16, hidden_states.shape[0],
+                                                  topk_ids.shape[-1])
         s13, s2 = self._scales(dt16)
         torch.ops._moe_C.mi355_fused_moe(
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
             topk_ids.contiguous(), w13, s13, b13, w2, s2, b2,
-            self._recipe, self._act, self.inter_size, clamp, expert_map,
-            self._w_layout, a1q_scale, self._w_group)
+            recipe, self._act, self.inter_size, clamp, expert_map,
+            layout, a1q_scale, self._w_group)
         return output
 
 

@@ -25,7 +25,7 @@ class MoeConfig:
     inter: int
     experts: int
     topk: int
-    recipe: str                 # "bf16" | "fp8block" | "mxfp4" | "mxfp8"
+    recipe: str                 # "bf16" | "fp8block" | "mxfp4" | "mxfp8" | "fp8"
     routing: str                # "softmax" | "grouped_sigmoid"
     activation: str = "silu"
     renormalize: bool = True
@@ -59,10 +59,12 @@ CONFIGS = {
 
 
 # Recipe variants on the same shapes (not BASELINE configurations): DeepSeek-V3
-# with mxfp8 weights, gpt-oss-20b with pre-quantised mxfp4 input (both GEMMs
-# e2m1 x e2m1).
+# with mxfp8 weights or per-expert-scaled e4m3 weights (the reference's
+# recipe "fp8", w8a16), gpt-oss-20b with pre-quantised mxfp4 input (both
+# GEMMs e2m1 x e2m1).
 VARIANTS = {
     "C3-mxfp8": replace(CONFIGS["C3"], recipe="mxfp8"),
+    "C3-fp8": replace(CONFIGS["C3"], recipe="fp8"),
     "C5-w4a4": replace(CONFIGS["C5"], prequant=True),
 }
 
@@ -163,6 +165,10 @@ def expert_weights_nk(cfg: MoeConfig, e: int, device, seed: int = 0):
         q13, s13 = mxfp8_quant(w13)
         q2, s2 = mxfp8_quant(w2)
         return q13, s13, q2, s2
+    if cfg.recipe == "fp8":   # one scale per expert and matrix: amax / 448
+        s13, s2 = w13.abs().amax() / 448.0, w2.abs().amax() / 448.0
+        return ((w13 / s13).to(torch.float8_e4m3fn), s13, (w2 / s2).to(torch.float8_e4m3fn),
+                s2)
     q13, s13 = mxfp4_quant(w13)
     q2, s2 = mxfp4_quant(w2)
     return q13, s13, q2, s2
@@ -188,6 +194,13 @@ def make_weights(cfg: MoeConfig, device, seed: int = 0) -> MoeWeights:
         w2 = torch.empty(E, H, K2, dtype=torch.float8_e4m3fn, device=device)
         s13 = torch.empty(E, 2 * I // 128, H // 128, device=device)
         s2 = torch.empty(E, H // 128, K2 // 128, device=device)
+    elif cfg.recipe == "fp8":
+        # reference layout [E, K, N] e4m3 + f32 [E] (its per-expert fp8 test,
+        # tests/fused_moe/test_fused_moe.py:226-246)
+        w13 = torch.empty(E, H, 2 * I, dtype=torch.float8_e4m3fn, device=device)
+        w2 = torch.empty(E, K2, H, dtype=torch.float8_e4m3fn, device=device)
+        s13 = torch.empty(E, device=device)
+        s2 = torch.empty(E, device=device)
     elif cfg.recipe == "mxfp8":
         # reference layout (moe_utils.py:80-82): [E, K, N] + e8m0 [E, K/32, N]
         w13 = torch.empty(E, H, 2 * I, dtype=torch.float8_e4m3fn, device=device)
@@ -204,6 +217,11 @@ def make_weights(cfg: MoeConfig, device, seed: int = 0) -> MoeWeights:
         if cfg.recipe == "bf16":
             w13[e].copy_(a.t())   # reference bf16 layout [E, K, N]
             w2[e].copy_(b.t())
+        elif cfg.recipe == "fp8":
+            w13[e].copy_(a.t())
+            w2[e].copy_(b.t())
+            s13[e] = sa
+            s2[e] = sb
         elif cfg.recipe == "mxfp8":
             w13[e].copy_(a.t())
             w2[e].copy_(b.t())
@@ -265,6 +283,8 @@ def algorithmic_bytes(cfg: MoeConfig, T: int, active: int) -> float:
         wb = n + 4 * n / (128 * 128)
     elif cfg.recipe == "mxfp8":
         wb = n + n / 32
+    elif cfg.recipe == "fp8":
+        wb = n + 8
     else:
         wb = n / 2 + n / 32
     if cfg.bias:
@@ -277,7 +297,8 @@ def algorithmic_flops(cfg: MoeConfig, T: int) -> float:
     return 6.0 * T * cfg.topk * cfg.hidden * cfg.inter
 
 
-PEAK_TFLOPS = {"bf16": 2500.0, "fp8block": 5000.0, "mxfp4": 2500.0, "mxfp8": 5000.0}
+PEAK_TFLOPS = {"bf16": 2500.0, "fp8block": 5000.0, "mxfp4": 2500.0, "mxfp8": 5000.0,
+               "fp8": 2500.0}   # per-expert fp8 runs 16-bit MFMAs (w8a16)
 PEAK_TFLOPS_FP4 = 10100.0   # e2m1 x e2m1 (pre-quantised mxfp4 input)
 PEAK_HBM_GBS = 8000.0
 
