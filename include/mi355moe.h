@@ -79,12 +79,12 @@ typedef enum {
                                    converted exactly to the activations'
                                    type as it is loaded and the expert's
                                    scale multiplies the accumulators.
-                                   Decode kernels only: layers averaging
-                                   more than 10 slots per active expert,
-                                   or with hidden or intermediate sizes not
-                                   % 32, return MI355MOE_ERR_UNSUPPORTED
-                                   (run them as RECIPE_BF16 on exact 16-bit
-                                   copies)                                */
+                                   STREAM and SMALL kernels only: layers
+                                   averaging more than 48 slots per active
+                                   expert, or with hidden or intermediate
+                                   sizes not % 32, return
+                                   MI355MOE_ERR_UNSUPPORTED (run them as
+                                   RECIPE_BF16 on exact 16-bit copies)    */
   MI355MOE_RECIPE_FP8E5M2 = 6   /* as RECIPE_FP8 with e5m2 weights        */
 } mi355moe_recipe;
 
@@ -404,8 +404,8 @@ int mi355moe_silu_and_mul_mxfp4_quant(uint8_t* out, const void* input, int in_dt
  *                    [E,N,K/32]
  *   recipe FP8 / FP8E5M2: A bf16 or f16 [M,K]; B e4m3 / e5m2 [E,N,K]
  *                    (K % 32 == 0) + b_scale f32 [E]: the weights read as
- *                    fp8 and converted exactly to a_dtype, the STREAM
- *                    kernels at any M
+ *                    fp8 and converted exactly to a_dtype, the STREAM or
+ *                    SMALL kernels at any M
  * bias: optional [E,N] in out_dtype; D [M,N] bf16 or f16 (out_dtype; equal
  * to a_dtype for recipes BF16, MXFP4, FP8 and FP8E5M2). */
 size_t mi355moe_grouped_gemm_workspace_size(int64_t total_rows,

@@ -623,10 +623,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
              "per-expert fp8 weights need hidden and intermediate sizes % 32 == 0 (others "
              "run on 16-bit copies, recipe BF16)");
     MI_ARG(a->w13_scale && a->w2_scale, "per-expert fp8 weights need f32 scales [E]");
-    // the decode kernels read them (the layout plan picks STREAM for these)
+    // the STREAM and SMALL kernels read them
     const int64_t slots = T * k, active = std::min<int64_t>(slots, E);
-    MI_CHECK(active == 0 || slots / active <= kStreamMaxAvg16, MI355MOE_ERR_UNSUPPORTED,
-             "per-expert fp8 weights: at most 10 slots per active expert on average "
+    MI_CHECK(active == 0 || slots / active <= kSmallMaxAvg16, MI355MOE_ERR_UNSUPPORTED,
+             "per-expert fp8 weights: at most 48 slots per active expert on average "
              "(larger layers run on 16-bit copies, recipe BF16)");
   } else {
     MI_ARG(recipe == MI355MOE_RECIPE_BF16, "unknown recipe");

@@ -26,8 +26,10 @@ __host__ __device__ constexpr bool is_w8a16_recipe(int r) {
   return r == MI355MOE_RECIPE_FP8 || r == MI355MOE_RECIPE_FP8E5M2;
 }
 // 16-bit (and w8a16) weights: layers averaging at most this many slots per
-// active expert run the STREAM kernels
+// active expert run the STREAM kernels, up to kSmallMaxAvg16 the 64-slot
+// SMALL kernels (w8a16 layers beyond that are not taken)
 constexpr int64_t kStreamMaxAvg16 = 10;
+constexpr int64_t kSmallMaxAvg16 = 48;
 
 // The split-K w13 GEMM of the fused layer left its partial tiles (no
 // finalize launch); the STREAM w2 launch rebuilds each workgroup's 16-bit

@@ -61,6 +61,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
     const GemmArgs a, void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
   constexpr bool kFp4 = RECIPE == MI355MOE_RECIPE_MXFP4 || RECIPE == MI355MOE_RECIPE_INT4;
+  constexpr bool kW8 = is_w8a16_recipe(RECIPE);  // fp8 weights, 16-bit activations
   constexpr int XB = kFp8 ? 1 : 2;      // bytes per activation element
   constexpr int ROWB = KB * XB + 16;    // padded LDS row pitch (bytes)
   constexpr int CPR = KB * XB / 16;     // 16-byte chunks per staged row
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
   if (blk * BM >= *a.ntp) return;  // uniform for the workgroup
   const int e = a.block_expert[blk];
   const int64_t K = a.K;
-  const int64_t wrow_bytes = kFp4 ? K / 2 : K * XB;
+  const int64_t wrow_bytes = kFp4 ? K / 2 : (kW8 ? K : K * XB);
 
   if (tid < BM) {
     const int rid = a.row_ids[static_cast<int64_t>(blk) * BM + tid];
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
   const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
   // weights (and mxfp4 scales) may be K-blocked
-  const WStride wst = kFp4 ? w_stride4(a) : (kFp8 ? w_stride8(a) : w_stride16(a));
+  const WStride wst = kFp4 ? w_stride4(a) : (kFp8 || kW8 ? w_stride8(a) : w_stride16(a));
   const WStride sst = s_stride4(a);
   const uint8_t* wptr[NB];
   bool wok[NB];
@@ -225,7 +226,8 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
     for (int64_t k0 = 0; k0 < K; k0 += KB) {
       const int kb = static_cast<int>(K - k0 < KB ? K - k0 : KB);
       // ---- weight fragments: HBM -> VGPR
-      uint4 wf[KS][NB][kFp8 ? 2 : 1];
+      // (fp8 weights: the lane's 32 K values 32q..32q+31 of the stage)
+      uint4 wf[kW8 ? 1 : KS][NB][kFp8 || kW8 ? 2 : 1];
       float wsc[NB];
   #pragma unroll
       for (int j = 0; j < NB; ++j) {
@@ -236,6 +238,11 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
           const float* bs = static_cast<const float*>(a.b_scale);
           wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wrow[j] / 128) *
                           (K / 128) + k0 / 128];
+        } else if constexpr (kW8) {  // K % 32 == 0: a chunk lies wholly in or past K
+          const int64_t kc = k0 + 32 * q < K ? k0 + 32 * q : K - 32;
+          const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (kc >> 7) * wst.kblk + (kc & 127));
+          wf[0][j][0] = kBatchX || wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
+          wf[0][j][1] = kBatchX || wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
         } else {
   #pragma unroll
           for (int s = 0; s < KS; ++s) {
@@ -310,6 +317,22 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
             f32x4 p = mfma_fp8(wf[0][j][0], wf[0][j][1], x0, x1);
             const float sc = xs * wsc[j];
             acc[mt][j] += p * sc;
+          }
+        } else if constexpr (kW8) {
+          // the activation in the weights' K order: step s takes K 32q + 8s
+          // .. + 7; a chunk past K (the last stage of a K % 128 != 0) reads
+          // back in-range data and is zeroed
+          const uint32_t m = 32 * q < kb ? ~0u : 0u;
+          constexpr bool k52 = RECIPE == MI355MOE_RECIPE_FP8E5M2;
+  #pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const uint4 x = *reinterpret_cast<const uint4*>(xr + (32 * q + 8 * s) * 2);
+  #pragma unroll
+            for (int j = 0; j < NB; ++j) {
+              const uint4 w = wf[0][j][s >> 1];
+              const uint2 h = (s & 1) ? make_uint2(w.z & m, w.w & m) : make_uint2(w.x & m, w.y & m);
+              acc[mt][j] = mfma16_16x16x32<F16>(fp8x8_to16<k52, F16>(h), x, acc[mt][j]);
+            }
           }
         } else {
   #pragma unroll
@@ -492,8 +515,13 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     // expert on (16-slot STREAM blocks would stream an expert's weights once
     // per block)
     t = TILE_WIDE, b = kWideBM;
-  } else if (is_mx_recipe(recipe) || is_w8a16_recipe(recipe)) {
+  } else if (is_mx_recipe(recipe)) {
     t = TILE_STREAM, b = 16;
+  } else if (is_w8a16_recipe(recipe)) {
+    // the 16-bit rule up to 64-slot SMALL blocks (larger layers are rejected
+    // by the fused layer: they run on 16-bit copies)
+    if (avg <= kStreamMaxAvg16) t = TILE_STREAM, b = 16;
+    else t = TILE_SMALL, b = 64;
   } else if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
     // a 320-slot fp8 stage is 73 KB, so the WIDE kernel keeps one stage of
     // DMA in flight against the 128-slot kernel's two: it wins where experts
@@ -513,7 +541,7 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
     else t = TILE_BIG, b = 128;
   } else {
     if (avg <= kStreamMaxAvg16) t = TILE_STREAM, b = 16;
-    else if (avg <= 48 || (!wide_ok && avg <= 96)) t = TILE_SMALL, b = 64;
+    else if (avg <= kSmallMaxAvg16 || (!wide_ok && avg <= 96)) t = TILE_SMALL, b = 64;
     else if (wide_ok) t = TILE_WIDE, b = kWideBM;
     else t = TILE_BIG, b = 128;
   }
@@ -544,8 +572,9 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
          "per-expert fp8 (K % 128 == 0) recipe and a kernel family that reads them");
   MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM || tile == TILE_WIDE,
          "MX recipes run the STREAM and WIDE kernels");
-  MI_CHECK(!is_w8a16_recipe(recipe) || tile == TILE_STREAM, MI355MOE_ERR_UNSUPPORTED,
-           "per-expert fp8 weights run the decode (STREAM) kernels only");
+  MI_CHECK(!is_w8a16_recipe(recipe) || tile == TILE_STREAM || tile == TILE_SMALL,
+           MI355MOE_ERR_UNSUPPORTED,
+           "per-expert fp8 weights run the STREAM and SMALL kernels only");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:
@@ -582,9 +611,22 @@ int launch_moe_gemm_q(int recipe, int epi, bool qout, int bm, const GemmArgs& a,
     case MI355MOE_RECIPE_FP8BLOCK: MI_EPI(MI355MOE_RECIPE_FP8BLOCK)
     case MI355MOE_RECIPE_MXFP4: MI_EPI(MI355MOE_RECIPE_MXFP4)
     case MI355MOE_RECIPE_INT4: MI_EPI(MI355MOE_RECIPE_INT4)
-    default: return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
+    default: break;
   }
 #undef MI_EPI
+  if (is_w8a16_recipe(recipe)) {  // 64-slot blocks only (the tile choice's)
+    MI_ARG(bm == 64, "per-expert fp8 weights: 64-slot blocks");
+    if (recipe == MI355MOE_RECIPE_FP8) {
+      if (epi == EPI_GLU) launch_tile<MI355MOE_RECIPE_FP8, 64, EPI_GLU, false>(a, max_blocks, qs, st);
+      else launch_tile<MI355MOE_RECIPE_FP8, 64, EPI_STORE, false>(a, max_blocks, qs, st);
+    } else {
+      if (epi == EPI_GLU) launch_tile<MI355MOE_RECIPE_FP8E5M2, 64, EPI_GLU, false>(a, max_blocks, qs, st);
+      else launch_tile<MI355MOE_RECIPE_FP8E5M2, 64, EPI_STORE, false>(a, max_blocks, qs, st);
+    }
+    MI_LAUNCH_CHECK();
+    return MI355MOE_OK;
+  }
+  return set_error(MI355MOE_ERR_INVALID, "unknown recipe");
 }
 
 int launch_moe_gemm(int recipe, int epi, int bm, const GemmArgs& a,

@@ -30,12 +30,12 @@ FP8_BLOCK_SIZE = 128
 RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4, RECIPE_INT4, RECIPE_MXFP8 = 0, 1, 2, 3, 4
 # per-expert fp8 weights read as they are (e4m3 / e5m2, converted in registers)
 RECIPE_FP8, RECIPE_FP8E5M2 = 5, 6
-# Layers averaging at most this many slots per active expert run the decode
-# (STREAM) kernels (moe_gemm.hip pick_tile, kStreamMaxAvg16): per-expert fp8
+# Layers averaging at most this many slots per active expert run the STREAM
+# and SMALL kernels (moe_gemm.hip pick_tile, kSmallMaxAvg16): per-expert fp8
 # calls in that range read the fp8 weights; larger ones run on exact 16-bit
 # copies, made on the first such call.  "0" always uses the copies.
 FP8_W8A16_ENV = "MI355MOE_FP8_W8A16"
-STREAM_MAX_AVG_SLOTS = 10
+W8A16_MAX_AVG_SLOTS = 48
 ACT_SILU, ACT_SWIGLUOAI, ACT_GELU, ACT_GELU_TANH, ACT_SWIGLUSTEP, ACT_RELU2 = range(6)
 # reference fused_moe_interface.py:119-133, 239-254
 _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
@@ -318,13 +318,12 @@ class XpuFusedMoe:
     def _call_plan(self, dtype, num_tokens, topk):
         """(recipe, w13, w2, weight layout) of a call in `dtype` with
         num_tokens x topk slots: per-expert fp8 weights are read as they
-        are by decode-sized calls (the C ABI's rule, at most
-        STREAM_MAX_AVG_SLOTS slots per active expert) and through exact
-        16-bit copies otherwise."""
+        are by calls up to the C ABI's limit (W8A16_MAX_AVG_SLOTS slots per
+        active expert) and through exact 16-bit copies beyond it."""
         if self._w8_recipe is not None and _is_env_enabled(FP8_W8A16_ENV, "1"):
             slots = num_tokens * topk
             active = min(slots, self.w13.shape[0])
-            if active == 0 or slots // active <= STREAM_MAX_AVG_SLOTS:
+            if active == 0 or slots // active <= W8A16_MAX_AVG_SLOTS:
                 return self._w8_recipe, self.w13, self.w2, self._w8_layout
         w13, w2 = self._call_weights(dtype)
         return self._recipe, w13, w2, self._w_layout
