@@ -238,10 +238,10 @@ def _workspace_query_checks(lib, a):
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"need the fp8block, mxfp8 or mxfp4" in lib.mi355moe_last_error()
     a.hidden_scale = None
-    # per-expert fp8 weights read as fp8 (recipes 5 / 6): calls of at most 48
-    # slots per active expert with sizes % 32 == 0, else
-    # MI355MOE_ERR_UNSUPPORTED (the layer then runs on 16-bit copies); 64
-    # tokens x top-8 over 256 experts is 2 slots per expert, 4096 tokens 128
+    # per-expert fp8 weights read as fp8 (recipes 5 / 6): sizes % 32 == 0
+    # (else MI355MOE_ERR_UNSUPPORTED: the layer then runs on 16-bit copies),
+    # any call size and either layout (these calls pass validation and stop
+    # at the missing workspace)
     for recipe in (5, 6):
         a.recipe, a.hidden, a.num_tokens = recipe, 7168, 64
         a.w13_scale = a.w2_scale = None
@@ -251,13 +251,11 @@ def _workspace_query_checks(lib, a):
         a.hidden = 7160
         rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
         assert rc == -2 and b"% 32 == 0" in lib.mi355moe_last_error()
-        a.hidden, a.num_tokens = 7168, 4096
-        rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
-        assert rc == -2 and b"at most 48 slots per active expert" in lib.mi355moe_last_error()
-        a.num_tokens, a.w_layout, a.hidden = 64, 1, 7200
-        rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
-        assert rc == -1 and b"K-blocked weights need" in lib.mi355moe_last_error()
-        a.w_layout, a.hidden = 0, 7168
+        for T, layout in ((4096, 0), (64, 1), (4096, 1)):
+            a.hidden, a.num_tokens, a.w_layout = 7200, T, layout
+            rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+            assert rc == -4 and b"workspace" in lib.mi355moe_last_error()
+        a.w_layout, a.hidden, a.num_tokens = 0, 7168, 64
     a.recipe = 7
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"unknown recipe" in lib.mi355moe_last_error()

@@ -787,19 +787,21 @@ def test_per_expert_fp8_weight_conversion_kat(dev, dt, fp8, scale):
 @pytest.mark.parametrize("fp8", [torch.float8_e5m2, torch.float8_e4m3fn])
 @pytest.mark.parametrize("shape", ["T1", "T2-k8", "T8", "C3-T1", "C2-T1", "rowmajor-T2",
                                    "k-tail-T2", "small-T256", "small-C2-T64",
-                                   "small-rowmajor-T256", "prefill-T1024"])
+                                   "small-rowmajor-T256", "prefill-T1024",
+                                   "prefill-ragged-T1024", "prefill-rowmajor-T1024"])
 def test_fused_moe_fp8_per_expert_reads_fp8(dev, monkeypatch, dt, fp8, shape):
-    """Per-expert fp8 layers of at most 48 slots per active expert read the
-    fp8 weights themselves (converted exactly in registers; no 16-bit copies
-    are made): every element within the reference's bar of the oracle (bf16
-    2e-2, fp16 1e-2) and of the 16-bit-copy path (MI355MOE_FP8_W8A16=0).
-    STREAM shapes: split-K and self-sorting w13 (T1), 16 slots (T2-k8), C3's
+    """Per-expert fp8 layers read the fp8 weights themselves (converted
+    exactly in registers; no 16-bit copies are made): every element within
+    the reference's bar of the oracle (bf16 2e-2, fp16 1e-2; 64 sampled
+    tokens) and of the 16-bit-copy path (MI355MOE_FP8_W8A16=0).  STREAM
+    shapes: split-K and self-sorting w13 (T1), 16 slots (T2-k8), C3's
     token-major w2 (C3-T1, H = 7168), C2's w2 rebuilding its rows from the
-    w13 partials (C2-T1), row-major weights (H = 1056, I = 544: the last K
-    stage one 32-value chunk).  SMALL shapes (32 slots per expert): GLU and
-    STORE kernels, K-blocked and row-major.  With H = 1000 (not % 32) or 128
-    slots per expert (prefill-T1024) the layer runs on the copies (the
-    oracle checks 64 sampled tokens there)."""
+    w13 partials (C2-T1).  SMALL shapes (32 slots per expert): GLU and STORE
+    kernels.  320-slot shapes (128 slots per expert): K-blocked weights,
+    also with I = 544 (a last GLU tile of 32 columns, H = 1056: a 32-value K
+    tail of the 128-value blocks); row-major weights (MI355MOE_WEIGHT_LAYOUT
+    = nk) run the STREAM / SMALL kernels.  With H = 1000 (not % 32) the
+    layer runs on the copies."""
     from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
     g = torch.Generator().manual_seed(11)
     E, H, I, T, topk = 16, 1024, 512, 1, 2
@@ -813,6 +815,7 @@ def test_fused_moe_fp8_per_expert_reads_fp8(dev, monkeypatch, dt, fp8, shape):
         E, H, I, topk = 16, 2048, 768, 8
     elif shape == "rowmajor-T2":
         H, I, T = 1056, 544, 2
+        monkeypatch.setenv("MI355MOE_WEIGHT_LAYOUT", "nk")
     elif shape == "k-tail-T2":
         H, I, T = 1000, 520, 2
     elif shape == "small-T256":
@@ -821,8 +824,14 @@ def test_fused_moe_fp8_per_expert_reads_fp8(dev, monkeypatch, dt, fp8, shape):
         E, H, I, T, topk = 16, 2048, 768, 64, 8
     elif shape == "small-rowmajor-T256":
         H, I, T = 1056, 544, 256
+        monkeypatch.setenv("MI355MOE_WEIGHT_LAYOUT", "nk")
     elif shape == "prefill-T1024":
         T = 1024
+    elif shape == "prefill-ragged-T1024":
+        H, I, T = 1056, 544, 1024
+    elif shape == "prefill-rowmajor-T1024":
+        T = 1024
+        monkeypatch.setenv("MI355MOE_WEIGHT_LAYOUT", "nk")
     q13, s13 = _fp8_expert_weights(E, 2 * I, H, fp8, g)
     q2, s2 = _fp8_expert_weights(E, H, I, fp8, g)
     b13 = (torch.randn(E, 2 * I, generator=g) / 16).to(dt)
@@ -832,8 +841,8 @@ def test_fused_moe_fp8_per_expert_reads_fp8(dev, monkeypatch, dt, fp8, shape):
     moe = XpuFusedMoe(q13.transpose(1, 2).contiguous().to(dev), s13.to(dev), b13.to(dev),
                       q2.transpose(1, 2).contiguous().to(dev), s2.to(dev), b2.to(dev),
                       topk, "silu", E)
-    native = shape not in ("k-tail-T2", "prefill-T1024")
-    assert (moe._w8_recipe is not None) == (shape != "k-tail-T2")
+    native = shape != "k-tail-T2"
+    assert (moe._w8_recipe is not None) == native
     if native:
         assert moe._w8_layout == (0 if "rowmajor" in shape else 1)
     xd, twd, tid = x.to(dev), tw.to(dev), ti.to(dev)

@@ -27,7 +27,7 @@ __host__ __device__ constexpr bool is_w8a16_recipe(int r) {
 }
 // 16-bit (and w8a16) weights: layers averaging at most this many slots per
 // active expert run the STREAM kernels, up to kSmallMaxAvg16 the 64-slot
-// SMALL kernels (w8a16 layers beyond that are not taken)
+// SMALL kernels
 constexpr int64_t kStreamMaxAvg16 = 10;
 constexpr int64_t kSmallMaxAvg16 = 48;
 
@@ -179,6 +179,11 @@ __device__ __forceinline__ int64_t w_koff16(const WStride& s, int64_t k) {
 // (k / 128) * kblk + k % 128.
 __device__ __forceinline__ WStride w_stride8(const GemmArgs& a) {
   return a.w_kblock ? WStride{128, a.ldb_rows * 128} : WStride{a.K, 128};
+}
+// per-expert fp8 weights (K blocks of 32 bytes): element (row r, k) at r *
+// row + (k / 32) * kblk + k % 32.
+__device__ __forceinline__ WStride w_stride8w(const GemmArgs& a) {
+  return a.w_kblock ? WStride{32, a.ldb_rows * 32} : WStride{a.K, 32};
 }
 // mxfp4 e2m1 pairs (K blocks of 32 values = 16 bytes): block kb of row r at
 // r * row + kb * kblk; its e8m0 scale byte at r * row + kb * kblk of

@@ -96,7 +96,8 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
   const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
   // weights (and mxfp4 scales) may be K-blocked
-  const WStride wst = kFp4 ? w_stride4(a) : (kFp8 || kW8 ? w_stride8(a) : w_stride16(a));
+  const WStride wst = kFp4 ? w_stride4(a)
+                           : (kW8 ? w_stride8w(a) : (kFp8 ? w_stride8(a) : w_stride16(a)));
   const WStride sst = s_stride4(a);
   const uint8_t* wptr[NB];
   bool wok[NB];
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
                           (K / 128) + k0 / 128];
         } else if constexpr (kW8) {  // K % 32 == 0: a chunk lies wholly in or past K
           const int64_t kc = k0 + 32 * q < K ? k0 + 32 * q : K - 32;
-          const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (kc >> 7) * wst.kblk + (kc & 127));
+          const uint4* p = reinterpret_cast<const uint4*>(wptr[j] + (kc >> 5) * wst.kblk);
           wf[0][j][0] = kBatchX || wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
           wf[0][j][1] = kBatchX || wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
         } else {
@@ -489,7 +490,7 @@ bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) return wide8_shape_ok(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_MXFP8) return w_kblock && wide8_shape_ok(a_rows, ldb_rows, K);
   if (recipe == RECIPE_MX4A4) return w_kblock && wide8_shape_ok_mx4(a_rows, ldb_rows, K);
-  if (recipe == MI355MOE_RECIPE_MXFP4)
+  if (recipe == MI355MOE_RECIPE_MXFP4 || is_w8a16_recipe(recipe))
     return w_kblock && wide4_shape_ok(a_rows, ldb_rows, ldb_rows, K);
   return false;
 }
@@ -518,10 +519,11 @@ GemmTile pick_tile(int recipe, bool wide_ok, int64_t slots, int64_t num_experts,
   } else if (is_mx_recipe(recipe)) {
     t = TILE_STREAM, b = 16;
   } else if (is_w8a16_recipe(recipe)) {
-    // the 16-bit rule up to 64-slot SMALL blocks (larger layers are rejected
-    // by the fused layer: they run on 16-bit copies)
+    // the 16-bit rule; prefill on the 320-slot kernel of the 4-bit weights
+    // (WIDE4 reads fp8 fragments too), which needs K-blocked weights
     if (avg <= kStreamMaxAvg16) t = TILE_STREAM, b = 16;
-    else t = TILE_SMALL, b = 64;
+    else if (avg <= kSmallMaxAvg16 || !wide_ok) t = TILE_SMALL, b = 64;
+    else t = TILE_WIDE, b = kWideBM;
   } else if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
     // a 320-slot fp8 stage is 73 KB, so the WIDE kernel keeps one stage of
     // DMA in flight against the 128-slot kernel's two: it wins where experts
@@ -567,14 +569,15 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
                (tile == TILE_BIG && big8_supported(recipe, a)))) ||
              recipe == MI355MOE_RECIPE_MXFP4 || is_mx_recipe(recipe) ||
-             (is_w8a16_recipe(recipe) && a.K % 128 == 0),
+             (is_w8a16_recipe(recipe) && a.K % 32 == 0),
          "K-blocked weights need the bf16 (K % 32 == 0), fp8block, mxfp4, mxfp8 or "
-         "per-expert fp8 (K % 128 == 0) recipe and a kernel family that reads them");
+         "per-expert fp8 (K % 32 == 0) recipe and a kernel family that reads them");
   MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM || tile == TILE_WIDE,
          "MX recipes run the STREAM and WIDE kernels");
-  MI_CHECK(!is_w8a16_recipe(recipe) || tile == TILE_STREAM || tile == TILE_SMALL,
+  MI_CHECK(!is_w8a16_recipe(recipe) || tile == TILE_STREAM || tile == TILE_SMALL ||
+               tile == TILE_WIDE,
            MI355MOE_ERR_UNSUPPORTED,
-           "per-expert fp8 weights run the STREAM and SMALL kernels only");
+           "per-expert fp8 weights run the STREAM, SMALL and WIDE kernels");
   switch (tile) {
     case TILE_STREAM: return launch_moe_gemm_stream(recipe, epi, qout, a, max_blocks, qs, st);
     case TILE_BIG:
@@ -588,7 +591,7 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
       if (recipe == MI355MOE_RECIPE_FP8BLOCK || is_mx_recipe(recipe))
         return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
       MI_ARG(!qout, "wide GEMM: no fp8 activation output");
-      if (recipe == MI355MOE_RECIPE_MXFP4)
+      if (recipe == MI355MOE_RECIPE_MXFP4 || is_w8a16_recipe(recipe))
         return launch_moe_gemm_wide4(recipe, epi, a, max_blocks, st);
       return launch_moe_gemm_wide(recipe, epi, a, max_blocks, st);
     default: return launch_moe_gemm_q(recipe, epi, qout, bm, a, max_blocks, qs, st);

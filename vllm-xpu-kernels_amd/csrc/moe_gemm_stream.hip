@@ -239,7 +239,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   }
   // weights (and mxfp4 scales) may be K-blocked
   const WStride wst = (kFp4 || kMx4) ? w_stride4(a)
-                                     : ((kFp8 || kMx8 || kW8) ? w_stride8(a) : w_stride16(a));
+                                     : (kW8 ? w_stride8w(a)
+                                            : ((kFp8 || kMx8) ? w_stride8(a) : w_stride16(a)));
   const WStride sst = s_stride4(a);
   const uint8_t* wp0 = wexp + wrow[0] * wst.row;
   const uint8_t* wp1 = wexp + wrow[1] * wst.row;
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       const int64_t kc = k < K ? k : K - 32;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint8_t* p = (t ? wp1 : wp0) + (kc >> 7) * wst.kblk + (kc & 127);
+        const uint8_t* p = (t ? wp1 : wp0) + (kc >> 5) * wst.kblk;  // one 32-byte K block
         f.w[t][0] = *reinterpret_cast<const uint4*>(p);
         f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
       }

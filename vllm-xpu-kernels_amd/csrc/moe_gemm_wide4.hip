@@ -23,6 +23,13 @@
 // the 8 values [16 ks + 8 h, +8): 4 bytes of e2m1, converted with
 // v_cvt_scalef32_pk_{bf16,f16}_fp4 (the call's 16-bit type) under the row's scale (2^(code - 127); code 0
 // gives 0, as the other mxfp4 kernels).
+//
+// Per-expert fp8 weights (recipes FP8 / FP8E5M2, K-blocked [E, K/32, N, 32
+// bytes]) run the same kernel: a stage's weights are 256 rows x 32 bytes
+// (8 KB, five stages in the ring, no scales), waves 4-7 move 64 rows each
+// with two transfers, a fragment is 8 fp8 bytes converted exactly by
+// v_cvt_scalef32_pk_{bf16,f16}_{fp8,bf8} at scale 1, and the epilogue
+// multiplies the accumulators by the expert's scale.
 #include <type_traits>
 
 #include "mfma16.h"
@@ -40,16 +47,23 @@ constexpr int MG = 5;                          // 32-row groups per wave
 constexpr int BM = 2 * 32 * MG, BN = 256, ROWB = 64, KE = 32;
 static_assert(BM == kWideBM, "block size of the WIDE family");
 constexpr int A_BYTES = BM * ROWB;             // 20 KB of bf16 activations
-constexpr int W_OFF = A_BYTES;                 // 256 rows x 16 bytes of e2m1
-constexpr int S_OFF = W_OFF + BN * 16;         // 256 e8m0 scale bytes
-constexpr int STAGE = S_OFF + BN;              // 24.25 KB
-constexpr int NSTAGE = 6;
+constexpr int W_OFF = A_BYTES;                 // 256 weight rows
 constexpr int A_DMA = BM / 16 / 4;             // activation blocks per wave (waves 0-3)
 constexpr int DMA_MAX = A_DMA;                 // DMA instructions per wave and stage
-constexpr int RING_BYTES = NSTAGE * STAGE;
-constexpr int LDS_BYTES = RING_BYTES;
-static_assert(BM * (2 * 128 + 16) <= RING_BYTES, "GLU output tile staged in one pass");
-static_assert(BM / 2 * (2 * 256 + 16) <= RING_BYTES, "STORE output tile staged in two passes");
+// Stage geometry of the weight format: e2m1 (16 bytes a row + 256 e8m0 scale
+// bytes, 24.25 KB, six stages) or fp8 (32 bytes a row, 28 KB, five stages).
+template <bool W8>
+struct Geom {
+  static constexpr int WROW = W8 ? 32 : 16;    // weight bytes per row and stage
+  static constexpr int S_OFF = W_OFF + BN * WROW;
+  static constexpr int STAGE = S_OFF + (W8 ? 0 : BN);
+  static constexpr int NSTAGE = W8 ? 5 : 6;
+  static constexpr int RING = NSTAGE * STAGE;
+  static_assert(RING <= 150 * 1024, "LDS budget");
+  static_assert(BM * (2 * 128 + 16) <= RING, "GLU output tile staged in one pass");
+  static_assert(BM / 2 * (2 * 256 + 16) <= RING, "STORE output tile staged in two passes");
+  static_assert(A_DMA >= 2, "two weight transfers per wave fit the offset array");
+};
 
 __device__ __forceinline__ uint32_t lds_off(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p));
@@ -131,19 +145,26 @@ struct Frag {
 };
 
 // Activation tile j sits 32 x 64 bytes past tile 0 (rows 32 apart share the
-// swizzle).  Weight tile i: row woff_r + i * wstep_r; its 4 e2m1 bytes at
-// W_OFF + 16 row + wb, its scale at S_OFF + row.
-template <int NJ, bool F16>
+// swizzle).  Weight tile i: row woff_r + i * wstep_r; e2m1: its 4 bytes at
+// W_OFF + 16 row + wb, its scale at S_OFF + row; fp8: its 8 bytes at W_OFF +
+// 32 row + wb.
+template <int NJ, bool F16, int WREC>
 __device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, int xoff, int wrow0,
                                           int wstep_r, int wb) {
+  constexpr bool W8 = is_w8a16_recipe(WREC);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) f.x[j] = *reinterpret_cast<const uint4*>(S + xoff + j * 32 * ROWB);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = wrow0 + i * wstep_r;
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(S + W_OFF + 16 * r + wb);
-    const uint32_t code = S[S_OFF + r];
-    f.w[i] = fp4x8_to16<F16>(w, __uint_as_float(code << 23));
+    if constexpr (W8) {
+      const uint2 w = *reinterpret_cast<const uint2*>(S + W_OFF + 32 * r + wb);
+      f.w[i] = fp8x8_to16<WREC == MI355MOE_RECIPE_FP8E5M2, F16>(w);
+    } else {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(S + W_OFF + 16 * r + wb);
+      const uint32_t code = S[Geom<false>::S_OFF + r];
+      f.w[i] = fp4x8_to16<F16>(w, __uint_as_float(code << 23));
+    }
   }
 }
 
@@ -155,12 +176,15 @@ __device__ __forceinline__ void mfma_step(f32x16 (&acc)[2][MG], const Frag& f) {
     for (int j = 0; j < NJ; ++j) acc[i][j] = mfma16_32x32x16<F16>(f.w[i], f.x[j], acc[i][j]);
 }
 
-template <int EPI, bool F16>
+template <int EPI, bool F16, int WREC>
 __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
+  constexpr bool W8 = is_w8a16_recipe(WREC);
+  using G = Geom<W8>;
+  constexpr int STAGE = G::STAGE, NSTAGE = G::NSTAGE, RING_BYTES = G::RING;
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[RING_BYTES];
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
 
@@ -212,12 +236,12 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   // scalar base plus 32-bit lane offsets (launch_moe_gemm_wide4 checks the
   // sizes).
   const bool a_wave = wave < 4;
-  const int64_t ebytes = a.ldb_rows * (K / 2);  // one expert's e2m1 bytes
+  const int64_t ebytes = a.ldb_rows * (W8 ? K : K / 2);  // one expert's weight bytes
   const uint8_t* abase = uniform_ptr(a.A);
   const uint8_t* wexp = uniform_ptr(static_cast<const uint8_t*>(a.B) + static_cast<int64_t>(e) * ebytes);
   const uint8_t* sexp = uniform_ptr(static_cast<const uint8_t*>(a.b_scale) +
                                     static_cast<int64_t>(e) * a.ldb_rows * (K / 32));
-  const int64_t wkstep = a.ldb_rows * 16;       // K-blocked: bytes between two K stages
+  const int64_t wkstep = a.ldb_rows * G::WROW;  // K-blocked: bytes between two K stages
   const int64_t skstep = a.ldb_rows;
   uint32_t voff[DMA_MAX];
   int nd = 0;
@@ -231,6 +255,15 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
                                       (((lane & 3) ^ swz(r)) << 4));
       nd += b * 16 < v ? 1 : 0;
     }
+  } else if constexpr (W8) {
+    // transfer i: rows 64 (wave - 4) + 32 i + lane / 2, 16-byte half lane % 2
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      voff[i] = static_cast<uint32_t>(wrow_of(64 * (wave - 4) + 32 * i + (lane >> 1)) * 32 +
+                                      16 * (lane & 1));
+#pragma unroll
+    for (int q = 2; q < DMA_MAX; ++q) voff[q] = 0;
+    nd = 2;
   } else {
     voff[0] = static_cast<uint32_t>(wrow_of(64 * (wave - 4) + lane) * 16);
     voff[1] = static_cast<uint32_t>(wrow_of(4 * lane));
@@ -248,12 +281,17 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
       for (int q = 0; q < A_DMA; ++q)
         if (q < nd)
           dma16(voff[q], sb, __builtin_amdgcn_readfirstlane(base + (A_DMA * wave + q) * 1024));
+    } else if constexpr (W8) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        dma16(voff[i], wexp + static_cast<int64_t>(kt) * wkstep,
+              __builtin_amdgcn_readfirstlane(base + W_OFF + 2048 * (wave - 4) + 1024 * i));
     } else {
       dma16(voff[0], wexp + static_cast<int64_t>(kt) * wkstep,
             __builtin_amdgcn_readfirstlane(base + W_OFF + 1024 * (wave - 4)));
       if (wave == 4)
         dma4(voff[1], sexp + static_cast<int64_t>(kt) * skstep,
-             __builtin_amdgcn_readfirstlane(base + S_OFF));
+             __builtin_amdgcn_readfirstlane(base + G::S_OFF));
     }
   };
   // this wave's DMA instructions still allowed in flight once stage s has
@@ -278,6 +316,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   }
   const int wrow0 = (kGlu ? 32 * wn : 64 * wn) + l32;
   constexpr int WSTEP_R = kGlu ? 128 : 32;
+  // byte offset of the lane's fragment in its weight row: K steps 0 and 1
+  const int wb0 = W8 ? 8 * h : 4 * h, wb1 = W8 ? 16 + 8 * h : 8 + 4 * h;
 
   f32x16 acc[2][MG];
 #pragma unroll
@@ -299,18 +339,18 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
     Frag f0, f1;
     wait_vm_dyn(pending_after(0, NSTAGE - 2));
     __builtin_amdgcn_s_barrier();
-    read_frag<NJ, F16>(f0, lds, xoff[0], wrow0, WSTEP_R, 4 * h);
-    read_frag<NJ, F16>(f1, lds, xoff[1], wrow0, WSTEP_R, 8 + 4 * h);
+    read_frag<NJ, F16, WREC>(f0, lds, xoff[0], wrow0, WSTEP_R, wb0);
+    read_frag<NJ, F16, WREC>(f1, lds, xoff[1], wrow0, WSTEP_R, wb1);
     for (int kt = 0; kt < nk; ++kt) {
       mfma_step<NJ, F16>(acc, f0);
       // stage kt+1 landed; later stages this wave issued may pend
       wait_vm_dyn(pending_after(kt + 1, kt + NSTAGE - 2));
       __builtin_amdgcn_s_barrier();
       const uint8_t* S1 = lds + ((kt + 1) % NSTAGE) * STAGE;
-      read_frag<NJ, F16>(f0, S1, xoff[0], wrow0, WSTEP_R, 4 * h);
+      read_frag<NJ, F16, WREC>(f0, S1, xoff[0], wrow0, WSTEP_R, wb0);
       if (kt + NSTAGE - 1 < nk) issue(kt + NSTAGE - 1);
       mfma_step<NJ, F16>(acc, f1);
-      read_frag<NJ, F16>(f1, S1, xoff[1], wrow0, WSTEP_R, 8 + 4 * h);
+      read_frag<NJ, F16, WREC>(f1, S1, xoff[1], wrow0, WSTEP_R, wb1);
     }
   };
   switch (nj) {
@@ -330,6 +370,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   constexpr int PASSES = BM * PITCH <= RING_BYTES ? 1 : 2;
   constexpr int PROWS = BM / PASSES;
   const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+  const float es = W8 && a.expert_scale ? a.expert_scale[e] : 1.f;  // per-expert fp8
   auto tcol = [&](int i, int r) -> int {  // tile output column of (i, r)
     return (kGlu ? 32 * wn : 64 * wn + 32 * i) + 8 * (r >> 2) + 4 * h + (r & 3);
   };
@@ -362,9 +403,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
           float ov[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            float g = round16<F16>(acc[i][j][r] + bg[r]);
+            float g = round16<F16>((W8 ? acc[i][j][r] * es : acc[i][j][r]) + bg[r]);
             if constexpr (kGlu) {
-              float u = round16<F16>(acc[1][j][r] + bu[r]);
+              float u = round16<F16>((W8 ? acc[1][j][r] * es : acc[1][j][r]) + bu[r]);
               glu_clamp(a, n0 + tcol(i, r), g, u);
               float y;
               if (a.act == MI355MOE_ACT_SILU) {
@@ -408,12 +449,12 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   }
 }
 
-template <int EPI, bool F16>
+template <int EPI, bool F16, int WREC>
 int launch_wide4(const GemmArgs& a, int64_t max_blocks, hipStream_t st) {
   const int64_t cols = EPI == EPI_GLU ? 128 : 256;
   const int64_t total = cdiv(a.N, cols) * max_blocks;
   dim3 grid(static_cast<unsigned>(cdiv(total, 8) * 8));
-  moe_gemm_wide4_kernel<EPI, F16><<<grid, dim3(512), 0, st>>>(a);
+  moe_gemm_wide4_kernel<EPI, F16, WREC><<<grid, dim3(512), 0, st>>>(a);
   MI_LAUNCH_CHECK();
   return MI355MOE_OK;
 }
@@ -423,24 +464,33 @@ int launch_wide4(const GemmArgs& a, int64_t max_blocks, hipStream_t st) {
 bool wide4_shape_ok(int64_t a_rows, int64_t ldb_rows, int64_t N, int64_t K) {
   const int64_t lim = int64_t(1) << 32;
   return K % 32 == 0 && K > 0 && ldb_rows % 4 == 0 && N % 4 == 0 && a_rows * K * 2 < lim &&
-         ldb_rows * K / 2 < lim;
+         ldb_rows * K < lim;
 }
 
-// kWideBM-slot blocks; K-blocked mxfp4 weights and scales, K % 32 == 0.
+template <int WREC>
+int launch_wide4_rec(int epi, const GemmArgs& a, int64_t max_blocks, hipStream_t st) {
+  if (epi == EPI_GLU)
+    return a.out_f16 ? launch_wide4<EPI_GLU, true, WREC>(a, max_blocks, st)
+                     : launch_wide4<EPI_GLU, false, WREC>(a, max_blocks, st);
+  return a.out_f16 ? launch_wide4<EPI_STORE, true, WREC>(a, max_blocks, st)
+                   : launch_wide4<EPI_STORE, false, WREC>(a, max_blocks, st);
+}
+
+// kWideBM-slot blocks; K-blocked mxfp4 weights and scales, or K-blocked
+// per-expert fp8 weights ([E, K/32, N, 32 bytes]); K % 32 == 0.
 int launch_moe_gemm_wide4(int recipe, int epi, const GemmArgs& a, int64_t max_blocks,
                           hipStream_t st) {
   if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
-  MI_ARG(recipe == MI355MOE_RECIPE_MXFP4 && a.w_kblock,
-         "mxfp4 prefill GEMM: needs K-blocked mxfp4 weights and scales");
+  MI_ARG((recipe == MI355MOE_RECIPE_MXFP4 || is_w8a16_recipe(recipe)) && a.w_kblock,
+         "4-bit / fp8-weight prefill GEMM: needs K-blocked mxfp4 or per-expert fp8 weights");
   const int64_t a_rows = a.a_by_pos ? max_blocks * BM : a.num_valid;
   MI_ARG(wide4_shape_ok(a_rows, a.ldb_rows, a.N, a.K) && (a.up_off & 3) == 0,
-         "mxfp4 prefill GEMM: needs K % 32 == 0, N and weight rows % 4 == 0 and "
-         "activation / per-expert weight bytes below 4 GiB");
-  if (epi == EPI_GLU)
-    return a.out_f16 ? launch_wide4<EPI_GLU, true>(a, max_blocks, st)
-                     : launch_wide4<EPI_GLU, false>(a, max_blocks, st);
-  return a.out_f16 ? launch_wide4<EPI_STORE, true>(a, max_blocks, st)
-                   : launch_wide4<EPI_STORE, false>(a, max_blocks, st);
+         "4-bit / fp8-weight prefill GEMM: needs K % 32 == 0, N and weight rows % 4 == 0 "
+         "and activation / per-expert weight bytes below 4 GiB");
+  if (recipe == MI355MOE_RECIPE_FP8) return launch_wide4_rec<MI355MOE_RECIPE_FP8>(epi, a, max_blocks, st);
+  if (recipe == MI355MOE_RECIPE_FP8E5M2)
+    return launch_wide4_rec<MI355MOE_RECIPE_FP8E5M2>(epi, a, max_blocks, st);
+  return launch_wide4_rec<MI355MOE_RECIPE_MXFP4>(epi, a, max_blocks, st);
 }
 
 }  // namespace mi355

@@ -30,12 +30,10 @@ FP8_BLOCK_SIZE = 128
 RECIPE_BF16, RECIPE_FP8BLOCK, RECIPE_MXFP4, RECIPE_INT4, RECIPE_MXFP8 = 0, 1, 2, 3, 4
 # per-expert fp8 weights read as they are (e4m3 / e5m2, converted in registers)
 RECIPE_FP8, RECIPE_FP8E5M2 = 5, 6
-# Layers averaging at most this many slots per active expert run the STREAM
-# and SMALL kernels (moe_gemm.hip pick_tile, kSmallMaxAvg16): per-expert fp8
-# calls in that range read the fp8 weights; larger ones run on exact 16-bit
-# copies, made on the first such call.  "0" always uses the copies.
+# Per-expert fp8 weights are read as fp8 by every kernel family (hidden and
+# intermediate sizes % 32 == 0; others run on exact 16-bit copies, made on
+# the first call).  "0" always uses the copies.
 FP8_W8A16_ENV = "MI355MOE_FP8_W8A16"
-W8A16_MAX_AVG_SLOTS = 48
 ACT_SILU, ACT_SWIGLUOAI, ACT_GELU, ACT_GELU_TANH, ACT_SWIGLUSTEP, ACT_RELU2 = range(6)
 # reference fused_moe_interface.py:119-133, 239-254
 _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
@@ -107,6 +105,13 @@ def pack_weights_kblock(w: torch.Tensor) -> torch.Tensor:
     out = torch.empty((E, Kb // B, N, B), dtype=w.dtype, device=w.device)
     torch.ops._moe_C.mi355_pack_weights_kblock(w.contiguous(), out)
     return out
+
+
+def _kblock32(w: torch.Tensor) -> torch.Tensor:
+    """1-byte weights [E, N, K] -> [E, K/32, N, 32] (K % 32 == 0)."""
+    E, N, K = w.shape
+    b = w.view(torch.uint8).view(E, N, K // 32, 32).permute(0, 2, 1, 3).contiguous()
+    return b.view(w.dtype)
 
 
 def pack_scales_kblock(s: torch.Tensor) -> torch.Tensor:
@@ -294,13 +299,11 @@ class XpuFusedMoe:
         if self._fp8_expert and H % 32 == 0 and K2 % 32 == 0:
             self._w8_recipe = (RECIPE_FP8E5M2 if w13c.dtype == torch.float8_e5m2
                                else RECIPE_FP8)
-            if (H % FP8_BLOCK_SIZE == 0 and K2 % FP8_BLOCK_SIZE == 0 and
-                    os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk"):
-                # K blocks of 128 bytes (the packing moves bytes; e5m2 goes
-                # through an e4m3 view)
-                e4 = torch.float8_e4m3fn
-                w13c = pack_weights_kblock(w13c.view(e4)).view(w13c.dtype)
-                w2c = pack_weights_kblock(w2c.view(e4)).view(w2c.dtype)
+            if os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk":
+                # K blocks of 32 bytes, [E, K/32, N, 32]: one 32-byte block
+                # per lane in the STREAM / SMALL kernels, a 32-value stage of
+                # 256 rows one 8 KB run in the 320-slot kernel
+                w13c, w2c = _kblock32(w13c), _kblock32(w2c)
                 self._w8_layout = WLAYOUT_KBLOCK
         self._w16_cache = {}
         self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
@@ -318,13 +321,10 @@ class XpuFusedMoe:
     def _call_plan(self, dtype, num_tokens, topk):
         """(recipe, w13, w2, weight layout) of a call in `dtype` with
         num_tokens x topk slots: per-expert fp8 weights are read as they
-        are by calls up to the C ABI's limit (W8A16_MAX_AVG_SLOTS slots per
-        active expert) and through exact 16-bit copies beyond it."""
+        are (sizes % 32 == 0), else through exact 16-bit copies."""
+        del num_tokens, topk  # every call size reads them
         if self._w8_recipe is not None and _is_env_enabled(FP8_W8A16_ENV, "1"):
-            slots = num_tokens * topk
-            active = min(slots, self.w13.shape[0])
-            if active == 0 or slots // active <= W8A16_MAX_AVG_SLOTS:
-                return self._w8_recipe, self.w13, self.w2, self._w8_layout
+            return self._w8_recipe, self.w13, self.w2, self._w8_layout
         w13, w2 = self._call_weights(dtype)
         return self._recipe, w13, w2, self._w_layout
 
