@@ -55,6 +55,8 @@ def gemm_work(cfg, T, active, which):
         bw, sc, bx, sx = 1.0, 1.0 / 32, 1.0, 1.0 / 32
     elif cfg.recipe == "fp8":    # per-expert e4m3 weights, 16-bit activations
         bw, sc, bx, sx = 1.0, 0.0, 2.0, 0.0
+    elif cfg.recipe == "int4":   # u4 + a 16-bit scale per 128 along K
+        bw, sc, bx, sx = 0.5, 2.0 / 128, 2.0, 0.0
     elif cfg.prequant:   # e2m1 x e2m1
         bw, sc, bx, sx = 0.5, 1.0 / 32, 0.5, 1.0 / 32
     else:
@@ -311,8 +313,8 @@ SWEEP = [("C1", 64), ("C2", 1), ("C2", 16), ("C2", 64), ("C2", 256), ("C2", 4096
          ("C3", 1), ("C3", 64), ("C3", 8192), ("C4", 2048), ("C5", 1), ("C5", 128),
          ("C5", 4096),
          # recipe variants on the same shapes: mxfp8 weights, w4a4 (e2m1 x e2m1),
-         # per-expert fp8 (decode reads the e4m3 weights themselves)
-         ("C3-mxfp8", 8192), ("C5-w4a4", 4096), ("C3-fp8", 1)]
+         # per-expert fp8 (the e4m3 weights read as such), int4 (w4a16)
+         ("C3-mxfp8", 8192), ("C5-w4a4", 4096), ("C3-fp8", 1), ("C2-int4", 4096)]
 
 
 def op_bandwidth(dev, steps):
@@ -548,7 +550,7 @@ def main():
         "vs_baseline": None,
         "dtype": ("mxfp4xmxfp4" if cfg.prequant else
                   {"bf16": "bf16", "fp8block": "fp8e4m3", "mxfp4": "mxfp4xbf16",
-                   "mxfp8": "mxfp8e4m3", "fp8": "e4m3xbf16"}[cfg.recipe]),
+                   "mxfp8": "mxfp8e4m3", "fp8": "e4m3xbf16", "int4": "int4xbf16"}[cfg.recipe]),
         "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights; random init)",
         "config": {"workload": f"{args.config} {cfg.name} fused MoE layer, T={args.tokens}",
                    "tokens": args.tokens, "hidden": cfg.hidden, "inter": cfg.inter,

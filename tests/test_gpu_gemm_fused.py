@@ -889,8 +889,8 @@ def test_fused_moe_int4(dev, dt, T, topk):
     """The reference's int4 layer (tests/fused_moe/test_fused_moe.py:303-420 at
     H=1024, I=512, 16 experts, group 128): u4 weights with zero point 8, scales
     2^-5 in the activation type, biases; every element within the reference's
-    bar.  T covers the split-K stream ... 128-slot kernels (int4 is
-    row-major only)."""
+    bar.  T covers the split-K stream, stream, small and 320-slot kernels
+    (K-blocked int4 weights and scales)."""
     from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
     g = torch.Generator().manual_seed(11 + T)
     E, H, I, grp = 16, 1024, 512, 128
@@ -912,6 +912,42 @@ def test_fused_moe_int4(dev, dt, T, topk):
                       ti[toks])
     tol = 2e-2 if dt == torch.bfloat16 else 1e-2
     torch.testing.assert_close(out.cpu()[toks], ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("grp", [32, 128, 256])
+@pytest.mark.parametrize("T", [2, 64, 2048])
+@pytest.mark.parametrize("layout", ["kblock", "nk"])
+def test_fused_moe_int4_group_scales(dev, monkeypatch, grp, T, layout):
+    """int4 with a different 16-bit scale in every (row, group) and random
+    biases, against the oracle (64 sampled tokens): K-blocked weights and
+    scales through the stream (T=2), small (T=64) and 320-slot (T=2048)
+    kernels, where one group spans 1, 4 or 8 of the 320-slot kernel's
+    32-value stages and the scales of a stage move with the weights; the
+    row-major layout (MI355MOE_WEIGHT_LAYOUT=nk) through the stream, small
+    and 128-slot kernels."""
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    if layout == "nk":
+        monkeypatch.setenv("MI355MOE_WEIGHT_LAYOUT", "nk")
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(31 + T + grp)
+    E, H, I, topk = 16, 1024, 512, 2
+    u13 = torch.randint(0, 0xff, (E, 2 * I, H // 2), generator=g).to(torch.uint8)
+    u2 = torch.randint(0, 0xff, (E, H, I // 2), generator=g).to(torch.uint8)
+    s13 = (torch.rand(E, 2 * I, H // grp, generator=g) * 2 ** -4 + 2 ** -7).to(dt)
+    s2 = (torch.rand(E, H, I // grp, generator=g) * 2 ** -4 + 2 ** -7).to(dt)
+    b13 = (torch.randn(E, 2 * I, generator=g) / 16).to(dt)
+    b2 = (torch.randn(E, H, generator=g) / 16).to(dt)
+    x = (torch.randn(T, H, generator=g) / 16).to(dt)
+    tw, ti = torch.topk(torch.randn(T, E, generator=g), k=topk, dim=-1, sorted=False)
+    moe = XpuFusedMoe(u13.to(dev), s13.to(dev), b13.to(dev), u2.to(dev), s2.to(dev), b2.to(dev),
+                      topk, "silu", E)
+    assert moe._w_layout == (1 if layout == "kblock" else 0)
+    out = torch.full((T, H), float("nan"), dtype=dt, device=dev)
+    moe.apply(out, x.to(dev), tw.to(dev), ti.to(dev))
+    toks = torch.linspace(0, T - 1, min(T, 64)).long()
+    ref = O.fused_moe("int4", x[toks], u13 ^ 0x88, s13, b13, u2 ^ 0x88, s2, b2, tw[toks],
+                      ti[toks])
+    torch.testing.assert_close(out.cpu()[toks], ref, rtol=2e-2, atol=2e-2)
 
 
 def test_fused_moe_a1q_scale_rejected_outside_fp8block(dev):

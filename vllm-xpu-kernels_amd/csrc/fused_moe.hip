@@ -611,7 +611,6 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     MI_ARG(H % g == 0 && act_width(a) % g == 0,
            "int4 weights need hidden and intermediate sizes % group_size == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "int4 weights need group scales");
-    MI_ARG(a->w_layout == MI355MOE_WLAYOUT_NK, "int4 weights are row-major only");
   } else if (recipe == MI355MOE_RECIPE_MXFP4) {
     MI_ARG(H % 32 == 0 && I % 32 == 0, "mxfp4 weights need K % 32 == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "mxfp4 weights need e8m0 scales");
@@ -633,11 +632,11 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   MI_ARG(!kblock || (recipe == MI355MOE_RECIPE_BF16 && H % 32 == 0 && I % 32 == 0) ||
              (recipe == MI355MOE_RECIPE_FP8BLOCK && H <= 8192 && act_width(a) <= 8192) ||
              (recipe == MI355MOE_RECIPE_MXFP8 && H % 128 == 0 && act_width(a) % 128 == 0) ||
-             is_w8a16_recipe(recipe) ||
+             is_w8a16_recipe(recipe) || recipe == MI355MOE_RECIPE_INT4 ||
              recipe == MI355MOE_RECIPE_MXFP4,
          "K-blocked weights need the bf16 recipe (hidden and intermediate sizes "
          "% 32 == 0), the fp8block recipe (sizes at most 8192), mxfp8 (sizes % 128 "
-         "== 0), per-expert fp8 or mxfp4");
+         "== 0), per-expert fp8, int4 or mxfp4");
   MI_ARG(!mx_layer(a) || epilogue_act(a->activation),
          "mxfp8 and pre-quantised mxfp4 layers support the silu and swigluoai activations");
   if (T == 0) return MI355MOE_OK;

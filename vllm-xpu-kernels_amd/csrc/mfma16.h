@@ -113,9 +113,11 @@ template <int RECIPE>
 __device__ __forceinline__ uint32_t w4_scale_code(const GemmArgs& a, int e, int64_t wrow,
                                                   int64_t blk32, const WStride& sst) {
   if constexpr (RECIPE == MI355MOE_RECIPE_INT4) {
-    const int64_t groups = a.K / a.w_group;
-    return static_cast<const uint16_t*>(a.b_scale)
-        [(static_cast<int64_t>(e) * a.ldb_rows + wrow) * groups + (blk32 * 32) / a.w_group];
+    // row-major [E, ldb_rows, K/group], or K-blocked [E, K/group, ldb_rows]
+    const int64_t groups = a.K / a.w_group, g = (blk32 * 32) / a.w_group;
+    const uint16_t* s = static_cast<const uint16_t*>(a.b_scale);
+    return a.w_kblock ? s[(static_cast<int64_t>(e) * groups + g) * a.ldb_rows + wrow]
+                      : s[(static_cast<int64_t>(e) * a.ldb_rows + wrow) * groups + g];
   } else {
     return static_cast<const uint8_t*>(a.b_scale)
         [static_cast<int64_t>(e) * a.ldb_rows * (a.K / 32) + wrow * sst.row + blk32 * sst.kblk];

@@ -490,7 +490,8 @@ bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) return wide8_shape_ok(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_MXFP8) return w_kblock && wide8_shape_ok(a_rows, ldb_rows, K);
   if (recipe == RECIPE_MX4A4) return w_kblock && wide8_shape_ok_mx4(a_rows, ldb_rows, K);
-  if (recipe == MI355MOE_RECIPE_MXFP4 || is_w8a16_recipe(recipe))
+  if (recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4 ||
+      is_w8a16_recipe(recipe))
     return w_kblock && wide4_shape_ok(a_rows, ldb_rows, ldb_rows, K);
   return false;
 }
@@ -568,8 +569,8 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
              (recipe == MI355MOE_RECIPE_FP8BLOCK &&
               (tile == TILE_STREAM || tile == TILE_SMALL || tile == TILE_WIDE ||
                (tile == TILE_BIG && big8_supported(recipe, a)))) ||
-             recipe == MI355MOE_RECIPE_MXFP4 || is_mx_recipe(recipe) ||
-             (is_w8a16_recipe(recipe) && a.K % 32 == 0),
+             recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4 ||
+             is_mx_recipe(recipe) || (is_w8a16_recipe(recipe) && a.K % 32 == 0),
          "K-blocked weights need the bf16 (K % 32 == 0), fp8block, mxfp4, mxfp8 or "
          "per-expert fp8 (K % 32 == 0) recipe and a kernel family that reads them");
   MI_ARG(!is_mx_recipe(recipe) || tile == TILE_STREAM || tile == TILE_WIDE,
@@ -591,7 +592,8 @@ int launch_tile_gemm(GemmTile tile, int bm, int recipe, int epi, bool qout,
       if (recipe == MI355MOE_RECIPE_FP8BLOCK || is_mx_recipe(recipe))
         return launch_moe_gemm_wide8(recipe, epi, qout, a, max_blocks, qs, st);
       MI_ARG(!qout, "wide GEMM: no fp8 activation output");
-      if (recipe == MI355MOE_RECIPE_MXFP4 || is_w8a16_recipe(recipe))
+      if (recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4 ||
+          is_w8a16_recipe(recipe))
         return launch_moe_gemm_wide4(recipe, epi, a, max_blocks, st);
       return launch_moe_gemm_wide(recipe, epi, a, max_blocks, st);
     default: return launch_moe_gemm_q(recipe, epi, qout, bm, a, max_blocks, qs, st);

@@ -51,12 +51,15 @@ constexpr int W_OFF = A_BYTES;                 // 256 weight rows
 constexpr int A_DMA = BM / 16 / 4;             // activation blocks per wave (waves 0-3)
 constexpr int DMA_MAX = A_DMA;                 // DMA instructions per wave and stage
 // Stage geometry of the weight format: e2m1 (16 bytes a row + 256 e8m0 scale
-// bytes, 24.25 KB, six stages) or fp8 (32 bytes a row, 28 KB, five stages).
-template <bool W8>
+// bytes, 24.25 KB, six stages), int4 (16 bytes a row + 256 16-bit group
+// scales, 24.5 KB, six stages) or fp8 (32 bytes a row, 28 KB, five stages).
+template <int WREC>
 struct Geom {
+  static constexpr bool W8 = is_w8a16_recipe(WREC);
   static constexpr int WROW = W8 ? 32 : 16;    // weight bytes per row and stage
+  static constexpr int SROW = W8 ? 0 : (WREC == MI355MOE_RECIPE_INT4 ? 2 : 1);  // scale bytes
   static constexpr int S_OFF = W_OFF + BN * WROW;
-  static constexpr int STAGE = S_OFF + (W8 ? 0 : BN);
+  static constexpr int STAGE = S_OFF + BN * SROW;
   static constexpr int NSTAGE = W8 ? 5 : 6;
   static constexpr int RING = NSTAGE * STAGE;
   static_assert(RING <= 150 * 1024, "LDS budget");
@@ -160,9 +163,13 @@ __device__ __forceinline__ void read_frag(Frag& f, const uint8_t* S, int xoff, i
     if constexpr (W8) {
       const uint2 w = *reinterpret_cast<const uint2*>(S + W_OFF + 32 * r + wb);
       f.w[i] = fp8x8_to16<WREC == MI355MOE_RECIPE_FP8E5M2, F16>(w);
+    } else if constexpr (WREC == MI355MOE_RECIPE_INT4) {  // T(v * scale)
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(S + W_OFF + 16 * r + wb);
+      const uint16_t sc = *reinterpret_cast<const uint16_t*>(S + Geom<WREC>::S_OFF + 2 * r);
+      f.w[i] = int4x8_to16<F16>(w, ld16<F16>(sc));
     } else {
       const uint32_t w = *reinterpret_cast<const uint32_t*>(S + W_OFF + 16 * r + wb);
-      const uint32_t code = S[Geom<false>::S_OFF + r];
+      const uint32_t code = S[Geom<WREC>::S_OFF + r];
       f.w[i] = fp4x8_to16<F16>(w, __uint_as_float(code << 23));
     }
   }
@@ -181,7 +188,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   constexpr bool kGlu = EPI == EPI_GLU;
   constexpr int NOUT = kGlu ? 128 : 256;  // output columns per tile
   constexpr bool W8 = is_w8a16_recipe(WREC);
-  using G = Geom<W8>;
+  constexpr bool I4 = WREC == MI355MOE_RECIPE_INT4;
+  using G = Geom<WREC>;
   constexpr int STAGE = G::STAGE, NSTAGE = G::NSTAGE, RING_BYTES = G::RING;
 
   __shared__ __attribute__((aligned(1024))) uint8_t lds[RING_BYTES];
@@ -239,10 +247,12 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   const int64_t ebytes = a.ldb_rows * (W8 ? K : K / 2);  // one expert's weight bytes
   const uint8_t* abase = uniform_ptr(a.A);
   const uint8_t* wexp = uniform_ptr(static_cast<const uint8_t*>(a.B) + static_cast<int64_t>(e) * ebytes);
+  // scales: e8m0 [E, K/32, N] bytes, or int4's 16-bit [E, K/group, N]
+  const int64_t sgroups = I4 ? K / a.w_group : K / 32;
   const uint8_t* sexp = uniform_ptr(static_cast<const uint8_t*>(a.b_scale) +
-                                    static_cast<int64_t>(e) * a.ldb_rows * (K / 32));
+                                    static_cast<int64_t>(e) * a.ldb_rows * sgroups * G::SROW);
   const int64_t wkstep = a.ldb_rows * G::WROW;  // K-blocked: bytes between two K stages
-  const int64_t skstep = a.ldb_rows;
+  const int64_t skstep = a.ldb_rows * G::SROW;  // bytes between two scale groups
   uint32_t voff[DMA_MAX];
   int nd = 0;
   if (a_wave) {
@@ -264,6 +274,16 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
 #pragma unroll
     for (int q = 2; q < DMA_MAX; ++q) voff[q] = 0;
     nd = 2;
+  } else if constexpr (I4) {
+    // wave 4 also moves the 256 rows' 16-bit scales: lane l rows 2 l, 2 l + 1
+    // (and 128 + 2 l, + 1); N and up_off % 4 == 0 keep each pair of rows on
+    // one side of N
+    voff[0] = static_cast<uint32_t>(wrow_of(64 * (wave - 4) + lane) * 16);
+    voff[1] = static_cast<uint32_t>(wrow_of(2 * lane) * 2);
+    voff[2] = static_cast<uint32_t>(wrow_of(128 + 2 * lane) * 2);
+#pragma unroll
+    for (int q = 3; q < DMA_MAX; ++q) voff[q] = 0;
+    nd = wave == 4 ? 3 : 1;
   } else {
     voff[0] = static_cast<uint32_t>(wrow_of(64 * (wave - 4) + lane) * 16);
     voff[1] = static_cast<uint32_t>(wrow_of(4 * lane));
@@ -286,6 +306,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
       for (int i = 0; i < 2; ++i)
         dma16(voff[i], wexp + static_cast<int64_t>(kt) * wkstep,
               __builtin_amdgcn_readfirstlane(base + W_OFF + 2048 * (wave - 4) + 1024 * i));
+    } else if constexpr (I4) {
+      dma16(voff[0], wexp + static_cast<int64_t>(kt) * wkstep,
+            __builtin_amdgcn_readfirstlane(base + W_OFF + 1024 * (wave - 4)));
+      if (wave == 4) {  // the group of this 32-value stage
+        const uint8_t* sb = sexp + static_cast<int64_t>(kt) * 32 / a.w_group * skstep;
+        dma4(voff[1], sb, __builtin_amdgcn_readfirstlane(base + G::S_OFF));
+        dma4(voff[2], sb, __builtin_amdgcn_readfirstlane(base + G::S_OFF + 256));
+      }
     } else {
       dma16(voff[0], wexp + static_cast<int64_t>(kt) * wkstep,
             __builtin_amdgcn_readfirstlane(base + W_OFF + 1024 * (wave - 4)));
@@ -481,8 +509,11 @@ int launch_wide4_rec(int epi, const GemmArgs& a, int64_t max_blocks, hipStream_t
 int launch_moe_gemm_wide4(int recipe, int epi, const GemmArgs& a, int64_t max_blocks,
                           hipStream_t st) {
   if (max_blocks <= 0 || a.N <= 0) return MI355MOE_OK;
-  MI_ARG((recipe == MI355MOE_RECIPE_MXFP4 || is_w8a16_recipe(recipe)) && a.w_kblock,
-         "4-bit / fp8-weight prefill GEMM: needs K-blocked mxfp4 or per-expert fp8 weights");
+  MI_ARG((recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4 ||
+          is_w8a16_recipe(recipe)) &&
+             a.w_kblock,
+         "4-bit / fp8-weight prefill GEMM: needs K-blocked mxfp4, int4 or per-expert fp8 "
+         "weights");
   const int64_t a_rows = a.a_by_pos ? max_blocks * BM : a.num_valid;
   MI_ARG(wide4_shape_ok(a_rows, a.ldb_rows, a.N, a.K) && (a.up_off & 3) == 0,
          "4-bit / fp8-weight prefill GEMM: needs K % 32 == 0, N and weight rows % 4 == 0 "
@@ -490,6 +521,10 @@ int launch_moe_gemm_wide4(int recipe, int epi, const GemmArgs& a, int64_t max_bl
   if (recipe == MI355MOE_RECIPE_FP8) return launch_wide4_rec<MI355MOE_RECIPE_FP8>(epi, a, max_blocks, st);
   if (recipe == MI355MOE_RECIPE_FP8E5M2)
     return launch_wide4_rec<MI355MOE_RECIPE_FP8E5M2>(epi, a, max_blocks, st);
+  if (recipe == MI355MOE_RECIPE_INT4) {
+    MI_ARG(a.w_group >= 32 && a.K % a.w_group == 0, "int4 prefill GEMM: group size >= 32");
+    return launch_wide4_rec<MI355MOE_RECIPE_INT4>(epi, a, max_blocks, st);
+  }
   return launch_wide4_rec<MI355MOE_RECIPE_MXFP4>(epi, a, max_blocks, st);
 }
 

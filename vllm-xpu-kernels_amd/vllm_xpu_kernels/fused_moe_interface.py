@@ -285,12 +285,16 @@ class XpuFusedMoe:
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
                   (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and K2 <= 8192) or
                   (self._recipe == RECIPE_MXFP8 and H % 128 == 0 and K2 % 128 == 0) or
-                  self._recipe == RECIPE_MXFP4)
+                  self._recipe in (RECIPE_MXFP4, RECIPE_INT4))
         self._kblock = kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk"
         if self._kblock and not self._fp8_expert:
             w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)
             if self._recipe in (RECIPE_MXFP4, RECIPE_MXFP8):
                 s13c, s2c = pack_scales_kblock(s13c), pack_scales_kblock(s2c)
+            elif self._recipe == RECIPE_INT4:
+                # 16-bit group scales [E, N, K/group] -> [E, K/group, N]
+                s13c = s13c.transpose(1, 2).contiguous()
+                s2c = s2c.transpose(1, 2).contiguous()
             self._w_layout = WLAYOUT_KBLOCK
         if self._fp8_expert and self._kblock:
             self._w_layout = WLAYOUT_KBLOCK   # applies to the 16-bit copies

@@ -25,7 +25,7 @@ class MoeConfig:
     inter: int
     experts: int
     topk: int
-    recipe: str                 # "bf16" | "fp8block" | "mxfp4" | "mxfp8" | "fp8"
+    recipe: str                 # "bf16" | "fp8block" | "mxfp4" | "mxfp8" | "fp8" | "int4"
     routing: str                # "softmax" | "grouped_sigmoid"
     activation: str = "silu"
     renormalize: bool = True
@@ -65,6 +65,9 @@ CONFIGS = {
 VARIANTS = {
     "C3-mxfp8": replace(CONFIGS["C3"], recipe="mxfp8"),
     "C3-fp8": replace(CONFIGS["C3"], recipe="fp8"),
+    # Qwen3-30B-A3B with int4 weights (u4, zero point 8, bf16 scale per 128
+    # along K: the reference's w4a16 recipe)
+    "C2-int4": replace(CONFIGS["C2"], recipe="int4"),
     "C5-w4a4": replace(CONFIGS["C5"], prequant=True),
 }
 
@@ -93,6 +96,16 @@ def fp8_block_quant(w: torch.Tensor, eps: float = 1e-6):
     s = torch.clamp(x.abs().amax(dim=(-3, -1)) / 448.0, min=eps)
     q = (x / s.unsqueeze(-2).unsqueeze(-1)).reshape(*lead, N, K)
     return q.to(torch.float8_e4m3fn), s
+
+
+def int4_quant(w: torch.Tensor, group: int = 128):
+    """[N, K] fp32 -> u4 pairs uint8 [N, K/2] (zero point 8, the even K
+    value in the low nibble) + bf16 scales [N, K/group]."""
+    N, K = w.shape
+    g = w.view(N, K // group, group)
+    s = (g.abs().amax(-1) / 7.0).clamp(min=1e-8).to(torch.bfloat16)
+    q = (torch.round(g / s.float().unsqueeze(-1)).clamp(-8, 7) + 8).to(torch.uint8).view(N, K)
+    return q[:, 0::2] | (q[:, 1::2] << 4), s
 
 
 def mxfp4_quant(w: torch.Tensor):
@@ -165,6 +178,8 @@ def expert_weights_nk(cfg: MoeConfig, e: int, device, seed: int = 0):
         q13, s13 = mxfp8_quant(w13)
         q2, s2 = mxfp8_quant(w2)
         return q13, s13, q2, s2
+    if cfg.recipe == "int4":  # u4 = round(w / s) + 8 in [0, 15], s = amax / 7 per 128
+        return (*int4_quant(w13), *int4_quant(w2))
     if cfg.recipe == "fp8":   # one scale per expert and matrix: amax / 448
         s13, s2 = w13.abs().amax() / 448.0, w2.abs().amax() / 448.0
         return ((w13 / s13).to(torch.float8_e4m3fn), s13, (w2 / s2).to(torch.float8_e4m3fn),
@@ -201,6 +216,12 @@ def make_weights(cfg: MoeConfig, device, seed: int = 0) -> MoeWeights:
         w2 = torch.empty(E, K2, H, dtype=torch.float8_e4m3fn, device=device)
         s13 = torch.empty(E, device=device)
         s2 = torch.empty(E, device=device)
+    elif cfg.recipe == "int4":
+        # reference layout: u4 pairs [E, N, K/2] + 16-bit scales [E, N, K/128]
+        w13 = torch.empty(E, 2 * I, H // 2, dtype=torch.uint8, device=device)
+        w2 = torch.empty(E, H, K2 // 2, dtype=torch.uint8, device=device)
+        s13 = torch.empty(E, 2 * I, H // 128, dtype=torch.bfloat16, device=device)
+        s2 = torch.empty(E, H, K2 // 128, dtype=torch.bfloat16, device=device)
     elif cfg.recipe == "mxfp8":
         # reference layout (moe_utils.py:80-82): [E, K, N] + e8m0 [E, K/32, N]
         w13 = torch.empty(E, H, 2 * I, dtype=torch.float8_e4m3fn, device=device)
@@ -285,6 +306,8 @@ def algorithmic_bytes(cfg: MoeConfig, T: int, active: int) -> float:
         wb = n + n / 32
     elif cfg.recipe == "fp8":
         wb = n + 8
+    elif cfg.recipe == "int4":
+        wb = n / 2 + 2 * n / 128
     else:
         wb = n / 2 + n / 32
     if cfg.bias:
@@ -298,7 +321,7 @@ def algorithmic_flops(cfg: MoeConfig, T: int) -> float:
 
 
 PEAK_TFLOPS = {"bf16": 2500.0, "fp8block": 5000.0, "mxfp4": 2500.0, "mxfp8": 5000.0,
-               "fp8": 2500.0}   # per-expert fp8 runs 16-bit MFMAs (w8a16)
+               "fp8": 2500.0, "int4": 2500.0}   # w8a16 / w4a16 run 16-bit MFMAs
 PEAK_TFLOPS_FP4 = 10100.0   # e2m1 x e2m1 (pre-quantised mxfp4 input)
 PEAK_HBM_GBS = 8000.0
 
