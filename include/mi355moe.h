@@ -61,7 +61,9 @@ typedef enum {
                                    packed along K [E, N, K/2], scales
                                    [E, N, K/group] in the activations'
                                    16-bit type, group 32/64/128/256:
-                                   w = T(v * scale) (w4a16)               */
+                                   w = T(v * scale) (w4a16); K-blocked:
+                                   weights [E, K/32, N, 16 bytes], scales
+                                   [E, K/group, N]                        */
   MI355MOE_RECIPE_MXFP8 = 4,    /* e4m3 weights [E, N, K] with an e8m0 scale
                                    (u8) per 32 along K, [E, N, K/32];
                                    activations quantised per 32 to e4m3
