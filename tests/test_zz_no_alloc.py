@@ -35,11 +35,14 @@ def _run_pair(cfg, T, dev, moe, w, seed):
     assert torch.equal(out, ref), f"T={T}: {(out.float() - ref.float()).abs().max()}"
 
 
-@pytest.mark.parametrize("name,E,sizes", [("C2", None, (64, 16)), ("C3", 32, (33, 4))])
+@pytest.mark.parametrize("name,E,sizes", [("C2", None, (64, 16)), ("C3", 32, (33, 4)),
+                                          ("C3-fp8", 32, (33, 4)), ("C2-int4", None, (64, 16))])
 def test_fused_moe_noalloc_matches_workspace_entry(dev, name, E, sizes):
+    """C2 bf16, C3 fp8 block-scaled, C3 shapes with per-expert e4m3 weights
+    (read as fp8) and C2 shapes with K-blocked int4 weights."""
     from vllm_xpu_kernels import workloads as W
     from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
-    cfg = W.CONFIGS[name]
+    cfg = W.config(name)
     if E is not None:
         cfg = dataclasses.replace(cfg, experts=E)
     w = W.make_weights(cfg, dev)
