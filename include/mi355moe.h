@@ -75,16 +75,15 @@ typedef enum {
                                    "fp8", vllm_xpu_kernels/
                                    fused_moe_interface.py:42-59, w8a16):
                                    e4m3 weights [E, N, K] (K-blocked
-                                   [E, K/128, N, 128]) with an f32 scale per
+                                   [E, K/32, N, 32]) with an f32 scale per
                                    expert ([E] in w13_scale / w2_scale) and
                                    16-bit activations; each weight is
                                    converted exactly to the activations'
                                    type as it is loaded and the expert's
-                                   scale multiplies the accumulators.
-                                   STREAM and SMALL kernels only: layers
-                                   averaging more than 48 slots per active
-                                   expert, or with hidden or intermediate
-                                   sizes not % 32, return
+                                   scale multiplies the accumulators (every
+                                   layer size; the prefill kernel needs the
+                                   K-blocked layout).  Hidden or
+                                   intermediate sizes not % 32 return
                                    MI355MOE_ERR_UNSUPPORTED (run them as
                                    RECIPE_BF16 on exact 16-bit copies)    */
   MI355MOE_RECIPE_FP8E5M2 = 6   /* as RECIPE_FP8 with e5m2 weights        */

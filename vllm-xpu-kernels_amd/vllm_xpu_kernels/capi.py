@@ -94,8 +94,7 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     after conversion: f32 for fp8block, e8m0 bytes for mxfp8 / mxfp4, whose
     hidden_states are then packed e2m1 bytes [T, H/2])."""
     a = FusedMoeArgs()
-    recipe, w13, w2, layout = moe._call_plan(hidden_states.dtype, hidden_states.shape[0],
-                                             topk_ids.shape[1])
+    recipe, w13, w2, layout = moe._call_plan(hidden_states.dtype)
     a.recipe = recipe
     a.activation = moe._act
     a.act_dtype = F16 if output.dtype == torch.float16 else BF16

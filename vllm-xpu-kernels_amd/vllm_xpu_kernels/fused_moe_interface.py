@@ -322,11 +322,10 @@ class XpuFusedMoe:
         E, KB, N, B = w.shape
         return w.permute(0, 2, 1, 3).reshape(E, N, KB * B)
 
-    def _call_plan(self, dtype, num_tokens, topk):
-        """(recipe, w13, w2, weight layout) of a call in `dtype` with
-        num_tokens x topk slots: per-expert fp8 weights are read as they
-        are (sizes % 32 == 0), else through exact 16-bit copies."""
-        del num_tokens, topk  # every call size reads them
+    def _call_plan(self, dtype):
+        """(recipe, w13, w2, weight layout) of a call in `dtype`: per-expert
+        fp8 weights are read as they are (sizes % 32 == 0), else through
+        exact 16-bit copies."""
         if self._w8_recipe is not None and _is_env_enabled(FP8_W8A16_ENV, "1"):
             return self._w8_recipe, self.w13, self.w2, self._w8_layout
         w13, w2 = self._call_weights(dtype)
@@ -414,8 +413,7 @@ class XpuFusedMoe:
             # clamp limit (fused_moe_interface.py:27-30, 296-317)
             clamp = 0.0
         b13, b2 = self._biases(dt16)
-        recipe, w13, w2, layout = self._call_plan(dt16, hidden_states.shape[0],
-                                                  topk_ids.shape[-1])
+        recipe, w13, w2, layout = self._call_plan(dt16)
         s13, s2 = self._scales(dt16)
         torch.ops._moe_C.mi355_fused_moe(
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
