@@ -56,11 +56,11 @@ __device__ __forceinline__ uint32_t lds_off(const void* p) {
 }
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(lds_base) : "memory");
+               :: "v"(g), "s"(lds_base) : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
-               :: "v"(g), "s"(lds_base) : "memory");
+               :: "v"(g), "s"(lds_base) : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vm() {

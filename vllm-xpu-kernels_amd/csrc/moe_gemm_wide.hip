@@ -66,7 +66,7 @@ __device__ __forceinline__ uint32_t lds_off(const void* p) {
 // LDS at lds_base + 16 lane.
 __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory");
+               :: "v"(voff), "s"(reinterpret_cast<uint64_t>(sbase)), "s"(lds_base) : "memory", "m0");
 }
 // readfirstlane returns int: each half goes through uint32_t so that the low
 // half is zero-extended (a sign-extended low half with bit 31 set would fill

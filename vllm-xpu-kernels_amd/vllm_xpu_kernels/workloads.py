@@ -38,10 +38,10 @@ class MoeConfig:
     prequant: bool = False      # mxfp4: input handed over as e2m1 + e8m0 (w4a4)
 
 
-# Calibrated once (tests/golden/calibrate_zipf.py, on the device generator
-# the bench and tests draw logits with): the 13 busiest of 128 experts
-# receive 50% +- 2% of the 16384 assignments at T=2048 (0.4980 at 0.520,
-# 0.5059 at 0.530).
+# Calibrated once by a bisection over tau on the device generator the bench
+# and tests draw logits with: the 13 busiest of 128 experts receive 50% +- 2%
+# of the 16384 assignments at T=2048 (0.4980 at 0.520, 0.5059 at 0.530);
+# test_moe_align_zipf_skew_c4 pins the share.
 ZIPF_TAU_C4 = 0.5225
 
 CONFIGS = {
