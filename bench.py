@@ -167,13 +167,13 @@ class Point:
         self.out = torch.empty_like(self.x)
         self.tw, self.ti = W.route(cfg, self.logits, self.bias)
         self.active = int(torch.unique(self.ti).numel())
-        # every XpuFusedMoe converts (and so copies) the expert weights: steps
-        # rotate over enough copies that one pass over them exceeds
-        # rotate_bytes
+        # steps rotate over enough layers, each on its own copy of the weights
+        # (prepared in place), that one pass over them exceeds rotate_bytes;
+        # self.w keeps the reference layouts for the CPU baseline
         per_step = W.algorithmic_bytes(cfg, T, self.active)
         self.copies = int(min(MAX_COPIES, max(1, math.ceil(rotate_bytes / per_step))))
-        self.moes = [XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale,
-                                 w.w2_bias, cfg.topk, cfg.activation, cfg.experts)
+        self.moes = [XpuFusedMoe(*w.layer_args(copy=True), cfg.topk, cfg.activation,
+                                 cfg.experts)
                      for _ in range(self.copies)]
         self.moe = self.moes[0]
         self.i = 0

@@ -484,6 +484,13 @@ typedef struct {
   const void* hidden_scale;
   /* recipe INT4: K values per group scale (32, 64, 128 or 256) */
   int64_t w_group;
+  /* recipe FP8BLOCK: w13 rows per w13_scale row, 128 (0 also means 128) or
+   * 64.  64 is the layout of an interleaved swigluoai w13 (gate row 2j, up
+   * row 2j + 1, 128 x 128 scale blocks, as the reference's) split into a
+   * gate half and an up half: row n of either half keeps the scale of
+   * interleaved block n / 64 of its half, so w13_scale is [E, 2I/64, H/128]
+   * with its two halves equal to the reference's [E, 2I/128, H/128]. */
+  int64_t w13_scale_rows;
 } mi355moe_fused_moe_args;
 
 /* One-time weight preparation, the counterpart of the repacking the

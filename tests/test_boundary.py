@@ -192,7 +192,7 @@ def test_fused_moe_workspace_query_and_validation(lib):
                     ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
                     ("w_layout", ctypes.c_int),
                     ("hidden_scale", ctypes.c_void_p),
-                    ("w_group", ctypes.c_int64)]
+                    ("w_group", ctypes.c_int64), ("w13_scale_rows", ctypes.c_int64)]
 
     a = Args(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=64,
              hidden=7168, inter=2048, num_experts=256, topk=8)
@@ -217,6 +217,18 @@ def _workspace_query_checks(lib, a):
     a.hidden = 7168
     rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
     assert rc == -1 and b"need scales" in lib.mi355moe_last_error()
+    # fp8block w13 scale rows: 128 weight rows per scale row, or 64 (the split
+    # swigluoai layout)
+    a.w13_scale = a.w2_scale = 1
+    a.w13_scale_rows = 96
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and b"w13_scale_rows" in lib.mi355moe_last_error()
+    for rows in (0, 64, 128):
+        a.w13_scale_rows = rows
+        rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+        assert rc == -4 and b"workspace" in lib.mi355moe_last_error()
+    a.w13_scale_rows = 0
+    a.w13_scale = a.w2_scale = None
     # the K-blocked layout: bf16 with K % 32 == 0 or fp8block with K <= 8192
     a.w_layout = 1
     a.w13_scale = a.w2_scale = 1
@@ -416,6 +428,57 @@ def test_block_fp8_inter_size_uses_scales(monkeypatch, weight_layout):
     moe = F.XpuFusedMoe(weight, torch.ones(2, 4, 2), None, w2, torch.ones(2, 2, 2), None,
                         1, "silu", 2)
     assert moe.inter_size == 256 and moe.recipe == "fp8block"
+
+
+def test_prepare_in_place_host_logic(monkeypatch):
+    """Weight preparation on host tensors (row-major layout, no device pass):
+    by default the converted weights are written over the caller's tensors,
+    which keep shape and dtype and hold exactly the bytes of
+    MI355MOE_PREPARE_IN_PLACE=0's converted copy (that mode leaves them as
+    they were); a second layer on them with the same arguments reuses the
+    preparation, other arguments or a different partner tensor are refused.
+    fp8 block-scaled swigluoai: the interleaved rows split into [gate; up]
+    halves, the 128-row block scales repeated for both (one row per 64)."""
+    from vllm_xpu_kernels import fused_moe_interface as F
+    monkeypatch.setenv(F.WEIGHT_LAYOUT_ENV, "nk")
+    E, H, I = 3, 64, 32
+    g = torch.Generator().manual_seed(0)
+    w13 = torch.randn(E, H, 2 * I, generator=g).to(torch.bfloat16)
+    w2 = torch.randn(E, I, H, generator=g).to(torch.bfloat16)
+    nk13, nk2 = w13.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
+    split = torch.cat([nk13[:, 0::2], nk13[:, 1::2]], dim=1)
+    for act, want13 in (("silu", nk13), ("swigluoai", split)):
+        monkeypatch.setenv(F.PREPARE_IN_PLACE_ENV, "0")
+        a13, a2 = w13.clone(), w2.clone()
+        m0 = F.XpuFusedMoe(a13, None, None, a2, None, None, 1, act, E)
+        assert torch.equal(a13, w13) and torch.equal(a2, w2)
+        assert torch.equal(m0.w13, want13) and torch.equal(m0.w2, nk2)
+        monkeypatch.delenv(F.PREPARE_IN_PLACE_ENV)
+        m = F.XpuFusedMoe(a13, None, None, a2, None, None, 1, act, E)
+        assert m.w13.data_ptr() == a13.data_ptr() and m.w2.data_ptr() == a2.data_ptr()
+        assert a13.shape == w13.shape and a13.dtype == w13.dtype
+        assert torch.equal(m.w13, want13) and torch.equal(m.w2, nk2)
+        assert torch.equal(a13.flatten(), want13.flatten())
+        m2 = F.XpuFusedMoe(a13, None, None, a2, None, None, 1, act, E)
+        assert m2.w13.data_ptr() == a13.data_ptr() and torch.equal(m2.w13, want13)
+        with pytest.raises(ValueError, match="other arguments"):
+            F.XpuFusedMoe(a13, None, None, a2, None, None, 1, "gelu", E)
+        with pytest.raises(ValueError, match="other arguments"):
+            F.XpuFusedMoe(a13, None, None, w2.clone(), None, None, 1, act, E)
+    # fp8 block scales: [E, 2I/128, H/128] -> [E, 2I/64, H/128], halves equal
+    I8, H8 = 128, 256
+    q13 = torch.randn(E, 2 * I8, H8, generator=g).to(torch.float8_e4m3fn)
+    q2 = torch.randn(E, H8, I8, generator=g).to(torch.float8_e4m3fn)
+    s13 = torch.rand(E, 2 * I8 // 128, H8 // 128, generator=g)
+    s2 = torch.rand(E, H8 // 128, I8 // 128, generator=g)
+    want = torch.cat([q13[:, 0::2], q13[:, 1::2]], dim=1).view(torch.uint8)
+    q13b, q2b = q13.clone(), q2.clone()
+    m = F.XpuFusedMoe(q13, s13, None, q2, s2, None, 1, "swigluoai", E)
+    assert m.recipe == "fp8block" and m._ws_rows == 64
+    assert torch.equal(m.w13.view(torch.uint8), want)
+    assert torch.equal(m.gemm1_wei_scales, torch.cat([s13, s13], dim=1))
+    assert torch.equal(m.gemm2_wei_scales, s2)
+    assert F.XpuFusedMoe(q13b, s13, None, q2b, s2, None, 1, "silu", E)._ws_rows == 128
 
 
 def test_mx_recipe_selection(monkeypatch):

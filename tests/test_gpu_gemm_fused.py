@@ -145,8 +145,8 @@ def _layer(cfg, T, dev, E=None, seed_shift=0):
     logits = W.make_router_logits(cfg, T, dev, seed=2 + seed_shift)
     bias = W.make_correction_bias(cfg, dev) if cfg.routing == "grouped_sigmoid" else None
     tw, ti = W.route(cfg, logits, bias)
-    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
-                      cfg.topk, cfg.activation, cfg.experts)
+    # the layer prepares copies in place; w keeps the reference layouts
+    moe = XpuFusedMoe(*w.layer_args(copy=True), cfg.topk, cfg.activation, cfg.experts)
     out = torch.empty_like(x)
     moe.apply(out, x, tw, ti)
     return cfg, w, x, tw, ti, out, moe
@@ -208,11 +208,27 @@ def test_fused_moe_c3_deepseek_fp8_32_experts(dev, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
 
 
-def test_fused_moe_c3_full_size_sampled_tokens(dev):
-    """Full DeepSeek-V3 shape (256 experts, T=64): oracle on 4 sampled tokens."""
+def test_fused_moe_c3_full_size_every_token(dev):
+    """Full DeepSeek-V3 shape (256 experts, T=64, the decode kernels): every
+    token against the oracle run on the device, to the fp8 bar."""
     cfg, w, x, tw, ti, out, _ = _layer(_W().CONFIGS["C3"], 64, dev)
-    toks = torch.tensor([0, 17, 42, 63], device=dev)
-    _close(out[toks], _oracle_layer(cfg, w, x, tw, ti, toks), fp8=True)
+    _close(out, _oracle_layer_on_device(cfg, w, x, tw, ti), fp8=True)
+
+
+@pytest.mark.parametrize("T", [1, 256, 2048, 8192])
+def test_fused_moe_fp8block_swigluoai_c3(dev, T):
+    """fp8 block-scaled weights with an interleaved swigluoai w13 (gate row
+    2j, up row 2j + 1, 128 x 128 scale blocks) at the DeepSeek-V3 shape (256
+    experts, H=7168, I=2048): the layer splits the rows into gate and up
+    halves read with one scale row per 64 weight rows, through the decode
+    (T=1), small (T=256), 128-slot (T=2048) and 320-slot (T=8192) kernels;
+    every token against the oracle run on the device (interleaved rows, the
+    reference's block scales), to the fp8 bar."""
+    import dataclasses
+    cfg = dataclasses.replace(_W().CONFIGS["C3"], activation="swigluoai")
+    cfg, w, x, tw, ti, out, moe = _layer(cfg, T, dev)
+    assert moe._ws_rows == 64 and moe.gemm1_wei_scales.shape[1] == 2 * cfg.inter // 64
+    _close(out, _oracle_layer_on_device(cfg, w, x, tw, ti), fp8=True)
 
 
 def test_fused_moe_c4_zipf_fp8(dev):
@@ -249,7 +265,9 @@ def test_fused_moe_expert_map(dev):
     tw, ti = W.route(cfg, W.make_router_logits(cfg, 48, dev))
     em = torch.full((16,), -1, dtype=torch.int32, device=dev)
     em[8:] = torch.arange(8, dtype=torch.int32, device=dev)
-    moe = XpuFusedMoe(w.w13[8:].contiguous(), None, None, w.w2[8:].contiguous(), None,
+    # the rank's experts as new tensors (a slice would share w's storage,
+    # which the layer's preparation rewrites)
+    moe = XpuFusedMoe(w.w13[8:].clone(), None, None, w.w2[8:].clone(), None,
                       None, cfg.topk, "silu", 8, ep_rank=1, ep_size=2, expert_map=em)
     out = torch.empty_like(x)
     moe.apply(out, x, tw, ti, expert_map=em)
@@ -457,16 +475,18 @@ def test_fused_moe_kblock_ragged(dev, monkeypatch, activation, T):
     _close(out, _oracle_layer(cfg, w, x, tw, ti))
 
 
+@pytest.mark.parametrize("activation", ["silu", "swigluoai"])
 @pytest.mark.parametrize("T", [8, 32, 48, 96, 500, 1024])
-def test_fused_moe_kblock_fp8_families(dev, monkeypatch, T):
+def test_fused_moe_kblock_fp8_families(dev, monkeypatch, T, activation):
     """fp8 block-scaled weights K-blocked in 128-byte blocks (H=384, I=256,
     8 experts, top-2: about T/4 slots per expert): stream (T=8), small
     (32, 48), 128-slot 8-wave (96, 500) and 320-slot (1024) kernels each give
     the row-major layer's output bit for bit, within the fp8 bar of the
-    oracle."""
+    oracle; swigluoai (interleaved rows, read as gate / up halves with
+    64-row scale blocks) through the same kernels."""
     import dataclasses
     cfg = dataclasses.replace(_W().CONFIGS["C2"], recipe="fp8block", hidden=384, inter=256,
-                              experts=8, topk=2)
+                              experts=8, topk=2, activation=activation)
     (cfg, w, x, tw, ti, out, _), out_nk = _layer_both_layouts(cfg, T, dev, monkeypatch)
     assert torch.equal(out, out_nk)
     _close(out, _oracle_layer(cfg, w, x, tw, ti), fp8=True)
@@ -546,8 +566,7 @@ def test_fused_moe_mxfp4_wide_skewed(dev, hot):
     ti = torch.stack([first, second], 1).to(torch.int32).to(dev)
     tw = torch.rand(T, 2, generator=g) + 0.1
     tw = (tw / tw.sum(1, keepdim=True)).to(dev)
-    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
-                      cfg.topk, cfg.activation, cfg.experts)
+    moe = XpuFusedMoe(*w.layer_args(copy=True), cfg.topk, cfg.activation, cfg.experts)
     assert moe._w_layout == 1
     out = torch.empty_like(x)
     moe.apply(out, x, tw, ti)
@@ -605,8 +624,8 @@ def test_fused_moe_generic_activation_clamp(dev):
         w = W.make_weights(cfg, dev)
         x = W.make_activations(cfg, 40, dev) * 30
         tw, ti = W.route(cfg, W.make_router_logits(cfg, 40, dev))
-        moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
-                          cfg.topk, act, cfg.experts, gemm1_clamp_limit=0.5)
+        moe = XpuFusedMoe(*w.layer_args(copy=True), cfg.topk, act, cfg.experts,
+                          gemm1_clamp_limit=0.5)
         out = torch.empty_like(x)
         moe.apply(out, x, tw, ti)
         ref = _oracle_layer(cfg, w, x, tw, ti)
@@ -643,8 +662,7 @@ def test_fused_moe_fp16(dev, recipe, T):
                             w13_bias=w.w13_bias.to(h), w2_bias=w.w2_bias.to(h))
     x = W.make_activations(cfg, T, dev).to(h)
     tw, ti = W.route(cfg, W.make_router_logits(cfg, T, dev))
-    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
-                      cfg.topk, cfg.activation, cfg.experts)
+    moe = XpuFusedMoe(*w.layer_args(copy=True), cfg.topk, cfg.activation, cfg.experts)
     out = torch.empty_like(x)
     moe.apply(out, x, tw, ti)
     toks = torch.linspace(0, T - 1, min(T, 48)).long().to(dev)
@@ -1124,27 +1142,99 @@ def test_fused_moe_hip_graph_replays(dev, T):
         del junk
 
 
-@pytest.mark.parametrize("name,E", [("C1", None), ("C3", 16), ("C5", 8)])
+IN_PLACE = "MI355MOE_PREPARE_IN_PLACE"
+
+
+@pytest.mark.parametrize("name,E", [("C1", None), ("C3", 16), ("C5", 8), ("C2-int4", 8),
+                                    ("C3-mxfp8", 16), ("C3-fp8", 16)])
 def test_fused_moe_prepare_in_place(dev, monkeypatch, name, E):
-    """MI355MOE_PREPARE_IN_PLACE=1: the prepared w13 / w2 replace the storage
-    of the caller's tensors (the weights are held once, as the reference
-    does for its int4 weights); the layer's output equals the default
-    preparation's bit for bit, and a second layer on the same tensors is
-    refused."""
+    """The default preparation writes the converted weights (and the mxfp4,
+    mxfp8 and int4 scales) over the caller's tensors, one expert at a time:
+    the layer's weights share their storage, those tensors keep shape and
+    dtype, the prepared bytes and the output (T=64) equal those of
+    MI355MOE_PREPARE_IN_PLACE=0 (a converted copy, the caller's tensors left
+    as they were) bit for bit; a second layer on the same tensors and
+    arguments reuses the preparation, one with other arguments is refused."""
     import dataclasses
     from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
-    cfg = _W().CONFIGS[name]
+    W = _W()
+    cfg = W.config(name)
     if E is not None:
         cfg = dataclasses.replace(cfg, experts=E)
-    cfg, w, x, tw, ti, out, _ = _layer(cfg, 64, dev)
-    w13, w2 = w.w13.clone(), w.w2.clone()
-    monkeypatch.setenv("MI355MOE_PREPARE_IN_PLACE", "1")
-    moe = XpuFusedMoe(w13, w.w13_scale, w.w13_bias, w2, w.w2_scale, w.w2_bias,
-                      cfg.topk, cfg.activation, cfg.experts)
-    assert w13.data_ptr() == moe.w13.data_ptr() and w2.data_ptr() == moe.w2.data_ptr()
-    out2 = torch.empty_like(out)
-    moe.apply(out2, x, tw, ti)
-    assert torch.equal(out2, out)
-    with pytest.raises(ValueError, match="prepared in place"):
-        XpuFusedMoe(w13, w.w13_scale, w.w13_bias, w2, w.w2_scale, w.w2_bias,
-                    cfg.topk, cfg.activation, cfg.experts)
+    w = W.make_weights(cfg, dev)
+    x = W.make_activations(cfg, 64, dev)
+    bias = W.make_correction_bias(cfg, dev) if cfg.routing == "grouped_sigmoid" else None
+    tw, ti = W.route(cfg, W.make_router_logits(cfg, 64, dev), bias)
+    args = w.layer_args(copy=True)
+    snap = [None if t is None else t.clone() for t in args]
+
+    def layer(activation=cfg.activation):
+        return XpuFusedMoe(*args, cfg.topk, activation, cfg.experts)
+
+    def run(moe):
+        out = torch.full_like(x, float("nan"))
+        moe.apply(out, x, tw, ti)
+        return out
+
+    monkeypatch.setenv(IN_PLACE, "0")
+    moe0 = layer()
+    out0 = run(moe0)
+    for t, t0 in zip(args, snap):
+        assert t is None or torch.equal(t.view(torch.uint8), t0.view(torch.uint8))
+    monkeypatch.delenv(IN_PLACE)
+    moe = layer()
+    assert moe.w13.data_ptr() == args[0].data_ptr() and moe.w2.data_ptr() == args[3].data_ptr()
+    for t, t0 in zip(args, snap):
+        assert t is None or (t.shape == t0.shape and t.dtype == t0.dtype)
+    for a0, a1 in ((moe0.w13, moe.w13), (moe0.w2, moe.w2),
+                   (moe0.gemm1_wei_scales, moe.gemm1_wei_scales),
+                   (moe0.gemm2_wei_scales, moe.gemm2_wei_scales)):
+        assert (a0 is None) == (a1 is None)
+        if a0 is not None:
+            assert a0.shape == a1.shape and a0.dtype == a1.dtype
+            assert torch.equal(a0.view(torch.uint8), a1.view(torch.uint8))
+    out = run(moe)
+    assert torch.equal(out, out0)
+    moe2 = layer()
+    assert moe2.w13.data_ptr() == moe.w13.data_ptr()
+    assert torch.equal(run(moe2), out0)
+    with pytest.raises(ValueError, match="other arguments"):
+        layer("gelu" if cfg.activation != "gelu" else "silu")
+
+
+def test_fused_moe_c3_weights_held_once(dev, monkeypatch):
+    """DeepSeek-V3 (C3: 256 experts, fp8 block-scaled, 11.3 GB of weights):
+    constructing the layer grows torch.cuda.memory_allocated() by at most 1%
+    of the weight bytes (the transient peak: at most 2%), and its output at
+    T=64 equals that of a layer holding a converted copy
+    (MI355MOE_PREPARE_IN_PLACE=0) bit for bit."""
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    W = _W()
+    cfg = W.CONFIGS["C3"]
+    w = W.make_weights(cfg, dev)
+    x = W.make_activations(cfg, 64, dev)
+    tw, ti = W.route(cfg, W.make_router_logits(cfg, 64, dev), W.make_correction_bias(cfg, dev))
+    nbytes = sum(t.numel() * t.element_size() for t in w.layer_args() if t is not None)
+    assert nbytes > 11e9
+
+    def run(moe):
+        out = torch.full_like(x, float("nan"))
+        moe.apply(out, x, tw, ti)
+        torch.cuda.synchronize()
+        return out
+
+    monkeypatch.setenv(IN_PLACE, "0")
+    moe0 = XpuFusedMoe(*w.layer_args(), cfg.topk, cfg.activation, cfg.experts)
+    out0 = run(moe0)
+    del moe0
+    monkeypatch.delenv(IN_PLACE)
+    torch.cuda.synchronize()
+    m0 = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    moe = XpuFusedMoe(*w.layer_args(), cfg.topk, cfg.activation, cfg.experts)
+    torch.cuda.synchronize()
+    grown, peak = torch.cuda.memory_allocated() - m0, torch.cuda.max_memory_allocated() - m0
+    print(f"C3 weights {nbytes / 1e9:.2f} GB: layer construction grew allocated memory by "
+          f"{grown / 1e6:.1f} MB, peak {peak / 1e6:.1f} MB", flush=True)
+    assert grown <= 0.01 * nbytes and peak <= 0.02 * nbytes
+    assert torch.equal(run(moe), out0)

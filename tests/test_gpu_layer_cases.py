@@ -123,8 +123,8 @@ def test_fused_moe_clamp_limit_mxfp4_swigluoai(dev, T):
     w = W.make_weights(cfg, dev)
     x = W.make_activations(cfg, T, dev) * 16
     tw, ti = W.route(cfg, W.make_router_logits(cfg, T, dev))
-    moe = _layer_cls()(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias, cfg.topk,
-                       "swigluoai", cfg.experts, gemm1_clamp_limit=3.0)
+    moe = _layer_cls()(*w.layer_args(copy=True), cfg.topk, "swigluoai", cfg.experts,
+                       gemm1_clamp_limit=3.0)
     out = torch.empty_like(x)
     moe.apply(out, x, tw, ti)
     toks = torch.linspace(0, T - 1, min(T, 48)).long().to(dev)

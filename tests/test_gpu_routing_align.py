@@ -165,6 +165,31 @@ def test_fused_grouped_topk_without_bias(dev):
     assert torch.equal(ids, rids) and torch.equal(v, rv)
 
 
+@pytest.mark.parametrize("name,T", [("C2", 4096), ("C4", 2048), ("C5", 4096), ("C3", 8192)])
+def test_route_full_size_bit_exact(dev, name, T):
+    """Each configuration's router at its prefill size on the benchmark's own
+    logits (C4 Zipf-skewed): every token's expert ids equal the oracle's bit
+    for bit, the weights within fp32 ulps.  C3 scores with the sigmoid the
+    reference's caller applies (tests/ops/grouped_topk_op.py:67-92), taken
+    from the device as the oracle's input."""
+    from vllm_xpu_kernels import workloads as W
+    cfg = W.CONFIGS[name]
+    logits = W.make_router_logits(cfg, T, dev)
+    bias = W.make_correction_bias(cfg, dev) if cfg.routing == "grouped_sigmoid" else None
+    tw, ti = W.route(cfg, logits, bias)
+    if cfg.routing == "grouped_sigmoid":
+        s = logits.sigmoid()
+        sb = s + bias.unsqueeze(0)
+        rw, rids = O.grouped_topk(s.cpu(), sb.cpu(), cfg.n_group, cfg.topk_group, cfg.topk,
+                                  cfg.renormalize, cfg.routed_scaling_factor)
+        tol = 4e-6
+    else:
+        rw, rids, _ = O.topk_softmax(logits.cpu(), cfg.topk, cfg.renormalize)
+        tol = 2e-6
+    assert torch.equal(ti.cpu(), rids)
+    torch.testing.assert_close(tw.cpu(), rw.float(), rtol=tol, atol=1e-7)
+
+
 def test_grouped_topk_full_size_invariants(dev):
     """T=8192 (C3 prefill): every id lies in one of the 4 kept groups and the
     kept groups are the top-4 by top-2 sums; ids unique per token."""

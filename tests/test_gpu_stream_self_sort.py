@@ -52,8 +52,7 @@ def _layer_call(cfg, T, dev, dt=torch.bfloat16, ids_dtype=torch.int32, ti=None, 
         bias = W.make_correction_bias(cfg, dev) if cfg.routing == "grouped_sigmoid" else None
         tw, ti = W.route(cfg, W.make_router_logits(cfg, T, dev), bias)
     ti = ti.to(ids_dtype)
-    moe = XpuFusedMoe(w.w13, w.w13_scale, w.w13_bias, w.w2, w.w2_scale, w.w2_bias,
-                      cfg.topk, cfg.activation, cfg.experts)
+    moe = XpuFusedMoe(*w.layer_args(copy=True), cfg.topk, cfg.activation, cfg.experts)
     kw = {} if expert_map is None else {"expert_map": expert_map}
     if prequant:
         xq, xs = ops.per_token_group_fp8_quant(x, 128)

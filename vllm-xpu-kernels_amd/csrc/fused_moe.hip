@@ -604,6 +604,8 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     MI_ARG(H % 128 == 0 && I % 128 == 0,
            "fp8 block-scaled weights need hidden and intermediate sizes % 128 == 0");
     MI_ARG(a->w13_scale && a->w2_scale, "fp8 block-scaled weights need scales");
+    MI_ARG(a->w13_scale_rows == 0 || a->w13_scale_rows == 128 || a->w13_scale_rows == 64,
+           "w13_scale_rows must be 128 or 64");
   } else if (recipe == MI355MOE_RECIPE_INT4) {
     const int64_t g = a->w_group;
     MI_ARG(g == 32 || g == 64 || g == 128 || g == 256,
@@ -750,6 +752,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.w_kblock = kblock;
   g1.out_f16 = f16;
   g1.w_group = static_cast<int32_t>(a->w_group);
+  g1.ws_rows64 = recipe == MI355MOE_RECIPE_FP8BLOCK && a->w13_scale_rows == 64;
   g1.expert_scale = recipe == MI355MOE_RECIPE_BF16 || is_w8a16_recipe(recipe)
                         ? static_cast<const float*>(a->w13_scale)
                         : nullptr;

@@ -52,7 +52,8 @@ struct GemmArgs {
   const void* A;
   const float* a_scale;  // fp8: [rowsA, K/128]
   const void* B;         // [E, ldb_rows, K] (mxfp4: K/2 bytes per row)
-  const void* b_scale;   // fp8: f32 [E, ldb_rows/128, K/128]; mxfp4: u8 [E, ldb_rows, K/32]
+  const void* b_scale;   // fp8: f32 [E, ldb_rows/128, K/128] (or /64, ws_rows64);
+                         // mxfp4: u8 [E, ldb_rows, K/32]
   const uint16_t* bias;  // [E, ldb_rows] bf16 or null
   void* D;
   const int32_t* row_ids;
@@ -93,6 +94,10 @@ struct GemmArgs {
   // 16-bit type: D = T(s_e * sum_k A W_e + bias_e)).
   const float* expert_scale;
   int32_t w_group;       // recipe INT4: K values per 16-bit scale (32..256)
+  // recipe FP8BLOCK: 1 = b_scale [E, ldb_rows/64, K/128], one scale row per
+  // 64 weight rows (the split gate / up halves of an interleaved swigluoai
+  // w13, whose 128-row blocks each held 64 gates and their 64 ups); 0 = 128
+  int32_t ws_rows64;
   // MX recipes: e8m0 activation scales u8, row r's 32-K group g at
   // a_mxs[r * a_mxs_ld + g] (a_mxs_ld >= K/32; a multiple of 4 where a kernel
   // moves them four at a time); the w13 epilogue of the fused layer writes

@@ -237,7 +237,8 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
           wf[0][j][0] = kBatchX || wok[j] ? p[0] : make_uint4(0, 0, 0, 0);
           wf[0][j][1] = kBatchX || wok[j] ? p[1] : make_uint4(0, 0, 0, 0);
           const float* bs = static_cast<const float*>(a.b_scale);
-          wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wrow[j] / 128) *
+          const int wsh = 7 - a.ws_rows64;  // weight rows per scale row: 128 or 64
+          wsc[j] = bs[(static_cast<int64_t>(e) * (a.ldb_rows >> wsh) + (wrow[j] >> wsh)) *
                           (K / 128) + k0 / 128];
         } else if constexpr (kW8) {  // K % 32 == 0: a chunk lies wholly in or past K
           const int64_t kc = k0 + 32 * q < K ? k0 + 32 * q : K - 32;

@@ -193,13 +193,14 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
     else
       wtile_row[i] = 128 * wn + 32 * i;
   }
-  // fp8 weight-block scales of the 4 n-tiles (128-row blocks)
+  // fp8 weight-block scale rows of the 4 n-tiles
   const float* bsc = static_cast<const float*>(a.b_scale);
+  const int wsh = 7 - a.ws_rows64;  // 32-row sub-tiles sit inside one 128- or 64-row block
   int64_t wsc_row[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     bool ok;
-    wsc_row[i] = tile_wrow(wtile_row[i], n0, kGlu, a.up_off, N, ok) / 128;
+    wsc_row[i] = tile_wrow(wtile_row[i], n0, kGlu, a.up_off, N, ok) >> wsh;
   }
 
   const int nk = static_cast<int>((K + KE - 1) / KE);
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(256, 1) void moe_gemm_big_kernel(const GemmArgs a,
       float ws[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        ws[i] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsc_row[i]) * (K / 128) +
+        ws[i] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows >> wsh) + wsc_row[i]) * (K / 128) +
                     k0 / 128];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {

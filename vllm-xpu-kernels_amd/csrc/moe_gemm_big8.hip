@@ -137,7 +137,7 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES];
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
-  __shared__ float s_wsc[2][MAX_KBLK];  // weight-block scales of the tile's two row blocks
+  __shared__ float s_wsc[4][MAX_KBLK];  // weight-block scales of the tile's four 64-row quarters
   __shared__ float s_amax[4][BM];       // QOUT: per-wave-column row maxima
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -179,10 +179,11 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
   };
   {
     const float* bsc = static_cast<const float*>(a.b_scale);
-    for (int i = tid; i < 2 * nkb; i += 512) {
+    const int wsh = 7 - a.ws_rows64;  // weight rows per scale row: 128 or 64
+    for (int i = tid; i < 4 * nkb; i += 512) {
       const int t = i / nkb, kb = i % nkb;
-      const int64_t wr = wrow_of(128 * t) / 128;
-      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wr) * nkb + kb];
+      const int64_t wr = wrow_of(64 * t) >> wsh;
+      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows >> wsh) + wr) * nkb + kb];
     }
   }
   __syncthreads();
@@ -247,10 +248,11 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
       wo[c] = A_BYTES + rw * ROWB + ((ch ^ swz(rw)) << 4);
     }
   }
-  // weight-block row of tile i (s_wsc index)
+  // s_wsc quarter of weight tile i: GLU tile rows 128 (i / 2) + 32 wn + 16 (i % 2),
+  // STORE 64 wn + 16 i
   int wblk[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wblk[i] = kGlu ? (i >> 1) : (wn >> 1);
+  for (int i = 0; i < 4; ++i) wblk[i] = kGlu ? 2 * (i >> 1) + (wn >> 1) : wn;
 
   f32x4_t acc[4][4];
 #pragma unroll

@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
   __shared__ float s_amax[2][128];
-  __shared__ float s_wsc[4][MAX_KBLK];  // fp8: weight-block scales of the 4 tile row blocks
+  __shared__ float s_wsc[4][MAX_KBLK];  // fp8: weight-block scales of the tile's four 64-row quarters
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -107,14 +107,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   };
   if constexpr (kFp8) {
-    // tile row blocks: non-GLU rows [0,128),[128,256) -> n0/128 + {0,1};
-    // GLU gate block n0/128 and up block (up_off + n0)/128
+    // the scale rows of tile rows 64 t .. 64 t + 63 (t < 4): non-GLU weight
+    // rows n0 + 64 t; GLU gate rows n0 + 64 t (t < 2), up rows up_off + n0 +
+    // 64 (t - 2); one scale row per 128 weight rows, or per 64 (ws_rows64)
     const int nkb = static_cast<int>(K / 128);
     const float* bsc = static_cast<const float*>(a.b_scale);
-    for (int i = tid; i < 2 * nkb; i += 256) {
+    const int wsh = 7 - a.ws_rows64;
+    for (int i = tid; i < 4 * nkb; i += 256) {
       const int t = i / nkb, kb = i % nkb;
-      const int64_t wr = wrow_of(128 * t) / 128;
-      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wr) * nkb + kb];
+      const int64_t wr = wrow_of(64 * t) >> wsh;
+      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows >> wsh) + wr) * nkb + kb];
     }
   }
   __syncthreads();
@@ -208,7 +210,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const float* xsc = reinterpret_cast<const float*>(Ws + W_BYTES);
       float ws[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ws[i] = s_wsc[wtile_row[i] >> 7][kt];
+      for (int i = 0; i < 4; ++i) ws[i] = s_wsc[wtile_row[i] >> 6][kt];  // 32-row tiles: one quarter
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int m = 64 * wm + 32 * j + l32;

@@ -251,10 +251,13 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const uint8_t* xsp8 = kMx ? a.a_mxs + static_cast<int64_t>(xok ? arow : 0) * a.a_mxs_ld
                             : nullptr;
 
-  // fp8 weight-block scale rows (16-row sub-tiles sit inside one 128-row block)
+  // fp8 weight-block scale rows (16-row sub-tiles sit inside one 128- or
+  // 64-row block)
+  const int wsh = 7 - a.ws_rows64;
+  const int64_t wsrows = a.ldb_rows >> wsh;
   int64_t wsr[2];
-  wsr[0] = (wrow[0] / 128);
-  wsr[1] = (wrow[1] / 128);
+  wsr[0] = wrow[0] >> wsh;
+  wsr[1] = wrow[1] >> wsh;
 
   const float* bsc = static_cast<const float*>(a.b_scale);
   const int64_t xsrow = static_cast<int64_t>(xok ? arow : 0) * (K / 128);
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         const uint8_t* p = (t ? wp1 : wp0) + (k0 >> 7) * wst.kblk + 32 * q;
         f.w[t][0] = *reinterpret_cast<const uint4*>(p);
         f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
-        f.ws[t] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wsr[t]) * (K / 128) + k0 / 128];
+        f.ws[t] = bsc[(static_cast<int64_t>(e) * wsrows + wsr[t]) * (K / 128) + k0 / 128];
       }
       if constexpr (SELF8) {  // the split's activation tile in LDS
         const int64_t kk = k0 - kx0;

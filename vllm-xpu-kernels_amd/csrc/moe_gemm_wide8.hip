@@ -137,7 +137,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
   __shared__ uint32_t s_woff[BN];       // byte offset of tile weight row r in the expert
-  __shared__ float s_wsc[2][MAX_KBLK];  // weight-block scales of the tile's two row blocks
+  __shared__ float s_wsc[4][MAX_KBLK];  // weight-block scales of the tile's four 64-row quarters
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
@@ -182,10 +182,11 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
   if (tid < BN) s_woff[tid] = static_cast<uint32_t>(wrow_of(tid) * wst.row);
   {
     const float* bsc = static_cast<const float*>(a.b_scale);
-    for (int i = tid; i < 2 * nkb; i += 512) {
+    const int wsh = 7 - a.ws_rows64;  // weight rows per scale row: 128 or 64
+    for (int i = tid; i < 4 * nkb; i += 512) {
       const int t = i / nkb, kb = i % nkb;
-      const int64_t wr = wrow_of(128 * t) / 128;
-      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wr) * nkb + kb];
+      const int64_t wr = wrow_of(64 * t) >> wsh;
+      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows >> wsh) + wr) * nkb + kb];
     }
   }
   // valid slots form a prefix of the block
@@ -262,10 +263,11 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
   const int xo1 = mx * ROWB + (((2 * g + 1) ^ swz(mx)) << 4);
   const int wo0 = A_BYTES + rw * ROWB + (((2 * g) ^ swz(rw)) << 4);
   const int wo1 = A_BYTES + rw * ROWB + (((2 * g + 1) ^ swz(rw)) << 4);
-  // weight-block row of tile i (s_wsc index)
+  // s_wsc quarter of weight tile i: GLU tile rows 128 (i / 2) + 32 wn + 16 (i % 2),
+  // STORE 64 wn + 16 i
   int wblk[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wblk[i] = kGlu ? (i >> 1) : (wn >> 1);
+  for (int i = 0; i < 4; ++i) wblk[i] = kGlu ? 2 * (i >> 1) + (wn >> 1) : wn;
   // activation tiles of this wave holding valid slots
   const int vw = v - (BM / 2) * wm;
   const int nj = vw <= 0 ? 0 : (vw >= BM / 2 ? TJ : (vw + 15) / 16);

@@ -138,7 +138,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   __shared__ __attribute__((aligned(1024))) uint8_t lds[MX ? RING_MX : RING];
   __shared__ int s_arow[BM];
   __shared__ int s_drow[BM];
-  __shared__ float s_wsc[2][MAX_KBLK];    // block scales of the tile's two row blocks
+  __shared__ float s_wsc[4][MAX_KBLK];    // block scales of the tile's four 64-row quarters
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -181,10 +181,11 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   };
   if constexpr (!MX) {
     const float* bsc = static_cast<const float*>(a.b_scale);
-    for (int i = tid; i < 2 * nkb; i += 512) {
+    const int wsh = 7 - a.ws_rows64;  // weight rows per scale row: 128 or 64
+    for (int i = tid; i < 4 * nkb; i += 512) {
       const int t = i / nkb, kb = i % nkb;
-      const int64_t wr = wrow_of(128 * t) / 128;
-      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows / 128) + wr) * nkb + kb];
+      const int64_t wr = wrow_of(64 * t) >> wsh;
+      s_wsc[t][kb] = bsc[(static_cast<int64_t>(e) * (a.ldb_rows >> wsh) + wr) * nkb + kb];
     }
   }
   const int v = __syncthreads_count(ok);  // valid slots form a prefix of the block
@@ -349,9 +350,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   const int xc0 = MX ? g : 2 * g, xc1 = MX ? g + 4 : 2 * g + 1;  // logical chunks
   const int xo0 = xr * KE + ((xc0 ^ swz(xr)) << 4);
   const int xo1 = xr * KE + ((xc1 ^ swz(xr)) << 4);
-  // s_wsc row of fragment f: GLU gate / up block; STORE the block of rows
-  // 32 wave .. 32 wave + 31
-  const int wsel0 = kGlu ? 0 : (wave >> 2), wsel1 = kGlu ? 1 : (wave >> 2);
+  // s_wsc quarter of fragment f: GLU tile rows 16 wave (gate) and 128 +
+  // 16 wave (up); STORE rows 32 wave .. 32 wave + 31
+  const int wsel0 = kGlu ? (wave >> 2) : (wave >> 1), wsel1 = kGlu ? 2 + (wave >> 2) : (wave >> 1);
   // slot tiles holding valid slots, rounded up to pairs
   const int njv = (v + 15) / 16;
   const int nj = njv <= 0 ? 0 : (njv >= TJ ? TJ : ((njv + 1) & ~1));

@@ -820,7 +820,8 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
                      const std::optional<at::Tensor>& w2_bias, int64_t recipe,
                      int64_t activation, int64_t inter_size, double clamp_limit,
                      const std::optional<at::Tensor>& expert_map, int64_t w_layout,
-                     const std::optional<at::Tensor>& hidden_scale, int64_t w_group) {
+                     const std::optional<at::Tensor>& hidden_scale, int64_t w_group,
+                     int64_t w13_scale_rows) {
   check_gpu(output, "output");
   check_gpu(hidden_states, "hidden_states");
   // packed e2m1 hidden states (mxfp4 with a1q_scale) hold two values a byte
@@ -865,6 +866,17 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
                     w13_scale->numel() == w13.size(0) && w2_scale->numel() == w2.size(0),
                 "per-expert fp8 weights need float32 scales [num_experts]");
   }
+  if (recipe == MI355MOE_RECIPE_FP8BLOCK) {
+    const int64_t rows = w13_scale_rows ? w13_scale_rows : 128;
+    TORCH_CHECK(rows == 128 || rows == 64, "w13_scale_rows must be 128 or 64");
+    TORCH_CHECK(w13_scale && w2_scale && w13_scale->scalar_type() == at::kFloat &&
+                    w2_scale->scalar_type() == at::kFloat && w13_scale->is_contiguous() &&
+                    w2_scale->is_contiguous(),
+                "fp8 block-scaled weights need contiguous float32 scales");
+    TORCH_CHECK(w13_scale->numel() == w13.size(0) * (2 * inter_size / rows) * (hidden / 128),
+                "w13_scale must be float32 [num_experts, 2 * inter_size / ", rows,
+                ", hidden_size / 128]");
+  }
   TORCH_CHECK(topk_weights.scalar_type() == at::kFloat, "topk_weights must be float32");
   TORCH_CHECK(topk_weights.sizes() == topk_ids.sizes(),
               "topk_weights must have the shape of topk_ids");
@@ -908,6 +920,7 @@ void mi355_fused_moe(at::Tensor& output, const at::Tensor& hidden_states,
   a.w_layout = static_cast<int>(w_layout);
   a.hidden_scale = hidden_scale ? hidden_scale->data_ptr() : nullptr;
   a.w_group = w_group;
+  a.w13_scale_rows = w13_scale_rows;
   for (const auto* b : {&w13_bias, &w2_bias})
     if (b->has_value())
       TORCH_CHECK((*b)->scalar_type() == output.scalar_type(),
@@ -994,7 +1007,7 @@ TORCH_LIBRARY(_moe_C, m) {
         "Tensor topk_ids, Tensor w13, Tensor? w13_scale, Tensor? w13_bias, Tensor w2, "
         "Tensor? w2_scale, Tensor? w2_bias, int recipe, int activation, int "
         "inter_size, float clamp_limit, Tensor? expert_map, int w_layout=0, "
-        "Tensor? hidden_scale=None, int w_group=0) -> ()");
+        "Tensor? hidden_scale=None, int w_group=0, int w13_scale_rows=0) -> ()");
   m.def("mi355_pack_weights_kblock(Tensor src, Tensor! dst) -> ()");
   m.def("mi355_fused_grouped_topk(Tensor gating_output, Tensor? bias, int n_group, "
         "int topk_group, int topk, bool renormalize, float routed_scaling_factor) -> "

@@ -34,7 +34,8 @@ class FusedMoeArgs(ctypes.Structure):
                 ("swiglu_limit", ctypes.c_float), ("output", ctypes.c_void_p),
                 ("w_layout", ctypes.c_int),
                 ("hidden_scale", ctypes.c_void_p),
-                ("w_group", ctypes.c_int64)]
+                ("w_group", ctypes.c_int64),
+                ("w13_scale_rows", ctypes.c_int64)]
 
 
 lib.mi355moe_fused_moe_workspace_size.restype = ctypes.c_size_t
@@ -126,6 +127,7 @@ def fused_args(moe, output, hidden_states, topk_weights, topk_ids,
     a.output = output.data_ptr()
     a.w_layout = layout
     a.w_group = moe._w_group
+    a.w13_scale_rows = moe._ws_rows
     return a
 
 

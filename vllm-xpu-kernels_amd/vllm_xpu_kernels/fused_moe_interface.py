@@ -41,9 +41,13 @@ _ACT_CODES = {"silu": ACT_SILU, "swigluoai": ACT_SWIGLUOAI, "gelu": ACT_GELU,
               "relu2_no_mul": ACT_RELU2}
 WLAYOUT_NK, WLAYOUT_KBLOCK = 0, 1
 WEIGHT_LAYOUT_ENV = "MI355MOE_WEIGHT_LAYOUT"
-# 1: the prepared w13 / w2 replace the storage of the caller's tensors (as the
-# reference does for its int4 weights, fused_moe_interface.py:195-205), so the
-# weights are not held twice; those tensors then hold the prepared layout
+# Default "1": the prepared weights (w13 / w2 and their mxfp4, mxfp8 and int4
+# scales) are written over the caller's tensors, one expert at a time, so the
+# weights are held once and the transient is one expert's bytes (the
+# reference rewrites its int4 weights in place too, fused_moe_interface.py:
+# 195-205).  Those tensors keep their shape and dtype but hold the prepared
+# layout; a later XpuFusedMoe on them with the same arguments reuses it.
+# "0" leaves the caller's tensors untouched and keeps a converted copy.
 PREPARE_IN_PLACE_ENV = "MI355MOE_PREPARE_IN_PLACE"
 
 
@@ -107,6 +111,31 @@ def pack_weights_kblock(w: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _prepare(src: torch.Tensor, steps, in_place: bool) -> torch.Tensor:
+    """Apply `steps` (maps of expert slices [e, ...] to their prepared
+    layout) to src.  in_place: one expert at a time, each result written back
+    over that expert's own bytes (every step keeps an expert's byte count),
+    so the result shares src's storage; else a new tensor."""
+    def run(t):
+        for f in steps:
+            t = f(t)
+        return t.contiguous()
+    if not in_place or not src.is_contiguous() or src.numel() == 0:
+        return run(src)
+    E = src.shape[0]
+    flat = src.view(torch.uint8).reshape(E, -1)
+    shape = dtype = None
+    for e in range(E):
+        p = run(src[e:e + 1])
+        pb = p.view(torch.uint8).reshape(-1)
+        if pb.numel() != flat.shape[1]:
+            raise AssertionError("a weight preparation step changed an expert's size")
+        if pb.data_ptr() != flat[e].data_ptr():
+            flat[e].copy_(pb)
+        shape, dtype = p.shape[1:], p.dtype
+    return flat.view(dtype).view(E, *shape)
+
+
 def _kblock32(w: torch.Tensor) -> torch.Tensor:
     """1-byte weights [E, N, K] -> [E, K/32, N, 32] (K % 32 == 0)."""
     E, N, K = w.shape
@@ -120,6 +149,13 @@ def pack_scales_kblock(s: torch.Tensor) -> torch.Tensor:
     out = torch.empty((E, KB, N), dtype=s.dtype, device=s.device)
     torch.ops._moe_C.mi355_pack_scales_kblock(s.contiguous(), out)
     return out
+
+
+# what _prepare_weights sets: a layer built on tensors prepared in place
+# takes these from the layer that prepared them
+_PREPARED_STATE = ("w13", "w2", "gemm1_wei_scales", "gemm2_wei_scales", "w13_bias",
+                   "w2_bias", "_w_group", "_ws_rows", "_w_layout", "_kblock",
+                   "_w8_recipe", "_w8_layout")
 
 
 class XpuFusedMoe:
@@ -190,17 +226,30 @@ class XpuFusedMoe:
             raise NotImplementedError(
                 f"{REF_FUSED_MOE_ENV}=1 (torch reference path) is not provided "
                 "by the MI355X build; the HIP kernels are the only path")
-        if getattr(w13, "mi355moe_prepared", False) or getattr(w2, "mi355moe_prepared", False):
-            raise ValueError(
-                f"w13 / w2 already hold weights prepared in place ({PREPARE_IN_PLACE_ENV}=1) "
-                "by another XpuFusedMoe; construct a layer once per weight tensor")
-        self._prepare_weights(w13, w13_scales, w13_bias, w2, w2_scales, w2_bias)
-        if _is_env_enabled(PREPARE_IN_PLACE_ENV):
-            for src, prepared in ((w13, self.w13), (w2, self.w2)):
-                if src.data_ptr() != prepared.data_ptr():
-                    src.data = prepared
-                src.mi355moe_prepared = True
-            self.w13, self.w2 = w13, w2
+        # tensors an earlier layer prepared in place carry that preparation:
+        # it is reused when every argument that shapes it is the same
+        key = (self._recipe, self._fp8_expert, self._act, self.inter_size,
+               os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower(),
+               _is_env_enabled(FP8_W8A16_ENV, "1"),
+               bool(getattr(w13, "xpu_fused_moe", False)),
+               tuple(None if t is None else (t.data_ptr(), tuple(t.shape), t.dtype)
+                     for t in (w13, w13_scales, w13_bias, w2, w2_scales, w2_bias)))
+        prev = [getattr(t, "mi355moe_prepared", None) for t in (w13, w2)]
+        if prev[0] is not None or prev[1] is not None:
+            if prev[0] is not prev[1] or prev[0][0] != key:
+                raise ValueError(
+                    "w13 / w2 hold weights another XpuFusedMoe prepared in place "
+                    f"({PREPARE_IN_PLACE_ENV}=1) with other arguments; pass the "
+                    "original tensors")
+            self.__dict__.update(prev[0][1])
+            self._w16_cache, self._bias_cache = {}, {}
+        else:
+            in_place = _is_env_enabled(PREPARE_IN_PLACE_ENV, "1")
+            self._prepare_weights(w13, w13_scales, w13_bias, w2, w2_scales, w2_bias,
+                                  in_place)
+            if in_place:
+                state = (key, {k: getattr(self, k) for k in _PREPARED_STATE})
+                w13.mi355moe_prepared = w2.mi355moe_prepared = state
 
         self.expert_map = expert_map
         if self.expert_map is None and self.ep_size > 1:
@@ -215,104 +264,123 @@ class XpuFusedMoe:
         self.local_experts_num = self.num_experts
 
     # ------------------------------------------------------------------
-    def _prepare_weights(self, w13, s13, b13, w2, s2, b2):
+    def _prepare_weights(self, w13, s13, b13, w2, s2, b2, in_place=False):
+        """Convert the reference layouts into the kernels' (see the module
+        docstring); in_place: over the caller's tensors, one expert at a
+        time."""
         I = self.inter_size
         K2 = I * self.inter_size_scale
         E = w13.shape[0]
         swiglu = self._act == ACT_SWIGLUOAI
+        tr = lambda t: t.transpose(1, 2).contiguous()  # noqa: E731
+        u8 = lambda t: t.view(torch.uint8)  # noqa: E731
+        # per-tensor steps, each a map of expert slices [e, ...] that keeps an
+        # expert's byte count
+        f13, f2, fs13, fs2 = [], [], [], []
         self._w_group = 0
+        self._ws_rows = 128
         if self._recipe == RECIPE_INT4:
             # u4 with zero point 8 -> two's-complement int4 (the reference's
             # implement_zp, :135-163, is (u4 - 8) & 0xF = u4 ^ 8 per nibble);
             # weights the reference already converted carry `xpu_fused_moe`
-            w13c, w2c = w13.view(torch.uint8), w2.view(torch.uint8)
+            f13 = [u8]
             if not getattr(w13, "xpu_fused_moe", False):
-                w13c, w2c = w13c ^ 0x88, w2c ^ 0x88
-            s13c, s2c = s13.contiguous(), s2.contiguous()
-            self._w_group = (w13c.shape[2] * 2) // s13c.shape[-1]
-            if (K2 // s2c.shape[-1]) != self._w_group:
+                f13 = [u8, lambda t: t ^ 0x88]
+            f2 = list(f13)
+            self._w_group = (w13.shape[2] * 2) // s13.shape[-1]
+            if (K2 // s2.shape[-1]) != self._w_group:
                 raise ValueError("w13 and w2 int4 scales must use one group size")
         elif self._fp8_expert:
             # reference layout [E, K, N] -> [E, N, K], kept in fp8 (read as
             # such by the decode kernels, K-blocked by 128 where the sizes
             # allow; exact 16-bit copies are made for larger calls)
-            w13c = w13.transpose(1, 2).contiguous()
-            w2c = w2.transpose(1, 2).contiguous()
-            s13c = s13.to(torch.float32).reshape(E).contiguous()
-            s2c = s2.to(torch.float32).reshape(E).contiguous()
+            f13, f2 = [tr], [tr]
         elif self._recipe == RECIPE_BF16:
             if w13.dtype not in (torch.bfloat16, torch.float16):
                 raise NotImplementedError("16-bit weights must be bfloat16 or float16")
-            # reference layout [E, K, N] -> [E, N, K]
-            w13c = w13.transpose(1, 2).contiguous()
-            w2c = w2.transpose(1, 2).contiguous()
-            s13c = s2c = None
+            f13, f2 = [tr], [tr]      # reference layout [E, K, N] -> [E, N, K]
         elif self._recipe == RECIPE_MXFP8:
             # reference layout (moe_utils.py:80-82): w [E, K, N] e4m3 with e8m0
             # scales [E, K/32, N] -> [E, N, K] and [E, N, K/32]
-            w13c = w13.transpose(1, 2).contiguous()
-            w2c = w2.transpose(1, 2).contiguous()
-            s13c = s13.view(torch.uint8).transpose(1, 2).contiguous()
-            s2c = s2.view(torch.uint8).transpose(1, 2).contiguous()
+            f13, f2 = [tr], [tr]
+            fs13, fs2 = [u8, tr], [u8, tr]
         elif self._recipe == RECIPE_FP8BLOCK:
             # [E, N, K] preferred when ambiguous, as the reference
             # (grouped_gemm_xe2_interface.hpp:206-223)
-            w13c = w13 if w13.shape[1] == 2 * I else w13.transpose(1, 2).contiguous()
-            w2c = w2 if w2.shape[2] == K2 else w2.transpose(1, 2).contiguous()
-            s13c, s2c = s13.contiguous(), s2.contiguous()
-            if swiglu:
-                raise NotImplementedError(
-                    "swigluoai with 128x128 fp8 block scales is not supported")
+            f13 = [] if w13.shape[1] == 2 * I else [tr]
+            f2 = [] if w2.shape[2] == K2 else [tr]
         else:
-            w13c = w13.view(torch.uint8)
-            w2c = w2.view(torch.uint8)
-            s13c = s13.view(torch.uint8) if s13.dtype != torch.uint8 else s13
-            s2c = s2.view(torch.uint8) if s2.dtype != torch.uint8 else s2
-        # biases keep their 16-bit type; apply() converts them to the call's
-        b13c = _bias16(b13)
-        b2c = _bias16(b2)
+            f13, f2, fs13, fs2 = [u8], [u8], [u8], [u8]
         if swiglu:
-            w13c = _deinterleave_rows(w13c, 1)
-            if s13c is not None and not self._fp8_expert:
-                s13c = _deinterleave_rows(s13c, 1)
-            if b13c is not None:
-                b13c = _deinterleave_rows(b13c, 1)
-        assert w13c.shape[0] == E and w13c.shape[1] == 2 * I
-        H = w13c.shape[2]
-        self._w_layout = WLAYOUT_NK
+            # gate / up rows interleaved -> [gate; up] halves
+            f13.append(lambda t: _deinterleave_rows(t, 1))
+            if not self._fp8_expert and self._recipe != RECIPE_FP8BLOCK:
+                fs13.append(lambda t: _deinterleave_rows(t, 1))
+        # hidden size: K of w13 ([E, 2I, H/2] packed 4-bit, [E, 2I, H] or
+        # [E, H, 2I] fp8 block, [E, H, 2I] otherwise)
         if self._recipe in (RECIPE_MXFP4, RECIPE_INT4):
-            H = w13c.shape[2] * 2
+            H = w13.shape[2] * 2
+        elif self._recipe == RECIPE_FP8BLOCK and w13.shape[1] == 2 * I:
+            H = w13.shape[2]
+        else:
+            H = w13.shape[1]
+        self._w_layout = WLAYOUT_NK
         kblock = ((self._recipe == RECIPE_BF16 and H % 32 == 0 and I % 32 == 0) or
                   (self._recipe == RECIPE_FP8BLOCK and H <= 8192 and K2 <= 8192) or
                   (self._recipe == RECIPE_MXFP8 and H % 128 == 0 and K2 % 128 == 0) or
                   self._recipe in (RECIPE_MXFP4, RECIPE_INT4))
         self._kblock = kblock and os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk"
         if self._kblock and not self._fp8_expert:
-            w13c, w2c = pack_weights_kblock(w13c), pack_weights_kblock(w2c)
+            f13.append(pack_weights_kblock)
+            f2.append(pack_weights_kblock)
             if self._recipe in (RECIPE_MXFP4, RECIPE_MXFP8):
-                s13c, s2c = pack_scales_kblock(s13c), pack_scales_kblock(s2c)
+                fs13.append(pack_scales_kblock)
+                fs2.append(pack_scales_kblock)
             elif self._recipe == RECIPE_INT4:
                 # 16-bit group scales [E, N, K/group] -> [E, K/group, N]
-                s13c = s13c.transpose(1, 2).contiguous()
-                s2c = s2c.transpose(1, 2).contiguous()
+                fs13.append(tr)
+                fs2.append(tr)
             self._w_layout = WLAYOUT_KBLOCK
         if self._fp8_expert and self._kblock:
             self._w_layout = WLAYOUT_KBLOCK   # applies to the 16-bit copies
         self._w8_recipe = None
         self._w8_layout = WLAYOUT_NK
         if self._fp8_expert and H % 32 == 0 and K2 % 32 == 0:
-            self._w8_recipe = (RECIPE_FP8E5M2 if w13c.dtype == torch.float8_e5m2
+            self._w8_recipe = (RECIPE_FP8E5M2 if w13.dtype == torch.float8_e5m2
                                else RECIPE_FP8)
             if os.environ.get(WEIGHT_LAYOUT_ENV, "kblock").lower() != "nk":
                 # K blocks of 32 bytes, [E, K/32, N, 32]: one 32-byte block
                 # per lane in the STREAM / SMALL kernels, a 32-value stage of
                 # 256 rows one 8 KB run in the 320-slot kernel
-                w13c, w2c = _kblock32(w13c), _kblock32(w2c)
+                f13.append(_kblock32)
+                f2.append(_kblock32)
                 self._w8_layout = WLAYOUT_KBLOCK
-        self._w16_cache = {}
-        self.w13, self.w2 = w13c.contiguous(), w2c.contiguous()
+        self.w13 = _prepare(w13, f13, in_place)
+        self.w2 = _prepare(w2, f2, in_place)
+        if self._fp8_expert:
+            s13c = s13.to(torch.float32).reshape(E).contiguous()
+            s2c = s2.to(torch.float32).reshape(E).contiguous()
+        elif self._recipe == RECIPE_BF16:
+            s13c = s2c = None
+        elif self._recipe == RECIPE_FP8BLOCK:
+            s13c, s2c = s13.contiguous(), s2.contiguous()
+            if swiglu:
+                # 128-row scale block b of the interleaved rows holds gates and
+                # ups j in [64 b, 64 b + 64): after the split, row n of either
+                # half has scale row n / 64 of that half, so the kernels read
+                # [E, 2I/64, K/128] scales (each half a copy of the original)
+                s13c = torch.cat([s13c, s13c], dim=1)
+                self._ws_rows = 64
+        else:
+            s13c = _prepare(s13, fs13, in_place)
+            s2c = _prepare(s2, fs2, in_place)
         self.gemm1_wei_scales, self.gemm2_wei_scales = s13c, s2c
-        self.w13_bias, self.w2_bias = b13c, b2c
+        # biases keep their 16-bit type; apply() converts them to the call's
+        b13c = _bias16(b13)
+        if swiglu and b13c is not None:
+            b13c = _deinterleave_rows(b13c, 1)
+        self.w13_bias, self.w2_bias = b13c, _bias16(b2)
+        self._w16_cache = {}
         self._bias_cache = {}
 
     def _fp8_rows(self, w):
@@ -419,7 +487,7 @@ class XpuFusedMoe:
             output, hidden_states, topk_weights.to(torch.float32).contiguous(),
             topk_ids.contiguous(), w13, s13, b13, w2, s2, b2,
             recipe, self._act, self.inter_size, clamp, expert_map,
-            layout, a1q_scale, self._w_group)
+            layout, a1q_scale, self._w_group, self._ws_rows)
         return output
 
 

@@ -155,6 +155,13 @@ class MoeWeights:
     w2_scale: Optional[torch.Tensor]
     w2_bias: Optional[torch.Tensor]
 
+    def layer_args(self, copy: bool = False):
+        """(w13, w13_scale, w13_bias, w2, w2_scale, w2_bias) for XpuFusedMoe;
+        copy: new tensors, so that these keep the reference layouts (a layer
+        prepares its weights over the tensors it is given)."""
+        ts = (self.w13, self.w13_scale, self.w13_bias, self.w2, self.w2_scale, self.w2_bias)
+        return tuple(None if t is None else t.clone() for t in ts) if copy else ts
+
 
 def act_width(cfg: MoeConfig) -> int:
     """Width of the activation, and K of w2: 2I for relu2_no_mul (no gate),
