@@ -301,13 +301,41 @@ REFERENCE_SCHEMAS = {
 }
 
 
+# arguments the reference's kernels write without a mutation annotation in
+# its schema: annotated here (Tensor(a!)), so that FakeTensor / functionalised
+# tracing keeps the writes (opcheck's schema check fails without them)
+WRITTEN_UNANNOTATED = {
+    "_moe_C::fused_moe_prologue": {"workspace"},
+    "_moe_C::init_expert_map": {"expert_map"},
+    "_moe_C::remap_hidden_states": {"remapped_hidden_states", "remapped_hidden_states_scales",
+                                    "rows_per_expert", "unpermuted_row_to_permuted_row"},
+    "_xpu_C::cutlass_grouped_gemm_interface": {"ptr_D", "<return>"},
+}
+
+
 @pytest.mark.parametrize("name", sorted(REFERENCE_SCHEMAS))
 def test_op_schemas_match_reference(name):
+    """Names, argument names, types, order and defaults as the reference's
+    registration; alias annotations too, except the writes it leaves
+    unannotated (WRITTEN_UNANNOTATED), which are annotated here."""
     import vllm_xpu_kernels  # noqa: F401
     ns, op = name.split("::")
-    packet = getattr(getattr(torch.ops, ns), op)
+    ours = getattr(getattr(torch.ops, ns), op).default._schema
     ref = torch._C.parse_schema(ns + "::" + REFERENCE_SCHEMAS[name])
-    assert str(packet.default._schema) == str(ref)
+    added = WRITTEN_UNANNOTATED.get(name, set())
+    if not added:
+        assert str(ours) == str(ref)
+        return
+    assert ours.name == ref.name and len(ours.arguments) == len(ref.arguments)
+    for a, b in zip(ours.arguments, ref.arguments):
+        assert (a.name, str(a.type), a.default_value) == (b.name, str(b.type), b.default_value)
+        if a.name in added:
+            assert b.alias_info is None and a.alias_info is not None and a.alias_info.is_write
+        else:
+            assert str(a.alias_info) == str(b.alias_info)
+    assert [str(r.type) for r in ours.returns] == [str(r.type) for r in ref.returns]
+    if "<return>" in added:
+        assert ours.returns[0].alias_info.is_write
 
 
 def test_no_cpu_kernel_registered():
@@ -509,3 +537,31 @@ def test_mx_recipe_selection(monkeypatch):
                   torch.zeros(3, H // 2, dtype=torch.uint8), torch.zeros(3, 1),
                   torch.zeros(3, 1, dtype=torch.int32),
                   a1q_scale=torch.zeros(3, H // 32, dtype=torch.uint8))
+
+
+def test_every_op_has_a_meta_kernel():
+    """Every op of the _moe_C, _C and _xpu_C namespaces has a Meta kernel
+    (FakeTensor tracing, torch.compile): on meta tensors the in-place ops
+    return nothing and the grouped GEMM returns its output argument, the
+    routers [T, k] values and int32 ids."""
+    from vllm_xpu_kernels import _ops  # noqa: F401
+    names = sorted({n.split(".")[0] for n in torch._C._dispatch_get_all_op_names()
+                    if n.partition("::")[0] in ("_moe_C", "_C", "_xpu_C")})
+    assert len(names) >= 25
+    missing = [n for n in names if not torch._C._dispatch_has_kernel_for_dispatch_key(n, "Meta")]
+    assert not missing, missing
+    m = torch.device("meta")
+    d = torch.empty(16, 256, dtype=torch.bfloat16, device=m)
+    out = torch.ops._xpu_C.cutlass_grouped_gemm_interface(
+        torch.empty(16, 512, dtype=torch.bfloat16, device=m), None,
+        torch.empty(3, 512, 256, dtype=torch.bfloat16, device=m), None, None, d,
+        torch.empty(3, dtype=torch.int32, device=m), 256, 512, 3)
+    assert out is d
+    v, i = torch.ops._moe_C.mi355_fused_grouped_topk(
+        torch.empty(33, 256, device=m), None, 8, 4, 8, True, 2.5)
+    assert v.shape == i.shape == (33, 8) and i.dtype == torch.int32
+    v, i = torch.ops._moe_C.grouped_topk(torch.empty(5, 64, device=m),
+                                         torch.empty(5, 64, device=m), 1, 1, 6, True, 1.0)
+    assert v.shape == (5, 6) and i.dtype == torch.int32
+    assert torch.ops._C.silu_and_mul(torch.empty(4, 8, device=m),
+                                     torch.empty(4, 16, device=m)) is None

@@ -207,11 +207,32 @@ std::tuple<at::Tensor, at::Tensor> mi355_fused_grouped_topk(
   return {vals, ids};
 }
 
+// ------------------------------------------------------------ meta kernels
+// Shape functions for FakeTensor tracing (torch.compile, opcheck): the ops
+// that only write into the caller's outputs change no metadata, so their
+// meta kernel consumes the arguments and returns nothing; the ops that return
+// tensors give them their shapes (symbolic sizes allowed).
+void meta_noop(const c10::OperatorHandle& op, torch::jit::Stack* stack) {
+  const size_t n = op.schema().arguments().size();
+  stack->erase(stack->end() - static_cast<std::ptrdiff_t>(n), stack->end());
+}
+
 std::tuple<at::Tensor, at::Tensor> grouped_topk_meta(
     at::Tensor& scores, at::Tensor&, int64_t, int64_t, int64_t topk, bool,
     double) {
-  auto vals = at::empty({scores.size(0), topk}, scores.options());
-  auto ids = at::empty({scores.size(0), topk}, scores.options().dtype(at::kInt));
+  auto vals = at::empty_symint({scores.sym_size(0), c10::SymInt(topk)}, scores.options());
+  auto ids = at::empty_symint({scores.sym_size(0), c10::SymInt(topk)},
+                              scores.options().dtype(at::kInt));
+  return {vals, ids};
+}
+
+std::tuple<at::Tensor, at::Tensor> fused_grouped_topk_meta(
+    const at::Tensor& gating_output, const std::optional<at::Tensor>&, int64_t, int64_t,
+    int64_t topk, bool, double) {
+  auto vals = at::empty_symint({gating_output.sym_size(0), c10::SymInt(topk)},
+                               gating_output.options());
+  auto ids = at::empty_symint({gating_output.sym_size(0), c10::SymInt(topk)},
+                              gating_output.options().dtype(at::kInt));
   return {vals, ids};
 }
 
@@ -682,6 +703,13 @@ void silu_and_mul_mxfp4_quant(at::Tensor& out, const at::Tensor& input, at::Tens
 }
 
 // ------------------------------------------------------------- grouped GEMM
+at::Tensor grouped_gemm_meta(at::Tensor&, const std::optional<at::Tensor>&, at::Tensor&,
+                             const std::optional<at::Tensor>&,
+                             const std::optional<at::Tensor>&, at::Tensor& ptr_D, at::Tensor&,
+                             int64_t, int64_t, int64_t) {
+  return ptr_D;  // written in place and returned
+}
+
 at::Tensor cutlass_grouped_gemm_interface(at::Tensor& ptr_A,
                                           const std::optional<at::Tensor>& ptr_A_scale,
                                           at::Tensor& ptr_B,
@@ -993,14 +1021,14 @@ TORCH_LIBRARY(_moe_C, m) {
   m.def("moe_gather(Tensor! output, Tensor moe_output, Tensor topk_weights, "
         "Tensor unpermuted_row_to_permuted_row, int num_experts) -> ()");
   m.def("fused_moe_prologue(Tensor input, Tensor? input_scales, Tensor "
-        "token_selected_experts, Tensor token_final_scales, Tensor workspace, int "
+        "token_selected_experts, Tensor token_final_scales, Tensor! workspace, int "
         "hidden_size, int inter_size, int block_k, int ep_rank, int ep_size,int "
         "num_experts_on_rank) -> ()");
-  m.def("init_expert_map(Tensor expert_map, int num_experts, int ep_rank, int "
+  m.def("init_expert_map(Tensor! expert_map, int num_experts, int ep_rank, int "
         "ep_size) -> ()");
   m.def("remap_hidden_states(Tensor hidden_states, Tensor? hidden_states_scales, "
-        "Tensor remapped_hidden_states, Tensor? remapped_hidden_states_scales, "
-        "Tensor? expert_map, Tensor rows_per_expert, Tensor "
+        "Tensor! remapped_hidden_states, Tensor(b!)? remapped_hidden_states_scales, "
+        "Tensor? expert_map, Tensor! rows_per_expert, Tensor! "
         "unpermuted_row_to_permuted_row, Tensor topk_ids, int total_experts_num, "
         "int local_experts_num) -> ()");
   m.def("mi355_fused_moe(Tensor! output, Tensor hidden_states, Tensor topk_weights, "
@@ -1033,7 +1061,16 @@ TORCH_LIBRARY_IMPL(_moe_C, CUDA, m) {
   m.impl("mi355_pack_scales_kblock", &mi355_pack_scales_kblock);
 }
 
-TORCH_LIBRARY_IMPL(_moe_C, Meta, m) { m.impl("grouped_topk", &grouped_topk_meta); }
+TORCH_LIBRARY_IMPL(_moe_C, Meta, m) {
+  m.impl("grouped_topk", &grouped_topk_meta);
+  m.impl("mi355_fused_grouped_topk", &fused_grouped_topk_meta);
+  for (const char* op : {"moe_sum", "moe_align_block_size", "moe_lora_align_block_size",
+                         "topk_softmax", "topk_sigmoid", "topk_softplus_sqrt", "moe_gather",
+                         "fused_moe_prologue", "init_expert_map", "remap_hidden_states",
+                         "mi355_fused_moe", "mi355_pack_weights_kblock",
+                         "mi355_pack_scales_kblock"})
+    m.impl(op, torch::CppFunction::makeFromBoxedFunction<&meta_noop>());
+}
 
 TORCH_LIBRARY(_C, m) {
   m.def("silu_and_mul(Tensor! result, Tensor input) -> ()");
@@ -1069,12 +1106,26 @@ TORCH_LIBRARY_IMPL(_C, CUDA, m) {
   m.impl("per_token_group_quant_mxfp4", &per_token_group_quant_mxfp4);
 }
 
+TORCH_LIBRARY_IMPL(_C, Meta, m) {
+  for (const char* op : {"silu_and_mul", "swigluoai_and_mul", "per_token_group_fp8_quant",
+                         "silu_and_mul_per_block_quant", "gelu_and_mul", "gelu_tanh_and_mul",
+                         "relu2_no_mul", "swiglustep_and_mul", "silu_and_mul_mxfp4_quant",
+                         "per_token_group_quant_mxfp4"})
+    m.impl(op, torch::CppFunction::makeFromBoxedFunction<&meta_noop>());
+}
+
 TORCH_LIBRARY(_xpu_C, m) {
+  // the reference's schema (csrc/xpu/torch_bindings.cpp:46-49) with the write
+  // to ptr_D, and the returned alias of it, annotated
   m.def("cutlass_grouped_gemm_interface(Tensor ptr_A, Tensor? ptr_A_scale, "
-        "Tensor ptr_B, Tensor? ptr_B_scale, Tensor? ptr_bias, Tensor ptr_D, "
-        "Tensor rows_per_expert, int N, int K, int num_experts) -> Tensor");
+        "Tensor ptr_B, Tensor? ptr_B_scale, Tensor? ptr_bias, Tensor(a!) ptr_D, "
+        "Tensor rows_per_expert, int N, int K, int num_experts) -> Tensor(a!)");
 }
 
 TORCH_LIBRARY_IMPL(_xpu_C, CUDA, m) {
   m.impl("cutlass_grouped_gemm_interface", &cutlass_grouped_gemm_interface);
+}
+
+TORCH_LIBRARY_IMPL(_xpu_C, Meta, m) {
+  m.impl("cutlass_grouped_gemm_interface", &grouped_gemm_meta);
 }
