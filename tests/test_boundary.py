@@ -435,12 +435,35 @@ def test_fused_moe_noalloc_rejects_calls_beyond_its_scratch(lib):
     from vllm_xpu_kernels import capi
     a = capi.FusedMoeArgs(recipe=1, activation=0, act_dtype=1, ids_dtype=3,
                           num_tokens=8192, hidden=7168, inter=2048, num_experts=256,
-                          topk=8, w_layout=1)
+                          topk=8, w_layout=1, w13_scale=1, w2_scale=1)
     lib.mi355moe_fused_moe_noalloc.argtypes = [ctypes.POINTER(capi.FusedMoeArgs),
                                                ctypes.c_void_p]
     rc = lib.mi355moe_fused_moe_noalloc(ctypes.byref(a), None)
     assert rc == -4
     assert b"more than the static" in lib.mi355moe_last_error()
+
+
+@pytest.mark.parametrize("field,value,message", [
+    ("num_tokens", -1, b"invalid layer shape"), ("topk", 0, b"invalid layer shape"),
+    ("num_experts", 2048, b"at most 1024"), ("hidden", 7100, b"% 128"),
+    ("w13_scale", None, b"need scales"), ("w_layout", 7, b"unknown weight layout"),
+    ("recipe", 9, b"unknown recipe"), ("ids_dtype", 1, b"int32 or int64")])
+def test_fused_moe_noalloc_validates_before_sizing(lib, field, value, message):
+    """The allocation-free entry checks its arguments before they size the
+    scratch: invalid ones return MI355MOE_ERR_INVALID (-1) with the same
+    message as the workspace entry, also when the shape would need more than
+    the static scratch."""
+    from vllm_xpu_kernels import capi
+    kw = dict(recipe=1, activation=0, act_dtype=1, ids_dtype=3, num_tokens=8192, hidden=7168,
+              inter=2048, num_experts=256, topk=8, w_layout=1, w13_scale=1, w2_scale=1)
+    kw[field] = value
+    a = capi.FusedMoeArgs(**kw)
+    lib.mi355moe_fused_moe_noalloc.argtypes = [ctypes.POINTER(capi.FusedMoeArgs),
+                                               ctypes.c_void_p]
+    assert lib.mi355moe_fused_moe_noalloc(ctypes.byref(a), None) == -1
+    assert message in lib.mi355moe_last_error()
+    rc = lib.mi355moe_fused_moe(ctypes.byref(a), None, ctypes.c_size_t(0), None)
+    assert rc == -1 and message in lib.mi355moe_last_error()
 
 
 @pytest.mark.parametrize("weight_layout", ["nk", "kn"])
@@ -565,3 +588,18 @@ def test_every_op_has_a_meta_kernel():
     assert v.shape == (5, 6) and i.dtype == torch.int32
     assert torch.ops._C.silu_and_mul(torch.empty(4, 8, device=m),
                                      torch.empty(4, 16, device=m)) is None
+
+
+@pytest.mark.parametrize("scoring", ["sigmoid", "softmax"])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fused_grouped_topk_bias_optional_on_both_paths(scoring, with_bias):
+    """Both scoring paths take e_score_correction_bias=None (no correction)
+    and give float32 weights and int32 ids [T, k] (meta tensors: shapes only,
+    through the ops' meta kernels)."""
+    from vllm_xpu_kernels import ops
+    m = torch.device("meta")
+    bias = torch.empty(256, device=m) if with_bias else None
+    v, i = ops.fused_grouped_topk(torch.empty(7, 256, device=m), 8, True, bias, 8, 4,
+                                  scoring, 2.5)
+    assert v.shape == i.shape == (7, 8)
+    assert v.dtype == torch.float32 and i.dtype == torch.int32

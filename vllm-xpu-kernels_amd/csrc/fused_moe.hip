@@ -475,6 +475,7 @@ extern "C" size_t mi355moe_fused_moe_workspace_size(const mi355moe_fused_moe_arg
 
 namespace mi355 {
 namespace {
+int validate(const mi355moe_fused_moe_args* a);
 int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
                    void* stream, hipEvent_t* ev);
 }
@@ -529,7 +530,7 @@ int scratch_address(hipStream_t stream, void** out) {
 }  // namespace
 
 extern "C" int mi355moe_fused_moe_noalloc(const mi355moe_fused_moe_args* a, void* stream) {
-  MI_ARG(a != nullptr, "null arguments");
+  if (int rc = validate(a)) return rc;   // before the arguments size anything
   const size_t need = mi355moe_fused_moe_workspace_size(a);
   MI_CHECK(need <= MI355MOE_NOALLOC_SCRATCH_BYTES, MI355MOE_ERR_WORKSPACE,
            "fused_moe_noalloc: this call needs " + std::to_string(need) +
@@ -582,8 +583,9 @@ extern "C" int mi355moe_timer_stage_ms(mi355moe_timer t, int step, float* ms) {
 
 namespace mi355 {
 namespace {
-int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
-                   void* stream, hipEvent_t* ev) {
+// Argument checks of the fused layer, before any sizing or launch (both
+// entry points): MI355MOE_OK or the error code, with the message set.
+int validate(const mi355moe_fused_moe_args* a) {
   MI_ARG(a != nullptr, "null arguments");
   const int64_t T = a->num_tokens, H = a->hidden, I = a->inter,
                 E = a->num_experts, k = a->topk;
@@ -641,6 +643,16 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
          "== 0), per-expert fp8, int4 or mxfp4");
   MI_ARG(!mx_layer(a) || epilogue_act(a->activation),
          "mxfp8 and pre-quantised mxfp4 layers support the silu and swigluoai activations");
+  return MI355MOE_OK;
+}
+
+int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
+                   void* stream, hipEvent_t* ev) {
+  if (int rc = validate(a)) return rc;
+  const int64_t T = a->num_tokens, H = a->hidden, I = a->inter, E = a->num_experts,
+                k = a->topk;
+  const int recipe = a->recipe;
+  const bool kblock = a->w_layout == MI355MOE_WLAYOUT_KBLOCK;
   if (T == 0) return MI355MOE_OK;
   FusedLayout L = plan(a, static_cast<uint8_t*>(ws));
   MI_CHECK(ws && ws_bytes >= L.bytes, MI355MOE_ERR_WORKSPACE,

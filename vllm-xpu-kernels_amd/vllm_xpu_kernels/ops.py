@@ -76,7 +76,9 @@ def fused_grouped_topk(gating_output: torch.Tensor, topk: int,
     """Score function + correction bias + grouped top-k (reference
     tests/ops/grouped_topk_op.py:67-92).  "sigmoid" runs as one kernel that
     forms scores and scores_with_bias itself (the same per-element roundings
-    as the torch ops); "softmax" keeps the caller-side torch.softmax."""
+    as the torch ops); "softmax" keeps the caller-side torch.softmax.  Both
+    take e_score_correction_bias=None as no correction (selection on the
+    scores themselves); the reference requires a bias."""
     if scoring_func == "sigmoid":
         bias = e_score_correction_bias
         if bias is not None:
@@ -89,7 +91,8 @@ def fused_grouped_topk(gating_output: torch.Tensor, topk: int,
         scores = torch.softmax(gating_output, dim=-1)
     else:
         raise ValueError(f"Unsupported scoring function: {scoring_func}")
-    swb = scores + e_score_correction_bias.unsqueeze(0)
+    swb = (scores if e_score_correction_bias is None
+           else scores + e_score_correction_bias.unsqueeze(0))
     v, i = grouped_topk(scores, swb.to(scores.dtype), num_expert_group,
                         topk_group, topk, renormalize, routed_scaling_factor)
     return v.to(torch.float32), i
