@@ -124,29 +124,36 @@ def host_cpu():
     return model, len(cores) or None, logical or os.cpu_count(), usable
 
 
-def cpu_baseline(cfg, w, x, tw, ti, n_tok, budget_s=20.0):
+def cpu_baseline(cfg, w, x, tw, ti, n_tok, budget_s=20.0, warmup=True):
     """Times the CPU oracle (torch on the host cores) on the first n_tok
-    tokens of the workload: 1 warm-up, then the median of up to 5 runs within
-    the budget."""
+    tokens of the workload (all of them: the whole timed batch): an optional
+    warm-up run, then the median of up to 5 runs within the budget (at least
+    one)."""
     from oracle import moe_oracle as O
+    T = x.shape[0]
     args = _oracle_inputs(cfg, w, x[:n_tok], tw[:n_tok], ti[:n_tok])
-    O.fused_moe(cfg.recipe, *args, activation=cfg.activation)
+    if warmup:
+        O.fused_moe(cfg.recipe, *args, activation=cfg.activation)
     times = []
     t_start = time.time()
-    while len(times) < 5 and (time.time() - t_start) < budget_s:
+    while len(times) < 5 and (not times or (time.time() - t_start) < budget_s):
         t0 = time.perf_counter()
         O.fused_moe(cfg.recipe, *args, activation=cfg.activation)
         times.append(time.perf_counter() - t0)
+        log(f"cpu baseline: {n_tok} tokens in {times[-1]:.2f} s")
     med = statistics.median(times)
     model, phys, logical, usable = host_cpu()
+    which = (f"all T={T} tokens of the timed batch" if n_tok == T
+             else f"the first {n_tok} of the timed batch's T={T} tokens")
     return {"value": n_tok / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{cfg.name} ({cfg.recipe}) first {n_tok} of the timed batch's tokens "
-                      f"(their {int(args[-1].max()) + 1} experts, weights dequantised per "
-                      f"expert inside the loop), oracle/moe_oracle.py fused_moe, median of "
-                      f"{len(times)} runs, {med * 1e3:.1f} ms per run; host {model}, "
-                      f"{phys} physical cores / {logical} logical CPUs, {usable} usable by "
-                      f"this process, torch threads {torch.get_num_threads()}"}
+            "sample": f"{cfg.name} ({cfg.recipe}) {which} (their {int(args[-1].max()) + 1} "
+                      f"experts, weights dequantised per expert inside the loop), "
+                      f"oracle/moe_oracle.py fused_moe, median of {len(times)} run(s)"
+                      f"{' after a warm-up run' if warmup else ' (weights already in host memory)'}"
+                      f", {med * 1e3:.1f} ms per run; host CPU {model}, {phys} physical cores / "
+                      f"{logical} logical CPUs, {usable} usable by this process, torch "
+                      f"threads {torch.get_num_threads()}"}
 
 
 ROTATE_BYTES = 512e6   # 2x the MI355X last-level cache (256 MB MALL)
@@ -458,7 +465,8 @@ def main():
     ap.add_argument("--config", default="C3")
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--cpu-tokens", type=int, default=0,
-                    help="tokens of the CPU-baseline sample (0: 16 for C3, else 64)")
+                    help="tokens of the CPU baseline (0: the whole batch); a 16-token "
+                         "sample is reported beside it")
     ap.add_argument("--sweep", default="default",
                     help="'none', 'default' or a list like C3:1,C3:8192")
     ap.add_argument("--no-graph", action="store_true")
@@ -499,11 +507,19 @@ def main():
     head = summarize(pt, ms, stages)
     log("headline:", json.dumps(head))
     roof = kernel_roofline(pt, stages, f"{args.config} T={args.tokens}")
+    head["kernel_roofline"] = roof
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
-        n_cpu = args.cpu_tokens or (16 if args.config == "C3" else 64)
-        cpu = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=min(n_cpu, args.tokens))
+        n_cpu = min(args.cpu_tokens or args.tokens, args.tokens)
+        # the whole batch once (about 20 s of host work at C3 T=8192), and a
+        # 16-token sample, median of up to 5 runs
+        cpu = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=n_cpu, budget_s=0.0,
+                           warmup=False)
+        if n_cpu > 16:
+            small = cpu_baseline(cfg, pt.w, pt.x, pt.tw, pt.ti, n_tok=16)
+            cpu["small_sample"] = {"value": small["value"], "unit": small["unit"],
+                                   "sample": small["sample"]}
         log("cpu baseline:", json.dumps(cpu))
 
     op_table = None
@@ -554,7 +570,8 @@ def main():
         "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights; random init)",
         "config": {"workload": f"{args.config} {cfg.name} fused MoE layer, T={args.tokens}",
                    "tokens": args.tokens, "hidden": cfg.hidden, "inter": cfg.inter,
-                   "experts": cfg.experts, "topk": cfg.topk, "recipe": cfg.recipe,
+                   "experts": cfg.experts, "active_experts": head["active_experts"],
+                   "topk": cfg.topk, "recipe": cfg.recipe,
                    "routing": cfg.routing, "graph": graph, "parallelism": "none (1 GPU)"},
         "layer_roofline_frac": head["roofline_frac"],
         "hbm_GBps": head["hbm_GBps"],
