@@ -127,7 +127,7 @@ def test_grouped_topk_deepseek_shape(dev, T, dtype, renorm):
     torch.testing.assert_close(v.cpu().float(), rv.float(), rtol=4e-6 if dtype == torch.float32 else 8e-3, atol=1e-7)
 
 
-@pytest.mark.parametrize("T", [1, 33, 8192])
+@pytest.mark.parametrize("T", [1, 33, 2051, 8192])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("E,n_group,topk_group,k", [(256, 8, 4, 8), (128, 4, 2, 6),
                                                     (512, 16, 8, 8), (256, 1, 1, 16),
@@ -137,9 +137,10 @@ def test_fused_grouped_topk_equals_torch_scoring(dev, T, dtype, E, n_group, topk
     """One-launch sigmoid + correction bias + grouped top-k equals the
     reference's caller-side torch ops followed by the grouped top-k op
     (tests/ops/grouped_topk_op.py:67-92) bit for bit: same ids, same values,
-    both against the oracle.  E 128 / 256 / 512 with n_group dividing 16 run
-    four tokens per wave; n_group 3 takes the serial group scan, 32 and E 64 /
-    96 the one-token-per-wave shuffle merge."""
+    both against the oracle.  From 2048 tokens (2051: a ragged last wave),
+    E 128 / 256 / 512 with n_group dividing 16 run four tokens per wave;
+    n_group 3 takes the serial group scan, 32 and E 64 / 96 the
+    one-token-per-wave shuffle merge."""
     g = torch.Generator(device=dev).manual_seed(T + E)
     logits = torch.randn(T, E, generator=g, device=dev).to(dtype)
     bias = torch.randn(E, generator=g, device=dev) * 0.01

@@ -319,12 +319,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
         f.ws[t] = bsc[(static_cast<int64_t>(e) * wsrows + wsr[t]) * (K / 128) + k0 / 128];
       }
-      if constexpr (SELF8) {  // the split's activation tile in LDS
-        const int64_t kk = k0 - kx0;
-        const uint8_t* px = s_xq + (xok ? arow : 0) * xrs + kk + 32 * q;
-        f.x[0] = *reinterpret_cast<const uint4*>(px);
-        f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
-        f.xs = s_xsc[(xok ? arow : 0) * (xrs / 128) + kk / 128];
+      if constexpr (SELF8) {
+        // the split's activation tile in LDS, read by compute(): the first
+        // stages' weights are requested before the tile is quantised
       } else {
         const uint8_t* px = xp + k0 + 32 * q;
         f.x[0] = *reinterpret_cast<const uint4*>(px);
@@ -408,6 +405,13 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         }
       }
     } else if constexpr (kFp8) {
+      if constexpr (SELF8) {
+        const int64_t kk = k0 - kx0;
+        const uint8_t* px = s_xq + (xok ? arow : 0) * xrs + kk + 32 * q;
+        f.x[0] = *reinterpret_cast<const uint4*>(px);
+        f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
+        f.xs = s_xsc[(xok ? arow : 0) * (xrs / 128) + kk / 128];
+      }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const f32x4 p = mma_fp8(f.w[t][0], f.w[t][1], f.x[0], f.x[1]);
@@ -442,7 +446,16 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   };
 
   // ---- K loop, PD stages in flight
+  FragT buf[PD];
+  auto prefetch = [&]() {
+    if (nk > 0) {
+#pragma unroll
+      for (int d = 0; d < PD; ++d)
+        load(buf[d], static_cast<int64_t>(s0 + (d < nk ? d : nk - 1)) * KS);
+    }
+  };
   if constexpr (SELF8) {
+    prefetch();  // the weights of the first stages, in flight while the tile is quantised
     // quantise the tile with the group quantiser itself: 16 lanes (8 values
     // each) per 128-value block; the trip count is uniform, lanes past the
     // end take part in the shuffles and store nothing
@@ -499,12 +512,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     }
     __syncthreads();
   }
-  FragT buf[PD];
-  if (nk > 0) {
-#pragma unroll
-    for (int d = 0; d < PD; ++d)
-      load(buf[d], static_cast<int64_t>(s0 + (d < nk ? d : nk - 1)) * KS);
-  }
+  if constexpr (!SELF8) prefetch();
   int kt = 0;
   // main part: every prefetch is in range, so no load sits in a branch
   for (; kt + 2 * PD <= nk; kt += PD) {
