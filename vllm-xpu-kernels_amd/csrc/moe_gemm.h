@@ -98,6 +98,11 @@ struct GemmArgs {
   // 64 weight rows (the split gate / up halves of an interleaved swigluoai
   // w13, whose 128-row blocks each held 64 gates and their 64 ups); 0 = 128
   int32_t ws_rows64;
+  // SMALL kernels, order of the (M-block, N-tile) pairs over the XCDs (set
+  // by the launcher): 1 = all N-tiles of an M-block on one XCD, -1 = spread
+  // round-robin, 0 = the first for 16-bit activations averaging 8 or more
+  // valid rows per block, else the second
+  int32_t xcd_order;
   // MX recipes: e8m0 activation scales u8, row r's 32-K group g at
   // a_mxs[r * a_mxs_ld + g] (a_mxs_ld >= K/32; a multiple of 4 where a kernel
   // moves them four at a time); the w13 epilogue of the fused layer writes

@@ -79,8 +79,29 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, q = lane >> 4;
-  const int blk = blockIdx.y;
-  if (blk * BM >= *a.ntp) return;  // uniform for the workgroup
+  int blk = blockIdx.y, ntile = blockIdx.x;
+  const int nblk = (*a.ntp + BM - 1) / BM;  // blocks holding valid slots
+  // Where the blocks hold enough 16-bit rows, XCD x (workgroups are
+  // dispatched round-robin over the 8 XCDs) takes the contiguous range
+  // [x*per, (x+1)*per) of the valid (block, N-tile) pairs in block-major
+  // order, so that one L2 serves a block's activation rows to all its
+  // N-tiles (C5 T=128 w2: 170 -> 144 MB fetched per launch, C2 T=256 -2 %);
+  // with e4m3 activations (C3 T=256 +1 %) or nearly empty blocks (C5 T=32
+  // w2 +5 %) the N-tiles stay spread over the XCDs
+  const bool xcd = a.xcd_order > 0 ||
+                   (a.xcd_order == 0 && XB == 2 && a.num_valid >= 8 * nblk);
+  if (xcd) {
+    const int n_tiles = static_cast<int>(gridDim.x);
+    const int valid = nblk * n_tiles;
+    const int lin = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+    const int per = (valid + 7) / 8;
+    const int tile = (lin & 7) * per + (lin >> 3);
+    if ((lin >> 3) >= per || tile >= valid) return;  // uniform
+    blk = tile / n_tiles;
+    ntile = tile - blk * n_tiles;
+  } else if (blk >= nblk) {
+    return;  // uniform for the workgroup
+  }
   const int e = a.block_expert[blk];
   const int64_t K = a.K;
   const int64_t wrow_bytes = kFp4 ? K / 2 : (kW8 ? K : K * XB);
@@ -92,7 +113,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
     s_drow[tid] = ok ? (a.d_by_pos ? blk * BM + tid : rid) : -1;
   }
 
-  const int64_t nbase = static_cast<int64_t>(blockIdx.x) * BN + wave * WN;
+  const int64_t nbase = static_cast<int64_t>(ntile) * BN + wave * WN;
   const uint8_t* wbase = static_cast<const uint8_t*>(a.B) +
                          static_cast<int64_t>(e) * a.ldb_rows * wrow_bytes;
   // weights (and mxfp4 scales) may be K-blocked
@@ -409,7 +430,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
                              fmaxf(s_amax[2][row], s_amax[3][row]));
       const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
       const float inv = 1.0f / sc;
-      if (wave == 0 && q == 0) ds[static_cast<int64_t>(drow) * ngroups + blockIdx.x] = sc;
+      if (wave == 0 && q == 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int64_t n = nbase + j * 16 + 4 * q;
@@ -453,12 +474,21 @@ template <int RECIPE, int BM, int EPI, bool QOUT>
 void launch_tile(const GemmArgs& a, int64_t max_blocks, void* qs,
                  hipStream_t st) {
   constexpr int BN = (BM == 16 && !QOUT) ? 64 : 128;
-  dim3 grid(static_cast<unsigned>(cdiv(a.N, BN)),
-            static_cast<unsigned>(max_blocks));
-  if (a.out_f16)
-    moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT, true><<<grid, dim3(256), 0, st>>>(a, qs);
+  GemmArgs b = a;
+  // MI355MOE_SMALL_XCD=1 / 0 forces the XCD order on / off (measurements);
+  // read per call
+  const char* xv = getenv("MI355MOE_SMALL_XCD");
+  b.xcd_order = !xv ? 0 : (xv[0] == '1' ? 1 : -1);
+  const int64_t nx = cdiv(a.N, BN);
+  // in the XCD order workgroup w takes tile (w % 8) * per + w / 8, per = the
+  // valid tiles / 8 rounded up: the launch covers a multiple of 8
+  // workgroups (those past max_blocks exit at once in the other order)
+  const int64_t ny = cdiv(cdiv(nx * max_blocks, 8) * 8, nx);
+  dim3 grid(static_cast<unsigned>(nx), static_cast<unsigned>(ny));
+  if (b.out_f16)
+    moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT, true><<<grid, dim3(256), 0, st>>>(b, qs);
   else
-    moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT, false><<<grid, dim3(256), 0, st>>>(a, qs);
+    moe_gemm_kernel<RECIPE, BM, BN, EPI, QOUT, false><<<grid, dim3(256), 0, st>>>(b, qs);
 }
 
 template <int RECIPE, int EPI, bool QOUT>
