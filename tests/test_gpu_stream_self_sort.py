@@ -9,7 +9,10 @@ the GPU (C3 shapes), w2 runs token-major and writes the layer output itself:
 bit for bit the top-k reduction launch's (MI355MOE_STREAM_TOKEN_W2=0).  (3)
 With a split-K w13 and a 16-bit activation (C2, C5), the w2 launch rebuilds
 its activation rows from the w13 partial tiles: bit for bit the w13
-finalize launch's (MI355MOE_STREAM_W2_FINISHES_W13=0)."""
+finalize launch's (MI355MOE_STREAM_W2_FINISHES_W13=0).  (4) An fp8 w13 that
+would split K runs in 64-column workgroups over both K halves instead and
+the token-major w2 quantises its activation rows
+(MI355MOE_STREAM_KHALVES=0)."""
 import dataclasses
 
 import pytest
@@ -181,6 +184,76 @@ def test_token_major_w2_matches_oracle(dev, T):
     _close(call(), _oracle_layer(cfg, w, x, tw, ti.long()), fp8=True)
 
 
+KHALVES = "MI355MOE_STREAM_KHALVES"
+
+
+def _c3_variant(dev, variant, T=1):
+    """C3-shaped decode layer calls for the fp8 decode paths."""
+    from vllm_xpu_kernels.fused_moe_interface import XpuFusedMoe
+    W = _W()
+    C3 = W.CONFIGS["C3"]
+    if variant == "T1":
+        return _layer_call(C3, T, dev)[0]
+    if variant == "fp16":
+        return _layer_call(C3, T, dev, dt=torch.float16)[0]
+    if variant == "int64_ids":
+        return _layer_call(C3, T, dev, ids_dtype=torch.int64)[0]
+    if variant == "prequant":
+        return _layer_call(C3, T, dev, prequant=True)[0]
+    if variant == "bias":
+        return _layer_call(dataclasses.replace(C3, bias=True), T, dev)[0]
+    if variant == "swigluoai":
+        return _layer_call(dataclasses.replace(C3, activation="swigluoai", bias=True), T, dev)[0]
+    if variant == "expert_map":
+        cfg = dataclasses.replace(C3, experts=32)
+        g = torch.Generator(device=dev).manual_seed(31)
+        ti = torch.randint(40, 120, (T, 8), generator=g, device=dev)
+        ti[0, :3] = torch.tensor([70, 70, 5], device=dev)
+        tw = torch.rand(T, 8, generator=g, device=dev)
+        emap = torch.full((256,), -1, dtype=torch.int32, device=dev)
+        emap[64:96] = torch.arange(32, dtype=torch.int32, device=dev)
+        return _layer_call(cfg, T, dev, ti=ti, tw=tw, expert_map=emap)[0]
+    assert variant == "clamp"
+    w = W.make_weights(C3, dev)
+    x = W.make_activations(C3, T, dev)
+    bias = W.make_correction_bias(C3, dev)
+    tw, ti = W.route(C3, W.make_router_logits(C3, T, dev), bias)
+    moe = XpuFusedMoe(*w.layer_args(copy=True), C3.topk, C3.activation, C3.experts,
+                      gemm1_clamp_limit=0.05)
+
+    def call():
+        out = torch.empty_like(x)
+        moe.apply(out, x, tw, ti)
+        return out
+    return call
+
+
+@pytest.mark.parametrize("variant", ["T1", "fp16", "int64_ids", "prequant", "bias",
+                                     "swigluoai", "expert_map", "clamp"])
+def test_khalves_bit_identical(dev, monkeypatch, variant):
+    """(4) fp8 decode whose w13 would split K: 64-column w13 workgroups over
+    both K halves store the 16-bit activation and every token-major w2 wave
+    quantises its own slot's row -- bit for bit the split launch, its
+    partial-sum launch and the w13 epilogue's quantisation
+    (MI355MOE_STREAM_KHALVES=0)."""
+    call = _c3_variant(dev, variant)
+    ref, got, again = _both(call, monkeypatch, KHALVES)
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, ref) and torch.equal(again, ref)
+
+
+@pytest.mark.parametrize("variant", ["T1", "bias", "swigluoai"])
+def test_khalves_matches_oracle(dev, variant):
+    from test_gpu_gemm_fused import _close, _oracle_layer_on_device
+    W = _W()
+    cfg = W.CONFIGS["C3"]
+    if variant != "T1":
+        cfg = dataclasses.replace(cfg, bias=True,
+                                  activation="swigluoai" if variant == "swigluoai" else "silu")
+    call, (cfg, w, x, tw, ti) = _layer_call(cfg, 1, dev)
+    _close(call(), _oracle_layer_on_device(cfg, w, x, tw, ti), fp8=True)
+
+
 W2_FIN = "MI355MOE_STREAM_W2_FINISHES_W13"
 
 
@@ -211,7 +284,7 @@ def test_w2_finishes_w13_bit_identical(dev, monkeypatch, variant):
     assert torch.equal(got, ref) and torch.equal(again, ref)
 
 
-ALL_OFF = ("MI355MOE_STREAM_SELF_SORT", TOKEN_W2, W2_FIN)
+ALL_OFF = ("MI355MOE_STREAM_SELF_SORT", TOKEN_W2, W2_FIN, KHALVES)
 
 
 @pytest.mark.parametrize("shape", ["tokw2_tail", "w2fin_tail"])

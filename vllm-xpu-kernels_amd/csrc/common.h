@@ -163,6 +163,21 @@ __device__ __forceinline__ uint32_t fp4_code(float x) {
   return c | (x < 0.f ? 0x8u : 0u);
 }
 
+// Maximum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15), in every
+// lane of the row: quad lane swaps (xor 1, xor 2), then the half-row and row
+// mirrors, each pairing a lane with one that holds the other half's
+// maximum.  All lanes of the row must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+}
+
 // e4m3 quantisation with one fp32 scale per 1 x 128 block, chunk c of 8
 // values (16 lanes per block, consecutive and aligned): amax from 1e-10,
 // scale = max(amax / 448, 1 / (448 * 512)), code = e4m3(clamp(v / scale))
@@ -170,13 +185,12 @@ __device__ __forceinline__ uint32_t fp4_code(float x) {
 // per_token_group_fp8_quant (group 128, eps 1e-10, fp8_max 448, no ue8m0).
 // Chunks >= `chunks` are inactive but take part in the block's shuffles;
 // all 64 lanes must be active.
+// fp8_quant_regs takes the chunk's 8 values already loaded (u).
 template <bool F16>
-__device__ __forceinline__ void fp8_quant_block8(const uint16_t* __restrict__ x,
-                                                 uint8_t* __restrict__ q,
-                                                 float* __restrict__ s, int64_t c,
-                                                 int64_t chunks) {
+__device__ __forceinline__ void fp8_quant_regs(const uint4 u, uint8_t* __restrict__ q,
+                                               float* __restrict__ s, int64_t c,
+                                               int64_t chunks) {
   const bool active = c < chunks;
-  const uint4 u = *reinterpret_cast<const uint4*>(x + (active ? c : 0) * 8);
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
   float v[8];
 #pragma unroll
@@ -188,7 +202,7 @@ __device__ __forceinline__ void fp8_quant_block8(const uint16_t* __restrict__ x,
   float amax = 1e-10f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  amax = row16_max(amax);
   const float ys = fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
   if (!active) return;
   if ((c & 15) == 0) s[c >> 4] = ys;
@@ -200,6 +214,14 @@ __device__ __forceinline__ void fp8_quant_block8(const uint16_t* __restrict__ x,
     if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
   }
   *reinterpret_cast<uint2*>(q + c * 8) = make_uint2(lo, hi);
+}
+template <bool F16>
+__device__ __forceinline__ void fp8_quant_block8(const uint16_t* __restrict__ x,
+                                                 uint8_t* __restrict__ q,
+                                                 float* __restrict__ s, int64_t c,
+                                                 int64_t chunks) {
+  const uint4 u = *reinterpret_cast<const uint4*>(x + (c < chunks ? c : 0) * 8);
+  fp8_quant_regs<F16>(u, q, s, c, chunks);
 }
 
 // ---------------------------------------------------------------------------

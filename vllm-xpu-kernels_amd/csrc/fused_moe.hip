@@ -338,6 +338,10 @@ struct FusedLayout {
   int64_t ld1, ld2;
   uint16_t* g1;   // generic activations: w13 output bf16 [max_padded, 2I]
   uint16_t* g2;   // bf16 [slots, H]
+  bool token_w2;  // STREAM w2 token-major: it writes the layer output
+  bool khalves;   // fp8 decode: w13 in K halves (no split launch) writes the
+                  // 16-bit activation act16, which the token-major w2 quantises
+  uint16_t* act16;  // [max_padded, K2]
   size_t bytes;
 };
 
@@ -397,6 +401,16 @@ bool stream_w2_finishes_w13_enabled() {
   const char* v = getenv("MI355MOE_STREAM_W2_FINISHES_W13");
   return !(v && v[0] == '0');
 }
+// fp8block decode whose w13 would split K (too few 128-column tiles to fill
+// the GPU) and whose w2 runs token-major: w13 runs 64-column workgroups over
+// both K halves (GemmArgs::khalves) and stores the 16-bit activation, which
+// each token-major w2 wave quantises for its own slot (GemmArgs::tok_xq) --
+// no partial-sum launch.  MI355MOE_STREAM_KHALVES=0 keeps the split launch
+// and its finalize (the same arithmetic).  Read per call.
+bool stream_khalves_enabled() {
+  const char* v = getenv("MI355MOE_STREAM_KHALVES");
+  return !(v && v[0] == '0');
+}
 
 FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   FusedLayout L{};
@@ -431,6 +445,15 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     const int64_t nt1 = glu ? cdiv(I, 128) : cdiv(2 * I, 256), nt2 = cdiv(H, 256);
     L.ks1 = stream_ksplit(nt1, act_blocks, H);
     L.ks2 = stream_ksplit(nt2, act_blocks, K2);
+    const int64_t T = a->num_tokens, k = a->topk;
+    L.token_w2 = L.ks2 <= 1 && L.slots <= 16 && k <= 8 && 8 % k == 0 &&
+                 cdiv(H, 32 * (8 / k)) * T >= 192 && stream_token_w2_enabled();
+    // (the w13 tile then quantises the whole K of every token: the LDS
+    // tile must hold it where the layer quantises its own activation)
+    L.khalves = L.token_w2 && L.ks1 > 1 && glu && a->recipe == MI355MOE_RECIPE_FP8BLOCK &&
+                K2 % 128 == 0 && K2 <= kStreamTokXBytes &&
+                (a->hidden_scale || T * H <= kStreamSelfXBytes) && stream_khalves_enabled();
+    if (L.khalves) L.ks1 = 1;
     const int64_t tile_f = 512 * 8;
     if (L.ks1 > 1) L.part1 = c.take<float>(L.max_blocks * nt1 * L.ks1 * tile_f);
     if (L.ks2 > 1) L.part2 = c.take<float>(L.max_blocks * nt2 * L.ks2 * tile_f);
@@ -459,6 +482,7 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
   }
   L.g1 = glu ? nullptr : c.take<uint16_t>(L.max_padded * 2 * I);
   L.g2 = c.take<uint16_t>(L.slots * a->hidden);
+  L.act16 = L.khalves ? c.take<uint16_t>(L.max_padded * K2) : nullptr;
   L.bytes = c.off + 256;
   return L;
 }
@@ -785,16 +809,18 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   }
   // decode: w2 writes the output token-major (C3 shapes), or rebuilds its
   // activation rows from the split-K w13 partials (16-bit activations)
-  const bool token_w2 = L.tile == TILE_STREAM && L.ks2 <= 1 && L.slots <= 16 && k <= 8 &&
-                        8 % k == 0 && cdiv(H, 32 * (8 / k)) * T >= 192 &&
-                        stream_token_w2_enabled();
+  const bool token_w2 = L.token_w2;
   const int64_t per2 = cdiv(cdiv(K2, 128), L.ks2 > 1 ? L.ks2 : 1);
   const bool w2_finishes_w13 = L.tile == TILE_STREAM && L.ks1 > 1 && glu && !fp8 && !mx &&
                                !token_w2 && 16 * per2 * 128 * 2 <= kStreamG1FinBytes &&
                                stream_w2_finishes_w13_enabled();
   g1.partials_only = w2_finishes_w13;
+  if (L.khalves) {
+    g1.khalves = 1;
+    g1.D = L.act16;
+  }
   if (glu) {
-    rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_GLU, fp8 || mx, g1, L.grid_blocks,
+    rc = launch_tile_gemm(L.tile, L.bm, grecipe, EPI_GLU, (fp8 && !L.khalves) || mx, g1, L.grid_blocks,
                           mx ? static_cast<void*>(L.acts8) : static_cast<void*>(L.acts), st);
     if (rc) return rc;
   } else {
@@ -860,6 +886,11 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     g2.g1f.act = g1.act;
   }
   if (token_w2) {
+    if (L.khalves) {  // each wave quantises its slot's 16-bit row
+      g2.A = L.act16;
+      g2.a_scale = nullptr;
+      g2.tok_xq = 1;
+    }
     g2.tok_inv = L.inv;
     g2.tok_w = a->topk_weights;
     g2.topk = static_cast<int32_t>(k);

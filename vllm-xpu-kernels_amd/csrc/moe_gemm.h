@@ -140,6 +140,16 @@ struct GemmArgs {
   const float* tok_w;
   int32_t topk;
   void* tok_out;
+  // Token-major w2, fp8block recipe: A is the 16-bit activation [rows, K]
+  // (no a_scale); each wave quantises its slot's row per 1 x 128 block with
+  // the group quantiser into LDS before its K loop (K <= kStreamTokXBytes).
+  int32_t tok_xq;
+  // STREAM w13 GLU without a split launch: the workgroup's 8 waves are 4
+  // groups of 16 activation columns (64 per workgroup) x 2 halves of the K
+  // stages; the upper half's sums are added to the lower half's through LDS
+  // (the split-K finalize's order), then the GLU epilogue stores the 16-bit
+  // activation.  Decode grids with too few 128-column tiles to fill the GPU.
+  int32_t khalves;
   // STREAM w2 of the fused layer (16-bit activation): its activation rows
   // rebuilt from the w13 partials (G1Fin) instead of read from A.
   G1Fin g1f;
@@ -147,6 +157,8 @@ struct GemmArgs {
 // LDS bytes a STREAM workgroup gives the in-kernel-quantised activation
 // (GemmArgs::sr_x): tokens x the split's K range, e4m3 (and 1 x 128 scales).
 constexpr int64_t kStreamSelfXBytes = 32768;
+// LDS bytes per wave for the token-major w2's quantised row (tok_xq).
+constexpr int64_t kStreamTokXBytes = 4096;
 
 // gemm1_clamp_limit on the (gate, up) pair of GLU output column n, both
 // already in the 16-bit type (the host rounds the limit to that type, so the

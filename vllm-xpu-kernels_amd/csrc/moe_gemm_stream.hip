@@ -169,7 +169,7 @@ __device__ __forceinline__ void write_routing(const GemmArgs& a, int tid, int nt
 }
 
 template <int RECIPE, int EPI, bool QOUT, int PD, bool F16, bool SELF8 = false,
-          bool TOKM = false, bool XL = false>
+          bool TOKM = false, bool XL = false, bool KH = false, bool XQ = false>
 __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                                                               void* __restrict__ qs) {
   constexpr bool kFp8 = RECIPE == MI355MOE_RECIPE_FP8BLOCK;
@@ -185,6 +185,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   static_assert(!TOKM || (!kGlu && !QOUT), "token-major form: STORE w2");
   static_assert(!XL || (!kGlu && !QOUT && !kFp8 && !kMx && !TOKM),
                 "activation rows from the w13 partials: 16-bit activation, STORE w2");
+  static_assert(!KH || (kGlu && !QOUT && !TOKM && !XL), "K halves: 16-bit GLU w13");
+  static_assert(!XQ || (TOKM && kFp8), "per-wave quantisation: token-major fp8block w2");
   using FragT = Frag<RECIPE>;
 
   __shared__ int s_arow[16];
@@ -222,9 +224,11 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   }
 
   // output columns of this wave: GLU 16 activation columns, STORE 32 columns
-  // (token-major: the 32 columns of its group, shared by the group's slots)
+  // (token-major: the 32 columns of its group, shared by the group's slots;
+  // K halves: column group wave % 4 of the workgroup's 64)
   const int64_t col0 =
       TOKM ? (static_cast<int64_t>(blockIdx.x) * (WAVES / a.topk) + wave / a.topk) * 32
+      : KH ? static_cast<int64_t>(blockIdx.x) * 64 + (wave & 3) * 16
            : static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) + wave * (kGlu ? 16 : 32);
   const int64_t wrow_bytes = (kFp4 || kMx4) ? K / 2 : (kW8 ? K : K * XB);
   const uint8_t* wexp = static_cast<const uint8_t*>(a.B) +
@@ -265,19 +269,23 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   // row 0 (their outputs are never stored), the K tail re-reads the last
   // chunk and compute() zeroes it.  A load under a condition would make the
   // compiler wait for every prefetched stage where the branches join.
-  // ---- this split's K stages [s0, s0 + nk)
+  // ---- this split's (K halves: this wave's half's) K stages [s0, s0 + nk)
   const int ks = a.ksplit > 1 ? a.ksplit : 1;
+  const int nparts = KH ? 2 : ks;
   const int nk_all = static_cast<int>((K + KS - 1) / KS);
-  const int per = (nk_all + ks - 1) / ks;
-  const int s0 = static_cast<int>(blockIdx.z) * per;
+  const int per = (nk_all + nparts - 1) / nparts;
+  const int s0 = (KH ? (wave >> 2) : static_cast<int>(blockIdx.z)) * per;
   const int nk = a.finalize || (TOKM && tpos < 0) ? 0  // a dropped slot streams nothing
                                                     : ((nk_all - s0) < per ? (nk_all - s0) : per);
-  // SELF8: every token row's K range of the split, e4m3, and its 1 x 128
-  // scales in LDS (row pitch xrs bytes)
+  // SELF8: every token row's K range of the split (K halves: the whole K),
+  // e4m3, and its 1 x 128 scales in LDS (row pitch xrs bytes)
   __shared__ __attribute__((aligned(16))) uint8_t s_xq[SELF8 ? kStreamSelfXBytes : 16];
   __shared__ float s_xsc[SELF8 ? kStreamSelfXBytes / 128 : 1];
-  const int64_t kx0 = static_cast<int64_t>(s0) * KS;
-  const int xrs = per * KS;
+  const int64_t kx0 = KH ? 0 : static_cast<int64_t>(s0) * KS;
+  const int xrs = (KH ? nk_all : per) * KS;
+  // XQ: each wave's slot row, e4m3, and its 1 x 128 scales
+  __shared__ __attribute__((aligned(16))) uint8_t s_tq[XQ ? WAVES * kStreamTokXBytes : 16];
+  __shared__ float s_tqs[XQ ? WAVES * (kStreamTokXBytes / 128) : 1];
   // XL: this workgroup's 16 activation rows over the split's K range (16-bit,
   // row pitch xrs elements), rebuilt from the w13 partials below
   __shared__ __attribute__((aligned(16))) uint16_t s_xa[XL ? kStreamG1FinBytes / 2 : 8];
@@ -319,9 +327,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         f.w[t][1] = *reinterpret_cast<const uint4*>(p + 16);
         f.ws[t] = bsc[(static_cast<int64_t>(e) * wsrows + wsr[t]) * (K / 128) + k0 / 128];
       }
-      if constexpr (SELF8) {
-        // the split's activation tile in LDS, read by compute(): the first
-        // stages' weights are requested before the tile is quantised
+      if constexpr (SELF8 || XQ) {
+        // the activation in LDS, read by compute(): the first stages'
+        // weights are requested before it is quantised
       } else {
         const uint8_t* px = xp + k0 + 32 * q;
         f.x[0] = *reinterpret_cast<const uint4*>(px);
@@ -447,6 +455,16 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
 
   // ---- K loop, PD stages in flight
   FragT buf[PD];
+  // XQ: the stage's activation operand from the wave's quantised row in LDS,
+  // read as the stage is prefetched (PD stages ahead of its MFMAs)
+  auto ldsx = [&](FragT& f, int64_t k0) {
+    if constexpr (XQ) {
+      const uint8_t* px = s_tq + wave * kStreamTokXBytes + k0 + 32 * q;
+      f.x[0] = *reinterpret_cast<const uint4*>(px);
+      f.x[1] = *reinterpret_cast<const uint4*>(px + 16);
+      f.xs = s_tqs[wave * (kStreamTokXBytes / 128) + k0 / 128];
+    }
+  };
   auto prefetch = [&]() {
     if (nk > 0) {
 #pragma unroll
@@ -460,7 +478,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     // each) per 128-value block; the trip count is uniform, lanes past the
     // end take part in the shuffles and store nothing
     const int T = a.num_valid / a.a_div;
-    const int cpr = nk * 16;  // 8-value chunks of a row in this split
+    const int cpr = (KH ? nk_all : nk) * 16;  // 8-value chunks of a row in this split
     const int nch = T * cpr;
     for (int base = 0; base < nch; base += WAVES * 64) {
       const int i = base + tid;
@@ -470,6 +488,35 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
                             s_xsc + r * (xrs / KS), act ? i % cpr : cpr, cpr);
     }
     __syncthreads();
+  }
+  if constexpr (XQ) {
+    prefetch();  // the weights of the first stages, in flight while the row is quantised
+    if (nk > 0) {  // wave-uniform: a kept slot
+      // the group quantiser over the wave's 16-bit row: 16 lanes (8 values
+      // each) per 128-value block, all 64 lanes in every round
+      // (every round's load in flight before the first is used)
+      constexpr int R = kStreamTokXBytes / 512;  // rounds of 64 chunks
+      const uint16_t* xr = static_cast<const uint16_t*>(a.A) + static_cast<int64_t>(tpos) * K;
+      const int cpr = static_cast<int>(K / 8);
+      uint4 u[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int c = 64 * r + lane;
+        u[r] = *reinterpret_cast<const uint4*>(xr + 8 * (c < cpr ? c : 0));
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int c = 64 * r + lane;
+        if (64 * r < cpr)  // uniform
+          fp8_quant_regs<F16>(u[r], s_tq + wave * kStreamTokXBytes,
+                              s_tqs + wave * (kStreamTokXBytes / 128), c < cpr ? c : cpr, cpr);
+      }
+      // the row is read back by other lanes of the same wave
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+      for (int d = 0; d < PD; ++d) ldsx(buf[d], static_cast<int64_t>(s0 + (d < nk ? d : nk - 1)) * KS);
+    }
   }
   if constexpr (XL) {
     // the w13 finalize of this block's valid slots on the split's columns:
@@ -512,7 +559,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     }
     __syncthreads();
   }
-  if constexpr (!SELF8) prefetch();
+  if constexpr (!SELF8 && !XQ) prefetch();
   int kt = 0;
   // main part: every prefetch is in range, so no load sits in a branch
   for (; kt + 2 * PD <= nk; kt += PD) {
@@ -520,6 +567,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     for (int d = 0; d < PD; ++d) {
       compute(buf[d], static_cast<int64_t>(s0 + kt + d) * KS);
       load(buf[d], static_cast<int64_t>(s0 + kt + d + PD) * KS);
+      ldsx(buf[d], static_cast<int64_t>(s0 + kt + d + PD) * KS);
     }
   }
   // remainder: fewer than 2 PD stages
@@ -529,11 +577,27 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       const int k = kt + d;
       if (k < nk) {
         compute(buf[d], static_cast<int64_t>(s0 + k) * KS);
-        if (k + PD < nk) load(buf[d], static_cast<int64_t>(s0 + k + PD) * KS);
+        if (k + PD < nk) {
+          load(buf[d], static_cast<int64_t>(s0 + k + PD) * KS);
+          ldsx(buf[d], static_cast<int64_t>(s0 + k + PD) * KS);
+        }
       }
     }
   }
 
+  // ---- K halves: the upper half's sums join the lower half's (the split-K
+  //      finalize's order: half 0, then half 1); the lower waves go on
+  if constexpr (KH) {
+    __shared__ f32x4 s_kh[4][2][64];
+    if (wave >= 4) {
+      s_kh[wave - 4][0][lane] = acc[0];
+      s_kh[wave - 4][1][lane] = acc[1];
+    }
+    __syncthreads();
+    if (wave >= 4) return;
+    acc[0] += s_kh[wave][0][lane];
+    acc[1] += s_kh[wave][1][lane];
+  }
   // ---- split-K: the split launch leaves its partial tile; the finalize
   //      launch sums the partials in split order (bit-reproducible)
   if (ks > 1) {
@@ -709,7 +773,28 @@ int launch_stream_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t
       const int groups = WAVES / a.topk;
       const dim3 tg(static_cast<unsigned>(cdiv(a.N, 32 * groups)),
                     static_cast<unsigned>(a.num_valid / a.topk), 1);
+      if constexpr (RECIPE == MI355MOE_RECIPE_FP8BLOCK) {
+        if (a.tok_xq) {  // each wave quantises its 16-bit activation row
+          moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, false, true, false, false, true>
+              <<<tg, dim3(512), 0, st>>>(g, qs);
+          MI_LAUNCH_CHECK();
+          return MI355MOE_OK;
+        }
+      }
       moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, false, true><<<tg, dim3(512), 0, st>>>(g, qs);
+      MI_LAUNCH_CHECK();
+      return MI355MOE_OK;
+    }
+  }
+  if constexpr (RECIPE == MI355MOE_RECIPE_FP8BLOCK && EPI == EPI_GLU && !QOUT) {
+    if (a.khalves) {  // 64 activation columns x both K halves per workgroup, no split
+      const dim3 kg(static_cast<unsigned>(cdiv(a.N, 64)), static_cast<unsigned>(max_blocks), 1);
+      if (a.sr_x)
+        moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, true, false, false, true>
+            <<<kg, dim3(512), 0, st>>>(g, qs);
+      else
+        moe_gemm_stream_kernel<RECIPE, EPI, QOUT, PD, F16, false, false, false, true>
+            <<<kg, dim3(512), 0, st>>>(g, qs);
       MI_LAUNCH_CHECK();
       return MI355MOE_OK;
     }
