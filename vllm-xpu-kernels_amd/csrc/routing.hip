@@ -35,8 +35,8 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);
 }
 
-// One in-row step of wave_argmax: every lane compares with the lane that
-// the DPP control CTRL names inside its row of 16.
+// One in-row argmax step over (value, aux, index): every lane compares with
+// the lane that the DPP control CTRL names inside its row of 16.
 template <int CTRL>
 __device__ __forceinline__ void argmax_dpp_step(float& v, float& aux, int& idx) {
   const float ov = __int_as_float(
@@ -51,35 +51,61 @@ __device__ __forceinline__ void argmax_dpp_step(float& v, float& aux, int& idx) 
   }
 }
 
-// Wave-wide argmax over (value, index) pairs; every lane gets the winner.
-// (value, index) pairs are distinct (or identical), so the winner does not
-// depend on the reduction order.  Within each row of 16 lanes: DPP quad
-// permutations (lane ^ 1, lane ^ 2), then the half-row and row mirrors,
-// which pair each lane with one of the other quad / half-row once those
-// agree; the four row winners (lanes 0, 16, 32, 48) are then read as
-// wave-uniform values.  All 64 lanes must be active.
-__device__ __forceinline__ void wave_argmax(float& v, float& aux, int& idx) {
-  argmax_dpp_step<0xB1>(v, aux, idx);   // quad_perm [1,0,3,2]
-  argmax_dpp_step<0x4E>(v, aux, idx);   // quad_perm [2,3,0,1]
-  argmax_dpp_step<0x141>(v, aux, idx);  // row_half_mirror
-  argmax_dpp_step<0x140>(v, aux, idx);  // row_mirror
-  float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  float ba = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aux), 0));
-  int bi = __builtin_amdgcn_readlane(idx, 0);
-#pragma unroll
-  for (int r = 16; r < 64; r += 16) {
-    const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), r));
-    const float ra = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(aux), r));
-    const int ri = __builtin_amdgcn_readlane(idx, r);
-    if (better(rv, ri, bv, bi)) {
-      bv = rv;
-      ba = ra;
-      bi = ri;
-    }
-  }
-  v = bv;
-  aux = ba;
-  idx = bi;
+// (value desc, index asc) as one unsigned key, larger = better: the value's
+// bits in an order-preserving map (-0 counted as +0, NaN below -inf) above
+// the complement of the index.  Distinct entries have distinct keys, so the
+// maximum does not depend on the reduction order, and it is the entry that
+// `better` prefers to every other.  Key 0 is below every entry.
+__device__ __forceinline__ uint64_t desc_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v + 0.0f);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  if (v != v) u = 0u;
+  return (static_cast<uint64_t>(u) << 32) | static_cast<uint32_t>(~idx);
+}
+__device__ __forceinline__ int key_index(uint64_t k) {
+  return static_cast<int>(~static_cast<uint32_t>(k));
+}
+__device__ __forceinline__ float key_value(uint64_t k) {  // non-NaN keys
+  const uint32_t u = static_cast<uint32_t>(k >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+// One DPP step of a 64-bit maximum: lanes of the rows in ROWMASK compare
+// with the lane CTRL names (the others keep their own key).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t k) {
+  const uint32_t lo = static_cast<uint32_t>(k), hi = static_cast<uint32_t>(k >> 32);
+  const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWMASK, 0xF, false);
+  const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWMASK, 0xF, false);
+  const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
+  return o > k ? o : k;
+}
+// Wave-wide maximum key, returned wave-uniform: within each row of 16 lanes
+// the quad swaps and the half-row and row mirrors, then lane 15 of rows 0
+// and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3
+// (row_bcast:31), so lane 63 holds the maximum.  All 64 lanes active.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+  k = dpp_max_u64<0xB1, 0xF>(k);   // quad_perm [1,0,3,2]
+  k = dpp_max_u64<0x4E, 0xF>(k);   // quad_perm [2,3,0,1]
+  k = dpp_max_u64<0x141, 0xF>(k);  // row_half_mirror
+  k = dpp_max_u64<0x140, 0xF>(k);  // row_mirror
+  k = dpp_max_u64<0x142, 0xA>(k);  // row_bcast:15
+  k = dpp_max_u64<0x143, 0xC>(k);  // row_bcast:31
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(k), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(k >> 32), 63);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Wave-wide fmaxf, wave-uniform (the same steps as wave_max_key; fmaxf is
+// exact and ignores NaN, so the order does not change the result).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                           0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                           0x143, 0xC, 0xF, false)));
+  return readlane_f32(v, 63);
 }
 
 enum GateMode { GATE_SOFTMAX = 0, GATE_SIGMOID = 1, GATE_SOFTPLUS_SQRT = 2 };
@@ -148,7 +174,7 @@ __global__ __launch_bounds__(256) void topk_gating_kernel(
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) m = fmaxf(m, p[i]);
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -182,34 +208,46 @@ __global__ __launch_bounds__(256) void topk_gating_kernel(
       sel[i] = -INFINITY;
   }
 
+  // selection keys (experts past E: key 0, never chosen over an expert)
+  uint64_t key[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = i * 64 + lane;
+    key[i] = e < num_experts ? desc_key(sel[i], e) : 0ull;
+  }
   float wsum = 0.f;
   float myw = 0.f;  // lane j < k keeps the j-th weight
   int myid = 0;
   for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY, bp = 0.f;
-    int bi = 0x7fffffff;
+    uint64_t bk = key[0];
+    float bp = p[0];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      int e = i * 64 + lane;
-      if (e < num_experts && better(sel[i], e, bv, bi)) {
-        bv = sel[i];
+    for (int i = 1; i < VPT; ++i)
+      if (key[i] > bk) {
+        bk = key[i];
         bp = p[i];
-        bi = e;
       }
-    }
-    wave_argmax(bv, bp, bi);
+    const uint64_t wk = wave_max_key(bk);  // the round's winner, wave-uniform
+    const int bi = key_index(wk);
+    const int wl = bi & 63;
+    bp = readlane_f32(bp, wl);  // the winning lane's best is the winner
     // softplus_sqrt reports the biased value minus the bias, (s + b) - b
-    if constexpr (MODE == GATE_SOFTPLUS_SQRT) bp = bias ? bv - bias[bi] : bv;
+    if constexpr (MODE == GATE_SOFTPLUS_SQRT) {
+      const float bv = key_value(wk);
+      bp = bias ? bv - bias[bi] : bv;
+    }
     wsum += bp;
     if (lane == j) {
       myw = bp;
       myid = bi;
     }
-    // retire the winner so the next round cannot pick it again (softplus_sqrt:
-    // -10000, as its reference kernel, :393-401)
+    // retire the winner (-inf, so that ties with other -inf entries still go
+    // by index; softplus_sqrt: -10000, as its reference kernel, :393-401)
+    if (lane == wl) {
 #pragma unroll
-    for (int i = 0; i < VPT; ++i)
-      if (i * 64 + lane == bi) sel[i] = MODE == GATE_SOFTPLUS_SQRT ? -10000.f : -INFINITY;
+      for (int i = 0; i < VPT; ++i)
+        if (i == (bi >> 6)) key[i] = desc_key(MODE == GATE_SOFTPLUS_SQRT ? -10000.f : -INFINITY, bi);
+    }
   }
   if (lane < k) {
     float scale = rsf;
@@ -384,19 +422,22 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
       gscore = __builtin_isfinite(sum) ? sum : -INFINITY;
     }
   }
-  // --- pick topk_group groups
+  // --- pick topk_group groups: group g (lane g) is kept when fewer than
+  //     topk_group groups beat it (score desc, group asc -- the order in
+  //     which rounds of argmax would pick them); thr is the score of the
+  //     last kept group
   unsigned long long kept = 0ull;
   float thr = -INFINITY;
   {
-    float gv = lane < n_group ? gscore : -INFINITY;
-    for (int j = 0; j < topk_group; ++j) {
-      float v = gv, aux = 0.f;
-      int gi = lane < n_group ? lane : 0x7fffffff;
-      wave_argmax(v, aux, gi);
-      thr = v;
-      if (gi >= 0 && gi < 64) kept |= (1ull << gi);
-      if (lane == gi) gv = -INFINITY;
+    int rank = 0;
+    for (int j = 0; j < n_group; ++j) {  // uniform
+      const float sj = readlane_f32(gscore, j);
+      rank += better(sj, j, gscore, lane) ? 1 : 0;
     }
+    const bool in = lane < n_group;
+    kept = __ballot(in && rank < topk_group);
+    const unsigned long long last = __ballot(in && rank == topk_group - 1);
+    thr = readlane_f32(gscore, static_cast<int>(__builtin_ctzll(last)));
   }
   const bool proceed = thr != -INFINITY;
   float myv = 0.f;
@@ -404,24 +445,27 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
   if (proceed) {
     float wsum = 1e-20f;
     // candidates: experts of dropped groups and non-finite values become
-    // -inf; each round retires its winner
+    // -inf; each round retires its winner (to -inf, as the candidates
+    // dropped above)
+    uint64_t key[VPT];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int e = i * 64 + lane;
       if (e >= num_experts || !((kept >> (e / epg)) & 1ull) || !__builtin_isfinite(sv[i]))
         sv[i] = -INFINITY;
+      key[i] = desc_key(sv[i], e);
     }
     for (int j = 0; j < k; ++j) {
-      float bv = sv[0], aux = sc[0];
-      int bi = lane;
+      uint64_t bk = key[0];
+      float aux = sc[0];
 #pragma unroll
       for (int i = 1; i < VPT; ++i)
-        if (sv[i] > bv) {   // ids grow with i: ties keep the lower one
-          bv = sv[i];
+        if (key[i] > bk) {
+          bk = key[i];
           aux = sc[i];
-          bi = i * 64 + lane;
         }
-      wave_argmax(bv, aux, bi);
+      const int bi = key_index(wave_max_key(bk));
+      aux = readlane_f32(aux, bi & 63);  // the winning lane's best is the winner
       wsum += aux;
       if (lane == j) {
         myv = aux;
@@ -430,7 +474,7 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
       if (lane == (bi & 63)) {
 #pragma unroll
         for (int i = 0; i < VPT; ++i)
-          if (i == (bi >> 6)) sv[i] = -INFINITY;
+          if (i == (bi >> 6)) key[i] = desc_key(-INFINITY, bi);
       }
     }
     if (lane < k) myv = renormalize ? myv / wsum * rsf : myv * rsf;
@@ -453,8 +497,8 @@ __global__ __launch_bounds__(256) void grouped_topk_kernel(
 // Four tokens per wave, one per row of 16 lanes (E = 16 VPT experts, lane
 // `sub` of a row holding experts sub * VPT .. sub * VPT + VPT - 1, groups of
 // E / n_group experts spanning whole lane chunks, n_group dividing 16, k up
-// to 16): every argmax is the row-local half of wave_argmax (four DPP steps,
-// no cross-row reads), and the four rows run side by side.  Same selection,
+// to 16): every argmax is row-local (four DPP steps over (value, aux,
+// index), no cross-row reads), and the four rows run side by side.  Same selection,
 // ties and roundings as grouped_topk_kernel.
 __device__ __forceinline__ void row_argmax(float& v, float& aux, int& idx) {
   argmax_dpp_step<0xB1>(v, aux, idx);   // quad_perm [1,0,3,2]
