@@ -143,6 +143,17 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false)) & 0xFFu;
 }
 
+// e4m3 bytes 0..3 of v0..v3, each clamped to [-448, 448] first (fmaxf /
+// fminf also take NaN into that range), two values per hardware convert:
+// byte for byte the codes f32_to_e4m3 gives for the clamped values, without
+// its out-of-range branch.
+__device__ __forceinline__ uint32_t e4m3x4_sat(float v0, float v1, float v2, float v3) {
+  auto c = [](float x) { return fminf(fmaxf(x, -448.f), 448.f); };
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(c(v0), c(v1), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c(v2), c(v3), w, true);
+  return static_cast<uint32_t>(w);
+}
+
 // ceil(log2(x)) of a positive finite float, exactly from its bits (a
 // mantissa above the power of two rounds the exponent up), and 2^e.
 __device__ __forceinline__ int ceil_log2(float x) {
@@ -207,12 +218,8 @@ __device__ __forceinline__ void fp8_quant_regs(const uint4 u, uint8_t* __restric
   if (!active) return;
   if ((c & 15) == 0) s[c >> 4] = ys;
   const float inv = 1.0f / ys;
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t b = f32_to_e4m3(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f));
-    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
-  }
+  const uint32_t lo = e4m3x4_sat(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+  const uint32_t hi = e4m3x4_sat(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
   *reinterpret_cast<uint2*>(q + c * 8) = make_uint2(lo, hi);
 }
 template <bool F16>

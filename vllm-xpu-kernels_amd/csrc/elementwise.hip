@@ -272,12 +272,8 @@ __global__ __launch_bounds__(256) void group_mx8_quant_kernel(
   if (!active) return;
   if (sub == 0) s[(g / gpr) * s_ld + g % gpr] = static_cast<uint8_t>(ex + 127);
   const float inv = 1.0f / ys;
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t b = f32_to_e4m3(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f));
-    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
-  }
+  const uint32_t lo = e4m3x4_sat(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+  const uint32_t hi = e4m3x4_sat(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
   store_nt(q + base, lo, hi);
 }
 
@@ -353,18 +349,21 @@ __global__ __launch_bounds__(256) void silu_mul_block_quant_kernel(
   if (!active) return;
   if ((gtid & (lpg - 1)) == 0) s[r * sst + (c0 / group) * ssg] = ys;
   uint32_t lo = 0, hi = 0;
+  if constexpr (QO == Q_E4M3) {
+    lo = e4m3x4_sat(v[0] / ys, v[1] / ys, v[2] / ys, v[3] / ys);
+    hi = e4m3x4_sat(v[4] / ys, v[5] / ys, v[6] / ys, v[7] / ys);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t b;
-    if constexpr (QO == Q_I8) {
-      const float t = fminf(fmaxf(__builtin_rintf(v[i] / ys), -128.0f), 127.0f);
-      b = static_cast<uint32_t>(static_cast<int32_t>(t)) & 0xFFu;
-    } else if constexpr (QO == Q_E4M3) {
-      b = f32_to_e4m3(fminf(fmaxf(v[i] / ys, -448.0f), 448.0f));
-    } else {
-      b = f32_to_e5m2(fminf(fmaxf(v[i] / ys, -57344.0f), 57344.0f));
+    for (int i = 0; i < 8; ++i) {
+      uint32_t b;
+      if constexpr (QO == Q_I8) {
+        const float t = fminf(fmaxf(__builtin_rintf(v[i] / ys), -128.0f), 127.0f);
+        b = static_cast<uint32_t>(static_cast<int32_t>(t)) & 0xFFu;
+      } else {
+        b = f32_to_e5m2(fminf(fmaxf(v[i] / ys, -57344.0f), 57344.0f));
+      }
+      if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
     }
-    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
   }
   store_nt(q + r * hidden + c0, lo, hi);
 }

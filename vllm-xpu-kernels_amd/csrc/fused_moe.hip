@@ -205,6 +205,19 @@ __global__ __launch_bounds__(256) void repack_codes_kernel(const uint8_t* __rest
   dst[i] = c < w ? src[r * w + c] : static_cast<uint8_t>(127);
 }
 
+// Rows of w units [rows, w] -> [rows, ld] (ld > w), the padding zeroed: the
+// caller's e2m1 hidden states copied to 128-byte-aligned rows (a zero e2m1
+// code meets only the zeroed weights past K).
+template <typename U>
+__global__ __launch_bounds__(256) void repack_rows_kernel(const U* __restrict__ src,
+                                                          U* __restrict__ dst, int64_t w,
+                                                          int64_t ld, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t r = i / ld, c = i % ld;
+  dst[i] = c < w ? src[r * w + c] : U{};
+}
+
 // Activations without a GEMM-epilogue form (gelu, gelu_tanh, swiglustep,
 // relu2_no_mul): the w13 output G1 (16-bit [rows, 2I] by sorted position,
 // gate | up) -> activation [rows, K2], K2 = I (gated) or 2I (relu2_no_mul),
@@ -270,12 +283,8 @@ __global__ __launch_bounds__(256) void fused_act_kernel(
     const float sc = fmaxf(amax / 448.0f, 1.0f / (448.0f * 512.0f));
     if ((gtid & 15) == 0) acts[r * (k2 / 128) + c0 / 128] = sc;
     const float inv = 1.0f / sc;
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t b = f32_to_e4m3(fminf(fmaxf(y[i] * inv, -448.0f), 448.0f));
-      if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
-    }
+    const uint32_t lo = e4m3x4_sat(y[0] * inv, y[1] * inv, y[2] * inv, y[3] * inv);
+    const uint32_t hi = e4m3x4_sat(y[4] * inv, y[5] * inv, y[6] * inv, y[7] * inv);
     *reinterpret_cast<uint2*>(static_cast<uint8_t*>(act) + r * k2 + c0) = make_uint2(lo, hi);
   } else {
     uint32_t w[4];
@@ -336,6 +345,11 @@ struct FusedLayout {
   uint8_t* xs8;   // MX: e8m0 scales of the quantised hidden [T, ld1]
   uint8_t* acts8; // MX: e8m0 scales of the activation [max_padded, ld2]
   int64_t ld1, ld2;
+  // w4a4 on the 320-slot kernel: row pitches (bytes, multiples of 128) of
+  // the e2m1 hidden copy xp [T, p1] (null when H / 2 is already one) and of
+  // the activation act [max_padded, p2]; 0 when unused
+  uint8_t* xp;
+  int64_t p1, p2;
   uint16_t* g1;   // generic activations: w13 output bf16 [max_padded, 2I]
   uint16_t* g2;   // bf16 [slots, H]
   bool token_w2;  // STREAM w2 token-major: it writes the layer output
@@ -470,7 +484,13 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     // the layer's own codes, or the caller's repacked to 4-byte rows
     if (!a->hidden_scale || L.ld1 != a->hidden / 32)
       L.xs8 = c.take<uint8_t>(a->num_tokens * L.ld1);
-    L.act = c.take<uint8_t>(L.max_padded * (gemm_recipe(a) == RECIPE_MX4A4 ? K2 / 2 : K2));
+    if (gemm_recipe(a) == RECIPE_MX4A4 && L.tile == TILE_WIDE) {
+      L.p1 = (a->hidden / 2 + 127) / 128 * 128;
+      L.p2 = (K2 / 2 + 127) / 128 * 128;
+      if (L.p1 != a->hidden / 2) L.xp = c.take<uint8_t>(a->num_tokens * L.p1);
+    }
+    L.act = c.take<uint8_t>(L.max_padded * (gemm_recipe(a) == RECIPE_MX4A4
+                                                ? (L.p2 ? L.p2 : K2 / 2) : K2));
     L.acts8 = c.take<uint8_t>(L.max_padded * L.ld2);
   } else if (fp8) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
@@ -746,6 +766,20 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
         static_cast<const uint8_t*>(a->hidden_scale), L.xs8, H / 32, L.ld1, n);
     MI_LAUNCH_CHECK();
   }
+  if (L.xp) {
+    const int64_t rb = H / 2;  // packed e2m1 row bytes (H % 32 == 0)
+    if ((reinterpret_cast<uintptr_t>(a->hidden_states) & 15) == 0) {
+      const int64_t n = T * (L.p1 / 16);
+      repack_rows_kernel<uint4><<<static_cast<unsigned>(cdiv(n, 256)), dim3(256), 0, st>>>(
+          static_cast<const uint4*>(a->hidden_states), reinterpret_cast<uint4*>(L.xp), rb / 16,
+          L.p1 / 16, n);
+    } else {
+      const int64_t n = T * L.p1;
+      repack_rows_kernel<uint8_t><<<static_cast<unsigned>(cdiv(n, 256)), dim3(256), 0, st>>>(
+          static_cast<const uint8_t*>(a->hidden_states), L.xp, rb, L.p1, n);
+    }
+    MI_LAUNCH_CHECK();
+  }
   if (int m = mark(2)) return m;
 
   // gelu / gelu_tanh / swiglustep / relu2_no_mul: w13 stores G1, a separate
@@ -753,7 +787,9 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   const int64_t K2 = act_width(a);
   GemmArgs g1{};
   g1.A = (fp8 && !preq) || (mx && !a->hidden_scale) ? static_cast<const void*>(L.xq)
-                                                     : a->hidden_states;
+         : L.xp ? static_cast<const void*>(L.xp) : a->hidden_states;
+  g1.lda = L.xp ? L.p1 : 0;
+  g1.ldd = L.p2;
   g1.a_scale = preq ? static_cast<const float*>(a->hidden_scale) : (fp8 ? L.xs : nullptr);
   if (mx) {
     g1.a_mxs = a->hidden_scale && !repack ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
@@ -842,6 +878,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
 
   GemmArgs g2{};
   g2.A = L.act;
+  g2.lda = L.p2;
   g2.a_scale = fp8 ? L.acts : nullptr;
   if (mx) {
     g2.a_mxs = L.acts8;
@@ -890,6 +927,21 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
       g2.A = L.act16;
       g2.a_scale = nullptr;
       g2.tok_xq = 1;
+    }
+    // column-group width: the fewest columns per CU over the rounds of
+    // workgroups (256 CUs), the widest group on ties
+    {
+      const int64_t groups = 8 / k;
+      int best = 32;
+      int64_t best_cost = cdiv(cdiv(H, 32 * groups) * T, 256) * 32;
+      for (int cw = 28; cw >= 16; cw -= 4) {
+        const int64_t cost = cdiv(cdiv(H, cw * groups) * T, 256) * cw;
+        if (cost < best_cost) {
+          best = cw;
+          best_cost = cost;
+        }
+      }
+      g2.tok_cw = best;
     }
     g2.tok_inv = L.inv;
     g2.tok_w = a->topk_weights;

@@ -144,12 +144,8 @@ __device__ __forceinline__ void epilogue_32x32(const GemmArgs& a, void* qs,
       for (int i = 0; i < NO; ++i) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          uint32_t w = 0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float x = fminf(fmaxf(ov[i][j][4 * g + r] * inv, -448.f), 448.f);
-            w |= f32_to_e4m3(x) << (8 * r);
-          }
+          const uint32_t w = e4m3x4_sat(ov[i][j][4 * g] * inv, ov[i][j][4 * g + 1] * inv,
+                                        ov[i][j][4 * g + 2] * inv, ov[i][j][4 * g + 3] * inv);
           *reinterpret_cast<uint32_t*>(stage + row * PITCH + tile_col(i, 4 * g)) = w;
         }
       }

@@ -140,6 +140,11 @@ struct GemmArgs {
   const float* tok_w;
   int32_t topk;
   void* tok_out;
+  // columns per group (a multiple of 4 up to 32; 0: 32): a narrower group
+  // gives more workgroups (7168 columns in 28-column groups: 256, one per
+  // CU, against 224); the rows of a wave's 32-row tile past the group read
+  // the group's last row again (the same cache lines) and are not stored
+  int32_t tok_cw;
   // Token-major w2, fp8block recipe: A is the 16-bit activation [rows, K]
   // (no a_scale); each wave quantises its slot's row per 1 x 128 block with
   // the group quantiser into LDS before its K loop (K <= kStreamTokXBytes).
@@ -153,6 +158,10 @@ struct GemmArgs {
   // STREAM w2 of the fused layer (16-bit activation): its activation rows
   // rebuilt from the w13 partials (G1Fin) instead of read from A.
   G1Fin g1f;
+  // 320-slot e2m1 x e2m1 kernel: row pitch in bytes of A and of its e2m1
+  // output D (0: the packed K / 2 and N / 2).  A pitch that is a multiple of
+  // 128 keeps every 128-byte stage of a row inside one cache line.
+  int64_t lda, ldd;
 };
 // LDS bytes a STREAM workgroup gives the in-kernel-quantised activation
 // (GemmArgs::sr_x): tokens x the split's K range, e4m3 (and 1 x 128 scales).

@@ -434,12 +434,8 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const int64_t n = nbase + j * 16 + 4 * q;
-        uint32_t w = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = fminf(fmaxf(outv[mt][j][r] * inv, -448.f), 448.f);
-          w |= f32_to_e4m3(x) << (8 * r);
-        }
+        const uint32_t w = e4m3x4_sat(outv[mt][j][0] * inv, outv[mt][j][1] * inv,
+                                      outv[mt][j][2] * inv, outv[mt][j][3] * inv);
         *reinterpret_cast<uint32_t*>(dq + static_cast<int64_t>(drow) * a.N + n) = w;
       }
     }

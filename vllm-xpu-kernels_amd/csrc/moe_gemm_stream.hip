@@ -226,8 +226,9 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   // output columns of this wave: GLU 16 activation columns, STORE 32 columns
   // (token-major: the 32 columns of its group, shared by the group's slots;
   // K halves: column group wave % 4 of the workgroup's 64)
+  const int tcw = TOKM && a.tok_cw > 0 ? a.tok_cw : 32;  // token-major group width
   const int64_t col0 =
-      TOKM ? (static_cast<int64_t>(blockIdx.x) * (WAVES / a.topk) + wave / a.topk) * 32
+      TOKM ? (static_cast<int64_t>(blockIdx.x) * (WAVES / a.topk) + wave / a.topk) * tcw
       : KH ? static_cast<int64_t>(blockIdx.x) * 64 + (wave & 3) * 16
            : static_cast<int64_t>(blockIdx.x) * (kGlu ? 128 : 256) + wave * (kGlu ? 16 : 32);
   const int64_t wrow_bytes = (kFp4 || kMx4) ? K / 2 : (kW8 ? K : K * XB);
@@ -237,7 +238,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   bool wok[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int64_t n = kGlu ? col0 + l16 : col0 + 16 * t + l16;
+    int64_t n = kGlu ? col0 + l16 : col0 + 16 * t + l16;
+    if (TOKM && 16 * t + l16 >= tcw) n = col0 + tcw - 1;
     wok[t] = n < N;
     wrow[t] = (kGlu && t == 1 ? a.up_off : 0) + (wok[t] ? n : 0);
   }
@@ -255,13 +257,18 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
   const uint8_t* xsp8 = kMx ? a.a_mxs + static_cast<int64_t>(xok ? arow : 0) * a.a_mxs_ld
                             : nullptr;
 
-  // fp8 weight-block scale rows (16-row sub-tiles sit inside one 128- or
-  // 64-row block)
+  // fp8 weight-block scale rows, applied to the MFMA result: the block of
+  // the lane's output rows 4 q .. 4 q + 3 of each sub-tile, which share one
+  // block (sub-tiles start at multiples of 4 rows; a token-major group of
+  // 28 columns puts the block boundary inside a sub-tile)
   const int wsh = 7 - a.ws_rows64;
   const int64_t wsrows = a.ldb_rows >> wsh;
   int64_t wsr[2];
-  wsr[0] = wrow[0] >> wsh;
-  wsr[1] = wrow[1] >> wsh;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t n = kGlu ? col0 + 4 * q : col0 + 16 * t + 4 * q;
+    wsr[t] = ((kGlu && t == 1 ? a.up_off : 0) + (n < N ? n : 0)) >> wsh;
+  }
 
   const float* bsc = static_cast<const float*>(a.b_scale);
   const int64_t xsrow = static_cast<int64_t>(xok ? arow : 0) * (K / 128);
@@ -652,7 +659,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
         for (int r = 0; r < 4; ++r) s_tok[wave][16 * t + 4 * q + r] = ov[t][r];
     }
     __syncthreads();
-    if (wave % a.topk != 0 || lane >= 32 || col0 + lane >= N) return;
+    if (wave % a.topk != 0 || lane >= tcw || col0 + lane >= N) return;
     const int64_t t = blockIdx.y;
     float acc1 = 0.f;
     for (int j = 0; j < a.topk; ++j) {
@@ -686,10 +693,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + col0 / 32] =
           static_cast<uint8_t>(ex + 127);
     if constexpr (kMx8) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        w |= f32_to_e4m3(fminf(fmaxf(ov[0][r] * inv, -448.f), 448.f)) << (8 * r);
+      const uint32_t w =
+          e4m3x4_sat(ov[0][0] * inv, ov[0][1] * inv, ov[0][2] * inv, ov[0][3] * inv);
       *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * N +
                                    col0 + 4 * q) = w;
     } else {
@@ -716,10 +721,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     const float inv = 1.0f / sc;
     if (wave == 0 && q == 0)
       static_cast<float*>(qs)[static_cast<int64_t>(drow) * (N / 128) + blockIdx.x] = sc;
-    uint32_t w = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      w |= f32_to_e4m3(fminf(fmaxf(ov[0][r] * inv, -448.f), 448.f)) << (8 * r);
+    const uint32_t w =
+        e4m3x4_sat(ov[0][0] * inv, ov[0][1] * inv, ov[0][2] * inv, ov[0][3] * inv);
     *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * N +
                                  col0 + 4 * q) = w;
   } else {
@@ -771,7 +774,8 @@ int launch_stream_t(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t
   if constexpr (EPI == EPI_STORE && !QOUT) {
     if (a.tok_out) {  // token-major w2: the output itself, no split
       const int groups = WAVES / a.topk;
-      const dim3 tg(static_cast<unsigned>(cdiv(a.N, 32 * groups)),
+      const int cw = a.tok_cw > 0 ? a.tok_cw : 32;
+      const dim3 tg(static_cast<unsigned>(cdiv(a.N, static_cast<int64_t>(cw) * groups)),
                     static_cast<unsigned>(a.num_valid / a.topk), 1);
       if constexpr (RECIPE == MI355MOE_RECIPE_FP8BLOCK) {
         if (a.tok_xq) {  // each wave quantises its 16-bit activation row

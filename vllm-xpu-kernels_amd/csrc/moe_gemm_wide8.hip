@@ -409,12 +409,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
       if (wn == 0 && g == 0 && drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = fminf(fmaxf(ov[i][j][r] * inv, -448.f), 448.f);
-          w |= f32_to_e4m3(x) << (8 * r);
-        }
+        const uint32_t w = e4m3x4_sat(ov[i][j][0] * inv, ov[i][j][1] * inv, ov[i][j][2] * inv,
+                                      ov[i][j][3] * inv);
         *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(i, 0)) = w;
       }
     }

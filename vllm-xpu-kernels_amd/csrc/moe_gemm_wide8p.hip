@@ -198,6 +198,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   const uint8_t* wbase = uniform_ptr(static_cast<const uint8_t*>(a.B) +
                                      static_cast<int64_t>(e) * a.ldb_rows * (MX4 ? K / 2 : K));
   const uint32_t Ku = static_cast<uint32_t>(MX4 ? K / 2 : K);  // activation row bytes
+  const uint32_t Kp = MX4 && a.lda ? static_cast<uint32_t>(a.lda) : Ku;  // row pitch
   // activation rows 40 wave + 8 q + lane / 8, 16-byte chunk lane % 8 of the
   // LDS row, read from source chunk (lane % 8) ^ swz(row)
   uint32_t aoff[AROWS / 8];
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   for (int q = 0; q < AROWS / 8; ++q) {
     const int r = AROWS * wave + 8 * q + (lane >> 3);
     const int ar = s_arow[(r & ~15) | slot_of_lds_row(r & 15)];
-    aoff[q] = static_cast<uint32_t>(ar >= 0 ? ar : 0) * Ku +
+    aoff[q] = static_cast<uint32_t>(ar >= 0 ? ar : 0) * Kp +
               (MX4 ? 0u : static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4);
   }
   // e2m1: the lane's source chunk of part q, added per stage (chunks past
@@ -627,12 +628,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         *reinterpret_cast<uint16_t*>(lds + row * PITCH + tcol(0, 0) / 2) =
             static_cast<uint16_t>(w);
       } else {
-        uint32_t w = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = fminf(fmaxf(ov[j][r] * inv, -448.f), 448.f);
-          w |= f32_to_e4m3(x) << (8 * r);
-        }
+        const uint32_t w =
+            e4m3x4_sat(ov[j][0] * inv, ov[j][1] * inv, ov[j][2] * inv, ov[j][3] * inv);
         *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
       }
     }
@@ -641,7 +638,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     // 16-byte chunks of an output row: 16 e4m3 or 32 e2m1 columns; N % 32 ==
     // 0, so an e2m1 chunk lies wholly inside or wholly past N
     constexpr int CPR = MX4 ? NOUT / 32 : NOUT / 16;
-    const int64_t orow = MX4 ? N / 2 : N;  // output row bytes
+    const int64_t orow = MX4 ? (a.ldd ? a.ldd : N / 2) : N;  // output row pitch (bytes)
     for (int idx = tid; idx < BM * CPR; idx += 512) {
       const int row = idx / CPR, ch = idx % CPR;
       const int drow = s_drow[row];
