@@ -532,20 +532,23 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     return (kGlu ? 16 * wave : 32 * wave + 16 * f) + 4 * g + r;
   };
   constexpr int NF = kGlu ? 1 : 2;
+  // the biases of the lane's output columns, the same for all its slots
+  float bgs[NF][4], bus[4];
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + tcol(f, r);
+      const bool has = a.bias && n < N;
+      bgs[f][r] = has ? ld16<F16>(a.bias[bias_base + n]) : 0.f;
+      if (f == 0) bus[r] = has && kGlu ? ld16<F16>(a.bias[bias_base + a.up_off + n]) : 0.f;
+    }
   auto outv = [&](int f, int j, float (&o)[4]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float bg = 0.f, bu = 0.f;
-      if (a.bias) {
-        const int64_t n = n0 + tcol(f, r);
-        if (n < N) {
-          bg = ld16<F16>(a.bias[bias_base + n]);
-          if constexpr (kGlu) bu = ld16<F16>(a.bias[bias_base + a.up_off + n]);
-        }
-      }
-      float gv = round16<F16>(acc[f][j][r] + bg);
+      float gv = round16<F16>(acc[f][j][r] + bgs[f][r]);
       if constexpr (kGlu) {
-        float u = round16<F16>(acc[1][j][r] + bu);
+        float u = round16<F16>(acc[1][j][r] + bus[r]);
         glu_clamp(a, n0 + tcol(f, r), gv, u);
         float y;
         if (a.act == MI355MOE_ACT_SILU) {
