@@ -523,179 +523,197 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   }
   static_assert(TJ == 20, "kloop variants cover the even tile counts up to TJ");
 
-  // ---- epilogue: lane holds slot 16 j + l16, rows 4 g + r of fragment f
-  const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();  // the ring is free
-  // output column (within the tile) of (fragment f, reg r)
-  auto tcol = [&](int f, int r) -> int {
-    return (kGlu ? 16 * wave : 32 * wave + 16 * f) + 4 * g + r;
-  };
-  constexpr int NF = kGlu ? 1 : 2;
-  // the biases of the lane's output columns, the same for all its slots
-  float bgs[NF][4], bus[4];
-#pragma unroll
-  for (int f = 0; f < NF; ++f)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t n = n0 + tcol(f, r);
-      const bool has = a.bias && n < N;
-      bgs[f][r] = has ? ld16<F16>(a.bias[bias_base + n]) : 0.f;
-      if (f == 0) bus[r] = has && kGlu ? ld16<F16>(a.bias[bias_base + a.up_off + n]) : 0.f;
-    }
-  auto outv = [&](int f, int j, float (&o)[4]) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float gv = round16<F16>(acc[f][j][r] + bgs[f][r]);
-      if constexpr (kGlu) {
-        float u = round16<F16>(acc[1][j][r] + bus[r]);
-        glu_clamp(a, n0 + tcol(f, r), gv, u);
-        float y;
-        if (a.act == MI355MOE_ACT_SILU) {
-          y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
-        } else {
-          gv = gv > a.limit ? a.limit : gv;
-          u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-          y = (u + 1.f) * x_sigmoid(gv, a.alpha);
-        }
-        gv = round16<F16>(y);
+  // The epilogue, specialised on the activation and on gemm1_clamp_limit
+  // (uniform per launch), so that no value of the tile branches on them.
+  auto epilogue = [&](auto silu_c, auto clamp_c) {
+    constexpr bool SILU = decltype(silu_c)::value;
+    constexpr bool CLAMP = decltype(clamp_c)::value;
+    // ---- epilogue: lane holds slot 16 j + l16, rows 4 g + r of fragment f
+    const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // the ring is free
+    // output column (within the tile) of (fragment f, reg r)
+    auto tcol = [&](int f, int r) -> int {
+      return (kGlu ? 16 * wave : 32 * wave + 16 * f) + 4 * g + r;
+    };
+    constexpr int NF = kGlu ? 1 : 2;
+    // the biases of the lane's output columns, the same for all its slots
+    float bgs[NF][4], bus[4];
+  #pragma unroll
+    for (int f = 0; f < NF; ++f)
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = n0 + tcol(f, r);
+        const bool has = a.bias && n < N;
+        bgs[f][r] = has ? ld16<F16>(a.bias[bias_base + n]) : 0.f;
+        if (f == 0) bus[r] = has && kGlu ? ld16<F16>(a.bias[bias_base + a.up_off + n]) : 0.f;
       }
-      o[r] = gv;
-    }
-  };
+    auto outv = [&](int f, int j, float (&o)[4]) {
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float gv = round16<F16>(acc[f][j][r] + bgs[f][r]);
+        if constexpr (kGlu) {
+          float u = round16<F16>(acc[1][j][r] + bus[r]);
+          if constexpr (CLAMP)
+            glu_clamp_with(a.clamp_limit, SILU ? MI355MOE_ACT_SILU : MI355MOE_ACT_SWIGLUOAI, N,
+                           n0 + tcol(f, r), gv, u);
+          float y;
+          if constexpr (SILU) {
+            y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
+          } else {
+            gv = gv > a.limit ? a.limit : gv;
+            u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
+            y = (u + 1.f) * x_sigmoid(gv, a.alpha);
+          }
+          gv = round16<F16>(y);
+        }
+        o[r] = gv;
+      }
+    };
 
-  if constexpr (QOUT) {
-    // e4m3 activation with one fp32 scale per (slot, 128 columns): the 8
-    // waves cover the tile's 128 columns (N % 128 == 0); lanes l, l+16, l+32,
-    // l+48 hold the same slot
-    constexpr int PITCH = NOUT + 16;
-    float (*s_amax)[BM] = reinterpret_cast<float (*)[BM]>(lds + BM * PITCH);
-    float* s_sc = reinterpret_cast<float*>(lds + BM * PITCH + WAVES * BM * 4);
-    float ov[TJ][4];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      outv(0, j, ov[j]);
-      float m = 1e-10f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[j][r]));
-      m = fmaxf(m, __shfl_xor(m, 16, 64));
-      m = fmaxf(m, __shfl_xor(m, 32, 64));
-      if (g == 0) s_amax[wave][16 * j + l16] = m;
-    }
-    __syncthreads();
-    if constexpr (MX) {
-      // MX activation for the w2 GEMM: one e8m0 code per 32 columns (the 16
-      // columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
-      // with ue8m0 scales, e2m1 as per_token_group_quant_mxfp4 (eps 1e-10);
-      // s_sc[slot][p] holds 1 / 2^code.  N % 32 == 0: groups past N (the
-      // last tile of an N % 128 != 0) are not written.
-      float (*s_inv)[4] = reinterpret_cast<float (*)[4]>(s_sc);
-      for (int i = tid; i < 4 * BM; i += 512) {
-        const int row = i >> 2, p = i & 3;
-        const float am = fmaxf(s_amax[2 * p][row], s_amax[2 * p + 1][row]);
-        int ex;
-        if constexpr (MX4) ex = ceil_log2(fmaxf(fabsf(am / 6.0f), 1e-10f));
-        else ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
-        s_inv[row][p] = 1.0f / pow2i(ex);
-        // groups past N inside the padded code row get 127 (scale 1.0): the
-        // w2 GEMM reads them, four codes at a time, against zero data
+    if constexpr (QOUT) {
+      // e4m3 activation with one fp32 scale per (slot, 128 columns): the 8
+      // waves cover the tile's 128 columns (N % 128 == 0); lanes l, l+16, l+32,
+      // l+48 hold the same slot
+      constexpr int PITCH = NOUT + 16;
+      float (*s_amax)[BM] = reinterpret_cast<float (*)[BM]>(lds + BM * PITCH);
+      float* s_sc = reinterpret_cast<float*>(lds + BM * PITCH + WAVES * BM * 4);
+      float ov[TJ][4];
+  #pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        outv(0, j, ov[j]);
+        float m = 1e-10f;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[j][r]));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        if (g == 0) s_amax[wave][16 * j + l16] = m;
+      }
+      __syncthreads();
+      if constexpr (MX) {
+        // MX activation for the w2 GEMM: one e8m0 code per 32 columns (the 16
+        // columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
+        // with ue8m0 scales, e2m1 as per_token_group_quant_mxfp4 (eps 1e-10);
+        // s_sc[slot][p] holds 1 / 2^code.  N % 32 == 0: groups past N (the
+        // last tile of an N % 128 != 0) are not written.
+        float (*s_inv)[4] = reinterpret_cast<float (*)[4]>(s_sc);
+        for (int i = tid; i < 4 * BM; i += 512) {
+          const int row = i >> 2, p = i & 3;
+          const float am = fmaxf(s_amax[2 * p][row], s_amax[2 * p + 1][row]);
+          int ex;
+          if constexpr (MX4) ex = ceil_log2(fmaxf(fabsf(am / 6.0f), 1e-10f));
+          else ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
+          s_inv[row][p] = 1.0f / pow2i(ex);
+          // groups past N inside the padded code row get 127 (scale 1.0): the
+          // w2 GEMM reads them, four codes at a time, against zero data
+          const int drow = s_drow[row];
+          if (drow >= 0 && n0 / 32 + p < a.q_mxs_ld)
+            static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] =
+                static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
+        }
+      } else {
+        float* ds = static_cast<float*>(qs);
+        const int64_t ngroups = N / 128;
+        if (tid < BM) {
+          float am = s_amax[0][tid];
+  #pragma unroll
+          for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
+          const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
+          s_sc[tid] = sc;
+          const int drow = s_drow[tid];
+          if (drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+        }
+      }
+      __syncthreads();
+  #pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int row = 16 * j + l16;
+        const float inv = MX ? s_sc[4 * row + (wave >> 1)] : 1.0f / s_sc[row];
+        if constexpr (MX4) {
+          // e2m1 pairs, the even column in the low nibble
+          uint32_t w = 0;
+  #pragma unroll
+          for (int r = 0; r < 4; ++r)
+            w |= fp4_code(fminf(fmaxf(ov[j][r] * inv, -6.f), 6.f)) << (4 * r);
+          *reinterpret_cast<uint16_t*>(lds + row * PITCH + tcol(0, 0) / 2) =
+              static_cast<uint16_t>(w);
+        } else {
+          const uint32_t w =
+              e4m3x4_sat(ov[j][0] * inv, ov[j][1] * inv, ov[j][2] * inv, ov[j][3] * inv);
+          *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
+        }
+      }
+      __syncthreads();
+      uint8_t* dq = static_cast<uint8_t*>(a.D);
+      // 16-byte chunks of an output row: 16 e4m3 or 32 e2m1 columns; N % 32 ==
+      // 0, so an e2m1 chunk lies wholly inside or wholly past N
+      constexpr int CPR = MX4 ? NOUT / 32 : NOUT / 16;
+      const int64_t orow = MX4 ? (a.ldd ? a.ldd : N / 2) : N;  // output row pitch (bytes)
+      for (int idx = tid; idx < BM * CPR; idx += 512) {
+        const int row = idx / CPR, ch = idx % CPR;
         const int drow = s_drow[row];
-        if (drow >= 0 && n0 / 32 + p < a.q_mxs_ld)
-          static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] =
-              static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
+        if (drow < 0 || n0 + ch * (MX4 ? 32 : 16) >= N) continue;
+        *reinterpret_cast<uint4*>(dq + static_cast<int64_t>(drow) * orow + (MX4 ? n0 / 2 : n0) +
+                                  ch * 16) =
+            *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
       }
     } else {
-      float* ds = static_cast<float*>(qs);
-      const int64_t ngroups = N / 128;
-      if (tid < BM) {
-        float am = s_amax[0][tid];
-#pragma unroll
-        for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
-        const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
-        s_sc[tid] = sc;
-        const int drow = s_drow[tid];
-        if (drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+      // 16-bit output staged in LDS (STORE tiles in two passes of 160 slots)
+      // and written with 16-byte row-contiguous stores
+      constexpr int PITCH = 2 * NOUT + 16;
+      // passes of a whole number of slot tiles each, as few as the ring holds
+      constexpr int PASSES = BM * PITCH <= RING ? 1 : BM / 2 * PITCH <= RING ? 2
+                           : BM / 4 * PITCH <= RING ? 4 : 5;
+      static_assert(BM / PASSES * PITCH <= RING && TJ % PASSES == 0, "staging passes");
+      constexpr int PROWS = BM / PASSES;
+      constexpr int PJ = TJ / PASSES;
+      uint16_t* d = static_cast<uint16_t*>(a.D);
+      const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
+      constexpr int CPR = 2 * NOUT / 16;
+  #pragma unroll
+      for (int pass = 0; pass < PASSES; ++pass) {
+  #pragma unroll
+        for (int f = 0; f < NF; ++f)
+  #pragma unroll
+          for (int jj = 0; jj < PJ; ++jj) {
+            const int j = pass * PJ + jj;
+            float o[4];
+            outv(f, j, o);
+            const int srow = 16 * jj + l16;
+            const uint32_t lo = to16<F16>(o[0]) | (to16<F16>(o[1]) << 16);
+            const uint32_t hi = to16<F16>(o[2]) | (to16<F16>(o[3]) << 16);
+            *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(f, 0)) = make_uint2(lo, hi);
+          }
+        __syncthreads();
+        for (int idx = tid; idx < PROWS * CPR; idx += 512) {
+          const int srow = idx / CPR, ch = idx % CPR;
+          const int drow = s_drow[pass * PROWS + srow];
+          const int64_t col = n0 + ch * 8;
+          if (drow < 0 || col >= N) continue;
+          const uint4 val = *reinterpret_cast<const uint4*>(lds + srow * PITCH + ch * 16);
+          uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
+          if (vec) {
+            *reinterpret_cast<uint4*>(dst) = val;
+          } else {
+            const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+  #pragma unroll
+            for (int k = 0; k < 8; ++k)
+              if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
+          }
+        }
+        if (pass + 1 < PASSES) __syncthreads();  // the staging area is rewritten
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int row = 16 * j + l16;
-      const float inv = MX ? s_sc[4 * row + (wave >> 1)] : 1.0f / s_sc[row];
-      if constexpr (MX4) {
-        // e2m1 pairs, the even column in the low nibble
-        uint32_t w = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          w |= fp4_code(fminf(fmaxf(ov[j][r] * inv, -6.f), 6.f)) << (4 * r);
-        *reinterpret_cast<uint16_t*>(lds + row * PITCH + tcol(0, 0) / 2) =
-            static_cast<uint16_t>(w);
-      } else {
-        const uint32_t w =
-            e4m3x4_sat(ov[j][0] * inv, ov[j][1] * inv, ov[j][2] * inv, ov[j][3] * inv);
-        *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
-      }
-    }
-    __syncthreads();
-    uint8_t* dq = static_cast<uint8_t*>(a.D);
-    // 16-byte chunks of an output row: 16 e4m3 or 32 e2m1 columns; N % 32 ==
-    // 0, so an e2m1 chunk lies wholly inside or wholly past N
-    constexpr int CPR = MX4 ? NOUT / 32 : NOUT / 16;
-    const int64_t orow = MX4 ? (a.ldd ? a.ldd : N / 2) : N;  // output row pitch (bytes)
-    for (int idx = tid; idx < BM * CPR; idx += 512) {
-      const int row = idx / CPR, ch = idx % CPR;
-      const int drow = s_drow[row];
-      if (drow < 0 || n0 + ch * (MX4 ? 32 : 16) >= N) continue;
-      *reinterpret_cast<uint4*>(dq + static_cast<int64_t>(drow) * orow + (MX4 ? n0 / 2 : n0) +
-                                ch * 16) =
-          *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
-    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  const bool clamp = kGlu && a.clamp_limit > 0.f;
+  if (!kGlu || a.act == MI355MOE_ACT_SILU) {
+    if (clamp) epilogue(T_{}, T_{});
+    else epilogue(T_{}, F_{});
   } else {
-    // 16-bit output staged in LDS (STORE tiles in two passes of 160 slots)
-    // and written with 16-byte row-contiguous stores
-    constexpr int PITCH = 2 * NOUT + 16;
-    // passes of a whole number of slot tiles each, as few as the ring holds
-    constexpr int PASSES = BM * PITCH <= RING ? 1 : BM / 2 * PITCH <= RING ? 2
-                         : BM / 4 * PITCH <= RING ? 4 : 5;
-    static_assert(BM / PASSES * PITCH <= RING && TJ % PASSES == 0, "staging passes");
-    constexpr int PROWS = BM / PASSES;
-    constexpr int PJ = TJ / PASSES;
-    uint16_t* d = static_cast<uint16_t*>(a.D);
-    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
-    constexpr int CPR = 2 * NOUT / 16;
-#pragma unroll
-    for (int pass = 0; pass < PASSES; ++pass) {
-#pragma unroll
-      for (int f = 0; f < NF; ++f)
-#pragma unroll
-        for (int jj = 0; jj < PJ; ++jj) {
-          const int j = pass * PJ + jj;
-          float o[4];
-          outv(f, j, o);
-          const int srow = 16 * jj + l16;
-          const uint32_t lo = to16<F16>(o[0]) | (to16<F16>(o[1]) << 16);
-          const uint32_t hi = to16<F16>(o[2]) | (to16<F16>(o[3]) << 16);
-          *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(f, 0)) = make_uint2(lo, hi);
-        }
-      __syncthreads();
-      for (int idx = tid; idx < PROWS * CPR; idx += 512) {
-        const int srow = idx / CPR, ch = idx % CPR;
-        const int drow = s_drow[pass * PROWS + srow];
-        const int64_t col = n0 + ch * 8;
-        if (drow < 0 || col >= N) continue;
-        const uint4 val = *reinterpret_cast<const uint4*>(lds + srow * PITCH + ch * 16);
-        uint16_t* dst = d + static_cast<int64_t>(drow) * N + col;
-        if (vec) {
-          *reinterpret_cast<uint4*>(dst) = val;
-        } else {
-          const uint32_t w[4] = {val.x, val.y, val.z, val.w};
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            if (col + k < N) dst[k] = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
-        }
-      }
-      if (pass + 1 < PASSES) __syncthreads();  // the staging area is rewritten
-    }
+    if (clamp) epilogue(F_{}, T_{});
+    else epilogue(F_{}, F_{});
   }
 }
 
