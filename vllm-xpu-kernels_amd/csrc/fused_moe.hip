@@ -205,6 +205,21 @@ __global__ __launch_bounds__(256) void repack_codes_kernel(const uint8_t* __rest
   dst[i] = c < w ? src[r * w + c] : static_cast<uint8_t>(127);
 }
 
+// Activation scales by sorted position: st[g * ldp + p] = the scale of
+// group g of the row that position p holds (its token for w13), 0 for
+// padding positions.  Positions past max_padded up to ldp are not written
+// (no GEMM tile reads them).
+__global__ __launch_bounds__(256) void scales_by_position_kernel(
+    const int32_t* __restrict__ sorted, const float* __restrict__ s, float* __restrict__ st,
+    int64_t groups, int64_t ldp, int64_t max_padded, int32_t num_valid, int32_t a_div) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t g = blockIdx.y;
+  if (p >= max_padded) return;
+  const int32_t rid = sorted[p];
+  const bool ok = rid >= 0 && rid < num_valid;
+  st[g * ldp + p] = ok ? s[static_cast<int64_t>(rid / a_div) * groups + g] : 0.f;
+}
+
 // Rows of w units [rows, w] -> [rows, ld] (ld > w), the padding zeroed: the
 // caller's e2m1 hidden states copied to 128-byte-aligned rows (a zero e2m1
 // code meets only the zeroed weights past K).
@@ -341,7 +356,12 @@ struct FusedLayout {
   float* xs;      // [T, H/128]
   void* act;      // bf16 [max_padded, K2] or e4m3 [max_padded, K2] (mxfp4 w4a4:
                   // packed e2m1 [max_padded, K2/2])
-  float* acts;    // [max_padded, K2/128]
+  float* acts;    // [max_padded, K2/128] (ldp: [K2/128, ldp], by sorted position)
+  // fp8 block-scaled prefill on the 320-slot kernel: both GEMMs read their
+  // activation scales by sorted position, [K/128, ldp] (ldp: max_padded
+  // rounded up to 64; 0 otherwise); xst holds the hidden states' scales so
+  float* xst;
+  int64_t ldp;
   uint8_t* xs8;   // MX: e8m0 scales of the quantised hidden [T, ld1]
   uint8_t* acts8; // MX: e8m0 scales of the activation [max_padded, ld2]
   int64_t ld1, ld2;
@@ -421,6 +441,15 @@ bool stream_w2_finishes_w13_enabled() {
 // each token-major w2 wave quantises for its own slot (GemmArgs::tok_xq) --
 // no partial-sum launch.  MI355MOE_STREAM_KHALVES=0 keeps the split launch
 // and its finalize (the same arithmetic).  Read per call.
+// fp8 block-scaled prefill on the 320-slot kernel: activation scales stored
+// by sorted position ([K/128, positions]), gathered once per layer, instead
+// of read row by row inside the GEMM (one cache line per slot row and K
+// stage).  MI355MOE_SCALES_BY_POSITION=0 keeps the row-major scales (the
+// same arithmetic).  Read per call.
+bool scales_by_position_enabled() {
+  const char* v = getenv("MI355MOE_SCALES_BY_POSITION");
+  return !(v && v[0] == '0');
+}
 bool stream_khalves_enabled() {
   const char* v = getenv("MI355MOE_STREAM_KHALVES");
   return !(v && v[0] == '0');
@@ -496,7 +525,13 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
     L.xs = c.take<float>(a->num_tokens * (a->hidden / 128));
     L.act = c.take<uint8_t>(L.max_padded * K2);
-    L.acts = c.take<float>(L.max_padded * (K2 / 128));
+    if (L.tile == TILE_WIDE && glu && K2 % 128 == 0 && scales_by_position_enabled()) {
+      L.ldp = (L.max_padded + 63) / 64 * 64;
+      L.xst = c.take<float>((a->hidden / 128) * L.ldp);
+      L.acts = c.take<float>((K2 / 128) * L.ldp);
+    } else {
+      L.acts = c.take<float>(L.max_padded * (K2 / 128));
+    }
   } else {
     L.act = c.take<uint16_t>(L.max_padded * K2);
   }
@@ -780,6 +815,13 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     }
     MI_LAUNCH_CHECK();
   }
+  if (L.xst) {  // the hidden states' scales by sorted position
+    const dim3 sg(static_cast<unsigned>(cdiv(L.max_padded, 256)), static_cast<unsigned>(H / 128));
+    scales_by_position_kernel<<<sg, dim3(256), 0, st>>>(
+        L.sorted, preq ? static_cast<const float*>(a->hidden_scale) : L.xs, L.xst, H / 128,
+        L.ldp, L.max_padded, static_cast<int32_t>(L.slots), static_cast<int32_t>(k));
+    MI_LAUNCH_CHECK();
+  }
   if (int m = mark(2)) return m;
 
   // gelu / gelu_tanh / swiglustep / relu2_no_mul: w13 stores G1, a separate
@@ -790,7 +832,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
          : L.xp ? static_cast<const void*>(L.xp) : a->hidden_states;
   g1.lda = L.xp ? L.p1 : 0;
   g1.ldd = L.p2;
-  g1.a_scale = preq ? static_cast<const float*>(a->hidden_scale) : (fp8 ? L.xs : nullptr);
+  g1.a_scale = L.xst ? L.xst
+               : preq ? static_cast<const float*>(a->hidden_scale) : (fp8 ? L.xs : nullptr);
+  g1.a_scale_tld = L.xst ? L.ldp : 0;
+  g1.q_scale_tld = L.xst ? L.ldp : 0;  // the w13 epilogue writes w2's scales by position
   if (mx) {
     g1.a_mxs = a->hidden_scale && !repack ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
     g1.a_mxs_ld = a->hidden_scale && !repack ? H / 32 : L.ld1;
@@ -880,6 +925,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g2.A = L.act;
   g2.lda = L.p2;
   g2.a_scale = fp8 ? L.acts : nullptr;
+  g2.a_scale_tld = L.xst ? L.ldp : 0;
   if (mx) {
     g2.a_mxs = L.acts8;
     g2.a_mxs_ld = L.ld2;

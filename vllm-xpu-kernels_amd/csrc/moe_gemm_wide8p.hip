@@ -224,9 +224,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   {
     const int p = s_wave ? 64 * wave + lane : lane;
     const int ar = s_arow[16 * (p % TJ) + p / TJ];
-    soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) *
-           (MX ? static_cast<uint32_t>(a.a_mxs_ld) : static_cast<uint32_t>(nkb) * 4u);
+    if (!MX && a.a_scale_tld)  // by sorted position: padding slots read their own (unused) entry
+      soff = static_cast<uint32_t>(blk * BM + 16 * (p % TJ) + p / TJ) * 4u;
+    else
+      soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) *
+             (MX ? static_cast<uint32_t>(a.a_mxs_ld) : static_cast<uint32_t>(nkb) * 4u);
   }
+  // byte step of the scale transfer from one K stage to the next
+  const uint32_t sstep = !MX && a.a_scale_tld ? static_cast<uint32_t>(a.a_scale_tld) * 4u : 4u;
   // the wave's weight fragments f = 0, 1: GLU gate rows 16 wave + l16 and the
   // matching up rows; STORE rows 32 wave + 16 f + l16.  Lane (l16, g) loads
   // the 32 bytes at K byte 32 g of its row of the stage (mxfp8: the 16 bytes
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       dma4(soff + c0, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
       dma4(soff + c1, sbase, s_wave ? slot + A_BYTES + BM * 4 + 256 * wave : ring0 + DUMMY);
     } else {
-      dma4(soff + 4u * kt, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
+      dma4(soff + sstep * kt, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
     }
   };
   // weight fragments of stage kt: the wave's 4 KB region of weight slot
@@ -621,7 +626,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
           const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
           s_sc[tid] = sc;
           const int drow = s_drow[tid];
-          if (drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+          if (drow >= 0) {
+            if (a.q_scale_tld) ds[static_cast<int64_t>(ntile) * a.q_scale_tld + drow] = sc;
+            else ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+          }
         }
       }
       __syncthreads();
