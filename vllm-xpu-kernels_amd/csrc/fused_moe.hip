@@ -220,6 +220,29 @@ __global__ __launch_bounds__(256) void scales_by_position_kernel(
   st[g * ldp + p] = ok ? s[static_cast<int64_t>(rid / a_div) * groups + g] : 0.f;
 }
 
+// e8m0 code words by sorted position: st[w * ldp + p] = codes 4w .. 4w + 3
+// of the row that position p holds (its token for w13; codes past the
+// row's w codes read 127, scale 1.0), 0x7f7f7f7f for padding positions.
+__global__ __launch_bounds__(256) void codes_by_position_kernel(
+    const int32_t* __restrict__ sorted, const uint8_t* __restrict__ c, uint32_t* __restrict__ st,
+    int64_t w, int64_t ld, int64_t ldp, int64_t max_padded, int32_t num_valid, int32_t a_div) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t wd = blockIdx.y;
+  if (p >= max_padded) return;
+  const int32_t rid = sorted[p];
+  uint32_t v = 0x7f7f7f7fu;
+  if (rid >= 0 && rid < num_valid) {
+    const uint8_t* row = c + static_cast<int64_t>(rid / a_div) * ld;
+    v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t j = 4 * wd + i;
+      v |= static_cast<uint32_t>(j < w ? row[j] : 127u) << (8 * i);
+    }
+  }
+  st[wd * ldp + p] = v;
+}
+
 // Rows of w units [rows, w] -> [rows, ld] (ld > w), the padding zeroed: the
 // caller's e2m1 hidden states copied to 128-byte-aligned rows (a zero e2m1
 // code meets only the zeroed weights past K).
@@ -362,6 +385,9 @@ struct FusedLayout {
   // rounded up to 64; 0 otherwise); xst holds the hidden states' scales so
   float* xst;
   int64_t ldp;
+  // MX on the 320-slot kernel: the hidden states' e8m0 code words by sorted
+  // position, [ld1 / 4, ldp] (and the activation's, acts8, [ld2 / 4, ldp])
+  uint32_t* xs8t;
   uint8_t* xs8;   // MX: e8m0 scales of the quantised hidden [T, ld1]
   uint8_t* acts8; // MX: e8m0 scales of the activation [max_padded, ld2]
   int64_t ld1, ld2;
@@ -520,7 +546,13 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     }
     L.act = c.take<uint8_t>(L.max_padded * (gemm_recipe(a) == RECIPE_MX4A4
                                                 ? (L.p2 ? L.p2 : K2 / 2) : K2));
-    L.acts8 = c.take<uint8_t>(L.max_padded * L.ld2);
+    if (L.tile == TILE_WIDE && scales_by_position_enabled()) {
+      L.ldp = (L.max_padded + 63) / 64 * 64;
+      L.xs8t = c.take<uint32_t>((L.ld1 / 4) * L.ldp);
+      L.acts8 = c.take<uint8_t>(L.ld2 * L.ldp);
+    } else {
+      L.acts8 = c.take<uint8_t>(L.max_padded * L.ld2);
+    }
   } else if (fp8) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
     L.xs = c.take<float>(a->num_tokens * (a->hidden / 128));
@@ -793,8 +825,9 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     if (rc) return rc;
   }
   // caller's codes [T, H/32] with rows not a multiple of 4 bytes: copied into
-  // 4-byte rows, which the 320-slot kernels move four codes at a time
-  const bool repack = mx && a->hidden_scale && L.ld1 != H / 32;
+  // 4-byte rows, which the 320-slot kernels move four codes at a time (unless
+  // the codes are gathered by position below, which pads the rows itself)
+  const bool repack = mx && a->hidden_scale && L.ld1 != H / 32 && !L.xs8t;
   if (repack) {
     const int64_t n = T * L.ld1;
     repack_codes_kernel<<<static_cast<unsigned>(cdiv(n, 256)), dim3(256), 0, st>>>(
@@ -813,6 +846,15 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
       repack_rows_kernel<uint8_t><<<static_cast<unsigned>(cdiv(n, 256)), dim3(256), 0, st>>>(
           static_cast<const uint8_t*>(a->hidden_states), L.xp, rb, L.p1, n);
     }
+    MI_LAUNCH_CHECK();
+  }
+  if (L.xs8t) {  // the hidden states' e8m0 codes by sorted position
+    const bool own = !a->hidden_scale;  // the layer's own codes, L.xs8: [T, ld1]
+    const dim3 sg(static_cast<unsigned>(cdiv(L.max_padded, 256)), static_cast<unsigned>(L.ld1 / 4));
+    codes_by_position_kernel<<<sg, dim3(256), 0, st>>>(
+        L.sorted, own ? L.xs8 : static_cast<const uint8_t*>(a->hidden_scale), L.xs8t,
+        own ? L.ld1 : H / 32, own ? L.ld1 : H / 32, L.ldp, L.max_padded,
+        static_cast<int32_t>(L.slots), static_cast<int32_t>(k));
     MI_LAUNCH_CHECK();
   }
   if (L.xst) {  // the hidden states' scales by sorted position
@@ -837,9 +879,12 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   g1.a_scale_tld = L.xst ? L.ldp : 0;
   g1.q_scale_tld = L.xst ? L.ldp : 0;  // the w13 epilogue writes w2's scales by position
   if (mx) {
-    g1.a_mxs = a->hidden_scale && !repack ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
-    g1.a_mxs_ld = a->hidden_scale && !repack ? H / 32 : L.ld1;
+    g1.a_mxs = L.xs8t ? reinterpret_cast<const uint8_t*>(L.xs8t)
+               : a->hidden_scale && !repack ? static_cast<const uint8_t*>(a->hidden_scale) : L.xs8;
+    g1.a_mxs_ld = a->hidden_scale && !repack && !L.xs8t ? H / 32 : L.ld1;
     g1.q_mxs_ld = L.ld2;
+    g1.a_scale_tld = L.xs8t ? L.ldp : 0;
+    g1.q_scale_tld = L.xs8t ? L.ldp : 0;
   }
   g1.B = a->w13;
   g1.b_scale = a->w13_scale;
@@ -929,6 +974,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   if (mx) {
     g2.a_mxs = L.acts8;
     g2.a_mxs_ld = L.ld2;
+    g2.a_scale_tld = L.xs8t ? L.ldp : 0;
   }
   g2.B = a->w2;
   g2.b_scale = a->w2_scale;

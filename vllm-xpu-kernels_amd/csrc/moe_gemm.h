@@ -158,11 +158,12 @@ struct GemmArgs {
   // STREAM w2 of the fused layer (16-bit activation): its activation rows
   // rebuilt from the w13 partials (G1Fin) instead of read from A.
   G1Fin g1f;
-  // 320-slot fp8 block-scaled kernel: activation scales by sorted position
-  // instead of by row (a_scale[kb * a_scale_tld + position], 0: the row-major
-  // [rows, K/128]), and the w13 epilogue's output scales the same way
-  // (q_scale_tld: qs[ntile * q_scale_tld + position]).  A stage's 320 scales
-  // are then about ten cache lines instead of one line per slot row.
+  // 320-slot fp8 / MX kernel: activation scales by sorted position instead
+  // of by row (a_scale[kb * a_scale_tld + position], 0: the row-major
+  // [rows, K/128]; MX: the 4-code words of a_mxs, word w of a position at
+  // (w * a_scale_tld + position) * 4 bytes), and the w13 epilogue's output
+  // scales / codes the same way (q_scale_tld).  A stage's 320 scales are then
+  // about ten cache lines instead of one line per slot row.
   int64_t a_scale_tld, q_scale_tld;
   // 320-slot e2m1 x e2m1 kernel: row pitch in bytes of A and of its e2m1
   // output D (0: the packed K / 2 and N / 2).  A pitch that is a multiple of

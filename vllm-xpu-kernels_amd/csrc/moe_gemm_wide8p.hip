@@ -224,14 +224,15 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   {
     const int p = s_wave ? 64 * wave + lane : lane;
     const int ar = s_arow[16 * (p % TJ) + p / TJ];
-    if (!MX && a.a_scale_tld)  // by sorted position: padding slots read their own (unused) entry
+    if (a.a_scale_tld)  // by sorted position: padding slots read their own (unused) entry
       soff = static_cast<uint32_t>(blk * BM + 16 * (p % TJ) + p / TJ) * 4u;
     else
       soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) *
              (MX ? static_cast<uint32_t>(a.a_mxs_ld) : static_cast<uint32_t>(nkb) * 4u);
   }
   // byte step of the scale transfer from one K stage to the next
-  const uint32_t sstep = !MX && a.a_scale_tld ? static_cast<uint32_t>(a.a_scale_tld) * 4u : 4u;
+  // (MX by position: code word w of position P at (w * a_scale_tld + P) * 4)
+  const uint32_t sstep = a.a_scale_tld ? static_cast<uint32_t>(a.a_scale_tld) * 4u : 4u;
   // the wave's weight fragments f = 0, 1: GLU gate rows 16 wave + l16 and the
   // matching up rows; STORE rows 32 wave + 16 f + l16.  Lane (l16, g) loads
   // the 32 bytes at K byte 32 g of its row of the stage (mxfp8: the 16 bytes
@@ -294,8 +295,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       // (the second word re-reads the first past the code row)
       const uint32_t c0 = 8u * static_cast<uint32_t>(kt);
       const uint32_t c1 = c0 + 4u < static_cast<uint32_t>(a.a_mxs_ld) ? c0 + 4u : c0;
-      dma4(soff + c0, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
-      dma4(soff + c1, sbase, s_wave ? slot + A_BYTES + BM * 4 + 256 * wave : ring0 + DUMMY);
+      const uint32_t o0 = a.a_scale_tld ? (c0 >> 2) * sstep : c0;
+      const uint32_t o1 = a.a_scale_tld ? (c1 >> 2) * sstep : c1;
+      dma4(soff + o0, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
+      dma4(soff + o1, sbase, s_wave ? slot + A_BYTES + BM * 4 + 256 * wave : ring0 + DUMMY);
     } else {
       dma4(soff + sstep * kt, sbase, s_wave ? slot + A_BYTES + 256 * wave : ring0 + DUMMY);
     }
@@ -612,9 +615,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
           // groups past N inside the padded code row get 127 (scale 1.0): the
           // w2 GEMM reads them, four codes at a time, against zero data
           const int drow = s_drow[row];
-          if (drow >= 0 && n0 / 32 + p < a.q_mxs_ld)
-            static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] =
-                static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
+          if (drow >= 0 && n0 / 32 + p < a.q_mxs_ld) {
+            const uint8_t code = static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
+            // by position: the tile's four codes are byte p of word n0 / 128
+            if (a.q_scale_tld)
+              static_cast<uint8_t*>(qs)[((n0 >> 7) * a.q_scale_tld + drow) * 4 + p] = code;
+            else
+              static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] = code;
+          }
         }
       } else {
         float* ds = static_cast<float*>(qs);
