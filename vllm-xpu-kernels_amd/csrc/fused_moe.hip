@@ -557,7 +557,9 @@ FusedLayout plan(const mi355moe_fused_moe_args* a, uint8_t* base) {
     L.xq = c.take<uint8_t>(a->num_tokens * a->hidden);
     L.xs = c.take<float>(a->num_tokens * (a->hidden / 128));
     L.act = c.take<uint8_t>(L.max_padded * K2);
-    if (L.tile == TILE_WIDE && glu && K2 % 128 == 0 && scales_by_position_enabled()) {
+    // (the 320-slot and 128-slot fp8 kernels, which take K <= 8192)
+    if ((L.tile == TILE_WIDE || L.tile == TILE_BIG) && glu && K2 % 128 == 0 &&
+        a->hidden <= 8192 && K2 <= 8192 && scales_by_position_enabled()) {
       L.ldp = (L.max_padded + 63) / 64 * 64;
       L.xst = c.take<float>((a->hidden / 128) * L.ldp);
       L.acts = c.take<float>((K2 / 128) * L.ldp);

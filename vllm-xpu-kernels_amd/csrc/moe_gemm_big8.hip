@@ -217,10 +217,18 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
   const int nd = DMA_PER_WAVE + (wave == 0 ? 2 : 0);
   const float* ssrc0 = a.a_scale;
   const float* ssrc1 = a.a_scale;
+  // scale step from one K stage to the next: 1 (row-major) or the by-position
+  // pitch, whose 128 scales of a stage are four cache lines
+  const int64_t sstep = a.a_scale_tld ? a.a_scale_tld : 1;
   if (wave == 0) {
-    const int r0 = s_arow[lane], r1 = s_arow[64 + lane];
-    ssrc0 += static_cast<int64_t>(r0 >= 0 ? r0 : 0) * nkb;
-    ssrc1 += static_cast<int64_t>(r1 >= 0 ? r1 : 0) * nkb;
+    if (a.a_scale_tld) {
+      ssrc0 += static_cast<int64_t>(blk) * BM + lane;
+      ssrc1 += static_cast<int64_t>(blk) * BM + 64 + lane;
+    } else {
+      const int r0 = s_arow[lane], r1 = s_arow[64 + lane];
+      ssrc0 += static_cast<int64_t>(r0 >= 0 ? r0 : 0) * nkb;
+      ssrc1 += static_cast<int64_t>(r1 >= 0 ? r1 : 0) * nkb;
+    }
   }
   const uint32_t ring0 = lds_off(lds);
   const uint32_t dst0 = DMA_PER_WAVE * wave * 1024;
@@ -230,8 +238,8 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
     for (int q = 0; q < DMA_PER_WAVE; ++q)
       dma16(src[q] + kt * kstep(q), __builtin_amdgcn_readfirstlane(base + dst0 + q * 1024));
     if (wave == 0) {
-      dma4(ssrc0 + kt, __builtin_amdgcn_readfirstlane(base + S_OFF));
-      dma4(ssrc1 + kt, __builtin_amdgcn_readfirstlane(base + S_OFF + 256));
+      dma4(ssrc0 + kt * sstep, __builtin_amdgcn_readfirstlane(base + S_OFF));
+      dma4(ssrc1 + kt * sstep, __builtin_amdgcn_readfirstlane(base + S_OFF + 256));
     }
   };
 
@@ -316,8 +324,8 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
           if (q < DMA_PER_WAVE)
             dma16(src[q] + kn * kstep(q), __builtin_amdgcn_readfirstlane(dbase + dst0 + q * 1024));
         if (i == 3 && wave == 0) {
-          dma4(ssrc0 + (kt + NSTAGE), __builtin_amdgcn_readfirstlane(dbase + S_OFF));
-          dma4(ssrc1 + (kt + NSTAGE), __builtin_amdgcn_readfirstlane(dbase + S_OFF + 256));
+          dma4(ssrc0 + (kt + NSTAGE) * sstep, __builtin_amdgcn_readfirstlane(dbase + S_OFF));
+          dma4(ssrc1 + (kt + NSTAGE) * sstep, __builtin_amdgcn_readfirstlane(dbase + S_OFF + 256));
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -405,7 +413,10 @@ __global__ __launch_bounds__(512) void moe_gemm_big8_kernel(const GemmArgs a, vo
       const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
       const float inv = 1.0f / sc;
       const int drow = s_drow[row];
-      if (wn == 0 && g == 0 && drow >= 0) ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+      if (wn == 0 && g == 0 && drow >= 0) {
+        if (a.q_scale_tld) ds[static_cast<int64_t>(ntile) * a.q_scale_tld + drow] = sc;
+        else ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+      }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const uint32_t w = e4m3x4_sat(ov[i][j][0] * inv, ov[i][j][1] * inv, ov[i][j][2] * inv,
