@@ -237,20 +237,31 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   // matching up rows; STORE rows 32 wave + 16 f + l16.  Lane (l16, g) loads
   // the 32 bytes at K byte 32 g of its row of the stage (mxfp8: the 16 bytes
   // at 16 g and at 64 + 16 g, the scaled MFMA's e4m3 operand order).
-  uint32_t woff[2];
+  // fp8 / mxfp8: a fragment's 16 rows x 128 bytes are staged like the
+  // activation rows (LDS row t holds fragment row slot_of_lds_row(t), its
+  // 16-byte chunk c source chunk c ^ swz(t)): transfer (f, h) moves LDS rows
+  // 8 h .. 8 h + 7 of fragment f, eight whole 128-byte rows of the stage
+  // (contiguous in the K-blocked layout), so every cache line it touches is
+  // read whole, and the fragments are read with the activation offsets.
+  uint32_t woff[2][2];
 #pragma unroll
-  for (int f = 0; f < 2; ++f) {
-    const int r = kGlu ? (f ? 128 : 0) + 16 * wave + l16 : 32 * wave + 16 * f + l16;
-    woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row) +
-              (MX ? 16u : 32u) * static_cast<uint32_t>(g);
-  }
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = 8 * h + (lane >> 3);
+      const int fr = slot_of_lds_row(t);
+      const int r = kGlu ? (f ? 128 : 0) + 16 * wave + fr : 32 * wave + 16 * f + fr;
+      woff[f][h] = static_cast<uint32_t>(wrow_of(r) * wst.row) +
+                   (static_cast<uint32_t>((lane & 7) ^ swz(t)) << 4);
+    }
   // e2m1 (K-blocked [E, K/32, ldb_rows, 16 bytes]): lane (l16, g) of half h
-  // moves the 16 bytes of 32-K block 8 kt + 4 h + g of its row
+  // moves the 16 bytes of 32-K block 8 kt + 4 h + g of its row (eight whole
+  // lines per transfer already), into the wave's region in lane order
   if constexpr (MX4) {
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
       const int r = kGlu ? (f ? 128 : 0) + 16 * wave + l16 : 32 * wave + 16 * f + l16;
-      woff[f] = static_cast<uint32_t>(wrow_of(r) * wst.row);
+      woff[f][0] = static_cast<uint32_t>(wrow_of(r) * wst.row);
     }
   }
   // MX weight codes (K-blocked [E, K/32, ldb_rows]), 4 bytes per lane into
@@ -315,9 +326,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         uint32_t off;
         if constexpr (MX4) {  // blocks past K re-read the last block
           const int b = 8 * kt + 4 * h + g;
-          off = woff[f] + static_cast<uint32_t>(b < nblk ? b : nblk - 1) * wkstep;
+          off = woff[f][0] + static_cast<uint32_t>(b < nblk ? b : nblk - 1) * wkstep;
         } else {
-          off = woff[f] + kofs + (MX ? 64u : 16u) * h;
+          off = woff[f][h] + kofs;
         }
         dma16(off, wbase, wring + slot * WSLOT + (2 * f + h) * 1024);
       }
@@ -330,10 +341,18 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
            ring0 + C_OFF + slot * CSLOT + wave * 256);
     }
   };
-  auto read_w = [&](int slot, i32x8_t (&w)[2]) {
-    const uint8_t* W = lds + W_OFF + slot * WSLOT + wave * 4096 + 16 * lane;
+  // the wave's weight fragments of ring slot `slot` (o0, o1: the activation
+  // fragment offsets of the lane)
+  auto read_w = [&](int slot, i32x8_t (&w)[2], int o0, int o1) {
+    if constexpr (MX4) {
+      const uint8_t* W = lds + W_OFF + slot * WSLOT + wave * 4096 + 16 * lane;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) w[f] = ld32(W, 2 * f * 1024, (2 * f + 1) * 1024);
+      for (int f = 0; f < 2; ++f) w[f] = ld32(W, 2 * f * 1024, (2 * f + 1) * 1024);
+    } else {
+      const uint8_t* W = lds + W_OFF + slot * WSLOT + wave * 4096;
+#pragma unroll
+      for (int f = 0; f < 2; ++f) w[f] = ld32(W + f * 2048, o0, o1);
+    }
   };
   // mxfp8: e8m0 code of the lane's weight row l16 of fragment f for its 32-K
   // block g of the stage
@@ -416,7 +435,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
                 *reinterpret_cast<uint4*>(W + (2 * f + h) * 1024) = make_uint4(0, 0, 0, 0);
         }
       }
-      read_w(kt & 1, wc);
+      read_w(kt & 1, wc, xo0, xo1);
       if constexpr (MX4 && NJ > 0) {
         uint32_t wcode[2][2];
         read_wc4(kt & 1, wcode);
