@@ -30,9 +30,9 @@
 // are skipped in pairs (the K loop is specialised on their number).
 //
 // LDS layout of an activation slot: rows of 128 bytes whose 16-byte chunk c
-// holds source chunk c ^ ((r >> 1) & 7), then the 320 scales ordered so
-// that lane l16 finds the scales of its slots 16 j + l16 (j = 0..19) at 20
-// consecutive floats.  Within each group of 16 rows, row t holds slot
+// holds source chunk c ^ ((r >> 1) & 7), then the 320 scales in slot order
+// (with scales by sorted position each wave's transfer reads 256 contiguous
+// bytes; lane l16 reads the scale of slot 16 j + l16 at float 16 j + l16).  Within each group of 16 rows, row t holds slot
 // (t >> 1) + 8 (t & 1): lane l16 reads row 2 (l16 & 7) + (l16 >> 3), so
 // lanes 0-7 read even rows and lanes 8-15 odd rows, and with the chunk
 // swizzle each 8-lane group covers one half of the banks.  A 16-byte read of
@@ -216,16 +216,16 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     return static_cast<uint32_t>((lane & 7) ^ swz(r)) << 4;
   };
   // scales: waves 0-4 move them, LDS position p = 64 wave + lane holding the
-  // scale of slot 16 (p % 20) + p / 20 (mxfp8: the four e8m0 codes of the
-  // stage's 32-K blocks); waves 5-7 issue the same DMA (so that no branch
-  // splits the K loop) into a dummy area
+  // scale of slot p (mxfp8: the four e8m0 codes of the stage's 32-K blocks);
+  // waves 5-7 issue the same DMA as wave 0 (so that no branch splits the K
+  // loop) into a dummy area
   const bool s_wave = wave < BM / 64;
   uint32_t soff = 0;
   {
     const int p = s_wave ? 64 * wave + lane : lane;
-    const int ar = s_arow[16 * (p % TJ) + p / TJ];
+    const int ar = s_arow[p];
     if (a.a_scale_tld)  // by sorted position: padding slots read their own (unused) entry
-      soff = static_cast<uint32_t>(blk * BM + 16 * (p % TJ) + p / TJ) * 4u;
+      soff = static_cast<uint32_t>(blk * BM + p) * 4u;
     else
       soff = static_cast<uint32_t>(ar >= 0 ? ar : 0) *
              (MX ? static_cast<uint32_t>(a.a_mxs_ld) : static_cast<uint32_t>(nkb) * 4u);
@@ -440,14 +440,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         uint32_t wcode[2][2];
         read_wc4(kt & 1, wcode);
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
-        const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + TJ * l16;
+        const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + l16;
         i32x8_t x = ld32(S, xo0, xo1);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           i32x8_t xn = x;
           if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
-          const uint32_t xc0 = (xsp[j] >> (8 * g)) & 0xffu;       // block g
-          const uint32_t xc1 = (xsp[BM + j] >> (8 * g)) & 0xffu;  // block 4 + g
+          const uint32_t xc0 = (xsp[16 * j] >> (8 * g)) & 0xffu;       // block g
+          const uint32_t xc1 = (xsp[BM + 16 * j] >> (8 * g)) & 0xffu;  // block 4 + g
           // an e2m1 operand is four VGPRs: the low half of a fragment feeds
           // K-step 0, the high half K-step 1
 #pragma unroll
@@ -470,13 +470,13 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         uint32_t wcode[2];
         read_wc(kt & 1, wcode);
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
-        const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + TJ * l16;
+        const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + l16;
         i32x8_t x = ld32(S, xo0, xo1);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           i32x8_t xn = x;
           if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
-          const uint32_t xcode = (xsp[j] >> (8 * g)) & 0xffu;  // slot's 32-K block g
+          const uint32_t xcode = (xsp[16 * j] >> (8 * g)) & 0xffu;  // slot's 32-K block g
           acc[0][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               wc[0], x, acc[0][j], 0, 0, 0, wcode[0], 0, xcode);
           acc[1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       } else if constexpr (NJ > 0) {
         const float ws0 = s_wsc[wsel0][kt], ws1 = s_wsc[wsel1][kt];
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
-        const float* xsp = reinterpret_cast<const float*>(S + A_BYTES) + TJ * l16;
+        const float* xsp = reinterpret_cast<const float*>(S + A_BYTES) + l16;
         // software pipeline: the scaling FMAs of slot tile j-1 follow the
         // MFMAs of tile j, so no wave waits for its own MFMA results
         i32x8_t x = ld32(S, xo0, xo1);
@@ -500,7 +500,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         for (int j = 0; j < NJ; ++j) {
           i32x8_t xn = x;
           if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
-          const float xs = xsp[j];
+          const float xs = xsp[16 * j];
           const f32x4_t p0 = mfma8(wc[0], x);
           const f32x4_t p1 = mfma8(wc[1], x);
 #pragma unroll
