@@ -207,17 +207,29 @@ __global__ __launch_bounds__(256) void repack_codes_kernel(const uint8_t* __rest
 
 // Activation scales by sorted position: st[g * ldp + p] = the scale of
 // group g of the row that position p holds (its token for w13), 0 for
-// padding positions.  Positions past max_padded up to ldp are not written
-// (no GEMM tile reads them).
+// padding positions.  One thread per position walks the row's groups (16-byte
+// loads of one row, stores coalesced across the wave's positions).
+// Positions past max_padded up to ldp are not written (no GEMM tile reads
+// them).
 __global__ __launch_bounds__(256) void scales_by_position_kernel(
     const int32_t* __restrict__ sorted, const float* __restrict__ s, float* __restrict__ st,
     int64_t groups, int64_t ldp, int64_t max_padded, int32_t num_valid, int32_t a_div) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t g = blockIdx.y;
   if (p >= max_padded) return;
   const int32_t rid = sorted[p];
   const bool ok = rid >= 0 && rid < num_valid;
-  st[g * ldp + p] = ok ? s[static_cast<int64_t>(rid / a_div) * groups + g] : 0.f;
+  const float* row = s + static_cast<int64_t>(ok ? rid / a_div : 0) * groups;
+  int64_t g = 0;
+  if ((groups & 3) == 0 && (reinterpret_cast<uintptr_t>(s) & 15) == 0) {
+    for (; g < groups; g += 4) {
+      const float4 v = ok ? *reinterpret_cast<const float4*>(row + g) : make_float4(0.f, 0.f, 0.f, 0.f);
+      st[g * ldp + p] = v.x;
+      st[(g + 1) * ldp + p] = v.y;
+      st[(g + 2) * ldp + p] = v.z;
+      st[(g + 3) * ldp + p] = v.w;
+    }
+  }
+  for (; g < groups; ++g) st[g * ldp + p] = ok ? row[g] : 0.f;
 }
 
 // e8m0 code words by sorted position: st[w * ldp + p] = codes 4w .. 4w + 3
@@ -860,8 +872,7 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     MI_LAUNCH_CHECK();
   }
   if (L.xst) {  // the hidden states' scales by sorted position
-    const dim3 sg(static_cast<unsigned>(cdiv(L.max_padded, 256)), static_cast<unsigned>(H / 128));
-    scales_by_position_kernel<<<sg, dim3(256), 0, st>>>(
+    scales_by_position_kernel<<<static_cast<unsigned>(cdiv(L.max_padded, 256)), dim3(256), 0, st>>>(
         L.sorted, preq ? static_cast<const float*>(a->hidden_scale) : L.xs, L.xst, H / 128,
         L.ldp, L.max_padded, static_cast<int32_t>(L.slots), static_cast<int32_t>(k));
     MI_LAUNCH_CHECK();
