@@ -100,6 +100,27 @@ def test_per_token_group_quant_mxfp4_bit_exact(dev, rows, cols):
     assert torch.equal(q.cpu().view(torch.uint8), rq)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k", [0, -3, 5])
+def test_mxfp4_quant_every_16bit_value(dev, dt, k):
+    """Every finite 16-bit value of magnitude <= 6, in groups of 32 led by a 6
+    (group scale 1), times 2^k (scale 2^k): the device's e2m1 codes for
+    16-bit input (the hardware conversion, round to nearest even, after the
+    operands are moved 2^-12 of themselves toward zero) equal the oracle's
+    strict-midpoint rounding -- every midpoint tie, values that round to a
+    signed zero, and -0 included."""
+    x = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(dt).float()
+    x = x[torch.isfinite(x) & (x.abs() <= 6)]
+    pad = (-x.numel()) % 31
+    x = torch.cat([x, torch.zeros(pad)]).reshape(-1, 31)
+    x = torch.cat([torch.full((x.shape[0], 1), 6.0), x], dim=1)
+    x = (x * 2.0 ** k).to(dt)
+    q, s = _ops().per_token_group_quant_mxfp4(x.to(dev))
+    rq, rs = O.per_token_group_quant_mxfp4(x)
+    assert torch.equal(s.cpu(), rs)
+    assert torch.equal(q.cpu().view(torch.uint8), rq)
+
+
 @pytest.mark.parametrize("val", [0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
 def test_mxfp4_known_values(dev, val):
     x = torch.zeros(1, 32)

@@ -174,6 +174,30 @@ __device__ __forceinline__ uint32_t fp4_code(float x) {
   return c | (x < 0.f ? 0x8u : 0u);
 }
 
+// fp4_code's rounding from the hardware conversion (round to nearest even),
+// for values that are 16-bit floats (at most 11 significant bits) times a
+// power of two s: the operands are multiplied by sn = s (1 - 2^-12) (exact:
+// 11 + 12 bits), which moves a value that lies on one of fp4_code's
+// midpoints just below it (the tie then rounds down in magnitude, as
+// fp4_code's strict comparisons do) and keeps every other value on its side
+// of every midpoint (its distance to one is more than 2^-11 of itself);
+// adding +0 gives -0 code 0, as in fp4_code, and the clamp to [-6, 6] is
+// fp4_code's.  fp4x4_code16: the codes of x0 .. x3 in bits 0-15, x0 in the
+// low nibble.
+__device__ __forceinline__ float fp4_prescale(float s) { return s * (1.0f - 1.0f / 4096.0f); }
+__device__ __forceinline__ float fp4_pre(float x, float sn) {
+  return fminf(fmaxf(__builtin_fmaf(x, sn, 0.0f), -6.0f), 6.0f);
+}
+template <int BYTE>
+__device__ __forceinline__ uint32_t fp4x2_code16(uint32_t old, float x0, float x1, float sn) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, fp4_pre(x0, sn), fp4_pre(x1, sn), 1.0f,
+                                                  BYTE);
+}
+__device__ __forceinline__ uint32_t fp4x4_code16(float x0, float x1, float x2, float x3,
+                                                 float sn) {
+  return fp4x2_code16<1>(fp4x2_code16<0>(0u, x0, x1, sn), x2, x3, sn) & 0xffffu;
+}
+
 // Maximum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15), in every
 // lane of the row: quad lane swaps (xor 1, xor 2), then the half-row and row
 // mirrors, each pairing a lane with one that holds the other half's

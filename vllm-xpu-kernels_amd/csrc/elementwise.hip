@@ -235,10 +235,18 @@ __global__ __launch_bounds__(256) void group_mxfp4_quant_kernel(
   if (sub == 0) s[g] = ys;
   const float inv = 1.0f / ys;
   uint32_t packed = 0;
+  if constexpr (sizeof(typename E::T) == 2) {  // 16-bit values: hardware conversion
+    const float sn = fp4_prescale(inv);
+    packed = fp4x2_code16<0>(packed, v[0], v[1], sn);
+    packed = fp4x2_code16<1>(packed, v[2], v[3], sn);
+    packed = fp4x2_code16<2>(packed, v[4], v[5], sn);
+    packed = fp4x2_code16<3>(packed, v[6], v[7], sn);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float x = fminf(fmaxf(v[i] * inv, -6.0f), 6.0f);
-    packed |= fp4_code(x) << (4 * i);
+    for (int i = 0; i < 8; ++i) {
+      float x = fminf(fmaxf(v[i] * inv, -6.0f), 6.0f);
+      packed |= fp4_code(x) << (4 * i);
+    }
   }
   store_nt(q + base / 2, packed);
 }

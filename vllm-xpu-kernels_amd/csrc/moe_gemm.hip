@@ -515,8 +515,10 @@ int pick_block_m(int64_t slots, int64_t num_experts) {
 bool wide_ok_for(int recipe, int64_t a_rows, int64_t ldb_rows, int64_t K, bool w_kblock) {
   if (recipe == MI355MOE_RECIPE_BF16) return K % 32 == 0 && wide_offsets_fit(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_FP8BLOCK) return wide8_shape_ok(a_rows, ldb_rows, K);
-  if (recipe == MI355MOE_RECIPE_MXFP8) return w_kblock && wide8_shape_ok(a_rows, ldb_rows, K);
-  if (recipe == RECIPE_MX4A4) return w_kblock && wide8_shape_ok_mx4(a_rows, ldb_rows, K);
+  if (recipe == MI355MOE_RECIPE_MXFP8)
+    return w_kblock && ldb_rows % 4 == 0 && wide8_shape_ok(a_rows, ldb_rows, K);
+  if (recipe == RECIPE_MX4A4)
+    return w_kblock && ldb_rows % 4 == 0 && wide8_shape_ok_mx4(a_rows, ldb_rows, K);
   if (recipe == MI355MOE_RECIPE_MXFP4 || recipe == MI355MOE_RECIPE_INT4 ||
       is_w8a16_recipe(recipe))
     return w_kblock && wide4_shape_ok(a_rows, ldb_rows, ldb_rows, K);

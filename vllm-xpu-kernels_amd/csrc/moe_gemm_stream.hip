@@ -698,10 +698,8 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
       *reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * N +
                                    col0 + 4 * q) = w;
     } else {
-      uint32_t w = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        w |= fp4_code(fminf(fmaxf(ov[0][r] * inv, -6.f), 6.f)) << (4 * r);
+      // (ov holds 16-bit values, inv is a power of two)
+      const uint32_t w = fp4x4_code16(ov[0][0], ov[0][1], ov[0][2], ov[0][3], fp4_prescale(inv));
       *reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(a.D) + static_cast<int64_t>(drow) * (N / 2) +
                                    (col0 + 4 * q) / 2) = static_cast<uint16_t>(w);
     }

@@ -483,10 +483,13 @@ int launch_w8(const GemmArgs& a, int64_t max_blocks, void* qs, hipStream_t st) {
 }  // namespace
 
 bool wide8_supported(int recipe, const GemmArgs& a) {
+  // MX weight codes move 4 tile rows per lane: row counts and the up-row
+  // offset in whole 4-byte words
+  const bool codes4 = a.ldb_rows % 4 == 0 && a.up_off % 4 == 0 && a.N % 4 == 0;
   if (recipe == RECIPE_MX4A4)
-    return a.w_kblock && a.a_mxs_ld % 4 == 0 && a.K % 32 == 0 && a.K > 0;
+    return a.w_kblock && codes4 && a.a_mxs_ld % 4 == 0 && a.K % 32 == 0 && a.K > 0;
   return (recipe == MI355MOE_RECIPE_FP8BLOCK ||
-          (recipe == MI355MOE_RECIPE_MXFP8 && a.w_kblock && a.a_mxs_ld % 4 == 0)) &&
+          (recipe == MI355MOE_RECIPE_MXFP8 && a.w_kblock && codes4 && a.a_mxs_ld % 4 == 0)) &&
          a.K % 128 == 0 && a.K > 0 && a.K / 128 <= MAX_KBLK;
 }
 

@@ -68,9 +68,12 @@ constexpr int DUMMY = 2 * A_SLOT;           // scale DMA target of waves 5-7
 constexpr int W_OFF = DUMMY + 256;          // weight ring: 2 slots x 8 waves x 4 KB
 constexpr int WSLOT = WAVES * 4096;
 constexpr int RING = W_OFF + 2 * WSLOT;
-// mxfp8: e8m0 codes of the weight fragments, 2 slots x 8 waves x 256 bytes
+// MX: e8m0 codes of the tile's weight rows, 2 slots x 8 32-K blocks; block b
+// at byte CPITCH b of a slot (the 16 padding bytes put the four blocks a
+// wave reads at once in different LDS banks)
 constexpr int C_OFF = RING;
-constexpr int CSLOT = WAVES * 256;
+constexpr int CPITCH = 256 + 16;
+constexpr int CSLOT = 8 * CPITCH;
 constexpr int RING_MX = C_OFF + 2 * CSLOT;
 constexpr int MAX_KBLK = 64;                // K <= 8192
 static_assert(RING <= 150 * 1024, "LDS budget");
@@ -264,27 +267,20 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       woff[f][0] = static_cast<uint32_t>(wrow_of(r) * wst.row);
     }
   }
-  // MX weight codes (K-blocked [E, K/32, ldb_rows]), 4 bytes per lane into
-  // LDS byte 4 lane of the wave's code region.  mxfp8: lane c = lane % 32
-  // moves rows 4 (c % 4) .. + 3 of fragment c / 16 for the stage's 32-K block
-  // (c / 4) % 4 (lanes 32-63 repeat lanes 0-31 into the upper half); e2m1:
-  // lane c moves rows 4 (c % 4) .. + 3 of fragment c / 32 for block
-  // 8 kt + (c / 4) % 8.
+  // MX weight codes (K-blocked [E, K/32, ldb_rows]): the workgroup stages the
+  // codes of its 256 tile rows for the stage's 32-K blocks, the code of
+  // (block b, tile row r) at byte CPITCH b + r of the code slot.  Wave w
+  // moves block w, lane l the 4 bytes of tile rows 4 l .. 4 l + 3 (two whole
+  // 128-byte lines per wave); mxfp8 has four blocks per stage, and waves 4-7
+  // repeat wave 0's transfer into the dummy area.
   uint32_t coff = 0;
   const uint8_t* cbase = nullptr;
-  uint32_t ckstep = 0;
   const uint32_t ldb = static_cast<uint32_t>(a.ldb_rows);
-  int cblk = 0;  // e2m1: the lane's block within the stage
+  const bool c_wave = MX4 || wave < 4;
   if constexpr (MX) {
-    const int c = MX4 ? lane : (lane & 31);
-    const int f = MX4 ? c >> 5 : c >> 4, b = MX4 ? (c >> 2) & 7 : (c >> 2) & 3;
-    const int r = kGlu ? (f ? 128 : 0) + 16 * wave : 32 * wave + 16 * f;
-    coff = (MX4 ? 0u : static_cast<uint32_t>(b) * ldb) + static_cast<uint32_t>(wrow_of(r)) +
-           4u * static_cast<uint32_t>(c & 3);
-    cblk = b;
+    coff = static_cast<uint32_t>(wrow_of(4 * lane));
     cbase = uniform_ptr(static_cast<const uint8_t*>(a.b_scale) +
                         static_cast<int64_t>(e) * (K / 32) * a.ldb_rows);
-    ckstep = 4u * ldb;
   }
   const uint32_t wkstep = static_cast<uint32_t>(wst.kblk);
 
@@ -332,14 +328,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         }
         dma16(off, wbase, wring + slot * WSLOT + (2 * f + h) * 1024);
       }
-    if constexpr (MX4) {
-      const int b = 8 * kt + cblk;
-      dma4(coff + static_cast<uint32_t>(b < nblk ? b : nblk - 1) * ldb, cbase,
-           ring0 + C_OFF + slot * CSLOT + wave * 256);
-    } else if constexpr (MX) {
-      dma4(coff + static_cast<uint32_t>(kt) * ckstep, cbase,
-           ring0 + C_OFF + slot * CSLOT + wave * 256);
-    }
+  };
+  // the weight codes of stage kt into code slot `slot` (e2m1: blocks past K
+  // re-read the last block)
+  auto issue_c = [&](int kt, int slot) {
+    const int b = (MX4 ? 8 : 4) * kt + (c_wave ? wave : 0);
+    const int bc = MX4 && b >= nblk ? nblk - 1 : b;
+    dma4(coff + static_cast<uint32_t>(bc) * ldb, cbase,
+         c_wave ? ring0 + C_OFF + slot * CSLOT + CPITCH * wave : ring0 + DUMMY);
   };
   // the wave's weight fragments of ring slot `slot` (o0, o1: the activation
   // fragment offsets of the lane)
@@ -354,21 +350,22 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       for (int f = 0; f < 2; ++f) w[f] = ld32(W + f * 2048, o0, o1);
     }
   };
-  // mxfp8: e8m0 code of the lane's weight row l16 of fragment f for its 32-K
-  // block g of the stage
+  // tile rows of the lane's weight row l16 in fragments 0 and 1
+  const int rf0 = kGlu ? 16 * wave + l16 : 32 * wave + l16;
+  const int rf1 = kGlu ? 128 + 16 * wave + l16 : 32 * wave + 16 + l16;
+  // mxfp8: e8m0 codes of the lane's weight rows for its 32-K block g
   auto read_wc = [&](int slot, uint32_t (&c)[2]) {
-    const uint8_t* C = lds + C_OFF + slot * CSLOT + wave * 256 + 16 * g + l16;
-#pragma unroll
-    for (int f = 0; f < 2; ++f) c[f] = C[64 * f];
+    const uint8_t* C = lds + C_OFF + slot * CSLOT + CPITCH * g;
+    c[0] = C[rf0];
+    c[1] = C[rf1];
   };
-  // e2m1: codes of the lane's row for its blocks g (step 0) and 4 + g (step 1)
+  // e2m1: the same for blocks g (step 0) and 4 + g (step 1)
   auto read_wc4 = [&](int slot, uint32_t (&c)[2][2]) {
-    const uint8_t* C = lds + C_OFF + slot * CSLOT + wave * 256 + 16 * g + l16;
-#pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      c[f][0] = C[128 * f];
-      c[f][1] = C[128 * f + 64];
-    }
+    const uint8_t* C = lds + C_OFF + slot * CSLOT + CPITCH * g;
+    c[0][0] = C[rf0];
+    c[0][1] = C[4 * CPITCH + rf0];
+    c[1][0] = C[rf1];
+    c[1][1] = C[4 * CPITCH + rf1];
   };
 
   // fragment offsets within an activation slot: chunks 2g and 2g + 1 of the
@@ -395,9 +392,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   // Stage kt: the six parts of the activation DMA of stage kt + 1 go out one
   // every second slot tile (a wave that issues them back to back stalls
   // until the DMA path takes them, and computes nothing meanwhile), then the
-  // weight DMA of stage kt + 2.  Transfers complete in issue order, so the
-  // wait at the top of stage kt + 1 for all but the four newest covers the
-  // activations of kt + 1 and the weights of kt + 1 (issued during kt - 1).
+  // weight DMA of stage kt + 2; MX weight codes of stage kt + 1 go out first,
+  // right after the barrier.  Transfers complete in issue order, so the wait
+  // at the top of stage kt + 1 for all but the four newest covers the codes
+  // and activations of kt + 1 and the weights of kt + 1 (issued during kt - 1).
   // Stages past the end move the last stage's (in-bounds, unused) data
   // instead of branching around the transfers.
   auto kloop = [&](auto nj_c) {
@@ -407,19 +405,23 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
     auto part_at = [](int q) { return 2 * q; };
     constexpr int W_AT = 11;   // tile after which the weight DMA of stage kt + 2 goes out
     i32x8_t wc[2];
+    if constexpr (MX) issue_c(0, 0);
 #pragma unroll
     for (int q = 0; q < ACT_PARTS; ++q) issue_act_part(q, 0, 0);
     issue_w(0, 0);
     issue_w(nk > 1 ? 1 : 0, 1);
     for (int kt = 0; kt < nk; ++kt) {
-      // everything but the newest transfers (the weights of stage kt + 2:
-      // four, mxfp8 five with the codes)
-      if constexpr (MX) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      // everything but the newest transfers (the four of the weights of
+      // stage kt + 1, issued during kt - 1)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
       __builtin_amdgcn_s_barrier();   // act(kt) visible; act slot (kt+1)&1 free
       asm volatile("" ::: "memory");  // no LDS read moves above the barrier
       const int kn = kt + 1 < nk ? kt + 1 : kt;
       const int kq = kt + 2 < nk ? kt + 2 : nk - 1;
+      // the codes of stage kt + 1, into the slot every wave finished reading
+      // in stage kt - 1 (all are past the barrier); they land before the
+      // weights issued later in this stage, so the wait above covers them
+      if constexpr (MX) issue_c(kn, (kt + 1) & 1);
       if constexpr (MX4) {
         // last stage of a K % 256 != 0: zero this lane's weight chunks of
         // blocks past K (the DMA re-read the last block there; with a zero
@@ -665,11 +667,10 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         const int row = 16 * j + l16;
         const float inv = MX ? s_sc[4 * row + (wave >> 1)] : 1.0f / s_sc[row];
         if constexpr (MX4) {
-          // e2m1 pairs, the even column in the low nibble
-          uint32_t w = 0;
-  #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            w |= fp4_code(fminf(fmaxf(ov[j][r] * inv, -6.f), 6.f)) << (4 * r);
+          // e2m1 pairs, the even column in the low nibble (ov holds 16-bit
+          // values, inv is a power of two)
+          const uint32_t w =
+              fp4x4_code16(ov[j][0], ov[j][1], ov[j][2], ov[j][3], fp4_prescale(inv));
           *reinterpret_cast<uint16_t*>(lds + row * PITCH + tcol(0, 0) / 2) =
               static_cast<uint16_t>(w);
         } else {
