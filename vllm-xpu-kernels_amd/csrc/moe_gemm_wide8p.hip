@@ -118,6 +118,33 @@ __device__ __forceinline__ float round16(float v) {
   if constexpr (F16) return f16_to_f32(f32_to_f16(v));
   else return bf16_to_f32(f32_to_bf16(v));
 }
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// a and b rounded to the 16-bit type (nearest even, one conversion for
+// both) and packed, a in the low half
+template <bool F16>
+__device__ __forceinline__ uint32_t pack16x2(float a, float b) {
+  if constexpr (F16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+// round16 of v[0..3], two values per conversion
+template <bool F16>
+__device__ __forceinline__ void round16x4(float (&v)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; i += 2) {
+    const uint32_t p = pack16x2<F16>(v[i], v[i + 1]);
+    if constexpr (F16) {
+      v[i] = f16_to_f32(static_cast<uint16_t>(p));
+      v[i + 1] = f16_to_f32(static_cast<uint16_t>(p >> 16));
+    } else {
+      v[i] = __uint_as_float(p << 16);
+      v[i + 1] = __uint_as_float(p & 0xffff0000u);
+    }
+  }
+}
 template <bool F16>
 __device__ __forceinline__ uint32_t to16(float v) {
   if constexpr (F16) return f32_to_f16(v);
@@ -552,11 +579,13 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   }
   static_assert(TJ == 20, "kloop variants cover the even tile counts up to TJ");
 
-  // The epilogue, specialised on the activation and on gemm1_clamp_limit
-  // (uniform per launch), so that no value of the tile branches on them.
-  auto epilogue = [&](auto silu_c, auto clamp_c) {
+  // The epilogue, specialised on the activation, on gemm1_clamp_limit and on
+  // the presence of a bias (uniform per launch), so that no value of the
+  // tile branches on them.
+  auto epilogue = [&](auto silu_c, auto clamp_c, auto bias_c) {
     constexpr bool SILU = decltype(silu_c)::value;
     constexpr bool CLAMP = decltype(clamp_c)::value;
+    constexpr bool HASB = decltype(bias_c)::value;
     // ---- epilogue: lane holds slot 16 j + l16, rows 4 g + r of fragment f
     const int64_t bias_base = static_cast<int64_t>(e) * a.ldb_rows;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -573,30 +602,46 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t n = n0 + tcol(f, r);
-        const bool has = a.bias && n < N;
+        const bool has = HASB && n < N;
         bgs[f][r] = has ? ld16<F16>(a.bias[bias_base + n]) : 0.f;
         if (f == 0) bus[r] = has && kGlu ? ld16<F16>(a.bias[bias_base + a.up_off + n]) : 0.f;
       }
+    // the lane's four outputs of (fragment f, slot tile j) before their final
+    // rounding to the 16-bit type: GLU act(round16(gate), round16(up)),
+    // STORE acc + bias (the accumulators are never -0, so no bias adds 0)
     auto outv = [&](int f, int j, float (&o)[4]) {
+      float gv[4];
   #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float gv = round16<F16>(acc[f][j][r] + bgs[f][r]);
-        if constexpr (kGlu) {
-          float u = round16<F16>(acc[1][j][r] + bus[r]);
-          if constexpr (CLAMP)
+      for (int r = 0; r < 4; ++r) gv[r] = HASB ? acc[f][j][r] + bgs[f][r] : acc[f][j][r];
+      if constexpr (kGlu) {
+        float u[4];
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = HASB ? acc[1][j][r] + bus[r] : acc[1][j][r];
+        round16x4<F16>(gv);
+        round16x4<F16>(u);
+        if constexpr (CLAMP)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r)
             glu_clamp_with(a.clamp_limit, SILU ? MI355MOE_ACT_SILU : MI355MOE_ACT_SWIGLUOAI, N,
-                           n0 + tcol(f, r), gv, u);
-          float y;
-          if constexpr (SILU) {
-            y = round16<F16>(x_sigmoid(gv, 1.f)) * u;
-          } else {
-            gv = gv > a.limit ? a.limit : gv;
-            u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-            y = (u + 1.f) * x_sigmoid(gv, a.alpha);
+                           n0 + tcol(f, r), gv[r], u[r]);
+        if constexpr (SILU) {
+          float sg[4];
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) sg[r] = x_sigmoid(gv[r], 1.f);
+          round16x4<F16>(sg);
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = sg[r] * u[r];
+        } else {
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float gc = gv[r] > a.limit ? a.limit : gv[r];
+            const float uc = u[r] > a.limit ? a.limit : (u[r] < -a.limit ? -a.limit : u[r]);
+            o[r] = (uc + 1.f) * x_sigmoid(gc, a.alpha);
           }
-          gv = round16<F16>(y);
         }
-        o[r] = gv;
+      } else {
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = gv[r];
       }
     };
 
@@ -611,6 +656,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   #pragma unroll
       for (int j = 0; j < TJ; ++j) {
         outv(0, j, ov[j]);
+        round16x4<F16>(ov[j]);
         float m = 1e-10f;
   #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[j][r]));
@@ -653,7 +699,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   #pragma unroll
           for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
           const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
-          s_sc[tid] = sc;
+          s_sc[tid] = 1.0f / sc;  // the multiplier of the quantisation
           const int drow = s_drow[tid];
           if (drow >= 0) {
             if (a.q_scale_tld) ds[static_cast<int64_t>(ntile) * a.q_scale_tld + drow] = sc;
@@ -665,7 +711,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   #pragma unroll
       for (int j = 0; j < TJ; ++j) {
         const int row = 16 * j + l16;
-        const float inv = MX ? s_sc[4 * row + (wave >> 1)] : 1.0f / s_sc[row];
+        const float inv = MX ? s_sc[4 * row + (wave >> 1)] : s_sc[row];
         if constexpr (MX4) {
           // e2m1 pairs, the even column in the low nibble (ov holds 16-bit
           // values, inv is a power of two)
@@ -716,8 +762,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
             float o[4];
             outv(f, j, o);
             const int srow = 16 * jj + l16;
-            const uint32_t lo = to16<F16>(o[0]) | (to16<F16>(o[1]) << 16);
-            const uint32_t hi = to16<F16>(o[2]) | (to16<F16>(o[3]) << 16);
+            const uint32_t lo = pack16x2<F16>(o[0], o[1]);
+            const uint32_t hi = pack16x2<F16>(o[2], o[3]);
             *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(f, 0)) = make_uint2(lo, hi);
           }
         __syncthreads();
@@ -743,13 +789,22 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
-  const bool clamp = kGlu && a.clamp_limit > 0.f;
-  if (!kGlu || a.act == MI355MOE_ACT_SILU) {
-    if (clamp) epilogue(T_{}, T_{});
-    else epilogue(T_{}, F_{});
+  const bool hasb = a.bias != nullptr;
+  auto run = [&](auto silu_c, auto clamp_c) {
+    if (hasb) epilogue(silu_c, clamp_c, T_{});
+    else epilogue(silu_c, clamp_c, F_{});
+  };
+  if constexpr (!kGlu) {
+    run(T_{}, F_{});
   } else {
-    if (clamp) epilogue(F_{}, T_{});
-    else epilogue(F_{}, F_{});
+    const bool clamp = a.clamp_limit > 0.f;
+    if (a.act == MI355MOE_ACT_SILU) {
+      if (clamp) run(T_{}, T_{});
+      else run(T_{}, F_{});
+    } else {
+      if (clamp) run(F_{}, T_{});
+      else run(F_{}, F_{});
+    }
   }
 }
 
