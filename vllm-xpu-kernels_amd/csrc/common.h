@@ -198,6 +198,18 @@ __device__ __forceinline__ uint32_t fp4x4_code16(float x0, float x1, float x2, f
   return fp4x2_code16<1>(fp4x2_code16<0>(0u, x0, x1, sn), x2, x3, sn) & 0xffffu;
 }
 
+// Maximum of a non-negative float over lanes l, l ^ 16, l ^ 32, l ^ 48, in every
+// one of them: the row-pair and half-wave swaps of gfx950 (VALU, no LDS
+// round trip), each called with both operands the same register so either
+// result holds the partner rows; non-negative floats order as their bits.
+__device__ __forceinline__ float max_over_rows(float m) {
+  uint32_t u = __float_as_uint(m);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  u = r16[0] > r16[1] ? r16[0] : r16[1];
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  u = r32[0] > r32[1] ? r32[0] : r32[1];
+  return __uint_as_float(u);
+}
 // Maximum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15), in every
 // lane of the row: quad lane swaps (xor 1, xor 2), then the half-row and row
 // mirrors, each pairing a lane with one that holds the other half's

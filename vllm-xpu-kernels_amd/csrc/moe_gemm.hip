@@ -413,8 +413,7 @@ __global__ __launch_bounds__(256, (small_min_waves<RECIPE, BM>())) void moe_gemm
       for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(outv[mt][j][r]));
-      m = fmaxf(m, __shfl_xor(m, 16, 64));
-      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      m = max_over_rows(m);
       if (q == 0) s_amax[wave][mt * 16 + l16] = m;
     }
     __syncthreads();

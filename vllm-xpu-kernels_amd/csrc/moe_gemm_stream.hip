@@ -676,8 +676,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     float m = 1e-10f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[0][r]));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = max_over_rows(m);
     if (q == 0) s_amax[wave][l16] = m;
     __syncthreads();
     if (drow < 0) return;
@@ -707,8 +706,7 @@ __global__ __launch_bounds__(512) void moe_gemm_stream_kernel(const GemmArgs a,
     float m = 1e-10f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[0][r]));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = max_over_rows(m);
     if (q == 0) s_amax[wave][l16] = m;
     __syncthreads();
     if (drow < 0) return;

@@ -391,8 +391,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8_kernel(const GemmArgs a, v
 #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[i][j][r]));
       }
-      m = fmaxf(m, __shfl_xor(m, 16, 64));
-      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      m = max_over_rows(m);
       if (g == 0) s_amax[wn][(BM / 2) * wm + 16 * j + l16] = m;
     }
     __syncthreads();

@@ -145,18 +145,6 @@ __device__ __forceinline__ void round16x4(float (&v)[4]) {
     }
   }
 }
-// Maximum of a positive float over lanes l, l ^ 16, l ^ 32, l ^ 48, in every
-// one of them: the row-pair and half-wave swaps of gfx950 (VALU, no LDS
-// round trip), each called with both operands the same register so either
-// result holds the partner rows; positive floats order as their bits.
-__device__ __forceinline__ float max_over_rows(float m) {
-  uint32_t u = __float_as_uint(m);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  u = r16[0] > r16[1] ? r16[0] : r16[1];
-  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  u = r32[0] > r32[1] ? r32[0] : r32[1];
-  return __uint_as_float(u);
-}
 template <bool F16>
 __device__ __forceinline__ uint32_t to16(float v) {
   if constexpr (F16) return f32_to_f16(v);
