@@ -174,6 +174,18 @@ __device__ __forceinline__ uint32_t fp4_code(float x) {
   return c | (x < 0.f ? 0x8u : 0u);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// a and b rounded to the 16-bit type (nearest even, one conversion for
+// both) and packed, a in the low half
+template <bool F16>
+__device__ __forceinline__ uint32_t pack16x2(float a, float b) {
+  if constexpr (F16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 // fp4_code's rounding from the hardware conversion (round to nearest even),
 // for values that are 16-bit floats (at most 11 significant bits) times a
 // power of two s: the operands are multiplied by sn = s (1 - 2^-12) (exact:

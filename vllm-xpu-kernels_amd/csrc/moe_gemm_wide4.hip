@@ -431,8 +431,9 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
           float ov[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            float g = round16<F16>((W8 ? acc[i][j][r] * es : acc[i][j][r]) + bg[r]);
+            float g = (W8 ? acc[i][j][r] * es : acc[i][j][r]) + bg[r];  // rounded below
             if constexpr (kGlu) {
+              g = round16<F16>(g);
               float u = round16<F16>((W8 ? acc[1][j][r] * es : acc[1][j][r]) + bu[r]);
               glu_clamp(a, n0 + tcol(i, r), g, u);
               float y;
@@ -443,14 +444,14 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
                 u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
                 y = (u + 1.f) * x_sigmoid(g, a.alpha);
               }
-              g = round16<F16>(y);
+              g = y;
             }
-            ov[r] = g;
+            ov[r] = g;  // one rounding to the 16-bit type, in the packing below
           }
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
-            const uint32_t lo = to16<F16>(ov[4 * g4]) | (to16<F16>(ov[4 * g4 + 1]) << 16);
-            const uint32_t hi = to16<F16>(ov[4 * g4 + 2]) | (to16<F16>(ov[4 * g4 + 3]) << 16);
+            const uint32_t lo = pack16x2<F16>(ov[4 * g4], ov[4 * g4 + 1]);
+            const uint32_t hi = pack16x2<F16>(ov[4 * g4 + 2], ov[4 * g4 + 3]);
             *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(i, 4 * g4)) = make_uint2(lo, hi);
           }
         }

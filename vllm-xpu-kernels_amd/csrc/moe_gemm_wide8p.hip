@@ -118,18 +118,6 @@ __device__ __forceinline__ float round16(float v) {
   if constexpr (F16) return f16_to_f32(f32_to_f16(v));
   else return bf16_to_f32(f32_to_bf16(v));
 }
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-// a and b rounded to the 16-bit type (nearest even, one conversion for
-// both) and packed, a in the low half
-template <bool F16>
-__device__ __forceinline__ uint32_t pack16x2(float a, float b) {
-  if constexpr (F16)
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
-  else
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
-}
 // round16 of v[0..3], two values per conversion
 template <bool F16>
 __device__ __forceinline__ void round16x4(float (&v)[4]) {
