@@ -186,6 +186,17 @@ __device__ __forceinline__ uint32_t pack16x2(float a, float b) {
   else
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
+// the two 16-bit values of a packed pair as floats (a the low half)
+template <bool F16>
+__device__ __forceinline__ void unpack16x2(uint32_t p, float& a, float& b) {
+  if constexpr (F16) {
+    a = f16_to_f32(static_cast<uint16_t>(p));
+    b = f16_to_f32(static_cast<uint16_t>(p >> 16));
+  } else {
+    a = __uint_as_float(p << 16);
+    b = __uint_as_float(p & 0xffff0000u);
+  }
+}
 // fp4_code's rounding from the hardware conversion (round to nearest even),
 // for values that are 16-bit floats (at most 11 significant bits) times a
 // power of two s: the operands are multiplied by sn = s (1 - 2^-12) (exact:

@@ -633,10 +633,57 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
       }
     };
 
-    if constexpr (QOUT) {
-      // e4m3 activation with one fp32 scale per (slot, 128 columns): the 8
-      // waves cover the tile's 128 columns (N % 128 == 0); lanes l, l+16, l+32,
-      // l+48 hold the same slot
+    if constexpr (QOUT && !MX) {
+      // e4m3 activation with one fp32 scale per (slot, 128 columns), the
+      // tile's 128 columns (N % 128 == 0): the GLU outputs staged in LDS as
+      // 16-bit values (their rounding), one barrier, then 16 lanes per slot
+      // row take its amax (one DPP reduction), quantise its 8-column chunks
+      // and store the row's 128 bytes
+      constexpr int P16 = 2 * NOUT + 16;  // staging row pitch (bytes)
+  #pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        float o[4];
+        outv(0, j, o);
+        *reinterpret_cast<uint2*>(lds + (16 * j + l16) * P16 + 2 * tcol(0, 0)) =
+            make_uint2(pack16x2<F16>(o[0], o[1]), pack16x2<F16>(o[2], o[3]));
+      }
+      __syncthreads();
+      float* ds = static_cast<float*>(qs);
+      uint8_t* dq = static_cast<uint8_t*>(a.D);
+      const int64_t ngroups = N / 128;
+      const int c = tid & 15;  // the lane's 8-column chunk of the row
+      for (int row = tid >> 4; row < BM; row += 512 / 16) {  // every lane, every pass
+        const uint4 u = *reinterpret_cast<const uint4*>(lds + row * P16 + 16 * c);
+        float x[8];
+        unpack16x2<F16>(u.x, x[0], x[1]);
+        unpack16x2<F16>(u.y, x[2], x[3]);
+        unpack16x2<F16>(u.z, x[4], x[5]);
+        unpack16x2<F16>(u.w, x[6], x[7]);
+        float m = 1e-10f;
+  #pragma unroll
+        for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(x[k]));
+        m = row16_max(m);
+        const float sc = fmaxf(m / 448.f, 1.0f / (448.f * 512.f));
+        const float inv = 1.0f / sc;
+        const int drow = s_drow[row];
+        if (drow >= 0) {
+          const uint32_t lo = e4m3x4_sat(x[0] * inv, x[1] * inv, x[2] * inv, x[3] * inv);
+          const uint32_t hi = e4m3x4_sat(x[4] * inv, x[5] * inv, x[6] * inv, x[7] * inv);
+          *reinterpret_cast<uint2*>(dq + static_cast<int64_t>(drow) * N + n0 + 8 * c) =
+              make_uint2(lo, hi);
+          if (c == 0) {
+            if (a.q_scale_tld) ds[static_cast<int64_t>(ntile) * a.q_scale_tld + drow] = sc;
+            else ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
+          }
+        }
+      }
+    } else if constexpr (QOUT) {
+      // MX activation for the w2 GEMM: one e8m0 code per 32 columns (the 16
+      // columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
+      // with ue8m0 scales, e2m1 as per_token_group_quant_mxfp4 (eps 1e-10);
+      // s_sc[slot][p] holds 1 / 2^code.  N % 32 == 0: groups past N (the
+      // last tile of an N % 128 != 0) are not written.  The 8 waves cover
+      // the tile's 128 columns; lanes l, l+16, l+32, l+48 hold the same slot.
       constexpr int PITCH = NOUT + 16;
       float (*s_amax)[BM] = reinterpret_cast<float (*)[BM]>(lds + BM * PITCH);
       float* s_sc = reinterpret_cast<float*>(lds + BM * PITCH + WAVES * BM * 4);
@@ -652,12 +699,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         if (g == 0) s_amax[wave][16 * j + l16] = m;
       }
       __syncthreads();
-      if constexpr (MX) {
-        // MX activation for the w2 GEMM: one e8m0 code per 32 columns (the 16
-        // columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
-        // with ue8m0 scales, e2m1 as per_token_group_quant_mxfp4 (eps 1e-10);
-        // s_sc[slot][p] holds 1 / 2^code.  N % 32 == 0: groups past N (the
-        // last tile of an N % 128 != 0) are not written.
+      {
         float (*s_inv)[4] = reinterpret_cast<float (*)[4]>(s_sc);
         for (int i = tid; i < 4 * BM; i += 512) {
           const int row = i >> 2, p = i & 3;
@@ -678,27 +720,12 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
               static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] = code;
           }
         }
-      } else {
-        float* ds = static_cast<float*>(qs);
-        const int64_t ngroups = N / 128;
-        if (tid < BM) {
-          float am = s_amax[0][tid];
-  #pragma unroll
-          for (int w = 1; w < WAVES; ++w) am = fmaxf(am, s_amax[w][tid]);
-          const float sc = fmaxf(am / 448.f, 1.0f / (448.f * 512.f));
-          s_sc[tid] = 1.0f / sc;  // the multiplier of the quantisation
-          const int drow = s_drow[tid];
-          if (drow >= 0) {
-            if (a.q_scale_tld) ds[static_cast<int64_t>(ntile) * a.q_scale_tld + drow] = sc;
-            else ds[static_cast<int64_t>(drow) * ngroups + ntile] = sc;
-          }
-        }
       }
       __syncthreads();
   #pragma unroll
       for (int j = 0; j < TJ; ++j) {
         const int row = 16 * j + l16;
-        const float inv = MX ? s_sc[4 * row + (wave >> 1)] : s_sc[row];
+        const float inv = s_sc[4 * row + (wave >> 1)];
         if constexpr (MX4) {
           // e2m1 pairs, the even column in the low nibble (ov holds 16-bit
           // values, inv is a power of two)
