@@ -678,80 +678,66 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         }
       }
     } else if constexpr (QOUT) {
-      // MX activation for the w2 GEMM: one e8m0 code per 32 columns (the 16
-      // columns of waves 2p and 2p + 1): mxfp8 as per_token_group_fp8_quant
-      // with ue8m0 scales, e2m1 as per_token_group_quant_mxfp4 (eps 1e-10);
-      // s_sc[slot][p] holds 1 / 2^code.  N % 32 == 0: groups past N (the
-      // last tile of an N % 128 != 0) are not written.  The 8 waves cover
-      // the tile's 128 columns; lanes l, l+16, l+32, l+48 hold the same slot.
-      constexpr int PITCH = NOUT + 16;
-      float (*s_amax)[BM] = reinterpret_cast<float (*)[BM]>(lds + BM * PITCH);
-      float* s_sc = reinterpret_cast<float*>(lds + BM * PITCH + WAVES * BM * 4);
-      float ov[TJ][4];
+      // MX activation for the w2 GEMM, one e8m0 code per 32 columns: mxfp8 as
+      // per_token_group_fp8_quant with ue8m0 scales, e2m1 as
+      // per_token_group_quant_mxfp4 (eps 1e-10).  Staged like the e4m3 path;
+      // 16 lanes per slot row, so a 32-column group is a DPP quad.  N % 32 ==
+      // 0: groups past N (the last tile of an N % 128 != 0) get code 127
+      // (scale 1.0) where the padded code row holds them -- the w2 GEMM reads
+      // them, four codes at a time, against zero data -- and no data.
+      constexpr int P16 = 2 * NOUT + 16;  // staging row pitch (bytes)
   #pragma unroll
       for (int j = 0; j < TJ; ++j) {
-        outv(0, j, ov[j]);
-        round16x4<F16>(ov[j]);
-        float m = 1e-10f;
-  #pragma unroll
-        for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(ov[j][r]));
-        m = max_over_rows(m);
-        if (g == 0) s_amax[wave][16 * j + l16] = m;
-      }
-      __syncthreads();
-      {
-        float (*s_inv)[4] = reinterpret_cast<float (*)[4]>(s_sc);
-        for (int i = tid; i < 4 * BM; i += 512) {
-          const int row = i >> 2, p = i & 3;
-          const float am = fmaxf(s_amax[2 * p][row], s_amax[2 * p + 1][row]);
-          int ex;
-          if constexpr (MX4) ex = ceil_log2(fmaxf(fabsf(am / 6.0f), 1e-10f));
-          else ex = ceil_log2(fmaxf(fabsf(fmaxf(am / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
-          s_inv[row][p] = 1.0f / pow2i(ex);
-          // groups past N inside the padded code row get 127 (scale 1.0): the
-          // w2 GEMM reads them, four codes at a time, against zero data
-          const int drow = s_drow[row];
-          if (drow >= 0 && n0 / 32 + p < a.q_mxs_ld) {
-            const uint8_t code = static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
-            // by position: the tile's four codes are byte p of word n0 / 128
-            if (a.q_scale_tld)
-              static_cast<uint8_t*>(qs)[((n0 >> 7) * a.q_scale_tld + drow) * 4 + p] = code;
-            else
-              static_cast<uint8_t*>(qs)[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] = code;
-          }
-        }
-      }
-      __syncthreads();
-  #pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int row = 16 * j + l16;
-        const float inv = s_sc[4 * row + (wave >> 1)];
-        if constexpr (MX4) {
-          // e2m1 pairs, the even column in the low nibble (ov holds 16-bit
-          // values, inv is a power of two)
-          const uint32_t w =
-              fp4x4_code16(ov[j][0], ov[j][1], ov[j][2], ov[j][3], fp4_prescale(inv));
-          *reinterpret_cast<uint16_t*>(lds + row * PITCH + tcol(0, 0) / 2) =
-              static_cast<uint16_t>(w);
-        } else {
-          const uint32_t w =
-              e4m3x4_sat(ov[j][0] * inv, ov[j][1] * inv, ov[j][2] * inv, ov[j][3] * inv);
-          *reinterpret_cast<uint32_t*>(lds + row * PITCH + tcol(0, 0)) = w;
-        }
+        float o[4];
+        outv(0, j, o);
+        *reinterpret_cast<uint2*>(lds + (16 * j + l16) * P16 + 2 * tcol(0, 0)) =
+            make_uint2(pack16x2<F16>(o[0], o[1]), pack16x2<F16>(o[2], o[3]));
       }
       __syncthreads();
       uint8_t* dq = static_cast<uint8_t*>(a.D);
-      // 16-byte chunks of an output row: 16 e4m3 or 32 e2m1 columns; N % 32 ==
-      // 0, so an e2m1 chunk lies wholly inside or wholly past N
-      constexpr int CPR = MX4 ? NOUT / 32 : NOUT / 16;
+      uint8_t* qc = static_cast<uint8_t*>(qs);
       const int64_t orow = MX4 ? (a.ldd ? a.ldd : N / 2) : N;  // output row pitch (bytes)
-      for (int idx = tid; idx < BM * CPR; idx += 512) {
-        const int row = idx / CPR, ch = idx % CPR;
+      const int c = tid & 15;  // the lane's 8-column chunk of the row
+      const int p = c >> 2;    // its 32-column group
+      for (int row = tid >> 4; row < BM; row += 512 / 16) {  // every lane, every pass
+        const uint4 u = *reinterpret_cast<const uint4*>(lds + row * P16 + 16 * c);
+        float x[8];
+        unpack16x2<F16>(u.x, x[0], x[1]);
+        unpack16x2<F16>(u.y, x[2], x[3]);
+        unpack16x2<F16>(u.z, x[4], x[5]);
+        unpack16x2<F16>(u.w, x[6], x[7]);
+        float m = 1e-10f;
+  #pragma unroll
+        for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(x[k]));
+        m = fmaxf(m, dpp_f32<0xB1>(m));  // quad_perm [1,0,3,2]
+        m = fmaxf(m, dpp_f32<0x4E>(m));  // quad_perm [2,3,0,1]
+        int ex;
+        if constexpr (MX4) ex = ceil_log2(fmaxf(fabsf(m / 6.0f), 1e-10f));
+        else ex = ceil_log2(fmaxf(fabsf(fmaxf(m / 448.f, 1.0f / (448.f * 512.f))), 1e-10f));
+        const float inv = 1.0f / pow2i(ex);
         const int drow = s_drow[row];
-        if (drow < 0 || n0 + ch * (MX4 ? 32 : 16) >= N) continue;
-        *reinterpret_cast<uint4*>(dq + static_cast<int64_t>(drow) * orow + (MX4 ? n0 / 2 : n0) +
-                                  ch * 16) =
-            *reinterpret_cast<const uint4*>(lds + row * PITCH + ch * 16);
+        if (drow < 0) continue;
+        if ((c & 3) == 0 && n0 / 32 + p < a.q_mxs_ld) {
+          const uint8_t code = static_cast<uint8_t>(n0 + 32 * p < N ? ex + 127 : 127);
+          // by position: the tile's four codes are byte p of word n0 / 128
+          if (a.q_scale_tld) qc[((n0 >> 7) * a.q_scale_tld + drow) * 4 + p] = code;
+          else qc[static_cast<int64_t>(drow) * a.q_mxs_ld + n0 / 32 + p] = code;
+        }
+        if (n0 + 8 * c >= N) continue;
+        if constexpr (MX4) {
+          // e2m1 pairs, the even column in the low nibble (x holds 16-bit
+          // values, inv is a power of two)
+          const float sn = fp4_prescale(inv);
+          const uint32_t w = fp4x4_code16(x[0], x[1], x[2], x[3], sn) |
+                             (fp4x4_code16(x[4], x[5], x[6], x[7], sn) << 16);
+          *reinterpret_cast<uint32_t*>(dq + static_cast<int64_t>(drow) * orow + (n0 + 8 * c) / 2) =
+              w;
+        } else {
+          const uint32_t lo = e4m3x4_sat(x[0] * inv, x[1] * inv, x[2] * inv, x[3] * inv);
+          const uint32_t hi = e4m3x4_sat(x[4] * inv, x[5] * inv, x[6] * inv, x[7] * inv);
+          *reinterpret_cast<uint2*>(dq + static_cast<int64_t>(drow) * orow + n0 + 8 * c) =
+              make_uint2(lo, hi);
+        }
       }
     } else {
       // 16-bit output staged in LDS (STORE tiles in two passes of 160 slots)
