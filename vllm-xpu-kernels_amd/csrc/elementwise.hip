@@ -196,18 +196,27 @@ __global__ __launch_bounds__(256) void group_fp8_quant_kernel(
   float amax = eps;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  for (int o = lpg >> 1; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if (lpg == 16) {  // a group of 128 is one DPP row of 16 lanes
+    amax = row16_max(amax);
+  } else {
+    for (int o = lpg >> 1; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  }
   float ys = fmaxf(amax / fp8_max, 1.0f / (fp8_max * 512.0f));
   if (ue8m0) ys = pow2i(ceil_log2(fmaxf(fabsf(ys), 1e-10f)));
   if (!active) return;
   if (sub == 0) s[g] = ys;
   const float inv = 1.0f / ys;
   uint32_t lo = 0, hi = 0;
+  if (fp8_max == 448.0f) {  // the e4m3 range: two values per hardware convert
+    lo = e4m3x4_sat(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    hi = e4m3x4_sat(v[4] * inv, v[5] * inv, v[6] * inv, v[7] * inv);
+  } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float x = fminf(fmaxf(v[i] * inv, -fp8_max), fp8_max);
-    uint32_t b = f32_to_e4m3(x);
-    if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+    for (int i = 0; i < 8; ++i) {
+      float x = fminf(fmaxf(v[i] * inv, -fp8_max), fp8_max);
+      uint32_t b = f32_to_e4m3(x);
+      if (i < 4) lo |= b << (8 * i); else hi |= b << (8 * (i - 4));
+    }
   }
   store_nt(q + base, lo, hi);
 }

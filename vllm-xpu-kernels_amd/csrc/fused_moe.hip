@@ -207,21 +207,24 @@ __global__ __launch_bounds__(256) void repack_codes_kernel(const uint8_t* __rest
 
 // Activation scales by sorted position: st[g * ldp + p] = the scale of
 // group g of the row that position p holds (its token for w13), 0 for
-// padding positions.  One thread per position walks the row's groups (16-byte
-// loads of one row, stores coalesced across the wave's positions).
-// Positions past max_padded up to ldp are not written (no GEMM tile reads
-// them).
+// padding positions.  Grid (positions / 256, groups / 8): a thread moves
+// eight groups of one position (16-byte loads of one row, stores coalesced
+// across the wave's positions).  Positions past the padded slot count
+// (*ntp, from the sort) are not written: no GEMM tile reads them.
 __global__ __launch_bounds__(256) void scales_by_position_kernel(
-    const int32_t* __restrict__ sorted, const float* __restrict__ s, float* __restrict__ st,
-    int64_t groups, int64_t ldp, int64_t max_padded, int32_t num_valid, int32_t a_div) {
+    const int32_t* __restrict__ sorted, const int32_t* __restrict__ ntp,
+    const float* __restrict__ s, float* __restrict__ st, int64_t groups, int64_t ldp,
+    int64_t max_padded, int32_t num_valid, int32_t a_div) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (p >= max_padded) return;
+  if (p >= max_padded || p >= *ntp) return;
+  const int64_t g0 = static_cast<int64_t>(blockIdx.y) * 8;
+  const int64_t ge = groups < g0 + 8 ? groups : g0 + 8;
   const int32_t rid = sorted[p];
   const bool ok = rid >= 0 && rid < num_valid;
   const float* row = s + static_cast<int64_t>(ok ? rid / a_div : 0) * groups;
-  int64_t g = 0;
+  int64_t g = g0;
   if ((groups & 3) == 0 && (reinterpret_cast<uintptr_t>(s) & 15) == 0) {
-    for (; g < groups; g += 4) {
+    for (; g < ge; g += 4) {
       const float4 v = ok ? *reinterpret_cast<const float4*>(row + g) : make_float4(0.f, 0.f, 0.f, 0.f);
       st[g * ldp + p] = v.x;
       st[(g + 1) * ldp + p] = v.y;
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(256) void scales_by_position_kernel(
       st[(g + 3) * ldp + p] = v.w;
     }
   }
-  for (; g < groups; ++g) st[g * ldp + p] = ok ? row[g] : 0.f;
+  for (; g < ge; ++g) st[g * ldp + p] = ok ? row[g] : 0.f;
 }
 
 // e8m0 code words by sorted position: st[w * ldp + p] = codes 4w .. 4w + 3
@@ -872,8 +875,10 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
     MI_LAUNCH_CHECK();
   }
   if (L.xst) {  // the hidden states' scales by sorted position
-    scales_by_position_kernel<<<static_cast<unsigned>(cdiv(L.max_padded, 256)), dim3(256), 0, st>>>(
-        L.sorted, preq ? static_cast<const float*>(a->hidden_scale) : L.xs, L.xst, H / 128,
+    const dim3 grid(static_cast<unsigned>(cdiv(L.max_padded, 256)),
+                    static_cast<unsigned>(cdiv(H / 128, 8)));
+    scales_by_position_kernel<<<grid, dim3(256), 0, st>>>(
+        L.sorted, L.ntp, preq ? static_cast<const float*>(a->hidden_scale) : L.xs, L.xst, H / 128,
         L.ldp, L.max_padded, static_cast<int32_t>(L.slots), static_cast<int32_t>(k));
     MI_LAUNCH_CHECK();
   }
