@@ -235,27 +235,44 @@ __global__ __launch_bounds__(256) void scales_by_position_kernel(
   for (; g < ge; ++g) st[g * ldp + p] = ok ? row[g] : 0.f;
 }
 
-// e8m0 code words by sorted position: st[w * ldp + p] = codes 4w .. 4w + 3
-// of the row that position p holds (its token for w13; codes past the
+// e8m0 code words by sorted position: st[wd * ldp + p] = codes 4 wd .. 4 wd
+// + 3 of the row that position p holds (its token for w13; codes past the
 // row's w codes read 127, scale 1.0), 0x7f7f7f7f for padding positions.
+// Grid (positions / 256, words / 4): a thread moves four words of one
+// position (one 16-byte load where the row allows it).  Positions past the
+// padded slot count (*ntp) are not written: no GEMM tile reads them.
 __global__ __launch_bounds__(256) void codes_by_position_kernel(
-    const int32_t* __restrict__ sorted, const uint8_t* __restrict__ c, uint32_t* __restrict__ st,
-    int64_t w, int64_t ld, int64_t ldp, int64_t max_padded, int32_t num_valid, int32_t a_div) {
+    const int32_t* __restrict__ sorted, const int32_t* __restrict__ ntp,
+    const uint8_t* __restrict__ c, uint32_t* __restrict__ st, int64_t w, int64_t ld,
+    int64_t nwords, int64_t ldp, int64_t max_padded, int32_t num_valid, int32_t a_div) {
   const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t wd = blockIdx.y;
-  if (p >= max_padded) return;
+  if (p >= max_padded || p >= *ntp) return;
+  const int64_t w0 = static_cast<int64_t>(blockIdx.y) * 4;
   const int32_t rid = sorted[p];
-  uint32_t v = 0x7f7f7f7fu;
+  uint32_t v[4] = {0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
   if (rid >= 0 && rid < num_valid) {
     const uint8_t* row = c + static_cast<int64_t>(rid / a_div) * ld;
-    v = 0;
+    if (4 * (w0 + 4) <= w && (reinterpret_cast<uintptr_t>(row + 4 * w0) & 15) == 0) {
+      const uint4 u = *reinterpret_cast<const uint4*>(row + 4 * w0);
+      v[0] = u.x;
+      v[1] = u.y;
+      v[2] = u.z;
+      v[3] = u.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t j = 4 * wd + i;
-      v |= static_cast<uint32_t>(j < w ? row[j] : 127u) << (8 * i);
+      for (int i = 0; i < 4; ++i) {
+        v[i] = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int64_t j = 4 * (w0 + i) + b;
+          v[i] |= static_cast<uint32_t>(j < w ? row[j] : 127u) << (8 * b);
+        }
+      }
     }
   }
-  st[wd * ldp + p] = v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (w0 + i < nwords) st[(w0 + i) * ldp + p] = v[i];
 }
 
 // Rows of w units [rows, w] -> [rows, ld] (ld > w), the padding zeroed: the
@@ -867,10 +884,12 @@ int fused_moe_impl(const mi355moe_fused_moe_args* a, void* ws, size_t ws_bytes,
   }
   if (L.xs8t) {  // the hidden states' e8m0 codes by sorted position
     const bool own = !a->hidden_scale;  // the layer's own codes, L.xs8: [T, ld1]
-    const dim3 sg(static_cast<unsigned>(cdiv(L.max_padded, 256)), static_cast<unsigned>(L.ld1 / 4));
+    const int64_t nwords = L.ld1 / 4;
+    const dim3 sg(static_cast<unsigned>(cdiv(L.max_padded, 256)),
+                  static_cast<unsigned>(cdiv(nwords, 4)));
     codes_by_position_kernel<<<sg, dim3(256), 0, st>>>(
-        L.sorted, own ? L.xs8 : static_cast<const uint8_t*>(a->hidden_scale), L.xs8t,
-        own ? L.ld1 : H / 32, own ? L.ld1 : H / 32, L.ldp, L.max_padded,
+        L.sorted, L.ntp, own ? L.xs8 : static_cast<const uint8_t*>(a->hidden_scale), L.xs8t,
+        own ? L.ld1 : H / 32, own ? L.ld1 : H / 32, nwords, L.ldp, L.max_padded,
         static_cast<int32_t>(L.slots), static_cast<int32_t>(k));
     MI_LAUNCH_CHECK();
   }
