@@ -459,30 +459,40 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         const uint8_t* S = lds + (kt & 1) * A_SLOT;
         const uint32_t* xsp = reinterpret_cast<const uint32_t*>(S + A_BYTES) + l16;
         i32x8_t x = ld32(S, xo0, xo1);
+        // an e2m1 operand is four VGPRs: the low half of a fragment feeds
+        // K-step 0, the high half K-step 1.  Step 1 of tile j - 1 goes out
+        // with step 0 of tile j, so the two MFMAs into one accumulator are
+        // four apart, not two.
+        i32x8_t xp = x;
+        uint32_t xc1p = 0;
+        auto step1 = [&](int jj, const i32x8_t& xv, uint32_t xc) {
+#pragma unroll
+          for (int f = 0; f < 2; ++f)
+            acc[f][jj] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                __builtin_shufflevector(wc[f], wc[f], 4, 5, 6, 7, 0, 1, 2, 3),
+                __builtin_shufflevector(xv, xv, 4, 5, 6, 7, 0, 1, 2, 3), acc[f][jj], 4, 4, 0,
+                wcode[f][1], 0, xc);
+        };
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           i32x8_t xn = x;
           if (j + 1 < NJ) xn = ld32(S + (j + 1) * 16 * KE, xo0, xo1);
           const uint32_t xc0 = (xsp[16 * j] >> (8 * g)) & 0xffu;       // block g
           const uint32_t xc1 = (xsp[BM + 16 * j] >> (8 * g)) & 0xffu;  // block 4 + g
-          // an e2m1 operand is four VGPRs: the low half of a fragment feeds
-          // K-step 0, the high half K-step 1
+          if (j > 0) step1(j - 1, xp, xc1p);
 #pragma unroll
           for (int f = 0; f < 2; ++f)
             acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                 wc[f], x, acc[f][j], 4, 4, 0, wcode[f][0], 0, xc0);
 #pragma unroll
-          for (int f = 0; f < 2; ++f)
-            acc[f][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                __builtin_shufflevector(wc[f], wc[f], 4, 5, 6, 7, 0, 1, 2, 3),
-                __builtin_shufflevector(x, x, 4, 5, 6, 7, 0, 1, 2, 3), acc[f][j], 4, 4, 0,
-                wcode[f][1], 0, xc1);
-#pragma unroll
           for (int q = 0; q < ACT_PARTS; ++q)
             if (part_at(q) == j) issue_act_part(q, kn, kt + 1);
           if (j == W_AT) issue_w(kq, kt & 1);
+          xp = x;
+          xc1p = xc1;
           x = xn;
         }
+        step1(NJ - 1, xp, xc1p);
       } else if constexpr (MX && NJ > 0) {
         uint32_t wcode[2];
         read_wc(kt & 1, wcode);
