@@ -105,11 +105,6 @@ __device__ __forceinline__ float round16(float v) {
   if constexpr (F16) return f16_to_f32(f32_to_f16(v));
   else return bf16_to_f32(f32_to_bf16(v));
 }
-template <bool F16>
-__device__ __forceinline__ uint32_t to16(float v) {
-  if constexpr (F16) return f32_to_f16(v);
-  else return f32_to_bf16(v);
-}
 // x * sigmoid(k x) with the hardware exp2 and reciprocal (about 1 ulp each,
 // far below the 16-bit rounding that follows)
 __device__ __forceinline__ float x_sigmoid(float x, float k) {

@@ -113,11 +113,6 @@ __device__ __forceinline__ i32x8_t ld32(const uint8_t* S, int o0, int o1) {
   const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(S + o1);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
-template <bool F16>
-__device__ __forceinline__ float round16(float v) {
-  if constexpr (F16) return f16_to_f32(f32_to_f16(v));
-  else return bf16_to_f32(f32_to_bf16(v));
-}
 // round16 of v[0..3], two values per conversion
 template <bool F16>
 __device__ __forceinline__ void round16x4(float (&v)[4]) {
@@ -132,11 +127,6 @@ __device__ __forceinline__ void round16x4(float (&v)[4]) {
       v[i + 1] = __uint_as_float(p & 0xffff0000u);
     }
   }
-}
-template <bool F16>
-__device__ __forceinline__ uint32_t to16(float v) {
-  if constexpr (F16) return f32_to_f16(v);
-  else return f32_to_bf16(v);
 }
 __device__ __forceinline__ float x_sigmoid(float x, float k) {
   const float e = __builtin_amdgcn_exp2f(-k * x * 1.4426950408889634f);
