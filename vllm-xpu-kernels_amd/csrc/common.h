@@ -197,6 +197,14 @@ __device__ __forceinline__ void unpack16x2(uint32_t p, float& a, float& b) {
     b = __uint_as_float(p & 0xffff0000u);
   }
 }
+// each of v[0..N-1] rounded to the 16-bit type (N even), two values per
+// conversion
+template <bool F16, int N>
+__device__ __forceinline__ void round16xn(float (&v)[N]) {
+  static_assert(N % 2 == 0, "pairs");
+#pragma unroll
+  for (int i = 0; i < N; i += 2) unpack16x2<F16>(pack16x2<F16>(v[i], v[i + 1]), v[i], v[i + 1]);
+}
 // fp4_code's rounding from the hardware conversion (round to nearest even),
 // for values that are 16-bit floats (at most 11 significant bits) times a
 // power of two s: the operands are multiplied by sn = s (1 - 2^-12) (exact:

@@ -402,56 +402,89 @@ __global__ __launch_bounds__(512) void moe_gemm_wide4_kernel(const GemmArgs a) {
   const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(a.D) & 15) == 0;
   constexpr int CPR = 2 * NOUT / 16;  // 16-byte chunks per row
   __syncthreads();  // every wave is done with the ring
+  // the tile's 16-bit outputs into the LDS staging rows of pass `pass`,
+  // specialised on the activation, gemm1_clamp_limit and the bias (uniform
+  // per launch) so that no value branches on them; gate and up rounded two
+  // values per conversion
+  auto stage_out = [&](int pass, auto silu_c, auto clamp_c, auto bias_c) {
+    constexpr bool SILU = decltype(silu_c)::value;
+    constexpr bool CLAMP = decltype(clamp_c)::value;
+    constexpr bool HASB = decltype(bias_c)::value;
 #pragma unroll
-  for (int pass = 0; pass < PASSES; ++pass) {
-    if (PASSES == 1 || wm == pass) {
+    for (int i = 0; i < NI; ++i) {
+      float bg[16], bu[16];
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        float bg[16], bu[16];
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + tcol(i, r);
+        const bool has = HASB && n < N;
+        bg[r] = has ? ld16<F16>(a.bias[bias_base + n]) : 0.f;
+        bu[r] = has && kGlu ? ld16<F16>(a.bias[bias_base + a.up_off + n]) : 0.f;
+      }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          bg[r] = 0.f;
-          bu[r] = 0.f;
-          if (a.bias) {
-            const int64_t n = n0 + tcol(i, r);
-            if (n < N) {
-              bg[r] = ld16<F16>(a.bias[bias_base + n]);
-              if constexpr (kGlu) bu[r] = ld16<F16>(a.bias[bias_base + a.up_off + n]);
+      for (int j = 0; j < MG; ++j) {
+        const int srow = 32 * MG * wm + 32 * j + l32 - pass * PROWS;
+        float ov[16];  // rounded to the 16-bit type once, in the packing below
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ov[r] = HASB ? (W8 ? acc[i][j][r] * es : acc[i][j][r]) + bg[r] : (W8 ? acc[i][j][r] * es : acc[i][j][r]);
+        if constexpr (kGlu) {
+          float u[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) u[r] = HASB ? (W8 ? acc[1][j][r] * es : acc[1][j][r]) + bu[r] : (W8 ? acc[1][j][r] * es : acc[1][j][r]);
+          round16xn<F16>(ov);
+          round16xn<F16>(u);
+          if constexpr (CLAMP)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              glu_clamp_with(a.clamp_limit, SILU ? MI355MOE_ACT_SILU : MI355MOE_ACT_SWIGLUOAI, N,
+                             n0 + tcol(i, r), ov[r], u[r]);
+          if constexpr (SILU) {
+            float sg[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sg[r] = x_sigmoid(ov[r], 1.f);
+            round16xn<F16>(sg);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ov[r] = sg[r] * u[r];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float gc = ov[r] > a.limit ? a.limit : ov[r];
+              const float uc = u[r] > a.limit ? a.limit : (u[r] < -a.limit ? -a.limit : u[r]);
+              ov[r] = (uc + 1.f) * x_sigmoid(gc, a.alpha);
             }
           }
         }
 #pragma unroll
-        for (int j = 0; j < MG; ++j) {
-          const int srow = 32 * MG * wm + 32 * j + l32 - pass * PROWS;
-          float ov[16];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float g = (W8 ? acc[i][j][r] * es : acc[i][j][r]) + bg[r];  // rounded below
-            if constexpr (kGlu) {
-              g = round16<F16>(g);
-              float u = round16<F16>((W8 ? acc[1][j][r] * es : acc[1][j][r]) + bu[r]);
-              glu_clamp(a, n0 + tcol(i, r), g, u);
-              float y;
-              if (a.act == MI355MOE_ACT_SILU) {
-                y = round16<F16>(x_sigmoid(g, 1.f)) * u;
-              } else {
-                g = g > a.limit ? a.limit : g;
-                u = u > a.limit ? a.limit : (u < -a.limit ? -a.limit : u);
-                y = (u + 1.f) * x_sigmoid(g, a.alpha);
-              }
-              g = y;
-            }
-            ov[r] = g;  // one rounding to the 16-bit type, in the packing below
-          }
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const uint32_t lo = pack16x2<F16>(ov[4 * g4], ov[4 * g4 + 1]);
-            const uint32_t hi = pack16x2<F16>(ov[4 * g4 + 2], ov[4 * g4 + 3]);
-            *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(i, 4 * g4)) = make_uint2(lo, hi);
-          }
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const uint32_t lo = pack16x2<F16>(ov[4 * g4], ov[4 * g4 + 1]);
+          const uint32_t hi = pack16x2<F16>(ov[4 * g4 + 2], ov[4 * g4 + 3]);
+          *reinterpret_cast<uint2*>(lds + srow * PITCH + 2 * tcol(i, 4 * g4)) = make_uint2(lo, hi);
         }
       }
     }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  auto stage_pass = [&](int pass) {
+    auto with_bias = [&](auto silu_c, auto clamp_c) {
+      if (a.bias) stage_out(pass, silu_c, clamp_c, T_{});
+      else stage_out(pass, silu_c, clamp_c, F_{});
+    };
+    if constexpr (!kGlu) {
+      with_bias(T_{}, F_{});
+    } else {
+      const bool clamp = a.clamp_limit > 0.f;
+      if (a.act == MI355MOE_ACT_SILU) {
+        if (clamp) with_bias(T_{}, T_{});
+        else with_bias(T_{}, F_{});
+      } else {
+        if (clamp) with_bias(F_{}, T_{});
+        else with_bias(F_{}, F_{});
+      }
+    }
+  };
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    if (PASSES == 1 || wm == pass) stage_pass(pass);
     __syncthreads();
     for (int idx = tid; idx < PROWS * CPR; idx += 512) {
       const int srow = idx / CPR, ch = idx % CPR;

@@ -113,21 +113,6 @@ __device__ __forceinline__ i32x8_t ld32(const uint8_t* S, int o0, int o1) {
   const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(S + o1);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
-// round16 of v[0..3], two values per conversion
-template <bool F16>
-__device__ __forceinline__ void round16x4(float (&v)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; i += 2) {
-    const uint32_t p = pack16x2<F16>(v[i], v[i + 1]);
-    if constexpr (F16) {
-      v[i] = f16_to_f32(static_cast<uint16_t>(p));
-      v[i + 1] = f16_to_f32(static_cast<uint16_t>(p >> 16));
-    } else {
-      v[i] = __uint_as_float(p << 16);
-      v[i + 1] = __uint_as_float(p & 0xffff0000u);
-    }
-  }
-}
 __device__ __forceinline__ float x_sigmoid(float x, float k) {
   const float e = __builtin_amdgcn_exp2f(-k * x * 1.4426950408889634f);
   return x * __builtin_amdgcn_rcpf(1.f + e);
@@ -605,8 +590,8 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
         float u[4];
   #pragma unroll
         for (int r = 0; r < 4; ++r) u[r] = HASB ? acc[1][j][r] + bus[r] : acc[1][j][r];
-        round16x4<F16>(gv);
-        round16x4<F16>(u);
+        round16xn<F16>(gv);
+        round16xn<F16>(u);
         if constexpr (CLAMP)
   #pragma unroll
           for (int r = 0; r < 4; ++r)
@@ -616,7 +601,7 @@ __global__ __launch_bounds__(512) void moe_gemm_wide8p_kernel(const GemmArgs a,
           float sg[4];
   #pragma unroll
           for (int r = 0; r < 4; ++r) sg[r] = x_sigmoid(gv[r], 1.f);
-          round16x4<F16>(sg);
+          round16xn<F16>(sg);
   #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = sg[r] * u[r];
         } else {
